@@ -1,0 +1,157 @@
+/*
+ * mamba3_amd.h — C-ABI of the MI355X (gfx950) Mamba-3 chunked-SSD forward path.
+ *
+ * Every entry point takes plain device pointers, sizes and a HIP stream passed as
+ * `void*` (a hipStream_t; NULL means the null stream). Nothing here allocates,
+ * synchronises the host, or keeps mutable global state: outputs and workspaces are
+ * owned by the caller, and every call is reentrant on distinct buffers. Each call
+ * returns M3_OK (0) or an m3_status code; m3_status_string() names it. Arguments
+ * are validated on the host before any launch, so a rejected call launches nothing.
+ *
+ * Layouts are row-major and contiguous. Shape letters: B batch, T sequence length,
+ * H heads, P headdim, N d_state, R mimo_rank, G ngroups, K number of chunks,
+ * d_in_proj = 2*H*P + 2*G*N*R + H (+H if trapezoidal) (+N/2 if complex).
+ * The in_proj row is split as [z | x | B | C | dt | lambda | theta]; inside B and C
+ * the flat index is g*N*R + n*R + r (rank fastest); inside z and x it is h*P + p.
+ */
+#ifndef MAMBA3_AMD_H
+#define MAMBA3_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types of activations (the in_proj output, the gated output). */
+enum m3_dtype {
+    M3_DTYPE_F32 = 0,
+    M3_DTYPE_BF16 = 1
+};
+
+enum m3_status {
+    M3_OK = 0,
+    M3_ERR_NULL_POINTER = 1,      /* a required pointer is NULL */
+    M3_ERR_INVALID_SHAPE = 2,     /* a size is non-positive or inconsistent */
+    M3_ERR_UNSUPPORTED = 3,       /* shape/dtype outside what the kernels handle */
+    M3_ERR_WORKSPACE = 4,         /* workspace missing or smaller than required */
+    M3_ERR_MISALIGNED = 5,        /* a pointer violates the documented alignment */
+    M3_ERR_LAUNCH = 6,            /* the HIP runtime rejected a kernel launch */
+    M3_ERR_DEVICE = 7             /* device query failed (no device / wrong arch) */
+};
+
+/* Static description of one KulaMamba layer and of the activation tensor it reads.
+ * Mirrors the constructor of KulaMamba (mamba3/mamba3.py:50-112). */
+typedef struct m3_layer_desc {
+    int32_t batch;            /* B */
+    int32_t seqlen;           /* T (1 for step) */
+    int32_t nheads;           /* H */
+    int32_t headdim;          /* P */
+    int32_t d_state;          /* N (even) */
+    int32_t mimo_rank;        /* R */
+    int32_t ngroups;          /* G (divides H) */
+    int32_t use_trapezoidal;  /* 0/1: lambda columns present, two-term update */
+    int32_t use_complex;      /* 0/1: theta columns present, data-dependent RoPE */
+    int32_t dtype;            /* m3_dtype of proj and of the gated output */
+    int64_t proj_row_stride;  /* elements between consecutive tokens of proj (>= d_in_proj) */
+    float rms_eps;            /* RMSNorm epsilon of B_norm / C_norm (1e-5 in the reference) */
+} m3_layer_desc;
+
+/* Small per-layer parameters, all fp32 device arrays. Names follow the reference's
+ * parameters (mamba3/mamba3.py:95-111). */
+typedef struct m3_layer_params {
+    const float* A_log;      /* [H] */
+    const float* D;          /* [H] */
+    const float* dt_bias;    /* [H] */
+    const float* B_norm_w;   /* [N*R] */
+    const float* C_norm_w;   /* [N*R] */
+    const float* B_bias;     /* [G,N,R] */
+    const float* C_bias;     /* [G,N,R] */
+    const float* mimo_x;     /* [H,P,R] */
+    const float* mimo_z;     /* [H,P,R] */
+    const float* mimo_down;  /* [H,P,R] */
+} m3_layer_params;
+
+const char* m3_status_string(int status);
+
+/* Library version as major*10000 + minor*100 + patch. */
+int m3_version(void);
+
+/*
+ * Inter-chunk state scan. Replaces the reference's native `scan_forward`
+ * (mamba3/csrc/scan.cu:128-166, bound at scan.cu:214-216) and its torch fallback
+ * (mamba3/scan.py:34-44):
+ *     h_states[b,0,h,:]   = h_init[b,h,:]  (or 0 when h_init is NULL)
+ *     h_states[b,k+1,h,:] = decay[b,k,h] * h_states[b,k,h,:] + h_chunk[b,k,h,:]
+ * decay [B,K,H], h_chunk [B,K,H,PN], h_init [B,H,PN] (nullable), h_states [B,K,H,PN];
+ * all fp32. Unlike the reference, PN is not limited to 16384.
+ * Pointers must be 16-byte aligned when PN % 4 == 0 (the vectorised path).
+ */
+int m3_scan_fwd(const float* decay, const float* h_chunk, const float* h_init,
+                float* h_states, int64_t batch, int64_t nchunks, int64_t nheads,
+                int64_t pn, void* stream);
+
+/*
+ * Bytes of device workspace m3_prefill_fwd needs for `desc` (0 is possible).
+ * No counterpart in the reference, which allocates inside ATen.
+ */
+int m3_prefill_workspace_size(const m3_layer_desc* desc, size_t* bytes);
+
+/*
+ * Fused chunked-SSD prefill of one KulaMamba layer, from the in_proj output to the
+ * gated, rank-reduced activation that feeds out_proj. Replaces the reference region
+ * mamba3/mamba3.py:199-256 (dt/decay prep, _process_BC_train, MIMO/trapezoid prep,
+ * chunked_ssd of mamba3/ssd.py:118-244 with _IntraChunkFn ssd.py:30-65 and ssd_scan,
+ * the SiLU gate and MIMO-down sum) and the prefill state of mamba3.py:241-256.
+ *   proj      [B,T,proj_row_stride] in desc->dtype
+ *   dt_scale  [B,T,H] fp32 or NULL (multiplies softplus(dt), mamba3.py:200-202)
+ *   y_out     [B,T,H*P] in desc->dtype (input of out_proj)
+ *   h_final   [B,H,P,N] fp32 or NULL   (state 'h')
+ *   angle     [B,H,N/2] fp32 or NULL   (state 'angle' = cumulative RoPE angle at T-1)
+ *   prev_bx   [B,H,P,N] fp32 or NULL   (state 'prev_BX' = B~_{T-1} x_{T-1}^T)
+ *   workspace of at least m3_prefill_workspace_size() bytes, 256-byte aligned.
+ */
+int m3_prefill_fwd(const m3_layer_desc* desc, const m3_layer_params* params,
+                   const void* proj, const float* dt_scale, void* y_out,
+                   float* h_final, float* angle, float* prev_bx,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * O(1) decode step of one KulaMamba layer for B tokens. Replaces
+ * mamba3/mamba3.py:275-316 (everything in KulaMamba.step between in_proj and
+ * out_proj, including _process_BC_step mamba3.py:170-190). Out of place, like the
+ * reference (which returns a new state dict, mamba3.py:322):
+ *   proj [B,proj_row_stride] in desc->dtype; dt_scale [B,H] fp32 or NULL;
+ *   h_in, prev_bx_in [B,H,P,N] fp32; angle_in [B,H,N/2] of angle_dtype;
+ *   y_out [B,H*P] desc->dtype; h_out, prev_bx_out [B,H,P,N] fp32;
+ *   angle_out [B,H,N/2] of angle_dtype. Output buffers must not alias inputs.
+ * desc->seqlen is ignored (one token per batch row).
+ */
+int m3_step_fwd(const m3_layer_desc* desc, const m3_layer_params* params,
+                const void* proj, const float* dt_scale,
+                const float* h_in, const float* prev_bx_in, const void* angle_in,
+                int angle_dtype, void* y_out, float* h_out, float* prev_bx_out,
+                void* angle_out, void* stream);
+
+/*
+ * Chunked SSD on pre-processed, head-expanded inputs: the public op
+ * chunked_ssd (mamba3/ssd.py:118-244). All tensors are in `dtype` except h_init,
+ * h_final (fp32) and A, D (fp32 [H]).
+ *   x_g, x_raw [B,T,H,P,R]; x_b [B,T,H,P,R] or NULL (then B_b must be NULL);
+ *   B_g, C [B,T,H,N,R]; B_b [B,T,H,N,R] or NULL; dt [B,T,H];
+ *   h_init [B,H,P,N] fp32 or NULL; y [B,T,H,P,R] in dtype; h_final [B,H,P,N] or NULL.
+ * state_ws: [B,H,P,N] fp32 scratch owned by the caller (may equal h_final).
+ */
+int m3_chunked_ssd_fwd(int32_t batch, int32_t seqlen, int32_t nheads, int32_t headdim,
+                       int32_t d_state, int32_t mimo_rank, int32_t dtype,
+                       const void* x_g, const void* x_b, const void* B_g, const void* B_b,
+                       const void* C, const void* dt, const float* A, const float* D,
+                       const void* x_raw, const float* h_init, void* y, float* h_final,
+                       float* state_ws, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MAMBA3_AMD_H */

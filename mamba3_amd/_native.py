@@ -1,0 +1,172 @@
+"""ctypes binding of `lib/libmamba3_amd.so` (C-ABI declared in include/mamba3_amd.h).
+
+PyTorch supplies device memory and the current HIP stream; every compute call goes
+through the native library. There is no CPU or eager fallback: a CPU tensor or a
+missing library raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libmamba3_amd.so"
+
+M3_DTYPE_F32 = 0
+M3_DTYPE_BF16 = 1
+
+_DTYPE_CODE = {torch.float32: M3_DTYPE_F32, torch.bfloat16: M3_DTYPE_BF16}
+
+# Exported symbols, kept in step with include/mamba3_amd.h.
+EXPORTED_SYMBOLS = (
+    "m3_status_string",
+    "m3_version",
+    "m3_scan_fwd",
+    "m3_prefill_workspace_size",
+    "m3_prefill_fwd",
+    "m3_step_fwd",
+    "m3_chunked_ssd_fwd",
+)
+
+
+class NativeError(RuntimeError):
+    """A native entry point returned a non-zero m3_status."""
+
+
+class LayerDesc(ctypes.Structure):
+    _fields_ = [
+        ("batch", ctypes.c_int32),
+        ("seqlen", ctypes.c_int32),
+        ("nheads", ctypes.c_int32),
+        ("headdim", ctypes.c_int32),
+        ("d_state", ctypes.c_int32),
+        ("mimo_rank", ctypes.c_int32),
+        ("ngroups", ctypes.c_int32),
+        ("use_trapezoidal", ctypes.c_int32),
+        ("use_complex", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("proj_row_stride", ctypes.c_int64),
+        ("rms_eps", ctypes.c_float),
+    ]
+
+
+class LayerParams(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_void_p) for name in (
+        "A_log", "D", "dt_bias", "B_norm_w", "C_norm_w", "B_bias", "C_bias",
+        "mimo_x", "mimo_z", "mimo_down")]
+
+
+_lib = None
+_lib_lock = threading.Lock()
+
+_vp = ctypes.c_void_p
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+
+
+def _declare(lib: ctypes.CDLL) -> None:
+    lib.m3_status_string.restype = ctypes.c_char_p
+    lib.m3_status_string.argtypes = [ctypes.c_int]
+    lib.m3_version.restype = ctypes.c_int
+    lib.m3_version.argtypes = []
+    lib.m3_scan_fwd.restype = ctypes.c_int
+    lib.m3_scan_fwd.argtypes = [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]
+    lib.m3_prefill_workspace_size.restype = ctypes.c_int
+    lib.m3_prefill_workspace_size.argtypes = [ctypes.POINTER(LayerDesc),
+                                              ctypes.POINTER(ctypes.c_size_t)]
+    lib.m3_prefill_fwd.restype = ctypes.c_int
+    lib.m3_prefill_fwd.argtypes = [ctypes.POINTER(LayerDesc), ctypes.POINTER(LayerParams),
+                                   _vp, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp]
+    lib.m3_step_fwd.restype = ctypes.c_int
+    lib.m3_step_fwd.argtypes = [ctypes.POINTER(LayerDesc), ctypes.POINTER(LayerParams),
+                                _vp, _vp, _vp, _vp, _vp, ctypes.c_int, _vp, _vp, _vp, _vp, _vp]
+    lib.m3_chunked_ssd_fwd.restype = ctypes.c_int
+    lib.m3_chunked_ssd_fwd.argtypes = [_i32, _i32, _i32, _i32, _i32, _i32, _i32,
+                                       _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                       _vp, _vp, _vp, _vp]
+
+
+def lib() -> ctypes.CDLL:
+    """Load the native library (once). Raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        with _lib_lock:
+            if _lib is None:
+                if not LIB_PATH.exists():
+                    raise RuntimeError(
+                        f"mamba3_amd native library not found at {LIB_PATH}; "
+                        "build it with `python -m mamba3_amd.build`")
+                handle = ctypes.CDLL(str(LIB_PATH))
+                _declare(handle)
+                _lib = handle
+    return _lib
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        msg = lib().m3_status_string(status).decode()
+        raise NativeError(f"{what}: {msg} (m3_status {status})")
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODE[dtype]
+    except KeyError:
+        raise TypeError(f"mamba3_amd kernels support float32 and bfloat16, got {dtype}") from None
+
+
+def require_gpu(*tensors: torch.Tensor) -> None:
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError(
+                "mamba3_amd runs its SSD path only as HIP kernels on an AMD GPU; "
+                f"got a tensor on {t.device}. Move the module and inputs to the GPU.")
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def scan_fwd(decay: torch.Tensor, h_chunk: torch.Tensor, h_init: torch.Tensor | None,
+             out: torch.Tensor) -> None:
+    B, K, H, PN = h_chunk.shape
+    check(lib().m3_scan_fwd(ptr(decay), ptr(h_chunk), ptr(h_init), ptr(out), B, K, H, PN,
+                            stream_of(h_chunk)), "m3_scan_fwd")
+
+
+def prefill_workspace_bytes(desc: LayerDesc) -> int:
+    n = ctypes.c_size_t(0)
+    check(lib().m3_prefill_workspace_size(ctypes.byref(desc), ctypes.byref(n)),
+          "m3_prefill_workspace_size")
+    return n.value
+
+
+def prefill_fwd(desc: LayerDesc, params: LayerParams, proj, dt_scale, y_out, h_final, angle,
+                prev_bx, workspace, workspace_bytes: int) -> None:
+    check(lib().m3_prefill_fwd(ctypes.byref(desc), ctypes.byref(params), ptr(proj),
+                               ptr(dt_scale), ptr(y_out), ptr(h_final), ptr(angle),
+                               ptr(prev_bx), ptr(workspace), workspace_bytes,
+                               stream_of(proj)), "m3_prefill_fwd")
+
+
+def step_fwd(desc: LayerDesc, params: LayerParams, proj, dt_scale, h_in, prev_in, angle_in,
+             y_out, h_out, prev_out, angle_out) -> None:
+    check(lib().m3_step_fwd(ctypes.byref(desc), ctypes.byref(params), ptr(proj),
+                            ptr(dt_scale), ptr(h_in), ptr(prev_in), ptr(angle_in),
+                            dtype_code(angle_in.dtype), ptr(y_out), ptr(h_out), ptr(prev_out),
+                            ptr(angle_out), stream_of(proj)), "m3_step_fwd")
+
+
+def chunked_fwd(B, T, H, P, N, R, dtype, x_g, x_b, B_g, B_b, C, dt, A, D, x_raw, h_init, y,
+                h_final, state_ws) -> None:
+    check(lib().m3_chunked_ssd_fwd(B, T, H, P, N, R, dtype_code(dtype), ptr(x_g), ptr(x_b),
+                                   ptr(B_g), ptr(B_b), ptr(C), ptr(dt), ptr(A), ptr(D),
+                                   ptr(x_raw), ptr(h_init), ptr(y), ptr(h_final),
+                                   ptr(state_ws), stream_of(x_g)), "m3_chunked_ssd_fwd")

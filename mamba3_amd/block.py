@@ -1,0 +1,206 @@
+"""Residual block and language model around KulaMamba: drop-in for mamba3.block
+(mamba3/block.py:16-231).
+
+These are the callers of the SSD path (norms, SwiGLU MLP, embedding, tied lm_head,
+greedy/sampled decode loop) and run as PyTorch ops; the SSD itself runs in the HIP
+kernels through KulaMamba. Module names, registration order and initialisation order
+equal the reference's so seeded models hold identical weights.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+from torch.utils.checkpoint import checkpoint as grad_checkpoint
+
+from .layer import KulaMamba, RMSNorm
+
+
+class SwiGLU(nn.Module):
+    """w_down(silu(w_gate x) * w_up x) (mamba3/block.py:16-26)."""
+
+    def __init__(self, d_model: int, d_ff: int | None = None, bias: bool = False):
+        super().__init__()
+        if d_ff is None:
+            d_ff = int(d_model * 8 / 3 / 64 + 1) * 64
+        self.w_gate = nn.Linear(d_model, d_ff, bias=bias)
+        self.w_up = nn.Linear(d_model, d_ff, bias=bias)
+        self.w_down = nn.Linear(d_ff, d_model, bias=bias)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self.w_down(F.silu(self.w_gate(x)) * self.w_up(x))
+
+
+class KulaMambaBlock(nn.Module):
+    """Pre-norm residual block: x + s*ssm(norm(x)), then x + s*mlp(norm(x))
+    (mamba3/block.py:29-107)."""
+
+    def __init__(
+        self,
+        d_model: int,
+        d_state: int = 128,
+        expand: int = 2,
+        headdim: int = 64,
+        ngroups: int | None = None,
+        mimo_rank: int = 2,
+        chunk_size: int = 64,
+        use_mlp: bool = True,
+        mlp_expand: float = 2.667,
+        norm_eps: float = 1e-5,
+        bias: bool = False,
+        residual_scale: float = 1.0,
+        gradient_checkpointing: bool = False,
+        use_trapezoidal: bool = True,
+        use_complex_ssm: bool = True,
+    ):
+        super().__init__()
+        self.residual_scale = residual_scale
+        self.gradient_checkpointing = gradient_checkpointing
+        self.ssm_norm = RMSNorm(d_model, eps=norm_eps)
+        self.ssm = KulaMamba(
+            d_model=d_model, d_state=d_state, expand=expand, headdim=headdim,
+            ngroups=ngroups, mimo_rank=mimo_rank, chunk_size=chunk_size, bias=bias,
+            use_trapezoidal=use_trapezoidal, use_complex_ssm=use_complex_ssm,
+        )
+        self.use_mlp = use_mlp
+        if use_mlp:
+            d_ff = int(d_model * mlp_expand / 64 + 1) * 64
+            self.mlp_norm = RMSNorm(d_model, eps=norm_eps)
+            self.mlp = SwiGLU(d_model, d_ff, bias=bias)
+
+    def _ssm_forward(self, x_normed):
+        return self.ssm(x_normed)
+
+    def _mlp_forward(self, x_normed):
+        return self.mlp(x_normed)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        ckpt = self.gradient_checkpointing and self.training
+        if ckpt:
+            h = grad_checkpoint(self._ssm_forward, self.ssm_norm(x), use_reentrant=False)
+        else:
+            h = self.ssm(self.ssm_norm(x))
+        x = x + h * self.residual_scale
+        if self.use_mlp:
+            if ckpt:
+                m = grad_checkpoint(self._mlp_forward, self.mlp_norm(x), use_reentrant=False)
+            else:
+                m = self.mlp(self.mlp_norm(x))
+            x = x + m * self.residual_scale
+        return x
+
+    def step(self, x: torch.Tensor, ssm_state: dict):
+        h, new_state = self.ssm.step(self.ssm_norm(x), ssm_state)
+        x = x + h * self.residual_scale
+        if self.use_mlp:
+            x = x + self.mlp(self.mlp_norm(x)) * self.residual_scale
+        return x, new_state
+
+    def prefill(self, x: torch.Tensor):
+        h, state = self.ssm.prefill(self.ssm_norm(x))
+        x = x + h * self.residual_scale
+        if self.use_mlp:
+            x = x + self.mlp(self.mlp_norm(x)) * self.residual_scale
+        return x, state
+
+
+class KulaMambaLM(nn.Module):
+    """Embedding -> n_layers KulaMambaBlock -> RMSNorm -> (tied) lm_head
+    (mamba3/block.py:110-231)."""
+
+    def __init__(
+        self,
+        vocab_size: int,
+        d_model: int = 768,
+        n_layers: int = 12,
+        d_state: int = 128,
+        expand: int = 2,
+        headdim: int = 64,
+        ngroups: int | None = None,
+        mimo_rank: int = 2,
+        chunk_size: int = 64,
+        use_mlp: bool = True,
+        tie_weights: bool = True,
+        norm_eps: float = 1e-5,
+        bias: bool = False,
+        residual_scale: str = "depth",
+        gradient_checkpointing: bool = False,
+        use_trapezoidal: bool = True,
+        use_complex_ssm: bool = True,
+    ):
+        super().__init__()
+        self.d_model = d_model
+        self.n_layers = n_layers
+        scale = 1.0 / math.sqrt(2 * n_layers) if residual_scale == "depth" else 1.0
+        self.embedding = nn.Embedding(vocab_size, d_model)
+        self.layers = nn.ModuleList([
+            KulaMambaBlock(
+                d_model=d_model, d_state=d_state, expand=expand, headdim=headdim,
+                ngroups=ngroups, mimo_rank=mimo_rank, chunk_size=chunk_size, use_mlp=use_mlp,
+                norm_eps=norm_eps, bias=bias, residual_scale=scale,
+                gradient_checkpointing=gradient_checkpointing,
+                use_trapezoidal=use_trapezoidal, use_complex_ssm=use_complex_ssm,
+            )
+            for _ in range(n_layers)
+        ])
+        self.norm = RMSNorm(d_model, eps=norm_eps)
+        self.lm_head = nn.Linear(d_model, vocab_size, bias=False)
+        if tie_weights:
+            self.lm_head.weight = self.embedding.weight
+        self._init_weights()
+
+    def _init_weights(self) -> None:
+        """N(0, 0.02) for the embedding and every Linear except the (tied) head, then the
+        KulaMamba-specific re-initialisation (mamba3/block.py:166-176)."""
+        nn.init.normal_(self.embedding.weight, std=0.02)
+        for m in self.modules():
+            if isinstance(m, nn.Linear) and m is not self.lm_head:
+                nn.init.normal_(m.weight, std=0.02)
+                if m.bias is not None:
+                    nn.init.zeros_(m.bias)
+        for m in self.modules():
+            if isinstance(m, KulaMamba):
+                m._init_weights(dt_min=0.001, dt_max=0.1)
+
+    def forward(self, input_ids: torch.Tensor, labels: torch.Tensor | None = None) -> dict:
+        x = self.embedding(input_ids)
+        for layer in self.layers:
+            x = layer(x)
+        logits = self.lm_head(self.norm(x))
+        result = {"logits": logits}
+        if labels is not None:
+            pred = logits[:, :-1].contiguous()
+            tgt = labels[:, 1:].contiguous()
+            result["loss"] = F.cross_entropy(pred.view(-1, pred.size(-1)), tgt.view(-1))
+        return result
+
+    @torch.no_grad()
+    def generate(self, input_ids: torch.Tensor, max_new_tokens: int = 100,
+                 temperature: float = 1.0, top_k: int | None = None) -> torch.Tensor:
+        """Parallel prefill of the prompt, then one `step` per new token
+        (mamba3/block.py:195-231). temperature=0 is greedy argmax."""
+        x = self.embedding(input_ids)
+        states = []
+        for layer in self.layers:
+            x, st = layer.prefill(x)
+            states.append(st)
+        logits = self.lm_head(self.norm(x)[:, -1])
+        out = [input_ids]
+        for _ in range(max_new_tokens):
+            scores = logits / temperature if temperature > 0 else logits
+            if top_k is not None:
+                kth = torch.topk(scores, min(top_k, scores.size(-1))).values[:, -1:]
+                scores = scores.masked_fill(scores < kth, float("-inf"))
+            if temperature > 0:
+                nxt = torch.multinomial(F.softmax(scores, dim=-1), num_samples=1)
+            else:
+                nxt = scores.argmax(dim=-1, keepdim=True)
+            out.append(nxt)
+            x = self.embedding(nxt.squeeze(1))
+            for i, layer in enumerate(self.layers):
+                x, states[i] = layer.step(x, states[i])
+            logits = self.lm_head(self.norm(x))
+        return torch.cat(out, dim=1)

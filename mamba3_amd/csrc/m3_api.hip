@@ -1,0 +1,139 @@
+// C-ABI entry points (declared in include/mamba3_amd.h). Validates every argument on
+// the host, then calls the launchers. Never throws, never allocates, never syncs.
+#include <hip/hip_runtime.h>
+
+#include "m3_kernels.h"
+
+namespace {
+
+using m3::proj_layout;
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+int check_desc(const m3_layer_desc* d) {
+    if (!d) return M3_ERR_NULL_POINTER;
+    if (d->batch <= 0 || d->seqlen <= 0 || d->nheads <= 0 || d->headdim <= 0 ||
+        d->d_state <= 0 || d->mimo_rank <= 0 || d->ngroups <= 0)
+        return M3_ERR_INVALID_SHAPE;
+    if (d->d_state % 2 != 0) return M3_ERR_INVALID_SHAPE;
+    if (d->nheads % d->ngroups != 0) return M3_ERR_INVALID_SHAPE;
+    if (d->dtype != M3_DTYPE_F32 && d->dtype != M3_DTYPE_BF16) return M3_ERR_UNSUPPORTED;
+    if (d->use_trapezoidal != 0 && d->use_trapezoidal != 1) return M3_ERR_INVALID_SHAPE;
+    if (d->use_complex != 0 && d->use_complex != 1) return M3_ERR_INVALID_SHAPE;
+    if (d->proj_row_stride < proj_layout(*d).width) return M3_ERR_INVALID_SHAPE;
+    if (!(d->rms_eps >= 0.f)) return M3_ERR_INVALID_SHAPE;
+    // Kernel limits: headdim <= 256, d_state <= 512, rank <= 8.
+    if (d->headdim > 256 || d->d_state > 512 || d->mimo_rank > 8) return M3_ERR_UNSUPPORTED;
+    return M3_OK;
+}
+
+int check_params(const m3_layer_params* p) {
+    if (!p) return M3_ERR_NULL_POINTER;
+    if (!p->A_log || !p->D || !p->dt_bias || !p->B_norm_w || !p->C_norm_w || !p->B_bias ||
+        !p->C_bias || !p->mimo_x || !p->mimo_z || !p->mimo_down)
+        return M3_ERR_NULL_POINTER;
+    return M3_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* m3_status_string(int status) {
+    switch (status) {
+        case M3_OK: return "ok";
+        case M3_ERR_NULL_POINTER: return "a required pointer is NULL";
+        case M3_ERR_INVALID_SHAPE: return "invalid or inconsistent shape";
+        case M3_ERR_UNSUPPORTED: return "shape or dtype not supported by the kernels";
+        case M3_ERR_WORKSPACE: return "workspace missing or too small";
+        case M3_ERR_MISALIGNED: return "pointer alignment violated";
+        case M3_ERR_LAUNCH: return "kernel launch failed";
+        case M3_ERR_DEVICE: return "device query failed";
+        default: return "unknown status";
+    }
+}
+
+int m3_version(void) { return 100; }
+
+int m3_scan_fwd(const float* decay, const float* h_chunk, const float* h_init,
+                float* h_states, int64_t batch, int64_t nchunks, int64_t nheads, int64_t pn,
+                void* stream) {
+    if (!decay || !h_chunk || !h_states) return M3_ERR_NULL_POINTER;
+    if (batch <= 0 || nchunks <= 0 || nheads <= 0 || pn <= 0) return M3_ERR_INVALID_SHAPE;
+    if (batch * nheads * pn > ((int64_t)1 << 40)) return M3_ERR_UNSUPPORTED;
+    if (nchunks > (1 << 30)) return M3_ERR_UNSUPPORTED;
+    return m3::launch_scan_fwd(decay, h_chunk, h_init, h_states, batch, nchunks, nheads, pn,
+                               as_stream(stream)) == 0
+               ? M3_OK
+               : M3_ERR_LAUNCH;
+}
+
+int m3_prefill_workspace_size(const m3_layer_desc* desc, size_t* bytes) {
+    if (!bytes) return M3_ERR_NULL_POINTER;
+    const int st = check_desc(desc);
+    if (st != M3_OK) return st;
+    *bytes = m3::generic_prefill_workspace(*desc);
+    return M3_OK;
+}
+
+int m3_prefill_fwd(const m3_layer_desc* desc, const m3_layer_params* params, const void* proj,
+                   const float* dt_scale, void* y_out, float* h_final, float* angle,
+                   float* prev_bx, void* workspace, size_t workspace_bytes, void* stream) {
+    int st = check_desc(desc);
+    if (st != M3_OK) return st;
+    st = check_params(params);
+    if (st != M3_OK) return st;
+    if (!proj || !y_out) return M3_ERR_NULL_POINTER;
+    const size_t need = m3::generic_prefill_workspace(*desc);
+    if (!h_final && (workspace == nullptr || workspace_bytes < need)) return M3_ERR_WORKSPACE;
+    if (workspace && !aligned(workspace, 256)) return M3_ERR_MISALIGNED;
+    return m3::launch_generic_prefill(*desc, *params, proj, dt_scale, y_out, h_final, angle,
+                                      prev_bx, workspace, as_stream(stream));
+}
+
+int m3_step_fwd(const m3_layer_desc* desc, const m3_layer_params* params, const void* proj,
+                const float* dt_scale, const float* h_in, const float* prev_bx_in,
+                const void* angle_in, int angle_dtype, void* y_out, float* h_out,
+                float* prev_bx_out, void* angle_out, void* stream) {
+    int st = check_desc(desc);
+    if (st != M3_OK) return st;
+    st = check_params(params);
+    if (st != M3_OK) return st;
+    if (!proj || !h_in || !prev_bx_in || !angle_in || !y_out || !h_out || !prev_bx_out ||
+        !angle_out)
+        return M3_ERR_NULL_POINTER;
+    if (angle_dtype != M3_DTYPE_F32 && angle_dtype != M3_DTYPE_BF16) return M3_ERR_UNSUPPORTED;
+    if (!m3::step_supported(desc->d_state, desc->mimo_rank)) return M3_ERR_UNSUPPORTED;
+    if (!aligned(h_in, 16) || !aligned(prev_bx_in, 16) || !aligned(h_out, 16) ||
+        !aligned(prev_bx_out, 16))
+        return M3_ERR_MISALIGNED;
+    if (h_in == h_out || prev_bx_in == prev_bx_out || h_in == prev_bx_out ||
+        prev_bx_in == h_out)
+        return M3_ERR_INVALID_SHAPE;
+    return m3::launch_step(*desc, *params, proj, dt_scale, h_in, prev_bx_in, angle_in,
+                           angle_dtype, y_out, h_out, prev_bx_out, angle_out,
+                           as_stream(stream));
+}
+
+int m3_chunked_ssd_fwd(int32_t batch, int32_t seqlen, int32_t nheads, int32_t headdim,
+                       int32_t d_state, int32_t mimo_rank, int32_t dtype, const void* x_g,
+                       const void* x_b, const void* B_g, const void* B_b, const void* C,
+                       const void* dt, const float* A, const float* D, const void* x_raw,
+                       const float* h_init, void* y, float* h_final, float* state_ws,
+                       void* stream) {
+    if (batch <= 0 || seqlen <= 0 || nheads <= 0 || headdim <= 0 || d_state <= 0 ||
+        mimo_rank <= 0)
+        return M3_ERR_INVALID_SHAPE;
+    if (dtype != M3_DTYPE_F32 && dtype != M3_DTYPE_BF16) return M3_ERR_UNSUPPORTED;
+    if (headdim > 256 || d_state > 512 || mimo_rank > 8) return M3_ERR_UNSUPPORTED;
+    if (!x_g || !B_g || !C || !dt || !A || !D || !x_raw || !y) return M3_ERR_NULL_POINTER;
+    if ((x_b == nullptr) != (B_b == nullptr)) return M3_ERR_NULL_POINTER;
+    if (!h_final && !state_ws) return M3_ERR_WORKSPACE;
+    return m3::launch_generic_chunked(batch, seqlen, nheads, headdim, d_state, mimo_rank, dtype,
+                                      x_g, x_b, B_g, B_b, C, dt, A, D, x_raw, h_init, y, h_final,
+                                      state_ws, as_stream(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,475 @@
+// Generic chunked-SSD forward kernels (fp32 arithmetic, any supported shape and dtype).
+//
+// One workgroup owns one (batch, head) pair and walks the sequence in chunks of
+// `Qi` tokens, carrying the (P,N) fp32 state in a global buffer (L2 resident). Inside a
+// chunk it evaluates the quadratic (L-matrix) form of the SSD
+//
+//   y[t,r,p] = sum_{u<=t} sum_{r'} (C~_t[r] . B~_u[r']) * M[t,u] * X_u[p,r']
+//            + exp(c_t) * C~_t[r] . H[p,:]  + D * x_t[p,r]
+//   M[t,u]   = exp(c_t - c_u) * (a_u + [u<t] b_u)
+//   H       <- exp(c_end) * H + sum_u sum_{r'} X_u[p,r'] exp(c_end - c_u) (a_u + b_u) B~_u[r',:]
+//
+// which equals the reference's factored-cumsum evaluation (mamba3/ssd.py:30-65,
+// 153-244) in exact arithmetic. For the layer, the trapezoid's beta term
+// (mamba3/mamba3.py:212-220) is folded into the coefficients: a_u = lambda_u dt_u and
+// b_u = (1 - lambda_{u+1}) dt_{u+1}, because the beta term of token u+1 uses B~_u x_u
+// scaled by beta_{u+1} = (1-lambda_{u+1}) dt_{u+1} dA_{u+1}, and dA_{u+1} turns
+// exp(c_t - c_{u+1}) into exp(c_t - c_u). The last token's b term hands its beta
+// contribution to the next chunk through the state. For chunked_ssd's general
+// two-term input (independent x_b, B_b) the B rank is doubled instead and b = 0.
+//
+// These kernels are the reference-shaped path for fp32 (1e-4 parity) and for shapes
+// the MFMA kernels do not cover; performance is not their goal.
+#include "m3_common.h"
+#include "m3_kernels.h"
+
+namespace m3 {
+
+constexpr int kGenThreads = 256;
+constexpr int kGenMaxLds = 64 * 1024;
+
+struct GenShape {
+    int B, T, H, P, N, R, Rb, G, Qi;
+};
+
+// LDS plan in floats for one workgroup.
+struct GenLds {
+    int tok_dt, tok_lam, c, a, bco, phi_run, ph, rmsB, rmsC, Cs, Bs, Xs, Sc, Ys, total;
+};
+
+__host__ __device__ inline GenLds gen_lds_plan(int Qi, int N, int P, int R, int Rb,
+                                               bool complex_rope) {
+    GenLds L;
+    int o = 0;
+    L.tok_dt = o; o += Qi + 1;
+    L.tok_lam = o; o += Qi + 1;
+    L.c = o; o += Qi;
+    L.a = o; o += Qi;
+    L.bco = o; o += Qi;
+    L.phi_run = o; o += N / 2;
+    L.ph = o; o += complex_rope ? Qi * (N / 2) : 0;
+    L.rmsB = o; o += Qi;
+    L.rmsC = o; o += Qi;
+    o = (o + 3) & ~3;
+    L.Cs = o; o += Qi * R * N;
+    L.Bs = o; o += Qi * Rb * N;
+    L.Xs = o; o += Qi * Rb * P;
+    L.Sc = o; o += Qi * R * Qi * Rb;
+    L.Ys = o; o += Qi * R * P;
+    L.total = o;
+    return L;
+}
+
+static int gen_pick_chunk(int N, int P, int R, int Rb, bool complex_rope) {
+    for (int q = 64; q >= 1; q >>= 1) {
+        if (gen_lds_plan(q, N, P, R, Rb, complex_rope).total * 4 <= kGenMaxLds) return q;
+    }
+    return 0;
+}
+
+// ---------------------------------------------------------------------------------
+// Shared chunk core: scores, outputs, state update. Operates on LDS-staged tiles.
+// ---------------------------------------------------------------------------------
+__device__ void gen_chunk_core(const GenShape& s, const GenLds& L, float* sm, float* __restrict__ Hs,
+                               int nvalid) {
+    const int tid = threadIdx.x;
+    const int Qi = s.Qi, N = s.N, P = s.P, R = s.R, Rb = s.Rb;
+    const int rowsC = Qi * R, rowsB = Qi * Rb;
+    const float* c = sm + L.c;
+    const float* a = sm + L.a;
+    const float* bco = sm + L.bco;
+    const float* Cs = sm + L.Cs;
+    const float* Bs = sm + L.Bs;
+    const float* Xs = sm + L.Xs;
+    float* Sc = sm + L.Sc;
+    float* Ys = sm + L.Ys;
+
+    // Masked, weighted scores.
+    for (int idx = tid; idx < rowsC * rowsB; idx += kGenThreads) {
+        const int i = idx / rowsB, j = idx % rowsB;
+        const int t = i / R, u = j / Rb;
+        float v = 0.f;
+        if (u <= t) {
+            const float* ci = Cs + i * N;
+            const float* bj = Bs + j * N;
+            float dot = 0.f;
+            for (int n = 0; n < N; ++n) dot += ci[n] * bj[n];
+            const float coef = a[u] + (u < t ? bco[u] : 0.f);
+            v = dot * expf(c[t] - c[u]) * coef;
+        }
+        Sc[idx] = v;
+    }
+    __syncthreads();
+
+    // Intra-chunk plus inter-chunk output.
+    for (int idx = tid; idx < rowsC * P; idx += kGenThreads) {
+        const int i = idx / P, p = idx % P;
+        const int t = i / R;
+        float acc = 0.f;
+        const float* si = Sc + i * rowsB;
+        for (int j = 0; j < (t + 1) * Rb; ++j) acc += si[j] * Xs[j * P + p];
+        const float* ci = Cs + i * N;
+        const float* hp = Hs + (size_t)p * N;
+        float inter = 0.f;
+        for (int n = 0; n < N; ++n) inter += ci[n] * hp[n];
+        Ys[idx] = acc + expf(c[t]) * inter;
+    }
+    __syncthreads();
+
+    // State update.
+    const float c_end = c[Qi - 1];
+    const float d_end = expf(c_end);
+    for (int idx = tid; idx < P * N; idx += kGenThreads) {
+        const int p = idx / N, n = idx % N;
+        float acc = 0.f;
+        for (int u = 0; u < nvalid; ++u) {
+            const float w = expf(c_end - c[u]) * (a[u] + bco[u]);
+            float bx = 0.f;
+            for (int r = 0; r < Rb; ++r) bx += Xs[(u * Rb + r) * P + p] * Bs[(u * Rb + r) * N + n];
+            acc += w * bx;
+        }
+        Hs[idx] = d_end * Hs[idx] + acc;
+    }
+}
+
+// ---------------------------------------------------------------------------------
+// Layer prefill from the in_proj output.
+// ---------------------------------------------------------------------------------
+struct GenLayerArgs {
+    GenShape s;
+    GenLds L;
+    ProjLayout pl;
+    int64_t row_stride;
+    int trap, cplx;
+    float eps;
+    m3_layer_params prm;
+    const void* proj;
+    const float* dt_scale;
+    void* y_out;
+    float* state;      // [B,H,P,N] running state (becomes h_final)
+    float* angle;      // [B,H,N/2] or null
+    float* prev_bx;    // [B,H,P,N] or null
+};
+
+template <typename T>
+__global__ __launch_bounds__(kGenThreads) void gen_layer_prefill(GenLayerArgs A) {
+    extern __shared__ float sm[];
+    const GenShape& s = A.s;
+    const GenLds& L = A.L;
+    const int tid = threadIdx.x;
+    const int b = blockIdx.x / s.H, h = blockIdx.x % s.H;
+    const int g = h / (s.H / s.G);
+    const int Qi = s.Qi, N = s.N, P = s.P, R = s.R, Nh = N / 2, NR = N * R;
+    const T* proj = reinterpret_cast<const T*>(A.proj) + (int64_t)b * s.T * A.row_stride;
+    T* yo = reinterpret_cast<T*>(A.y_out) + (int64_t)b * s.T * s.H * P;
+    float* Hs = A.state + ((int64_t)b * s.H + h) * P * N;
+    const float Ah = -expf(A.prm.A_log[h]);
+    const float Dh = A.prm.D[h];
+    const float dtb = A.prm.dt_bias[h];
+    const float* wB = A.prm.B_norm_w;
+    const float* wC = A.prm.C_norm_w;
+    const float* biasB = A.prm.B_bias + (int64_t)g * NR;
+    const float* biasC = A.prm.C_bias + (int64_t)g * NR;
+    const float* mx = A.prm.mimo_x + (int64_t)h * P * R;
+    const float* mz = A.prm.mimo_z + (int64_t)h * P * R;
+    const float* md = A.prm.mimo_down + (int64_t)h * P * R;
+
+    for (int idx = tid; idx < P * N; idx += kGenThreads) Hs[idx] = 0.f;
+    for (int i = tid; i < Nh; i += kGenThreads) sm[L.phi_run + i] = 0.f;
+    __syncthreads();
+
+    const int nchunks = (s.T + Qi - 1) / Qi;
+    for (int k = 0; k < nchunks; ++k) {
+        const int s0 = k * Qi;
+        const int nvalid = min(Qi, s.T - s0);
+        // Token scalars for tokens s0 .. s0+Qi (one past the chunk for the trapezoid).
+        for (int t = tid; t <= Qi; t += kGenThreads) {
+            const int st = s0 + t;
+            float dt = 0.f, lam = 1.f;
+            if (st < s.T) {
+                const T* row = proj + (int64_t)st * A.row_stride;
+                const float sc = A.dt_scale ? A.dt_scale[((int64_t)b * s.T + st) * s.H + h] : 1.f;
+                TokenGate tg = token_gate(ld_f32(row + A.pl.dt + h), dtb, sc, Ah,
+                                          A.trap ? ld_f32(row + A.pl.lam + h) : 0.f, A.trap);
+                dt = tg.dt;
+                lam = tg.lam;
+            }
+            sm[L.tok_dt + t] = dt;
+            sm[L.tok_lam + t] = lam;
+        }
+        // RMS of B and C rows of this chunk's tokens (mamba3/mamba3.py:28-35, 151-152).
+        for (int t = tid; t < Qi; t += kGenThreads) {
+            const int st = s0 + t;
+            float rb = 0.f, rc = 0.f;
+            if (st < s.T) {
+                const T* row = proj + (int64_t)st * A.row_stride;
+                float ssb = 0.f, ssc = 0.f;
+                for (int e = 0; e < NR; ++e) {
+                    const float vb = ld_f32(row + A.pl.B + (int64_t)g * NR + e);
+                    const float vc = ld_f32(row + A.pl.C + (int64_t)g * NR + e);
+                    ssb += vb * vb;
+                    ssc += vc * vc;
+                }
+                rb = rsqrtf(ssb / NR + A.eps);
+                rc = rsqrtf(ssc / NR + A.eps);
+            }
+            sm[L.rmsB + t] = rb;
+            sm[L.rmsC + t] = rc;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            float c = 0.f;
+            for (int t = 0; t < Qi; ++t) {
+                const float dt = sm[L.tok_dt + t];
+                c += Ah * dt;
+                sm[L.c + t] = c;
+                sm[L.a + t] = (A.trap ? sm[L.tok_lam + t] : 1.f) * dt;
+                sm[L.bco + t] = A.trap ? (1.f - sm[L.tok_lam + t + 1]) * sm[L.tok_dt + t + 1] : 0.f;
+            }
+        }
+        // Data-dependent RoPE angles (mamba3/mamba3.py:160-162): phi -= dt * theta.
+        if (A.cplx) {
+            for (int i = tid; i < Nh; i += kGenThreads) {
+                float phi = sm[L.phi_run + i];
+                for (int t = 0; t < Qi; ++t) {
+                    const int st = s0 + t;
+                    if (st < s.T) {
+                        const float th = ld_f32(proj + (int64_t)st * A.row_stride + A.pl.theta + i);
+                        phi -= sm[L.tok_dt + t] * th;
+                    }
+                    sm[L.ph + t * Nh + i] = phi;
+                }
+                sm[L.phi_run + i] = phi;
+            }
+        }
+        __syncthreads();
+        // B~ and C~: RMSNorm * w + bias, then rotate pairs (2i, 2i+1) (mamba3/mamba3.py:38-45).
+        for (int idx = tid; idx < Qi * Nh * R; idx += kGenThreads) {
+            const int t = idx / (Nh * R);
+            const int rem = idx % (Nh * R);
+            const int i = rem / R, r = rem % R;
+            const int st = s0 + t;
+            float be = 0.f, bo = 0.f, ce = 0.f, co = 0.f;
+            if (st < s.T) {
+                const T* row = proj + (int64_t)st * A.row_stride;
+                const int e0 = (2 * i) * R + r, e1 = (2 * i + 1) * R + r;
+                const float rb = sm[L.rmsB + t], rc = sm[L.rmsC + t];
+                be = ld_f32(row + A.pl.B + (int64_t)g * NR + e0) * rb * wB[e0] + biasB[e0];
+                bo = ld_f32(row + A.pl.B + (int64_t)g * NR + e1) * rb * wB[e1] + biasB[e1];
+                ce = ld_f32(row + A.pl.C + (int64_t)g * NR + e0) * rc * wC[e0] + biasC[e0];
+                co = ld_f32(row + A.pl.C + (int64_t)g * NR + e1) * rc * wC[e1] + biasC[e1];
+                if (A.cplx) {
+                    float sn, cs;
+                    sincosf(sm[L.ph + t * Nh + i], &sn, &cs);
+                    const float be2 = be * cs - bo * sn, bo2 = be * sn + bo * cs;
+                    const float ce2 = ce * cs - co * sn, co2 = ce * sn + co * cs;
+                    be = be2; bo = bo2; ce = ce2; co = co2;
+                }
+            }
+            float* bs = sm + L.Bs + (t * R + r) * N;
+            float* cs_ = sm + L.Cs + (t * R + r) * N;
+            bs[2 * i] = be;
+            bs[2 * i + 1] = bo;
+            cs_[2 * i] = ce;
+            cs_[2 * i + 1] = co;
+        }
+        // MIMO x expansion (mamba3/mamba3.py:210).
+        for (int idx = tid; idx < Qi * R * P; idx += kGenThreads) {
+            const int t = idx / (R * P);
+            const int r = (idx / P) % R, p = idx % P;
+            const int st = s0 + t;
+            float v = 0.f;
+            if (st < s.T)
+                v = ld_f32(proj + (int64_t)st * A.row_stride + A.pl.x + (int64_t)h * P + p) * mx[p * R + r];
+            sm[L.Xs + idx] = v;
+        }
+        __syncthreads();
+
+        gen_chunk_core(s, L, sm, Hs, nvalid);
+
+        // Gate and MIMO-down (mamba3/mamba3.py:233-238).
+        for (int idx = tid; idx < Qi * P; idx += kGenThreads) {
+            const int t = idx / P, p = idx % P;
+            const int st = s0 + t;
+            if (st < s.T) {
+                const float z = ld_f32(proj + (int64_t)st * A.row_stride + A.pl.z + (int64_t)h * P + p);
+                float out = 0.f;
+                for (int r = 0; r < R; ++r) {
+                    const int i = t * R + r;
+                    const float y = sm[L.Ys + i * P + p] + Dh * sm[L.Xs + i * P + p];
+                    out += md[p * R + r] * y * silu_f(z * mz[p * R + r]);
+                }
+                yo[((int64_t)st * s.H + h) * P + p] = cvt_out<T>(out);
+            }
+        }
+        // prev_BX = B~_{T-1} x_{T-1}^T (mamba3/mamba3.py:247-250).
+        if (A.prev_bx && k == nchunks - 1) {
+            const int tl = nvalid - 1;
+            float* pb = A.prev_bx + ((int64_t)b * s.H + h) * P * N;
+            for (int idx = tid; idx < P * N; idx += kGenThreads) {
+                const int p = idx / N, n = idx % N;
+                float v = 0.f;
+                for (int r = 0; r < R; ++r)
+                    v += sm[L.Bs + (tl * R + r) * N + n] * sm[L.Xs + (tl * R + r) * P + p];
+                pb[idx] = v;
+            }
+        }
+        __syncthreads();
+    }
+    if (A.angle) {
+        for (int i = tid; i < Nh; i += kGenThreads)
+            A.angle[((int64_t)b * s.H + h) * Nh + i] = A.cplx ? sm[L.phi_run + i] : 0.f;
+    }
+}
+
+size_t generic_prefill_workspace(const m3_layer_desc& d) {
+    // Running state when the caller does not want h_final.
+    return (size_t)d.batch * d.nheads * d.headdim * d.d_state * sizeof(float);
+}
+
+int launch_generic_prefill(const m3_layer_desc& d, const m3_layer_params& p, const void* proj,
+                           const float* dt_scale, void* y_out, float* h_final, float* angle,
+                           float* prev_bx, void* workspace, hipStream_t stream) {
+    GenLayerArgs A;
+    A.s.B = d.batch; A.s.T = d.seqlen; A.s.H = d.nheads; A.s.P = d.headdim; A.s.N = d.d_state;
+    A.s.R = d.mimo_rank; A.s.Rb = d.mimo_rank; A.s.G = d.ngroups;
+    A.s.Qi = gen_pick_chunk(A.s.N, A.s.P, A.s.R, A.s.Rb, d.use_complex != 0);
+    if (A.s.Qi == 0) return M3_ERR_UNSUPPORTED;
+    A.L = gen_lds_plan(A.s.Qi, A.s.N, A.s.P, A.s.R, A.s.Rb, d.use_complex != 0);
+    A.pl = proj_layout(d);
+    A.row_stride = d.proj_row_stride;
+    A.trap = d.use_trapezoidal;
+    A.cplx = d.use_complex;
+    A.eps = d.rms_eps;
+    A.prm = p;
+    A.proj = proj;
+    A.dt_scale = dt_scale;
+    A.y_out = y_out;
+    A.state = h_final ? h_final : reinterpret_cast<float*>(workspace);
+    A.angle = angle;
+    A.prev_bx = prev_bx;
+    const size_t lds = (size_t)A.L.total * sizeof(float);
+    const dim3 grid((unsigned)(d.batch * d.nheads));
+    if (d.dtype == M3_DTYPE_BF16)
+        hipLaunchKernelGGL(gen_layer_prefill<bf16>, grid, dim3(kGenThreads), lds, stream, A);
+    else
+        hipLaunchKernelGGL(gen_layer_prefill<float>, grid, dim3(kGenThreads), lds, stream, A);
+    return hipGetLastError() == hipSuccess ? M3_OK : M3_ERR_LAUNCH;
+}
+
+// ---------------------------------------------------------------------------------
+// chunked_ssd on pre-processed inputs (mamba3/ssd.py:118-244).
+// ---------------------------------------------------------------------------------
+struct GenChunkedArgs {
+    GenShape s;
+    GenLds L;
+    const void *x_g, *x_b, *B_g, *B_b, *C, *dt, *x_raw;
+    const float *A, *D, *h_init;
+    void* y;
+    float* state;
+};
+
+template <typename T>
+__global__ __launch_bounds__(kGenThreads) void gen_chunked(GenChunkedArgs A) {
+    extern __shared__ float sm[];
+    const GenShape& s = A.s;
+    const GenLds& L = A.L;
+    const int tid = threadIdx.x;
+    const int b = blockIdx.x / s.H, h = blockIdx.x % s.H;
+    const int Qi = s.Qi, N = s.N, P = s.P, R = s.R, Rb = s.Rb;
+    const bool beta = A.x_b != nullptr;
+    const T* xg = reinterpret_cast<const T*>(A.x_g);
+    const T* xb = reinterpret_cast<const T*>(A.x_b);
+    const T* Bg = reinterpret_cast<const T*>(A.B_g);
+    const T* Bb = reinterpret_cast<const T*>(A.B_b);
+    const T* Cc = reinterpret_cast<const T*>(A.C);
+    const T* dtp = reinterpret_cast<const T*>(A.dt);
+    const T* xr = reinterpret_cast<const T*>(A.x_raw);
+    T* yo = reinterpret_cast<T*>(A.y);
+    float* Hs = A.state + ((int64_t)b * s.H + h) * P * N;
+    const float Ah = A.A[h], Dh = A.D[h];
+
+    const float* hi = A.h_init ? A.h_init + ((int64_t)b * s.H + h) * P * N : nullptr;
+    for (int idx = tid; idx < P * N; idx += kGenThreads) Hs[idx] = hi ? hi[idx] : 0.f;
+    __syncthreads();
+
+    const int nchunks = (s.T + Qi - 1) / Qi;
+    for (int k = 0; k < nchunks; ++k) {
+        const int s0 = k * Qi;
+        const int nvalid = min(Qi, s.T - s0);
+        for (int t = tid; t < Qi; t += kGenThreads) {
+            const int st = s0 + t;
+            sm[L.tok_dt + t] = st < s.T ? ld_f32(dtp + ((int64_t)b * s.T + st) * s.H + h) : 0.f;
+        }
+        // token-major (B,T,H,X,R) element (t, x, r)
+        for (int idx = tid; idx < Qi * R * N; idx += kGenThreads) {
+            const int t = idx / (R * N), r = (idx / N) % R, n = idx % N;
+            const int st = s0 + t;
+            const int64_t off = (((int64_t)b * s.T + st) * s.H + h) * N * R + (int64_t)n * R + r;
+            const bool v = st < s.T;
+            sm[L.Cs + (t * R + r) * N + n] = v ? ld_f32(Cc + off) : 0.f;
+            sm[L.Bs + (t * Rb + r) * N + n] = v ? ld_f32(Bg + off) : 0.f;
+            if (beta) sm[L.Bs + (t * Rb + R + r) * N + n] = v ? ld_f32(Bb + off) : 0.f;
+        }
+        for (int idx = tid; idx < Qi * R * P; idx += kGenThreads) {
+            const int t = idx / (R * P), r = (idx / P) % R, p = idx % P;
+            const int st = s0 + t;
+            const int64_t off = (((int64_t)b * s.T + st) * s.H + h) * P * R + (int64_t)p * R + r;
+            const bool v = st < s.T;
+            sm[L.Xs + (t * Rb + r) * P + p] = v ? ld_f32(xg + off) : 0.f;
+            if (beta) sm[L.Xs + (t * Rb + R + r) * P + p] = v ? ld_f32(xb + off) : 0.f;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            float c = 0.f;
+            for (int t = 0; t < Qi; ++t) {
+                const float dt = sm[L.tok_dt + t];
+                c += Ah * dt;
+                sm[L.c + t] = c;
+                sm[L.a + t] = dt;
+                sm[L.bco + t] = 0.f;
+            }
+        }
+        __syncthreads();
+
+        gen_chunk_core(s, L, sm, Hs, nvalid);
+        __syncthreads();
+
+        for (int idx = tid; idx < Qi * R * P; idx += kGenThreads) {
+            const int t = idx / (R * P), r = (idx / P) % R, p = idx % P;
+            const int st = s0 + t;
+            if (st < s.T) {
+                const int64_t off = (((int64_t)b * s.T + st) * s.H + h) * P * R + (int64_t)p * R + r;
+                const float v = sm[L.Ys + (t * R + r) * P + p] + Dh * ld_f32(xr + off);
+                yo[off] = cvt_out<T>(v);
+            }
+        }
+        __syncthreads();
+    }
+}
+
+int launch_generic_chunked(int B, int T, int H, int P, int N, int R, int dtype,
+                           const void* x_g, const void* x_b, const void* B_g, const void* B_b,
+                           const void* C, const void* dt, const float* A, const float* D,
+                           const void* x_raw, const float* h_init, void* y, float* h_final,
+                           float* state_ws, hipStream_t stream) {
+    GenChunkedArgs a;
+    a.s.B = B; a.s.T = T; a.s.H = H; a.s.P = P; a.s.N = N; a.s.R = R;
+    a.s.Rb = x_b ? 2 * R : R;
+    a.s.G = 1;
+    a.s.Qi = gen_pick_chunk(N, P, R, a.s.Rb, false);
+    if (a.s.Qi == 0) return M3_ERR_UNSUPPORTED;
+    a.L = gen_lds_plan(a.s.Qi, N, P, R, a.s.Rb, false);
+    a.x_g = x_g; a.x_b = x_b; a.B_g = B_g; a.B_b = B_b; a.C = C; a.dt = dt; a.x_raw = x_raw;
+    a.A = A; a.D = D; a.h_init = h_init; a.y = y;
+    a.state = h_final ? h_final : state_ws;
+    const size_t lds = (size_t)a.L.total * sizeof(float);
+    const dim3 grid((unsigned)(B * H));
+    if (dtype == M3_DTYPE_BF16)
+        hipLaunchKernelGGL(gen_chunked<bf16>, grid, dim3(kGenThreads), lds, stream, a);
+    else
+        hipLaunchKernelGGL(gen_chunked<float>, grid, dim3(kGenThreads), lds, stream, a);
+    return hipGetLastError() == hipSuccess ? M3_OK : M3_ERR_LAUNCH;
+}
+
+}  // namespace m3

@@ -1,0 +1,59 @@
+// Host-side launchers of the Mamba-3 kernels. Arguments are validated by the C-ABI
+// layer (m3_api.cpp) before any of these is called.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/mamba3_amd.h"
+
+namespace m3 {
+
+// Column offsets of one in_proj row: [z | x | B | C | dt | lambda | theta].
+struct ProjLayout {
+    int64_t z, x, B, C, dt, lam, theta, width;
+};
+
+inline ProjLayout proj_layout(const m3_layer_desc& d) {
+    ProjLayout L;
+    const int64_t d_inner = (int64_t)d.nheads * d.headdim;
+    const int64_t d_bc = (int64_t)d.ngroups * d.d_state * d.mimo_rank;
+    L.z = 0;
+    L.x = d_inner;
+    L.B = 2 * d_inner;
+    L.C = L.B + d_bc;
+    L.dt = L.C + d_bc;
+    int64_t o = L.dt + d.nheads;
+    L.lam = d.use_trapezoidal ? o : -1;
+    if (d.use_trapezoidal) o += d.nheads;
+    L.theta = d.use_complex ? o : -1;
+    if (d.use_complex) o += d.d_state / 2;
+    L.width = o;
+    return L;
+}
+
+int launch_scan_fwd(const float* decay, const float* h_chunk, const float* h_init,
+                    float* h_states, int64_t B, int64_t K, int64_t H, int64_t PN,
+                    hipStream_t stream);
+
+// Generic (fp32 VALU) fused layer prefill: any supported shape, any dtype.
+size_t generic_prefill_workspace(const m3_layer_desc& d);
+int launch_generic_prefill(const m3_layer_desc& d, const m3_layer_params& p, const void* proj,
+                           const float* dt_scale, void* y_out, float* h_final, float* angle,
+                           float* prev_bx, void* workspace, hipStream_t stream);
+
+int launch_generic_chunked(int B, int T, int H, int P, int N, int R, int dtype,
+                           const void* x_g, const void* x_b, const void* B_g, const void* B_b,
+                           const void* C, const void* dt, const float* A, const float* D,
+                           const void* x_raw, const float* h_init, void* y, float* h_final,
+                           float* state_ws, hipStream_t stream);
+
+// Returns 1 when the step kernel supports (N, R), else 0.
+int step_supported(int N, int R);
+int launch_step(const m3_layer_desc& d, const m3_layer_params& p, const void* proj,
+                const float* dt_scale, const float* h_in, const float* prev_in,
+                const void* angle_in, int angle_dtype, void* y_out, float* h_out,
+                float* prev_out, void* angle_out, hipStream_t stream);
+
+}  // namespace m3

@@ -1,0 +1,104 @@
+"""The C-ABI library: loads, exports every symbol include/mamba3_amd.h declares, and
+rejects bad arguments on the host before any launch (no GPU needed for these paths)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+
+import pytest
+
+from conftest import ROOT
+from mamba3_amd import _native
+
+HEADER = ROOT / "include" / "mamba3_amd.h"
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _native.LIB_PATH.exists():
+        from mamba3_amd import build
+        build.build(verbose=False)
+    return _native.lib()
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(m3_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_binding_list():
+    assert declared_functions() == sorted(_native.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+
+
+def test_status_strings(lib):
+    assert lib.m3_status_string(0) == b"ok"
+    for code in range(1, 8):
+        assert lib.m3_status_string(code) != b"unknown status"
+    assert lib.m3_status_string(99) == b"unknown status"
+    assert lib.m3_version() >= 100
+
+
+def test_scan_rejects_bad_arguments(lib):
+    assert lib.m3_scan_fwd(None, None, None, None, 1, 1, 1, 1, None) == 1
+    fake = 256  # never dereferenced: validation fails before any launch
+    assert lib.m3_scan_fwd(fake, fake, None, fake, 0, 1, 1, 1, None) == 2
+    assert lib.m3_scan_fwd(fake, fake, None, fake, 1, -1, 1, 1, None) == 2
+
+
+def _desc(**kw):
+    d = dict(batch=1, seqlen=4, nheads=8, headdim=16, d_state=16, mimo_rank=2, ngroups=1,
+             use_trapezoidal=1, use_complex=1, dtype=0, proj_row_stride=0, rms_eps=1e-5)
+    d.update(kw)
+    if d["proj_row_stride"] == 0:
+        H, P, N, R, G = d["nheads"], d["headdim"], d["d_state"], d["mimo_rank"], d["ngroups"]
+        d["proj_row_stride"] = (2 * H * P + 2 * G * N * R + H + d["use_trapezoidal"] * H
+                                + d["use_complex"] * (N // 2))
+    return _native.LayerDesc(**d)
+
+
+def test_workspace_query_and_desc_validation(lib):
+    n = ctypes.c_size_t(0)
+    assert lib.m3_prefill_workspace_size(ctypes.byref(_desc()), ctypes.byref(n)) == 0
+    assert n.value == 1 * 8 * 16 * 16 * 4
+    bad = [dict(batch=0), dict(d_state=15), dict(nheads=8, ngroups=3), dict(dtype=7),
+           dict(proj_row_stride=10), dict(use_complex=2), dict(rms_eps=float("nan"))]
+    for kw in bad:
+        st = lib.m3_prefill_workspace_size(ctypes.byref(_desc(**kw)), ctypes.byref(n))
+        assert st in (2, 3), (kw, st)
+    assert lib.m3_prefill_workspace_size(None, ctypes.byref(n)) == 1
+
+
+def test_prefill_and_step_reject_missing_pointers(lib):
+    params = _native.LayerParams()
+    d = _desc()
+    assert lib.m3_prefill_fwd(ctypes.byref(d), ctypes.byref(params), 256, None, 256, None,
+                              None, None, None, 0, None) == 1
+    full = _native.LayerParams(*([256] * 10))
+    # no h_final and no workspace
+    assert lib.m3_prefill_fwd(ctypes.byref(d), ctypes.byref(full), 256, None, 256, None,
+                              None, None, None, 0, None) == 4
+    assert lib.m3_step_fwd(ctypes.byref(d), ctypes.byref(full), 256, None, None, 256, 256, 0,
+                           256, 256, 256, 256, None) == 1
+    # unsupported d_state for the step kernel
+    d12 = _desc(d_state=12)
+    assert lib.m3_step_fwd(ctypes.byref(d12), ctypes.byref(full), 256, None, 256, 512, 256, 0,
+                           256, 768, 1024, 256, None) == 3
+    # aliasing in/out state is refused
+    assert lib.m3_step_fwd(ctypes.byref(d), ctypes.byref(full), 256, None, 256, 512, 256, 0,
+                           256, 256, 1024, 256, None) == 2
+
+
+def test_chunked_rejects_bad_arguments(lib):
+    assert lib.m3_chunked_ssd_fwd(1, 4, 2, 4, 8, 2, 0, 256, 256, 256, None, 256, 256, 256, 256,
+                                  256, None, 256, 256, None, None) == 1
+    assert lib.m3_chunked_ssd_fwd(1, 0, 2, 4, 8, 2, 0, 256, None, 256, None, 256, 256, 256, 256,
+                                  256, None, 256, 256, None, None) == 2
+    assert lib.m3_chunked_ssd_fwd(1, 4, 2, 4, 8, 2, 5, 256, None, 256, None, 256, 256, 256, 256,
+                                  256, None, 256, 256, None, None) == 3

@@ -1,0 +1,348 @@
+"""GPU parity of the HIP path against the oracle and the reference's golden vectors.
+
+Tolerances (normwise max-relative error, max|y - y_ref| / max|y_ref|):
+  * fp32 kernels vs fp32 reference/oracle: 1e-4
+  * bf16 kernels vs fp32 oracle on the bf16-rounded weights and inputs: 2e-2
+Every test calls the kernels through the C-ABI library (mamba3_amd/lib).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import mamba3_amd
+from conftest import (CHUNKED_CASES, LAYER_CASES, golden_config, golden_params, load_golden,
+                      max_rel, oracle_cfg)
+from mamba3_amd import _native
+from oracle import recurrence as rec
+from oracle import reference_path as ref
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = 1e-4
+BF16_TOL = 2e-2
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _native_loaded(cuda_device):
+    lib = _native.lib()  # raises if the library is missing
+    assert lib.m3_version() >= 100
+    torch.backends.cuda.matmul.allow_tf32 = False
+    torch.backends.cudnn.allow_tf32 = False
+
+
+def _layer_from_golden(g, dev, dtype=torch.float32):
+    kw = golden_config(g)
+    torch.manual_seed(0)
+    layer = mamba3_amd.KulaMamba(**kw)
+    layer.load_state_dict(golden_params(g))
+    return layer.to(dev, dtype).eval(), kw
+
+
+# ------------------------------------------------------------------ golden, fp32
+@pytest.mark.parametrize("name", LAYER_CASES)
+def test_forward_prefill_step_match_reference_golden(name, cuda_device):
+    g = load_golden(name)
+    layer, _ = _layer_from_golden(g, cuda_device)
+    x = torch.from_numpy(g["x"]).to(cuda_device)
+    with torch.no_grad():
+        y = layer(x)
+        assert max_rel(y, torch.from_numpy(g["y"])) < FP32_TOL
+        y_pf, st = layer.prefill(x)
+        assert max_rel(y_pf, torch.from_numpy(g["y_prefill"])) < FP32_TOL
+        for k in ("h", "angle", "prev_BX"):
+            assert max_rel(st[k], torch.from_numpy(g[f"prefill/{k}"])) < FP32_TOL, k
+        xs = torch.from_numpy(g["x_steps"]).to(cuda_device)
+        outs = []
+        for t in range(xs.shape[1]):
+            if t % 2 == 0:
+                o, st = layer.step(xs[:, t], st)
+            else:
+                o, st = layer.step(xs[:, t:t + 1], st)
+                assert o.dim() == 3
+                o = o.squeeze(1)
+            outs.append(o)
+        assert max_rel(torch.stack(outs, 1), torch.from_numpy(g["y_steps"])) < FP32_TOL
+        for k in ("h", "angle", "prev_BX"):
+            assert max_rel(st[k], torch.from_numpy(g[f"steps/{k}"])) < FP32_TOL, k
+
+
+def test_dt_scale_matches_reference_golden(cuda_device):
+    g = load_golden("layer_tiny_dtscale")
+    layer, _ = _layer_from_golden(g, cuda_device)
+    x = torch.from_numpy(g["x"]).to(cuda_device)
+    ds = torch.from_numpy(g["dt_scale"]).to(cuda_device)
+    with torch.no_grad():
+        y = layer(x, dt_scale=ds)
+        y1 = layer(x)
+    assert max_rel(y, torch.from_numpy(g["y"])) < FP32_TOL
+    assert not torch.allclose(y, y1, atol=1e-5)
+
+
+@pytest.mark.parametrize("name", CHUNKED_CASES)
+def test_chunked_ssd_matches_reference_golden(name, cuda_device):
+    g = load_golden(name)
+    t = {k: torch.from_numpy(v).to(cuda_device) for k, v in g.items() if v.dtype != np.int64}
+    res = mamba3_amd.chunked_ssd(t["x_g"], t.get("x_b"), t["B_g"], t.get("B_b"), t["C"],
+                                 t["dt"], t["A"], t["D"], t["x_raw"], int(g["chunk_size"]),
+                                 h_init=t.get("h_init"), return_final_state=True)
+    assert max_rel(res.y, torch.from_numpy(g["y"])) < FP32_TOL
+    assert max_rel(res.h_final, torch.from_numpy(g["h_final"])) < FP32_TOL
+
+
+def test_chunked_ssd_h_init_zero_equals_none(cuda_device):
+    """Reference test_ssd_h_init (tests/test_mamba3.py:670-695)."""
+    g = load_golden("chunked_beta_hinit")
+    t = {k: torch.from_numpy(v).to(cuda_device) for k, v in g.items() if v.dtype != np.int64}
+    args = (t["x_g"], t["x_b"], t["B_g"], t["B_b"], t["C"], t["dt"], t["A"], t["D"], t["x_raw"])
+    out0 = mamba3_amd.chunked_ssd(*args, 8, return_final_state=True)
+    out1 = mamba3_amd.chunked_ssd(*args, 8, h_init=torch.zeros_like(t["h_init"]),
+                                  return_final_state=True)
+    out2 = mamba3_amd.chunked_ssd(*args, 8, h_init=t["h_init"], return_final_state=True)
+    assert (out0.y - out1.y).abs().max().item() < 1e-6
+    assert (out0.y - out2.y).abs().max().item() > 1e-3
+
+
+def test_d768_fp32_forward_matches_reference_golden(cuda_device):
+    """d_model=768, N=128, P=64, R=2 layer, seed-0 weights, x (4,1024,768) from seed 1."""
+    g = load_golden("layer_d768")
+    torch.manual_seed(0)
+    layer = mamba3_amd.KulaMamba(768, d_state=128, expand=2, headdim=64, mimo_rank=2)
+    layer = layer.to(cuda_device).eval()
+    torch.manual_seed(1)
+    x = torch.randn(4, 1024, 768)
+    assert float(x.double().sum()) == pytest.approx(float(g["x_sum"]), rel=1e-12)
+    with torch.no_grad():
+        y, st = layer.prefill(x.to(cuda_device))
+    ys = torch.from_numpy(g["y_slice"])
+    assert max_rel(y[:, ::64, ::16], ys) < FP32_TOL
+    assert float(y.double().sum()) == pytest.approx(float(g["y_sum"]), rel=1e-3, abs=1e-2)
+    assert max_rel(st["h"][:, :, ::8, ::16], torch.from_numpy(g["h_slice"])) < FP32_TOL
+    assert max_rel(st["angle"][:, :, ::8], torch.from_numpy(g["angle_slice"])) < FP32_TOL
+    assert max_rel(st["prev_BX"][:, :, ::8, ::16], torch.from_numpy(g["prev_slice"])) < FP32_TOL
+
+
+def test_tiny_lm_logits_and_greedy_generation_match_reference(cuda_device):
+    g = load_golden("lm_tiny")
+    torch.manual_seed(0)
+    lm = mamba3_amd.KulaMambaLM(vocab_size=256, d_model=64, n_layers=2, d_state=16, headdim=16,
+                                mimo_rank=2, chunk_size=8)
+    lm.load_state_dict(golden_params(g))
+    lm = lm.to(cuda_device).eval()
+    ids = torch.from_numpy(g["ids"]).to(cuda_device)
+    with torch.no_grad():
+        logits = lm(ids)["logits"]
+        gen = lm.generate(ids[:, :5], max_new_tokens=6, temperature=0)
+    assert max_rel(logits, torch.from_numpy(g["logits"])) < FP32_TOL
+    assert torch.equal(gen.cpu(), torch.from_numpy(g["generated"]))
+
+
+# ------------------------------------------------------------------ scan
+@pytest.mark.parametrize("shape", [(2, 4, 3, 8), (2, 7, 3, 10), (1, 33, 2, 32768), (8, 16, 24, 8192)])
+@pytest.mark.parametrize("with_init", [True, False])
+def test_scan_matches_closed_form(shape, with_init, cuda_device):
+    B, K, H, PN = shape
+    g = torch.Generator().manual_seed(K * 31 + PN)
+    d = torch.rand(B, K, H, generator=g) * 0.9 + 0.05
+    hc = torch.randn(B, K, H, PN, generator=g)
+    h0 = torch.randn(B, H, PN, generator=g) if with_init else None
+    out = mamba3_amd.ssd_scan(d.to(cuda_device), hc.to(cuda_device),
+                              None if h0 is None else h0.to(cuda_device))
+    if B * K * H * PN <= 1 << 20:
+        expect = torch.from_numpy(rec.scan_closed_form(d.numpy(), hc.numpy(),
+                                                       None if h0 is None else h0.numpy()))
+    else:
+        expect = ref.scan_forward(d, hc, h0)
+    assert max_rel(out, expect) < 1e-5
+
+
+def test_scan_bf16_roundtrip_dtype(cuda_device):
+    d = torch.rand(1, 5, 2, device=cuda_device)
+    hc = torch.randn(1, 5, 2, 4, 6, device=cuda_device, dtype=torch.bfloat16)
+    out = mamba3_amd.ssd_scan(d, hc)
+    assert out.dtype == torch.bfloat16 and out.shape == hc.shape
+    expect = ref.scan_forward(d.cpu(), hc.float().cpu().reshape(1, 5, 2, 24)).reshape(hc.shape)
+    assert max_rel(out.float(), expect) < 1e-2
+
+
+# ------------------------------------------------------------------ reference invariants
+def _tiny(dev, **kw):
+    d = dict(d_model=64, d_state=16, headdim=16, mimo_rank=2, expand=2, chunk_size=8)
+    d.update(kw)
+    torch.manual_seed(0)
+    return mamba3_amd.KulaMamba(**d).to(dev).eval()
+
+
+def _steps(layer, x):
+    st = layer.allocate_inference_state(x.shape[0], device=x.device)
+    outs = []
+    for t in range(x.shape[1]):
+        o, st = layer.step(x[:, t:t + 1], st)
+        outs.append(o.squeeze(1))
+    return torch.stack(outs, 1), st
+
+
+@pytest.mark.parametrize("kw,T,tol", [
+    ({}, 24, 1e-4), (dict(ngroups=2), 16, 1e-4), (dict(use_trapezoidal=False), 16, 1e-4),
+    (dict(use_complex_ssm=False), 16, 1e-4),
+    (dict(use_trapezoidal=False, use_complex_ssm=False, mimo_rank=1), 16, 1e-4),
+    ({}, 512, 1e-3), ({}, 1, 1e-4)])
+def test_forward_equals_sequential_steps(kw, T, tol, cuda_device):
+    """Reference tests 35-52, 182-258, 355-374, 698-764: parallel == recurrent."""
+    layer = _tiny(cuda_device, **kw)
+    torch.manual_seed(1)
+    x = torch.randn(1 if T > 1 else 2, T, 64, device=cuda_device)
+    with torch.no_grad():
+        y_par = layer(x)
+        y_seq, st = _steps(layer, x)
+        _, st_pf = layer.prefill(x)
+    assert (y_par - y_seq).abs().max().item() < tol
+    for k in ("h", "angle", "prev_BX"):
+        assert (st[k] - st_pf[k]).abs().max().item() < tol, k
+
+
+def test_prefill_then_step_equals_all_steps(cuda_device):
+    layer = _tiny(cuda_device)
+    torch.manual_seed(2)
+    x = torch.randn(1, 24, 64, device=cuda_device)
+    with torch.no_grad():
+        y_gt, _ = _steps(layer, x)
+        _, st = layer.prefill(x[:, :16])
+        outs = []
+        for t in range(16, 24):
+            o, st = layer.step(x[:, t], st)
+            outs.append(o)
+    assert (torch.stack(outs, 1) - y_gt[:, 16:]).abs().max().item() < 1e-4
+
+
+def test_extreme_decay(cuda_device):
+    """Reference tests 410-447: A_log=0, dt_bias=3 finite; A_log=-0.5, dt_bias=2 within 5e-3."""
+    layer = _tiny(cuda_device)
+    with torch.no_grad():
+        layer.A_log.fill_(0.0)
+        layer.dt_bias.fill_(3.0)
+        y = layer(torch.randn(1, 64, 64, device=cuda_device))
+    assert torch.isfinite(y).all() and y.abs().max() > 0
+    layer = _tiny(cuda_device)
+    with torch.no_grad():
+        layer.A_log.fill_(-0.5)
+        layer.dt_bias.fill_(2.0)
+        x = torch.randn(1, 24, 64, device=cuda_device)
+        y_par = layer(x)
+        y_seq, _ = _steps(layer, x)
+    assert (y_par - y_seq).abs().max().item() < 5e-3
+
+
+def test_mimo_cross_rank(cuda_device):
+    layer = _tiny(cuda_device)
+    x = torch.randn(1, 16, 64, device=cuda_device)
+    with torch.no_grad():
+        y_full = layer(x)
+        layer.mimo_x.data[:, :, 1] = 0.0
+        y_zero = layer(x)
+    assert (y_full - y_zero).abs().max().item() > 1e-5
+
+
+def test_backward_raises_instead_of_wrong_gradients(cuda_device):
+    layer = _tiny(cuda_device).train()
+    y = layer(torch.randn(1, 8, 64, device=cuda_device))
+    with pytest.raises(NotImplementedError):
+        y.sum().backward()
+
+
+# ------------------------------------------------------------------ bf16 vs fp32 oracle
+def _bf16_pair(kw, dev, seed=0):
+    torch.manual_seed(seed)
+    layer = mamba3_amd.KulaMamba(**kw).to(dev, torch.bfloat16).eval()
+    params = {k: v.detach().float().cpu() for k, v in layer.state_dict().items()}
+    return layer, oracle_cfg(kw), params
+
+
+@pytest.mark.parametrize("kw,shape", [
+    (dict(d_model=64, d_state=16, headdim=16, mimo_rank=2, chunk_size=8), (2, 37, 64)),
+    (dict(d_model=768, d_state=128, headdim=64, mimo_rank=2), (1, 1024, 768)),
+    (dict(d_model=768, d_state=128, headdim=64, mimo_rank=2), (2, 333, 768)),
+])
+def test_bf16_prefill_matches_fp32_oracle(kw, shape, cuda_device):
+    layer, cfg, p = _bf16_pair(kw, cuda_device)
+    torch.manual_seed(2)
+    x = torch.randn(*shape).to(torch.bfloat16)
+    with torch.no_grad():
+        y, st = layer.prefill(x.to(cuda_device))
+        y_ref, st_ref = ref.layer_forward(cfg, p, x.float(), return_state=True)
+    assert max_rel(y.float(), y_ref) < BF16_TOL
+    for k in ("h", "prev_BX", "angle"):
+        assert max_rel(st[k], st_ref[k]) < BF16_TOL, k
+
+
+def test_bf16_step_matches_fp32_oracle(cuda_device):
+    """B=64 decode steps from a random state on the d768 layer, bf16 vs fp32."""
+    kw = dict(d_model=768, d_state=128, headdim=64, mimo_rank=2)
+    layer, cfg, p = _bf16_pair(kw, cuda_device)
+    g = torch.Generator().manual_seed(4)
+    B, H, P, N = 64, layer.nheads, 64, 128
+    st = {"h": torch.randn(B, H, P, N, generator=g) * 0.5,
+          "prev_BX": torch.randn(B, H, P, N, generator=g) * 0.5,
+          "angle": torch.randn(B, H, N // 2, generator=g) * 3}
+    st_dev = {k: v.to(cuda_device) for k, v in st.items()}
+    for i in range(4):
+        x = torch.randn(B, 768, generator=g).to(torch.bfloat16)
+        with torch.no_grad():
+            y, st_dev = layer.step(x.to(cuda_device), st_dev)
+            y_ref, st = ref.layer_step(cfg, p, x.float(), st)
+        assert max_rel(y.float(), y_ref) < BF16_TOL
+        for k in ("h", "prev_BX", "angle"):
+            assert max_rel(st_dev[k], st[k]) < BF16_TOL, (i, k)
+
+
+def test_fp32_step_matches_oracle_from_random_state(cuda_device):
+    kw = dict(d_model=768, d_state=128, headdim=64, mimo_rank=2)
+    torch.manual_seed(0)
+    layer = mamba3_amd.KulaMamba(**kw).to(cuda_device).eval()
+    cfg = oracle_cfg(kw)
+    p = {k: v.detach().cpu() for k, v in layer.state_dict().items()}
+    g = torch.Generator().manual_seed(5)
+    B, H, P, N = 16, layer.nheads, 64, 128
+    st = {"h": torch.randn(B, H, P, N, generator=g), "prev_BX": torch.randn(B, H, P, N, generator=g),
+          "angle": torch.randn(B, H, N // 2, generator=g)}
+    x = torch.randn(B, 768, generator=g)
+    with torch.no_grad():
+        y, st2 = layer.step(x.to(cuda_device), {k: v.to(cuda_device) for k, v in st.items()})
+        y_ref, st_ref = ref.layer_step(cfg, p, x, st)
+    assert max_rel(y, y_ref) < FP32_TOL
+    for k in ("h", "prev_BX", "angle"):
+        assert max_rel(st2[k], st_ref[k]) < FP32_TOL, k
+
+
+# ------------------------------------------------------------------ full-size properties
+def test_bf16_d768_long_prefill_properties(cuda_device):
+    """x (8, 8192, 768) bf16 (the long-prefill workload): batch independence and causality
+    of the kernel (bit-exact on the same in_proj output), and the prefill -> step
+    hand-off through the full layer."""
+    kw = dict(d_model=768, d_state=128, headdim=64, mimo_rank=2)
+    torch.manual_seed(0)
+    layer = mamba3_amd.KulaMamba(**kw).to(cuda_device, torch.bfloat16).eval()
+    torch.manual_seed(2)
+    x = torch.randn(8, 8192, 768, device=cuda_device).to(torch.bfloat16)
+    with torch.no_grad():
+        proj = layer.in_proj(x)
+        y, st = layer.ssd_from_proj(proj, return_state=True)
+        assert torch.isfinite(y.float()).all() and torch.isfinite(st["h"]).all()
+        y3, st3 = layer.ssd_from_proj(proj[3:4].contiguous(), return_state=True)
+        assert torch.equal(y3, y[3:4])
+        assert torch.equal(st3["h"], st["h"][3:4])
+        yp, _ = layer.ssd_from_proj(proj[:2, :3000].contiguous())
+        assert torch.equal(yp, y[:2, :3000])
+        # hand-off: prefill 8176 tokens then 16 steps == prefill of all 8192
+        _, sp = layer.prefill(x[:2, :8176])
+        outs = []
+        for t in range(8176, 8192):
+            o, sp = layer.step(x[:2, t], sp)
+            outs.append(o)
+        y_full = layer.out_proj(y[:2, 8176:])
+    ys = torch.stack(outs, 1).float()
+    assert max_rel(ys, y_full.float()) < BF16_TOL
+    assert max_rel(sp["h"], st["h"][:2]) < BF16_TOL
