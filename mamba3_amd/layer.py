@@ -209,175 +209,6 @@ class KulaMamba(nn.Module):
             state = {"h": h_final, "angle": angle, "prev_BX": prev_bx}
         return y, state
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
-        scale = torch.rsqrt(x.float().square().mean(self.dim, keepdim=True) + self.eps)
-        shape = [1] * x.ndim
-        shape[self.dim] = -1
-        return x * scale.to(x.dtype) * self.weight.view(*shape)
-
-
-class _ForwardOnly(torch.autograd.Function):
-    """Ties a kernel output to its input so that backward raises instead of silently
-    producing wrong gradients (backward kernels are not part of this build)."""
-
-    @staticmethod
-    def forward(ctx, anchor, out):
-        return out
-
-    @staticmethod
-    def backward(ctx, grad):
-        raise NotImplementedError(
-            "mamba3_amd implements the Mamba-3 forward path only (prefill, forward, step); "
-            "its HIP kernels have no backward")
-
-
-class KulaMamba(nn.Module):
-    """Mamba-3 SSD layer (mamba3/mamba3.py:48-332) on MI355X HIP kernels."""
-
-    def __init__(
-        self,
-        d_model: int,
-        d_state: int = 128,
-        expand: int = 2,
-        headdim: int = 64,
-        ngroups: int | None = None,
-        mimo_rank: int = 2,
-        chunk_size: int = 64,
-        bias: bool = False,
-        dt_min: float = 0.001,
-        dt_max: float = 0.1,
-        use_trapezoidal: bool = True,
-        use_complex_ssm: bool = True,
-    ):
-        super().__init__()
-        self.d_model = d_model
-        self.d_state = d_state
-        self.expand = expand
-        self.headdim = headdim
-        self.mimo_rank = max(mimo_rank, 1)
-        # The kernels pick their own internal chunking; chunk_size is kept for API
-        # compatibility (results do not depend on it beyond rounding).
-        self.chunk_size = chunk_size
-        self.use_trapezoidal = use_trapezoidal
-        self.use_complex_ssm = use_complex_ssm
-
-        self.d_inner = expand * d_model
-        if self.d_inner % headdim != 0:
-            raise ValueError(f"d_inner={self.d_inner} is not a multiple of headdim={headdim}")
-        self.nheads = self.d_inner // headdim
-        if d_state % 2 != 0:
-            raise ValueError("d_state must be even (RoPE acts on pairs)")
-        self.ngroups = 1 if ngroups is None else ngroups
-        if self.nheads % self.ngroups != 0:
-            raise ValueError(f"nheads={self.nheads} is not a multiple of ngroups={self.ngroups}")
-        self.heads_per_group = self.nheads // self.ngroups
-
-        H, P, N, R, G = self.nheads, headdim, d_state, self.mimo_rank, self.ngroups
-        self._d_bc = G * N * R
-        self._d_x = self.d_inner
-        width = 2 * self.d_inner + 2 * self._d_bc + H
-        width += H if use_trapezoidal else 0
-        width += N // 2 if use_complex_ssm else 0
-        self.in_proj = nn.Linear(d_model, width, bias=bias)
-
-        self.A_log = nn.Parameter(torch.zeros(H))
-        self.D = nn.Parameter(torch.ones(H))
-        self.dt_bias = nn.Parameter(torch.zeros(H))
-        self.B_norm = RMSNorm(N * R)
-        self.C_norm = RMSNorm(N * R)
-        self.B_bias = nn.Parameter(torch.ones(G, N, R))
-        self.C_bias = nn.Parameter(torch.ones(G, N, R))
-        self.mimo_x = nn.Parameter(torch.ones(H, P, R))
-        self.mimo_z = nn.Parameter(torch.ones(H, P, R))
-        self.mimo_down = nn.Parameter(torch.full((H, P, R), 1.0 / R))
-        self.out_proj = nn.Linear(self.d_inner, d_model, bias=bias)
-        self._init_weights(dt_min, dt_max)
-        self._pack_key = None
-        self._pack = None
-
-    def _init_weights(self, dt_min: float, dt_max: float) -> None:
-        """Reference initialisation (mamba3/mamba3.py:114-123): kaiming in_proj, dt_bias
-        as the inverse softplus of a log-uniform dt in [dt_min, dt_max], A_log ~ U(-4,-1)."""
-        nn.init.kaiming_uniform_(self.in_proj.weight, a=math.sqrt(5))
-        with torch.no_grad():
-            lo, hi = math.log(dt_min), math.log(dt_max)
-            dt = torch.exp(torch.rand(self.nheads) * (hi - lo) + lo)
-            self.dt_bias.copy_(dt + torch.log(-torch.expm1(-dt)))
-            nn.init.uniform_(self.A_log, -4.0, -1.0)
-
-    # ------------------------------------------------------------------ native glue
-    def _small_params(self):
-        return (self.A_log, self.D, self.dt_bias, self.B_norm.weight, self.C_norm.weight,
-                self.B_bias, self.C_bias, self.mimo_x, self.mimo_z, self.mimo_down)
-
-    def _param_pack(self) -> _native.LayerParams:
-        """fp32 contiguous copies of the small parameters, rebuilt when any changes."""
-        tensors = self._small_params()
-        key = tuple((t.data_ptr(), t._version, t.dtype, t.device) for t in tensors)
-        if key != self._pack_key:
-            with torch.no_grad():
-                f32 = [t.detach().float().contiguous() for t in tensors]
-            pack = _native.LayerParams(*[t.data_ptr() for t in f32])
-            self._pack = (pack, f32)
-            self._pack_key = key
-        return self._pack[0]
-
-    def _desc(self, batch: int, seqlen: int, proj: torch.Tensor) -> _native.LayerDesc:
-        return _native.LayerDesc(
-            batch=batch, seqlen=seqlen, nheads=self.nheads, headdim=self.headdim,
-            d_state=self.d_state, mimo_rank=self.mimo_rank, ngroups=self.ngroups,
-            use_trapezoidal=int(self.use_trapezoidal), use_complex=int(self.use_complex_ssm),
-            dtype=_native.dtype_code(proj.dtype), proj_row_stride=proj.stride(-2),
-            rms_eps=float(self.B_norm.eps))
-
-    def _check_norm_eps(self) -> None:
-        if self.B_norm.eps != self.C_norm.eps:
-            raise ValueError("B_norm and C_norm must share eps")
-
-    @staticmethod
-    def _dt_scale(dt_scale, shape, device):
-        if dt_scale is None:
-            return None
-        if not torch.is_tensor(dt_scale):
-            dt_scale = torch.tensor(float(dt_scale), device=device)
-        return dt_scale.to(device=device, dtype=torch.float32).expand(shape).contiguous()
-
-    # ------------------------------------------------------------------ forward paths
-    def _forward_impl(self, x: torch.Tensor, dt_scale=None, return_state: bool = False):
-        if x.dim() != 3:
-            raise ValueError(f"expected (batch, seqlen, d_model), got {tuple(x.shape)}")
-        Bat, T, _ = x.shape
-        if T <= 0:
-            raise ValueError(f"Sequence length must be positive, got {T}")
-        _native.require_gpu(x)
-        self._check_norm_eps()
-        H, P, N = self.nheads, self.headdim, self.d_state
-
-        proj = self.in_proj(x).contiguous()
-        desc = self._desc(Bat, T, proj)
-        params = self._param_pack()
-        scale = self._dt_scale(dt_scale, (Bat, T, H), x.device)
-
-        dev = x.device
-        y = torch.empty(Bat, T, self.d_inner, device=dev, dtype=proj.dtype)
-        h_final = angle = prev_bx = None
-        if return_state:
-            h_final = torch.empty(Bat, H, P, N, device=dev, dtype=torch.float32)
-            angle = torch.empty(Bat, H, N // 2, device=dev, dtype=torch.float32)
-            prev_bx = torch.empty(Bat, H, P, N, device=dev, dtype=torch.float32)
-        ws_bytes = _native.prefill_workspace_bytes(desc)
-        workspace = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
-        _native.prefill_fwd(desc, params, proj, scale, y, h_final, angle, prev_bx, workspace,
-                            ws_bytes)
-        if torch.is_grad_enabled() and (proj.requires_grad or
-                                        any(p.requires_grad for p in self._small_params())):
-            y = _ForwardOnly.apply(proj, y)
-        output = self.out_proj(y)
-        state = None
-        if return_state:
-            state = {"h": h_final, "angle": angle, "prev_BX": prev_bx}
-        return output, state
-
     def forward(self, x: torch.Tensor, dt_scale=None) -> torch.Tensor:
         output, _ = self._forward_impl(x, dt_scale, return_state=False)
         return output
