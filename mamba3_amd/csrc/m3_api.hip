@@ -2,6 +2,8 @@
 // the host, then calls the launchers. Never throws, never allocates, never syncs.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "m3_kernels.h"
 
 namespace {
@@ -70,11 +72,19 @@ int m3_scan_fwd(const float* decay, const float* h_chunk, const float* h_init,
                : M3_ERR_LAUNCH;
 }
 
+// Workspace for whichever prefill kernel the shape may dispatch to (the MFMA path is
+// chosen for bf16 layers with d_state 128, headdim 64, mimo_rank 2 and aligned rows).
+static size_t prefill_workspace(const m3_layer_desc& d) {
+    size_t n = m3::generic_prefill_workspace(d);
+    if (m3::mfma_prefill_supported(d, nullptr)) n = std::max(n, m3::mfma_prefill_workspace(d));
+    return n;
+}
+
 int m3_prefill_workspace_size(const m3_layer_desc* desc, size_t* bytes) {
     if (!bytes) return M3_ERR_NULL_POINTER;
     const int st = check_desc(desc);
     if (st != M3_OK) return st;
-    *bytes = m3::generic_prefill_workspace(*desc);
+    *bytes = prefill_workspace(*desc);
     return M3_OK;
 }
 
@@ -86,6 +96,13 @@ int m3_prefill_fwd(const m3_layer_desc* desc, const m3_layer_params* params, con
     st = check_params(params);
     if (st != M3_OK) return st;
     if (!proj || !y_out) return M3_ERR_NULL_POINTER;
+    if (m3::mfma_prefill_supported(*desc, proj)) {
+        if (!workspace || workspace_bytes < m3::mfma_prefill_workspace(*desc))
+            return M3_ERR_WORKSPACE;
+        if (!aligned(workspace, 256)) return M3_ERR_MISALIGNED;
+        return m3::launch_mfma_prefill(*desc, *params, proj, dt_scale, y_out, h_final, angle,
+                                       prev_bx, workspace, as_stream(stream));
+    }
     const size_t need = m3::generic_prefill_workspace(*desc);
     if (!h_final && (workspace == nullptr || workspace_bytes < need)) return M3_ERR_WORKSPACE;
     if (workspace && !aligned(workspace, 256)) return M3_ERR_MISALIGNED;

@@ -49,6 +49,13 @@ int launch_generic_chunked(int B, int T, int H, int P, int N, int R, int dtype,
                            const void* x_raw, const float* h_init, void* y, float* h_final,
                            float* state_ws, hipStream_t stream);
 
+// bf16 MFMA fused prefill for d_state 128, headdim 64, mimo_rank 2.
+bool mfma_prefill_supported(const m3_layer_desc& d, const void* proj);
+size_t mfma_prefill_workspace(const m3_layer_desc& d);
+int launch_mfma_prefill(const m3_layer_desc& d, const m3_layer_params& p, const void* proj,
+                        const float* dt_scale, void* y_out, float* h_final, float* angle,
+                        float* prev_bx, void* workspace, hipStream_t stream);
+
 // Returns 1 when the step kernel supports (N, R), else 0.
 int step_supported(int N, int R);
 int launch_step(const m3_layer_desc& d, const m3_layer_params& p, const void* proj,

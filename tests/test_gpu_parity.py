@@ -278,6 +278,49 @@ def test_bf16_prefill_matches_fp32_oracle(kw, shape, cuda_device):
         assert max_rel(st[k], st_ref[k]) < BF16_TOL, k
 
 
+@pytest.mark.parametrize("extra", [dict(ngroups=2), dict(use_trapezoidal=False),
+                                   dict(use_complex_ssm=False), dict(ngroups=24)])
+def test_bf16_d768_variants_match_fp32_oracle(extra, cuda_device):
+    """The MFMA prefill kernel (d_state 128, headdim 64, rank 2) across its flags."""
+    kw = dict(d_model=768, d_state=128, headdim=64, mimo_rank=2, **extra)
+    layer, cfg, p = _bf16_pair(kw, cuda_device, seed=3)
+    torch.manual_seed(4)
+    x = torch.randn(2, 300, 768).to(torch.bfloat16)
+    with torch.no_grad():
+        y, st = layer.prefill(x.to(cuda_device))
+        y_ref, st_ref = ref.layer_forward(cfg, p, x.float(), return_state=True)
+    assert max_rel(y.float(), y_ref) < BF16_TOL
+    for k in ("h", "prev_BX", "angle"):
+        assert max_rel(st[k], st_ref[k]) < BF16_TOL, k
+
+
+def test_bf16_d768_dt_scale_matches_fp32_oracle(cuda_device):
+    kw = dict(d_model=768, d_state=128, headdim=64, mimo_rank=2)
+    layer, cfg, p = _bf16_pair(kw, cuda_device, seed=5)
+    torch.manual_seed(6)
+    x = torch.randn(1, 200, 768).to(torch.bfloat16)
+    ds = torch.rand(1, 200, layer.nheads) * 1.5 + 0.5
+    with torch.no_grad():
+        y = layer(x.to(cuda_device), dt_scale=ds.to(cuda_device))
+        y_ref, _ = ref.layer_forward(cfg, p, x.float(), dt_scale=ds)
+    assert max_rel(y.float(), y_ref) < BF16_TOL
+
+
+@pytest.mark.parametrize("T", [1, 63, 64, 65, 4096])
+def test_bf16_d768_lengths_match_fp32_oracle(T, cuda_device):
+    """Single token, chunk edges, and a long sequence split into many segments."""
+    kw = dict(d_model=768, d_state=128, headdim=64, mimo_rank=2)
+    layer, cfg, p = _bf16_pair(kw, cuda_device, seed=7)
+    torch.manual_seed(T)
+    x = torch.randn(1, T, 768).to(torch.bfloat16)
+    with torch.no_grad():
+        y, st = layer.prefill(x.to(cuda_device))
+        y_ref, st_ref = ref.layer_forward(cfg, p, x.float(), return_state=True)
+    assert max_rel(y.float(), y_ref) < BF16_TOL
+    for k in ("h", "prev_BX", "angle"):
+        assert max_rel(st[k], st_ref[k]) < BF16_TOL, k
+
+
 def test_bf16_step_matches_fp32_oracle(cuda_device):
     """B=64 decode steps from a random state on the d768 layer, bf16 vs fp32."""
     kw = dict(d_model=768, d_state=128, headdim=64, mimo_rank=2)
@@ -320,8 +363,12 @@ def test_fp32_step_matches_oracle_from_random_state(cuda_device):
 # ------------------------------------------------------------------ full-size properties
 def test_bf16_d768_long_prefill_properties(cuda_device):
     """x (8, 8192, 768) bf16 (the long-prefill workload): batch independence and causality
-    of the kernel (bit-exact on the same in_proj output), and the prefill -> step
-    hand-off through the full layer."""
+    of the kernel on the same in_proj output, and the prefill -> step hand-off through
+    the full layer. The kernel splits each sequence into a number of segments that
+    depends on batch*heads, so a sub-batch is evaluated in a different order and may
+    round the bf16 output differently by one ulp (2^-7 of the largest |y| = 7.8e-3), and
+    its RoPE angles are taken relative to different segment starts, so B~ and C~ round
+    differently in bf16: the comparison allows 1e-2."""
     kw = dict(d_model=768, d_state=128, headdim=64, mimo_rank=2)
     torch.manual_seed(0)
     layer = mamba3_amd.KulaMamba(**kw).to(cuda_device, torch.bfloat16).eval()
@@ -332,10 +379,11 @@ def test_bf16_d768_long_prefill_properties(cuda_device):
         y, st = layer.ssd_from_proj(proj, return_state=True)
         assert torch.isfinite(y.float()).all() and torch.isfinite(st["h"]).all()
         y3, st3 = layer.ssd_from_proj(proj[3:4].contiguous(), return_state=True)
-        assert torch.equal(y3, y[3:4])
-        assert torch.equal(st3["h"], st["h"][3:4])
+        e1 = max_rel(y3.float(), y[3:4].float())
+        e2 = max_rel(st3["h"], st["h"][3:4])
         yp, _ = layer.ssd_from_proj(proj[:2, :3000].contiguous())
-        assert torch.equal(yp, y[:2, :3000])
+        e3 = max_rel(yp.float(), y[:2, :3000].float())
+        assert e1 < 1e-2 and e2 < 1e-2 and e3 < 1e-2, (e1, e2, e3)
         # hand-off: prefill 8176 tokens then 16 steps == prefill of all 8192
         _, sp = layer.prefill(x[:2, :8176])
         outs = []
@@ -344,5 +392,5 @@ def test_bf16_d768_long_prefill_properties(cuda_device):
             outs.append(o)
         y_full = layer.out_proj(y[:2, 8176:])
     ys = torch.stack(outs, 1).float()
-    assert max_rel(ys, y_full.float()) < BF16_TOL
-    assert max_rel(sp["h"], st["h"][:2]) < BF16_TOL
+    e4, e5 = max_rel(ys, y_full.float()), max_rel(sp["h"], st["h"][:2])
+    assert e4 < BF16_TOL and e5 < BF16_TOL, (e4, e5)
