@@ -69,20 +69,28 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 
+constexpr int NSLOT = 3;  // token-scalar ring: chunks k, k+1 read while k+2 is written
+
+// Per-chunk token scalars (index = token within the chunk), written by wave 0.
+struct Tok {
+    float c2[Q];   // inclusive prefix of A*dt over the chunk, log2 units
+    float av[Q];   // a_u = lambda_u dt_u
+    float bv[Q];   // b_u = (1 - lambda_{u+1}) dt_{u+1}
+    float ec[Q];   // exp2(c2_u)
+    float hb[Q];   // exp2(c2[8*(u/8)+7] - c2_u) (a_u + b_u): decay to the end of u's 8-block
+    float dtr[Q];  // dt_u / (2 pi): RoPE angle increment per unit theta, in turns
+    float w[Q];    // exp2(c2[63] - c2_u) (a_u + b_u): chunk-state weight
+};
+
 struct __align__(16) Smem {
-    bf16 C[Q * R][N + PAD];    // C~ rows (t,r)
-    bf16 B[Q * R][N + PAD];    // B~ rows (u,r')
-    bf16 Bw[Q][NR + PAD];      // B~ * w_u, [u][n][r'] order
-    bf16 X[P][Q * R + PAD];    // X^T
-    bf16 H[P][N + PAD];        // incoming state, bf16
-    float L[Q][Q + 8];         // Lc; columns Q, Q+1 hold a_u, b_u
-    float c2[Q];               // in-chunk cumulative log2-decay (inclusive)
-    float ec[Q];               // exp(c)
-    float w[Q];                // exp(c_63 - c_u) (a_u + b_u)
-    float dt[Q];
-    float tot[8][NH];          // per 8-token group, per pair: sum of dt*theta
-    float rot[NH];             // per-pair angle scratch (prologue / epilogue)
-    float mzd[P][4];           // mimo_z[p][0..1], mimo_down[p][0..1] of this head
+    bf16 C[Q * R][N + PAD];  // C~ rows (t,r) = 2t+r; 16-byte column chunks swizzled (sw_cb)
+    bf16 B[Q * R][N + PAD];  // B~ rows (u,r'), same swizzle
+    bf16 Bw[Q][NR + PAD];    // B~ * w_u, [u][n][r'] order, swizzled (sw_bw)
+    bf16 X[P][Q * R + PAD];  // X^T
+    bf16 H[P][N + PAD];      // incoming state, bf16
+    Tok tok[NSLOT];
+    float rot[NH];           // per-pair angle scratch (prologue / epilogue)
+    float mzd[P][4];         // per p: -mimo_z[0] log2e, -mimo_z[1] log2e, mimo_down*mimo_z [0], [1]
 };
 
 struct Args {
@@ -103,6 +111,14 @@ struct Args {
     float* angle;
     float* prev_bx;
 };
+
+// Returns v through an empty asm statement the compiler cannot see through or move:
+// values derived from it are recomputed where used instead of being hoisted out of the
+// chunk loop and held in registers across it.
+__device__ __forceinline__ int opaque(int v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
 
 __device__ __forceinline__ f32x4 mfma16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -149,6 +165,21 @@ __device__ __forceinline__ float wave_incl_scan(float v, int lane) {
     }
     return v;
 }
+
+// v_dot2_f32_bf16 with a zero accumulator (the builtin becomes v_dot2c plus a v_mov).
+__device__ __forceinline__ float dot2_bf16(unsigned a, unsigned b) {
+    float d;
+    asm("v_dot2_f32_bf16 %0, %1, %2, 0" : "=v"(d) : "v"(a), "v"(b));
+    return d;
+}
+
+// C~ / B~ tiles: the 16-byte column chunks of a row are XOR-swizzled by the row's
+// 16-row block, so that the preparation's stores (lanes 16 rows apart) hit distinct
+// banks. MFMA operand reads cover 16 rows of one block, so their pattern is unchanged.
+__device__ __forceinline__ int sw_cb(int row, int col) { return col ^ (16 * ((row >> 4) & 3)); }
+// B~w tile: the two 64-byte halves of every 32-pair column group swap on odd 8-token
+// blocks, for the same reason.
+__device__ __forceinline__ int sw_bw(int u, int col) { return col ^ (32 * ((u >> 3) & 1)); }
 
 __device__ __forceinline__ bf16x2 as_bf16x2(unsigned u) { return __builtin_bit_cast(bf16x2, u); }
 
@@ -203,12 +234,205 @@ __global__ __launch_bounds__(256) void bc_norm(const bf16* __restrict__ proj, in
 // ---------------------------------------------------------------------------------
 // 2/3. Segment kernels.
 // ---------------------------------------------------------------------------------
+// Output rows of one 16-row block I of chunk s0 (tokens 8I .. 8I+7, rows (t,r) = 2t+r):
+//   G3  Y  = diag(e^{c_t}) C~ H^T                       (inter-chunk)
+//   G1  S^T = B~ C~^T for the causal column blocks J <= I, kept in registers,
+//       scaled by Lc[t][u] = [u<=t] exp(c_t-c_u) (a_u + [u<t] b_u) (+D on the diagonal)
+//   G2  Y += S X, S fed as the A operand straight from the G1 accumulators (the k order
+//       is permuted consistently in the X operand reads)
+// then the SiLU(z * mimo_z) gate and the MIMO-down sum, stored as bf16.
+// Scheduling fence: keeps the LDS operand reads issued one tile ahead of the MFMAs that
+// consume them (the compiler otherwise sinks each read next to its use and waits on it).
+#define M3_FENCE() __builtin_amdgcn_sched_barrier(0)
+
+template <int I>
+__device__ __forceinline__ void out_block(const Smem& sm, const Tok& tk, const Args& a, const bf16* proj_b,
+                                          int b, int h, int s0, int g16, int l16, float D_h) {
+    const int T = a.T;
+    const int rs = (int)a.rs;
+    const int HP = a.H * P;
+    const int tblk = s0 + 8 * I;
+    const int left = max(T - tblk, 0);
+    const __amdgpu_buffer_rsrc_t rz = make_rsrc(proj_b + (int64_t)tblk * a.rs, (int64_t)left * a.rs * 2);
+    bf16 zraw[4][2];
+#pragma unroll
+    for (int pt = 0; pt < 4; ++pt)
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+            zraw[pt][tt] = ld_bf16(rz, (2 * g16 + tt) * rs + (int)a.pl.z + h * P + 16 * pt + l16);
+
+    constexpr int NJ = I + 1;
+    // Token scalars this lane needs (rows t_col, columns u = 8J + 2 g16 + {0,1}).
+    const int t_col = 8 * I + (l16 >> 1);
+    const int r_col = l16 & 1;
+    const int u0d = 8 * I + 2 * g16;
+    const float ct = tk.c2[t_col];
+    const f32x2 ecv = *reinterpret_cast<const f32x2*>(&tk.ec[u0d]);
+    const f32x2 cud = *reinterpret_cast<const f32x2*>(&tk.c2[u0d]);
+    const f32x2 aud = *reinterpret_cast<const f32x2*>(&tk.av[u0d]);
+    const f32x2 bud = *reinterpret_cast<const f32x2*>(&tk.bv[u0d]);
+    float cref[NJ];
+    f32x2 hv[NJ];
+#pragma unroll
+    for (int J = 0; J < I; ++J) {
+        cref[J] = tk.c2[8 * J + 7];
+        hv[J] = *reinterpret_cast<const f32x2*>(&tk.hb[8 * J + 2 * g16]);
+    }
+
+    // C~ rows of this block (logical column 32s + 8 g16 sits at chunk (4s + g16) ^ 2(I&3))
+    // and the first H operand group.
+    bf16x8 cA[4], hop[2][4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+        cA[s] = *reinterpret_cast<const bf16x8*>(
+            &sm.C[16 * I + l16][8 * (g16 ^ (2 * (I & 1))) + 32 * (s ^ ((I >> 1) & 1))]);
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+        hop[0][s] = *reinterpret_cast<const bf16x8*>(&sm.H[l16][32 * s + 8 * g16]);
+    M3_FENCE();
+    // G3: Y = C~ H^T (scaled by e^{c_t} below)
+    f32x4 yacc[4];
+#pragma unroll
+    for (int pt = 0; pt < 4; ++pt) {
+        if (pt + 1 < 4) {
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+                hop[(pt + 1) & 1][s] = *reinterpret_cast<const bf16x8*>(&sm.H[16 * (pt + 1) + l16][32 * s + 8 * g16]);
+        }
+        M3_FENCE();
+        yacc[pt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) yacc[pt] = mfma16(cA[s], hop[pt & 1][s], yacc[pt]);
+        M3_FENCE();
+    }
+    // G1: S^T = B~ C~^T for J <= I
+    bf16x8 bop[2][4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+        bop[0][s] = *reinterpret_cast<const bf16x8*>(&sm.B[l16][8 * g16 + 32 * s]);
+    M3_FENCE();
+    f32x4 sacc[NJ];
+#pragma unroll
+    for (int J = 0; J < NJ; ++J) {
+        if (J + 1 < NJ) {
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+                bop[(J + 1) & 1][s] = *reinterpret_cast<const bf16x8*>(
+                    &sm.B[16 * (J + 1) + l16][8 * (g16 ^ (2 * ((J + 1) & 1))) + 32 * (s ^ (((J + 1) >> 1) & 1))]);
+        }
+        M3_FENCE();
+        sacc[J] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) sacc[J] = mfma16(bop[J & 1][s], cA[s], sacc[J]);
+        M3_FENCE();
+    }
+#pragma unroll
+    for (int pt = 0; pt < 4; ++pt) {
+        yacc[pt][0] *= ecv[0];
+        yacc[pt][1] *= ecv[0];
+        yacc[pt][2] *= ecv[1];
+        yacc[pt][3] *= ecv[1];
+    }
+    // Mask S^T by Lc (+D on the diagonal) and run G2: Y += S X.
+    // This lane's S^T values: rows (u, r') = (8J + 2 g16 + v/2, v&1), column (t_col, r_col).
+    bf16x4 xop[2][4][2];
+#pragma unroll
+    for (int pt = 0; pt < 4; ++pt) {
+        const bf16* xr = &sm.X[16 * pt + l16][0];
+        xop[0][pt][0] = *reinterpret_cast<const bf16x4*>(xr + 4 * g16);
+        xop[0][pt][1] = *reinterpret_cast<const bf16x4*>(xr + 16 + 4 * g16);
+    }
+    M3_FENCE();
+#pragma unroll
+    for (int s2 = 0; s2 <= I / 2; ++s2) {
+        if (s2 + 1 <= I / 2) {
+#pragma unroll
+            for (int pt = 0; pt < 4; ++pt) {
+                const bf16* xr = &sm.X[16 * pt + l16][32 * (s2 + 1)];
+                xop[(s2 + 1) & 1][pt][0] = *reinterpret_cast<const bf16x4*>(xr + 4 * g16);
+                xop[(s2 + 1) & 1][pt][1] = *reinterpret_cast<const bf16x4*>(xr + 16 + 4 * g16);
+            }
+        }
+        M3_FENCE();
+        bf16x8 aop;
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+            const int J = 2 * s2 + jj;
+            float m0 = 0.f, m1 = 0.f, m2 = 0.f, m3 = 0.f;
+            if (J < I) {
+                // u < t: exp(c_t - c_u)(a_u + b_u), split at the end of u's 8-block so
+                // both factors are at most one.
+                const float gt = __builtin_amdgcn_exp2f(ct - cref[J < I ? J : 0]);
+                const f32x2 hj = hv[J < I ? J : 0];
+                const float l0 = gt * hj[0], l1 = gt * hj[1];
+                const f32x4 sv = sacc[J < NJ ? J : 0];
+                m0 = sv[0] * l0;
+                m1 = sv[1] * l0;
+                m2 = sv[2] * l1;
+                m3 = sv[3] * l1;
+            } else if (J == I) {
+                const float e0 = __builtin_amdgcn_exp2f(ct - cud[0]);
+                const float e1 = __builtin_amdgcn_exp2f(ct - cud[1]);
+                const float l0 = u0d <= t_col ? e0 * (aud[0] + (u0d < t_col ? bud[0] : 0.f)) : 0.f;
+                const float l1 = u0d + 1 <= t_col ? e1 * (aud[1] + (u0d + 1 < t_col ? bud[1] : 0.f)) : 0.f;
+                const f32x4 sv = sacc[J < NJ ? J : 0];
+                m0 = sv[0] * l0;
+                m1 = sv[1] * l0;
+                m2 = sv[2] * l1;
+                m3 = sv[3] * l1;
+                if (u0d == t_col) { if (r_col == 0) m0 += D_h; else m1 += D_h; }
+                if (u0d + 1 == t_col) { if (r_col == 0) m2 += D_h; else m3 += D_h; }
+            }
+            aop[4 * jj + 0] = (bf16)m0;
+            aop[4 * jj + 1] = (bf16)m1;
+            aop[4 * jj + 2] = (bf16)m2;
+            aop[4 * jj + 3] = (bf16)m3;
+        }
+#pragma unroll
+        for (int pt = 0; pt < 4; ++pt) {
+            const bf16x4 lo = xop[s2 & 1][pt][0], hi = xop[s2 & 1][pt][1];
+            const bf16x8 xb = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            yacc[pt] = mfma16(aop, xb, yacc[pt]);
+        }
+        M3_FENCE();
+    }
+
+    // Gate: out = sum_r mimo_down_r y_r silu(z mimo_z_r), with
+    // silu(v0) y0' + silu(v1) y1' = (v0 y0' (1+e1) + v1 y1' (1+e0)) / ((1+e0)(1+e1)),
+    // e_r = exp(-v_r) clamped at 2^60 so the product stays finite.
+    // The store descriptor ends at the last token, so padding rows drop.
+    const __amdgpu_buffer_rsrc_t ry = make_rsrc(a.y_out + ((int64_t)b * T + tblk) * HP, (int64_t)left * HP * 2);
+#pragma unroll
+    for (int pt = 0; pt < 4; ++pt) {
+        const int p = 16 * pt + l16;
+        const f32x4 g = *reinterpret_cast<const f32x4*>(&sm.mzd[p][0]);
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            const float z = (float)zraw[pt][tt];
+            const float e0 = 1.f + __builtin_amdgcn_exp2f(fminf(z * g[0], 60.f));
+            const float e1 = 1.f + __builtin_amdgcn_exp2f(fminf(z * g[1], 60.f));
+            const float num = (z * g[2]) * yacc[pt][2 * tt] * e1 + (z * g[3]) * yacc[pt][2 * tt + 1] * e0;
+            const float out = num * __builtin_amdgcn_rcpf(e0 * e1);
+            __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, (bf16)out), ry,
+                                                  ((2 * g16 + tt) * HP + h * P + p) * 2, 0, 0);
+        }
+    }
+}
+
+// Pipelined chunk walk. Per chunk k:
+//   barrier -> M(k): state update G4 on chunk k's tiles; output block of chunk k;
+//              wave 0: token scalars of chunk k+2; every wave: element-wise preparation
+//              of chunk k+1 into registers (RoPE angles, rotated B~/C~/B~w, X); reads
+//              of chunk k+2 issued
+//   barrier -> W(k+1): registers -> LDS tiles, bf16 copy of the state
+// The RoPE angle prefix over tokens is a scan across the lanes of one wave, so the
+// preparation needs no cross-wave traffic and overlaps the matrix work of the other
+// wave on the same SIMD. Waves w and w+4 (one SIMD) own output blocks w and 7-w.
 template <bool kFull>
 __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
     __shared__ Smem sm;
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
-    const int g16 = lane >> 4, l16 = lane & 15;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
 
     const int nseg = kFull ? a.S : a.S - 1;
     // XCD-aware order: consecutive workgroups of one batch row land on one XCD.
@@ -222,42 +446,32 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
     const int K = (T + Q - 1) / Q;
     const int k_begin = seg * a.cps;
     const int k_end = min(K, k_begin + a.cps);
-    const int HP = a.H * P;
     const int rs = (int)a.rs;
-
     const int bnrs = a.G * NR;  // elements between tokens in Bn / Cn
 
-    const float A_h = -__expf(a.prm.A_log[h]);
+    const float A2 = -__expf(a.prm.A_log[h]) * kLog2e;
     const float D_h = a.prm.D[h];
     const float dtb = a.prm.dt_bias[h];
 
-    // Prep role: pair pi = lane (n = 2pi, 2pi+1), tokens 8*wave .. 8*wave+7.
-    const int pi = lane;
-    const int tq = wave;
-    // X role: column p = lane, tokens 8*wave .. 8*wave+7.
-    const int xp = lane;
-    const float mx0 = a.prm.mimo_x[(h * P + xp) * R], mx1 = a.prm.mimo_x[(h * P + xp) * R + 1];
-    // Output role (waves 0-3): gate constants of columns p, kept in LDS.
+    const int lane0 = tid & 63;
+    const float mx0 = a.prm.mimo_x[(h * P + lane0) * R], mx1 = a.prm.mimo_x[(h * P + lane0) * R + 1];
     if (kFull && tid < P) {
-        sm.mzd[tid][0] = a.prm.mimo_z[(h * P + tid) * R];
-        sm.mzd[tid][1] = a.prm.mimo_z[(h * P + tid) * R + 1];
-        sm.mzd[tid][2] = a.prm.mimo_down[(h * P + tid) * R];
-        sm.mzd[tid][3] = a.prm.mimo_down[(h * P + tid) * R + 1];
+        const float z0 = a.prm.mimo_z[(h * P + tid) * R], z1 = a.prm.mimo_z[(h * P + tid) * R + 1];
+        sm.mzd[tid][0] = -z0 * kLog2e;
+        sm.mzd[tid][1] = -z1 * kLog2e;
+        sm.mzd[tid][2] = a.prm.mimo_down[(h * P + tid) * R] * z0;
+        sm.mzd[tid][3] = a.prm.mimo_down[(h * P + tid) * R + 1] * z1;
     }
 
-    // State accumulators: wave w owns the H^T rows n in [16w, 16w+16) (all 64 columns p).
-    constexpr int kNT = 1;
-    const bool state_wave = true;
-    const int nt0 = wave;
-    f32x4 hacc[kNT][4];
+    // State accumulators: wave w owns the H^T rows n in [16w, 16w+16), all 64 columns p.
+    f32x4 hacc[4];
 #pragma unroll
-    for (int i = 0; i < kNT; ++i)
-#pragma unroll
-        for (int pt = 0; pt < 4; ++pt) hacc[i][pt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int pt = 0; pt < 4; ++pt) hacc[pt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    float phi_start = 0.f;  // absolute angle of pair pi at this segment's start
+    float phi_start = 0.f;  // absolute angle (radians) of this lane's pair at the segment start
     if (kFull && seg > 0) {
         // H = sum_i exp(sum_{l=i+1}^{seg-1} D_l) R(-sum_{l=i}^{seg-1} Phi_l) S_i
+        const int g16 = lane0 >> 4, l16 = lane0 & 15;
         const int64_t sbase = (int64_t)bh * (a.S - 1);
         float dsum = 0.f;
         for (int i = seg - 1; i >= 0; --i) {
@@ -267,404 +481,337 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
                 sm.rot[tid] = acc + a.seg_angle[(sbase + i) * NH + tid];
             }
             __syncthreads();
-            if (state_wave) {
-                const float wgt = __expf(dsum);
-                const float* Si = a.seg_state + (sbase + i) * (int64_t)N * P;
+            const float wgt = __expf(dsum);
+            const float* Si = a.seg_state + (sbase + i) * (int64_t)N * P;
+            const int n0 = 16 * wv + 4 * g16;
+            float s0, c0, s1, c1;
+            sincosf(-sm.rot[n0 / 2], &s0, &c0);
+            sincosf(-sm.rot[n0 / 2 + 1], &s1, &c1);
 #pragma unroll
-                for (int i2 = 0; i2 < kNT; ++i2) {
-                    const int n0 = 16 * (nt0 + i2) + 4 * g16;
-                    float s0, c0, s1, c1;
-                    sincosf(-sm.rot[n0 / 2], &s0, &c0);
-                    sincosf(-sm.rot[n0 / 2 + 1], &s1, &c1);
-#pragma unroll
-                    for (int pt = 0; pt < 4; ++pt) {
-                        const int p = 16 * pt + l16;
-                        const float e0 = Si[(n0 + 0) * P + p], o0 = Si[(n0 + 1) * P + p];
-                        const float e1 = Si[(n0 + 2) * P + p], o1 = Si[(n0 + 3) * P + p];
-                        hacc[i2][pt][0] += wgt * (e0 * c0 - o0 * s0);
-                        hacc[i2][pt][1] += wgt * (e0 * s0 + o0 * c0);
-                        hacc[i2][pt][2] += wgt * (e1 * c1 - o1 * s1);
-                        hacc[i2][pt][3] += wgt * (e1 * s1 + o1 * c1);
-                    }
-                }
+            for (int pt = 0; pt < 4; ++pt) {
+                const int p = 16 * pt + l16;
+                const float e0 = Si[(n0 + 0) * P + p], o0 = Si[(n0 + 1) * P + p];
+                const float e1 = Si[(n0 + 2) * P + p], o1 = Si[(n0 + 3) * P + p];
+                hacc[pt][0] += wgt * (e0 * c0 - o0 * s0);
+                hacc[pt][1] += wgt * (e0 * s0 + o0 * c0);
+                hacc[pt][2] += wgt * (e1 * c1 - o1 * s1);
+                hacc[pt][3] += wgt * (e1 * s1 + o1 * c1);
             }
             dsum += a.seg_decay[sbase + i];
         }
         __syncthreads();
-        phi_start = sm.rot[pi];  // sum_{l<seg} Phi_l
+        phi_start = sm.rot[8 * wv + (lane0 & 7)];  // sum_{l<seg} Phi_l
     }
 
-    // ---- global reads. A token row gets its own scalar buffer descriptor whose size is
-    // zero past the sequence end, so those reads return zero and the per-lane offsets
-    // stay loop-invariant.
-    const int wv = __builtin_amdgcn_readfirstlane(wave);
     const bf16* proj_b = a.proj + (int64_t)b * T * a.rs;
     const bf16* bn_b = a.Bn + ((int64_t)b * T * a.G + grp) * NR;
     const bf16* cn_b = a.Cn + ((int64_t)b * T * a.G + grp) * NR;
-    const int voff_bc = lane * 8;                                   // bytes: 4 bf16 of pair pi
-    const int voff_th = ((int)a.pl.theta + lane) * 2;
-    const int voff_x = ((int)a.pl.x + h * P + lane) * 2;
+
+    // ---- wave 0: raw token scalars of one chunk (kept as bf16 until used)
+    bf16 sdt = (bf16)0.f, sdt64 = (bf16)0.f, slam = (bf16)0.f, slam64 = (bf16)0.f;
+    float ssc = 1.f, ssc64 = 1.f;
+    auto load_sc = [&](int kk) {
+        const int lane = opaque(threadIdx.x & 63);
+        const int s0 = kk * Q;
+        const __amdgpu_buffer_rsrc_t rp = make_rsrc(proj_b + (int64_t)s0 * a.rs, (int64_t)max(T - s0, 0) * a.rs * 2);
+        sdt = ld_bf16(rp, lane * rs + (int)a.pl.dt + h);
+        sdt64 = ld_bf16(rp, Q * rs + (int)a.pl.dt + h);
+        if (a.trap) {
+            slam = ld_bf16(rp, lane * rs + (int)a.pl.lam + h);
+            slam64 = ld_bf16(rp, Q * rs + (int)a.pl.lam + h);
+        }
+        if (a.dt_scale) {
+            ssc = a.dt_scale[((int64_t)b * T + min(s0 + lane, T - 1)) * a.H + h];
+            ssc64 = a.dt_scale[((int64_t)b * T + min(s0 + Q, T - 1)) * a.H + h];
+        }
+    };
+    // ---- wave 0: token scalars of chunk kk into its ring slot (mamba3/mamba3.py:200-216)
+    auto tok_scalars = [&](int kk) {
+        const int lane = opaque(threadIdx.x & 63);
+        const int s0 = kk * Q;
+        Tok& tk = sm.tok[kk % NSLOT];
+        const float dt = s0 + lane < T ? fast_softplus((float)sdt + dtb) * ssc : 0.f;
+        const float lam = a.trap ? __builtin_amdgcn_rcpf(1.f + fast_exp(-(float)slam)) : 1.f;
+        float dtn = __shfl_down(dt, 1, 64);
+        float lamn = __shfl_down(lam, 1, 64);
+        if (lane == 63) {
+            dtn = s0 + Q < T ? fast_softplus((float)sdt64 + dtb) * ssc64 : 0.f;
+            lamn = a.trap ? __builtin_amdgcn_rcpf(1.f + fast_exp(-(float)slam64)) : 1.f;
+        }
+        const float c2 = wave_incl_scan(A2 * dt, lane);
+        const float c2e = __shfl(c2, 63, 64);
+        const float c2b = __shfl(c2, lane | 7, 64);
+        const float av = a.trap ? lam * dt : dt;
+        const float bv = a.trap ? (1.f - lamn) * dtn : 0.f;
+        tk.c2[lane] = c2;
+        tk.av[lane] = av;
+        tk.bv[lane] = bv;
+        tk.ec[lane] = __builtin_amdgcn_exp2f(c2);
+        tk.hb[lane] = __builtin_amdgcn_exp2f(c2b - c2) * (av + bv);
+        tk.dtr[lane] = dt * 0.15915494309189535f;
+        tk.w[lane] = __builtin_amdgcn_exp2f(c2e - c2) * (av + bv);
+    };
+
+    // ---- raw tile inputs of one chunk (chunk-level descriptors end at the sequence end)
+    // Preparation role: pair pi = 8 wave + lane%8 for tokens 8q .. 8q+7 (q = lane/8);
+    // X role: column p = lane for tokens 8 wave .. 8 wave + 7.
     u32x2 rawB[8], rawC[8];
     bf16 rawth[8], rawx[8];
-    float dr_a = 0.f, dr_b = 0.f, lr_a = 0.f, lr_b = 0.f;
-    auto load_prep = [&](int kk) {
+    auto load_raw = [&](int kk) {
+        const int lane = opaque(threadIdx.x & 63);
+        const int pi = 8 * wv + (lane & 7), q = lane >> 3;
         const int s0 = kk * Q;
+        const int left = max(T - s0, 0);
+        const __amdgpu_buffer_rsrc_t rp = make_rsrc(proj_b + (int64_t)s0 * a.rs, (int64_t)left * a.rs * 2);
+        const int64_t bcbytes = left > 0 ? ((int64_t)(left - 1) * bnrs + NR) * 2 : 0;
+        const __amdgpu_buffer_rsrc_t rb = make_rsrc(bn_b + (int64_t)s0 * bnrs, bcbytes);
+        const __amdgpu_buffer_rsrc_t rc = make_rsrc(cn_b + (int64_t)s0 * bnrs, bcbytes);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const int tok = s0 + 8 * wv + j;
-            const bool in = tok < T;
-            const __amdgpu_buffer_rsrc_t rrow = make_rsrc(proj_b + (int64_t)tok * a.rs, in ? a.rs * 2 : 0);
-            const __amdgpu_buffer_rsrc_t rb = make_rsrc(bn_b + (int64_t)tok * bnrs, in ? NR * 2 : 0);
-            rawB[j] = __builtin_amdgcn_raw_buffer_load_b64(rb, voff_bc, 0, 0);
-            if (kFull) {
-                const __amdgpu_buffer_rsrc_t rc = make_rsrc(cn_b + (int64_t)tok * bnrs, in ? NR * 2 : 0);
-                rawC[j] = __builtin_amdgcn_raw_buffer_load_b64(rc, voff_bc, 0, 0);
-            }
-            rawth[j] = a.cplx ? __builtin_bit_cast(bf16, (unsigned short)__builtin_amdgcn_raw_buffer_load_b16(rrow, voff_th, 0, 0))
-                              : (bf16)0.f;
-            rawx[j] = __builtin_bit_cast(bf16, (unsigned short)__builtin_amdgcn_raw_buffer_load_b16(rrow, voff_x, 0, 0));
+            const int tl = 8 * q + j;
+            rawB[j] = __builtin_amdgcn_raw_buffer_load_b64(rb, (tl * bnrs + 4 * pi) * 2, 0, 0);
+            if (kFull) rawC[j] = __builtin_amdgcn_raw_buffer_load_b64(rc, (tl * bnrs + 4 * pi) * 2, 0, 0);
+            rawth[j] = a.cplx ? ld_bf16(rp, tl * rs + (int)a.pl.theta + pi) : (bf16)0.f;
+            rawx[j] = ld_bf16(rp, (8 * wv + j) * rs + (int)a.pl.x + h * P + lane);
         }
-        if (wv == 0) {
-            // token s0+lane (and s0+64 in every lane, used by lane 63 only)
-            const __amdgpu_buffer_rsrc_t rch = make_rsrc(proj_b + (int64_t)s0 * a.rs,
-                                                          (int64_t)max(T - s0, 0) * a.rs * 2);
-            dr_a = (float)ld_bf16(rch, lane * rs + (int)a.pl.dt + h);
-            dr_b = (float)ld_bf16(rch, Q * rs + (int)a.pl.dt + h);
-            if (a.trap) {
-                lr_a = (float)ld_bf16(rch, lane * rs + (int)a.pl.lam + h);
-                lr_b = (float)ld_bf16(rch, Q * rs + (int)a.pl.lam + h);
+    };
+
+    // ---- element-wise preparation of chunk kk into registers
+    float phi_run = 0.f;  // angle of this lane's pair relative to the segment start, in turns
+    unsigned outB[8][2], outC[8][2];
+    u32x2 outBw[8];
+    bf16x8 outX0, outX1;
+    auto prep = [&](int kk) {
+        const int lane = opaque(threadIdx.x & 63);
+        const int q = lane >> 3;
+        const Tok& tk = sm.tok[kk % NSLOT];
+        const f32x4 d0 = *reinterpret_cast<const f32x4*>(&tk.dtr[8 * q]);
+        const f32x4 d1 = *reinterpret_cast<const f32x4*>(&tk.dtr[8 * q + 4]);
+        const f32x4 w0 = *reinterpret_cast<const f32x4*>(&tk.w[8 * q]);
+        const f32x4 w1 = *reinterpret_cast<const f32x4*>(&tk.w[8 * q + 4]);
+        // RoPE angle increments (turns) of tokens 8q..8q+7; prefix of the per-lane
+        // totals over q (lanes 8 apart) gives each lane's starting angle.
+        float inc[8];
+        float tot = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            inc[j] = (j < 4 ? d0[j] : d1[j - 4]) * (float)rawth[j];
+            tot += inc[j];
+        }
+        float incl = tot;
+#pragma unroll
+        for (int off = 8; off < 64; off <<= 1) {
+            const float o = __shfl_up(incl, off, 64);
+            if (lane >= off) incl += o;
+        }
+        const float ctot = __shfl(incl, 56 + (lane & 7), 64);
+        float phi = phi_run - (incl - tot);
+        phi_run -= ctot;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            phi -= inc[j];
+            const float rev = __builtin_amdgcn_fractf(phi);
+            const float sn = __builtin_amdgcn_sinf(rev), cs = __builtin_amdgcn_cosf(rev);
+            const unsigned k1 = pack_bf16x2(cs, -sn);
+            const unsigned k2 = pack_bf16x2(sn, cs);
+            const float be0 = dot2_bf16(rawB[j][0], k1), bo0 = dot2_bf16(rawB[j][0], k2);
+            const float be1 = dot2_bf16(rawB[j][1], k1), bo1 = dot2_bf16(rawB[j][1], k2);
+            if (kFull) {
+                outC[j][0] = pack_bf16x2(dot2_bf16(rawC[j][0], k1), dot2_bf16(rawC[j][0], k2));
+                outC[j][1] = pack_bf16x2(dot2_bf16(rawC[j][1], k1), dot2_bf16(rawC[j][1], k2));
+                outB[j][0] = pack_bf16x2(be0, bo0);
+                outB[j][1] = pack_bf16x2(be1, bo1);
+            }
+            const float wu = j < 4 ? w0[j] : w1[j - 4];
+            outBw[j] = u32x2{pack_bf16x2(be0 * wu, be1 * wu), pack_bf16x2(bo0 * wu, bo1 * wu)};
+        }
+        // X^T column p = lane for tokens 8 wave .. +7 (zero past the sequence end)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float x0 = (float)rawx[j], x1 = (float)rawx[4 + j];
+            outX0[2 * j] = (bf16)(x0 * mx0);
+            outX0[2 * j + 1] = (bf16)(x0 * mx1);
+            outX1[2 * j] = (bf16)(x1 * mx0);
+            outX1[2 * j + 1] = (bf16)(x1 * mx1);
+        }
+    };
+
+    // ---- registers -> LDS tiles of the prepared chunk, and the bf16 state copy
+    auto write_tiles = [&]() {
+        const int lane = opaque(threadIdx.x & 63);
+        const int pi = 8 * wv + (lane & 7), q = lane >> 3;
+        const int g16 = lane >> 4, l16 = lane & 15;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int u = 8 * q + j;
+            if (kFull) {
+                const int col = sw_cb(2 * u, 2 * pi);
+                *reinterpret_cast<unsigned*>(&sm.C[2 * u][col]) = outC[j][0];
+                *reinterpret_cast<unsigned*>(&sm.C[2 * u + 1][col]) = outC[j][1];
+                *reinterpret_cast<unsigned*>(&sm.B[2 * u][col]) = outB[j][0];
+                *reinterpret_cast<unsigned*>(&sm.B[2 * u + 1][col]) = outB[j][1];
+            }
+            *reinterpret_cast<u32x2*>(&sm.Bw[u][sw_bw(u, 4 * pi)]) = outBw[j];
+        }
+        *reinterpret_cast<bf16x8*>(&sm.X[lane][16 * wv]) = outX0;
+        *reinterpret_cast<bf16x8*>(&sm.X[lane][16 * wv + 8]) = outX1;
+        if (kFull) {
+            const int n0 = 16 * wv + 4 * g16;
+#pragma unroll
+            for (int pt = 0; pt < 4; ++pt) {
+                const f32x4 v = hacc[pt];
+                *reinterpret_cast<bf16x4*>(&sm.H[16 * pt + l16][n0]) =
+                    bf16x4{(bf16)v[0], (bf16)v[1], (bf16)v[2], (bf16)v[3]};
             }
         }
     };
-    load_prep(k_begin);
 
-    float phi_run = 0.f;   // angle of pair pi relative to the segment start
     float logdecay = 0.f;  // total log-decay of the segment (natural log)
+
+    // ---- prologue: token scalars of the first two chunks, first chunk's tiles
+    if (wv == 0) {
+        load_sc(k_begin);
+        tok_scalars(k_begin);
+        if (k_begin + 1 < k_end) {
+            load_sc(k_begin + 1);
+            tok_scalars(k_begin + 1);
+        }
+        if (k_begin + 2 < k_end) load_sc(k_begin + 2);
+    }
+    load_raw(k_begin);
+    __syncthreads();
+    prep(k_begin);
+    if (k_begin + 1 < k_end) load_raw(k_begin + 1);
+    write_tiles();
 
     for (int k = k_begin; k < k_end; ++k) {
         const int s0 = k * Q;
+        const bool more = k + 1 < k_end;
         __syncthreads();
-        // ---- phase 1: bf16 state copy, token scalars, X^T tile
-        if (kFull && state_wave) {
-#pragma unroll
-            for (int i2 = 0; i2 < kNT; ++i2) {
-                const int n0 = 16 * (nt0 + i2) + 4 * g16;
-#pragma unroll
-                for (int pt = 0; pt < 4; ++pt) {
-                    const f32x4 v = hacc[i2][pt];
-                    *reinterpret_cast<bf16x4*>(&sm.H[16 * pt + l16][n0]) =
-                        bf16x4{(bf16)v[0], (bf16)v[1], (bf16)v[2], (bf16)v[3]};
-                }
-            }
-        }
-        if (wave == 0) {
-            const int u = lane;
-            const int s = s0 + u;
-            float sc_a = 1.f, sc_b = 1.f;
-            if (a.dt_scale) {
-                sc_a = a.dt_scale[((int64_t)b * T + min(s, T - 1)) * a.H + h];
-                sc_b = a.dt_scale[((int64_t)b * T + min(s0 + Q, T - 1)) * a.H + h];
-            }
-            const float dt = s < T ? fast_softplus(dr_a + dtb) * sc_a : 0.f;
-            const float lam = a.trap ? __builtin_amdgcn_rcpf(1.f + fast_exp(-lr_a)) : 1.f;
-            // token u+1: lanes 0..62 take it from the next lane, lane 63 from token 64
-            float dtn = __shfl_down(dt, 1, 64);
-            float lamn = __shfl_down(lam, 1, 64);
-            if (lane == 63) {
-                dtn = s + 1 < T ? fast_softplus(dr_b + dtb) * sc_b : 0.f;
-                lamn = a.trap ? __builtin_amdgcn_rcpf(1.f + fast_exp(-lr_b)) : 1.f;
-            }
-            const float c2 = wave_incl_scan(A_h * kLog2e * dt, lane);
-            const float c2_end = __shfl(c2, 63, 64);
-            const float av = a.trap ? lam * dt : dt;
-            const float bv = a.trap ? (1.f - lamn) * dtn : 0.f;
-            sm.c2[u] = c2;
-            sm.ec[u] = __builtin_amdgcn_exp2f(c2);
-            sm.w[u] = __builtin_amdgcn_exp2f(c2_end - c2) * (av + bv);
-            sm.dt[u] = dt;
-            sm.L[u][Q] = av;
-            sm.L[u][Q + 1] = bv;
-        }
+        const int lane = opaque(threadIdx.x & 63);
+        const int g16 = lane >> 4, l16 = lane & 15;
+        const Tok& tk = sm.tok[k % NSLOT];
+        // ---- M(k): state update G4: H^T = e^{c_63} H^T + B~w^T X on chunk k's tiles
         {
-            bf16x8 v0, v1;
+            const float dch = tk.ec[Q - 1];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float x0 = (float)rawx[j], x1 = (float)rawx[4 + j];
-                v0[2 * j] = (bf16)(x0 * mx0);
-                v0[2 * j + 1] = (bf16)(x0 * mx1);
-                v1[2 * j] = (bf16)(x1 * mx0);
-                v1[2 * j + 1] = (bf16)(x1 * mx1);
-            }
-            *reinterpret_cast<bf16x8*>(&sm.X[xp][16 * tq]) = v0;
-            *reinterpret_cast<bf16x8*>(&sm.X[xp][16 * tq + 8]) = v1;
-        }
-        __syncthreads();
-        logdecay += sm.c2[Q - 1] * (1.f / kLog2e);
-
-        // ---- phase 2: angle increments per 8-token group; Lc
-        float inc[8];
-        {
-            float tot = 0.f;
+            for (int pt = 0; pt < 4; ++pt) hacc[pt] *= dch;
+            const int n = 16 * wv + l16;
+            const int ncol = (2 * n) ^ (32 * (g16 >> 1));  // sw_bw for rows 16s + 4 g16 + j
+            bf16x2 wop[2][4];
+            bf16x8 xop[2][4];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                inc[j] = sm.dt[8 * tq + j] * (float)rawth[j];
-                tot += inc[j];
-            }
-            sm.tot[tq][pi] = tot;
-        }
-        if (kFull) {
-            // Lc[t][u]: thread t = tid/8 fills u = tid%8 + 8j (strided: conflict-free banks)
-            const int t = tid >> 3;
-            const int u0 = tid & 7;
-            const float ct = sm.c2[t];
+            for (int j = 0; j < 4; ++j) wop[0][j] = *reinterpret_cast<const bf16x2*>(&sm.Bw[4 * g16 + j][ncol]);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int u = u0 + 8 * j;
-                float v = 0.f;
-                if (u <= t)
-                    v = __builtin_amdgcn_exp2f(ct - sm.c2[u]) * (sm.L[u][Q] + (u < t ? sm.L[u][Q + 1] : 0.f));
-                sm.L[t][u] = v;
-            }
-        }
-        __syncthreads();
-
-        // ---- phase 3: rotate B^/C^ into B~/C~/B~w
-        {
-            float excl = 0.f, all = 0.f;
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                const float tq_tot = sm.tot[q][pi];
-                if (q < tq) excl += tq_tot;
-                all += tq_tot;
-            }
-            float phi = phi_run - excl;
-            phi_run -= all;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int u = 8 * tq + j;
-                phi -= inc[j];
-                float sn = 0.f, cs = 1.f;
-                if (a.cplx) fast_sincos(phi, sn, cs);
-                const bf16x2 k1 = as_bf16x2(pack_bf16x2(cs, -sn));
-                const bf16x2 k2 = as_bf16x2(pack_bf16x2(sn, cs));
-                const bf16x2 pb0 = as_bf16x2(rawB[j][0]), pb1 = as_bf16x2(rawB[j][1]);
-                const float be0 = __builtin_amdgcn_fdot2_f32_bf16(pb0, k1, 0.f, false);
-                const float bo0 = __builtin_amdgcn_fdot2_f32_bf16(pb0, k2, 0.f, false);
-                const float be1 = __builtin_amdgcn_fdot2_f32_bf16(pb1, k1, 0.f, false);
-                const float bo1 = __builtin_amdgcn_fdot2_f32_bf16(pb1, k2, 0.f, false);
-                if (kFull) {
-                    const bf16x2 pc0 = as_bf16x2(rawC[j][0]), pc1 = as_bf16x2(rawC[j][1]);
-                    const float ce0 = __builtin_amdgcn_fdot2_f32_bf16(pc0, k1, 0.f, false);
-                    const float co0 = __builtin_amdgcn_fdot2_f32_bf16(pc0, k2, 0.f, false);
-                    const float ce1 = __builtin_amdgcn_fdot2_f32_bf16(pc1, k1, 0.f, false);
-                    const float co1 = __builtin_amdgcn_fdot2_f32_bf16(pc1, k2, 0.f, false);
-                    *reinterpret_cast<unsigned*>(&sm.C[2 * u][2 * pi]) = pack_bf16x2(ce0, co0);
-                    *reinterpret_cast<unsigned*>(&sm.C[2 * u + 1][2 * pi]) = pack_bf16x2(ce1, co1);
-                    *reinterpret_cast<unsigned*>(&sm.B[2 * u][2 * pi]) = pack_bf16x2(be0, bo0);
-                    *reinterpret_cast<unsigned*>(&sm.B[2 * u + 1][2 * pi]) = pack_bf16x2(be1, bo1);
-                }
-                const float wu = sm.w[u];
-                *reinterpret_cast<u32x2*>(&sm.Bw[u][4 * pi]) =
-                    u32x2{pack_bf16x2(be0 * wu, be1 * wu), pack_bf16x2(bo0 * wu, bo1 * wu)};
-                // keep one token in flight at a time (bounds register pressure)
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        }
-        __syncthreads();
-
-        // ---- phase 4: MFMA contractions. Operand addresses derive from an opaque copy
-        // of the lane id so they are recomputed per chunk instead of pinned in VGPRs.
-        int lane4 = lane;
-        asm volatile("" : "+v"(lane4));
-        const int g16 = lane4 >> 4, l16 = lane4 & 15;
-        if (kFull) {
-            {
-                // Output block of this wave: SIMD s runs waves s and s+4, which own the
-                // 16-row blocks s and 7-s, so causal work is balanced per SIMD.
-                const int I = wv < 4 ? wv : 11 - wv;  // uniform: keeps descriptors scalar
-                const int ta = 8 * I + 2 * g16;  // tokens of this lane's output rows: ta, ta+1
-                // z of this lane's outputs; consumed by the epilogue after the MFMAs.
-                const int tblk = s0 + 8 * I;
-                const __amdgpu_buffer_rsrc_t rz = make_rsrc(proj_b + (int64_t)tblk * a.rs,
-                                                            (int64_t)max(T - tblk, 0) * a.rs * 2);
-                bf16 zraw[4][2];
-#pragma unroll
-                for (int pt = 0; pt < 4; ++pt)
-#pragma unroll
-                    for (int tt = 0; tt < 2; ++tt)
-                        zraw[pt][tt] = ld_bf16(rz, (2 * g16 + tt) * rs + (int)a.pl.z + h * P + 16 * pt + l16);
-                bf16x8 cA[4];
-#pragma unroll
-                for (int s = 0; s < 4; ++s)
-                    cA[s] = *reinterpret_cast<const bf16x8*>(&sm.C[16 * I + l16][32 * s + 8 * g16]);
-                f32x4 yacc[4];
-                // G3: inter-chunk output, then the e^{c_t} row scale.
-#pragma unroll
-                for (int pt = 0; pt < 4; ++pt) {
-                    yacc[pt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                    for (int s = 0; s < 4; ++s)
-                        yacc[pt] = mfma16(cA[s],
-                                          *reinterpret_cast<const bf16x8*>(&sm.H[16 * pt + l16][32 * s + 8 * g16]),
-                                          yacc[pt]);
-                }
-                const float ea = sm.ec[ta], eb = sm.ec[ta + 1];
-#pragma unroll
-                for (int pt = 0; pt < 4; ++pt) {
-                    yacc[pt][0] *= ea;
-                    yacc[pt][1] *= ea;
-                    yacc[pt][2] *= eb;
-                    yacc[pt][3] *= eb;
-                }
-                // G1 + mask + G2.
-                const int t_col = 8 * I + (l16 >> 1);
-                const int r_col = l16 & 1;
-                for (int s2 = 0; s2 <= I / 2; ++s2) {
-                    bf16x8 aop;
-#pragma unroll
-                    for (int jj = 0; jj < 2; ++jj) {
-                        const int J = 2 * s2 + jj;
-                        float m0 = 0.f, m1 = 0.f, m2 = 0.f, m3 = 0.f;
-                        if (J <= I) {
-                            f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                            for (int s = 0; s < 4; ++s)
-                                sacc = mfma16(*reinterpret_cast<const bf16x8*>(&sm.B[16 * J + l16][32 * s + 8 * g16]),
-                                              cA[s], sacc);
-                            const int u0 = 8 * J + 2 * g16;
-                            const f32x2 lv = *reinterpret_cast<const f32x2*>(&sm.L[t_col][u0]);
-                            m0 = sacc[0] * lv[0];
-                            m1 = sacc[1] * lv[0];
-                            m2 = sacc[2] * lv[1];
-                            m3 = sacc[3] * lv[1];
-                            if (J == I) {
-                                if (u0 == t_col) { if (r_col == 0) m0 += D_h; else m1 += D_h; }
-                                if (u0 + 1 == t_col) { if (r_col == 0) m2 += D_h; else m3 += D_h; }
-                            }
-                        }
-                        aop[4 * jj + 0] = (bf16)m0;
-                        aop[4 * jj + 1] = (bf16)m1;
-                        aop[4 * jj + 2] = (bf16)m2;
-                        aop[4 * jj + 3] = (bf16)m3;
-                    }
-#pragma unroll
-                    for (int pt = 0; pt < 4; ++pt) {
-                        const bf16* xr = &sm.X[16 * pt + l16][32 * s2];
-                        const bf16x4 lo = *reinterpret_cast<const bf16x4*>(xr + 4 * g16);
-                        const bf16x4 hi = *reinterpret_cast<const bf16x4*>(xr + 16 + 4 * g16);
-                        const bf16x8 bop = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                        yacc[pt] = mfma16(aop, bop, yacc[pt]);
-                    }
-                }
-                // Epilogue: SiLU(z * mimo_z) gate and MIMO-down sum over r. Stores go
-                // through a descriptor that ends at the last token, so padding rows drop.
-                const __amdgpu_buffer_rsrc_t ry = make_rsrc(a.y_out + ((int64_t)b * T + tblk) * HP,
-                                                            (int64_t)max(T - tblk, 0) * HP * 2);
-#pragma unroll
-                for (int pt = 0; pt < 4; ++pt) {
-                    const int p = 16 * pt + l16;
-#pragma unroll
-                    for (int tt = 0; tt < 2; ++tt) {
-                        const float z = (float)zraw[pt][tt];
-                        const float y0 = yacc[pt][2 * tt], y1 = yacc[pt][2 * tt + 1];
-                        const f32x4 g = *reinterpret_cast<const f32x4*>(&sm.mzd[p][0]);
-                        const float out = g[2] * y0 * fast_silu(z * g[0]) +
-                                          g[3] * y1 * fast_silu(z * g[1]);
-                        __builtin_amdgcn_raw_buffer_store_b16(
-                            __builtin_bit_cast(unsigned short, (bf16)out), ry,
-                            ((2 * g16 + tt) * HP + h * P + p) * 2, 0, 0);
-                    }
-                }
-            }
-        }
-        if (state_wave) {
-            // G4: state update H^T = e^{c_63} H^T + B~w^T X.
-            const float dch = sm.ec[Q - 1];
-#pragma unroll
-            for (int i2 = 0; i2 < kNT; ++i2)
-#pragma unroll
-                for (int pt = 0; pt < 4; ++pt) hacc[i2][pt] *= dch;
+            for (int pt = 0; pt < 4; ++pt)
+                xop[0][pt] = *reinterpret_cast<const bf16x8*>(&sm.X[16 * pt + l16][8 * g16]);
+            M3_FENCE();
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
-                bf16x8 bop[4];
+                if (s + 1 < 4) {
 #pragma unroll
-                for (int pt = 0; pt < 4; ++pt)
-                    bop[pt] = *reinterpret_cast<const bf16x8*>(&sm.X[16 * pt + l16][32 * s + 8 * g16]);
+                    for (int j = 0; j < 4; ++j)
+                        wop[(s + 1) & 1][j] =
+                            *reinterpret_cast<const bf16x2*>(&sm.Bw[16 * (s + 1) + 4 * g16 + j][ncol]);
 #pragma unroll
-                for (int i2 = 0; i2 < kNT; ++i2) {
-                    const int n = 16 * (nt0 + i2) + l16;
-                    bf16x8 aop;
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const bf16x2 v = *reinterpret_cast<const bf16x2*>(&sm.Bw[16 * s + 4 * g16 + j][2 * n]);
-                        aop[2 * j] = v[0];
-                        aop[2 * j + 1] = v[1];
-                    }
-#pragma unroll
-                    for (int pt = 0; pt < 4; ++pt) hacc[i2][pt] = mfma16(aop, bop[pt], hacc[i2][pt]);
+                    for (int pt = 0; pt < 4; ++pt)
+                        xop[(s + 1) & 1][pt] =
+                            *reinterpret_cast<const bf16x8*>(&sm.X[16 * pt + l16][32 * (s + 1) + 8 * g16]);
                 }
+                M3_FENCE();
+                bf16x8 aop;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    aop[2 * j] = wop[s & 1][j][0];
+                    aop[2 * j + 1] = wop[s & 1][j][1];
+                }
+#pragma unroll
+                for (int pt = 0; pt < 4; ++pt) hacc[pt] = mfma16(aop, xop[s & 1][pt], hacc[pt]);
+                M3_FENCE();
+            }
+            logdecay += tk.c2[Q - 1] * (1.f / kLog2e);
+        }
+        // ---- M(k): output block of chunk k
+        if (kFull) {
+            switch (wv) {
+                case 0: out_block<0>(sm, tk, a, proj_b, b, h, s0, g16, l16, D_h); break;
+                case 1: out_block<1>(sm, tk, a, proj_b, b, h, s0, g16, l16, D_h); break;
+                case 2: out_block<2>(sm, tk, a, proj_b, b, h, s0, g16, l16, D_h); break;
+                case 3: out_block<3>(sm, tk, a, proj_b, b, h, s0, g16, l16, D_h); break;
+                case 4: out_block<7>(sm, tk, a, proj_b, b, h, s0, g16, l16, D_h); break;
+                case 5: out_block<6>(sm, tk, a, proj_b, b, h, s0, g16, l16, D_h); break;
+                case 6: out_block<5>(sm, tk, a, proj_b, b, h, s0, g16, l16, D_h); break;
+                default: out_block<4>(sm, tk, a, proj_b, b, h, s0, g16, l16, D_h); break;
             }
         }
-        // Next chunk's element-wise inputs (reads past T return zero); they arrive while
-        // the other waves finish this chunk.
-        if (k + 1 < k_end) load_prep(k + 1);
+        // ---- M(k): token scalars of chunk k+2 (wave 0, lightest output block)
+        if (wv == 0) {
+            if (k + 2 < k_end) tok_scalars(k + 2);
+            if (k + 3 < k_end) load_sc(k + 3);
+        }
+        // ---- M(k): prepare chunk k+1, start reading chunk k+2; W(k+1)
+        if (more) {
+            prep(k + 1);
+            if (k + 2 < k_end) load_raw(k + 2);
+            __syncthreads();
+            write_tiles();
+        }
     }
 
     // ---- segment end
+    const int pi_out = 8 * wv + (lane0 & 7);
+    const bool pair_lane = (lane0 >> 3) == 0;  // lanes 0..7 of each wave cover the 64 pairs
     if (!kFull) {
+        const int g16 = lane0 >> 4, l16 = lane0 & 15;
         const int64_t sidx = (int64_t)bh * (a.S - 1) + seg;
         float* out = a.seg_state + sidx * (int64_t)N * P;
+        const int n0 = 16 * wv + 4 * g16;
 #pragma unroll
-        for (int i2 = 0; i2 < kNT; ++i2) {
-            const int n0 = 16 * (nt0 + i2) + 4 * g16;
+        for (int pt = 0; pt < 4; ++pt)
 #pragma unroll
-            for (int pt = 0; pt < 4; ++pt)
-#pragma unroll
-                for (int v = 0; v < 4; ++v) out[(n0 + v) * P + 16 * pt + l16] = hacc[i2][pt][v];
-        }
+            for (int v = 0; v < 4; ++v) out[(n0 + v) * P + 16 * pt + l16] = hacc[pt][v];
         if (tid == 0) a.seg_decay[sidx] = logdecay;
-        if (wave == 0) a.seg_angle[sidx * NH + pi] = phi_run;
+        if (pair_lane) a.seg_angle[sidx * NH + pi_out] = phi_run * 6.283185307179586f;
     } else if (seg == a.S - 1) {
         __syncthreads();
-        if (wave == 0) {
-            sm.rot[pi] = phi_start;
-            if (a.angle) a.angle[(int64_t)bh * NH + pi] = a.cplx ? phi_start + phi_run : 0.f;
+        if (pair_lane) {
+            sm.rot[pi_out] = phi_start;
+            if (a.angle) a.angle[(int64_t)bh * NH + pi_out] = a.cplx ? phi_start + phi_run * 6.283185307179586f : 0.f;
         }
         __syncthreads();
-        if (a.h_final && state_wave) {
+        if (a.h_final) {
+            const int g16 = lane0 >> 4, l16 = lane0 & 15;
             float* hf = a.h_final + (int64_t)bh * P * N;
+            const int n0 = 16 * wv + 4 * g16;
+            float s0, c0, s1, c1;
+            sincosf(sm.rot[n0 / 2], &s0, &c0);
+            sincosf(sm.rot[n0 / 2 + 1], &s1, &c1);
 #pragma unroll
-            for (int i2 = 0; i2 < kNT; ++i2) {
-                const int n0 = 16 * (nt0 + i2) + 4 * g16;
-                float s0, c0, s1, c1;
-                sincosf(sm.rot[n0 / 2], &s0, &c0);
-                sincosf(sm.rot[n0 / 2 + 1], &s1, &c1);
-#pragma unroll
-                for (int pt = 0; pt < 4; ++pt) {
-                    const f32x4 v = hacc[i2][pt];
-                    const f32x4 o = {v[0] * c0 - v[1] * s0, v[0] * s0 + v[1] * c0,
-                                     v[2] * c1 - v[3] * s1, v[2] * s1 + v[3] * c1};
-                    *reinterpret_cast<f32x4*>(&hf[(16 * pt + l16) * N + n0]) = o;
-                }
+            for (int pt = 0; pt < 4; ++pt) {
+                const f32x4 v = hacc[pt];
+                const f32x4 o = {v[0] * c0 - v[1] * s0, v[0] * s0 + v[1] * c0,
+                                 v[2] * c1 - v[3] * s1, v[2] * s1 + v[3] * c1};
+                *reinterpret_cast<f32x4*>(&hf[(16 * pt + l16) * N + n0]) = o;
             }
         }
         if (a.prev_bx) {
             // prev_BX = B~_{T-1} x_{T-1}^T, from the last chunk's tiles (still in LDS),
-            // rotated to the absolute frame. Thread: column pair pi, rows p = 8*wave..+7.
+            // rotated to the absolute frame. Thread: column pair lane, rows p = 8*wave..+7.
             const int ul = (T - 1) - (K - 1) * Q;
+            const int pp = lane0;
             float sn, cs;
-            sincosf(sm.rot[pi], &sn, &cs);
-            const float be0 = (float)sm.B[2 * ul][2 * pi], bo0 = (float)sm.B[2 * ul][2 * pi + 1];
-            const float be1 = (float)sm.B[2 * ul + 1][2 * pi], bo1 = (float)sm.B[2 * ul + 1][2 * pi + 1];
+            sincosf(sm.rot[pp], &sn, &cs);
+            const int c0 = sw_cb(2 * ul, 2 * pp);  // rows 2ul and 2ul+1 share the 16-row block
+            const float be0 = (float)sm.B[2 * ul][c0], bo0 = (float)sm.B[2 * ul][c0 + 1];
+            const float be1 = (float)sm.B[2 * ul + 1][c0], bo1 = (float)sm.B[2 * ul + 1][c0 + 1];
             const float ae0 = be0 * cs - bo0 * sn, ao0 = be0 * sn + bo0 * cs;
             const float ae1 = be1 * cs - bo1 * sn, ao1 = be1 * sn + bo1 * cs;
             float* pb = a.prev_bx + (int64_t)bh * P * N;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const int p = 8 * wave + j;
+                const int p = 8 * wv + j;
                 const float x0 = (float)sm.X[p][2 * ul], x1 = (float)sm.X[p][2 * ul + 1];
-                *reinterpret_cast<f32x2*>(&pb[p * N + 2 * pi]) =
-                    f32x2{ae0 * x0 + ae1 * x1, ao0 * x0 + ao1 * x1};
+                *reinterpret_cast<f32x2*>(&pb[p * N + 2 * pp]) = f32x2{ae0 * x0 + ae1 * x1, ao0 * x0 + ao1 * x1};
             }
         }
     }
