@@ -49,6 +49,22 @@ def step_bytes(B, H, d_in_proj, d_inner):
     return 16 * B * H * P * N + 2 * B * d_in_proj + 2 * B * d_inner + 8 * B * H * (N // 2)
 
 
+TRAFFIC_FILE = ROOT / "profiles" / "pmc_traffic_d768.md"
+
+
+def recorded_traffic():
+    """HBM bytes per call measured with rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE, scaled by
+    a 256 MiB copy), as recorded in the profiles summary: {'prefill': B, 'step': B}."""
+    out = {}
+    if TRAFFIC_FILE.exists():
+        for line in TRAFFIC_FILE.read_text().splitlines():
+            for key in ("prefill", "step"):
+                tag = f"traffic_bytes_{key}:"
+                if line.strip().startswith(tag):
+                    out[key] = int(line.split(":", 1)[1].strip())
+    return out
+
+
 def time_events(torch, fn, steps, warmup):
     """Warmup, then `steps` calls bracketed by synchronize; per-call HIP events on the
     current stream (the stream the native entry points launch on)."""
@@ -118,6 +134,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--decode-steps", type=int, default=200)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibration-copy", action="store_true",
+                    help="also run one 256 MiB device-to-device copy (the known-size kernel that "
+                         "scales FETCH_SIZE / WRITE_SIZE in rocprofv3 --pmc runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1"}))
@@ -176,6 +195,14 @@ def main() -> int:
                                             s0["angle"], y_out, h_out, p_out, a_out),
             args.decode_steps, 10)
 
+        if args.calibration_copy:
+            src = torch.ones(128 << 20, dtype=torch.bfloat16, device=dev)
+            dst = torch.empty_like(src)
+            dst.copy_(src)
+            torch.cuda.synchronize()
+            del src, dst
+
+    traffic = recorded_traffic()
     tokens = BATCH * SEQLEN
     flops = ssd_flops(BATCH, SEQLEN, H)
     achieved_tf = flops / (kern_ms * 1e-3) / 1e12
@@ -202,7 +229,8 @@ def main() -> int:
                    "global_batch": BATCH, "seq_len": SEQLEN, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(achieved_tf, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved_tf / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "frac": round(achieved_tf / PEAK_BF16_TFLOPS, 4),
+                     "traffic": traffic.get("prefill"),
                      "kernel": "native SSD prefill (all launches of m3_prefill_fwd)",
                      "algorithmic_flops": flops, "avg_ms": round(kern_ms, 4)},
         "whole_layer_prefill_tok_s": round(tokens / (layer_ms * 1e-3), 1),
@@ -214,7 +242,8 @@ def main() -> int:
             "kernel_us": round(step_kern_ms * 1e3, 2),
             "roofline": {"bound": "hbm", "achieved": round(achieved_gbs, 1),
                          "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                         "frac": round(achieved_gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                         "frac": round(achieved_gbs / PEAK_HBM_GBS, 4),
+                         "traffic": traffic.get("step"),
                          "algorithmic_bytes": sbytes},
         },
     }
