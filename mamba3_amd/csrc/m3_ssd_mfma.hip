@@ -45,6 +45,7 @@
 // segment states are rotated into the local frame when combined, and the final state,
 // angle and prev_BX are rotated back to the absolute frame.
 #include <algorithm>
+#include <type_traits>
 
 #include "m3_common.h"
 #include "m3_kernels.h"
@@ -68,6 +69,7 @@ typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int NSLOT = 3;  // token-scalar ring: chunks k, k+1 read while k+2 is written
 
@@ -85,7 +87,7 @@ struct Tok {
 struct __align__(16) Smem {
     bf16 C[Q * R][N + PAD];  // C~ rows (t,r) = 2t+r; 16-byte column chunks swizzled (sw_cb)
     bf16 B[Q * R][N + PAD];  // B~ rows (u,r'), same swizzle
-    bf16 Bw[Q][NR + PAD];    // B~ * w_u, [u][n][r'] order, swizzled (sw_bw)
+    bf16 Bw[Q][NR + PAD];    // B~ * w_u, [u][n][r'] order
     bf16 X[P][Q * R + PAD];  // X^T
     bf16 H[P][N + PAD];      // incoming state, bf16
     Tok tok[NSLOT];
@@ -130,10 +132,14 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, in
                                              kRsrcFlags);
 }
 
-__device__ __forceinline__ bf16 ld_bf16(__amdgpu_buffer_rsrc_t r, int off_elems) {
-    const unsigned short v = __builtin_amdgcn_raw_buffer_load_b16(r, off_elems * 2, 0, 0);
-    return __builtin_bit_cast(bf16, v);
+
+// 16-bit load kept zero-extended in its own 32-bit register. Holding loaded bf16 values
+// as bf16 lets the compiler pack two per register, which forces a wait on the load right
+// after it is issued; the value is widened only where it is used (bf16_f32).
+__device__ __forceinline__ unsigned ld_u16(__amdgpu_buffer_rsrc_t r, int off_bytes) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, off_bytes, 0, 0);
 }
+__device__ __forceinline__ float bf16_f32(unsigned u) { return __builtin_bit_cast(float, u << 16); }
 
 __device__ __forceinline__ u32x2 ld_b64(__amdgpu_buffer_rsrc_t r, int off_elems) {
     return __builtin_amdgcn_raw_buffer_load_b64(r, off_elems * 2, 0, 0);
@@ -166,22 +172,22 @@ __device__ __forceinline__ float wave_incl_scan(float v, int lane) {
     return v;
 }
 
-// v_dot2_f32_bf16 with a zero accumulator (the builtin becomes v_dot2c plus a v_mov).
-__device__ __forceinline__ float dot2_bf16(unsigned a, unsigned b) {
-    float d;
-    asm("v_dot2_f32_bf16 %0, %1, %2, 0" : "=v"(d) : "v"(a), "v"(b));
-    return d;
+__device__ __forceinline__ bf16x2 as_bf16x2(unsigned u) { return __builtin_bit_cast(bf16x2, u); }
+
+// bf16 pair dot product (v_dot2 family). Through the builtin only: dot instructions have
+// read/write hazards with neighbouring VALU instructions that the compiler resolves for
+// its own instructions but cannot see through inline assembly.
+// `zero` is a register holding 0.0 that the compiler cannot fold: with a constant
+// accumulator it picks the accumulate-in-place v_dot2c form plus a v_mov per call.
+__device__ __forceinline__ float dot2_bf16(unsigned a, unsigned b, float zero) {
+    return __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(a), as_bf16x2(b), zero, false);
 }
 
-// C~ / B~ tiles: the 16-byte column chunks of a row are XOR-swizzled by the row's
-// 16-row block, so that the preparation's stores (lanes 16 rows apart) hit distinct
-// banks. MFMA operand reads cover 16 rows of one block, so their pattern is unchanged.
-__device__ __forceinline__ int sw_cb(int row, int col) { return col ^ (16 * ((row >> 4) & 3)); }
-// B~w tile: the two 64-byte halves of every 32-pair column group swap on odd 8-token
-// blocks, for the same reason.
-__device__ __forceinline__ int sw_bw(int u, int col) { return col ^ (32 * ((u >> 3) & 1)); }
+// C~ / B~ tiles: 64-byte column groups of a row are XOR-swizzled by the row's 16-row
+// block, so the preparation's 64-bit stores (lanes 16 rows apart) hit distinct banks.
+// MFMA operand reads cover 16 rows of one block, so their pattern is only permuted.
+__device__ __forceinline__ int sw_cb(int row, int col) { return col ^ (32 * ((row >> 4) & 3)); }
 
-__device__ __forceinline__ bf16x2 as_bf16x2(unsigned u) { return __builtin_bit_cast(bf16x2, u); }
 
 __device__ __forceinline__ unsigned pack_bf16x2(float lo, float hi) {
     return __builtin_bit_cast(unsigned, bf16x2{(bf16)lo, (bf16)hi});
@@ -254,12 +260,12 @@ __device__ __forceinline__ void out_block(const Smem& sm, const Tok& tk, const A
     const int tblk = s0 + 8 * I;
     const int left = max(T - tblk, 0);
     const __amdgpu_buffer_rsrc_t rz = make_rsrc(proj_b + (int64_t)tblk * a.rs, (int64_t)left * a.rs * 2);
-    bf16 zraw[4][2];
+    unsigned zraw[4][2];
 #pragma unroll
     for (int pt = 0; pt < 4; ++pt)
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt)
-            zraw[pt][tt] = ld_bf16(rz, (2 * g16 + tt) * rs + (int)a.pl.z + h * P + 16 * pt + l16);
+            zraw[pt][tt] = ld_u16(rz, ((2 * g16 + tt) * rs + (int)a.pl.z + h * P + 16 * pt + l16) * 2);
 
     constexpr int NJ = I + 1;
     // Token scalars this lane needs (rows t_col, columns u = 8J + 2 g16 + {0,1}).
@@ -279,13 +285,13 @@ __device__ __forceinline__ void out_block(const Smem& sm, const Tok& tk, const A
         hv[J] = *reinterpret_cast<const f32x2*>(&tk.hb[8 * J + 2 * g16]);
     }
 
-    // C~ rows of this block (logical column 32s + 8 g16 sits at chunk (4s + g16) ^ 2(I&3))
+    // C~ rows of this block (logical column 32s + 8 g16 sits at 32 (s ^ (I&3)) + 8 g16)
     // and the first H operand group.
     bf16x8 cA[4], hop[2][4];
 #pragma unroll
     for (int s = 0; s < 4; ++s)
         cA[s] = *reinterpret_cast<const bf16x8*>(
-            &sm.C[16 * I + l16][8 * (g16 ^ (2 * (I & 1))) + 32 * (s ^ ((I >> 1) & 1))]);
+            &sm.C[16 * I + l16][8 * g16 + 32 * (s ^ (I & 3))]);
 #pragma unroll
     for (int s = 0; s < 4; ++s)
         hop[0][s] = *reinterpret_cast<const bf16x8*>(&sm.H[l16][32 * s + 8 * g16]);
@@ -318,7 +324,7 @@ __device__ __forceinline__ void out_block(const Smem& sm, const Tok& tk, const A
 #pragma unroll
             for (int s = 0; s < 4; ++s)
                 bop[(J + 1) & 1][s] = *reinterpret_cast<const bf16x8*>(
-                    &sm.B[16 * (J + 1) + l16][8 * (g16 ^ (2 * ((J + 1) & 1))) + 32 * (s ^ (((J + 1) >> 1) & 1))]);
+                    &sm.B[16 * (J + 1) + l16][8 * g16 + 32 * (s ^ ((J + 1) & 3))]);
         }
         M3_FENCE();
         sacc[J] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -408,7 +414,7 @@ __device__ __forceinline__ void out_block(const Smem& sm, const Tok& tk, const A
         const f32x4 g = *reinterpret_cast<const f32x4*>(&sm.mzd[p][0]);
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
-            const float z = (float)zraw[pt][tt];
+            const float z = bf16_f32(zraw[pt][tt]);
             const float e0 = 1.f + __builtin_amdgcn_exp2f(fminf(z * g[0], 60.f));
             const float e1 = 1.f + __builtin_amdgcn_exp2f(fminf(z * g[1], 60.f));
             const float num = (z * g[2]) * yacc[pt][2 * tt] * e1 + (z * g[3]) * yacc[pt][2 * tt + 1] * e0;
@@ -420,14 +426,16 @@ __device__ __forceinline__ void out_block(const Smem& sm, const Tok& tk, const A
 }
 
 // Pipelined chunk walk. Per chunk k:
-//   barrier -> M(k): state update G4 on chunk k's tiles; output block of chunk k;
-//              wave 0: token scalars of chunk k+2; every wave: element-wise preparation
-//              of chunk k+1 into registers (RoPE angles, rotated B~/C~/B~w, X); reads
-//              of chunk k+2 issued
+//   barrier -> M(k): reads of chunk k+1 issued; state update G4 on chunk k's tiles; output
+//              block of chunk k; element-wise preparation of chunk k+1 into registers
 //   barrier -> W(k+1): registers -> LDS tiles, bf16 copy of the state
-// The RoPE angle prefix over tokens is a scan across the lanes of one wave, so the
-// preparation needs no cross-wave traffic and overlaps the matrix work of the other
-// wave on the same SIMD. Waves w and w+4 (one SIMD) own output blocks w and 7-w.
+// Roles: SIMD s runs waves s and s+4. Wave s owns output block s (light: 1..4 causal
+// column blocks) and prepares the RoPE-rotated B~ / C~ / B~w tiles of pairs
+// 16s .. 16s+15; wave s+4 owns output block 7-s (heavy: 5..8 column blocks) and
+// prepares a quarter of the X^T tile; wave 7 also computes the token scalars. So each
+// SIMD carries the same matrix and element-wise work. The two roles run separate copies
+// of the loop (same barrier sequence), so their loop-carried registers are allocated
+// independently.
 template <bool kFull>
 __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
     __shared__ Smem sm;
@@ -454,7 +462,6 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
     const float dtb = a.prm.dt_bias[h];
 
     const int lane0 = tid & 63;
-    const float mx0 = a.prm.mimo_x[(h * P + lane0) * R], mx1 = a.prm.mimo_x[(h * P + lane0) * R + 1];
     if (kFull && tid < P) {
         const float z0 = a.prm.mimo_z[(h * P + tid) * R], z1 = a.prm.mimo_z[(h * P + tid) * R + 1];
         sm.mzd[tid][0] = -z0 * kLog2e;
@@ -468,7 +475,11 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
 #pragma unroll
     for (int pt = 0; pt < 4; ++pt) hacc[pt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    float phi_start = 0.f;  // absolute angle (radians) of this lane's pair at the segment start
+    // Preparation lanes of waves 0-3: pairs pa = 16 wave + 2 (lane%8) and pa+1, tokens
+    // 8 (lane/8) .. +7. phi_start: absolute angles (radians) of the two pairs at the
+    // segment start.
+    const int pa0 = 16 * (wv & 3) + 2 * (lane0 & 7);
+    float phi_start0 = 0.f, phi_start1 = 0.f;
     if (kFull && seg > 0) {
         // H = sum_i exp(sum_{l=i+1}^{seg-1} D_l) R(-sum_{l=i}^{seg-1} Phi_l) S_i
         const int g16 = lane0 >> 4, l16 = lane0 & 15;
@@ -500,162 +511,63 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
             dsum += a.seg_decay[sbase + i];
         }
         __syncthreads();
-        phi_start = sm.rot[8 * wv + (lane0 & 7)];  // sum_{l<seg} Phi_l
+        phi_start0 = sm.rot[pa0];  // sum_{l<seg} Phi_l
+        phi_start1 = sm.rot[pa0 + 1];
     }
 
     const bf16* proj_b = a.proj + (int64_t)b * T * a.rs;
     const bf16* bn_b = a.Bn + ((int64_t)b * T * a.G + grp) * NR;
     const bf16* cn_b = a.Cn + ((int64_t)b * T * a.G + grp) * NR;
 
-    // ---- wave 0: raw token scalars of one chunk (kept as bf16 until used)
-    bf16 sdt = (bf16)0.f, sdt64 = (bf16)0.f, slam = (bf16)0.f, slam64 = (bf16)0.f;
-    float ssc = 1.f, ssc64 = 1.f;
-    auto load_sc = [&](int kk) {
-        const int lane = opaque(threadIdx.x & 63);
-        const int s0 = kk * Q;
-        const __amdgpu_buffer_rsrc_t rp = make_rsrc(proj_b + (int64_t)s0 * a.rs, (int64_t)max(T - s0, 0) * a.rs * 2);
-        sdt = ld_bf16(rp, lane * rs + (int)a.pl.dt + h);
-        sdt64 = ld_bf16(rp, Q * rs + (int)a.pl.dt + h);
-        if (a.trap) {
-            slam = ld_bf16(rp, lane * rs + (int)a.pl.lam + h);
-            slam64 = ld_bf16(rp, Q * rs + (int)a.pl.lam + h);
-        }
-        if (a.dt_scale) {
-            ssc = a.dt_scale[((int64_t)b * T + min(s0 + lane, T - 1)) * a.H + h];
-            ssc64 = a.dt_scale[((int64_t)b * T + min(s0 + Q, T - 1)) * a.H + h];
-        }
-    };
-    // ---- wave 0: token scalars of chunk kk into its ring slot (mamba3/mamba3.py:200-216)
-    auto tok_scalars = [&](int kk) {
-        const int lane = opaque(threadIdx.x & 63);
-        const int s0 = kk * Q;
-        Tok& tk = sm.tok[kk % NSLOT];
-        const float dt = s0 + lane < T ? fast_softplus((float)sdt + dtb) * ssc : 0.f;
-        const float lam = a.trap ? __builtin_amdgcn_rcpf(1.f + fast_exp(-(float)slam)) : 1.f;
-        float dtn = __shfl_down(dt, 1, 64);
-        float lamn = __shfl_down(lam, 1, 64);
-        if (lane == 63) {
-            dtn = s0 + Q < T ? fast_softplus((float)sdt64 + dtb) * ssc64 : 0.f;
-            lamn = a.trap ? __builtin_amdgcn_rcpf(1.f + fast_exp(-(float)slam64)) : 1.f;
-        }
-        const float c2 = wave_incl_scan(A2 * dt, lane);
-        const float c2e = __shfl(c2, 63, 64);
-        const float c2b = __shfl(c2, lane | 7, 64);
-        const float av = a.trap ? lam * dt : dt;
-        const float bv = a.trap ? (1.f - lamn) * dtn : 0.f;
-        tk.c2[lane] = c2;
-        tk.av[lane] = av;
-        tk.bv[lane] = bv;
-        tk.ec[lane] = __builtin_amdgcn_exp2f(c2);
-        tk.hb[lane] = __builtin_amdgcn_exp2f(c2b - c2) * (av + bv);
-        tk.dtr[lane] = dt * 0.15915494309189535f;
-        tk.w[lane] = __builtin_amdgcn_exp2f(c2e - c2) * (av + bv);
-    };
+    float logdecay = 0.f;  // total log-decay of the segment (natural log)
+    float phi_run0 = 0.f, phi_run1 = 0.f;  // pair angles relative to the segment start, turns
 
-    // ---- raw tile inputs of one chunk (chunk-level descriptors end at the sequence end)
-    // Preparation role: pair pi = 8 wave + lane%8 for tokens 8q .. 8q+7 (q = lane/8);
-    // X role: column p = lane for tokens 8 wave .. 8 wave + 7.
-    u32x2 rawB[8], rawC[8];
-    bf16 rawth[8], rawx[8];
-    auto load_raw = [&](int kk) {
+    // ---- G4: H^T = e^{c_63} H^T + B~w^T X on chunk k's tiles (all waves)
+    auto state_update = [&](const Tok& tk) {
         const int lane = opaque(threadIdx.x & 63);
-        const int pi = 8 * wv + (lane & 7), q = lane >> 3;
-        const int s0 = kk * Q;
-        const int left = max(T - s0, 0);
-        const __amdgpu_buffer_rsrc_t rp = make_rsrc(proj_b + (int64_t)s0 * a.rs, (int64_t)left * a.rs * 2);
-        const int64_t bcbytes = left > 0 ? ((int64_t)(left - 1) * bnrs + NR) * 2 : 0;
-        const __amdgpu_buffer_rsrc_t rb = make_rsrc(bn_b + (int64_t)s0 * bnrs, bcbytes);
-        const __amdgpu_buffer_rsrc_t rc = make_rsrc(cn_b + (int64_t)s0 * bnrs, bcbytes);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int tl = 8 * q + j;
-            rawB[j] = __builtin_amdgcn_raw_buffer_load_b64(rb, (tl * bnrs + 4 * pi) * 2, 0, 0);
-            if (kFull) rawC[j] = __builtin_amdgcn_raw_buffer_load_b64(rc, (tl * bnrs + 4 * pi) * 2, 0, 0);
-            rawth[j] = a.cplx ? ld_bf16(rp, tl * rs + (int)a.pl.theta + pi) : (bf16)0.f;
-            rawx[j] = ld_bf16(rp, (8 * wv + j) * rs + (int)a.pl.x + h * P + lane);
-        }
-    };
-
-    // ---- element-wise preparation of chunk kk into registers
-    float phi_run = 0.f;  // angle of this lane's pair relative to the segment start, in turns
-    unsigned outB[8][2], outC[8][2];
-    u32x2 outBw[8];
-    bf16x8 outX0, outX1;
-    auto prep = [&](int kk) {
-        const int lane = opaque(threadIdx.x & 63);
-        const int q = lane >> 3;
-        const Tok& tk = sm.tok[kk % NSLOT];
-        const f32x4 d0 = *reinterpret_cast<const f32x4*>(&tk.dtr[8 * q]);
-        const f32x4 d1 = *reinterpret_cast<const f32x4*>(&tk.dtr[8 * q + 4]);
-        const f32x4 w0 = *reinterpret_cast<const f32x4*>(&tk.w[8 * q]);
-        const f32x4 w1 = *reinterpret_cast<const f32x4*>(&tk.w[8 * q + 4]);
-        // RoPE angle increments (turns) of tokens 8q..8q+7; prefix of the per-lane
-        // totals over q (lanes 8 apart) gives each lane's starting angle.
-        float inc[8];
-        float tot = 0.f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            inc[j] = (j < 4 ? d0[j] : d1[j - 4]) * (float)rawth[j];
-            tot += inc[j];
-        }
-        float incl = tot;
-#pragma unroll
-        for (int off = 8; off < 64; off <<= 1) {
-            const float o = __shfl_up(incl, off, 64);
-            if (lane >= off) incl += o;
-        }
-        const float ctot = __shfl(incl, 56 + (lane & 7), 64);
-        float phi = phi_run - (incl - tot);
-        phi_run -= ctot;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            phi -= inc[j];
-            const float rev = __builtin_amdgcn_fractf(phi);
-            const float sn = __builtin_amdgcn_sinf(rev), cs = __builtin_amdgcn_cosf(rev);
-            const unsigned k1 = pack_bf16x2(cs, -sn);
-            const unsigned k2 = pack_bf16x2(sn, cs);
-            const float be0 = dot2_bf16(rawB[j][0], k1), bo0 = dot2_bf16(rawB[j][0], k2);
-            const float be1 = dot2_bf16(rawB[j][1], k1), bo1 = dot2_bf16(rawB[j][1], k2);
-            if (kFull) {
-                outC[j][0] = pack_bf16x2(dot2_bf16(rawC[j][0], k1), dot2_bf16(rawC[j][0], k2));
-                outC[j][1] = pack_bf16x2(dot2_bf16(rawC[j][1], k1), dot2_bf16(rawC[j][1], k2));
-                outB[j][0] = pack_bf16x2(be0, bo0);
-                outB[j][1] = pack_bf16x2(be1, bo1);
-            }
-            const float wu = j < 4 ? w0[j] : w1[j - 4];
-            outBw[j] = u32x2{pack_bf16x2(be0 * wu, be1 * wu), pack_bf16x2(bo0 * wu, bo1 * wu)};
-        }
-        // X^T column p = lane for tokens 8 wave .. +7 (zero past the sequence end)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float x0 = (float)rawx[j], x1 = (float)rawx[4 + j];
-            outX0[2 * j] = (bf16)(x0 * mx0);
-            outX0[2 * j + 1] = (bf16)(x0 * mx1);
-            outX1[2 * j] = (bf16)(x1 * mx0);
-            outX1[2 * j + 1] = (bf16)(x1 * mx1);
-        }
-    };
-
-    // ---- registers -> LDS tiles of the prepared chunk, and the bf16 state copy
-    auto write_tiles = [&]() {
-        const int lane = opaque(threadIdx.x & 63);
-        const int pi = 8 * wv + (lane & 7), q = lane >> 3;
         const int g16 = lane >> 4, l16 = lane & 15;
+        const float dch = tk.ec[Q - 1];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int u = 8 * q + j;
-            if (kFull) {
-                const int col = sw_cb(2 * u, 2 * pi);
-                *reinterpret_cast<unsigned*>(&sm.C[2 * u][col]) = outC[j][0];
-                *reinterpret_cast<unsigned*>(&sm.C[2 * u + 1][col]) = outC[j][1];
-                *reinterpret_cast<unsigned*>(&sm.B[2 * u][col]) = outB[j][0];
-                *reinterpret_cast<unsigned*>(&sm.B[2 * u + 1][col]) = outB[j][1];
+        for (int pt = 0; pt < 4; ++pt) hacc[pt] *= dch;
+        const int ncol = 2 * (16 * wv + l16);
+        bf16x2 wop[2][4];
+        bf16x8 xop[2][4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) wop[0][j] = *reinterpret_cast<const bf16x2*>(&sm.Bw[4 * g16 + j][ncol]);
+#pragma unroll
+        for (int pt = 0; pt < 4; ++pt)
+            xop[0][pt] = *reinterpret_cast<const bf16x8*>(&sm.X[16 * pt + l16][8 * g16]);
+        M3_FENCE();
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            if (s + 1 < 4) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    wop[(s + 1) & 1][j] = *reinterpret_cast<const bf16x2*>(&sm.Bw[16 * (s + 1) + 4 * g16 + j][ncol]);
+#pragma unroll
+                for (int pt = 0; pt < 4; ++pt)
+                    xop[(s + 1) & 1][pt] =
+                        *reinterpret_cast<const bf16x8*>(&sm.X[16 * pt + l16][32 * (s + 1) + 8 * g16]);
             }
-            *reinterpret_cast<u32x2*>(&sm.Bw[u][sw_bw(u, 4 * pi)]) = outBw[j];
+            M3_FENCE();
+            bf16x8 aop;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                aop[2 * j] = wop[s & 1][j][0];
+                aop[2 * j + 1] = wop[s & 1][j][1];
+            }
+#pragma unroll
+            for (int pt = 0; pt < 4; ++pt) hacc[pt] = mfma16(aop, xop[s & 1][pt], hacc[pt]);
+            M3_FENCE();
         }
-        *reinterpret_cast<bf16x8*>(&sm.X[lane][16 * wv]) = outX0;
-        *reinterpret_cast<bf16x8*>(&sm.X[lane][16 * wv + 8]) = outX1;
+        logdecay += tk.c2[Q - 1] * (1.f / kLog2e);
+    };
+
+    // ---- bf16 copy of the state for G3 (all waves, W phase)
+    auto write_state = [&]() {
         if (kFull) {
+            const int lane = opaque(threadIdx.x & 63);
+            const int g16 = lane >> 4, l16 = lane & 15;
             const int n0 = 16 * wv + 4 * g16;
 #pragma unroll
             for (int pt = 0; pt < 4; ++pt) {
@@ -666,101 +578,275 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
         }
     };
 
-    float logdecay = 0.f;  // total log-decay of the segment (natural log)
+    auto role_loop = [&](auto role) {
+        constexpr bool kPrep = decltype(role)::value;
 
-    // ---- prologue: token scalars of the first two chunks, first chunk's tiles
-    if (wv == 0) {
-        load_sc(k_begin);
-        tok_scalars(k_begin);
-        if (k_begin + 1 < k_end) {
-            load_sc(k_begin + 1);
-            tok_scalars(k_begin + 1);
-        }
-        if (k_begin + 2 < k_end) load_sc(k_begin + 2);
-    }
-    load_raw(k_begin);
-    __syncthreads();
-    prep(k_begin);
-    if (k_begin + 1 < k_end) load_raw(k_begin + 1);
-    write_tiles();
-
-    for (int k = k_begin; k < k_end; ++k) {
-        const int s0 = k * Q;
-        const bool more = k + 1 < k_end;
-        __syncthreads();
-        const int lane = opaque(threadIdx.x & 63);
-        const int g16 = lane >> 4, l16 = lane & 15;
-        const Tok& tk = sm.tok[k % NSLOT];
-        // ---- M(k): state update G4: H^T = e^{c_63} H^T + B~w^T X on chunk k's tiles
-        {
-            const float dch = tk.ec[Q - 1];
+        // ---------------- preparation role (waves 0-3) ----------------
+        u32x4 rawB[8], rawC[8];
+        unsigned rawth[8];
+        u32x2 outB[8][2], outC[8][2];
+        u32x4 outBw[8];
+        auto load_prep = [&](int kk) {
+            const int lane = opaque(threadIdx.x & 63);
+            const int q = lane >> 3;
+            const int pa = 16 * (wv & 3) + 2 * (lane & 7);
+            const int s0 = kk * Q;
+            const int left = max(T - s0, 0);
+            const int64_t bcbytes = left > 0 ? ((int64_t)(left - 1) * bnrs + NR) * 2 : 0;
+            const __amdgpu_buffer_rsrc_t rb = make_rsrc(bn_b + (int64_t)s0 * bnrs, bcbytes);
+            const __amdgpu_buffer_rsrc_t rc = make_rsrc(cn_b + (int64_t)s0 * bnrs, bcbytes);
+            const int vbc = (8 * q * bnrs + 4 * pa) * 2;
 #pragma unroll
-            for (int pt = 0; pt < 4; ++pt) hacc[pt] *= dch;
-            const int n = 16 * wv + l16;
-            const int ncol = (2 * n) ^ (32 * (g16 >> 1));  // sw_bw for rows 16s + 4 g16 + j
-            bf16x2 wop[2][4];
-            bf16x8 xop[2][4];
+            for (int j = 0; j < 8; ++j) {
+                rawB[j] = __builtin_amdgcn_raw_buffer_load_b128(rb, vbc + j * bnrs * 2, 0, 0);
+                if (kFull) rawC[j] = __builtin_amdgcn_raw_buffer_load_b128(rc, vbc + j * bnrs * 2, 0, 0);
+            }
+            if (a.cplx) {
+                const __amdgpu_buffer_rsrc_t rp =
+                    make_rsrc(proj_b + (int64_t)s0 * a.rs, (int64_t)left * a.rs * 2);
+                const int vth = (8 * q * rs + (int)a.pl.theta + pa) * 2;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) wop[0][j] = *reinterpret_cast<const bf16x2*>(&sm.Bw[4 * g16 + j][ncol]);
+                for (int j = 0; j < 8; ++j) rawth[j] = __builtin_amdgcn_raw_buffer_load_b32(rp, vth + j * rs * 2, 0, 0);
+            } else {
 #pragma unroll
-            for (int pt = 0; pt < 4; ++pt)
-                xop[0][pt] = *reinterpret_cast<const bf16x8*>(&sm.X[16 * pt + l16][8 * g16]);
-            M3_FENCE();
+                for (int j = 0; j < 8; ++j) rawth[j] = 0u;
+            }
+        };
+        auto prep = [&](int kk) {
+            const int lane = opaque(threadIdx.x & 63);
+            const int q = lane >> 3;
+            const float zero = __builtin_bit_cast(float, opaque(0));
+            const Tok& tk = sm.tok[kk % NSLOT];
+            const f32x4 d0 = *reinterpret_cast<const f32x4*>(&tk.dtr[8 * q]);
+            const f32x4 d1 = *reinterpret_cast<const f32x4*>(&tk.dtr[8 * q + 4]);
+            const f32x4 w0 = *reinterpret_cast<const f32x4*>(&tk.w[8 * q]);
+            const f32x4 w1 = *reinterpret_cast<const f32x4*>(&tk.w[8 * q + 4]);
+            // RoPE angle increments (turns) of tokens 8q..8q+7 for both pairs; the prefix of
+            // the per-lane totals over q (lanes 8 apart) gives each lane's starting angles.
+            float inc0[8], inc1[8];
+            float tot0 = 0.f, tot1 = 0.f;
 #pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                if (s + 1 < 4) {
+            for (int j = 0; j < 8; ++j) {
+                const float dt = j < 4 ? d0[j] : d1[j - 4];
+                inc0[j] = dt * __builtin_bit_cast(float, rawth[j] << 16);
+                inc1[j] = dt * __builtin_bit_cast(float, rawth[j] & 0xffff0000u);
+                tot0 += inc0[j];
+                tot1 += inc1[j];
+            }
+            float incl0 = tot0, incl1 = tot1;
 #pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        wop[(s + 1) & 1][j] =
-                            *reinterpret_cast<const bf16x2*>(&sm.Bw[16 * (s + 1) + 4 * g16 + j][ncol]);
-#pragma unroll
-                    for (int pt = 0; pt < 4; ++pt)
-                        xop[(s + 1) & 1][pt] =
-                            *reinterpret_cast<const bf16x8*>(&sm.X[16 * pt + l16][32 * (s + 1) + 8 * g16]);
+            for (int off = 8; off < 64; off <<= 1) {
+                const float o0 = __shfl_up(incl0, off, 64);
+                const float o1 = __shfl_up(incl1, off, 64);
+                if (lane >= off) {
+                    incl0 += o0;
+                    incl1 += o1;
                 }
-                M3_FENCE();
-                bf16x8 aop;
+            }
+            const float ctot0 = __shfl(incl0, 56 + (lane & 7), 64);
+            const float ctot1 = __shfl(incl1, 56 + (lane & 7), 64);
+            float phi0 = phi_run0 - (incl0 - tot0);
+            float phi1 = phi_run1 - (incl1 - tot1);
+            phi_run0 -= ctot0;
+            phi_run1 -= ctot1;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float wu = j < 4 ? w0[j] : w1[j - 4];
+                float be[2][2], bo[2][2];  // [pair][rank]
+#pragma unroll
+                for (int pr = 0; pr < 2; ++pr) {
+                    float& phi = pr == 0 ? phi0 : phi1;
+                    phi -= pr == 0 ? inc0[j] : inc1[j];
+                    const float rev = __builtin_amdgcn_fractf(phi);
+                    const float sn = __builtin_amdgcn_sinf(rev), cs = __builtin_amdgcn_cosf(rev);
+                    const unsigned k1 = pack_bf16x2(cs, -sn);
+                    const unsigned k2 = pack_bf16x2(sn, cs);
+                    const unsigned b0 = rawB[j][2 * pr], b1 = rawB[j][2 * pr + 1];
+                    be[pr][0] = dot2_bf16(b0, k1, zero);
+                    bo[pr][0] = dot2_bf16(b0, k2, zero);
+                    be[pr][1] = dot2_bf16(b1, k1, zero);
+                    bo[pr][1] = dot2_bf16(b1, k2, zero);
+                    if (kFull) {
+                        const unsigned c0 = rawC[j][2 * pr], c1 = rawC[j][2 * pr + 1];
+                        outC[j][0][pr] = pack_bf16x2(dot2_bf16(c0, k1, zero), dot2_bf16(c0, k2, zero));
+                        outC[j][1][pr] = pack_bf16x2(dot2_bf16(c1, k1, zero), dot2_bf16(c1, k2, zero));
+                    }
+                }
+                if (kFull) {
+                    outB[j][0] = u32x2{pack_bf16x2(be[0][0], bo[0][0]), pack_bf16x2(be[1][0], bo[1][0])};
+                    outB[j][1] = u32x2{pack_bf16x2(be[0][1], bo[0][1]), pack_bf16x2(be[1][1], bo[1][1])};
+                }
+                outBw[j] = u32x4{pack_bf16x2(be[0][0] * wu, be[0][1] * wu), pack_bf16x2(bo[0][0] * wu, bo[0][1] * wu),
+                                 pack_bf16x2(be[1][0] * wu, be[1][1] * wu), pack_bf16x2(bo[1][0] * wu, bo[1][1] * wu)};
+            }
+        };
+        auto write_prep = [&]() {
+            const int lane = opaque(threadIdx.x & 63);
+            const int q = lane >> 3;
+            const int pa = 16 * (wv & 3) + 2 * (lane & 7);
+            const int col = sw_cb(16 * q, 2 * pa);  // rows 16q .. 16q+15 share the swizzle
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                if (kFull) {
+                    *reinterpret_cast<u32x2*>(&sm.C[16 * q + 2 * j][col]) = outC[j][0];
+                    *reinterpret_cast<u32x2*>(&sm.C[16 * q + 2 * j + 1][col]) = outC[j][1];
+                    *reinterpret_cast<u32x2*>(&sm.B[16 * q + 2 * j][col]) = outB[j][0];
+                    *reinterpret_cast<u32x2*>(&sm.B[16 * q + 2 * j + 1][col]) = outB[j][1];
+                }
+                *reinterpret_cast<u32x4*>(&sm.Bw[8 * q + j][4 * pa]) = outBw[j];
+            }
+        };
+
+        // ---------------- X / token-scalar role (waves 4-7) ----------------
+        unsigned rawx[16];
+        bf16x8 outX[4];
+        unsigned sdt = 0u, sdt64 = 0u, slam = 0u, slam64 = 0u;
+        float ssc = 1.f, ssc64 = 1.f;
+        const float mx0 = a.prm.mimo_x[(h * P + lane0) * R], mx1 = a.prm.mimo_x[(h * P + lane0) * R + 1];
+        auto load_x = [&](int kk) {
+            // X role: column p = lane for tokens 16 (wave-4) .. +15
+            const int lane = opaque(threadIdx.x & 63);
+            const int s0 = kk * Q;
+            const __amdgpu_buffer_rsrc_t rp = make_rsrc(proj_b + (int64_t)s0 * a.rs, (int64_t)max(T - s0, 0) * a.rs * 2);
+            const int vx = (16 * (wv - 4) * rs + (int)a.pl.x + h * P + lane) * 2;
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+                rawx[j] = ld_u16(rp, vx + j * rs * 2);
+        };
+        auto prep_x = [&]() {
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    aop[2 * j] = wop[s & 1][j][0];
-                    aop[2 * j + 1] = wop[s & 1][j][1];
+                    const float x = bf16_f32(rawx[4 * c + j]);
+                    outX[c][2 * j] = (bf16)(x * mx0);
+                    outX[c][2 * j + 1] = (bf16)(x * mx1);
                 }
+        };
+        auto write_x = [&]() {
+            const int lane = opaque(threadIdx.x & 63);
 #pragma unroll
-                for (int pt = 0; pt < 4; ++pt) hacc[pt] = mfma16(aop, xop[s & 1][pt], hacc[pt]);
-                M3_FENCE();
+            for (int c = 0; c < 4; ++c)
+                *reinterpret_cast<bf16x8*>(&sm.X[lane][32 * (wv - 4) + 8 * c]) = outX[c];
+        };
+        auto load_sc = [&](int kk) {
+            const int lane = opaque(threadIdx.x & 63);
+            const int s0 = kk * Q;
+            const __amdgpu_buffer_rsrc_t rp = make_rsrc(proj_b + (int64_t)s0 * a.rs, (int64_t)max(T - s0, 0) * a.rs * 2);
+            sdt = ld_u16(rp, (lane * rs + (int)a.pl.dt + h) * 2);
+            sdt64 = ld_u16(rp, (Q * rs + (int)a.pl.dt + h) * 2);
+            if (a.trap) {
+                slam = ld_u16(rp, (lane * rs + (int)a.pl.lam + h) * 2);
+                slam64 = ld_u16(rp, (Q * rs + (int)a.pl.lam + h) * 2);
             }
-            logdecay += tk.c2[Q - 1] * (1.f / kLog2e);
-        }
-        // ---- M(k): output block of chunk k
-        if (kFull) {
-            switch (wv) {
-                case 0: out_block<0>(sm, tk, a, proj_b, b, h, s0, g16, l16, D_h); break;
-                case 1: out_block<1>(sm, tk, a, proj_b, b, h, s0, g16, l16, D_h); break;
-                case 2: out_block<2>(sm, tk, a, proj_b, b, h, s0, g16, l16, D_h); break;
-                case 3: out_block<3>(sm, tk, a, proj_b, b, h, s0, g16, l16, D_h); break;
-                case 4: out_block<7>(sm, tk, a, proj_b, b, h, s0, g16, l16, D_h); break;
-                case 5: out_block<6>(sm, tk, a, proj_b, b, h, s0, g16, l16, D_h); break;
-                case 6: out_block<5>(sm, tk, a, proj_b, b, h, s0, g16, l16, D_h); break;
-                default: out_block<4>(sm, tk, a, proj_b, b, h, s0, g16, l16, D_h); break;
+            if (a.dt_scale) {
+                ssc = a.dt_scale[((int64_t)b * T + min(s0 + lane, T - 1)) * a.H + h];
+                ssc64 = a.dt_scale[((int64_t)b * T + min(s0 + Q, T - 1)) * a.H + h];
+            }
+        };
+        // token scalars of chunk kk into its ring slot (mamba3/mamba3.py:200-216)
+        auto tok_scalars = [&](int kk) {
+            const int lane = opaque(threadIdx.x & 63);
+            const int s0 = kk * Q;
+            Tok& tk = sm.tok[kk % NSLOT];
+            const float dt = s0 + lane < T ? fast_softplus(bf16_f32(sdt) + dtb) * ssc : 0.f;
+            const float lam = a.trap ? __builtin_amdgcn_rcpf(1.f + fast_exp(-bf16_f32(slam))) : 1.f;
+            float dtn = __shfl_down(dt, 1, 64);
+            float lamn = __shfl_down(lam, 1, 64);
+            if (lane == 63) {
+                dtn = s0 + Q < T ? fast_softplus(bf16_f32(sdt64) + dtb) * ssc64 : 0.f;
+                lamn = a.trap ? __builtin_amdgcn_rcpf(1.f + fast_exp(-bf16_f32(slam64))) : 1.f;
+            }
+            const float c2 = wave_incl_scan(A2 * dt, lane);
+            const float c2e = __shfl(c2, 63, 64);
+            const float c2b = __shfl(c2, lane | 7, 64);
+            const float av = a.trap ? lam * dt : dt;
+            const float bv = a.trap ? (1.f - lamn) * dtn : 0.f;
+            tk.c2[lane] = c2;
+            tk.av[lane] = av;
+            tk.bv[lane] = bv;
+            tk.ec[lane] = __builtin_amdgcn_exp2f(c2);
+            tk.hb[lane] = __builtin_amdgcn_exp2f(c2b - c2) * (av + bv);
+            tk.dtr[lane] = dt * 0.15915494309189535f;
+            tk.w[lane] = __builtin_amdgcn_exp2f(c2e - c2) * (av + bv);
+        };
+        constexpr int kTokWave = 7;
+
+        // ---------------- prologue: first chunk ----------------
+        if (kPrep) {
+            load_prep(k_begin);
+        } else {
+            load_x(k_begin);
+            if (wv == kTokWave) {
+                load_sc(k_begin);
+                tok_scalars(k_begin);
+                if (k_begin + 1 < k_end) {
+                    load_sc(k_begin + 1);
+                    tok_scalars(k_begin + 1);
+                }
+                if (k_begin + 2 < k_end) load_sc(k_begin + 2);
             }
         }
-        // ---- M(k): token scalars of chunk k+2 (wave 0, lightest output block)
-        if (wv == 0) {
-            if (k + 2 < k_end) tok_scalars(k + 2);
-            if (k + 3 < k_end) load_sc(k + 3);
+        __syncthreads();
+        if (kPrep) {
+            prep(k_begin);
+            write_prep();
+        } else {
+            prep_x();
+            write_x();
         }
-        // ---- M(k): prepare chunk k+1, start reading chunk k+2; W(k+1)
-        if (more) {
-            prep(k + 1);
-            if (k + 2 < k_end) load_raw(k + 2);
+        write_state();
+
+        // ---------------- chunk loop ----------------
+        // Reads of chunk k+1 are issued right after the barrier that opens M(k), so they are
+        // in flight during the state update and the output block and only live within M(k).
+        for (int k = k_begin; k < k_end; ++k) {
+            const int s0 = k * Q;
+            const bool more = k + 1 < k_end;
             __syncthreads();
-            write_tiles();
+            if (more) {
+                if (kPrep) load_prep(k + 1);
+                else load_x(k + 1);
+            }
+            const Tok& tk = sm.tok[k % NSLOT];
+            state_update(tk);
+            if (kFull) {
+                const int lane = opaque(threadIdx.x & 63);
+                const int g16 = lane >> 4, l16 = lane & 15;
+                if (kPrep) {
+                    switch (wv) {
+                        case 0: out_block<0>(sm, tk, a, proj_b, b, h, s0, g16, l16, D_h); break;
+                        case 1: out_block<1>(sm, tk, a, proj_b, b, h, s0, g16, l16, D_h); break;
+                        case 2: out_block<2>(sm, tk, a, proj_b, b, h, s0, g16, l16, D_h); break;
+                        default: out_block<3>(sm, tk, a, proj_b, b, h, s0, g16, l16, D_h); break;
+                    }
+                } else {
+                    switch (wv) {
+                        case 4: out_block<7>(sm, tk, a, proj_b, b, h, s0, g16, l16, D_h); break;
+                        case 5: out_block<6>(sm, tk, a, proj_b, b, h, s0, g16, l16, D_h); break;
+                        case 6: out_block<5>(sm, tk, a, proj_b, b, h, s0, g16, l16, D_h); break;
+                        default: out_block<4>(sm, tk, a, proj_b, b, h, s0, g16, l16, D_h); break;
+                    }
+                }
+            }
+            if (!kPrep && wv == kTokWave) {
+                if (k + 2 < k_end) tok_scalars(k + 2);
+                if (k + 3 < k_end) load_sc(k + 3);
+            }
+            if (more) {
+                if (kPrep) prep(k + 1);
+                else prep_x();
+                __syncthreads();
+                if (kPrep) write_prep(); else write_x();
+                write_state();
+            }
         }
-    }
+    };
+    if (wv < 4) role_loop(std::true_type{});
+    else role_loop(std::false_type{});
 
     // ---- segment end
-    const int pi_out = 8 * wv + (lane0 & 7);
-    const bool pair_lane = (lane0 >> 3) == 0;  // lanes 0..7 of each wave cover the 64 pairs
+    const bool pair_lane = wv < 4 && (lane0 >> 3) == 0;  // lanes 0..7 of waves 0-3: pairs pa0, pa0+1
     if (!kFull) {
         const int g16 = lane0 >> 4, l16 = lane0 & 15;
         const int64_t sidx = (int64_t)bh * (a.S - 1) + seg;
@@ -771,12 +857,19 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
 #pragma unroll
             for (int v = 0; v < 4; ++v) out[(n0 + v) * P + 16 * pt + l16] = hacc[pt][v];
         if (tid == 0) a.seg_decay[sidx] = logdecay;
-        if (pair_lane) a.seg_angle[sidx * NH + pi_out] = phi_run * 6.283185307179586f;
+        if (pair_lane) {
+            a.seg_angle[sidx * NH + pa0] = phi_run0 * 6.283185307179586f;
+            a.seg_angle[sidx * NH + pa0 + 1] = phi_run1 * 6.283185307179586f;
+        }
     } else if (seg == a.S - 1) {
         __syncthreads();
         if (pair_lane) {
-            sm.rot[pi_out] = phi_start;
-            if (a.angle) a.angle[(int64_t)bh * NH + pi_out] = a.cplx ? phi_start + phi_run * 6.283185307179586f : 0.f;
+            sm.rot[pa0] = phi_start0;
+            sm.rot[pa0 + 1] = phi_start1;
+            if (a.angle) {
+                a.angle[(int64_t)bh * NH + pa0] = a.cplx ? phi_start0 + phi_run0 * 6.283185307179586f : 0.f;
+                a.angle[(int64_t)bh * NH + pa0 + 1] = a.cplx ? phi_start1 + phi_run1 * 6.283185307179586f : 0.f;
+            }
         }
         __syncthreads();
         if (a.h_final) {
@@ -823,7 +916,7 @@ bool mfma_prefill_supported(const m3_layer_desc& d, const void* proj) {
     if (d.dtype != M3_DTYPE_BF16) return false;
     if (d.d_state != mf::N || d.headdim != mf::P || d.mimo_rank != mf::R) return false;
     const ProjLayout pl = proj_layout(d);
-    if (d.proj_row_stride % 4 != 0 || pl.B % 4 != 0 || pl.C % 4 != 0) return false;
+    if (d.proj_row_stride % 4 != 0 || pl.B % 4 != 0 || pl.C % 4 != 0 || pl.theta % 2 != 0) return false;
     if (reinterpret_cast<uintptr_t>(proj) % 8 != 0) return false;
     // 32-bit buffer offsets: one batch row of proj (and of B^/C^) stays below 2 GiB.
     if ((int64_t)(d.seqlen + 1) * d.proj_row_stride * 2 >= ((int64_t)1 << 31)) return false;
