@@ -73,10 +73,11 @@ int m3_scan_fwd(const float* decay, const float* h_chunk, const float* h_init,
 }
 
 // Workspace for whichever prefill kernel the shape may dispatch to (the MFMA path is
-// chosen for bf16 layers with d_state 128, headdim 64, mimo_rank 2 and aligned rows).
+// chosen for bf16 layers with d_state 128, headdim 64, mimo_rank 2, aligned rows and
+// 16-byte aligned proj / y_out).
 static size_t prefill_workspace(const m3_layer_desc& d) {
     size_t n = m3::generic_prefill_workspace(d);
-    if (m3::mfma_prefill_supported(d, nullptr)) n = std::max(n, m3::mfma_prefill_workspace(d));
+    if (m3::mfma_prefill_supported(d, nullptr, nullptr)) n = std::max(n, m3::mfma_prefill_workspace(d));
     return n;
 }
 
@@ -96,7 +97,7 @@ int m3_prefill_fwd(const m3_layer_desc* desc, const m3_layer_params* params, con
     st = check_params(params);
     if (st != M3_OK) return st;
     if (!proj || !y_out) return M3_ERR_NULL_POINTER;
-    if (m3::mfma_prefill_supported(*desc, proj)) {
+    if (m3::mfma_prefill_supported(*desc, proj, y_out)) {
         if (!workspace || workspace_bytes < m3::mfma_prefill_workspace(*desc))
             return M3_ERR_WORKSPACE;
         if (!aligned(workspace, 256)) return M3_ERR_MISALIGNED;

@@ -50,7 +50,7 @@ int launch_generic_chunked(int B, int T, int H, int P, int N, int R, int dtype,
                            float* state_ws, hipStream_t stream);
 
 // bf16 MFMA fused prefill for d_state 128, headdim 64, mimo_rank 2.
-bool mfma_prefill_supported(const m3_layer_desc& d, const void* proj);
+bool mfma_prefill_supported(const m3_layer_desc& d, const void* proj, const void* y_out);
 size_t mfma_prefill_workspace(const m3_layer_desc& d);
 int launch_mfma_prefill(const m3_layer_desc& d, const m3_layer_params& p, const void* proj,
                         const float* dt_scale, void* y_out, float* h_final, float* angle,

@@ -90,6 +90,8 @@ struct __align__(16) Smem {
     bf16 Bw[Q][NR + PAD];    // B~ * w_u, [u][n][r'] order
     bf16 X[P][Q * R + PAD];  // X^T
     bf16 H[P][N + PAD];      // incoming state, bf16
+    bf16 ZY[Q][P];           // z of the chunk, overwritten in place by its gated output y;
+                             // 16-byte chunks swizzled (zy_col)
     Tok tok[NSLOT];
     float rot[NH];           // per-pair angle scratch (prologue / epilogue)
     float mzd[P][4];         // per p: -mimo_z[0] log2e, -mimo_z[1] log2e, mimo_down*mimo_z [0], [1]
@@ -187,6 +189,10 @@ __device__ __forceinline__ float dot2_bf16(unsigned a, unsigned b, float zero) {
 // block, so the preparation's 64-bit stores (lanes 16 rows apart) hit distinct banks.
 // MFMA operand reads cover 16 rows of one block, so their pattern is only permuted.
 __device__ __forceinline__ int sw_cb(int row, int col) { return col ^ (32 * ((row >> 4) & 3)); }
+// ZY tile: column of 16-byte chunk c of token row t. Swapping chunk pairs on every other
+// token pair keeps both the 128-bit staging accesses and the epilogue's 16-bit accesses
+// (rows 2 apart across lanes) free of bank conflicts.
+__device__ __forceinline__ int zy_col(int t, int c) { return 8 * (c ^ (2 * ((t >> 1) & 1))); }
 
 
 __device__ __forceinline__ unsigned pack_bf16x2(float lo, float hi) {
@@ -252,20 +258,7 @@ __global__ __launch_bounds__(256) void bc_norm(const bf16* __restrict__ proj, in
 #define M3_FENCE() __builtin_amdgcn_sched_barrier(0)
 
 template <int I>
-__device__ __forceinline__ void out_block(const Smem& sm, const Tok& tk, const Args& a, const bf16* proj_b,
-                                          int b, int h, int s0, int g16, int l16, float D_h) {
-    const int T = a.T;
-    const int rs = (int)a.rs;
-    const int HP = a.H * P;
-    const int tblk = s0 + 8 * I;
-    const int left = max(T - tblk, 0);
-    const __amdgpu_buffer_rsrc_t rz = make_rsrc(proj_b + (int64_t)tblk * a.rs, (int64_t)left * a.rs * 2);
-    unsigned zraw[4][2];
-#pragma unroll
-    for (int pt = 0; pt < 4; ++pt)
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
-            zraw[pt][tt] = ld_u16(rz, ((2 * g16 + tt) * rs + (int)a.pl.z + h * P + 16 * pt + l16) * 2);
+__device__ __forceinline__ void out_block(Smem& sm, const Tok& tk, int g16, int l16, float D_h) {
 
     constexpr int NJ = I + 1;
     // Token scalars this lane needs (rows t_col, columns u = 8J + 2 g16 + {0,1}).
@@ -405,34 +398,33 @@ __device__ __forceinline__ void out_block(const Smem& sm, const Tok& tk, const A
 
     // Gate: out = sum_r mimo_down_r y_r silu(z mimo_z_r), with
     // silu(v0) y0' + silu(v1) y1' = (v0 y0' (1+e1) + v1 y1' (1+e0)) / ((1+e0)(1+e1)),
-    // e_r = exp(-v_r) clamped at 2^60 so the product stays finite.
-    // The store descriptor ends at the last token, so padding rows drop.
-    const __amdgpu_buffer_rsrc_t ry = make_rsrc(a.y_out + ((int64_t)b * T + tblk) * HP, (int64_t)left * HP * 2);
+    // e_r = exp(-v_r) clamped at 2^60 so the product stays finite. z is read from the ZY
+    // tile and the output overwrites it in place (stored to HBM by the whole workgroup).
 #pragma unroll
     for (int pt = 0; pt < 4; ++pt) {
         const int p = 16 * pt + l16;
         const f32x4 g = *reinterpret_cast<const f32x4*>(&sm.mzd[p][0]);
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
-            const float z = bf16_f32(zraw[pt][tt]);
+            const int t = 8 * I + 2 * g16 + tt;
+            bf16* zy = &sm.ZY[t][zy_col(t, p >> 3) + (p & 7)];
+            const float z = (float)*zy;
             const float e0 = 1.f + __builtin_amdgcn_exp2f(fminf(z * g[0], 60.f));
             const float e1 = 1.f + __builtin_amdgcn_exp2f(fminf(z * g[1], 60.f));
             const float num = (z * g[2]) * yacc[pt][2 * tt] * e1 + (z * g[3]) * yacc[pt][2 * tt + 1] * e0;
-            const float out = num * __builtin_amdgcn_rcpf(e0 * e1);
-            __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, (bf16)out), ry,
-                                                  ((2 * g16 + tt) * HP + h * P + p) * 2, 0, 0);
+            *zy = (bf16)(num * __builtin_amdgcn_rcpf(e0 * e1));
         }
     }
 }
 
 // Pipelined chunk walk. Per chunk k:
-//   barrier -> M(k): reads of chunk k+1 issued; state update G4 on chunk k's tiles; output
+//   barrier -> M(k): state update G4 on chunk k's tiles; reads of chunk k+1 issued; output
 //              block of chunk k; element-wise preparation of chunk k+1 into registers
 //   barrier -> W(k+1): registers -> LDS tiles, bf16 copy of the state
 // Roles: SIMD s runs waves s and s+4. Wave s owns output block s (light: 1..4 causal
 // column blocks) and prepares the RoPE-rotated B~ / C~ / B~w tiles of pairs
 // 16s .. 16s+15; wave s+4 owns output block 7-s (heavy: 5..8 column blocks) and
-// prepares a quarter of the X^T tile; wave 7 also computes the token scalars. So each
+// prepares a quarter of the X^T tile; wave 0 also computes the token scalars. So each
 // SIMD carries the same matrix and element-wise work. The two roles run separate copies
 // of the loop (same barrier sequence), so their loop-carried registers are allocated
 // independently.
@@ -576,6 +568,30 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
                     bf16x4{(bf16)v[0], (bf16)v[1], (bf16)v[2], (bf16)v[3]};
             }
         }
+    };
+
+    // ---- ZY staging (all 512 lanes, one 16-byte chunk each: token t = tid/8, chunk tid%8):
+    // z of chunk kk is read from HBM into a register during the preceding M phase and
+    // written to ZY in the W phase, right after the same lane has stored the previous
+    // chunk's y from the same LDS address.
+    u32x4 zreg = u32x4{0u, 0u, 0u, 0u};
+    auto load_z = [&](int kk) {
+        const int t = opaque(threadIdx.x) >> 3, c = threadIdx.x & 7;
+        const int s0 = kk * Q;
+        const __amdgpu_buffer_rsrc_t rz = make_rsrc(proj_b + (int64_t)s0 * a.rs, (int64_t)max(T - s0, 0) * a.rs * 2);
+        zreg = __builtin_amdgcn_raw_buffer_load_b128(rz, (t * rs + (int)a.pl.z + h * P + 8 * c) * 2, 0, 0);
+    };
+    auto zy_exchange = [&](int k_prev, bool store_prev, bool write_next) {
+        const int t = opaque(threadIdx.x) >> 3, c = threadIdx.x & 7;
+        u32x4* cell = reinterpret_cast<u32x4*>(&sm.ZY[t][zy_col(t, c)]);
+        if (store_prev) {
+            const int s0 = k_prev * Q;
+            const int HP = a.H * P;
+            const __amdgpu_buffer_rsrc_t ry =
+                make_rsrc(a.y_out + ((int64_t)b * T + s0) * HP, (int64_t)max(T - s0, 0) * HP * 2);
+            __builtin_amdgcn_raw_buffer_store_b128(*cell, ry, (t * HP + h * P + 8 * c) * 2, 0, 0);
+        }
+        if (write_next) *cell = zreg;
     };
 
     auto role_loop = [&](auto role) {
@@ -770,22 +786,20 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
             tk.dtr[lane] = dt * 0.15915494309189535f;
             tk.w[lane] = __builtin_amdgcn_exp2f(c2e - c2) * (av + bv);
         };
-        constexpr int kTokWave = 7;
+        constexpr int kTokWave = 0;  // lightest output block
 
         // ---------------- prologue: first chunk ----------------
-        if (kPrep) {
-            load_prep(k_begin);
-        } else {
-            load_x(k_begin);
-            if (wv == kTokWave) {
-                load_sc(k_begin);
-                tok_scalars(k_begin);
-                if (k_begin + 1 < k_end) {
-                    load_sc(k_begin + 1);
-                    tok_scalars(k_begin + 1);
-                }
-                if (k_begin + 2 < k_end) load_sc(k_begin + 2);
+        if (kFull) load_z(k_begin);
+        if (kPrep) load_prep(k_begin);
+        else load_x(k_begin);
+        if (wv == kTokWave) {
+            load_sc(k_begin);
+            tok_scalars(k_begin);
+            if (k_begin + 1 < k_end) {
+                load_sc(k_begin + 1);
+                tok_scalars(k_begin + 1);
             }
+            if (k_begin + 2 < k_end) load_sc(k_begin + 2);
         }
         __syncthreads();
         if (kPrep) {
@@ -796,40 +810,43 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
             write_x();
         }
         write_state();
+        if (kFull) zy_exchange(k_begin, false, true);
 
         // ---------------- chunk loop ----------------
-        // Reads of chunk k+1 are issued right after the barrier that opens M(k), so they are
-        // in flight during the state update and the output block and only live within M(k).
+        // Reads of chunk k+1 are issued after the state update of M(k) (the waves reach that
+        // point at different times, which spreads the requests), so they are in flight during
+        // the output block and live only within M(k).
         for (int k = k_begin; k < k_end; ++k) {
             const int s0 = k * Q;
             const bool more = k + 1 < k_end;
             __syncthreads();
+            const Tok& tk = sm.tok[k % NSLOT];
+            state_update(tk);
             if (more) {
+                if (kFull) load_z(k + 1);
                 if (kPrep) load_prep(k + 1);
                 else load_x(k + 1);
             }
-            const Tok& tk = sm.tok[k % NSLOT];
-            state_update(tk);
             if (kFull) {
                 const int lane = opaque(threadIdx.x & 63);
                 const int g16 = lane >> 4, l16 = lane & 15;
                 if (kPrep) {
                     switch (wv) {
-                        case 0: out_block<0>(sm, tk, a, proj_b, b, h, s0, g16, l16, D_h); break;
-                        case 1: out_block<1>(sm, tk, a, proj_b, b, h, s0, g16, l16, D_h); break;
-                        case 2: out_block<2>(sm, tk, a, proj_b, b, h, s0, g16, l16, D_h); break;
-                        default: out_block<3>(sm, tk, a, proj_b, b, h, s0, g16, l16, D_h); break;
+                        case 0: out_block<0>(sm, tk, g16, l16, D_h); break;
+                        case 1: out_block<1>(sm, tk, g16, l16, D_h); break;
+                        case 2: out_block<2>(sm, tk, g16, l16, D_h); break;
+                        default: out_block<3>(sm, tk, g16, l16, D_h); break;
                     }
                 } else {
                     switch (wv) {
-                        case 4: out_block<7>(sm, tk, a, proj_b, b, h, s0, g16, l16, D_h); break;
-                        case 5: out_block<6>(sm, tk, a, proj_b, b, h, s0, g16, l16, D_h); break;
-                        case 6: out_block<5>(sm, tk, a, proj_b, b, h, s0, g16, l16, D_h); break;
-                        default: out_block<4>(sm, tk, a, proj_b, b, h, s0, g16, l16, D_h); break;
+                        case 4: out_block<7>(sm, tk, g16, l16, D_h); break;
+                        case 5: out_block<6>(sm, tk, g16, l16, D_h); break;
+                        case 6: out_block<5>(sm, tk, g16, l16, D_h); break;
+                        default: out_block<4>(sm, tk, g16, l16, D_h); break;
                     }
                 }
             }
-            if (!kPrep && wv == kTokWave) {
+            if (wv == kTokWave) {
                 if (k + 2 < k_end) tok_scalars(k + 2);
                 if (k + 3 < k_end) load_sc(k + 3);
             }
@@ -839,7 +856,12 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
                 __syncthreads();
                 if (kPrep) write_prep(); else write_x();
                 write_state();
+                if (kFull) zy_exchange(k, true, true);
             }
+        }
+        if (kFull) {
+            __syncthreads();
+            zy_exchange(k_end - 1, true, false);
         }
     };
     if (wv < 4) role_loop(std::true_type{});
@@ -912,12 +934,14 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
 
 }  // namespace mf
 
-bool mfma_prefill_supported(const m3_layer_desc& d, const void* proj) {
+bool mfma_prefill_supported(const m3_layer_desc& d, const void* proj, const void* y_out) {
     if (d.dtype != M3_DTYPE_BF16) return false;
     if (d.d_state != mf::N || d.headdim != mf::P || d.mimo_rank != mf::R) return false;
     const ProjLayout pl = proj_layout(d);
-    if (d.proj_row_stride % 4 != 0 || pl.B % 4 != 0 || pl.C % 4 != 0 || pl.theta % 2 != 0) return false;
-    if (reinterpret_cast<uintptr_t>(proj) % 8 != 0) return false;
+    // 128-bit z loads and y stores, 32-bit theta loads.
+    if (d.proj_row_stride % 8 != 0 || pl.z % 8 != 0 || pl.theta % 2 != 0) return false;
+    if (reinterpret_cast<uintptr_t>(proj) % 16 != 0 || reinterpret_cast<uintptr_t>(y_out) % 16 != 0)
+        return false;
     // 32-bit buffer offsets: one batch row of proj (and of B^/C^) stays below 2 GiB.
     if ((int64_t)(d.seqlen + 1) * d.proj_row_stride * 2 >= ((int64_t)1 << 31)) return false;
     if ((int64_t)(d.seqlen + 1) * d.ngroups * mf::NR * 2 >= ((int64_t)1 << 31)) return false;
