@@ -67,11 +67,20 @@ constexpr int kRsrcFlags = 0x00020000;
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+// MFMA operand tiles are f16: same dense rate as bf16 on gfx950, three more mantissa
+// bits, and packed f16 arithmetic for the RoPE rotation.
+typedef _Float16 f16;
+typedef f16 f16x8 __attribute__((ext_vector_type(8)));
+typedef f16 f16x4 __attribute__((ext_vector_type(4)));
+typedef f16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int NSLOT = 3;  // token-scalar ring: chunks k, k+1 read while k+2 is written
+constexpr int NSLOT = 3;
+// The f16 copy of the state used by G3 holds h * kHScale (|h| up to ~1.6e7 fits); the
+// G3 row scale multiplies by 1/kHScale.
+constexpr float kHScale = 1.f / 256.f;  // token-scalar ring: chunks k, k+1 read while k+2 is written
 
 // Per-chunk token scalars (index = token within the chunk), written by wave 0.
 struct Tok {
@@ -85,11 +94,11 @@ struct Tok {
 };
 
 struct __align__(16) Smem {
-    bf16 C[Q * R][N + PAD];  // C~ rows (t,r) = 2t+r; 16-byte column chunks swizzled (sw_cb)
-    bf16 B[Q * R][N + PAD];  // B~ rows (u,r'), same swizzle
-    bf16 Bw[Q][NR + PAD];    // B~ * w_u, [u][n][r'] order
-    bf16 X[P][Q * R + PAD];  // X^T
-    bf16 H[P][N + PAD];      // incoming state, bf16
+    f16 C[Q * R][N + PAD];  // C~ rows (t,r) = 2t+r; 16-byte column chunks swizzled (sw_cb)
+    f16 B[Q * R][N + PAD];  // B~ rows (u,r'), same swizzle
+    f16 Bw[Q][NR + PAD];    // B~ * w_u, [u][n][r'] order
+    f16 X[P][Q * R + PAD];  // X^T
+    f16 H[P][N + PAD];       // incoming state times kHScale, f16
     bf16 ZY[Q][P];           // z of the chunk, overwritten in place by its gated output y;
                              // 16-byte chunks swizzled (zy_col)
     Tok tok[NSLOT];
@@ -105,8 +114,8 @@ struct Args {
     m3_layer_params prm;
     const bf16* proj;
     const float* dt_scale;
-    const bf16* Bn;    // [B*T][G][NR] pair-packed normalised B
-    const bf16* Cn;
+    const f16* Bn;    // [B*T][G][NR] pair-packed normalised B
+    const f16* Cn;
     float* seg_state;  // [B*H*(S-1)][N][P]
     float* seg_decay;  // [B*H*(S-1)]
     float* seg_angle;  // [B*H*(S-1)][NH]
@@ -124,8 +133,8 @@ __device__ __forceinline__ int opaque(int v) {
     return v;
 }
 
-__device__ __forceinline__ f32x4 mfma16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+__device__ __forceinline__ f32x4 mfma16(const f16x8& a, const f16x8& b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
@@ -174,16 +183,9 @@ __device__ __forceinline__ float wave_incl_scan(float v, int lane) {
     return v;
 }
 
-__device__ __forceinline__ bf16x2 as_bf16x2(unsigned u) { return __builtin_bit_cast(bf16x2, u); }
+__device__ __forceinline__ f16x2 as_f16x2(unsigned u) { return __builtin_bit_cast(f16x2, u); }
+__device__ __forceinline__ unsigned bits(f16x2 v) { return __builtin_bit_cast(unsigned, v); }
 
-// bf16 pair dot product (v_dot2 family). Through the builtin only: dot instructions have
-// read/write hazards with neighbouring VALU instructions that the compiler resolves for
-// its own instructions but cannot see through inline assembly.
-// `zero` is a register holding 0.0 that the compiler cannot fold: with a constant
-// accumulator it picks the accumulate-in-place v_dot2c form plus a v_mov per call.
-__device__ __forceinline__ float dot2_bf16(unsigned a, unsigned b, float zero) {
-    return __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(a), as_bf16x2(b), zero, false);
-}
 
 // C~ / B~ tiles: 64-byte column groups of a row are XOR-swizzled by the row's 16-row
 // block, so the preparation's 64-bit stores (lanes 16 rows apart) hit distinct banks.
@@ -195,9 +197,6 @@ __device__ __forceinline__ int sw_cb(int row, int col) { return col ^ (32 * ((ro
 __device__ __forceinline__ int zy_col(int t, int c) { return 8 * (c ^ (2 * ((t >> 1) & 1))); }
 
 
-__device__ __forceinline__ unsigned pack_bf16x2(float lo, float hi) {
-    return __builtin_bit_cast(unsigned, bf16x2{(bf16)lo, (bf16)hi});
-}
 
 // ---------------------------------------------------------------------------------
 // 1. Normalised B^ / C^ per (token, group): x * rsqrt(mean(x^2) + eps) * w + bias,
@@ -210,7 +209,7 @@ __global__ __launch_bounds__(256) void bc_norm(const bf16* __restrict__ proj, in
                                                const float* __restrict__ biasB,
                                                const float* __restrict__ wC,
                                                const float* __restrict__ biasC,
-                                               bf16* __restrict__ Bn, bf16* __restrict__ Cn) {
+                                               f16* __restrict__ Bn, f16* __restrict__ Cn) {
     const int lane = threadIdx.x & 63;
     const int64_t tg = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (tg >= ntok_grp) return;
@@ -239,8 +238,8 @@ __global__ __launch_bounds__(256) void bc_norm(const bf16* __restrict__ proj, in
         oc[j] = c[j] * rc * wC[e + j] + biasC[(int64_t)g * NR + e + j];
     }
     // pair-packed: (e_r0, o_r0, e_r1, o_r1)
-    *reinterpret_cast<bf16x4*>(Bn + tg * NR + e) = bf16x4{(bf16)ob[0], (bf16)ob[2], (bf16)ob[1], (bf16)ob[3]};
-    *reinterpret_cast<bf16x4*>(Cn + tg * NR + e) = bf16x4{(bf16)oc[0], (bf16)oc[2], (bf16)oc[1], (bf16)oc[3]};
+    *reinterpret_cast<f16x4*>(Bn + tg * NR + e) = f16x4{(f16)ob[0], (f16)ob[2], (f16)ob[1], (f16)ob[3]};
+    *reinterpret_cast<f16x4*>(Cn + tg * NR + e) = f16x4{(f16)oc[0], (f16)oc[2], (f16)oc[1], (f16)oc[3]};
 }
 
 // ---------------------------------------------------------------------------------
@@ -266,7 +265,8 @@ __device__ __forceinline__ void out_block(Smem& sm, const Tok& tk, int g16, int 
     const int r_col = l16 & 1;
     const int u0d = 8 * I + 2 * g16;
     const float ct = tk.c2[t_col];
-    const f32x2 ecv = *reinterpret_cast<const f32x2*>(&tk.ec[u0d]);
+    // e^{c_t}, times 1/kHScale for the scaled f16 state copy
+    const f32x2 ecv = *reinterpret_cast<const f32x2*>(&tk.ec[u0d]) * (1.f / kHScale);
     const f32x2 cud = *reinterpret_cast<const f32x2*>(&tk.c2[u0d]);
     const f32x2 aud = *reinterpret_cast<const f32x2*>(&tk.av[u0d]);
     const f32x2 bud = *reinterpret_cast<const f32x2*>(&tk.bv[u0d]);
@@ -280,14 +280,14 @@ __device__ __forceinline__ void out_block(Smem& sm, const Tok& tk, int g16, int 
 
     // C~ rows of this block (logical column 32s + 8 g16 sits at 32 (s ^ (I&3)) + 8 g16)
     // and the first H operand group.
-    bf16x8 cA[4], hop[2][4];
+    f16x8 cA[4], hop[2][4];
 #pragma unroll
     for (int s = 0; s < 4; ++s)
-        cA[s] = *reinterpret_cast<const bf16x8*>(
+        cA[s] = *reinterpret_cast<const f16x8*>(
             &sm.C[16 * I + l16][8 * g16 + 32 * (s ^ (I & 3))]);
 #pragma unroll
     for (int s = 0; s < 4; ++s)
-        hop[0][s] = *reinterpret_cast<const bf16x8*>(&sm.H[l16][32 * s + 8 * g16]);
+        hop[0][s] = *reinterpret_cast<const f16x8*>(&sm.H[l16][32 * s + 8 * g16]);
     M3_FENCE();
     // G3: Y = C~ H^T (scaled by e^{c_t} below)
     f32x4 yacc[4];
@@ -296,7 +296,7 @@ __device__ __forceinline__ void out_block(Smem& sm, const Tok& tk, int g16, int 
         if (pt + 1 < 4) {
 #pragma unroll
             for (int s = 0; s < 4; ++s)
-                hop[(pt + 1) & 1][s] = *reinterpret_cast<const bf16x8*>(&sm.H[16 * (pt + 1) + l16][32 * s + 8 * g16]);
+                hop[(pt + 1) & 1][s] = *reinterpret_cast<const f16x8*>(&sm.H[16 * (pt + 1) + l16][32 * s + 8 * g16]);
         }
         M3_FENCE();
         yacc[pt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -305,10 +305,10 @@ __device__ __forceinline__ void out_block(Smem& sm, const Tok& tk, int g16, int 
         M3_FENCE();
     }
     // G1: S^T = B~ C~^T for J <= I
-    bf16x8 bop[2][4];
+    f16x8 bop[2][4];
 #pragma unroll
     for (int s = 0; s < 4; ++s)
-        bop[0][s] = *reinterpret_cast<const bf16x8*>(&sm.B[l16][8 * g16 + 32 * s]);
+        bop[0][s] = *reinterpret_cast<const f16x8*>(&sm.B[l16][8 * g16 + 32 * s]);
     M3_FENCE();
     f32x4 sacc[NJ];
 #pragma unroll
@@ -316,7 +316,7 @@ __device__ __forceinline__ void out_block(Smem& sm, const Tok& tk, int g16, int 
         if (J + 1 < NJ) {
 #pragma unroll
             for (int s = 0; s < 4; ++s)
-                bop[(J + 1) & 1][s] = *reinterpret_cast<const bf16x8*>(
+                bop[(J + 1) & 1][s] = *reinterpret_cast<const f16x8*>(
                     &sm.B[16 * (J + 1) + l16][8 * g16 + 32 * (s ^ ((J + 1) & 3))]);
         }
         M3_FENCE();
@@ -334,12 +334,12 @@ __device__ __forceinline__ void out_block(Smem& sm, const Tok& tk, int g16, int 
     }
     // Mask S^T by Lc (+D on the diagonal) and run G2: Y += S X.
     // This lane's S^T values: rows (u, r') = (8J + 2 g16 + v/2, v&1), column (t_col, r_col).
-    bf16x4 xop[2][4][2];
+    f16x4 xop[2][4][2];
 #pragma unroll
     for (int pt = 0; pt < 4; ++pt) {
-        const bf16* xr = &sm.X[16 * pt + l16][0];
-        xop[0][pt][0] = *reinterpret_cast<const bf16x4*>(xr + 4 * g16);
-        xop[0][pt][1] = *reinterpret_cast<const bf16x4*>(xr + 16 + 4 * g16);
+        const f16* xr = &sm.X[16 * pt + l16][0];
+        xop[0][pt][0] = *reinterpret_cast<const f16x4*>(xr + 4 * g16);
+        xop[0][pt][1] = *reinterpret_cast<const f16x4*>(xr + 16 + 4 * g16);
     }
     M3_FENCE();
 #pragma unroll
@@ -347,13 +347,13 @@ __device__ __forceinline__ void out_block(Smem& sm, const Tok& tk, int g16, int 
         if (s2 + 1 <= I / 2) {
 #pragma unroll
             for (int pt = 0; pt < 4; ++pt) {
-                const bf16* xr = &sm.X[16 * pt + l16][32 * (s2 + 1)];
-                xop[(s2 + 1) & 1][pt][0] = *reinterpret_cast<const bf16x4*>(xr + 4 * g16);
-                xop[(s2 + 1) & 1][pt][1] = *reinterpret_cast<const bf16x4*>(xr + 16 + 4 * g16);
+                const f16* xr = &sm.X[16 * pt + l16][32 * (s2 + 1)];
+                xop[(s2 + 1) & 1][pt][0] = *reinterpret_cast<const f16x4*>(xr + 4 * g16);
+                xop[(s2 + 1) & 1][pt][1] = *reinterpret_cast<const f16x4*>(xr + 16 + 4 * g16);
             }
         }
         M3_FENCE();
-        bf16x8 aop;
+        f16x8 aop;
 #pragma unroll
         for (int jj = 0; jj < 2; ++jj) {
             const int J = 2 * s2 + jj;
@@ -382,15 +382,15 @@ __device__ __forceinline__ void out_block(Smem& sm, const Tok& tk, int g16, int 
                 if (u0d == t_col) { if (r_col == 0) m0 += D_h; else m1 += D_h; }
                 if (u0d + 1 == t_col) { if (r_col == 0) m2 += D_h; else m3 += D_h; }
             }
-            aop[4 * jj + 0] = (bf16)m0;
-            aop[4 * jj + 1] = (bf16)m1;
-            aop[4 * jj + 2] = (bf16)m2;
-            aop[4 * jj + 3] = (bf16)m3;
+            aop[4 * jj + 0] = (f16)m0;
+            aop[4 * jj + 1] = (f16)m1;
+            aop[4 * jj + 2] = (f16)m2;
+            aop[4 * jj + 3] = (f16)m3;
         }
 #pragma unroll
         for (int pt = 0; pt < 4; ++pt) {
-            const bf16x4 lo = xop[s2 & 1][pt][0], hi = xop[s2 & 1][pt][1];
-            const bf16x8 xb = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            const f16x4 lo = xop[s2 & 1][pt][0], hi = xop[s2 & 1][pt][1];
+            const f16x8 xb = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
             yacc[pt] = mfma16(aop, xb, yacc[pt]);
         }
         M3_FENCE();
@@ -508,8 +508,8 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
     }
 
     const bf16* proj_b = a.proj + (int64_t)b * T * a.rs;
-    const bf16* bn_b = a.Bn + ((int64_t)b * T * a.G + grp) * NR;
-    const bf16* cn_b = a.Cn + ((int64_t)b * T * a.G + grp) * NR;
+    const f16* bn_b = a.Bn + ((int64_t)b * T * a.G + grp) * NR;
+    const f16* cn_b = a.Cn + ((int64_t)b * T * a.G + grp) * NR;
 
     float logdecay = 0.f;  // total log-decay of the segment (natural log)
     float phi_run0 = 0.f, phi_run1 = 0.f;  // pair angles relative to the segment start, turns
@@ -522,27 +522,27 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
 #pragma unroll
         for (int pt = 0; pt < 4; ++pt) hacc[pt] *= dch;
         const int ncol = 2 * (16 * wv + l16);
-        bf16x2 wop[2][4];
-        bf16x8 xop[2][4];
+        f16x2 wop[2][4];
+        f16x8 xop[2][4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) wop[0][j] = *reinterpret_cast<const bf16x2*>(&sm.Bw[4 * g16 + j][ncol]);
+        for (int j = 0; j < 4; ++j) wop[0][j] = *reinterpret_cast<const f16x2*>(&sm.Bw[4 * g16 + j][ncol]);
 #pragma unroll
         for (int pt = 0; pt < 4; ++pt)
-            xop[0][pt] = *reinterpret_cast<const bf16x8*>(&sm.X[16 * pt + l16][8 * g16]);
+            xop[0][pt] = *reinterpret_cast<const f16x8*>(&sm.X[16 * pt + l16][8 * g16]);
         M3_FENCE();
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             if (s + 1 < 4) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
-                    wop[(s + 1) & 1][j] = *reinterpret_cast<const bf16x2*>(&sm.Bw[16 * (s + 1) + 4 * g16 + j][ncol]);
+                    wop[(s + 1) & 1][j] = *reinterpret_cast<const f16x2*>(&sm.Bw[16 * (s + 1) + 4 * g16 + j][ncol]);
 #pragma unroll
                 for (int pt = 0; pt < 4; ++pt)
                     xop[(s + 1) & 1][pt] =
-                        *reinterpret_cast<const bf16x8*>(&sm.X[16 * pt + l16][32 * (s + 1) + 8 * g16]);
+                        *reinterpret_cast<const f16x8*>(&sm.X[16 * pt + l16][32 * (s + 1) + 8 * g16]);
             }
             M3_FENCE();
-            bf16x8 aop;
+            f16x8 aop;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 aop[2 * j] = wop[s & 1][j][0];
@@ -563,9 +563,9 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
             const int n0 = 16 * wv + 4 * g16;
 #pragma unroll
             for (int pt = 0; pt < 4; ++pt) {
-                const f32x4 v = hacc[pt];
-                *reinterpret_cast<bf16x4*>(&sm.H[16 * pt + l16][n0]) =
-                    bf16x4{(bf16)v[0], (bf16)v[1], (bf16)v[2], (bf16)v[3]};
+                const f32x4 v = hacc[pt] * kHScale;
+                *reinterpret_cast<f16x4*>(&sm.H[16 * pt + l16][n0]) =
+                    f16x4{(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
             }
         }
     };
@@ -631,7 +631,6 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
         auto prep = [&](int kk) {
             const int lane = opaque(threadIdx.x & 63);
             const int q = lane >> 3;
-            const float zero = __builtin_bit_cast(float, opaque(0));
             const Tok& tk = sm.tok[kk % NSLOT];
             const f32x4 d0 = *reinterpret_cast<const f32x4*>(&tk.dtr[8 * q]);
             const f32x4 d1 = *reinterpret_cast<const f32x4*>(&tk.dtr[8 * q + 4]);
@@ -668,32 +667,34 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const float wu = j < 4 ? w0[j] : w1[j - 4];
-                float be[2][2], bo[2][2];  // [pair][rank]
+                const f16x2 w2 = f16x2{(f16)wu, (f16)wu};
+                f16x2 rb[2][2];  // [pair][rank]: rotated (even, odd) of B^
 #pragma unroll
                 for (int pr = 0; pr < 2; ++pr) {
                     float& phi = pr == 0 ? phi0 : phi1;
                     phi -= pr == 0 ? inc0[j] : inc1[j];
                     const float rev = __builtin_amdgcn_fractf(phi);
                     const float sn = __builtin_amdgcn_sinf(rev), cs = __builtin_amdgcn_cosf(rev);
-                    const unsigned k1 = pack_bf16x2(cs, -sn);
-                    const unsigned k2 = pack_bf16x2(sn, cs);
-                    const unsigned b0 = rawB[j][2 * pr], b1 = rawB[j][2 * pr + 1];
-                    be[pr][0] = dot2_bf16(b0, k1, zero);
-                    bo[pr][0] = dot2_bf16(b0, k2, zero);
-                    be[pr][1] = dot2_bf16(b1, k1, zero);
-                    bo[pr][1] = dot2_bf16(b1, k2, zero);
-                    if (kFull) {
-                        const unsigned c0 = rawC[j][2 * pr], c1 = rawC[j][2 * pr + 1];
-                        outC[j][0][pr] = pack_bf16x2(dot2_bf16(c0, k1, zero), dot2_bf16(c0, k2, zero));
-                        outC[j][1][pr] = pack_bf16x2(dot2_bf16(c1, k1, zero), dot2_bf16(c1, k2, zero));
+                    // (e, o) -> (e cos - o sin, e sin + o cos) = e (cos, sin) + o (-sin, cos)
+                    const f16x2 kA = f16x2{(f16)cs, (f16)sn};
+                    const f16x2 kB = f16x2{(f16)(-sn), (f16)cs};
+#pragma unroll
+                    for (int r = 0; r < 2; ++r) {
+                        const f16x2 v = as_f16x2(rawB[j][2 * pr + r]);
+                        rb[pr][r] = f16x2{v[0], v[0]} * kA + f16x2{v[1], v[1]} * kB;
+                        if (kFull) {
+                            const f16x2 c = as_f16x2(rawC[j][2 * pr + r]);
+                            outC[j][r][pr] = bits(f16x2{c[0], c[0]} * kA + f16x2{c[1], c[1]} * kB);
+                        }
                     }
                 }
                 if (kFull) {
-                    outB[j][0] = u32x2{pack_bf16x2(be[0][0], bo[0][0]), pack_bf16x2(be[1][0], bo[1][0])};
-                    outB[j][1] = u32x2{pack_bf16x2(be[0][1], bo[0][1]), pack_bf16x2(be[1][1], bo[1][1])};
+                    outB[j][0] = u32x2{bits(rb[0][0]), bits(rb[1][0])};
+                    outB[j][1] = u32x2{bits(rb[0][1]), bits(rb[1][1])};
                 }
-                outBw[j] = u32x4{pack_bf16x2(be[0][0] * wu, be[0][1] * wu), pack_bf16x2(bo[0][0] * wu, bo[0][1] * wu),
-                                 pack_bf16x2(be[1][0] * wu, be[1][1] * wu), pack_bf16x2(bo[1][0] * wu, bo[1][1] * wu)};
+                // B~w in [n][r'] order: (e r0, e r1), (o r0, o r1) of each pair, times w_u
+                outBw[j] = u32x4{bits(f16x2{rb[0][0][0], rb[0][1][0]} * w2), bits(f16x2{rb[0][0][1], rb[0][1][1]} * w2),
+                                 bits(f16x2{rb[1][0][0], rb[1][1][0]} * w2), bits(f16x2{rb[1][0][1], rb[1][1][1]} * w2)};
             }
         };
         auto write_prep = [&]() {
@@ -715,7 +716,7 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
 
         // ---------------- X / token-scalar role (waves 4-7) ----------------
         unsigned rawx[16];
-        bf16x8 outX[4];
+        f16x8 outX[4];
         unsigned sdt = 0u, sdt64 = 0u, slam = 0u, slam64 = 0u;
         float ssc = 1.f, ssc64 = 1.f;
         const float mx0 = a.prm.mimo_x[(h * P + lane0) * R], mx1 = a.prm.mimo_x[(h * P + lane0) * R + 1];
@@ -735,15 +736,15 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const float x = bf16_f32(rawx[4 * c + j]);
-                    outX[c][2 * j] = (bf16)(x * mx0);
-                    outX[c][2 * j + 1] = (bf16)(x * mx1);
+                    outX[c][2 * j] = (f16)(x * mx0);
+                    outX[c][2 * j + 1] = (f16)(x * mx1);
                 }
         };
         auto write_x = [&]() {
             const int lane = opaque(threadIdx.x & 63);
 #pragma unroll
             for (int c = 0; c < 4; ++c)
-                *reinterpret_cast<bf16x8*>(&sm.X[lane][32 * (wv - 4) + 8 * c]) = outX[c];
+                *reinterpret_cast<f16x8*>(&sm.X[lane][32 * (wv - 4) + 8 * c]) = outX[c];
         };
         auto load_sc = [&](int kk) {
             const int lane = opaque(threadIdx.x & 63);
@@ -977,7 +978,7 @@ size_t mfma_prefill_workspace(const m3_layer_desc& d) {
     mfma_segments(d, S, cps);
     const size_t ntg = (size_t)d.batch * d.seqlen * d.ngroups;
     const size_t nseg = (size_t)d.batch * d.nheads * (S - 1);
-    const size_t bc_bytes = 2 * ntg * mf::NR * sizeof(bf16);
+    const size_t bc_bytes = 2 * ntg * mf::NR * sizeof(mf::f16);
     return bc_bytes + nseg * ((size_t)mf::N * mf::P + 1 + mf::NH) * sizeof(float) + 256;
 }
 
@@ -996,8 +997,8 @@ int launch_mfma_prefill(const m3_layer_desc& d, const m3_layer_params& p, const 
     a.dt_scale = dt_scale;
     const int64_t ntg = (int64_t)d.batch * d.seqlen * d.ngroups;
     const int64_t nseg = (int64_t)d.batch * d.nheads * (S - 1);
-    bf16* bn = reinterpret_cast<bf16*>(workspace);
-    bf16* cn = bn + ntg * mf::NR;
+    mf::f16* bn = reinterpret_cast<mf::f16*>(workspace);
+    mf::f16* cn = bn + ntg * mf::NR;
     float* ws = reinterpret_cast<float*>(cn + ntg * mf::NR);
     a.Bn = bn;
     a.Cn = cn;
