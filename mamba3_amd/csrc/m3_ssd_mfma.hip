@@ -96,11 +96,11 @@ struct Tok {
 struct __align__(16) Smem {
     f16 C[Q * R][N + PAD];  // C~ rows (t,r) = 2t+r; 16-byte column chunks swizzled (sw_cb)
     f16 B[Q * R][N + PAD];  // B~ rows (u,r'), same swizzle
-    f16 Bw[Q][NR + PAD];    // B~ * w_u, [u][n][r'] order
-    f16 X[P][Q * R + PAD];  // X^T
-    f16 H[P][N + PAD];       // incoming state times kHScale, f16
-    bf16 ZY[Q][P];           // z of the chunk, overwritten in place by its gated output y;
-                             // 16-byte chunks swizzled (zy_col)
+    f16 Xw[P][Q * R + PAD];  // X^T * w_u (state-update operand)
+    f16 X[P][Q * R + PAD];   // X^T
+    f16 H[2][P][N + PAD];    // incoming state times kHScale, double-buffered by chunk parity
+    bf16 ZY[2][Q][P];        // z of the chunk, overwritten in place by its gated output y;
+                             // double-buffered by chunk parity; 16-byte chunks swizzled
     Tok tok[NSLOT];
     float rot[NH];           // per-pair angle scratch (prologue / epilogue)
     float mzd[P][4];         // per p: -mimo_z[0] log2e, -mimo_z[1] log2e, mimo_down*mimo_z [0], [1]
@@ -183,6 +183,16 @@ __device__ __forceinline__ float wave_incl_scan(float v, int lane) {
     return v;
 }
 
+typedef short s16x4 __attribute__((vector_size(8)));
+// ds_read_b64_tr_b16: within each 16-lane group, lane j addresses 4 consecutive 16-bit
+// elements (row j/4, column group j%4 of a 4 x 16 block); lane i receives element m of
+// row m, column i. Two of these give the 8 k-values of an MFMA operand column from a
+// row-major [k][col] tile.
+__device__ __forceinline__ f16x4 ld_tr(const f16* p) {
+    const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s16x4*)(p));
+    return __builtin_bit_cast(f16x4, v);
+}
 __device__ __forceinline__ f16x2 as_f16x2(unsigned u) { return __builtin_bit_cast(f16x2, u); }
 __device__ __forceinline__ unsigned bits(f16x2 v) { return __builtin_bit_cast(unsigned, v); }
 
@@ -195,6 +205,12 @@ __device__ __forceinline__ int sw_cb(int row, int col) { return col ^ (32 * ((ro
 // token pair keeps both the 128-bit staging accesses and the epilogue's 16-bit accesses
 // (rows 2 apart across lanes) free of bank conflicts.
 __device__ __forceinline__ int zy_col(int t, int c) { return 8 * (c ^ (2 * ((t >> 1) & 1))); }
+// X^T tile (G2 operand): logical column c = 32 s + 16 jj + 4 g + v is stored at
+// 32 s + 8 g + 4 jj + v, so the 8 k-values one lane feeds to G2 (jj = 0, 1 for its g) are
+// one contiguous 16-byte chunk (a single ds_read_b128).
+__device__ __forceinline__ int x_col(int c) {
+    return (c & ~31) | (((c >> 2) & 3) << 3) | (((c >> 4) & 1) << 2) | (c & 3);
+}
 
 
 
@@ -255,9 +271,12 @@ __global__ __launch_bounds__(256) void bc_norm(const bf16* __restrict__ proj, in
 // Scheduling fence: keeps the LDS operand reads issued one tile ahead of the MFMAs that
 // consume them (the compiler otherwise sinks each read next to its use and waits on it).
 #define M3_FENCE() __builtin_amdgcn_sched_barrier(0)
+// Compiler memory fence between LDS stores (no instruction): stops the pairing of
+// neighbouring stores into ds_write2_b64.
+#define M3_LDS_FENCE() asm volatile("" ::: "memory")
 
 template <int I>
-__device__ __forceinline__ void out_block(Smem& sm, const Tok& tk, int g16, int l16, float D_h) {
+__device__ __forceinline__ void out_block(Smem& sm, const Tok& tk, int par, int g16, int l16, float D_h) {
 
     constexpr int NJ = I + 1;
     // Token scalars this lane needs (rows t_col, columns u = 8J + 2 g16 + {0,1}).
@@ -287,7 +306,7 @@ __device__ __forceinline__ void out_block(Smem& sm, const Tok& tk, int g16, int 
             &sm.C[16 * I + l16][8 * g16 + 32 * (s ^ (I & 3))]);
 #pragma unroll
     for (int s = 0; s < 4; ++s)
-        hop[0][s] = *reinterpret_cast<const f16x8*>(&sm.H[l16][32 * s + 8 * g16]);
+        hop[0][s] = *reinterpret_cast<const f16x8*>(&sm.H[par][l16][32 * s + 8 * g16]);
     M3_FENCE();
     // G3: Y = C~ H^T (scaled by e^{c_t} below)
     f32x4 yacc[4];
@@ -296,7 +315,7 @@ __device__ __forceinline__ void out_block(Smem& sm, const Tok& tk, int g16, int 
         if (pt + 1 < 4) {
 #pragma unroll
             for (int s = 0; s < 4; ++s)
-                hop[(pt + 1) & 1][s] = *reinterpret_cast<const f16x8*>(&sm.H[16 * (pt + 1) + l16][32 * s + 8 * g16]);
+                hop[(pt + 1) & 1][s] = *reinterpret_cast<const f16x8*>(&sm.H[par][16 * (pt + 1) + l16][32 * s + 8 * g16]);
         }
         M3_FENCE();
         yacc[pt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -334,23 +353,16 @@ __device__ __forceinline__ void out_block(Smem& sm, const Tok& tk, int g16, int 
     }
     // Mask S^T by Lc (+D on the diagonal) and run G2: Y += S X.
     // This lane's S^T values: rows (u, r') = (8J + 2 g16 + v/2, v&1), column (t_col, r_col).
-    f16x4 xop[2][4][2];
+    f16x8 xop[2][4];
 #pragma unroll
-    for (int pt = 0; pt < 4; ++pt) {
-        const f16* xr = &sm.X[16 * pt + l16][0];
-        xop[0][pt][0] = *reinterpret_cast<const f16x4*>(xr + 4 * g16);
-        xop[0][pt][1] = *reinterpret_cast<const f16x4*>(xr + 16 + 4 * g16);
-    }
+    for (int pt = 0; pt < 4; ++pt) xop[0][pt] = *reinterpret_cast<const f16x8*>(&sm.X[16 * pt + l16][8 * g16]);
     M3_FENCE();
 #pragma unroll
     for (int s2 = 0; s2 <= I / 2; ++s2) {
         if (s2 + 1 <= I / 2) {
 #pragma unroll
-            for (int pt = 0; pt < 4; ++pt) {
-                const f16* xr = &sm.X[16 * pt + l16][32 * (s2 + 1)];
-                xop[(s2 + 1) & 1][pt][0] = *reinterpret_cast<const f16x4*>(xr + 4 * g16);
-                xop[(s2 + 1) & 1][pt][1] = *reinterpret_cast<const f16x4*>(xr + 16 + 4 * g16);
-            }
+            for (int pt = 0; pt < 4; ++pt)
+                xop[(s2 + 1) & 1][pt] = *reinterpret_cast<const f16x8*>(&sm.X[16 * pt + l16][32 * (s2 + 1) + 8 * g16]);
         }
         M3_FENCE();
         f16x8 aop;
@@ -388,11 +400,7 @@ __device__ __forceinline__ void out_block(Smem& sm, const Tok& tk, int g16, int 
             aop[4 * jj + 3] = (f16)m3;
         }
 #pragma unroll
-        for (int pt = 0; pt < 4; ++pt) {
-            const f16x4 lo = xop[s2 & 1][pt][0], hi = xop[s2 & 1][pt][1];
-            const f16x8 xb = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-            yacc[pt] = mfma16(aop, xb, yacc[pt]);
-        }
+        for (int pt = 0; pt < 4; ++pt) yacc[pt] = mfma16(aop, xop[s2 & 1][pt], yacc[pt]);
         M3_FENCE();
     }
 
@@ -407,7 +415,7 @@ __device__ __forceinline__ void out_block(Smem& sm, const Tok& tk, int g16, int 
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
             const int t = 8 * I + 2 * g16 + tt;
-            bf16* zy = &sm.ZY[t][zy_col(t, p >> 3) + (p & 7)];
+            bf16* zy = &sm.ZY[par][t][zy_col(t, p >> 3) + (p & 7)];
             const float z = (float)*zy;
             const float e0 = 1.f + __builtin_amdgcn_exp2f(fminf(z * g[0], 60.f));
             const float e1 = 1.f + __builtin_amdgcn_exp2f(fminf(z * g[1], 60.f));
@@ -418,9 +426,10 @@ __device__ __forceinline__ void out_block(Smem& sm, const Tok& tk, int g16, int 
 }
 
 // Pipelined chunk walk. Per chunk k:
-//   barrier -> M(k): state update G4 on chunk k's tiles; reads of chunk k+1 issued; output
-//              block of chunk k; element-wise preparation of chunk k+1 into registers
-//   barrier -> W(k+1): registers -> LDS tiles, bf16 copy of the state
+//   barrier -> M(k): y of chunk k-1 stored; state update G4 on chunk k's tiles; f16 copy of
+//              the new state written; reads of chunk k+1 issued; output block of chunk k;
+//              z of chunk k+1 staged; element-wise preparation of chunk k+1 into registers
+//   barrier -> W(k+1): registers -> LDS tiles (C~, B~, X^T, X^T w)
 // Roles: SIMD s runs waves s and s+4. Wave s owns output block s (light: 1..4 causal
 // column blocks) and prepares the RoPE-rotated B~ / C~ / B~w tiles of pairs
 // 16s .. 16s+15; wave s+4 owns output block 7-s (heavy: 5..8 column blocks) and
@@ -521,33 +530,36 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
         const float dch = tk.ec[Q - 1];
 #pragma unroll
         for (int pt = 0; pt < 4; ++pt) hacc[pt] *= dch;
-        const int ncol = 2 * (16 * wv + l16);
-        f16x2 wop[2][4];
+        // A operand (B~^T, rows n = 16 wave + lane%16, k = (u, r)) by transpose reads of the
+        // B~ tile: lane j of a 16-lane group addresses row k0 + j/4, columns n0 + 4 (j%4)
+        // (the tile swizzle is uniform over the 8 rows k0 .. k0+7 of one group).
+        const int jr = (lane & 15) >> 2, jc = 4 * (lane & 3);
+        const int n0 = 16 * wv;
+        auto a_ptr = [&](int s, int half) {
+            const int row = 32 * s + 8 * g16 + 4 * half + jr;
+            return &sm.B[row][sw_cb(row, n0 + jc)];
+        };
+        f16x4 aop_lo[2], aop_hi[2];
         f16x8 xop[2][4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) wop[0][j] = *reinterpret_cast<const f16x2*>(&sm.Bw[4 * g16 + j][ncol]);
+        aop_lo[0] = ld_tr(a_ptr(0, 0));
+        aop_hi[0] = ld_tr(a_ptr(0, 1));
 #pragma unroll
         for (int pt = 0; pt < 4; ++pt)
-            xop[0][pt] = *reinterpret_cast<const f16x8*>(&sm.X[16 * pt + l16][8 * g16]);
+            xop[0][pt] = *reinterpret_cast<const f16x8*>(&sm.Xw[16 * pt + l16][8 * g16]);
         M3_FENCE();
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             if (s + 1 < 4) {
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    wop[(s + 1) & 1][j] = *reinterpret_cast<const f16x2*>(&sm.Bw[16 * (s + 1) + 4 * g16 + j][ncol]);
+                aop_lo[(s + 1) & 1] = ld_tr(a_ptr(s + 1, 0));
+                aop_hi[(s + 1) & 1] = ld_tr(a_ptr(s + 1, 1));
 #pragma unroll
                 for (int pt = 0; pt < 4; ++pt)
                     xop[(s + 1) & 1][pt] =
-                        *reinterpret_cast<const f16x8*>(&sm.X[16 * pt + l16][32 * (s + 1) + 8 * g16]);
+                        *reinterpret_cast<const f16x8*>(&sm.Xw[16 * pt + l16][32 * (s + 1) + 8 * g16]);
             }
             M3_FENCE();
-            f16x8 aop;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                aop[2 * j] = wop[s & 1][j][0];
-                aop[2 * j + 1] = wop[s & 1][j][1];
-            }
+            const f16x4 lo = aop_lo[s & 1], hi = aop_hi[s & 1];
+            const f16x8 aop = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 #pragma unroll
             for (int pt = 0; pt < 4; ++pt) hacc[pt] = mfma16(aop, xop[s & 1][pt], hacc[pt]);
             M3_FENCE();
@@ -556,7 +568,7 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
     };
 
     // ---- bf16 copy of the state for G3 (all waves, W phase)
-    auto write_state = [&]() {
+    auto write_state = [&](int par) {
         if (kFull) {
             const int lane = opaque(threadIdx.x & 63);
             const int g16 = lane >> 4, l16 = lane & 15;
@@ -564,7 +576,7 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
 #pragma unroll
             for (int pt = 0; pt < 4; ++pt) {
                 const f32x4 v = hacc[pt] * kHScale;
-                *reinterpret_cast<f16x4*>(&sm.H[16 * pt + l16][n0]) =
+                *reinterpret_cast<f16x4*>(&sm.H[par][16 * pt + l16][n0]) =
                     f16x4{(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
             }
         }
@@ -581,17 +593,18 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
         const __amdgpu_buffer_rsrc_t rz = make_rsrc(proj_b + (int64_t)s0 * a.rs, (int64_t)max(T - s0, 0) * a.rs * 2);
         zreg = __builtin_amdgcn_raw_buffer_load_b128(rz, (t * rs + (int)a.pl.z + h * P + 8 * c) * 2, 0, 0);
     };
-    auto zy_exchange = [&](int k_prev, bool store_prev, bool write_next) {
+    auto store_y = [&](int kk) {  // y of chunk kk from its ZY buffer to HBM
         const int t = opaque(threadIdx.x) >> 3, c = threadIdx.x & 7;
-        u32x4* cell = reinterpret_cast<u32x4*>(&sm.ZY[t][zy_col(t, c)]);
-        if (store_prev) {
-            const int s0 = k_prev * Q;
-            const int HP = a.H * P;
-            const __amdgpu_buffer_rsrc_t ry =
-                make_rsrc(a.y_out + ((int64_t)b * T + s0) * HP, (int64_t)max(T - s0, 0) * HP * 2);
-            __builtin_amdgcn_raw_buffer_store_b128(*cell, ry, (t * HP + h * P + 8 * c) * 2, 0, 0);
-        }
-        if (write_next) *cell = zreg;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(&sm.ZY[kk & 1][t][zy_col(t, c)]);
+        const int s0 = kk * Q;
+        const int HP = a.H * P;
+        const __amdgpu_buffer_rsrc_t ry =
+            make_rsrc(a.y_out + ((int64_t)b * T + s0) * HP, (int64_t)max(T - s0, 0) * HP * 2);
+        __builtin_amdgcn_raw_buffer_store_b128(v, ry, (t * HP + h * P + 8 * c) * 2, 0, 0);
+    };
+    auto write_z = [&](int kk) {  // z of chunk kk (in zreg) into its ZY buffer
+        const int t = opaque(threadIdx.x) >> 3, c = threadIdx.x & 7;
+        *reinterpret_cast<u32x4*>(&sm.ZY[kk & 1][t][zy_col(t, c)]) = zreg;
     };
 
     auto role_loop = [&](auto role) {
@@ -601,7 +614,6 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
         u32x4 rawB[8], rawC[8];
         unsigned rawth[8];
         u32x2 outB[8][2], outC[8][2];
-        u32x4 outBw[8];
         auto load_prep = [&](int kk) {
             const int lane = opaque(threadIdx.x & 63);
             const int q = lane >> 3;
@@ -634,8 +646,6 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
             const Tok& tk = sm.tok[kk % NSLOT];
             const f32x4 d0 = *reinterpret_cast<const f32x4*>(&tk.dtr[8 * q]);
             const f32x4 d1 = *reinterpret_cast<const f32x4*>(&tk.dtr[8 * q + 4]);
-            const f32x4 w0 = *reinterpret_cast<const f32x4*>(&tk.w[8 * q]);
-            const f32x4 w1 = *reinterpret_cast<const f32x4*>(&tk.w[8 * q + 4]);
             // RoPE angle increments (turns) of tokens 8q..8q+7 for both pairs; the prefix of
             // the per-lane totals over q (lanes 8 apart) gives each lane's starting angles.
             float inc0[8], inc1[8];
@@ -666,8 +676,6 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
             phi_run1 -= ctot1;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const float wu = j < 4 ? w0[j] : w1[j - 4];
-                const f16x2 w2 = f16x2{(f16)wu, (f16)wu};
                 f16x2 rb[2][2];  // [pair][rank]: rotated (even, odd) of B^
 #pragma unroll
                 for (int pr = 0; pr < 2; ++pr) {
@@ -688,13 +696,9 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
                         }
                     }
                 }
-                if (kFull) {
-                    outB[j][0] = u32x2{bits(rb[0][0]), bits(rb[1][0])};
-                    outB[j][1] = u32x2{bits(rb[0][1]), bits(rb[1][1])};
-                }
-                // B~w in [n][r'] order: (e r0, e r1), (o r0, o r1) of each pair, times w_u
-                outBw[j] = u32x4{bits(f16x2{rb[0][0][0], rb[0][1][0]} * w2), bits(f16x2{rb[0][0][1], rb[0][1][1]} * w2),
-                                 bits(f16x2{rb[1][0][0], rb[1][1][0]} * w2), bits(f16x2{rb[1][0][1], rb[1][1][1]} * w2)};
+                // B~ is needed by both passes (G1 scores and, via transpose reads, G4)
+                outB[j][0] = u32x2{bits(rb[0][0]), bits(rb[1][0])};
+                outB[j][1] = u32x2{bits(rb[0][1]), bits(rb[1][1])};
             }
         };
         auto write_prep = [&]() {
@@ -704,19 +708,24 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
             const int col = sw_cb(16 * q, 2 * pa);  // rows 16q .. 16q+15 share the swizzle
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
+                // The fences keep these as single 64-bit stores: the compiler would pair
+                // neighbouring rows into ds_write2_b64, which is about twice as slow here.
                 if (kFull) {
                     *reinterpret_cast<u32x2*>(&sm.C[16 * q + 2 * j][col]) = outC[j][0];
+                    M3_LDS_FENCE();
                     *reinterpret_cast<u32x2*>(&sm.C[16 * q + 2 * j + 1][col]) = outC[j][1];
-                    *reinterpret_cast<u32x2*>(&sm.B[16 * q + 2 * j][col]) = outB[j][0];
-                    *reinterpret_cast<u32x2*>(&sm.B[16 * q + 2 * j + 1][col]) = outB[j][1];
+                    M3_LDS_FENCE();
                 }
-                *reinterpret_cast<u32x4*>(&sm.Bw[8 * q + j][4 * pa]) = outBw[j];
+                *reinterpret_cast<u32x2*>(&sm.B[16 * q + 2 * j][col]) = outB[j][0];
+                M3_LDS_FENCE();
+                *reinterpret_cast<u32x2*>(&sm.B[16 * q + 2 * j + 1][col]) = outB[j][1];
+                M3_LDS_FENCE();
             }
         };
 
         // ---------------- X / token-scalar role (waves 4-7) ----------------
         unsigned rawx[16];
-        f16x8 outX[4];
+        f16x8 outX[4], outXw[4];
         unsigned sdt = 0u, sdt64 = 0u, slam = 0u, slam64 = 0u;
         float ssc = 1.f, ssc64 = 1.f;
         const float mx0 = a.prm.mimo_x[(h * P + lane0) * R], mx1 = a.prm.mimo_x[(h * P + lane0) * R + 1];
@@ -730,21 +739,38 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
             for (int j = 0; j < 16; ++j)
                 rawx[j] = ld_u16(rp, vx + j * rs * 2);
         };
-        auto prep_x = [&]() {
+        auto prep_x = [&](int kk) {
+            // X^T and X^T * w_u for tokens 16 (wave-4) .. +15 of chunk kk
+            const Tok& tk = sm.tok[kk % NSLOT];
+            float x0[16], x1[16];
 #pragma unroll
-            for (int c = 0; c < 4; ++c)
+            for (int j = 0; j < 16; ++j) {
+                const float x = bf16_f32(rawx[j]);
+                x0[j] = x * mx0;
+                x1[j] = x * mx1;
+            }
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const f32x4 wv4 = *reinterpret_cast<const f32x4*>(&tk.w[16 * (wv - 4) + 4 * c]);
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const float x = bf16_f32(rawx[4 * c + j]);
-                    outX[c][2 * j] = (f16)(x * mx0);
-                    outX[c][2 * j + 1] = (f16)(x * mx1);
+                    // Xw chunk c: tokens 4c..4c+3 in natural (t, r) order
+                    outXw[c][2 * j] = (f16)(x0[4 * c + j] * wv4[j]);
+                    outXw[c][2 * j + 1] = (f16)(x1[4 * c + j] * wv4[j]);
+                    // X chunk c (x_col order): tokens 2c, 2c+1 then 8+2c, 9+2c
+                    const int tj = (j < 2 ? 2 * c : 6 + 2 * c) + j;
+                    outX[c][2 * j] = (f16)x0[tj];
+                    outX[c][2 * j + 1] = (f16)x1[tj];
                 }
+            }
         };
         auto write_x = [&]() {
             const int lane = opaque(threadIdx.x & 63);
 #pragma unroll
-            for (int c = 0; c < 4; ++c)
+            for (int c = 0; c < 4; ++c) {
                 *reinterpret_cast<f16x8*>(&sm.X[lane][32 * (wv - 4) + 8 * c]) = outX[c];
+                *reinterpret_cast<f16x8*>(&sm.Xw[lane][32 * (wv - 4) + 8 * c]) = outXw[c];
+            }
         };
         auto load_sc = [&](int kk) {
             const int lane = opaque(threadIdx.x & 63);
@@ -807,23 +833,26 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
             prep(k_begin);
             write_prep();
         } else {
-            prep_x();
+            prep_x(k_begin);
             write_x();
         }
-        write_state();
-        if (kFull) zy_exchange(k_begin, false, true);
+        write_state(k_begin & 1);
+        if (kFull) write_z(k_begin);
 
         // ---------------- chunk loop ----------------
-        // Reads of chunk k+1 are issued after the state update of M(k) (the waves reach that
-        // point at different times, which spreads the requests), so they are in flight during
-        // the output block and live only within M(k).
+        // The state copy of chunk k+1 is written right after the state update of M(k), and
+        // z of chunk k+1 (read after the state update) at the end of M(k), both into the
+        // buffers of the other parity; y of chunk k-1 is stored at the start of M(k).
         for (int k = k_begin; k < k_end; ++k) {
             const int s0 = k * Q;
             const bool more = k + 1 < k_end;
+            const int par = k & 1;
             __syncthreads();
+            if (kFull && k > k_begin) store_y(k - 1);
             const Tok& tk = sm.tok[k % NSLOT];
             state_update(tk);
             if (more) {
+                write_state(par ^ 1);
                 if (kFull) load_z(k + 1);
                 if (kPrep) load_prep(k + 1);
                 else load_x(k + 1);
@@ -833,17 +862,17 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
                 const int g16 = lane >> 4, l16 = lane & 15;
                 if (kPrep) {
                     switch (wv) {
-                        case 0: out_block<0>(sm, tk, g16, l16, D_h); break;
-                        case 1: out_block<1>(sm, tk, g16, l16, D_h); break;
-                        case 2: out_block<2>(sm, tk, g16, l16, D_h); break;
-                        default: out_block<3>(sm, tk, g16, l16, D_h); break;
+                        case 0: out_block<0>(sm, tk, par, g16, l16, D_h); break;
+                        case 1: out_block<1>(sm, tk, par, g16, l16, D_h); break;
+                        case 2: out_block<2>(sm, tk, par, g16, l16, D_h); break;
+                        default: out_block<3>(sm, tk, par, g16, l16, D_h); break;
                     }
                 } else {
                     switch (wv) {
-                        case 4: out_block<7>(sm, tk, g16, l16, D_h); break;
-                        case 5: out_block<6>(sm, tk, g16, l16, D_h); break;
-                        case 6: out_block<5>(sm, tk, g16, l16, D_h); break;
-                        default: out_block<4>(sm, tk, g16, l16, D_h); break;
+                        case 4: out_block<7>(sm, tk, par, g16, l16, D_h); break;
+                        case 5: out_block<6>(sm, tk, par, g16, l16, D_h); break;
+                        case 6: out_block<5>(sm, tk, par, g16, l16, D_h); break;
+                        default: out_block<4>(sm, tk, par, g16, l16, D_h); break;
                     }
                 }
             }
@@ -852,17 +881,16 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
                 if (k + 3 < k_end) load_sc(k + 3);
             }
             if (more) {
+                if (kFull) write_z(k + 1);
                 if (kPrep) prep(k + 1);
-                else prep_x();
+                else prep_x(k + 1);
                 __syncthreads();
                 if (kPrep) write_prep(); else write_x();
-                write_state();
-                if (kFull) zy_exchange(k, true, true);
             }
         }
         if (kFull) {
             __syncthreads();
-            zy_exchange(k_end - 1, true, false);
+            store_y(k_end - 1);
         }
     };
     if (wv < 4) role_loop(std::true_type{});
@@ -926,7 +954,7 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const int p = 8 * wv + j;
-                const float x0 = (float)sm.X[p][2 * ul], x1 = (float)sm.X[p][2 * ul + 1];
+                const float x0 = (float)sm.X[p][x_col(2 * ul)], x1 = (float)sm.X[p][x_col(2 * ul + 1)];
                 *reinterpret_cast<f32x2*>(&pb[p * N + 2 * pp]) = f32x2{ae0 * x0 + ae1 * x1, ao0 * x0 + ao1 * x1};
             }
         }
