@@ -1,5 +1,5 @@
-// Fused chunked-SSD prefill on bf16 MFMA for the d_state=128, headdim=64, mimo_rank=2
-// layer (the shape of the d_model 768 KulaMamba), gfx950.
+// Fused chunked-SSD prefill on MFMA for bf16 layers with d_state=128, headdim=64,
+// mimo_rank=2 (the shape of the d_model 768 KulaMamba), gfx950.
 //
 // Work decomposition
 // ------------------
@@ -8,7 +8,7 @@
 // chunks in order, carrying the (P=64, N=128) fp32 state in MFMA accumulators, so no
 // per-chunk state ever goes to HBM. Three launches:
 //   1. bc_norm:    per token and group, B^ = RMSNorm(B) * w + bias and C^ likewise in
-//                  bf16 (shared by every head, so computed once), pair-packed so that a
+//                  f16 (shared by every head, so computed once), pair-packed so that a
 //                  RoPE pair (n=2i, n=2i+1) of one rank is one 32-bit word.
 //   2. ssd_chunks<false> for segments 0..S-2: only the state update, giving each
 //                  segment's end state from a zero start plus its total log-decay and
@@ -17,27 +17,29 @@
 //                  into the incoming state, then computes every chunk's output.
 //
 // Per chunk (Q=64 tokens, rows (t,r) = 2t+r, 128 rows) the kernel forms in LDS
-//   C~ [(t,r)][n], B~ [(u,r')][n]      bf16, B^/C^ rotated by the RoPE angle
-//   B~w[u][n][r'] = B~ * w_u            bf16 (state-update operand)
-//   X^T[p][(u,r')] = x * mimo_x         bf16
-//   H[p][n]                             bf16 copy of the incoming state
-//   Lc[t][u] = [u<=t] exp(c_t-c_u) (a_u + [u<t] b_u)   fp32
-// and runs four MFMA contractions (v_mfma_f32_16x16x32_bf16):
+//   C~ [(t,r)][n], B~ [(u,r')][n]      f16, B^/C^ rotated by the RoPE angle
+//   X^T[p][(u,r')] = x * mimo_x         f16 (columns permuted for the G2 operand reads)
+//   Xw [p][(u,r')] = X^T * w_u          f16 (state-update operand, w_u the chunk weight)
+//   H[p][n]                             f16 copy of the incoming state, scaled by 1/256
+// and runs four MFMA contractions (v_mfma_f32_16x16x32_f16, fp32 accumulation):
 //   G3  Y  = diag(e^{c_t}) C~ H^T          inter-chunk output
-//   G1  S^T = B~ C~^T, masked by Lc (+D on the diagonal), kept in registers
+//   G1  S^T = B~ C~^T, masked by Lc[t][u] = [u<=t] exp(c_t-c_u) (a_u + [u<t] b_u)
+//       (+D on the diagonal), kept in registers
 //   G2  Y += S X                           intra-chunk output, S fed straight from the
 //                                          G1 accumulators as the A operand (the k
-//                                          order is permuted consistently in X)
-//   G4  H^T = e^{c_63} H^T + B~w^T X       state update
-// All eight waves share the element-wise preparation. In the MFMA phase waves 0-3 own
-// the 16-row output blocks {w, 7-w} (balanced causal work) and waves 4-7 own the state
-// update, so each SIMD interleaves one output wave with one state wave.
+//                                          order is permuted consistently in X^T)
+//   G4  H^T = e^{c_63} H^T + B~^T Xw       state update (A operand by LDS transpose
+//                                          reads of the B~ tile)
+// Roles: SIMD s runs waves s and s+4. Every wave holds 16 state rows and runs its share
+// of G4; wave s then computes output block s and wave s+4 output block 7-s (so each
+// SIMD carries the same causal work), wave s prepares the RoPE rotation of pairs
+// 16s..16s+15 for the next chunk and wave s+4 a quarter of X^T / Xw.
 // The trapezoid is folded into a_u = lambda_u dt_u, b_u = (1-lambda_{u+1}) dt_{u+1}
 // (the beta term of token u+1 multiplies B~_u x_u), so the rank is not doubled.
 //
 // Memory: every global read goes through a buffer descriptor whose size ends at the
 // batch row's last token, so reads past the sequence return zero (padding for free).
-// The next chunk's reads are issued as soon as a wave finishes its MFMA work.
+// The next chunk's reads are issued right after the state update.
 //
 // RoPE frame: inside a segment every angle is taken relative to the segment start.
 // Dot products C~.B~ and C~.H are invariant under a common rotation, so outputs are
@@ -431,9 +433,9 @@ __device__ __forceinline__ void out_block(Smem& sm, const Tok& tk, int par, int 
 //              z of chunk k+1 staged; element-wise preparation of chunk k+1 into registers
 //   barrier -> W(k+1): registers -> LDS tiles (C~, B~, X^T, X^T w)
 // Roles: SIMD s runs waves s and s+4. Wave s owns output block s (light: 1..4 causal
-// column blocks) and prepares the RoPE-rotated B~ / C~ / B~w tiles of pairs
-// 16s .. 16s+15; wave s+4 owns output block 7-s (heavy: 5..8 column blocks) and
-// prepares a quarter of the X^T tile; wave 0 also computes the token scalars. So each
+// column blocks) and prepares the RoPE-rotated B~ / C~ tiles of pairs 16s .. 16s+15;
+// wave s+4 owns output block 7-s (heavy: 5..8 column blocks) and prepares a quarter of
+// the X^T and X^T w tiles; wave 0 also computes the token scalars. So each
 // SIMD carries the same matrix and element-wise work. The two roles run separate copies
 // of the loop (same barrier sequence), so their loop-carried registers are allocated
 // independently.
@@ -523,7 +525,7 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
     float logdecay = 0.f;  // total log-decay of the segment (natural log)
     float phi_run0 = 0.f, phi_run1 = 0.f;  // pair angles relative to the segment start, turns
 
-    // ---- G4: H^T = e^{c_63} H^T + B~w^T X on chunk k's tiles (all waves)
+    // ---- G4: H^T = e^{c_63} H^T + B~^T Xw on chunk k's tiles (all waves)
     auto state_update = [&](const Tok& tk) {
         const int lane = opaque(threadIdx.x & 63);
         const int g16 = lane >> 4, l16 = lane & 15;
