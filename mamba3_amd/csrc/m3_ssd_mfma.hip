@@ -61,7 +61,8 @@ constexpr int P = 64;
 constexpr int R = 2;
 constexpr int NR = N * R;
 constexpr int NH = N / 2;
-constexpr int THREADS = 512;
+constexpr int THREADS = 1024;  // 8 MFMA waves + 8 helper waves, four per SIMD
+constexpr int NMW = 8;          // waves 0..7 run the MFMA work, 8..15 are helpers
 constexpr int PAD = 8;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kRsrcFlags = 0x00020000;
@@ -84,7 +85,7 @@ constexpr int NSLOT = 3;
 // G3 row scale multiplies by 1/kHScale.
 constexpr float kHScale = 1.f / 256.f;  // token-scalar ring: chunks k, k+1 read while k+2 is written
 
-// Per-chunk token scalars (index = token within the chunk), written by wave 0.
+// Per-chunk token scalars (index = token within the chunk), written by MFMA wave 0.
 struct Tok {
     float c2[Q];   // inclusive prefix of A*dt over the chunk, log2 units
     float av[Q];   // a_u = lambda_u dt_u
@@ -92,20 +93,22 @@ struct Tok {
     float ec[Q];   // exp2(c2_u)
     float hb[Q];   // exp2(c2[8*(u/8)+7] - c2_u) (a_u + b_u): decay to the end of u's 8-block
     float dtr[Q];  // dt_u / (2 pi): RoPE angle increment per unit theta, in turns
-    float w[Q];    // exp2(c2[63] - c2_u) (a_u + b_u): chunk-state weight
+    f16 w16[Q];    // exp2(c2[63] - c2_u) (a_u + b_u): chunk-state weight
 };
 
 struct __align__(16) Smem {
-    f16 C[Q * R][N + PAD];  // C~ rows (t,r) = 2t+r; 16-byte column chunks swizzled (sw_cb)
-    f16 B[Q * R][N + PAD];  // B~ rows (u,r'), same swizzle
-    f16 Xw[P][Q * R + PAD];  // X^T * w_u (state-update operand)
-    f16 X[P][Q * R + PAD];   // X^T
-    f16 H[2][P][N + PAD];    // incoming state times kHScale, double-buffered by chunk parity
-    bf16 ZY[2][Q][P];        // z of the chunk, overwritten in place by its gated output y;
-                             // double-buffered by chunk parity; 16-byte chunks swizzled
+    f16 C[Q * R][N + PAD];    // C~ rows (t,r) = 2t+r; 16-byte column chunks swizzled (sw_cb)
+    f16 B[Q * R][N + PAD];    // B~ rows (u,r'), same swizzle
+    f16 X[2][Q * R][P];       // X rows (u,r') = x_u * mimo_x[r'], columns p swizzled (xsw);
+                              // double-buffered by chunk parity
+    f16 H[P][N + PAD];        // incoming state times kHScale
+    unsigned Gt[2][Q][P];     // gate factors (g_0, g_1) as a bf16 pair per (t, p), columns
+                              // swizzled (gsw); the low half is then replaced by the output.
+                              // Double-buffered by chunk parity.
     Tok tok[NSLOT];
-    float rot[NH];           // per-pair angle scratch (prologue / epilogue)
-    float mzd[P][4];         // per p: -mimo_z[0] log2e, -mimo_z[1] log2e, mimo_down*mimo_z [0], [1]
+    float rot[NH];            // per-pair angle scratch (prologue / epilogue)
+    float mzdT[4][P];         // per p: -mimo_z[0] log2e, -mimo_z[1] log2e, mimo_down*mimo_z [0], [1]
+    f16 mxT[R][P];            // mimo_x per rank and p
 };
 
 struct Args {
@@ -176,12 +179,29 @@ __device__ __forceinline__ float fast_softplus(float x) {
     return x > 20.f ? x : __logf(1.f + fast_exp(x));
 }
 
-__device__ __forceinline__ float wave_incl_scan(float v, int lane) {
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const float o = __shfl_up(v, off, 64);
-        if (lane >= off) v += o;
-    }
+// Lane exchange through ds_bpermute: value of lane src. The index is computed by the
+// caller from its own lane number, so no address register lives across loops.
+__device__ __forceinline__ float bperm(float v, int src) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src << 2, __builtin_bit_cast(int, v)));
+}
+// DPP move: lanes whose source is outside the row (or outside row_mask) read 0.
+template <int kCtrl, int kRowMask = 0xf>
+__device__ __forceinline__ float dpp0(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, kRowMask,
+                                                                 0xf, true));
+}
+constexpr int kRowShr = 0x110;      // row_shr:n = kRowShr + n
+constexpr int kRowBcast15 = 0x142;  // lane 15 of each row to the next row
+constexpr int kRowBcast31 = 0x143;  // lane 31 to rows 2 and 3
+// Inclusive prefix sum over the 64 lanes: within 16-lane rows by row shifts, then across
+// rows by the row broadcasts.
+__device__ __forceinline__ float wave_incl_scan(float v) {
+    v += dpp0<kRowShr + 1>(v);
+    v += dpp0<kRowShr + 2>(v);
+    v += dpp0<kRowShr + 4>(v);
+    v += dpp0<kRowShr + 8>(v);
+    v += dpp0<kRowBcast15, 0xa>(v);
+    v += dpp0<kRowBcast31, 0xc>(v);
     return v;
 }
 
@@ -203,16 +223,13 @@ __device__ __forceinline__ unsigned bits(f16x2 v) { return __builtin_bit_cast(un
 // block, so the preparation's 64-bit stores (lanes 16 rows apart) hit distinct banks.
 // MFMA operand reads cover 16 rows of one block, so their pattern is only permuted.
 __device__ __forceinline__ int sw_cb(int row, int col) { return col ^ (32 * ((row >> 4) & 3)); }
-// ZY tile: column of 16-byte chunk c of token row t. Swapping chunk pairs on every other
-// token pair keeps both the 128-bit staging accesses and the epilogue's 16-bit accesses
-// (rows 2 apart across lanes) free of bank conflicts.
-__device__ __forceinline__ int zy_col(int t, int c) { return 8 * (c ^ (2 * ((t >> 1) & 1))); }
-// X^T tile (G2 operand): logical column c = 32 s + 16 jj + 4 g + v is stored at
-// 32 s + 8 g + 4 jj + v, so the 8 k-values one lane feeds to G2 (jj = 0, 1 for its g) are
-// one contiguous 16-byte chunk (a single ds_read_b128).
-__device__ __forceinline__ int x_col(int c) {
-    return (c & ~31) | (((c >> 2) & 3) << 3) | (((c >> 4) & 1) << 2) | (c & 3);
-}
+// X tile [(u,r)][p] (128-byte rows): 16-column groups XOR-swizzled by (row/2)%4, so the
+// transpose reads of the MFMA operands (4 rows x 16 columns per 16 lanes, 8 rows per
+// 32-lane pass) and the 128-bit row writes are free of bank conflicts.
+__device__ __forceinline__ int xsw(int row, int col) { return col ^ (16 * ((row >> 1) & 3)); }
+// Gate tile [t][p] of 32-bit words: 16-word groups swapped on every other token pair, so
+// the MFMA waves' 32-bit accesses (rows 2 apart across 16-lane groups) use distinct banks.
+__device__ __forceinline__ int gsw(int t, int p) { return p ^ (16 * ((t >> 1) & 1)); }
 
 
 
@@ -263,24 +280,32 @@ __global__ __launch_bounds__(256) void bc_norm(const bf16* __restrict__ proj, in
 // ---------------------------------------------------------------------------------
 // 2/3. Segment kernels.
 // ---------------------------------------------------------------------------------
-// Output rows of one 16-row block I of chunk s0 (tokens 8I .. 8I+7, rows (t,r) = 2t+r):
-//   G3  Y  = diag(e^{c_t}) C~ H^T                       (inter-chunk)
-//   G1  S^T = B~ C~^T for the causal column blocks J <= I, kept in registers,
-//       scaled by Lc[t][u] = [u<=t] exp(c_t-c_u) (a_u + [u<t] b_u) (+D on the diagonal)
-//   G2  Y += S X, S fed as the A operand straight from the G1 accumulators (the k order
-//       is permuted consistently in the X operand reads)
-// then the SiLU(z * mimo_z) gate and the MIMO-down sum, stored as bf16.
-// Scheduling fence: keeps the LDS operand reads issued one tile ahead of the MFMAs that
-// consume them (the compiler otherwise sinks each read next to its use and waits on it).
+// Scheduling fence: keeps LDS operand reads issued ahead of the MFMAs that consume them
+// (the compiler otherwise sinks each read next to its use and waits on it).
 #define M3_FENCE() __builtin_amdgcn_sched_barrier(0)
 // Compiler memory fence between LDS stores (no instruction): stops the pairing of
-// neighbouring stores into ds_write2_b64.
+// neighbouring stores into ds_write2_b64, which is about twice as slow as two single
+// 64-bit stores on gfx950.
 #define M3_LDS_FENCE() asm volatile("" ::: "memory")
 
+__device__ __forceinline__ f16x8 cat8(const f16x4& lo, const f16x4& hi) {
+    return f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// Output rows of one 16-row block I of the chunk (tokens 8I .. 8I+7, rows (t,r) = 2t+r),
+// computed by one MFMA wave:
+//   G3  Y  = diag(e^{c_t}) C~ H^T                       (inter-chunk)
+//   G1  S^T = B~ C~^T for the causal column blocks J <= I, two blocks at a time; each pair
+//       is scaled by Lc[t][u] = [u<=t] exp(c_t-c_u) (a_u + [u<t] b_u) (+D on the
+//       diagonal) and fed straight into
+//   G2  Y += S X as the A operand. The pair's accumulator rows give this lane the k values
+//       (u,r') = 32 s2 + 4 g + v and 32 s2 + 16 + 4 g + v (g = lane/16, v < 4); the X
+//       operand is read with transpose reads in the same row order.
+// Then out[t][p] = y_0 g_0 + y_1 g_1 with the gate factors of the gate tile; the bf16
+// result replaces the low half of the factor word.
 template <int I>
 __device__ __forceinline__ void out_block(Smem& sm, const Tok& tk, int par, int g16, int l16, float D_h) {
-
-    constexpr int NJ = I + 1;
+    constexpr int NP = I / 2 + 1;  // column-block pairs
     // Token scalars this lane needs (rows t_col, columns u = 8J + 2 g16 + {0,1}).
     const int t_col = 8 * I + (l16 >> 1);
     const int r_col = l16 & 1;
@@ -288,27 +313,16 @@ __device__ __forceinline__ void out_block(Smem& sm, const Tok& tk, int par, int 
     const float ct = tk.c2[t_col];
     // e^{c_t}, times 1/kHScale for the scaled f16 state copy
     const f32x2 ecv = *reinterpret_cast<const f32x2*>(&tk.ec[u0d]) * (1.f / kHScale);
-    const f32x2 cud = *reinterpret_cast<const f32x2*>(&tk.c2[u0d]);
-    const f32x2 aud = *reinterpret_cast<const f32x2*>(&tk.av[u0d]);
-    const f32x2 bud = *reinterpret_cast<const f32x2*>(&tk.bv[u0d]);
-    float cref[NJ];
-    f32x2 hv[NJ];
-#pragma unroll
-    for (int J = 0; J < I; ++J) {
-        cref[J] = tk.c2[8 * J + 7];
-        hv[J] = *reinterpret_cast<const f32x2*>(&tk.hb[8 * J + 2 * g16]);
-    }
 
     // C~ rows of this block (logical column 32s + 8 g16 sits at 32 (s ^ (I&3)) + 8 g16)
     // and the first H operand group.
     f16x8 cA[4], hop[2][4];
 #pragma unroll
     for (int s = 0; s < 4; ++s)
-        cA[s] = *reinterpret_cast<const f16x8*>(
-            &sm.C[16 * I + l16][8 * g16 + 32 * (s ^ (I & 3))]);
+        cA[s] = *reinterpret_cast<const f16x8*>(&sm.C[16 * I + l16][8 * g16 + 32 * (s ^ (I & 3))]);
 #pragma unroll
     for (int s = 0; s < 4; ++s)
-        hop[0][s] = *reinterpret_cast<const f16x8*>(&sm.H[par][l16][32 * s + 8 * g16]);
+        hop[0][s] = *reinterpret_cast<const f16x8*>(&sm.H[l16][32 * s + 8 * g16]);
     M3_FENCE();
     // G3: Y = C~ H^T (scaled by e^{c_t} below)
     f32x4 yacc[4];
@@ -317,33 +331,12 @@ __device__ __forceinline__ void out_block(Smem& sm, const Tok& tk, int par, int 
         if (pt + 1 < 4) {
 #pragma unroll
             for (int s = 0; s < 4; ++s)
-                hop[(pt + 1) & 1][s] = *reinterpret_cast<const f16x8*>(&sm.H[par][16 * (pt + 1) + l16][32 * s + 8 * g16]);
+                hop[(pt + 1) & 1][s] = *reinterpret_cast<const f16x8*>(&sm.H[16 * (pt + 1) + l16][32 * s + 8 * g16]);
         }
         M3_FENCE();
         yacc[pt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s = 0; s < 4; ++s) yacc[pt] = mfma16(cA[s], hop[pt & 1][s], yacc[pt]);
-        M3_FENCE();
-    }
-    // G1: S^T = B~ C~^T for J <= I
-    f16x8 bop[2][4];
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-        bop[0][s] = *reinterpret_cast<const f16x8*>(&sm.B[l16][8 * g16 + 32 * s]);
-    M3_FENCE();
-    f32x4 sacc[NJ];
-#pragma unroll
-    for (int J = 0; J < NJ; ++J) {
-        if (J + 1 < NJ) {
-#pragma unroll
-            for (int s = 0; s < 4; ++s)
-                bop[(J + 1) & 1][s] = *reinterpret_cast<const f16x8*>(
-                    &sm.B[16 * (J + 1) + l16][8 * g16 + 32 * (s ^ ((J + 1) & 3))]);
-        }
-        M3_FENCE();
-        sacc[J] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s = 0; s < 4; ++s) sacc[J] = mfma16(bop[J & 1][s], cA[s], sacc[J]);
         M3_FENCE();
     }
 #pragma unroll
@@ -353,20 +346,41 @@ __device__ __forceinline__ void out_block(Smem& sm, const Tok& tk, int par, int 
         yacc[pt][2] *= ecv[1];
         yacc[pt][3] *= ecv[1];
     }
-    // Mask S^T by Lc (+D on the diagonal) and run G2: Y += S X.
-    // This lane's S^T values: rows (u, r') = (8J + 2 g16 + v/2, v&1), column (t_col, r_col).
-    f16x8 xop[2][4];
+
+    // Fused G1 / mask / G2 over pairs of causal column blocks.
+    const int jr = l16 >> 2, jc = 4 * (l16 & 3);
 #pragma unroll
-    for (int pt = 0; pt < 4; ++pt) xop[0][pt] = *reinterpret_cast<const f16x8*>(&sm.X[16 * pt + l16][8 * g16]);
-    M3_FENCE();
+    for (int s2 = 0; s2 < NP; ++s2) {
+        const int rlo = 32 * s2 + 4 * g16 + jr, rhi = rlo + 16;
+        f16x8 bop[4];
+        f16x4 xlo[4], xhi[4];
 #pragma unroll
-    for (int s2 = 0; s2 <= I / 2; ++s2) {
-        if (s2 + 1 <= I / 2) {
+        for (int s = 0; s < 4; ++s)
+            bop[s] = *reinterpret_cast<const f16x8*>(&sm.B[32 * s2 + l16][8 * g16 + 32 * (s ^ ((2 * s2) & 3))]);
 #pragma unroll
-            for (int pt = 0; pt < 4; ++pt)
-                xop[(s2 + 1) & 1][pt] = *reinterpret_cast<const f16x8*>(&sm.X[16 * pt + l16][32 * (s2 + 1) + 8 * g16]);
+        for (int pt = 0; pt < 4; ++pt) {
+            xlo[pt] = ld_tr(&sm.X[par][rlo][xsw(rlo, 16 * pt + jc)]);
+            xhi[pt] = ld_tr(&sm.X[par][rhi][xsw(rhi, 16 * pt + jc)]);
         }
         M3_FENCE();
+        f32x4 sacc[2];
+        sacc[0] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) sacc[0] = mfma16(bop[s], cA[s], sacc[0]);
+        M3_FENCE();
+        sacc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (2 * s2 + 1 <= I) {
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+                bop[s] = *reinterpret_cast<const f16x8*>(
+                    &sm.B[32 * s2 + 16 + l16][8 * g16 + 32 * (s ^ ((2 * s2 + 1) & 3))]);
+            M3_FENCE();
+#pragma unroll
+            for (int s = 0; s < 4; ++s) sacc[1] = mfma16(bop[s], cA[s], sacc[1]);
+            M3_FENCE();
+        }
+        // This lane's S^T values of block J: rows (u, r') = (8J + 2 g16 + v/2, v&1),
+        // column (t_col, r_col).
         f16x8 aop;
 #pragma unroll
         for (int jj = 0; jj < 2; ++jj) {
@@ -375,24 +389,25 @@ __device__ __forceinline__ void out_block(Smem& sm, const Tok& tk, int par, int 
             if (J < I) {
                 // u < t: exp(c_t - c_u)(a_u + b_u), split at the end of u's 8-block so
                 // both factors are at most one.
-                const float gt = __builtin_amdgcn_exp2f(ct - cref[J < I ? J : 0]);
-                const f32x2 hj = hv[J < I ? J : 0];
+                const float gt = __builtin_amdgcn_exp2f(ct - tk.c2[8 * J + 7]);
+                const f32x2 hj = *reinterpret_cast<const f32x2*>(&tk.hb[8 * J + 2 * g16]);
                 const float l0 = gt * hj[0], l1 = gt * hj[1];
-                const f32x4 sv = sacc[J < NJ ? J : 0];
-                m0 = sv[0] * l0;
-                m1 = sv[1] * l0;
-                m2 = sv[2] * l1;
-                m3 = sv[3] * l1;
+                m0 = sacc[jj][0] * l0;
+                m1 = sacc[jj][1] * l0;
+                m2 = sacc[jj][2] * l1;
+                m3 = sacc[jj][3] * l1;
             } else if (J == I) {
+                const f32x2 cud = *reinterpret_cast<const f32x2*>(&tk.c2[u0d]);
+                const f32x2 aud = *reinterpret_cast<const f32x2*>(&tk.av[u0d]);
+                const f32x2 bud = *reinterpret_cast<const f32x2*>(&tk.bv[u0d]);
                 const float e0 = __builtin_amdgcn_exp2f(ct - cud[0]);
                 const float e1 = __builtin_amdgcn_exp2f(ct - cud[1]);
                 const float l0 = u0d <= t_col ? e0 * (aud[0] + (u0d < t_col ? bud[0] : 0.f)) : 0.f;
                 const float l1 = u0d + 1 <= t_col ? e1 * (aud[1] + (u0d + 1 < t_col ? bud[1] : 0.f)) : 0.f;
-                const f32x4 sv = sacc[J < NJ ? J : 0];
-                m0 = sv[0] * l0;
-                m1 = sv[1] * l0;
-                m2 = sv[2] * l1;
-                m3 = sv[3] * l1;
+                m0 = sacc[jj][0] * l0;
+                m1 = sacc[jj][1] * l0;
+                m2 = sacc[jj][2] * l1;
+                m3 = sacc[jj][3] * l1;
                 if (u0d == t_col) { if (r_col == 0) m0 += D_h; else m1 += D_h; }
                 if (u0d + 1 == t_col) { if (r_col == 0) m2 += D_h; else m3 += D_h; }
             }
@@ -402,43 +417,41 @@ __device__ __forceinline__ void out_block(Smem& sm, const Tok& tk, int par, int 
             aop[4 * jj + 3] = (f16)m3;
         }
 #pragma unroll
-        for (int pt = 0; pt < 4; ++pt) yacc[pt] = mfma16(aop, xop[s2 & 1][pt], yacc[pt]);
+        for (int pt = 0; pt < 4; ++pt) yacc[pt] = mfma16(aop, cat8(xlo[pt], xhi[pt]), yacc[pt]);
         M3_FENCE();
     }
 
-    // Gate: out = sum_r mimo_down_r y_r silu(z mimo_z_r), with
-    // silu(v0) y0' + silu(v1) y1' = (v0 y0' (1+e1) + v1 y1' (1+e0)) / ((1+e0)(1+e1)),
-    // e_r = exp(-v_r) clamped at 2^60 so the product stays finite. z is read from the ZY
-    // tile and the output overwrites it in place (stored to HBM by the whole workgroup).
+    // out = y_0 g_0 + y_1 g_1, written over the low half of the factor word.
 #pragma unroll
     for (int pt = 0; pt < 4; ++pt) {
         const int p = 16 * pt + l16;
-        const f32x4 g = *reinterpret_cast<const f32x4*>(&sm.mzd[p][0]);
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
             const int t = 8 * I + 2 * g16 + tt;
-            bf16* zy = &sm.ZY[par][t][zy_col(t, p >> 3) + (p & 7)];
-            const float z = (float)*zy;
-            const float e0 = 1.f + __builtin_amdgcn_exp2f(fminf(z * g[0], 60.f));
-            const float e1 = 1.f + __builtin_amdgcn_exp2f(fminf(z * g[1], 60.f));
-            const float num = (z * g[2]) * yacc[pt][2 * tt] * e1 + (z * g[3]) * yacc[pt][2 * tt + 1] * e0;
-            *zy = (bf16)(num * __builtin_amdgcn_rcpf(e0 * e1));
+            unsigned* gp = &sm.Gt[par][t][gsw(t, p)];
+            const unsigned gw = *gp;
+            const float o = yacc[pt][2 * tt] * bf16_f32(gw & 0xffffu) +
+                            yacc[pt][2 * tt + 1] * __builtin_bit_cast(float, gw & 0xffff0000u);
+            *reinterpret_cast<bf16*>(gp) = (bf16)o;
         }
     }
 }
 
-// Pipelined chunk walk. Per chunk k:
-//   barrier -> M(k): y of chunk k-1 stored; state update G4 on chunk k's tiles; f16 copy of
-//              the new state written; reads of chunk k+1 issued; output block of chunk k;
-//              z of chunk k+1 staged; element-wise preparation of chunk k+1 into registers
-//   barrier -> W(k+1): registers -> LDS tiles (C~, B~, X^T, X^T w)
-// Roles: SIMD s runs waves s and s+4. Wave s owns output block s (light: 1..4 causal
-// column blocks) and prepares the RoPE-rotated B~ / C~ tiles of pairs 16s .. 16s+15;
-// wave s+4 owns output block 7-s (heavy: 5..8 column blocks) and prepares a quarter of
-// the X^T and X^T w tiles; wave 0 also computes the token scalars. So each
-// SIMD carries the same matrix and element-wise work. The two roles run separate copies
-// of the loop (same barrier sequence), so their loop-carried registers are allocated
-// independently.
+// Pipelined chunk walk, per chunk k:
+//   barrier A -> M(k): MFMA waves: state update G4 on chunk k's tiles, output block of
+//                chunk k. Helper waves: RoPE rotation, X rows and gate factors of chunk k+1
+//                (X rows and gate factors straight into the buffers of the other parity),
+//                reads of chunk k+2 issued as registers free up.
+//   barrier B -> W(k+1): MFMA waves write the f16 state copy H_{k+1}; helper waves store
+//                chunk k's output and write the C~ / B~ tiles of chunk k+1.
+// Roles (SIMD s runs waves s, s+4, s+8, s+12):
+//   MFMA wave w < 8: state rows n = 16w .. 16w+15; output block w (w < 4) or 11-w, so
+//                each SIMD carries blocks {s, 7-s} (the same causal work); wave 0 also
+//                computes the token scalars two chunks ahead.
+//   helper wave 8+h: RoPE pairs 16 (h%4) + 2 (lane%8) + {0, 1} for tokens 8 (lane/8) +
+//                4 (h/4) + {0..3}; X rows and gate factors of token 8h + lane/8, columns
+//                8 (lane%8) .. +7. Helpers issue every global read and store, so the MFMA
+//                waves never wait on memory.
 template <bool kFull>
 __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
     __shared__ Smem sm;
@@ -467,21 +480,29 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
     const int lane0 = tid & 63;
     if (kFull && tid < P) {
         const float z0 = a.prm.mimo_z[(h * P + tid) * R], z1 = a.prm.mimo_z[(h * P + tid) * R + 1];
-        sm.mzd[tid][0] = -z0 * kLog2e;
-        sm.mzd[tid][1] = -z1 * kLog2e;
-        sm.mzd[tid][2] = a.prm.mimo_down[(h * P + tid) * R] * z0;
-        sm.mzd[tid][3] = a.prm.mimo_down[(h * P + tid) * R + 1] * z1;
+        sm.mzdT[0][tid] = -z0 * kLog2e;
+        sm.mzdT[1][tid] = -z1 * kLog2e;
+        sm.mzdT[2][tid] = a.prm.mimo_down[(h * P + tid) * R] * z0;
+        sm.mzdT[3][tid] = a.prm.mimo_down[(h * P + tid) * R + 1] * z1;
+    }
+    if (tid < P) {
+        sm.mxT[0][tid] = (f16)a.prm.mimo_x[(h * P + tid) * R];
+        sm.mxT[1][tid] = (f16)a.prm.mimo_x[(h * P + tid) * R + 1];
     }
 
-    // State accumulators: wave w owns the H^T rows n in [16w, 16w+16), all 64 columns p.
+    // State accumulators of the MFMA waves: wave w owns the H^T rows n in [16w, 16w+16),
+    // all 64 columns p.
     f32x4 hacc[4];
 #pragma unroll
     for (int pt = 0; pt < 4; ++pt) hacc[pt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // Preparation lanes of waves 0-3: pairs pa = 16 wave + 2 (lane%8) and pa+1, tokens
-    // 8 (lane/8) .. +7. phi_start: absolute angles (radians) of the two pairs at the
-    // segment start.
-    const int pa0 = 16 * (wv & 3) + 2 * (lane0 & 7);
+    // Helper lanes: hw = helper index, q = token octet, c8 = column slot.
+    const int hw = wv - NMW;
+    const int q8 = lane0 >> 3, c8 = lane0 & 7;
+    // RoPE pairs of helper lanes (pa0, pa0+1); pair lanes (helpers 0-3, lanes 0-7) own the
+    // per-pair outputs. phi_start: absolute angles (radians) of the pairs at the segment start.
+    const int pa0 = 16 * (hw & 3) + 2 * c8;
+    const bool pair_lane = wv >= NMW && hw < 4 && q8 == 0;
     float phi_start0 = 0.f, phi_start1 = 0.f;
     if (kFull && seg > 0) {
         // H = sum_i exp(sum_{l=i+1}^{seg-1} D_l) R(-sum_{l=i}^{seg-1} Phi_l) S_i
@@ -495,27 +516,31 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
                 sm.rot[tid] = acc + a.seg_angle[(sbase + i) * NH + tid];
             }
             __syncthreads();
-            const float wgt = __expf(dsum);
-            const float* Si = a.seg_state + (sbase + i) * (int64_t)N * P;
-            const int n0 = 16 * wv + 4 * g16;
-            float s0, c0, s1, c1;
-            sincosf(-sm.rot[n0 / 2], &s0, &c0);
-            sincosf(-sm.rot[n0 / 2 + 1], &s1, &c1);
+            if (wv < NMW) {
+                const float wgt = __expf(dsum);
+                const float* Si = a.seg_state + (sbase + i) * (int64_t)N * P;
+                const int n0 = 16 * wv + 4 * g16;
+                float s0, c0, s1, c1;
+                sincosf(-sm.rot[n0 / 2], &s0, &c0);
+                sincosf(-sm.rot[n0 / 2 + 1], &s1, &c1);
 #pragma unroll
-            for (int pt = 0; pt < 4; ++pt) {
-                const int p = 16 * pt + l16;
-                const float e0 = Si[(n0 + 0) * P + p], o0 = Si[(n0 + 1) * P + p];
-                const float e1 = Si[(n0 + 2) * P + p], o1 = Si[(n0 + 3) * P + p];
-                hacc[pt][0] += wgt * (e0 * c0 - o0 * s0);
-                hacc[pt][1] += wgt * (e0 * s0 + o0 * c0);
-                hacc[pt][2] += wgt * (e1 * c1 - o1 * s1);
-                hacc[pt][3] += wgt * (e1 * s1 + o1 * c1);
+                for (int pt = 0; pt < 4; ++pt) {
+                    const int p = 16 * pt + l16;
+                    const float e0 = Si[(n0 + 0) * P + p], o0 = Si[(n0 + 1) * P + p];
+                    const float e1 = Si[(n0 + 2) * P + p], o1 = Si[(n0 + 3) * P + p];
+                    hacc[pt][0] += wgt * (e0 * c0 - o0 * s0);
+                    hacc[pt][1] += wgt * (e0 * s0 + o0 * c0);
+                    hacc[pt][2] += wgt * (e1 * c1 - o1 * s1);
+                    hacc[pt][3] += wgt * (e1 * s1 + o1 * c1);
+                }
             }
             dsum += a.seg_decay[sbase + i];
         }
         __syncthreads();
-        phi_start0 = sm.rot[pa0];  // sum_{l<seg} Phi_l
-        phi_start1 = sm.rot[pa0 + 1];
+        if (pair_lane) {
+            phi_start0 = sm.rot[pa0];  // sum_{l<seg} Phi_l
+            phi_start1 = sm.rot[pa0 + 1];
+        }
     }
 
     const bf16* proj_b = a.proj + (int64_t)b * T * a.rs;
@@ -525,255 +550,58 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
     float logdecay = 0.f;  // total log-decay of the segment (natural log)
     float phi_run0 = 0.f, phi_run1 = 0.f;  // pair angles relative to the segment start, turns
 
-    // ---- G4: H^T = e^{c_63} H^T + B~^T Xw on chunk k's tiles (all waves)
-    auto state_update = [&](const Tok& tk) {
-        const int lane = opaque(threadIdx.x & 63);
-        const int g16 = lane >> 4, l16 = lane & 15;
-        const float dch = tk.ec[Q - 1];
+    if (wv < NMW) {
+        // ======================= MFMA waves =======================
+        // ---- G4: H^T = e^{c_63} H^T + (B~ diag(w))^T X on chunk k's tiles
+        auto state_update = [&](const Tok& tk, int par) {
+            const int lane = opaque(threadIdx.x & 63);
+            const int g16 = lane >> 4, l16 = lane & 15;
+            const float dch = tk.ec[Q - 1];
 #pragma unroll
-        for (int pt = 0; pt < 4; ++pt) hacc[pt] *= dch;
-        // A operand (B~^T, rows n = 16 wave + lane%16, k = (u, r)) by transpose reads of the
-        // B~ tile: lane j of a 16-lane group addresses row k0 + j/4, columns n0 + 4 (j%4)
-        // (the tile swizzle is uniform over the 8 rows k0 .. k0+7 of one group).
-        const int jr = (lane & 15) >> 2, jc = 4 * (lane & 3);
-        const int n0 = 16 * wv;
-        auto a_ptr = [&](int s, int half) {
-            const int row = 32 * s + 8 * g16 + 4 * half + jr;
-            return &sm.B[row][sw_cb(row, n0 + jc)];
-        };
-        f16x4 aop_lo[2], aop_hi[2];
-        f16x8 xop[2][4];
-        aop_lo[0] = ld_tr(a_ptr(0, 0));
-        aop_hi[0] = ld_tr(a_ptr(0, 1));
+            for (int pt = 0; pt < 4; ++pt) hacc[pt] *= dch;
+            // Operand k order (u,r) = 32 s + 16 half + 4 g16 + m. A operand (B~^T, rows
+            // n = 16 wave + lane%16) and B operand (X, columns p) both come from transpose
+            // reads: lane j of a 16-lane group addresses row k0 + j/4, columns c0 + 4 (j%4).
+            const int jr = l16 >> 2, jc = 4 * (l16 & 3);
+            const int n0 = 16 * wv;
 #pragma unroll
-        for (int pt = 0; pt < 4; ++pt)
-            xop[0][pt] = *reinterpret_cast<const f16x8*>(&sm.Xw[16 * pt + l16][8 * g16]);
-        M3_FENCE();
+            for (int s = 0; s < 4; ++s) {
+                const int rlo = 32 * s + 4 * g16 + jr, rhi = rlo + 16;
+                const f16x4 alo = ld_tr(&sm.B[rlo][sw_cb(rlo, n0 + jc)]);
+                const f16x4 ahi = ld_tr(&sm.B[rhi][sw_cb(rhi, n0 + jc)]);
+                f16x4 xlo[4], xhi[4];
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            if (s + 1 < 4) {
-                aop_lo[(s + 1) & 1] = ld_tr(a_ptr(s + 1, 0));
-                aop_hi[(s + 1) & 1] = ld_tr(a_ptr(s + 1, 1));
+                for (int pt = 0; pt < 4; ++pt) {
+                    xlo[pt] = ld_tr(&sm.X[par][rlo][xsw(rlo, 16 * pt + jc)]);
+                    xhi[pt] = ld_tr(&sm.X[par][rhi][xsw(rhi, 16 * pt + jc)]);
+                }
+                // chunk-state weights of tokens 16s + 2 g16 + {0,1} and 16s + 8 + 2 g16 + {0,1}
+                const f16x2 wlo = *reinterpret_cast<const f16x2*>(&tk.w16[16 * s + 2 * g16]);
+                const f16x2 whi = *reinterpret_cast<const f16x2*>(&tk.w16[16 * s + 8 + 2 * g16]);
+                M3_FENCE();
+                const f16x8 aop = {alo[0] * wlo[0], alo[1] * wlo[0], alo[2] * wlo[1], alo[3] * wlo[1],
+                                   ahi[0] * whi[0], ahi[1] * whi[0], ahi[2] * whi[1], ahi[3] * whi[1]};
 #pragma unroll
-                for (int pt = 0; pt < 4; ++pt)
-                    xop[(s + 1) & 1][pt] =
-                        *reinterpret_cast<const f16x8*>(&sm.Xw[16 * pt + l16][32 * (s + 1) + 8 * g16]);
+                for (int pt = 0; pt < 4; ++pt) hacc[pt] = mfma16(aop, cat8(xlo[pt], xhi[pt]), hacc[pt]);
+                M3_FENCE();
             }
-            M3_FENCE();
-            const f16x4 lo = aop_lo[s & 1], hi = aop_hi[s & 1];
-            const f16x8 aop = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-#pragma unroll
-            for (int pt = 0; pt < 4; ++pt) hacc[pt] = mfma16(aop, xop[s & 1][pt], hacc[pt]);
-            M3_FENCE();
-        }
-        logdecay += tk.c2[Q - 1] * (1.f / kLog2e);
-    };
-
-    // ---- bf16 copy of the state for G3 (all waves, W phase)
-    auto write_state = [&](int par) {
-        if (kFull) {
+            logdecay += tk.c2[Q - 1] * (1.f / kLog2e);
+        };
+        // ---- f16 copy of the state for G3 (W phase)
+        auto write_state = [&]() {
             const int lane = opaque(threadIdx.x & 63);
             const int g16 = lane >> 4, l16 = lane & 15;
             const int n0 = 16 * wv + 4 * g16;
 #pragma unroll
             for (int pt = 0; pt < 4; ++pt) {
                 const f32x4 v = hacc[pt] * kHScale;
-                *reinterpret_cast<f16x4*>(&sm.H[par][16 * pt + l16][n0]) =
+                *reinterpret_cast<f16x4*>(&sm.H[16 * pt + l16][n0]) =
                     f16x4{(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
             }
-        }
-    };
-
-    // ---- ZY staging (all 512 lanes, one 16-byte chunk each: token t = tid/8, chunk tid%8):
-    // z of chunk kk is read from HBM into a register during the preceding M phase and
-    // written to ZY in the W phase, right after the same lane has stored the previous
-    // chunk's y from the same LDS address.
-    u32x4 zreg = u32x4{0u, 0u, 0u, 0u};
-    auto load_z = [&](int kk) {
-        const int t = opaque(threadIdx.x) >> 3, c = threadIdx.x & 7;
-        const int s0 = kk * Q;
-        const __amdgpu_buffer_rsrc_t rz = make_rsrc(proj_b + (int64_t)s0 * a.rs, (int64_t)max(T - s0, 0) * a.rs * 2);
-        zreg = __builtin_amdgcn_raw_buffer_load_b128(rz, (t * rs + (int)a.pl.z + h * P + 8 * c) * 2, 0, 0);
-    };
-    auto store_y = [&](int kk) {  // y of chunk kk from its ZY buffer to HBM
-        const int t = opaque(threadIdx.x) >> 3, c = threadIdx.x & 7;
-        const u32x4 v = *reinterpret_cast<const u32x4*>(&sm.ZY[kk & 1][t][zy_col(t, c)]);
-        const int s0 = kk * Q;
-        const int HP = a.H * P;
-        const __amdgpu_buffer_rsrc_t ry =
-            make_rsrc(a.y_out + ((int64_t)b * T + s0) * HP, (int64_t)max(T - s0, 0) * HP * 2);
-        __builtin_amdgcn_raw_buffer_store_b128(v, ry, (t * HP + h * P + 8 * c) * 2, 0, 0);
-    };
-    auto write_z = [&](int kk) {  // z of chunk kk (in zreg) into its ZY buffer
-        const int t = opaque(threadIdx.x) >> 3, c = threadIdx.x & 7;
-        *reinterpret_cast<u32x4*>(&sm.ZY[kk & 1][t][zy_col(t, c)]) = zreg;
-    };
-
-    auto role_loop = [&](auto role) {
-        constexpr bool kPrep = decltype(role)::value;
-
-        // ---------------- preparation role (waves 0-3) ----------------
-        u32x4 rawB[8], rawC[8];
-        unsigned rawth[8];
-        u32x2 outB[8][2], outC[8][2];
-        auto load_prep = [&](int kk) {
-            const int lane = opaque(threadIdx.x & 63);
-            const int q = lane >> 3;
-            const int pa = 16 * (wv & 3) + 2 * (lane & 7);
-            const int s0 = kk * Q;
-            const int left = max(T - s0, 0);
-            const int64_t bcbytes = left > 0 ? ((int64_t)(left - 1) * bnrs + NR) * 2 : 0;
-            const __amdgpu_buffer_rsrc_t rb = make_rsrc(bn_b + (int64_t)s0 * bnrs, bcbytes);
-            const __amdgpu_buffer_rsrc_t rc = make_rsrc(cn_b + (int64_t)s0 * bnrs, bcbytes);
-            const int vbc = (8 * q * bnrs + 4 * pa) * 2;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                rawB[j] = __builtin_amdgcn_raw_buffer_load_b128(rb, vbc + j * bnrs * 2, 0, 0);
-                if (kFull) rawC[j] = __builtin_amdgcn_raw_buffer_load_b128(rc, vbc + j * bnrs * 2, 0, 0);
-            }
-            if (a.cplx) {
-                const __amdgpu_buffer_rsrc_t rp =
-                    make_rsrc(proj_b + (int64_t)s0 * a.rs, (int64_t)left * a.rs * 2);
-                const int vth = (8 * q * rs + (int)a.pl.theta + pa) * 2;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) rawth[j] = __builtin_amdgcn_raw_buffer_load_b32(rp, vth + j * rs * 2, 0, 0);
-            } else {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) rawth[j] = 0u;
-            }
         };
-        auto prep = [&](int kk) {
-            const int lane = opaque(threadIdx.x & 63);
-            const int q = lane >> 3;
-            const Tok& tk = sm.tok[kk % NSLOT];
-            const f32x4 d0 = *reinterpret_cast<const f32x4*>(&tk.dtr[8 * q]);
-            const f32x4 d1 = *reinterpret_cast<const f32x4*>(&tk.dtr[8 * q + 4]);
-            // RoPE angle increments (turns) of tokens 8q..8q+7 for both pairs; the prefix of
-            // the per-lane totals over q (lanes 8 apart) gives each lane's starting angles.
-            float inc0[8], inc1[8];
-            float tot0 = 0.f, tot1 = 0.f;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float dt = j < 4 ? d0[j] : d1[j - 4];
-                inc0[j] = dt * __builtin_bit_cast(float, rawth[j] << 16);
-                inc1[j] = dt * __builtin_bit_cast(float, rawth[j] & 0xffff0000u);
-                tot0 += inc0[j];
-                tot1 += inc1[j];
-            }
-            float incl0 = tot0, incl1 = tot1;
-#pragma unroll
-            for (int off = 8; off < 64; off <<= 1) {
-                const float o0 = __shfl_up(incl0, off, 64);
-                const float o1 = __shfl_up(incl1, off, 64);
-                if (lane >= off) {
-                    incl0 += o0;
-                    incl1 += o1;
-                }
-            }
-            const float ctot0 = __shfl(incl0, 56 + (lane & 7), 64);
-            const float ctot1 = __shfl(incl1, 56 + (lane & 7), 64);
-            float phi0 = phi_run0 - (incl0 - tot0);
-            float phi1 = phi_run1 - (incl1 - tot1);
-            phi_run0 -= ctot0;
-            phi_run1 -= ctot1;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                f16x2 rb[2][2];  // [pair][rank]: rotated (even, odd) of B^
-#pragma unroll
-                for (int pr = 0; pr < 2; ++pr) {
-                    float& phi = pr == 0 ? phi0 : phi1;
-                    phi -= pr == 0 ? inc0[j] : inc1[j];
-                    const float rev = __builtin_amdgcn_fractf(phi);
-                    const float sn = __builtin_amdgcn_sinf(rev), cs = __builtin_amdgcn_cosf(rev);
-                    // (e, o) -> (e cos - o sin, e sin + o cos) = e (cos, sin) + o (-sin, cos)
-                    const f16x2 kA = f16x2{(f16)cs, (f16)sn};
-                    const f16x2 kB = f16x2{(f16)(-sn), (f16)cs};
-#pragma unroll
-                    for (int r = 0; r < 2; ++r) {
-                        const f16x2 v = as_f16x2(rawB[j][2 * pr + r]);
-                        rb[pr][r] = f16x2{v[0], v[0]} * kA + f16x2{v[1], v[1]} * kB;
-                        if (kFull) {
-                            const f16x2 c = as_f16x2(rawC[j][2 * pr + r]);
-                            outC[j][r][pr] = bits(f16x2{c[0], c[0]} * kA + f16x2{c[1], c[1]} * kB);
-                        }
-                    }
-                }
-                // B~ is needed by both passes (G1 scores and, via transpose reads, G4)
-                outB[j][0] = u32x2{bits(rb[0][0]), bits(rb[1][0])};
-                outB[j][1] = u32x2{bits(rb[0][1]), bits(rb[1][1])};
-            }
-        };
-        auto write_prep = [&]() {
-            const int lane = opaque(threadIdx.x & 63);
-            const int q = lane >> 3;
-            const int pa = 16 * (wv & 3) + 2 * (lane & 7);
-            const int col = sw_cb(16 * q, 2 * pa);  // rows 16q .. 16q+15 share the swizzle
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                // The fences keep these as single 64-bit stores: the compiler would pair
-                // neighbouring rows into ds_write2_b64, which is about twice as slow here.
-                if (kFull) {
-                    *reinterpret_cast<u32x2*>(&sm.C[16 * q + 2 * j][col]) = outC[j][0];
-                    M3_LDS_FENCE();
-                    *reinterpret_cast<u32x2*>(&sm.C[16 * q + 2 * j + 1][col]) = outC[j][1];
-                    M3_LDS_FENCE();
-                }
-                *reinterpret_cast<u32x2*>(&sm.B[16 * q + 2 * j][col]) = outB[j][0];
-                M3_LDS_FENCE();
-                *reinterpret_cast<u32x2*>(&sm.B[16 * q + 2 * j + 1][col]) = outB[j][1];
-                M3_LDS_FENCE();
-            }
-        };
-
-        // ---------------- X / token-scalar role (waves 4-7) ----------------
-        unsigned rawx[16];
-        f16x8 outX[4], outXw[4];
+        // ---- token scalars (wave 0)
         unsigned sdt = 0u, sdt64 = 0u, slam = 0u, slam64 = 0u;
         float ssc = 1.f, ssc64 = 1.f;
-        const float mx0 = a.prm.mimo_x[(h * P + lane0) * R], mx1 = a.prm.mimo_x[(h * P + lane0) * R + 1];
-        auto load_x = [&](int kk) {
-            // X role: column p = lane for tokens 16 (wave-4) .. +15
-            const int lane = opaque(threadIdx.x & 63);
-            const int s0 = kk * Q;
-            const __amdgpu_buffer_rsrc_t rp = make_rsrc(proj_b + (int64_t)s0 * a.rs, (int64_t)max(T - s0, 0) * a.rs * 2);
-            const int vx = (16 * (wv - 4) * rs + (int)a.pl.x + h * P + lane) * 2;
-#pragma unroll
-            for (int j = 0; j < 16; ++j)
-                rawx[j] = ld_u16(rp, vx + j * rs * 2);
-        };
-        auto prep_x = [&](int kk) {
-            // X^T and X^T * w_u for tokens 16 (wave-4) .. +15 of chunk kk
-            const Tok& tk = sm.tok[kk % NSLOT];
-            float x0[16], x1[16];
-#pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                const float x = bf16_f32(rawx[j]);
-                x0[j] = x * mx0;
-                x1[j] = x * mx1;
-            }
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const f32x4 wv4 = *reinterpret_cast<const f32x4*>(&tk.w[16 * (wv - 4) + 4 * c]);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    // Xw chunk c: tokens 4c..4c+3 in natural (t, r) order
-                    outXw[c][2 * j] = (f16)(x0[4 * c + j] * wv4[j]);
-                    outXw[c][2 * j + 1] = (f16)(x1[4 * c + j] * wv4[j]);
-                    // X chunk c (x_col order): tokens 2c, 2c+1 then 8+2c, 9+2c
-                    const int tj = (j < 2 ? 2 * c : 6 + 2 * c) + j;
-                    outX[c][2 * j] = (f16)x0[tj];
-                    outX[c][2 * j + 1] = (f16)x1[tj];
-                }
-            }
-        };
-        auto write_x = [&]() {
-            const int lane = opaque(threadIdx.x & 63);
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                *reinterpret_cast<f16x8*>(&sm.X[lane][32 * (wv - 4) + 8 * c]) = outX[c];
-                *reinterpret_cast<f16x8*>(&sm.Xw[lane][32 * (wv - 4) + 8 * c]) = outXw[c];
-            }
-        };
         auto load_sc = [&](int kk) {
             const int lane = opaque(threadIdx.x & 63);
             const int s0 = kk * Q;
@@ -796,15 +624,15 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
             Tok& tk = sm.tok[kk % NSLOT];
             const float dt = s0 + lane < T ? fast_softplus(bf16_f32(sdt) + dtb) * ssc : 0.f;
             const float lam = a.trap ? __builtin_amdgcn_rcpf(1.f + fast_exp(-bf16_f32(slam))) : 1.f;
-            float dtn = __shfl_down(dt, 1, 64);
-            float lamn = __shfl_down(lam, 1, 64);
+            float dtn = bperm(dt, lane + 1);
+            float lamn = bperm(lam, lane + 1);
             if (lane == 63) {
                 dtn = s0 + Q < T ? fast_softplus(bf16_f32(sdt64) + dtb) * ssc64 : 0.f;
                 lamn = a.trap ? __builtin_amdgcn_rcpf(1.f + fast_exp(-bf16_f32(slam64))) : 1.f;
             }
-            const float c2 = wave_incl_scan(A2 * dt, lane);
-            const float c2e = __shfl(c2, 63, 64);
-            const float c2b = __shfl(c2, lane | 7, 64);
+            const float c2 = wave_incl_scan(A2 * dt);
+            const float c2e = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, c2), 63));
+            const float c2b = bperm(c2, lane | 7);
             const float av = a.trap ? lam * dt : dt;
             const float bv = a.trap ? (1.f - lamn) * dtn : 0.f;
             tk.c2[lane] = c2;
@@ -813,15 +641,11 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
             tk.ec[lane] = __builtin_amdgcn_exp2f(c2);
             tk.hb[lane] = __builtin_amdgcn_exp2f(c2b - c2) * (av + bv);
             tk.dtr[lane] = dt * 0.15915494309189535f;
-            tk.w[lane] = __builtin_amdgcn_exp2f(c2e - c2) * (av + bv);
+            tk.w16[lane] = (f16)(__builtin_amdgcn_exp2f(c2e - c2) * (av + bv));
         };
-        constexpr int kTokWave = 0;  // lightest output block
 
-        // ---------------- prologue: first chunk ----------------
-        if (kFull) load_z(k_begin);
-        if (kPrep) load_prep(k_begin);
-        else load_x(k_begin);
-        if (wv == kTokWave) {
+        // prologue: token scalars of the first two chunks
+        if (wv == 0) {
             load_sc(k_begin);
             tok_scalars(k_begin);
             if (k_begin + 1 < k_end) {
@@ -831,136 +655,369 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
             if (k_begin + 2 < k_end) load_sc(k_begin + 2);
         }
         __syncthreads();
-        if (kPrep) {
-            prep(k_begin);
-            write_prep();
-        } else {
-            prep_x(k_begin);
-            write_x();
-        }
-        write_state(k_begin & 1);
-        if (kFull) write_z(k_begin);
+        if (kFull) write_state();
 
-        // ---------------- chunk loop ----------------
-        // The state copy of chunk k+1 is written right after the state update of M(k), and
-        // z of chunk k+1 (read after the state update) at the end of M(k), both into the
-        // buffers of the other parity; y of chunk k-1 is stored at the start of M(k).
         for (int k = k_begin; k < k_end; ++k) {
-            const int s0 = k * Q;
             const bool more = k + 1 < k_end;
             const int par = k & 1;
             __syncthreads();
-            if (kFull && k > k_begin) store_y(k - 1);
             const Tok& tk = sm.tok[k % NSLOT];
-            state_update(tk);
-            if (more) {
-                write_state(par ^ 1);
-                if (kFull) load_z(k + 1);
-                if (kPrep) load_prep(k + 1);
-                else load_x(k + 1);
-            }
+            state_update(tk, par);
             if (kFull) {
                 const int lane = opaque(threadIdx.x & 63);
                 const int g16 = lane >> 4, l16 = lane & 15;
-                if (kPrep) {
-                    switch (wv) {
-                        case 0: out_block<0>(sm, tk, par, g16, l16, D_h); break;
-                        case 1: out_block<1>(sm, tk, par, g16, l16, D_h); break;
-                        case 2: out_block<2>(sm, tk, par, g16, l16, D_h); break;
-                        default: out_block<3>(sm, tk, par, g16, l16, D_h); break;
-                    }
-                } else {
-                    switch (wv) {
-                        case 4: out_block<7>(sm, tk, par, g16, l16, D_h); break;
-                        case 5: out_block<6>(sm, tk, par, g16, l16, D_h); break;
-                        case 6: out_block<5>(sm, tk, par, g16, l16, D_h); break;
-                        default: out_block<4>(sm, tk, par, g16, l16, D_h); break;
-                    }
+                switch (wv) {
+                    case 0: out_block<0>(sm, tk, par, g16, l16, D_h); break;
+                    case 1: out_block<1>(sm, tk, par, g16, l16, D_h); break;
+                    case 2: out_block<2>(sm, tk, par, g16, l16, D_h); break;
+                    case 3: out_block<3>(sm, tk, par, g16, l16, D_h); break;
+                    case 4: out_block<7>(sm, tk, par, g16, l16, D_h); break;
+                    case 5: out_block<6>(sm, tk, par, g16, l16, D_h); break;
+                    case 6: out_block<5>(sm, tk, par, g16, l16, D_h); break;
+                    default: out_block<4>(sm, tk, par, g16, l16, D_h); break;
                 }
             }
-            if (wv == kTokWave) {
+            if (wv == 0) {
                 if (k + 2 < k_end) tok_scalars(k + 2);
                 if (k + 3 < k_end) load_sc(k + 3);
             }
-            if (more) {
-                if (kFull) write_z(k + 1);
-                if (kPrep) prep(k + 1);
-                else prep_x(k + 1);
-                __syncthreads();
-                if (kPrep) write_prep(); else write_x();
-            }
-        }
-        if (kFull) {
             __syncthreads();
-            store_y(k_end - 1);
+            if (kFull && more) write_state();  // H_{k+1}, read by G3 of chunk k+1
         }
-    };
-    if (wv < 4) role_loop(std::true_type{});
-    else role_loop(std::false_type{});
-
-    // ---- segment end
-    const bool pair_lane = wv < 4 && (lane0 >> 3) == 0;  // lanes 0..7 of waves 0-3: pairs pa0, pa0+1
-    if (!kFull) {
+        // ---- segment end (MFMA waves: state outputs)
+        __syncthreads();
         const int g16 = lane0 >> 4, l16 = lane0 & 15;
-        const int64_t sidx = (int64_t)bh * (a.S - 1) + seg;
-        float* out = a.seg_state + sidx * (int64_t)N * P;
-        const int n0 = 16 * wv + 4 * g16;
-#pragma unroll
-        for (int pt = 0; pt < 4; ++pt)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) out[(n0 + v) * P + 16 * pt + l16] = hacc[pt][v];
-        if (tid == 0) a.seg_decay[sidx] = logdecay;
-        if (pair_lane) {
-            a.seg_angle[sidx * NH + pa0] = phi_run0 * 6.283185307179586f;
-            a.seg_angle[sidx * NH + pa0 + 1] = phi_run1 * 6.283185307179586f;
-        }
-    } else if (seg == a.S - 1) {
-        __syncthreads();
-        if (pair_lane) {
-            sm.rot[pa0] = phi_start0;
-            sm.rot[pa0 + 1] = phi_start1;
-            if (a.angle) {
-                a.angle[(int64_t)bh * NH + pa0] = a.cplx ? phi_start0 + phi_run0 * 6.283185307179586f : 0.f;
-                a.angle[(int64_t)bh * NH + pa0 + 1] = a.cplx ? phi_start1 + phi_run1 * 6.283185307179586f : 0.f;
-            }
-        }
-        __syncthreads();
-        if (a.h_final) {
-            const int g16 = lane0 >> 4, l16 = lane0 & 15;
-            float* hf = a.h_final + (int64_t)bh * P * N;
+        if (!kFull) {
+            const int64_t sidx = (int64_t)bh * (a.S - 1) + seg;
+            float* out = a.seg_state + sidx * (int64_t)N * P;
             const int n0 = 16 * wv + 4 * g16;
-            float s0, c0, s1, c1;
-            sincosf(sm.rot[n0 / 2], &s0, &c0);
-            sincosf(sm.rot[n0 / 2 + 1], &s1, &c1);
 #pragma unroll
-            for (int pt = 0; pt < 4; ++pt) {
-                const f32x4 v = hacc[pt];
-                const f32x4 o = {v[0] * c0 - v[1] * s0, v[0] * s0 + v[1] * c0,
-                                 v[2] * c1 - v[3] * s1, v[2] * s1 + v[3] * c1};
-                *reinterpret_cast<f32x4*>(&hf[(16 * pt + l16) * N + n0]) = o;
+            for (int pt = 0; pt < 4; ++pt)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) out[(n0 + v) * P + 16 * pt + l16] = hacc[pt][v];
+            if (tid == 0) a.seg_decay[sidx] = logdecay;
+        } else if (seg == a.S - 1) {
+            __syncthreads();  // absolute start angles of every pair in sm.rot
+            if (a.h_final) {
+                float* hf = a.h_final + (int64_t)bh * P * N;
+                const int n0 = 16 * wv + 4 * g16;
+                float s0, c0, s1, c1;
+                sincosf(sm.rot[n0 / 2], &s0, &c0);
+                sincosf(sm.rot[n0 / 2 + 1], &s1, &c1);
+#pragma unroll
+                for (int pt = 0; pt < 4; ++pt) {
+                    const f32x4 v = hacc[pt];
+                    const f32x4 o = {v[0] * c0 - v[1] * s0, v[0] * s0 + v[1] * c0,
+                                     v[2] * c1 - v[3] * s1, v[2] * s1 + v[3] * c1};
+                    *reinterpret_cast<f32x4*>(&hf[(16 * pt + l16) * N + n0]) = o;
+                }
+            }
+            if (a.prev_bx) {
+                // prev_BX = B~_{T-1} x_{T-1}^T, from the last chunk's tiles (still in LDS),
+                // rotated to the absolute frame. Thread: column pair lane, rows p = 8*wave..+7.
+                const int ul = (T - 1) - (K - 1) * Q;
+                const int pp = lane0;
+                float sn, cs;
+                sincosf(sm.rot[pp], &sn, &cs);
+                const int c0 = sw_cb(2 * ul, 2 * pp);  // rows 2ul and 2ul+1 share the 16-row block
+                const float be0 = (float)sm.B[2 * ul][c0], bo0 = (float)sm.B[2 * ul][c0 + 1];
+                const float be1 = (float)sm.B[2 * ul + 1][c0], bo1 = (float)sm.B[2 * ul + 1][c0 + 1];
+                const float ae0 = be0 * cs - bo0 * sn, ao0 = be0 * sn + bo0 * cs;
+                const float ae1 = be1 * cs - bo1 * sn, ao1 = be1 * sn + bo1 * cs;
+                float* pb = a.prev_bx + (int64_t)bh * P * N;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int p = 8 * wv + j;
+                    const float x0 = (float)sm.X[(K - 1) & 1][2 * ul][xsw(2 * ul, p)];
+                    const float x1 = (float)sm.X[(K - 1) & 1][2 * ul + 1][xsw(2 * ul + 1, p)];
+                    *reinterpret_cast<f32x2*>(&pb[p * N + 2 * pp]) = f32x2{ae0 * x0 + ae1 * x1, ao0 * x0 + ao1 * x1};
+                }
             }
         }
-        if (a.prev_bx) {
-            // prev_BX = B~_{T-1} x_{T-1}^T, from the last chunk's tiles (still in LDS),
-            // rotated to the absolute frame. Thread: column pair lane, rows p = 8*wave..+7.
-            const int ul = (T - 1) - (K - 1) * Q;
-            const int pp = lane0;
-            float sn, cs;
-            sincosf(sm.rot[pp], &sn, &cs);
-            const int c0 = sw_cb(2 * ul, 2 * pp);  // rows 2ul and 2ul+1 share the 16-row block
-            const float be0 = (float)sm.B[2 * ul][c0], bo0 = (float)sm.B[2 * ul][c0 + 1];
-            const float be1 = (float)sm.B[2 * ul + 1][c0], bo1 = (float)sm.B[2 * ul + 1][c0 + 1];
-            const float ae0 = be0 * cs - bo0 * sn, ao0 = be0 * sn + bo0 * cs;
-            const float ae1 = be1 * cs - bo1 * sn, ao1 = be1 * sn + bo1 * cs;
-            float* pb = a.prev_bx + (int64_t)bh * P * N;
+    } else {
+        // ======================= helper waves =======================
+        const int th = hw >> 2;        // which four tokens of the octet this lane rotates
+        u32x4 rawB[4], rawC[4], xr, zr;
+        unsigned rawth[8];
+        u32x2 outB[4][2], outC[4][2];
+
+        // ---- reads of chunk kk (past the sequence end the descriptors return zero). Each
+        // group is issued right after its registers' previous contents are consumed, so the
+        // reads spread over the M phase and have a whole chunk step to arrive.
+        auto rsrc_proj = [&](int kk) {
+            const int s0 = kk * Q;
+            return make_rsrc(proj_b + (int64_t)s0 * a.rs, (int64_t)max(T - s0, 0) * a.rs * 2);
+        };
+        auto load_x = [&](int kk) {
+            const int lane = opaque(threadIdx.x & 63);
+            const int t = 8 * hw + (lane >> 3), p = 8 * (lane & 7);
+            xr = __builtin_amdgcn_raw_buffer_load_b128(rsrc_proj(kk), (t * rs + (int)a.pl.x + h * P + p) * 2, 0, 0);
+        };
+        auto load_z = [&](int kk) {
+            const int lane = opaque(threadIdx.x & 63);
+            const int t = 8 * hw + (lane >> 3), p = 8 * (lane & 7);
+            zr = __builtin_amdgcn_raw_buffer_load_b128(rsrc_proj(kk), (t * rs + (int)a.pl.z + h * P + p) * 2, 0, 0);
+        };
+        auto load_th = [&](int kk) {
+            const int lane = opaque(threadIdx.x & 63);
+            const int q = lane >> 3;
+            const int pa = 16 * (hw & 3) + 2 * (lane & 7);
+            const int s0 = kk * Q;
+            // theta through a descriptor of size zero when the layer has no RoPE (reads give
+            // 0, so the angles stay zero): no branch, so the reads stay where they are written.
+            const __amdgpu_buffer_rsrc_t rth =
+                make_rsrc(proj_b + (int64_t)s0 * a.rs, a.cplx ? (int64_t)max(T - s0, 0) * a.rs * 2 : 0);
+            const int vth = (8 * q * rs + (a.cplx ? (int)a.pl.theta : 0) + pa) * 2;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int p = 8 * wv + j;
-                const float x0 = (float)sm.X[p][x_col(2 * ul)], x1 = (float)sm.X[p][x_col(2 * ul + 1)];
-                *reinterpret_cast<f32x2*>(&pb[p * N + 2 * pp]) = f32x2{ae0 * x0 + ae1 * x1, ao0 * x0 + ao1 * x1};
+            for (int j = 0; j < 8; ++j) rawth[j] = __builtin_amdgcn_raw_buffer_load_b32(rth, vth, j * rs * 2, 0);
+        };
+        auto load_bc = [&](int kk, int j) {  // token 8q + 4th + j
+            const int lane = opaque(threadIdx.x & 63);
+            const int q = lane >> 3;
+            const int pa = 16 * (hw & 3) + 2 * (lane & 7);
+            const int s0 = kk * Q;
+            const int left = max(T - s0, 0);
+            const int64_t bcbytes = left > 0 ? ((int64_t)(left - 1) * bnrs + NR) * 2 : 0;
+            const int vbc = ((8 * q + 4 * th) * bnrs + 4 * pa) * 2;
+            rawB[j] = __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(bn_b + (int64_t)s0 * bnrs, bcbytes), vbc,
+                                                            j * bnrs * 2, 0);
+            if (kFull)
+                rawC[j] = __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(cn_b + (int64_t)s0 * bnrs, bcbytes), vbc,
+                                                                j * bnrs * 2, 0);
+        };
+        auto load_all = [&](int kk) {
+            load_x(kk);
+            if (kFull) load_z(kk);
+            load_th(kk);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) load_bc(kk, j);
+        };
+        // ---- RoPE rotation of this lane's four tokens, two pairs, both ranks
+        // kn: chunk whose theta reads are issued once the prefix has used this chunk's.
+        auto prep = [&](int kk, int kn) {
+            const int lane = opaque(threadIdx.x & 63);
+            const int q = lane >> 3;
+            const Tok& tk = sm.tok[kk % NSLOT];
+            const f32x4 d0 = *reinterpret_cast<const f32x4*>(&tk.dtr[8 * q]);
+            const f32x4 d1 = *reinterpret_cast<const f32x4*>(&tk.dtr[8 * q + 4]);
+            // RoPE angle increments (turns) dt_u theta_u of tokens 8q..8q+7 for both pairs:
+            // totals of the first and second four; the prefix of the per-lane totals over q
+            // (lanes 8 apart) gives each lane's starting angles.
+            float lo0 = 0.f, lo1 = 0.f, hi0 = 0.f, hi1 = 0.f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                lo0 += d0[j] * __builtin_bit_cast(float, rawth[j] << 16);
+                lo1 += d0[j] * __builtin_bit_cast(float, rawth[j] & 0xffff0000u);
+                hi0 += d1[j] * __builtin_bit_cast(float, rawth[4 + j] << 16);
+                hi1 += d1[j] * __builtin_bit_cast(float, rawth[4 + j] & 0xffff0000u);
             }
+            const float tot0 = lo0 + hi0, tot1 = lo1 + hi1;
+            // inclusive prefix over q (lanes 8 apart; the step-8 partner of an even q is in
+            // the previous 16-lane row, so every step goes through bpermute)
+            float incl0 = tot0, incl1 = tot1;
+#pragma unroll
+            for (int off = 8; off < 64; off <<= 1) {
+                const float o0 = bperm(incl0, lane - off);
+                const float o1 = bperm(incl1, lane - off);
+                if (lane >= off) {
+                    incl0 += o0;
+                    incl1 += o1;
+                }
+            }
+            const float ctot0 = bperm(incl0, 56 + (lane & 7));
+            const float ctot1 = bperm(incl1, 56 + (lane & 7));
+            float phi0 = phi_run0 - (incl0 - tot0);
+            float phi1 = phi_run1 - (incl1 - tot1);
+            phi_run0 -= ctot0;
+            phi_run1 -= ctot1;
+            // tokens 8q .. 8q+3 precede this lane's four when th = 1
+            phi0 -= th ? lo0 : 0.f;
+            phi1 -= th ? lo1 : 0.f;
+            // this lane's four tokens: dt and theta words
+            float dsel[4];
+            unsigned tsel[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                dsel[j] = th ? d1[j] : d0[j];
+                tsel[j] = th ? rawth[4 + j] : rawth[j];
+            }
+            M3_FENCE();
+            load_th(kn);
+            M3_FENCE();
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float dt = dsel[j];
+                const unsigned thw = tsel[j];
+                phi0 -= dt * __builtin_bit_cast(float, thw << 16);
+                phi1 -= dt * __builtin_bit_cast(float, thw & 0xffff0000u);
+                f16x2 rb[2][2];  // [pair][rank]: rotated (even, odd) of B^
+#pragma unroll
+                for (int pr = 0; pr < 2; ++pr) {
+                    const float phi = pr == 0 ? phi0 : phi1;
+                    const float rev = __builtin_amdgcn_fractf(phi);
+                    const float sn = __builtin_amdgcn_sinf(rev), cs = __builtin_amdgcn_cosf(rev);
+                    // (e, o) -> (e cos - o sin, e sin + o cos) = e (cos, sin) + o (-sin, cos)
+                    const f16x2 kA = f16x2{(f16)cs, (f16)sn};
+                    const f16x2 kB = f16x2{(f16)(-sn), (f16)cs};
+#pragma unroll
+                    for (int r = 0; r < 2; ++r) {
+                        const f16x2 v = as_f16x2(rawB[j][2 * pr + r]);
+                        rb[pr][r] = f16x2{v[0], v[0]} * kA + f16x2{v[1], v[1]} * kB;
+                        if (kFull) {
+                            const f16x2 c = as_f16x2(rawC[j][2 * pr + r]);
+                            outC[j][r][pr] = bits(f16x2{c[0], c[0]} * kA + f16x2{c[1], c[1]} * kB);
+                        }
+                    }
+                }
+                outB[j][0] = u32x2{bits(rb[0][0]), bits(rb[1][0])};
+                outB[j][1] = u32x2{bits(rb[0][1]), bits(rb[1][1])};
+            }
+        };
+        // ---- X rows (u,r) = x_u mimo_x[r], columns 8 (lane%8) .. +7, of token 8 hw + lane/8,
+        // straight into X buffer par (not read in this M phase)
+        auto prep_x = [&](int par) {
+            const int lane = opaque(threadIdx.x & 63);
+            const int p = 8 * (lane & 7);
+            const f16x8 mx0 = *reinterpret_cast<const f16x8*>(&sm.mxT[0][p]);
+            const f16x8 mx1 = *reinterpret_cast<const f16x8*>(&sm.mxT[1][p]);
+            f16x8 xv;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                xv[2 * i] = (f16)bf16_f32(xr[i] & 0xffffu);
+                xv[2 * i + 1] = (f16)__builtin_bit_cast(float, xr[i] & 0xffff0000u);
+            }
+            const int t = 8 * hw + (lane >> 3);
+            *reinterpret_cast<f16x8*>(&sm.X[par][2 * t][xsw(2 * t, p)]) = xv * mx0;
+            *reinterpret_cast<f16x8*>(&sm.X[par][2 * t + 1][xsw(2 * t + 1, p)]) = xv * mx1;
+        };
+        // ---- gate factors g_r = mimo_down_r silu(z mimo_z_r) of token tx, columns p0..p0+7,
+        // into gate buffer par: with e_r = exp(-z mimo_z_r) (clamped at 2^60 so the product
+        // stays finite), g_r = (mimo_down_r mimo_z_r) z (1 + e_{1-r}) / ((1+e_0)(1+e_1)).
+        auto gate = [&](int par) {
+            const int lane = opaque(threadIdx.x & 63);
+            const int t = 8 * hw + (lane >> 3), p = 8 * (lane & 7);
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const f32x4 a0 = *reinterpret_cast<const f32x4*>(&sm.mzdT[0][p + 4 * hh]);
+                const f32x4 a1 = *reinterpret_cast<const f32x4*>(&sm.mzdT[1][p + 4 * hh]);
+                const f32x4 b0 = *reinterpret_cast<const f32x4*>(&sm.mzdT[2][p + 4 * hh]);
+                const f32x4 b1 = *reinterpret_cast<const f32x4*>(&sm.mzdT[3][p + 4 * hh]);
+                u32x4 gw;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const unsigned zw = zr[2 * hh + (i >> 1)];
+                    const float z = (i & 1) ? __builtin_bit_cast(float, zw & 0xffff0000u) : bf16_f32(zw & 0xffffu);
+                    const float e0 = __builtin_amdgcn_exp2f(fminf(z * a0[i], 60.f));
+                    const float e1 = __builtin_amdgcn_exp2f(fminf(z * a1[i], 60.f));
+                    const float zi = z * __builtin_amdgcn_rcpf((1.f + e0) * (1.f + e1));
+                    const float g0 = zi * __builtin_fmaf(b0[i], e1, b0[i]);
+                    const float g1 = zi * __builtin_fmaf(b1[i], e0, b1[i]);
+                    const bf16x2 gp = bf16x2{(bf16)g0, (bf16)g1};
+                    gw[i] = __builtin_bit_cast(unsigned, gp);
+                }
+                *reinterpret_cast<u32x4*>(&sm.Gt[par][t][gsw(t, p + 4 * hh)]) = gw;
+            }
+        };
+        // ---- W phase: tiles of the prepared chunk
+        auto write_tiles = [&]() {
+            const int lane = opaque(threadIdx.x & 63);
+            const int q = lane >> 3;
+            const int pa = 16 * (hw & 3) + 2 * (lane & 7);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int row = 2 * (8 * q + 4 * th + j);
+                const int col = sw_cb(row, 2 * pa);  // rows row, row+1 share the swizzle
+                // The fences keep these as single 64-bit stores.
+                if (kFull) {
+                    *reinterpret_cast<u32x2*>(&sm.C[row][col]) = outC[j][0];
+                    M3_LDS_FENCE();
+                    *reinterpret_cast<u32x2*>(&sm.C[row + 1][col]) = outC[j][1];
+                    M3_LDS_FENCE();
+                }
+                *reinterpret_cast<u32x2*>(&sm.B[row][col]) = outB[j][0];
+                M3_LDS_FENCE();
+                *reinterpret_cast<u32x2*>(&sm.B[row + 1][col]) = outB[j][1];
+                M3_LDS_FENCE();
+            }
+        };
+        // ---- W phase: chunk kk's output (low halves of its gate buffer) to HBM
+        auto store_out = [&](int kk) {
+            const int lane = opaque(threadIdx.x & 63);
+            const int t = 8 * hw + (lane >> 3), p = 8 * (lane & 7);
+            const u32x4 w0 = *reinterpret_cast<const u32x4*>(&sm.Gt[kk & 1][t][gsw(t, p)]);
+            const u32x4 w1 = *reinterpret_cast<const u32x4*>(&sm.Gt[kk & 1][t][gsw(t, p + 4)]);
+            const u32x4 o = {__builtin_amdgcn_perm(w0[1], w0[0], 0x05040100u),
+                             __builtin_amdgcn_perm(w0[3], w0[2], 0x05040100u),
+                             __builtin_amdgcn_perm(w1[1], w1[0], 0x05040100u),
+                             __builtin_amdgcn_perm(w1[3], w1[2], 0x05040100u)};
+            const int s0 = kk * Q;
+            const int HP = a.H * P;
+            const __amdgpu_buffer_rsrc_t ry =
+                make_rsrc(a.y_out + ((int64_t)b * T + s0) * HP, (int64_t)max(T - s0, 0) * HP * 2);
+            __builtin_amdgcn_raw_buffer_store_b128(o, ry, (t * HP + h * P + p) * 2, 0, 0);
+        };
+
+        // prologue: first chunk's tiles and gate factors, reads of the second chunk
+        load_all(k_begin);
+        __syncthreads();
+        prep_x(k_begin & 1);
+        M3_FENCE();  // each read group after the last use of its registers
+        load_x(k_begin + 1);
+        M3_FENCE();
+        if (kFull) {
+            gate(k_begin & 1);
+            M3_FENCE();
+            load_z(k_begin + 1);
+            M3_FENCE();
+        }
+        prep(k_begin, k_begin + 1);
+        write_tiles();
+
+        for (int k = k_begin; k < k_end; ++k) {
+            const bool more = k + 1 < k_end;
+            __syncthreads();
+            if (more) {
+                // B^ / C^ of chunk k+1 (shared by all heads of the batch row, mostly L2
+                // hits) are read now and rotated last; x, z and theta are a chunk ahead.
+#pragma unroll
+                for (int j = 0; j < 4; ++j) load_bc(k + 1, j);
+                prep_x((k + 1) & 1);
+                M3_FENCE();
+                load_x(k + 2);
+                M3_FENCE();
+                if (kFull) {
+                    gate((k + 1) & 1);
+                    M3_FENCE();
+                    load_z(k + 2);
+                    M3_FENCE();
+                }
+                prep(k + 1, k + 2);
+            }
+            __syncthreads();
+            if (kFull) store_out(k);
+            if (more) write_tiles();
+        }
+        // ---- segment end (helper waves: per-pair angles)
+        __syncthreads();
+        if (!kFull) {
+            const int64_t sidx = (int64_t)bh * (a.S - 1) + seg;
+            if (pair_lane) {
+                a.seg_angle[sidx * NH + pa0] = phi_run0 * 6.283185307179586f;
+                a.seg_angle[sidx * NH + pa0 + 1] = phi_run1 * 6.283185307179586f;
+            }
+        } else if (seg == a.S - 1) {
+            if (pair_lane) {
+                sm.rot[pa0] = phi_start0;
+                sm.rot[pa0 + 1] = phi_start1;
+                if (a.angle) {
+                    a.angle[(int64_t)bh * NH + pa0] = a.cplx ? phi_start0 + phi_run0 * 6.283185307179586f : 0.f;
+                    a.angle[(int64_t)bh * NH + pa0 + 1] = a.cplx ? phi_start1 + phi_run1 * 6.283185307179586f : 0.f;
+                }
+            }
+            __syncthreads();
         }
     }
+
 }
 
 }  // namespace mf
@@ -969,8 +1026,8 @@ bool mfma_prefill_supported(const m3_layer_desc& d, const void* proj, const void
     if (d.dtype != M3_DTYPE_BF16) return false;
     if (d.d_state != mf::N || d.headdim != mf::P || d.mimo_rank != mf::R) return false;
     const ProjLayout pl = proj_layout(d);
-    // 128-bit z loads and y stores, 32-bit theta loads.
-    if (d.proj_row_stride % 8 != 0 || pl.z % 8 != 0 || pl.theta % 2 != 0) return false;
+    // 128-bit x / z loads and y stores, 32-bit theta loads.
+    if (d.proj_row_stride % 8 != 0 || pl.x % 8 != 0 || pl.z % 8 != 0 || pl.theta % 2 != 0) return false;
     if (reinterpret_cast<uintptr_t>(proj) % 16 != 0 || reinterpret_cast<uintptr_t>(y_out) % 16 != 0)
         return false;
     // 32-bit buffer offsets: one batch row of proj (and of B^/C^) stays below 2 GiB.
