@@ -856,16 +856,20 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
                     const float phi = pr == 0 ? phi0 : phi1;
                     const float rev = __builtin_amdgcn_fractf(phi);
                     const float sn = __builtin_amdgcn_sinf(rev), cs = __builtin_amdgcn_cosf(rev);
-                    // (e, o) -> (e cos - o sin, e sin + o cos) = e (cos, sin) + o (-sin, cos)
+                    // (e, o) -> (e cos - o sin, e sin + o cos) = e (cos, sin) + (-u0, u1) with
+                    // u = o (sin, cos): one packed multiply and one packed fma (the negation
+                    // is a source modifier)
                     const f16x2 kA = f16x2{(f16)cs, (f16)sn};
-                    const f16x2 kB = f16x2{(f16)(-sn), (f16)cs};
+                    const f16x2 kS = __builtin_shufflevector(kA, kA, 1, 0);
 #pragma unroll
                     for (int r = 0; r < 2; ++r) {
                         const f16x2 v = as_f16x2(rawB[j][2 * pr + r]);
-                        rb[pr][r] = f16x2{v[0], v[0]} * kA + f16x2{v[1], v[1]} * kB;
+                        const f16x2 u = f16x2{v[1], v[1]} * kS;
+                        rb[pr][r] = f16x2{v[0], v[0]} * kA + f16x2{-u[0], u[1]};
                         if (kFull) {
                             const f16x2 c = as_f16x2(rawC[j][2 * pr + r]);
-                            outC[j][r][pr] = bits(f16x2{c[0], c[0]} * kA + f16x2{c[1], c[1]} * kB);
+                            const f16x2 uc = f16x2{c[1], c[1]} * kS;
+                            outC[j][r][pr] = bits(f16x2{c[0], c[0]} * kA + f16x2{-uc[0], uc[1]});
                         }
                     }
                 }
