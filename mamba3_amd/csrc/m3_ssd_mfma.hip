@@ -348,10 +348,15 @@ __device__ __forceinline__ void out_block(Smem& sm, const Tok& tk, int par, int 
     }
 
     // Fused G1 / mask / G2 over pairs of causal column blocks.
+    // X transpose reads: rows 32 s2 + 16 h + 4 g16 + jr share (row/2)%4 = (2 g16 + jr/2)%4,
+    // so one pointer per column group pt serves every (s2, h) with a constant offset.
     const int jr = l16 >> 2, jc = 4 * (l16 & 3);
+    const int xm = (2 * g16 + (jr >> 1)) & 3;
+    const f16* xp[4];
+#pragma unroll
+    for (int pt = 0; pt < 4; ++pt) xp[pt] = &sm.X[par][4 * g16 + jr][16 * (pt ^ xm) + jc];
 #pragma unroll
     for (int s2 = 0; s2 < NP; ++s2) {
-        const int rlo = 32 * s2 + 4 * g16 + jr, rhi = rlo + 16;
         f16x8 bop[4];
         f16x4 xlo[4], xhi[4];
 #pragma unroll
@@ -359,8 +364,8 @@ __device__ __forceinline__ void out_block(Smem& sm, const Tok& tk, int par, int 
             bop[s] = *reinterpret_cast<const f16x8*>(&sm.B[32 * s2 + l16][8 * g16 + 32 * (s ^ ((2 * s2) & 3))]);
 #pragma unroll
         for (int pt = 0; pt < 4; ++pt) {
-            xlo[pt] = ld_tr(&sm.X[par][rlo][xsw(rlo, 16 * pt + jc)]);
-            xhi[pt] = ld_tr(&sm.X[par][rhi][xsw(rhi, 16 * pt + jc)]);
+            xlo[pt] = ld_tr(xp[pt] + (32 * s2) * P);
+            xhi[pt] = ld_tr(xp[pt] + (32 * s2 + 16) * P);
         }
         M3_FENCE();
         f32x4 sacc[2];
@@ -564,16 +569,26 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
             // reads: lane j of a 16-lane group addresses row k0 + j/4, columns c0 + 4 (j%4).
             const int jr = l16 >> 2, jc = 4 * (l16 & 3);
             const int n0 = 16 * wv;
+            // Rows 32 s + 16 h + 4 g16 + jr: the B~ swizzle depends only on (2s + h)%4 and the
+            // X swizzle only on the lane, so a few pointers serve every (s, h) with constant
+            // offsets.
+            const int xm = (2 * g16 + (jr >> 1)) & 3;
+            const f16* xp[4];
+            const f16* bp[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                xp[c] = &sm.X[par][4 * g16 + jr][16 * (c ^ xm) + jc];
+                bp[c] = &sm.B[4 * g16 + jr][(n0 + jc) ^ (32 * c)];
+            }
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
-                const int rlo = 32 * s + 4 * g16 + jr, rhi = rlo + 16;
-                const f16x4 alo = ld_tr(&sm.B[rlo][sw_cb(rlo, n0 + jc)]);
-                const f16x4 ahi = ld_tr(&sm.B[rhi][sw_cb(rhi, n0 + jc)]);
+                const f16x4 alo = ld_tr(bp[(2 * s) & 3] + (32 * s) * (N + PAD));
+                const f16x4 ahi = ld_tr(bp[(2 * s + 1) & 3] + (32 * s + 16) * (N + PAD));
                 f16x4 xlo[4], xhi[4];
 #pragma unroll
                 for (int pt = 0; pt < 4; ++pt) {
-                    xlo[pt] = ld_tr(&sm.X[par][rlo][xsw(rlo, 16 * pt + jc)]);
-                    xhi[pt] = ld_tr(&sm.X[par][rhi][xsw(rhi, 16 * pt + jc)]);
+                    xlo[pt] = ld_tr(xp[pt] + (32 * s) * P);
+                    xhi[pt] = ld_tr(xp[pt] + (32 * s + 16) * P);
                 }
                 // chunk-state weights of tokens 16s + 2 g16 + {0,1} and 16s + 8 + 2 g16 + {0,1}
                 const f16x2 wlo = *reinterpret_cast<const f16x2*>(&tk.w16[16 * s + 2 * g16]);
