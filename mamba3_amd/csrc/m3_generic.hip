@@ -34,7 +34,7 @@ struct GenShape {
 
 // LDS plan in floats for one workgroup.
 struct GenLds {
-    int tok_dt, tok_lam, c, a, bco, phi_run, ph, rmsB, rmsC, Cs, Bs, Xs, Sc, Ys, total;
+    int tok_dt, tok_lam, c, a, bco, ec, wst, phi_run, ph, rmsB, rmsC, Cs, Bs, Xs, Sc, Ys, total;
 };
 
 __host__ __device__ inline GenLds gen_lds_plan(int Qi, int N, int P, int R, int Rb,
@@ -46,6 +46,8 @@ __host__ __device__ inline GenLds gen_lds_plan(int Qi, int N, int P, int R, int 
     L.c = o; o += Qi;
     L.a = o; o += Qi;
     L.bco = o; o += Qi;
+    L.ec = o; o += Qi;   // exp(c_t)
+    L.wst = o; o += Qi;  // exp(c_end - c_u) (a_u + b_u): chunk-state weights
     L.phi_run = o; o += N / 2;
     L.ph = o; o += complex_rope ? Qi * (N / 2) : 0;
     L.rmsB = o; o += Qi;
@@ -83,6 +85,16 @@ __device__ void gen_chunk_core(const GenShape& s, const GenLds& L, float* sm, fl
     const float* Xs = sm + L.Xs;
     float* Sc = sm + L.Sc;
     float* Ys = sm + L.Ys;
+    float* ec = sm + L.ec;
+    float* wst = sm + L.wst;
+
+    // Per-token exponentials, once per chunk.
+    const float c_end = c[Qi - 1];
+    for (int t = tid; t < Qi; t += kGenThreads) {
+        ec[t] = expf(c[t]);
+        wst[t] = t < nvalid ? expf(c_end - c[t]) * (a[t] + bco[t]) : 0.f;
+    }
+    __syncthreads();
 
     // Masked, weighted scores.
     for (int idx = tid; idx < rowsC * rowsB; idx += kGenThreads) {
@@ -112,18 +124,17 @@ __device__ void gen_chunk_core(const GenShape& s, const GenLds& L, float* sm, fl
         const float* hp = Hs + (size_t)p * N;
         float inter = 0.f;
         for (int n = 0; n < N; ++n) inter += ci[n] * hp[n];
-        Ys[idx] = acc + expf(c[t]) * inter;
+        Ys[idx] = acc + ec[t] * inter;
     }
     __syncthreads();
 
     // State update.
-    const float c_end = c[Qi - 1];
-    const float d_end = expf(c_end);
+    const float d_end = ec[Qi - 1];
     for (int idx = tid; idx < P * N; idx += kGenThreads) {
         const int p = idx / N, n = idx % N;
         float acc = 0.f;
         for (int u = 0; u < nvalid; ++u) {
-            const float w = expf(c_end - c[u]) * (a[u] + bco[u]);
+            const float w = wst[u];
             float bx = 0.f;
             for (int r = 0; r < Rb; ++r) bx += Xs[(u * Rb + r) * P + p] * Bs[(u * Rb + r) * N + n];
             acc += w * bx;
@@ -197,24 +208,26 @@ __global__ __launch_bounds__(kGenThreads) void gen_layer_prefill(GenLayerArgs A)
             sm[L.tok_dt + t] = dt;
             sm[L.tok_lam + t] = lam;
         }
-        // RMS of B and C rows of this chunk's tokens (mamba3/mamba3.py:28-35, 151-152).
-        for (int t = tid; t < Qi; t += kGenThreads) {
-            const int st = s0 + t;
-            float rb = 0.f, rc = 0.f;
+        // RMS of B and C rows of this chunk's tokens (mamba3/mamba3.py:28-35, 151-152):
+        // one wave per token, lanes strided over the row, then a wave sum.
+        for (int t = tid >> 6; t < Qi; t += kGenThreads / 64) {
+            const int st = s0 + t;  // uniform over the wave
+            float ssb = 0.f, ssc = 0.f;
             if (st < s.T) {
                 const T* row = proj + (int64_t)st * A.row_stride;
-                float ssb = 0.f, ssc = 0.f;
-                for (int e = 0; e < NR; ++e) {
+                for (int e = tid & 63; e < NR; e += 64) {
                     const float vb = ld_f32(row + A.pl.B + (int64_t)g * NR + e);
                     const float vc = ld_f32(row + A.pl.C + (int64_t)g * NR + e);
                     ssb += vb * vb;
                     ssc += vc * vc;
                 }
-                rb = rsqrtf(ssb / NR + A.eps);
-                rc = rsqrtf(ssc / NR + A.eps);
             }
-            sm[L.rmsB + t] = rb;
-            sm[L.rmsC + t] = rc;
+            ssb = group_sum<64>(ssb);
+            ssc = group_sum<64>(ssc);
+            if ((tid & 63) == 0) {
+                sm[L.rmsB + t] = st < s.T ? rsqrtf(ssb / NR + A.eps) : 0.f;
+                sm[L.rmsC + t] = st < s.T ? rsqrtf(ssc / NR + A.eps) : 0.f;
+            }
         }
         __syncthreads();
         if (tid == 0) {
@@ -227,16 +240,21 @@ __global__ __launch_bounds__(kGenThreads) void gen_layer_prefill(GenLayerArgs A)
                 sm[L.bco + t] = A.trap ? (1.f - sm[L.tok_lam + t + 1]) * sm[L.tok_dt + t + 1] : 0.f;
             }
         }
-        // Data-dependent RoPE angles (mamba3/mamba3.py:160-162): phi -= dt * theta.
+        // Data-dependent RoPE angles (mamba3/mamba3.py:160-162): phi -= dt * theta. The
+        // increments of all (token, pair) are read in parallel, then each pair's running
+        // sum walks the chunk in LDS.
         if (A.cplx) {
+            for (int idx = tid; idx < Qi * Nh; idx += kGenThreads) {
+                const int t = idx / Nh, i = idx % Nh;
+                const int st = s0 + t;
+                sm[L.ph + idx] = st < s.T ? sm[L.tok_dt + t] * ld_f32(proj + (int64_t)st * A.row_stride + A.pl.theta + i)
+                                          : 0.f;
+            }
+            __syncthreads();
             for (int i = tid; i < Nh; i += kGenThreads) {
                 float phi = sm[L.phi_run + i];
                 for (int t = 0; t < Qi; ++t) {
-                    const int st = s0 + t;
-                    if (st < s.T) {
-                        const float th = ld_f32(proj + (int64_t)st * A.row_stride + A.pl.theta + i);
-                        phi -= sm[L.tok_dt + t] * th;
-                    }
+                    phi -= sm[L.ph + t * Nh + i];
                     sm[L.ph + t * Nh + i] = phi;
                 }
                 sm[L.phi_run + i] = phi;
