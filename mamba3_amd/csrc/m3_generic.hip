@@ -30,6 +30,7 @@ constexpr int kGenMaxLds = 64 * 1024;
 
 struct GenShape {
     int B, T, H, P, N, R, Rb, G, Qi;
+    int Pb, PS;  // headdim columns per workgroup and the number of column blocks (P = Pb * PS)
 };
 
 // LDS plan in floats for one workgroup.
@@ -55,7 +56,7 @@ __host__ __device__ inline GenLds gen_lds_plan(int Qi, int N, int P, int R, int 
     o = (o + 3) & ~3;
     L.Cs = o; o += Qi * R * N;
     L.Bs = o; o += Qi * Rb * N;
-    L.Xs = o; o += Qi * Rb * P;
+    L.Xs = o; o += Qi * Rb * P;  // P = columns of this workgroup
     L.Sc = o; o += Qi * R * Qi * Rb;
     L.Ys = o; o += Qi * R * P;
     L.total = o;
@@ -75,7 +76,7 @@ static int gen_pick_chunk(int N, int P, int R, int Rb, bool complex_rope) {
 __device__ void gen_chunk_core(const GenShape& s, const GenLds& L, float* sm, float* __restrict__ Hs,
                                int nvalid) {
     const int tid = threadIdx.x;
-    const int Qi = s.Qi, N = s.N, P = s.P, R = s.R, Rb = s.Rb;
+    const int Qi = s.Qi, N = s.N, P = s.Pb, R = s.R, Rb = s.Rb;  // P: this workgroup's columns
     const int rowsC = Qi * R, rowsB = Qi * Rb;
     const float* c = sm + L.c;
     const float* a = sm + L.a;
@@ -168,12 +169,15 @@ __global__ __launch_bounds__(kGenThreads) void gen_layer_prefill(GenLayerArgs A)
     const GenShape& s = A.s;
     const GenLds& L = A.L;
     const int tid = threadIdx.x;
-    const int b = blockIdx.x / s.H, h = blockIdx.x % s.H;
+    // workgroup = (batch, head, column block): headdim columns p0 .. p0 + Pb - 1
+    const int bh = blockIdx.x / s.PS, pblk = blockIdx.x % s.PS;
+    const int b = bh / s.H, h = bh % s.H;
     const int g = h / (s.H / s.G);
-    const int Qi = s.Qi, N = s.N, P = s.P, R = s.R, Nh = N / 2, NR = N * R;
+    const int Qi = s.Qi, N = s.N, P = s.P, Pb = s.Pb, R = s.R, Nh = N / 2, NR = N * R;
+    const int p0 = pblk * Pb;
     const T* proj = reinterpret_cast<const T*>(A.proj) + (int64_t)b * s.T * A.row_stride;
     T* yo = reinterpret_cast<T*>(A.y_out) + (int64_t)b * s.T * s.H * P;
-    float* Hs = A.state + ((int64_t)b * s.H + h) * P * N;
+    float* Hs = A.state + ((int64_t)b * s.H + h) * P * N + (int64_t)p0 * N;  // this block's rows
     const float Ah = -expf(A.prm.A_log[h]);
     const float Dh = A.prm.D[h];
     const float dtb = A.prm.dt_bias[h];
@@ -185,7 +189,7 @@ __global__ __launch_bounds__(kGenThreads) void gen_layer_prefill(GenLayerArgs A)
     const float* mz = A.prm.mimo_z + (int64_t)h * P * R;
     const float* md = A.prm.mimo_down + (int64_t)h * P * R;
 
-    for (int idx = tid; idx < P * N; idx += kGenThreads) Hs[idx] = 0.f;
+    for (int idx = tid; idx < Pb * N; idx += kGenThreads) Hs[idx] = 0.f;
     for (int i = tid; i < Nh; i += kGenThreads) sm[L.phi_run + i] = 0.f;
     __syncthreads();
 
@@ -291,10 +295,10 @@ __global__ __launch_bounds__(kGenThreads) void gen_layer_prefill(GenLayerArgs A)
             cs_[2 * i] = ce;
             cs_[2 * i + 1] = co;
         }
-        // MIMO x expansion (mamba3/mamba3.py:210).
-        for (int idx = tid; idx < Qi * R * P; idx += kGenThreads) {
-            const int t = idx / (R * P);
-            const int r = (idx / P) % R, p = idx % P;
+        // MIMO x expansion (mamba3/mamba3.py:210), this block's columns.
+        for (int idx = tid; idx < Qi * R * Pb; idx += kGenThreads) {
+            const int t = idx / (R * Pb);
+            const int r = (idx / Pb) % R, p = p0 + idx % Pb;
             const int st = s0 + t;
             float v = 0.f;
             if (st < s.T)
@@ -305,36 +309,36 @@ __global__ __launch_bounds__(kGenThreads) void gen_layer_prefill(GenLayerArgs A)
 
         gen_chunk_core(s, L, sm, Hs, nvalid);
 
-        // Gate and MIMO-down (mamba3/mamba3.py:233-238).
-        for (int idx = tid; idx < Qi * P; idx += kGenThreads) {
-            const int t = idx / P, p = idx % P;
+        // Gate and MIMO-down (mamba3/mamba3.py:233-238), this block's columns.
+        for (int idx = tid; idx < Qi * Pb; idx += kGenThreads) {
+            const int t = idx / Pb, pl = idx % Pb, p = p0 + pl;
             const int st = s0 + t;
             if (st < s.T) {
                 const float z = ld_f32(proj + (int64_t)st * A.row_stride + A.pl.z + (int64_t)h * P + p);
                 float out = 0.f;
                 for (int r = 0; r < R; ++r) {
                     const int i = t * R + r;
-                    const float y = sm[L.Ys + i * P + p] + Dh * sm[L.Xs + i * P + p];
+                    const float y = sm[L.Ys + i * Pb + pl] + Dh * sm[L.Xs + i * Pb + pl];
                     out += md[p * R + r] * y * silu_f(z * mz[p * R + r]);
                 }
                 yo[((int64_t)st * s.H + h) * P + p] = cvt_out<T>(out);
             }
         }
-        // prev_BX = B~_{T-1} x_{T-1}^T (mamba3/mamba3.py:247-250).
+        // prev_BX = B~_{T-1} x_{T-1}^T (mamba3/mamba3.py:247-250), this block's rows.
         if (A.prev_bx && k == nchunks - 1) {
             const int tl = nvalid - 1;
-            float* pb = A.prev_bx + ((int64_t)b * s.H + h) * P * N;
-            for (int idx = tid; idx < P * N; idx += kGenThreads) {
-                const int p = idx / N, n = idx % N;
+            float* pb = A.prev_bx + ((int64_t)b * s.H + h) * P * N + (int64_t)p0 * N;
+            for (int idx = tid; idx < Pb * N; idx += kGenThreads) {
+                const int pl = idx / N, n = idx % N;
                 float v = 0.f;
                 for (int r = 0; r < R; ++r)
-                    v += sm[L.Bs + (tl * R + r) * N + n] * sm[L.Xs + (tl * R + r) * P + p];
+                    v += sm[L.Bs + (tl * R + r) * N + n] * sm[L.Xs + (tl * R + r) * Pb + pl];
                 pb[idx] = v;
             }
         }
         __syncthreads();
     }
-    if (A.angle) {
+    if (A.angle && pblk == 0) {
         for (int i = tid; i < Nh; i += kGenThreads)
             A.angle[((int64_t)b * s.H + h) * Nh + i] = A.cplx ? sm[L.phi_run + i] : 0.f;
     }
@@ -351,9 +355,15 @@ int launch_generic_prefill(const m3_layer_desc& d, const m3_layer_params& p, con
     GenLayerArgs A;
     A.s.B = d.batch; A.s.T = d.seqlen; A.s.H = d.nheads; A.s.P = d.headdim; A.s.N = d.d_state;
     A.s.R = d.mimo_rank; A.s.Rb = d.mimo_rank; A.s.G = d.ngroups;
-    A.s.Qi = gen_pick_chunk(A.s.N, A.s.P, A.s.R, A.s.Rb, d.use_complex != 0);
+    // Split headdim over workgroups while there are idle CUs (256) and blocks keep at
+    // least 16 columns: everything but the per-chunk preparation and the scores divides.
+    int PS = 1;
+    while (A.s.P % (2 * PS) == 0 && A.s.P / (2 * PS) >= 16 && (int64_t)d.batch * d.nheads * 2 * PS <= 256) PS *= 2;
+    A.s.PS = PS;
+    A.s.Pb = A.s.P / PS;
+    A.s.Qi = gen_pick_chunk(A.s.N, A.s.Pb, A.s.R, A.s.Rb, d.use_complex != 0);
     if (A.s.Qi == 0) return M3_ERR_UNSUPPORTED;
-    A.L = gen_lds_plan(A.s.Qi, A.s.N, A.s.P, A.s.R, A.s.Rb, d.use_complex != 0);
+    A.L = gen_lds_plan(A.s.Qi, A.s.N, A.s.Pb, A.s.R, A.s.Rb, d.use_complex != 0);
     A.pl = proj_layout(d);
     A.row_stride = d.proj_row_stride;
     A.trap = d.use_trapezoidal;
@@ -367,7 +377,7 @@ int launch_generic_prefill(const m3_layer_desc& d, const m3_layer_params& p, con
     A.angle = angle;
     A.prev_bx = prev_bx;
     const size_t lds = (size_t)A.L.total * sizeof(float);
-    const dim3 grid((unsigned)(d.batch * d.nheads));
+    const dim3 grid((unsigned)(d.batch * d.nheads * PS));
     if (d.dtype == M3_DTYPE_BF16)
         hipLaunchKernelGGL(gen_layer_prefill<bf16>, grid, dim3(kGenThreads), lds, stream, A);
     else
@@ -475,6 +485,7 @@ int launch_generic_chunked(int B, int T, int H, int P, int N, int R, int dtype,
     a.s.B = B; a.s.T = T; a.s.H = H; a.s.P = P; a.s.N = N; a.s.R = R;
     a.s.Rb = x_b ? 2 * R : R;
     a.s.G = 1;
+    a.s.Pb = P; a.s.PS = 1;
     a.s.Qi = gen_pick_chunk(N, P, R, a.s.Rb, false);
     if (a.s.Qi == 0) return M3_ERR_UNSUPPORTED;
     a.L = gen_lds_plan(a.s.Qi, N, P, R, a.s.Rb, false);
