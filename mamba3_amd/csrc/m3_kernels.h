@@ -56,6 +56,13 @@ int launch_mfma_prefill(const m3_layer_desc& d, const m3_layer_params& p, const 
                         const float* dt_scale, void* y_out, float* h_final, float* angle,
                         float* prev_bx, void* workspace, hipStream_t stream);
 
+// bf16 MFMA fused prefill for d_state 64/128/256, mimo_rank 1/2/4, headdim % 32 == 0.
+bool wide_prefill_supported(const m3_layer_desc& d);
+size_t wide_prefill_workspace(const m3_layer_desc& d);
+int launch_wide_prefill(const m3_layer_desc& d, const m3_layer_params& p, const void* proj,
+                        const float* dt_scale, void* y_out, float* h_final, float* angle,
+                        float* prev_bx, void* workspace, hipStream_t stream);
+
 // Returns 1 when the step kernel supports (N, R), else 0.
 int step_supported(int N, int R);
 int launch_step(const m3_layer_desc& d, const m3_layer_params& p, const void* proj,

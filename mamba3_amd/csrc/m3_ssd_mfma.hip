@@ -51,6 +51,7 @@
 
 #include "m3_common.h"
 #include "m3_kernels.h"
+#include "m3_mfma.h"
 
 namespace m3 {
 namespace mf {
@@ -64,21 +65,8 @@ constexpr int NH = N / 2;
 constexpr int THREADS = 1024;  // 8 MFMA waves + 8 helper waves, four per SIMD
 constexpr int NMW = 8;          // waves 0..7 run the MFMA work, 8..15 are helpers
 constexpr int PAD = 8;
-constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kRsrcFlags = 0x00020000;
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-// MFMA operand tiles are f16: same dense rate as bf16 on gfx950, three more mantissa
-// bits, and packed f16 arithmetic for the RoPE rotation.
-typedef _Float16 f16;
-typedef f16 f16x8 __attribute__((ext_vector_type(8)));
-typedef f16 f16x4 __attribute__((ext_vector_type(4)));
-typedef f16 f16x2 __attribute__((ext_vector_type(2)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
-typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int NSLOT = 3;
 // The f16 copy of the state used by G3 holds h * kHScale (|h| up to ~1.6e7 fits); the
@@ -130,17 +118,6 @@ struct Args {
     float* prev_bx;
 };
 
-// Returns v through an empty asm statement the compiler cannot see through or move:
-// values derived from it are recomputed where used instead of being hoisted out of the
-// chunk loop and held in registers across it.
-__device__ __forceinline__ int opaque(int v) {
-    asm volatile("" : "+v"(v));
-    return v;
-}
-
-__device__ __forceinline__ f32x4 mfma16(const f16x8& a, const f16x8& b, const f32x4& c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0,
@@ -160,64 +137,6 @@ __device__ __forceinline__ float bf16_f32(unsigned u) { return __builtin_bit_cas
 __device__ __forceinline__ u32x2 ld_b64(__amdgpu_buffer_rsrc_t r, int off_elems) {
     return __builtin_amdgcn_raw_buffer_load_b64(r, off_elems * 2, 0, 0);
 }
-
-// sin and cos of an angle in radians, reduced to [-0.5, 0.5) turns for the hardware.
-__device__ __forceinline__ void fast_sincos(float x, float& s, float& c) {
-    float rev = x * 0.15915494309189535f;
-    rev = rev - rintf(rev);
-    s = __builtin_amdgcn_sinf(rev);
-    c = __builtin_amdgcn_cosf(rev);
-}
-
-__device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
-
-__device__ __forceinline__ float fast_silu(float x) {
-    return x * __builtin_amdgcn_rcpf(1.f + fast_exp(-x));
-}
-
-__device__ __forceinline__ float fast_softplus(float x) {
-    return x > 20.f ? x : __logf(1.f + fast_exp(x));
-}
-
-// Lane exchange through ds_bpermute: value of lane src. The index is computed by the
-// caller from its own lane number, so no address register lives across loops.
-__device__ __forceinline__ float bperm(float v, int src) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src << 2, __builtin_bit_cast(int, v)));
-}
-// DPP move: lanes whose source is outside the row (or outside row_mask) read 0.
-template <int kCtrl, int kRowMask = 0xf>
-__device__ __forceinline__ float dpp0(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, kRowMask,
-                                                                 0xf, true));
-}
-constexpr int kRowShr = 0x110;      // row_shr:n = kRowShr + n
-constexpr int kRowBcast15 = 0x142;  // lane 15 of each row to the next row
-constexpr int kRowBcast31 = 0x143;  // lane 31 to rows 2 and 3
-// Inclusive prefix sum over the 64 lanes: within 16-lane rows by row shifts, then across
-// rows by the row broadcasts.
-__device__ __forceinline__ float wave_incl_scan(float v) {
-    v += dpp0<kRowShr + 1>(v);
-    v += dpp0<kRowShr + 2>(v);
-    v += dpp0<kRowShr + 4>(v);
-    v += dpp0<kRowShr + 8>(v);
-    v += dpp0<kRowBcast15, 0xa>(v);
-    v += dpp0<kRowBcast31, 0xc>(v);
-    return v;
-}
-
-typedef short s16x4 __attribute__((vector_size(8)));
-// ds_read_b64_tr_b16: within each 16-lane group, lane j addresses 4 consecutive 16-bit
-// elements (row j/4, column group j%4 of a 4 x 16 block); lane i receives element m of
-// row m, column i. Two of these give the 8 k-values of an MFMA operand column from a
-// row-major [k][col] tile.
-__device__ __forceinline__ f16x4 ld_tr(const f16* p) {
-    const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (__attribute__((address_space(3))) s16x4*)(p));
-    return __builtin_bit_cast(f16x4, v);
-}
-__device__ __forceinline__ f16x2 as_f16x2(unsigned u) { return __builtin_bit_cast(f16x2, u); }
-__device__ __forceinline__ unsigned bits(f16x2 v) { return __builtin_bit_cast(unsigned, v); }
-
 
 // C~ / B~ tiles: 64-byte column groups of a row are XOR-swizzled by the row's 16-row
 // block, so the preparation's 64-bit stores (lanes 16 rows apart) hit distinct banks.
@@ -1084,7 +1003,7 @@ size_t mfma_prefill_workspace(const m3_layer_desc& d) {
     mfma_segments(d, S, cps);
     const size_t ntg = (size_t)d.batch * d.seqlen * d.ngroups;
     const size_t nseg = (size_t)d.batch * d.nheads * (S - 1);
-    const size_t bc_bytes = 2 * ntg * mf::NR * sizeof(mf::f16);
+    const size_t bc_bytes = 2 * ntg * mf::NR * sizeof(f16);
     return bc_bytes + nseg * ((size_t)mf::N * mf::P + 1 + mf::NH) * sizeof(float) + 256;
 }
 
@@ -1103,8 +1022,8 @@ int launch_mfma_prefill(const m3_layer_desc& d, const m3_layer_params& p, const 
     a.dt_scale = dt_scale;
     const int64_t ntg = (int64_t)d.batch * d.seqlen * d.ngroups;
     const int64_t nseg = (int64_t)d.batch * d.nheads * (S - 1);
-    mf::f16* bn = reinterpret_cast<mf::f16*>(workspace);
-    mf::f16* cn = bn + ntg * mf::NR;
+    f16* bn = reinterpret_cast<f16*>(workspace);
+    f16* cn = bn + ntg * mf::NR;
     float* ws = reinterpret_cast<float*>(cn + ntg * mf::NR);
     a.Bn = bn;
     a.Cn = cn;

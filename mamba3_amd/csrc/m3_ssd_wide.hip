@@ -1,0 +1,520 @@
+// bf16 fused chunked-SSD prefill on f16 MFMA for general layer shapes: d_state N in
+// {64, 128, 256}, mimo_rank R in {1, 2, 4}, headdim P a multiple of 32 (the d_model 2048
+// layer: N=256, P=128, R=4). d_state 128 / headdim 64 / rank 2 has its own kernel
+// (m3_ssd_mfma.hip).
+//
+// Same algorithm as the other prefill kernels: the quadratic form inside a chunk and the
+// state carried across chunks (mamba3/ssd.py:118-244), with the layer's preparation fused
+// (mamba3/mamba3.py:197-256). It is organised for shapes whose (batch, head) pairs alone
+// do not fill the GPU:
+//   * a workgroup owns (batch, head, 32 headdim columns), so B*H*P/32 workgroups share
+//     the work (256 for the d_model 2048 layer at batch 2); the scores and the RoPE
+//     rotation are recomputed by each column block;
+//   * a chunk has 64 (t, r) rows, i.e. Q = 64 / R tokens;
+//   * eight waves (two per SIMD) share every phase: prepare -> contract -> output.
+//
+// Per chunk, in LDS (f16 unless noted):
+//   C [(t,r)][n], B [(u,r')][n]       C~ / B~: normalised B^ / C^ (bc_norm_wide) rotated
+//                                     by the RoPE angle; row (t,r) = t*R + r
+//   XT [p][(u,r')], XwT [p][(u,r')]   x * mimo_x, and the same times the chunk weight w_u
+//   S [(t,r)][(u,r')]                 masked scores (fp32 accumulated)
+//   H [p][n]                          copy of the incoming state times kHScale
+//   tok, phi (fp32)                   token scalars and RoPE angles of the chunk
+// The fp32 state H^T lives in MFMA accumulators (wave w owns N/64 tiles of 16 x 16).
+// Contractions (v_mfma_f32_16x16x32_f16, fp32 accumulation):
+//   G4  H^T = e^{c_end} H^T + B~^T Xw    (A operand by LDS transpose reads of B~)
+//   G3  Y   = diag(e^{c_t}) C~ H^T
+//   G1  S^T = B~ C~^T per causal 16x16 tile, masked by
+//             Lc[t][u] = [u<=t] e^{c_t - c_u} (a_u + [u<t] b_u), plus D on the diagonal
+//   G2  Y  += S X
+// Output: out[t][p] = sum_r mimo_down[p,r] silu(z[t,p] mimo_z[p,r]) Y[(t,r)][p]
+// (mamba3/mamba3.py:233-238). The trapezoid is folded into a_u = lambda_u dt_u and
+// b_u = (1 - lambda_{u+1}) dt_{u+1}, as in the other kernels.
+#include "m3_common.h"
+#include "m3_kernels.h"
+#include "m3_mfma.h"
+
+namespace m3 {
+namespace wd {
+
+constexpr int ROWS = 64;              // (t, r) rows per chunk
+constexpr int PB = 32;                // headdim columns per workgroup
+constexpr int THREADS = 512;          // eight waves
+constexpr int PAD = 8;                // f16 row padding of the LDS tiles
+constexpr int kTokWave = 2;           // wave that prepares the next chunk's token scalars
+constexpr float kHScale = 1.f / 256.f;  // the f16 state copy holds h * kHScale
+
+struct Tok {
+    float c2[ROWS];  // inclusive prefix of A dt over the chunk, log2 units
+    float av[ROWS];  // a_u = lambda_u dt_u
+    float bv[ROWS];  // b_u = (1 - lambda_{u+1}) dt_{u+1}
+    float ec[ROWS];  // exp2(c2_t) / kHScale: inter-chunk output scale
+    float w[ROWS];   // exp2(c2_end - c2_u) (a_u + b_u): chunk-state weight
+    float dec;       // exp2(c2_end): chunk decay of the state
+};
+
+template <int N, int R>
+struct __align__(16) Smem {
+    static constexpr int Q = ROWS / R;
+    f16 C[ROWS][N + PAD];
+    f16 B[ROWS][N + PAD];
+    f16 XT[PB][ROWS + PAD];
+    f16 XwT[PB][ROWS + PAD];
+    f16 S[ROWS][ROWS + PAD];
+    f16 H[PB][N + PAD];
+    // Written for chunk k+1 in the output phase of chunk k, after every read of chunk k.
+    Tok tok;
+    float phi[Q][N / 2];  // RoPE angle of each (token, pair)
+};
+
+struct Args {
+    int B, T, H, G, P, PS;
+    int trap, cplx;
+    int64_t rs;  // proj row stride (elements)
+    ProjLayout pl;
+    m3_layer_params prm;
+    const bf16* proj;
+    const float* dt_scale;
+    const f16* Bn;  // [B*T][G][N*R] pair-packed normalised B^
+    const f16* Cn;
+    bf16* y_out;    // [B*T][H*P]
+    float* h_final;
+    float* angle;
+    float* prev_bx;
+};
+
+__device__ __forceinline__ float readlane(float v, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+
+// ---------------------------------------------------------------------------------
+// Normalised B^ / C^ per (token, group) (mamba3/mamba3.py:19-35, 142-157): RMSNorm over
+// the N*R row times the weight, plus the bias, in f16, pair-packed: the 32-bit word
+// i*R + r holds (value[n=2i][r], value[n=2i+1][r]). One wave per row.
+// ---------------------------------------------------------------------------------
+template <int N, int R>
+__global__ __launch_bounds__(256) void bc_norm_wide(const bf16* __restrict__ proj, int64_t rs,
+                                                    int64_t offB, int64_t offC, int G,
+                                                    int64_t nrows, float eps,
+                                                    const float* __restrict__ wB,
+                                                    const float* __restrict__ biasB,
+                                                    const float* __restrict__ wC,
+                                                    const float* __restrict__ biasC,
+                                                    f16* __restrict__ Bn, f16* __restrict__ Cn) {
+    constexpr int NH = N / 2, NR = N * R, PPL = (NH + 63) / 64;
+    const int lane = threadIdx.x & 63;
+    const int64_t tg = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (tg >= nrows) return;
+    const int64_t tok = tg / G;
+    const int g = (int)(tg % G);
+    const bf16* rowB = proj + tok * rs + offB + (int64_t)g * NR;
+    const bf16* rowC = proj + tok * rs + offC + (int64_t)g * NR;
+    // pair i covers raw elements 2iR .. 2iR+2R-1: (n=2i, r) at 2iR + r, (n=2i+1, r) at 2iR + R + r
+    float vb[PPL][2 * R], vc[PPL][2 * R];
+    float sb = 0.f, sc = 0.f;
+#pragma unroll
+    for (int j = 0; j < PPL; ++j) {
+        const int i = lane + 64 * j;
+#pragma unroll
+        for (int e = 0; e < 2 * R; ++e) {
+            vb[j][e] = i < NH ? (float)rowB[2 * i * R + e] : 0.f;
+            vc[j][e] = i < NH ? (float)rowC[2 * i * R + e] : 0.f;
+            sb += vb[j][e] * vb[j][e];
+            sc += vc[j][e] * vc[j][e];
+        }
+    }
+    sb = group_sum<64>(sb);
+    sc = group_sum<64>(sc);
+    const float rb = rsqrtf(sb * (1.f / NR) + eps), rc = rsqrtf(sc * (1.f / NR) + eps);
+    const float* bB = biasB + (int64_t)g * NR;
+    const float* bC = biasC + (int64_t)g * NR;
+#pragma unroll
+    for (int j = 0; j < PPL; ++j) {
+        const int i = lane + 64 * j;
+        if (i >= NH) continue;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int e0 = 2 * i * R + r, e1 = e0 + R;
+            const f16x2 ob = f16x2{(f16)(vb[j][r] * rb * wB[e0] + bB[e0]),
+                                   (f16)(vb[j][R + r] * rb * wB[e1] + bB[e1])};
+            const f16x2 oc = f16x2{(f16)(vc[j][r] * rc * wC[e0] + bC[e0]),
+                                   (f16)(vc[j][R + r] * rc * wC[e1] + bC[e1])};
+            *reinterpret_cast<f16x2*>(Bn + tg * NR + 2 * (i * R + r)) = ob;
+            *reinterpret_cast<f16x2*>(Cn + tg * NR + 2 * (i * R + r)) = oc;
+        }
+    }
+}
+
+// R consecutive 32-bit words (one RoPE pair, all ranks).
+template <int R>
+__device__ __forceinline__ void load_pair_words(const f16* p, unsigned (&w)[R]) {
+    if constexpr (R == 4) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(p);
+        w[0] = v[0]; w[1] = v[1]; w[2] = v[2]; w[3] = v[3];
+    } else if constexpr (R == 2) {
+        const u32x2 v = *reinterpret_cast<const u32x2*>(p);
+        w[0] = v[0]; w[1] = v[1];
+    } else {
+        w[0] = *reinterpret_cast<const unsigned*>(p);
+    }
+}
+
+// (e, o) rotated by the angle whose (cos, sin) is kA: (e cos - o sin, e sin + o cos).
+__device__ __forceinline__ unsigned rotate_pair(unsigned word, f16x2 kA, f16x2 kS) {
+    const f16x2 v = as_f16x2(word);
+    const f16x2 u = f16x2{v[1], v[1]} * kS;
+    return bits(f16x2{v[0], v[0]} * kA + f16x2{-u[0], u[1]});
+}
+
+template <int N, int R>
+__global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
+    constexpr int Q = ROWS / R;    // tokens per chunk
+    constexpr int NH = N / 2;      // RoPE pairs
+    constexpr int NR = N * R;
+    constexpr int TPW = N / 64;    // state tiles per wave
+    constexpr int KN = N / 32;     // k-steps over n
+    constexpr int PPL = (NH + 63) / 64;
+    constexpr int TPL = 4 / R;     // tokens per lane in an output tile
+    __shared__ Smem<N, R> sm;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g16 = lane >> 4, l16 = lane & 15;
+    const int pblk = blockIdx.x % a.PS;
+    const int bh = blockIdx.x / a.PS;
+    const int b = bh / a.H, h = bh % a.H;
+    const int grp = h / (a.H / a.G);
+    const int p0 = pblk * PB;
+    const int T = a.T;
+    const int64_t rs = a.rs;
+    const bf16* proj = a.proj + (int64_t)b * T * rs;
+    const int64_t nrs = (int64_t)a.G * NR;  // B^ / C^ token stride
+    const f16* Bn = a.Bn + (int64_t)b * T * nrs + (int64_t)grp * NR;
+    const f16* Cn = a.Cn + (int64_t)b * T * nrs + (int64_t)grp * NR;
+    const int nchunks = (T + Q - 1) / Q;
+    const float Ah = -expf(a.prm.A_log[h]);
+    const float Dh = a.prm.D[h];
+    const float dtb = a.prm.dt_bias[h];
+    const int hp = h * a.P;  // first column of this head in x, z and y
+
+    // Output tile of this wave: rows 16 tt .. 16 tt + 15, columns 16 pt .. 16 pt + 15.
+    const int tt = wave >> 1, pt = wave & 1;
+    const int pe = p0 + 16 * pt + l16;  // this lane's output column
+    float mzr[R], mdr[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        mzr[r] = a.prm.mimo_z[(int64_t)(hp + pe) * R + r];
+        mdr[r] = a.prm.mimo_down[(int64_t)(hp + pe) * R + r];
+    }
+    // X preparation job: column xp, rows 4 xj .. 4 xj + 3.
+    const int xp = tid & (PB - 1), xj = tid / PB;
+    float mxr[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) mxr[q] = a.prm.mimo_x[(int64_t)(hp + p0 + xp) * R + (4 * xj + q) % R];
+
+    // Token scalars and RoPE angles of chunk kk (wave kTokWave; lane t = token s0 + t).
+    float phi_run[PPL];
+#pragma unroll
+    for (int j = 0; j < PPL; ++j) phi_run[j] = 0.f;
+    auto gate_at = [&](int st, float& dt, float& lam) {
+        dt = 0.f;
+        lam = 1.f;
+        if (st < T) {
+            const bf16* row = proj + (int64_t)st * rs;
+            const float sc = a.dt_scale ? a.dt_scale[((int64_t)b * T + st) * a.H + h] : 1.f;
+            dt = softplus_f((float)row[a.pl.dt + h] + dtb) * sc;
+            if (a.trap) lam = sigmoid_f((float)row[a.pl.lam + h]);
+        }
+    };
+    auto prep_tokens = [&](int kk) {
+        const int s0 = kk * Q;
+        const int t = lane;
+        float dt_t = 0.f, lam_t = 1.f, dt_n = 0.f, lam_n = 1.f;
+        if (t < Q) {
+            gate_at(s0 + t, dt_t, lam_t);
+            gate_at(s0 + t + 1, dt_n, lam_n);
+        }
+        const float c2 = wave_incl_scan(Ah * dt_t * kLog2e);
+        const float c2_end = readlane(c2, Q - 1);
+        const float av = a.trap ? lam_t * dt_t : dt_t;
+        const float bv = a.trap ? (1.f - lam_n) * dt_n : 0.f;
+        Tok& tk = sm.tok;
+        if (t < Q) {
+            tk.c2[t] = c2;
+            tk.av[t] = av;
+            tk.bv[t] = bv;
+            tk.ec[t] = __builtin_amdgcn_exp2f(c2) * (1.f / kHScale);
+            tk.w[t] = __builtin_amdgcn_exp2f(c2_end - c2) * (av + bv);
+        }
+        if (t == 0) tk.dec = __builtin_amdgcn_exp2f(c2_end);
+        if (a.cplx) {
+            // phi_t[i] = phi_{t-1}[i] - dt_t theta_t[i] (mamba3/mamba3.py:160-162)
+#pragma unroll
+            for (int j = 0; j < PPL; ++j) {
+                const int i = lane + 64 * j;
+                if (i < NH) {
+                    float th[Q];
+#pragma unroll
+                    for (int q = 0; q < Q; ++q)
+                        th[q] = s0 + q < T ? (float)proj[(int64_t)(s0 + q) * rs + a.pl.theta + i] : 0.f;
+                    float ph = phi_run[j];
+#pragma unroll
+                    for (int q = 0; q < Q; ++q) {
+                        ph -= readlane(dt_t, q) * th[q];
+                        sm.phi[q][i] = ph;
+                    }
+                    phi_run[j] = ph;
+                }
+            }
+        }
+    };
+
+    // State tiles of this wave: j -> (n tile, p tile) = ((wave*TPW + j) / 2, (wave*TPW + j) % 2).
+    f32x4 hacc[TPW];
+#pragma unroll
+    for (int j = 0; j < TPW; ++j) hacc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int idx = tid; idx < PB * (N + PAD) / 2; idx += THREADS)
+        reinterpret_cast<unsigned*>(&sm.H[0][0])[idx] = 0u;
+    if (wave == kTokWave) prep_tokens(0);
+    __syncthreads();
+
+    for (int k = 0; k < nchunks; ++k) {
+        const int s0 = k * Q;
+        const Tok& tk = sm.tok;
+
+        // ---- prepare: rotated C~ / B~ rows, X rows ----
+        for (int job = tid; job < Q * NH; job += THREADS) {
+            const int t = job / NH, i = job % NH;
+            const int st = s0 + t;
+            unsigned wb[R], wc[R];
+            if (st < T) {
+                load_pair_words<R>(Bn + (int64_t)st * nrs + 2 * i * R, wb);
+                load_pair_words<R>(Cn + (int64_t)st * nrs + 2 * i * R, wc);
+            } else {
+#pragma unroll
+                for (int r = 0; r < R; ++r) wb[r] = wc[r] = 0u;
+            }
+            f16x2 kA = f16x2{(f16)1.f, (f16)0.f};
+            if (a.cplx) {
+                float sn, cs;
+                fast_sincos(sm.phi[t][i], sn, cs);
+                kA = f16x2{(f16)cs, (f16)sn};
+            }
+            const f16x2 kS = __builtin_shufflevector(kA, kA, 1, 0);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                *reinterpret_cast<unsigned*>(&sm.B[t * R + r][2 * i]) = rotate_pair(wb[r], kA, kS);
+                *reinterpret_cast<unsigned*>(&sm.C[t * R + r][2 * i]) = rotate_pair(wc[r], kA, kS);
+            }
+        }
+        {
+            f16x4 xv, xw;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int row = 4 * xj + q;
+                const int t = row / R;
+                const int st = s0 + t;
+                const float xval = st < T ? (float)proj[(int64_t)st * rs + a.pl.x + hp + p0 + xp] : 0.f;
+                const float X = xval * mxr[q];
+                xv[q] = (f16)X;
+                xw[q] = (f16)(X * tk.w[t]);
+            }
+            *reinterpret_cast<f16x4*>(&sm.XT[xp][4 * xj]) = xv;
+            *reinterpret_cast<f16x4*>(&sm.XwT[xp][4 * xj]) = xw;
+        }
+        __syncthreads();
+
+        // ---- contract: G4, G3, G1 ----
+        float zv[TPL];
+#pragma unroll
+        for (int q = 0; q < TPL; ++q) {
+            const int st = s0 + (16 * tt + 4 * g16) / R + q;
+            zv[q] = st < T ? (float)proj[(int64_t)st * rs + a.pl.z + hp + pe] : 0.f;
+        }
+        {
+            const float dec = tk.dec;
+#pragma unroll
+            for (int j = 0; j < TPW; ++j) hacc[j] *= dec;
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+#pragma unroll
+                for (int j = 0; j < TPW; ++j) {
+                    const int jt = wave * TPW + j;
+                    const int nt = jt >> 1, ptj = jt & 1;
+                    const f16* bp = &sm.B[32 * s + 8 * g16 + (l16 >> 2)][16 * nt + 4 * (l16 & 3)];
+                    const f16x4 lo = ld_tr(bp);
+                    const f16x4 hi = ld_tr(bp + 4 * (N + PAD));
+                    const f16x8 A = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+                    const f16x8 Bo = *reinterpret_cast<const f16x8*>(&sm.XwT[16 * ptj + l16][32 * s + 8 * g16]);
+                    hacc[j] = mfma16(A, Bo, hacc[j]);
+                }
+            }
+        }
+        f32x4 yacc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < KN; ++s) {
+            const f16x8 A = *reinterpret_cast<const f16x8*>(&sm.C[16 * tt + l16][32 * s + 8 * g16]);
+            const f16x8 Bo = *reinterpret_cast<const f16x8*>(&sm.H[16 * pt + l16][32 * s + 8 * g16]);
+            yacc = mfma16(A, Bo, yacc);
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v) yacc[v] *= tk.ec[(16 * tt + 4 * g16 + v) / R];
+
+        // Causal score tiles (ti, ui), ui <= ti, listed row by row: waves 0..7 take tiles
+        // 0..7, waves 0 and 1 also tiles 8 and 9 (their G2 is the shortest).
+        for (int idx = wave; idx < 10; idx += 8) {
+            const int ti = idx < 1 ? 0 : idx < 3 ? 1 : idx < 6 ? 2 : 3;
+            const int ui = idx - ti * (ti + 1) / 2;
+            f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < KN; ++s) {
+                const f16x8 A = *reinterpret_cast<const f16x8*>(&sm.B[16 * ui + l16][32 * s + 8 * g16]);
+                const f16x8 Bo = *reinterpret_cast<const f16x8*>(&sm.C[16 * ti + l16][32 * s + 8 * g16]);
+                sacc = mfma16(A, Bo, sacc);
+            }
+            // lane: u-row 16 ui + 4 g16 + v, t-row 16 ti + l16
+            const int trow = 16 * ti + l16;
+            const int t = trow / R;
+            const float ct = tk.c2[t];
+            f16x4 sv;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int urow = 16 * ui + 4 * g16 + v;
+                const int u = urow / R;
+                float val = 0.f;
+                if (u <= t)
+                    val = sacc[v] * __builtin_amdgcn_exp2f(ct - tk.c2[u]) * (tk.av[u] + (u < t ? tk.bv[u] : 0.f));
+                if (urow == trow) val += Dh;
+                sv[v] = (f16)val;
+            }
+            *reinterpret_cast<f16x4*>(&sm.S[trow][16 * ui + 4 * g16]) = sv;
+        }
+        if (wave == 3) {
+            // G2 reads 32 score columns per step: the tiles right of the diagonal in row
+            // blocks 0 and 2 are zero.
+#pragma unroll
+            for (int ti = 0; ti < 4; ti += 2)
+                *reinterpret_cast<f16x4*>(&sm.S[16 * ti + l16][16 * (ti + 1) + 4 * g16]) = f16x4{0, 0, 0, 0};
+        }
+        __syncthreads();
+
+        // ---- output: G2, gate, store; state copy; next chunk's token scalars ----
+        for (int s = 0; s <= tt / 2; ++s) {
+            const f16x8 A = *reinterpret_cast<const f16x8*>(&sm.S[16 * tt + l16][32 * s + 8 * g16]);
+            const f16x8 Bo = *reinterpret_cast<const f16x8*>(&sm.XT[16 * pt + l16][32 * s + 8 * g16]);
+            yacc = mfma16(A, Bo, yacc);
+        }
+#pragma unroll
+        for (int q = 0; q < TPL; ++q) {
+            const int st = s0 + (16 * tt + 4 * g16) / R + q;
+            float o = 0.f;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const float zr = zv[q] * mzr[r];
+                o += mdr[r] * zr * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-zr * kLog2e)) * yacc[q * R + r];
+            }
+            if (st < T) a.y_out[((int64_t)b * T + st) * a.H * a.P + hp + pe] = (bf16)o;
+        }
+#pragma unroll
+        for (int j = 0; j < TPW; ++j) {
+            const int jt = wave * TPW + j;
+            const int nt = jt >> 1, ptj = jt & 1;
+            const f16x4 hv = f16x4{(f16)(hacc[j][0] * kHScale), (f16)(hacc[j][1] * kHScale),
+                                   (f16)(hacc[j][2] * kHScale), (f16)(hacc[j][3] * kHScale)};
+            *reinterpret_cast<f16x4*>(&sm.H[16 * ptj + l16][16 * nt + 4 * g16]) = hv;
+        }
+        if (wave == kTokWave && k + 1 < nchunks) prep_tokens(k + 1);
+        __syncthreads();
+    }
+
+    // Final state h[p][n] (fp32) from the accumulators: lane holds n = 16 nt + 4 g16 + v.
+    if (a.h_final) {
+#pragma unroll
+        for (int j = 0; j < TPW; ++j) {
+            const int jt = wave * TPW + j;
+            const int nt = jt >> 1, ptj = jt & 1;
+            const int p = p0 + 16 * ptj + l16;
+            *reinterpret_cast<f32x4*>(a.h_final + ((int64_t)bh * a.P + p) * N + 16 * nt + 4 * g16) = hacc[j];
+        }
+    }
+    if (a.angle && pblk == 0 && wave == kTokWave) {
+#pragma unroll
+        for (int j = 0; j < PPL; ++j) {
+            const int i = lane + 64 * j;
+            if (i < NH) a.angle[(int64_t)bh * NH + i] = a.cplx ? phi_run[j] : 0.f;
+        }
+    }
+    // prev_BX = sum_r B~_{T-1}[n][r] X_{T-1}[p][r] (mamba3/mamba3.py:247-250) from the last
+    // chunk's tiles.
+    if (a.prev_bx) {
+        const int tl = T - 1 - (nchunks - 1) * Q;
+        for (int idx = tid; idx < PB * N; idx += THREADS) {
+            const int p = idx / N, n = idx % N;
+            float v = 0.f;
+#pragma unroll
+            for (int r = 0; r < R; ++r) v += (float)sm.B[tl * R + r][n] * (float)sm.XT[p][tl * R + r];
+            a.prev_bx[((int64_t)bh * a.P + p0 + p) * N + n] = v;
+        }
+    }
+}
+
+template <int N, int R>
+int launch(const m3_layer_desc& d, const m3_layer_params& p, const void* proj,
+           const float* dt_scale, void* y_out, float* h_final, float* angle, float* prev_bx,
+           void* workspace, hipStream_t stream) {
+    Args a;
+    a.B = d.batch; a.T = d.seqlen; a.H = d.nheads; a.G = d.ngroups; a.P = d.headdim;
+    a.PS = d.headdim / PB;
+    a.trap = d.use_trapezoidal; a.cplx = d.use_complex;
+    a.rs = d.proj_row_stride;
+    a.pl = proj_layout(d);
+    a.prm = p;
+    a.proj = reinterpret_cast<const bf16*>(proj);
+    a.dt_scale = dt_scale;
+    const int64_t nrows = (int64_t)d.batch * d.seqlen * d.ngroups;
+    f16* bn = reinterpret_cast<f16*>(workspace);
+    f16* cn = bn + nrows * N * R;
+    a.Bn = bn;
+    a.Cn = cn;
+    a.y_out = reinterpret_cast<bf16*>(y_out);
+    a.h_final = h_final;
+    a.angle = angle;
+    a.prev_bx = prev_bx;
+    hipLaunchKernelGGL((bc_norm_wide<N, R>), dim3((unsigned)((nrows + 3) / 4)), dim3(256), 0, stream,
+                       a.proj, a.rs, a.pl.B, a.pl.C, a.G, nrows, d.rms_eps, p.B_norm_w, p.B_bias,
+                       p.C_norm_w, p.C_bias, bn, cn);
+    hipLaunchKernelGGL((ssd_wide<N, R>), dim3((unsigned)(d.batch * d.nheads * a.PS)), dim3(THREADS), 0,
+                       stream, a);
+    return hipGetLastError() == hipSuccess ? M3_OK : M3_ERR_LAUNCH;
+}
+
+}  // namespace wd
+
+bool wide_prefill_supported(const m3_layer_desc& d) {
+    if (d.dtype != M3_DTYPE_BF16) return false;
+    if (d.headdim % wd::PB != 0) return false;
+    const int N = d.d_state, R = d.mimo_rank;
+    if (N != 64 && N != 128 && N != 256) return false;
+    if (R != 1 && R != 2 && R != 4) return false;
+    return true;
+}
+
+size_t wide_prefill_workspace(const m3_layer_desc& d) {
+    const size_t nrows = (size_t)d.batch * d.seqlen * d.ngroups;
+    return 2 * nrows * d.d_state * d.mimo_rank * sizeof(f16) + 256;
+}
+
+int launch_wide_prefill(const m3_layer_desc& d, const m3_layer_params& p, const void* proj,
+                        const float* dt_scale, void* y_out, float* h_final, float* angle,
+                        float* prev_bx, void* workspace, hipStream_t stream) {
+#define M3_WIDE_CASE(n, r)                                                                      \
+    if (d.d_state == n && d.mimo_rank == r)                                                     \
+        return wd::launch<n, r>(d, p, proj, dt_scale, y_out, h_final, angle, prev_bx, workspace, \
+                                stream);
+    M3_WIDE_CASE(64, 1) M3_WIDE_CASE(64, 2) M3_WIDE_CASE(64, 4)
+    M3_WIDE_CASE(128, 1) M3_WIDE_CASE(128, 2) M3_WIDE_CASE(128, 4)
+    M3_WIDE_CASE(256, 1) M3_WIDE_CASE(256, 2) M3_WIDE_CASE(256, 4)
+#undef M3_WIDE_CASE
+    return M3_ERR_UNSUPPORTED;
+}
+
+}  // namespace m3

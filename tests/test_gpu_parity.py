@@ -360,6 +360,55 @@ def test_fp32_step_matches_oracle_from_random_state(cuda_device):
         assert max_rel(st2[k], st_ref[k]) < FP32_TOL, k
 
 
+# ------------------------------------------------------------------ general MFMA prefill kernel
+# bf16 layers with d_state 64/128/256, rank 1/2/4 and headdim % 32 == 0 (other than
+# d_state 128 / headdim 64 / rank 2) run on the general MFMA kernel: one case per
+# (d_state, rank) instantiation, lengths that end mid-chunk, and the layer flags.
+WIDE_CASES = [
+    (dict(d_model=64, d_state=64, headdim=32, mimo_rank=1), 150),
+    (dict(d_model=64, d_state=64, headdim=32, mimo_rank=2), 97),
+    (dict(d_model=64, d_state=64, headdim=32, mimo_rank=4), 77),
+    (dict(d_model=128, d_state=128, headdim=64, mimo_rank=1), 200),
+    (dict(d_model=96, d_state=128, headdim=32, mimo_rank=2), 129),
+    (dict(d_model=64, d_state=128, headdim=32, mimo_rank=4), 61),
+    (dict(d_model=128, d_state=256, headdim=64, mimo_rank=1), 70),
+    (dict(d_model=128, d_state=256, headdim=64, mimo_rank=2), 100),
+    (dict(d_model=256, d_state=256, headdim=128, mimo_rank=4), 130),
+    (dict(d_model=192, d_state=256, headdim=96, mimo_rank=4, ngroups=2), 45),
+    (dict(d_model=256, d_state=256, headdim=128, mimo_rank=4, use_trapezoidal=False), 33),
+    (dict(d_model=256, d_state=256, headdim=128, mimo_rank=4, use_complex_ssm=False), 17),
+    (dict(d_model=128, d_state=128, headdim=32, mimo_rank=4, ngroups=8), 1),
+]
+
+
+@pytest.mark.parametrize("kw,T", WIDE_CASES)
+def test_bf16_wide_prefill_matches_fp32_oracle(kw, T, cuda_device):
+    layer, cfg, p = _bf16_pair(kw, cuda_device, seed=11)
+    torch.manual_seed(T)
+    x = torch.randn(2, T, kw["d_model"]).to(torch.bfloat16)
+    with torch.no_grad():
+        y, st = layer.prefill(x.to(cuda_device))
+        y_ref, st_ref = ref.layer_forward(cfg, p, x.float(), return_state=True)
+    assert max_rel(y.float(), y_ref) < BF16_TOL
+    for k in ("h", "prev_BX", "angle"):
+        assert max_rel(st[k], st_ref[k]) < BF16_TOL, k
+
+
+def test_bf16_d2048_prefill_matches_fp32_oracle(cuda_device):
+    """The d_model 2048 layer (d_state 256, headdim 128, rank 4), with dt_scale."""
+    kw = dict(d_model=2048, d_state=256, headdim=128, mimo_rank=4)
+    layer, cfg, p = _bf16_pair(kw, cuda_device, seed=12)
+    torch.manual_seed(13)
+    x = torch.randn(1, 130, 2048).to(torch.bfloat16)
+    ds = torch.rand(1, 130, layer.nheads) * 1.5 + 0.5
+    with torch.no_grad():
+        y, st = layer.prefill(x.to(cuda_device), dt_scale=ds.to(cuda_device))
+        y_ref, st_ref = ref.layer_forward(cfg, p, x.float(), dt_scale=ds, return_state=True)
+    assert max_rel(y.float(), y_ref) < BF16_TOL
+    for k in ("h", "prev_BX", "angle"):
+        assert max_rel(st[k], st_ref[k]) < BF16_TOL, k
+
+
 # ------------------------------------------------------------------ full-size properties
 def test_bf16_d768_long_prefill_properties(cuda_device):
     """x (8, 8192, 768) bf16 (the long-prefill workload): batch independence and causality
@@ -393,4 +442,33 @@ def test_bf16_d768_long_prefill_properties(cuda_device):
         y_full = layer.out_proj(y[:2, 8176:])
     ys = torch.stack(outs, 1).float()
     e4, e5 = max_rel(ys, y_full.float()), max_rel(sp["h"], st["h"][:2])
+    assert e4 < BF16_TOL and e5 < BF16_TOL, (e4, e5)
+
+
+def test_bf16_d2048_long_prefill_properties(cuda_device):
+    """x (2, 16384, 2048) bf16 (the wide-layer workload): every (batch, head, column
+    block) runs independently and chunks start at fixed positions, so a sub-batch and a
+    prefix reproduce the full run bit for bit; the prefill -> step hand-off agrees with
+    the full prefill."""
+    kw = dict(d_model=2048, d_state=256, headdim=128, mimo_rank=4)
+    torch.manual_seed(0)
+    layer = mamba3_amd.KulaMamba(**kw).to(cuda_device, torch.bfloat16).eval()
+    torch.manual_seed(6)
+    x = torch.randn(2, 16384, 2048, device=cuda_device).to(torch.bfloat16)
+    with torch.no_grad():
+        proj = layer.in_proj(x)
+        y, st = layer.ssd_from_proj(proj, return_state=True)
+        assert torch.isfinite(y.float()).all() and torch.isfinite(st["h"]).all()
+        y1, st1 = layer.ssd_from_proj(proj[1:2].contiguous(), return_state=True)
+        assert torch.equal(y1, y[1:2]) and torch.equal(st1["h"], st["h"][1:2])
+        yp, _ = layer.ssd_from_proj(proj[:, :3000].contiguous())
+        assert torch.equal(yp, y[:, :3000])
+        _, sp = layer.prefill(x[:, :16368])
+        outs = []
+        for t in range(16368, 16384):
+            o, sp = layer.step(x[:, t], sp)
+            outs.append(o)
+        y_full = layer.out_proj(y[:, 16368:])
+    ys = torch.stack(outs, 1).float()
+    e4, e5 = max_rel(ys, y_full.float()), max_rel(sp["h"], st["h"])
     assert e4 < BF16_TOL and e5 < BF16_TOL, (e4, e5)
