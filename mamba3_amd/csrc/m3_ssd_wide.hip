@@ -41,7 +41,6 @@ constexpr int ROWS = 64;              // (t, r) rows per chunk
 constexpr int PB = 32;                // headdim columns per workgroup
 constexpr int THREADS = 512;          // eight waves
 constexpr int PAD = 8;                // f16 row padding of the LDS tiles
-constexpr int kTokWave = 2;           // wave that prepares the next chunk's token scalars
 constexpr float kHScale = 1.f / 256.f;  // the f16 state copy holds h * kHScale
 
 struct Tok {
@@ -173,7 +172,6 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
     constexpr int NR = N * R;
     constexpr int TPW = N / 64;    // state tiles per wave
     constexpr int KN = N / 32;     // k-steps over n
-    constexpr int PPL = (NH + 63) / 64;
     constexpr int TPL = 4 / R;     // tokens per lane in an output tile
     __shared__ Smem<N, R> sm;
 
@@ -211,60 +209,91 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) mxr[q] = a.prm.mimo_x[(int64_t)(hp + p0 + xp) * R + (4 * xj + q) % R];
 
-    // Token scalars and RoPE angles of chunk kk (wave kTokWave; lane t = token s0 + t).
-    float phi_run[PPL];
+    // ---- per-chunk inputs, loaded into registers one phase before they are used ----
+    // Rotation jobs: this thread's RoPE pair ri at tokens rt0 + m * TSTEP (m < J).
+    constexpr int J = Q * NH / THREADS;
+    constexpr int TSTEP = THREADS / NH;
+    const int ri = tid % NH, rt0 = tid / NH;
+    unsigned pwb[J][R], pwc[J][R];
+    auto load_bc = [&](int kk) {
 #pragma unroll
-    for (int j = 0; j < PPL; ++j) phi_run[j] = 0.f;
-    auto gate_at = [&](int st, float& dt, float& lam) {
-        dt = 0.f;
-        lam = 1.f;
-        if (st < T) {
-            const bf16* row = proj + (int64_t)st * rs;
-            const float sc = a.dt_scale ? a.dt_scale[((int64_t)b * T + st) * a.H + h] : 1.f;
-            dt = softplus_f((float)row[a.pl.dt + h] + dtb) * sc;
-            if (a.trap) lam = sigmoid_f((float)row[a.pl.lam + h]);
+        for (int m = 0; m < J; ++m) {
+            const int st = kk * Q + rt0 + m * TSTEP;
+            const int64_t off = (int64_t)min(st, T - 1) * nrs + 2 * ri * R;  // in range; zeroed below
+            load_pair_words<R>(Bn + off, pwb[m]);
+            load_pair_words<R>(Cn + off, pwc[m]);
         }
     };
+    // X job tokens: raw bf16 bits of x for rows 4 xj + q.
+    unsigned pxv[4];
+    auto load_x = [&](int kk) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int st = min(kk * Q + (4 * xj + q) / R, T - 1);
+            pxv[q] = *reinterpret_cast<const unsigned short*>(proj + (int64_t)st * rs + a.pl.x + hp + p0 + xp);
+        }
+    };
+    // Token scalars and RoPE angles: waves 0 .. NWA-1, lane t = token t of the chunk for
+    // the scalars and pair 64 wave + lane for the angles.
+    constexpr int NWA = (NH + 63) / 64;
+    const bool angle_wave = wave < NWA;
+    const int ai = 64 * wave + lane;  // this lane's RoPE pair in an angle wave
+    float phi_run = 0.f;
+    unsigned rdt0, rlam0, rdt1, rlam1, thr[Q];
+    float sc0, sc1;
+    auto load_tokens = [&](int kk) {
+        const int s0 = kk * Q;
+        const int st0 = min(s0 + lane, T - 1), st1 = min(s0 + lane + 1, T - 1);
+        const bf16* row0 = proj + (int64_t)st0 * rs;
+        const bf16* row1 = proj + (int64_t)st1 * rs;
+        rdt0 = *reinterpret_cast<const unsigned short*>(row0 + a.pl.dt + h);
+        rdt1 = *reinterpret_cast<const unsigned short*>(row1 + a.pl.dt + h);
+        rlam0 = a.trap ? *reinterpret_cast<const unsigned short*>(row0 + a.pl.lam + h) : 0u;
+        rlam1 = a.trap ? *reinterpret_cast<const unsigned short*>(row1 + a.pl.lam + h) : 0u;
+        sc0 = a.dt_scale ? a.dt_scale[((int64_t)b * T + st0) * a.H + h] : 1.f;
+        sc1 = a.dt_scale ? a.dt_scale[((int64_t)b * T + st1) * a.H + h] : 1.f;
+        if (a.cplx) {
+            const int i = min(ai, NH - 1);
+#pragma unroll
+            for (int q = 0; q < Q; ++q)
+                thr[q] = *reinterpret_cast<const unsigned short*>(
+                    proj + (int64_t)min(s0 + q, T - 1) * rs + a.pl.theta + i);
+        }
+    };
+    auto bf = [](unsigned u) { return __builtin_bit_cast(float, u << 16); };
     auto prep_tokens = [&](int kk) {
         const int s0 = kk * Q;
         const int t = lane;
-        float dt_t = 0.f, lam_t = 1.f, dt_n = 0.f, lam_n = 1.f;
-        if (t < Q) {
-            gate_at(s0 + t, dt_t, lam_t);
-            gate_at(s0 + t + 1, dt_n, lam_n);
-        }
+        const bool v0 = t < Q && s0 + t < T, v1 = t < Q && s0 + t + 1 < T;
+        // mamba3/mamba3.py:200-204, 212-216
+        const float dt_t = v0 ? softplus_f(bf(rdt0) + dtb) * sc0 : 0.f;
+        const float dt_n = v1 ? softplus_f(bf(rdt1) + dtb) * sc1 : 0.f;
+        const float lam_t = v0 && a.trap ? sigmoid_f(bf(rlam0)) : 1.f;
+        const float lam_n = v1 && a.trap ? sigmoid_f(bf(rlam1)) : 1.f;
         const float c2 = wave_incl_scan(Ah * dt_t * kLog2e);
         const float c2_end = readlane(c2, Q - 1);
-        const float av = a.trap ? lam_t * dt_t : dt_t;
-        const float bv = a.trap ? (1.f - lam_n) * dt_n : 0.f;
-        Tok& tk = sm.tok;
-        if (t < Q) {
-            tk.c2[t] = c2;
-            tk.av[t] = av;
-            tk.bv[t] = bv;
-            tk.ec[t] = __builtin_amdgcn_exp2f(c2) * (1.f / kHScale);
-            tk.w[t] = __builtin_amdgcn_exp2f(c2_end - c2) * (av + bv);
-        }
-        if (t == 0) tk.dec = __builtin_amdgcn_exp2f(c2_end);
-        if (a.cplx) {
-            // phi_t[i] = phi_{t-1}[i] - dt_t theta_t[i] (mamba3/mamba3.py:160-162)
-#pragma unroll
-            for (int j = 0; j < PPL; ++j) {
-                const int i = lane + 64 * j;
-                if (i < NH) {
-                    float th[Q];
-#pragma unroll
-                    for (int q = 0; q < Q; ++q)
-                        th[q] = s0 + q < T ? (float)proj[(int64_t)(s0 + q) * rs + a.pl.theta + i] : 0.f;
-                    float ph = phi_run[j];
-#pragma unroll
-                    for (int q = 0; q < Q; ++q) {
-                        ph -= readlane(dt_t, q) * th[q];
-                        sm.phi[q][i] = ph;
-                    }
-                    phi_run[j] = ph;
-                }
+        if (wave == 0) {
+            const float av = a.trap ? lam_t * dt_t : dt_t;
+            const float bv = a.trap ? (1.f - lam_n) * dt_n : 0.f;
+            Tok& tk = sm.tok;
+            if (t < Q) {
+                tk.c2[t] = c2;
+                tk.av[t] = av;
+                tk.bv[t] = bv;
+                tk.ec[t] = __builtin_amdgcn_exp2f(c2) * (1.f / kHScale);
+                tk.w[t] = __builtin_amdgcn_exp2f(c2_end - c2) * (av + bv);
             }
+            if (t == 0) tk.dec = __builtin_amdgcn_exp2f(c2_end);
+        }
+        if (a.cplx && ai < NH) {
+            // phi_t[i] = phi_{t-1}[i] - dt_t theta_t[i] (mamba3/mamba3.py:160-162)
+            float ph = phi_run;
+#pragma unroll
+            for (int q = 0; q < Q; ++q) {
+                ph -= readlane(dt_t, q) * bf(thr[q]);
+                sm.phi[q][ai] = ph;
+            }
+            phi_run = ph;
         }
     };
 
@@ -274,62 +303,62 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
     for (int j = 0; j < TPW; ++j) hacc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
     for (int idx = tid; idx < PB * (N + PAD) / 2; idx += THREADS)
         reinterpret_cast<unsigned*>(&sm.H[0][0])[idx] = 0u;
-    if (wave == kTokWave) prep_tokens(0);
+    load_bc(0);
+    load_x(0);
+    if (angle_wave) {
+        load_tokens(0);
+        prep_tokens(0);
+    }
     __syncthreads();
 
     for (int k = 0; k < nchunks; ++k) {
         const int s0 = k * Q;
         const Tok& tk = sm.tok;
 
-        // ---- prepare: rotated C~ / B~ rows, X rows ----
-        for (int job = tid; job < Q * NH; job += THREADS) {
-            const int t = job / NH, i = job % NH;
-            const int st = s0 + t;
-            unsigned wb[R], wc[R];
-            if (st < T) {
-                load_pair_words<R>(Bn + (int64_t)st * nrs + 2 * i * R, wb);
-                load_pair_words<R>(Cn + (int64_t)st * nrs + 2 * i * R, wc);
-            } else {
+        // ---- prepare: rotated C~ / B~ rows, X rows; then the next chunk's reads ----
 #pragma unroll
-                for (int r = 0; r < R; ++r) wb[r] = wc[r] = 0u;
-            }
+        for (int m = 0; m < J; ++m) {
+            const int t = rt0 + m * TSTEP;
+            const bool valid = s0 + t < T;
             f16x2 kA = f16x2{(f16)1.f, (f16)0.f};
             if (a.cplx) {
                 float sn, cs;
-                fast_sincos(sm.phi[t][i], sn, cs);
+                fast_sincos(sm.phi[t][ri], sn, cs);
                 kA = f16x2{(f16)cs, (f16)sn};
             }
             const f16x2 kS = __builtin_shufflevector(kA, kA, 1, 0);
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                *reinterpret_cast<unsigned*>(&sm.B[t * R + r][2 * i]) = rotate_pair(wb[r], kA, kS);
-                *reinterpret_cast<unsigned*>(&sm.C[t * R + r][2 * i]) = rotate_pair(wc[r], kA, kS);
+                *reinterpret_cast<unsigned*>(&sm.B[t * R + r][2 * ri]) = valid ? rotate_pair(pwb[m][r], kA, kS) : 0u;
+                *reinterpret_cast<unsigned*>(&sm.C[t * R + r][2 * ri]) = valid ? rotate_pair(pwc[m][r], kA, kS) : 0u;
             }
         }
         {
             f16x4 xv, xw;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const int row = 4 * xj + q;
-                const int t = row / R;
-                const int st = s0 + t;
-                const float xval = st < T ? (float)proj[(int64_t)st * rs + a.pl.x + hp + p0 + xp] : 0.f;
-                const float X = xval * mxr[q];
+                const int t = (4 * xj + q) / R;
+                const float X = s0 + t < T ? bf(pxv[q]) * mxr[q] : 0.f;
                 xv[q] = (f16)X;
                 xw[q] = (f16)(X * tk.w[t]);
             }
             *reinterpret_cast<f16x4*>(&sm.XT[xp][4 * xj]) = xv;
             *reinterpret_cast<f16x4*>(&sm.XwT[xp][4 * xj]) = xw;
         }
+        if (k + 1 < nchunks) {
+            load_bc(k + 1);
+            load_x(k + 1);
+        }
         __syncthreads();
 
         // ---- contract: G4, G3, G1 ----
-        float zv[TPL];
+        unsigned zr_bits[TPL];
 #pragma unroll
         for (int q = 0; q < TPL; ++q) {
-            const int st = s0 + (16 * tt + 4 * g16) / R + q;
-            zv[q] = st < T ? (float)proj[(int64_t)st * rs + a.pl.z + hp + pe] : 0.f;
+            const int st = min(s0 + (16 * tt + 4 * g16) / R + q, T - 1);
+            zr_bits[q] = *reinterpret_cast<const unsigned short*>(proj + (int64_t)st * rs + a.pl.z + hp + pe);
         }
+        if (angle_wave && k + 1 < nchunks) load_tokens(k + 1);
         {
             const float dec = tk.dec;
 #pragma unroll
@@ -406,10 +435,11 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
 #pragma unroll
         for (int q = 0; q < TPL; ++q) {
             const int st = s0 + (16 * tt + 4 * g16) / R + q;
+            const float z = bf(zr_bits[q]);
             float o = 0.f;
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                const float zr = zv[q] * mzr[r];
+                const float zr = z * mzr[r];
                 o += mdr[r] * zr * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-zr * kLog2e)) * yacc[q * R + r];
             }
             if (st < T) a.y_out[((int64_t)b * T + st) * a.H * a.P + hp + pe] = (bf16)o;
@@ -422,7 +452,7 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
                                    (f16)(hacc[j][2] * kHScale), (f16)(hacc[j][3] * kHScale)};
             *reinterpret_cast<f16x4*>(&sm.H[16 * ptj + l16][16 * nt + 4 * g16]) = hv;
         }
-        if (wave == kTokWave && k + 1 < nchunks) prep_tokens(k + 1);
+        if (angle_wave && k + 1 < nchunks) prep_tokens(k + 1);
         __syncthreads();
     }
 
@@ -436,13 +466,8 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
             *reinterpret_cast<f32x4*>(a.h_final + ((int64_t)bh * a.P + p) * N + 16 * nt + 4 * g16) = hacc[j];
         }
     }
-    if (a.angle && pblk == 0 && wave == kTokWave) {
-#pragma unroll
-        for (int j = 0; j < PPL; ++j) {
-            const int i = lane + 64 * j;
-            if (i < NH) a.angle[(int64_t)bh * NH + i] = a.cplx ? phi_run[j] : 0.f;
-        }
-    }
+    if (a.angle && pblk == 0 && angle_wave && ai < NH)
+        a.angle[(int64_t)bh * NH + ai] = a.cplx ? phi_run : 0.f;
     // prev_BX = sum_r B~_{T-1}[n][r] X_{T-1}[p][r] (mamba3/mamba3.py:247-250) from the last
     // chunk's tiles.
     if (a.prev_bx) {
