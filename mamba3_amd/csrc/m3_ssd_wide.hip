@@ -52,6 +52,12 @@ struct Tok {
     float dec;       // exp2(c2_end): chunk decay of the state
 };
 
+// The R ranks of one token's X row, stored together.
+template <int R>
+struct __align__(2 * R) XRow {
+    f16 v[R];
+};
+
 template <int N, int R>
 struct __align__(16) Smem {
     static constexpr int Q = ROWS / R;
@@ -64,6 +70,7 @@ struct __align__(16) Smem {
     // Written for chunk k+1 in the output phase of chunk k, after every read of chunk k.
     Tok tok;
     float phi[Q][N / 2];  // RoPE angle of each (token, pair)
+    u32x4 th[Q][N / 16];  // theta of the next chunk, bf16, 8 pairs per entry
 };
 
 struct Args {
@@ -165,6 +172,16 @@ __device__ __forceinline__ unsigned rotate_pair(unsigned word, f16x2 kA, f16x2 k
     return bits(f16x2{v[0], v[0]} * kA + f16x2{-u[0], u[1]});
 }
 
+// 8 consecutive bf16 (raw bits): one 128-bit load when the address is 16-byte aligned.
+__device__ __forceinline__ u32x4 load8(const bf16* p, bool vec) {
+    if (vec) return *reinterpret_cast<const u32x4*>(p);
+    const unsigned short* q = reinterpret_cast<const unsigned short*>(p);
+    u32x4 v;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = (unsigned)q[2 * j] | ((unsigned)q[2 * j + 1] << 16);
+    return v;
+}
+
 template <int N, int R>
 __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
     constexpr int Q = ROWS / R;    // tokens per chunk
@@ -203,11 +220,20 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
         mzr[r] = a.prm.mimo_z[(int64_t)(hp + pe) * R + r];
         mdr[r] = a.prm.mimo_down[(int64_t)(hp + pe) * R + r];
     }
-    // X preparation job: column xp, rows 4 xj .. 4 xj + 3.
-    const int xp = tid & (PB - 1), xj = tid / PB;
-    float mxr[4];
+    // X preparation job (threads below XU): token xt, columns 8 xg .. 8 xg + 7.
+    constexpr int XU = Q * PB / 8;
+    const bool x_job = tid < XU;
+    const int xt = tid / (PB / 8), xg = tid % (PB / 8);
+    float mxr[8][R];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) mxr[q] = a.prm.mimo_x[(int64_t)(hp + p0 + xp) * R + (4 * xj + q) % R];
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int r = 0; r < R; ++r) mxr[j][r] = a.prm.mimo_x[(int64_t)(hp + p0 + 8 * xg + j) * R + r];
+    const bool xvec = a.rs % 8 == 0 && a.pl.x % 8 == 0;
+    // theta staging jobs: units of 8 pairs of one token.
+    constexpr int THU = Q * NH / 8;
+    constexpr int THJ = (THU + THREADS - 1) / THREADS;
+    const bool thvec = a.rs % 8 == 0 && a.pl.theta % 8 == 0;
 
     // ---- per-chunk inputs, loaded into registers one phase before they are used ----
     // Rotation jobs: this thread's RoPE pair ri at tokens rt0 + m * TSTEP (m < J).
@@ -224,24 +250,44 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
             load_pair_words<R>(Cn + off, pwc[m]);
         }
     };
-    // X job tokens: raw bf16 bits of x for rows 4 xj + q.
-    unsigned pxv[4];
+    // x of the X job (8 columns, raw bf16) and theta of the staging jobs.
+    u32x4 pxv, pth[THJ];
     auto load_x = [&](int kk) {
+        if (x_job) {
+            const int st = min(kk * Q + xt, T - 1);
+            pxv = load8(proj + (int64_t)st * rs + a.pl.x + hp + p0 + 8 * xg, xvec);
+        }
+        if (a.cplx) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int st = min(kk * Q + (4 * xj + q) / R, T - 1);
-            pxv[q] = *reinterpret_cast<const unsigned short*>(proj + (int64_t)st * rs + a.pl.x + hp + p0 + xp);
+            for (int m = 0; m < THJ; ++m) {
+                const int u = tid + m * THREADS;
+                if (u < THU) {
+                    const int st = min(kk * Q + u / (NH / 8), T - 1);
+                    pth[m] = load8(proj + (int64_t)st * rs + a.pl.theta + 8 * (u % (NH / 8)), thvec);
+                }
+            }
         }
     };
-    // Token scalars and RoPE angles: waves 0 .. NWA-1, lane t = token t of the chunk for
-    // the scalars and pair 64 wave + lane for the angles.
+    auto store_theta = [&]() {
+        if (a.cplx) {
+#pragma unroll
+            for (int m = 0; m < THJ; ++m) {
+                const int u = tid + m * THREADS;
+                if (u < THU) sm.th[u / (NH / 8)][u % (NH / 8)] = pth[m];
+            }
+        }
+    };
+    // Token scalars and RoPE angles: lane t = token t of the chunk for the scalars and
+    // pair ai for the angles.
+    // Waves 2 .. 2+NWA-1 (waves 0 and 1 carry two score tiles each).
     constexpr int NWA = (NH + 63) / 64;
-    const bool angle_wave = wave < NWA;
-    const int ai = 64 * wave + lane;  // this lane's RoPE pair in an angle wave
+    const bool angle_wave = wave >= 2 && wave < 2 + NWA;
+    const int ai = 64 * (wave - 2) + lane;  // this lane's RoPE pair in an angle wave
     float phi_run = 0.f;
-    unsigned rdt0, rlam0, rdt1, rlam1, thr[Q];
-    float sc0, sc1;
+    unsigned rdt0 = 0, rlam0 = 0, rdt1 = 0, rlam1 = 0;
+    float sc0 = 1.f, sc1 = 1.f;
     auto load_tokens = [&](int kk) {
+        if (lane > Q) return;
         const int s0 = kk * Q;
         const int st0 = min(s0 + lane, T - 1), st1 = min(s0 + lane + 1, T - 1);
         const bf16* row0 = proj + (int64_t)st0 * rs;
@@ -252,13 +298,6 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
         rlam1 = a.trap ? *reinterpret_cast<const unsigned short*>(row1 + a.pl.lam + h) : 0u;
         sc0 = a.dt_scale ? a.dt_scale[((int64_t)b * T + st0) * a.H + h] : 1.f;
         sc1 = a.dt_scale ? a.dt_scale[((int64_t)b * T + st1) * a.H + h] : 1.f;
-        if (a.cplx) {
-            const int i = min(ai, NH - 1);
-#pragma unroll
-            for (int q = 0; q < Q; ++q)
-                thr[q] = *reinterpret_cast<const unsigned short*>(
-                    proj + (int64_t)min(s0 + q, T - 1) * rs + a.pl.theta + i);
-        }
     };
     auto bf = [](unsigned u) { return __builtin_bit_cast(float, u << 16); };
     auto prep_tokens = [&](int kk) {
@@ -266,13 +305,13 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
         const int t = lane;
         const bool v0 = t < Q && s0 + t < T, v1 = t < Q && s0 + t + 1 < T;
         // mamba3/mamba3.py:200-204, 212-216
-        const float dt_t = v0 ? softplus_f(bf(rdt0) + dtb) * sc0 : 0.f;
-        const float dt_n = v1 ? softplus_f(bf(rdt1) + dtb) * sc1 : 0.f;
-        const float lam_t = v0 && a.trap ? sigmoid_f(bf(rlam0)) : 1.f;
-        const float lam_n = v1 && a.trap ? sigmoid_f(bf(rlam1)) : 1.f;
+        const float dt_t = v0 ? fast_softplus(bf(rdt0) + dtb) * sc0 : 0.f;
+        const float dt_n = v1 ? fast_softplus(bf(rdt1) + dtb) * sc1 : 0.f;
+        const float lam_t = v0 && a.trap ? __builtin_amdgcn_rcpf(1.f + fast_exp(-bf(rlam0))) : 1.f;
+        const float lam_n = v1 && a.trap ? __builtin_amdgcn_rcpf(1.f + fast_exp(-bf(rlam1))) : 1.f;
         const float c2 = wave_incl_scan(Ah * dt_t * kLog2e);
         const float c2_end = readlane(c2, Q - 1);
-        if (wave == 0) {
+        if (wave == 2) {
             const float av = a.trap ? lam_t * dt_t : dt_t;
             const float bv = a.trap ? (1.f - lam_n) * dt_n : 0.f;
             Tok& tk = sm.tok;
@@ -288,9 +327,10 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
         if (a.cplx && ai < NH) {
             // phi_t[i] = phi_{t-1}[i] - dt_t theta_t[i] (mamba3/mamba3.py:160-162)
             float ph = phi_run;
+            const unsigned short* thq = reinterpret_cast<const unsigned short*>(&sm.th[0][0]) + ai;
 #pragma unroll
             for (int q = 0; q < Q; ++q) {
-                ph -= readlane(dt_t, q) * bf(thr[q]);
+                ph -= readlane(dt_t, q) * bf(thq[q * NH]);
                 sm.phi[q][ai] = ph;
             }
             phi_run = ph;
@@ -305,10 +345,10 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
         reinterpret_cast<unsigned*>(&sm.H[0][0])[idx] = 0u;
     load_bc(0);
     load_x(0);
-    if (angle_wave) {
-        load_tokens(0);
-        prep_tokens(0);
-    }
+    store_theta();
+    if (angle_wave) load_tokens(0);
+    __syncthreads();
+    if (angle_wave) prep_tokens(0);
     __syncthreads();
 
     for (int k = 0; k < nchunks; ++k) {
@@ -333,21 +373,28 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
                 *reinterpret_cast<unsigned*>(&sm.C[t * R + r][2 * ri]) = valid ? rotate_pair(pwc[m][r], kA, kS) : 0u;
             }
         }
-        {
-            f16x4 xv, xw;
+        if (x_job) {
+            // X rows (xt, r) = x * mimo_x[p, r] (mamba3/mamba3.py:210), and times w_xt.
+            const bool valid = s0 + xt < T;
+            const float w = tk.w[xt];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int t = (4 * xj + q) / R;
-                const float X = s0 + t < T ? bf(pxv[q]) * mxr[q] : 0.f;
-                xv[q] = (f16)X;
-                xw[q] = (f16)(X * tk.w[t]);
+            for (int j = 0; j < 8; ++j) {
+                const unsigned u = pxv[j >> 1];
+                const float xval = valid ? bf((j & 1) ? (u >> 16) : (u & 0xffffu)) : 0.f;
+                XRow<R> xv, xw;
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    xv.v[r] = (f16)(xval * mxr[j][r]);
+                    xw.v[r] = (f16)(xval * mxr[j][r] * w);
+                }
+                *reinterpret_cast<XRow<R>*>(&sm.XT[8 * xg + j][xt * R]) = xv;
+                *reinterpret_cast<XRow<R>*>(&sm.XwT[8 * xg + j][xt * R]) = xw;
             }
-            *reinterpret_cast<f16x4*>(&sm.XT[xp][4 * xj]) = xv;
-            *reinterpret_cast<f16x4*>(&sm.XwT[xp][4 * xj]) = xw;
         }
         if (k + 1 < nchunks) {
             load_bc(k + 1);
             load_x(k + 1);
+            if (angle_wave) load_tokens(k + 1);
         }
         __syncthreads();
 
@@ -358,7 +405,6 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
             const int st = min(s0 + (16 * tt + 4 * g16) / R + q, T - 1);
             zr_bits[q] = *reinterpret_cast<const unsigned short*>(proj + (int64_t)st * rs + a.pl.z + hp + pe);
         }
-        if (angle_wave && k + 1 < nchunks) load_tokens(k + 1);
         {
             const float dec = tk.dec;
 #pragma unroll
@@ -424,6 +470,7 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
             for (int ti = 0; ti < 4; ti += 2)
                 *reinterpret_cast<f16x4*>(&sm.S[16 * ti + l16][16 * (ti + 1) + 4 * g16]) = f16x4{0, 0, 0, 0};
         }
+        if (k + 1 < nchunks) store_theta();
         __syncthreads();
 
         // ---- output: G2, gate, store; state copy; next chunk's token scalars ----
