@@ -11,6 +11,16 @@ Workload (one "step" = one pass of the hot path over one batch of synthetic inpu
   decode   the same layer at batch 64: state filled by prefilling 512 N(0,1) tokens, then
            `step` calls on (64, 768) N(0,1) tokens.
 
+Other workloads (`--workload`; the default is `prefill_d768` above), one JSON line each in
+the same format:
+  prefill_d2048   KulaMamba(d_model=2048, d_state=256, headdim=128, mimo_rank=4), bf16,
+                  x (2, 16384, 2048) from seed 6: SSD prefill tokens/s of the native core.
+  layer_fp32_d768 the d_model 768 layer in fp32, x (4, 1024, 768) from seed 1 (weights from
+                  seed 0): whole-layer forward tokens/s (fp32 arithmetic throughout).
+  lm_d768         KulaMambaLM(vocab 32000, d_model 768, 24 layers, d_state 128, headdim 64,
+                  mimo_rank 2, residual_scale 'depth'), bf16, ids (4, 2048) from seed 5:
+                  prefill tokens/s, then 256 greedy decode steps (decode tokens/s).
+
 Prints ONE JSON line. `value` is SSD prefill tokens/s; `roofline` is the fused SSD kernel
 against the bf16 MFMA peak with the algorithmic FLOP count
   F = B*T*H*(2(Q+1)R^2(N+P) + 6RPN), Q = 64;
@@ -34,6 +44,7 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "SSD prefill tokens/s at d768 T=8192 bf16; step-decode tok/s at B=64; %roofline"
 PEAK_BF16_TFLOPS = 2500.0
+PEAK_FP32_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
 
 D_MODEL, N, P, R, EXPAND, Q = 768, 128, 64, 2, 2, 64
@@ -41,8 +52,9 @@ BATCH, SEQLEN = 8, 8192
 DEC_BATCH, DEC_PREFILL = 64, 512
 
 
-def ssd_flops(B, T, H):
-    return B * T * H * (2 * (Q + 1) * R * R * (N + P) + 6 * R * P * N)
+def ssd_flops(B, T, H, n=N, p=P, r=R):
+    """Algorithmic FLOPs of the SSD core: per token and head 2(Q+1)R^2(N+P) + 6RPN, Q=64."""
+    return B * T * H * (2 * (Q + 1) * r * r * (n + p) + 6 * r * p * n)
 
 
 def step_bytes(B, H, d_in_proj, d_inner):
@@ -52,17 +64,182 @@ def step_bytes(B, H, d_in_proj, d_inner):
 TRAFFIC_FILE = ROOT / "profiles" / "pmc_traffic_d768.md"
 
 
-def recorded_traffic():
+def recorded_traffic(path=TRAFFIC_FILE, keys=("prefill", "step")):
     """HBM bytes per call measured with rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE, scaled by
-    a 256 MiB copy), as recorded in the profiles summary: {'prefill': B, 'step': B}."""
+    a 256 MiB copy), as recorded in a profiles summary: {'prefill': B, 'step': B}."""
     out = {}
-    if TRAFFIC_FILE.exists():
-        for line in TRAFFIC_FILE.read_text().splitlines():
-            for key in ("prefill", "step"):
+    if path.exists():
+        for line in path.read_text().splitlines():
+            for key in keys:
                 tag = f"traffic_bytes_{key}:"
                 if line.strip().startswith(tag):
                     out[key] = int(line.split(":", 1)[1].strip())
     return out
+
+
+def calibration_copy(torch, dev):
+    """One 256 MiB device-to-device copy: the known-size kernel that scales FETCH_SIZE and
+    WRITE_SIZE in rocprofv3 --pmc runs."""
+    src = torch.ones(128 << 20, dtype=torch.bfloat16, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return ""
+
+
+def base_result(args, value, ms_per_step, workload, batch, seq_len, dtype="bf16"):
+    return {
+        "metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": dtype,
+        "data": "synthetic: N(0,1) inputs / uniform ids, seeded random init weights",
+        "config": {"workload": workload, "global_batch": batch, "seq_len": seq_len,
+                   "parallelism": "single GPU"},
+    }
+
+
+def bench_prefill_d2048(args, torch, mamba3_amd):
+    """x (2, 16384, 2048) bf16 through the d_model 2048 layer's native SSD core."""
+    dev = torch.device("cuda:0")
+    kw = dict(d_state=256, expand=2, headdim=128, mimo_rank=4)
+    torch.manual_seed(0)
+    layer_cpu = mamba3_amd.KulaMamba(2048, **kw)
+    layer = layer_cpu.to(dev, torch.bfloat16).eval()
+    torch.manual_seed(6)
+    x_cpu = torch.randn(2, 16384, 2048).to(torch.bfloat16)
+    with torch.no_grad():
+        proj = layer.in_proj(x_cpu.to(dev)).contiguous()
+        wall, kern_ms = time_events(torch, lambda: layer.ssd_from_proj(proj, return_state=True),
+                                    args.steps, args.warmup)
+    ms = wall * 1e3 / args.steps
+    tokens = 2 * 16384
+    flops = ssd_flops(2, 16384, layer.nheads, 256, 128, 4)
+    tf = flops / (kern_ms * 1e-3) / 1e12
+    traffic = recorded_traffic(ROOT / "profiles" / "pmc_traffic_d2048.md", ("prefill",))
+    res = base_result(args, tokens / (ms * 1e-3), ms,
+                      "KulaMamba SSD prefill, d_model 2048, d_state 256, headdim 128, 32 heads, "
+                      "mimo_rank 4, x (2, 16384, 2048) bf16, in_proj output resident in HBM",
+                      2, 16384)
+    res["roofline"] = {"bound": "mfma", "achieved": round(tf, 2), "peak": PEAK_BF16_TFLOPS,
+                       "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4),
+                       "traffic": traffic.get("prefill"),
+                       "kernel": "native SSD prefill (all launches of m3_prefill_fwd)",
+                       "algorithmic_flops": flops, "avg_ms": round(kern_ms, 4)}
+    if not args.no_cpu_baseline:
+        from oracle import reference_path as ref
+        cores = len(os.sched_getaffinity(0))
+        torch.set_num_threads(cores)
+        cfg = ref.LayerCfg(d_model=2048, **kw)
+        p = {k: v.detach().cpu().to(torch.bfloat16) for k, v in layer_cpu.state_dict().items()}
+        with torch.no_grad():
+            t0 = time.perf_counter()
+            pr = torch.nn.functional.linear(x_cpu[:1, :512], p["in_proj.weight"])
+            ref.layer_core(cfg, p, pr)
+            dt = time.perf_counter() - t0
+        res["cpu_baseline"] = {"value": round(512 / dt, 1), "unit": "tokens/s", "cores": cores,
+                               "kind": "port", "cpu_model": cpu_model(),
+                               "sample": "oracle layer core (reference algorithm) in bf16 on "
+                                         "x[0, :512] of the (2,16384,2048) workload, in_proj "
+                                         "included"}
+    return res
+
+
+def bench_layer_fp32_d768(args, torch, mamba3_amd):
+    """KulaMamba(768) fp32 forward on x (4, 1024, 768): the layer's fp32 reference config."""
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    layer_cpu = mamba3_amd.KulaMamba(D_MODEL, d_state=N, expand=EXPAND, headdim=P, mimo_rank=R)
+    layer = layer_cpu.to(dev).eval()
+    torch.manual_seed(1)
+    x_cpu = torch.randn(4, 1024, D_MODEL)
+    x = x_cpu.to(dev)
+    with torch.no_grad():
+        proj = layer.in_proj(x).contiguous()
+        _, core_ms = time_events(torch, lambda: layer.ssd_from_proj(proj), args.steps, args.warmup)
+        wall, layer_ms = time_events(torch, lambda: layer(x), args.steps, args.warmup)
+    ms = wall * 1e3 / args.steps
+    tokens = 4 * 1024
+    flops = ssd_flops(4, 1024, layer.nheads)
+    tf = flops / (core_ms * 1e-3) / 1e12
+    res = base_result(args, tokens / (ms * 1e-3), ms,
+                      "KulaMamba forward (whole layer), d_model 768, fp32, x (4, 1024, 768)",
+                      4, 1024, dtype="fp32")
+    res["roofline"] = {"bound": "valu-fp32", "achieved": round(tf, 3), "peak": PEAK_FP32_TFLOPS,
+                       "unit": "TFLOP/s", "frac": round(tf / PEAK_FP32_TFLOPS, 4),
+                       "traffic": None, "kernel": "native fp32 SSD core (generic kernel)",
+                       "algorithmic_flops": flops, "avg_ms": round(core_ms, 4)}
+    if not args.no_cpu_baseline:
+        from oracle import reference_path as ref
+        cores = len(os.sched_getaffinity(0))
+        torch.set_num_threads(cores)
+        cfg = ref.LayerCfg(d_model=D_MODEL, d_state=N, headdim=P, mimo_rank=R)
+        p = {k: v.detach().cpu() for k, v in layer_cpu.state_dict().items()}
+        with torch.no_grad():
+            t0 = time.perf_counter()
+            ref.layer_forward(cfg, p, x_cpu[:2])
+            dt = time.perf_counter() - t0
+        res["cpu_baseline"] = {"value": round(2048 / dt, 1), "unit": "tokens/s", "cores": cores,
+                               "kind": "port", "cpu_model": cpu_model(),
+                               "sample": "oracle layer forward (reference algorithm) in fp32 on "
+                                         "x[:2] of the (4,1024,768) input"}
+    return res
+
+
+def bench_lm_d768(args, torch, mamba3_amd):
+    """KulaMambaLM (24 layers, d_model 768) bf16: prefill of ids (4, 2048), then 256 greedy
+    decode steps."""
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    lm = mamba3_amd.KulaMambaLM(32000, D_MODEL, n_layers=24, d_state=N, headdim=P, mimo_rank=R,
+                                residual_scale="depth").to(dev, torch.bfloat16).eval()
+    torch.manual_seed(5)
+    ids = torch.randint(0, 32000, (4, 2048)).to(dev)
+    new = 256
+    with torch.no_grad():
+        wall, pre_ms = time_events(torch, lambda: lm(ids), args.steps, args.warmup)
+        def gen(n):  # second call timed
+            for _ in range(2):
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                lm.generate(ids, max_new_tokens=n, temperature=0)
+                torch.cuda.synchronize()
+            return (time.perf_counter() - t0) * 1e3
+
+        gen0_ms = gen(0)  # prefill with state, last-position logits
+        gen_ms = gen(new)
+        # the native SSD core of one layer on the same shape, for the roofline
+        layer = lm.layers[0].ssm
+        proj = layer.in_proj(lm.embedding(ids)).contiguous()
+        _, core_ms = time_events(torch, lambda: layer.ssd_from_proj(proj), args.steps, args.warmup)
+    ms = wall * 1e3 / args.steps
+    tokens = 4 * 2048
+    decode_s = max(gen_ms - gen0_ms, 1e-6) * 1e-3
+    flops = ssd_flops(4, 2048, layer.nheads)
+    tf = flops / (core_ms * 1e-3) / 1e12
+    res = base_result(args, tokens / (ms * 1e-3), ms,
+                      "KulaMambaLM prefill (logits), vocab 32000, d_model 768, 24 layers, "
+                      "ids (4, 2048) bf16; then 256 greedy decode steps", 4, 2048)
+    res["decode_tok_s"] = round(4 * new / decode_s, 1)
+    res["generate_ms"] = round(gen_ms, 2)
+    res["roofline"] = {"bound": "mfma", "achieved": round(tf, 2), "peak": PEAK_BF16_TFLOPS,
+                       "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                       "kernel": "native SSD prefill of one layer at (4, 2048)",
+                       "algorithmic_flops": flops, "avg_ms": round(core_ms, 4)}
+    return res
+
+
+WORKLOADS = {"prefill_d2048": bench_prefill_d2048, "layer_fp32_d768": bench_layer_fp32_d768,
+             "lm_d768": bench_lm_d768}
 
 
 def time_events(torch, fn, steps, warmup):
@@ -134,6 +311,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--decode-steps", type=int, default=200)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--workload", default="prefill_d768",
+                    choices=["prefill_d768", *WORKLOADS],
+                    help="prefill_d768 (default: the (8, 8192, 768) prefill and B=64 decode)")
     ap.add_argument("--calibration-copy", action="store_true",
                     help="also run one 256 MiB device-to-device copy (the known-size kernel that "
                          "scales FETCH_SIZE / WRITE_SIZE in rocprofv3 --pmc runs)")
@@ -151,6 +331,12 @@ def main() -> int:
         return 2
     dev = torch.device("cuda:0")
     torch.backends.cuda.matmul.allow_tf32 = False
+    if args.workload in WORKLOADS:
+        res = WORKLOADS[args.workload](args, torch, mamba3_amd)
+        if args.calibration_copy:
+            calibration_copy(torch, dev)
+        print(json.dumps(res))
+        return 0
 
     torch.manual_seed(0)
     layer_cpu = mamba3_amd.KulaMamba(D_MODEL, d_state=N, expand=EXPAND, headdim=P, mimo_rank=R)
@@ -196,11 +382,7 @@ def main() -> int:
             args.decode_steps, 10)
 
         if args.calibration_copy:
-            src = torch.ones(128 << 20, dtype=torch.bfloat16, device=dev)
-            dst = torch.empty_like(src)
-            dst.copy_(src)
-            torch.cuda.synchronize()
-            del src, dst
+            calibration_copy(torch, dev)
 
     traffic = recorded_traffic()
     tokens = BATCH * SEQLEN
