@@ -177,6 +177,10 @@ class KulaMambaLM(nn.Module):
             result["loss"] = F.cross_entropy(pred.view(-1, pred.size(-1)), tgt.view(-1))
         return result
 
+    # Replay the per-token decode step (embedding, every block's step, norm, lm_head) as one
+    # captured HIP graph instead of launching each op from Python. Sampling stays eager.
+    decode_graph: bool = True
+
     @torch.no_grad()
     def generate(self, input_ids: torch.Tensor, max_new_tokens: int = 100,
                  temperature: float = 1.0, top_k: int | None = None) -> torch.Tensor:
@@ -189,6 +193,9 @@ class KulaMambaLM(nn.Module):
             states.append(st)
         logits = self.lm_head(self.norm(x)[:, -1])
         out = [input_ids]
+        graph = None
+        if self.decode_graph and max_new_tokens > 1 and input_ids.is_cuda:
+            graph = _DecodeGraph(self, states, input_ids.shape[0])
         for _ in range(max_new_tokens):
             scores = logits / temperature if temperature > 0 else logits
             if top_k is not None:
@@ -199,8 +206,54 @@ class KulaMambaLM(nn.Module):
             else:
                 nxt = scores.argmax(dim=-1, keepdim=True)
             out.append(nxt)
+            if graph is not None:
+                logits = graph(nxt.squeeze(1))
+                continue
             x = self.embedding(nxt.squeeze(1))
             for i, layer in enumerate(self.layers):
                 x, states[i] = layer.step(x, states[i])
             logits = self.lm_head(self.norm(x))
         return torch.cat(out, dim=1)
+
+
+class _DecodeGraph:
+    """One decode step of a KulaMambaLM captured as a HIP graph (torch.cuda.CUDAGraph):
+    token ids -> embedding -> every block's step -> norm -> lm_head logits. The decode
+    state lives in static buffers: each layer's step writes a new state (out of place, as
+    KulaMamba.step does) and the graph copies it back into the buffers it reads, so every
+    replay advances the state by one token. Outputs are bitwise those of the eager step
+    (same kernels, same order)."""
+
+    def __init__(self, lm: KulaMambaLM, states: list, batch: int):
+        dev = lm.embedding.weight.device
+        self.tok = torch.zeros(batch, dtype=torch.long, device=dev)
+        self.states = [{k: v.clone() for k, v in st.items()} for st in states]
+        snapshot = [{k: v.clone() for k, v in st.items()} for st in self.states]
+
+        def step():
+            x = lm.embedding(self.tok)
+            for i, layer in enumerate(lm.layers):
+                x, new = layer.step(x, self.states[i])
+                for k in ("h", "prev_BX", "angle"):
+                    self.states[i][k].copy_(new[k])
+            return lm.lm_head(lm.norm(x))
+
+        # Warm up outside the capture on a side stream (allocator and library handles),
+        # then restore the state the warm-up advanced.
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            step()
+        torch.cuda.current_stream(dev).wait_stream(side)
+        for st, sv in zip(self.states, snapshot):
+            for k in st:
+                st[k].copy_(sv[k])
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.logits = step()
+        torch.cuda.synchronize(dev)
+
+    def __call__(self, tok: torch.Tensor) -> torch.Tensor:
+        self.tok.copy_(tok)
+        self.graph.replay()
+        return self.logits

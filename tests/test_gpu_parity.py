@@ -140,6 +140,41 @@ def test_tiny_lm_logits_and_greedy_generation_match_reference(cuda_device):
     assert torch.equal(gen.cpu(), torch.from_numpy(g["generated"]))
 
 
+def test_lm_decode_graph_replays_equal_eager_steps(cuda_device):
+    """The captured decode step (HIP graph) against the eager step loop, on a 3-layer
+    d_model-768 LM in bf16: every replay's logits are bitwise the eager logits, with eager
+    work and synchronisations between replays, and greedy generation agrees token for token."""
+    from mamba3_amd.block import _DecodeGraph
+    torch.manual_seed(0)
+    lm = mamba3_amd.KulaMambaLM(32000, 768, n_layers=3, d_state=128, headdim=64,
+                                mimo_rank=2).to(cuda_device, torch.bfloat16).eval()
+    torch.manual_seed(5)
+    ids = torch.randint(0, 32000, (4, 64), device=cuda_device)
+    with torch.no_grad():
+        x = lm.embedding(ids)
+        states = []
+        for layer in lm.layers:
+            x, st = layer.prefill(x)
+            states.append(st)
+        graph = _DecodeGraph(lm, states, 4)
+        g = torch.Generator(device=cuda_device).manual_seed(1)
+        for _ in range(8):
+            tok = torch.randint(0, 32000, (4,), device=cuda_device, generator=g)
+            xe = lm.embedding(tok)
+            for i, layer in enumerate(lm.layers):
+                xe, states[i] = layer.step(xe, states[i])
+            ref_logits = lm.lm_head(lm.norm(xe))
+            torch.cuda.synchronize()
+            out = graph(tok)
+            torch.cuda.synchronize()
+            assert torch.equal(out, ref_logits)
+        lm.decode_graph = False
+        eager = lm.generate(ids, max_new_tokens=16, temperature=0)
+        lm.decode_graph = True
+        graphed = lm.generate(ids, max_new_tokens=16, temperature=0)
+    assert torch.equal(eager, graphed)
+
+
 # ------------------------------------------------------------------ scan
 @pytest.mark.parametrize("shape", [(2, 4, 3, 8), (2, 7, 3, 10), (1, 33, 2, 32768), (8, 16, 24, 8192)])
 @pytest.mark.parametrize("with_init", [True, False])
