@@ -114,7 +114,7 @@ int m3_prefill_fwd(const m3_layer_desc* desc, const m3_layer_params* params, con
                                        prev_bx, workspace, as_stream(stream));
     }
     const size_t need = m3::generic_prefill_workspace(*desc);
-    if (!h_final && (workspace == nullptr || workspace_bytes < need)) return M3_ERR_WORKSPACE;
+    if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return M3_ERR_WORKSPACE;
     if (workspace && !aligned(workspace, 256)) return M3_ERR_MISALIGNED;
     return m3::launch_generic_prefill(*desc, *params, proj, dt_scale, y_out, h_final, angle,
                                       prev_bx, workspace, as_stream(stream));

@@ -1,8 +1,9 @@
 // Generic chunked-SSD forward kernels (fp32 arithmetic, any supported shape and dtype).
 //
-// One workgroup owns one (batch, head) pair and walks the sequence in chunks of
-// `Qi` tokens, carrying the (P,N) fp32 state in a global buffer (L2 resident). Inside a
-// chunk it evaluates the quadratic (L-matrix) form of the SSD
+// One workgroup owns one (batch, head) pair (the layer prefill: one block of headdim
+// columns of it) and walks the sequence in chunks of `Qi` tokens, carrying the fp32 state
+// (in LDS for the layer prefill, in a global buffer for chunked_ssd). Inside a chunk it
+// evaluates the quadratic (L-matrix) form of the SSD
 //
 //   y[t,r,p] = sum_{u<=t} sum_{r'} (C~_t[r] . B~_u[r']) * M[t,u] * X_u[p,r']
 //            + exp(c_t) * C~_t[r] . H[p,:]  + D * x_t[p,r]
@@ -25,8 +26,9 @@
 
 namespace m3 {
 
-constexpr int kGenThreads = 256;
-constexpr int kGenMaxLds = 64 * 1024;
+constexpr int kGenThreads = 1024;  // 16 waves: the loops are latency-bound
+constexpr int kGenMaxLds = 64 * 1024;       // dynamic LDS without a function attribute
+constexpr int kGenMaxLdsBig = 160 * 1024;   // gfx950's LDS per CU
 
 struct GenShape {
     int B, T, H, P, N, R, Rb, G, Qi;
@@ -35,11 +37,12 @@ struct GenShape {
 
 // LDS plan in floats for one workgroup.
 struct GenLds {
-    int tok_dt, tok_lam, c, a, bco, ec, wst, phi_run, ph, rmsB, rmsC, Cs, Bs, Xs, Sc, Ys, total;
+    int tok_dt, tok_lam, c, a, bco, ec, wst, phi_run, ph, rmsB, rmsC, Cs, Bs, Xs, Sc, Ys, Hs, total;
 };
 
+// hs_lds: the (P, N) state lives in LDS with rows padded to N+1 floats.
 __host__ __device__ inline GenLds gen_lds_plan(int Qi, int N, int P, int R, int Rb,
-                                               bool complex_rope) {
+                                               bool complex_rope, bool hs_lds = false) {
     GenLds L;
     int o = 0;
     L.tok_dt = o; o += Qi + 1;
@@ -54,18 +57,21 @@ __host__ __device__ inline GenLds gen_lds_plan(int Qi, int N, int P, int R, int 
     L.rmsB = o; o += Qi;
     L.rmsC = o; o += Qi;
     o = (o + 3) & ~3;
-    L.Cs = o; o += Qi * R * N;
-    L.Bs = o; o += Qi * Rb * N;
+    // C~ / B~ rows padded to N+1 floats: the score loop reads rows j, j+1, ... across lanes.
+    L.Cs = o; o += Qi * R * (N + 1);
+    L.Bs = o; o += Qi * Rb * (N + 1);
     L.Xs = o; o += Qi * Rb * P;  // P = columns of this workgroup
     L.Sc = o; o += Qi * R * Qi * Rb;
     L.Ys = o; o += Qi * R * P;
+    L.Hs = o; o += hs_lds ? P * (N + 1) : 0;
     L.total = o;
     return L;
 }
 
-static int gen_pick_chunk(int N, int P, int R, int Rb, bool complex_rope) {
+static int gen_pick_chunk(int N, int P, int R, int Rb, bool complex_rope, bool hs_lds = false,
+                          int max_lds = kGenMaxLds) {
     for (int q = 64; q >= 1; q >>= 1) {
-        if (gen_lds_plan(q, N, P, R, Rb, complex_rope).total * 4 <= kGenMaxLds) return q;
+        if (gen_lds_plan(q, N, P, R, Rb, complex_rope, hs_lds).total * 4 <= max_lds) return q;
     }
     return 0;
 }
@@ -73,8 +79,9 @@ static int gen_pick_chunk(int N, int P, int R, int Rb, bool complex_rope) {
 // ---------------------------------------------------------------------------------
 // Shared chunk core: scores, outputs, state update. Operates on LDS-staged tiles.
 // ---------------------------------------------------------------------------------
+// Hs: the (P, N) state, row p at Hs + p * hs_ld (LDS or global).
 __device__ void gen_chunk_core(const GenShape& s, const GenLds& L, float* sm, float* __restrict__ Hs,
-                               int nvalid) {
+                               int hs_ld, int nvalid) {
     const int tid = threadIdx.x;
     const int Qi = s.Qi, N = s.N, P = s.Pb, R = s.R, Rb = s.Rb;  // P: this workgroup's columns
     const int rowsC = Qi * R, rowsB = Qi * Rb;
@@ -103,8 +110,8 @@ __device__ void gen_chunk_core(const GenShape& s, const GenLds& L, float* sm, fl
         const int t = i / R, u = j / Rb;
         float v = 0.f;
         if (u <= t) {
-            const float* ci = Cs + i * N;
-            const float* bj = Bs + j * N;
+            const float* ci = Cs + i * (N + 1);
+            const float* bj = Bs + j * (N + 1);
             float dot = 0.f;
             for (int n = 0; n < N; ++n) dot += ci[n] * bj[n];
             const float coef = a[u] + (u < t ? bco[u] : 0.f);
@@ -121,8 +128,8 @@ __device__ void gen_chunk_core(const GenShape& s, const GenLds& L, float* sm, fl
         float acc = 0.f;
         const float* si = Sc + i * rowsB;
         for (int j = 0; j < (t + 1) * Rb; ++j) acc += si[j] * Xs[j * P + p];
-        const float* ci = Cs + i * N;
-        const float* hp = Hs + (size_t)p * N;
+        const float* ci = Cs + i * (N + 1);
+        const float* hp = Hs + (size_t)p * hs_ld;
         float inter = 0.f;
         for (int n = 0; n < N; ++n) inter += ci[n] * hp[n];
         Ys[idx] = acc + ec[t] * inter;
@@ -137,10 +144,10 @@ __device__ void gen_chunk_core(const GenShape& s, const GenLds& L, float* sm, fl
         for (int u = 0; u < nvalid; ++u) {
             const float w = wst[u];
             float bx = 0.f;
-            for (int r = 0; r < Rb; ++r) bx += Xs[(u * Rb + r) * P + p] * Bs[(u * Rb + r) * N + n];
+            for (int r = 0; r < Rb; ++r) bx += Xs[(u * Rb + r) * P + p] * Bs[(u * Rb + r) * (N + 1) + n];
             acc += w * bx;
         }
-        Hs[idx] = d_end * Hs[idx] + acc;
+        Hs[p * hs_ld + n] = d_end * Hs[p * hs_ld + n] + acc;
     }
 }
 
@@ -158,7 +165,7 @@ struct GenLayerArgs {
     const void* proj;
     const float* dt_scale;
     void* y_out;
-    float* state;      // [B,H,P,N] running state (becomes h_final)
+    float* state;      // [B,H,P,N] final state (h_final) or null
     float* angle;      // [B,H,N/2] or null
     float* prev_bx;    // [B,H,P,N] or null
 };
@@ -177,7 +184,7 @@ __global__ __launch_bounds__(kGenThreads) void gen_layer_prefill(GenLayerArgs A)
     const int p0 = pblk * Pb;
     const T* proj = reinterpret_cast<const T*>(A.proj) + (int64_t)b * s.T * A.row_stride;
     T* yo = reinterpret_cast<T*>(A.y_out) + (int64_t)b * s.T * s.H * P;
-    float* Hs = A.state + ((int64_t)b * s.H + h) * P * N + (int64_t)p0 * N;  // this block's rows
+    float* Hs = sm + L.Hs;  // this block's state rows, padded to N+1
     const float Ah = -expf(A.prm.A_log[h]);
     const float Dh = A.prm.D[h];
     const float dtb = A.prm.dt_bias[h];
@@ -189,7 +196,7 @@ __global__ __launch_bounds__(kGenThreads) void gen_layer_prefill(GenLayerArgs A)
     const float* mz = A.prm.mimo_z + (int64_t)h * P * R;
     const float* md = A.prm.mimo_down + (int64_t)h * P * R;
 
-    for (int idx = tid; idx < Pb * N; idx += kGenThreads) Hs[idx] = 0.f;
+    for (int idx = tid; idx < Pb * (N + 1); idx += kGenThreads) Hs[idx] = 0.f;
     for (int i = tid; i < Nh; i += kGenThreads) sm[L.phi_run + i] = 0.f;
     __syncthreads();
 
@@ -288,8 +295,8 @@ __global__ __launch_bounds__(kGenThreads) void gen_layer_prefill(GenLayerArgs A)
                     be = be2; bo = bo2; ce = ce2; co = co2;
                 }
             }
-            float* bs = sm + L.Bs + (t * R + r) * N;
-            float* cs_ = sm + L.Cs + (t * R + r) * N;
+            float* bs = sm + L.Bs + (t * R + r) * (N + 1);
+            float* cs_ = sm + L.Cs + (t * R + r) * (N + 1);
             bs[2 * i] = be;
             bs[2 * i + 1] = bo;
             cs_[2 * i] = ce;
@@ -307,7 +314,7 @@ __global__ __launch_bounds__(kGenThreads) void gen_layer_prefill(GenLayerArgs A)
         }
         __syncthreads();
 
-        gen_chunk_core(s, L, sm, Hs, nvalid);
+        gen_chunk_core(s, L, sm, Hs, N + 1, nvalid);
 
         // Gate and MIMO-down (mamba3/mamba3.py:233-238), this block's columns.
         for (int idx = tid; idx < Qi * Pb; idx += kGenThreads) {
@@ -332,7 +339,7 @@ __global__ __launch_bounds__(kGenThreads) void gen_layer_prefill(GenLayerArgs A)
                 const int pl = idx / N, n = idx % N;
                 float v = 0.f;
                 for (int r = 0; r < R; ++r)
-                    v += sm[L.Bs + (tl * R + r) * N + n] * sm[L.Xs + (tl * R + r) * Pb + pl];
+                    v += sm[L.Bs + (tl * R + r) * (N + 1) + n] * sm[L.Xs + (tl * R + r) * Pb + pl];
                 pb[idx] = v;
             }
         }
@@ -342,11 +349,14 @@ __global__ __launch_bounds__(kGenThreads) void gen_layer_prefill(GenLayerArgs A)
         for (int i = tid; i < Nh; i += kGenThreads)
             A.angle[((int64_t)b * s.H + h) * Nh + i] = A.cplx ? sm[L.phi_run + i] : 0.f;
     }
+    if (A.state) {
+        float* hf = A.state + ((int64_t)b * s.H + h) * P * N + (int64_t)p0 * N;
+        for (int idx = tid; idx < Pb * N; idx += kGenThreads) hf[idx] = Hs[(idx / N) * (N + 1) + idx % N];
+    }
 }
 
-size_t generic_prefill_workspace(const m3_layer_desc& d) {
-    // Running state when the caller does not want h_final.
-    return (size_t)d.batch * d.nheads * d.headdim * d.d_state * sizeof(float);
+size_t generic_prefill_workspace(const m3_layer_desc&) {
+    return 0;  // the running state lives in LDS
 }
 
 int launch_generic_prefill(const m3_layer_desc& d, const m3_layer_params& p, const void* proj,
@@ -361,9 +371,19 @@ int launch_generic_prefill(const m3_layer_desc& d, const m3_layer_params& p, con
     while (A.s.P % (2 * PS) == 0 && A.s.P / (2 * PS) >= 16 && (int64_t)d.batch * d.nheads * 2 * PS <= 256) PS *= 2;
     A.s.PS = PS;
     A.s.Pb = A.s.P / PS;
-    A.s.Qi = gen_pick_chunk(A.s.N, A.s.Pb, A.s.R, A.s.Rb, d.use_complex != 0);
+    // Up to the CU's full LDS (one workgroup per CU): raise the kernel's dynamic-LDS limit.
+    int max_lds = kGenMaxLds;
+    if (d.dtype == M3_DTYPE_BF16)
+        max_lds = hipFuncSetAttribute(reinterpret_cast<const void*>(&gen_layer_prefill<bf16>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, kGenMaxLdsBig) == hipSuccess
+                      ? kGenMaxLdsBig : kGenMaxLds;
+    else
+        max_lds = hipFuncSetAttribute(reinterpret_cast<const void*>(&gen_layer_prefill<float>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, kGenMaxLdsBig) == hipSuccess
+                      ? kGenMaxLdsBig : kGenMaxLds;
+    A.s.Qi = gen_pick_chunk(A.s.N, A.s.Pb, A.s.R, A.s.Rb, d.use_complex != 0, true, max_lds);
     if (A.s.Qi == 0) return M3_ERR_UNSUPPORTED;
-    A.L = gen_lds_plan(A.s.Qi, A.s.N, A.s.Pb, A.s.R, A.s.Rb, d.use_complex != 0);
+    A.L = gen_lds_plan(A.s.Qi, A.s.N, A.s.Pb, A.s.R, A.s.Rb, d.use_complex != 0, true);
     A.pl = proj_layout(d);
     A.row_stride = d.proj_row_stride;
     A.trap = d.use_trapezoidal;
@@ -373,7 +393,7 @@ int launch_generic_prefill(const m3_layer_desc& d, const m3_layer_params& p, con
     A.proj = proj;
     A.dt_scale = dt_scale;
     A.y_out = y_out;
-    A.state = h_final ? h_final : reinterpret_cast<float*>(workspace);
+    A.state = h_final;
     A.angle = angle;
     A.prev_bx = prev_bx;
     const size_t lds = (size_t)A.L.total * sizeof(float);
@@ -435,9 +455,9 @@ __global__ __launch_bounds__(kGenThreads) void gen_chunked(GenChunkedArgs A) {
             const int st = s0 + t;
             const int64_t off = (((int64_t)b * s.T + st) * s.H + h) * N * R + (int64_t)n * R + r;
             const bool v = st < s.T;
-            sm[L.Cs + (t * R + r) * N + n] = v ? ld_f32(Cc + off) : 0.f;
-            sm[L.Bs + (t * Rb + r) * N + n] = v ? ld_f32(Bg + off) : 0.f;
-            if (beta) sm[L.Bs + (t * Rb + R + r) * N + n] = v ? ld_f32(Bb + off) : 0.f;
+            sm[L.Cs + (t * R + r) * (N + 1) + n] = v ? ld_f32(Cc + off) : 0.f;
+            sm[L.Bs + (t * Rb + r) * (N + 1) + n] = v ? ld_f32(Bg + off) : 0.f;
+            if (beta) sm[L.Bs + (t * Rb + R + r) * (N + 1) + n] = v ? ld_f32(Bb + off) : 0.f;
         }
         for (int idx = tid; idx < Qi * R * P; idx += kGenThreads) {
             const int t = idx / (R * P), r = (idx / P) % R, p = idx % P;
@@ -460,7 +480,7 @@ __global__ __launch_bounds__(kGenThreads) void gen_chunked(GenChunkedArgs A) {
         }
         __syncthreads();
 
-        gen_chunk_core(s, L, sm, Hs, nvalid);
+        gen_chunk_core(s, L, sm, Hs, N, nvalid);
         __syncthreads();
 
         for (int idx = tid; idx < Qi * R * P; idx += kGenThreads) {

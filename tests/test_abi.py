@@ -65,8 +65,13 @@ def _desc(**kw):
 
 def test_workspace_query_and_desc_validation(lib):
     n = ctypes.c_size_t(0)
+    # fp32 layers run on the generic kernel, which keeps its state in LDS: no workspace
     assert lib.m3_prefill_workspace_size(ctypes.byref(_desc()), ctypes.byref(n)) == 0
-    assert n.value == 1 * 8 * 16 * 16 * 4
+    assert n.value == 0
+    # bf16 d_state 128 / headdim 64 / rank 2: normalised B^ and C^ in f16, per token
+    d768 = _desc(dtype=1, seqlen=64, nheads=24, headdim=64, d_state=128)
+    assert lib.m3_prefill_workspace_size(ctypes.byref(d768), ctypes.byref(n)) == 0
+    assert n.value >= 2 * 64 * 128 * 2 * 2
     bad = [dict(batch=0), dict(d_state=15), dict(nheads=8, ngroups=3), dict(dtype=7),
            dict(proj_row_stride=10), dict(use_complex=2), dict(rms_eps=float("nan"))]
     for kw in bad:
@@ -81,8 +86,9 @@ def test_prefill_and_step_reject_missing_pointers(lib):
     assert lib.m3_prefill_fwd(ctypes.byref(d), ctypes.byref(params), 256, None, 256, None,
                               None, None, None, 0, None) == 1
     full = _native.LayerParams(*([256] * 10))
-    # no h_final and no workspace
-    assert lib.m3_prefill_fwd(ctypes.byref(d), ctypes.byref(full), 256, None, 256, None,
+    # a bf16 MFMA-path layer without its workspace
+    d768 = _desc(dtype=1, seqlen=64, nheads=24, headdim=64, d_state=128)
+    assert lib.m3_prefill_fwd(ctypes.byref(d768), ctypes.byref(full), 256, None, 256, None,
                               None, None, None, 0, None) == 4
     assert lib.m3_step_fwd(ctypes.byref(d), ctypes.byref(full), 256, None, None, 256, 256, 0,
                            256, 256, 256, 256, None) == 1
