@@ -11,7 +11,8 @@
 //     the work (256 for the d_model 2048 layer at batch 2); the scores and the RoPE
 //     rotation are recomputed by each column block;
 //   * a chunk has 64 (t, r) rows, i.e. Q = 64 / R tokens;
-//   * eight waves (two per SIMD) share every phase: prepare -> contract -> output.
+//   * eight waves (two per SIMD) share both phases of a chunk: contract (and the next
+//     chunk's token scalars and RoPE angles), then output (and the next chunk's tiles).
 //
 // Per chunk, in LDS (f16 unless noted):
 //   C [(t,r)][n], B [(u,r')][n]       C~ / B~: normalised B^ / C^ (bc_norm_wide) rotated
@@ -63,14 +64,13 @@ struct __align__(16) Smem {
     static constexpr int Q = ROWS / R;
     f16 C[ROWS][N + PAD];
     f16 B[ROWS][N + PAD];
-    f16 XT[PB][ROWS + PAD];
+    f16 XT[2][PB][ROWS + PAD];  // by chunk parity: G2 of chunk k reads while chunk k+1's is written
     f16 XwT[PB][ROWS + PAD];
     f16 S[ROWS][ROWS + PAD];
     f16 H[PB][N + PAD];
-    // Written for chunk k+1 in the output phase of chunk k, after every read of chunk k.
-    Tok tok;
-    float phi[Q][N / 2];  // RoPE angle of each (token, pair)
-    u32x4 th[Q][N / 16];  // theta of the next chunk, bf16, 8 pairs per entry
+    Tok tok[2];           // by chunk parity
+    float phi[Q][N / 2];  // RoPE angle of each (token, pair) of the chunk being prepared
+    u32x4 th[Q][N / 16];  // theta of that chunk, bf16, 8 pairs per entry
 };
 
 struct Args {
@@ -235,7 +235,7 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
     constexpr int THJ = (THU + THREADS - 1) / THREADS;
     const bool thvec = a.rs % 8 == 0 && a.pl.theta % 8 == 0;
 
-    // ---- per-chunk inputs, loaded into registers one phase before they are used ----
+    // ---- per-chunk inputs, read into registers at least a phase before they are used ----
     // Rotation jobs: this thread's RoPE pair ri at tokens rt0 + m * TSTEP (m < J).
     constexpr int J = Q * NH / THREADS;
     constexpr int TSTEP = THREADS / NH;
@@ -245,18 +245,20 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
 #pragma unroll
         for (int m = 0; m < J; ++m) {
             const int st = kk * Q + rt0 + m * TSTEP;
-            const int64_t off = (int64_t)min(st, T - 1) * nrs + 2 * ri * R;  // in range; zeroed below
+            const int64_t off = (int64_t)min(st, T - 1) * nrs + 2 * ri * R;  // in range; zeroed when used
             load_pair_words<R>(Bn + off, pwb[m]);
             load_pair_words<R>(Cn + off, pwc[m]);
         }
     };
     // x of the X job (8 columns, raw bf16) and theta of the staging jobs.
     u32x4 pxv, pth[THJ];
-    auto load_x = [&](int kk) {
+    auto load_xv = [&](int kk) {
         if (x_job) {
             const int st = min(kk * Q + xt, T - 1);
             pxv = load8(proj + (int64_t)st * rs + a.pl.x + hp + p0 + 8 * xg, xvec);
         }
+    };
+    auto load_theta = [&](int kk) {
         if (a.cplx) {
 #pragma unroll
             for (int m = 0; m < THJ; ++m) {
@@ -277,12 +279,11 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
             }
         }
     };
-    // Token scalars and RoPE angles: lane t = token t of the chunk for the scalars and
-    // pair ai for the angles.
-    // Waves 2 .. 2+NWA-1 (waves 0 and 1 carry two score tiles each).
+    // Token scalars and RoPE angles (waves 2 .. 2+NWA-1; waves 0 and 1 carry two score
+    // tiles each): lane t = token t of the chunk for the scalars, pair ai for the angles.
     constexpr int NWA = (NH + 63) / 64;
     const bool angle_wave = wave >= 2 && wave < 2 + NWA;
-    const int ai = 64 * (wave - 2) + lane;  // this lane's RoPE pair in an angle wave
+    const int ai = 64 * (wave - 2) + lane;
     float phi_run = 0.f;
     unsigned rdt0 = 0, rlam0 = 0, rdt1 = 0, rlam1 = 0;
     float sc0 = 1.f, sc1 = 1.f;
@@ -300,6 +301,7 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
         sc1 = a.dt_scale ? a.dt_scale[((int64_t)b * T + st1) * a.H + h] : 1.f;
     };
     auto bf = [](unsigned u) { return __builtin_bit_cast(float, u << 16); };
+    // Token scalars of chunk kk into tok[kk & 1], its RoPE angles into phi.
     auto prep_tokens = [&](int kk) {
         const int s0 = kk * Q;
         const int t = lane;
@@ -314,7 +316,7 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
         if (wave == 2) {
             const float av = a.trap ? lam_t * dt_t : dt_t;
             const float bv = a.trap ? (1.f - lam_n) * dt_n : 0.f;
-            Tok& tk = sm.tok;
+            Tok& tk = sm.tok[kk & 1];
             if (t < Q) {
                 tk.c2[t] = c2;
                 tk.av[t] = av;
@@ -336,26 +338,10 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
             phi_run = ph;
         }
     };
-
-    // State tiles of this wave: j -> (n tile, p tile) = ((wave*TPW + j) / 2, (wave*TPW + j) % 2).
-    f32x4 hacc[TPW];
-#pragma unroll
-    for (int j = 0; j < TPW; ++j) hacc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int idx = tid; idx < PB * (N + PAD) / 2; idx += THREADS)
-        reinterpret_cast<unsigned*>(&sm.H[0][0])[idx] = 0u;
-    load_bc(0);
-    load_x(0);
-    store_theta();
-    if (angle_wave) load_tokens(0);
-    __syncthreads();
-    if (angle_wave) prep_tokens(0);
-    __syncthreads();
-
-    for (int k = 0; k < nchunks; ++k) {
-        const int s0 = k * Q;
-        const Tok& tk = sm.tok;
-
-        // ---- prepare: rotated C~ / B~ rows, X rows; then the next chunk's reads ----
+    // Tiles of chunk kk: rotated C~ / B~ rows, X rows into XT[kk & 1] and XwT.
+    auto prep_chunk = [&](int kk) {
+        const int s0 = kk * Q;
+        const Tok& tk = sm.tok[kk & 1];
 #pragma unroll
         for (int m = 0; m < J; ++m) {
             const int t = rt0 + m * TSTEP;
@@ -387,23 +373,57 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
                     xv.v[r] = (f16)(xval * mxr[j][r]);
                     xw.v[r] = (f16)(xval * mxr[j][r] * w);
                 }
-                *reinterpret_cast<XRow<R>*>(&sm.XT[8 * xg + j][xt * R]) = xv;
+                *reinterpret_cast<XRow<R>*>(&sm.XT[kk & 1][8 * xg + j][xt * R]) = xv;
                 *reinterpret_cast<XRow<R>*>(&sm.XwT[8 * xg + j][xt * R]) = xw;
             }
         }
-        if (k + 1 < nchunks) {
-            load_bc(k + 1);
-            load_x(k + 1);
-            if (angle_wave) load_tokens(k + 1);
-        }
-        __syncthreads();
+    };
 
-        // ---- contract: G4, G3, G1 ----
+    // State tiles of this wave: j -> (n tile, p tile) = ((wave*TPW + j) / 2, (wave*TPW + j) % 2).
+    f32x4 hacc[TPW];
+#pragma unroll
+    for (int j = 0; j < TPW; ++j) hacc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int idx = tid; idx < PB * (N + PAD) / 2; idx += THREADS)
+        reinterpret_cast<unsigned*>(&sm.H[0][0])[idx] = 0u;
+    // Prologue: chunk 0's token scalars and tiles; chunk 1's reads and theta.
+    load_bc(0);
+    load_xv(0);
+    load_theta(0);
+    if (angle_wave) load_tokens(0);
+    store_theta();
+    __syncthreads();
+    if (angle_wave) {
+        prep_tokens(0);
+        if (nchunks > 1) load_tokens(1);
+    }
+    if (nchunks > 1) load_theta(1);
+    __syncthreads();
+    prep_chunk(0);
+    if (nchunks > 1) {
+        load_bc(1);
+        load_xv(1);
+        store_theta();
+    }
+    __syncthreads();
+
+    // Per chunk k, two phases:
+    //   contract: G4, G3, G1 of chunk k; token scalars and RoPE angles of chunk k+1
+    //   output:   G2, gate, store of chunk k, its state copy; tiles of chunk k+1
+    for (int k = 0; k < nchunks; ++k) {
+        const int s0 = k * Q;
+        const Tok& tk = sm.tok[k & 1];
+
+        // ---- contract ----
         unsigned zr_bits[TPL];
 #pragma unroll
         for (int q = 0; q < TPL; ++q) {
             const int st = min(s0 + (16 * tt + 4 * g16) / R + q, T - 1);
             zr_bits[q] = *reinterpret_cast<const unsigned short*>(proj + (int64_t)st * rs + a.pl.z + hp + pe);
+        }
+        if (k + 2 < nchunks) load_theta(k + 2);
+        if (angle_wave && k + 1 < nchunks) {
+            prep_tokens(k + 1);
+            if (k + 2 < nchunks) load_tokens(k + 2);
         }
         {
             const float dec = tk.dec;
@@ -470,13 +490,12 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
             for (int ti = 0; ti < 4; ti += 2)
                 *reinterpret_cast<f16x4*>(&sm.S[16 * ti + l16][16 * (ti + 1) + 4 * g16]) = f16x4{0, 0, 0, 0};
         }
-        if (k + 1 < nchunks) store_theta();
         __syncthreads();
 
-        // ---- output: G2, gate, store; state copy; next chunk's token scalars ----
+        // ---- output ----
         for (int s = 0; s <= tt / 2; ++s) {
             const f16x8 A = *reinterpret_cast<const f16x8*>(&sm.S[16 * tt + l16][32 * s + 8 * g16]);
-            const f16x8 Bo = *reinterpret_cast<const f16x8*>(&sm.XT[16 * pt + l16][32 * s + 8 * g16]);
+            const f16x8 Bo = *reinterpret_cast<const f16x8*>(&sm.XT[k & 1][16 * pt + l16][32 * s + 8 * g16]);
             yacc = mfma16(A, Bo, yacc);
         }
 #pragma unroll
@@ -499,7 +518,14 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
                                    (f16)(hacc[j][2] * kHScale), (f16)(hacc[j][3] * kHScale)};
             *reinterpret_cast<f16x4*>(&sm.H[16 * ptj + l16][16 * nt + 4 * g16]) = hv;
         }
-        if (angle_wave && k + 1 < nchunks) prep_tokens(k + 1);
+        if (k + 1 < nchunks) {
+            prep_chunk(k + 1);
+            if (k + 2 < nchunks) {
+                load_bc(k + 2);
+                load_xv(k + 2);
+                store_theta();
+            }
+        }
         __syncthreads();
     }
 
@@ -523,7 +549,7 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
             const int p = idx / N, n = idx % N;
             float v = 0.f;
 #pragma unroll
-            for (int r = 0; r < R; ++r) v += (float)sm.B[tl * R + r][n] * (float)sm.XT[p][tl * R + r];
+            for (int r = 0; r < R; ++r) v += (float)sm.B[tl * R + r][n] * (float)sm.XT[(nchunks - 1) & 1][p][tl * R + r];
             a.prev_bx[((int64_t)bh * a.P + p0 + p) * N + n] = v;
         }
     }
