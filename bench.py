@@ -20,6 +20,9 @@ the same format:
   lm_d768         KulaMambaLM(vocab 32000, d_model 768, 24 layers, d_state 128, headdim 64,
                   mimo_rank 2, residual_scale 'depth'), bf16, ids (4, 2048) from seed 5:
                   prefill tokens/s, then 256 greedy decode steps (decode tokens/s).
+  scan_d768       the inter-chunk state scan (ssd_scan) at the d_model 768 prefill's shape:
+                  decay (8, 128, 24), h_chunk (8, 128, 24, 64*128) and h_init, fp32: GB/s.
+  scan_d2048      the same at the d_model 2048 shape: (2, 256, 32, 128*256).
 
 Prints ONE JSON line. `value` is SSD prefill tokens/s; `roofline` is the fused SSD kernel
 against the bf16 MFMA peak with the algorithmic FLOP count
@@ -238,27 +241,69 @@ def bench_lm_d768(args, torch, mamba3_amd):
     return res
 
 
+def bench_scan(args, torch, shape, name):
+    """m3_scan_fwd on resident fp32 inputs: h[0] = h_init, h[k+1] = d[k] h[k] + h_chunk[k]."""
+    from mamba3_amd import _native
+    dev = torch.device("cuda:0")
+    B, K, H, PN = shape
+    g = torch.Generator().manual_seed(7)
+    decay = (torch.rand(B, K, H, generator=g) * 0.5 + 0.5).to(dev)
+    h_chunk = torch.randn(B, K, H, PN, generator=g).to(dev)
+    h_init = torch.randn(B, H, PN, generator=g).to(dev)
+    out = torch.empty_like(h_chunk)
+    wall, kern_ms = time_events(torch, lambda: _native.scan_fwd(decay, h_chunk, h_init, out),
+                                args.steps, args.warmup)
+    ms = wall * 1e3 / args.steps
+    nbytes = B * K * H * (PN * 8 + 4) + B * H * PN * 4
+    gbs = nbytes / (kern_ms * 1e-3) / 1e9
+    traffic = recorded_traffic(ROOT / "profiles" / "pmc_traffic_scan.md", (name,))
+    res = base_result(args, nbytes / (ms * 1e-3) / 1e9, ms,
+                      f"ssd_scan (m3_scan_fwd), decay ({B}, {K}, {H}), h_chunk ({B}, {K}, {H}, {PN}) "
+                      "and h_init, fp32, resident in HBM", B, K, dtype="fp32")
+    res["unit"] = "GB/s"
+    res["roofline"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                       "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic.get(name),
+                       "kernel": "scan_fwd_vec4", "algorithmic_bytes": nbytes,
+                       "avg_ms": round(kern_ms, 4)}
+    if not args.no_cpu_baseline:
+        from oracle import reference_path as ref
+        cores = len(os.sched_getaffinity(0))
+        torch.set_num_threads(cores)
+        d1, c1, i1 = decay[:1].cpu(), h_chunk[:1].cpu(), h_init[:1].cpu()
+        t0 = time.perf_counter()
+        ref.scan_forward(d1, c1, i1)
+        dt = time.perf_counter() - t0
+        res["cpu_baseline"] = {"value": round(nbytes / B / dt / 1e9, 2), "unit": "GB/s",
+                               "cores": cores, "kind": "port", "cpu_model": cpu_model(),
+                               "sample": "oracle scan (the reference's torch loop) on batch row 0, "
+                                         "same algorithmic bytes per row"}
+    return res
+
+
 WORKLOADS = {"prefill_d2048": bench_prefill_d2048, "layer_fp32_d768": bench_layer_fp32_d768,
-             "lm_d768": bench_lm_d768}
+             "lm_d768": bench_lm_d768,
+             "scan_d768": lambda args, torch, m: bench_scan(args, torch, (8, 128, 24, 8192), "scan_d768"),
+             "scan_d2048": lambda args, torch, m: bench_scan(args, torch, (2, 256, 32, 32768), "scan_d2048")}
 
 
 def time_events(torch, fn, steps, warmup):
-    """Warmup, then `steps` calls bracketed by synchronize; per-call HIP events on the
-    current stream (the stream the native entry points launch on)."""
+    """Warmup, then `steps` calls bracketed by synchronize. Returns (wall seconds, average
+    ms per call from two HIP events on the current stream -- the stream the native entry
+    points launch on -- around the whole timed region, so per-call host gaps are not
+    counted while the launches queue ahead of the GPU)."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
-    for i in range(steps):
-        starts[i].record()
+    start.record()
+    for _ in range(steps):
         fn()
-        ends[i].record()
+    end.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    per = [s.elapsed_time(e) for s, e in zip(starts, ends)]
-    return wall, sum(per) / len(per)
+    return wall, start.elapsed_time(end) / steps
 
 
 def cpu_baseline(torch, layer_sd, x_cpu, dec_inputs):
@@ -367,19 +412,25 @@ def main() -> int:
             st["i"] += 1
 
         _, step_layer_ms = time_events(torch, one_step, args.decode_steps, 10)
-        # Kernel-only decode: the native step on preallocated buffers.
+        # Kernel-only decode: the native step on preallocated buffers, chained through 9
+        # state sets (each step reads the state the previous one wrote to another set;
+        # 9 x 100 MB exceeds the 256 MB last-level cache, as the per-layer states of a
+        # multi-layer model do), so the state traffic is served by HBM.
         dproj = layer.in_proj(dec_x[0]).contiguous()
         s0 = st["s"]
-        h_out = torch.empty_like(s0["h"])
-        p_out = torch.empty_like(s0["prev_BX"])
-        a_out = torch.empty_like(s0["angle"])
+        sets = [(s0["h"].clone(), s0["prev_BX"].clone(), s0["angle"].clone()) for _ in range(9)]
         y_out = torch.empty(DEC_BATCH, layer.d_inner, device=dev, dtype=torch.bfloat16)
         desc = layer._desc(DEC_BATCH, 1, dproj)
         params = layer._param_pack()
-        _, step_kern_ms = time_events(
-            torch, lambda: _native.step_fwd(desc, params, dproj, None, s0["h"], s0["prev_BX"],
-                                            s0["angle"], y_out, h_out, p_out, a_out),
-            args.decode_steps, 10)
+        ks = {"i": 0}
+
+        def kernel_step():
+            i = ks["i"]
+            (hi, pi, ai), (ho, po, ao) = sets[i % 9], sets[(i + 1) % 9]
+            _native.step_fwd(desc, params, dproj, None, hi, pi, ai, y_out, ho, po, ao)
+            ks["i"] = i + 1
+
+        _, step_kern_ms = time_events(torch, kernel_step, args.decode_steps, 10)
 
         if args.calibration_copy:
             calibration_copy(torch, dev)

@@ -6,7 +6,9 @@
 // Design: the recurrence is independent per (b,h,j) column, so every lane owns one
 // float4 column slice and walks k. A wave reads/writes 1 KiB contiguous per k, and the
 // loads of kUnroll consecutive chunks are issued before the dependent FMA chain, so
-// each wave keeps kUnroll x 1 KiB in flight. HBM-bound: B*K*H*PN*8 bytes + decay.
+// each wave keeps kUnroll x 1 KiB in flight. HBM-bound: B*K*H*PN*8 bytes + decay. Every
+// h_chunk element is read once and every state written once, so both go through
+// non-temporal (streaming) loads and stores, which keep them out of the caches' way.
 #include "m3_common.h"
 #include "m3_kernels.h"
 
@@ -39,7 +41,7 @@ __global__ __launch_bounds__(kScanBlock) void scan_fwd_vec4(
 #pragma unroll
         for (int u = 0; u < kScanUnroll; ++u) {
             if (k0 + u < K - 1) {
-                v[u] = h_chunk[base + (int64_t)(k0 + u) * kstride];
+                v[u] = __builtin_nontemporal_load(&h_chunk[base + (int64_t)(k0 + u) * kstride]);
                 d[u] = dptr[(int64_t)(k0 + u) * H];
             }
         }
@@ -47,7 +49,7 @@ __global__ __launch_bounds__(kScanBlock) void scan_fwd_vec4(
         for (int u = 0; u < kScanUnroll; ++u) {
             if (k0 + u < K - 1) {
                 s = d[u] * s + v[u];
-                h_states[base + (int64_t)(k0 + u + 1) * kstride] = s;
+                __builtin_nontemporal_store(s, &h_states[base + (int64_t)(k0 + u + 1) * kstride]);
             }
         }
     }
@@ -70,8 +72,8 @@ __global__ __launch_bounds__(kScanBlock) void scan_fwd_scalar(
     float s = h_init ? h_init[bh * pn + j] : 0.f;
     h_states[base] = s;
     for (int k = 0; k < K - 1; ++k) {
-        s = dptr[(int64_t)k * H] * s + h_chunk[base + (int64_t)k * kstride];
-        h_states[base + (int64_t)(k + 1) * kstride] = s;
+        s = dptr[(int64_t)k * H] * s + __builtin_nontemporal_load(&h_chunk[base + (int64_t)k * kstride]);
+        __builtin_nontemporal_store(s, &h_states[base + (int64_t)(k + 1) * kstride]);
     }
 }
 

@@ -137,8 +137,10 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(StepArgs a) {
         for (int it = 0; it < kStepRowsPerLane; ++it) {
             const int p = pbase + it * kRows;
             if (p < P) {
-                hv[it] = hin[p * n4 + q];
-                pv[it] = pin[p * n4 + q];
+                // streaming reads of the incoming state; the outgoing state is stored
+                // normally so the next step finds it in the caches
+                hv[it] = __builtin_nontemporal_load(&hin[p * n4 + q]);
+                pv[it] = __builtin_nontemporal_load(&pin[p * n4 + q]);
                 xv[it] = ld_f32(pr + a.pl.x + (int64_t)h * P + p);
             }
         }
