@@ -66,6 +66,9 @@ constexpr int THREADS = 1024;  // 8 MFMA waves + 8 helper waves, four per SIMD
 constexpr int NMW = 8;          // waves 0..7 run the MFMA work, 8..15 are helpers
 constexpr int PAD = 8;
 constexpr int kRsrcFlags = 0x00020000;
+// Cache policy of the reads and writes that touch their data once (x, z, y): non-temporal,
+// so they do not evict the normalised B^ / C^ rows that the 24 heads share from L2.
+constexpr int kStream = 2;
 
 
 constexpr int NSLOT = 3;
@@ -685,12 +688,12 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
         auto load_x = [&](int kk) {
             const int lane = opaque(threadIdx.x & 63);
             const int t = 8 * hw + (lane >> 3), p = 8 * (lane & 7);
-            xr = __builtin_amdgcn_raw_buffer_load_b128(rsrc_proj(kk), (t * rs + (int)a.pl.x + h * P + p) * 2, 0, 0);
+            xr = __builtin_amdgcn_raw_buffer_load_b128(rsrc_proj(kk), (t * rs + (int)a.pl.x + h * P + p) * 2, 0, kStream);
         };
         auto load_z = [&](int kk) {
             const int lane = opaque(threadIdx.x & 63);
             const int t = 8 * hw + (lane >> 3), p = 8 * (lane & 7);
-            zr = __builtin_amdgcn_raw_buffer_load_b128(rsrc_proj(kk), (t * rs + (int)a.pl.z + h * P + p) * 2, 0, 0);
+            zr = __builtin_amdgcn_raw_buffer_load_b128(rsrc_proj(kk), (t * rs + (int)a.pl.z + h * P + p) * 2, 0, kStream);
         };
         auto load_th = [&](int kk) {
             const int lane = opaque(threadIdx.x & 63);
@@ -892,7 +895,7 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
             const int HP = a.H * P;
             const __amdgpu_buffer_rsrc_t ry =
                 make_rsrc(a.y_out + ((int64_t)b * T + s0) * HP, (int64_t)max(T - s0, 0) * HP * 2);
-            __builtin_amdgcn_raw_buffer_store_b128(o, ry, (t * HP + h * P + p) * 2, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b128(o, ry, (t * HP + h * P + p) * 2, 0, kStream);
         };
 
         // prologue: first chunk's tiles and gate factors, reads of the second chunk
