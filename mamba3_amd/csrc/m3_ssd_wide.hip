@@ -173,8 +173,13 @@ __device__ __forceinline__ unsigned rotate_pair(unsigned word, f16x2 kA, f16x2 k
 }
 
 // 8 consecutive bf16 (raw bits): one 128-bit load when the address is 16-byte aligned.
+// kStreaming: data read once (x) goes through non-temporal loads.
+template <bool kStreaming = false>
 __device__ __forceinline__ u32x4 load8(const bf16* p, bool vec) {
-    if (vec) return *reinterpret_cast<const u32x4*>(p);
+    if (vec) {
+        const u32x4* q = reinterpret_cast<const u32x4*>(p);
+        return kStreaming ? __builtin_nontemporal_load(q) : *q;
+    }
     const unsigned short* q = reinterpret_cast<const unsigned short*>(p);
     u32x4 v;
 #pragma unroll
@@ -255,7 +260,7 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
     auto load_xv = [&](int kk) {
         if (x_job) {
             const int st = min(kk * Q + xt, T - 1);
-            pxv = load8(proj + (int64_t)st * rs + a.pl.x + hp + p0 + 8 * xg, xvec);
+            pxv = load8<true>(proj + (int64_t)st * rs + a.pl.x + hp + p0 + 8 * xg, xvec);
         }
     };
     auto load_theta = [&](int kk) {
@@ -418,7 +423,7 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
 #pragma unroll
         for (int q = 0; q < TPL; ++q) {
             const int st = min(s0 + (16 * tt + 4 * g16) / R + q, T - 1);
-            zr_bits[q] = *reinterpret_cast<const unsigned short*>(proj + (int64_t)st * rs + a.pl.z + hp + pe);
+            zr_bits[q] = __builtin_nontemporal_load(reinterpret_cast<const unsigned short*>(proj + (int64_t)st * rs + a.pl.z + hp + pe));
         }
         if (k + 2 < nchunks) load_theta(k + 2);
         if (angle_wave && k + 1 < nchunks) {
@@ -508,7 +513,7 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
                 const float zr = z * mzr[r];
                 o += mdr[r] * zr * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-zr * kLog2e)) * yacc[q * R + r];
             }
-            if (st < T) a.y_out[((int64_t)b * T + st) * a.H * a.P + hp + pe] = (bf16)o;
+            if (st < T) __builtin_nontemporal_store((bf16)o, &a.y_out[((int64_t)b * T + st) * a.H * a.P + hp + pe]);
         }
 #pragma unroll
         for (int j = 0; j < TPW; ++j) {
