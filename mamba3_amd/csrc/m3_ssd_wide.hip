@@ -199,8 +199,13 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g16 = lane >> 4, l16 = lane & 15;
-    const int pblk = blockIdx.x % a.PS;
-    const int bh = blockIdx.x / a.PS;
+    // Workgroups go to the 8 XCDs round-robin; renumber them so that consecutive logical
+    // workgroups -- the column blocks and heads of one batch row, which read the same
+    // normalised B^ / C^ rows -- share an XCD and its L2.
+    const int nblk = gridDim.x;
+    const int blk = (nblk % 8 == 0) ? (blockIdx.x % 8) * (nblk / 8) + blockIdx.x / 8 : blockIdx.x;
+    const int pblk = blk % a.PS;
+    const int bh = blk / a.PS;
     const int b = bh / a.H, h = bh % a.H;
     const int grp = h / (a.H / a.G);
     const int p0 = pblk * PB;
