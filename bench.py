@@ -23,6 +23,7 @@ the same format:
   scan_d768       the inter-chunk state scan (ssd_scan) at the d_model 768 prefill's shape:
                   decay (8, 128, 24), h_chunk (8, 128, 24, 64*128) and h_init, fp32: GB/s.
   scan_d2048      the same at the d_model 2048 shape: (2, 256, 32, 128*256).
+  scan_bwd_d768   the scan's backward (m3_scan_bwd) at the scan_d768 shape: GB/s.
 
 Prints ONE JSON line. `value` is SSD prefill tokens/s; `roofline` is the fused SSD kernel
 against the bf16 MFMA peak with the algorithmic FLOP count
@@ -280,10 +281,53 @@ def bench_scan(args, torch, shape, name):
     return res
 
 
+def bench_scan_bwd(args, torch, shape, name):
+    """m3_scan_bwd on resident fp32 inputs (states, incoming gradient), writing d_chunk,
+    d_decay and d_h_init."""
+    from mamba3_amd import _native
+    dev = torch.device("cuda:0")
+    B, K, H, PN = shape
+    g = torch.Generator().manual_seed(8)
+    decay = (torch.rand(B, K, H, generator=g) * 0.5 + 0.5).to(dev)
+    states = torch.randn(B, K, H, PN, generator=g).to(dev)
+    grad = torch.randn(B, K, H, PN, generator=g).to(dev)
+    d_decay = torch.empty_like(decay)
+    d_chunk = torch.empty_like(states)
+    d_init = torch.empty(B, H, PN, device=dev)
+    wall, kern_ms = time_events(
+        torch, lambda: _native.scan_bwd(decay, states, grad, d_decay, d_chunk, d_init),
+        args.steps, args.warmup)
+    ms = wall * 1e3 / args.steps
+    nbytes = B * K * H * (PN * 12 + 8) + B * H * PN * 4
+    gbs = nbytes / (kern_ms * 1e-3) / 1e9
+    res = base_result(args, nbytes / (ms * 1e-3) / 1e9, ms,
+                      f"ssd_scan backward (m3_scan_bwd), states and gradient ({B}, {K}, {H}, {PN}), "
+                      "fp32, resident in HBM", B, K, dtype="fp32")
+    res["unit"] = "GB/s"
+    res["roofline"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                       "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                       "kernel": "scan_bwd_vec4 + scan_bwd_reduce", "algorithmic_bytes": nbytes,
+                       "avg_ms": round(kern_ms, 4)}
+    if not args.no_cpu_baseline:
+        from oracle import reference_path as ref
+        cores = len(os.sched_getaffinity(0))
+        torch.set_num_threads(cores)
+        t0 = time.perf_counter()
+        ref.scan_backward(decay[:1].cpu(), states[:1].cpu(), grad[:1].cpu(), True)
+        dt = time.perf_counter() - t0
+        res["cpu_baseline"] = {"value": round(nbytes / B / dt / 1e9, 2), "unit": "GB/s",
+                               "cores": cores, "kind": "port", "cpu_model": cpu_model(),
+                               "sample": "oracle scan backward (the reference's torch loop) on "
+                                         "batch row 0, same algorithmic bytes per row"}
+    return res
+
+
 WORKLOADS = {"prefill_d2048": bench_prefill_d2048, "layer_fp32_d768": bench_layer_fp32_d768,
              "lm_d768": bench_lm_d768,
              "scan_d768": lambda args, torch, m: bench_scan(args, torch, (8, 128, 24, 8192), "scan_d768"),
-             "scan_d2048": lambda args, torch, m: bench_scan(args, torch, (2, 256, 32, 32768), "scan_d2048")}
+             "scan_d2048": lambda args, torch, m: bench_scan(args, torch, (2, 256, 32, 32768), "scan_d2048"),
+             "scan_bwd_d768": lambda args, torch, m: bench_scan_bwd(args, torch, (8, 128, 24, 8192),
+                                                                    "scan_bwd_d768")}
 
 
 def time_events(torch, fn, steps, warmup):

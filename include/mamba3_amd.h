@@ -93,6 +93,25 @@ int m3_scan_fwd(const float* decay, const float* h_chunk, const float* h_init,
                 int64_t pn, void* stream);
 
 /*
+ * Backward of the inter-chunk state scan. Replaces the reference's native
+ * `scan_backward` (mamba3/csrc/scan.cu:168-211, kernel at scan.cu:52-126, bound at
+ * scan.cu:217-219) and its torch fallback `_scan_backward_torch` (mamba3/scan.py:47-62).
+ * With G[K-1] = grad[K-1] and G[k] = grad[k] + decay[b,k,h] G[k+1]:
+ *     d_chunk[b,k,h,:] = G[k+1] for k < K-1, 0 for k = K-1
+ *     d_decay[b,k,h]   = sum_j G[k+1][j] h_states[b,k,h,j] for k < K-1, 0 for k = K-1
+ *     d_h_init[b,h,:]  = G[0]   (not written when d_h_init is NULL)
+ * decay, d_decay [B,K,H]; h_states, grad, d_chunk [B,K,H,PN]; d_h_init [B,H,PN]; all fp32.
+ * d_decay sums are formed in a fixed order (deterministic). PN must be a multiple of 256
+ * or at most 16384. workspace: m3_scan_bwd_workspace_size() bytes (0 is possible),
+ * 256-byte aligned.
+ */
+int m3_scan_bwd_workspace_size(int64_t batch, int64_t nchunks, int64_t nheads, int64_t pn,
+                               size_t* bytes);
+int m3_scan_bwd(const float* decay, const float* h_states, const float* grad, float* d_decay,
+                float* d_chunk, float* d_h_init, void* workspace, size_t workspace_bytes,
+                int64_t batch, int64_t nchunks, int64_t nheads, int64_t pn, void* stream);
+
+/*
  * Bytes of device workspace m3_prefill_fwd needs for `desc` (0 is possible).
  * No counterpart in the reference, which allocates inside ATen.
  */

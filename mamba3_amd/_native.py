@@ -25,6 +25,8 @@ EXPORTED_SYMBOLS = (
     "m3_status_string",
     "m3_version",
     "m3_scan_fwd",
+    "m3_scan_bwd_workspace_size",
+    "m3_scan_bwd",
     "m3_prefill_workspace_size",
     "m3_prefill_fwd",
     "m3_step_fwd",
@@ -74,6 +76,11 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.m3_version.argtypes = []
     lib.m3_scan_fwd.restype = ctypes.c_int
     lib.m3_scan_fwd.argtypes = [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]
+    lib.m3_scan_bwd_workspace_size.restype = ctypes.c_int
+    lib.m3_scan_bwd_workspace_size.argtypes = [_i64, _i64, _i64, _i64, ctypes.POINTER(ctypes.c_size_t)]
+    lib.m3_scan_bwd.restype = ctypes.c_int
+    lib.m3_scan_bwd.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t,
+                                _i64, _i64, _i64, _i64, _vp]
     lib.m3_prefill_workspace_size.restype = ctypes.c_int
     lib.m3_prefill_workspace_size.argtypes = [ctypes.POINTER(LayerDesc),
                                               ctypes.POINTER(ctypes.c_size_t)]
@@ -139,6 +146,18 @@ def scan_fwd(decay: torch.Tensor, h_chunk: torch.Tensor, h_init: torch.Tensor | 
     B, K, H, PN = h_chunk.shape
     check(lib().m3_scan_fwd(ptr(decay), ptr(h_chunk), ptr(h_init), ptr(out), B, K, H, PN,
                             stream_of(h_chunk)), "m3_scan_fwd")
+
+
+def scan_bwd(decay: torch.Tensor, h_states: torch.Tensor, grad: torch.Tensor,
+             d_decay: torch.Tensor, d_chunk: torch.Tensor, d_h_init: torch.Tensor | None) -> None:
+    """m3_scan_bwd on contiguous fp32 tensors (B,K,H) / (B,K,H,PN) / (B,H,PN)."""
+    B, K, H, PN = h_states.shape
+    n = ctypes.c_size_t(0)
+    check(lib().m3_scan_bwd_workspace_size(B, K, H, PN, ctypes.byref(n)), "m3_scan_bwd_workspace_size")
+    ws = torch.empty(max(n.value, 1), dtype=torch.uint8, device=h_states.device)
+    check(lib().m3_scan_bwd(ptr(decay), ptr(h_states), ptr(grad), ptr(d_decay), ptr(d_chunk),
+                            ptr(d_h_init), ptr(ws), n.value, B, K, H, PN, stream_of(h_states)),
+          "m3_scan_bwd")
 
 
 def prefill_workspace_bytes(desc: LayerDesc) -> int:

@@ -39,6 +39,14 @@ int check_params(const m3_layer_params* p) {
     return M3_OK;
 }
 
+int check_scan_bwd_shape(int64_t batch, int64_t nchunks, int64_t nheads, int64_t pn) {
+    if (batch <= 0 || nchunks <= 0 || nheads <= 0 || pn <= 0) return M3_ERR_INVALID_SHAPE;
+    if (batch * nheads * pn > ((int64_t)1 << 40) || nchunks > (1 << 30)) return M3_ERR_UNSUPPORTED;
+    if (pn % 256 != 0 && pn > 16384) return M3_ERR_UNSUPPORTED;
+    if (batch * nheads > 0x7fffffff) return M3_ERR_UNSUPPORTED;
+    return M3_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -67,6 +75,31 @@ int m3_scan_fwd(const float* decay, const float* h_chunk, const float* h_init,
     if (batch * nheads * pn > ((int64_t)1 << 40)) return M3_ERR_UNSUPPORTED;
     if (nchunks > (1 << 30)) return M3_ERR_UNSUPPORTED;
     return m3::launch_scan_fwd(decay, h_chunk, h_init, h_states, batch, nchunks, nheads, pn,
+                               as_stream(stream)) == 0
+               ? M3_OK
+               : M3_ERR_LAUNCH;
+}
+
+int m3_scan_bwd_workspace_size(int64_t batch, int64_t nchunks, int64_t nheads, int64_t pn,
+                               size_t* bytes) {
+    if (!bytes) return M3_ERR_NULL_POINTER;
+    const int st = check_scan_bwd_shape(batch, nchunks, nheads, pn);
+    if (st != M3_OK) return st;
+    *bytes = m3::scan_bwd_workspace(batch, nchunks, nheads, pn);
+    return M3_OK;
+}
+
+int m3_scan_bwd(const float* decay, const float* h_states, const float* grad, float* d_decay,
+                float* d_chunk, float* d_h_init, void* workspace, size_t workspace_bytes,
+                int64_t batch, int64_t nchunks, int64_t nheads, int64_t pn, void* stream) {
+    if (!decay || !h_states || !grad || !d_decay || !d_chunk) return M3_ERR_NULL_POINTER;
+    const int st = check_scan_bwd_shape(batch, nchunks, nheads, pn);
+    if (st != M3_OK) return st;
+    const size_t need = m3::scan_bwd_workspace(batch, nchunks, nheads, pn);
+    if (need > 0 && (!workspace || workspace_bytes < need)) return M3_ERR_WORKSPACE;
+    if (workspace && !aligned(workspace, 256)) return M3_ERR_MISALIGNED;
+    return m3::launch_scan_bwd(decay, h_states, grad, d_decay, d_chunk, d_h_init,
+                               reinterpret_cast<float*>(workspace), batch, nchunks, nheads, pn,
                                as_stream(stream)) == 0
                ? M3_OK
                : M3_ERR_LAUNCH;

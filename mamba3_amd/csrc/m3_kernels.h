@@ -37,6 +37,12 @@ int launch_scan_fwd(const float* decay, const float* h_chunk, const float* h_ini
                     float* h_states, int64_t B, int64_t K, int64_t H, int64_t PN,
                     hipStream_t stream);
 
+// Backward of the scan: workspace bytes (0 when PN % 256 != 0) and launcher.
+size_t scan_bwd_workspace(int64_t B, int64_t K, int64_t H, int64_t PN);
+int launch_scan_bwd(const float* decay, const float* h_states, const float* grad,
+                    float* d_decay, float* d_chunk, float* d_h_init, float* workspace,
+                    int64_t B, int64_t K, int64_t H, int64_t PN, hipStream_t stream);
+
 // Generic (fp32 VALU) fused layer prefill: any supported shape, any dtype.
 size_t generic_prefill_workspace(const m3_layer_desc& d);
 int launch_generic_prefill(const m3_layer_desc& d, const m3_layer_params& p, const void* proj,

@@ -11,6 +11,7 @@
 // non-temporal (streaming) loads and stores, which keep them out of the caches' way.
 #include "m3_common.h"
 #include "m3_kernels.h"
+#include "m3_mfma.h"
 
 namespace m3 {
 
@@ -75,6 +76,150 @@ __global__ __launch_bounds__(kScanBlock) void scan_fwd_scalar(
         s = dptr[(int64_t)k * H] * s + __builtin_nontemporal_load(&h_chunk[base + (int64_t)k * kstride]);
         __builtin_nontemporal_store(s, &h_states[base + (int64_t)(k + 1) * kstride]);
     }
+}
+
+// ---------------------------------------------------------------------------------
+// Backward of the scan (replaces mamba3/csrc/scan.cu:52-126 and mamba3/scan.py:47-62).
+// With G[K-1] = dL/dh[K-1] and G[k] = dL/dh[k] + decay[k] G[k+1]:
+//   d_chunk[k] = G[k+1] (k < K-1),  d_chunk[K-1] = 0
+//   d_decay[k] = sum_j G[k+1][j] h[k][j] (k < K-1),  d_decay[K-1] = 0
+//   d_h_init   = G[0]
+// Pass 1: every lane owns a float4 column and walks k down; each wave reduces its share of
+// the d_decay sum (DPP scan, fixed order) and writes one partial per (b,k,h,wave).
+// Pass 2 adds the partials of every (b,k,h) in wave order: deterministic, no atomics.
+// ---------------------------------------------------------------------------------
+constexpr int kScanBwdBlock = 256;
+
+// Sum over the wave in a fixed order (DPP inclusive scan; lane 63 holds the total).
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wave_incl_scan(v)), 63));
+}
+
+// PN % 256 == 0: a wave's 64 float4 columns belong to one (b,h); nw = PN / 256 waves per (b,h).
+__global__ __launch_bounds__(kScanBwdBlock) void scan_bwd_vec4(
+    const float* __restrict__ decay, const f32x4* __restrict__ h_states,
+    const f32x4* __restrict__ grad, f32x4* __restrict__ d_chunk, f32x4* __restrict__ d_h_init,
+    float* __restrict__ part, int K, int H, int pn4, int64_t total_cols) {
+    const int64_t col = (int64_t)blockIdx.x * kScanBwdBlock + threadIdx.x;
+    if (col >= total_cols) return;  // total_cols is a multiple of 64: whole waves exit
+    const int j4 = (int)(col % pn4);
+    const int64_t bh = col / pn4;
+    const int h = (int)(bh % H);
+    const int64_t b = bh / H;
+    const int nw = pn4 / 64, w = j4 / 64;
+    const int64_t kstride = (int64_t)H * pn4;
+    const int64_t base = (b * K * H + h) * (int64_t)pn4 + j4;
+    const float* dptr = decay + b * K * H + h;
+    float* pptr = part + (b * K * H + h) * (int64_t)nw + w;  // (b,k,h,w) at k * H * nw
+
+    f32x4 g = __builtin_nontemporal_load(&grad[base + (int64_t)(K - 1) * kstride]);
+    __builtin_nontemporal_store(f32x4{0.f, 0.f, 0.f, 0.f}, &d_chunk[base + (int64_t)(K - 1) * kstride]);
+    for (int k = K - 2; k >= 0; --k) {
+        const int64_t o = base + (int64_t)k * kstride;
+        const f32x4 hs = __builtin_nontemporal_load(&h_states[o]);
+        const f32x4 gk = __builtin_nontemporal_load(&grad[o]);
+        __builtin_nontemporal_store(g, &d_chunk[o]);
+        const float acc = wave_sum_dpp(g[0] * hs[0] + g[1] * hs[1] + g[2] * hs[2] + g[3] * hs[3]);
+        if ((threadIdx.x & 63) == 0) pptr[(int64_t)k * H * nw] = acc;
+        g = gk + dptr[(int64_t)k * H] * g;
+    }
+    if (d_h_init) d_h_init[bh * pn4 + j4] = g;
+}
+
+// d_decay[b,k,h] = sum over the nw partials (k < K-1), 0 for k = K-1.
+__global__ __launch_bounds__(kScanBwdBlock) void scan_bwd_reduce(const float* __restrict__ part,
+                                                                 float* __restrict__ d_decay,
+                                                                 int K, int H, int nw,
+                                                                 int64_t total) {
+    const int64_t i = (int64_t)blockIdx.x * kScanBwdBlock + threadIdx.x;  // (b,k,h)
+    if (i >= total) return;
+    const int k = (int)((i / H) % K);
+    float acc = 0.f;
+    if (k < K - 1)
+        for (int w = 0; w < nw; ++w) acc += part[i * nw + w];
+    d_decay[i] = acc;
+}
+
+// Any PN: one workgroup per (b,h), columns strided over its threads, the d_decay sum of
+// every k reduced through LDS in a fixed order.
+__global__ __launch_bounds__(kScanBwdBlock) void scan_bwd_block(
+    const float* __restrict__ decay, const float* __restrict__ h_states,
+    const float* __restrict__ grad, float* __restrict__ d_chunk, float* __restrict__ d_decay,
+    float* __restrict__ d_h_init, int K, int H, int PN) {
+    constexpr int kMaxPer = 64;  // columns per thread: PN <= 256 * 64
+    __shared__ float red[kScanBwdBlock / 64];
+    const int64_t bh = blockIdx.x;
+    const int h = (int)(bh % H);
+    const int64_t b = bh / H;
+    const int64_t kstride = (int64_t)H * PN;
+    const int64_t base = (b * K * H + h) * (int64_t)PN;
+    const int64_t db = b * K * H + h;
+    const int tid = threadIdx.x;
+    float g[kMaxPer];
+    for (int i = 0; i < kMaxPer; ++i) {
+        const int j = tid + i * kScanBwdBlock;
+        if (j < PN) {
+            g[i] = grad[base + (int64_t)(K - 1) * kstride + j];
+            d_chunk[base + (int64_t)(K - 1) * kstride + j] = 0.f;
+        }
+    }
+    if (tid == 0) d_decay[db + (int64_t)(K - 1) * H] = 0.f;
+    for (int k = K - 2; k >= 0; --k) {
+        const int64_t o = base + (int64_t)k * kstride;
+        const float d = decay[db + (int64_t)k * H];
+        float acc = 0.f;
+        for (int i = 0; i < kMaxPer; ++i) {
+            const int j = tid + i * kScanBwdBlock;
+            if (j < PN) {
+                acc += g[i] * h_states[o + j];
+                d_chunk[o + j] = g[i];
+                g[i] = grad[o + j] + d * g[i];
+            }
+        }
+        acc = wave_sum_dpp(acc);
+        if ((tid & 63) == 0) red[tid >> 6] = acc;
+        __syncthreads();
+        if (tid == 0) {
+            float s = 0.f;
+            for (int w = 0; w < kScanBwdBlock / 64; ++w) s += red[w];
+            d_decay[db + (int64_t)k * H] = s;
+        }
+        __syncthreads();
+    }
+    if (d_h_init)
+        for (int i = 0; i < kMaxPer; ++i) {
+            const int j = tid + i * kScanBwdBlock;
+            if (j < PN) d_h_init[bh * PN + j] = g[i];
+        }
+}
+
+size_t scan_bwd_workspace(int64_t B, int64_t K, int64_t H, int64_t PN) {
+    if (PN % 256 != 0) return 0;
+    return (size_t)(B * K * H * (PN / 256)) * sizeof(float);
+}
+
+int launch_scan_bwd(const float* decay, const float* h_states, const float* grad,
+                    float* d_decay, float* d_chunk, float* d_h_init, float* workspace,
+                    int64_t B, int64_t K, int64_t H, int64_t PN, hipStream_t stream) {
+    const bool vec = (PN % 256 == 0) &&
+                     ((reinterpret_cast<uintptr_t>(h_states) | reinterpret_cast<uintptr_t>(grad) |
+                       reinterpret_cast<uintptr_t>(d_chunk) | reinterpret_cast<uintptr_t>(d_h_init)) % 16 == 0);
+    if (vec) {
+        const int64_t cols = B * H * (PN / 4);
+        hipLaunchKernelGGL(scan_bwd_vec4, dim3((unsigned)((cols + kScanBwdBlock - 1) / kScanBwdBlock)),
+                           dim3(kScanBwdBlock), 0, stream, decay,
+                           reinterpret_cast<const f32x4*>(h_states), reinterpret_cast<const f32x4*>(grad),
+                           reinterpret_cast<f32x4*>(d_chunk), reinterpret_cast<f32x4*>(d_h_init), workspace,
+                           (int)K, (int)H, (int)(PN / 4), cols);
+        const int64_t n = B * K * H;
+        hipLaunchKernelGGL(scan_bwd_reduce, dim3((unsigned)((n + kScanBwdBlock - 1) / kScanBwdBlock)),
+                           dim3(kScanBwdBlock), 0, stream, workspace, d_decay, (int)K, (int)H,
+                           (int)(PN / 256), n);
+    } else {
+        hipLaunchKernelGGL(scan_bwd_block, dim3((unsigned)(B * H)), dim3(kScanBwdBlock), 0, stream,
+                           decay, h_states, grad, d_chunk, d_decay, d_h_init, (int)K, (int)H, (int)PN);
+    }
+    return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 int launch_scan_fwd(const float* decay, const float* h_chunk, const float* h_init,

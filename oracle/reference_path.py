@@ -97,6 +97,24 @@ def scan_forward(decay: torch.Tensor, h_chunk: torch.Tensor,
     return torch.stack(states, dim=1)
 
 
+def scan_backward(decay: torch.Tensor, h_states: torch.Tensor, grad: torch.Tensor,
+                  has_h_init: bool = False):
+    """mamba3/scan.py:47-62: walk k down; G[k] = grad[k] + d[k] G[k+1]; d_chunk[k] = G[k+1],
+    d_decay[k] = sum_j G[k+1] h[k] (both 0 at k = K-1); d_h_init = G[0]."""
+    B, K, H, PN = h_states.shape
+    d = decay.float()
+    hs = h_states.float()
+    dh = grad.float().clone()
+    d_decay = torch.zeros_like(d)
+    d_chunk = torch.zeros_like(hs)
+    for k in range(K - 2, -1, -1):
+        g = dh[:, k + 1]
+        d_chunk[:, k] = g
+        d_decay[:, k] = (g * hs[:, k]).sum(dim=-1)
+        dh[:, k] = dh[:, k] + d[:, k, :, None] * g
+    return d_decay, d_chunk, (dh[:, 0] if has_h_init else None)
+
+
 def _intra_chunk(BX: torch.Tensor, cum: torch.Tensor, Cw: torch.Tensor):
     """mamba3/ssd.py:30-65 forward: factored cumsum.
     BX (B,K,H,Q,P,N), cum (B,K,H,Q) fp32, Cw (B,K,H,R,Q,N)."""

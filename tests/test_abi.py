@@ -50,6 +50,15 @@ def test_scan_rejects_bad_arguments(lib):
     fake = 256  # never dereferenced: validation fails before any launch
     assert lib.m3_scan_fwd(fake, fake, None, fake, 0, 1, 1, 1, None) == 2
     assert lib.m3_scan_fwd(fake, fake, None, fake, 1, -1, 1, 1, None) == 2
+    n = ctypes.c_size_t(7)
+    assert lib.m3_scan_bwd_workspace_size(2, 16, 24, 8192, ctypes.byref(n)) == 0
+    assert n.value == 2 * 16 * 24 * (8192 // 256) * 4  # one partial per wave and chunk
+    assert lib.m3_scan_bwd_workspace_size(2, 16, 24, 100, ctypes.byref(n)) == 0 and n.value == 0
+    assert lib.m3_scan_bwd_workspace_size(2, 16, 24, 20000, ctypes.byref(n)) == 3
+    assert lib.m3_scan_bwd(None, fake, fake, fake, fake, None, None, 0, 1, 2, 1, 256, None) == 1
+    assert lib.m3_scan_bwd(fake, fake, fake, fake, fake, None, None, 0, 1, 0, 1, 256, None) == 2
+    # the per-wave partials need a workspace
+    assert lib.m3_scan_bwd(fake, fake, fake, fake, fake, None, None, 0, 1, 2, 1, 256, None) == 4
 
 
 def _desc(**kw):

@@ -154,6 +154,33 @@ def test_scan_matches_closed_form_and_reference_loop():
     assert torch.count_nonzero(out0[:, 0]) == 0
 
 
+def test_scan_backward_equals_autograd_of_the_forward():
+    """The oracle's scan backward (mamba3/scan.py:47-62) against torch autograd through the
+    oracle's forward loop, with and without h_init; a backward that dropped the decay
+    carry (G[k] = grad[k]) must fail."""
+    g = torch.Generator().manual_seed(5)
+    B, K, H, PN = 2, 6, 3, 5
+    for with_init in (True, False):
+        d = (torch.rand(B, K, H, generator=g, dtype=torch.float64) * 0.5 + 0.5).requires_grad_()
+        hc = torch.randn(B, K, H, PN, generator=g, dtype=torch.float64, requires_grad=True)
+        h0 = torch.randn(B, H, PN, generator=g, dtype=torch.float64, requires_grad=True) if with_init else None
+        out = ref.scan_forward(d, hc, h0)
+        gout = torch.randn(B, K, H, PN, generator=g, dtype=torch.float32)
+        out.backward(gout)
+        dd, dc, dh0 = ref.scan_backward(d.detach(), out.detach(), gout, with_init)
+        np.testing.assert_allclose(dd.numpy(), d.grad.numpy(), rtol=1e-5, atol=1e-5)
+        np.testing.assert_allclose(dc.numpy(), hc.grad.numpy(), rtol=1e-5, atol=1e-5)
+        if with_init:
+            np.testing.assert_allclose(dh0.numpy(), h0.grad.numpy(), rtol=1e-5, atol=1e-5)
+        else:
+            assert dh0 is None
+        # planted mistake: no carry through the decay
+        bad = gout.clone()
+        bad[:, :-1] = gout[:, 1:]
+        bad[:, -1] = 0
+        assert np.abs(bad.numpy() - hc.grad.numpy()).max() > 1e-2
+
+
 def test_zero_dt_leaves_only_skip_path():
     """dt=0: no state is injected, so y == D * x_raw exactly and h stays h_init."""
     g = torch.Generator().manual_seed(4)
