@@ -89,6 +89,9 @@ struct Args {
     float* prev_bx;
 };
 
+// Keeps the LDS reads issued above ahead of the LDS writes that follow.
+#define M3_LDS_ORDER() asm volatile("" ::: "memory")
+
 __device__ __forceinline__ float readlane(float v, int l) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
 }
@@ -173,13 +176,8 @@ __device__ __forceinline__ unsigned rotate_pair(unsigned word, f16x2 kA, f16x2 k
 }
 
 // 8 consecutive bf16 (raw bits): one 128-bit load when the address is 16-byte aligned.
-// kStreaming: data read once (x) goes through non-temporal loads.
-template <bool kStreaming = false>
 __device__ __forceinline__ u32x4 load8(const bf16* p, bool vec) {
-    if (vec) {
-        const u32x4* q = reinterpret_cast<const u32x4*>(p);
-        return kStreaming ? __builtin_nontemporal_load(q) : *q;
-    }
+    if (vec) return *reinterpret_cast<const u32x4*>(p);
     const unsigned short* q = reinterpret_cast<const unsigned short*>(p);
     u32x4 v;
 #pragma unroll
@@ -230,16 +228,12 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
         mzr[r] = a.prm.mimo_z[(int64_t)(hp + pe) * R + r];
         mdr[r] = a.prm.mimo_down[(int64_t)(hp + pe) * R + r];
     }
-    // X preparation job (threads below XU): token xt, columns 8 xg .. 8 xg + 7.
-    constexpr int XU = Q * PB / 8;
-    const bool x_job = tid < XU;
-    const int xt = tid / (PB / 8), xg = tid % (PB / 8);
-    float mxr[8][R];
+    // X preparation jobs: column xp of tokens xt0 + m * (THREADS / PB), m < XJ.
+    constexpr int XJ = Q * PB / THREADS;
+    const int xp = tid % PB, xt0 = tid / PB;
+    float mxr[R];
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-#pragma unroll
-        for (int r = 0; r < R; ++r) mxr[j][r] = a.prm.mimo_x[(int64_t)(hp + p0 + 8 * xg + j) * R + r];
-    const bool xvec = a.rs % 8 == 0 && a.pl.x % 8 == 0;
+    for (int r = 0; r < R; ++r) mxr[r] = a.prm.mimo_x[(int64_t)(hp + p0 + xp) * R + r];
     // theta staging jobs: units of 8 pairs of one token.
     constexpr int THU = Q * NH / 8;
     constexpr int THJ = (THU + THREADS - 1) / THREADS;
@@ -261,11 +255,14 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
         }
     };
     // x of the X job (8 columns, raw bf16) and theta of the staging jobs.
-    u32x4 pxv, pth[THJ];
+    unsigned pxv[XJ];
+    u32x4 pth[THJ];
     auto load_xv = [&](int kk) {
-        if (x_job) {
-            const int st = min(kk * Q + xt, T - 1);
-            pxv = load8<true>(proj + (int64_t)st * rs + a.pl.x + hp + p0 + 8 * xg, xvec);
+#pragma unroll
+        for (int m = 0; m < XJ; ++m) {
+            const int st = min(kk * Q + xt0 + m * (THREADS / PB), T - 1);
+            pxv[m] = __builtin_nontemporal_load(
+                reinterpret_cast<const unsigned short*>(proj + (int64_t)st * rs + a.pl.x + hp + p0 + xp));
         }
     };
     auto load_theta = [&](int kk) {
@@ -338,11 +335,16 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
         }
         if (a.cplx && ai < NH) {
             // phi_t[i] = phi_{t-1}[i] - dt_t theta_t[i] (mamba3/mamba3.py:160-162)
-            float ph = phi_run;
+            // all theta reads first: the angle stores below may not be ordered before them
             const unsigned short* thq = reinterpret_cast<const unsigned short*>(&sm.th[0][0]) + ai;
+            unsigned thv[Q];
+#pragma unroll
+            for (int q = 0; q < Q; ++q) thv[q] = thq[q * NH];
+            M3_LDS_ORDER();
+            float ph = phi_run;
 #pragma unroll
             for (int q = 0; q < Q; ++q) {
-                ph -= readlane(dt_t, q) * bf(thq[q * NH]);
+                ph -= readlane(dt_t, q) * bf(thv[q]);
                 sm.phi[q][ai] = ph;
             }
             phi_run = ph;
@@ -369,23 +371,20 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
                 *reinterpret_cast<unsigned*>(&sm.C[t * R + r][2 * ri]) = valid ? rotate_pair(pwc[m][r], kA, kS) : 0u;
             }
         }
-        if (x_job) {
-            // X rows (xt, r) = x * mimo_x[p, r] (mamba3/mamba3.py:210), and times w_xt.
-            const bool valid = s0 + xt < T;
-            const float w = tk.w[xt];
+        // X rows (t, r) = x_t * mimo_x[p, r] (mamba3/mamba3.py:210), and times w_t.
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const unsigned u = pxv[j >> 1];
-                const float xval = valid ? bf((j & 1) ? (u >> 16) : (u & 0xffffu)) : 0.f;
-                XRow<R> xv, xw;
+        for (int m = 0; m < XJ; ++m) {
+            const int t = xt0 + m * (THREADS / PB);
+            const float xval = s0 + t < T ? bf(pxv[m]) : 0.f;
+            const float w = tk.w[t];
+            XRow<R> xv, xw;
 #pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    xv.v[r] = (f16)(xval * mxr[j][r]);
-                    xw.v[r] = (f16)(xval * mxr[j][r] * w);
-                }
-                *reinterpret_cast<XRow<R>*>(&sm.XT[kk & 1][8 * xg + j][xt * R]) = xv;
-                *reinterpret_cast<XRow<R>*>(&sm.XwT[8 * xg + j][xt * R]) = xw;
+            for (int r = 0; r < R; ++r) {
+                xv.v[r] = (f16)(xval * mxr[r]);
+                xw.v[r] = (f16)(xval * mxr[r] * w);
             }
+            *reinterpret_cast<XRow<R>*>(&sm.XT[kk & 1][xp][t * R]) = xv;
+            *reinterpret_cast<XRow<R>*>(&sm.XwT[xp][t * R]) = xw;
         }
     };
 
