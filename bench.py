@@ -257,7 +257,7 @@ def bench_scan(args, torch, shape, name):
     ms = wall * 1e3 / args.steps
     nbytes = B * K * H * (PN * 8 + 4) + B * H * PN * 4
     gbs = nbytes / (kern_ms * 1e-3) / 1e9
-    traffic = recorded_traffic(ROOT / "profiles" / "pmc_traffic_scan.md", (name,))
+    traffic = recorded_traffic(ROOT / "profiles" / "scan_d768_trace_and_traffic.md", (name,))
     res = base_result(args, nbytes / (ms * 1e-3) / 1e9, ms,
                       f"ssd_scan (m3_scan_fwd), decay ({B}, {K}, {H}), h_chunk ({B}, {K}, {H}, {PN}) "
                       "and h_init, fp32, resident in HBM", B, K, dtype="fp32")
@@ -304,8 +304,9 @@ def bench_scan_bwd(args, torch, shape, name):
                       f"ssd_scan backward (m3_scan_bwd), states and gradient ({B}, {K}, {H}, {PN}), "
                       "fp32, resident in HBM", B, K, dtype="fp32")
     res["unit"] = "GB/s"
+    traffic = recorded_traffic(ROOT / "profiles" / "scan_d768_trace_and_traffic.md", (name,))
     res["roofline"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                       "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                       "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic.get(name),
                        "kernel": "scan_bwd_vec4 + scan_bwd_reduce", "algorithmic_bytes": nbytes,
                        "avg_ms": round(kern_ms, 4)}
     if not args.no_cpu_baseline:
