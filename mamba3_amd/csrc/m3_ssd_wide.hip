@@ -11,8 +11,10 @@
 //     the work (256 for the d_model 2048 layer at batch 2); the scores and the RoPE
 //     rotation are recomputed by each column block;
 //   * a chunk has 64 (t, r) rows, i.e. Q = 64 / R tokens;
-//   * eight waves (two per SIMD) share both phases of a chunk: contract (and the next
-//     chunk's token scalars and RoPE angles), then output (and the next chunk's tiles).
+//   * sixteen waves (four per SIMD) share both phases of a chunk: contract (waves 0-7 the
+//     inter-chunk output of their tile, waves 8-15 the score tiles, all the state update;
+//     two score waves also the next chunk's token scalars and RoPE angles), then output
+//     (waves 0-7 the intra-chunk output, gate and store; all the next chunk's tiles).
 //
 // Per chunk, in LDS (f16 unless noted):
 //   C [(t,r)][n], B [(u,r')][n]       C~ / B~: normalised B^ / C^ (bc_norm_wide) rotated
@@ -40,7 +42,7 @@ namespace wd {
 
 constexpr int ROWS = 64;              // (t, r) rows per chunk
 constexpr int PB = 32;                // headdim columns per workgroup
-constexpr int THREADS = 512;          // eight waves
+constexpr int THREADS = 1024;         // 16 waves: 0-7 own output tiles, 8-15 score tiles
 constexpr int PAD = 8;                // f16 row padding of the LDS tiles
 constexpr float kHScale = 1.f / 256.f;  // the f16 state copy holds h * kHScale
 
@@ -190,7 +192,7 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
     constexpr int Q = ROWS / R;    // tokens per chunk
     constexpr int NH = N / 2;      // RoPE pairs
     constexpr int NR = N * R;
-    constexpr int TPW = N / 64;    // state tiles per wave
+    constexpr int TPW = N >= 128 ? N / 128 : 1;  // state tiles per wave (N/8 tiles in all)
     constexpr int KN = N / 32;     // k-steps over n
     constexpr int TPL = 4 / R;     // tokens per lane in an output tile
     __shared__ Smem<N, R> sm;
@@ -219,8 +221,12 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
     const float dtb = a.prm.dt_bias[h];
     const int hp = h * a.P;  // first column of this head in x, z and y
 
-    // Output tile of this wave: rows 16 tt .. 16 tt + 15, columns 16 pt .. 16 pt + 15.
-    const int tt = wave >> 1, pt = wave & 1;
+    // Waves 0-7: output tile rows 16 tt .. 16 tt + 15, columns 16 pt .. 16 pt + 15 (G3, G2,
+    // gate, store). Waves 8-15: score tiles (G1 and its mask). All waves: state tiles (G4)
+    // while there are tiles left, and the next chunk's tiles.
+    const bool out_wave = wave < 8;
+    const bool g4_wave = wave * TPW < N / 8;
+    const int tt = (wave & 7) >> 1, pt = wave & 1;
     const int pe = p0 + 16 * pt + l16;  // this lane's output column
     float mzr[R], mdr[R];
 #pragma unroll
@@ -228,8 +234,8 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
         mzr[r] = a.prm.mimo_z[(int64_t)(hp + pe) * R + r];
         mdr[r] = a.prm.mimo_down[(int64_t)(hp + pe) * R + r];
     }
-    // X preparation jobs: column xp of tokens xt0 + m * (THREADS / PB), m < XJ.
-    constexpr int XJ = Q * PB / THREADS;
+    // X preparation jobs: column xp of tokens xt0 + m * (THREADS / PB) below Q, m < XJ.
+    constexpr int XJ = (Q * PB + THREADS - 1) / THREADS;
     const int xp = tid % PB, xt0 = tid / PB;
     float mxr[R];
 #pragma unroll
@@ -241,7 +247,7 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
 
     // ---- per-chunk inputs, read into registers at least a phase before they are used ----
     // Rotation jobs: this thread's RoPE pair ri at tokens rt0 + m * TSTEP (m < J).
-    constexpr int J = Q * NH / THREADS;
+    constexpr int J = (Q * NH + THREADS - 1) / THREADS;  // jobs at tokens below Q
     constexpr int TSTEP = THREADS / NH;
     const int ri = tid % NH, rt0 = tid / NH;
     unsigned pwb[J][R], pwc[J][R];
@@ -286,11 +292,12 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
             }
         }
     };
-    // Token scalars and RoPE angles (waves 2 .. 2+NWA-1; waves 0 and 1 carry two score
-    // tiles each): lane t = token t of the chunk for the scalars, pair ai for the angles.
+    // Token scalars and RoPE angles (waves 10 .. 10+NWA-1, score waves with one tile each):
+    // lane t = token t of the chunk for the scalars, pair ai for the angles.
     constexpr int NWA = (NH + 63) / 64;
-    const bool angle_wave = wave >= 2 && wave < 2 + NWA;
-    const int ai = 64 * (wave - 2) + lane;
+    constexpr int kAngleWave0 = 10;
+    const bool angle_wave = wave >= kAngleWave0 && wave < kAngleWave0 + NWA;
+    const int ai = 64 * (wave - kAngleWave0) + lane;
     float phi_run = 0.f;
     unsigned rdt0 = 0, rlam0 = 0, rdt1 = 0, rlam1 = 0;
     float sc0 = 1.f, sc1 = 1.f;
@@ -320,7 +327,7 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
         const float lam_n = v1 && a.trap ? __builtin_amdgcn_rcpf(1.f + fast_exp(-bf(rlam1))) : 1.f;
         const float c2 = wave_incl_scan(Ah * dt_t * kLog2e);
         const float c2_end = readlane(c2, Q - 1);
-        if (wave == 2) {
+        if (wave == kAngleWave0 + NWA - 1) {
             const float av = a.trap ? lam_t * dt_t : dt_t;
             const float bv = a.trap ? (1.f - lam_n) * dt_n : 0.f;
             Tok& tk = sm.tok[kk & 1];
@@ -335,17 +342,21 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
         }
         if (a.cplx && ai < NH) {
             // phi_t[i] = phi_{t-1}[i] - dt_t theta_t[i] (mamba3/mamba3.py:160-162)
-            // all theta reads first: the angle stores below may not be ordered before them
+            // 16 theta reads ahead of each group's angle stores (which the reads may not be
+            // ordered after)
             const unsigned short* thq = reinterpret_cast<const unsigned short*>(&sm.th[0][0]) + ai;
-            unsigned thv[Q];
-#pragma unroll
-            for (int q = 0; q < Q; ++q) thv[q] = thq[q * NH];
-            M3_LDS_ORDER();
             float ph = phi_run;
 #pragma unroll
-            for (int q = 0; q < Q; ++q) {
-                ph -= readlane(dt_t, q) * bf(thv[q]);
-                sm.phi[q][ai] = ph;
+            for (int q0 = 0; q0 < Q; q0 += 16) {
+                unsigned thv[16];
+#pragma unroll
+                for (int j = 0; j < 16; ++j) thv[j] = thq[(q0 + j) * NH];
+                M3_LDS_ORDER();
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    ph -= readlane(dt_t, q0 + j) * bf(thv[j]);
+                    sm.phi[q0 + j][ai] = ph;
+                }
             }
             phi_run = ph;
         }
@@ -357,6 +368,7 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
 #pragma unroll
         for (int m = 0; m < J; ++m) {
             const int t = rt0 + m * TSTEP;
+            if (t >= Q) break;  // threads past the chunk's jobs (small d_state)
             const bool valid = s0 + t < T;
             f16x2 kA = f16x2{(f16)1.f, (f16)0.f};
             if (a.cplx) {
@@ -375,6 +387,7 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
 #pragma unroll
         for (int m = 0; m < XJ; ++m) {
             const int t = xt0 + m * (THREADS / PB);
+            if (t >= Q) break;
             const float xval = s0 + t < T ? bf(pxv[m]) : 0.f;
             const float w = tk.w[t];
             XRow<R> xv, xw;
@@ -424,17 +437,20 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
 
         // ---- contract ----
         unsigned zr_bits[TPL];
+        if (out_wave) {
 #pragma unroll
-        for (int q = 0; q < TPL; ++q) {
-            const int st = min(s0 + (16 * tt + 4 * g16) / R + q, T - 1);
-            zr_bits[q] = __builtin_nontemporal_load(reinterpret_cast<const unsigned short*>(proj + (int64_t)st * rs + a.pl.z + hp + pe));
+            for (int q = 0; q < TPL; ++q) {
+                const int st = min(s0 + (16 * tt + 4 * g16) / R + q, T - 1);
+                zr_bits[q] = __builtin_nontemporal_load(
+                    reinterpret_cast<const unsigned short*>(proj + (int64_t)st * rs + a.pl.z + hp + pe));
+            }
         }
         if (k + 2 < nchunks) load_theta(k + 2);
         if (angle_wave && k + 1 < nchunks) {
             prep_tokens(k + 1);
             if (k + 2 < nchunks) load_tokens(k + 2);
         }
-        {
+        if (g4_wave) {
             const float dec = tk.dec;
 #pragma unroll
             for (int j = 0; j < TPW; ++j) hacc[j] *= dec;
@@ -454,18 +470,20 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
             }
         }
         f32x4 yacc = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (out_wave) {
 #pragma unroll
-        for (int s = 0; s < KN; ++s) {
-            const f16x8 A = *reinterpret_cast<const f16x8*>(&sm.C[16 * tt + l16][32 * s + 8 * g16]);
-            const f16x8 Bo = *reinterpret_cast<const f16x8*>(&sm.H[16 * pt + l16][32 * s + 8 * g16]);
-            yacc = mfma16(A, Bo, yacc);
+            for (int s = 0; s < KN; ++s) {
+                const f16x8 A = *reinterpret_cast<const f16x8*>(&sm.C[16 * tt + l16][32 * s + 8 * g16]);
+                const f16x8 Bo = *reinterpret_cast<const f16x8*>(&sm.H[16 * pt + l16][32 * s + 8 * g16]);
+                yacc = mfma16(A, Bo, yacc);
+            }
+#pragma unroll
+            for (int v = 0; v < 4; ++v) yacc[v] *= tk.ec[(16 * tt + 4 * g16 + v) / R];
         }
-#pragma unroll
-        for (int v = 0; v < 4; ++v) yacc[v] *= tk.ec[(16 * tt + 4 * g16 + v) / R];
 
-        // Causal score tiles (ti, ui), ui <= ti, listed row by row: waves 0..7 take tiles
-        // 0..7, waves 0 and 1 also tiles 8 and 9 (their G2 is the shortest).
-        for (int idx = wave; idx < 10; idx += 8) {
+        // Causal score tiles (ti, ui), ui <= ti, listed row by row: waves 8..15 take tiles
+        // 0..7, waves 8 and 9 also tiles 8 and 9.
+        for (int idx = wave - 8; idx >= 0 && idx < 10; idx += 8) {
             const int ti = idx < 1 ? 0 : idx < 3 ? 1 : idx < 6 ? 2 : 3;
             const int ui = idx - ti * (ti + 1) / 2;
             f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -492,7 +510,7 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
             }
             *reinterpret_cast<f16x4*>(&sm.S[trow][16 * ui + 4 * g16]) = sv;
         }
-        if (wave == 3) {
+        if (wave == 15) {
             // G2 reads 32 score columns per step: the tiles right of the diagonal in row
             // blocks 0 and 2 are zero.
 #pragma unroll
@@ -502,13 +520,14 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
         __syncthreads();
 
         // ---- output ----
-        for (int s = 0; s <= tt / 2; ++s) {
-            const f16x8 A = *reinterpret_cast<const f16x8*>(&sm.S[16 * tt + l16][32 * s + 8 * g16]);
-            const f16x8 Bo = *reinterpret_cast<const f16x8*>(&sm.XT[k & 1][16 * pt + l16][32 * s + 8 * g16]);
-            yacc = mfma16(A, Bo, yacc);
-        }
+        if (out_wave) {
+            for (int s = 0; s <= tt / 2; ++s) {
+                const f16x8 A = *reinterpret_cast<const f16x8*>(&sm.S[16 * tt + l16][32 * s + 8 * g16]);
+                const f16x8 Bo = *reinterpret_cast<const f16x8*>(&sm.XT[k & 1][16 * pt + l16][32 * s + 8 * g16]);
+                yacc = mfma16(A, Bo, yacc);
+            }
 #pragma unroll
-        for (int q = 0; q < TPL; ++q) {
+            for (int q = 0; q < TPL; ++q) {
             const int st = s0 + (16 * tt + 4 * g16) / R + q;
             const float z = bf(zr_bits[q]);
             float o = 0.f;
@@ -518,14 +537,17 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
                 o += mdr[r] * zr * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-zr * kLog2e)) * yacc[q * R + r];
             }
             if (st < T) __builtin_nontemporal_store((bf16)o, &a.y_out[((int64_t)b * T + st) * a.H * a.P + hp + pe]);
+            }
         }
+        if (g4_wave) {
 #pragma unroll
-        for (int j = 0; j < TPW; ++j) {
-            const int jt = wave * TPW + j;
-            const int nt = jt >> 1, ptj = jt & 1;
-            const f16x4 hv = f16x4{(f16)(hacc[j][0] * kHScale), (f16)(hacc[j][1] * kHScale),
-                                   (f16)(hacc[j][2] * kHScale), (f16)(hacc[j][3] * kHScale)};
-            *reinterpret_cast<f16x4*>(&sm.H[16 * ptj + l16][16 * nt + 4 * g16]) = hv;
+            for (int j = 0; j < TPW; ++j) {
+                const int jt = wave * TPW + j;
+                const int nt = jt >> 1, ptj = jt & 1;
+                const f16x4 hv = f16x4{(f16)(hacc[j][0] * kHScale), (f16)(hacc[j][1] * kHScale),
+                                       (f16)(hacc[j][2] * kHScale), (f16)(hacc[j][3] * kHScale)};
+                *reinterpret_cast<f16x4*>(&sm.H[16 * ptj + l16][16 * nt + 4 * g16]) = hv;
+            }
         }
         if (k + 1 < nchunks) {
             prep_chunk(k + 1);
@@ -539,7 +561,7 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
     }
 
     // Final state h[p][n] (fp32) from the accumulators: lane holds n = 16 nt + 4 g16 + v.
-    if (a.h_final) {
+    if (a.h_final && g4_wave) {
 #pragma unroll
         for (int j = 0; j < TPW; ++j) {
             const int jt = wave * TPW + j;
