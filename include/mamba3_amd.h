@@ -169,6 +169,32 @@ int m3_chunked_ssd_fwd(int32_t batch, int32_t seqlen, int32_t nheads, int32_t he
                        const void* x_raw, const float* h_init, void* y, float* h_final,
                        float* state_ws, void* stream);
 
+/*
+ * Backward of m3_chunked_ssd_fwd, all tensors fp32 (the caller upcasts bf16). Replaces the
+ * reference's autograd through chunked_ssd (mamba3/ssd.py:118-244): _IntraChunkFn.backward
+ * (ssd.py:67-115), SSDScanFn.backward (mamba3/scan.py:101-141) with the native
+ * scan_backward (mamba3/csrc/scan.cu:168-211), and ATen's backward of the bmm / cumsum /
+ * exp / cat around them, without the per-token (P,N) outer products.
+ * Inputs are the forward's (same shapes; x_b / B_b NULL for no beta terms; h_init
+ * nullable) plus dy [B,T,H,P,R] = dL/dy and dh_final [B,H,P,N] = dL/dh_final (nullable).
+ * Outputs (all written, not accumulated): dx_g, dx_b, dB_g, dB_b, dC, dx_raw like their
+ * inputs (dx_b / dB_b NULL exactly when x_b is), ddt [B,T,H], dA [H], dD [H],
+ * dh_init [B,H,P,N] (nullable: not written). mimo_rank must be 1, 2, 4 or 8, and
+ * headdim * d_state a multiple of 256 or at most 16384. Sums run in a fixed order
+ * (deterministic). workspace: m3_chunked_ssd_bwd_workspace_size() bytes, 256-byte aligned.
+ */
+int m3_chunked_ssd_bwd_workspace_size(int32_t batch, int32_t seqlen, int32_t nheads,
+                                      int32_t headdim, int32_t d_state, int32_t mimo_rank,
+                                      int32_t has_beta, size_t* bytes);
+int m3_chunked_ssd_bwd(int32_t batch, int32_t seqlen, int32_t nheads, int32_t headdim,
+                       int32_t d_state, int32_t mimo_rank, const float* x_g, const float* x_b,
+                       const float* B_g, const float* B_b, const float* C, const float* dt,
+                       const float* A, const float* D, const float* x_raw, const float* h_init,
+                       const float* dy, const float* dh_final, float* dx_g, float* dx_b,
+                       float* dB_g, float* dB_b, float* dC, float* ddt, float* dA, float* dD,
+                       float* dx_raw, float* dh_init, void* workspace, size_t workspace_bytes,
+                       void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -31,6 +31,8 @@ EXPORTED_SYMBOLS = (
     "m3_prefill_fwd",
     "m3_step_fwd",
     "m3_chunked_ssd_fwd",
+    "m3_chunked_ssd_bwd_workspace_size",
+    "m3_chunked_ssd_bwd",
 )
 
 
@@ -94,6 +96,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.m3_chunked_ssd_fwd.argtypes = [_i32, _i32, _i32, _i32, _i32, _i32, _i32,
                                        _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                        _vp, _vp, _vp, _vp]
+    lib.m3_chunked_ssd_bwd_workspace_size.restype = ctypes.c_int
+    lib.m3_chunked_ssd_bwd_workspace_size.argtypes = [_i32] * 7 + [ctypes.POINTER(ctypes.c_size_t)]
+    lib.m3_chunked_ssd_bwd.restype = ctypes.c_int
+    lib.m3_chunked_ssd_bwd.argtypes = [_i32] * 6 + [_vp] * 23 + [ctypes.c_size_t, _vp]
 
 
 def lib() -> ctypes.CDLL:
@@ -189,3 +195,23 @@ def chunked_fwd(B, T, H, P, N, R, dtype, x_g, x_b, B_g, B_b, C, dt, A, D, x_raw,
                                    ptr(B_g), ptr(B_b), ptr(C), ptr(dt), ptr(A), ptr(D),
                                    ptr(x_raw), ptr(h_init), ptr(y), ptr(h_final),
                                    ptr(state_ws), stream_of(x_g)), "m3_chunked_ssd_fwd")
+
+
+def chunked_bwd_workspace_bytes(B, T, H, P, N, R, has_beta: bool) -> int:
+    n = ctypes.c_size_t(0)
+    check(lib().m3_chunked_ssd_bwd_workspace_size(B, T, H, P, N, R, int(has_beta), ctypes.byref(n)),
+          "m3_chunked_ssd_bwd_workspace_size")
+    return n.value
+
+
+def chunked_bwd(B, T, H, P, N, R, x_g, x_b, B_g, B_b, C, dt, A, D, x_raw, h_init, dy, dh_final,
+                dx_g, dx_b, dB_g, dB_b, dC, ddt, dA, dD, dx_raw, dh_init) -> None:
+    """m3_chunked_ssd_bwd on contiguous fp32 tensors; allocates the workspace."""
+    n = chunked_bwd_workspace_bytes(B, T, H, P, N, R, x_b is not None)
+    ws = torch.empty(max(n, 1), dtype=torch.uint8, device=x_g.device)
+    check(lib().m3_chunked_ssd_bwd(B, T, H, P, N, R, ptr(x_g), ptr(x_b), ptr(B_g), ptr(B_b),
+                                   ptr(C), ptr(dt), ptr(A), ptr(D), ptr(x_raw), ptr(h_init),
+                                   ptr(dy), ptr(dh_final), ptr(dx_g), ptr(dx_b), ptr(dB_g),
+                                   ptr(dB_b), ptr(dC), ptr(ddt), ptr(dA), ptr(dD), ptr(dx_raw),
+                                   ptr(dh_init), ptr(ws), n, stream_of(x_g)),
+          "m3_chunked_ssd_bwd")

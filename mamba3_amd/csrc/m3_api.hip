@@ -196,4 +196,48 @@ int m3_chunked_ssd_fwd(int32_t batch, int32_t seqlen, int32_t nheads, int32_t he
                                       state_ws, as_stream(stream));
 }
 
+int m3_chunked_ssd_bwd_workspace_size(int32_t batch, int32_t seqlen, int32_t nheads,
+                                      int32_t headdim, int32_t d_state, int32_t mimo_rank,
+                                      int32_t has_beta, size_t* bytes) {
+    if (!bytes) return M3_ERR_NULL_POINTER;
+    if (batch <= 0 || seqlen <= 0 || nheads <= 0 || headdim <= 0 || d_state <= 0 ||
+        mimo_rank <= 0 || (has_beta != 0 && has_beta != 1))
+        return M3_ERR_INVALID_SHAPE;
+    if (!m3::chunked_bwd_shape_ok(batch, seqlen, nheads, headdim, d_state, mimo_rank, has_beta))
+        return M3_ERR_UNSUPPORTED;
+    *bytes = m3::chunked_bwd_workspace(batch, seqlen, nheads, headdim, d_state, mimo_rank, has_beta);
+    return M3_OK;
+}
+
+int m3_chunked_ssd_bwd(int32_t batch, int32_t seqlen, int32_t nheads, int32_t headdim,
+                       int32_t d_state, int32_t mimo_rank, const float* x_g, const float* x_b,
+                       const float* B_g, const float* B_b, const float* C, const float* dt,
+                       const float* A, const float* D, const float* x_raw, const float* h_init,
+                       const float* dy, const float* dh_final, float* dx_g, float* dx_b,
+                       float* dB_g, float* dB_b, float* dC, float* ddt, float* dA, float* dD,
+                       float* dx_raw, float* dh_init, void* workspace, size_t workspace_bytes,
+                       void* stream) {
+    if (batch <= 0 || seqlen <= 0 || nheads <= 0 || headdim <= 0 || d_state <= 0 ||
+        mimo_rank <= 0)
+        return M3_ERR_INVALID_SHAPE;
+    if (!x_g || !B_g || !C || !dt || !A || !D || !x_raw || !dy || !dx_g || !dB_g || !dC ||
+        !ddt || !dA || !dD || !dx_raw)
+        return M3_ERR_NULL_POINTER;
+    const bool beta = x_b != nullptr;
+    if ((B_b != nullptr) != beta || (dx_b != nullptr) != beta || (dB_b != nullptr) != beta)
+        return M3_ERR_NULL_POINTER;
+    if (!m3::chunked_bwd_shape_ok(batch, seqlen, nheads, headdim, d_state, mimo_rank, beta))
+        return M3_ERR_UNSUPPORTED;
+    const size_t need =
+        m3::chunked_bwd_workspace(batch, seqlen, nheads, headdim, d_state, mimo_rank, beta);
+    if (!workspace || workspace_bytes < need) return M3_ERR_WORKSPACE;
+    if (!aligned(workspace, 256)) return M3_ERR_MISALIGNED;
+    return m3::launch_chunked_bwd(batch, seqlen, nheads, headdim, d_state, mimo_rank, x_g, x_b,
+                                  B_g, B_b, C, dt, A, D, x_raw, h_init, dy, dh_final, dx_g, dx_b,
+                                  dB_g, dB_b, dC, ddt, dA, dD, dx_raw, dh_init, workspace,
+                                  as_stream(stream)) == 0
+               ? M3_OK
+               : M3_ERR_LAUNCH;
+}
+
 }  // extern "C"

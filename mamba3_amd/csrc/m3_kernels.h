@@ -69,6 +69,17 @@ int launch_wide_prefill(const m3_layer_desc& d, const m3_layer_params& p, const 
                         const float* dt_scale, void* y_out, float* h_final, float* angle,
                         float* prev_bx, void* workspace, hipStream_t stream);
 
+// Backward of the chunked SSD (fp32): shape support, workspace bytes and launcher.
+bool chunked_bwd_shape_ok(int B, int T, int H, int P, int N, int R, bool beta);
+size_t chunked_bwd_workspace(int B, int T, int H, int P, int N, int R, bool beta);
+int launch_chunked_bwd(int B, int T, int H, int P, int N, int R, const float* x_g,
+                       const float* x_b, const float* B_g, const float* B_b, const float* C,
+                       const float* dt, const float* A, const float* D, const float* x_raw,
+                       const float* h_init, const float* dy, const float* dh_final, float* dx_g,
+                       float* dx_b, float* dB_g, float* dB_b, float* dC, float* ddt, float* dA,
+                       float* dD, float* dx_raw, float* dh_init, void* workspace,
+                       hipStream_t stream);
+
 // Returns 1 when the step kernel supports (N, R), else 0.
 int step_supported(int N, int R);
 int launch_step(const m3_layer_desc& d, const m3_layer_params& p, const void* proj,

@@ -1,0 +1,678 @@
+// Backward of the chunked SSD on pre-processed inputs (the op of m3_chunked_ssd_fwd), fp32.
+//
+// Replaces, under autograd, the reference's chunked_ssd (mamba3/ssd.py:118-244): the custom
+// backward of _IntraChunkFn (ssd.py:67-115), the scan backward (mamba3/scan.py:101-141,
+// mamba3/csrc/scan.cu:52-126) and ATen's backward of the bmm / cumsum / exp around them. The
+// reference differentiates through the materialised per-token outer products
+// BX_total (B,K,H,Q,P,N); this file never forms them.
+//
+// Per (batch b, head h) and chunk k of Qb tokens (positions t, s in [0, Qb)), with
+// c_t = sum_{j<=t} A dt_j, W[t,s] = exp(c_t - c_s) for s <= t (else 0), the R2 = R or 2R
+// factor columns Xf[s,p,j] = dt_s x[s,p,j] (x_g, then x_b) and Bf[s,n,j] (B_g, then B_b):
+//   h at token t     = exp(c_t) H_k + sum_{s<=t} W[t,s] sum_j Xf[s,:,j] Bf[s,:,j]^T
+//   y[t,p,r]         = sum_n C[t,n,r] h_t[p,n] + D x_raw[t,p,r]
+//   H_{k+1}          = exp(c_end) H_k + sum_s exp(c_end - c_s) sum_j Xf[s,:,j] Bf[s,:,j]^T
+// Gradients, with dH = dL/dH_{k+1} (from the reverse scan), G[(t,r),(s,j)] = C_t.Bf_s and
+// DX[(t,r),(s,j)] = dy_t.Xf_s, M = W o G, DM = W o DX:
+//   dXf[s,p,j] = sum_{t,r} M[(t,r),(s,j)] dy[t,p,r] + exp(c_end - c_s) sum_n Bf[s,n,j] dH[p,n]
+//   dBf[s,n,j] = sum_{t,r} DM[(t,r),(s,j)] C[t,n,r] + exp(c_end - c_s) sum_p Xf[s,p,j] dH[p,n]
+//   dC[t,n,r]  = sum_{s,j} DM[(t,r),(s,j)] Bf[s,n,j] + exp(c_t) sum_p dy[t,p,r] H_k[p,n]
+//   dc_t       = sum_s W Z[t,s] - sum_{t'} W Z[t',t] + sum_{p,r} dy[t,p,r] y_inter[t,p,r]
+//                - q_t + [t = Qb-1] (sum_s q_s + exp(c_end) <dH, H_k>),
+//                Z = sum_{r,j} G o DX,  q_s = sum_{p,j} Xf[s,p,j] (state term of dXf)[s,p,j]
+//   d(A dt_t)  = sum_{t'>=t} dc_t';  ddt_t = A d(A dt_t) + sum_{p,j} dXf[s,p,j] x[s,p,j]
+// Qb = 64 / R2 (a power of two), so that the score tiles are at most 128 x 128. The chunk
+// states H_k and dH come from the state scan kernels over K+1 chunks, the last one carrying
+// dL/dh_final. Every sum runs in a fixed order: results are deterministic.
+#include <hip/hip_runtime.h>
+
+#include "m3_kernels.h"
+#include "m3_mfma.h"
+
+namespace m3 {
+namespace bw {
+
+constexpr int TT = 64;    // output tile edge
+constexpr int KT = 16;    // contraction step
+constexpr int NTH = 256;  // threads per tile block
+
+struct Shape {
+    int B, T, H, P, N, R, R2, Qb, K, nPt, nNt;
+    int64_t PN;
+    __host__ __device__ int QR() const { return Qb * R; }
+    __host__ __device__ int QR2() const { return Qb * R2; }
+};
+
+struct Args {
+    Shape s;
+    const float *xg, *xb, *Bg, *Bb, *C, *dt, *A, *D, *xr, *hinit, *dy, *dhf;
+    float *dxg, *dxb, *dBg, *dBb, *dC, *ddt, *dA, *dD, *dxr, *dhinit;
+    // workspace
+    float *cum, *dec, *ddec, *hext, *Hs, *gext, *dch, *M, *DM, *dcI, *pInter, *pState, *pDt,
+        *pA, *pD;
+};
+
+// Chunk ch = (b K + k) H + h (the scan's (B,K,H) order); its position in the (B,K+1,H)
+// arrays of the extended scan.
+__device__ __forceinline__ int64_t chx(const Shape& s, int b, int k, int h) {
+    return ((int64_t)b * (s.K + 1) + k) * s.H + h;
+}
+// Offset of token row (b, tg, h) of a (B,T,H,X,R) tensor, in units of X*R elements.
+__device__ __forceinline__ int64_t row(const Shape& s, int b, int tg, int h) {
+    return ((int64_t)b * s.T + tg) * s.H + h;
+}
+
+struct Lds {
+    float A[KT][TT];
+    float B[KT][TT];
+};
+
+// acc[i][j] += sum_k fa(4 ty + i, k) fb(k, 4 tx + j) over k < kdim, for the 64 x 64 tile of
+// a 256-thread block (tx = tid % 16, ty = tid / 16). fa / fb return 0 outside the operands.
+template <class FA, class FB>
+__device__ __forceinline__ void gemm_acc(float (&acc)[4][4], int kdim, FA fa, FB fb, Lds& l) {
+    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+    for (int k0 = 0; k0 < kdim; k0 += KT) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int e = tid + NTH * i, kk = e >> 6, mm = e & 63;
+            const bool in = k0 + kk < kdim;
+            l.A[kk][mm] = in ? fa(mm, k0 + kk) : 0.f;
+            l.B[kk][mm] = in ? fb(k0 + kk, mm) : 0.f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < KT; ++kk) {
+            const float4 av = *reinterpret_cast<const float4*>(&l.A[kk][4 * ty]);
+            const float4 bv = *reinterpret_cast<const float4*>(&l.B[kk][4 * tx]);
+            const float a4[4] = {av.x, av.y, av.z, av.w};
+            const float b4[4] = {bv.x, bv.y, bv.z, bv.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] += a4[i] * b4[j];
+        }
+        __syncthreads();
+    }
+}
+
+__device__ __forceinline__ void zero(float (&acc)[4][4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
+}
+
+// Accessors of chunk (b, k, h). Token positions at or past T read as 0.
+struct Chunk {
+    const Args* a;
+    int b, k, h;
+    __device__ bool real(int t) const { return k * a->s.Qb + t < a->s.T; }
+    __device__ float dtv(int t) const {
+        return real(t) ? a->dt[row(a->s, b, k * a->s.Qb + t, h)] : 0.f;
+    }
+    // x factor j of token t (x_g for j < R, else x_b), without dt.
+    __device__ float x(int t, int p, int j) const {
+        const Shape& s = a->s;
+        if (!real(t)) return 0.f;
+        const float* base = j < s.R ? a->xg : a->xb;
+        return base[row(s, b, k * s.Qb + t, h) * s.P * s.R + (int64_t)p * s.R + (j < s.R ? j : j - s.R)];
+    }
+    __device__ float bf(int t, int n, int j) const {
+        const Shape& s = a->s;
+        if (!real(t)) return 0.f;
+        const float* base = j < s.R ? a->Bg : a->Bb;
+        return base[row(s, b, k * s.Qb + t, h) * s.N * s.R + (int64_t)n * s.R + (j < s.R ? j : j - s.R)];
+    }
+    __device__ float c(int t, int n, int r) const {
+        const Shape& s = a->s;
+        return real(t) ? a->C[row(s, b, k * s.Qb + t, h) * s.N * s.R + (int64_t)n * s.R + r] : 0.f;
+    }
+    __device__ float dy(int t, int p, int r) const {
+        const Shape& s = a->s;
+        return real(t) ? a->dy[row(s, b, k * s.Qb + t, h) * s.P * s.R + (int64_t)p * s.R + r] : 0.f;
+    }
+};
+
+// ---- K0: c_t (inclusive cumsum of A dt within the chunk) and the chunk decays.
+__global__ __launch_bounds__(64) void bwd_cum(Args a) {
+    const Shape& s = a.s;
+    const int ch = blockIdx.x, h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
+    const int t = threadIdx.x, tg = k * s.Qb + t;
+    const float l = (t < s.Qb && tg < s.T) ? a.A[h] * a.dt[row(s, b, tg, h)] : 0.f;
+    const float c = wave_incl_scan(l);
+    if (t < s.Qb) a.cum[(int64_t)ch * s.Qb + t] = c;
+    if (t == s.Qb - 1) {
+        a.dec[chx(s, b, k, h)] = __expf(c);
+        if (k == s.K - 1) a.dec[chx(s, b, s.K, h)] = 1.f;
+    }
+}
+
+// ---- K2: chunk-local states (scan input) and the y_inter gradient of each chunk state:
+//   hext[k][p,n] = sum_{s,j} exp(c_end - c_s) Xf[s,p,j] Bf[s,n,j]
+//   gext[k][p,n] = sum_{t,r} exp(c_t) dy[t,p,r] C[t,n,r]
+// plus the extra chunk K: hext = 0, gext = dL/dh_final (or 0).
+__global__ __launch_bounds__(NTH) void bwd_states(Args a) {
+    __shared__ Lds l;
+    __shared__ float cs[64];
+    const Shape& s = a.s;
+    const int ch = blockIdx.x, h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
+    const int pt = blockIdx.y / s.nNt, nt = blockIdx.y % s.nNt;
+    const int p0 = pt * TT, n0 = nt * TT;
+    const Chunk q{&a, b, k, h};
+    if (threadIdx.x < s.Qb) cs[threadIdx.x] = a.cum[(int64_t)ch * s.Qb + threadIdx.x];
+    __syncthreads();
+    const float cend = cs[s.Qb - 1];
+    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+    float acc[4][4];
+    zero(acc);
+    gemm_acc(acc, s.Qb * s.R2,
+             [&](int mm, int j) {
+                 const int p = p0 + mm, t = j / s.R2;
+                 return p < s.P ? __expf(cend - cs[t]) * q.dtv(t) * q.x(t, p, j % s.R2) : 0.f;
+             },
+             [&](int j, int nn) {
+                 const int n = n0 + nn;
+                 return n < s.N ? q.bf(j / s.R2, n, j % s.R2) : 0.f;
+             },
+             l);
+    float* ho = a.hext + chx(s, b, k, h) * s.PN;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int p = p0 + 4 * ty + i, n = n0 + 4 * tx + j;
+            if (p < s.P && n < s.N) ho[(int64_t)p * s.N + n] = acc[i][j];
+        }
+    zero(acc);
+    gemm_acc(acc, s.Qb * s.R,
+             [&](int mm, int j) {
+                 const int p = p0 + mm, t = j / s.R;
+                 return p < s.P ? __expf(cs[t]) * q.dy(t, p, j % s.R) : 0.f;
+             },
+             [&](int j, int nn) {
+                 const int n = n0 + nn;
+                 return n < s.N ? q.c(j / s.R, n, j % s.R) : 0.f;
+             },
+             l);
+    float* go = a.gext + chx(s, b, k, h) * s.PN;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int p = p0 + 4 * ty + i, n = n0 + 4 * tx + j;
+            if (p < s.P && n < s.N) go[(int64_t)p * s.N + n] = acc[i][j];
+        }
+    if (k == s.K - 1) {
+        float* he = a.hext + chx(s, b, s.K, h) * s.PN;
+        float* ge = a.gext + chx(s, b, s.K, h) * s.PN;
+        const float* df = a.dhf ? a.dhf + ((int64_t)b * s.H + h) * s.PN : nullptr;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int p = p0 + 4 * ty + i, n = n0 + 4 * tx + j;
+                if (p < s.P && n < s.N) {
+                    const int64_t o = (int64_t)p * s.N + n;
+                    he[o] = 0.f;
+                    ge[o] = df ? df[o] : 0.f;
+                }
+            }
+    }
+}
+
+// ---- K1: masked scores M = W o G and DM = W o DX of the chunk, and the intra-chunk part of
+// dc: sum_s W Z[t,s] - sum_t' W Z[t',t]. One block per chunk, looping over its tiles.
+__global__ __launch_bounds__(NTH) void bwd_scores(Args a) {
+    __shared__ Lds l;
+    __shared__ float zp[TT][TT + 1];
+    __shared__ float cs[64], rowacc[64], colacc[64];
+    const Shape& s = a.s;
+    const int ch = blockIdx.x, h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
+    const Chunk q{&a, b, k, h};
+    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+    if (tid < 64) {
+        cs[tid] = tid < s.Qb ? a.cum[(int64_t)ch * s.Qb + tid] : 0.f;
+        rowacc[tid] = 0.f;
+        colacc[tid] = 0.f;
+    }
+    __syncthreads();
+    const int QR = s.QR(), QR2 = s.QR2();
+    float* Mo = a.M + (int64_t)ch * QR * QR2;
+    float* DMo = a.DM + (int64_t)ch * QR * QR2;
+    for (int m0 = 0; m0 < QR; m0 += TT) {
+        for (int c0 = 0; c0 < QR2; c0 += TT) {
+            float g[4][4], d[4][4];
+            zero(g);
+            zero(d);
+            // G[(t,r),(s,j)] = sum_n C[t,n,r] Bf[s,n,j]
+            gemm_acc(g, s.N,
+                     [&](int mm, int n) { const int m = m0 + mm; return q.c(m / s.R, n, m % s.R); },
+                     [&](int n, int cc) { const int c = c0 + cc; return q.bf(c / s.R2, n, c % s.R2); },
+                     l);
+            // DX[(t,r),(s,j)] = sum_p dy[t,p,r] dt_s x[s,p,j]
+            gemm_acc(d, s.P,
+                     [&](int mm, int p) { const int m = m0 + mm; return q.dy(m / s.R, p, m % s.R); },
+                     [&](int p, int cc) {
+                         const int c = c0 + cc, t = c / s.R2;
+                         return q.dtv(t) * q.x(t, p, c % s.R2);
+                     },
+                     l);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int m = m0 + 4 * ty + i, c = c0 + 4 * tx + j;
+                    const int t = m / s.R, u = c / s.R2;
+                    const float w = u <= t ? __expf(cs[t] - cs[u]) : 0.f;
+                    Mo[(int64_t)m * QR2 + c] = w * g[i][j];
+                    DMo[(int64_t)m * QR2 + c] = w * d[i][j];
+                    zp[4 * ty + i][4 * tx + j] = w * g[i][j] * d[i][j];
+                }
+            __syncthreads();
+            // Z over the (r, j) blocks of the tile, summed into rows (t) and columns (s).
+            const int nt = TT / s.R, ns = TT / s.R2;
+            if (tid < nt) {
+                float v = 0.f;
+                for (int u = 0; u < ns; ++u)
+                    for (int r = 0; r < s.R; ++r)
+                        for (int j = 0; j < s.R2; ++j) v += zp[tid * s.R + r][u * s.R2 + j];
+                rowacc[m0 / s.R + tid] += v;
+            } else if (tid >= 128 && tid < 128 + ns) {
+                const int u = tid - 128;
+                float v = 0.f;
+                for (int t = 0; t < nt; ++t)
+                    for (int r = 0; r < s.R; ++r)
+                        for (int j = 0; j < s.R2; ++j) v += zp[t * s.R + r][u * s.R2 + j];
+                colacc[c0 / s.R2 + u] += v;
+            }
+            __syncthreads();
+        }
+    }
+    if (tid < s.Qb) a.dcI[(int64_t)ch * s.Qb + tid] = rowacc[tid] - colacc[tid];
+}
+
+// Sums v over the rows of the 64 x 64 tile that belong to one token (R2 consecutive rows per
+// token, `per` of them) and over the 16 column groups, in a fixed order; token u of the tile
+// gets the sum in out[u] (threads tid < 64 / per). `red` holds 64 x 16 floats.
+__device__ __forceinline__ void tile_token_sums(const float (&v)[4], int per, float (*red)[17],
+                                                float* out) {
+    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[4 * ty + i][tx] = v[i];
+    __syncthreads();
+    if (tid < TT / per) {
+        float acc = 0.f;
+        for (int r = 0; r < per; ++r)
+            for (int x = 0; x < 16; ++x) acc += red[tid * per + r][x];
+        out[tid] = acc;
+    }
+    __syncthreads();
+}
+
+// ---- K3: dXf rows (s,j) x columns p; writes dx_g / dx_b = dt_s dXf and the per-token
+// partials q_s (state term . Xf) and sum_{p,j} dXf x.
+__global__ __launch_bounds__(NTH) void bwd_dxf(Args a) {
+    __shared__ Lds l;
+    __shared__ float red[TT][17];
+    __shared__ float cs[64], outv[64];
+    const Shape& s = a.s;
+    const int ch = blockIdx.x, h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
+    const int rt = blockIdx.y / s.nPt, pt = blockIdx.y % s.nPt;
+    const int m0 = rt * TT, p0 = pt * TT;
+    const Chunk q{&a, b, k, h};
+    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+    if (tid < s.Qb) cs[tid] = a.cum[(int64_t)ch * s.Qb + tid];
+    __syncthreads();
+    const float cend = cs[s.Qb - 1];
+    const float* dH = a.dch + chx(s, b, k, h) * s.PN;
+    float acc[4][4];
+    zero(acc);
+    gemm_acc(acc, s.N,
+             [&](int mm, int n) { const int m = m0 + mm; return q.bf(m / s.R2, n, m % s.R2); },
+             [&](int n, int pp) { const int p = p0 + pp; return p < s.P ? dH[(int64_t)p * s.N + n] : 0.f; },
+             l);
+    float xv[4][4], rv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = m0 + 4 * ty + i, t = m / s.R2, j = m % s.R2;
+        const float e = __expf(cend - cs[t]), d = q.dtv(t);
+        rv[i] = 0.f;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+            const int p = p0 + 4 * tx + jj;
+            xv[i][jj] = p < s.P ? q.x(t, p, j) : 0.f;
+            acc[i][jj] *= e;
+            rv[i] += d * xv[i][jj] * acc[i][jj];
+        }
+    }
+    const int per = s.R2, nts = TT / per;
+    tile_token_sums(rv, per, red, outv);
+    if (tid < nts) a.pState[((int64_t)ch * s.nPt + pt) * s.Qb + m0 / per + tid] = outv[tid];
+    const float* Mi = a.M + (int64_t)ch * s.QR() * s.QR2();
+    gemm_acc(acc, s.QR(),
+             [&](int mm, int jr) { return Mi[(int64_t)jr * s.QR2() + m0 + mm]; },
+             [&](int jr, int pp) {
+                 const int p = p0 + pp;
+                 return p < s.P ? q.dy(jr / s.R, p, jr % s.R) : 0.f;
+             },
+             l);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = m0 + 4 * ty + i, t = m / s.R2, j = m % s.R2;
+        const float d = q.dtv(t);
+        rv[i] = 0.f;
+        const bool w = q.real(t);
+        float* out = j < s.R ? a.dxg : a.dxb;
+        const int64_t base = row(s, b, k * s.Qb + t, h) * s.P * s.R + (j < s.R ? j : j - s.R);
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+            const int p = p0 + 4 * tx + jj;
+            rv[i] += acc[i][jj] * xv[i][jj];
+            if (w && p < s.P) out[base + (int64_t)p * s.R] = d * acc[i][jj];
+        }
+    }
+    tile_token_sums(rv, per, red, outv);
+    if (tid < nts) a.pDt[((int64_t)ch * s.nPt + pt) * s.Qb + m0 / per + tid] = outv[tid];
+}
+
+// ---- K4: dBf rows (s,j) x columns n; writes dB_g / dB_b.
+__global__ __launch_bounds__(NTH) void bwd_dbf(Args a) {
+    __shared__ Lds l;
+    __shared__ float cs[64];
+    const Shape& s = a.s;
+    const int ch = blockIdx.x, h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
+    const int rt = blockIdx.y / s.nNt, nt = blockIdx.y % s.nNt;
+    const int m0 = rt * TT, n0 = nt * TT;
+    const Chunk q{&a, b, k, h};
+    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+    if (tid < s.Qb) cs[tid] = a.cum[(int64_t)ch * s.Qb + tid];
+    __syncthreads();
+    const float cend = cs[s.Qb - 1];
+    const float* dH = a.dch + chx(s, b, k, h) * s.PN;
+    float acc[4][4];
+    zero(acc);
+    gemm_acc(acc, s.P,
+             [&](int mm, int p) {
+                 const int m = m0 + mm, t = m / s.R2;
+                 return q.dtv(t) * q.x(t, p, m % s.R2);
+             },
+             [&](int p, int nn) { const int n = n0 + nn; return n < s.N ? dH[(int64_t)p * s.N + n] : 0.f; },
+             l);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float e = __expf(cend - cs[(m0 + 4 * ty + i) / s.R2]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] *= e;
+    }
+    const float* DMi = a.DM + (int64_t)ch * s.QR() * s.QR2();
+    gemm_acc(acc, s.QR(),
+             [&](int mm, int jr) { return DMi[(int64_t)jr * s.QR2() + m0 + mm]; },
+             [&](int jr, int nn) {
+                 const int n = n0 + nn;
+                 return n < s.N ? q.c(jr / s.R, n, jr % s.R) : 0.f;
+             },
+             l);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = m0 + 4 * ty + i, t = m / s.R2, j = m % s.R2;
+        if (!q.real(t)) continue;
+        float* out = j < s.R ? a.dBg : a.dBb;
+        const int64_t base = row(s, b, k * s.Qb + t, h) * s.N * s.R + (j < s.R ? j : j - s.R);
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+            const int n = n0 + 4 * tx + jj;
+            if (n < s.N) out[base + (int64_t)n * s.R] = acc[i][jj];
+        }
+    }
+}
+
+// ---- K5: dC rows (t,r) x columns n, and the per-token partials sum_{n,r} C dC_inter.
+__global__ __launch_bounds__(NTH) void bwd_dc(Args a) {
+    __shared__ Lds l;
+    __shared__ float red[TT][17];
+    __shared__ float cs[64], outv[64];
+    const Shape& s = a.s;
+    const int ch = blockIdx.x, h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
+    const int rt = blockIdx.y / s.nNt, nt = blockIdx.y % s.nNt;
+    const int m0 = rt * TT, n0 = nt * TT;
+    const Chunk q{&a, b, k, h};
+    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+    if (tid < s.Qb) cs[tid] = a.cum[(int64_t)ch * s.Qb + tid];
+    __syncthreads();
+    const float* Hk = a.Hs + chx(s, b, k, h) * s.PN;
+    float acc[4][4];
+    zero(acc);
+    gemm_acc(acc, s.P,
+             [&](int mm, int p) { const int m = m0 + mm; return q.dy(m / s.R, p, m % s.R); },
+             [&](int p, int nn) { const int n = n0 + nn; return n < s.N ? Hk[(int64_t)p * s.N + n] : 0.f; },
+             l);
+    float rv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = m0 + 4 * ty + i, t = m / s.R, r = m % s.R;
+        const float e = __expf(cs[t]);
+        rv[i] = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int n = n0 + 4 * tx + j;
+            acc[i][j] *= e;
+            if (n < s.N) rv[i] += q.c(t, n, r) * acc[i][j];
+        }
+    }
+    const int per = s.R, nts = TT / per;
+    tile_token_sums(rv, per, red, outv);
+    if (tid < nts) a.pInter[((int64_t)ch * s.nNt + nt) * s.Qb + m0 / per + tid] = outv[tid];
+    const float* DMi = a.DM + (int64_t)ch * s.QR() * s.QR2();
+    gemm_acc(acc, s.QR2(),
+             [&](int mm, int jc) { return DMi[(int64_t)(m0 + mm) * s.QR2() + jc]; },
+             [&](int jc, int nn) {
+                 const int n = n0 + nn;
+                 return n < s.N ? q.bf(jc / s.R2, n, jc % s.R2) : 0.f;
+             },
+             l);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = m0 + 4 * ty + i, t = m / s.R, r = m % s.R;
+        if (!q.real(t)) continue;
+        const int64_t base = row(s, b, k * s.Qb + t, h) * s.N * s.R + r;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int n = n0 + 4 * tx + j;
+            if (n < s.N) a.dC[base + (int64_t)n * s.R] = acc[i][j];
+        }
+    }
+}
+
+// ---- K6: per chunk: dc -> d(A dt) (suffix sums), ddt, the chunk's partials of dA and dD,
+// and dx_raw = D dy.
+__global__ __launch_bounds__(NTH) void bwd_tokens(Args a) {
+    __shared__ float dcs[64], part[NTH];
+    const Shape& s = a.s;
+    const int ch = blockIdx.x, h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
+    const Chunk q{&a, b, k, h};
+    const int tid = threadIdx.x;
+    if (tid < 64) {
+        const int t = tid;
+        float dc = 0.f, qs = 0.f;
+        if (t < s.Qb) {
+            dc = a.dcI[(int64_t)ch * s.Qb + t];
+            for (int nt = 0; nt < s.nNt; ++nt) dc += a.pInter[((int64_t)ch * s.nNt + nt) * s.Qb + t];
+            for (int pt = 0; pt < s.nPt; ++pt) qs += a.pState[((int64_t)ch * s.nPt + pt) * s.Qb + t];
+            dc -= qs;
+        }
+        const float qtot = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                                         __builtin_bit_cast(int, wave_incl_scan(qs)), 63));
+        if (t == s.Qb - 1) dc += qtot + a.dec[chx(s, b, k, h)] * a.ddec[chx(s, b, k, h)];
+        dcs[t] = dc;
+    }
+    __syncthreads();
+    if (tid < 64) {
+        const int t = tid;
+        float dl = 0.f;
+        for (int u = s.Qb - 1; u >= t; --u) dl += dcs[u];
+        float contrib = 0.f;
+        if (t < s.Qb && q.real(t)) {
+            float pd = 0.f;
+            for (int pt = 0; pt < s.nPt; ++pt) pd += a.pDt[((int64_t)ch * s.nPt + pt) * s.Qb + t];
+            a.ddt[row(s, b, k * s.Qb + t, h)] = a.A[h] * dl + pd;
+            contrib = q.dtv(t) * dl;
+        }
+        const float tot = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                                        __builtin_bit_cast(int, wave_incl_scan(contrib)), 63));
+        if (t == 0) a.pA[ch] = tot;
+    }
+    // dD partial and dx_raw over the chunk's real tokens.
+    const float Dh = a.D[h];
+    const int nreal = min(s.Qb, s.T - k * s.Qb);
+    const int per_tok = s.P * s.R;
+    float v = 0.f;
+    for (int e = tid; e < nreal * per_tok; e += NTH) {
+        const int t = e / per_tok, pr = e % per_tok;
+        const int64_t o = row(s, b, k * s.Qb + t, h) * per_tok + pr;
+        const float g = a.dy[o];
+        v += g * a.xr[o];
+        a.dxr[o] = Dh * g;
+    }
+    part[tid] = v;
+    __syncthreads();
+    for (int w = NTH / 2; w > 0; w >>= 1) {
+        if (tid < w) part[tid] += part[tid + w];
+        __syncthreads();
+    }
+    if (tid == 0) a.pD[ch] = part[0];
+}
+
+// ---- K7: dA[h], dD[h] = sums of the chunk partials over (b, k), in a fixed order.
+__global__ __launch_bounds__(NTH) void bwd_reduce(Args a) {
+    __shared__ float pa[NTH], pd[NTH];
+    const Shape& s = a.s;
+    const int h = blockIdx.x, tid = threadIdx.x;
+    const int n = s.B * s.K;
+    float va = 0.f, vd = 0.f;
+    for (int i = tid; i < n; i += NTH) {
+        va += a.pA[(int64_t)i * s.H + h];
+        vd += a.pD[(int64_t)i * s.H + h];
+    }
+    pa[tid] = va;
+    pd[tid] = vd;
+    __syncthreads();
+    for (int w = NTH / 2; w > 0; w >>= 1) {
+        if (tid < w) {
+            pa[tid] += pa[tid + w];
+            pd[tid] += pd[tid + w];
+        }
+        __syncthreads();
+    }
+    if (tid == 0) {
+        a.dA[h] = pa[0];
+        a.dD[h] = pd[0];
+    }
+}
+
+// Workspace carve-up (all fp32, each part 256-byte aligned).
+struct Plan {
+    Shape s;
+    size_t off[16];
+    size_t scan_off, total;
+};
+
+inline size_t al(size_t x) { return (x + 255) & ~(size_t)255; }
+
+bool make_shape(int B, int T, int H, int P, int N, int R, bool beta, Shape& s) {
+    if (R != 1 && R != 2 && R != 4 && R != 8) return false;
+    s.B = B, s.T = T, s.H = H, s.P = P, s.N = N, s.R = R, s.R2 = beta ? 2 * R : R;
+    s.Qb = 64;
+    while (s.Qb * s.R2 > 128) s.Qb /= 2;
+    s.K = (T + s.Qb - 1) / s.Qb;
+    s.nPt = (P + TT - 1) / TT;
+    s.nNt = (N + TT - 1) / TT;
+    s.PN = (int64_t)P * N;
+    return true;
+}
+
+Plan make_plan(const Shape& s) {
+    Plan pl;
+    pl.s = s;
+    const size_t BKH = (size_t)s.B * s.K * s.H, BK1H = (size_t)s.B * (s.K + 1) * s.H;
+    const size_t sizes[15] = {
+        BKH * s.Qb,                              // cum
+        BK1H,                                    // dec
+        BK1H,                                    // ddec
+        BK1H * s.PN, BK1H * s.PN, BK1H * s.PN,   // hext, Hs, gext
+        BK1H * s.PN,                             // dch
+        BKH * s.QR() * s.QR2(),                  // M
+        BKH * s.QR() * s.QR2(),                  // DM
+        BKH * s.Qb,                              // dcI
+        BKH * s.nNt * s.Qb,                      // pInter
+        BKH * s.nPt * s.Qb, BKH * s.nPt * s.Qb,  // pState, pDt
+        BKH, BKH};                               // pA, pD
+    size_t o = 0;
+    for (int i = 0; i < 15; ++i) {
+        pl.off[i] = o;
+        o += al(sizes[i] * sizeof(float));
+    }
+    pl.scan_off = o;
+    o += al(scan_bwd_workspace(s.B, s.K + 1, s.H, s.PN));
+    pl.total = o;
+    return pl;
+}
+
+}  // namespace bw
+
+bool chunked_bwd_shape_ok(int B, int T, int H, int P, int N, int R, bool beta) {
+    bw::Shape s;
+    if (!bw::make_shape(B, T, H, P, N, R, beta, s)) return false;
+    const int64_t pn = s.PN;
+    if (pn % 256 != 0 && pn > 16384) return false;  // the scan backward's limit
+    return true;
+}
+
+size_t chunked_bwd_workspace(int B, int T, int H, int P, int N, int R, bool beta) {
+    bw::Shape s;
+    if (!bw::make_shape(B, T, H, P, N, R, beta, s)) return 0;
+    return bw::make_plan(s).total;
+}
+
+int launch_chunked_bwd(int B, int T, int H, int P, int N, int R, const float* x_g,
+                       const float* x_b, const float* B_g, const float* B_b, const float* C,
+                       const float* dt, const float* A, const float* D, const float* x_raw,
+                       const float* h_init, const float* dy, const float* dh_final, float* dx_g,
+                       float* dx_b, float* dB_g, float* dB_b, float* dC, float* ddt, float* dA,
+                       float* dD, float* dx_raw, float* dh_init, void* workspace,
+                       hipStream_t stream) {
+    using namespace bw;
+    Shape s;
+    if (!make_shape(B, T, H, P, N, R, x_b != nullptr, s)) return 1;
+    const Plan pl = make_plan(s);
+    char* ws = reinterpret_cast<char*>(workspace);
+    auto part = [&](int i) { return reinterpret_cast<float*>(ws + pl.off[i]); };
+    Args a;
+    a.s = s;
+    a.xg = x_g, a.xb = x_b, a.Bg = B_g, a.Bb = B_b, a.C = C, a.dt = dt, a.A = A, a.D = D;
+    a.xr = x_raw, a.hinit = h_init, a.dy = dy, a.dhf = dh_final;
+    a.dxg = dx_g, a.dxb = dx_b, a.dBg = dB_g, a.dBb = dB_b, a.dC = dC, a.ddt = ddt, a.dA = dA;
+    a.dD = dD, a.dxr = dx_raw, a.dhinit = dh_init;
+    a.cum = part(0), a.dec = part(1), a.ddec = part(2), a.hext = part(3), a.Hs = part(4);
+    a.gext = part(5), a.dch = part(6), a.M = part(7), a.DM = part(8), a.dcI = part(9);
+    a.pInter = part(10), a.pState = part(11), a.pDt = part(12), a.pA = part(13), a.pD = part(14);
+    float* scan_ws = reinterpret_cast<float*>(ws + pl.scan_off);
+
+    const unsigned nch = (unsigned)((int64_t)s.B * s.K * s.H);
+    const int nRt = s.QR() / TT, nRt2 = s.QR2() / TT;
+    hipLaunchKernelGGL(bwd_cum, dim3(nch), dim3(64), 0, stream, a);
+    hipLaunchKernelGGL(bwd_states, dim3(nch, s.nPt * s.nNt), dim3(NTH), 0, stream, a);
+    if (launch_scan_fwd(a.dec, a.hext, h_init, a.Hs, s.B, s.K + 1, s.H, s.PN, stream) != 0) return 1;
+    if (launch_scan_bwd(a.dec, a.Hs, a.gext, a.ddec, a.dch, dh_init, scan_ws, s.B, s.K + 1, s.H,
+                        s.PN, stream) != 0)
+        return 1;
+    hipLaunchKernelGGL(bwd_scores, dim3(nch), dim3(NTH), 0, stream, a);
+    hipLaunchKernelGGL(bwd_dxf, dim3(nch, nRt2 * s.nPt), dim3(NTH), 0, stream, a);
+    hipLaunchKernelGGL(bwd_dbf, dim3(nch, nRt2 * s.nNt), dim3(NTH), 0, stream, a);
+    hipLaunchKernelGGL(bwd_dc, dim3(nch, nRt * s.nNt), dim3(NTH), 0, stream, a);
+    hipLaunchKernelGGL(bwd_tokens, dim3(nch), dim3(NTH), 0, stream, a);
+    hipLaunchKernelGGL(bwd_reduce, dim3(s.H), dim3(NTH), 0, stream, a);
+    return hipGetLastError() == hipSuccess ? 0 : 1;
+}
+
+}  // namespace m3

@@ -42,8 +42,8 @@ class RMSNorm(nn.Module):
 
 
 class _ForwardOnly(torch.autograd.Function):
-    """Ties a kernel output to its input so that backward raises instead of silently
-    producing wrong gradients (backward kernels are not part of this build)."""
+    """Ties a decode-step output to its input so that backward raises instead of silently
+    producing wrong gradients (the step kernel has no backward)."""
 
     @staticmethod
     def forward(ctx, anchor, out):
@@ -52,8 +52,7 @@ class _ForwardOnly(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad):
         raise NotImplementedError(
-            "mamba3_amd implements the Mamba-3 forward path only (prefill, forward, step); "
-            "its HIP kernels have no backward")
+            "KulaMamba.step has no backward in mamba3_amd; train through forward / prefill")
 
 
 class KulaMamba(nn.Module):
@@ -183,6 +182,9 @@ class KulaMamba(nn.Module):
         kernels: proj (B,T,d_in_proj) -> (y (B,T,d_inner) in proj.dtype, state or None)."""
         _native.require_gpu(proj)
         self._check_norm_eps()
+        if torch.is_grad_enabled() and (proj.requires_grad or
+                                        any(p.requires_grad for p in self._small_params())):
+            return self._ssd_train(proj, dt_scale, return_state)
         proj = proj.contiguous()
         Bat, T, _ = proj.shape
         H, P, N = self.nheads, self.headdim, self.d_state
@@ -201,12 +203,76 @@ class KulaMamba(nn.Module):
         workspace = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
         _native.prefill_fwd(desc, params, proj, scale, y, h_final, angle, prev_bx, workspace,
                             ws_bytes)
-        if torch.is_grad_enabled() and (proj.requires_grad or
-                                        any(p.requires_grad for p in self._small_params())):
-            y = _ForwardOnly.apply(proj, y)
         state = None
         if return_state:
             state = {"h": h_final, "angle": angle, "prev_BX": prev_bx}
+        return y, state
+
+    def _ssd_train(self, proj: torch.Tensor, dt_scale=None, return_state: bool = False):
+        """Differentiable form of ssd_from_proj, used when autograd needs gradients: the
+        reference's element-wise preparation and gate (mamba3/mamba3.py:142-166, 197-239)
+        as PyTorch ops in fp32 around chunked_ssd, whose forward and backward run on the
+        HIP kernels (m3_chunked_ssd_fwd / m3_chunked_ssd_bwd). The state it returns
+        matches the fused path's (fp32 h, angle and prev_BX; mamba3/mamba3.py:241-256)."""
+        from .ssd import chunked_ssd
+
+        Bat, T, _ = proj.shape
+        H, P, N, R, G = self.nheads, self.headdim, self.d_state, self.mimo_rank, self.ngroups
+        sizes = [self.d_inner, self._d_x, self._d_bc, self._d_bc, H]
+        sizes += [H] if self.use_trapezoidal else []
+        sizes += [N // 2] if self.use_complex_ssm else []
+        parts = list(proj.float().split(sizes, dim=-1))
+        z, x_flat, B_flat, C_flat, dt_raw = parts[:5]
+        lam_raw = parts[5] if self.use_trapezoidal else None
+        theta_raw = parts[-1] if self.use_complex_ssm else None
+
+        dt = nn.functional.softplus(dt_raw + self.dt_bias.float())
+        if dt_scale is not None:
+            dt = dt * self._dt_scale(dt_scale, (Bat, T, H), proj.device)
+        A = -torch.exp(self.A_log.float())
+        dA = torch.exp(A * dt)
+
+        def norm_bias(flat, norm, bias):
+            v = norm(flat.reshape(Bat, T, G, N * R)).float().reshape(Bat, T, G, N, R)
+            v = v + bias.float()
+            return v.repeat_interleave(H // G, dim=2) if G != H else v
+
+        B_r = norm_bias(B_flat, self.B_norm, self.B_bias)
+        C_r = norm_bias(C_flat, self.C_norm, self.C_bias)
+        angles = None
+        if self.use_complex_ssm:
+            angles = -(dt.unsqueeze(-1) * theta_raw.unsqueeze(-2)).cumsum(dim=1)  # (B,T,H,N/2)
+            cos = torch.cos(angles)[..., None, None]
+            sin = torch.sin(angles)[..., None, None]
+
+            def rope(v):
+                v = v.reshape(Bat, T, H, N // 2, 2, R)
+                ev, od = v[..., 0:1, :], v[..., 1:2, :]
+                return torch.cat([ev * cos - od * sin, ev * sin + od * cos], dim=-2).reshape(
+                    Bat, T, H, N, R)
+
+            B_r, C_r = rope(B_r), rope(C_r)
+
+        x_r = x_flat.reshape(Bat, T, H, P, 1) * self.mimo_x.float()
+        if self.use_trapezoidal:
+            lam = torch.sigmoid(lam_raw)
+            x_g = x_r * lam[..., None, None]
+            x_b = nn.functional.pad(x_r[:, :-1], (0, 0, 0, 0, 0, 0, 1, 0)) * \
+                ((1.0 - lam) * dA)[..., None, None]
+            B_b = nn.functional.pad(B_r[:, :-1], (0, 0, 0, 0, 0, 0, 1, 0))
+        else:
+            x_g, x_b, B_b = x_r, None, None
+        out = chunked_ssd(x_g, x_b, B_r, B_b, C_r, dt, A, self.D.float(), x_r,
+                          self.chunk_size, return_final_state=return_state)
+        z_r = z.reshape(Bat, T, H, P, 1) * self.mimo_z.float()
+        y = (out.y * nn.functional.silu(z_r) * self.mimo_down.float()).sum(dim=-1)
+        y = y.reshape(Bat, T, self.d_inner).to(proj.dtype)
+        state = None
+        if return_state:
+            angle = angles[:, T - 1] if angles is not None else \
+                torch.zeros(Bat, H, N // 2, device=proj.device, dtype=torch.float32)
+            prev_bx = torch.einsum("bhnr,bhpr->bhpn", B_r[:, T - 1], x_r[:, T - 1])
+            state = {"h": out.h_final, "angle": angle, "prev_BX": prev_bx}
         return y, state
 
     def forward(self, x: torch.Tensor, dt_scale=None) -> torch.Tensor:

@@ -8,6 +8,9 @@
   L-matrix product (no chunking, no factored cumsum), used to pin the chunked algorithm
   on the reduced case trapezoid-off / complex-off / rank-1.
 * `scan_closed_form` evaluates the chunk recurrence as explicit sums of products.
+* `chunked_recurrent` runs chunked_ssd's inputs (mamba3/ssd.py:118-244) through the
+  per-token recurrence in float64, as differentiable torch ops: autograd through it is an
+  independent formulation of chunked_ssd's gradients.
 """
 
 from __future__ import annotations
@@ -129,3 +132,25 @@ def scan_closed_form(decay: np.ndarray, h_chunk: np.ndarray, h_init: np.ndarray 
             acc += np.prod(d[:, i + 1:k], axis=1)[..., None] * hc[:, i]
         out[:, k] = acc
     return out
+
+
+def chunked_recurrent(x_g, x_b, B_g, B_b, C, dt, A, D, x_raw, h_init=None):
+    """chunked_ssd's contract (mamba3/ssd.py:118-244) token by token, float64, autograd-able:
+        h_t = exp(A dt_t) h_{t-1} + dt_t (sum_r x_g[t,:,r] B_g[t,:,r]^T + x_b B_b likewise)
+        y_t[p,r] = sum_n C[t,n,r] h_t[p,n] + D x_raw[t,p,r]
+    (the per-token update of mamba3/mamba3.py:298-310 with the chunked inputs). Returns
+    (y (B,T,H,P,R), h_final (B,H,P,N))."""
+    Bat, T, H, P, R = x_g.shape
+    N = B_g.shape[3]
+    f = lambda t: None if t is None else t.double()
+    x_g, x_b, B_g, B_b, C, dt, A, D, x_raw, h_init = map(f, (x_g, x_b, B_g, B_b, C, dt, A, D,
+                                                            x_raw, h_init))
+    h = h_init.reshape(Bat, H, P, N) if h_init is not None else x_g.new_zeros(Bat, H, P, N)
+    ys = []
+    for t in range(T):
+        bx = torch.einsum("bhpr,bhnr->bhpn", x_g[:, t], B_g[:, t])
+        if x_b is not None:
+            bx = bx + torch.einsum("bhpr,bhnr->bhpn", x_b[:, t], B_b[:, t])
+        h = torch.exp(A * dt[:, t])[..., None, None] * h + dt[:, t][..., None, None] * bx
+        ys.append(torch.einsum("bhnr,bhpn->bhpr", C[:, t], h) + D[None, :, None, None] * x_raw[:, t])
+    return torch.stack(ys, dim=1), h

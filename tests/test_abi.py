@@ -61,6 +61,38 @@ def test_scan_rejects_bad_arguments(lib):
     assert lib.m3_scan_bwd(fake, fake, fake, fake, fake, None, None, 0, 1, 2, 1, 256, None) == 4
 
 
+def test_chunked_bwd_workspace_and_validation(lib):
+    n = ctypes.c_size_t(0)
+    # d_model 768 shapes: B=4, T=1024, H=24, P=64, N=128, R=2 with beta terms -> chunks of 32
+    assert lib.m3_chunked_ssd_bwd_workspace_size(4, 1024, 24, 64, 128, 2, 1, ctypes.byref(n)) == 0
+    K = 1024 // 32
+    states = 4 * (K + 1) * 24 * 64 * 128 * 4
+    scores = 4 * K * 24 * 64 * 128 * 4
+    assert n.value >= 4 * states + 2 * scores
+    assert lib.m3_chunked_ssd_bwd_workspace_size(4, 1024, 24, 64, 128, 3, 1, ctypes.byref(n)) == 3
+    assert lib.m3_chunked_ssd_bwd_workspace_size(4, 1024, 24, 64, 128, 2, 2, ctypes.byref(n)) == 2
+    assert lib.m3_chunked_ssd_bwd_workspace_size(0, 1024, 24, 64, 128, 2, 1, ctypes.byref(n)) == 2
+    assert lib.m3_chunked_ssd_bwd_workspace_size(1, 8, 1, 8, 128, 2, 1, None) == 1
+    fake = ctypes.c_void_p(256)
+    ins = [fake] * 10  # x_g x_b B_g B_b C dt A D x_raw h_init
+    outs = [fake] * 10  # dx_g dx_b dB_g dB_b dC ddt dA dD dx_raw dh_init
+    args = lambda i, o: [1, 8, 1, 16, 16, 2, *i, fake, None, *o]
+    # missing dy
+    a = args(ins, outs)
+    a[6 + 10] = None
+    assert lib.m3_chunked_ssd_bwd(*a, fake, 1 << 30, None) == 1
+    # x_b given but dx_b missing
+    o = list(outs)
+    o[1] = None
+    assert lib.m3_chunked_ssd_bwd(*args(ins, o), fake, 1 << 30, None) == 1
+    # rank 3 is not supported by the backward
+    a = args(ins, outs)
+    a[5] = 3
+    assert lib.m3_chunked_ssd_bwd(*a, fake, 1 << 30, None) == 3
+    # no workspace
+    assert lib.m3_chunked_ssd_bwd(*args(ins, outs), None, 0, None) == 4
+
+
 def _desc(**kw):
     d = dict(batch=1, seqlen=4, nheads=8, headdim=16, d_state=16, mimo_rank=2, ngroups=1,
              use_trapezoidal=1, use_complex=1, dtype=0, proj_row_stride=0, rms_eps=1e-5)

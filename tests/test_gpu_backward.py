@@ -1,0 +1,221 @@
+"""GPU parity of the backward path: chunked_ssd's HIP backward (m3_chunked_ssd_bwd) and the
+layer's differentiable forward / prefill, against autograd through the float64 oracle
+(whose gradients are pinned on the CPU against the per-token recurrence and finite
+differences).
+
+Tolerances (normwise max-relative error, max|g - g_ref| / max|g_ref|, per gradient):
+  * fp32 kernels vs the oracle: 1e-4
+  * bf16 layer vs the fp32 oracle on the bf16-rounded weights and inputs: 2e-2
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import mamba3_amd
+from conftest import max_rel, oracle_cfg
+from oracle import reference_path as ref
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = 1e-4
+BF16_TOL = 2e-2
+
+NAMES = ("x_g", "x_b", "B_g", "B_b", "C", "dt", "A", "D", "x_raw", "h_init")
+
+# B, T, H, P, N, R, beta terms, h_init, dL/dh_final
+CASES = [
+    (2, 100, 3, 16, 32, 2, True, True, True),
+    (1, 130, 2, 8, 16, 1, False, False, True),
+    (1, 64, 2, 32, 64, 4, True, False, False),
+    (2, 37, 1, 64, 128, 2, True, True, True),
+    (1, 50, 2, 16, 16, 8, True, False, True),
+    (1, 200, 1, 64, 128, 2, False, True, False),
+    (1, 1, 2, 16, 32, 2, True, True, True),
+]
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _no_tf32(cuda_device):
+    torch.backends.cuda.matmul.allow_tf32 = False
+    torch.backends.cudnn.allow_tf32 = False
+
+
+def _inputs(case, seed=0):
+    B, T, H, P, N, R, beta, with_init, _ = case
+    g = torch.Generator().manual_seed(seed)
+    r = lambda *s: torch.randn(*s, generator=g, dtype=torch.float64)
+    return dict(x_g=r(B, T, H, P, R), x_b=r(B, T, H, P, R) if beta else None,
+                B_g=r(B, T, H, N, R), B_b=r(B, T, H, N, R) if beta else None,
+                C=r(B, T, H, N, R), dt=torch.rand(B, T, H, generator=g, dtype=torch.float64) * 0.5,
+                A=-torch.rand(H, generator=g, dtype=torch.float64) - 0.2, D=r(H),
+                x_raw=r(B, T, H, P, R), h_init=r(B, H, P, N) if with_init else None)
+
+
+def _gpu_grads(ins, dy, dhf, dev):
+    leaf = {k: (v.float().to(dev).requires_grad_() if v is not None else None) for k, v in ins.items()}
+    out = mamba3_amd.chunked_ssd(*[leaf[k] for k in NAMES[:9]], chunk_size=64,
+                                 h_init=leaf["h_init"], return_final_state=True)
+    loss = (out.y * dy.float().to(dev)).sum()
+    if dhf is not None:
+        loss = loss + (out.h_final * dhf.float().to(dev)).sum()
+    loss.backward()
+    return out, {k: v.grad for k, v in leaf.items() if v is not None}
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "B{}T{}H{}P{}N{}R{}{}{}{}".format(
+    *c[:6], "b" if c[6] else "", "i" if c[7] else "", "f" if c[8] else ""))
+def test_chunked_ssd_backward_matches_oracle(case, cuda_device):
+    B, T, H, P, N, R = case[:6]
+    print(f"chunked_ssd backward case {case}", flush=True)
+    ins = _inputs(case)
+    g = torch.Generator().manual_seed(1)
+    dy = torch.randn(B, T, H, P, R, generator=g, dtype=torch.float64)
+    dhf = torch.randn(B, H, P, N, generator=g, dtype=torch.float64) if case[8] else None
+    leaf = {k: (v.clone().requires_grad_() if v is not None else None) for k, v in ins.items()}
+    y, hf = ref.chunked_ssd(*[leaf[k] for k in NAMES[:9]], chunk_size=64, h_init=leaf["h_init"],
+                            return_final_state=True)
+    loss = (y * dy).sum() + ((hf * dhf).sum() if dhf is not None else 0.0)
+    loss.backward()
+    out, grads = _gpu_grads(ins, dy, dhf, cuda_device)
+    assert max_rel(out.y, y) < FP32_TOL
+    for k, gk in grads.items():
+        err = max_rel(gk, leaf[k].grad)
+        assert err < FP32_TOL, (k, err)
+        assert gk.dtype == torch.float32 and gk.shape == leaf[k].shape
+
+
+def test_chunked_ssd_backward_is_deterministic(cuda_device):
+    case = (2, 150, 2, 32, 64, 2, True, True, True)
+    B, T, H, P, N, R = case[:6]
+    ins = _inputs(case, seed=3)
+    g = torch.Generator().manual_seed(4)
+    dy = torch.randn(B, T, H, P, R, generator=g, dtype=torch.float64)
+    dhf = torch.randn(B, H, P, N, generator=g, dtype=torch.float64)
+    _, g1 = _gpu_grads(ins, dy, dhf, cuda_device)
+    _, g2 = _gpu_grads(ins, dy, dhf, cuda_device)
+    for k in g1:
+        assert torch.equal(g1[k], g2[k]), k
+
+
+def test_chunked_ssd_unsupported_rank_fails_before_the_forward(cuda_device):
+    x = torch.randn(1, 8, 1, 4, 3, device=cuda_device, requires_grad=True)
+    Bm = torch.randn(1, 8, 1, 8, 3, device=cuda_device)
+    with pytest.raises(RuntimeError, match="not supported"):
+        mamba3_amd.chunked_ssd(x, None, Bm, None, Bm, torch.rand(1, 8, 1, device=cuda_device),
+                               -torch.ones(1, device=cuda_device), torch.ones(1, device=cuda_device),
+                               x.detach())
+
+
+LAYER_KW = [
+    dict(d_model=64, d_state=16, headdim=16, mimo_rank=2),
+    dict(d_model=64, d_state=16, headdim=16, mimo_rank=2, use_trapezoidal=False),
+    dict(d_model=64, d_state=16, headdim=16, mimo_rank=2, use_complex_ssm=False),
+    dict(d_model=64, d_state=32, headdim=16, mimo_rank=4, ngroups=2),
+    dict(d_model=64, d_state=16, headdim=16, mimo_rank=1, use_trapezoidal=False,
+         use_complex_ssm=False),
+    dict(d_model=128, d_state=64, headdim=32, mimo_rank=2),
+]
+
+
+def _oracle_layer_grads(kw, layer, x, w, wh, dt_scale=None):
+    params = {k: v.detach().double().cpu().clone().requires_grad_()
+              for k, v in layer.state_dict().items()}
+    xr = x.detach().double().cpu().clone().requires_grad_()
+    ds = None if dt_scale is None else dt_scale.double().cpu()
+    out, st = ref.layer_forward(oracle_cfg(kw), params, xr, dt_scale=ds, return_state=True)
+    ((out * w.double().cpu()).sum() + (st["h"] * wh.double().cpu()).sum()).backward()
+    return out, {k: v.grad for k, v in params.items()}, xr.grad
+
+
+@pytest.mark.parametrize("kw", LAYER_KW, ids=lambda k: "-".join(f"{a}{b}" for a, b in k.items()))
+def test_layer_prefill_gradients_match_oracle(kw, cuda_device):
+    """Autograd through KulaMamba.prefill (torch element-wise prep in fp32 around the HIP
+    chunked_ssd forward and backward) against autograd through the fp64 oracle layer
+    (mamba3/mamba3.py:192-258), for every parameter and the input; the loss also reads the
+    returned state h."""
+    print(f"layer backward {kw}", flush=True)
+    torch.manual_seed(0)
+    layer = mamba3_amd.KulaMamba(**kw).to(cuda_device).train()
+    H, P, N = layer.nheads, layer.headdim, layer.d_state
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(2, 45, kw["d_model"], generator=g)
+    w = torch.randn(2, 45, kw["d_model"], generator=g)
+    wh = torch.randn(2, H, P, N, generator=g)
+    out_ref, pg, xg_ref = _oracle_layer_grads(kw, layer, x, w, wh)
+    xd = x.to(cuda_device).requires_grad_()
+    out, st = layer.prefill(xd)
+    ((out * w.to(cuda_device)).sum() + (st["h"] * wh.to(cuda_device)).sum()).backward()
+    assert max_rel(out, out_ref) < FP32_TOL
+    assert max_rel(xd.grad, xg_ref) < FP32_TOL
+    for name, p in layer.named_parameters():
+        err = max_rel(p.grad, pg[name])
+        assert err < FP32_TOL, (name, err)
+
+
+def test_layer_forward_gradients_with_dt_scale(cuda_device):
+    kw = dict(d_model=64, d_state=16, headdim=16, mimo_rank=2)
+    torch.manual_seed(0)
+    layer = mamba3_amd.KulaMamba(**kw).to(cuda_device).train()
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(1, 30, 64, generator=g)
+    w = torch.randn(1, 30, 64, generator=g)
+    ds = torch.rand(1, 30, layer.nheads, generator=g) + 0.5
+    wh = torch.zeros(1, layer.nheads, 16, 16)
+    out_ref, pg, xg_ref = _oracle_layer_grads(kw, layer, x, w, wh, dt_scale=ds)
+    xd = x.to(cuda_device).requires_grad_()
+    out = layer(xd, dt_scale=ds.to(cuda_device))
+    (out * w.to(cuda_device)).sum().backward()
+    assert max_rel(out, out_ref) < FP32_TOL
+    assert max_rel(xd.grad, xg_ref) < FP32_TOL
+    for name, p in layer.named_parameters():
+        assert max_rel(p.grad, pg[name]) < FP32_TOL, name
+
+
+def test_layer_bf16_gradients_match_fp32_oracle(cuda_device):
+    kw = dict(d_model=128, d_state=64, headdim=32, mimo_rank=2)
+    torch.manual_seed(0)
+    layer = mamba3_amd.KulaMamba(**kw).to(cuda_device, torch.bfloat16).train()
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(2, 70, 128, generator=g).bfloat16()
+    w = torch.randn(2, 70, 128, generator=g)
+    wh = torch.zeros(2, layer.nheads, 32, 64)
+    out_ref, pg, xg_ref = _oracle_layer_grads(kw, layer, x.float(), w, wh)
+    xd = x.to(cuda_device).requires_grad_()
+    out = layer(xd)
+    (out.float() * w.to(cuda_device)).sum().backward()
+    assert max_rel(out, out_ref) < BF16_TOL
+    assert max_rel(xd.grad, xg_ref) < BF16_TOL
+    for name, p in layer.named_parameters():
+        assert max_rel(p.grad, pg[name]) < BF16_TOL, name
+
+
+def test_lm_training_steps_reduce_the_loss(cuda_device):
+    """A few SGD steps of the LM through forward(ids, labels) (mamba3/block.py:168-178)
+    lower the loss on a fixed batch, with finite gradients everywhere."""
+    torch.manual_seed(0)
+    lm = mamba3_amd.KulaMambaLM(vocab_size=64, d_model=64, n_layers=2, d_state=16, headdim=16,
+                                mimo_rank=2).to(cuda_device).train()
+    opt = torch.optim.SGD(lm.parameters(), lr=0.05)
+    g = torch.Generator().manual_seed(7)
+    ids = torch.randint(0, 64, (2, 33), generator=g).to(cuda_device)
+    losses = []
+    for _ in range(6):
+        opt.zero_grad()
+        loss = lm(ids, labels=ids)["loss"]
+        loss.backward()
+        for p in lm.parameters():
+            assert p.grad is not None and torch.isfinite(p.grad).all()
+        opt.step()
+        losses.append(loss.item())
+    assert losses[-1] < losses[0] - 1e-3, losses
+
+
+def test_step_backward_raises_instead_of_wrong_gradients(cuda_device):
+    torch.manual_seed(0)
+    layer = mamba3_amd.KulaMamba(64, d_state=16, headdim=16).to(cuda_device).train()
+    st = layer.allocate_inference_state(1)
+    out, _ = layer.step(torch.randn(1, 64, device=cuda_device), st)
+    with pytest.raises(NotImplementedError):
+        out.sum().backward()

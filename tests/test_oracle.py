@@ -268,3 +268,58 @@ def test_trapezoid_collapse_identity():
     # agreement is bounded by the reference's fp32 decay cumsum
     assert torch.allclose(y, y_ref, atol=1e-6)
     assert torch.allclose(h, h_ref.double(), atol=1e-6)
+
+
+def _chunked_inputs(g, B, T, H, P, N, R, beta, with_init):
+    r = lambda *s: torch.randn(*s, generator=g, dtype=torch.float64)
+    ins = dict(x_g=r(B, T, H, P, R), x_b=r(B, T, H, P, R) if beta else None,
+               B_g=r(B, T, H, N, R), B_b=r(B, T, H, N, R) if beta else None,
+               C=r(B, T, H, N, R), dt=torch.rand(B, T, H, generator=g, dtype=torch.float64) * 0.5,
+               A=-torch.rand(H, generator=g, dtype=torch.float64) - 0.2, D=r(H),
+               x_raw=r(B, T, H, P, R), h_init=r(B, H, P, N) if with_init else None)
+    return {k: (v.requires_grad_() if v is not None else None) for k, v in ins.items()}
+
+
+def _grads(fn, ins, dy, dhf):
+    for v in ins.values():
+        if v is not None:
+            v.grad = None
+    y, hf = fn(ins)
+    ((y * dy).sum() + (hf * dhf).sum()).backward()
+    return {k: v.grad.clone() for k, v in ins.items() if v is not None and v.grad is not None}
+
+
+def test_chunked_gradients_of_the_oracle_equal_the_recurrence():
+    """Autograd through the oracle's chunked_ssd (factored cumsum, chunk states, scan;
+    mamba3/ssd.py:118-244) equals autograd through the independent per-token recurrence
+    for every input, including h_init and a dL/dh_final; chunks of 4 over a ragged T. A
+    recurrence that dropped the beta term must disagree."""
+    g = torch.Generator().manual_seed(11)
+    for (B, T, H, P, N, R, beta, with_init) in [(2, 11, 2, 3, 4, 2, True, True),
+                                                (1, 9, 1, 2, 6, 1, False, False),
+                                                (1, 7, 2, 3, 2, 4, True, False)]:
+        ins = _chunked_inputs(g, B, T, H, P, N, R, beta, with_init)
+        dy = torch.randn(B, T, H, P, R, generator=g, dtype=torch.float64)
+        dhf = torch.randn(B, H, P, N, generator=g, dtype=torch.float64)
+        chunk = lambda d: ref.chunked_ssd(*[d[k] for k in ("x_g", "x_b", "B_g", "B_b", "C", "dt", "A",
+                                                            "D", "x_raw")], chunk_size=4,
+                                          h_init=d["h_init"], return_final_state=True)
+        recur = lambda d: rec.chunked_recurrent(**d)
+        ga = _grads(chunk, ins, dy, dhf)
+        gb = _grads(recur, ins, dy, dhf)
+        for k in ga:
+            # the oracle, like the reference, takes the within-chunk cumsum in fp32
+            assert (ga[k] - gb[k]).abs().max() <= 1e-5 * gb[k].abs().max(), k
+        if beta:
+            nob = lambda d: rec.chunked_recurrent(**{**d, "x_b": None, "B_b": None})
+            gc = _grads(nob, ins, dy, dhf)
+            assert (gc["dt"] - gb["dt"]).abs().max() > 1e-3 * gb["dt"].abs().max()
+
+
+def test_chunked_recurrent_gradcheck():
+    """Finite differences pin the recurrence's gradients (torch.autograd.gradcheck)."""
+    g = torch.Generator().manual_seed(12)
+    ins = _chunked_inputs(g, 1, 5, 2, 2, 3, 2, True, True)
+    keys = [k for k, v in ins.items() if v is not None]
+    fn = lambda *vs: rec.chunked_recurrent(**dict(zip(keys, vs)))
+    assert torch.autograd.gradcheck(fn, tuple(ins[k] for k in keys), eps=1e-6, atol=1e-6)
