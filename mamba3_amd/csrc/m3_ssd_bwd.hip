@@ -39,9 +39,18 @@ constexpr int NTH = 256;  // threads per tile block
 struct Shape {
     int B, T, H, P, N, R, R2, Qb, K, nPt, nNt;
     int64_t PN;
-    __host__ __device__ int QR() const { return Qb * R; }
-    __host__ __device__ int QR2() const { return Qb * R2; }
+    int QR() const { return Qb * R; }
+    int QR2() const { return Qb * R2; }
 };
+
+// Chunk of QB = min(64, 128 / R2) tokens for rank R (R2 = 2R with the beta terms): score
+// tiles (t,r) x (s,j) of QR x QR2 <= 128 x 128.
+#define BW_CONSTS                                   \
+    constexpr int R2 = BETA ? 2 * R : R;            \
+    constexpr int QB = 128 / R2 >= 64 ? 64 : 128 / R2; \
+    constexpr int QR = QB * R, QR2 = QB * R2;       \
+    (void)QR;                                        \
+    (void)QR2;
 
 struct Args {
     Shape s;
@@ -69,18 +78,31 @@ struct Lds {
 
 // acc[i][j] += sum_k fa(4 ty + i, k) fb(k, 4 tx + j) over k < kdim, for the 64 x 64 tile of
 // a 256-thread block (tx = tid % 16, ty = tid / 16). fa / fb return 0 outside the operands.
+// The operands of step k0 + KT are loaded into registers while step k0 is multiplied.
 template <class FA, class FB>
 __device__ __forceinline__ void gemm_acc(float (&acc)[4][4], int kdim, FA fa, FB fb, Lds& l) {
     const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
-    for (int k0 = 0; k0 < kdim; k0 += KT) {
+    float ra[4], rb[4];
+    auto fetch = [&](int k0) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int e = tid + NTH * i, kk = e >> 6, mm = e & 63;
             const bool in = k0 + kk < kdim;
-            l.A[kk][mm] = in ? fa(mm, k0 + kk) : 0.f;
-            l.B[kk][mm] = in ? fb(k0 + kk, mm) : 0.f;
+            ra[i] = in ? fa(mm, k0 + kk) : 0.f;
+            rb[i] = in ? fb(k0 + kk, mm) : 0.f;
+        }
+    };
+    fetch(0);
+#pragma unroll 1
+    for (int k0 = 0; k0 < kdim; k0 += KT) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int e = tid + NTH * i, kk = e >> 6, mm = e & 63;
+            l.A[kk][mm] = ra[i];
+            l.B[kk][mm] = rb[i];
         }
         __syncthreads();
+        if (k0 + KT < kdim) fetch(k0 + KT);
 #pragma unroll
         for (int kk = 0; kk < KT; ++kk) {
             const float4 av = *reinterpret_cast<const float4*>(&l.A[kk][4 * ty]);
@@ -104,45 +126,50 @@ __device__ __forceinline__ void zero(float (&acc)[4][4]) {
 }
 
 // Accessors of chunk (b, k, h). Token positions at or past T read as 0.
+template <int R, bool BETA>
 struct Chunk {
+    static constexpr int R2 = BETA ? 2 * R : R;
+    static constexpr int QB = 128 / R2 >= 64 ? 64 : 128 / R2;
     const Args* a;
     int b, k, h;
-    __device__ bool real(int t) const { return k * a->s.Qb + t < a->s.T; }
+    __device__ bool real(int t) const { return k * QB + t < a->s.T; }
     __device__ float dtv(int t) const {
-        return real(t) ? a->dt[row(a->s, b, k * a->s.Qb + t, h)] : 0.f;
+        return real(t) ? a->dt[row(a->s, b, k * QB + t, h)] : 0.f;
     }
     // x factor j of token t (x_g for j < R, else x_b), without dt.
     __device__ float x(int t, int p, int j) const {
         const Shape& s = a->s;
         if (!real(t)) return 0.f;
-        const float* base = j < s.R ? a->xg : a->xb;
-        return base[row(s, b, k * s.Qb + t, h) * s.P * s.R + (int64_t)p * s.R + (j < s.R ? j : j - s.R)];
+        const float* base = j < R ? a->xg : a->xb;
+        return base[row(s, b, k * QB + t, h) * s.P * R + (int64_t)p * R + (j < R ? j : j - R)];
     }
     __device__ float bf(int t, int n, int j) const {
         const Shape& s = a->s;
         if (!real(t)) return 0.f;
-        const float* base = j < s.R ? a->Bg : a->Bb;
-        return base[row(s, b, k * s.Qb + t, h) * s.N * s.R + (int64_t)n * s.R + (j < s.R ? j : j - s.R)];
+        const float* base = j < R ? a->Bg : a->Bb;
+        return base[row(s, b, k * QB + t, h) * s.N * R + (int64_t)n * R + (j < R ? j : j - R)];
     }
     __device__ float c(int t, int n, int r) const {
         const Shape& s = a->s;
-        return real(t) ? a->C[row(s, b, k * s.Qb + t, h) * s.N * s.R + (int64_t)n * s.R + r] : 0.f;
+        return real(t) ? a->C[row(s, b, k * QB + t, h) * s.N * R + (int64_t)n * R + r] : 0.f;
     }
     __device__ float dy(int t, int p, int r) const {
         const Shape& s = a->s;
-        return real(t) ? a->dy[row(s, b, k * s.Qb + t, h) * s.P * s.R + (int64_t)p * s.R + r] : 0.f;
+        return real(t) ? a->dy[row(s, b, k * QB + t, h) * s.P * R + (int64_t)p * R + r] : 0.f;
     }
 };
 
 // ---- K0: c_t (inclusive cumsum of A dt within the chunk) and the chunk decays.
+template <int R, bool BETA>
 __global__ __launch_bounds__(64) void bwd_cum(Args a) {
+    BW_CONSTS
     const Shape& s = a.s;
     const int ch = blockIdx.x, h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
-    const int t = threadIdx.x, tg = k * s.Qb + t;
-    const float l = (t < s.Qb && tg < s.T) ? a.A[h] * a.dt[row(s, b, tg, h)] : 0.f;
+    const int t = threadIdx.x, tg = k * QB + t;
+    const float l = (t < QB && tg < s.T) ? a.A[h] * a.dt[row(s, b, tg, h)] : 0.f;
     const float c = wave_incl_scan(l);
-    if (t < s.Qb) a.cum[(int64_t)ch * s.Qb + t] = c;
-    if (t == s.Qb - 1) {
+    if (t < QB) a.cum[(int64_t)ch * QB + t] = c;
+    if (t == QB - 1) {
         a.dec[chx(s, b, k, h)] = __expf(c);
         if (k == s.K - 1) a.dec[chx(s, b, s.K, h)] = 1.f;
     }
@@ -152,28 +179,30 @@ __global__ __launch_bounds__(64) void bwd_cum(Args a) {
 //   hext[k][p,n] = sum_{s,j} exp(c_end - c_s) Xf[s,p,j] Bf[s,n,j]
 //   gext[k][p,n] = sum_{t,r} exp(c_t) dy[t,p,r] C[t,n,r]
 // plus the extra chunk K: hext = 0, gext = dL/dh_final (or 0).
+template <int R, bool BETA>
 __global__ __launch_bounds__(NTH) void bwd_states(Args a) {
+    BW_CONSTS
     __shared__ Lds l;
     __shared__ float cs[64];
     const Shape& s = a.s;
     const int ch = blockIdx.x, h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
     const int pt = blockIdx.y / s.nNt, nt = blockIdx.y % s.nNt;
     const int p0 = pt * TT, n0 = nt * TT;
-    const Chunk q{&a, b, k, h};
-    if (threadIdx.x < s.Qb) cs[threadIdx.x] = a.cum[(int64_t)ch * s.Qb + threadIdx.x];
+    const Chunk<R, BETA> q{&a, b, k, h};
+    if (threadIdx.x < QB) cs[threadIdx.x] = a.cum[(int64_t)ch * QB + threadIdx.x];
     __syncthreads();
-    const float cend = cs[s.Qb - 1];
+    const float cend = cs[QB - 1];
     const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
     float acc[4][4];
     zero(acc);
-    gemm_acc(acc, s.Qb * s.R2,
+    gemm_acc(acc, QB * R2,
              [&](int mm, int j) {
-                 const int p = p0 + mm, t = j / s.R2;
-                 return p < s.P ? __expf(cend - cs[t]) * q.dtv(t) * q.x(t, p, j % s.R2) : 0.f;
+                 const int p = p0 + mm, t = j / R2;
+                 return p < s.P ? __expf(cend - cs[t]) * q.dtv(t) * q.x(t, p, j % R2) : 0.f;
              },
              [&](int j, int nn) {
                  const int n = n0 + nn;
-                 return n < s.N ? q.bf(j / s.R2, n, j % s.R2) : 0.f;
+                 return n < s.N ? q.bf(j / R2, n, j % R2) : 0.f;
              },
              l);
     float* ho = a.hext + chx(s, b, k, h) * s.PN;
@@ -185,14 +214,14 @@ __global__ __launch_bounds__(NTH) void bwd_states(Args a) {
             if (p < s.P && n < s.N) ho[(int64_t)p * s.N + n] = acc[i][j];
         }
     zero(acc);
-    gemm_acc(acc, s.Qb * s.R,
+    gemm_acc(acc, QB * R,
              [&](int mm, int j) {
-                 const int p = p0 + mm, t = j / s.R;
-                 return p < s.P ? __expf(cs[t]) * q.dy(t, p, j % s.R) : 0.f;
+                 const int p = p0 + mm, t = j / R;
+                 return p < s.P ? __expf(cs[t]) * q.dy(t, p, j % R) : 0.f;
              },
              [&](int j, int nn) {
                  const int n = n0 + nn;
-                 return n < s.N ? q.c(j / s.R, n, j % s.R) : 0.f;
+                 return n < s.N ? q.c(j / R, n, j % R) : 0.f;
              },
              l);
     float* go = a.gext + chx(s, b, k, h) * s.PN;
@@ -223,21 +252,22 @@ __global__ __launch_bounds__(NTH) void bwd_states(Args a) {
 
 // ---- K1: masked scores M = W o G and DM = W o DX of the chunk, and the intra-chunk part of
 // dc: sum_s W Z[t,s] - sum_t' W Z[t',t]. One block per chunk, looping over its tiles.
+template <int R, bool BETA>
 __global__ __launch_bounds__(NTH) void bwd_scores(Args a) {
+    BW_CONSTS
     __shared__ Lds l;
     __shared__ float zp[TT][TT + 1];
     __shared__ float cs[64], rowacc[64], colacc[64];
     const Shape& s = a.s;
     const int ch = blockIdx.x, h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
-    const Chunk q{&a, b, k, h};
+    const Chunk<R, BETA> q{&a, b, k, h};
     const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
     if (tid < 64) {
-        cs[tid] = tid < s.Qb ? a.cum[(int64_t)ch * s.Qb + tid] : 0.f;
+        cs[tid] = tid < QB ? a.cum[(int64_t)ch * QB + tid] : 0.f;
         rowacc[tid] = 0.f;
         colacc[tid] = 0.f;
     }
     __syncthreads();
-    const int QR = s.QR(), QR2 = s.QR2();
     float* Mo = a.M + (int64_t)ch * QR * QR2;
     float* DMo = a.DM + (int64_t)ch * QR * QR2;
     for (int m0 = 0; m0 < QR; m0 += TT) {
@@ -247,15 +277,15 @@ __global__ __launch_bounds__(NTH) void bwd_scores(Args a) {
             zero(d);
             // G[(t,r),(s,j)] = sum_n C[t,n,r] Bf[s,n,j]
             gemm_acc(g, s.N,
-                     [&](int mm, int n) { const int m = m0 + mm; return q.c(m / s.R, n, m % s.R); },
-                     [&](int n, int cc) { const int c = c0 + cc; return q.bf(c / s.R2, n, c % s.R2); },
+                     [&](int mm, int n) { const int m = m0 + mm; return q.c(m / R, n, m % R); },
+                     [&](int n, int cc) { const int c = c0 + cc; return q.bf(c / R2, n, c % R2); },
                      l);
             // DX[(t,r),(s,j)] = sum_p dy[t,p,r] dt_s x[s,p,j]
             gemm_acc(d, s.P,
-                     [&](int mm, int p) { const int m = m0 + mm; return q.dy(m / s.R, p, m % s.R); },
+                     [&](int mm, int p) { const int m = m0 + mm; return q.dy(m / R, p, m % R); },
                      [&](int p, int cc) {
-                         const int c = c0 + cc, t = c / s.R2;
-                         return q.dtv(t) * q.x(t, p, c % s.R2);
+                         const int c = c0 + cc, t = c / R2;
+                         return q.dtv(t) * q.x(t, p, c % R2);
                      },
                      l);
 #pragma unroll
@@ -263,7 +293,7 @@ __global__ __launch_bounds__(NTH) void bwd_scores(Args a) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const int m = m0 + 4 * ty + i, c = c0 + 4 * tx + j;
-                    const int t = m / s.R, u = c / s.R2;
+                    const int t = m / R, u = c / R2;
                     const float w = u <= t ? __expf(cs[t] - cs[u]) : 0.f;
                     Mo[(int64_t)m * QR2 + c] = w * g[i][j];
                     DMo[(int64_t)m * QR2 + c] = w * d[i][j];
@@ -271,25 +301,25 @@ __global__ __launch_bounds__(NTH) void bwd_scores(Args a) {
                 }
             __syncthreads();
             // Z over the (r, j) blocks of the tile, summed into rows (t) and columns (s).
-            const int nt = TT / s.R, ns = TT / s.R2;
+            const int nt = TT / R, ns = TT / R2;
             if (tid < nt) {
                 float v = 0.f;
                 for (int u = 0; u < ns; ++u)
-                    for (int r = 0; r < s.R; ++r)
-                        for (int j = 0; j < s.R2; ++j) v += zp[tid * s.R + r][u * s.R2 + j];
-                rowacc[m0 / s.R + tid] += v;
+                    for (int r = 0; r < R; ++r)
+                        for (int j = 0; j < R2; ++j) v += zp[tid * R + r][u * R2 + j];
+                rowacc[m0 / R + tid] += v;
             } else if (tid >= 128 && tid < 128 + ns) {
                 const int u = tid - 128;
                 float v = 0.f;
                 for (int t = 0; t < nt; ++t)
-                    for (int r = 0; r < s.R; ++r)
-                        for (int j = 0; j < s.R2; ++j) v += zp[t * s.R + r][u * s.R2 + j];
-                colacc[c0 / s.R2 + u] += v;
+                    for (int r = 0; r < R; ++r)
+                        for (int j = 0; j < R2; ++j) v += zp[t * R + r][u * R2 + j];
+                colacc[c0 / R2 + u] += v;
             }
             __syncthreads();
         }
     }
-    if (tid < s.Qb) a.dcI[(int64_t)ch * s.Qb + tid] = rowacc[tid] - colacc[tid];
+    if (tid < QB) a.dcI[(int64_t)ch * QB + tid] = rowacc[tid] - colacc[tid];
 }
 
 // Sums v over the rows of the 64 x 64 tile that belong to one token (R2 consecutive rows per
@@ -312,7 +342,9 @@ __device__ __forceinline__ void tile_token_sums(const float (&v)[4], int per, fl
 
 // ---- K3: dXf rows (s,j) x columns p; writes dx_g / dx_b = dt_s dXf and the per-token
 // partials q_s (state term . Xf) and sum_{p,j} dXf x.
+template <int R, bool BETA>
 __global__ __launch_bounds__(NTH) void bwd_dxf(Args a) {
+    BW_CONSTS
     __shared__ Lds l;
     __shared__ float red[TT][17];
     __shared__ float cs[64], outv[64];
@@ -320,22 +352,22 @@ __global__ __launch_bounds__(NTH) void bwd_dxf(Args a) {
     const int ch = blockIdx.x, h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
     const int rt = blockIdx.y / s.nPt, pt = blockIdx.y % s.nPt;
     const int m0 = rt * TT, p0 = pt * TT;
-    const Chunk q{&a, b, k, h};
+    const Chunk<R, BETA> q{&a, b, k, h};
     const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
-    if (tid < s.Qb) cs[tid] = a.cum[(int64_t)ch * s.Qb + tid];
+    if (tid < QB) cs[tid] = a.cum[(int64_t)ch * QB + tid];
     __syncthreads();
-    const float cend = cs[s.Qb - 1];
+    const float cend = cs[QB - 1];
     const float* dH = a.dch + chx(s, b, k, h) * s.PN;
     float acc[4][4];
     zero(acc);
     gemm_acc(acc, s.N,
-             [&](int mm, int n) { const int m = m0 + mm; return q.bf(m / s.R2, n, m % s.R2); },
+             [&](int mm, int n) { const int m = m0 + mm; return q.bf(m / R2, n, m % R2); },
              [&](int n, int pp) { const int p = p0 + pp; return p < s.P ? dH[(int64_t)p * s.N + n] : 0.f; },
              l);
     float xv[4][4], rv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int m = m0 + 4 * ty + i, t = m / s.R2, j = m % s.R2;
+        const int m = m0 + 4 * ty + i, t = m / R2, j = m % R2;
         const float e = __expf(cend - cs[t]), d = q.dtv(t);
         rv[i] = 0.f;
 #pragma unroll
@@ -346,89 +378,93 @@ __global__ __launch_bounds__(NTH) void bwd_dxf(Args a) {
             rv[i] += d * xv[i][jj] * acc[i][jj];
         }
     }
-    const int per = s.R2, nts = TT / per;
+    const int per = R2, nts = TT / per;
     tile_token_sums(rv, per, red, outv);
-    if (tid < nts) a.pState[((int64_t)ch * s.nPt + pt) * s.Qb + m0 / per + tid] = outv[tid];
-    const float* Mi = a.M + (int64_t)ch * s.QR() * s.QR2();
-    gemm_acc(acc, s.QR(),
-             [&](int mm, int jr) { return Mi[(int64_t)jr * s.QR2() + m0 + mm]; },
+    if (tid < nts) a.pState[((int64_t)ch * s.nPt + pt) * QB + m0 / per + tid] = outv[tid];
+    const float* Mi = a.M + (int64_t)ch * QR * QR2;
+    gemm_acc(acc, QR,
+             [&](int mm, int jr) { return Mi[(int64_t)jr * QR2 + m0 + mm]; },
              [&](int jr, int pp) {
                  const int p = p0 + pp;
-                 return p < s.P ? q.dy(jr / s.R, p, jr % s.R) : 0.f;
+                 return p < s.P ? q.dy(jr / R, p, jr % R) : 0.f;
              },
              l);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int m = m0 + 4 * ty + i, t = m / s.R2, j = m % s.R2;
+        const int m = m0 + 4 * ty + i, t = m / R2, j = m % R2;
         const float d = q.dtv(t);
         rv[i] = 0.f;
         const bool w = q.real(t);
-        float* out = j < s.R ? a.dxg : a.dxb;
-        const int64_t base = row(s, b, k * s.Qb + t, h) * s.P * s.R + (j < s.R ? j : j - s.R);
+        float* out = j < R ? a.dxg : a.dxb;
+        const int64_t base = row(s, b, k * QB + t, h) * s.P * R + (j < R ? j : j - R);
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
             const int p = p0 + 4 * tx + jj;
             rv[i] += acc[i][jj] * xv[i][jj];
-            if (w && p < s.P) out[base + (int64_t)p * s.R] = d * acc[i][jj];
+            if (w && p < s.P) out[base + (int64_t)p * R] = d * acc[i][jj];
         }
     }
     tile_token_sums(rv, per, red, outv);
-    if (tid < nts) a.pDt[((int64_t)ch * s.nPt + pt) * s.Qb + m0 / per + tid] = outv[tid];
+    if (tid < nts) a.pDt[((int64_t)ch * s.nPt + pt) * QB + m0 / per + tid] = outv[tid];
 }
 
 // ---- K4: dBf rows (s,j) x columns n; writes dB_g / dB_b.
+template <int R, bool BETA>
 __global__ __launch_bounds__(NTH) void bwd_dbf(Args a) {
+    BW_CONSTS
     __shared__ Lds l;
     __shared__ float cs[64];
     const Shape& s = a.s;
     const int ch = blockIdx.x, h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
     const int rt = blockIdx.y / s.nNt, nt = blockIdx.y % s.nNt;
     const int m0 = rt * TT, n0 = nt * TT;
-    const Chunk q{&a, b, k, h};
+    const Chunk<R, BETA> q{&a, b, k, h};
     const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
-    if (tid < s.Qb) cs[tid] = a.cum[(int64_t)ch * s.Qb + tid];
+    if (tid < QB) cs[tid] = a.cum[(int64_t)ch * QB + tid];
     __syncthreads();
-    const float cend = cs[s.Qb - 1];
+    const float cend = cs[QB - 1];
     const float* dH = a.dch + chx(s, b, k, h) * s.PN;
     float acc[4][4];
     zero(acc);
     gemm_acc(acc, s.P,
              [&](int mm, int p) {
-                 const int m = m0 + mm, t = m / s.R2;
-                 return q.dtv(t) * q.x(t, p, m % s.R2);
+                 const int m = m0 + mm, t = m / R2;
+                 return q.dtv(t) * q.x(t, p, m % R2);
              },
              [&](int p, int nn) { const int n = n0 + nn; return n < s.N ? dH[(int64_t)p * s.N + n] : 0.f; },
              l);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const float e = __expf(cend - cs[(m0 + 4 * ty + i) / s.R2]);
+        const float e = __expf(cend - cs[(m0 + 4 * ty + i) / R2]);
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] *= e;
     }
-    const float* DMi = a.DM + (int64_t)ch * s.QR() * s.QR2();
-    gemm_acc(acc, s.QR(),
-             [&](int mm, int jr) { return DMi[(int64_t)jr * s.QR2() + m0 + mm]; },
+    const float* DMi = a.DM + (int64_t)ch * QR * QR2;
+    gemm_acc(acc, QR,
+             [&](int mm, int jr) { return DMi[(int64_t)jr * QR2 + m0 + mm]; },
              [&](int jr, int nn) {
                  const int n = n0 + nn;
-                 return n < s.N ? q.c(jr / s.R, n, jr % s.R) : 0.f;
+                 return n < s.N ? q.c(jr / R, n, jr % R) : 0.f;
              },
              l);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int m = m0 + 4 * ty + i, t = m / s.R2, j = m % s.R2;
+        const int m = m0 + 4 * ty + i, t = m / R2, j = m % R2;
         if (!q.real(t)) continue;
-        float* out = j < s.R ? a.dBg : a.dBb;
-        const int64_t base = row(s, b, k * s.Qb + t, h) * s.N * s.R + (j < s.R ? j : j - s.R);
+        float* out = j < R ? a.dBg : a.dBb;
+        const int64_t base = row(s, b, k * QB + t, h) * s.N * R + (j < R ? j : j - R);
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
             const int n = n0 + 4 * tx + jj;
-            if (n < s.N) out[base + (int64_t)n * s.R] = acc[i][jj];
+            if (n < s.N) out[base + (int64_t)n * R] = acc[i][jj];
         }
     }
 }
 
 // ---- K5: dC rows (t,r) x columns n, and the per-token partials sum_{n,r} C dC_inter.
+template <int R, bool BETA>
 __global__ __launch_bounds__(NTH) void bwd_dc(Args a) {
+    BW_CONSTS
     __shared__ Lds l;
     __shared__ float red[TT][17];
     __shared__ float cs[64], outv[64];
@@ -436,21 +472,21 @@ __global__ __launch_bounds__(NTH) void bwd_dc(Args a) {
     const int ch = blockIdx.x, h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
     const int rt = blockIdx.y / s.nNt, nt = blockIdx.y % s.nNt;
     const int m0 = rt * TT, n0 = nt * TT;
-    const Chunk q{&a, b, k, h};
+    const Chunk<R, BETA> q{&a, b, k, h};
     const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
-    if (tid < s.Qb) cs[tid] = a.cum[(int64_t)ch * s.Qb + tid];
+    if (tid < QB) cs[tid] = a.cum[(int64_t)ch * QB + tid];
     __syncthreads();
     const float* Hk = a.Hs + chx(s, b, k, h) * s.PN;
     float acc[4][4];
     zero(acc);
     gemm_acc(acc, s.P,
-             [&](int mm, int p) { const int m = m0 + mm; return q.dy(m / s.R, p, m % s.R); },
+             [&](int mm, int p) { const int m = m0 + mm; return q.dy(m / R, p, m % R); },
              [&](int p, int nn) { const int n = n0 + nn; return n < s.N ? Hk[(int64_t)p * s.N + n] : 0.f; },
              l);
     float rv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int m = m0 + 4 * ty + i, t = m / s.R, r = m % s.R;
+        const int m = m0 + 4 * ty + i, t = m / R, r = m % R;
         const float e = __expf(cs[t]);
         rv[i] = 0.f;
 #pragma unroll
@@ -460,62 +496,64 @@ __global__ __launch_bounds__(NTH) void bwd_dc(Args a) {
             if (n < s.N) rv[i] += q.c(t, n, r) * acc[i][j];
         }
     }
-    const int per = s.R, nts = TT / per;
+    const int per = R, nts = TT / per;
     tile_token_sums(rv, per, red, outv);
-    if (tid < nts) a.pInter[((int64_t)ch * s.nNt + nt) * s.Qb + m0 / per + tid] = outv[tid];
-    const float* DMi = a.DM + (int64_t)ch * s.QR() * s.QR2();
-    gemm_acc(acc, s.QR2(),
-             [&](int mm, int jc) { return DMi[(int64_t)(m0 + mm) * s.QR2() + jc]; },
+    if (tid < nts) a.pInter[((int64_t)ch * s.nNt + nt) * QB + m0 / per + tid] = outv[tid];
+    const float* DMi = a.DM + (int64_t)ch * QR * QR2;
+    gemm_acc(acc, QR2,
+             [&](int mm, int jc) { return DMi[(int64_t)(m0 + mm) * QR2 + jc]; },
              [&](int jc, int nn) {
                  const int n = n0 + nn;
-                 return n < s.N ? q.bf(jc / s.R2, n, jc % s.R2) : 0.f;
+                 return n < s.N ? q.bf(jc / R2, n, jc % R2) : 0.f;
              },
              l);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int m = m0 + 4 * ty + i, t = m / s.R, r = m % s.R;
+        const int m = m0 + 4 * ty + i, t = m / R, r = m % R;
         if (!q.real(t)) continue;
-        const int64_t base = row(s, b, k * s.Qb + t, h) * s.N * s.R + r;
+        const int64_t base = row(s, b, k * QB + t, h) * s.N * R + r;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int n = n0 + 4 * tx + j;
-            if (n < s.N) a.dC[base + (int64_t)n * s.R] = acc[i][j];
+            if (n < s.N) a.dC[base + (int64_t)n * R] = acc[i][j];
         }
     }
 }
 
 // ---- K6: per chunk: dc -> d(A dt) (suffix sums), ddt, the chunk's partials of dA and dD,
 // and dx_raw = D dy.
+template <int R, bool BETA>
 __global__ __launch_bounds__(NTH) void bwd_tokens(Args a) {
+    BW_CONSTS
     __shared__ float dcs[64], part[NTH];
     const Shape& s = a.s;
     const int ch = blockIdx.x, h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
-    const Chunk q{&a, b, k, h};
+    const Chunk<R, BETA> q{&a, b, k, h};
     const int tid = threadIdx.x;
     if (tid < 64) {
         const int t = tid;
         float dc = 0.f, qs = 0.f;
-        if (t < s.Qb) {
-            dc = a.dcI[(int64_t)ch * s.Qb + t];
-            for (int nt = 0; nt < s.nNt; ++nt) dc += a.pInter[((int64_t)ch * s.nNt + nt) * s.Qb + t];
-            for (int pt = 0; pt < s.nPt; ++pt) qs += a.pState[((int64_t)ch * s.nPt + pt) * s.Qb + t];
+        if (t < QB) {
+            dc = a.dcI[(int64_t)ch * QB + t];
+            for (int nt = 0; nt < s.nNt; ++nt) dc += a.pInter[((int64_t)ch * s.nNt + nt) * QB + t];
+            for (int pt = 0; pt < s.nPt; ++pt) qs += a.pState[((int64_t)ch * s.nPt + pt) * QB + t];
             dc -= qs;
         }
         const float qtot = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
                                                          __builtin_bit_cast(int, wave_incl_scan(qs)), 63));
-        if (t == s.Qb - 1) dc += qtot + a.dec[chx(s, b, k, h)] * a.ddec[chx(s, b, k, h)];
+        if (t == QB - 1) dc += qtot + a.dec[chx(s, b, k, h)] * a.ddec[chx(s, b, k, h)];
         dcs[t] = dc;
     }
     __syncthreads();
     if (tid < 64) {
         const int t = tid;
         float dl = 0.f;
-        for (int u = s.Qb - 1; u >= t; --u) dl += dcs[u];
+        for (int u = QB - 1; u >= t; --u) dl += dcs[u];
         float contrib = 0.f;
-        if (t < s.Qb && q.real(t)) {
+        if (t < QB && q.real(t)) {
             float pd = 0.f;
-            for (int pt = 0; pt < s.nPt; ++pt) pd += a.pDt[((int64_t)ch * s.nPt + pt) * s.Qb + t];
-            a.ddt[row(s, b, k * s.Qb + t, h)] = a.A[h] * dl + pd;
+            for (int pt = 0; pt < s.nPt; ++pt) pd += a.pDt[((int64_t)ch * s.nPt + pt) * QB + t];
+            a.ddt[row(s, b, k * QB + t, h)] = a.A[h] * dl + pd;
             contrib = q.dtv(t) * dl;
         }
         const float tot = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
@@ -524,12 +562,12 @@ __global__ __launch_bounds__(NTH) void bwd_tokens(Args a) {
     }
     // dD partial and dx_raw over the chunk's real tokens.
     const float Dh = a.D[h];
-    const int nreal = min(s.Qb, s.T - k * s.Qb);
-    const int per_tok = s.P * s.R;
+    const int nreal = min(QB, s.T - k * QB);
+    const int per_tok = s.P * R;
     float v = 0.f;
     for (int e = tid; e < nreal * per_tok; e += NTH) {
         const int t = e / per_tok, pr = e % per_tok;
-        const int64_t o = row(s, b, k * s.Qb + t, h) * per_tok + pr;
+        const int64_t o = row(s, b, k * QB + t, h) * per_tok + pr;
         const float g = a.dy[o];
         v += g * a.xr[o];
         a.dxr[o] = Dh * g;
@@ -582,8 +620,7 @@ inline size_t al(size_t x) { return (x + 255) & ~(size_t)255; }
 bool make_shape(int B, int T, int H, int P, int N, int R, bool beta, Shape& s) {
     if (R != 1 && R != 2 && R != 4 && R != 8) return false;
     s.B = B, s.T = T, s.H = H, s.P = P, s.N = N, s.R = R, s.R2 = beta ? 2 * R : R;
-    s.Qb = 64;
-    while (s.Qb * s.R2 > 128) s.Qb /= 2;
+    s.Qb = 128 / s.R2 >= 64 ? 64 : 128 / s.R2;  // as BW_CONSTS
     s.K = (T + s.Qb - 1) / s.Qb;
     s.nPt = (P + TT - 1) / TT;
     s.nNt = (N + TT - 1) / TT;
@@ -616,6 +653,27 @@ Plan make_plan(const Shape& s) {
     o += al(scan_bwd_workspace(s.B, s.K + 1, s.H, s.PN));
     pl.total = o;
     return pl;
+}
+
+template <int R, bool BETA>
+int launch(const Args& a, const float* h_init, float* dh_init, float* scan_ws, hipStream_t stream) {
+    BW_CONSTS
+    const Shape& s = a.s;
+    const unsigned nch = (unsigned)((int64_t)s.B * s.K * s.H);
+    constexpr int nRt = QR / TT, nRt2 = QR2 / TT;
+    hipLaunchKernelGGL((bwd_cum<R, BETA>), dim3(nch), dim3(64), 0, stream, a);
+    hipLaunchKernelGGL((bwd_states<R, BETA>), dim3(nch, s.nPt * s.nNt), dim3(NTH), 0, stream, a);
+    if (launch_scan_fwd(a.dec, a.hext, h_init, a.Hs, s.B, s.K + 1, s.H, s.PN, stream) != 0) return 1;
+    if (launch_scan_bwd(a.dec, a.Hs, a.gext, a.ddec, a.dch, dh_init, scan_ws, s.B, s.K + 1, s.H,
+                        s.PN, stream) != 0)
+        return 1;
+    hipLaunchKernelGGL((bwd_scores<R, BETA>), dim3(nch), dim3(NTH), 0, stream, a);
+    hipLaunchKernelGGL((bwd_dxf<R, BETA>), dim3(nch, nRt2 * s.nPt), dim3(NTH), 0, stream, a);
+    hipLaunchKernelGGL((bwd_dbf<R, BETA>), dim3(nch, nRt2 * s.nNt), dim3(NTH), 0, stream, a);
+    hipLaunchKernelGGL((bwd_dc<R, BETA>), dim3(nch, nRt * s.nNt), dim3(NTH), 0, stream, a);
+    hipLaunchKernelGGL((bwd_tokens<R, BETA>), dim3(nch), dim3(NTH), 0, stream, a);
+    hipLaunchKernelGGL(bwd_reduce, dim3(s.H), dim3(NTH), 0, stream, a);
+    return hipGetLastError() == hipSuccess ? 0 : 1;
 }
 
 }  // namespace bw
@@ -658,21 +716,18 @@ int launch_chunked_bwd(int B, int T, int H, int P, int N, int R, const float* x_
     a.pInter = part(10), a.pState = part(11), a.pDt = part(12), a.pA = part(13), a.pD = part(14);
     float* scan_ws = reinterpret_cast<float*>(ws + pl.scan_off);
 
-    const unsigned nch = (unsigned)((int64_t)s.B * s.K * s.H);
-    const int nRt = s.QR() / TT, nRt2 = s.QR2() / TT;
-    hipLaunchKernelGGL(bwd_cum, dim3(nch), dim3(64), 0, stream, a);
-    hipLaunchKernelGGL(bwd_states, dim3(nch, s.nPt * s.nNt), dim3(NTH), 0, stream, a);
-    if (launch_scan_fwd(a.dec, a.hext, h_init, a.Hs, s.B, s.K + 1, s.H, s.PN, stream) != 0) return 1;
-    if (launch_scan_bwd(a.dec, a.Hs, a.gext, a.ddec, a.dch, dh_init, scan_ws, s.B, s.K + 1, s.H,
-                        s.PN, stream) != 0)
-        return 1;
-    hipLaunchKernelGGL(bwd_scores, dim3(nch), dim3(NTH), 0, stream, a);
-    hipLaunchKernelGGL(bwd_dxf, dim3(nch, nRt2 * s.nPt), dim3(NTH), 0, stream, a);
-    hipLaunchKernelGGL(bwd_dbf, dim3(nch, nRt2 * s.nNt), dim3(NTH), 0, stream, a);
-    hipLaunchKernelGGL(bwd_dc, dim3(nch, nRt * s.nNt), dim3(NTH), 0, stream, a);
-    hipLaunchKernelGGL(bwd_tokens, dim3(nch), dim3(NTH), 0, stream, a);
-    hipLaunchKernelGGL(bwd_reduce, dim3(s.H), dim3(NTH), 0, stream, a);
-    return hipGetLastError() == hipSuccess ? 0 : 1;
+    const bool beta = x_b != nullptr;
+    switch (R * 2 + (beta ? 1 : 0)) {
+        case 2: return launch<1, false>(a, h_init, dh_init, scan_ws, stream);
+        case 3: return launch<1, true>(a, h_init, dh_init, scan_ws, stream);
+        case 4: return launch<2, false>(a, h_init, dh_init, scan_ws, stream);
+        case 5: return launch<2, true>(a, h_init, dh_init, scan_ws, stream);
+        case 8: return launch<4, false>(a, h_init, dh_init, scan_ws, stream);
+        case 9: return launch<4, true>(a, h_init, dh_init, scan_ws, stream);
+        case 16: return launch<8, false>(a, h_init, dh_init, scan_ws, stream);
+        case 17: return launch<8, true>(a, h_init, dh_init, scan_ws, stream);
+        default: return 1;
+    }
 }
 
 }  // namespace m3
