@@ -24,6 +24,8 @@ the same format:
                   decay (8, 128, 24), h_chunk (8, 128, 24, 64*128) and h_init, fp32: GB/s.
   scan_d2048      the same at the d_model 2048 shape: (2, 256, 32, 128*256).
   scan_bwd_d768   the scan's backward (m3_scan_bwd) at the scan_d768 shape: GB/s.
+  ssd_bwd_d768    the chunked SSD's backward (m3_chunked_ssd_bwd, fp32) at the d_model 768
+                  prefill shape (8, 8192): tokens/s, roofline over the call's GEMM FLOPs.
 
 Prints ONE JSON line. `value` is SSD prefill tokens/s; `roofline` is the fused SSD kernel
 against the bf16 MFMA peak with the algorithmic FLOP count
@@ -323,7 +325,85 @@ def bench_scan_bwd(args, torch, shape, name):
     return res
 
 
-WORKLOADS = {"prefill_d2048": bench_prefill_d2048, "layer_fp32_d768": bench_layer_fp32_d768,
+def bwd_flops_per_chunk(P, N, R, beta):
+    """GEMM FLOPs of m3_chunked_ssd_bwd per (batch, head, chunk of Qb = min(64, 128/R2)
+    tokens), R2 = 2R with the beta terms: chunk states and their y_inter gradient
+    2PN(QR + QR2), scores 2 QR QR2 (N + P), dXf 2 QR2 P (N + QR), dBf 2 QR2 N (P + QR),
+    dC 2 QR N (P + QR2), with QR = Qb R, QR2 = Qb R2."""
+    R2 = 2 * R if beta else R
+    qb = min(64, 128 // R2)
+    qr, qr2 = qb * R, qb * R2
+    f = 2 * P * N * (qr + qr2) + 2 * qr * qr2 * (N + P) + 2 * qr2 * P * (N + qr)
+    f += 2 * qr2 * N * (P + qr) + 2 * qr * N * (P + qr2)
+    return qb, f
+
+
+def bench_ssd_bwd(args, torch, mamba3_amd):
+    """m3_chunked_ssd_bwd (the chunked SSD's backward, fp32) on resident inputs of the
+    d_model 768 layer at the prefill shape: x_g, x_b, x_raw, dy (8, 8192, 24, 64, 2),
+    B_g, B_b, C (8, 8192, 24, 128, 2), dt in [1e-3, 0.1], A = -exp(U(-4, -1)), dL/dh_final."""
+    import ctypes
+    from mamba3_amd import _native
+    dev = torch.device("cuda:0")
+    B, T, H = BATCH, SEQLEN, D_MODEL * EXPAND // P
+    g = torch.Generator().manual_seed(9)
+    rn = lambda *s: torch.randn(*s, generator=g).to(dev)
+    xg, xb, xr, dy = (rn(B, T, H, P, R) for _ in range(4))
+    Bg, Bb, C = (rn(B, T, H, N, R) for _ in range(3))
+    dt = torch.exp(torch.rand(B, T, H, generator=g) * (2.303 * 2) - 6.908).to(dev)
+    A = -torch.exp(torch.rand(H, generator=g) * 3 - 4).to(dev)
+    D = torch.ones(H, device=dev)
+    dhf = rn(B, H, P, N)
+    outs = [torch.empty_like(xg), torch.empty_like(xb), torch.empty_like(Bg), torch.empty_like(Bb),
+            torch.empty_like(C), torch.empty_like(dt), torch.empty(H, device=dev),
+            torch.empty(H, device=dev), torch.empty_like(xr), None]
+    nbytes_ws = _native.chunked_bwd_workspace_bytes(B, T, H, P, N, R, True)
+    ws = torch.empty(nbytes_ws, dtype=torch.uint8, device=dev)
+    lib = _native.lib()
+    ptr = _native.ptr
+    argv = [B, T, H, P, N, R, *map(ptr, (xg, xb, Bg, Bb, C, dt, A, D, xr)), None, ptr(dy),
+            ptr(dhf), *map(ptr, outs), ptr(ws), nbytes_ws]
+
+    def call():
+        _native.check(lib.m3_chunked_ssd_bwd(*argv, _native.stream_of(xg)), "m3_chunked_ssd_bwd")
+
+    wall, kern_ms = time_events(torch, call, args.steps, args.warmup)
+    ms = wall * 1e3 / args.steps
+    qb, f_chunk = bwd_flops_per_chunk(P, N, R, True)
+    flops = B * H * ((T + qb - 1) // qb) * f_chunk
+    tflops = flops / (kern_ms * 1e-3) / 1e12
+    res = base_result(args, B * T / (ms * 1e-3), ms,
+                      f"chunked_ssd backward (m3_chunked_ssd_bwd), d_model 768 shapes "
+                      f"(B, T, H, P, N, R) = ({B}, {T}, {H}, {P}, {N}, {R}) with beta terms and "
+                      "dL/dh_final, fp32 inputs resident in HBM", B, T, dtype="fp32")
+    traffic = recorded_traffic(ROOT / "profiles" / "ssd_bwd_d768_trace_and_traffic.md", ("ssd_bwd",))
+    res["roofline"] = {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_FP32_TFLOPS,
+                       "unit": "TFLOP/s", "frac": round(tflops / PEAK_FP32_TFLOPS, 4),
+                       "traffic": traffic.get("ssd_bwd"),
+                       "kernel": "m3_chunked_ssd_bwd, all kernels of one call (fp32 VALU GEMM tiles "
+                                 "against the fp32 matrix peak)",
+                       "algorithmic_flops": flops, "avg_ms": round(kern_ms, 4)}
+    if not args.no_cpu_baseline:
+        from oracle import reference_path as ref
+        cores = len(os.sched_getaffinity(0))
+        torch.set_num_threads(cores)
+        Ts = 1024
+        sl = lambda t: t[:1, :Ts].detach().cpu().clone().requires_grad_()
+        leaf = [sl(t) for t in (xg, xb, Bg, Bb, C, dt)] + [A.cpu().requires_grad_(),
+                                                           D.cpu().requires_grad_(), sl(xr)]
+        t0 = time.perf_counter()
+        y, hf = ref.chunked_ssd(*leaf, chunk_size=64, return_final_state=True)
+        ((y * dy[:1, :Ts].cpu()).sum() + (hf * dhf[:1].cpu()).sum()).backward()
+        dt_s = time.perf_counter() - t0
+        res["cpu_baseline"] = {"value": round(Ts / dt_s, 1), "unit": "tokens/s", "cores": cores,
+                               "kind": "port", "cpu_model": cpu_model(),
+                               "sample": f"autograd forward + backward through the oracle's "
+                                         f"chunked_ssd (the reference algorithm) on batch row 0, "
+                                         f"first {Ts} tokens, fp32"}
+    return res
+
+
+WORKLOADS = {"prefill_d2048": bench_prefill_d2048, "ssd_bwd_d768": bench_ssd_bwd, "layer_fp32_d768": bench_layer_fp32_d768,
              "lm_d768": bench_lm_d768,
              "scan_d768": lambda args, torch, m: bench_scan(args, torch, (8, 128, 24, 8192), "scan_d768"),
              "scan_d2048": lambda args, torch, m: bench_scan(args, torch, (2, 256, 32, 32768), "scan_d2048"),
