@@ -35,6 +35,7 @@ namespace bw {
 constexpr int TT = 64;    // output tile edge
 constexpr int KT = 16;    // contraction step
 constexpr int NTH = 256;  // threads per tile block
+constexpr int TW = 128;   // wide output tile (columns over N or the score columns)
 
 struct Shape {
     int B, T, H, P, N, R, R2, Qb, K, nPt, nNt;
@@ -71,25 +72,34 @@ __device__ __forceinline__ int64_t row(const Shape& s, int b, int tg, int h) {
     return ((int64_t)b * s.T + tg) * s.H + h;
 }
 
+template <int TN>
 struct Lds {
     float A[KT][TT];
-    float B[KT][TT];
+    float B[KT][TN];
 };
 
-// acc[i][j] += sum_k fa(4 ty + i, k) fb(k, 4 tx + j) over k < kdim, for the 64 x 64 tile of
+// Column of a thread's accumulator j in a TN-wide tile (TN = 64 or 128): 4 tx + j % 4 + 64 (j / 4).
+__device__ __forceinline__ int tcol(int tx, int j) { return 4 * tx + (j & 3) + 64 * (j >> 2); }
+
+// acc[i][j] += sum_k fa(4 ty + i, k) fb(k, tcol(tx, j)) over k < kdim, for the 64 x TN tile of
 // a 256-thread block (tx = tid % 16, ty = tid / 16). fa / fb return 0 outside the operands.
 // The operands of step k0 + KT are loaded into registers while step k0 is multiplied.
-template <class FA, class FB>
-__device__ __forceinline__ void gemm_acc(float (&acc)[4][4], int kdim, FA fa, FB fb, Lds& l) {
+template <int TN, class FA, class FB>
+__device__ __forceinline__ void gemm_acc(float (&acc)[4][TN / 16], int kdim, FA fa, FB fb,
+                                         Lds<TN>& l) {
+    constexpr int NB = KT * TN / NTH;  // B elements per thread and step
     const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
-    float ra[4], rb[4];
+    float ra[4], rb[NB];
     auto fetch = [&](int k0) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int e = tid + NTH * i, kk = e >> 6, mm = e & 63;
-            const bool in = k0 + kk < kdim;
-            ra[i] = in ? fa(mm, k0 + kk) : 0.f;
-            rb[i] = in ? fb(k0 + kk, mm) : 0.f;
+            ra[i] = k0 + kk < kdim ? fa(mm, k0 + kk) : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            const int e = tid + NTH * i, kk = e / TN, nn = e % TN;
+            rb[i] = k0 + kk < kdim ? fb(k0 + kk, nn) : 0.f;
         }
     };
     fetch(0);
@@ -97,32 +107,40 @@ __device__ __forceinline__ void gemm_acc(float (&acc)[4][4], int kdim, FA fa, FB
     for (int k0 = 0; k0 < kdim; k0 += KT) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int e = tid + NTH * i, kk = e >> 6, mm = e & 63;
-            l.A[kk][mm] = ra[i];
-            l.B[kk][mm] = rb[i];
+            const int e = tid + NTH * i;
+            l.A[e >> 6][e & 63] = ra[i];
+        }
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            const int e = tid + NTH * i;
+            l.B[e / TN][e % TN] = rb[i];
         }
         __syncthreads();
         if (k0 + KT < kdim) fetch(k0 + KT);
 #pragma unroll
         for (int kk = 0; kk < KT; ++kk) {
             const float4 av = *reinterpret_cast<const float4*>(&l.A[kk][4 * ty]);
-            const float4 bv = *reinterpret_cast<const float4*>(&l.B[kk][4 * tx]);
             const float a4[4] = {av.x, av.y, av.z, av.w};
-            const float b4[4] = {bv.x, bv.y, bv.z, bv.w};
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int g = 0; g < TN / 64; ++g) {
+                const float4 bv = *reinterpret_cast<const float4*>(&l.B[kk][64 * g + 4 * tx]);
+                const float b4[4] = {bv.x, bv.y, bv.z, bv.w};
 #pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] += a4[i] * b4[j];
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) acc[i][4 * g + j] += a4[i] * b4[j];
+            }
         }
         __syncthreads();
     }
 }
 
-__device__ __forceinline__ void zero(float (&acc)[4][4]) {
+template <int NJ>
+__device__ __forceinline__ void zero(float (&acc)[4][NJ]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
+        for (int j = 0; j < NJ; ++j) acc[i][j] = 0.f;
 }
 
 // Accessors of chunk (b, k, h). Token positions at or past T read as 0.
@@ -178,58 +196,59 @@ __global__ __launch_bounds__(64) void bwd_cum(Args a) {
 // ---- K2: chunk-local states (scan input) and the y_inter gradient of each chunk state:
 //   hext[k][p,n] = sum_{s,j} exp(c_end - c_s) Xf[s,p,j] Bf[s,n,j]
 //   gext[k][p,n] = sum_{t,r} exp(c_t) dy[t,p,r] C[t,n,r]
-// plus the extra chunk K: hext = 0, gext = dL/dh_final (or 0).
+// plus the extra chunk K: hext = 0, gext = dL/dh_final (or 0). Tiles of 64 p x 128 n.
 template <int R, bool BETA>
 __global__ __launch_bounds__(NTH) void bwd_states(Args a) {
     BW_CONSTS
-    __shared__ Lds l;
+    __shared__ Lds<TW> l;
     __shared__ float cs[64];
     const Shape& s = a.s;
     const int ch = blockIdx.x, h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
     const int pt = blockIdx.y / s.nNt, nt = blockIdx.y % s.nNt;
-    const int p0 = pt * TT, n0 = nt * TT;
+    const int p0 = pt * TT, n0 = nt * TW;
     const Chunk<R, BETA> q{&a, b, k, h};
     if (threadIdx.x < QB) cs[threadIdx.x] = a.cum[(int64_t)ch * QB + threadIdx.x];
     __syncthreads();
     const float cend = cs[QB - 1];
     const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
-    float acc[4][4];
+    constexpr int NJ = TW / 16;
+    float acc[4][NJ];
     zero(acc);
-    gemm_acc(acc, QB * R2,
-             [&](int mm, int j) {
-                 const int p = p0 + mm, t = j / R2;
-                 return p < s.P ? __expf(cend - cs[t]) * q.dtv(t) * q.x(t, p, j % R2) : 0.f;
-             },
-             [&](int j, int nn) {
-                 const int n = n0 + nn;
-                 return n < s.N ? q.bf(j / R2, n, j % R2) : 0.f;
-             },
-             l);
+    gemm_acc<TW>(acc, QB * R2,
+                 [&](int mm, int j) {
+                     const int p = p0 + mm, t = j / R2;
+                     return p < s.P ? __expf(cend - cs[t]) * q.dtv(t) * q.x(t, p, j % R2) : 0.f;
+                 },
+                 [&](int j, int nn) {
+                     const int n = n0 + nn;
+                     return n < s.N ? q.bf(j / R2, n, j % R2) : 0.f;
+                 },
+                 l);
     float* ho = a.hext + chx(s, b, k, h) * s.PN;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int p = p0 + 4 * ty + i, n = n0 + 4 * tx + j;
+        for (int j = 0; j < NJ; ++j) {
+            const int p = p0 + 4 * ty + i, n = n0 + tcol(tx, j);
             if (p < s.P && n < s.N) ho[(int64_t)p * s.N + n] = acc[i][j];
         }
     zero(acc);
-    gemm_acc(acc, QB * R,
-             [&](int mm, int j) {
-                 const int p = p0 + mm, t = j / R;
-                 return p < s.P ? __expf(cs[t]) * q.dy(t, p, j % R) : 0.f;
-             },
-             [&](int j, int nn) {
-                 const int n = n0 + nn;
-                 return n < s.N ? q.c(j / R, n, j % R) : 0.f;
-             },
-             l);
+    gemm_acc<TW>(acc, QB * R,
+                 [&](int mm, int j) {
+                     const int p = p0 + mm, t = j / R;
+                     return p < s.P ? __expf(cs[t]) * q.dy(t, p, j % R) : 0.f;
+                 },
+                 [&](int j, int nn) {
+                     const int n = n0 + nn;
+                     return n < s.N ? q.c(j / R, n, j % R) : 0.f;
+                 },
+                 l);
     float* go = a.gext + chx(s, b, k, h) * s.PN;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int p = p0 + 4 * ty + i, n = n0 + 4 * tx + j;
+        for (int j = 0; j < NJ; ++j) {
+            const int p = p0 + 4 * ty + i, n = n0 + tcol(tx, j);
             if (p < s.P && n < s.N) go[(int64_t)p * s.N + n] = acc[i][j];
         }
     if (k == s.K - 1) {
@@ -239,8 +258,8 @@ __global__ __launch_bounds__(NTH) void bwd_states(Args a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int p = p0 + 4 * ty + i, n = n0 + 4 * tx + j;
+            for (int j = 0; j < NJ; ++j) {
+                const int p = p0 + 4 * ty + i, n = n0 + tcol(tx, j);
                 if (p < s.P && n < s.N) {
                     const int64_t o = (int64_t)p * s.N + n;
                     he[o] = 0.f;
@@ -251,12 +270,13 @@ __global__ __launch_bounds__(NTH) void bwd_states(Args a) {
 }
 
 // ---- K1: masked scores M = W o G and DM = W o DX of the chunk, and the intra-chunk part of
-// dc: sum_s W Z[t,s] - sum_t' W Z[t',t]. One block per chunk, looping over its tiles.
+// dc: sum_s W Z[t,s] - sum_t' W Z[t',t]. One block per chunk, looping over its 64 x 128 tiles;
+// W o G waits in LDS while DX is formed.
 template <int R, bool BETA>
 __global__ __launch_bounds__(NTH) void bwd_scores(Args a) {
     BW_CONSTS
-    __shared__ Lds l;
-    __shared__ float zp[TT][TT + 1];
+    __shared__ Lds<TW> l;
+    __shared__ float zp[TT][TW + 1];
     __shared__ float cs[64], rowacc[64], colacc[64];
     const Shape& s = a.s;
     const int ch = blockIdx.x, h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
@@ -270,38 +290,52 @@ __global__ __launch_bounds__(NTH) void bwd_scores(Args a) {
     __syncthreads();
     float* Mo = a.M + (int64_t)ch * QR * QR2;
     float* DMo = a.DM + (int64_t)ch * QR * QR2;
+    constexpr int NJ = TW / 16;
     for (int m0 = 0; m0 < QR; m0 += TT) {
-        for (int c0 = 0; c0 < QR2; c0 += TT) {
-            float g[4][4], d[4][4];
+        for (int c0 = 0; c0 < QR2; c0 += TW) {
+            float g[4][NJ];
             zero(g);
-            zero(d);
             // G[(t,r),(s,j)] = sum_n C[t,n,r] Bf[s,n,j]
-            gemm_acc(g, s.N,
-                     [&](int mm, int n) { const int m = m0 + mm; return q.c(m / R, n, m % R); },
-                     [&](int n, int cc) { const int c = c0 + cc; return q.bf(c / R2, n, c % R2); },
-                     l);
-            // DX[(t,r),(s,j)] = sum_p dy[t,p,r] dt_s x[s,p,j]
-            gemm_acc(d, s.P,
-                     [&](int mm, int p) { const int m = m0 + mm; return q.dy(m / R, p, m % R); },
-                     [&](int p, int cc) {
-                         const int c = c0 + cc, t = c / R2;
-                         return q.dtv(t) * q.x(t, p, c % R2);
-                     },
-                     l);
+            gemm_acc<TW>(g, s.N,
+                         [&](int mm, int n) { const int m = m0 + mm; return q.c(m / R, n, m % R); },
+                         [&](int n, int cc) {
+                             const int c = c0 + cc;
+                             return c < QR2 ? q.bf(c / R2, n, c % R2) : 0.f;
+                         },
+                         l);
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int m = m0 + 4 * ty + i, c = c0 + 4 * tx + j;
+                for (int j = 0; j < NJ; ++j) {
+                    const int m = m0 + 4 * ty + i, c = c0 + tcol(tx, j);
                     const int t = m / R, u = c / R2;
-                    const float w = u <= t ? __expf(cs[t] - cs[u]) : 0.f;
-                    Mo[(int64_t)m * QR2 + c] = w * g[i][j];
-                    DMo[(int64_t)m * QR2 + c] = w * d[i][j];
-                    zp[4 * ty + i][4 * tx + j] = w * g[i][j] * d[i][j];
+                    const float w = c < QR2 && u <= t ? __expf(cs[t] - cs[u]) : 0.f;
+                    if (c < QR2) Mo[(int64_t)m * QR2 + c] = w * g[i][j];
+                    zp[4 * ty + i][tcol(tx, j)] = w * g[i][j];
+                }
+            // DX[(t,r),(s,j)] = sum_p dy[t,p,r] dt_s x[s,p,j]; gemm_acc's first barrier orders
+            // the zp writes above before the reads below
+            zero(g);
+            gemm_acc<TW>(g, s.P,
+                         [&](int mm, int p) { const int m = m0 + mm; return q.dy(m / R, p, m % R); },
+                         [&](int p, int cc) {
+                             const int c = c0 + cc, t = c / R2;
+                             return c < QR2 ? q.dtv(t) * q.x(t, p, c % R2) : 0.f;
+                         },
+                         l);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) {
+                    const int m = m0 + 4 * ty + i, c = c0 + tcol(tx, j);
+                    const int t = m / R, u = c / R2;
+                    const float w = c < QR2 && u <= t ? __expf(cs[t] - cs[u]) : 0.f;
+                    if (c < QR2) DMo[(int64_t)m * QR2 + c] = w * g[i][j];
+                    zp[4 * ty + i][tcol(tx, j)] *= g[i][j];
                 }
             __syncthreads();
             // Z over the (r, j) blocks of the tile, summed into rows (t) and columns (s).
-            const int nt = TT / R, ns = TT / R2;
+            const int nt = TT / R, ns = min(TW, QR2 - c0) / R2;
             if (tid < nt) {
                 float v = 0.f;
                 for (int u = 0; u < ns; ++u)
@@ -345,7 +379,7 @@ __device__ __forceinline__ void tile_token_sums(const float (&v)[4], int per, fl
 template <int R, bool BETA>
 __global__ __launch_bounds__(NTH) void bwd_dxf(Args a) {
     BW_CONSTS
-    __shared__ Lds l;
+    __shared__ Lds<TT> l;
     __shared__ float red[TT][17];
     __shared__ float cs[64], outv[64];
     const Shape& s = a.s;
@@ -360,7 +394,7 @@ __global__ __launch_bounds__(NTH) void bwd_dxf(Args a) {
     const float* dH = a.dch + chx(s, b, k, h) * s.PN;
     float acc[4][4];
     zero(acc);
-    gemm_acc(acc, s.N,
+    gemm_acc<TT>(acc, s.N,
              [&](int mm, int n) { const int m = m0 + mm; return q.bf(m / R2, n, m % R2); },
              [&](int n, int pp) { const int p = p0 + pp; return p < s.P ? dH[(int64_t)p * s.N + n] : 0.f; },
              l);
@@ -382,7 +416,7 @@ __global__ __launch_bounds__(NTH) void bwd_dxf(Args a) {
     tile_token_sums(rv, per, red, outv);
     if (tid < nts) a.pState[((int64_t)ch * s.nPt + pt) * QB + m0 / per + tid] = outv[tid];
     const float* Mi = a.M + (int64_t)ch * QR * QR2;
-    gemm_acc(acc, QR,
+    gemm_acc<TT>(acc, QR,
              [&](int mm, int jr) { return Mi[(int64_t)jr * QR2 + m0 + mm]; },
              [&](int jr, int pp) {
                  const int p = p0 + pp;
@@ -412,21 +446,22 @@ __global__ __launch_bounds__(NTH) void bwd_dxf(Args a) {
 template <int R, bool BETA>
 __global__ __launch_bounds__(NTH) void bwd_dbf(Args a) {
     BW_CONSTS
-    __shared__ Lds l;
+    __shared__ Lds<TW> l;
     __shared__ float cs[64];
     const Shape& s = a.s;
     const int ch = blockIdx.x, h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
     const int rt = blockIdx.y / s.nNt, nt = blockIdx.y % s.nNt;
-    const int m0 = rt * TT, n0 = nt * TT;
+    const int m0 = rt * TT, n0 = nt * TW;
+    constexpr int NJ = TW / 16;
     const Chunk<R, BETA> q{&a, b, k, h};
     const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
     if (tid < QB) cs[tid] = a.cum[(int64_t)ch * QB + tid];
     __syncthreads();
     const float cend = cs[QB - 1];
     const float* dH = a.dch + chx(s, b, k, h) * s.PN;
-    float acc[4][4];
+    float acc[4][NJ];
     zero(acc);
-    gemm_acc(acc, s.P,
+    gemm_acc<TW>(acc, s.P,
              [&](int mm, int p) {
                  const int m = m0 + mm, t = m / R2;
                  return q.dtv(t) * q.x(t, p, m % R2);
@@ -437,10 +472,10 @@ __global__ __launch_bounds__(NTH) void bwd_dbf(Args a) {
     for (int i = 0; i < 4; ++i) {
         const float e = __expf(cend - cs[(m0 + 4 * ty + i) / R2]);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] *= e;
+        for (int j = 0; j < NJ; ++j) acc[i][j] *= e;
     }
     const float* DMi = a.DM + (int64_t)ch * QR * QR2;
-    gemm_acc(acc, QR,
+    gemm_acc<TW>(acc, QR,
              [&](int mm, int jr) { return DMi[(int64_t)jr * QR2 + m0 + mm]; },
              [&](int jr, int nn) {
                  const int n = n0 + nn;
@@ -454,8 +489,8 @@ __global__ __launch_bounds__(NTH) void bwd_dbf(Args a) {
         float* out = j < R ? a.dBg : a.dBb;
         const int64_t base = row(s, b, k * QB + t, h) * s.N * R + (j < R ? j : j - R);
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-            const int n = n0 + 4 * tx + jj;
+        for (int jj = 0; jj < NJ; ++jj) {
+            const int n = n0 + tcol(tx, jj);
             if (n < s.N) out[base + (int64_t)n * R] = acc[i][jj];
         }
     }
@@ -465,21 +500,22 @@ __global__ __launch_bounds__(NTH) void bwd_dbf(Args a) {
 template <int R, bool BETA>
 __global__ __launch_bounds__(NTH) void bwd_dc(Args a) {
     BW_CONSTS
-    __shared__ Lds l;
+    __shared__ Lds<TW> l;
     __shared__ float red[TT][17];
     __shared__ float cs[64], outv[64];
     const Shape& s = a.s;
     const int ch = blockIdx.x, h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
     const int rt = blockIdx.y / s.nNt, nt = blockIdx.y % s.nNt;
-    const int m0 = rt * TT, n0 = nt * TT;
+    const int m0 = rt * TT, n0 = nt * TW;
+    constexpr int NJ = TW / 16;
     const Chunk<R, BETA> q{&a, b, k, h};
     const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
     if (tid < QB) cs[tid] = a.cum[(int64_t)ch * QB + tid];
     __syncthreads();
     const float* Hk = a.Hs + chx(s, b, k, h) * s.PN;
-    float acc[4][4];
+    float acc[4][NJ];
     zero(acc);
-    gemm_acc(acc, s.P,
+    gemm_acc<TW>(acc, s.P,
              [&](int mm, int p) { const int m = m0 + mm; return q.dy(m / R, p, m % R); },
              [&](int p, int nn) { const int n = n0 + nn; return n < s.N ? Hk[(int64_t)p * s.N + n] : 0.f; },
              l);
@@ -490,8 +526,8 @@ __global__ __launch_bounds__(NTH) void bwd_dc(Args a) {
         const float e = __expf(cs[t]);
         rv[i] = 0.f;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int n = n0 + 4 * tx + j;
+        for (int j = 0; j < NJ; ++j) {
+            const int n = n0 + tcol(tx, j);
             acc[i][j] *= e;
             if (n < s.N) rv[i] += q.c(t, n, r) * acc[i][j];
         }
@@ -500,7 +536,7 @@ __global__ __launch_bounds__(NTH) void bwd_dc(Args a) {
     tile_token_sums(rv, per, red, outv);
     if (tid < nts) a.pInter[((int64_t)ch * s.nNt + nt) * QB + m0 / per + tid] = outv[tid];
     const float* DMi = a.DM + (int64_t)ch * QR * QR2;
-    gemm_acc(acc, QR2,
+    gemm_acc<TW>(acc, QR2,
              [&](int mm, int jc) { return DMi[(int64_t)(m0 + mm) * QR2 + jc]; },
              [&](int jc, int nn) {
                  const int n = n0 + nn;
@@ -513,8 +549,8 @@ __global__ __launch_bounds__(NTH) void bwd_dc(Args a) {
         if (!q.real(t)) continue;
         const int64_t base = row(s, b, k * QB + t, h) * s.N * R + r;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int n = n0 + 4 * tx + j;
+        for (int j = 0; j < NJ; ++j) {
+            const int n = n0 + tcol(tx, j);
             if (n < s.N) a.dC[base + (int64_t)n * R] = acc[i][j];
         }
     }
@@ -623,7 +659,7 @@ bool make_shape(int B, int T, int H, int P, int N, int R, bool beta, Shape& s) {
     s.Qb = 128 / s.R2 >= 64 ? 64 : 128 / s.R2;  // as BW_CONSTS
     s.K = (T + s.Qb - 1) / s.Qb;
     s.nPt = (P + TT - 1) / TT;
-    s.nNt = (N + TT - 1) / TT;
+    s.nNt = (N + TW - 1) / TW;
     s.PN = (int64_t)P * N;
     return true;
 }
