@@ -74,21 +74,24 @@ __device__ __forceinline__ int64_t row(const Shape& s, int b, int tg, int h) {
 
 template <int TN>
 struct Lds {
-    float A[KT][TT];
-    float B[KT][TN];
+    float A[KT][TT + 16];  // rows padded so that the 4 k-rows one MFMA operand read spans
+    float B[KT][TN + 16];  // land on distinct banks
 };
 
-// Column of a thread's accumulator j in a TN-wide tile (TN = 64 or 128): 4 tx + j % 4 + 64 (j / 4).
-__device__ __forceinline__ int tcol(int tx, int j) { return 4 * tx + (j & 3) + 64 * (j >> 2); }
+// Tile layout of the fp32 MFMA accumulators (v_mfma_f32_16x16x4_f32: lane l holds rows
+// 4 (l / 16) + v, v < 4, of column l % 16 of a 16 x 16 block): wave w owns rows 16w..16w+15 of
+// the 64-row tile, so thread (tx, ty) = (tid % 16, tid / 16) holds rows 4 ty + v of the columns
+// tcol(tx, j) = tx + 16 j; its accumulator acc[j][v].
+__device__ __forceinline__ int tcol(int tx, int j) { return tx + 16 * j; }
 
-// acc[i][j] += sum_k fa(4 ty + i, k) fb(k, tcol(tx, j)) over k < kdim, for the 64 x TN tile of
-// a 256-thread block (tx = tid % 16, ty = tid / 16). fa / fb return 0 outside the operands.
-// The operands of step k0 + KT are loaded into registers while step k0 is multiplied.
+// acc[j][v] += sum_k fa(4 ty + v, k) fb(k, tcol(tx, j)) over k < kdim, for the 64 x TN tile of
+// a 256-thread block, on fp32 MFMA. fa / fb return 0 outside the operands. The operands of
+// step k0 + KT are loaded into registers while step k0 is multiplied.
 template <int TN, class FA, class FB>
-__device__ __forceinline__ void gemm_acc(float (&acc)[4][TN / 16], int kdim, FA fa, FB fb,
+__device__ __forceinline__ void gemm_acc(f32x4 (&acc)[TN / 16], int kdim, FA fa, FB fb,
                                          Lds<TN>& l) {
     constexpr int NB = KT * TN / NTH;  // B elements per thread and step
-    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     float ra[4], rb[NB];
     auto fetch = [&](int k0) {
 #pragma unroll
@@ -118,17 +121,12 @@ __device__ __forceinline__ void gemm_acc(float (&acc)[4][TN / 16], int kdim, FA 
         __syncthreads();
         if (k0 + KT < kdim) fetch(k0 + KT);
 #pragma unroll
-        for (int kk = 0; kk < KT; ++kk) {
-            const float4 av = *reinterpret_cast<const float4*>(&l.A[kk][4 * ty]);
-            const float a4[4] = {av.x, av.y, av.z, av.w};
+        for (int k4 = 0; k4 < KT; k4 += 4) {
+            const float av = l.A[k4 + (lane >> 4)][16 * wave + (lane & 15)];
 #pragma unroll
-            for (int g = 0; g < TN / 64; ++g) {
-                const float4 bv = *reinterpret_cast<const float4*>(&l.B[kk][64 * g + 4 * tx]);
-                const float b4[4] = {bv.x, bv.y, bv.z, bv.w};
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) acc[i][4 * g + j] += a4[i] * b4[j];
+            for (int j = 0; j < TN / 16; ++j) {
+                const float bv = l.B[k4 + (lane >> 4)][16 * j + (lane & 15)];
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[j], 0, 0, 0);
             }
         }
         __syncthreads();
@@ -136,11 +134,9 @@ __device__ __forceinline__ void gemm_acc(float (&acc)[4][TN / 16], int kdim, FA 
 }
 
 template <int NJ>
-__device__ __forceinline__ void zero(float (&acc)[4][NJ]) {
+__device__ __forceinline__ void zero(f32x4 (&acc)[NJ]) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) acc[i][j] = 0.f;
+    for (int j = 0; j < NJ; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
 }
 
 // Accessors of chunk (b, k, h). Token positions at or past T read as 0.
@@ -212,7 +208,7 @@ __global__ __launch_bounds__(NTH) void bwd_states(Args a) {
     const float cend = cs[QB - 1];
     const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
     constexpr int NJ = TW / 16;
-    float acc[4][NJ];
+    f32x4 acc[NJ];
     zero(acc);
     gemm_acc<TW>(acc, QB * R2,
                  [&](int mm, int j) {
@@ -230,7 +226,7 @@ __global__ __launch_bounds__(NTH) void bwd_states(Args a) {
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
             const int p = p0 + 4 * ty + i, n = n0 + tcol(tx, j);
-            if (p < s.P && n < s.N) ho[(int64_t)p * s.N + n] = acc[i][j];
+            if (p < s.P && n < s.N) ho[(int64_t)p * s.N + n] = acc[j][i];
         }
     zero(acc);
     gemm_acc<TW>(acc, QB * R,
@@ -249,7 +245,7 @@ __global__ __launch_bounds__(NTH) void bwd_states(Args a) {
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
             const int p = p0 + 4 * ty + i, n = n0 + tcol(tx, j);
-            if (p < s.P && n < s.N) go[(int64_t)p * s.N + n] = acc[i][j];
+            if (p < s.P && n < s.N) go[(int64_t)p * s.N + n] = acc[j][i];
         }
     if (k == s.K - 1) {
         float* he = a.hext + chx(s, b, s.K, h) * s.PN;
@@ -293,7 +289,7 @@ __global__ __launch_bounds__(NTH) void bwd_scores(Args a) {
     constexpr int NJ = TW / 16;
     for (int m0 = 0; m0 < QR; m0 += TT) {
         for (int c0 = 0; c0 < QR2; c0 += TW) {
-            float g[4][NJ];
+            f32x4 g[NJ];
             zero(g);
             // G[(t,r),(s,j)] = sum_n C[t,n,r] Bf[s,n,j]
             gemm_acc<TW>(g, s.N,
@@ -310,8 +306,8 @@ __global__ __launch_bounds__(NTH) void bwd_scores(Args a) {
                     const int m = m0 + 4 * ty + i, c = c0 + tcol(tx, j);
                     const int t = m / R, u = c / R2;
                     const float w = c < QR2 && u <= t ? __expf(cs[t] - cs[u]) : 0.f;
-                    if (c < QR2) Mo[(int64_t)m * QR2 + c] = w * g[i][j];
-                    zp[4 * ty + i][tcol(tx, j)] = w * g[i][j];
+                    if (c < QR2) Mo[(int64_t)m * QR2 + c] = w * g[j][i];
+                    zp[4 * ty + i][tcol(tx, j)] = w * g[j][i];
                 }
             // DX[(t,r),(s,j)] = sum_p dy[t,p,r] dt_s x[s,p,j]; gemm_acc's first barrier orders
             // the zp writes above before the reads below
@@ -330,8 +326,8 @@ __global__ __launch_bounds__(NTH) void bwd_scores(Args a) {
                     const int m = m0 + 4 * ty + i, c = c0 + tcol(tx, j);
                     const int t = m / R, u = c / R2;
                     const float w = c < QR2 && u <= t ? __expf(cs[t] - cs[u]) : 0.f;
-                    if (c < QR2) DMo[(int64_t)m * QR2 + c] = w * g[i][j];
-                    zp[4 * ty + i][tcol(tx, j)] *= g[i][j];
+                    if (c < QR2) DMo[(int64_t)m * QR2 + c] = w * g[j][i];
+                    zp[4 * ty + i][tcol(tx, j)] *= g[j][i];
                 }
             __syncthreads();
             // Z over the (r, j) blocks of the tile, summed into rows (t) and columns (s).
@@ -392,7 +388,7 @@ __global__ __launch_bounds__(NTH) void bwd_dxf(Args a) {
     __syncthreads();
     const float cend = cs[QB - 1];
     const float* dH = a.dch + chx(s, b, k, h) * s.PN;
-    float acc[4][4];
+    f32x4 acc[4];
     zero(acc);
     gemm_acc<TT>(acc, s.N,
              [&](int mm, int n) { const int m = m0 + mm; return q.bf(m / R2, n, m % R2); },
@@ -406,10 +402,10 @@ __global__ __launch_bounds__(NTH) void bwd_dxf(Args a) {
         rv[i] = 0.f;
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
-            const int p = p0 + 4 * tx + jj;
+            const int p = p0 + tcol(tx, jj);
             xv[i][jj] = p < s.P ? q.x(t, p, j) : 0.f;
-            acc[i][jj] *= e;
-            rv[i] += d * xv[i][jj] * acc[i][jj];
+            acc[jj][i] *= e;
+            rv[i] += d * xv[i][jj] * acc[jj][i];
         }
     }
     const int per = R2, nts = TT / per;
@@ -433,9 +429,9 @@ __global__ __launch_bounds__(NTH) void bwd_dxf(Args a) {
         const int64_t base = row(s, b, k * QB + t, h) * s.P * R + (j < R ? j : j - R);
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
-            const int p = p0 + 4 * tx + jj;
-            rv[i] += acc[i][jj] * xv[i][jj];
-            if (w && p < s.P) out[base + (int64_t)p * R] = d * acc[i][jj];
+            const int p = p0 + tcol(tx, jj);
+            rv[i] += acc[jj][i] * xv[i][jj];
+            if (w && p < s.P) out[base + (int64_t)p * R] = d * acc[jj][i];
         }
     }
     tile_token_sums(rv, per, red, outv);
@@ -459,7 +455,7 @@ __global__ __launch_bounds__(NTH) void bwd_dbf(Args a) {
     __syncthreads();
     const float cend = cs[QB - 1];
     const float* dH = a.dch + chx(s, b, k, h) * s.PN;
-    float acc[4][NJ];
+    f32x4 acc[NJ];
     zero(acc);
     gemm_acc<TW>(acc, s.P,
              [&](int mm, int p) {
@@ -472,7 +468,7 @@ __global__ __launch_bounds__(NTH) void bwd_dbf(Args a) {
     for (int i = 0; i < 4; ++i) {
         const float e = __expf(cend - cs[(m0 + 4 * ty + i) / R2]);
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) acc[i][j] *= e;
+        for (int j = 0; j < NJ; ++j) acc[j][i] *= e;
     }
     const float* DMi = a.DM + (int64_t)ch * QR * QR2;
     gemm_acc<TW>(acc, QR,
@@ -491,7 +487,7 @@ __global__ __launch_bounds__(NTH) void bwd_dbf(Args a) {
 #pragma unroll
         for (int jj = 0; jj < NJ; ++jj) {
             const int n = n0 + tcol(tx, jj);
-            if (n < s.N) out[base + (int64_t)n * R] = acc[i][jj];
+            if (n < s.N) out[base + (int64_t)n * R] = acc[jj][i];
         }
     }
 }
@@ -513,7 +509,7 @@ __global__ __launch_bounds__(NTH) void bwd_dc(Args a) {
     if (tid < QB) cs[tid] = a.cum[(int64_t)ch * QB + tid];
     __syncthreads();
     const float* Hk = a.Hs + chx(s, b, k, h) * s.PN;
-    float acc[4][NJ];
+    f32x4 acc[NJ];
     zero(acc);
     gemm_acc<TW>(acc, s.P,
              [&](int mm, int p) { const int m = m0 + mm; return q.dy(m / R, p, m % R); },
@@ -528,8 +524,8 @@ __global__ __launch_bounds__(NTH) void bwd_dc(Args a) {
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
             const int n = n0 + tcol(tx, j);
-            acc[i][j] *= e;
-            if (n < s.N) rv[i] += q.c(t, n, r) * acc[i][j];
+            acc[j][i] *= e;
+            if (n < s.N) rv[i] += q.c(t, n, r) * acc[j][i];
         }
     }
     const int per = R, nts = TT / per;
@@ -551,7 +547,7 @@ __global__ __launch_bounds__(NTH) void bwd_dc(Args a) {
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
             const int n = n0 + tcol(tx, j);
-            if (n < s.N) a.dC[base + (int64_t)n * R] = acc[i][j];
+            if (n < s.N) a.dC[base + (int64_t)n * R] = acc[j][i];
         }
     }
 }
