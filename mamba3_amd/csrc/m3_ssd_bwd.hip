@@ -197,7 +197,7 @@ template <int R, bool BETA>
 __global__ __launch_bounds__(NTH) void bwd_states(Args a) {
     BW_CONSTS
     __shared__ Lds<TW> l;
-    __shared__ float cs[64];
+    __shared__ float cs[64], wx[64], ec[64];
     const Shape& s = a.s;
     const int ch = blockIdx.x, h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
     const int pt = blockIdx.y / s.nNt, nt = blockIdx.y % s.nNt;
@@ -205,7 +205,12 @@ __global__ __launch_bounds__(NTH) void bwd_states(Args a) {
     const Chunk<R, BETA> q{&a, b, k, h};
     if (threadIdx.x < QB) cs[threadIdx.x] = a.cum[(int64_t)ch * QB + threadIdx.x];
     __syncthreads();
-    const float cend = cs[QB - 1];
+    if (threadIdx.x < QB) {  // per-token weights of the two contractions
+        const int t = threadIdx.x;
+        wx[t] = __expf(cs[QB - 1] - cs[t]) * q.dtv(t);
+        ec[t] = __expf(cs[t]);
+    }
+    __syncthreads();
     const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
     constexpr int NJ = TW / 16;
     f32x4 acc[NJ];
@@ -213,7 +218,7 @@ __global__ __launch_bounds__(NTH) void bwd_states(Args a) {
     gemm_acc<TW>(acc, QB * R2,
                  [&](int mm, int j) {
                      const int p = p0 + mm, t = j / R2;
-                     return p < s.P ? __expf(cend - cs[t]) * q.dtv(t) * q.x(t, p, j % R2) : 0.f;
+                     return p < s.P ? wx[t] * q.x(t, p, j % R2) : 0.f;
                  },
                  [&](int j, int nn) {
                      const int n = n0 + nn;
@@ -232,7 +237,7 @@ __global__ __launch_bounds__(NTH) void bwd_states(Args a) {
     gemm_acc<TW>(acc, QB * R,
                  [&](int mm, int j) {
                      const int p = p0 + mm, t = j / R;
-                     return p < s.P ? __expf(cs[t]) * q.dy(t, p, j % R) : 0.f;
+                     return p < s.P ? ec[t] * q.dy(t, p, j % R) : 0.f;
                  },
                  [&](int j, int nn) {
                      const int n = n0 + nn;
@@ -273,13 +278,14 @@ __global__ __launch_bounds__(NTH) void bwd_scores(Args a) {
     BW_CONSTS
     __shared__ Lds<TW> l;
     __shared__ float zp[TT][TW + 1];
-    __shared__ float cs[64], rowacc[64], colacc[64];
+    __shared__ float cs[64], dts[64], rowacc[64], colacc[64];
     const Shape& s = a.s;
     const int ch = blockIdx.x, h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
     const Chunk<R, BETA> q{&a, b, k, h};
     const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
     if (tid < 64) {
         cs[tid] = tid < QB ? a.cum[(int64_t)ch * QB + tid] : 0.f;
+        dts[tid] = tid < QB ? q.dtv(tid) : 0.f;
         rowacc[tid] = 0.f;
         colacc[tid] = 0.f;
     }
@@ -316,7 +322,7 @@ __global__ __launch_bounds__(NTH) void bwd_scores(Args a) {
                          [&](int mm, int p) { const int m = m0 + mm; return q.dy(m / R, p, m % R); },
                          [&](int p, int cc) {
                              const int c = c0 + cc, t = c / R2;
-                             return c < QR2 ? q.dtv(t) * q.x(t, p, c % R2) : 0.f;
+                             return c < QR2 ? dts[t] * q.x(t, p, c % R2) : 0.f;
                          },
                          l);
 #pragma unroll
@@ -443,7 +449,7 @@ template <int R, bool BETA>
 __global__ __launch_bounds__(NTH) void bwd_dbf(Args a) {
     BW_CONSTS
     __shared__ Lds<TW> l;
-    __shared__ float cs[64];
+    __shared__ float cs[64], dts[64];
     const Shape& s = a.s;
     const int ch = blockIdx.x, h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
     const int rt = blockIdx.y / s.nNt, nt = blockIdx.y % s.nNt;
@@ -451,7 +457,10 @@ __global__ __launch_bounds__(NTH) void bwd_dbf(Args a) {
     constexpr int NJ = TW / 16;
     const Chunk<R, BETA> q{&a, b, k, h};
     const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
-    if (tid < QB) cs[tid] = a.cum[(int64_t)ch * QB + tid];
+    if (tid < QB) {
+        cs[tid] = a.cum[(int64_t)ch * QB + tid];
+        dts[tid] = q.dtv(tid);
+    }
     __syncthreads();
     const float cend = cs[QB - 1];
     const float* dH = a.dch + chx(s, b, k, h) * s.PN;
@@ -460,7 +469,7 @@ __global__ __launch_bounds__(NTH) void bwd_dbf(Args a) {
     gemm_acc<TW>(acc, s.P,
              [&](int mm, int p) {
                  const int m = m0 + mm, t = m / R2;
-                 return q.dtv(t) * q.x(t, p, m % R2);
+                 return dts[t] * q.x(t, p, m % R2);
              },
              [&](int p, int nn) { const int n = n0 + nn; return n < s.N ? dH[(int64_t)p * s.N + n] : 0.f; },
              l);
