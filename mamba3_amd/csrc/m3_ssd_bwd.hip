@@ -72,10 +72,12 @@ __device__ __forceinline__ int64_t row(const Shape& s, int b, int tg, int h) {
     return ((int64_t)b * s.T + tg) * s.H + h;
 }
 
+// Rows padded to a stride of 17 (mod 32) floats: the MFMA operand reads (16 lanes per k-row,
+// 4 k-rows) and the stores of k-fastest fetches (16 k-rows per column) spread over the banks.
 template <int TN>
 struct Lds {
-    float A[KT][TT + 16];  // rows padded so that the 4 k-rows one MFMA operand read spans
-    float B[KT][TN + 16];  // land on distinct banks
+    float A[KT][TT + 17];
+    float B[KT][TN + 17];
 };
 
 // Tile layout of the fp32 MFMA accumulators (v_mfma_f32_16x16x4_f32: lane l holds rows
@@ -85,24 +87,30 @@ struct Lds {
 __device__ __forceinline__ int tcol(int tx, int j) { return tx + 16 * j; }
 
 // acc[j][v] += sum_k fa(4 ty + v, k) fb(k, tcol(tx, j)) over k < kdim, for the 64 x TN tile of
-// a 256-thread block, on fp32 MFMA. fa / fb return 0 outside the operands. The operands of
-// step k0 + KT are loaded into registers while step k0 is multiplied.
-template <int TN, class FA, class FB>
+// a 256-thread block, on fp32 MFMA. fa / fb return 0 outside the operands. AK / BK pick the
+// order in which consecutive threads fetch an operand: k fastest (for operands contiguous
+// along k in memory) or row / column fastest. The operands of step k0 + KT are loaded into
+// registers while step k0 is multiplied.
+template <int TN, bool AK, bool BK, class FA, class FB>
 __device__ __forceinline__ void gemm_acc(f32x4 (&acc)[TN / 16], int kdim, FA fa, FB fb,
                                          Lds<TN>& l) {
     constexpr int NB = KT * TN / NTH;  // B elements per thread and step
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    auto ak = [](int e) { return AK ? e % KT : e / TT; };
+    auto am = [](int e) { return AK ? e / KT : e % TT; };
+    auto bk = [](int e) { return BK ? e % KT : e / TN; };
+    auto bn = [](int e) { return BK ? e / KT : e % TN; };
     float ra[4], rb[NB];
     auto fetch = [&](int k0) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int e = tid + NTH * i, kk = e >> 6, mm = e & 63;
-            ra[i] = k0 + kk < kdim ? fa(mm, k0 + kk) : 0.f;
+            const int e = tid + NTH * i;
+            ra[i] = k0 + ak(e) < kdim ? fa(am(e), k0 + ak(e)) : 0.f;
         }
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
-            const int e = tid + NTH * i, kk = e / TN, nn = e % TN;
-            rb[i] = k0 + kk < kdim ? fb(k0 + kk, nn) : 0.f;
+            const int e = tid + NTH * i;
+            rb[i] = k0 + bk(e) < kdim ? fb(k0 + bk(e), bn(e)) : 0.f;
         }
     };
     fetch(0);
@@ -111,12 +119,12 @@ __device__ __forceinline__ void gemm_acc(f32x4 (&acc)[TN / 16], int kdim, FA fa,
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int e = tid + NTH * i;
-            l.A[e >> 6][e & 63] = ra[i];
+            l.A[ak(e)][am(e)] = ra[i];
         }
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
             const int e = tid + NTH * i;
-            l.B[e / TN][e % TN] = rb[i];
+            l.B[bk(e)][bn(e)] = rb[i];
         }
         __syncthreads();
         if (k0 + KT < kdim) fetch(k0 + KT);
@@ -215,7 +223,7 @@ __global__ __launch_bounds__(NTH) void bwd_states(Args a) {
     constexpr int NJ = TW / 16;
     f32x4 acc[NJ];
     zero(acc);
-    gemm_acc<TW>(acc, QB * R2,
+    gemm_acc<TW, false, false>(acc, QB * R2,
                  [&](int mm, int j) {
                      const int p = p0 + mm, t = j / R2;
                      return p < s.P ? wx[t] * q.x(t, p, j % R2) : 0.f;
@@ -234,7 +242,7 @@ __global__ __launch_bounds__(NTH) void bwd_states(Args a) {
             if (p < s.P && n < s.N) ho[(int64_t)p * s.N + n] = acc[j][i];
         }
     zero(acc);
-    gemm_acc<TW>(acc, QB * R,
+    gemm_acc<TW, false, false>(acc, QB * R,
                  [&](int mm, int j) {
                      const int p = p0 + mm, t = j / R;
                      return p < s.P ? ec[t] * q.dy(t, p, j % R) : 0.f;
@@ -298,7 +306,7 @@ __global__ __launch_bounds__(NTH) void bwd_scores(Args a) {
             f32x4 g[NJ];
             zero(g);
             // G[(t,r),(s,j)] = sum_n C[t,n,r] Bf[s,n,j]
-            gemm_acc<TW>(g, s.N,
+            gemm_acc<TW, true, true>(g, s.N,
                          [&](int mm, int n) { const int m = m0 + mm; return q.c(m / R, n, m % R); },
                          [&](int n, int cc) {
                              const int c = c0 + cc;
@@ -318,7 +326,7 @@ __global__ __launch_bounds__(NTH) void bwd_scores(Args a) {
             // DX[(t,r),(s,j)] = sum_p dy[t,p,r] dt_s x[s,p,j]; gemm_acc's first barrier orders
             // the zp writes above before the reads below
             zero(g);
-            gemm_acc<TW>(g, s.P,
+            gemm_acc<TW, true, true>(g, s.P,
                          [&](int mm, int p) { const int m = m0 + mm; return q.dy(m / R, p, m % R); },
                          [&](int p, int cc) {
                              const int c = c0 + cc, t = c / R2;
@@ -396,7 +404,7 @@ __global__ __launch_bounds__(NTH) void bwd_dxf(Args a) {
     const float* dH = a.dch + chx(s, b, k, h) * s.PN;
     f32x4 acc[4];
     zero(acc);
-    gemm_acc<TT>(acc, s.N,
+    gemm_acc<TT, true, true>(acc, s.N,
              [&](int mm, int n) { const int m = m0 + mm; return q.bf(m / R2, n, m % R2); },
              [&](int n, int pp) { const int p = p0 + pp; return p < s.P ? dH[(int64_t)p * s.N + n] : 0.f; },
              l);
@@ -418,7 +426,7 @@ __global__ __launch_bounds__(NTH) void bwd_dxf(Args a) {
     tile_token_sums(rv, per, red, outv);
     if (tid < nts) a.pState[((int64_t)ch * s.nPt + pt) * QB + m0 / per + tid] = outv[tid];
     const float* Mi = a.M + (int64_t)ch * QR * QR2;
-    gemm_acc<TT>(acc, QR,
+    gemm_acc<TT, false, false>(acc, QR,
              [&](int mm, int jr) { return Mi[(int64_t)jr * QR2 + m0 + mm]; },
              [&](int jr, int pp) {
                  const int p = p0 + pp;
@@ -466,7 +474,7 @@ __global__ __launch_bounds__(NTH) void bwd_dbf(Args a) {
     const float* dH = a.dch + chx(s, b, k, h) * s.PN;
     f32x4 acc[NJ];
     zero(acc);
-    gemm_acc<TW>(acc, s.P,
+    gemm_acc<TW, true, false>(acc, s.P,
              [&](int mm, int p) {
                  const int m = m0 + mm, t = m / R2;
                  return dts[t] * q.x(t, p, m % R2);
@@ -480,7 +488,7 @@ __global__ __launch_bounds__(NTH) void bwd_dbf(Args a) {
         for (int j = 0; j < NJ; ++j) acc[j][i] *= e;
     }
     const float* DMi = a.DM + (int64_t)ch * QR * QR2;
-    gemm_acc<TW>(acc, QR,
+    gemm_acc<TW, false, false>(acc, QR,
              [&](int mm, int jr) { return DMi[(int64_t)jr * QR2 + m0 + mm]; },
              [&](int jr, int nn) {
                  const int n = n0 + nn;
@@ -520,7 +528,7 @@ __global__ __launch_bounds__(NTH) void bwd_dc(Args a) {
     const float* Hk = a.Hs + chx(s, b, k, h) * s.PN;
     f32x4 acc[NJ];
     zero(acc);
-    gemm_acc<TW>(acc, s.P,
+    gemm_acc<TW, true, false>(acc, s.P,
              [&](int mm, int p) { const int m = m0 + mm; return q.dy(m / R, p, m % R); },
              [&](int p, int nn) { const int n = n0 + nn; return n < s.N ? Hk[(int64_t)p * s.N + n] : 0.f; },
              l);
@@ -541,7 +549,7 @@ __global__ __launch_bounds__(NTH) void bwd_dc(Args a) {
     tile_token_sums(rv, per, red, outv);
     if (tid < nts) a.pInter[((int64_t)ch * s.nNt + nt) * QB + m0 / per + tid] = outv[tid];
     const float* DMi = a.DM + (int64_t)ch * QR * QR2;
-    gemm_acc<TW>(acc, QR2,
+    gemm_acc<TW, true, false>(acc, QR2,
              [&](int mm, int jc) { return DMi[(int64_t)(m0 + mm) * QR2 + jc]; },
              [&](int jc, int nn) {
                  const int n = n0 + nn;
