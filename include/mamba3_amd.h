@@ -160,14 +160,28 @@ int m3_step_fwd(const m3_layer_desc* desc, const m3_layer_params* params,
  *   x_g, x_raw [B,T,H,P,R]; x_b [B,T,H,P,R] or NULL (then B_b must be NULL);
  *   B_g, C [B,T,H,N,R]; B_b [B,T,H,N,R] or NULL; dt [B,T,H];
  *   h_init [B,H,P,N] fp32 or NULL; y [B,T,H,P,R] in dtype; h_final [B,H,P,N] or NULL.
- * state_ws: [B,H,P,N] fp32 scratch owned by the caller (may equal h_final).
+ * state_ws: [B,H,P,N] fp32 scratch owned by the caller (may equal h_final), used by the
+ * generic kernel. workspace (256-byte aligned, m3_chunked_ssd_fwd_workspace_size() bytes, or
+ * NULL): with it, fp32 inputs run on the fp32-MFMA chunk kernels shared with
+ * m3_chunked_ssd_bwd (chunk states, state scan, masked scores, output tiles).
  */
 int m3_chunked_ssd_fwd(int32_t batch, int32_t seqlen, int32_t nheads, int32_t headdim,
                        int32_t d_state, int32_t mimo_rank, int32_t dtype,
                        const void* x_g, const void* x_b, const void* B_g, const void* B_b,
                        const void* C, const void* dt, const float* A, const float* D,
                        const void* x_raw, const float* h_init, void* y, float* h_final,
-                       float* state_ws, void* stream);
+                       float* state_ws, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Bytes of device workspace with which m3_chunked_ssd_fwd runs fp32 inputs on its fp32-MFMA
+ * chunk kernels (mimo_rank 1, 2, 4 or 8; headdim * d_state a multiple of 256 or at most
+ * 16384). 0: that path does not apply (bf16, other shapes); m3_chunked_ssd_fwd then runs the
+ * generic kernel, as it also does when no workspace (or too small a one) is passed. No
+ * counterpart in the reference, which allocates inside ATen.
+ */
+int m3_chunked_ssd_fwd_workspace_size(int32_t batch, int32_t seqlen, int32_t nheads,
+                                      int32_t headdim, int32_t d_state, int32_t mimo_rank,
+                                      int32_t dtype, int32_t has_beta, size_t* bytes);
 
 /*
  * Backward of m3_chunked_ssd_fwd, all tensors fp32 (the caller upcasts bf16). Replaces the

@@ -31,6 +31,7 @@ EXPORTED_SYMBOLS = (
     "m3_prefill_fwd",
     "m3_step_fwd",
     "m3_chunked_ssd_fwd",
+    "m3_chunked_ssd_fwd_workspace_size",
     "m3_chunked_ssd_bwd_workspace_size",
     "m3_chunked_ssd_bwd",
 )
@@ -95,7 +96,9 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.m3_chunked_ssd_fwd.restype = ctypes.c_int
     lib.m3_chunked_ssd_fwd.argtypes = [_i32, _i32, _i32, _i32, _i32, _i32, _i32,
                                        _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
-                                       _vp, _vp, _vp, _vp]
+                                       _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp]
+    lib.m3_chunked_ssd_fwd_workspace_size.restype = ctypes.c_int
+    lib.m3_chunked_ssd_fwd_workspace_size.argtypes = [_i32] * 8 + [ctypes.POINTER(ctypes.c_size_t)]
     lib.m3_chunked_ssd_bwd_workspace_size.restype = ctypes.c_int
     lib.m3_chunked_ssd_bwd_workspace_size.argtypes = [_i32] * 7 + [ctypes.POINTER(ctypes.c_size_t)]
     lib.m3_chunked_ssd_bwd.restype = ctypes.c_int
@@ -191,10 +194,17 @@ def step_fwd(desc: LayerDesc, params: LayerParams, proj, dt_scale, h_in, prev_in
 
 def chunked_fwd(B, T, H, P, N, R, dtype, x_g, x_b, B_g, B_b, C, dt, A, D, x_raw, h_init, y,
                 h_final, state_ws) -> None:
+    """m3_chunked_ssd_fwd; allocates the workspace of the fp32-MFMA path when it applies."""
+    n = ctypes.c_size_t(0)
+    check(lib().m3_chunked_ssd_fwd_workspace_size(B, T, H, P, N, R, dtype_code(dtype),
+                                                  int(x_b is not None), ctypes.byref(n)),
+          "m3_chunked_ssd_fwd_workspace_size")
+    ws = torch.empty(n.value, dtype=torch.uint8, device=x_g.device) if n.value else None
     check(lib().m3_chunked_ssd_fwd(B, T, H, P, N, R, dtype_code(dtype), ptr(x_g), ptr(x_b),
                                    ptr(B_g), ptr(B_b), ptr(C), ptr(dt), ptr(A), ptr(D),
                                    ptr(x_raw), ptr(h_init), ptr(y), ptr(h_final),
-                                   ptr(state_ws), stream_of(x_g)), "m3_chunked_ssd_fwd")
+                                   ptr(state_ws), ptr(ws), n.value, stream_of(x_g)),
+          "m3_chunked_ssd_fwd")
 
 
 def chunked_bwd_workspace_bytes(B, T, H, P, N, R, has_beta: bool) -> int:

@@ -177,12 +177,26 @@ int m3_step_fwd(const m3_layer_desc* desc, const m3_layer_params* params, const 
                            as_stream(stream));
 }
 
+int m3_chunked_ssd_fwd_workspace_size(int32_t batch, int32_t seqlen, int32_t nheads,
+                                      int32_t headdim, int32_t d_state, int32_t mimo_rank,
+                                      int32_t dtype, int32_t has_beta, size_t* bytes) {
+    if (!bytes) return M3_ERR_NULL_POINTER;
+    if (batch <= 0 || seqlen <= 0 || nheads <= 0 || headdim <= 0 || d_state <= 0 ||
+        mimo_rank <= 0 || (has_beta != 0 && has_beta != 1))
+        return M3_ERR_INVALID_SHAPE;
+    if (dtype != M3_DTYPE_F32 && dtype != M3_DTYPE_BF16) return M3_ERR_UNSUPPORTED;
+    *bytes = dtype == M3_DTYPE_F32 ? m3::chunked_fwd_mfma_workspace(batch, seqlen, nheads, headdim,
+                                                                    d_state, mimo_rank, has_beta)
+                                   : 0;
+    return M3_OK;
+}
+
 int m3_chunked_ssd_fwd(int32_t batch, int32_t seqlen, int32_t nheads, int32_t headdim,
                        int32_t d_state, int32_t mimo_rank, int32_t dtype, const void* x_g,
                        const void* x_b, const void* B_g, const void* B_b, const void* C,
                        const void* dt, const float* A, const float* D, const void* x_raw,
                        const float* h_init, void* y, float* h_final, float* state_ws,
-                       void* stream) {
+                       void* workspace, size_t workspace_bytes, void* stream) {
     if (batch <= 0 || seqlen <= 0 || nheads <= 0 || headdim <= 0 || d_state <= 0 ||
         mimo_rank <= 0)
         return M3_ERR_INVALID_SHAPE;
@@ -190,6 +204,20 @@ int m3_chunked_ssd_fwd(int32_t batch, int32_t seqlen, int32_t nheads, int32_t he
     if (headdim > 256 || d_state > 512 || mimo_rank > 8) return M3_ERR_UNSUPPORTED;
     if (!x_g || !B_g || !C || !dt || !A || !D || !x_raw || !y) return M3_ERR_NULL_POINTER;
     if ((x_b == nullptr) != (B_b == nullptr)) return M3_ERR_NULL_POINTER;
+    const size_t need = dtype == M3_DTYPE_F32
+                            ? m3::chunked_fwd_mfma_workspace(batch, seqlen, nheads, headdim,
+                                                             d_state, mimo_rank, x_b != nullptr)
+                            : 0;
+    if (need > 0 && workspace && workspace_bytes >= need) {
+        if (!aligned(workspace, 256)) return M3_ERR_MISALIGNED;
+        auto fp = [](const void* v) { return reinterpret_cast<const float*>(v); };
+        return m3::launch_chunked_fwd_mfma(batch, seqlen, nheads, headdim, d_state, mimo_rank,
+                                           fp(x_g), fp(x_b), fp(B_g), fp(B_b), fp(C), fp(dt), A, D,
+                                           fp(x_raw), h_init, reinterpret_cast<float*>(y),
+                                           h_final, workspace, as_stream(stream)) == 0
+                   ? M3_OK
+                   : M3_ERR_LAUNCH;
+    }
     if (!h_final && !state_ws) return M3_ERR_WORKSPACE;
     return m3::launch_generic_chunked(batch, seqlen, nheads, headdim, d_state, mimo_rank, dtype,
                                       x_g, x_b, B_g, B_b, C, dt, A, D, x_raw, h_init, y, h_final,

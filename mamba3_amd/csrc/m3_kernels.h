@@ -71,6 +71,13 @@ int launch_wide_prefill(const m3_layer_desc& d, const m3_layer_params& p, const 
 
 // Backward of the chunked SSD (fp32): shape support, workspace bytes and launcher.
 bool chunked_bwd_shape_ok(int B, int T, int H, int P, int N, int R, bool beta);
+// fp32 chunked SSD forward on the same chunk kernels (fp32 MFMA); 0 bytes = not supported.
+size_t chunked_fwd_mfma_workspace(int B, int T, int H, int P, int N, int R, bool beta);
+int launch_chunked_fwd_mfma(int B, int T, int H, int P, int N, int R, const float* x_g,
+                            const float* x_b, const float* B_g, const float* B_b, const float* C,
+                            const float* dt, const float* A, const float* D, const float* x_raw,
+                            const float* h_init, float* y, float* h_final, void* workspace,
+                            hipStream_t stream);
 size_t chunked_bwd_workspace(int B, int T, int H, int P, int N, int R, bool beta);
 int launch_chunked_bwd(int B, int T, int H, int P, int N, int R, const float* x_g,
                        const float* x_b, const float* B_g, const float* B_b, const float* C,

@@ -60,6 +60,9 @@ struct Args {
     // workspace
     float *cum, *dec, *ddec, *hext, *Hs, *gext, *dch, *M, *DM, *dcI, *pInter, *pState, *pDt,
         *pA, *pD;
+    // forward (fwd = 1): the chunk-state and score kernels skip their gradient halves
+    int fwd;
+    float *y, *hfin;
 };
 
 // Chunk ch = (b K + k) H + h (the scan's (B,K,H) order); its position in the (B,K+1,H)
@@ -241,6 +244,7 @@ __global__ __launch_bounds__(NTH) void bwd_states(Args a) {
             const int p = p0 + 4 * ty + i, n = n0 + tcol(tx, j);
             if (p < s.P && n < s.N) ho[(int64_t)p * s.N + n] = acc[j][i];
         }
+    if (!a.fwd) {
     zero(acc);
     gemm_acc<TW, false, false>(acc, QB * R,
                  [&](int mm, int j) {
@@ -260,6 +264,7 @@ __global__ __launch_bounds__(NTH) void bwd_states(Args a) {
             const int p = p0 + 4 * ty + i, n = n0 + tcol(tx, j);
             if (p < s.P && n < s.N) go[(int64_t)p * s.N + n] = acc[j][i];
         }
+    }
     if (k == s.K - 1) {
         float* he = a.hext + chx(s, b, s.K, h) * s.PN;
         float* ge = a.gext + chx(s, b, s.K, h) * s.PN;
@@ -272,7 +277,7 @@ __global__ __launch_bounds__(NTH) void bwd_states(Args a) {
                 if (p < s.P && n < s.N) {
                     const int64_t o = (int64_t)p * s.N + n;
                     he[o] = 0.f;
-                    ge[o] = df ? df[o] : 0.f;
+                    if (!a.fwd) ge[o] = df ? df[o] : 0.f;
                 }
             }
     }
@@ -323,6 +328,7 @@ __global__ __launch_bounds__(NTH) void bwd_scores(Args a) {
                     if (c < QR2) Mo[(int64_t)m * QR2 + c] = w * g[j][i];
                     zp[4 * ty + i][tcol(tx, j)] = w * g[j][i];
                 }
+            if (a.fwd) continue;
             // DX[(t,r),(s,j)] = sum_p dy[t,p,r] dt_s x[s,p,j]; gemm_acc's first barrier orders
             // the zp writes above before the reads below
             zero(g);
@@ -363,7 +369,7 @@ __global__ __launch_bounds__(NTH) void bwd_scores(Args a) {
             __syncthreads();
         }
     }
-    if (tid < QB) a.dcI[(int64_t)ch * QB + tid] = rowacc[tid] - colacc[tid];
+    if (!a.fwd && tid < QB) a.dcI[(int64_t)ch * QB + tid] = rowacc[tid] - colacc[tid];
 }
 
 // Sums v over the rows of the 64 x 64 tile that belong to one token (R2 consecutive rows per
@@ -657,6 +663,71 @@ __global__ __launch_bounds__(NTH) void bwd_reduce(Args a) {
     }
 }
 
+// ---- forward output: y rows (t,r) x columns p of the chunk,
+//   y = (W o G) Xf + exp(c_t) C H_k^T + D x_raw   (M = W o G from bwd_scores in forward mode)
+template <int R, bool BETA>
+__global__ __launch_bounds__(NTH) void fwd_out(Args a) {
+    BW_CONSTS
+    __shared__ Lds<TT> l;
+    __shared__ float cs[64], dts[64];
+    const Shape& s = a.s;
+    const int ch = blockIdx.x, h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
+    const int rt = blockIdx.y / s.nPt, pt = blockIdx.y % s.nPt;
+    const int m0 = rt * TT, p0 = pt * TT;
+    const Chunk<R, BETA> q{&a, b, k, h};
+    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+    if (tid < QB) {
+        cs[tid] = a.cum[(int64_t)ch * QB + tid];
+        dts[tid] = q.dtv(tid);
+    }
+    __syncthreads();
+    const float* Hk = a.Hs + chx(s, b, k, h) * s.PN;
+    f32x4 acc[4];
+    zero(acc);
+    gemm_acc<TT, true, true>(acc, s.N,
+                             [&](int mm, int n) { const int m = m0 + mm; return q.c(m / R, n, m % R); },
+                             [&](int n, int pp) {
+                                 const int p = p0 + pp;
+                                 return p < s.P ? Hk[(int64_t)p * s.N + n] : 0.f;
+                             },
+                             l);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float e = __expf(cs[(m0 + 4 * ty + i) / R]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[j][i] *= e;
+    }
+    const float* Mi = a.M + (int64_t)ch * QR * QR2;
+    gemm_acc<TT, true, false>(acc, QR2,
+                              [&](int mm, int jc) { return Mi[(int64_t)(m0 + mm) * QR2 + jc]; },
+                              [&](int jc, int pp) {
+                                  const int p = p0 + pp, u = jc / R2;
+                                  return p < s.P ? dts[u] * q.x(u, p, jc % R2) : 0.f;
+                              },
+                              l);
+    const float Dh = a.D[h];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = m0 + 4 * ty + i, t = m / R, r = m % R;
+        if (!q.real(t)) continue;
+        const int64_t base = row(s, b, k * QB + t, h) * s.P * R + r;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int p = p0 + tcol(tx, j);
+            if (p < s.P) a.y[base + (int64_t)p * R] = acc[j][i] + Dh * a.xr[base + (int64_t)p * R];
+        }
+    }
+}
+
+// h_final = the state after the last chunk (entry K of the extended scan output).
+__global__ __launch_bounds__(NTH) void fwd_final(Args a) {
+    const Shape& s = a.s;
+    const int bh = blockIdx.x, b = bh / s.H, h = bh % s.H;
+    const float* src = a.Hs + chx(s, b, s.K, h) * s.PN;
+    float* dst = a.hfin + (int64_t)bh * s.PN;
+    for (int64_t i = threadIdx.x; i < s.PN; i += NTH) dst[i] = src[i];
+}
+
 // Workspace carve-up (all fp32, each part 256-byte aligned).
 struct Plan {
     Shape s;
@@ -725,7 +796,75 @@ int launch(const Args& a, const float* h_init, float* dh_init, float* scan_ws, h
     return hipGetLastError() == hipSuccess ? 0 : 1;
 }
 
+// Forward workspace: c, chunk decays, chunk-local states, scanned states, W o G.
+Plan make_plan_fwd(const Shape& s) {
+    Plan pl;
+    pl.s = s;
+    const size_t BKH = (size_t)s.B * s.K * s.H, BK1H = (size_t)s.B * (s.K + 1) * s.H;
+    const size_t sizes[5] = {BKH * s.Qb, BK1H, BK1H * s.PN, BK1H * s.PN, BKH * s.QR() * s.QR2()};
+    size_t o = 0;
+    for (int i = 0; i < 5; ++i) {
+        pl.off[i] = o;
+        o += al(sizes[i] * sizeof(float));
+    }
+    pl.scan_off = o;
+    pl.total = o;
+    return pl;
+}
+
+template <int R, bool BETA>
+int launch_fwd(const Args& a, const float* h_init, hipStream_t stream) {
+    BW_CONSTS
+    const Shape& s = a.s;
+    const unsigned nch = (unsigned)((int64_t)s.B * s.K * s.H);
+    constexpr int nRt = QR / TT;
+    hipLaunchKernelGGL((bwd_cum<R, BETA>), dim3(nch), dim3(64), 0, stream, a);
+    hipLaunchKernelGGL((bwd_states<R, BETA>), dim3(nch, s.nPt * s.nNt), dim3(NTH), 0, stream, a);
+    if (launch_scan_fwd(a.dec, a.hext, h_init, a.Hs, s.B, s.K + 1, s.H, s.PN, stream) != 0) return 1;
+    hipLaunchKernelGGL((bwd_scores<R, BETA>), dim3(nch), dim3(NTH), 0, stream, a);
+    hipLaunchKernelGGL((fwd_out<R, BETA>), dim3(nch, nRt * s.nPt), dim3(NTH), 0, stream, a);
+    if (a.hfin) hipLaunchKernelGGL(fwd_final, dim3(s.B * s.H), dim3(NTH), 0, stream, a);
+    return hipGetLastError() == hipSuccess ? 0 : 1;
+}
+
 }  // namespace bw
+
+size_t chunked_fwd_mfma_workspace(int B, int T, int H, int P, int N, int R, bool beta) {
+    bw::Shape s;
+    if (!chunked_bwd_shape_ok(B, T, H, P, N, R, beta) || !bw::make_shape(B, T, H, P, N, R, beta, s))
+        return 0;
+    return bw::make_plan_fwd(s).total;
+}
+
+int launch_chunked_fwd_mfma(int B, int T, int H, int P, int N, int R, const float* x_g,
+                            const float* x_b, const float* B_g, const float* B_b, const float* C,
+                            const float* dt, const float* A, const float* D, const float* x_raw,
+                            const float* h_init, float* y, float* h_final, void* workspace,
+                            hipStream_t stream) {
+    using namespace bw;
+    Shape s;
+    if (!make_shape(B, T, H, P, N, R, x_b != nullptr, s)) return 1;
+    const Plan pl = make_plan_fwd(s);
+    char* ws = reinterpret_cast<char*>(workspace);
+    auto part = [&](int i) { return reinterpret_cast<float*>(ws + pl.off[i]); };
+    Args a = {};
+    a.s = s;
+    a.xg = x_g, a.xb = x_b, a.Bg = B_g, a.Bb = B_b, a.C = C, a.dt = dt, a.A = A, a.D = D;
+    a.xr = x_raw, a.hinit = h_init;
+    a.cum = part(0), a.dec = part(1), a.hext = part(2), a.Hs = part(3), a.M = part(4);
+    a.fwd = 1, a.y = y, a.hfin = h_final;
+    switch (R * 2 + (x_b != nullptr ? 1 : 0)) {
+        case 2: return launch_fwd<1, false>(a, h_init, stream);
+        case 3: return launch_fwd<1, true>(a, h_init, stream);
+        case 4: return launch_fwd<2, false>(a, h_init, stream);
+        case 5: return launch_fwd<2, true>(a, h_init, stream);
+        case 8: return launch_fwd<4, false>(a, h_init, stream);
+        case 9: return launch_fwd<4, true>(a, h_init, stream);
+        case 16: return launch_fwd<8, false>(a, h_init, stream);
+        case 17: return launch_fwd<8, true>(a, h_init, stream);
+        default: return 1;
+    }
+}
 
 bool chunked_bwd_shape_ok(int B, int T, int H, int P, int N, int R, bool beta) {
     bw::Shape s;
@@ -764,6 +903,7 @@ int launch_chunked_bwd(int B, int T, int H, int P, int N, int R, const float* x_
     a.gext = part(5), a.dch = part(6), a.M = part(7), a.DM = part(8), a.dcI = part(9);
     a.pInter = part(10), a.pState = part(11), a.pDt = part(12), a.pA = part(13), a.pD = part(14);
     float* scan_ws = reinterpret_cast<float*>(ws + pl.scan_off);
+    a.fwd = 0, a.y = nullptr, a.hfin = nullptr;
 
     const bool beta = x_b != nullptr;
     switch (R * 2 + (beta ? 1 : 0)) {

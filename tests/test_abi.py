@@ -144,8 +144,29 @@ def test_prefill_and_step_reject_missing_pointers(lib):
 
 def test_chunked_rejects_bad_arguments(lib):
     assert lib.m3_chunked_ssd_fwd(1, 4, 2, 4, 8, 2, 0, 256, 256, 256, None, 256, 256, 256, 256,
-                                  256, None, 256, 256, None, None) == 1
+                                  256, None, 256, 256, None, None, 0, None) == 1
     assert lib.m3_chunked_ssd_fwd(1, 0, 2, 4, 8, 2, 0, 256, None, 256, None, 256, 256, 256, 256,
-                                  256, None, 256, 256, None, None) == 2
+                                  256, None, 256, 256, None, None, 0, None) == 2
     assert lib.m3_chunked_ssd_fwd(1, 4, 2, 4, 8, 2, 5, 256, None, 256, None, 256, 256, 256, 256,
-                                  256, None, 256, 256, None, None) == 3
+                                  256, None, 256, 256, None, None, 0, None) == 3
+    # the generic path needs h_final or state_ws when no (or too small a) workspace is given
+    assert lib.m3_chunked_ssd_fwd(1, 4, 2, 4, 8, 2, 0, 256, None, 256, None, 256, 256, 256, 256,
+                                  256, None, 256, None, None, None, 0, None) == 4
+    # a misaligned workspace for the fp32-MFMA path
+    assert lib.m3_chunked_ssd_fwd(1, 4, 2, 4, 8, 2, 0, 256, None, 256, None, 256, 256, 256, 256,
+                                  256, None, 256, 256, None, 260, 1 << 30, None) == 5
+
+
+def test_chunked_fwd_workspace_query(lib):
+    n = ctypes.c_size_t(7)
+    # fp32 d_model 768 shapes: c, decays, two (B, K+1, H, P*N) state arrays and W o G
+    assert lib.m3_chunked_ssd_fwd_workspace_size(4, 1024, 24, 64, 128, 2, 0, 1, ctypes.byref(n)) == 0
+    K = 1024 // 32
+    assert n.value >= 2 * 4 * (K + 1) * 24 * 64 * 128 * 4 + 4 * K * 24 * 64 * 128 * 4
+    # bf16 and unsupported ranks take the generic kernel: no workspace
+    assert lib.m3_chunked_ssd_fwd_workspace_size(4, 1024, 24, 64, 128, 2, 1, 1, ctypes.byref(n)) == 0
+    assert n.value == 0
+    assert lib.m3_chunked_ssd_fwd_workspace_size(4, 1024, 24, 64, 128, 3, 0, 1, ctypes.byref(n)) == 0
+    assert n.value == 0
+    assert lib.m3_chunked_ssd_fwd_workspace_size(4, 1024, 24, 64, 128, 2, 0, 2, ctypes.byref(n)) == 2
+    assert lib.m3_chunked_ssd_fwd_workspace_size(4, 1024, 24, 64, 128, 2, 7, 1, ctypes.byref(n)) == 3
