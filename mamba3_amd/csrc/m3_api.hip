@@ -107,10 +107,11 @@ int m3_scan_bwd(const float* decay, const float* h_states, const float* grad, fl
 
 // Workspace for whichever prefill kernel the shape may dispatch to: the d_state 128 /
 // headdim 64 / rank 2 MFMA kernel (bf16, aligned rows, 16-byte aligned proj / y_out), the
-// general MFMA kernel (bf16, d_state 64/128/256, rank 1/2/4, headdim % 32 == 0) or the
-// generic kernel.
+// general MFMA kernel (bf16, d_state 64/128/256, rank 1/2/4, headdim % 32 == 0), the fp32
+// layer path on the fp32-MFMA chunk kernels (fp32, rank 1/2/4/8) or the generic kernel.
 static size_t prefill_workspace(const m3_layer_desc& d) {
     size_t n = m3::generic_prefill_workspace(d);
+    n = std::max(n, m3::fp32_layer_workspace(d));
     if (m3::mfma_prefill_supported(d, nullptr, nullptr)) n = std::max(n, m3::mfma_prefill_workspace(d));
     if (m3::wide_prefill_supported(d)) n = std::max(n, m3::wide_prefill_workspace(d));
     return n;
@@ -145,6 +146,14 @@ int m3_prefill_fwd(const m3_layer_desc* desc, const m3_layer_params* params, con
         if (!aligned(workspace, 256)) return M3_ERR_MISALIGNED;
         return m3::launch_wide_prefill(*desc, *params, proj, dt_scale, y_out, h_final, angle,
                                        prev_bx, workspace, as_stream(stream));
+    }
+    if (m3::fp32_layer_supported(*desc)) {
+        if (!workspace || workspace_bytes < m3::fp32_layer_workspace(*desc)) return M3_ERR_WORKSPACE;
+        if (!aligned(workspace, 256)) return M3_ERR_MISALIGNED;
+        return m3::launch_fp32_layer(*desc, *params, proj, dt_scale, y_out, h_final, angle,
+                                     prev_bx, workspace, as_stream(stream)) == 0
+                   ? M3_OK
+                   : M3_ERR_LAUNCH;
     }
     const size_t need = m3::generic_prefill_workspace(*desc);
     if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return M3_ERR_WORKSPACE;

@@ -87,6 +87,13 @@ int launch_chunked_bwd(int B, int T, int H, int P, int N, int R, const float* x_
                        float* dD, float* dx_raw, float* dh_init, void* workspace,
                        hipStream_t stream);
 
+// fp32 layer prefill on the fp32-MFMA chunk kernels (preparation, chunked SSD, gate).
+bool fp32_layer_supported(const m3_layer_desc& d);
+size_t fp32_layer_workspace(const m3_layer_desc& d);
+int launch_fp32_layer(const m3_layer_desc& d, const m3_layer_params& p, const void* proj,
+                      const float* dt_scale, void* y_out, float* h_final, float* angle,
+                      float* prev_bx, void* workspace, hipStream_t stream);
+
 // Returns 1 when the step kernel supports (N, R), else 0.
 int step_supported(int N, int R);
 int launch_step(const m3_layer_desc& d, const m3_layer_params& p, const void* proj,

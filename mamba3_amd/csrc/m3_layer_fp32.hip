@@ -1,0 +1,301 @@
+// fp32 layer prefill on the fp32-MFMA chunk kernels: the region between in_proj and out_proj
+// (mamba3/mamba3.py:199-256) for fp32 layers, as
+//   lp_dt      dt = softplus(dt_raw + dt_bias) [* dt_scale], A = -exp(A_log)
+//              (mamba3/mamba3.py:200-204)
+//   lp_angle_sums, lp_angles
+//              the RoPE angle prefix phi_t = -sum_{s<=t} dt_s theta_s (mamba3/mamba3.py:160-162)
+//              in chunks of 64 tokens
+//   lp_prep    per token: B/C RMSNorm + weight + bias per group (mamba3/mamba3.py:19-35,
+//              147-157), the rotation by phi per head (mamba3/mamba3.py:38-45, 163-166), the
+//              MIMO x (mamba3/mamba3.py:219) and the trapezoid terms x_g = lambda x_r,
+//              x_b = (1 - lambda) dA x_r[t-1], B_b = B~[t-1] (mamba3/mamba3.py:221-229)
+//   chunked SSD forward (m3_ssd_bwd.hip, fp32 MFMA)
+//   lp_gate    out = sum_r mimo_down y silu(z mimo_z) (mamba3/mamba3.py:233-239)
+//   lp_state   angle = phi_{T-1}, prev_BX = B~_{T-1} x_r,{T-1}^T (mamba3/mamba3.py:241-256)
+// The intermediate tensors (chunked_ssd's inputs, in its (B,T,H,X,R) layouts) live in the
+// caller's workspace.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "m3_kernels.h"
+
+namespace m3 {
+namespace lp {
+
+struct Args {
+    int B, T, H, P, N, R, G, trap, cplx;
+    int64_t rs;  // proj row stride
+    ProjLayout pl;
+    float eps;
+    m3_layer_params prm;
+    const float* proj;
+    const float* dt_scale;
+    float *dt, *A, *phi, *phi_sum, *xg, *xb, *xr, *Bt, *Bb, *Ct, *ys;  // workspace
+    float *y, *h_final, *angle, *prev_bx;                     // outputs
+};
+
+constexpr int NTH = 256;
+
+__device__ __forceinline__ float softplus(float v) { return v > 20.f ? v : log1pf(expf(v)); }
+
+// dt[b,t,h] and A[h].
+__global__ __launch_bounds__(NTH) void lp_dt(Args a) {
+    const int64_t n = (int64_t)a.B * a.T * a.H;
+    const int64_t e = (int64_t)blockIdx.x * NTH + threadIdx.x;
+    if (e < a.H) a.A[e] = -expf(a.prm.A_log[e]);
+    if (e >= n) return;
+    const int h = (int)(e % a.H);
+    float d = softplus(a.proj[(e / a.H) * a.rs + a.pl.dt + h] + a.prm.dt_bias[h]);
+    if (a.dt_scale) d *= a.dt_scale[e];
+    a.dt[e] = d;
+}
+
+// RoPE angles phi_t = -sum_{s<=t} dt_s theta_s in chunks of kAC tokens: pass 1 writes each
+// chunk's sum, pass 2 walks each chunk from the sum of the chunks before it. One thread per
+// (b, chunk, h, pair).
+constexpr int kAC = 64;
+
+__device__ __forceinline__ void angle_job(const Args& a, int64_t e, int& b, int& c, int& h, int& i) {
+    const int NH = a.N / 2;
+    i = (int)(e % NH);
+    h = (int)((e / NH) % a.H);
+    const int64_t bc = e / ((int64_t)NH * a.H);
+    const int nc = (a.T + kAC - 1) / kAC;
+    c = (int)(bc % nc);
+    b = (int)(bc / nc);
+}
+
+__global__ __launch_bounds__(NTH) void lp_angle_sums(Args a) {
+    const int nc = (a.T + kAC - 1) / kAC;
+    const int64_t n = (int64_t)a.B * nc * a.H * (a.N / 2);
+    const int64_t e = (int64_t)blockIdx.x * NTH + threadIdx.x;
+    if (e >= n) return;
+    int b, c, h, i;
+    angle_job(a, e, b, c, h, i);
+    float s = 0.f;
+    const int t1 = min(a.T, (c + 1) * kAC);
+    for (int t = c * kAC; t < t1; ++t) {
+        const int64_t tok = (int64_t)b * a.T + t;
+        s += a.dt[tok * a.H + h] * a.proj[tok * a.rs + a.pl.theta + i];
+    }
+    a.phi_sum[e] = s;
+}
+
+__global__ __launch_bounds__(NTH) void lp_angles(Args a) {
+    const int nc = (a.T + kAC - 1) / kAC;
+    const int NH = a.N / 2;
+    const int64_t n = (int64_t)a.B * nc * a.H * NH;
+    const int64_t e = (int64_t)blockIdx.x * NTH + threadIdx.x;
+    if (e >= n) return;
+    int b, c, h, i;
+    angle_job(a, e, b, c, h, i);
+    float s = 0.f;
+    for (int cc = 0; cc < c; ++cc) s += a.phi_sum[(((int64_t)b * nc + cc) * a.H + h) * NH + i];
+    const int t1 = min(a.T, (c + 1) * kAC);
+    for (int t = c * kAC; t < t1; ++t) {
+        const int64_t tok = (int64_t)b * a.T + t;
+        s += a.dt[tok * a.H + h] * a.proj[tok * a.rs + a.pl.theta + i];
+        a.phi[(tok * a.H + h) * NH + i] = -s;
+    }
+}
+
+// One block per (b, t): normalised B^ / C^ of every group in LDS, then per head the rotated
+// rows and the x terms.
+__global__ __launch_bounds__(NTH) void lp_prep(Args a) {
+    extern __shared__ float sm[];  // B^ [G*N*R], C^ [G*N*R], reduction scratch [2*NTH]
+    const int bt = blockIdx.x, b = bt / a.T, t = bt % a.T;
+    const int NR = a.N * a.R, GNR = a.G * NR, NH = a.N / 2;
+    float* Bh = sm;
+    float* Ch = sm + GNR;
+    float* red = sm + 2 * GNR;
+    const float* row = a.proj + ((int64_t)b * a.T + t) * a.rs;
+    const int tid = threadIdx.x;
+    for (int g = 0; g < a.G; ++g) {
+        float sb = 0.f, sc = 0.f;
+        for (int e = tid; e < NR; e += NTH) {
+            const float vb = row[a.pl.B + (int64_t)g * NR + e], vc = row[a.pl.C + (int64_t)g * NR + e];
+            sb += vb * vb;
+            sc += vc * vc;
+        }
+        red[tid] = sb;
+        red[NTH + tid] = sc;
+        __syncthreads();
+        for (int w = NTH / 2; w > 0; w >>= 1) {
+            if (tid < w) {
+                red[tid] += red[tid + w];
+                red[NTH + tid] += red[NTH + tid + w];
+            }
+            __syncthreads();
+        }
+        const float rb = rsqrtf(red[0] / NR + a.eps), rc = rsqrtf(red[NTH] / NR + a.eps);
+        for (int e = tid; e < NR; e += NTH) {
+            const int64_t o = (int64_t)g * NR + e;
+            Bh[o] = row[a.pl.B + o] * rb * a.prm.B_norm_w[e] + a.prm.B_bias[o];
+            Ch[o] = row[a.pl.C + o] * rc * a.prm.C_norm_w[e] + a.prm.C_bias[o];
+        }
+        __syncthreads();
+    }
+    const int hpg = a.H / a.G;
+    for (int h = 0; h < a.H; ++h) {
+        const int g = h / hpg;
+        const int64_t tok = ((int64_t)b * a.T + t) * a.H + h;
+        const float* ph = a.phi + tok * NH;
+        for (int e = tid; e < NR; e += NTH) {
+            const int n = e / a.R, r = e % a.R, i = n >> 1;
+            const int64_t ev = (int64_t)g * NR + (2 * i) * a.R + r, od = ev + a.R;
+            float vb = Bh[(int64_t)g * NR + e], vc = Ch[(int64_t)g * NR + e];
+            if (a.cplx) {
+                float s, c;
+                sincosf(ph[i], &s, &c);
+                vb = (n & 1) ? Bh[ev] * s + Bh[od] * c : Bh[ev] * c - Bh[od] * s;
+                vc = (n & 1) ? Ch[ev] * s + Ch[od] * c : Ch[ev] * c - Ch[od] * s;
+            }
+            a.Bt[tok * NR + e] = vb;
+            a.Ct[tok * NR + e] = vc;
+            if (a.trap) {
+                if (t + 1 < a.T) a.Bb[(tok + a.H) * NR + e] = vb;  // B_b[t+1] = B~[t]
+                if (t == 0) a.Bb[tok * NR + e] = 0.f;
+            }
+        }
+        const float d = a.dt[tok];
+        float lam = 1.f, sb = 0.f;
+        if (a.trap) {
+            lam = 1.f / (1.f + expf(-row[a.pl.lam + h]));
+            sb = (1.f - lam) * expf(a.A[h] * d);
+        }
+        const int PR = a.P * a.R;
+        for (int e = tid; e < PR; e += NTH) {
+            const int p = e / a.R;
+            const float mx = a.prm.mimo_x[((int64_t)h * a.P + p) * a.R + e % a.R];
+            const float xr = row[a.pl.x + (int64_t)h * a.P + p] * mx;
+            a.xr[tok * PR + e] = xr;
+            a.xg[tok * PR + e] = xr * lam;
+            if (a.trap) {
+                const float xp = t > 0 ? row[a.pl.x + (int64_t)h * a.P + p - a.rs] * mx : 0.f;
+                a.xb[tok * PR + e] = xp * sb;
+            }
+        }
+    }
+}
+
+// out[b,t,h*P+p] = sum_r mimo_down[h,p,r] y[b,t,h,p,r] silu(z[b,t,h*P+p] mimo_z[h,p,r]).
+__global__ __launch_bounds__(NTH) void lp_gate(Args a) {
+    const int64_t n = (int64_t)a.B * a.T * a.H * a.P;
+    const int64_t HP = (int64_t)a.H * a.P;
+    for (int64_t e = (int64_t)blockIdx.x * NTH + threadIdx.x; e < n; e += (int64_t)gridDim.x * NTH) {
+        const int64_t tok = e / HP;
+        const int hp = (int)(e % HP);
+        const float z = a.proj[tok * a.rs + a.pl.z + hp];
+        float acc = 0.f;
+        for (int r = 0; r < a.R; ++r) {
+            const int64_t pr = (int64_t)hp * a.R + r;
+            const float zz = z * a.prm.mimo_z[pr];
+            acc += a.prm.mimo_down[pr] * a.ys[e * a.R + r] * (zz / (1.f + expf(-zz)));
+        }
+        a.y[e] = acc;
+    }
+}
+
+// angle = phi at t = T-1 (0 without RoPE); prev_BX[b,h,p,n] = sum_r B~[T-1,n,r] x_r[T-1,p,r].
+__global__ __launch_bounds__(NTH) void lp_state(Args a) {
+    const int bh = blockIdx.x, b = bh / a.H, h = bh % a.H;
+    const int NH = a.N / 2;
+    const int64_t tok = ((int64_t)b * a.T + a.T - 1) * a.H + h;
+    if (a.angle)
+        for (int i = threadIdx.x; i < NH; i += NTH)
+            a.angle[(int64_t)bh * NH + i] = a.cplx ? a.phi[tok * NH + i] : 0.f;
+    if (a.prev_bx) {
+        const int PN = a.P * a.N;
+        for (int e = threadIdx.x; e < PN; e += NTH) {
+            const int p = e / a.N, nn = e % a.N;
+            float acc = 0.f;
+            for (int r = 0; r < a.R; ++r)
+                acc += a.Bt[tok * a.N * a.R + (int64_t)nn * a.R + r] * a.xr[tok * a.P * a.R + (int64_t)p * a.R + r];
+            a.prev_bx[(int64_t)bh * PN + e] = acc;
+        }
+    }
+}
+
+struct Plan {
+    size_t off[11], chunk_off, total;
+};
+
+inline size_t al(size_t x) { return (x + 255) & ~(size_t)255; }
+
+Plan plan(const m3_layer_desc& d) {
+    const size_t BTH = (size_t)d.batch * d.seqlen * d.nheads;
+    const size_t X = BTH * d.headdim * d.mimo_rank, BN = BTH * d.d_state * d.mimo_rank;
+    const bool trap = d.use_trapezoidal != 0;
+    const size_t nc = (d.seqlen + kAC - 1) / kAC;
+    const size_t sizes[11] = {BTH, (size_t)d.nheads, BTH * (d.d_state / 2), X, trap ? X : 0, X,
+                              BN, trap ? BN : 0, BN, X,
+                              (size_t)d.batch * nc * d.nheads * (d.d_state / 2)};
+    Plan p;
+    size_t o = 0;
+    for (int i = 0; i < 11; ++i) {
+        p.off[i] = o;
+        o += al(sizes[i] * sizeof(float));
+    }
+    p.chunk_off = o;
+    o += al(chunked_fwd_mfma_workspace(d.batch, d.seqlen, d.nheads, d.headdim, d.d_state,
+                                       d.mimo_rank, trap));
+    p.total = o;
+    return p;
+}
+
+}  // namespace lp
+
+bool fp32_layer_supported(const m3_layer_desc& d) {
+    return d.dtype == M3_DTYPE_F32 &&
+           chunked_fwd_mfma_workspace(d.batch, d.seqlen, d.nheads, d.headdim, d.d_state,
+                                      d.mimo_rank, d.use_trapezoidal != 0) > 0;
+}
+
+size_t fp32_layer_workspace(const m3_layer_desc& d) {
+    return fp32_layer_supported(d) ? lp::plan(d).total : 0;
+}
+
+int launch_fp32_layer(const m3_layer_desc& d, const m3_layer_params& p, const void* proj,
+                      const float* dt_scale, void* y_out, float* h_final, float* angle,
+                      float* prev_bx, void* workspace, hipStream_t stream) {
+    using namespace lp;
+    const Plan pl = plan(d);
+    char* ws = reinterpret_cast<char*>(workspace);
+    auto part = [&](int i) { return reinterpret_cast<float*>(ws + pl.off[i]); };
+    Args a;
+    a.B = d.batch, a.T = d.seqlen, a.H = d.nheads, a.P = d.headdim, a.N = d.d_state;
+    a.R = d.mimo_rank, a.G = d.ngroups, a.trap = d.use_trapezoidal, a.cplx = d.use_complex;
+    a.rs = d.proj_row_stride, a.pl = proj_layout(d), a.eps = d.rms_eps, a.prm = p;
+    a.proj = reinterpret_cast<const float*>(proj);
+    a.dt_scale = dt_scale;
+    a.dt = part(0), a.A = part(1), a.phi = part(2), a.xg = part(3);
+    a.xb = a.trap ? part(4) : nullptr;
+    a.xr = part(5), a.Bt = part(6), a.Bb = a.trap ? part(7) : nullptr, a.Ct = part(8);
+    a.ys = part(9), a.phi_sum = part(10);
+    a.y = reinterpret_cast<float*>(y_out), a.h_final = h_final, a.angle = angle;
+    a.prev_bx = prev_bx;
+    const size_t lds = (2 * (size_t)d.ngroups * d.d_state * d.mimo_rank + 2 * NTH) * sizeof(float);
+    if (lds > 64 * 1024) return 1;
+    const int64_t nbth = (int64_t)d.batch * d.seqlen * d.nheads;
+    hipLaunchKernelGGL(lp_dt, dim3((unsigned)((std::max<int64_t>(nbth, d.nheads) + NTH - 1) / NTH)),
+                       dim3(NTH), 0, stream, a);
+    if (a.cplx) {
+        const int64_t na = (int64_t)d.batch * ((d.seqlen + kAC - 1) / kAC) * d.nheads * (d.d_state / 2);
+        const unsigned ga = (unsigned)((na + NTH - 1) / NTH);
+        hipLaunchKernelGGL(lp_angle_sums, dim3(ga), dim3(NTH), 0, stream, a);
+        hipLaunchKernelGGL(lp_angles, dim3(ga), dim3(NTH), 0, stream, a);
+    }
+    hipLaunchKernelGGL(lp_prep, dim3(d.batch * d.seqlen), dim3(NTH), lds, stream, a);
+    if (launch_chunked_fwd_mfma(a.B, a.T, a.H, a.P, a.N, a.R, a.xg, a.xb, a.Bt, a.Bb, a.Ct, a.dt,
+                                a.A, p.D, a.xr, nullptr, a.ys, h_final, ws + pl.chunk_off,
+                                stream) != 0)
+        return 1;
+    const int64_t n = (int64_t)d.batch * d.seqlen * d.nheads * d.headdim;
+    const unsigned grid = (unsigned)std::min<int64_t>((n + NTH - 1) / NTH, 65536);
+    hipLaunchKernelGGL(lp_gate, dim3(grid), dim3(NTH), 0, stream, a);
+    if (angle || prev_bx) hipLaunchKernelGGL(lp_state, dim3(d.batch * d.nheads), dim3(NTH), 0, stream, a);
+    return hipGetLastError() == hipSuccess ? 0 : 1;
+}
+
+}  // namespace m3

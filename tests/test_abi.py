@@ -106,8 +106,12 @@ def _desc(**kw):
 
 def test_workspace_query_and_desc_validation(lib):
     n = ctypes.c_size_t(0)
-    # fp32 layers run on the generic kernel, which keeps its state in LDS: no workspace
+    # fp32 layers run on the fp32-MFMA chunk kernels: chunked_ssd's inputs and the chunk
+    # workspace (B=1, T=4, H=8, P=16, N=16, R=2 with beta terms: chunks of 32 tokens)
     assert lib.m3_prefill_workspace_size(ctypes.byref(_desc()), ctypes.byref(n)) == 0
+    assert n.value >= 4 * 8 * (3 * 16 * 2 + 3 * 16 * 2 + 16 * 2) * 4
+    # ranks the chunk kernels do not cover run on the generic kernel (state in LDS): none
+    assert lib.m3_prefill_workspace_size(ctypes.byref(_desc(mimo_rank=3)), ctypes.byref(n)) == 0
     assert n.value == 0
     # bf16 d_state 128 / headdim 64 / rank 2: normalised B^ and C^ in f16, per token
     d768 = _desc(dtype=1, seqlen=64, nheads=24, headdim=64, d_state=128)
