@@ -192,13 +192,25 @@ def step_fwd(desc: LayerDesc, params: LayerParams, proj, dt_scale, h_in, prev_in
                             ptr(angle_out), stream_of(proj)), "m3_step_fwd")
 
 
+def chunked_fwd_mfma_applies(B, T, H, P, N, R, has_beta: bool) -> bool:
+    """True when m3_chunked_ssd_fwd runs fp32 inputs of this shape on its fp32-MFMA path."""
+    n = ctypes.c_size_t(0)
+    check(lib().m3_chunked_ssd_fwd_workspace_size(B, T, H, P, N, R, 0, int(has_beta),
+                                                  ctypes.byref(n)),
+          "m3_chunked_ssd_fwd_workspace_size")
+    return n.value > 0
+
+
 def chunked_fwd(B, T, H, P, N, R, dtype, x_g, x_b, B_g, B_b, C, dt, A, D, x_raw, h_init, y,
-                h_final, state_ws) -> None:
-    """m3_chunked_ssd_fwd; allocates the workspace of the fp32-MFMA path when it applies."""
+                h_final, state_ws, use_workspace: bool = True) -> None:
+    """m3_chunked_ssd_fwd; allocates the workspace of the fp32-MFMA path when it applies
+    (use_workspace=False runs the generic kernel)."""
     n = ctypes.c_size_t(0)
     check(lib().m3_chunked_ssd_fwd_workspace_size(B, T, H, P, N, R, dtype_code(dtype),
                                                   int(x_b is not None), ctypes.byref(n)),
           "m3_chunked_ssd_fwd_workspace_size")
+    if not use_workspace:
+        n.value = 0
     ws = torch.empty(n.value, dtype=torch.uint8, device=x_g.device) if n.value else None
     check(lib().m3_chunked_ssd_fwd(B, T, H, P, N, R, dtype_code(dtype), ptr(x_g), ptr(x_b),
                                    ptr(B_g), ptr(B_b), ptr(C), ptr(dt), ptr(A), ptr(D),

@@ -100,16 +100,21 @@ __global__ __launch_bounds__(NTH) void lp_angles(Args a) {
     }
 }
 
-// One block per (b, t): normalised B^ / C^ of every group in LDS, then per head the rotated
-// rows and the x terms.
+// One block per (b, t): normalised B^ / C^ of every group in LDS, the sin / cos of every
+// head's RoPE pairs in LDS, then the rotated rows of every head and the x terms, as flat loops
+// over (head, element).
 __global__ __launch_bounds__(NTH) void lp_prep(Args a) {
-    extern __shared__ float sm[];  // B^ [G*N*R], C^ [G*N*R], reduction scratch [2*NTH]
+    // B^ [G*N*R], C^ [G*N*R], reduction scratch [2*NTH], sin / cos [H*N/2] each
+    extern __shared__ float sm[];
     const int bt = blockIdx.x, b = bt / a.T, t = bt % a.T;
     const int NR = a.N * a.R, GNR = a.G * NR, NH = a.N / 2;
     float* Bh = sm;
     float* Ch = sm + GNR;
     float* red = sm + 2 * GNR;
+    float* sn = red + 2 * NTH;
+    float* cn = sn + (int64_t)a.H * NH;
     const float* row = a.proj + ((int64_t)b * a.T + t) * a.rs;
+    const int64_t tok0 = ((int64_t)b * a.T + t) * a.H;  // token row of head 0
     const int tid = threadIdx.x;
     for (int g = 0; g < a.G; ++g) {
         float sb = 0.f, sc = 0.f;
@@ -136,45 +141,43 @@ __global__ __launch_bounds__(NTH) void lp_prep(Args a) {
         }
         __syncthreads();
     }
+    if (a.cplx) {
+        for (int j = tid; j < a.H * NH; j += NTH) sincosf(a.phi[tok0 * NH + j], &sn[j], &cn[j]);
+        __syncthreads();
+    }
     const int hpg = a.H / a.G;
-    for (int h = 0; h < a.H; ++h) {
-        const int g = h / hpg;
-        const int64_t tok = ((int64_t)b * a.T + t) * a.H + h;
-        const float* ph = a.phi + tok * NH;
-        for (int e = tid; e < NR; e += NTH) {
-            const int n = e / a.R, r = e % a.R, i = n >> 1;
-            const int64_t ev = (int64_t)g * NR + (2 * i) * a.R + r, od = ev + a.R;
-            float vb = Bh[(int64_t)g * NR + e], vc = Ch[(int64_t)g * NR + e];
-            if (a.cplx) {
-                float s, c;
-                sincosf(ph[i], &s, &c);
-                vb = (n & 1) ? Bh[ev] * s + Bh[od] * c : Bh[ev] * c - Bh[od] * s;
-                vc = (n & 1) ? Ch[ev] * s + Ch[od] * c : Ch[ev] * c - Ch[od] * s;
-            }
-            a.Bt[tok * NR + e] = vb;
-            a.Ct[tok * NR + e] = vc;
-            if (a.trap) {
-                if (t + 1 < a.T) a.Bb[(tok + a.H) * NR + e] = vb;  // B_b[t+1] = B~[t]
-                if (t == 0) a.Bb[tok * NR + e] = 0.f;
-            }
+    for (int j = tid; j < a.H * NR; j += NTH) {
+        const int h = j / NR, e = j % NR, g = h / hpg;
+        const int n = e / a.R, r = e % a.R, i = n >> 1;
+        const int64_t ev = (int64_t)g * NR + (2 * i) * a.R + r, od = ev + a.R;
+        float vb = Bh[(int64_t)g * NR + e], vc = Ch[(int64_t)g * NR + e];
+        if (a.cplx) {
+            const float s = sn[h * NH + i], c = cn[h * NH + i];
+            vb = (n & 1) ? Bh[ev] * s + Bh[od] * c : Bh[ev] * c - Bh[od] * s;
+            vc = (n & 1) ? Ch[ev] * s + Ch[od] * c : Ch[ev] * c - Ch[od] * s;
         }
-        const float d = a.dt[tok];
-        float lam = 1.f, sb = 0.f;
+        const int64_t tok = tok0 + h;
+        a.Bt[tok * NR + e] = vb;
+        a.Ct[tok * NR + e] = vc;
         if (a.trap) {
-            lam = 1.f / (1.f + expf(-row[a.pl.lam + h]));
-            sb = (1.f - lam) * expf(a.A[h] * d);
+            if (t + 1 < a.T) a.Bb[(tok + a.H) * NR + e] = vb;  // B_b[t+1] = B~[t]
+            if (t == 0) a.Bb[tok * NR + e] = 0.f;
         }
-        const int PR = a.P * a.R;
-        for (int e = tid; e < PR; e += NTH) {
-            const int p = e / a.R;
-            const float mx = a.prm.mimo_x[((int64_t)h * a.P + p) * a.R + e % a.R];
-            const float xr = row[a.pl.x + (int64_t)h * a.P + p] * mx;
-            a.xr[tok * PR + e] = xr;
-            a.xg[tok * PR + e] = xr * lam;
-            if (a.trap) {
-                const float xp = t > 0 ? row[a.pl.x + (int64_t)h * a.P + p - a.rs] * mx : 0.f;
-                a.xb[tok * PR + e] = xp * sb;
-            }
+    }
+    const int PR = a.P * a.R;
+    for (int j = tid; j < a.H * PR; j += NTH) {
+        const int h = j / PR, e = j % PR, p = e / a.R;
+        const int64_t tok = tok0 + h;
+        const float mx = a.prm.mimo_x[(int64_t)h * PR + e];
+        const float xr = row[a.pl.x + (int64_t)h * a.P + p] * mx;
+        float lam = 1.f;
+        if (a.trap) lam = 1.f / (1.f + expf(-row[a.pl.lam + h]));
+        a.xr[tok * PR + e] = xr;
+        a.xg[tok * PR + e] = xr * lam;
+        if (a.trap) {
+            const float sb = (1.f - lam) * expf(a.A[h] * a.dt[tok]);
+            const float xp = t > 0 ? row[a.pl.x + (int64_t)h * a.P + p - a.rs] * mx : 0.f;
+            a.xb[tok * PR + e] = xp * sb;
         }
     }
 }
@@ -246,8 +249,16 @@ Plan plan(const m3_layer_desc& d) {
 
 }  // namespace lp
 
+namespace {
+// LDS of lp_prep: B^ and C^ of every group, the reduction scratch, sin / cos of every pair.
+size_t prep_lds(const m3_layer_desc& d) {
+    return (2 * (size_t)d.ngroups * d.d_state * d.mimo_rank + 2 * lp::NTH +
+            (size_t)d.nheads * d.d_state) * sizeof(float);
+}
+}  // namespace
+
 bool fp32_layer_supported(const m3_layer_desc& d) {
-    return d.dtype == M3_DTYPE_F32 &&
+    return d.dtype == M3_DTYPE_F32 && prep_lds(d) <= 64 * 1024 &&
            chunked_fwd_mfma_workspace(d.batch, d.seqlen, d.nheads, d.headdim, d.d_state,
                                       d.mimo_rank, d.use_trapezoidal != 0) > 0;
 }
@@ -275,7 +286,7 @@ int launch_fp32_layer(const m3_layer_desc& d, const m3_layer_params& p, const vo
     a.ys = part(9), a.phi_sum = part(10);
     a.y = reinterpret_cast<float*>(y_out), a.h_final = h_final, a.angle = angle;
     a.prev_bx = prev_bx;
-    const size_t lds = (2 * (size_t)d.ngroups * d.d_state * d.mimo_rank + 2 * NTH) * sizeof(float);
+    const size_t lds = prep_lds(d);
     if (lds > 64 * 1024) return 1;
     const int64_t nbth = (int64_t)d.batch * d.seqlen * d.nheads;
     hipLaunchKernelGGL(lp_dt, dim3((unsigned)((std::max<int64_t>(nbth, d.nheads) + NTH - 1) / NTH)),

@@ -69,6 +69,14 @@ def _forward(x_g, x_b, B_g, B_b, C, dt, A, D, x_raw, h_init):
     Bat, T, H, P, R = x_g.shape
     N = B_g.shape[3]
     dtype = x_g.dtype
+    if dtype != torch.float32 and _native.chunked_fwd_mfma_applies(Bat, T, H, P, N, R,
+                                                                   x_b is not None):
+        # bf16 inputs run on the fp32-MFMA chunk kernels (more accurate than the reference's
+        # bf16 intermediates, and far faster than the generic kernel)
+        f32 = [None if t is None else t.float() for t in (x_g, x_b, B_g, B_b, C, dt, x_raw)]
+        y, h_final = _forward(f32[0], f32[1], f32[2], f32[3], f32[4], f32[5], A, D, f32[6],
+                              h_init)
+        return y.to(dtype), h_final
 
     def prep(t):
         return None if t is None else t.to(dtype).contiguous()

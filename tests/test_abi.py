@@ -113,6 +113,11 @@ def test_workspace_query_and_desc_validation(lib):
     # ranks the chunk kernels do not cover run on the generic kernel (state in LDS): none
     assert lib.m3_prefill_workspace_size(ctypes.byref(_desc(mimo_rank=3)), ctypes.byref(n)) == 0
     assert n.value == 0
+    # so do layers whose per-token preparation would not fit its 64 KB of LDS (H * N floats of
+    # sin / cos): 64 heads x d_state 256
+    assert lib.m3_prefill_workspace_size(ctypes.byref(_desc(nheads=64, d_state=256)),
+                                         ctypes.byref(n)) == 0
+    assert n.value == 0
     # bf16 d_state 128 / headdim 64 / rank 2: normalised B^ and C^ in f16, per token
     d768 = _desc(dtype=1, seqlen=64, nheads=24, headdim=64, d_state=128)
     assert lib.m3_prefill_workspace_size(ctypes.byref(d768), ctypes.byref(n)) == 0

@@ -93,6 +93,46 @@ def test_chunked_ssd_matches_reference_golden(name, cuda_device):
     assert max_rel(res.h_final, torch.from_numpy(g["h_final"])) < FP32_TOL
 
 
+@pytest.mark.parametrize("beta,R", [(True, 2), (False, 1), (True, 4), (False, 3)])
+def test_chunked_ssd_generic_and_mfma_paths_match_oracle(beta, R, cuda_device):
+    """fp32 chunked_ssd on both native paths (the fp32-MFMA chunk kernels, used when a
+    workspace is given and the rank is 1/2/4/8, and the generic kernel) and in bf16 against
+    the fp32 oracle (mamba3/ssd.py:118-244)."""
+    g = torch.Generator().manual_seed(13)
+    Bt, T, H, P, N = 2, 150, 3, 16, 32
+    r = lambda *s: torch.randn(*s, generator=g)
+    x_g, x_raw = r(Bt, T, H, P, R), r(Bt, T, H, P, R)
+    x_b = r(Bt, T, H, P, R) if beta else None
+    B_g, C = r(Bt, T, H, N, R), r(Bt, T, H, N, R)
+    B_b = r(Bt, T, H, N, R) if beta else None
+    dt = torch.rand(Bt, T, H, generator=g) * 0.3
+    A, D, h0 = -torch.rand(H, generator=g) - 0.1, r(H), r(Bt, H, P, N)
+    y_ref, h_ref = ref.chunked_ssd(x_g.double(), None if x_b is None else x_b.double(),
+                                   B_g.double(), None if B_b is None else B_b.double(),
+                                   C.double(), dt.double(), A.double(), D.double(),
+                                   x_raw.double(), 64, h_init=h0.double(), return_final_state=True)
+    dev = cuda_device
+    to = lambda t, dtype=torch.float32: None if t is None else t.to(dev, dtype).contiguous()
+    for use_ws in (True, False):
+        y = torch.empty(Bt, T, H, P, R, device=dev)
+        hf = torch.empty(Bt, H, P, N, device=dev)
+        _native.chunked_fwd(Bt, T, H, P, N, R, torch.float32, to(x_g), to(x_b), to(B_g), to(B_b),
+                            to(C), to(dt), to(A), to(D), to(x_raw), to(h0), y, hf, None,
+                            use_workspace=use_ws)
+        assert max_rel(y, y_ref) < FP32_TOL, use_ws
+        assert max_rel(hf, h_ref) < FP32_TOL, use_ws
+    bf = lambda t: to(t, torch.bfloat16)
+    out = mamba3_amd.chunked_ssd(bf(x_g), bf(x_b), bf(B_g), bf(B_b), bf(C), bf(dt), to(A), to(D),
+                                 bf(x_raw), h_init=to(h0), return_final_state=True)
+    assert out.y.dtype == torch.bfloat16
+    y_ref_b, h_ref_b = ref.chunked_ssd(*[None if t is None else t.to(torch.bfloat16).double()
+                                         for t in (x_g, x_b, B_g, B_b, C, dt)],
+                                       A.double(), D.double(), x_raw.to(torch.bfloat16).double(),
+                                       64, h_init=h0.double(), return_final_state=True)
+    assert max_rel(out.y, y_ref_b) < BF16_TOL
+    assert max_rel(out.h_final, h_ref_b) < BF16_TOL
+
+
 def test_chunked_ssd_h_init_zero_equals_none(cuda_device):
     """Reference test_ssd_h_init (tests/test_mamba3.py:670-695)."""
     g = load_golden("chunked_beta_hinit")
