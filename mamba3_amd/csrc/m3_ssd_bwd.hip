@@ -1,6 +1,9 @@
-// Backward of the chunked SSD on pre-processed inputs (the op of m3_chunked_ssd_fwd), fp32.
+// fp32-MFMA chunk kernels of the chunked SSD on pre-processed inputs (the op of
+// m3_chunked_ssd_fwd): its backward, and (with Args::fwd set) its fp32 forward, which reuses
+// the chunk-state, scan and score kernels (their gradient halves skipped) and adds the output
+// tiles fwd_out (y = (W o G) Xf + exp(c_t) C H_k^T + D x_raw).
 //
-// Replaces, under autograd, the reference's chunked_ssd (mamba3/ssd.py:118-244): the custom
+// The backward replaces, under autograd, the reference's chunked_ssd (mamba3/ssd.py:118-244): the custom
 // backward of _IntraChunkFn (ssd.py:67-115), the scan backward (mamba3/scan.py:101-141,
 // mamba3/csrc/scan.cu:52-126) and ATen's backward of the bmm / cumsum / exp around them. The
 // reference differentiates through the materialised per-token outer products
