@@ -86,6 +86,25 @@ def test_chunked_ssd_backward_matches_oracle(case, cuda_device):
         assert gk.dtype == torch.float32 and gk.shape == leaf[k].shape
 
 
+def test_chunked_ssd_backward_long_sequence(cuda_device):
+    """2048 tokens (64 backward chunks): gradients carried through the state scans over many
+    chunks, against the fp64 oracle at the fp32 tolerance."""
+    case = (1, 2048, 2, 32, 64, 2, True, True, True)
+    B, T, H, P, N, R = case[:6]
+    ins = _inputs(case, seed=21)
+    ins["dt"] = ins["dt"] * 0.2  # keep exp(sum A dt) from underflowing over the sequence
+    g = torch.Generator().manual_seed(22)
+    dy = torch.randn(B, T, H, P, R, generator=g, dtype=torch.float64)
+    dhf = torch.randn(B, H, P, N, generator=g, dtype=torch.float64)
+    leaf = {k: (v.clone().requires_grad_() if v is not None else None) for k, v in ins.items()}
+    y, hf = ref.chunked_ssd(*[leaf[k] for k in NAMES[:9]], chunk_size=64, h_init=leaf["h_init"],
+                            return_final_state=True)
+    ((y * dy).sum() + (hf * dhf).sum()).backward()
+    _, grads = _gpu_grads(ins, dy, dhf, cuda_device)
+    for k, gk in grads.items():
+        assert max_rel(gk, leaf[k].grad) < FP32_TOL, k
+
+
 def test_chunked_ssd_backward_is_deterministic(cuda_device):
     case = (2, 150, 2, 32, 64, 2, True, True, True)
     B, T, H, P, N, R = case[:6]
@@ -152,6 +171,26 @@ def test_layer_prefill_gradients_match_oracle(kw, cuda_device):
     for name, p in layer.named_parameters():
         err = max_rel(p.grad, pg[name])
         assert err < FP32_TOL, (name, err)
+
+
+def test_layer_d768_gradients_match_oracle(cuda_device):
+    """The d_model 768 layer (24 heads, headdim 64, d_state 128, rank 2) over 160 tokens:
+    every parameter's gradient and the input's against the fp64 oracle layer."""
+    kw = dict(d_model=768, d_state=128, headdim=64, mimo_rank=2)
+    torch.manual_seed(0)
+    layer = mamba3_amd.KulaMamba(**kw).to(cuda_device).train()
+    g = torch.Generator().manual_seed(23)
+    x = torch.randn(1, 160, 768, generator=g)
+    w = torch.randn(1, 160, 768, generator=g)
+    wh = torch.randn(1, layer.nheads, 64, 128, generator=g)
+    out_ref, pg, xg_ref = _oracle_layer_grads(kw, layer, x, w, wh)
+    xd = x.to(cuda_device).requires_grad_()
+    out, st = layer.prefill(xd)
+    ((out * w.to(cuda_device)).sum() + (st["h"] * wh.to(cuda_device)).sum()).backward()
+    assert max_rel(out, out_ref) < FP32_TOL
+    assert max_rel(xd.grad, xg_ref) < FP32_TOL
+    for name, p in layer.named_parameters():
+        assert max_rel(p.grad, pg[name]) < FP32_TOL, name
 
 
 def test_layer_forward_gradients_with_dt_scale(cuda_device):
