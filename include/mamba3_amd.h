@@ -73,6 +73,21 @@ typedef struct m3_layer_params {
     const float* mimo_down;  /* [H,P,R] */
 } m3_layer_params;
 
+/* Gradients of the small per-layer parameters (fp32 device arrays, same shapes as
+ * m3_layer_params; written, not accumulated). */
+typedef struct m3_layer_param_grads {
+    float* A_log;
+    float* D;
+    float* dt_bias;
+    float* B_norm_w;
+    float* C_norm_w;
+    float* B_bias;
+    float* C_bias;
+    float* mimo_x;
+    float* mimo_z;
+    float* mimo_down;
+} m3_layer_param_grads;
+
 const char* m3_status_string(int status);
 
 /* Library version as major*10000 + minor*100 + patch. */
@@ -110,6 +125,25 @@ int m3_scan_bwd_workspace_size(int64_t batch, int64_t nchunks, int64_t nheads, i
 int m3_scan_bwd(const float* decay, const float* h_states, const float* grad, float* d_decay,
                 float* d_chunk, float* d_h_init, void* workspace, size_t workspace_bytes,
                 int64_t batch, int64_t nchunks, int64_t nheads, int64_t pn, void* stream);
+
+/*
+ * Backward of m3_prefill_fwd for fp32 layers (desc->dtype fp32, mimo_rank 1/2/4/8), from the
+ * workspace of that forward call, which holds its intermediates (pass the same buffer, unchanged,
+ * with its size). Replaces the reference's autograd through mamba3/mamba3.py:197-256 (ATen's
+ * backward of the dt softplus, the B/C RMSNorm + bias, the RoPE rotation and its angle cumsum,
+ * the MIMO and trapezoid terms and the SiLU gate) and through chunked_ssd (see
+ * m3_chunked_ssd_bwd). Inputs: g_out [B,T,H*P] = dL/d(gated output), and nullable g_h
+ * [B,H,P,N], g_angle [B,H,N/2], g_prev [B,H,P,N] for the prefill state; outputs g_proj
+ * [B,proj_row_stride] (every column of the in_proj layout written) and the parameter
+ * gradients `grads` (written, not accumulated). fp32 throughout; deterministic.
+ * workspace: m3_layer_bwd_workspace_size() bytes, 256-byte aligned.
+ */
+int m3_layer_bwd_workspace_size(const m3_layer_desc* desc, size_t* bytes);
+int m3_layer_bwd(const m3_layer_desc* desc, const m3_layer_params* params, const void* proj,
+                 const float* dt_scale, void* fwd_workspace, size_t fwd_workspace_bytes,
+                 const float* g_out, const float* g_h, const float* g_angle, const float* g_prev,
+                 float* g_proj, const m3_layer_param_grads* grads, void* workspace,
+                 size_t workspace_bytes, void* stream);
 
 /*
  * Bytes of device workspace m3_prefill_fwd needs for `desc` (0 is possible).

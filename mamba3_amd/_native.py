@@ -34,6 +34,8 @@ EXPORTED_SYMBOLS = (
     "m3_chunked_ssd_fwd_workspace_size",
     "m3_chunked_ssd_bwd_workspace_size",
     "m3_chunked_ssd_bwd",
+    "m3_layer_bwd_workspace_size",
+    "m3_layer_bwd",
 )
 
 
@@ -62,6 +64,10 @@ class LayerParams(ctypes.Structure):
     _fields_ = [(name, ctypes.c_void_p) for name in (
         "A_log", "D", "dt_bias", "B_norm_w", "C_norm_w", "B_bias", "C_bias",
         "mimo_x", "mimo_z", "mimo_down")]
+
+
+class LayerParamGrads(ctypes.Structure):
+    _fields_ = LayerParams._fields_
 
 
 _lib = None
@@ -99,6 +105,12 @@ def _declare(lib: ctypes.CDLL) -> None:
                                        _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp]
     lib.m3_chunked_ssd_fwd_workspace_size.restype = ctypes.c_int
     lib.m3_chunked_ssd_fwd_workspace_size.argtypes = [_i32] * 8 + [ctypes.POINTER(ctypes.c_size_t)]
+    lib.m3_layer_bwd_workspace_size.restype = ctypes.c_int
+    lib.m3_layer_bwd_workspace_size.argtypes = [ctypes.POINTER(LayerDesc), ctypes.POINTER(ctypes.c_size_t)]
+    lib.m3_layer_bwd.restype = ctypes.c_int
+    lib.m3_layer_bwd.argtypes = ([ctypes.POINTER(LayerDesc), ctypes.POINTER(LayerParams)]
+                                 + [_vp] * 3 + [ctypes.c_size_t] + [_vp] * 5
+                                 + [ctypes.POINTER(LayerParamGrads), _vp, ctypes.c_size_t, _vp])
     lib.m3_chunked_ssd_bwd_workspace_size.restype = ctypes.c_int
     lib.m3_chunked_ssd_bwd_workspace_size.argtypes = [_i32] * 7 + [ctypes.POINTER(ctypes.c_size_t)]
     lib.m3_chunked_ssd_bwd.restype = ctypes.c_int
@@ -237,3 +249,29 @@ def chunked_bwd(B, T, H, P, N, R, x_g, x_b, B_g, B_b, C, dt, A, D, x_raw, h_init
                                    ptr(dB_b), ptr(dC), ptr(ddt), ptr(dA), ptr(dD), ptr(dx_raw),
                                    ptr(dh_init), ptr(ws), n, stream_of(x_g)),
           "m3_chunked_ssd_bwd")
+
+
+def layer_bwd_supported(desc: LayerDesc) -> bool:
+    """True when m3_layer_bwd covers this (fp32) layer shape."""
+    n = ctypes.c_size_t(0)
+    st = lib().m3_layer_bwd_workspace_size(ctypes.byref(desc), ctypes.byref(n))
+    return st == 0 and n.value > 0
+
+
+def layer_bwd_workspace_bytes(desc: LayerDesc) -> int:
+    n = ctypes.c_size_t(0)
+    check(lib().m3_layer_bwd_workspace_size(ctypes.byref(desc), ctypes.byref(n)),
+          "m3_layer_bwd_workspace_size")
+    return n.value
+
+
+def layer_bwd(desc: LayerDesc, params: LayerParams, proj, dt_scale, fwd_ws, g_out, g_h, g_angle,
+              g_prev, g_proj, grads: LayerParamGrads) -> None:
+    """m3_layer_bwd; allocates its workspace."""
+    n = layer_bwd_workspace_bytes(desc)
+    ws = torch.empty(n, dtype=torch.uint8, device=proj.device)
+    check(lib().m3_layer_bwd(ctypes.byref(desc), ctypes.byref(params), ptr(proj), ptr(dt_scale),
+                             ptr(fwd_ws), fwd_ws.numel(), ptr(g_out), ptr(g_h), ptr(g_angle),
+                             ptr(g_prev), ptr(g_proj), ctypes.byref(grads), ptr(ws), n,
+                             stream_of(proj)),
+          "m3_layer_bwd")

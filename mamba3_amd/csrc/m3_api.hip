@@ -162,6 +162,39 @@ int m3_prefill_fwd(const m3_layer_desc* desc, const m3_layer_params* params, con
                                       prev_bx, workspace, as_stream(stream));
 }
 
+int m3_layer_bwd_workspace_size(const m3_layer_desc* desc, size_t* bytes) {
+    if (!bytes) return M3_ERR_NULL_POINTER;
+    const int st = check_desc(desc);
+    if (st != M3_OK) return st;
+    *bytes = m3::layer_bwd_workspace(*desc);
+    return *bytes > 0 ? M3_OK : M3_ERR_UNSUPPORTED;
+}
+
+int m3_layer_bwd(const m3_layer_desc* desc, const m3_layer_params* params, const void* proj,
+                 const float* dt_scale, void* fwd_workspace, size_t fwd_workspace_bytes,
+                 const float* g_out, const float* g_h, const float* g_angle, const float* g_prev,
+                 float* g_proj, const m3_layer_param_grads* grads, void* workspace,
+                 size_t workspace_bytes, void* stream) {
+    int st = check_desc(desc);
+    if (st != M3_OK) return st;
+    st = check_params(params);
+    if (st != M3_OK) return st;
+    if (!proj || !fwd_workspace || !g_out || !g_proj || !grads) return M3_ERR_NULL_POINTER;
+    if (!grads->A_log || !grads->D || !grads->dt_bias || !grads->B_norm_w || !grads->C_norm_w ||
+        !grads->B_bias || !grads->C_bias || !grads->mimo_x || !grads->mimo_z || !grads->mimo_down)
+        return M3_ERR_NULL_POINTER;
+    const size_t need = m3::layer_bwd_workspace(*desc);
+    if (need == 0) return M3_ERR_UNSUPPORTED;
+    if (fwd_workspace_bytes < m3::fp32_layer_workspace(*desc)) return M3_ERR_WORKSPACE;
+    if (!workspace || workspace_bytes < need) return M3_ERR_WORKSPACE;
+    if (!aligned(workspace, 256) || !aligned(fwd_workspace, 256)) return M3_ERR_MISALIGNED;
+    return m3::launch_layer_bwd(*desc, *params, proj, dt_scale, fwd_workspace, g_out, g_h,
+                                g_angle, g_prev, g_proj, *grads, workspace,
+                                as_stream(stream)) == 0
+               ? M3_OK
+               : M3_ERR_LAUNCH;
+}
+
 int m3_step_fwd(const m3_layer_desc* desc, const m3_layer_params* params, const void* proj,
                 const float* dt_scale, const float* h_in, const float* prev_bx_in,
                 const void* angle_in, int angle_dtype, void* y_out, float* h_out,

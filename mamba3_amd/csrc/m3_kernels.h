@@ -88,11 +88,24 @@ int launch_chunked_bwd(int B, int T, int H, int P, int N, int R, const float* x_
                        hipStream_t stream);
 
 // fp32 layer prefill on the fp32-MFMA chunk kernels (preparation, chunked SSD, gate).
+// Its workspace holds chunked_ssd's inputs and the SSD output, which the layer backward reads.
+struct Fp32LayerParts {
+    float *dt, *A, *phi, *xg, *xb, *xr, *Bt, *Bb, *Ct, *ys;
+};
+Fp32LayerParts fp32_layer_parts(const m3_layer_desc& d, void* workspace);
 bool fp32_layer_supported(const m3_layer_desc& d);
 size_t fp32_layer_workspace(const m3_layer_desc& d);
 int launch_fp32_layer(const m3_layer_desc& d, const m3_layer_params& p, const void* proj,
                       const float* dt_scale, void* y_out, float* h_final, float* angle,
                       float* prev_bx, void* workspace, hipStream_t stream);
+
+// Backward of the fp32 layer prefill (gate, chunked SSD, preparation) from the forward's
+// workspace: workspace bytes and launcher.
+size_t layer_bwd_workspace(const m3_layer_desc& d);
+int launch_layer_bwd(const m3_layer_desc& d, const m3_layer_params& p, const void* proj,
+                     const float* dt_scale, void* fwd_workspace, const float* g_out,
+                     const float* g_h, const float* g_angle, const float* g_prev, float* g_proj,
+                     const m3_layer_param_grads& g, void* workspace, hipStream_t stream);
 
 // Returns 1 when the step kernel supports (N, R), else 0.
 int step_supported(int N, int R);

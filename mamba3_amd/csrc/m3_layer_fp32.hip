@@ -257,6 +257,15 @@ size_t prep_lds(const m3_layer_desc& d) {
 }
 }  // namespace
 
+Fp32LayerParts fp32_layer_parts(const m3_layer_desc& d, void* workspace) {
+    const lp::Plan pl = lp::plan(d);
+    char* ws = reinterpret_cast<char*>(workspace);
+    auto part = [&](int i) { return reinterpret_cast<float*>(ws + pl.off[i]); };
+    const bool trap = d.use_trapezoidal != 0;
+    return Fp32LayerParts{part(0), part(1), part(2), part(3), trap ? part(4) : nullptr, part(5),
+                          part(6), trap ? part(7) : nullptr, part(8), part(9)};
+}
+
 bool fp32_layer_supported(const m3_layer_desc& d) {
     return d.dtype == M3_DTYPE_F32 && prep_lds(d) <= 64 * 1024 &&
            chunked_fwd_mfma_workspace(d.batch, d.seqlen, d.nheads, d.headdim, d.d_state,

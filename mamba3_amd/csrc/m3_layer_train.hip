@@ -1,0 +1,499 @@
+// Backward of the fp32 layer prefill (m3_layer_fp32.hip): from dL/d(gated output) (and
+// optionally dL/dh, dL/dangle, dL/dprev_BX of the prefill state) to dL/d(in_proj output) and
+// the gradients of the small parameters. Replaces, under autograd, the reference's backward
+// of mamba3/mamba3.py:197-256 (ATen's backward of softplus, RMSNorm, the RoPE rotation and
+// its cumsum, the trapezoid terms, SiLU and the MIMO sums) around chunked_ssd, whose backward
+// is m3_ssd_bwd.hip.
+//
+// Forward (per batch b, token t, head h, group g of h), restated from m3_layer_fp32.hip:
+//   dt = softplus(u) s, u = dt_raw + dt_bias, s = dt_scale or 1;  A = -exp(A_log)
+//   phi_t[i] = -sum_{t'<=t} dt_t' theta_t'[i]
+//   B^[g] = v rho w + bias (v the raw B row of g, rho = rsqrt(mean(v^2) + eps))
+//   B~[h] = rot(B^[g], phi[h]): e' = e cos - o sin, o' = e sin + o cos per pair (2i, 2i+1)
+//   B_b[t] = B~[t-1];  x_r = x mimo_x;  lambda = sigmoid(lam_raw);  dA = exp(A dt)
+//   x_g = lambda x_r;  x_b[t] = (1 - lambda_t) dA_t x_r[t-1]
+//   y = chunked_ssd(x_g, x_b, B~, B_b, C~, dt, A, D, x_r)
+//   out = sum_r mimo_down y silu(z mimo_z);  angle = phi_{T-1};  prev_BX = B~_{T-1} x_r,{T-1}^T
+// Backward, in kernel order:
+//   tb_gate   dL/dy, dL/dz and the per-block partials of dL/dmimo_down, dL/dmimo_z
+//   (chunked SSD backward: dL/d of x_g, x_b, B~, B_b, C~, dt, A, D, x_r)
+//   tb_x      dL/dx_r = g_xr + lambda g_xg + (1 - lambda_{t+1}) dA_{t+1} g_xb[t+1] (+ prev_BX),
+//             dL/dx, dL/dlam_raw, the dt and A terms of dA, partials of dL/dmimo_x
+//   tb_bc     dL/dB~ (+ g_Bb[t+1], + prev_BX), rotated back (by -phi) and summed over the heads
+//             of the group, dL/dphi = sum_r (g_o' e' - g_e' o') over B and C, the RMSNorm
+//             backward g_v = rho w g - v rho^3 sum(w g v) / (N R), partials of dL/dw, dL/dbias
+//   tb_asum, tb_angle   Phi_t = sum_{t'>=t} dL/dphi_t' (+ dL/dangle), in chunks of 64 tokens
+//   tb_tok    dL/dtheta_t = -sum_h dt Phi_t, dL/du = s sigmoid(u) (g_dt + -sum_i theta Phi)
+//   tb_colsum, tb_finish   the parameter gradients from the partials, in a fixed order
+// Every reduction runs in a fixed order: results are deterministic.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "m3_kernels.h"
+
+namespace m3 {
+namespace tb {
+
+constexpr int NTH = 256;
+constexpr int TBK = 64;  // tokens per block of tb_gate / tb_x
+constexpr int TBC = 8;   // tokens per block of tb_bc
+constexpr int kAC = 64;  // tokens per chunk of the angle suffix scan
+
+struct Args {
+    int B, T, H, P, N, R, G, trap, cplx;
+    int64_t rs;
+    ProjLayout pl;
+    float eps;
+    m3_layer_params prm;
+    const float* proj;
+    const float* dt_scale;
+    Fp32LayerParts f;
+    const float *gout, *gh, *gang, *gprev;
+    float* gproj;
+    m3_layer_param_grads out;
+    // workspace
+    float *gys, *gxg, *gxb, *gxr, *gBt, *gBb, *gCt, *gdtc, *gAc, *gD, *gdtx, *gphi, *Phi,
+        *Phi_sum, *gA_part, *p_md, *p_mz, *p_mx, *p_Bw, *p_Cw, *p_Bb, *p_Cb, *p_dtb;
+};
+
+__device__ __forceinline__ float sigm(float v) { return 1.f / (1.f + expf(-v)); }
+
+__device__ float block_sum(float v, float* red) {
+    const int tid = threadIdx.x;
+    red[tid] = v;
+    __syncthreads();
+    for (int w = NTH / 2; w > 0; w >>= 1) {
+        if (tid < w) red[tid] += red[tid + w];
+        __syncthreads();
+    }
+    const float s = red[0];
+    __syncthreads();
+    return s;
+}
+
+// ---- gate: one block per (b, token block, h), one thread per headdim column p.
+__global__ __launch_bounds__(NTH) void tb_gate(Args a) {
+    const int nTB = (a.T + TBK - 1) / TBK;
+    const int h = blockIdx.x % a.H, tb = (blockIdx.x / a.H) % nTB, b = blockIdx.x / (a.H * nTB);
+    const int p = threadIdx.x;
+    if (p >= a.P) return;
+    const int64_t HP = (int64_t)a.H * a.P;
+    float pmd[8] = {0, 0, 0, 0, 0, 0, 0, 0}, pmz[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    const int t1 = min(a.T, (tb + 1) * TBK);
+    for (int t = tb * TBK; t < t1; ++t) {
+        const int64_t tok = (int64_t)b * a.T + t;
+        const float z = a.proj[tok * a.rs + a.pl.z + (int64_t)h * a.P + p];
+        const float g = a.gout[tok * HP + (int64_t)h * a.P + p];
+        const int64_t yb = (tok * a.H + h) * a.P * a.R + (int64_t)p * a.R;
+        float gz = 0.f;
+        for (int r = 0; r < a.R; ++r) {
+            const int64_t pr = ((int64_t)h * a.P + p) * a.R + r;
+            const float mz = a.prm.mimo_z[pr], md = a.prm.mimo_down[pr];
+            const float zz = z * mz, sg = sigm(zz), silu = zz * sg, ds = sg * (1.f + zz * (1.f - sg));
+            const float y = a.f.ys[yb + r];
+            a.gys[yb + r] = g * md * silu;
+            gz += g * md * y * ds * mz;
+            pmd[r] += g * y * silu;
+            pmz[r] += g * md * y * ds * z;
+        }
+        a.gproj[tok * a.rs + a.pl.z + (int64_t)h * a.P + p] = gz;
+    }
+    const int64_t o = (((int64_t)b * nTB + tb) * HP + (int64_t)h * a.P + p) * a.R;
+    for (int r = 0; r < a.R; ++r) {
+        a.p_md[o + r] = pmd[r];
+        a.p_mz[o + r] = pmz[r];
+    }
+}
+
+// ---- x terms: one block per (b, token block, h), one thread per headdim column p.
+__global__ __launch_bounds__(NTH) void tb_x(Args a) {
+    __shared__ float red[NTH];
+    const int nTB = (a.T + TBK - 1) / TBK;
+    const int h = blockIdx.x % a.H, tb = (blockIdx.x / a.H) % nTB, b = blockIdx.x / (a.H * nTB);
+    const int p = threadIdx.x;
+    const bool col = p < a.P;
+    const int PR = a.P * a.R;
+    const float Ah = a.f.A[h];
+    float pmx[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    float gA = 0.f;
+    const int t1 = min(a.T, (tb + 1) * TBK);
+    for (int t = tb * TBK; t < t1; ++t) {
+        const int64_t tok = (int64_t)b * a.T + t;
+        const int64_t th = tok * a.H + h;
+        const float* row = a.proj + tok * a.rs;
+        float lam = 1.f, dA = 1.f, lamn = 1.f, dAn = 1.f;
+        if (a.trap) {
+            lam = sigm(row[a.pl.lam + h]);
+            dA = expf(Ah * a.f.dt[th]);
+            if (t + 1 < a.T) {
+                lamn = sigm(row[a.rs + a.pl.lam + h]);
+                dAn = expf(Ah * a.f.dt[th + a.H]);
+            }
+        }
+        float sl = 0.f, sa = 0.f;
+        if (col) {
+            const float x = row[a.pl.x + (int64_t)h * a.P + p];
+            float gx = 0.f;
+            for (int r = 0; r < a.R; ++r) {
+                const int64_t e = th * PR + (int64_t)p * a.R + r;
+                float g = a.gxr[e] + (a.trap ? lam : 1.f) * a.gxg[e];
+                if (a.trap && t + 1 < a.T) g += (1.f - lamn) * dAn * a.gxb[e + (int64_t)a.H * PR];
+                if (t == a.T - 1 && a.gprev) {
+                    const float* gp = a.gprev + (((int64_t)b * a.H + h) * a.P + p) * a.N;
+                    const float* bt = a.f.Bt + th * a.N * a.R + r;
+                    for (int n = 0; n < a.N; ++n) g += gp[n] * bt[(int64_t)n * a.R];
+                }
+                const float mx = a.prm.mimo_x[((int64_t)h * a.P + p) * a.R + r];
+                gx += g * mx;
+                pmx[r] += g * x;
+                if (a.trap) {
+                    sl += a.gxg[e] * a.f.xr[e];
+                    if (t > 0) sa += a.gxb[e] * a.f.xr[e - (int64_t)a.H * PR];
+                }
+            }
+            a.gproj[tok * a.rs + a.pl.x + (int64_t)h * a.P + p] = gx;
+        }
+        float gdt = 0.f;
+        if (a.trap) {
+            const float slt = block_sum(sl, red), sat = block_sum(sa, red);
+            const float glam = slt - sat * dA;   // dL/dlambda
+            const float gdA = sat * (1.f - lam);  // dL/d(dA)
+            if (p == 0) a.gproj[tok * a.rs + a.pl.lam + h] = glam * lam * (1.f - lam);
+            gdt = gdA * dA * Ah;
+            gA += gdA * dA * a.f.dt[th];
+        }
+        if (p == 0) a.gdtx[th] = gdt;
+    }
+    if (col) {
+        const int64_t o = (((int64_t)b * nTB + tb) * a.H * a.P + (int64_t)h * a.P + p) * a.R;
+        for (int r = 0; r < a.R; ++r) a.p_mx[o + r] = pmx[r];
+    }
+    if (p == 0) a.gA_part[((int64_t)b * nTB + tb) * a.H + h] = gA;
+}
+
+// ---- B / C: one block per (b, TBC tokens). LDS: dL/dB^, dL/dC^ of every group, the
+// per-thread parameter partials, the reduction scratch.
+__global__ __launch_bounds__(NTH) void tb_bc(Args a) {
+    extern __shared__ float sm[];
+    const int NR = a.N * a.R, GNR = a.G * NR, NH = a.N / 2, hpg = a.H / a.G;
+    float* gBh = sm;
+    float* gCh = gBh + GNR;
+    float* pBw = gCh + GNR;
+    float* pCw = pBw + NR;
+    float* pBb = pCw + NR;
+    float* pCb = pBb + GNR;
+    float* red = pCb + GNR;
+    const int nTB = (a.T + TBC - 1) / TBC;
+    const int tb = blockIdx.x % nTB, b = blockIdx.x / nTB;
+    const int tid = threadIdx.x;
+    for (int e = tid; e < NR; e += NTH) pBw[e] = pCw[e] = 0.f;
+    for (int e = tid; e < GNR; e += NTH) pBb[e] = pCb[e] = 0.f;
+    const int t1 = min(a.T, (tb + 1) * TBC);
+    for (int t = tb * TBC; t < t1; ++t) {
+        const int64_t tok = (int64_t)b * a.T + t;
+        const float* row = a.proj + tok * a.rs;
+        for (int e = tid; e < GNR; e += NTH) gBh[e] = gCh[e] = 0.f;
+        __syncthreads();
+        // per head: total dL/dB~, dL/dC~ of each pair, rotated back into the group's rows
+        for (int h = 0; h < a.H; ++h) {
+            const int g = h / hpg;
+            const int64_t th = tok * a.H + h;
+            const int64_t bt = th * NR;
+            for (int i = tid; i < NH; i += NTH) {
+                float s = 0.f, c = 1.f;
+                if (a.cplx) sincosf(a.f.phi[th * NH + i], &s, &c);
+                float gphi = 0.f;
+                for (int r = 0; r < a.R; ++r) {
+                    const int64_t ie = bt + (int64_t)(2 * i) * a.R + r, io = ie + a.R;
+                    float gbe = a.gBt[ie], gbo = a.gBt[io];
+                    if (a.trap && t + 1 < a.T) {
+                        gbe += a.gBb[ie + (int64_t)a.H * NR];
+                        gbo += a.gBb[io + (int64_t)a.H * NR];
+                    }
+                    if (t == a.T - 1 && a.gprev) {
+                        const float* gp = a.gprev + ((int64_t)b * a.H + h) * a.P * a.N;
+                        const float* xr = a.f.xr + th * a.P * a.R + r;
+                        for (int pp = 0; pp < a.P; ++pp) {
+                            gbe += gp[(int64_t)pp * a.N + 2 * i] * xr[(int64_t)pp * a.R];
+                            gbo += gp[(int64_t)pp * a.N + 2 * i + 1] * xr[(int64_t)pp * a.R];
+                        }
+                    }
+                    const float gce = a.gCt[ie], gco = a.gCt[io];
+                    if (a.cplx) {
+                        gphi += gbo * a.f.Bt[ie] - gbe * a.f.Bt[io] + gco * a.f.Ct[ie] - gce * a.f.Ct[io];
+                    }
+                    const int64_t je = (int64_t)g * NR + (2 * i) * a.R + r, jo = je + a.R;
+                    gBh[je] += gbe * c + gbo * s;
+                    gBh[jo] += gbo * c - gbe * s;
+                    gCh[je] += gce * c + gco * s;
+                    gCh[jo] += gco * c - gce * s;
+                }
+                if (a.cplx) a.gphi[th * NH + i] = gphi;
+            }
+        }
+        __syncthreads();
+        // RMSNorm backward per group; parameter partials
+        for (int g = 0; g < a.G; ++g) {
+            const float* vb = row + a.pl.B + (int64_t)g * NR;
+            const float* vc = row + a.pl.C + (int64_t)g * NR;
+            float sb = 0.f, sc = 0.f, wb = 0.f, wc = 0.f;
+            for (int e = tid; e < NR; e += NTH) {
+                sb += vb[e] * vb[e];
+                sc += vc[e] * vc[e];
+                wb += gBh[g * NR + e] * a.prm.B_norm_w[e] * vb[e];
+                wc += gCh[g * NR + e] * a.prm.C_norm_w[e] * vc[e];
+            }
+            sb = block_sum(sb, red);
+            sc = block_sum(sc, red);
+            wb = block_sum(wb, red);
+            wc = block_sum(wc, red);
+            const float rb = rsqrtf(sb / NR + a.eps), rc = rsqrtf(sc / NR + a.eps);
+            const float kb = rb * rb * rb * wb / NR, kc = rc * rc * rc * wc / NR;
+            for (int e = tid; e < NR; e += NTH) {
+                const float gb = gBh[g * NR + e], gc = gCh[g * NR + e];
+                a.gproj[tok * a.rs + a.pl.B + (int64_t)g * NR + e] = rb * a.prm.B_norm_w[e] * gb - vb[e] * kb;
+                a.gproj[tok * a.rs + a.pl.C + (int64_t)g * NR + e] = rc * a.prm.C_norm_w[e] * gc - vc[e] * kc;
+                pBw[e] += gb * vb[e] * rb;
+                pCw[e] += gc * vc[e] * rc;
+                pBb[g * NR + e] += gb;
+                pCb[g * NR + e] += gc;
+            }
+        }
+        __syncthreads();
+    }
+    const int64_t ob = (int64_t)blockIdx.x;
+    for (int e = tid; e < NR; e += NTH) {
+        a.p_Bw[ob * NR + e] = pBw[e];
+        a.p_Cw[ob * NR + e] = pCw[e];
+    }
+    for (int e = tid; e < GNR; e += NTH) {
+        a.p_Bb[ob * GNR + e] = pBb[e];
+        a.p_Cb[ob * GNR + e] = pCb[e];
+    }
+}
+
+// ---- Phi_t = sum_{t'>=t} dL/dphi_t' + dL/dangle: chunk sums, then each chunk walked down
+// from the sum of the chunks after it. One thread per (b, chunk, h, pair).
+__device__ __forceinline__ void ajob(const Args& a, int64_t e, int& b, int& c, int& h, int& i) {
+    const int NH = a.N / 2;
+    const int nc = (a.T + kAC - 1) / kAC;
+    i = (int)(e % NH);
+    h = (int)((e / NH) % a.H);
+    const int64_t bc = e / ((int64_t)NH * a.H);
+    c = (int)(bc % nc);
+    b = (int)(bc / nc);
+}
+
+__global__ __launch_bounds__(NTH) void tb_asum(Args a) {
+    const int NH = a.N / 2, nc = (a.T + kAC - 1) / kAC;
+    const int64_t e = (int64_t)blockIdx.x * NTH + threadIdx.x;
+    if (e >= (int64_t)a.B * nc * a.H * NH) return;
+    int b, c, h, i;
+    ajob(a, e, b, c, h, i);
+    float s = 0.f;
+    const int t1 = min(a.T, (c + 1) * kAC);
+    for (int t = c * kAC; t < t1; ++t) s += a.gphi[(((int64_t)b * a.T + t) * a.H + h) * NH + i];
+    a.Phi_sum[e] = s;
+}
+
+__global__ __launch_bounds__(NTH) void tb_angle(Args a) {
+    const int NH = a.N / 2, nc = (a.T + kAC - 1) / kAC;
+    const int64_t e = (int64_t)blockIdx.x * NTH + threadIdx.x;
+    if (e >= (int64_t)a.B * nc * a.H * NH) return;
+    int b, c, h, i;
+    ajob(a, e, b, c, h, i);
+    float s = a.gang ? a.gang[((int64_t)b * a.H + h) * NH + i] : 0.f;
+    for (int cc = nc - 1; cc > c; --cc) s += a.Phi_sum[(((int64_t)b * nc + cc) * a.H + h) * NH + i];
+    const int t1 = min(a.T, (c + 1) * kAC);
+    for (int t = t1 - 1; t >= c * kAC; --t) {
+        const int64_t o = (((int64_t)b * a.T + t) * a.H + h) * NH + i;
+        s += a.gphi[o];
+        a.Phi[o] = s;
+    }
+}
+
+// ---- per token: dL/dtheta, dL/ddt_raw and the dt_bias partials. One block per (b, t).
+__global__ __launch_bounds__(NTH) void tb_tok(Args a) {
+    const int64_t tok = blockIdx.x;
+    const int NH = a.N / 2;
+    const float* row = a.proj + tok * a.rs;
+    if (a.cplx) {
+        for (int i = threadIdx.x; i < NH; i += NTH) {
+            float s = 0.f;
+            for (int h = 0; h < a.H; ++h) s += a.f.dt[tok * a.H + h] * a.Phi[(tok * a.H + h) * NH + i];
+            a.gproj[tok * a.rs + a.pl.theta + i] = -s;
+        }
+    }
+    for (int h = threadIdx.x; h < a.H; h += NTH) {
+        const int64_t th = tok * a.H + h;
+        float g = a.gdtc[th] + a.gdtx[th];
+        if (a.cplx) {
+            float s = 0.f;
+            for (int i = 0; i < NH; ++i) s += row[a.pl.theta + i] * a.Phi[th * NH + i];
+            g -= s;
+        }
+        const float u = row[a.pl.dt + h] + a.prm.dt_bias[h];
+        const float gu = g * (a.dt_scale ? a.dt_scale[th] : 1.f) * sigm(u);
+        a.gproj[tok * a.rs + a.pl.dt + h] = gu;
+        a.p_dtb[th] = gu;
+    }
+}
+
+// ---- parameter gradients: column sums of the (K x M) partial matrices in a fixed order.
+// A block sums a slab of 256 rows for 64 columns (4 row groups of 64 rows each, then the
+// groups in order); slabs are summed by the next pass.
+constexpr int kSlab = 256;
+
+__global__ __launch_bounds__(NTH) void tb_colsum(const float* in, int64_t K, int M, float* out) {
+    __shared__ float red[4][64];
+    const int c = threadIdx.x & 63, grp = threadIdx.x >> 6;
+    const int col = blockIdx.x * 64 + c;
+    const int64_t r0 = (int64_t)blockIdx.y * kSlab, r1 = min(K, r0 + kSlab);
+    float s = 0.f;
+    if (col < M)
+        for (int64_t r = r0 + grp; r < r1; r += 4) s += in[r * M + col];
+    red[grp][c] = s;
+    __syncthreads();
+    if (grp == 0 && col < M) out[(int64_t)blockIdx.y * M + col] = red[0][c] + red[1][c] + red[2][c] + red[3][c];
+}
+
+// dL/dA_log = (dL/dA of the chunked SSD + of the trapezoid decays) A;  dL/dD.
+__global__ __launch_bounds__(NTH) void tb_finish(Args a, const float* gA_x) {
+    const int h = blockIdx.x * NTH + threadIdx.x;
+    if (h >= a.H) return;
+    a.out.A_log[h] = (a.gAc[h] + gA_x[h]) * a.f.A[h];
+    a.out.D[h] = a.gD[h];
+}
+
+struct Plan {
+    size_t off[26], chunk_off, total;
+};
+
+// Largest slab-sum matrix of the parameter reductions (rows ceil(K / kSlab) x M).
+size_t colsum_scratch(const m3_layer_desc& d) {
+    const size_t B = d.batch, T = d.seqlen, H = d.nheads;
+    const size_t NR = (size_t)d.d_state * d.mimo_rank, HPR = H * d.headdim * d.mimo_rank;
+    const size_t nTB = (T + TBK - 1) / TBK, nTC = (T + TBC - 1) / TBC;
+    const size_t KM[4][2] = {{B * T, H}, {B * nTC, d.ngroups * NR}, {B * nTB, HPR}, {B * nTB, H}};
+    size_t m = 0;
+    for (const auto& km : KM) m = std::max(m, (km[0] + kSlab - 1) / kSlab * km[1]);
+    return m;
+}
+
+inline size_t al(size_t x) { return (x + 255) & ~(size_t)255; }
+
+Plan plan(const m3_layer_desc& d) {
+    const size_t B = d.batch, T = d.seqlen, H = d.nheads, P = d.headdim, N = d.d_state,
+                 R = d.mimo_rank, G = d.ngroups;
+    const size_t BTH = B * T * H, X = BTH * P * R, BN = BTH * N * R, NH = N / 2;
+    const size_t nTB = (T + TBK - 1) / TBK, nTC = (T + TBC - 1) / TBC, nc = (T + kAC - 1) / kAC;
+    const bool trap = d.use_trapezoidal != 0;
+    const size_t sizes[26] = {
+        X, X, trap ? X : 0, X,                         // gys, gxg, gxb, gxr
+        BN, trap ? BN : 0, BN,                         // gBt, gBb, gCt
+        BTH, H, H, BTH,                                // gdtc, gAc, gD, gdtx
+        BTH * NH, BTH * NH, B * nc * H * NH,           // gphi, Phi, Phi_sum
+        B * nTB * H,                                   // gA_part
+        B * nTB * H * P * R, B * nTB * H * P * R, B * nTB * H * P * R,  // p_md, p_mz, p_mx
+        B * nTC * N * R, B * nTC * N * R,              // p_Bw, p_Cw
+        B * nTC * G * N * R, B * nTC * G * N * R,      // p_Bb, p_Cb
+        BTH,                                           // p_dtb
+        colsum_scratch(d), colsum_scratch(d), H};      // column-sum passes, dL/dA (x terms)
+    Plan p;
+    size_t o = 0;
+    for (int i = 0; i < 26; ++i) {
+        p.off[i] = o;
+        o += al(sizes[i] * sizeof(float));
+    }
+    p.chunk_off = o;
+    o += al(chunked_bwd_workspace(d.batch, d.seqlen, d.nheads, d.headdim, d.d_state, d.mimo_rank,
+                                  trap));
+    p.total = o;
+    return p;
+}
+
+size_t bc_lds(const m3_layer_desc& d) {
+    const size_t NR = (size_t)d.d_state * d.mimo_rank, GNR = d.ngroups * NR;
+    return (4 * GNR + 2 * NR + NTH) * sizeof(float);
+}
+
+}  // namespace tb
+
+size_t layer_bwd_workspace(const m3_layer_desc& d) {
+    if (!fp32_layer_supported(d) || tb::bc_lds(d) > 64 * 1024 || d.mimo_rank > 8) return 0;
+    return tb::plan(d).total;
+}
+
+int launch_layer_bwd(const m3_layer_desc& d, const m3_layer_params& p, const void* proj,
+                     const float* dt_scale, void* fwd_workspace, const float* g_out,
+                     const float* g_h, const float* g_angle, const float* g_prev, float* g_proj,
+                     const m3_layer_param_grads& g, void* workspace, hipStream_t stream) {
+    using namespace tb;
+    const Plan pl = plan(d);
+    char* ws = reinterpret_cast<char*>(workspace);
+    auto part = [&](int i) { return reinterpret_cast<float*>(ws + pl.off[i]); };
+    Args a;
+    a.B = d.batch, a.T = d.seqlen, a.H = d.nheads, a.P = d.headdim, a.N = d.d_state;
+    a.R = d.mimo_rank, a.G = d.ngroups, a.trap = d.use_trapezoidal, a.cplx = d.use_complex;
+    a.rs = d.proj_row_stride, a.pl = proj_layout(d), a.eps = d.rms_eps, a.prm = p;
+    a.proj = reinterpret_cast<const float*>(proj);
+    a.dt_scale = dt_scale;
+    a.f = fp32_layer_parts(d, fwd_workspace);
+    a.gout = g_out, a.gh = g_h, a.gang = g_angle, a.gprev = g_prev, a.gproj = g_proj, a.out = g;
+    a.gys = part(0), a.gxg = part(1), a.gxb = a.trap ? part(2) : nullptr, a.gxr = part(3);
+    a.gBt = part(4), a.gBb = a.trap ? part(5) : nullptr, a.gCt = part(6);
+    a.gdtc = part(7), a.gAc = part(8), a.gD = part(9), a.gdtx = part(10);
+    a.gphi = part(11), a.Phi = part(12), a.Phi_sum = part(13), a.gA_part = part(14);
+    a.p_md = part(15), a.p_mz = part(16), a.p_mx = part(17);
+    a.p_Bw = part(18), a.p_Cw = part(19), a.p_Bb = part(20), a.p_Cb = part(21), a.p_dtb = part(22);
+
+    const int nTB = (a.T + TBK - 1) / TBK, nTC = (a.T + TBC - 1) / TBC;
+    const unsigned gbh = (unsigned)((int64_t)a.B * nTB * a.H);
+    hipLaunchKernelGGL(tb_gate, dim3(gbh), dim3(NTH), 0, stream, a);
+    if (launch_chunked_bwd(a.B, a.T, a.H, a.P, a.N, a.R, a.f.xg, a.f.xb, a.f.Bt, a.f.Bb, a.f.Ct,
+                           a.f.dt, a.f.A, p.D, a.f.xr, nullptr, a.gys, g_h, a.gxg, a.gxb, a.gBt,
+                           a.gBb, a.gCt, a.gdtc, a.gAc, a.gD, a.gxr, nullptr,
+                           ws + pl.chunk_off, stream) != 0)
+        return 1;
+    hipLaunchKernelGGL(tb_x, dim3(gbh), dim3(NTH), 0, stream, a);
+    hipLaunchKernelGGL(tb_bc, dim3((unsigned)((int64_t)a.B * nTC)), dim3(NTH), bc_lds(d), stream, a);
+    if (a.cplx) {
+        const int nc = (a.T + kAC - 1) / kAC;
+        const int64_t na = (int64_t)a.B * nc * a.H * (a.N / 2);
+        const unsigned ga = (unsigned)((na + NTH - 1) / NTH);
+        hipLaunchKernelGGL(tb_asum, dim3(ga), dim3(NTH), 0, stream, a);
+        hipLaunchKernelGGL(tb_angle, dim3(ga), dim3(NTH), 0, stream, a);
+    }
+    hipLaunchKernelGGL(tb_tok, dim3((unsigned)((int64_t)a.B * a.T)), dim3(NTH), 0, stream, a);
+    float* tmp[2] = {part(23), part(24)};
+    auto colsum = [&](const float* in, int64_t K, int M, float* out) {
+        int w = 0;
+        while (K > kSlab) {  // slab sums, then sums of those
+            const int64_t ks = (K + kSlab - 1) / kSlab;
+            hipLaunchKernelGGL(tb_colsum, dim3((unsigned)((M + 63) / 64), (unsigned)ks), dim3(NTH), 0,
+                               stream, in, K, M, tmp[w]);
+            in = tmp[w];
+            w ^= 1;
+            K = ks;
+        }
+        hipLaunchKernelGGL(tb_colsum, dim3((unsigned)((M + 63) / 64), 1), dim3(NTH), 0, stream, in, K,
+                           M, out);
+    };
+    const int NR = a.N * a.R, HPR = a.H * a.P * a.R;
+    const int64_t nbt = (int64_t)a.B * nTB, nbc = (int64_t)a.B * nTC;
+    colsum(a.p_dtb, (int64_t)a.B * a.T, a.H, g.dt_bias);
+    colsum(a.p_Bw, nbc, NR, g.B_norm_w);
+    colsum(a.p_Cw, nbc, NR, g.C_norm_w);
+    colsum(a.p_Bb, nbc, a.G * NR, g.B_bias);
+    colsum(a.p_Cb, nbc, a.G * NR, g.C_bias);
+    colsum(a.p_mx, nbt, HPR, g.mimo_x);
+    colsum(a.p_mz, nbt, HPR, g.mimo_z);
+    colsum(a.p_md, nbt, HPR, g.mimo_down);
+    colsum(a.gA_part, nbt, a.H, part(25));
+    hipLaunchKernelGGL(tb_finish, dim3((unsigned)((a.H + NTH - 1) / NTH)), dim3(NTH), 0, stream, a,
+                       part(25));
+    return hipGetLastError() == hipSuccess ? 0 : 1;
+}
+
+}  // namespace m3

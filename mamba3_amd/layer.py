@@ -55,6 +55,57 @@ class _ForwardOnly(torch.autograd.Function):
             "KulaMamba.step has no backward in mamba3_amd; train through forward / prefill")
 
 
+class _LayerTrainFn(torch.autograd.Function):
+    """Differentiable ssd_from_proj on HIP kernels in both directions: the forward is the fp32
+    layer prefill (m3_prefill_fwd on an fp32 desc), whose workspace keeps its intermediates
+    for the backward, m3_layer_bwd (gate, chunked SSD and preparation backward). bf16
+    inputs and parameters are computed in fp32; gradients come back in their dtypes."""
+
+    @staticmethod
+    def forward(ctx, layer, proj, dt_scale, return_state, *params):
+        Bat, T, _ = proj.shape
+        H, P, N = layer.nheads, layer.headdim, layer.d_state
+        dev = proj.device
+        proj32 = proj.detach().float().contiguous()
+        p32 = [t.detach().float().contiguous() for t in params]
+        desc = layer._desc(Bat, T, proj32)
+        pack = _native.LayerParams(*[t.data_ptr() for t in p32])
+        scale = layer._dt_scale(dt_scale, (Bat, T, H), dev)
+        ws_bytes = _native.prefill_workspace_bytes(desc)
+        ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
+        y = torch.empty(Bat, T, layer.d_inner, device=dev, dtype=torch.float32)
+        h_final = angle = prev_bx = None
+        if return_state:
+            h_final = torch.empty(Bat, H, P, N, device=dev, dtype=torch.float32)
+            angle = torch.empty(Bat, H, N // 2, device=dev, dtype=torch.float32)
+            prev_bx = torch.empty(Bat, H, P, N, device=dev, dtype=torch.float32)
+        _native.prefill_fwd(desc, pack, proj32, scale, y, h_final, angle, prev_bx, ws, ws_bytes)
+        ctx.save_for_backward(proj32, ws, scale, *p32)
+        ctx.desc = desc
+        ctx.proj_dtype = proj.dtype
+        ctx.param_dtypes = [t.dtype for t in params]
+        ctx.set_materialize_grads(False)
+        return y.to(proj.dtype), h_final, angle, prev_bx
+
+    @staticmethod
+    def backward(ctx, g_y, g_h, g_angle, g_prev):
+        proj32, ws, scale, *p32 = ctx.saved_tensors
+        if g_y is None:
+            g_y = torch.zeros(proj32.shape[0], proj32.shape[1], ctx.desc.nheads * ctx.desc.headdim,
+                              device=proj32.device)
+
+        def f32(t):
+            return None if t is None else t.float().contiguous()
+
+        g_proj = torch.empty_like(proj32)
+        grads = [torch.empty_like(t) for t in p32]
+        _native.layer_bwd(ctx.desc, _native.LayerParams(*[t.data_ptr() for t in p32]), proj32,
+                          scale, ws, f32(g_y), f32(g_h), f32(g_angle), f32(g_prev), g_proj,
+                          _native.LayerParamGrads(*[t.data_ptr() for t in grads]))
+        return (None, g_proj.to(ctx.proj_dtype), None, None,
+                *[g.to(dt) for g, dt in zip(grads, ctx.param_dtypes)])
+
+
 class KulaMamba(nn.Module):
     """Mamba-3 SSD layer (mamba3/mamba3.py:48-332) on MI355X HIP kernels."""
 
@@ -184,6 +235,13 @@ class KulaMamba(nn.Module):
         self._check_norm_eps()
         if torch.is_grad_enabled() and (proj.requires_grad or
                                         any(p.requires_grad for p in self._small_params())):
+            Bat, T, _ = proj.shape
+            desc32 = self._desc(Bat, T, proj.detach().float())
+            if _native.layer_bwd_supported(desc32):
+                y, h, angle, prev = _LayerTrainFn.apply(self, proj, dt_scale, return_state,
+                                                        *self._small_params())
+                state = {"h": h, "angle": angle, "prev_BX": prev} if return_state else None
+                return y, state
             return self._ssd_train(proj, dt_scale, return_state)
         proj = proj.contiguous()
         Bat, T, _ = proj.shape
@@ -209,11 +267,12 @@ class KulaMamba(nn.Module):
         return y, state
 
     def _ssd_train(self, proj: torch.Tensor, dt_scale=None, return_state: bool = False):
-        """Differentiable form of ssd_from_proj, used when autograd needs gradients: the
-        reference's element-wise preparation and gate (mamba3/mamba3.py:142-166, 197-239)
-        as PyTorch ops in fp32 around chunked_ssd, whose forward and backward run on the
-        HIP kernels (m3_chunked_ssd_fwd / m3_chunked_ssd_bwd). The state it returns
-        matches the fused path's (fp32 h, angle and prev_BX; mamba3/mamba3.py:241-256)."""
+        """Differentiable form of ssd_from_proj for the shapes m3_layer_bwd does not cover
+        (its per-token LDS would exceed 64 KB): the reference's element-wise preparation and
+        gate (mamba3/mamba3.py:142-166, 197-239) as PyTorch ops in fp32 around chunked_ssd,
+        whose forward and backward run on the HIP kernels (m3_chunked_ssd_fwd /
+        m3_chunked_ssd_bwd). The state it returns matches the fused path's (fp32 h, angle
+        and prev_BX; mamba3/mamba3.py:241-256)."""
         from .ssd import chunked_ssd
 
         Bat, T, _ = proj.shape
