@@ -26,6 +26,8 @@ the same format:
   scan_bwd_d768   the scan's backward (m3_scan_bwd) at the scan_d768 shape: GB/s.
   ssd_bwd_d768    the chunked SSD's backward (m3_chunked_ssd_bwd, fp32) at the d_model 768
                   prefill shape (8, 8192): tokens/s, roofline over the call's GEMM FLOPs.
+  layer_bwd_d768  the fp32 layer's backward (m3_layer_bwd) for x (4, 1024, 768): tokens/s
+                  of the native call, and the whole layer's training step beside it.
 
 Prints ONE JSON line. `value` is SSD prefill tokens/s; `roofline` is the fused SSD kernel
 against the bf16 MFMA peak with the algorithmic FLOP count
@@ -405,7 +407,88 @@ def bench_ssd_bwd(args, torch, mamba3_amd):
     return res
 
 
-WORKLOADS = {"prefill_d2048": bench_prefill_d2048, "ssd_bwd_d768": bench_ssd_bwd, "layer_fp32_d768": bench_layer_fp32_d768,
+def bench_layer_bwd(args, torch, mamba3_amd):
+    """m3_layer_bwd (the fp32 layer's backward: gate, chunked SSD, preparation, parameter
+    reductions) for KulaMamba(768) fp32 on x (4, 1024, 768) (weights seed 0, x seed 1), on
+    resident inputs (in_proj output, the forward's workspace, dL/dout); beside it the whole
+    layer's training step (forward + backward through autograd, projections included)."""
+    from mamba3_amd import _native
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    layer = mamba3_amd.KulaMamba(D_MODEL, d_state=N, expand=EXPAND, headdim=P, mimo_rank=R)
+    layer = layer.to(dev).train()
+    torch.manual_seed(1)
+    x = torch.randn(4, 1024, D_MODEL).to(dev)
+    B, T = x.shape[:2]
+    H = layer.nheads
+    with torch.no_grad():
+        proj = layer.in_proj(x).contiguous()
+    desc = layer._desc(B, T, proj)
+    p32 = [t.detach().float().contiguous() for t in layer._small_params()]
+    pack = _native.LayerParams(*[t.data_ptr() for t in p32])
+    nfw = _native.prefill_workspace_bytes(desc)
+    fws = torch.empty(nfw, dtype=torch.uint8, device=dev)
+    y = torch.empty(B, T, layer.d_inner, device=dev)
+    _native.prefill_fwd(desc, pack, proj, None, y, None, None, None, fws, nfw)
+    g_out = torch.randn(B, T, layer.d_inner, generator=torch.Generator().manual_seed(3)).to(dev)
+    g_proj = torch.empty_like(proj)
+    grads = [torch.empty_like(t) for t in p32]
+    gpack = _native.LayerParamGrads(*[t.data_ptr() for t in grads])
+    nbw = _native.layer_bwd_workspace_bytes(desc)
+    bws = torch.empty(nbw, dtype=torch.uint8, device=dev)
+    lib = _native.lib()
+    import ctypes
+
+    def call():
+        _native.check(lib.m3_layer_bwd(ctypes.byref(desc), ctypes.byref(pack), proj.data_ptr(), None,
+                                       fws.data_ptr(), nfw, g_out.data_ptr(), None, None, None,
+                                       g_proj.data_ptr(), ctypes.byref(gpack), bws.data_ptr(), nbw,
+                                       _native.stream_of(proj)), "m3_layer_bwd")
+
+    wall, kern_ms = time_events(torch, call, args.steps, args.warmup)
+    ms = wall * 1e3 / args.steps
+    qb, f_chunk = bwd_flops_per_chunk(P, N, R, True)
+    flops = B * H * ((T + qb - 1) // qb) * f_chunk
+    tflops = flops / (kern_ms * 1e-3) / 1e12
+
+    xg = x.clone().requires_grad_()
+    g_layer = torch.randn(B, T, D_MODEL, generator=torch.Generator().manual_seed(4)).to(dev)
+
+    def train_step():
+        out = layer(xg)
+        out.backward(g_layer)
+
+    train_wall, train_ms = time_events(torch, train_step, args.steps, args.warmup)
+    res = base_result(args, B * T / (ms * 1e-3), ms,
+                      "KulaMamba backward between out_proj and in_proj (m3_layer_bwd), d_model 768, "
+                      "fp32, x (4, 1024, 768), inputs resident in HBM", B, T, dtype="fp32")
+    res["train_step"] = {"ms": round(train_ms, 4), "tokens_per_s": round(B * T / (train_ms * 1e-3), 1),
+                         "what": "layer forward + backward through autograd (projections included)"}
+    res["roofline"] = {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_FP32_TFLOPS,
+                       "unit": "TFLOP/s", "frac": round(tflops / PEAK_FP32_TFLOPS, 4), "traffic": None,
+                       "kernel": "m3_layer_bwd, all kernels of one call; FLOPs of its chunked-SSD "
+                                 "backward GEMMs",
+                       "algorithmic_flops": flops, "avg_ms": round(kern_ms, 4)}
+    if not args.no_cpu_baseline:
+        from oracle import reference_path as ref
+        cores = len(os.sched_getaffinity(0))
+        torch.set_num_threads(cores)
+        cfg = ref.LayerCfg(d_model=D_MODEL, d_state=N, headdim=P, mimo_rank=R)
+        pc = {k: v.detach().cpu().clone().requires_grad_() for k, v in layer.state_dict().items()}
+        xs = x[:1, :512].detach().cpu().clone().requires_grad_()
+        t0 = time.perf_counter()
+        out, _ = ref.layer_forward(cfg, pc, xs)
+        out.backward(torch.ones_like(out))
+        dt = time.perf_counter() - t0
+        res["cpu_baseline"] = {"value": round(512 / dt, 1), "unit": "tokens/s", "cores": cores,
+                               "kind": "port", "cpu_model": cpu_model(),
+                               "sample": "autograd forward + backward through the oracle layer "
+                                         "(reference algorithm) in fp32 on x[:1, :512]"}
+    return res
+
+
+WORKLOADS = {"prefill_d2048": bench_prefill_d2048, "ssd_bwd_d768": bench_ssd_bwd,
+             "layer_bwd_d768": bench_layer_bwd, "layer_fp32_d768": bench_layer_fp32_d768,
              "lm_d768": bench_lm_d768,
              "scan_d768": lambda args, torch, m: bench_scan(args, torch, (8, 128, 24, 8192), "scan_d768"),
              "scan_d2048": lambda args, torch, m: bench_scan(args, torch, (2, 256, 32, 32768), "scan_d2048"),

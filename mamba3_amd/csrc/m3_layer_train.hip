@@ -37,7 +37,7 @@ namespace tb {
 
 constexpr int NTH = 256;
 constexpr int TBK = 64;  // tokens per block of tb_gate / tb_x
-constexpr int TBC = 8;   // tokens per block of tb_bc
+constexpr int TBC = 4;   // tokens per block of tb_bc
 constexpr int kAC = 64;  // tokens per chunk of the angle suffix scan
 
 struct Args {
@@ -59,11 +59,12 @@ struct Args {
 
 __device__ __forceinline__ float sigm(float v) { return 1.f / (1.f + expf(-v)); }
 
+// Sum over the block (blockDim.x a power of two, at most NTH), in a fixed order.
 __device__ float block_sum(float v, float* red) {
     const int tid = threadIdx.x;
     red[tid] = v;
     __syncthreads();
-    for (int w = NTH / 2; w > 0; w >>= 1) {
+    for (int w = blockDim.x / 2; w > 0; w >>= 1) {
         if (tid < w) red[tid] += red[tid + w];
         __syncthreads();
     }
@@ -72,7 +73,8 @@ __device__ float block_sum(float v, float* red) {
     return s;
 }
 
-// ---- gate: one block per (b, token block, h), one thread per headdim column p.
+// ---- gate: one block per (b, token block, h), one thread per headdim column p (blocks of
+// P threads rounded up to a power of two).
 __global__ __launch_bounds__(NTH) void tb_gate(Args a) {
     const int nTB = (a.T + TBK - 1) / TBK;
     const int h = blockIdx.x % a.H, tb = (blockIdx.x / a.H) % nTB, b = blockIdx.x / (a.H * nTB);
@@ -106,7 +108,8 @@ __global__ __launch_bounds__(NTH) void tb_gate(Args a) {
     }
 }
 
-// ---- x terms: one block per (b, token block, h), one thread per headdim column p.
+// ---- x terms: one block per (b, token block, h), one thread per headdim column p (blocks of
+// P threads rounded up to a power of two).
 __global__ __launch_bounds__(NTH) void tb_x(Args a) {
     __shared__ float red[NTH];
     const int nTB = (a.T + TBK - 1) / TBK;
@@ -172,12 +175,19 @@ __global__ __launch_bounds__(NTH) void tb_x(Args a) {
     if (p == 0) a.gA_part[((int64_t)b * nTB + tb) * a.H + h] = gA;
 }
 
-// ---- B / C: one block per (b, TBC tokens). LDS: dL/dB^, dL/dC^ of every group, the
-// per-thread parameter partials, the reduction scratch.
+// ---- B / C: one block per (b, TBC tokens). Thread (pair i, head group hg) handles the heads
+// h = hg (mod HS) of pair i and accumulates into its own LDS partial of dL/dB^, dL/dC^; the HS
+// partials are then summed in order. LDS: the partials, dL/dB^, dL/dC^, the parameter
+// partials, the reduction scratch.
+__device__ __forceinline__ int bc_hs(int N) { return max(1, NTH / (N / 2)); }
+
 __global__ __launch_bounds__(NTH) void tb_bc(Args a) {
     extern __shared__ float sm[];
     const int NR = a.N * a.R, GNR = a.G * NR, NH = a.N / 2, hpg = a.H / a.G;
-    float* gBh = sm;
+    const int HS = bc_hs(a.N);
+    float* qB = sm;                 // [HS][GNR]
+    float* qC = qB + HS * GNR;      // [HS][GNR]
+    float* gBh = qC + HS * GNR;
     float* gCh = gBh + GNR;
     float* pBw = gCh + GNR;
     float* pCw = pBw + NR;
@@ -187,20 +197,23 @@ __global__ __launch_bounds__(NTH) void tb_bc(Args a) {
     const int nTB = (a.T + TBC - 1) / TBC;
     const int tb = blockIdx.x % nTB, b = blockIdx.x / nTB;
     const int tid = threadIdx.x;
+    const int hg = tid / NH < HS ? tid / NH : a.H;  // a.H: no heads for this thread
+    const int i0 = tid % NH;
     for (int e = tid; e < NR; e += NTH) pBw[e] = pCw[e] = 0.f;
     for (int e = tid; e < GNR; e += NTH) pBb[e] = pCb[e] = 0.f;
     const int t1 = min(a.T, (tb + 1) * TBC);
     for (int t = tb * TBC; t < t1; ++t) {
         const int64_t tok = (int64_t)b * a.T + t;
         const float* row = a.proj + tok * a.rs;
-        for (int e = tid; e < GNR; e += NTH) gBh[e] = gCh[e] = 0.f;
+        for (int e = tid; e < HS * GNR; e += NTH) qB[e] = qC[e] = 0.f;
         __syncthreads();
-        // per head: total dL/dB~, dL/dC~ of each pair, rotated back into the group's rows
-        for (int h = 0; h < a.H; ++h) {
+        for (int h = hg; h < a.H; h += HS) {
             const int g = h / hpg;
             const int64_t th = tok * a.H + h;
             const int64_t bt = th * NR;
-            for (int i = tid; i < NH; i += NTH) {
+            float* qb = qB + (int64_t)hg * GNR;
+            float* qc = qC + (int64_t)hg * GNR;
+            for (int i = i0; i < NH; i += NTH) {
                 float s = 0.f, c = 1.f;
                 if (a.cplx) sincosf(a.f.phi[th * NH + i], &s, &c);
                 float gphi = 0.f;
@@ -224,13 +237,23 @@ __global__ __launch_bounds__(NTH) void tb_bc(Args a) {
                         gphi += gbo * a.f.Bt[ie] - gbe * a.f.Bt[io] + gco * a.f.Ct[ie] - gce * a.f.Ct[io];
                     }
                     const int64_t je = (int64_t)g * NR + (2 * i) * a.R + r, jo = je + a.R;
-                    gBh[je] += gbe * c + gbo * s;
-                    gBh[jo] += gbo * c - gbe * s;
-                    gCh[je] += gce * c + gco * s;
-                    gCh[jo] += gco * c - gce * s;
+                    qb[je] += gbe * c + gbo * s;
+                    qb[jo] += gbo * c - gbe * s;
+                    qc[je] += gce * c + gco * s;
+                    qc[jo] += gco * c - gce * s;
                 }
                 if (a.cplx) a.gphi[th * NH + i] = gphi;
             }
+        }
+        __syncthreads();
+        for (int e = tid; e < GNR; e += NTH) {
+            float sb = 0.f, sc = 0.f;
+            for (int k = 0; k < HS; ++k) {
+                sb += qB[(int64_t)k * GNR + e];
+                sc += qC[(int64_t)k * GNR + e];
+            }
+            gBh[e] = sb;
+            gCh[e] = sc;
         }
         __syncthreads();
         // RMSNorm backward per group; parameter partials
@@ -415,7 +438,15 @@ Plan plan(const m3_layer_desc& d) {
 
 size_t bc_lds(const m3_layer_desc& d) {
     const size_t NR = (size_t)d.d_state * d.mimo_rank, GNR = d.ngroups * NR;
-    return (4 * GNR + 2 * NR + NTH) * sizeof(float);
+    const size_t HS = std::max(1, NTH / (d.d_state / 2));
+    return ((2 * HS + 4) * GNR + 2 * NR + NTH) * sizeof(float);
+}
+
+// Threads of the tb_gate / tb_x blocks: P rounded up to a power of two (P <= 256).
+int col_threads(int P) {
+    int n = 64;
+    while (n < P) n *= 2;
+    return n;
 }
 
 }  // namespace tb
@@ -450,13 +481,14 @@ int launch_layer_bwd(const m3_layer_desc& d, const m3_layer_params& p, const voi
 
     const int nTB = (a.T + TBK - 1) / TBK, nTC = (a.T + TBC - 1) / TBC;
     const unsigned gbh = (unsigned)((int64_t)a.B * nTB * a.H);
-    hipLaunchKernelGGL(tb_gate, dim3(gbh), dim3(NTH), 0, stream, a);
+    const int nth_col = col_threads(a.P);
+    hipLaunchKernelGGL(tb_gate, dim3(gbh), dim3(nth_col), 0, stream, a);
     if (launch_chunked_bwd(a.B, a.T, a.H, a.P, a.N, a.R, a.f.xg, a.f.xb, a.f.Bt, a.f.Bb, a.f.Ct,
                            a.f.dt, a.f.A, p.D, a.f.xr, nullptr, a.gys, g_h, a.gxg, a.gxb, a.gBt,
                            a.gBb, a.gCt, a.gdtc, a.gAc, a.gD, a.gxr, nullptr,
                            ws + pl.chunk_off, stream) != 0)
         return 1;
-    hipLaunchKernelGGL(tb_x, dim3(gbh), dim3(NTH), 0, stream, a);
+    hipLaunchKernelGGL(tb_x, dim3(gbh), dim3(nth_col), 0, stream, a);
     hipLaunchKernelGGL(tb_bc, dim3((unsigned)((int64_t)a.B * nTC)), dim3(NTH), bc_lds(d), stream, a);
     if (a.cplx) {
         const int nc = (a.T + kAC - 1) / kAC;

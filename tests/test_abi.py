@@ -166,6 +166,33 @@ def test_chunked_rejects_bad_arguments(lib):
                                   256, None, 256, 256, None, 260, 1 << 30, None) == 5
 
 
+def test_layer_bwd_workspace_and_validation(lib):
+    n = ctypes.c_size_t(0)
+    d32 = _desc(seqlen=64)
+    assert lib.m3_layer_bwd_workspace_size(ctypes.byref(d32), ctypes.byref(n)) == 0 and n.value > 0
+    # bf16 layers and ranks outside 1/2/4/8 are not covered (they train through the fallback)
+    assert lib.m3_layer_bwd_workspace_size(ctypes.byref(_desc(dtype=1)), ctypes.byref(n)) == 3
+    assert lib.m3_layer_bwd_workspace_size(ctypes.byref(_desc(mimo_rank=3)), ctypes.byref(n)) == 3
+    assert lib.m3_layer_bwd_workspace_size(ctypes.byref(_desc(batch=0)), ctypes.byref(n)) == 2
+    fake = ctypes.c_void_p(256)
+    params = _native.LayerParams(*([256] * 10))
+    grads = _native.LayerParamGrads(*([256] * 10))
+    args = lambda **kw: dict(dict(proj=fake, fws=fake, fbytes=1 << 40, gout=fake, gproj=fake,
+                                  grads=ctypes.byref(grads), ws=fake, wbytes=1 << 40), **kw)
+    def call(**kw):
+        a = args(**kw)
+        return lib.m3_layer_bwd(ctypes.byref(d32), ctypes.byref(params), a["proj"], None, a["fws"],
+                                a["fbytes"], a["gout"], None, None, None, a["gproj"], a["grads"],
+                                a["ws"], a["wbytes"], None)
+    assert call(gout=None) == 1
+    assert call(gproj=None) == 1
+    bad = _native.LayerParamGrads(*([256] * 9 + [0]))
+    assert call(grads=ctypes.byref(bad)) == 1
+    assert call(fbytes=16) == 4   # the forward's workspace must be the whole fp32-layer one
+    assert call(ws=None) == 4
+    assert call(ws=ctypes.c_void_p(260)) == 5
+
+
 def test_chunked_fwd_workspace_query(lib):
     n = ctypes.c_size_t(7)
     # fp32 d_model 768 shapes: c, decays, two (B, K+1, H, P*N) state arrays and W o G
