@@ -100,16 +100,17 @@ __device__ __forceinline__ int tcol(int tx, int j) { return tx + 16 * j; }
 template <int TN, bool AK, bool BK, class FA, class FB>
 __device__ __forceinline__ void gemm_acc(f32x4 (&acc)[TN / 16], int kdim, FA fa, FB fb,
                                          Lds<TN>& l) {
+    constexpr int NA = KT * TT / NTH;  // A elements per thread and step
     constexpr int NB = KT * TN / NTH;  // B elements per thread and step
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     auto ak = [](int e) { return AK ? e % KT : e / TT; };
     auto am = [](int e) { return AK ? e / KT : e % TT; };
     auto bk = [](int e) { return BK ? e % KT : e / TN; };
     auto bn = [](int e) { return BK ? e / KT : e % TN; };
-    float ra[4], rb[NB];
+    float ra[NA], rb[NB];
     auto fetch = [&](int k0) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < NA; ++i) {
             const int e = tid + NTH * i;
             ra[i] = k0 + ak(e) < kdim ? fa(am(e), k0 + ak(e)) : 0.f;
         }
@@ -123,7 +124,7 @@ __device__ __forceinline__ void gemm_acc(f32x4 (&acc)[TN / 16], int kdim, FA fa,
 #pragma unroll 1
     for (int k0 = 0; k0 < kdim; k0 += KT) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < NA; ++i) {
             const int e = tid + NTH * i;
             l.A[ak(e)][am(e)] = ra[i];
         }
