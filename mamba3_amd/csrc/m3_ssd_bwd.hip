@@ -397,7 +397,7 @@ __device__ __forceinline__ void tile_token_sums(const float (&v)[4], int per, fl
 // ---- K3: dXf rows (s,j) x columns p; writes dx_g / dx_b = dt_s dXf and the per-token
 // partials q_s (state term . Xf) and sum_{p,j} dXf x.
 template <int R, bool BETA>
-__global__ __launch_bounds__(NTH) void bwd_dxf(Args a) {
+__global__ __launch_bounds__(NTH, 4) void bwd_dxf(Args a) {
     BW_CONSTS
     __shared__ Lds<TT> l;
     __shared__ float red[TT][17];
@@ -464,7 +464,7 @@ __global__ __launch_bounds__(NTH) void bwd_dxf(Args a) {
 
 // ---- K4: dBf rows (s,j) x columns n; writes dB_g / dB_b.
 template <int R, bool BETA>
-__global__ __launch_bounds__(NTH) void bwd_dbf(Args a) {
+__global__ __launch_bounds__(NTH, 4) void bwd_dbf(Args a) {
     BW_CONSTS
     __shared__ Lds<TW> l;
     __shared__ float cs[64], dts[64];
@@ -670,7 +670,7 @@ __global__ __launch_bounds__(NTH) void bwd_reduce(Args a) {
 // ---- forward output: y rows (t,r) x columns p of the chunk,
 //   y = (W o G) Xf + exp(c_t) C H_k^T + D x_raw   (M = W o G from bwd_scores in forward mode)
 template <int R, bool BETA>
-__global__ __launch_bounds__(NTH) void fwd_out(Args a) {
+__global__ __launch_bounds__(NTH, 4) void fwd_out(Args a) {
     BW_CONSTS
     __shared__ Lds<TT> l;
     __shared__ float cs[64], dts[64];
