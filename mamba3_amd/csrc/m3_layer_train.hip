@@ -108,25 +108,33 @@ __global__ __launch_bounds__(NTH) void tb_gate(Args a) {
     }
 }
 
-// ---- x terms: one block per (b, token block, h), one thread per headdim column p (blocks of
-// P threads rounded up to a power of two).
+// ---- x terms: one block per (b, token block, h) of NTH threads = slots of PT threads (PT = P
+// rounded up to a power of two): slot s handles tokens t0 + s, t0 + s + slots, ...; the
+// per-token sums over p are segmented block sums; the slots' partials are added in order.
 __global__ __launch_bounds__(NTH) void tb_x(Args a) {
-    __shared__ float red[NTH];
+    __shared__ float red[2][NTH];
+    __shared__ float part[NTH / 64];  // per slot: dL/dA
     const int nTB = (a.T + TBK - 1) / TBK;
     const int h = blockIdx.x % a.H, tb = (blockIdx.x / a.H) % nTB, b = blockIdx.x / (a.H * nTB);
-    const int p = threadIdx.x;
+    int PT = 64;
+    while (PT < a.P) PT *= 2;
+    const int slots = NTH / PT;
+    const int tid = threadIdx.x, slot = tid / PT, p = tid % PT;
     const bool col = p < a.P;
     const int PR = a.P * a.R;
     const float Ah = a.f.A[h];
     float pmx[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     float gA = 0.f;
-    const int t1 = min(a.T, (tb + 1) * TBK);
-    for (int t = tb * TBK; t < t1; ++t) {
-        const int64_t tok = (int64_t)b * a.T + t;
+    const int t0 = tb * TBK, t1 = min(a.T, (tb + 1) * TBK);
+    const int rounds = (t1 - t0 + slots - 1) / slots;
+    for (int k = 0; k < rounds; ++k) {
+        const int t = t0 + k * slots + slot;
+        const bool act = t < t1;
+        const int64_t tok = (int64_t)b * a.T + (act ? t : t0);
         const int64_t th = tok * a.H + h;
         const float* row = a.proj + tok * a.rs;
         float lam = 1.f, dA = 1.f, lamn = 1.f, dAn = 1.f;
-        if (a.trap) {
+        if (a.trap && act) {
             lam = sigm(row[a.pl.lam + h]);
             dA = expf(Ah * a.f.dt[th]);
             if (t + 1 < a.T) {
@@ -135,7 +143,7 @@ __global__ __launch_bounds__(NTH) void tb_x(Args a) {
             }
         }
         float sl = 0.f, sa = 0.f;
-        if (col) {
+        if (col && act) {
             const float x = row[a.pl.x + (int64_t)h * a.P + p];
             float gx = 0.f;
             for (int r = 0; r < a.R; ++r) {
@@ -157,22 +165,53 @@ __global__ __launch_bounds__(NTH) void tb_x(Args a) {
             }
             a.gproj[tok * a.rs + a.pl.x + (int64_t)h * a.P + p] = gx;
         }
-        float gdt = 0.f;
         if (a.trap) {
-            const float slt = block_sum(sl, red), sat = block_sum(sa, red);
-            const float glam = slt - sat * dA;   // dL/dlambda
-            const float gdA = sat * (1.f - lam);  // dL/d(dA)
-            if (p == 0) a.gproj[tok * a.rs + a.pl.lam + h] = glam * lam * (1.f - lam);
-            gdt = gdA * dA * Ah;
-            gA += gdA * dA * a.f.dt[th];
+            // segmented sums over the PT threads of each slot
+            red[0][tid] = sl;
+            red[1][tid] = sa;
+            __syncthreads();
+            for (int w = PT / 2; w > 0; w >>= 1) {
+                if (p < w) {
+                    red[0][tid] += red[0][tid + w];
+                    red[1][tid] += red[1][tid + w];
+                }
+                __syncthreads();
+            }
+            const float slt = red[0][slot * PT], sat = red[1][slot * PT];
+            __syncthreads();
+            if (act) {
+                const float glam = slt - sat * dA;   // dL/dlambda
+                const float gdA = sat * (1.f - lam);  // dL/d(dA)
+                if (p == 0) {
+                    a.gproj[tok * a.rs + a.pl.lam + h] = glam * lam * (1.f - lam);
+                    a.gdtx[th] = gdA * dA * Ah;
+                }
+                gA += gdA * dA * a.f.dt[th];
+            }
+        } else if (act && p == 0) {
+            a.gdtx[th] = 0.f;
         }
-        if (p == 0) a.gdtx[th] = gdt;
     }
-    if (col) {
-        const int64_t o = (((int64_t)b * nTB + tb) * a.H * a.P + (int64_t)h * a.P + p) * a.R;
-        for (int r = 0; r < a.R; ++r) a.p_mx[o + r] = pmx[r];
+    // the slots' mimo_x partials and dL/dA, added in slot order
+    float* pm = &red[0][0];  // one rank at a time
+    for (int r = 0; r < a.R; ++r) {
+        __syncthreads();
+        pm[tid] = pmx[r];
+        __syncthreads();
+        if (slot == 0 && col) {
+            float s = 0.f;
+            for (int k = 0; k < slots; ++k) s += pm[k * PT + p];
+            const int64_t o = (((int64_t)b * nTB + tb) * a.H * a.P + (int64_t)h * a.P + p) * a.R;
+            a.p_mx[o + r] = s;
+        }
     }
-    if (p == 0) a.gA_part[((int64_t)b * nTB + tb) * a.H + h] = gA;
+    if (p == 0) part[slot] = gA;
+    __syncthreads();
+    if (tid == 0) {
+        float s = 0.f;
+        for (int k = 0; k < slots; ++k) s += part[k];
+        a.gA_part[((int64_t)b * nTB + tb) * a.H + h] = s;
+    }
 }
 
 // ---- B / C: one block per (b, TBC tokens). Thread (pair i, head group hg) handles the heads
@@ -488,7 +527,7 @@ int launch_layer_bwd(const m3_layer_desc& d, const m3_layer_params& p, const voi
                            a.gBb, a.gCt, a.gdtc, a.gAc, a.gD, a.gxr, nullptr,
                            ws + pl.chunk_off, stream) != 0)
         return 1;
-    hipLaunchKernelGGL(tb_x, dim3(gbh), dim3(nth_col), 0, stream, a);
+    hipLaunchKernelGGL(tb_x, dim3(gbh), dim3(NTH), 0, stream, a);
     hipLaunchKernelGGL(tb_bc, dim3((unsigned)((int64_t)a.B * nTC)), dim3(NTH), bc_lds(d), stream, a);
     if (a.cplx) {
         const int nc = (a.T + kAC - 1) / kAC;
