@@ -193,6 +193,38 @@ def test_layer_d768_gradients_match_oracle(cuda_device):
         assert max_rel(p.grad, pg[name]) < FP32_TOL, name
 
 
+@pytest.mark.parametrize("kw", [LAYER_KW[0], LAYER_KW[3], LAYER_KW[2]],
+                         ids=["default", "rank4-groups2", "complex-off"])
+def test_layer_state_gradients_match_oracle(kw, cuda_device):
+    """A loss over every prefill state tensor (h, angle, prev_BX) as well as the output: the
+    state-gradient paths of the backward against the fp64 oracle."""
+    torch.manual_seed(0)
+    layer = mamba3_amd.KulaMamba(**kw).to(cuda_device).train()
+    H, P, N = layer.nheads, layer.headdim, layer.d_state
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(2, 37, kw["d_model"], generator=g)
+    w = torch.randn(2, 37, kw["d_model"], generator=g)
+    wst = {"h": torch.randn(2, H, P, N, generator=g), "angle": torch.randn(2, H, N // 2, generator=g),
+           "prev_BX": torch.randn(2, H, P, N, generator=g)}
+    params = {k: v.detach().double().cpu().clone().requires_grad_()
+              for k, v in layer.state_dict().items()}
+    xr = x.double().requires_grad_()
+    out_ref, st_ref = ref.layer_forward(oracle_cfg(kw), params, xr, return_state=True)
+    loss = (out_ref * w.double()).sum()
+    for k, v in wst.items():
+        loss = loss + (st_ref[k].double() * v.double()).sum()
+    loss.backward()
+    xd = x.to(cuda_device).requires_grad_()
+    out, st = layer.prefill(xd)
+    loss = (out * w.to(cuda_device)).sum()
+    for k, v in wst.items():
+        loss = loss + (st[k] * v.to(cuda_device)).sum()
+    loss.backward()
+    assert max_rel(xd.grad, xr.grad) < FP32_TOL
+    for name, p in layer.named_parameters():
+        assert max_rel(p.grad, params[name].grad) < FP32_TOL, name
+
+
 def test_layer_training_runs_on_the_native_backward(cuda_device):
     """The parity tests above go through m3_layer_bwd: it covers every configuration they use."""
     from mamba3_amd import _native
