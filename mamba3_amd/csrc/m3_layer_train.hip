@@ -73,38 +73,56 @@ __device__ float block_sum(float v, float* red) {
     return s;
 }
 
-// ---- gate: one block per (b, token block, h), one thread per headdim column p (blocks of
-// P threads rounded up to a power of two).
+// ---- gate: one block per (b, token block, h) of NTH threads = slots of PT threads (PT = P
+// rounded up to a power of two), slot s handling tokens t0 + s, t0 + s + slots, ...; the
+// slots' parameter partials are added in order.
 __global__ __launch_bounds__(NTH) void tb_gate(Args a) {
+    __shared__ float red[2][NTH];
     const int nTB = (a.T + TBK - 1) / TBK;
     const int h = blockIdx.x % a.H, tb = (blockIdx.x / a.H) % nTB, b = blockIdx.x / (a.H * nTB);
-    const int p = threadIdx.x;
-    if (p >= a.P) return;
+    int PT = 64;
+    while (PT < a.P) PT *= 2;
+    const int slots = NTH / PT;
+    const int tid = threadIdx.x, slot = tid / PT, p = tid % PT;
+    const bool col = p < a.P;
     const int64_t HP = (int64_t)a.H * a.P;
     float pmd[8] = {0, 0, 0, 0, 0, 0, 0, 0}, pmz[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     const int t1 = min(a.T, (tb + 1) * TBK);
-    for (int t = tb * TBK; t < t1; ++t) {
-        const int64_t tok = (int64_t)b * a.T + t;
-        const float z = a.proj[tok * a.rs + a.pl.z + (int64_t)h * a.P + p];
-        const float g = a.gout[tok * HP + (int64_t)h * a.P + p];
-        const int64_t yb = (tok * a.H + h) * a.P * a.R + (int64_t)p * a.R;
-        float gz = 0.f;
-        for (int r = 0; r < a.R; ++r) {
-            const int64_t pr = ((int64_t)h * a.P + p) * a.R + r;
-            const float mz = a.prm.mimo_z[pr], md = a.prm.mimo_down[pr];
-            const float zz = z * mz, sg = sigm(zz), silu = zz * sg, ds = sg * (1.f + zz * (1.f - sg));
-            const float y = a.f.ys[yb + r];
-            a.gys[yb + r] = g * md * silu;
-            gz += g * md * y * ds * mz;
-            pmd[r] += g * y * silu;
-            pmz[r] += g * md * y * ds * z;
+    if (col) {
+        for (int t = tb * TBK + slot; t < t1; t += slots) {
+            const int64_t tok = (int64_t)b * a.T + t;
+            const float z = a.proj[tok * a.rs + a.pl.z + (int64_t)h * a.P + p];
+            const float g = a.gout[tok * HP + (int64_t)h * a.P + p];
+            const int64_t yb = (tok * a.H + h) * a.P * a.R + (int64_t)p * a.R;
+            float gz = 0.f;
+            for (int r = 0; r < a.R; ++r) {
+                const int64_t pr = ((int64_t)h * a.P + p) * a.R + r;
+                const float mz = a.prm.mimo_z[pr], md = a.prm.mimo_down[pr];
+                const float zz = z * mz, sg = sigm(zz), silu = zz * sg, ds = sg * (1.f + zz * (1.f - sg));
+                const float y = a.f.ys[yb + r];
+                a.gys[yb + r] = g * md * silu;
+                gz += g * md * y * ds * mz;
+                pmd[r] += g * y * silu;
+                pmz[r] += g * md * y * ds * z;
+            }
+            a.gproj[tok * a.rs + a.pl.z + (int64_t)h * a.P + p] = gz;
         }
-        a.gproj[tok * a.rs + a.pl.z + (int64_t)h * a.P + p] = gz;
     }
     const int64_t o = (((int64_t)b * nTB + tb) * HP + (int64_t)h * a.P + p) * a.R;
     for (int r = 0; r < a.R; ++r) {
-        a.p_md[o + r] = pmd[r];
-        a.p_mz[o + r] = pmz[r];
+        __syncthreads();
+        red[0][tid] = pmd[r];
+        red[1][tid] = pmz[r];
+        __syncthreads();
+        if (slot == 0 && col) {
+            float sd = 0.f, sz = 0.f;
+            for (int k = 0; k < slots; ++k) {
+                sd += red[0][k * PT + p];
+                sz += red[1][k * PT + p];
+            }
+            a.p_md[o + r] = sd;
+            a.p_mz[o + r] = sz;
+        }
     }
 }
 
@@ -481,12 +499,6 @@ size_t bc_lds(const m3_layer_desc& d) {
     return ((2 * HS + 4) * GNR + 2 * NR + NTH) * sizeof(float);
 }
 
-// Threads of the tb_gate / tb_x blocks: P rounded up to a power of two (P <= 256).
-int col_threads(int P) {
-    int n = 64;
-    while (n < P) n *= 2;
-    return n;
-}
 
 }  // namespace tb
 
@@ -520,8 +532,7 @@ int launch_layer_bwd(const m3_layer_desc& d, const m3_layer_params& p, const voi
 
     const int nTB = (a.T + TBK - 1) / TBK, nTC = (a.T + TBC - 1) / TBC;
     const unsigned gbh = (unsigned)((int64_t)a.B * nTB * a.H);
-    const int nth_col = col_threads(a.P);
-    hipLaunchKernelGGL(tb_gate, dim3(gbh), dim3(nth_col), 0, stream, a);
+    hipLaunchKernelGGL(tb_gate, dim3(gbh), dim3(NTH), 0, stream, a);
     if (launch_chunked_bwd(a.B, a.T, a.H, a.P, a.N, a.R, a.f.xg, a.f.xb, a.f.Bt, a.f.Bb, a.f.Ct,
                            a.f.dt, a.f.A, p.D, a.f.xr, nullptr, a.gys, g_h, a.gxg, a.gxb, a.gBt,
                            a.gBb, a.gCt, a.gdtc, a.gAc, a.gD, a.gxr, nullptr,
