@@ -313,6 +313,22 @@ def test_lm_training_steps_reduce_the_loss(cuda_device):
     assert losses[-1] < losses[0] - 1e-3, losses
 
 
+def test_lm_gradient_checkpointing_gives_the_same_gradients(cuda_device):
+    """KulaMambaLM(gradient_checkpointing=True) recomputes each block's forward during the
+    backward (mamba3/block.py:79-92); the native kernels are deterministic, so the gradients
+    equal the stored-activation run bit for bit."""
+    def grads(ckpt):
+        torch.manual_seed(0)
+        lm = mamba3_amd.KulaMambaLM(vocab_size=64, d_model=64, n_layers=2, d_state=16, headdim=16,
+                                    mimo_rank=2, gradient_checkpointing=ckpt).to(cuda_device).train()
+        ids = torch.randint(0, 64, (2, 40), generator=torch.Generator().manual_seed(10)).to(cuda_device)
+        lm(ids, labels=ids)["loss"].backward()
+        return {n: p.grad.clone() for n, p in lm.named_parameters()}
+    g0, g1 = grads(False), grads(True)
+    for n in g0:
+        assert torch.equal(g0[n], g1[n]), n
+
+
 def test_step_backward_raises_instead_of_wrong_gradients(cuda_device):
     torch.manual_seed(0)
     layer = mamba3_amd.KulaMamba(64, d_state=16, headdim=16).to(cuda_device).train()
