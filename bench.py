@@ -182,9 +182,10 @@ def bench_layer_fp32_d768(args, torch, mamba3_amd):
     res = base_result(args, tokens / (ms * 1e-3), ms,
                       "KulaMamba forward (whole layer), d_model 768, fp32, x (4, 1024, 768)",
                       4, 1024, dtype="fp32")
+    traffic = recorded_traffic(ROOT / "profiles" / "kernel_trace_fp32_layer_d768.md", ("layer_fp32",))
     res["roofline"] = {"bound": "mfma", "achieved": round(tf, 3), "peak": PEAK_FP32_TFLOPS,
                        "unit": "TFLOP/s", "frac": round(tf / PEAK_FP32_TFLOPS, 4),
-                       "traffic": None,
+                       "traffic": traffic.get("layer_fp32"),
                        "kernel": "native fp32 SSD core (all launches of m3_prefill_fwd: preparation, "
                                  "fp32-MFMA chunk kernels, gate)",
                        "algorithmic_flops": flops, "avg_ms": round(core_ms, 4)}
@@ -464,8 +465,10 @@ def bench_layer_bwd(args, torch, mamba3_amd):
                       "fp32, x (4, 1024, 768), inputs resident in HBM", B, T, dtype="fp32")
     res["train_step"] = {"ms": round(train_ms, 4), "tokens_per_s": round(B * T / (train_ms * 1e-3), 1),
                          "what": "layer forward + backward through autograd (projections included)"}
+    traffic = recorded_traffic(ROOT / "profiles" / "layer_bwd_d768_trace.md", ("layer_bwd",))
     res["roofline"] = {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_FP32_TFLOPS,
-                       "unit": "TFLOP/s", "frac": round(tflops / PEAK_FP32_TFLOPS, 4), "traffic": None,
+                       "unit": "TFLOP/s", "frac": round(tflops / PEAK_FP32_TFLOPS, 4),
+                       "traffic": traffic.get("layer_bwd"),
                        "kernel": "m3_layer_bwd, all kernels of one call; FLOPs of its chunked-SSD "
                                  "backward GEMMs",
                        "algorithmic_flops": flops, "avg_ms": round(kern_ms, 4)}
