@@ -440,6 +440,32 @@ def test_bf16_step_matches_fp32_oracle(cuda_device):
             assert max_rel(st_dev[k], st[k]) < BF16_TOL, (i, k)
 
 
+def test_bf16_decode_1024_steps_match_fp32_oracle(cuda_device):
+    """The decode workload: d768 layer in bf16, batch 64, the state filled by prefilling 512
+    N(0,1) tokens, then 1024 sequential steps on (64, 768) N(0,1) tokens. The oracle steps
+    in fp32 from the same prefilled state (copied to the host); every step's output and
+    the final h, prev_BX and angle are compared, within the bf16 tolerance."""
+    kw = dict(d_model=768, d_state=128, headdim=64, mimo_rank=2)
+    layer, cfg, p = _bf16_pair(kw, cuda_device)
+    g = torch.Generator().manual_seed(3)
+    xp = torch.randn(64, 512, 768, generator=g).to(torch.bfloat16)
+    with torch.no_grad():
+        _, st_dev = layer.prefill(xp.to(cuda_device))
+    st = {k: v.float().cpu() for k, v in st_dev.items()}
+    worst = 0.0
+    for i in range(1024):
+        x = torch.randn(64, 768, generator=g).to(torch.bfloat16)
+        with torch.no_grad():
+            y, st_dev = layer.step(x.to(cuda_device), st_dev)
+            y_ref, st = ref.layer_step(cfg, p, x.float(), st)
+        e = max_rel(y.float(), y_ref)
+        worst = max(worst, e)
+        assert e < BF16_TOL, (i, e)
+    for k in ("h", "prev_BX", "angle"):
+        assert max_rel(st_dev[k], st[k]) < BF16_TOL, k
+    assert worst > 0.0
+
+
 def test_fp32_step_matches_oracle_from_random_state(cuda_device):
     kw = dict(d_model=768, d_state=128, headdim=64, mimo_rank=2)
     torch.manual_seed(0)
