@@ -35,6 +35,9 @@
 namespace m3 {
 namespace tb {
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
 constexpr int NTH = 256;
 constexpr int TBK = 64;  // tokens per block of tb_gate / tb_x
 constexpr int TBC = 4;   // tokens per block of tb_bc
@@ -238,9 +241,28 @@ __global__ __launch_bounds__(NTH) void tb_x(Args a) {
 // partials, the reduction scratch.
 __device__ __forceinline__ int bc_hs(int N) { return max(1, NTH / (N / 2)); }
 
+// The 2R values of pair i (even column, ranks 0..R-1, then odd column) are contiguous and
+// 8R-byte aligned: one vector load per array.
+template <int K>
+__device__ __forceinline__ void ldv(const float* p, float (&v)[K]) {
+    if constexpr (K % 4 == 0) {
+#pragma unroll
+        for (int j = 0; j < K / 4; ++j) {
+            const f32x4 q = *reinterpret_cast<const f32x4*>(p + 4 * j);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) v[4 * j + k] = q[k];
+        }
+    } else {
+        const f32x2 q = *reinterpret_cast<const f32x2*>(p);
+        v[0] = q[0];
+        v[1] = q[1];
+    }
+}
+
+template <int R>
 __global__ __launch_bounds__(NTH) void tb_bc(Args a) {
     extern __shared__ float sm[];
-    const int NR = a.N * a.R, GNR = a.G * NR, NH = a.N / 2, hpg = a.H / a.G;
+    const int NR = a.N * R, GNR = a.G * NR, NH = a.N / 2, hpg = a.H / a.G;
     const int HS = bc_hs(a.N);
     float* qB = sm;                 // [HS][GNR]
     float* qC = qB + HS * GNR;      // [HS][GNR]
@@ -274,26 +296,34 @@ __global__ __launch_bounds__(NTH) void tb_bc(Args a) {
                 float s = 0.f, c = 1.f;
                 if (a.cplx) sincosf(a.f.phi[th * NH + i], &s, &c);
                 float gphi = 0.f;
-                for (int r = 0; r < a.R; ++r) {
-                    const int64_t ie = bt + (int64_t)(2 * i) * a.R + r, io = ie + a.R;
-                    float gbe = a.gBt[ie], gbo = a.gBt[io];
-                    if (a.trap && t + 1 < a.T) {
-                        gbe += a.gBb[ie + (int64_t)a.H * NR];
-                        gbo += a.gBb[io + (int64_t)a.H * NR];
-                    }
+                const int64_t e0 = bt + (int64_t)(2 * i) * R;
+                float gb[2 * R], gc[2 * R], vb[2 * R], vc[2 * R];
+                ldv<2 * R>(a.gBt + e0, gb);
+                ldv<2 * R>(a.gCt + e0, gc);
+                if (a.trap && t + 1 < a.T) {
+                    float nb[2 * R];
+                    ldv<2 * R>(a.gBb + e0 + (int64_t)a.H * NR, nb);
+#pragma unroll
+                    for (int k = 0; k < 2 * R; ++k) gb[k] += nb[k];
+                }
+                if (a.cplx) {
+                    ldv<2 * R>(a.f.Bt + e0, vb);
+                    ldv<2 * R>(a.f.Ct + e0, vc);
+                }
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    float gbe = gb[r], gbo = gb[R + r];
                     if (t == a.T - 1 && a.gprev) {
                         const float* gp = a.gprev + ((int64_t)b * a.H + h) * a.P * a.N;
-                        const float* xr = a.f.xr + th * a.P * a.R + r;
+                        const float* xr = a.f.xr + th * a.P * R + r;
                         for (int pp = 0; pp < a.P; ++pp) {
-                            gbe += gp[(int64_t)pp * a.N + 2 * i] * xr[(int64_t)pp * a.R];
-                            gbo += gp[(int64_t)pp * a.N + 2 * i + 1] * xr[(int64_t)pp * a.R];
+                            gbe += gp[(int64_t)pp * a.N + 2 * i] * xr[(int64_t)pp * R];
+                            gbo += gp[(int64_t)pp * a.N + 2 * i + 1] * xr[(int64_t)pp * R];
                         }
                     }
-                    const float gce = a.gCt[ie], gco = a.gCt[io];
-                    if (a.cplx) {
-                        gphi += gbo * a.f.Bt[ie] - gbe * a.f.Bt[io] + gco * a.f.Ct[ie] - gce * a.f.Ct[io];
-                    }
-                    const int64_t je = (int64_t)g * NR + (2 * i) * a.R + r, jo = je + a.R;
+                    const float gce = gc[r], gco = gc[R + r];
+                    if (a.cplx) gphi += gbo * vb[r] - gbe * vb[R + r] + gco * vc[r] - gce * vc[R + r];
+                    const int64_t je = (int64_t)g * NR + (2 * i) * R + r, jo = je + R;
                     qb[je] += gbe * c + gbo * s;
                     qb[jo] += gbo * c - gbe * s;
                     qc[je] += gce * c + gco * s;
@@ -539,7 +569,13 @@ int launch_layer_bwd(const m3_layer_desc& d, const m3_layer_params& p, const voi
                            ws + pl.chunk_off, stream) != 0)
         return 1;
     hipLaunchKernelGGL(tb_x, dim3(gbh), dim3(NTH), 0, stream, a);
-    hipLaunchKernelGGL(tb_bc, dim3((unsigned)((int64_t)a.B * nTC)), dim3(NTH), bc_lds(d), stream, a);
+    const dim3 gbc((unsigned)((int64_t)a.B * nTC));
+    switch (a.R) {
+        case 1: hipLaunchKernelGGL(tb_bc<1>, gbc, dim3(NTH), bc_lds(d), stream, a); break;
+        case 2: hipLaunchKernelGGL(tb_bc<2>, gbc, dim3(NTH), bc_lds(d), stream, a); break;
+        case 4: hipLaunchKernelGGL(tb_bc<4>, gbc, dim3(NTH), bc_lds(d), stream, a); break;
+        default: hipLaunchKernelGGL(tb_bc<8>, gbc, dim3(NTH), bc_lds(d), stream, a); break;
+    }
     if (a.cplx) {
         const int nc = (a.T + kAC - 1) / kAC;
         const int64_t na = (int64_t)a.B * nc * a.H * (a.N / 2);
