@@ -39,6 +39,14 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int NTH = 256;
+constexpr int kW = 64;   // wavefront size
+
+// Sum over the 64 lanes of a wave (butterfly: every lane gets the same result).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = kW / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kW);
+    return v;
+}
 constexpr int TBK = 64;  // tokens per block of tb_gate / tb_x
 constexpr int TBC = 4;   // tokens per block of tb_bc
 constexpr int kAC = 64;  // tokens per chunk of the angle suffix scan
@@ -187,19 +195,25 @@ __global__ __launch_bounds__(NTH) void tb_x(Args a) {
             a.gproj[tok * a.rs + a.pl.x + (int64_t)h * a.P + p] = gx;
         }
         if (a.trap) {
-            // segmented sums over the PT threads of each slot
-            red[0][tid] = sl;
-            red[1][tid] = sa;
-            __syncthreads();
-            for (int w = PT / 2; w > 0; w >>= 1) {
-                if (p < w) {
-                    red[0][tid] += red[0][tid + w];
-                    red[1][tid] += red[1][tid + w];
+            // segmented sums over the PT threads of each slot: a butterfly within each wave
+            // (a slot of 64 threads is one wave), then, for wider slots, the slot's waves
+            // added in order through LDS
+            float slt = wave_sum(sl), sat = wave_sum(sa);
+            if (PT > kW) {
+                const int nw = PT / kW;
+                if ((tid & (kW - 1)) == 0) {
+                    red[0][tid / kW] = slt;
+                    red[1][tid / kW] = sat;
+                }
+                __syncthreads();
+                slt = 0.f;
+                sat = 0.f;
+                for (int w = 0; w < nw; ++w) {
+                    slt += red[0][slot * nw + w];
+                    sat += red[1][slot * nw + w];
                 }
                 __syncthreads();
             }
-            const float slt = red[0][slot * PT], sat = red[1][slot * PT];
-            __syncthreads();
             if (act) {
                 const float glam = slt - sat * dA;   // dL/dlambda
                 const float gdA = sat * (1.f - lam);  // dL/d(dA)

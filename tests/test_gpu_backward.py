@@ -135,6 +135,7 @@ LAYER_KW = [
     dict(d_model=64, d_state=16, headdim=16, mimo_rank=1, use_trapezoidal=False,
          use_complex_ssm=False),
     dict(d_model=128, d_state=64, headdim=32, mimo_rank=2),
+    dict(d_model=128, d_state=32, headdim=128, mimo_rank=2),  # slots wider than a wave
 ]
 
 
