@@ -29,6 +29,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <initializer_list>
 
 #include "m3_kernels.h"
 
@@ -469,14 +470,35 @@ __global__ __launch_bounds__(NTH) void tb_tok(Args a) {
 // groups in order); slabs are summed by the next pass.
 constexpr int kSlab = 256;
 
-__global__ __launch_bounds__(NTH) void tb_colsum(const float* in, int64_t K, int M, float* out) {
+// Up to four column-sum jobs of the same row count K in one launch (blockIdx.z picks one);
+// each has its own input, output and column count.
+struct ColJobs {
+    const float* in[4];
+    float* out[4];
+    int M[4];
+};
+
+__global__ __launch_bounds__(NTH) void tb_colsum(ColJobs jobs, int64_t K) {
     __shared__ float red[4][64];
+    const float* in = jobs.in[blockIdx.z];
+    float* out = jobs.out[blockIdx.z];
+    const int M = jobs.M[blockIdx.z];
     const int c = threadIdx.x & 63, grp = threadIdx.x >> 6;
     const int col = blockIdx.x * 64 + c;
     const int64_t r0 = (int64_t)blockIdx.y * kSlab, r1 = min(K, r0 + kSlab);
     float s = 0.f;
-    if (col < M)
-        for (int64_t r = r0 + grp; r < r1; r += 4) s += in[r * M + col];
+    if (col < M) {
+        // rows r0+grp, +4, +8, ... added in that order; eight loads go out before their adds
+        int64_t r = r0 + grp;
+        for (; r + 28 < r1; r += 32) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = in[(r + 4 * u) * M + col];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) s += v[u];
+        }
+        for (; r < r1; r += 4) s += in[r * M + col];
+    }
     red[grp][c] = s;
     __syncthreads();
     if (grp == 0 && col < M) out[(int64_t)blockIdx.y * M + col] = red[0][c] + red[1][c] + red[2][c] + red[3][c];
@@ -523,7 +545,7 @@ Plan plan(const m3_layer_desc& d) {
         B * nTC * N * R, B * nTC * N * R,              // p_Bw, p_Cw
         B * nTC * G * N * R, B * nTC * G * N * R,      // p_Bb, p_Cb
         BTH,                                           // p_dtb
-        colsum_scratch(d), colsum_scratch(d), H};      // column-sum passes, dL/dA (x terms)
+        4 * colsum_scratch(d), 4 * colsum_scratch(d), H};  // column-sum passes (4 jobs), dL/dA (x terms)
     Plan p;
     size_t o = 0;
     for (int i = 0; i < 26; ++i) {
@@ -599,30 +621,39 @@ int launch_layer_bwd(const m3_layer_desc& d, const m3_layer_params& p, const voi
     }
     hipLaunchKernelGGL(tb_tok, dim3((unsigned)((int64_t)a.B * a.T)), dim3(NTH), 0, stream, a);
     float* tmp[2] = {part(23), part(24)};
-    auto colsum = [&](const float* in, int64_t K, int M, float* out) {
+    const size_t unit = colsum_scratch(d);  // floats per job and pass
+    // Column sums of nz partial matrices with K rows: slab sums (kSlab rows), then sums of
+    // those, every job in its own scratch region; rows are added in a fixed order.
+    auto colsum = [&](int nz, std::initializer_list<const float*> ins, std::initializer_list<float*> outs,
+                      std::initializer_list<int> Ms, int64_t K) {
+        ColJobs j{};
+        int Mmax = 0;
+        for (int z = 0; z < nz; ++z) {
+            j.in[z] = ins.begin()[z];
+            j.M[z] = Ms.begin()[z];
+            Mmax = std::max(Mmax, j.M[z]);
+        }
         int w = 0;
-        while (K > kSlab) {  // slab sums, then sums of those
+        while (K > kSlab) {
             const int64_t ks = (K + kSlab - 1) / kSlab;
-            hipLaunchKernelGGL(tb_colsum, dim3((unsigned)((M + 63) / 64), (unsigned)ks), dim3(NTH), 0,
-                               stream, in, K, M, tmp[w]);
-            in = tmp[w];
+            for (int z = 0; z < nz; ++z) j.out[z] = tmp[w] + z * unit;
+            hipLaunchKernelGGL(tb_colsum, dim3((unsigned)((Mmax + 63) / 64), (unsigned)ks, (unsigned)nz),
+                               dim3(NTH), 0, stream, j, K);
+            for (int z = 0; z < nz; ++z) j.in[z] = j.out[z];
             w ^= 1;
             K = ks;
         }
-        hipLaunchKernelGGL(tb_colsum, dim3((unsigned)((M + 63) / 64), 1), dim3(NTH), 0, stream, in, K,
-                           M, out);
+        for (int z = 0; z < nz; ++z) j.out[z] = outs.begin()[z];
+        hipLaunchKernelGGL(tb_colsum, dim3((unsigned)((Mmax + 63) / 64), 1, (unsigned)nz), dim3(NTH), 0,
+                           stream, j, K);
     };
     const int NR = a.N * a.R, HPR = a.H * a.P * a.R;
     const int64_t nbt = (int64_t)a.B * nTB, nbc = (int64_t)a.B * nTC;
-    colsum(a.p_dtb, (int64_t)a.B * a.T, a.H, g.dt_bias);
-    colsum(a.p_Bw, nbc, NR, g.B_norm_w);
-    colsum(a.p_Cw, nbc, NR, g.C_norm_w);
-    colsum(a.p_Bb, nbc, a.G * NR, g.B_bias);
-    colsum(a.p_Cb, nbc, a.G * NR, g.C_bias);
-    colsum(a.p_mx, nbt, HPR, g.mimo_x);
-    colsum(a.p_mz, nbt, HPR, g.mimo_z);
-    colsum(a.p_md, nbt, HPR, g.mimo_down);
-    colsum(a.gA_part, nbt, a.H, part(25));
+    colsum(1, {a.p_dtb}, {g.dt_bias}, {a.H}, (int64_t)a.B * a.T);
+    colsum(4, {a.p_Bw, a.p_Cw, a.p_Bb, a.p_Cb}, {g.B_norm_w, g.C_norm_w, g.B_bias, g.C_bias},
+           {NR, NR, a.G * NR, a.G * NR}, nbc);
+    colsum(4, {a.p_mx, a.p_mz, a.p_md, a.gA_part}, {g.mimo_x, g.mimo_z, g.mimo_down, part(25)},
+           {HPR, HPR, HPR, a.H}, nbt);
     hipLaunchKernelGGL(tb_finish, dim3((unsigned)((a.H + NTH - 1) / NTH)), dim3(NTH), 0, stream, a,
                        part(25));
     return hipGetLastError() == hipSuccess ? 0 : 1;
