@@ -418,7 +418,17 @@ __global__ __launch_bounds__(NTH) void tb_asum(Args a) {
     ajob(a, e, b, c, h, i);
     float s = 0.f;
     const int t1 = min(a.T, (c + 1) * kAC);
-    for (int t = c * kAC; t < t1; ++t) s += a.gphi[(((int64_t)b * a.T + t) * a.H + h) * NH + i];
+    const int64_t ts = (int64_t)a.H * NH;  // token stride
+    const float* gp = a.gphi + (((int64_t)b * a.T) * a.H + h) * NH + i;
+    int t = c * kAC;
+    for (; t + 8 <= t1; t += 8) {  // tokens added in order; eight loads ahead of their adds
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = gp[(t + u) * ts];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s += v[u];
+    }
+    for (; t < t1; ++t) s += gp[t * ts];
     a.Phi_sum[e] = s;
 }
 
@@ -431,10 +441,24 @@ __global__ __launch_bounds__(NTH) void tb_angle(Args a) {
     float s = a.gang ? a.gang[((int64_t)b * a.H + h) * NH + i] : 0.f;
     for (int cc = nc - 1; cc > c; --cc) s += a.Phi_sum[(((int64_t)b * nc + cc) * a.H + h) * NH + i];
     const int t1 = min(a.T, (c + 1) * kAC);
-    for (int t = t1 - 1; t >= c * kAC; --t) {
-        const int64_t o = (((int64_t)b * a.T + t) * a.H + h) * NH + i;
-        s += a.gphi[o];
-        a.Phi[o] = s;
+    const int64_t ts = (int64_t)a.H * NH;  // token stride
+    const int64_t o0 = (((int64_t)b * a.T) * a.H + h) * NH + i;
+    // tokens walked down in order; gphi and Phi are separate buffers, so eight loads of gphi
+    // go out ahead of the running sums
+    int t = t1 - 1;
+    for (; t - 7 >= c * kAC; t -= 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = a.gphi[o0 + (t - u) * ts];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            s += v[u];
+            a.Phi[o0 + (t - u) * ts] = s;
+        }
+    }
+    for (; t >= c * kAC; --t) {
+        s += a.gphi[o0 + t * ts];
+        a.Phi[o0 + t * ts] = s;
     }
 }
 
@@ -445,8 +469,20 @@ __global__ __launch_bounds__(NTH) void tb_tok(Args a) {
     const float* row = a.proj + tok * a.rs;
     if (a.cplx) {
         for (int i = threadIdx.x; i < NH; i += NTH) {
+            // heads added in order; eight heads' loads go out before their products
             float s = 0.f;
-            for (int h = 0; h < a.H; ++h) s += a.f.dt[tok * a.H + h] * a.Phi[(tok * a.H + h) * NH + i];
+            int h = 0;
+            for (; h + 8 <= a.H; h += 8) {
+                float dv[8], pv[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    dv[u] = a.f.dt[tok * a.H + h + u];
+                    pv[u] = a.Phi[(tok * a.H + h + u) * NH + i];
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) s += dv[u] * pv[u];
+            }
+            for (; h < a.H; ++h) s += a.f.dt[tok * a.H + h] * a.Phi[(tok * a.H + h) * NH + i];
             a.gproj[tok * a.rs + a.pl.theta + i] = -s;
         }
     }
@@ -455,7 +491,18 @@ __global__ __launch_bounds__(NTH) void tb_tok(Args a) {
         float g = a.gdtc[th] + a.gdtx[th];
         if (a.cplx) {
             float s = 0.f;
-            for (int i = 0; i < NH; ++i) s += row[a.pl.theta + i] * a.Phi[th * NH + i];
+            int i = 0;
+            for (; i + 8 <= NH; i += 8) {
+                float tv[8], pv[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    tv[u] = row[a.pl.theta + i + u];
+                    pv[u] = a.Phi[th * NH + i + u];
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) s += tv[u] * pv[u];
+            }
+            for (; i < NH; ++i) s += row[a.pl.theta + i] * a.Phi[th * NH + i];
             g -= s;
         }
         const float u = row[a.pl.dt + h] + a.prm.dt_bias[h];
