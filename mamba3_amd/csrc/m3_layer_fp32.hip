@@ -75,10 +75,20 @@ __global__ __launch_bounds__(NTH) void lp_angle_sums(Args a) {
     angle_job(a, e, b, c, h, i);
     float s = 0.f;
     const int t1 = min(a.T, (c + 1) * kAC);
-    for (int t = c * kAC; t < t1; ++t) {
-        const int64_t tok = (int64_t)b * a.T + t;
-        s += a.dt[tok * a.H + h] * a.proj[tok * a.rs + a.pl.theta + i];
+    const float* dtp = a.dt + (int64_t)b * a.T * a.H + h;                  // stride H
+    const float* thp = a.proj + (int64_t)b * a.T * a.rs + a.pl.theta + i;  // stride rs
+    int t = c * kAC;
+    for (; t + 8 <= t1; t += 8) {  // tokens added in order; eight loads ahead of their products
+        float dv[8], tv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            dv[u] = dtp[(int64_t)(t + u) * a.H];
+            tv[u] = thp[(int64_t)(t + u) * a.rs];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s += dv[u] * tv[u];
     }
+    for (; t < t1; ++t) s += dtp[(int64_t)t * a.H] * thp[(int64_t)t * a.rs];
     a.phi_sum[e] = s;
 }
 
@@ -93,10 +103,29 @@ __global__ __launch_bounds__(NTH) void lp_angles(Args a) {
     float s = 0.f;
     for (int cc = 0; cc < c; ++cc) s += a.phi_sum[(((int64_t)b * nc + cc) * a.H + h) * NH + i];
     const int t1 = min(a.T, (c + 1) * kAC);
-    for (int t = c * kAC; t < t1; ++t) {
-        const int64_t tok = (int64_t)b * a.T + t;
-        s += a.dt[tok * a.H + h] * a.proj[tok * a.rs + a.pl.theta + i];
-        a.phi[(tok * a.H + h) * NH + i] = -s;
+    const float* dtp = a.dt + (int64_t)b * a.T * a.H + h;                  // stride H
+    const float* thp = a.proj + (int64_t)b * a.T * a.rs + a.pl.theta + i;  // stride rs
+    float* php = a.phi + ((int64_t)b * a.T * a.H + h) * NH + i;            // stride H*NH
+    const int64_t ps = (int64_t)a.H * NH;
+    // tokens in order; phi is a buffer of its own, so eight tokens' loads go out ahead of the
+    // running sums and their stores
+    int t = c * kAC;
+    for (; t + 8 <= t1; t += 8) {
+        float dv[8], tv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            dv[u] = dtp[(int64_t)(t + u) * a.H];
+            tv[u] = thp[(int64_t)(t + u) * a.rs];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            s += dv[u] * tv[u];
+            php[(t + u) * ps] = -s;
+        }
+    }
+    for (; t < t1; ++t) {
+        s += dtp[(int64_t)t * a.H] * thp[(int64_t)t * a.rs];
+        php[t * ps] = -s;
     }
 }
 
