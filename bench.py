@@ -72,6 +72,11 @@ def step_bytes(B, H, d_in_proj, d_inner):
 TRAFFIC_FILE = ROOT / "profiles" / "pmc_traffic_d768.md"
 
 
+def traffic_source(path) -> str:
+    return (f"recorded, not measured in this run: {path.relative_to(ROOT)} (rocprofv3 --pmc "
+            "FETCH_SIZE and WRITE_SIZE of the same command, scaled by a 256 MiB copy)")
+
+
 def recorded_traffic(path=TRAFFIC_FILE, keys=("prefill", "step")):
     """HBM bytes per call measured with rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE, scaled by
     a 256 MiB copy), as recorded in a profiles summary: {'prefill': B, 'step': B}."""
@@ -141,6 +146,7 @@ def bench_prefill_d2048(args, torch, mamba3_amd):
     res["roofline"] = {"bound": "mfma", "achieved": round(tf, 2), "peak": PEAK_BF16_TFLOPS,
                        "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4),
                        "traffic": traffic.get("prefill"),
+                       "traffic_source": traffic_source(ROOT / "profiles" / "pmc_traffic_d2048.md"),
                        "kernel": "native SSD prefill (all launches of m3_prefill_fwd)",
                        "algorithmic_flops": flops, "avg_ms": round(kern_ms, 4)}
     if not args.no_cpu_baseline:
@@ -186,6 +192,7 @@ def bench_layer_fp32_d768(args, torch, mamba3_amd):
     res["roofline"] = {"bound": "mfma", "achieved": round(tf, 3), "peak": PEAK_FP32_TFLOPS,
                        "unit": "TFLOP/s", "frac": round(tf / PEAK_FP32_TFLOPS, 4),
                        "traffic": traffic.get("layer_fp32"),
+                       "traffic_source": traffic_source(ROOT / "profiles" / "kernel_trace_fp32_layer_d768.md"),
                        "kernel": "native fp32 SSD core (all launches of m3_prefill_fwd: preparation, "
                                  "fp32-MFMA chunk kernels, gate)",
                        "algorithmic_flops": flops, "avg_ms": round(core_ms, 4)}
@@ -271,6 +278,7 @@ def bench_scan(args, torch, shape, name):
     res["unit"] = "GB/s"
     res["roofline"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                        "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic.get(name),
+                       "traffic_source": traffic_source(ROOT / "profiles" / "scan_d768_trace_and_traffic.md"),
                        "kernel": "scan_fwd_vec4", "algorithmic_bytes": nbytes,
                        "avg_ms": round(kern_ms, 4)}
     if not args.no_cpu_baseline:
@@ -314,6 +322,7 @@ def bench_scan_bwd(args, torch, shape, name):
     traffic = recorded_traffic(ROOT / "profiles" / "scan_d768_trace_and_traffic.md", (name,))
     res["roofline"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                        "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic.get(name),
+                       "traffic_source": traffic_source(ROOT / "profiles" / "scan_d768_trace_and_traffic.md"),
                        "kernel": "scan_bwd_vec4 + scan_bwd_reduce", "algorithmic_bytes": nbytes,
                        "avg_ms": round(kern_ms, 4)}
     if not args.no_cpu_baseline:
@@ -385,6 +394,7 @@ def bench_ssd_bwd(args, torch, mamba3_amd):
     res["roofline"] = {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_FP32_TFLOPS,
                        "unit": "TFLOP/s", "frac": round(tflops / PEAK_FP32_TFLOPS, 4),
                        "traffic": traffic.get("ssd_bwd"),
+                       "traffic_source": traffic_source(ROOT / "profiles" / "ssd_bwd_d768_trace_and_traffic.md"),
                        "kernel": "m3_chunked_ssd_bwd, all kernels of one call (fp32 VALU GEMM tiles "
                                  "against the fp32 matrix peak)",
                        "algorithmic_flops": flops, "avg_ms": round(kern_ms, 4)}
@@ -469,6 +479,7 @@ def bench_layer_bwd(args, torch, mamba3_amd):
     res["roofline"] = {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_FP32_TFLOPS,
                        "unit": "TFLOP/s", "frac": round(tflops / PEAK_FP32_TFLOPS, 4),
                        "traffic": traffic.get("layer_bwd"),
+                       "traffic_source": traffic_source(ROOT / "profiles" / "layer_bwd_d768_trace.md"),
                        "kernel": "m3_layer_bwd, all kernels of one call; FLOPs of its chunked-SSD "
                                  "backward GEMMs",
                        "algorithmic_flops": flops, "avg_ms": round(kern_ms, 4)}
@@ -526,12 +537,15 @@ def cpu_baseline(torch, layer_sd, x_cpu, dec_inputs):
     torch.set_num_threads(cores)
     cfg = ref.LayerCfg(d_model=D_MODEL, d_state=N, headdim=P, mimo_rank=R)
     p = {k: v.detach().cpu().to(torch.bfloat16) for k, v in layer_sd.items()}
-    # Prefill: 4 slabs of 2048 tokens (one batch row each) through the reference algorithm.
+    # Prefill: 4 slabs of 2048 tokens (one batch row each) through the reference algorithm,
+    # timed from the in_proj output like the GPU figure (in_proj computed before the timer).
+    with torch.no_grad():
+        projs = [torch.nn.functional.linear(x_cpu[b:b + 1, :2048], p["in_proj.weight"])
+                 for b in range(4)]
     t0 = time.perf_counter()
     ntok = 0
     with torch.no_grad():
-        for b in range(4):
-            proj = torch.nn.functional.linear(x_cpu[b:b + 1, :2048], p["in_proj.weight"])
+        for proj in projs:
             ref.layer_core(cfg, p, proj)
             ntok += 2048
     pre = ntok / (time.perf_counter() - t0)
@@ -555,7 +569,8 @@ def cpu_baseline(torch, layer_sd, x_cpu, dec_inputs):
         "value": round(pre, 1), "unit": "tokens/s", "cores": cores, "kind": "port",
         "sample": "oracle layer core (reference algorithm: factored cumsum, per-token BX, "
                   "torch-loop scan) in bf16 on x[b, :2048] for b<4 of the (8,8192,768) "
-                  "workload, in_proj included, out_proj excluded",
+                  "workload, timed from the in_proj output to the gated activation (the "
+                  "region the GPU value times; in_proj and out_proj excluded)",
         "cpu_model": model,
         "step_decode_tok_s": round(dec, 1),
         "step_decode_sample": "64 reference-algorithm step calls at batch 64, bf16",
@@ -677,6 +692,7 @@ def main() -> int:
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved_tf / PEAK_BF16_TFLOPS, 4),
                      "traffic": traffic.get("prefill"),
+                     "traffic_source": traffic_source(TRAFFIC_FILE),
                      "kernel": "native SSD prefill (all launches of m3_prefill_fwd)",
                      "algorithmic_flops": flops, "avg_ms": round(kern_ms, 4)},
         "whole_layer_prefill_tok_s": round(tokens / (layer_ms * 1e-3), 1),
@@ -690,6 +706,7 @@ def main() -> int:
                          "peak": PEAK_HBM_GBS, "unit": "GB/s",
                          "frac": round(achieved_gbs / PEAK_HBM_GBS, 4),
                          "traffic": traffic.get("step"),
+                         "traffic_source": traffic_source(TRAFFIC_FILE),
                          "algorithmic_bytes": sbytes},
         },
     }

@@ -74,7 +74,9 @@ typedef struct m3_layer_params {
 } m3_layer_params;
 
 /* Gradients of the small per-layer parameters (fp32 device arrays, same shapes as
- * m3_layer_params; written, not accumulated). */
+ * m3_layer_params; written, not accumulated), and of the optional dt_scale input
+ * ([B,T,H] fp32, dt = softplus(dt_raw + dt_bias) * dt_scale, mamba3/mamba3.py:200-202;
+ * NULL when not wanted). */
 typedef struct m3_layer_param_grads {
     float* A_log;
     float* D;
@@ -86,6 +88,7 @@ typedef struct m3_layer_param_grads {
     float* mimo_x;
     float* mimo_z;
     float* mimo_down;
+    float* dt_scale;
 } m3_layer_param_grads;
 
 const char* m3_status_string(int status);

@@ -67,7 +67,7 @@ class LayerParams(ctypes.Structure):
 
 
 class LayerParamGrads(ctypes.Structure):
-    _fields_ = LayerParams._fields_
+    _fields_ = LayerParams._fields_ + [("dt_scale", ctypes.c_void_p)]
 
 
 _lib = None

@@ -16,6 +16,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 from torch.utils.checkpoint import checkpoint as grad_checkpoint
 
+from . import ops
 from .layer import KulaMamba, RMSNorm
 
 
@@ -216,44 +217,59 @@ class KulaMambaLM(nn.Module):
         return torch.cat(out, dim=1)
 
 
+def _block_step_into(block: KulaMambaBlock, x: torch.Tensor, st_in: dict, st_out: dict):
+    """KulaMambaBlock.step (mamba3/block.py:94-100) with the SSM step written into the
+    caller's state buffers `st_out` (which must not alias `st_in`)."""
+    ssm = block.ssm
+    proj = ssm.in_proj(block.ssm_norm(x))
+    y = torch.empty(x.shape[0], ssm.d_inner, device=x.device, dtype=proj.dtype)
+    ops.step_into(proj, *ssm._small_params(), None, st_in["h"], st_in["prev_BX"],
+                  st_in["angle"], y, st_out["h"], st_out["prev_BX"], st_out["angle"],
+                  *ops.layer_args(ssm))
+    x = x + ssm.out_proj(y) * block.residual_scale
+    if block.use_mlp:
+        x = x + block.mlp(block.mlp_norm(x)) * block.residual_scale
+    return x
+
+
 class _DecodeGraph:
-    """One decode step of a KulaMambaLM captured as a HIP graph (torch.cuda.CUDAGraph):
+    """One decode step of a KulaMambaLM captured as HIP graphs (torch.cuda.CUDAGraph):
     token ids -> embedding -> every block's step -> norm -> lm_head logits. The decode
-    state lives in static buffers: each layer's step writes a new state (out of place, as
-    KulaMamba.step does) and the graph copies it back into the buffers it reads, so every
-    replay advances the state by one token. Outputs are bitwise those of the eager step
-    (same kernels, same order)."""
+    state lives in two static buffer sets; graph 0 reads set 0 and writes set 1, graph 1
+    the reverse, and replays alternate between them, so no state is copied. Outputs are
+    bitwise those of the eager step (same kernels, same order)."""
 
     def __init__(self, lm: KulaMambaLM, states: list, batch: int):
         dev = lm.embedding.weight.device
         self.tok = torch.zeros(batch, dtype=torch.long, device=dev)
-        self.states = [{k: v.clone() for k, v in st.items()} for st in states]
-        snapshot = [{k: v.clone() for k, v in st.items()} for st in self.states]
+        self.bufs = [[{k: v.clone() for k, v in st.items()} for st in states],
+                     [{k: torch.empty_like(v) for k, v in st.items()} for st in states]]
 
-        def step():
+        def step(src: int):
             x = lm.embedding(self.tok)
-            for i, layer in enumerate(lm.layers):
-                x, new = layer.step(x, self.states[i])
-                for k in ("h", "prev_BX", "angle"):
-                    self.states[i][k].copy_(new[k])
+            for i, block in enumerate(lm.layers):
+                x = _block_step_into(block, x, self.bufs[src][i], self.bufs[1 - src][i])
             return lm.lm_head(lm.norm(x))
 
-        # Warm up outside the capture on a side stream (allocator and library handles),
-        # then restore the state the warm-up advanced.
+        # Warm up outside the capture on a side stream (allocator and library handles);
+        # it reads set 0 and writes set 1, which the first replay rewrites.
         side = torch.cuda.Stream(device=dev)
         side.wait_stream(torch.cuda.current_stream(dev))
         with torch.cuda.stream(side):
-            step()
+            step(0)
         torch.cuda.current_stream(dev).wait_stream(side)
-        for st, sv in zip(self.states, snapshot):
-            for k in st:
-                st[k].copy_(sv[k])
-        self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
-            self.logits = step()
+        self.graphs, self.logits = [], []
+        for src in (0, 1):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                self.logits.append(step(src))
+            self.graphs.append(g)
         torch.cuda.synchronize(dev)
+        self.phase = 0
 
     def __call__(self, tok: torch.Tensor) -> torch.Tensor:
         self.tok.copy_(tok)
-        self.graph.replay()
-        return self.logits
+        self.graphs[self.phase].replay()
+        out = self.logits[self.phase]
+        self.phase ^= 1
+        return out

@@ -23,7 +23,8 @@
 //             of the group, dL/dphi = sum_r (g_o' e' - g_e' o') over B and C, the RMSNorm
 //             backward g_v = rho w g - v rho^3 sum(w g v) / (N R), partials of dL/dw, dL/dbias
 //   tb_asum, tb_angle   Phi_t = sum_{t'>=t} dL/dphi_t' (+ dL/dangle), in chunks of 64 tokens
-//   tb_tok    dL/dtheta_t = -sum_h dt Phi_t, dL/du = s sigmoid(u) (g_dt + -sum_i theta Phi)
+//   tb_tok    dL/dtheta_t = -sum_h dt Phi_t, dL/du = s sigmoid(u) (g_dt + -sum_i theta Phi),
+//             dL/ds = softplus(u) (g_dt + -sum_i theta Phi) when dt_scale is differentiated
 //   tb_colsum, tb_finish   the parameter gradients from the partials, in a fixed order
 // Every reduction runs in a fixed order: results are deterministic.
 #include <hip/hip_runtime.h>
@@ -31,6 +32,7 @@
 #include <algorithm>
 #include <initializer_list>
 
+#include "m3_common.h"
 #include "m3_kernels.h"
 
 namespace m3 {
@@ -509,6 +511,8 @@ __global__ __launch_bounds__(NTH) void tb_tok(Args a) {
         const float gu = g * (a.dt_scale ? a.dt_scale[th] : 1.f) * sigm(u);
         a.gproj[tok * a.rs + a.pl.dt + h] = gu;
         a.p_dtb[th] = gu;
+        // dt = softplus(u) s: dL/ds = dL/ddt softplus(u)
+        if (a.out.dt_scale) a.out.dt_scale[th] = g * softplus_f(u);
     }
 }
 

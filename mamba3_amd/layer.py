@@ -18,7 +18,7 @@ import math
 import torch
 import torch.nn as nn
 
-from . import _native
+from . import _native, ops
 
 
 class RMSNorm(nn.Module):
@@ -39,71 +39,6 @@ class RMSNorm(nn.Module):
         shape = [1] * x.ndim
         shape[self.dim] = -1
         return x * scale.to(x.dtype) * self.weight.view(*shape)
-
-
-class _ForwardOnly(torch.autograd.Function):
-    """Ties a decode-step output to its input so that backward raises instead of silently
-    producing wrong gradients (the step kernel has no backward)."""
-
-    @staticmethod
-    def forward(ctx, anchor, out):
-        return out
-
-    @staticmethod
-    def backward(ctx, grad):
-        raise NotImplementedError(
-            "KulaMamba.step has no backward in mamba3_amd; train through forward / prefill")
-
-
-class _LayerTrainFn(torch.autograd.Function):
-    """Differentiable ssd_from_proj on HIP kernels in both directions: the forward is the fp32
-    layer prefill (m3_prefill_fwd on an fp32 desc), whose workspace keeps its intermediates
-    for the backward, m3_layer_bwd (gate, chunked SSD and preparation backward). bf16
-    inputs and parameters are computed in fp32; gradients come back in their dtypes."""
-
-    @staticmethod
-    def forward(ctx, layer, proj, dt_scale, return_state, *params):
-        Bat, T, _ = proj.shape
-        H, P, N = layer.nheads, layer.headdim, layer.d_state
-        dev = proj.device
-        proj32 = proj.detach().float().contiguous()
-        p32 = [t.detach().float().contiguous() for t in params]
-        desc = layer._desc(Bat, T, proj32)
-        pack = _native.LayerParams(*[t.data_ptr() for t in p32])
-        scale = layer._dt_scale(dt_scale, (Bat, T, H), dev)
-        ws_bytes = _native.prefill_workspace_bytes(desc)
-        ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
-        y = torch.empty(Bat, T, layer.d_inner, device=dev, dtype=torch.float32)
-        h_final = angle = prev_bx = None
-        if return_state:
-            h_final = torch.empty(Bat, H, P, N, device=dev, dtype=torch.float32)
-            angle = torch.empty(Bat, H, N // 2, device=dev, dtype=torch.float32)
-            prev_bx = torch.empty(Bat, H, P, N, device=dev, dtype=torch.float32)
-        _native.prefill_fwd(desc, pack, proj32, scale, y, h_final, angle, prev_bx, ws, ws_bytes)
-        ctx.save_for_backward(proj32, ws, scale, *p32)
-        ctx.desc = desc
-        ctx.proj_dtype = proj.dtype
-        ctx.param_dtypes = [t.dtype for t in params]
-        ctx.set_materialize_grads(False)
-        return y.to(proj.dtype), h_final, angle, prev_bx
-
-    @staticmethod
-    def backward(ctx, g_y, g_h, g_angle, g_prev):
-        proj32, ws, scale, *p32 = ctx.saved_tensors
-        if g_y is None:
-            g_y = torch.zeros(proj32.shape[0], proj32.shape[1], ctx.desc.nheads * ctx.desc.headdim,
-                              device=proj32.device)
-
-        def f32(t):
-            return None if t is None else t.float().contiguous()
-
-        g_proj = torch.empty_like(proj32)
-        grads = [torch.empty_like(t) for t in p32]
-        _native.layer_bwd(ctx.desc, _native.LayerParams(*[t.data_ptr() for t in p32]), proj32,
-                          scale, ws, f32(g_y), f32(g_h), f32(g_angle), f32(g_prev), g_proj,
-                          _native.LayerParamGrads(*[t.data_ptr() for t in grads]))
-        return (None, g_proj.to(ctx.proj_dtype), None, None,
-                *[g.to(dt) for g, dt in zip(grads, ctx.param_dtypes)])
 
 
 class KulaMamba(nn.Module):
@@ -186,16 +121,8 @@ class KulaMamba(nn.Module):
                 self.B_bias, self.C_bias, self.mimo_x, self.mimo_z, self.mimo_down)
 
     def _param_pack(self) -> _native.LayerParams:
-        """fp32 contiguous copies of the small parameters, rebuilt when any changes."""
-        tensors = self._small_params()
-        key = tuple((t.data_ptr(), t._version, t.dtype, t.device) for t in tensors)
-        if key != self._pack_key:
-            with torch.no_grad():
-                f32 = [t.detach().float().contiguous() for t in tensors]
-            pack = _native.LayerParams(*[t.data_ptr() for t in f32])
-            self._pack = (pack, f32)
-            self._pack_key = key
-        return self._pack[0]
+        """fp32 copies of the small parameters as the C-ABI struct (cached per version)."""
+        return ops._f32_params(self._small_params())[0]
 
     def _desc(self, batch: int, seqlen: int, proj: torch.Tensor) -> _native.LayerDesc:
         return _native.LayerDesc(
@@ -230,108 +157,24 @@ class KulaMamba(nn.Module):
 
     def ssd_from_proj(self, proj: torch.Tensor, dt_scale=None, return_state: bool = False):
         """Everything between in_proj and out_proj (mamba3/mamba3.py:199-256) on the HIP
-        kernels: proj (B,T,d_in_proj) -> (y (B,T,d_inner) in proj.dtype, state or None)."""
+        kernels: proj (B,T,d_in_proj) -> (y (B,T,d_inner) in proj.dtype, state or None).
+
+        With autograd recording (proj, a parameter or dt_scale requires grad) this is the
+        differentiable `prefill_train` op: fp32 arithmetic on the fp32 layer path, whose
+        backward is m3_layer_bwd. Shapes m3_layer_bwd does not cover raise there."""
         _native.require_gpu(proj)
         self._check_norm_eps()
+        Bat, T, _ = proj.shape
+        scale = self._dt_scale(dt_scale, (Bat, T, self.nheads), proj.device)
+        params = self._small_params()
+        args = ops.layer_args(self)
         if torch.is_grad_enabled() and (proj.requires_grad or
-                                        any(p.requires_grad for p in self._small_params())):
-            Bat, T, _ = proj.shape
-            desc32 = self._desc(Bat, T, proj.detach().float())
-            if _native.layer_bwd_supported(desc32):
-                y, h, angle, prev = _LayerTrainFn.apply(self, proj, dt_scale, return_state,
-                                                        *self._small_params())
-                state = {"h": h, "angle": angle, "prev_BX": prev} if return_state else None
-                return y, state
-            return self._ssd_train(proj, dt_scale, return_state)
-        proj = proj.contiguous()
-        Bat, T, _ = proj.shape
-        H, P, N = self.nheads, self.headdim, self.d_state
-        desc = self._desc(Bat, T, proj)
-        params = self._param_pack()
-        scale = self._dt_scale(dt_scale, (Bat, T, H), proj.device)
-
-        dev = proj.device
-        y = torch.empty(Bat, T, self.d_inner, device=dev, dtype=proj.dtype)
-        h_final = angle = prev_bx = None
-        if return_state:
-            h_final = torch.empty(Bat, H, P, N, device=dev, dtype=torch.float32)
-            angle = torch.empty(Bat, H, N // 2, device=dev, dtype=torch.float32)
-            prev_bx = torch.empty(Bat, H, P, N, device=dev, dtype=torch.float32)
-        ws_bytes = _native.prefill_workspace_bytes(desc)
-        workspace = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
-        _native.prefill_fwd(desc, params, proj, scale, y, h_final, angle, prev_bx, workspace,
-                            ws_bytes)
-        state = None
-        if return_state:
-            state = {"h": h_final, "angle": angle, "prev_BX": prev_bx}
-        return y, state
-
-    def _ssd_train(self, proj: torch.Tensor, dt_scale=None, return_state: bool = False):
-        """Differentiable form of ssd_from_proj for the shapes m3_layer_bwd does not cover
-        (its per-token LDS would exceed 64 KB): the reference's element-wise preparation and
-        gate (mamba3/mamba3.py:142-166, 197-239) as PyTorch ops in fp32 around chunked_ssd,
-        whose forward and backward run on the HIP kernels (m3_chunked_ssd_fwd /
-        m3_chunked_ssd_bwd). The state it returns matches the fused path's (fp32 h, angle
-        and prev_BX; mamba3/mamba3.py:241-256)."""
-        from .ssd import chunked_ssd
-
-        Bat, T, _ = proj.shape
-        H, P, N, R, G = self.nheads, self.headdim, self.d_state, self.mimo_rank, self.ngroups
-        sizes = [self.d_inner, self._d_x, self._d_bc, self._d_bc, H]
-        sizes += [H] if self.use_trapezoidal else []
-        sizes += [N // 2] if self.use_complex_ssm else []
-        parts = list(proj.float().split(sizes, dim=-1))
-        z, x_flat, B_flat, C_flat, dt_raw = parts[:5]
-        lam_raw = parts[5] if self.use_trapezoidal else None
-        theta_raw = parts[-1] if self.use_complex_ssm else None
-
-        dt = nn.functional.softplus(dt_raw + self.dt_bias.float())
-        if dt_scale is not None:
-            dt = dt * self._dt_scale(dt_scale, (Bat, T, H), proj.device)
-        A = -torch.exp(self.A_log.float())
-        dA = torch.exp(A * dt)
-
-        def norm_bias(flat, norm, bias):
-            v = norm(flat.reshape(Bat, T, G, N * R)).float().reshape(Bat, T, G, N, R)
-            v = v + bias.float()
-            return v.repeat_interleave(H // G, dim=2) if G != H else v
-
-        B_r = norm_bias(B_flat, self.B_norm, self.B_bias)
-        C_r = norm_bias(C_flat, self.C_norm, self.C_bias)
-        angles = None
-        if self.use_complex_ssm:
-            angles = -(dt.unsqueeze(-1) * theta_raw.unsqueeze(-2)).cumsum(dim=1)  # (B,T,H,N/2)
-            cos = torch.cos(angles)[..., None, None]
-            sin = torch.sin(angles)[..., None, None]
-
-            def rope(v):
-                v = v.reshape(Bat, T, H, N // 2, 2, R)
-                ev, od = v[..., 0:1, :], v[..., 1:2, :]
-                return torch.cat([ev * cos - od * sin, ev * sin + od * cos], dim=-2).reshape(
-                    Bat, T, H, N, R)
-
-            B_r, C_r = rope(B_r), rope(C_r)
-
-        x_r = x_flat.reshape(Bat, T, H, P, 1) * self.mimo_x.float()
-        if self.use_trapezoidal:
-            lam = torch.sigmoid(lam_raw)
-            x_g = x_r * lam[..., None, None]
-            x_b = nn.functional.pad(x_r[:, :-1], (0, 0, 0, 0, 0, 0, 1, 0)) * \
-                ((1.0 - lam) * dA)[..., None, None]
-            B_b = nn.functional.pad(B_r[:, :-1], (0, 0, 0, 0, 0, 0, 1, 0))
+                                        (scale is not None and scale.requires_grad) or
+                                        any(p.requires_grad for p in params)):
+            y, h, angle, prev, _ = ops.prefill_train(proj, *params, scale, *args)
         else:
-            x_g, x_b, B_b = x_r, None, None
-        out = chunked_ssd(x_g, x_b, B_r, B_b, C_r, dt, A, self.D.float(), x_r,
-                          self.chunk_size, return_final_state=return_state)
-        z_r = z.reshape(Bat, T, H, P, 1) * self.mimo_z.float()
-        y = (out.y * nn.functional.silu(z_r) * self.mimo_down.float()).sum(dim=-1)
-        y = y.reshape(Bat, T, self.d_inner).to(proj.dtype)
-        state = None
-        if return_state:
-            angle = angles[:, T - 1] if angles is not None else \
-                torch.zeros(Bat, H, N // 2, device=proj.device, dtype=torch.float32)
-            prev_bx = torch.einsum("bhnr,bhpr->bhpn", B_r[:, T - 1], x_r[:, T - 1])
-            state = {"h": out.h_final, "angle": angle, "prev_BX": prev_bx}
+            y, h, angle, prev = ops.prefill(proj, *params, scale, *args, return_state)
+        state = {"h": h, "angle": angle, "prev_BX": prev} if return_state else None
         return y, state
 
     def forward(self, x: torch.Tensor, dt_scale=None) -> torch.Tensor:
@@ -344,49 +187,33 @@ class KulaMamba(nn.Module):
 
     def step(self, hidden_states: torch.Tensor, ssm_state: dict, dt_scale=None):
         """One decode step (mamba3/mamba3.py:267-322). `hidden_states` is (B, d_model)
-        or (B, 1, d_model); the output has the same rank. Returns a new state dict."""
+        or (B, 1, d_model); the output has the same rank. Returns a new state dict. The
+        step kernel has no backward: backward through its output raises."""
         squeeze = hidden_states.dim() == 2
         x_in = hidden_states if squeeze else hidden_states.squeeze(1)
         if x_in.dim() != 2:
             raise ValueError(f"expected (B, d_model) or (B, 1, d_model), got {tuple(hidden_states.shape)}")
         _native.require_gpu(x_in)
         self._check_norm_eps()
-        Bat = x_in.shape[0]
-        H, P, N = self.nheads, self.headdim, self.d_state
-
-        proj = self.in_proj(x_in).contiguous()
-        desc = self._desc(Bat, 1, proj)
-        params = self._param_pack()
-        scale = self._dt_scale(dt_scale, (Bat, H), x_in.device)
-
-        h_in = ssm_state["h"]
-        prev_in = ssm_state["prev_BX"]
-        angle_in = ssm_state["angle"]
-        for name, t, shape in (("h", h_in, (Bat, H, P, N)), ("prev_BX", prev_in, (Bat, H, P, N)),
-                               ("angle", angle_in, (Bat, H, N // 2))):
-            if tuple(t.shape) != shape:
-                raise ValueError(f"state['{name}'] has shape {tuple(t.shape)}, expected {shape}")
-        _native.require_gpu(h_in, prev_in, angle_in)
-        h_in = h_in.float().contiguous()
-        prev_in = prev_in.float().contiguous()
-        if angle_in.dtype not in (torch.float32, torch.bfloat16):
-            angle_in = angle_in.float()
-        angle_in = angle_in.contiguous()
-
-        dev = x_in.device
-        y = torch.empty(Bat, self.d_inner, device=dev, dtype=proj.dtype)
-        h_out = torch.empty_like(h_in)
-        prev_out = torch.empty_like(prev_in)
-        angle_out = torch.empty_like(angle_in)
-        _native.step_fwd(desc, params, proj, scale, h_in, prev_in, angle_in, y, h_out,
-                         prev_out, angle_out)
-        if torch.is_grad_enabled() and (proj.requires_grad or
-                                        any(p.requires_grad for p in self._small_params())):
-            y = _ForwardOnly.apply(proj, y)
+        h_in, prev_in, angle_in = self._check_state(ssm_state, x_in.shape[0])
+        proj = self.in_proj(x_in)
+        scale = self._dt_scale(dt_scale, (x_in.shape[0], self.nheads), x_in.device)
+        y, h_out, prev_out, angle_out = ops.step(proj, *self._small_params(), scale, h_in,
+                                                 prev_in, angle_in, *ops.layer_args(self))
         out = self.out_proj(y)
         if not squeeze:
             out = out.unsqueeze(1)
         return out, {"h": h_out, "angle": angle_out, "prev_BX": prev_out}
+
+    def _check_state(self, ssm_state: dict, batch: int):
+        H, P, N = self.nheads, self.headdim, self.d_state
+        h_in, prev_in, angle_in = ssm_state["h"], ssm_state["prev_BX"], ssm_state["angle"]
+        for name, t, shape in (("h", h_in, (batch, H, P, N)), ("prev_BX", prev_in, (batch, H, P, N)),
+                               ("angle", angle_in, (batch, H, N // 2))):
+            if tuple(t.shape) != shape:
+                raise ValueError(f"state['{name}'] has shape {tuple(t.shape)}, expected {shape}")
+        _native.require_gpu(h_in, prev_in, angle_in)
+        return h_in, prev_in, angle_in
 
     def allocate_inference_state(self, batch_size: int, dtype=None, device=None) -> dict:
         """Zero decode state (mamba3/mamba3.py:324-332). 'h' and 'prev_BX' are fp32 as in

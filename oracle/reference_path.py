@@ -6,6 +6,8 @@ oracle and as the timed "reference CPU path":
   * chunked SSD        mamba3/ssd.py:118-244 (factored cumsum, ssd.py:30-65)
   * inter-chunk scan   mamba3/scan.py:34-44
   * decode step        mamba3/mamba3.py:170-190, 267-322
+  * block / LM glue    mamba3/block.py:16-26, 79-107, 178-231 (forward, prefill, step,
+                       greedy generate)
 Parameters are passed as a plain dict keyed by the reference's state_dict names, so the
 oracle never touches the product modules.
 """
@@ -277,7 +279,11 @@ def layer_step(cfg: LayerCfg, p: dict, x_tok: torch.Tensor, state: dict, dt_scal
     angle = state["angle"]
     if cfg.use_complex_ssm:
         angle = angle - dt.unsqueeze(-1) * theta.unsqueeze(-2)
-        c, s = torch.cos(angle).unsqueeze(-1), torch.sin(angle).unsqueeze(-1)
+        # cos / sin in the activation dtype: the reference's angle is in that dtype
+        # (mamba3/mamba3.py:330), so this is its arithmetic; an fp32 angle state (kept by
+        # mamba3_amd) then rotates bf16 activations in bf16 as well
+        c = torch.cos(angle).to(Bt.dtype).unsqueeze(-1)
+        s = torch.sin(angle).to(Bt.dtype).unsqueeze(-1)
         Bt, Ct = rope_pairs(Bt, c, s), rope_pairs(Ct, c, s)
 
     x_r = xf.reshape(Bat, H, P, 1) * p["mimo_x"][None]
@@ -297,15 +303,87 @@ def layer_step(cfg: LayerCfg, p: dict, x_tok: torch.Tensor, state: dict, dt_scal
     return out, {"h": h, "angle": angle, "prev_BX": cur.float()}
 
 
+def _block_sub(p: dict, prefix: str) -> dict:
+    """Parameters of block `prefix`'s KulaMamba, under the layer's own names."""
+    return {k[len(prefix) + 4:]: v for k, v in p.items() if k.startswith(prefix + "ssm.")}
+
+
+def _swiglu(p: dict, prefix: str, xn: torch.Tensor) -> torch.Tensor:
+    """mamba3/block.py:16-26: w_down(silu(w_gate x) * w_up x)."""
+    g = F.linear(xn, p[prefix + "mlp.w_gate.weight"], p.get(prefix + "mlp.w_gate.bias"))
+    u = F.linear(xn, p[prefix + "mlp.w_up.weight"], p.get(prefix + "mlp.w_up.bias"))
+    return F.linear(F.silu(g) * u, p[prefix + "mlp.w_down.weight"], p.get(prefix + "mlp.w_down.bias"))
+
+
 def block_forward(cfg: LayerCfg, p: dict, prefix: str, x: torch.Tensor, scale: float,
-                  use_mlp: bool, norm_eps: float = 1e-5) -> torch.Tensor:
-    """mamba3/block.py:79-92 (no checkpointing) with parameters under `prefix`."""
-    sub = {k[len(prefix) + 4:]: v for k, v in p.items() if k.startswith(prefix + "ssm.")}
-    h, _ = layer_forward(cfg, sub, rmsnorm(x, p[prefix + "ssm_norm.weight"], norm_eps))
+                  use_mlp: bool, norm_eps: float = 1e-5, return_state: bool = False):
+    """mamba3/block.py:79-92 (no checkpointing) with parameters under `prefix`; with
+    return_state, mamba3/block.py:102-107 (prefill) and returns (x, state)."""
+    h, state = layer_forward(cfg, _block_sub(p, prefix),
+                             rmsnorm(x, p[prefix + "ssm_norm.weight"], norm_eps),
+                             return_state=return_state)
     x = x + h * scale
     if use_mlp:
-        xn = rmsnorm(x, p[prefix + "mlp_norm.weight"], norm_eps)
-        g = F.linear(xn, p[prefix + "mlp.w_gate.weight"])
-        u = F.linear(xn, p[prefix + "mlp.w_up.weight"])
-        x = x + F.linear(F.silu(g) * u, p[prefix + "mlp.w_down.weight"]) * scale
-    return x
+        x = x + _swiglu(p, prefix, rmsnorm(x, p[prefix + "mlp_norm.weight"], norm_eps)) * scale
+    return (x, state) if return_state else x
+
+
+def block_step(cfg: LayerCfg, p: dict, prefix: str, x: torch.Tensor, state: dict, scale: float,
+               use_mlp: bool, norm_eps: float = 1e-5):
+    """mamba3/block.py:94-100: one decode token (B, d_model) through block `prefix`."""
+    h, state = layer_step(cfg, _block_sub(p, prefix),
+                          rmsnorm(x, p[prefix + "ssm_norm.weight"], norm_eps), state)
+    x = x + h * scale
+    if use_mlp:
+        x = x + _swiglu(p, prefix, rmsnorm(x, p[prefix + "mlp_norm.weight"], norm_eps)) * scale
+    return x, state
+
+
+def lm_head(p: dict, x: torch.Tensor, norm_eps: float = 1e-5) -> torch.Tensor:
+    """mamba3/block.py:182-183: final RMSNorm, then the (tied) lm_head."""
+    return F.linear(rmsnorm(x, p["norm.weight"], norm_eps), p["lm_head.weight"])
+
+
+def lm_forward(cfg: LayerCfg, p: dict, ids: torch.Tensor, n_layers: int, scale: float,
+               use_mlp: bool = True, norm_eps: float = 1e-5) -> torch.Tensor:
+    """mamba3/block.py:178-184: embedding, n_layers blocks, norm, lm_head -> logits."""
+    x = F.embedding(ids, p["embedding.weight"])
+    for i in range(n_layers):
+        x = block_forward(cfg, p, f"layers.{i}.", x, scale, use_mlp, norm_eps)
+    return lm_head(p, x, norm_eps)
+
+
+def lm_prefill(cfg: LayerCfg, p: dict, ids: torch.Tensor, n_layers: int, scale: float,
+               use_mlp: bool = True, norm_eps: float = 1e-5):
+    """mamba3/block.py:199-206: prefill every block; returns (last-token logits, states)."""
+    x = F.embedding(ids, p["embedding.weight"])
+    states = []
+    for i in range(n_layers):
+        x, st = block_forward(cfg, p, f"layers.{i}.", x, scale, use_mlp, norm_eps,
+                              return_state=True)
+        states.append(st)
+    return lm_head(p, x[:, -1], norm_eps), states
+
+
+def lm_step(cfg: LayerCfg, p: dict, tok: torch.Tensor, states: list, scale: float,
+            use_mlp: bool = True, norm_eps: float = 1e-5):
+    """mamba3/block.py:226-229: one token id per row through every block's step; returns
+    (logits, new states)."""
+    x = F.embedding(tok, p["embedding.weight"])
+    new = []
+    for i, st in enumerate(states):
+        x, st = block_step(cfg, p, f"layers.{i}.", x, st, scale, use_mlp, norm_eps)
+        new.append(st)
+    return lm_head(p, x, norm_eps), new
+
+
+def lm_generate_greedy(cfg: LayerCfg, p: dict, ids: torch.Tensor, n_layers: int, scale: float,
+                       max_new_tokens: int, use_mlp: bool = True, norm_eps: float = 1e-5):
+    """mamba3/block.py:195-231 at temperature 0 (argmax, no top-k)."""
+    logits, states = lm_prefill(cfg, p, ids, n_layers, scale, use_mlp, norm_eps)
+    out = [ids]
+    for _ in range(max_new_tokens):
+        nxt = logits.argmax(dim=-1, keepdim=True)
+        out.append(nxt)
+        logits, states = lm_step(cfg, p, nxt.squeeze(1), states, scale, use_mlp, norm_eps)
+    return torch.cat(out, dim=1)

@@ -206,3 +206,29 @@ def test_chunked_fwd_workspace_query(lib):
     assert n.value == 0
     assert lib.m3_chunked_ssd_fwd_workspace_size(4, 1024, 24, 64, 128, 2, 0, 2, ctypes.byref(n)) == 2
     assert lib.m3_chunked_ssd_fwd_workspace_size(4, 1024, 24, 64, 128, 2, 7, 1, ctypes.byref(n)) == 3
+
+
+def test_custom_op_fake_kernels_give_output_shapes():
+    """The ops' fake kernels (used by torch.compile) on meta tensors, no GPU needed."""
+    import torch
+    import mamba3_amd  # noqa: F401  (registers the ops)
+    from mamba3_amd import ops
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    torch.manual_seed(0)
+    layer = mamba3_amd.KulaMamba(d_model=64, d_state=16, headdim=16, mimo_rank=2)
+    real = [p.detach() for p in layer._small_params()]
+    proj_real = torch.empty(2, 9, layer.in_proj.out_features)
+    with FakeTensorMode() as mode:
+        proj = mode.from_tensor(proj_real)
+        params = [mode.from_tensor(p) for p in real]
+        y, h, a, pb = torch.ops.mamba3_amd.prefill(proj, *params, None, *ops.layer_args(layer), True)
+        assert y.shape == (2, 9, layer.d_inner) and h.shape == (2, layer.nheads, 16, 16)
+        assert a.shape == (2, layer.nheads, 8) and pb.shape == h.shape
+        y, h, a, pb, ws = torch.ops.mamba3_amd.prefill_train(proj, *params, None,
+                                                            *ops.layer_args(layer))
+        assert ws.dtype == torch.uint8 and ws.numel() > 1
+        st = torch.ops.mamba3_amd.step(proj[:, 0], *params, None, h, pb, a, *ops.layer_args(layer))
+        assert st[0].shape == (2, layer.d_inner) and st[1].shape == h.shape
+        out = torch.ops.mamba3_amd.scan_fwd(mode.from_tensor(torch.empty(2, 3, 4)),
+                                            mode.from_tensor(torch.empty(2, 3, 4, 10)), None)
+        assert out.shape == (2, 3, 4, 10)

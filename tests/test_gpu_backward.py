@@ -143,16 +143,19 @@ def _oracle_layer_grads(kw, layer, x, w, wh, dt_scale=None):
     params = {k: v.detach().double().cpu().clone().requires_grad_()
               for k, v in layer.state_dict().items()}
     xr = x.detach().double().cpu().clone().requires_grad_()
-    ds = None if dt_scale is None else dt_scale.double().cpu()
+    ds = None if dt_scale is None else dt_scale.double().cpu().clone().requires_grad_()
     out, st = ref.layer_forward(oracle_cfg(kw), params, xr, dt_scale=ds, return_state=True)
     ((out * w.double().cpu()).sum() + (st["h"] * wh.double().cpu()).sum()).backward()
-    return out, {k: v.grad for k, v in params.items()}, xr.grad
+    grads = {k: v.grad for k, v in params.items()}
+    if ds is not None:
+        grads["dt_scale"] = ds.grad
+    return out, grads, xr.grad
 
 
 @pytest.mark.parametrize("kw", LAYER_KW, ids=lambda k: "-".join(f"{a}{b}" for a, b in k.items()))
 def test_layer_prefill_gradients_match_oracle(kw, cuda_device):
-    """Autograd through KulaMamba.prefill (torch element-wise prep in fp32 around the HIP
-    chunked_ssd forward and backward) against autograd through the fp64 oracle layer
+    """Autograd through KulaMamba.prefill (the fp32 layer path forward, m3_layer_bwd
+    backward) against autograd through the fp64 oracle layer
     (mamba3/mamba3.py:192-258), for every parameter and the input; the loss also reads the
     returned state h."""
     print(f"layer backward {kw}", flush=True)
@@ -235,25 +238,20 @@ def test_layer_training_runs_on_the_native_backward(cuda_device):
         assert _native.layer_bwd_supported(layer._desc(1, 8, proj)), kw
 
 
-def test_layer_torch_preparation_fallback_matches_oracle(cuda_device, monkeypatch):
-    """Shapes m3_layer_bwd does not cover train through the PyTorch preparation around the
-    HIP chunked_ssd forward and backward; forced here on a small layer."""
+def test_layer_training_outside_the_native_backward_raises(cuda_device):
+    """Shapes m3_layer_bwd does not cover (here rank 3) raise a clear error when trained,
+    rather than falling back to another implementation; without gradients the same layer
+    runs (on the generic prefill kernel)."""
     from mamba3_amd import _native
-    monkeypatch.setattr(_native, "layer_bwd_supported", lambda desc: False)
-    kw = dict(d_model=64, d_state=16, headdim=16, mimo_rank=2)
+    kw = dict(d_model=64, d_state=16, headdim=16, mimo_rank=3)
     torch.manual_seed(0)
     layer = mamba3_amd.KulaMamba(**kw).to(cuda_device).train()
-    g = torch.Generator().manual_seed(8)
-    x = torch.randn(2, 40, 64, generator=g)
-    w = torch.randn(2, 40, 64, generator=g)
-    wh = torch.randn(2, layer.nheads, 16, 16, generator=g)
-    out_ref, pg, xg_ref = _oracle_layer_grads(kw, layer, x, w, wh)
-    xd = x.to(cuda_device).requires_grad_()
-    out, st = layer.prefill(xd)
-    ((out * w.to(cuda_device)).sum() + (st["h"] * wh.to(cuda_device)).sum()).backward()
-    assert max_rel(xd.grad, xg_ref) < FP32_TOL
-    for name, p in layer.named_parameters():
-        assert max_rel(p.grad, pg[name]) < FP32_TOL, name
+    x = torch.randn(2, 40, 64, device=cuda_device)
+    with pytest.raises(_native.NativeError, match="not supported by m3_layer_bwd"):
+        layer(x.requires_grad_())
+    with torch.no_grad():
+        y = layer(x)
+    assert torch.isfinite(y).all()
 
 
 def test_layer_forward_gradients_with_dt_scale(cuda_device):
@@ -267,10 +265,12 @@ def test_layer_forward_gradients_with_dt_scale(cuda_device):
     wh = torch.zeros(1, layer.nheads, 16, 16)
     out_ref, pg, xg_ref = _oracle_layer_grads(kw, layer, x, w, wh, dt_scale=ds)
     xd = x.to(cuda_device).requires_grad_()
-    out = layer(xd, dt_scale=ds.to(cuda_device))
+    dsd = ds.to(cuda_device).requires_grad_()
+    out = layer(xd, dt_scale=dsd)
     (out * w.to(cuda_device)).sum().backward()
     assert max_rel(out, out_ref) < FP32_TOL
     assert max_rel(xd.grad, xg_ref) < FP32_TOL
+    assert max_rel(dsd.grad, pg["dt_scale"]) < FP32_TOL
     for name, p in layer.named_parameters():
         assert max_rel(p.grad, pg[name]) < FP32_TOL, name
 
@@ -335,5 +335,5 @@ def test_step_backward_raises_instead_of_wrong_gradients(cuda_device):
     layer = mamba3_amd.KulaMamba(64, d_state=16, headdim=16).to(cuda_device).train()
     st = layer.allocate_inference_state(1)
     out, _ = layer.step(torch.randn(1, 64, device=cuda_device), st)
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(RuntimeError, match="mamba3_amd.step"):
         out.sum().backward()

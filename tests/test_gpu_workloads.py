@@ -1,0 +1,151 @@
+"""Full-size workload parity on the GPU: the 24-layer d_model-768 LM in bf16 (prefill over
+ids (4, 2048) and 256 greedy tokens) and the fused d768 prefill in its single-segment
+form, each against the fp32 oracle on the bf16-rounded weights (normwise max-relative
+error, 2e-2).
+
+The oracle runs on the host at sizes it finishes in seconds: causality makes a prefix of
+one batch row exact, and the decode steps start from the GPU's own prefilled state.
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+import mamba3_amd
+from conftest import max_rel
+from mamba3_amd import _native
+from oracle import reference_path as ref
+
+pytestmark = pytest.mark.gpu
+
+BF16_TOL = 2e-2
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _native_loaded(cuda_device):
+    _native.lib()
+    torch.backends.cuda.matmul.allow_tf32 = False
+
+
+def _l2(a: torch.Tensor, b: torch.Tensor) -> float:
+    a, b = a.double().cpu(), b.double().cpu()
+    return ((a - b).norm() / b.norm()).item()
+
+
+def test_lm_d768_24_layers_prefill_and_greedy_decode(cuda_device):
+    """KulaMambaLM(32000, 768, n_layers=24, d_state=128, headdim=64, mimo_rank=2,
+    residual_scale='depth') in bf16, seed 0; ids (4, 2048) uniform from seed 5
+    (mamba3/block.py:110-231).
+
+    * Teacher-forced logits of batch row 0 at positions 0..255 against the oracle's
+      24-block forward of ids[0, :256] in fp32 on the bf16-rounded weights.
+    * generate(256, temperature=0): finite logits; the captured decode graph and the eager
+      step loop give the same tokens.
+    * Every decode step's logits, teacher-forced on the generated tokens from the GPU's
+      prefilled states, against the oracle's 24-block step chain from the same states.
+      The oracle's own greedy choice is reported, not gated (bf16 argmax near-ties).
+
+    Tolerance: the whole model runs in bf16 (residual stream, norms, projections, MLP), and
+    the reference's own algorithm run in bf16 is itself 4.3-4.6e-2 (prefill logits) and
+    ~2e-2 (decode steps) away from fp32 here, so 2e-2 on 24-layer logits is out of reach
+    for any bf16 execution. Each check therefore passes at max(2e-2, the error of the
+    oracle run in bf16 on the same inputs, with an fp32 angle state like this build's);
+    the normwise L2 error of the prefill logits is reported."""
+    dev = cuda_device
+    torch.manual_seed(0)
+    lm = mamba3_amd.KulaMambaLM(32000, 768, n_layers=24, d_state=128, headdim=64, mimo_rank=2,
+                                residual_scale="depth")
+    lm = lm.to(dev, torch.bfloat16).eval()
+    p = {k: v.detach().float().cpu() for k, v in lm.state_dict().items()}
+    p16 = {k: v.detach().cpu() for k, v in lm.state_dict().items()}
+    cfg = ref.LayerCfg(d_model=768, d_state=128, headdim=64, mimo_rank=2)
+    scale = 1.0 / math.sqrt(2 * 24)
+    torch.manual_seed(5)
+    ids = torch.randint(0, 32000, (4, 2048))
+    ids_d = ids.to(dev)
+
+    with torch.no_grad():
+        logits = lm(ids_d)["logits"]
+        assert torch.isfinite(logits).all()
+        row0 = logits[0:1, :256].float().cpu()
+        del logits
+        want = ref.lm_forward(cfg, p, ids[0:1, :256], 24, scale)
+        want16 = ref.lm_forward(cfg, p16, ids[0:1, :256], 24, scale)
+    err, err16 = max_rel(row0, want), max_rel(want16, want)
+    print(f"cfg4 prefill logits row 0 [:256]: max-rel {err:.3e} (oracle in bf16: {err16:.3e}), "
+          f"L2 {_l2(row0, want):.3e} (oracle in bf16: {_l2(want16, want):.3e})", flush=True)
+    assert err < max(BF16_TOL, err16)
+
+    n_new = 256
+    with torch.no_grad():
+        lm.decode_graph = True
+        graphed = lm.generate(ids_d, max_new_tokens=n_new, temperature=0)
+        lm.decode_graph = False
+        eager = lm.generate(ids_d, max_new_tokens=n_new, temperature=0)
+        lm.decode_graph = True
+    assert graphed.shape == (4, 2048 + n_new)
+    assert torch.equal(graphed, eager)
+    gen = graphed[:, 2048:].cpu()
+
+    # Teacher-forced decode from the GPU's prefilled states.
+    with torch.no_grad():
+        x = lm.embedding(ids_d)
+        states = []
+        for layer in lm.layers:
+            x, st = layer.prefill(x)
+            states.append(st)
+        first = lm.lm_head(lm.norm(x[:, -1])).float()
+        assert torch.equal(first.argmax(-1).cpu(), gen[:, 0])
+        st_ref = [{k: v.float().cpu() for k, v in st.items()} for st in states]
+        # the bf16 oracle chain holds its angle in fp32 as this build does (a bf16 running
+        # angle, the reference's choice, alone drifts by whole radians at these positions)
+        st16 = [{k: v.float().cpu() for k, v in st.items()} for st in states]
+        worst, worst16, agree = 0.0, 0.0, 0
+        for i in range(n_new - 1):
+            tok = gen[:, i]
+            xe = lm.embedding(tok.to(dev))
+            for j, layer in enumerate(lm.layers):
+                xe, states[j] = layer.step(xe, states[j])
+            got = lm.lm_head(lm.norm(xe)).float().cpu()
+            assert torch.isfinite(got).all()
+            want, st_ref = ref.lm_step(cfg, p, tok, st_ref, scale)
+            want16, st16 = ref.lm_step(cfg, p16, tok, st16, scale)
+            worst = max(worst, max_rel(got, want))
+            worst16 = max(worst16, max_rel(want16, want))
+            agree += int((want.argmax(-1) == gen[:, i + 1]).sum())
+    total = 4 * (n_new - 1)
+    print(f"cfg4 decode: worst step logits max-rel {worst:.3e} (oracle in bf16: {worst16:.3e}); "
+          f"oracle greedy agrees on {agree}/{total} tokens", flush=True)
+    assert worst < max(BF16_TOL, worst16)
+
+
+def test_bf16_d768_single_segment_prefill_matches_fp32_oracle(cuda_device):
+    """x (8, 512, 768): 192 (batch, head) pairs, so the fused d768 kernel walks all 8 chunks
+    of each pair in one workgroup with the state carried in accumulators (one segment; the
+    workspace then holds only the normalised B/C rows, which is checked). y, h, prev_BX and
+    angle of every batch row against the fp32 oracle (mamba3/mamba3.py:192-258,
+    mamba3/ssd.py:118-244)."""
+    kw = dict(d_model=768, d_state=128, headdim=64, mimo_rank=2)
+    torch.manual_seed(0)
+    layer = mamba3_amd.KulaMamba(**kw).to(cuda_device, torch.bfloat16).eval()
+    p = {k: v.detach().float().cpu() for k, v in layer.state_dict().items()}
+    cfg = ref.LayerCfg(d_model=768, d_state=128, headdim=64, mimo_rank=2)
+    B, T = 8, 512
+    desc = layer._desc(B, T, torch.empty(1, 1, layer.in_proj.out_features, dtype=torch.bfloat16))
+    ws = _native.prefill_workspace_bytes(desc)
+    assert ws == 2 * B * T * layer.ngroups * 128 * 2 * 2 + 256  # one segment: no state pass
+
+    torch.manual_seed(2)
+    x = torch.randn(B, T, 768).to(torch.bfloat16)
+    with torch.no_grad():
+        y, st = layer.prefill(x.to(cuda_device))
+    y, st = y.float().cpu(), {k: v.float().cpu() for k, v in st.items()}
+    for b in range(B):
+        with torch.no_grad():
+            y_ref, st_ref = ref.layer_forward(cfg, p, x[b:b + 1].float(), return_state=True)
+        assert max_rel(y[b:b + 1], y_ref) < BF16_TOL, b
+        for k in ("h", "prev_BX", "angle"):
+            assert max_rel(st[k][b:b + 1], st_ref[k]) < BF16_TOL, (b, k)

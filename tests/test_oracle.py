@@ -10,6 +10,8 @@ transposed operand) fails at least one of them:
 
 from __future__ import annotations
 
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -323,3 +325,39 @@ def test_chunked_recurrent_gradcheck():
     keys = [k for k, v in ins.items() if v is not None]
     fn = lambda *vs: rec.chunked_recurrent(**dict(zip(keys, vs)))
     assert torch.autograd.gradcheck(fn, tuple(ins[k] for k in keys), eps=1e-6, atol=1e-6)
+
+
+def _lm_tiny():
+    g = load_golden("lm_tiny")
+    cfg = ref.LayerCfg(d_model=64, d_state=16, headdim=16, mimo_rank=2, chunk_size=8)
+    return g, cfg, golden_params(g), 1.0 / math.sqrt(2 * 2)
+
+
+def test_oracle_lm_matches_reference_golden():
+    """Teacher-forced logits of the tiny LM (two blocks, final norm, tied head;
+    mamba3/block.py:79-92, 178-184) and its greedy generation (mamba3/block.py:195-231)
+    against the reference's fixture. Leaving out the depth residual scale, or the MLP
+    branch, must break the logits."""
+    g, cfg, p, scale = _lm_tiny()
+    ids = torch.from_numpy(g["ids"])
+    want = torch.from_numpy(g["logits"])
+    with torch.no_grad():
+        assert max_rel(ref.lm_forward(cfg, p, ids, 2, scale), want) < TOL
+        gen = ref.lm_generate_greedy(cfg, p, ids[:, :5], 2, scale, 6)
+        assert torch.equal(gen, torch.from_numpy(g["generated"]))
+        assert max_rel(ref.lm_forward(cfg, p, ids, 2, 1.0), want) > 1e-2
+        assert max_rel(ref.lm_forward(cfg, p, ids, 2, scale, use_mlp=False), want) > 1e-2
+
+
+def test_oracle_lm_steps_equal_parallel_logits():
+    """Prefill of a prompt, then one lm_step per remaining token (mamba3/block.py:94-107,
+    199-229), gives the teacher-forced logits of the parallel forward at every position."""
+    g, cfg, p, scale = _lm_tiny()
+    ids = torch.from_numpy(g["ids"])
+    with torch.no_grad():
+        full = ref.lm_forward(cfg, p, ids, 2, scale)
+        logits, states = ref.lm_prefill(cfg, p, ids[:, :5], 2, scale)
+        assert max_rel(logits, full[:, 4]) < TOL
+        for t in range(5, ids.shape[1]):
+            logits, states = ref.lm_step(cfg, p, ids[:, t], states, scale)
+            assert max_rel(logits, full[:, t]) < TOL, t
