@@ -2,9 +2,10 @@
  * mamba3_amd.h — C-ABI of the MI355X (gfx950) Mamba-3 chunked-SSD forward path.
  *
  * Every entry point takes plain device pointers, sizes and a HIP stream passed as
- * `void*` (a hipStream_t; NULL means the null stream). Nothing here allocates,
- * synchronises the host, or keeps mutable global state: outputs and workspaces are
- * owned by the caller, and every call is reentrant on distinct buffers. Each call
+ * `void*` (a hipStream_t; NULL means the null stream). Nothing here allocates or
+ * synchronises the host: outputs and workspaces are owned by the caller, and every call
+ * is reentrant on distinct buffers. The one exception to "no global state" is
+ * m3_prefill_fwd_noalloc, whose workspace is a static per-device array of the library. Each call
  * returns M3_OK (0) or an m3_status code; m3_status_string() names it. Arguments
  * are validated on the host before any launch, so a rejected call launches nothing.
  *
@@ -38,8 +39,12 @@ enum m3_status {
     M3_ERR_WORKSPACE = 4,         /* workspace missing or smaller than required */
     M3_ERR_MISALIGNED = 5,        /* a pointer violates the documented alignment */
     M3_ERR_LAUNCH = 6,            /* the HIP runtime rejected a kernel launch */
-    M3_ERR_DEVICE = 7             /* device query failed (no device / wrong arch) */
+    M3_ERR_DEVICE = 7,            /* device query failed (no device / wrong arch) */
+    M3_ERR_SCRATCH_LIMIT = 8      /* m3_prefill_fwd_noalloc: workspace need exceeds its scratch */
 };
+
+/* Size of the static per-device scratch of m3_prefill_fwd_noalloc (64 MiB). */
+#define M3_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
 
 /* Static description of one KulaMamba layer and of the activation tensor it reads.
  * Mirrors the constructor of KulaMamba (mamba3/mamba3.py:50-112). */
@@ -172,6 +177,22 @@ int m3_prefill_fwd(const m3_layer_desc* desc, const m3_layer_params* params,
                    const void* proj, const float* dt_scale, void* y_out,
                    float* h_final, float* angle, float* prev_bx,
                    void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * m3_prefill_fwd without a caller workspace: no counterpart in the reference. For callers
+ * that cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). Same arguments, dispatch, kernels and results as
+ * m3_prefill_fwd, but the workspace is a static array of the library on each GPU
+ * (M3_NOALLOC_SCRATCH_BYTES, held from the first call on that GPU until the process
+ * ends); calls needing more return M3_ERR_SCRATCH_LIMIT and launch nothing. It calls no
+ * allocator. The scratch keeps the last call's contents and needs no clearing (every
+ * kernel writes what it later reads). All calls on one GPU share the array: calls that
+ * overlap in time on one GPU (other streams or threads) race and must be serialised by
+ * the caller.
+ */
+int m3_prefill_fwd_noalloc(const m3_layer_desc* desc, const m3_layer_params* params,
+                           const void* proj, const float* dt_scale, void* y_out,
+                           float* h_final, float* angle, float* prev_bx, void* stream);
 
 /*
  * O(1) decode step of one KulaMamba layer for B tokens. Replaces

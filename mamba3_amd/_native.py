@@ -36,7 +36,11 @@ EXPORTED_SYMBOLS = (
     "m3_chunked_ssd_bwd",
     "m3_layer_bwd_workspace_size",
     "m3_layer_bwd",
+    "m3_prefill_fwd_noalloc",
 )
+
+M3_ERR_SCRATCH_LIMIT = 8
+NOALLOC_SCRATCH_BYTES = 64 << 20
 
 
 class NativeError(RuntimeError):
@@ -96,6 +100,9 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.m3_prefill_fwd.restype = ctypes.c_int
     lib.m3_prefill_fwd.argtypes = [ctypes.POINTER(LayerDesc), ctypes.POINTER(LayerParams),
                                    _vp, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp]
+    lib.m3_prefill_fwd_noalloc.restype = ctypes.c_int
+    lib.m3_prefill_fwd_noalloc.argtypes = [ctypes.POINTER(LayerDesc), ctypes.POINTER(LayerParams),
+                                           _vp, _vp, _vp, _vp, _vp, _vp, _vp]
     lib.m3_step_fwd.restype = ctypes.c_int
     lib.m3_step_fwd.argtypes = [ctypes.POINTER(LayerDesc), ctypes.POINTER(LayerParams),
                                 _vp, _vp, _vp, _vp, _vp, ctypes.c_int, _vp, _vp, _vp, _vp, _vp]
@@ -194,6 +201,14 @@ def prefill_fwd(desc: LayerDesc, params: LayerParams, proj, dt_scale, y_out, h_f
                                ptr(dt_scale), ptr(y_out), ptr(h_final), ptr(angle),
                                ptr(prev_bx), ptr(workspace), workspace_bytes,
                                stream_of(proj)), "m3_prefill_fwd")
+
+
+def prefill_fwd_noalloc(desc: LayerDesc, params: LayerParams, proj, dt_scale, y_out, h_final,
+                        angle, prev_bx) -> None:
+    """m3_prefill_fwd_noalloc: m3_prefill_fwd on the library's static per-device scratch."""
+    check(lib().m3_prefill_fwd_noalloc(ctypes.byref(desc), ctypes.byref(params), ptr(proj),
+                                       ptr(dt_scale), ptr(y_out), ptr(h_final), ptr(angle),
+                                       ptr(prev_bx), stream_of(proj)), "m3_prefill_fwd_noalloc")
 
 
 def step_fwd(desc: LayerDesc, params: LayerParams, proj, dt_scale, h_in, prev_in, angle_in,

@@ -1,8 +1,10 @@
 // C-ABI entry points (declared in include/mamba3_amd.h). Validates every argument on
-// the host, then calls the launchers. Never throws, never allocates, never syncs.
+// the host, then calls the launchers. Never throws, never allocates, never syncs. The one
+// piece of global state is the static scratch of m3_prefill_fwd_noalloc (below).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "m3_kernels.h"
 
@@ -47,6 +49,94 @@ int check_scan_bwd_shape(int64_t batch, int64_t nchunks, int64_t nheads, int64_t
     return M3_OK;
 }
 
+// Which prefill kernel a call dispatches to: the d_state 128 / headdim 64 / rank 2 MFMA
+// kernel (bf16, aligned rows, 16-byte aligned proj / y_out), the general MFMA kernel
+// (bf16, d_state 64/128/256, rank 1/2/4, headdim % 32 == 0, 16-byte aligned h_final), the
+// fp32 layer path on the fp32-MFMA chunk kernels (fp32, rank 1/2/4/8) or the generic one.
+enum class PrefillPath { kMfma, kWide, kFp32, kGeneric };
+
+PrefillPath prefill_path(const m3_layer_desc& d, const void* proj, const void* y_out,
+                         const void* h_final) {
+    if (m3::mfma_prefill_supported(d, proj, y_out)) return PrefillPath::kMfma;
+    if (m3::wide_prefill_supported(d) && aligned(h_final, 16)) return PrefillPath::kWide;
+    if (m3::fp32_layer_supported(d)) return PrefillPath::kFp32;
+    return PrefillPath::kGeneric;
+}
+
+size_t prefill_path_workspace(const m3_layer_desc& d, PrefillPath path) {
+    switch (path) {
+        case PrefillPath::kMfma: return m3::mfma_prefill_workspace(d);
+        case PrefillPath::kWide: return m3::wide_prefill_workspace(d);
+        case PrefillPath::kFp32: return m3::fp32_layer_workspace(d);
+        default: return m3::generic_prefill_workspace(d);
+    }
+}
+
+int check_prefill_args(const m3_layer_desc* desc, const m3_layer_params* params,
+                       const void* proj, const void* y_out) {
+    int st = check_desc(desc);
+    if (st != M3_OK) return st;
+    st = check_params(params);
+    if (st != M3_OK) return st;
+    if (!proj || !y_out) return M3_ERR_NULL_POINTER;
+    return M3_OK;
+}
+
+int launch_prefill_path(PrefillPath path, const m3_layer_desc& d, const m3_layer_params& p,
+                        const void* proj, const float* dt_scale, void* y_out, float* h_final,
+                        float* angle, float* prev_bx, void* ws, hipStream_t stream) {
+    switch (path) {
+        case PrefillPath::kMfma:
+            return m3::launch_mfma_prefill(d, p, proj, dt_scale, y_out, h_final, angle, prev_bx,
+                                           ws, stream);
+        case PrefillPath::kWide:
+            return m3::launch_wide_prefill(d, p, proj, dt_scale, y_out, h_final, angle, prev_bx,
+                                           ws, stream);
+        case PrefillPath::kFp32:
+            return m3::launch_fp32_layer(d, p, proj, dt_scale, y_out, h_final, angle, prev_bx,
+                                         ws, stream) == 0
+                       ? M3_OK
+                       : M3_ERR_LAUNCH;
+        default:
+            return m3::launch_generic_prefill(d, p, proj, dt_scale, y_out, h_final, angle,
+                                              prev_bx, ws, stream);
+    }
+}
+
+// ---- static scratch of m3_prefill_fwd_noalloc
+// One copy of this array exists on every GPU the library runs on, from the first call on
+// that GPU until the process ends. Host code never uses the array's name as an address:
+// its device address is looked up once per device (hipGetSymbolAddress, with that device
+// current) and kept in g_scratch.
+static __device__ __align__(256) unsigned char scratch[M3_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices];
+
+int scratch_for_stream(hipStream_t stream, void** out) {
+    int cur = -1;
+    if (hipGetDevice(&cur) != hipSuccess) return M3_ERR_DEVICE;
+    int dev = cur;
+    if (stream != nullptr) {
+        hipDevice_t sd;
+        if (hipStreamGetDevice(stream, &sd) != hipSuccess) return M3_ERR_DEVICE;
+        dev = static_cast<int>(sd);
+    }
+    if (dev < 0 || dev >= kMaxDevices) return M3_ERR_DEVICE;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch[dev] == nullptr) {
+        if (dev != cur && hipSetDevice(dev) != hipSuccess) return M3_ERR_DEVICE;
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (dev != cur) (void)hipSetDevice(cur);
+        if (e != hipSuccess || ptr == nullptr) return M3_ERR_DEVICE;
+        g_scratch[dev] = ptr;
+    }
+    *out = g_scratch[dev];
+    return M3_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -61,6 +151,9 @@ const char* m3_status_string(int status) {
         case M3_ERR_MISALIGNED: return "pointer alignment violated";
         case M3_ERR_LAUNCH: return "kernel launch failed";
         case M3_ERR_DEVICE: return "device query failed";
+        case M3_ERR_SCRATCH_LIMIT:
+            return "workspace need exceeds the static scratch of m3_prefill_fwd_noalloc "
+                   "(M3_NOALLOC_SCRATCH_BYTES); use m3_prefill_fwd with a caller workspace";
         default: return "unknown status";
     }
 }
@@ -105,10 +198,8 @@ int m3_scan_bwd(const float* decay, const float* h_states, const float* grad, fl
                : M3_ERR_LAUNCH;
 }
 
-// Workspace for whichever prefill kernel the shape may dispatch to: the d_state 128 /
-// headdim 64 / rank 2 MFMA kernel (bf16, aligned rows, 16-byte aligned proj / y_out), the
-// general MFMA kernel (bf16, d_state 64/128/256, rank 1/2/4, headdim % 32 == 0), the fp32
-// layer path on the fp32-MFMA chunk kernels (fp32, rank 1/2/4/8) or the generic kernel.
+// Workspace for whichever prefill kernel the shape may dispatch to (the pointers' alignment
+// is not known here, so the largest of the candidates).
 static size_t prefill_workspace(const m3_layer_desc& d) {
     size_t n = m3::generic_prefill_workspace(d);
     n = std::max(n, m3::fp32_layer_workspace(d));
@@ -128,38 +219,31 @@ int m3_prefill_workspace_size(const m3_layer_desc* desc, size_t* bytes) {
 int m3_prefill_fwd(const m3_layer_desc* desc, const m3_layer_params* params, const void* proj,
                    const float* dt_scale, void* y_out, float* h_final, float* angle,
                    float* prev_bx, void* workspace, size_t workspace_bytes, void* stream) {
-    int st = check_desc(desc);
+    int st = check_prefill_args(desc, params, proj, y_out);
     if (st != M3_OK) return st;
-    st = check_params(params);
-    if (st != M3_OK) return st;
-    if (!proj || !y_out) return M3_ERR_NULL_POINTER;
-    if (m3::mfma_prefill_supported(*desc, proj, y_out)) {
-        if (!workspace || workspace_bytes < m3::mfma_prefill_workspace(*desc))
-            return M3_ERR_WORKSPACE;
-        if (!aligned(workspace, 256)) return M3_ERR_MISALIGNED;
-        return m3::launch_mfma_prefill(*desc, *params, proj, dt_scale, y_out, h_final, angle,
-                                       prev_bx, workspace, as_stream(stream));
-    }
-    if (m3::wide_prefill_supported(*desc) && aligned(h_final, 16)) {
-        if (!workspace || workspace_bytes < m3::wide_prefill_workspace(*desc))
-            return M3_ERR_WORKSPACE;
-        if (!aligned(workspace, 256)) return M3_ERR_MISALIGNED;
-        return m3::launch_wide_prefill(*desc, *params, proj, dt_scale, y_out, h_final, angle,
-                                       prev_bx, workspace, as_stream(stream));
-    }
-    if (m3::fp32_layer_supported(*desc)) {
-        if (!workspace || workspace_bytes < m3::fp32_layer_workspace(*desc)) return M3_ERR_WORKSPACE;
-        if (!aligned(workspace, 256)) return M3_ERR_MISALIGNED;
-        return m3::launch_fp32_layer(*desc, *params, proj, dt_scale, y_out, h_final, angle,
-                                     prev_bx, workspace, as_stream(stream)) == 0
-                   ? M3_OK
-                   : M3_ERR_LAUNCH;
-    }
-    const size_t need = m3::generic_prefill_workspace(*desc);
-    if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return M3_ERR_WORKSPACE;
+    const PrefillPath path = prefill_path(*desc, proj, y_out, h_final);
+    const size_t need = prefill_path_workspace(*desc, path);
+    if (need > 0 && (!workspace || workspace_bytes < need)) return M3_ERR_WORKSPACE;
     if (workspace && !aligned(workspace, 256)) return M3_ERR_MISALIGNED;
-    return m3::launch_generic_prefill(*desc, *params, proj, dt_scale, y_out, h_final, angle,
-                                      prev_bx, workspace, as_stream(stream));
+    return launch_prefill_path(path, *desc, *params, proj, dt_scale, y_out, h_final, angle,
+                               prev_bx, workspace, as_stream(stream));
+}
+
+int m3_prefill_fwd_noalloc(const m3_layer_desc* desc, const m3_layer_params* params,
+                           const void* proj, const float* dt_scale, void* y_out, float* h_final,
+                           float* angle, float* prev_bx, void* stream) {
+    int st = check_prefill_args(desc, params, proj, y_out);
+    if (st != M3_OK) return st;
+    const PrefillPath path = prefill_path(*desc, proj, y_out, h_final);
+    const size_t need = prefill_path_workspace(*desc, path);
+    if (need > M3_NOALLOC_SCRATCH_BYTES) return M3_ERR_SCRATCH_LIMIT;
+    void* ws = nullptr;
+    if (need > 0) {
+        st = scratch_for_stream(as_stream(stream), &ws);
+        if (st != M3_OK) return st;
+    }
+    return launch_prefill_path(path, *desc, *params, proj, dt_scale, y_out, h_final, angle,
+                               prev_bx, ws, as_stream(stream));
 }
 
 int m3_layer_bwd_workspace_size(const m3_layer_desc* desc, size_t* bytes) {

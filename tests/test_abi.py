@@ -232,3 +232,20 @@ def test_custom_op_fake_kernels_give_output_shapes():
         out = torch.ops.mamba3_amd.scan_fwd(mode.from_tensor(torch.empty(2, 3, 4)),
                                             mode.from_tensor(torch.empty(2, 3, 4, 10)), None)
         assert out.shape == (2, 3, 4, 10)
+
+
+def test_noalloc_prefill_refuses_workspace_beyond_scratch_before_any_launch():
+    """m3_prefill_fwd_noalloc rejects a workload whose workspace exceeds the static scratch
+    on the host, before touching the device (so this runs without a GPU); the pointers
+    are never dereferenced."""
+    lib = _native.lib()
+    d = _desc(dtype=1, batch=8, seqlen=8192, nheads=24, headdim=64, d_state=128)
+    n = ctypes.c_size_t(0)
+    assert lib.m3_prefill_workspace_size(ctypes.byref(d), ctypes.byref(n)) == 0
+    assert n.value > _native.NOALLOC_SCRATCH_BYTES
+    fake = ctypes.c_void_p(1 << 20)
+    params = _native.LayerParams(*([fake.value] * 10))
+    st = lib.m3_prefill_fwd_noalloc(ctypes.byref(d), ctypes.byref(params), fake, None, fake,
+                                    None, None, None, None)
+    assert st == _native.M3_ERR_SCRATCH_LIMIT
+    assert b"scratch" in lib.m3_status_string(st)
