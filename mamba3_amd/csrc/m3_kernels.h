@@ -57,6 +57,10 @@ int launch_generic_chunked(int B, int T, int H, int P, int N, int R, int dtype,
 
 // bf16 MFMA fused prefill for d_state 128, headdim 64, mimo_rank 2.
 bool mfma_prefill_supported(const m3_layer_desc& d, const void* proj, const void* y_out);
+// Normalised B^ / C^ rows (RMSNorm * weight + bias) per (token, group), pair-packed f16
+// (N*R values per row; word R*i + r holds the pair (2i, 2i+1) of rank r).
+void launch_bc_norm(const m3_layer_desc& d, const m3_layer_params& p, const void* proj,
+                    _Float16* bn, _Float16* cn, hipStream_t stream);
 size_t mfma_prefill_workspace(const m3_layer_desc& d);
 int launch_mfma_prefill(const m3_layer_desc& d, const m3_layer_params& p, const void* proj,
                         const float* dt_scale, void* y_out, float* h_final, float* angle,

@@ -90,4 +90,44 @@ __device__ __forceinline__ f16x4 ld_tr(const f16* p) {
 __device__ __forceinline__ f16x2 as_f16x2(unsigned u) { return __builtin_bit_cast(f16x2, u); }
 __device__ __forceinline__ unsigned bits(f16x2 v) { return __builtin_bit_cast(unsigned, v); }
 
+// ---- buffer-descriptor global access (gfx950 raw buffer instructions)
+// Descriptor flags of every buffer resource built here.
+constexpr int kRsrcFlags = 0x00020000;
+// Cache policy of the reads and writes that touch their data once (x, z, y): non-temporal,
+// so they do not evict the normalised B^ / C^ rows that all heads of a batch row share
+// from L2.
+constexpr int kStream = 2;
+
+// A buffer resource over [base, base + bytes): reads past the end return zero, stores past
+// the end are dropped.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0,
+                                             (int)(bytes < 0x7fffffff ? bytes : 0x7fffffff),
+                                             kRsrcFlags);
+}
+
+// 16-bit load kept zero-extended in its own 32-bit register. Holding loaded bf16 values
+// as bf16 lets the compiler pack two per register, which forces a wait on the load right
+// after it is issued; the value is widened only where it is used (bf16_f32).
+__device__ __forceinline__ unsigned ld_u16(__amdgpu_buffer_rsrc_t r, int off_bytes) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, off_bytes, 0, 0);
+}
+__device__ __forceinline__ float bf16_f32(unsigned u) { return __builtin_bit_cast(float, u << 16); }
+
+__device__ __forceinline__ u32x2 ld_b64(__amdgpu_buffer_rsrc_t r, int off_elems) {
+    return __builtin_amdgcn_raw_buffer_load_b64(r, off_elems * 2, 0, 0);
+}
+
+// Scheduling fence: keeps LDS operand reads issued ahead of the MFMAs that consume them
+// (the compiler otherwise sinks each read next to its use and waits on it).
+#define M3_FENCE() __builtin_amdgcn_sched_barrier(0)
+// Compiler memory fence between LDS stores (no instruction): stops the pairing of
+// neighbouring stores into ds_write2_b64, which is about twice as slow as two single
+// 64-bit stores on gfx950.
+#define M3_LDS_FENCE() asm volatile("" ::: "memory")
+
+__device__ __forceinline__ f16x8 cat8(const f16x4& lo, const f16x4& hi) {
+    return f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
 }  // namespace m3

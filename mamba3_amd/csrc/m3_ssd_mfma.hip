@@ -65,10 +65,6 @@ constexpr int NH = N / 2;
 constexpr int THREADS = 1024;  // 8 MFMA waves + 8 helper waves, four per SIMD
 constexpr int NMW = 8;          // waves 0..7 run the MFMA work, 8..15 are helpers
 constexpr int PAD = 8;
-constexpr int kRsrcFlags = 0x00020000;
-// Cache policy of the reads and writes that touch their data once (x, z, y): non-temporal,
-// so they do not evict the normalised B^ / C^ rows that the 24 heads share from L2.
-constexpr int kStream = 2;
 
 
 constexpr int NSLOT = 3;
@@ -122,24 +118,8 @@ struct Args {
 };
 
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0,
-                                             (int)(bytes < 0x7fffffff ? bytes : 0x7fffffff),
-                                             kRsrcFlags);
-}
 
 
-// 16-bit load kept zero-extended in its own 32-bit register. Holding loaded bf16 values
-// as bf16 lets the compiler pack two per register, which forces a wait on the load right
-// after it is issued; the value is widened only where it is used (bf16_f32).
-__device__ __forceinline__ unsigned ld_u16(__amdgpu_buffer_rsrc_t r, int off_bytes) {
-    return __builtin_amdgcn_raw_buffer_load_b16(r, off_bytes, 0, 0);
-}
-__device__ __forceinline__ float bf16_f32(unsigned u) { return __builtin_bit_cast(float, u << 16); }
-
-__device__ __forceinline__ u32x2 ld_b64(__amdgpu_buffer_rsrc_t r, int off_elems) {
-    return __builtin_amdgcn_raw_buffer_load_b64(r, off_elems * 2, 0, 0);
-}
 
 // C~ / B~ tiles: 64-byte column groups of a row are XOR-swizzled by the row's 16-row
 // block, so the preparation's 64-bit stores (lanes 16 rows apart) hit distinct banks.
@@ -202,17 +182,6 @@ __global__ __launch_bounds__(256) void bc_norm(const bf16* __restrict__ proj, in
 // ---------------------------------------------------------------------------------
 // 2/3. Segment kernels.
 // ---------------------------------------------------------------------------------
-// Scheduling fence: keeps LDS operand reads issued ahead of the MFMAs that consume them
-// (the compiler otherwise sinks each read next to its use and waits on it).
-#define M3_FENCE() __builtin_amdgcn_sched_barrier(0)
-// Compiler memory fence between LDS stores (no instruction): stops the pairing of
-// neighbouring stores into ds_write2_b64, which is about twice as slow as two single
-// 64-bit stores on gfx950.
-#define M3_LDS_FENCE() asm volatile("" ::: "memory")
-
-__device__ __forceinline__ f16x8 cat8(const f16x4& lo, const f16x4& hi) {
-    return f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-}
 
 // Output rows of one 16-row block I of the chunk (tokens 8I .. 8I+7, rows (t,r) = 2t+r),
 // computed by one MFMA wave:
@@ -1001,6 +970,17 @@ static void mfma_segments(const m3_layer_desc& d, int& S, int& cps) {
     S = (K + cps - 1) / cps;
 }
 
+// B^ / C^ rows of every (token, group) of the layer, pair-packed f16 (bc_norm).
+void launch_bc_norm(const m3_layer_desc& d, const m3_layer_params& p, const void* proj,
+                    f16* bn, f16* cn, hipStream_t stream) {
+    const ProjLayout pl = proj_layout(d);
+    const int64_t ntg = (int64_t)d.batch * d.seqlen * d.ngroups;
+    hipLaunchKernelGGL(mf::bc_norm, dim3((unsigned)((ntg + 3) / 4)), dim3(256), 0, stream,
+                       reinterpret_cast<const bf16*>(proj), d.proj_row_stride, pl.B, pl.C,
+                       d.ngroups, ntg, d.rms_eps, p.B_norm_w, p.B_bias, p.C_norm_w, p.C_bias,
+                       bn, cn);
+}
+
 size_t mfma_prefill_workspace(const m3_layer_desc& d) {
     int S, cps;
     mfma_segments(d, S, cps);
@@ -1038,9 +1018,7 @@ int launch_mfma_prefill(const m3_layer_desc& d, const m3_layer_params& p, const 
     a.angle = angle;
     a.prev_bx = prev_bx;
 
-    hipLaunchKernelGGL(mf::bc_norm, dim3((unsigned)((ntg + 3) / 4)), dim3(256), 0, stream,
-                       a.proj, a.rs, a.pl.B, a.pl.C, a.G, ntg, d.rms_eps, p.B_norm_w, p.B_bias,
-                       p.C_norm_w, p.C_bias, bn, cn);
+    launch_bc_norm(d, p, proj, bn, cn, stream);
     if (S > 1)
         hipLaunchKernelGGL(mf::ssd_chunks<false>, dim3((unsigned)(d.batch * d.nheads * (S - 1))),
                            dim3(mf::THREADS), 0, stream, a);

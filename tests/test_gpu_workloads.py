@@ -1,7 +1,7 @@
 """Full-size workload parity on the GPU: the 24-layer d_model-768 LM in bf16 (prefill over
-ids (4, 2048) and 256 greedy tokens) and the fused d768 prefill in its single-segment
-form, each against the fp32 oracle on the bf16-rounded weights (normwise max-relative
-error, 2e-2).
+ids (4, 2048) and 256 greedy tokens) and the fused d768 prefill in both of its work plans,
+each against the fp32 oracle on the bf16-rounded weights (normwise max-relative error,
+2e-2).
 
 The oracle runs on the host at sizes it finishes in seconds: causality makes a prefix of
 one batch row exact, and the decode steps start from the GPU's own prefilled state.
@@ -122,24 +122,30 @@ def test_lm_d768_24_layers_prefill_and_greedy_decode(cuda_device):
     assert worst < max(BF16_TOL, worst16)
 
 
-def test_bf16_d768_single_segment_prefill_matches_fp32_oracle(cuda_device):
-    """x (8, 512, 768): 192 (batch, head) pairs, so the fused d768 kernel walks all 8 chunks
-    of each pair in one workgroup with the state carried in accumulators (one segment; the
-    workspace then holds only the normalised B/C rows, which is checked). y, h, prev_BX and
-    angle of every batch row against the fp32 oracle (mamba3/mamba3.py:192-258,
-    mamba3/ssd.py:118-244)."""
+@pytest.mark.parametrize("B,T,split", [(8, 512, False), (2, 1200, True)])
+def test_bf16_d768_prefill_plans_match_fp32_oracle(B, T, split, cuda_device):
+    """The fused d768 prefill in both of its work plans, every batch row against the fp32
+    oracle (mamba3/mamba3.py:192-258, mamba3/ssd.py:118-244): y, h, prev_BX and angle.
+
+    * x (8, 512, 768): 192 (batch, head) pairs nearly fill the GPU, so each workgroup walks
+      all 8 chunks of its pair with the state carried in MFMA accumulators (one segment; the
+      form the (8, 8192) workload runs in).
+    * x (2, 1200, 768): 48 pairs, so each sequence is cut into segments: a state-only pass,
+      then each segment combines its predecessors' end states (rotated into its RoPE frame).
+    The plan is checked through the workspace size (segment states only when split)."""
     kw = dict(d_model=768, d_state=128, headdim=64, mimo_rank=2)
     torch.manual_seed(0)
     layer = mamba3_amd.KulaMamba(**kw).to(cuda_device, torch.bfloat16).eval()
     p = {k: v.detach().float().cpu() for k, v in layer.state_dict().items()}
     cfg = ref.LayerCfg(d_model=768, d_state=128, headdim=64, mimo_rank=2)
-    B, T = 8, 512
     desc = layer._desc(B, T, torch.empty(1, 1, layer.in_proj.out_features, dtype=torch.bfloat16))
     ws = _native.prefill_workspace_bytes(desc)
-    assert ws == 2 * B * T * layer.ngroups * 128 * 2 * 2 + 256  # one segment: no state pass
+    bc_only = 2 * B * T * layer.ngroups * 128 * 2 * 2 + 256
+    assert (ws > bc_only) == split
 
     torch.manual_seed(2)
     x = torch.randn(B, T, 768).to(torch.bfloat16)
+    print(f"d768 prefill plan: x {tuple(x.shape)}, split {split}", flush=True)
     with torch.no_grad():
         y, st = layer.prefill(x.to(cuda_device))
     y, st = y.float().cpu(), {k: v.float().cpu() for k, v in st.items()}
