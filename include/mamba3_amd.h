@@ -61,7 +61,16 @@ typedef struct m3_layer_desc {
     int32_t dtype;            /* m3_dtype of proj and of the gated output */
     int64_t proj_row_stride;  /* elements between consecutive tokens of proj (>= d_in_proj) */
     float rms_eps;            /* RMSNorm epsilon of B_norm / C_norm (1e-5 in the reference) */
+    int32_t flags;            /* M3_FLAG_* bits (0 by default) */
 } m3_layer_desc;
+
+/* The bf16 MFMA prefill kernels hold these as f16 MFMA operands: the normalised B^ / C^
+ * values (|v| <= sqrt(N R) max|w| + max|bias|), x * mimo_x, the decay-masked scores
+ * C~.B~ * exp(c_t - c_u) (a_u + b_u) and the state copy h / 256, each below 65504 in
+ * magnitude. A caller whose parameters may break that (e.g. large B/C norm weights or
+ * biases, or mimo_x, in a trained checkpoint) sets this flag: such layers then run on the
+ * fp32 generic kernel, which has no such range limit. */
+#define M3_FLAG_NO_F16_OPERANDS 1
 
 /* Small per-layer parameters, all fp32 device arrays. Names follow the reference's
  * parameters (mamba3/mamba3.py:95-111). */
@@ -124,9 +133,9 @@ int m3_scan_fwd(const float* decay, const float* h_chunk, const float* h_init,
  *     d_decay[b,k,h]   = sum_j G[k+1][j] h_states[b,k,h,j] for k < K-1, 0 for k = K-1
  *     d_h_init[b,h,:]  = G[0]   (not written when d_h_init is NULL)
  * decay, d_decay [B,K,H]; h_states, grad, d_chunk [B,K,H,PN]; d_h_init [B,H,PN]; all fp32.
- * d_decay sums are formed in a fixed order (deterministic). PN must be a multiple of 256
- * or at most 16384. workspace: m3_scan_bwd_workspace_size() bytes (0 is possible),
- * 256-byte aligned.
+ * d_decay sums are formed in a fixed order (deterministic). Any PN and any pointer
+ * alignment (PN a multiple of 256 with 16-byte aligned arrays takes the vectorised path).
+ * workspace: m3_scan_bwd_workspace_size() bytes (0 is possible), 256-byte aligned.
  */
 int m3_scan_bwd_workspace_size(int64_t batch, int64_t nchunks, int64_t nheads, int64_t pn,
                                size_t* bytes);
@@ -251,8 +260,8 @@ int m3_chunked_ssd_fwd_workspace_size(int32_t batch, int32_t seqlen, int32_t nhe
  * nullable) plus dy [B,T,H,P,R] = dL/dy and dh_final [B,H,P,N] = dL/dh_final (nullable).
  * Outputs (all written, not accumulated): dx_g, dx_b, dB_g, dB_b, dC, dx_raw like their
  * inputs (dx_b / dB_b NULL exactly when x_b is), ddt [B,T,H], dA [H], dD [H],
- * dh_init [B,H,P,N] (nullable: not written). mimo_rank must be 1, 2, 4 or 8, and
- * headdim * d_state a multiple of 256 or at most 16384. Sums run in a fixed order
+ * dh_init [B,H,P,N] (nullable: not written). mimo_rank must be 1, 2, 4 or 8. Sums run in a
+ * fixed order
  * (deterministic). workspace: m3_chunked_ssd_bwd_workspace_size() bytes, 256-byte aligned.
  */
 int m3_chunked_ssd_bwd_workspace_size(int32_t batch, int32_t seqlen, int32_t nheads,

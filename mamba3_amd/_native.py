@@ -61,7 +61,11 @@ class LayerDesc(ctypes.Structure):
         ("dtype", ctypes.c_int32),
         ("proj_row_stride", ctypes.c_int64),
         ("rms_eps", ctypes.c_float),
+        ("flags", ctypes.c_int32),
     ]
+
+
+M3_FLAG_NO_F16_OPERANDS = 1
 
 
 class LayerParams(ctypes.Structure):

@@ -28,6 +28,7 @@ int check_desc(const m3_layer_desc* d) {
     if (d->use_complex != 0 && d->use_complex != 1) return M3_ERR_INVALID_SHAPE;
     if (d->proj_row_stride < proj_layout(*d).width) return M3_ERR_INVALID_SHAPE;
     if (!(d->rms_eps >= 0.f)) return M3_ERR_INVALID_SHAPE;
+    if (d->flags & ~M3_FLAG_NO_F16_OPERANDS) return M3_ERR_INVALID_SHAPE;
     // Kernel limits: headdim <= 256, d_state <= 512, rank <= 8.
     if (d->headdim > 256 || d->d_state > 512 || d->mimo_rank > 8) return M3_ERR_UNSUPPORTED;
     return M3_OK;
@@ -44,21 +45,22 @@ int check_params(const m3_layer_params* p) {
 int check_scan_bwd_shape(int64_t batch, int64_t nchunks, int64_t nheads, int64_t pn) {
     if (batch <= 0 || nchunks <= 0 || nheads <= 0 || pn <= 0) return M3_ERR_INVALID_SHAPE;
     if (batch * nheads * pn > ((int64_t)1 << 40) || nchunks > (1 << 30)) return M3_ERR_UNSUPPORTED;
-    if (pn % 256 != 0 && pn > 16384) return M3_ERR_UNSUPPORTED;
     if (batch * nheads > 0x7fffffff) return M3_ERR_UNSUPPORTED;
     return M3_OK;
 }
 
 // Which prefill kernel a call dispatches to: the d_state 128 / headdim 64 / rank 2 MFMA
 // kernel (bf16, aligned rows, 16-byte aligned proj / y_out), the general MFMA kernel
-// (bf16, d_state 64/128/256, rank 1/2/4, headdim % 32 == 0, 16-byte aligned h_final), the
-// fp32 layer path on the fp32-MFMA chunk kernels (fp32, rank 1/2/4/8) or the generic one.
+// (bf16, d_state 64/128/256, rank 1/2/4, headdim % 32 == 0, 16-byte aligned h_final) --
+// both with f16 operands, so not under M3_FLAG_NO_F16_OPERANDS -- the fp32 layer path on
+// the fp32-MFMA chunk kernels (fp32, rank 1/2/4/8) or the generic one.
 enum class PrefillPath { kMfma, kWide, kFp32, kGeneric };
 
 PrefillPath prefill_path(const m3_layer_desc& d, const void* proj, const void* y_out,
                          const void* h_final) {
-    if (m3::mfma_prefill_supported(d, proj, y_out)) return PrefillPath::kMfma;
-    if (m3::wide_prefill_supported(d) && aligned(h_final, 16)) return PrefillPath::kWide;
+    const bool f16_ok = !(d.flags & M3_FLAG_NO_F16_OPERANDS);
+    if (f16_ok && m3::mfma_prefill_supported(d, proj, y_out)) return PrefillPath::kMfma;
+    if (f16_ok && m3::wide_prefill_supported(d) && aligned(h_final, 16)) return PrefillPath::kWide;
     if (m3::fp32_layer_supported(d)) return PrefillPath::kFp32;
     return PrefillPath::kGeneric;
 }

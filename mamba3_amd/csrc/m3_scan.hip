@@ -140,57 +140,64 @@ __global__ __launch_bounds__(kScanBwdBlock) void scan_bwd_reduce(const float* __
     d_decay[i] = acc;
 }
 
-// Any PN: one workgroup per (b,h), columns strided over its threads, the d_decay sum of
-// every k reduced through LDS in a fixed order.
+// Any PN and any alignment: one workgroup per (b,h). The columns are walked in tiles of
+// 256 * 64 (64 per thread in registers); within a tile the chunks are walked down with the
+// d_decay sum of every k reduced through LDS, and the tiles' sums are added in tile order,
+// so the result does not depend on timing.
 __global__ __launch_bounds__(kScanBwdBlock) void scan_bwd_block(
     const float* __restrict__ decay, const float* __restrict__ h_states,
     const float* __restrict__ grad, float* __restrict__ d_chunk, float* __restrict__ d_decay,
     float* __restrict__ d_h_init, int K, int H, int PN) {
-    constexpr int kMaxPer = 64;  // columns per thread: PN <= 256 * 64
+    constexpr int kMaxPer = 64;                      // columns per thread and tile
+    constexpr int kTile = kScanBwdBlock * kMaxPer;  // columns per tile
     __shared__ float red[kScanBwdBlock / 64];
     const int64_t bh = blockIdx.x;
     const int h = (int)(bh % H);
     const int64_t b = bh / H;
     const int64_t kstride = (int64_t)H * PN;
-    const int64_t base = (b * K * H + h) * (int64_t)PN;
     const int64_t db = b * K * H + h;
     const int tid = threadIdx.x;
-    float g[kMaxPer];
-    for (int i = 0; i < kMaxPer; ++i) {
-        const int j = tid + i * kScanBwdBlock;
-        if (j < PN) {
-            g[i] = grad[base + (int64_t)(K - 1) * kstride + j];
-            d_chunk[base + (int64_t)(K - 1) * kstride + j] = 0.f;
-        }
-    }
     if (tid == 0) d_decay[db + (int64_t)(K - 1) * H] = 0.f;
-    for (int k = K - 2; k >= 0; --k) {
-        const int64_t o = base + (int64_t)k * kstride;
-        const float d = decay[db + (int64_t)k * H];
-        float acc = 0.f;
+    for (int c0 = 0; c0 < PN; c0 += kTile) {
+        const int64_t base = (b * K * H + h) * (int64_t)PN + c0;
+        const int cols = PN - c0 < kTile ? PN - c0 : kTile;
+        float g[kMaxPer];
         for (int i = 0; i < kMaxPer; ++i) {
             const int j = tid + i * kScanBwdBlock;
-            if (j < PN) {
-                acc += g[i] * h_states[o + j];
-                d_chunk[o + j] = g[i];
-                g[i] = grad[o + j] + d * g[i];
+            if (j < cols) {
+                g[i] = grad[base + (int64_t)(K - 1) * kstride + j];
+                d_chunk[base + (int64_t)(K - 1) * kstride + j] = 0.f;
             }
         }
-        acc = wave_sum_dpp(acc);
-        if ((tid & 63) == 0) red[tid >> 6] = acc;
-        __syncthreads();
-        if (tid == 0) {
-            float s = 0.f;
-            for (int w = 0; w < kScanBwdBlock / 64; ++w) s += red[w];
-            d_decay[db + (int64_t)k * H] = s;
+        for (int k = K - 2; k >= 0; --k) {
+            const int64_t o = base + (int64_t)k * kstride;
+            const float d = decay[db + (int64_t)k * H];
+            float acc = 0.f;
+            for (int i = 0; i < kMaxPer; ++i) {
+                const int j = tid + i * kScanBwdBlock;
+                if (j < cols) {
+                    acc += g[i] * h_states[o + j];
+                    d_chunk[o + j] = g[i];
+                    g[i] = grad[o + j] + d * g[i];
+                }
+            }
+            acc = wave_sum_dpp(acc);
+            if ((tid & 63) == 0) red[tid >> 6] = acc;
+            __syncthreads();
+            if (tid == 0) {
+                float s = 0.f;
+                for (int w = 0; w < kScanBwdBlock / 64; ++w) s += red[w];
+                float* dd = &d_decay[db + (int64_t)k * H];
+                *dd = c0 == 0 ? s : *dd + s;
+            }
+            __syncthreads();
         }
-        __syncthreads();
+        if (d_h_init)
+            for (int i = 0; i < kMaxPer; ++i) {
+                const int j = tid + i * kScanBwdBlock;
+                if (j < cols) d_h_init[bh * PN + c0 + j] = g[i];
+            }
     }
-    if (d_h_init)
-        for (int i = 0; i < kMaxPer; ++i) {
-            const int j = tid + i * kScanBwdBlock;
-            if (j < PN) d_h_init[bh * PN + j] = g[i];
-        }
 }
 
 size_t scan_bwd_workspace(int64_t B, int64_t K, int64_t H, int64_t PN) {

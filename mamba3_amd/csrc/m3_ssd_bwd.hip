@@ -873,8 +873,6 @@ int launch_chunked_fwd_mfma(int B, int T, int H, int P, int N, int R, const floa
 bool chunked_bwd_shape_ok(int B, int T, int H, int P, int N, int R, bool beta) {
     bw::Shape s;
     if (!bw::make_shape(B, T, H, P, N, R, beta, s)) return false;
-    const int64_t pn = s.PN;
-    if (pn % 256 != 0 && pn > 16384) return false;  // the scan backward's limit
     return true;
 }
 

@@ -54,7 +54,8 @@ def test_scan_rejects_bad_arguments(lib):
     assert lib.m3_scan_bwd_workspace_size(2, 16, 24, 8192, ctypes.byref(n)) == 0
     assert n.value == 2 * 16 * 24 * (8192 // 256) * 4  # one partial per wave and chunk
     assert lib.m3_scan_bwd_workspace_size(2, 16, 24, 100, ctypes.byref(n)) == 0 and n.value == 0
-    assert lib.m3_scan_bwd_workspace_size(2, 16, 24, 20000, ctypes.byref(n)) == 3
+    # any PN: beyond 16384 and not a multiple of 256 the per-(b,h) kernel tiles the columns
+    assert lib.m3_scan_bwd_workspace_size(2, 16, 24, 20000, ctypes.byref(n)) == 0 and n.value == 0
     assert lib.m3_scan_bwd(None, fake, fake, fake, fake, None, None, 0, 1, 2, 1, 256, None) == 1
     assert lib.m3_scan_bwd(fake, fake, fake, fake, fake, None, None, 0, 1, 0, 1, 256, None) == 2
     # the per-wave partials need a workspace
@@ -142,9 +143,10 @@ def test_prefill_and_step_reject_missing_pointers(lib):
                               None, None, None, 0, None) == 4
     assert lib.m3_step_fwd(ctypes.byref(d), ctypes.byref(full), 256, None, None, 256, 256, 0,
                            256, 256, 256, 256, None) == 1
-    # unsupported d_state for the step kernel
-    d12 = _desc(d_state=12)
-    assert lib.m3_step_fwd(ctypes.byref(d12), ctypes.byref(full), 256, None, 256, 512, 256, 0,
+    # d_state beyond the kernels' 512 is refused on the host, before any launch (every
+    # even d_state up to 512 is supported)
+    d600 = _desc(d_state=600)
+    assert lib.m3_step_fwd(ctypes.byref(d600), ctypes.byref(full), 256, None, 256, 512, 256, 0,
                            256, 768, 1024, 256, None) == 3
     # aliasing in/out state is refused
     assert lib.m3_step_fwd(ctypes.byref(d), ctypes.byref(full), 256, None, 256, 512, 256, 0,

@@ -352,6 +352,34 @@ def test_mimo_cross_rank(cuda_device):
     assert (y_full - y_zero).abs().max().item() > 1e-5
 
 
+@pytest.mark.parametrize("PN,offset", [(20000, 0), (32768, 1)])
+def test_scan_backward_many_columns_off_the_vector_path(PN, offset, cuda_device):
+    """m3_scan_bwd with more than 16384 columns on the per-(b,h) kernel: PN not a multiple of
+    256, or grad viewed at a 4-byte offset (not 16-byte aligned), so the vectorised path does
+    not apply and the columns are walked in tiles. Called through the C-ABI against the
+    oracle's backward (mamba3/scan.py:47-62)."""
+    B, K, H = 1, 5, 2
+    g = torch.Generator().manual_seed(PN + offset)
+    d = torch.rand(B, K, H, generator=g) * 0.5 + 0.5
+    hc = torch.randn(B, K, H, PN, generator=g)
+    h0 = torch.randn(B, H, PN, generator=g)
+    gout = torch.randn(B, K, H, PN, generator=g)
+    states = ref.scan_forward(d, hc, h0)
+    dd_r, dc_r, dh_r = ref.scan_backward(d, states, gout, True)
+    gbuf = torch.zeros(B * K * H * PN + offset, device=cuda_device)
+    grad = gbuf[offset:].view(B, K, H, PN)
+    grad.copy_(gout.to(cuda_device))
+    assert (grad.data_ptr() % 16 != 0) == (offset != 0)
+    d_decay = torch.empty(B, K, H, device=cuda_device)
+    d_chunk = torch.empty(B, K, H, PN, device=cuda_device)
+    d_init = torch.empty(B, H, PN, device=cuda_device)
+    _native.scan_bwd(d.to(cuda_device), states.to(cuda_device), grad, d_decay, d_chunk, d_init)
+    torch.cuda.synchronize()
+    assert max_rel(d_decay, dd_r) < FP32_TOL
+    assert max_rel(d_chunk, dc_r) < FP32_TOL
+    assert max_rel(d_init, dh_r) < FP32_TOL
+
+
 # ------------------------------------------------------------------ bf16 vs fp32 oracle
 def _bf16_pair(kw, dev, seed=0):
     torch.manual_seed(seed)
@@ -391,6 +419,42 @@ def test_bf16_d768_variants_match_fp32_oracle(extra, cuda_device):
     assert max_rel(y.float(), y_ref) < BF16_TOL
     for k in ("h", "prev_BX", "angle"):
         assert max_rel(st[k], st_ref[k]) < BF16_TOL, k
+
+
+@pytest.mark.parametrize("scale", [4.0, 32.0, 256.0])
+def test_bf16_d768_large_parameters_match_fp32_oracle(scale, cuda_device):
+    """A checkpoint with large B/C norm weights and biases and mimo_x (all multiplied by
+    `scale`). x4 stays within the (conservative) f16 operand bounds and runs on the MFMA
+    kernel; x32 and x256 exceed them, so the layer runs on the fp32 generic kernel
+    (M3_FLAG_NO_F16_OPERANDS). All match the fp32 oracle. At x256 the f16 kernel, forced
+    through the C-ABI, overflows: the scores C~.B~ reach ~1e7 before the decay mask."""
+    from mamba3_amd import ops
+    kw = dict(d_model=768, d_state=128, headdim=64, mimo_rank=2)
+    layer, cfg, _ = _bf16_pair(kw, cuda_device, seed=9)
+    with torch.no_grad():
+        for name in ("B_norm.weight", "C_norm.weight", "B_bias", "C_bias", "mimo_x"):
+            layer.get_parameter(name).mul_(scale)
+    p = {k: v.detach().float().cpu() for k, v in layer.state_dict().items()}
+    fast = ops.f16_operands_ok(layer._small_params(), 128, 2)
+    assert fast == (scale == 4.0)
+    torch.manual_seed(10)
+    x = torch.randn(1, 300, 768).to(torch.bfloat16)
+    with torch.no_grad():
+        y, st = layer.prefill(x.to(cuda_device))
+        y_ref, st_ref = ref.layer_forward(cfg, p, x.float(), return_state=True)
+    assert max_rel(y.float(), y_ref) < BF16_TOL
+    for k in ("h", "prev_BX", "angle"):
+        assert max_rel(st[k], st_ref[k]) < BF16_TOL, k
+    if scale == 256.0:
+        with torch.no_grad():
+            proj = layer.in_proj(x.to(cuda_device)).contiguous()
+            desc = layer._desc(1, 300, proj)  # flags 0: the f16 MFMA kernel
+            n = _native.prefill_workspace_bytes(desc)
+            ws = torch.empty(n, device=cuda_device, dtype=torch.uint8)
+            yf = torch.empty(1, 300, layer.d_inner, device=cuda_device, dtype=torch.bfloat16)
+            _native.prefill_fwd(desc, layer._param_pack(), proj, None, yf, None, None, None, ws, n)
+            forced = layer.out_proj(yf).float()
+        assert not (torch.isfinite(forced).all() and max_rel(forced, y_ref) < BF16_TOL)
 
 
 def test_bf16_d768_dt_scale_matches_fp32_oracle(cuda_device):
@@ -464,6 +528,60 @@ def test_bf16_decode_1024_steps_match_fp32_oracle(cuda_device):
     for k in ("h", "prev_BX", "angle"):
         assert max_rel(st_dev[k], st[k]) < BF16_TOL, k
     assert worst > 0.0
+
+
+STEP_SHAPES = [dict(d_state=48, mimo_rank=2), dict(d_state=96, mimo_rank=2),
+               dict(d_state=128, mimo_rank=8), dict(d_state=16, mimo_rank=3),
+               dict(d_state=6, mimo_rank=1), dict(d_state=130, mimo_rank=4),
+               dict(d_state=258, mimo_rank=1), dict(d_state=300, mimo_rank=2)]
+
+
+@pytest.mark.parametrize("shape", STEP_SHAPES, ids=lambda k: f"N{k['d_state']}-R{k['mimo_rank']}")
+def test_step_any_even_d_state_and_rank_matches_oracle(shape, cuda_device):
+    """The decode step for every even d_state up to 512 and every rank up to 8, as the
+    reference's step (mamba3/mamba3.py:267-322): lanes past the row end (N/4 not a power of
+    two), 2-wide column vectors (N % 4 == 2), several vectors per lane with a partial last
+    lane (N > 256), and ranks that run under a wider template. fp32 prefill of 20 tokens,
+    then 5 steps, each output and the final state against the oracle at 1e-4."""
+    kw = dict(d_model=32, headdim=16, **shape)
+    torch.manual_seed(0)
+    layer = mamba3_amd.KulaMamba(**kw)
+    p = {k: v.detach().clone() for k, v in layer.state_dict().items()}
+    layer = layer.to(cuda_device).eval()
+    cfg = oracle_cfg(kw)
+    g = torch.Generator().manual_seed(shape["d_state"] * 10 + shape["mimo_rank"])
+    x = torch.randn(2, 20, 32, generator=g)
+    with torch.no_grad():
+        _, st = layer.prefill(x.to(cuda_device))
+        _, st_ref = ref.layer_forward(cfg, p, x, return_state=True)
+        for i in range(5):
+            xt = torch.randn(2, 32, generator=g)
+            y, st = layer.step(xt.to(cuda_device), st)
+            y_ref, st_ref = ref.layer_step(cfg, p, xt, st_ref)
+            assert max_rel(y, y_ref) < FP32_TOL, i
+    for k in ("h", "prev_BX", "angle"):
+        assert max_rel(st[k], st_ref[k]) < FP32_TOL, k
+
+
+def test_bf16_step_d_state_96_matches_fp32_oracle(cuda_device):
+    """bf16 decode at d_state 96 (24 of 32 lanes per state row hold columns) and batch 16,
+    steps from a random state against the fp32 oracle."""
+    kw = dict(d_model=256, d_state=96, headdim=64, mimo_rank=2)
+    layer, cfg, p = _bf16_pair(kw, cuda_device, seed=11)
+    g = torch.Generator().manual_seed(12)
+    B, H, P, N = 16, layer.nheads, 64, 96
+    st = {"h": torch.randn(B, H, P, N, generator=g) * 0.5,
+          "prev_BX": torch.randn(B, H, P, N, generator=g) * 0.5,
+          "angle": torch.randn(B, H, N // 2, generator=g) * 3}
+    st_dev = {k: v.to(cuda_device) for k, v in st.items()}
+    for i in range(3):
+        x = torch.randn(B, 256, generator=g).to(torch.bfloat16)
+        with torch.no_grad():
+            y, st_dev = layer.step(x.to(cuda_device), st_dev)
+            y_ref, st = ref.layer_step(cfg, p, x.float(), st)
+        assert max_rel(y.float(), y_ref) < BF16_TOL
+        for k in ("h", "prev_BX", "angle"):
+            assert max_rel(st_dev[k], st[k]) < BF16_TOL, (i, k)
 
 
 def test_fp32_step_matches_oracle_from_random_state(cuda_device):
