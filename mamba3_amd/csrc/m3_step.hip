@@ -14,8 +14,11 @@
 //
 // Shapes: any even N <= 512 and mimo_rank R <= 8 (R <= RM, a template bound). VW = 4 when
 // N % 4 == 0 (16-byte rows), else 2; NV = 2 when N > 64 * VW (or N > 256 with VW = 2),
-// else 1. All loads of a lane's rows are issued before the dependent arithmetic so each
-// wave keeps up to kStepRowsPerLane rows per lane in flight. HBM-bound: 16*P*N bytes per
+// else 1. Full layouts (power-of-two N >= 4 with rank 1, 2 or 4: every lane inside the row)
+// read a lane's B / C entries, norm weights and biases as contiguous runs with wide loads;
+// the others read entry by entry, clamped into the row and masked. Every prologue load is
+// issued before the dependent arithmetic, as are all loads of a lane's rows, so each wave
+// keeps up to kStepRowsPerLane rows per lane in flight. HBM-bound: 16*P*N bytes per
 // (batch, head).
 #include "m3_common.h"
 #include "m3_kernels.h"
@@ -48,15 +51,22 @@ template <int VW> struct StepVec;
 template <> struct StepVec<4> { typedef f32x4 type; };
 template <> struct StepVec<2> { typedef float type __attribute__((ext_vector_type(2))); };
 
+// Element i of a bf16 or fp32 angle array, read as 16-bit halves so neither dtype needs a
+// branch (a bf16 element is the high half of its fp32 value; an fp32 element's halves are
+// little-endian).
 __device__ __forceinline__ float ld_angle(const void* p, int64_t i, bool is_bf16) {
-    return is_bf16 ? (float)reinterpret_cast<const bf16*>(p)[i] : reinterpret_cast<const float*>(p)[i];
+    const unsigned short* u = reinterpret_cast<const unsigned short*>(p);
+    const int64_t e = is_bf16 ? i : 2 * i;
+    const unsigned lo = u[e], hi = u[is_bf16 ? e : e + 1];
+    const unsigned sh = is_bf16 ? 16u : 0u, hmask = is_bf16 ? 0u : 0xffff0000u;
+    return __uint_as_float((lo << sh) | ((hi << 16) & hmask));
 }
 __device__ __forceinline__ void st_angle(void* p, int64_t i, float v, bool is_bf16) {
     if (is_bf16) reinterpret_cast<bf16*>(p)[i] = (bf16)v;
     else reinterpret_cast<float*>(p)[i] = v;
 }
 
-template <typename T, int RM, bool kExactR, int LPR, int VW, int NV>
+template <typename T, int RM, bool kExactR, int LPR, int VW, int NV, bool kFull>
 __global__ __launch_bounds__(kStepThreads) void step_kernel(StepArgs a) {
     typedef typename StepVec<VW>::type vec;
     constexpr int CPL = VW * NV;               // state columns per lane
@@ -71,82 +81,128 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(StepArgs a) {
     const int row0 = tid / LPR;
     const int n0 = q * CPL;
     // vectors of this lane inside the row (0: the lane is past the row end)
-    const int nvq = n0 >= N ? 0 : ((N - n0) / VW < NV ? (N - n0) / VW : NV);
+    const int nvq = kFull ? NV : n0 >= N ? 0 : ((N - n0) / VW < NV ? (N - n0) / VW : NV);
     const T* pr = reinterpret_cast<const T*>(a.proj) + (int64_t)b * a.row_stride;
 
+    // Prologue loads, all unconditional and issued as one flight before the arithmetic:
+    // absent inputs, and entries past the row end or the rank, read a valid element and are
+    // blended out arithmetically (a select on a loaded value lets the compiler move the load
+    // under a branch, which serialises the flight).
+    constexpr int NPL = CPL / 2;  // column pairs per lane
+    const float dt_raw = ld_f32(pr + a.pl.dt + h);
+    const float trapf = a.trap ? 1.f : 0.f;
+    const float lam_raw = ld_f32(pr + (a.trap ? a.pl.lam + h : 0));
+    const float scf = a.dt_scale ? 1.f : 0.f;
+    const float sc_raw = *(a.dt_scale ? a.dt_scale + (int64_t)b * a.H + h : a.prm.dt_bias + h);
+    const float A_log = a.prm.A_log[h], dt_bias = a.prm.dt_bias[h];
+    // running angle and theta of the lane's column pairs (pairs past the row end read pair
+    // 0; without complex RoPE theta reads element 0 of the row and is unused)
+    const int64_t abase = ((int64_t)b * a.H + h) * Nh;
+    const bool abf = a.angle_bf16 != 0;
+    float ang[NPL], th[NPL];
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) {
+        const int i = 2 * j < nvq * VW ? n0 / 2 + j : 0;
+        ang[j] = ld_angle(a.angle_in, abase + i, abf);
+        th[j] = ld_f32(pr + (a.cplx ? a.pl.theta + i : 0));
+    }
+    // B, C columns n0 .. n0 + CPL - 1, with their norm weights and biases when the lane
+    // holds at most 16 entries (more would cost occupancy; those load them below). In the
+    // full layouts (every lane's columns inside the row, the rank a compile-time constant:
+    // every power-of-two d_state >= 4 with rank 1, 2 or 4) a lane's CPL * RM entries are one
+    // contiguous run from n0 * RM, which the compiler reads with wide loads; otherwise each
+    // entry is read on its own, clamped into the row.
+    constexpr bool kPreW = CPL * RM <= 16;
+    constexpr int WD = kPreW ? CPL : 1, WR = kPreW ? RM : 1;
+    float Bv[CPL][RM], Cv[CPL][RM], msk[CPL][RM];
+    float wb[WD][WR], wc[WD][WR], bb[WD][WR], bc[WD][WR];
+    const T* Braw = pr + a.pl.B + (int64_t)g * NR;
+    const T* Craw = pr + a.pl.C + (int64_t)g * NR;
+    const float* bB = a.prm.B_bias + (int64_t)g * NR;
+    const float* bC = a.prm.C_bias + (int64_t)g * NR;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+#pragma unroll
+        for (int r = 0; r < RM; ++r) {
+            bool ok;
+            int o;
+            if constexpr (kFull) {
+                ok = true;
+                o = n0 * RM + j * RM + r;
+            } else {
+                ok = j < nvq * VW && r < R;
+                o = ok ? (n0 + j) * R + r : 0;
+            }
+            msk[j][r] = ok ? 1.f : 0.f;
+            Bv[j][r] = ld_f32(Braw + o);
+            Cv[j][r] = ld_f32(Craw + o);
+            if constexpr (kPreW) {
+                wb[j][r] = a.prm.B_norm_w[o];
+                wc[j][r] = a.prm.C_norm_w[o];
+                bb[j][r] = bB[o];
+                bc[j][r] = bC[o];
+            }
+        }
+    }
+
     // Per-head scalars (mamba3/mamba3.py:278-282, 290-296).
-    const float Ah = -expf(a.prm.A_log[h]);
-    const float sc = a.dt_scale ? a.dt_scale[(int64_t)b * a.H + h] : 1.f;
-    const TokenGate tg = token_gate(ld_f32(pr + a.pl.dt + h), a.prm.dt_bias[h], sc, Ah,
-                                    a.trap ? ld_f32(pr + a.pl.lam + h) : 0.f, a.trap != 0);
+    const float sc = sc_raw * scf + (1.f - scf);
+    const TokenGate tg = token_gate(dt_raw, dt_bias, sc, -expf(A_log), lam_raw * trapf, a.trap != 0);
     const float dA = expf(tg.logdA);
     const float gamma = a.trap ? tg.lam * tg.dt : tg.dt;
     const float beta = a.trap ? (1.f - tg.lam) * tg.dt * dA : 0.f;
 
-    // B~, C~ for columns n0 .. n0 + CPL - 1 (mamba3/mamba3.py:170-190).
-    float Bv[CPL][RM], Cv[CPL][RM];
+    // B~, C~: RMSNorm over the group's N*R entries, weight and bias (mamba3/mamba3.py:170-184)
     float ssb = 0.f, ssc = 0.f;
-    const T* Braw = pr + a.pl.B + (int64_t)g * NR + (int64_t)n0 * R;
-    const T* Craw = pr + a.pl.C + (int64_t)g * NR + (int64_t)n0 * R;
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-        const bool live = j < nvq * VW;
+    for (int j = 0; j < CPL; ++j)
 #pragma unroll
         for (int r = 0; r < RM; ++r) {
-            const bool ok = live && r < R;
-            Bv[j][r] = ok ? ld_f32(Braw + j * R + r) : 0.f;
-            Cv[j][r] = ok ? ld_f32(Craw + j * R + r) : 0.f;
+            Bv[j][r] *= msk[j][r];
+            Cv[j][r] *= msk[j][r];
             ssb += Bv[j][r] * Bv[j][r];
             ssc += Cv[j][r] * Cv[j][r];
         }
-    }
     ssb = group_sum<LPR>(ssb);
     ssc = group_sum<LPR>(ssc);
     const float rb = rsqrtf(ssb / NR + a.eps), rc = rsqrtf(ssc / NR + a.eps);
-    const float* wB = a.prm.B_norm_w + (int64_t)n0 * R;
-    const float* wC = a.prm.C_norm_w + (int64_t)n0 * R;
-    const float* bB = a.prm.B_bias + (int64_t)g * NR + (int64_t)n0 * R;
-    const float* bC = a.prm.C_bias + (int64_t)g * NR + (int64_t)n0 * R;
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-        const bool live = j < nvq * VW;
 #pragma unroll
         for (int r = 0; r < RM; ++r) {
-            if (live && r < R) {
-                Bv[j][r] = Bv[j][r] * rb * wB[j * R + r] + bB[j * R + r];
-                Cv[j][r] = Cv[j][r] * rc * wC[j * R + r] + bC[j * R + r];
+            if constexpr (kPreW) {
+                Bv[j][r] = (Bv[j][r] * rb * wb[j][r] + bb[j][r]) * msk[j][r];
+                Cv[j][r] = (Cv[j][r] * rc * wc[j][r] + bc[j][r]) * msk[j][r];
+            } else {
+                const int o = j < nvq * VW && r < R ? (n0 + j) * R + r : 0;
+                Bv[j][r] = (Bv[j][r] * rb * a.prm.B_norm_w[o] + bB[o]) * msk[j][r];
+                Cv[j][r] = (Cv[j][r] * rc * a.prm.C_norm_w[o] + bC[o]) * msk[j][r];
             }
         }
     }
-    const int64_t abase = ((int64_t)b * a.H + h) * Nh;
-    const bool abf = a.angle_bf16 != 0;
     if (a.cplx) {
 #pragma unroll
-        for (int j = 0; j < CPL / 2; ++j) {
-            if (2 * j < nvq * VW) {
-                const int i = n0 / 2 + j;
-                const float phi = ld_angle(a.angle_in, abase + i, abf) - tg.dt * ld_f32(pr + a.pl.theta + i);
-                if (row0 == 0) st_angle(a.angle_out, abase + i, phi, abf);
-                float sn, cs;
-                sincosf(phi, &sn, &cs);
+        for (int j = 0; j < NPL; ++j) {
+            // pairs past the row end rotate zero columns and store nothing
+            const float phi = ang[j] - tg.dt * th[j];
+            if (row0 == 0 && 2 * j < nvq * VW) st_angle(a.angle_out, abase + n0 / 2 + j, phi, abf);
+            float sn, cs;
+            sincosf(phi, &sn, &cs);
 #pragma unroll
-                for (int r = 0; r < RM; ++r) {
-                    const float be = Bv[2 * j][r], bo = Bv[2 * j + 1][r];
-                    Bv[2 * j][r] = be * cs - bo * sn;
-                    Bv[2 * j + 1][r] = be * sn + bo * cs;
-                    const float ce = Cv[2 * j][r], co = Cv[2 * j + 1][r];
-                    Cv[2 * j][r] = ce * cs - co * sn;
-                    Cv[2 * j + 1][r] = ce * sn + co * cs;
-                }
+            for (int r = 0; r < RM; ++r) {
+                const float be = Bv[2 * j][r], bo = Bv[2 * j + 1][r];
+                Bv[2 * j][r] = be * cs - bo * sn;
+                Bv[2 * j + 1][r] = be * sn + bo * cs;
+                const float ce = Cv[2 * j][r], co = Cv[2 * j + 1][r];
+                Cv[2 * j][r] = ce * cs - co * sn;
+                Cv[2 * j + 1][r] = ce * sn + co * cs;
             }
         }
-    } else if (row0 == 0 && a.angle_out) {
+    } else if (row0 == 0) {
         // Angle stays zero without complex RoPE; pass the input through.
-        for (int j = 0; j < CPL / 2; ++j)
-            if (2 * j < nvq * VW) {
-                const int i = n0 / 2 + j;
-                st_angle(a.angle_out, abase + i, ld_angle(a.angle_in, abase + i, abf), abf);
-            }
+#pragma unroll
+        for (int j = 0; j < NPL; ++j)
+            if (2 * j < nvq * VW) st_angle(a.angle_out, abase + n0 / 2 + j, ang[j], abf);
     }
 
     const float Dh = a.prm.D[h];
@@ -164,21 +220,21 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(StepArgs a) {
 
     for (int pbase = row0; pbase < P; pbase += kRows * kStepRowsPerLane) {
         vec hv[kStepRowsPerLane][NV], pv[kStepRowsPerLane][NV];
-        float xv[kStepRowsPerLane];
+        T xv[kStepRowsPerLane];
+        // Streaming reads of the incoming state (the outgoing state is stored normally so
+        // the next step finds it in the caches). All loads are unconditional and issued
+        // before the arithmetic: rows past P read row P - 1 and lanes past the row end read
+        // the row's last vector (their B / C columns are zero); neither stores anything.
 #pragma unroll
         for (int it = 0; it < kStepRowsPerLane; ++it) {
-            const int p = pbase + it * kRows;
-            if (p < P) {
-                // streaming reads of the incoming state; the outgoing state is stored
-                // normally so the next step finds it in the caches
+            const int p = pbase + it * kRows < P ? pbase + it * kRows : P - 1;
 #pragma unroll
-                for (int v = 0; v < NV; ++v)
-                    if (v < nvq) {
-                        hv[it][v] = __builtin_nontemporal_load(&hin[p * nvr + v0 + v]);
-                        pv[it][v] = __builtin_nontemporal_load(&pin[p * nvr + v0 + v]);
-                    }
-                xv[it] = ld_f32(pr + a.pl.x + (int64_t)h * P + p);
+            for (int v = 0; v < NV; ++v) {
+                const int vi = v0 + v < nvr ? v0 + v : nvr - 1;
+                hv[it][v] = __builtin_nontemporal_load(&hin[p * nvr + vi]);
+                pv[it][v] = __builtin_nontemporal_load(&pin[p * nvr + vi]);
             }
+            xv[it] = pr[a.pl.x + (int64_t)h * P + p];
         }
 #pragma unroll
         for (int it = 0; it < kStepRowsPerLane; ++it) {
@@ -186,25 +242,25 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(StepArgs a) {
             if (p < P) {
                 float xr[RM];
 #pragma unroll
-                for (int r = 0; r < RM; ++r) xr[r] = r < R ? xv[it] * mx[p * R + r] : 0.f;
+                for (int r = 0; r < RM; ++r) xr[r] = r < R ? (float)xv[it] * mx[p * R + r] : 0.f;
                 float yacc[RM];
 #pragma unroll
                 for (int r = 0; r < RM; ++r) yacc[r] = 0.f;
 #pragma unroll
                 for (int v = 0; v < NV; ++v) {
+                    vec cur, hn;
+#pragma unroll
+                    for (int e = 0; e < VW; ++e) {
+                        const int j = v * VW + e;
+                        float c = 0.f;
+#pragma unroll
+                        for (int r = 0; r < RM; ++r) c += Bv[j][r] * xr[r];
+                        cur[e] = c;
+                        hn[e] = dA * hv[it][v][e] + gamma * c + beta * pv[it][v][e];
+#pragma unroll
+                        for (int r = 0; r < RM; ++r) yacc[r] += Cv[j][r] * hn[e];
+                    }
                     if (v < nvq) {
-                        vec cur, hn;
-#pragma unroll
-                        for (int e = 0; e < VW; ++e) {
-                            const int j = v * VW + e;
-                            float c = 0.f;
-#pragma unroll
-                            for (int r = 0; r < RM; ++r) c += Bv[j][r] * xr[r];
-                            cur[e] = c;
-                            hn[e] = dA * hv[it][v][e] + gamma * c + beta * pv[it][v][e];
-#pragma unroll
-                            for (int r = 0; r < RM; ++r) yacc[r] += Cv[j][r] * hn[e];
-                        }
                         hout[p * nvr + v0 + v] = hn;
                         pout[p * nvr + v0 + v] = cur;
                     }
@@ -244,44 +300,58 @@ static void step_layout(int N, int& vw, int& nv, int& lpr) {
 
 // Reachable layouts: one vector per lane for any power-of-two lane count (N <= 64 VW);
 // several vectors per lane only with all 64 lanes (N > 256, or N > 128 with VW = 2).
-template <typename T, int RM, bool kX, int VW>
+template <typename T, int RM, bool kX, int VW, bool kF>
 static void launch_step_l(int lpr, dim3 grid, hipStream_t stream, const StepArgs& a) {
     switch (lpr) {
-        case 1: hipLaunchKernelGGL((step_kernel<T, RM, kX, 1, VW, 1>), grid, dim3(kStepThreads), 0, stream, a); break;
-        case 2: hipLaunchKernelGGL((step_kernel<T, RM, kX, 2, VW, 1>), grid, dim3(kStepThreads), 0, stream, a); break;
-        case 4: hipLaunchKernelGGL((step_kernel<T, RM, kX, 4, VW, 1>), grid, dim3(kStepThreads), 0, stream, a); break;
-        case 8: hipLaunchKernelGGL((step_kernel<T, RM, kX, 8, VW, 1>), grid, dim3(kStepThreads), 0, stream, a); break;
-        case 16: hipLaunchKernelGGL((step_kernel<T, RM, kX, 16, VW, 1>), grid, dim3(kStepThreads), 0, stream, a); break;
-        case 32: hipLaunchKernelGGL((step_kernel<T, RM, kX, 32, VW, 1>), grid, dim3(kStepThreads), 0, stream, a); break;
-        default: hipLaunchKernelGGL((step_kernel<T, RM, kX, 64, VW, 1>), grid, dim3(kStepThreads), 0, stream, a); break;
+        case 1: hipLaunchKernelGGL((step_kernel<T, RM, kX, 1, VW, 1, kF>), grid, dim3(kStepThreads), 0, stream, a); break;
+        case 2: hipLaunchKernelGGL((step_kernel<T, RM, kX, 2, VW, 1, kF>), grid, dim3(kStepThreads), 0, stream, a); break;
+        case 4: hipLaunchKernelGGL((step_kernel<T, RM, kX, 4, VW, 1, kF>), grid, dim3(kStepThreads), 0, stream, a); break;
+        case 8: hipLaunchKernelGGL((step_kernel<T, RM, kX, 8, VW, 1, kF>), grid, dim3(kStepThreads), 0, stream, a); break;
+        case 16: hipLaunchKernelGGL((step_kernel<T, RM, kX, 16, VW, 1, kF>), grid, dim3(kStepThreads), 0, stream, a); break;
+        case 32: hipLaunchKernelGGL((step_kernel<T, RM, kX, 32, VW, 1, kF>), grid, dim3(kStepThreads), 0, stream, a); break;
+        default: hipLaunchKernelGGL((step_kernel<T, RM, kX, 64, VW, 1, kF>), grid, dim3(kStepThreads), 0, stream, a); break;
     }
 }
 
-// Reachable layouts: one vector per lane for any power-of-two lane count (N <= 64 VW);
-// several vectors per lane only with all 64 lanes (N > 256, or N > 128 with VW = 2).
 template <typename T, int RM, bool kX>
 static void launch_step_v(int vw, int nv, int lpr, dim3 grid, hipStream_t stream, const StepArgs& a) {
     if (nv == 1) {
-        if (vw == 4) launch_step_l<T, RM, kX, 4>(lpr, grid, stream, a);
-        else launch_step_l<T, RM, kX, 2>(lpr, grid, stream, a);
+        if (vw == 4) launch_step_l<T, RM, kX, 4, false>(lpr, grid, stream, a);
+        else launch_step_l<T, RM, kX, 2, false>(lpr, grid, stream, a);
     } else if (vw == 4) {
-        hipLaunchKernelGGL((step_kernel<T, RM, kX, 64, 4, 2>), grid, dim3(kStepThreads), 0, stream, a);
+        hipLaunchKernelGGL((step_kernel<T, RM, kX, 64, 4, 2, false>), grid, dim3(kStepThreads), 0, stream, a);
     } else if (nv == 2) {
-        hipLaunchKernelGGL((step_kernel<T, RM, kX, 64, 2, 2>), grid, dim3(kStepThreads), 0, stream, a);
+        hipLaunchKernelGGL((step_kernel<T, RM, kX, 64, 2, 2, false>), grid, dim3(kStepThreads), 0, stream, a);
     } else {
-        hipLaunchKernelGGL((step_kernel<T, RM, kX, 64, 2, 4>), grid, dim3(kStepThreads), 0, stream, a);
+        hipLaunchKernelGGL((step_kernel<T, RM, kX, 64, 2, 4, false>), grid, dim3(kStepThreads), 0, stream, a);
     }
+}
+
+// Full layouts (4-column vectors, every lane inside the row, exact rank).
+template <typename T, int RM>
+static void launch_step_full(int nv, int lpr, dim3 grid, hipStream_t stream, const StepArgs& a) {
+    if (nv == 2) hipLaunchKernelGGL((step_kernel<T, RM, true, 64, 4, 2, true>), grid, dim3(kStepThreads), 0, stream, a);
+    else launch_step_l<T, RM, true, 4, true>(lpr, grid, stream, a);
 }
 
 // Ranks 1, 2 and 4 are compile-time constants; the others run under RM = 8 with the rank
 // as a run-time bound.
 template <typename T>
-static void launch_step_t(int R, int vw, int nv, int lpr, dim3 grid, hipStream_t stream,
+static void launch_step_t(int N, int R, int vw, int nv, int lpr, dim3 grid, hipStream_t stream,
                           const StepArgs& a) {
-    if (R == 1) launch_step_v<T, 1, true>(vw, nv, lpr, grid, stream, a);
-    else if (R == 2) launch_step_v<T, 2, true>(vw, nv, lpr, grid, stream, a);
-    else if (R == 4) launch_step_v<T, 4, true>(vw, nv, lpr, grid, stream, a);
-    else launch_step_v<T, 8, false>(vw, nv, lpr, grid, stream, a);
+    const bool full = vw == 4 && N == lpr * vw * nv;
+    if (R == 1) {
+        if (full) launch_step_full<T, 1>(nv, lpr, grid, stream, a);
+        else launch_step_v<T, 1, true>(vw, nv, lpr, grid, stream, a);
+    } else if (R == 2) {
+        if (full) launch_step_full<T, 2>(nv, lpr, grid, stream, a);
+        else launch_step_v<T, 2, true>(vw, nv, lpr, grid, stream, a);
+    } else if (R == 4) {
+        if (full) launch_step_full<T, 4>(nv, lpr, grid, stream, a);
+        else launch_step_v<T, 4, true>(vw, nv, lpr, grid, stream, a);
+    } else {
+        launch_step_v<T, 8, false>(vw, nv, lpr, grid, stream, a);
+    }
 }
 
 int launch_step(const m3_layer_desc& d, const m3_layer_params& p, const void* proj,
@@ -301,8 +371,8 @@ int launch_step(const m3_layer_desc& d, const m3_layer_params& p, const void* pr
     int vw, nv, lpr;
     step_layout(d.d_state, vw, nv, lpr);
     const dim3 grid((unsigned)(d.batch * d.nheads));
-    if (d.dtype == M3_DTYPE_BF16) launch_step_t<bf16>(d.mimo_rank, vw, nv, lpr, grid, stream, a);
-    else launch_step_t<float>(d.mimo_rank, vw, nv, lpr, grid, stream, a);
+    if (d.dtype == M3_DTYPE_BF16) launch_step_t<bf16>(d.d_state, d.mimo_rank, vw, nv, lpr, grid, stream, a);
+    else launch_step_t<float>(d.d_state, d.mimo_rank, vw, nv, lpr, grid, stream, a);
     return hipGetLastError() == hipSuccess ? M3_OK : M3_ERR_LAUNCH;
 }
 
