@@ -276,6 +276,33 @@ int m3_chunked_ssd_bwd(int32_t batch, int32_t seqlen, int32_t nheads, int32_t he
                        float* dx_raw, float* dh_init, void* workspace, size_t workspace_bytes,
                        void* stream);
 
+/*
+ * RMSNorm of the residual blocks in one pass over the activations. Replaces the reference's
+ * RMSNorm.forward (mamba3/mamba3.py:19-35) as used by KulaMambaBlock / KulaMambaLM
+ * (mamba3/block.py:45-72, 138-140, 182), which runs it as several element-wise ATen ops.
+ *   s[r] = rsqrt(mean_j x[r,j]^2 + eps)            (fp32)
+ *   y[r,j] = (x[r,j] * s[r]) * weight[j]            the scale and x*s rounded to x's dtype,
+ *                                                  as the reference does
+ * x [rows, d] in x_dtype; weight [d] in w_dtype; y [rows, d] in y_dtype, which must be bf16
+ * when both x and weight are bf16 and fp32 otherwise (the promotion of the two); rstd [rows]
+ * fp32 or NULL (s, kept for the backward). 0 < rows < 2^33, 0 < d <= 2^24.
+ */
+int m3_rmsnorm_fwd(const void* x, int x_dtype, const void* weight, int w_dtype, void* y,
+                   int y_dtype, float* rstd, int64_t rows, int32_t d, float eps, void* stream);
+
+/*
+ * Backward of m3_rmsnorm_fwd (the reference differentiates it through ATen), fp32
+ * arithmetic: with g = dL/dy (grad_dtype = the forward's y_dtype) and a = sum_j w_j g_j x_j,
+ *   dx = s w g - x s^3 a / d   (x_dtype)     dweight = sum_rows g x s   (w_dtype)
+ * dweight is summed in a fixed order (deterministic). workspace:
+ * m3_rmsnorm_bwd_workspace_size() bytes, 256-byte aligned.
+ */
+int m3_rmsnorm_bwd_workspace_size(int64_t rows, int32_t d, size_t* bytes);
+int m3_rmsnorm_bwd(const void* x, int x_dtype, const void* weight, int w_dtype,
+                   const float* rstd, const void* grad, int grad_dtype, void* dx, void* dweight,
+                   void* workspace, size_t workspace_bytes, int64_t rows, int32_t d,
+                   void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -37,6 +37,9 @@ EXPORTED_SYMBOLS = (
     "m3_layer_bwd_workspace_size",
     "m3_layer_bwd",
     "m3_prefill_fwd_noalloc",
+    "m3_rmsnorm_fwd",
+    "m3_rmsnorm_bwd_workspace_size",
+    "m3_rmsnorm_bwd",
 )
 
 M3_ERR_SCRATCH_LIMIT = 8
@@ -107,6 +110,14 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.m3_prefill_fwd_noalloc.restype = ctypes.c_int
     lib.m3_prefill_fwd_noalloc.argtypes = [ctypes.POINTER(LayerDesc), ctypes.POINTER(LayerParams),
                                            _vp, _vp, _vp, _vp, _vp, _vp, _vp]
+    lib.m3_rmsnorm_fwd.restype = ctypes.c_int
+    lib.m3_rmsnorm_fwd.argtypes = [_vp, ctypes.c_int, _vp, ctypes.c_int, _vp, ctypes.c_int, _vp,
+                                   _i64, _i32, ctypes.c_float, _vp]
+    lib.m3_rmsnorm_bwd_workspace_size.restype = ctypes.c_int
+    lib.m3_rmsnorm_bwd_workspace_size.argtypes = [_i64, _i32, ctypes.POINTER(ctypes.c_size_t)]
+    lib.m3_rmsnorm_bwd.restype = ctypes.c_int
+    lib.m3_rmsnorm_bwd.argtypes = [_vp, ctypes.c_int, _vp, ctypes.c_int, _vp, _vp, ctypes.c_int,
+                                   _vp, _vp, _vp, ctypes.c_size_t, _i64, _i32, _vp]
     lib.m3_step_fwd.restype = ctypes.c_int
     lib.m3_step_fwd.argtypes = [ctypes.POINTER(LayerDesc), ctypes.POINTER(LayerParams),
                                 _vp, _vp, _vp, _vp, _vp, ctypes.c_int, _vp, _vp, _vp, _vp, _vp]
@@ -294,3 +305,22 @@ def layer_bwd(desc: LayerDesc, params: LayerParams, proj, dt_scale, fwd_ws, g_ou
                              ptr(g_prev), ptr(g_proj), ctypes.byref(grads), ptr(ws), n,
                              stream_of(proj)),
           "m3_layer_bwd")
+
+
+def rmsnorm_fwd(x, weight, y, rstd, eps: float) -> None:
+    """m3_rmsnorm_fwd on contiguous x (rows, d)."""
+    rows, d = x.shape
+    check(lib().m3_rmsnorm_fwd(ptr(x), dtype_code(x.dtype), ptr(weight), dtype_code(weight.dtype),
+                               ptr(y), dtype_code(y.dtype), ptr(rstd), rows, d, eps,
+                               stream_of(x)), "m3_rmsnorm_fwd")
+
+
+def rmsnorm_bwd(x, weight, rstd, grad, dx, dweight) -> None:
+    """m3_rmsnorm_bwd on contiguous (rows, d) tensors; allocates the workspace."""
+    rows, d = x.shape
+    n = ctypes.c_size_t(0)
+    check(lib().m3_rmsnorm_bwd_workspace_size(rows, d, ctypes.byref(n)), "m3_rmsnorm_bwd_workspace_size")
+    ws = torch.empty(max(n.value, 1), dtype=torch.uint8, device=x.device)
+    check(lib().m3_rmsnorm_bwd(ptr(x), dtype_code(x.dtype), ptr(weight), dtype_code(weight.dtype),
+                               ptr(rstd), ptr(grad), dtype_code(grad.dtype), ptr(dx), ptr(dweight),
+                               ptr(ws), n.value, rows, d, stream_of(x)), "m3_rmsnorm_bwd")

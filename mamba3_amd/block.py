@@ -20,6 +20,18 @@ from . import ops
 from .layer import KulaMamba, RMSNorm
 
 
+def add_scaled_linear(x: torch.Tensor, lin: nn.Linear, inp: torch.Tensor, scale: float) -> torch.Tensor:
+    """x + scale * lin(inp) as one GEMM: the residual x enters hipBLASLt as C with beta = 1
+    and the scale as alpha, so the projection's output is neither rounded nor stored before
+    the add (the reference runs the projection, the scale and the add as three ops,
+    mamba3/block.py:84-91)."""
+    out = torch.addmm(x.reshape(-1, x.shape[-1]), inp.reshape(-1, inp.shape[-1]), lin.weight.t(),
+                      beta=1.0, alpha=scale)
+    if lin.bias is not None:
+        out = out + lin.bias * scale
+    return out.view(x.shape)
+
+
 class SwiGLU(nn.Module):
     """w_down(silu(w_gate x) * w_up x) (mamba3/block.py:16-26)."""
 
@@ -31,8 +43,12 @@ class SwiGLU(nn.Module):
         self.w_up = nn.Linear(d_model, d_ff, bias=bias)
         self.w_down = nn.Linear(d_ff, d_model, bias=bias)
 
+    def hidden(self, x: torch.Tensor) -> torch.Tensor:
+        """silu(w_gate x) * w_up x: w_down's input."""
+        return F.silu(self.w_gate(x)) * self.w_up(x)
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return self.w_down(F.silu(self.w_gate(x)) * self.w_up(x))
+        return self.w_down(self.hidden(x))
 
 
 class KulaMambaBlock(nn.Module):
@@ -78,33 +94,40 @@ class KulaMambaBlock(nn.Module):
     def _mlp_forward(self, x_normed):
         return self.mlp(x_normed)
 
+    # The residual adds run as the beta = 1 input of the out_proj / w_down GEMMs
+    # (add_scaled_linear); with gradient checkpointing the branches are recomputed whole.
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         ckpt = self.gradient_checkpointing and self.training
         if ckpt:
             h = grad_checkpoint(self._ssm_forward, self.ssm_norm(x), use_reentrant=False)
+            x = x + h * self.residual_scale
         else:
-            h = self.ssm(self.ssm_norm(x))
-        x = x + h * self.residual_scale
+            y, _ = self.ssm._pre_out(self.ssm_norm(x))
+            x = add_scaled_linear(x, self.ssm.out_proj, y, self.residual_scale)
         if self.use_mlp:
             if ckpt:
                 m = grad_checkpoint(self._mlp_forward, self.mlp_norm(x), use_reentrant=False)
+                x = x + m * self.residual_scale
             else:
-                m = self.mlp(self.mlp_norm(x))
-            x = x + m * self.residual_scale
+                x = self._mlp_residual(x)
         return x
 
+    def _mlp_residual(self, x: torch.Tensor) -> torch.Tensor:
+        return add_scaled_linear(x, self.mlp.w_down, self.mlp.hidden(self.mlp_norm(x)),
+                                 self.residual_scale)
+
     def step(self, x: torch.Tensor, ssm_state: dict):
-        h, new_state = self.ssm.step(self.ssm_norm(x), ssm_state)
-        x = x + h * self.residual_scale
+        y, new_state = self.ssm._step_pre_out(self.ssm_norm(x), ssm_state)
+        x = add_scaled_linear(x, self.ssm.out_proj, y.view(*x.shape[:-1], -1), self.residual_scale)
         if self.use_mlp:
-            x = x + self.mlp(self.mlp_norm(x)) * self.residual_scale
+            x = self._mlp_residual(x)
         return x, new_state
 
     def prefill(self, x: torch.Tensor):
-        h, state = self.ssm.prefill(self.ssm_norm(x))
-        x = x + h * self.residual_scale
+        y, state = self.ssm._pre_out(self.ssm_norm(x), return_state=True)
+        x = add_scaled_linear(x, self.ssm.out_proj, y, self.residual_scale)
         if self.use_mlp:
-            x = x + self.mlp(self.mlp_norm(x)) * self.residual_scale
+            x = self._mlp_residual(x)
         return x, state
 
 
@@ -226,9 +249,9 @@ def _block_step_into(block: KulaMambaBlock, x: torch.Tensor, st_in: dict, st_out
     ops.step_into(proj, *ssm._small_params(), None, st_in["h"], st_in["prev_BX"],
                   st_in["angle"], y, st_out["h"], st_out["prev_BX"], st_out["angle"],
                   *ops.layer_args(ssm))
-    x = x + ssm.out_proj(y) * block.residual_scale
+    x = add_scaled_linear(x, ssm.out_proj, y, block.residual_scale)
     if block.use_mlp:
-        x = x + block.mlp(block.mlp_norm(x)) * block.residual_scale
+        x = block._mlp_residual(x)
     return x
 
 

@@ -305,6 +305,52 @@ int m3_step_fwd(const m3_layer_desc* desc, const m3_layer_params* params, const 
                            as_stream(stream));
 }
 
+static bool norm_dtypes_ok(int xd, int wd, int yd) {
+    auto ok = [](int t) { return t == M3_DTYPE_F32 || t == M3_DTYPE_BF16; };
+    if (!ok(xd) || !ok(wd) || !ok(yd)) return false;
+    // the output dtype is the promotion of the activation and weight dtypes
+    return yd == ((xd == M3_DTYPE_BF16 && wd == M3_DTYPE_BF16) ? M3_DTYPE_BF16 : M3_DTYPE_F32);
+}
+
+// Grid limits of the norm kernels: rows / 4 blocks (x) forward, d / 256 column blocks (y)
+// for the dweight partials.
+static bool norm_shape_ok(int64_t rows, int32_t d) {
+    return rows > 0 && rows < ((int64_t)1 << 33) && d > 0 && d <= (1 << 24);
+}
+
+int m3_rmsnorm_fwd(const void* x, int x_dtype, const void* weight, int w_dtype, void* y,
+                   int y_dtype, float* rstd, int64_t rows, int32_t d, float eps, void* stream) {
+    if (!x || !weight || !y) return M3_ERR_NULL_POINTER;
+    if (!norm_shape_ok(rows, d) || !(eps >= 0.f)) return M3_ERR_INVALID_SHAPE;
+    if (!norm_dtypes_ok(x_dtype, w_dtype, y_dtype)) return M3_ERR_UNSUPPORTED;
+    return m3::launch_rmsnorm_fwd(x, x_dtype, weight, w_dtype, y, y_dtype, rstd, rows, d, eps,
+                                  as_stream(stream)) == 0
+               ? M3_OK
+               : M3_ERR_LAUNCH;
+}
+
+int m3_rmsnorm_bwd_workspace_size(int64_t rows, int32_t d, size_t* bytes) {
+    if (!bytes) return M3_ERR_NULL_POINTER;
+    if (!norm_shape_ok(rows, d)) return M3_ERR_INVALID_SHAPE;
+    *bytes = m3::rmsnorm_bwd_workspace(rows, d);
+    return M3_OK;
+}
+
+int m3_rmsnorm_bwd(const void* x, int x_dtype, const void* weight, int w_dtype,
+                   const float* rstd, const void* grad, int grad_dtype, void* dx, void* dweight,
+                   void* workspace, size_t workspace_bytes, int64_t rows, int32_t d,
+                   void* stream) {
+    if (!x || !weight || !rstd || !grad || !dx || !dweight) return M3_ERR_NULL_POINTER;
+    if (!norm_shape_ok(rows, d)) return M3_ERR_INVALID_SHAPE;
+    if (!norm_dtypes_ok(x_dtype, w_dtype, grad_dtype)) return M3_ERR_UNSUPPORTED;
+    if (!workspace || workspace_bytes < m3::rmsnorm_bwd_workspace(rows, d)) return M3_ERR_WORKSPACE;
+    if (!aligned(workspace, 256)) return M3_ERR_MISALIGNED;
+    return m3::launch_rmsnorm_bwd(x, x_dtype, weight, w_dtype, rstd, grad, grad_dtype, dx,
+                                  dweight, workspace, rows, d, as_stream(stream)) == 0
+               ? M3_OK
+               : M3_ERR_LAUNCH;
+}
+
 int m3_chunked_ssd_fwd_workspace_size(int32_t batch, int32_t seqlen, int32_t nheads,
                                       int32_t headdim, int32_t d_state, int32_t mimo_rank,
                                       int32_t dtype, int32_t has_beta, size_t* bytes) {

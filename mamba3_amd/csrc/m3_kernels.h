@@ -111,6 +111,15 @@ int launch_layer_bwd(const m3_layer_desc& d, const m3_layer_params& p, const voi
                      const float* g_h, const float* g_angle, const float* g_prev, float* g_proj,
                      const m3_layer_param_grads& g, void* workspace, hipStream_t stream);
 
+// Block RMSNorm (m3_norm.hip): forward, and backward workspace bytes and launcher.
+int launch_rmsnorm_fwd(const void* x, int xdtype, const void* w, int wdtype, void* y,
+                       int ydtype, float* rstd, int64_t rows, int d, float eps,
+                       hipStream_t stream);
+size_t rmsnorm_bwd_workspace(int64_t rows, int d);
+int launch_rmsnorm_bwd(const void* x, int xdtype, const void* w, int wdtype, const float* rstd,
+                       const void* g, int gdtype, void* dx, void* dw, void* workspace,
+                       int64_t rows, int d, hipStream_t stream);
+
 // Returns 1 when the step kernel supports (N, R), else 0.
 int step_supported(int N, int R);
 int launch_step(const m3_layer_desc& d, const m3_layer_params& p, const void* proj,

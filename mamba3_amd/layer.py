@@ -24,9 +24,11 @@ from . import _native, ops
 class RMSNorm(nn.Module):
     """Root-mean-square norm with learned scale (mamba3/mamba3.py:19-35).
 
-    Used as a PyTorch op by the block/LM glue; inside KulaMamba only its weight is read
-    (the B/C normalisation itself runs in the HIP kernels).
-    """
+    The block / LM norms run as one HIP kernel pass (m3_rmsnorm_fwd, backward
+    m3_rmsnorm_bwd) with the reference's arithmetic: fp32 statistics, the scale and x*scale
+    rounded to x's dtype. Inside KulaMamba only B_norm / C_norm's weights are read (that
+    normalisation is fused into the SSD kernels). GPU tensors only, like the rest of the
+    package."""
 
     def __init__(self, d: int, eps: float = 1e-5, dim: int = -1):
         super().__init__()
@@ -35,10 +37,13 @@ class RMSNorm(nn.Module):
         self.dim = dim
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        scale = torch.rsqrt(x.float().square().mean(self.dim, keepdim=True) + self.eps)
-        shape = [1] * x.ndim
-        shape[self.dim] = -1
-        return x * scale.to(x.dtype) * self.weight.view(*shape)
+        _native.require_gpu(x)
+        d = self.dim % x.ndim
+        if d != x.ndim - 1:
+            y, _ = ops.rmsnorm(x.movedim(d, -1), self.weight, float(self.eps))
+            return y.movedim(-1, d)
+        y, _ = ops.rmsnorm(x, self.weight, float(self.eps))
+        return y
 
 
 class KulaMamba(nn.Module):
@@ -145,14 +150,18 @@ class KulaMamba(nn.Module):
         return dt_scale.to(device=device, dtype=torch.float32).expand(shape).contiguous()
 
     # ------------------------------------------------------------------ forward paths
-    def _forward_impl(self, x: torch.Tensor, dt_scale=None, return_state: bool = False):
+    def _pre_out(self, x: torch.Tensor, dt_scale=None, return_state: bool = False):
+        """in_proj and the SSD core: x (B,T,d_model) -> (out_proj's input (B,T,d_inner),
+        state or None)."""
         if x.dim() != 3:
             raise ValueError(f"expected (batch, seqlen, d_model), got {tuple(x.shape)}")
         if x.shape[1] <= 0:
             raise ValueError(f"Sequence length must be positive, got {x.shape[1]}")
         _native.require_gpu(x)
-        proj = self.in_proj(x)
-        y, state = self.ssd_from_proj(proj, dt_scale, return_state)
+        return self.ssd_from_proj(self.in_proj(x), dt_scale, return_state)
+
+    def _forward_impl(self, x: torch.Tensor, dt_scale=None, return_state: bool = False):
+        y, state = self._pre_out(x, dt_scale, return_state)
         return self.out_proj(y), state
 
     def ssd_from_proj(self, proj: torch.Tensor, dt_scale=None, return_state: bool = False):
@@ -190,7 +199,15 @@ class KulaMamba(nn.Module):
         or (B, 1, d_model); the output has the same rank. Returns a new state dict. The
         step kernel has no backward: backward through its output raises."""
         squeeze = hidden_states.dim() == 2
-        x_in = hidden_states if squeeze else hidden_states.squeeze(1)
+        y, state = self._step_pre_out(hidden_states, ssm_state, dt_scale)
+        out = self.out_proj(y)
+        if not squeeze:
+            out = out.unsqueeze(1)
+        return out, state
+
+    def _step_pre_out(self, hidden_states: torch.Tensor, ssm_state: dict, dt_scale=None):
+        """in_proj and the step kernel: (out_proj's input (B, d_inner), new state)."""
+        x_in = hidden_states if hidden_states.dim() == 2 else hidden_states.squeeze(1)
         if x_in.dim() != 2:
             raise ValueError(f"expected (B, d_model) or (B, 1, d_model), got {tuple(hidden_states.shape)}")
         _native.require_gpu(x_in)
@@ -200,10 +217,7 @@ class KulaMamba(nn.Module):
         scale = self._dt_scale(dt_scale, (x_in.shape[0], self.nheads), x_in.device)
         y, h_out, prev_out, angle_out = ops.step(proj, *self._small_params(), scale, h_in,
                                                  prev_in, angle_in, *ops.layer_args(self))
-        out = self.out_proj(y)
-        if not squeeze:
-            out = out.unsqueeze(1)
-        return out, {"h": h_out, "angle": angle_out, "prev_BX": prev_out}
+        return y, {"h": h_out, "angle": angle_out, "prev_BX": prev_out}
 
     def _check_state(self, ssm_state: dict, batch: int):
         H, P, N = self.nheads, self.headdim, self.d_state

@@ -477,3 +477,57 @@ def layer_args(layer) -> tuple:
     """The integer / flag arguments of the layer ops for a KulaMamba module."""
     return (layer.nheads, layer.headdim, layer.d_state, layer.mimo_rank, layer.ngroups,
             bool(layer.use_trapezoidal), bool(layer.use_complex_ssm), float(layer.B_norm.eps))
+
+
+# ---------------------------------------------------------------------------- RMSNorm
+@torch.library.custom_op(f"{NS}::rmsnorm", mutates_args=())
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """m3_rmsnorm_fwd over the last dimension of x: (y in the promotion of x's and the
+    weight's dtypes, rstd (rows,) fp32)."""
+    _native.require_gpu(x, weight)
+    d = x.shape[-1]
+    x2 = x.reshape(-1, d).contiguous()
+    wc = weight.contiguous()
+    y = torch.empty(x2.shape, device=x.device, dtype=torch.promote_types(x.dtype, weight.dtype))
+    rstd = torch.empty(x2.shape[0], device=x.device, dtype=torch.float32)
+    _native.rmsnorm_fwd(x2, wc, y, rstd, eps)
+    return y.reshape(x.shape), rstd
+
+
+@rmsnorm.register_fake
+def _(x, weight, eps):
+    rows = x.numel() // x.shape[-1]
+    return (x.new_empty(x.shape, dtype=torch.promote_types(x.dtype, weight.dtype)),
+            x.new_empty(rows, dtype=torch.float32))
+
+
+@torch.library.custom_op(f"{NS}::rmsnorm_bwd", mutates_args=())
+def rmsnorm_bwd(x: torch.Tensor, weight: torch.Tensor, rstd: torch.Tensor,
+                grad: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """m3_rmsnorm_bwd: (dL/dx in x's dtype, dL/dweight in the weight's dtype)."""
+    d = x.shape[-1]
+    x2 = x.reshape(-1, d).contiguous()
+    g2 = grad.reshape(-1, d).contiguous().to(torch.promote_types(x.dtype, weight.dtype))
+    dx = torch.empty_like(x2)
+    dw = torch.empty_like(weight.contiguous())
+    _native.rmsnorm_bwd(x2, weight.contiguous(), rstd, g2, dx, dw)
+    return dx.reshape(x.shape), dw
+
+
+@rmsnorm_bwd.register_fake
+def _(x, weight, rstd, grad):
+    return x.new_empty(x.shape), weight.new_empty(weight.shape)
+
+
+def _rmsnorm_setup(ctx, inputs, output):
+    x, weight, eps = inputs
+    ctx.save_for_backward(x, weight, output[1])
+
+
+def _rmsnorm_backward(ctx, g_y, g_rstd):
+    x, weight, rstd = ctx.saved_tensors
+    dx, dw = rmsnorm_bwd(x, weight, rstd, g_y)
+    return dx, dw, None
+
+
+rmsnorm.register_autograd(_rmsnorm_backward, setup_context=_rmsnorm_setup)

@@ -251,3 +251,28 @@ def test_noalloc_prefill_refuses_workspace_beyond_scratch_before_any_launch():
                                     None, None, None, None)
     assert st == _native.M3_ERR_SCRATCH_LIMIT
     assert b"scratch" in lib.m3_status_string(st)
+
+
+def test_rmsnorm_rejects_bad_arguments(lib):
+    fake = 256  # never dereferenced: validation fails before any launch
+    F32, BF16 = 0, 1
+    assert lib.m3_rmsnorm_fwd(None, F32, fake, F32, fake, F32, None, 4, 8, 1e-5, None) == 1
+    assert lib.m3_rmsnorm_fwd(fake, F32, fake, F32, fake, F32, None, 0, 8, 1e-5, None) == 2
+    assert lib.m3_rmsnorm_fwd(fake, F32, fake, F32, fake, F32, None, 4, (1 << 24) + 1, 1e-5, None) == 2
+    assert lib.m3_rmsnorm_fwd(fake, F32, fake, F32, fake, F32, None, 1 << 33, 8, 1e-5, None) == 2
+    assert lib.m3_rmsnorm_fwd(fake, F32, fake, F32, fake, F32, None, 4, 8, -1.0, None) == 2
+    assert lib.m3_rmsnorm_fwd(fake, F32, fake, F32, fake, F32, None, 4, 8, float("nan"), None) == 2
+    # y must be the promotion of x's and the weight's dtypes
+    assert lib.m3_rmsnorm_fwd(fake, BF16, fake, BF16, fake, F32, None, 4, 8, 1e-5, None) == 3
+    assert lib.m3_rmsnorm_fwd(fake, BF16, fake, F32, fake, BF16, None, 4, 8, 1e-5, None) == 3
+    assert lib.m3_rmsnorm_fwd(fake, 7, fake, F32, fake, F32, None, 4, 8, 1e-5, None) == 3
+    n = ctypes.c_size_t(0)
+    assert lib.m3_rmsnorm_bwd_workspace_size(1000, 768, ctypes.byref(n)) == 0
+    assert n.value == 4 * 768 * 4  # one fp32 partial row per 256 rows
+    assert lib.m3_rmsnorm_bwd_workspace_size(0, 768, ctypes.byref(n)) == 2
+    args = [fake, F32, fake, F32, fake, fake, F32, fake, fake]
+    assert lib.m3_rmsnorm_bwd(*args, None, 0, 1000, 768, None) == 4
+    assert lib.m3_rmsnorm_bwd(*args, fake, 4 * 768 * 4 - 1, 1000, 768, None) == 4
+    assert lib.m3_rmsnorm_bwd(*args, fake + 4, 4 * 768 * 4, 1000, 768, None) == 5
+    assert lib.m3_rmsnorm_bwd(fake, F32, fake, F32, None, fake, F32, fake, fake, fake, 1 << 20,
+                              1000, 768, None) == 1
