@@ -65,6 +65,27 @@ def ssd_flops(B, T, H, n=N, p=P, r=R):
     return B * T * H * (2 * (Q + 1) * r * r * (n + p) + 6 * r * p * n)
 
 
+def whole_layer_line(tokens, layer_ms, in_ms, out_ms, ssd_ms, ssd_flops_, d_model, d_in_proj,
+                     d_inner):
+    """Whole-layer prefill (in_proj, SSD core, out_proj) beside its parts, against one
+    bf16 MFMA roofline: the GEMMs' FLOPs plus the SSD core's algorithmic FLOPs over the
+    layer time."""
+    gemm = 2 * tokens * d_model * (d_in_proj + d_inner)
+    total = gemm + ssd_flops_
+    return {
+        "tok_s": round(tokens / (layer_ms * 1e-3), 1),
+        "ms": round(layer_ms, 4),
+        "in_proj_ms": round(in_ms, 4),
+        "ssd_core_ms": round(ssd_ms, 4),
+        "out_proj_ms": round(out_ms, 4),
+        "gemm_flops": gemm,
+        "ssd_flops": ssd_flops_,
+        "roofline": {"bound": "mfma", "achieved": round(total / (layer_ms * 1e-3) / 1e12, 2),
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(total / (layer_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)},
+    }
+
+
 def step_bytes(B, H, d_in_proj, d_inner):
     return 16 * B * H * P * N + 2 * B * d_in_proj + 2 * B * d_inner + 8 * B * H * (N // 2)
 
@@ -626,6 +647,11 @@ def main() -> int:
                                     args.steps, args.warmup)
         ms_per_step = wall * 1e3 / args.steps
         _, layer_ms = time_events(torch, lambda: layer.prefill(x), max(3, args.steps // 4), 1)
+        # the layer's two GEMMs alone, on the shapes the prefill runs them at
+        y_in = torch.randn(BATCH, SEQLEN, layer.d_inner, device=dev).to(torch.bfloat16)
+        _, in_ms = time_events(torch, lambda: layer._in_proj_wide(x), max(3, args.steps // 4), 1)
+        _, out_ms = time_events(torch, lambda: layer.out_proj(y_in), max(3, args.steps // 4), 1)
+        del y_in
 
         # Decode at batch 64.
         torch.manual_seed(3)
@@ -696,6 +722,8 @@ def main() -> int:
                      "kernel": "native SSD prefill (all launches of m3_prefill_fwd)",
                      "algorithmic_flops": flops, "avg_ms": round(kern_ms, 4)},
         "whole_layer_prefill_tok_s": round(tokens / (layer_ms * 1e-3), 1),
+        "whole_layer": whole_layer_line(tokens, layer_ms, in_ms, out_ms, kern_ms, flops,
+                                        D_MODEL, layer.in_proj.out_features, layer.d_inner),
         "step_decode": {
             "batch": DEC_BATCH,
             "tok_s_layer": round(DEC_BATCH / (step_layer_ms * 1e-3), 1),

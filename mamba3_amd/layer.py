@@ -158,7 +158,38 @@ class KulaMamba(nn.Module):
         if x.shape[1] <= 0:
             raise ValueError(f"Sequence length must be positive, got {x.shape[1]}")
         _native.require_gpu(x)
-        return self.ssd_from_proj(self.in_proj(x), dt_scale, return_state)
+        # A 3-D input whose batch rows are not adjacent would send the projection down
+        # torch's batched bf16 GEMM with a transposed weight view, which returned wrong rows
+        # on this GPU; a contiguous input folds to one 2-D GEMM.
+        return self.ssd_from_proj(self._in_proj_wide(x.contiguous()), dt_scale, return_state)
+
+    def _in_proj_wide(self, x: torch.Tensor) -> torch.Tensor:
+        """in_proj(x) for the prefill. Without autograd the output width is padded to a
+        multiple of 256 columns when that adds at most 1/16 (zero weight rows): hipBLASLt's
+        256-wide output tiles then cover each row exactly (d_model 768: 3696 -> 3840 columns,
+        the (65536, 768) x (768, N) GEMM measured 443 -> 331 us), and the kernels read proj
+        through its row stride, never the padding. With autograd the plain projection runs
+        (the layer backward leaves the padding columns of its proj gradient unwritten)."""
+        w = self.in_proj.weight
+        n = w.shape[0]
+        npad = -(-n // 256) * 256
+        if (torch.is_grad_enabled() or npad == n or (npad - n) * 16 > n
+                or torch.compiler.is_compiling()):
+            return self.in_proj(x)
+        b = self.in_proj.bias
+        key = (w.data_ptr(), w._version, w.dtype, w.device,
+               None if b is None else (b.data_ptr(), b._version))
+        cache = self.__dict__.get("_wide_in_proj")
+        if cache is None or cache[0] != key:
+            wp = torch.zeros(npad, w.shape[1], dtype=w.dtype, device=w.device)
+            wp[:n] = w
+            bp = None
+            if b is not None:
+                bp = torch.zeros(npad, dtype=b.dtype, device=b.device)
+                bp[:n] = b
+            cache = (key, wp, bp)
+            self.__dict__["_wide_in_proj"] = cache
+        return nn.functional.linear(x, cache[1], cache[2])
 
     def _forward_impl(self, x: torch.Tensor, dt_scale=None, return_state: bool = False):
         y, state = self._pre_out(x, dt_scale, return_state)

@@ -715,3 +715,24 @@ def test_bf16_d2048_long_prefill_properties(cuda_device):
     ys = torch.stack(outs, 1).float()
     e4, e5 = max_rel(ys, y_full.float()), max_rel(sp["h"], st["h"])
     assert e4 < BF16_TOL and e5 < BF16_TOL, (e4, e5)
+
+
+def test_prefill_of_a_strided_batch_view_equals_its_contiguous_copy(cuda_device):
+    """A batch-sliced input view (rows not adjacent in memory) prefills exactly like its
+    contiguous copy, through the width-padded in_proj of the d768 layer (3696 -> 3840
+    columns): output and state bit for bit, all finite."""
+    torch.manual_seed(0)
+    layer = mamba3_amd.KulaMamba(768, d_state=128, headdim=64, mimo_rank=2)
+    layer = layer.to(cuda_device, torch.bfloat16).eval()
+    torch.manual_seed(7)
+    x = torch.randn(4, 300, 768, device=cuda_device).to(torch.bfloat16)
+    view = x[1:3, :250]
+    assert not view.is_contiguous()
+    with torch.no_grad():
+        assert layer._in_proj_wide(view.contiguous()).shape[-1] == 3840
+        y1, s1 = layer.prefill(view)
+        y2, s2 = layer.prefill(view.contiguous())
+    assert torch.isfinite(y1.float()).all()
+    assert torch.equal(y1, y2)
+    for k in ("h", "prev_BX", "angle"):
+        assert torch.equal(s1[k], s2[k]), k
