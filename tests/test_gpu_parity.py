@@ -533,7 +533,10 @@ def test_bf16_decode_1024_steps_match_fp32_oracle(cuda_device):
 STEP_SHAPES = [dict(d_state=48, mimo_rank=2), dict(d_state=96, mimo_rank=2),
                dict(d_state=128, mimo_rank=8), dict(d_state=16, mimo_rank=3),
                dict(d_state=6, mimo_rank=1), dict(d_state=130, mimo_rank=4),
-               dict(d_state=258, mimo_rank=1), dict(d_state=300, mimo_rank=2)]
+               dict(d_state=258, mimo_rank=1), dict(d_state=300, mimo_rank=2),
+               dict(d_state=4, mimo_rank=1), dict(d_state=64, mimo_rank=4),
+               dict(d_state=512, mimo_rank=2), dict(d_state=510, mimo_rank=8),
+               dict(d_state=2, mimo_rank=2)]
 
 
 @pytest.mark.parametrize("shape", STEP_SHAPES, ids=lambda k: f"N{k['d_state']}-R{k['mimo_rank']}")
@@ -541,7 +544,8 @@ def test_step_any_even_d_state_and_rank_matches_oracle(shape, cuda_device):
     """The decode step for every even d_state up to 512 and every rank up to 8, as the
     reference's step (mamba3/mamba3.py:267-322): lanes past the row end (N/4 not a power of
     two), 2-wide column vectors (N % 4 == 2), several vectors per lane with a partial last
-    lane (N > 256), and ranks that run under a wider template. fp32 prefill of 20 tokens,
+    lane (N > 256), ranks that run under a wider template, and the full layouts (power-of-two
+    N >= 4, rank 1/2/4) with one to 64 lanes per row. fp32 prefill of 20 tokens,
     then 5 steps, each output and the final state against the oracle at 1e-4."""
     kw = dict(d_model=32, headdim=16, **shape)
     torch.manual_seed(0)
