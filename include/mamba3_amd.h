@@ -303,6 +303,27 @@ int m3_rmsnorm_bwd(const void* x, int x_dtype, const void* weight, int w_dtype,
                    void* workspace, size_t workspace_bytes, int64_t rows, int32_t d,
                    void* stream);
 
+/*
+ * Small-batch projections of the decode step, bf16, bound by the weight read. For decode
+ * batches of at most 8 rows they replace, each in one kernel, the block step's projections
+ * with the work around them (mamba3/block.py:94-100: ssm_norm + in_proj, out_proj + residual,
+ * mlp_norm + SwiGLU, w_down + residual; mamba3/mamba3.py:275-316 in_proj / out_proj of
+ * KulaMamba.step; mamba3/block.py:182-183 the final norm + lm_head).
+ *   m3_small_linear:  out = n W^T, or res + scale * (n W^T) when residual is given
+ *   m3_small_swiglu:  out = silu(n W_gate^T) * (n W_up^T)   (mamba3/block.py:16-26)
+ * with n = RMSNorm(x; norm_w, eps) (mamba3/mamba3.py:19-35, the reference's bf16 roundings)
+ * when norm_w is given, else n = x. x [m, k], weights [n, k] (nn.Linear's layout), norm_w
+ * [k], residual and out [m, n]; all bf16, rows contiguous. 1 <= m <= 8, k % 64 == 0,
+ * (m' k + 8) * 2 <= 65536 bytes of staged rows (m' = m rounded up to 1, 2, 4 or 8); x and the
+ * weights 16-byte aligned. out may alias residual (each element is read and written by one
+ * thread), not x or the weights. Accumulation in fp32; one bf16 rounding of the result.
+ */
+int m3_small_linear(const void* x, const void* norm_w, float eps, const void* weight,
+                    const void* residual, float scale, void* out, int32_t m, int32_t n, int32_t k,
+                    void* stream);
+int m3_small_swiglu(const void* x, const void* norm_w, float eps, const void* w_gate,
+                    const void* w_up, void* out, int32_t m, int32_t n, int32_t k, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

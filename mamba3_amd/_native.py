@@ -40,6 +40,8 @@ EXPORTED_SYMBOLS = (
     "m3_rmsnorm_fwd",
     "m3_rmsnorm_bwd_workspace_size",
     "m3_rmsnorm_bwd",
+    "m3_small_linear",
+    "m3_small_swiglu",
 )
 
 M3_ERR_SCRATCH_LIMIT = 8
@@ -118,6 +120,11 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.m3_rmsnorm_bwd.restype = ctypes.c_int
     lib.m3_rmsnorm_bwd.argtypes = [_vp, ctypes.c_int, _vp, ctypes.c_int, _vp, _vp, ctypes.c_int,
                                    _vp, _vp, _vp, ctypes.c_size_t, _i64, _i32, _vp]
+    lib.m3_small_linear.restype = ctypes.c_int
+    lib.m3_small_linear.argtypes = [_vp, _vp, ctypes.c_float, _vp, _vp, ctypes.c_float, _vp,
+                                    _i32, _i32, _i32, _vp]
+    lib.m3_small_swiglu.restype = ctypes.c_int
+    lib.m3_small_swiglu.argtypes = [_vp, _vp, ctypes.c_float, _vp, _vp, _vp, _i32, _i32, _i32, _vp]
     lib.m3_step_fwd.restype = ctypes.c_int
     lib.m3_step_fwd.argtypes = [ctypes.POINTER(LayerDesc), ctypes.POINTER(LayerParams),
                                 _vp, _vp, _vp, _vp, _vp, ctypes.c_int, _vp, _vp, _vp, _vp, _vp]
@@ -313,6 +320,32 @@ def rmsnorm_fwd(x, weight, y, rstd, eps: float) -> None:
     check(lib().m3_rmsnorm_fwd(ptr(x), dtype_code(x.dtype), ptr(weight), dtype_code(weight.dtype),
                                ptr(y), dtype_code(y.dtype), ptr(rstd), rows, d, eps,
                                stream_of(x)), "m3_rmsnorm_fwd")
+
+
+SMALL_PROJ_MAX_ROWS = 8
+
+
+def small_proj_ok(m: int, k: int, norm: bool = False) -> bool:
+    """The shapes m3_small_linear / m3_small_swiglu take: m <= 8 rows, k a multiple of 64
+    whose staged rows (m rounded up to 1, 2, 4 or 8) and, with a norm, the norm weight fit
+    64 KB of LDS."""
+    mm = 1 if m <= 1 else 2 if m <= 2 else 4 if m <= 4 else 8
+    need = (mm * k + 8 + (k if norm else 0)) * 2
+    return 1 <= m <= SMALL_PROJ_MAX_ROWS and k >= 64 and k % 64 == 0 and need <= 65536
+
+
+def small_linear(x, norm_w, eps, weight, residual, scale, out) -> None:
+    """m3_small_linear on contiguous bf16 x (m, k), weight (n, k), out (m, n)."""
+    m, k = x.shape
+    check(lib().m3_small_linear(ptr(x), ptr(norm_w), eps, ptr(weight), ptr(residual), scale,
+                                ptr(out), m, weight.shape[0], k, stream_of(x)), "m3_small_linear")
+
+
+def small_swiglu(x, norm_w, eps, w_gate, w_up, out) -> None:
+    """m3_small_swiglu on contiguous bf16 x (m, k), weights (n, k), out (m, n)."""
+    m, k = x.shape
+    check(lib().m3_small_swiglu(ptr(x), ptr(norm_w), eps, ptr(w_gate), ptr(w_up), ptr(out), m,
+                                w_gate.shape[0], k, stream_of(x)), "m3_small_swiglu")
 
 
 def rmsnorm_bwd(x, weight, rstd, grad, dx, dweight) -> None:

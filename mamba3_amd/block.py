@@ -16,7 +16,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 from torch.utils.checkpoint import checkpoint as grad_checkpoint
 
-from . import ops
+from . import _native, ops
 from .layer import KulaMamba, RMSNorm
 
 
@@ -116,7 +116,42 @@ class KulaMambaBlock(nn.Module):
         return add_scaled_linear(x, self.mlp.w_down, self.mlp.hidden(self.mlp_norm(x)),
                                  self.residual_scale)
 
+    def _small_step_usable(self, x: torch.Tensor) -> bool:
+        """The decode step runs on the small-batch projection kernels (norm + in_proj,
+        out_proj + residual, norm + SwiGLU, w_down + residual): bf16, at most 8 rows, no
+        biases, last-dimension norms, nothing to differentiate."""
+        ssm = self.ssm
+        ws = [self.ssm_norm.weight, ssm.in_proj.weight, ssm.out_proj.weight]
+        lins = [ssm.in_proj, ssm.out_proj]
+        if self.use_mlp:
+            ws += [self.mlp_norm.weight, self.mlp.w_gate.weight, self.mlp.w_up.weight,
+                   self.mlp.w_down.weight]
+            lins += [self.mlp.w_gate, self.mlp.w_up, self.mlp.w_down]
+        norms = [self.ssm_norm] + ([self.mlp_norm] if self.use_mlp else [])
+        m = x.shape[0]
+        # every projection's K: d_model (with a norm), d_inner, d_ff
+        ks_ok = _native.small_proj_ok(m, ssm.out_proj.in_features) and (
+            not self.use_mlp or _native.small_proj_ok(m, self.mlp.w_down.in_features))
+        return (ks_ok and all(l.bias is None for l in lins) and all(n.dim in (-1, 1) for n in norms)
+                and ops.small_proj_usable(x, *ws, norm=True))
+
+    def _small_step_tail(self, x: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
+        """x + s out_proj(y), then the MLP residual, on the small-batch kernels."""
+        s = self.residual_scale
+        x = ops.small_linear(y, None, 0.0, self.ssm.out_proj.weight, x, s)
+        if self.use_mlp:
+            mlp = self.mlp
+            h = ops.small_swiglu(x, self.mlp_norm.weight, float(self.mlp_norm.eps),
+                                 mlp.w_gate.weight, mlp.w_up.weight)
+            x = ops.small_linear(h, None, 0.0, mlp.w_down.weight, x, s)
+        return x
+
     def step(self, x: torch.Tensor, ssm_state: dict):
+        if self._small_step_usable(x):
+            proj = ops.small_linear(x, self.ssm_norm.weight, float(self.ssm_norm.eps),
+                                    self.ssm.in_proj.weight, None, 1.0)
+            y, new_state = self.ssm._step_from_proj(proj, ssm_state)
+            return self._small_step_tail(x, y), new_state
         y, new_state = self.ssm._step_pre_out(self.ssm_norm(x), ssm_state)
         x = add_scaled_linear(x, self.ssm.out_proj, y.view(*x.shape[:-1], -1), self.residual_scale)
         if self.use_mlp:
@@ -236,7 +271,7 @@ class KulaMambaLM(nn.Module):
             x = self.embedding(nxt.squeeze(1))
             for i, layer in enumerate(self.layers):
                 x, states[i] = layer.step(x, states[i])
-            logits = self.lm_head(self.norm(x))
+            logits = _lm_logits(self, x)
         return torch.cat(out, dim=1)
 
 
@@ -244,15 +279,32 @@ def _block_step_into(block: KulaMambaBlock, x: torch.Tensor, st_in: dict, st_out
     """KulaMambaBlock.step (mamba3/block.py:94-100) with the SSM step written into the
     caller's state buffers `st_out` (which must not alias `st_in`)."""
     ssm = block.ssm
-    proj = ssm.in_proj(block.ssm_norm(x))
+    small = block._small_step_usable(x)
+    if small:
+        proj = ops.small_linear(x, block.ssm_norm.weight, float(block.ssm_norm.eps),
+                                ssm.in_proj.weight, None, 1.0)
+    else:
+        proj = ssm.in_proj(block.ssm_norm(x))
     y = torch.empty(x.shape[0], ssm.d_inner, device=x.device, dtype=proj.dtype)
     ops.step_into(proj, *ssm._small_params(), None, st_in["h"], st_in["prev_BX"],
                   st_in["angle"], y, st_out["h"], st_out["prev_BX"], st_out["angle"],
                   *ops.layer_args(ssm))
+    if small:
+        return block._small_step_tail(x, y)
     x = add_scaled_linear(x, ssm.out_proj, y, block.residual_scale)
     if block.use_mlp:
         x = block._mlp_residual(x)
     return x
+
+
+def _lm_logits(lm: "KulaMambaLM", x: torch.Tensor) -> torch.Tensor:
+    """lm_head(norm(x)) for decode rows x (B, d_model): one small-batch kernel (norm in its
+    prologue) when it applies (mamba3/block.py:182-183)."""
+    w = lm.lm_head.weight
+    if (lm.lm_head.bias is None and lm.norm.dim in (-1, 1)
+            and ops.small_proj_usable(x, lm.norm.weight, w, norm=True)):
+        return ops.small_linear(x, lm.norm.weight, float(lm.norm.eps), w, None, 1.0)
+    return lm.lm_head(lm.norm(x))
 
 
 class _DecodeGraph:
@@ -272,7 +324,7 @@ class _DecodeGraph:
             x = lm.embedding(self.tok)
             for i, block in enumerate(lm.layers):
                 x = _block_step_into(block, x, self.bufs[src][i], self.bufs[1 - src][i])
-            return lm.lm_head(lm.norm(x))
+            return _lm_logits(lm, x)
 
         # Warm up outside the capture on a side stream (allocator and library handles);
         # it reads set 0 and writes set 1, which the first replay rewrites.

@@ -351,6 +351,43 @@ int m3_rmsnorm_bwd(const void* x, int x_dtype, const void* weight, int w_dtype,
                : M3_ERR_LAUNCH;
 }
 
+// Shapes the small-batch projection kernels take: at most 8 activation rows, K a multiple
+// of 64 whose staged rows (and norm weight) fit 64 KB of LDS, 16-byte aligned activation,
+// norm-weight and weight rows.
+static int small_proj_check(const void* x, const void* nw, const void* w0, const void* w1,
+                            const void* out, int32_t m, int32_t n, int32_t k) {
+    if (!x || !w0 || !out) return M3_ERR_NULL_POINTER;
+    if (m < 1 || m > 8 || n < 1 || k < 64 || k % 64 != 0) return M3_ERR_INVALID_SHAPE;
+    if (m3::gemv_small_lds_bytes(m, k, nw != nullptr) > 65536) return M3_ERR_UNSUPPORTED;
+    if (!aligned(x, 16) || !aligned(w0, 16) || (w1 && !aligned(w1, 16)) || (nw && !aligned(nw, 16)))
+        return M3_ERR_MISALIGNED;
+    return M3_OK;
+}
+
+int m3_small_linear(const void* x, const void* norm_w, float eps, const void* weight,
+                    const void* residual, float scale, void* out, int32_t m, int32_t n, int32_t k,
+                    void* stream) {
+    const int st = small_proj_check(x, norm_w, weight, nullptr, out, m, n, k);
+    if (st != M3_OK) return st;
+    if (norm_w && !(eps >= 0.f)) return M3_ERR_INVALID_SHAPE;
+    return m3::launch_gemv_small(x, norm_w, eps, weight, nullptr, residual, scale, out, m, n, k,
+                                 as_stream(stream)) == 0
+               ? M3_OK
+               : M3_ERR_LAUNCH;
+}
+
+int m3_small_swiglu(const void* x, const void* norm_w, float eps, const void* w_gate,
+                    const void* w_up, void* out, int32_t m, int32_t n, int32_t k, void* stream) {
+    if (!w_up) return M3_ERR_NULL_POINTER;
+    const int st = small_proj_check(x, norm_w, w_gate, w_up, out, m, n, k);
+    if (st != M3_OK) return st;
+    if (norm_w && !(eps >= 0.f)) return M3_ERR_INVALID_SHAPE;
+    return m3::launch_gemv_small(x, norm_w, eps, w_gate, w_up, nullptr, 1.f, out, m, n, k,
+                                 as_stream(stream)) == 0
+               ? M3_OK
+               : M3_ERR_LAUNCH;
+}
+
 int m3_chunked_ssd_fwd_workspace_size(int32_t batch, int32_t seqlen, int32_t nheads,
                                       int32_t headdim, int32_t d_state, int32_t mimo_rank,
                                       int32_t dtype, int32_t has_beta, size_t* bytes) {

@@ -116,6 +116,14 @@ int launch_rmsnorm_fwd(const void* x, int xdtype, const void* w, int wdtype, voi
                        int ydtype, float* rstd, int64_t rows, int d, float eps,
                        hipStream_t stream);
 size_t rmsnorm_bwd_workspace(int64_t rows, int d);
+
+// Small-batch decode projections (m3_gemv.hip): out = [res +] s (n W0^T), or with W1
+// silu(n W0^T) * (n W1^T); n = RMSNorm(x; norm_w) when norm_w is given. bf16, m <= 8,
+// k % 64 == 0, gemv_small_lds_bytes(m, k, norm) <= 65536.
+int gemv_small_lds_bytes(int m, int k, bool norm);
+int launch_gemv_small(const void* x, const void* norm_w, float eps, const void* w0, const void* w1,
+                      const void* res, float scale, void* out, int m, int n, int k,
+                      hipStream_t stream);
 int launch_rmsnorm_bwd(const void* x, int xdtype, const void* w, int wdtype, const float* rstd,
                        const void* g, int gdtype, void* dx, void* dw, void* workspace,
                        int64_t rows, int d, hipStream_t stream);

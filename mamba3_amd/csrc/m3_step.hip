@@ -1,9 +1,10 @@
 // O(1) decode step of one KulaMamba layer (replaces mamba3/mamba3.py:275-316).
 //
-// One workgroup per (batch, head). Each lane owns NV vectors of VW consecutive state
-// columns (CPL = NV * VW columns, n0 = q * CPL) of one headdim row p, so a row of N
-// columns is spread over ceil(N / CPL) lanes, rounded up to LPR (a power of two; lanes
-// past the row end hold no columns), and a wave covers 64 / LPR rows. The lane recomputes
+// One workgroup per (batch, head), or at small batch per (batch, head, block of P / psplit
+// rows), so that about 1024 workgroups share the step. Each lane owns NV vectors of VW
+// consecutive state columns (CPL = NV * VW columns, n0 = q * CPL) of one headdim row p, so a
+// row of N columns is spread over ceil(N / CPL) lanes, rounded up to LPR (a power of two;
+// lanes past the row end hold no columns), and a wave covers 64 / LPR rows. The lane recomputes
 // the RMSNorm / bias / RoPE of its B and C columns (a butterfly over the LPR lanes gives
 // the row RMS), then streams its rows of h and prev_BX with VW*4-byte loads:
 //
@@ -30,6 +31,7 @@ constexpr int kStepRowsPerLane = 8;
 
 struct StepArgs {
     int H, P, N, G, R;
+    int psplit;  // workgroups per (batch, head), each P / psplit rows
     int trap, cplx;
     int angle_bf16;
     float eps;
@@ -72,7 +74,8 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(StepArgs a) {
     constexpr int CPL = VW * NV;               // state columns per lane
     constexpr int kRows = kStepThreads / LPR;  // rows handled per pass of the block
     const int tid = threadIdx.x;
-    const int b = blockIdx.x / a.H, h = blockIdx.x % a.H;
+    const int bh = blockIdx.x / a.psplit, ps = blockIdx.x - bh * a.psplit;
+    const int b = bh / a.H, h = bh % a.H;
     const int g = h / (a.H / a.G);
     // the rank: RM itself, or a.R <= RM (ranks 3, 5, 6 and 7 run under RM = 4 or 8)
     const int R = kExactR ? RM : a.R;
@@ -185,7 +188,7 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(StepArgs a) {
         for (int j = 0; j < NPL; ++j) {
             // pairs past the row end rotate zero columns and store nothing
             const float phi = ang[j] - tg.dt * th[j];
-            if (row0 == 0 && 2 * j < nvq * VW) st_angle(a.angle_out, abase + n0 / 2 + j, phi, abf);
+            if (row0 == 0 && ps == 0 && 2 * j < nvq * VW) st_angle(a.angle_out, abase + n0 / 2 + j, phi, abf);
             float sn, cs;
             sincosf(phi, &sn, &cs);
 #pragma unroll
@@ -198,7 +201,7 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(StepArgs a) {
                 Cv[2 * j + 1][r] = ce * sn + co * cs;
             }
         }
-    } else if (row0 == 0) {
+    } else if (row0 == 0 && ps == 0) {
         // Angle stays zero without complex RoPE; pass the input through.
 #pragma unroll
         for (int j = 0; j < NPL; ++j)
@@ -218,16 +221,19 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(StepArgs a) {
     const int nvr = N / VW;       // vectors per row (P * N <= 256 * 512: int offsets)
     const int v0 = q * NV;        // this lane's first vector in the row
 
-    for (int pbase = row0; pbase < P; pbase += kRows * kStepRowsPerLane) {
+    // this workgroup's rows [pb, pe)
+    const int pb = ps * (P / a.psplit), pe = pb + P / a.psplit;
+    for (int pbase = pb + row0; pbase < pe; pbase += kRows * kStepRowsPerLane) {
         vec hv[kStepRowsPerLane][NV], pv[kStepRowsPerLane][NV];
         T xv[kStepRowsPerLane];
         // Streaming reads of the incoming state (the outgoing state is stored normally so
         // the next step finds it in the caches). All loads are unconditional and issued
-        // before the arithmetic: rows past P read row P - 1 and lanes past the row end read
-        // the row's last vector (their B / C columns are zero); neither stores anything.
+        // before the arithmetic: rows past the block's end read its last row and lanes past
+        // the row end read the row's last vector (their B / C columns are zero); neither
+        // stores anything.
 #pragma unroll
         for (int it = 0; it < kStepRowsPerLane; ++it) {
-            const int p = pbase + it * kRows < P ? pbase + it * kRows : P - 1;
+            const int p = pbase + it * kRows < pe ? pbase + it * kRows : pe - 1;
 #pragma unroll
             for (int v = 0; v < NV; ++v) {
                 const int vi = v0 + v < nvr ? v0 + v : nvr - 1;
@@ -239,7 +245,7 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(StepArgs a) {
 #pragma unroll
         for (int it = 0; it < kStepRowsPerLane; ++it) {
             const int p = pbase + it * kRows;
-            if (p < P) {
+            if (p < pe) {
                 float xr[RM];
 #pragma unroll
                 for (int r = 0; r < RM; ++r) xr[r] = r < R ? (float)xv[it] * mx[p * R + r] : 0.f;
@@ -370,7 +376,12 @@ int launch_step(const m3_layer_desc& d, const m3_layer_params& p, const void* pr
     a.angle_out = angle_out;
     int vw, nv, lpr;
     step_layout(d.d_state, vw, nv, lpr);
-    const dim3 grid((unsigned)(d.batch * d.nheads));
+    // Small batches split each (batch, head) over up to 8 workgroups of P / psplit rows
+    // (the per-head prologue is repeated), so that about 1024 workgroups share the work.
+    a.psplit = 1;
+    while (a.psplit < 8 && (int64_t)d.batch * d.nheads * a.psplit < 1024 && d.headdim % (2 * a.psplit) == 0)
+        a.psplit *= 2;
+    const dim3 grid((unsigned)(d.batch * d.nheads * a.psplit));
     if (d.dtype == M3_DTYPE_BF16) launch_step_t<bf16>(d.d_state, d.mimo_rank, vw, nv, lpr, grid, stream, a);
     else launch_step_t<float>(d.d_state, d.mimo_rank, vw, nv, lpr, grid, stream, a);
     return hipGetLastError() == hipSuccess ? M3_OK : M3_ERR_LAUNCH;

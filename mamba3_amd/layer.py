@@ -231,7 +231,11 @@ class KulaMamba(nn.Module):
         step kernel has no backward: backward through its output raises."""
         squeeze = hidden_states.dim() == 2
         y, state = self._step_pre_out(hidden_states, ssm_state, dt_scale)
-        out = self.out_proj(y)
+        w = self.out_proj.weight
+        if self.out_proj.bias is None and ops.small_proj_usable(y, w):
+            out = ops.small_linear(y, None, 0.0, w, None, 1.0)
+        else:
+            out = self.out_proj(y)
         if not squeeze:
             out = out.unsqueeze(1)
         return out, state
@@ -242,10 +246,19 @@ class KulaMamba(nn.Module):
         if x_in.dim() != 2:
             raise ValueError(f"expected (B, d_model) or (B, 1, d_model), got {tuple(hidden_states.shape)}")
         _native.require_gpu(x_in)
+        w = self.in_proj.weight
+        if self.in_proj.bias is None and ops.small_proj_usable(x_in, w):
+            proj = ops.small_linear(x_in, None, 0.0, w, None, 1.0)
+        else:
+            proj = self.in_proj(x_in)
+        return self._step_from_proj(proj, ssm_state, dt_scale)
+
+    def _step_from_proj(self, proj: torch.Tensor, ssm_state: dict, dt_scale=None):
+        """The step kernel on the in_proj output proj (B, d_in_proj): (out_proj's input
+        (B, d_inner), new state)."""
         self._check_norm_eps()
-        h_in, prev_in, angle_in = self._check_state(ssm_state, x_in.shape[0])
-        proj = self.in_proj(x_in)
-        scale = self._dt_scale(dt_scale, (x_in.shape[0], self.nheads), x_in.device)
+        h_in, prev_in, angle_in = self._check_state(ssm_state, proj.shape[0])
+        scale = self._dt_scale(dt_scale, (proj.shape[0], self.nheads), proj.device)
         y, h_out, prev_out, angle_out = ops.step(proj, *self._small_params(), scale, h_in,
                                                  prev_in, angle_in, *ops.layer_args(self))
         return y, {"h": h_out, "angle": angle_out, "prev_BX": prev_out}

@@ -531,3 +531,55 @@ def _rmsnorm_backward(ctx, g_y, g_rstd):
 
 
 rmsnorm.register_autograd(_rmsnorm_backward, setup_context=_rmsnorm_setup)
+
+
+# ---------------------------------------------------------------- small-batch projections
+def small_proj_usable(x: torch.Tensor, *weights, norm: bool = False) -> bool:
+    """True when m3_small_linear / m3_small_swiglu take x (m, k) with these weights (norm
+    weight and projection weights): bf16, at most 8 rows, k a multiple of 64 that fits their
+    LDS (with the norm weight when `norm`), contiguous 16-byte aligned rows, and no autograd
+    to record (the kernels have no backward)."""
+    if torch.compiler.is_compiling() or x.dim() != 2 or x.dtype != torch.bfloat16:
+        return False
+    if not _native.small_proj_ok(x.shape[0], x.shape[1], norm):
+        return False
+    grad = torch.is_grad_enabled()
+    for t in (x, *weights):
+        if t is None or t.dtype != torch.bfloat16 or not t.is_cuda or not t.is_contiguous():
+            return False
+        if t.data_ptr() % 16 != 0 or (grad and t.requires_grad):
+            return False
+    return True
+
+
+@torch.library.custom_op(f"{NS}::small_linear", mutates_args=())
+def small_linear(x: torch.Tensor, norm_w: Optional[torch.Tensor], eps: float, weight: torch.Tensor,
+                 residual: Optional[torch.Tensor], scale: float) -> torch.Tensor:
+    """m3_small_linear: [residual +] scale * (n W^T), n = RMSNorm(x; norm_w) or x, for bf16
+    x (m <= 8, k) (check with small_proj_usable); no backward."""
+    _native.require_gpu(x, weight)
+    out = torch.empty(x.shape[0], weight.shape[0], device=x.device, dtype=torch.bfloat16)
+    res = None if residual is None else residual.contiguous()
+    _native.small_linear(x, norm_w, eps, weight, res, scale, out)
+    return out
+
+
+@small_linear.register_fake
+def _(x, norm_w, eps, weight, residual, scale):
+    return x.new_empty(x.shape[0], weight.shape[0])
+
+
+@torch.library.custom_op(f"{NS}::small_swiglu", mutates_args=())
+def small_swiglu(x: torch.Tensor, norm_w: Optional[torch.Tensor], eps: float,
+                 w_gate: torch.Tensor, w_up: torch.Tensor) -> torch.Tensor:
+    """m3_small_swiglu: silu(n W_gate^T) * (n W_up^T), n = RMSNorm(x; norm_w) or x, for bf16
+    x (m <= 8, k); no backward."""
+    _native.require_gpu(x, w_gate, w_up)
+    out = torch.empty(x.shape[0], w_gate.shape[0], device=x.device, dtype=torch.bfloat16)
+    _native.small_swiglu(x, norm_w, eps, w_gate, w_up, out)
+    return out
+
+
+@small_swiglu.register_fake
+def _(x, norm_w, eps, w_gate, w_up):
+    return x.new_empty(x.shape[0], w_gate.shape[0])

@@ -276,3 +276,27 @@ def test_rmsnorm_rejects_bad_arguments(lib):
     assert lib.m3_rmsnorm_bwd(*args, fake + 4, 4 * 768 * 4, 1000, 768, None) == 5
     assert lib.m3_rmsnorm_bwd(fake, F32, fake, F32, None, fake, F32, fake, fake, fake, 1 << 20,
                               1000, 768, None) == 1
+
+
+def test_small_projections_reject_bad_arguments(lib):
+    fake = 256  # 16-byte aligned, never dereferenced: validation fails before any launch
+    args = lambda m, n, k: (m, n, k, None)
+    assert lib.m3_small_linear(None, None, 0.0, fake, None, 1.0, fake, *args(4, 8, 64)) == 1
+    assert lib.m3_small_linear(fake, None, 0.0, fake, None, 1.0, None, *args(4, 8, 64)) == 1
+    assert lib.m3_small_linear(fake, None, 0.0, fake, None, 1.0, fake, *args(0, 8, 64)) == 2
+    assert lib.m3_small_linear(fake, None, 0.0, fake, None, 1.0, fake, *args(9, 8, 64)) == 2
+    assert lib.m3_small_linear(fake, None, 0.0, fake, None, 1.0, fake, *args(4, 0, 64)) == 2
+    assert lib.m3_small_linear(fake, None, 0.0, fake, None, 1.0, fake, *args(4, 8, 96)) == 2
+    # staged rows beyond 64 KB of LDS: 8 rows x 4160 bf16
+    assert lib.m3_small_linear(fake, None, 0.0, fake, None, 1.0, fake, *args(8, 8, 4160)) == 3
+    assert lib.m3_small_linear(fake + 8, None, 0.0, fake, None, 1.0, fake, *args(4, 8, 64)) == 5
+    assert lib.m3_small_linear(fake, fake, -1.0, fake, None, 1.0, fake, *args(4, 8, 64)) == 2
+    assert lib.m3_small_swiglu(fake, None, 0.0, fake, None, fake, *args(4, 8, 64)) == 1
+    assert lib.m3_small_swiglu(fake, None, 0.0, fake, fake + 2, fake, *args(4, 8, 64)) == 5
+    # (8 rows x k + one 8-element zero piece [+ the k-element norm weight]) x 2 bytes <= 65536
+    assert _native.small_proj_ok(8, 4032) and not _native.small_proj_ok(8, 4096)
+    assert _native.small_proj_ok(4, 8128) and not _native.small_proj_ok(9, 64)
+    assert _native.small_proj_ok(8, 3584, norm=True) and not _native.small_proj_ok(8, 3648, norm=True)
+    # the norm weight counts toward the limit on the C side too (8 x 3648 + 8 + 3648 > 32768)
+    assert lib.m3_small_linear(fake, fake, 1e-5, fake, None, 1.0, fake, *args(8, 8, 3648)) == 3
+    assert lib.m3_small_linear(fake, fake + 8, 1e-5, fake, None, 1.0, fake, *args(4, 8, 64)) == 5

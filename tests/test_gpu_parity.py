@@ -184,7 +184,7 @@ def test_lm_decode_graph_replays_equal_eager_steps(cuda_device):
     """The captured decode step (HIP graph) against the eager step loop, on a 3-layer
     d_model-768 LM in bf16: every replay's logits are bitwise the eager logits, with eager
     work and synchronisations between replays, and greedy generation agrees token for token."""
-    from mamba3_amd.block import _DecodeGraph
+    from mamba3_amd.block import _DecodeGraph, _lm_logits
     torch.manual_seed(0)
     lm = mamba3_amd.KulaMambaLM(32000, 768, n_layers=3, d_state=128, headdim=64,
                                 mimo_rank=2).to(cuda_device, torch.bfloat16).eval()
@@ -203,7 +203,7 @@ def test_lm_decode_graph_replays_equal_eager_steps(cuda_device):
             xe = lm.embedding(tok)
             for i, layer in enumerate(lm.layers):
                 xe, states[i] = layer.step(xe, states[i])
-            ref_logits = lm.lm_head(lm.norm(xe))
+            ref_logits = _lm_logits(lm, xe)
             torch.cuda.synchronize()
             out = graph(tok)
             torch.cuda.synchronize()
