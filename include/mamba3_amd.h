@@ -304,6 +304,15 @@ int m3_rmsnorm_bwd(const void* x, int x_dtype, const void* weight, int w_dtype,
                    void* stream);
 
 /*
+ * SwiGLU's element-wise step (mamba3/block.py:16-26: silu(w_gate x) * w_up x) on the output of
+ * one GEMM over the concatenated [w_gate; w_up] weight: gate_up [rows, row_stride] bf16 with
+ * the gate in columns [0, d_ff) and up in [d_ff, 2 d_ff); out [rows, d_ff] bf16 =
+ * silu(gate) * up, computed in fp32 and rounded once. out must not alias gate_up.
+ */
+int m3_silu_mul(const void* gate_up, int64_t rows, int32_t d_ff, int64_t row_stride, void* out,
+                void* stream);
+
+/*
  * Small-batch projections of the decode step, bf16, bound by the weight read. For decode
  * batches of at most 8 rows they replace, each in one kernel, the block step's projections
  * with the work around them (mamba3/block.py:94-100: ssm_norm + in_proj, out_proj + residual,

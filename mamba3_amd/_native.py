@@ -42,6 +42,7 @@ EXPORTED_SYMBOLS = (
     "m3_rmsnorm_bwd",
     "m3_small_linear",
     "m3_small_swiglu",
+    "m3_silu_mul",
 )
 
 M3_ERR_SCRATCH_LIMIT = 8
@@ -123,6 +124,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.m3_small_linear.restype = ctypes.c_int
     lib.m3_small_linear.argtypes = [_vp, _vp, ctypes.c_float, _vp, _vp, ctypes.c_float, _vp,
                                     _i32, _i32, _i32, _vp]
+    lib.m3_silu_mul.restype = ctypes.c_int
+    lib.m3_silu_mul.argtypes = [_vp, _i64, _i32, _i64, _vp, _vp]
     lib.m3_small_swiglu.restype = ctypes.c_int
     lib.m3_small_swiglu.argtypes = [_vp, _vp, ctypes.c_float, _vp, _vp, _vp, _i32, _i32, _i32, _vp]
     lib.m3_step_fwd.restype = ctypes.c_int
@@ -346,6 +349,12 @@ def small_swiglu(x, norm_w, eps, w_gate, w_up, out) -> None:
     m, k = x.shape
     check(lib().m3_small_swiglu(ptr(x), ptr(norm_w), eps, ptr(w_gate), ptr(w_up), ptr(out), m,
                                 w_gate.shape[0], k, stream_of(x)), "m3_small_swiglu")
+
+
+def silu_mul(gate_up, d_ff, out) -> None:
+    """m3_silu_mul on bf16 gate_up (rows, >= 2 d_ff) with unit column stride."""
+    check(lib().m3_silu_mul(ptr(gate_up), gate_up.shape[0], d_ff, gate_up.stride(0), ptr(out),
+                            stream_of(gate_up)), "m3_silu_mul")
 
 
 def rmsnorm_bwd(x, weight, rstd, grad, dx, dweight) -> None:

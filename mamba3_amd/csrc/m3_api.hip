@@ -351,6 +351,16 @@ int m3_rmsnorm_bwd(const void* x, int x_dtype, const void* weight, int w_dtype,
                : M3_ERR_LAUNCH;
 }
 
+int m3_silu_mul(const void* gate_up, int64_t rows, int32_t d_ff, int64_t row_stride, void* out,
+                void* stream) {
+    if (!gate_up || !out) return M3_ERR_NULL_POINTER;
+    if (rows <= 0 || d_ff <= 0 || row_stride < 2 * (int64_t)d_ff) return M3_ERR_INVALID_SHAPE;
+    if (rows * (int64_t)d_ff >= ((int64_t)1 << 39)) return M3_ERR_INVALID_SHAPE;  // 32-bit grid
+    return m3::launch_silu_mul(gate_up, out, rows, d_ff, row_stride, as_stream(stream)) == 0
+               ? M3_OK
+               : M3_ERR_LAUNCH;
+}
+
 // Shapes the small-batch projection kernels take: at most 8 activation rows, K a multiple
 // of 64 whose staged rows (and norm weight) fit 64 KB of LDS, 16-byte aligned activation,
 // norm-weight and weight rows.

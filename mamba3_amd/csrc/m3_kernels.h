@@ -117,6 +117,10 @@ int launch_rmsnorm_fwd(const void* x, int xdtype, const void* w, int wdtype, voi
                        hipStream_t stream);
 size_t rmsnorm_bwd_workspace(int64_t rows, int d);
 
+// out (rows x d_ff) = silu(gu[:, :d_ff]) * gu[:, d_ff:2 d_ff], bf16 (m3_norm.hip).
+int launch_silu_mul(const void* gu, void* out, int64_t rows, int dff, int64_t stride,
+                    hipStream_t stream);
+
 // Small-batch decode projections (m3_gemv.hip): out = [res +] s (n W0^T), or with W1
 // silu(n W0^T) * (n W1^T); n = RMSNorm(x; norm_w) when norm_w is given. bf16, m <= 8,
 // k % 64 == 0, gemv_small_lds_bytes(m, k, norm) <= 65536.

@@ -1,5 +1,6 @@
 // RMSNorm of the residual blocks (mamba3/mamba3.py:19-35, used by mamba3/block.py:45-72) in
-// one pass over the activations, and its backward.
+// one pass over the activations, and its backward; and SwiGLU's silu * mul over a
+// concatenated gate / up projection.
 //
 // Forward, per row of d elements (the reference's arithmetic and roundings):
 //   s = rsqrt(mean(x^2) + eps)   in fp32
@@ -12,6 +13,8 @@
 //   dw_j = sum over rows of g_j x_j s   (per-block column partials summed in block order,
 //          so the result does not depend on timing)
 #include <hip/hip_runtime.h>
+
+#include <type_traits>
 
 #include "m3_common.h"
 #include "m3_kernels.h"
@@ -51,6 +54,82 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_fwd_kernel(
         const float xs = (float)(TX)(ldf<TX>(x, base + j) * st);
         stf<TY>(y, base + j, xs * ldf<TW>(w, j));
     }
+}
+
+// bf16 rows of d % 8 == 0 elements, 16-byte aligned: the same arithmetic on 16-byte pieces
+// (each lane sums the squares of its pieces, then the 64-lane butterfly).
+typedef __bf16 nb16x8 __attribute__((ext_vector_type(8)));
+
+template <typename TW, typename TY>
+__global__ __launch_bounds__(kNormThreads) void rmsnorm_fwd_vec_kernel(
+    const bf16* __restrict__ x, const TW* __restrict__ w, TY* __restrict__ y,
+    float* __restrict__ rstd, int64_t rows, int d, float eps) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * (kNormThreads / 64) + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const int pieces = d / 8;
+    const nb16x8* xr = reinterpret_cast<const nb16x8*>(x + row * d);
+    float ss = 0.f;
+    for (int c = lane; c < pieces; c += 64) {
+        const nb16x8 v = xr[c];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += (float)v[e] * (float)v[e];
+    }
+    ss = group_sum<64>(ss);
+    const float s = rsqrtf(ss / (float)d + eps);
+    if (rstd && lane == 0) rstd[row] = s;
+    const float st = (float)(bf16)s;  // the scale in the activation dtype
+    for (int c = lane; c < pieces; c += 64) {
+        const nb16x8 v = xr[c];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float xs = (float)(bf16)((float)v[e] * st);
+            y[row * d + c * 8 + e] = (TY)(xs * (float)w[c * 8 + e]);
+        }
+    }
+}
+
+// SwiGLU's element-wise step (mamba3/block.py:16-26) on the concatenated gate / up
+// projection gu (rows x row_stride, gate in columns [0, d_ff), up in [d_ff, 2 d_ff)):
+// out = silu(gate) * up in fp32, rounded once to bf16.
+__global__ __launch_bounds__(256) void silu_mul_kernel(const bf16* __restrict__ gu,
+                                                       bf16* __restrict__ out, int64_t rows,
+                                                       int dff, int64_t stride) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int pieces = dff / 8;
+    if (i >= rows * pieces) return;
+    const int64_t r = i / pieces;
+    const int c = (int)(i - r * pieces);
+    const nb16x8 g = *reinterpret_cast<const nb16x8*>(gu + r * stride + c * 8);
+    const nb16x8 u = *reinterpret_cast<const nb16x8*>(gu + r * stride + dff + c * 8);
+    nb16x8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = (bf16)(silu_f((float)g[e]) * (float)u[e]);
+    *reinterpret_cast<nb16x8*>(out + r * dff + c * 8) = o;
+}
+
+__global__ __launch_bounds__(256) void silu_mul_scalar_kernel(const bf16* __restrict__ gu,
+                                                              bf16* __restrict__ out,
+                                                              int64_t rows, int dff,
+                                                              int64_t stride) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= rows * dff) return;
+    const int64_t r = i / dff;
+    const int j = (int)(i - r * dff);
+    out[r * dff + j] = (bf16)(silu_f((float)gu[r * stride + j]) * (float)gu[r * stride + dff + j]);
+}
+
+int launch_silu_mul(const void* gu, void* out, int64_t rows, int dff, int64_t stride,
+                    hipStream_t stream) {
+    const bf16* g = reinterpret_cast<const bf16*>(gu);
+    bf16* o = reinterpret_cast<bf16*>(out);
+    const bool vec = dff % 8 == 0 && stride % 8 == 0 && reinterpret_cast<uintptr_t>(gu) % 16 == 0 &&
+                     reinterpret_cast<uintptr_t>(out) % 16 == 0;
+    const int64_t n = vec ? rows * (dff / 8) : rows * dff;
+    const dim3 grid((unsigned)((n + 255) / 256));
+    if (vec) hipLaunchKernelGGL(silu_mul_kernel, grid, dim3(256), 0, stream, g, o, rows, dff, stride);
+    else hipLaunchKernelGGL(silu_mul_scalar_kernel, grid, dim3(256), 0, stream, g, o, rows, dff, stride);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 template <typename TX, typename TW, typename TG>
@@ -105,6 +184,19 @@ template <typename TX, typename TW>
 static void launch_fwd_w(int ydtype, const void* x, const void* w, void* y, float* rstd,
                          int64_t rows, int d, float eps, hipStream_t stream) {
     const dim3 grid((unsigned)((rows + 3) / 4));
+    if constexpr (std::is_same<TX, bf16>::value) {
+        if (d % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0) {
+            const bf16* xb = reinterpret_cast<const bf16*>(x);
+            const TW* wt = reinterpret_cast<const TW*>(w);
+            if (ydtype == M3_DTYPE_BF16)
+                hipLaunchKernelGGL((rmsnorm_fwd_vec_kernel<TW, bf16>), grid, dim3(kNormThreads), 0,
+                                   stream, xb, wt, reinterpret_cast<bf16*>(y), rstd, rows, d, eps);
+            else
+                hipLaunchKernelGGL((rmsnorm_fwd_vec_kernel<TW, float>), grid, dim3(kNormThreads), 0,
+                                   stream, xb, wt, reinterpret_cast<float*>(y), rstd, rows, d, eps);
+            return;
+        }
+    }
     if (ydtype == M3_DTYPE_BF16)
         hipLaunchKernelGGL((rmsnorm_fwd_kernel<TX, TW, bf16>), grid, dim3(kNormThreads), 0, stream,
                            x, w, y, rstd, rows, d, eps);

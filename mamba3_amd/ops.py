@@ -583,3 +583,21 @@ def small_swiglu(x: torch.Tensor, norm_w: Optional[torch.Tensor], eps: float,
 @small_swiglu.register_fake
 def _(x, norm_w, eps, w_gate, w_up):
     return x.new_empty(x.shape[0], w_gate.shape[0])
+
+
+@torch.library.custom_op(f"{NS}::silu_mul", mutates_args=())
+def silu_mul(gate_up: torch.Tensor, d_ff: int) -> torch.Tensor:
+    """m3_silu_mul: silu(gate_up[..., :d_ff]) * gate_up[..., d_ff:2 d_ff] for bf16 rows (the
+    output of one GEMM over [w_gate; w_up]); no backward."""
+    _native.require_gpu(gate_up)
+    g2 = gate_up.reshape(-1, gate_up.shape[-1])
+    if g2.stride(-1) != 1:
+        g2 = g2.contiguous()
+    out = torch.empty(g2.shape[0], d_ff, device=gate_up.device, dtype=torch.bfloat16)
+    _native.silu_mul(g2, d_ff, out)
+    return out.view(*gate_up.shape[:-1], d_ff)
+
+
+@silu_mul.register_fake
+def _(gate_up, d_ff):
+    return gate_up.new_empty(*gate_up.shape[:-1], d_ff)

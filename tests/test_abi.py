@@ -300,3 +300,12 @@ def test_small_projections_reject_bad_arguments(lib):
     # the norm weight counts toward the limit on the C side too (8 x 3648 + 8 + 3648 > 32768)
     assert lib.m3_small_linear(fake, fake, 1e-5, fake, None, 1.0, fake, *args(8, 8, 3648)) == 3
     assert lib.m3_small_linear(fake, fake + 8, 1e-5, fake, None, 1.0, fake, *args(4, 8, 64)) == 5
+
+
+def test_silu_mul_rejects_bad_arguments(lib):
+    fake = 256
+    assert lib.m3_silu_mul(None, 4, 8, 16, fake, None) == 1
+    assert lib.m3_silu_mul(fake, 4, 8, 16, None, None) == 1
+    assert lib.m3_silu_mul(fake, 0, 8, 16, fake, None) == 2
+    assert lib.m3_silu_mul(fake, 4, 8, 15, fake, None) == 2  # the row must hold gate and up
+    assert lib.m3_silu_mul(fake, 1 << 30, 1 << 10, 1 << 11, fake, None) == 2  # 32-bit grid

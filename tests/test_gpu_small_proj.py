@@ -129,3 +129,31 @@ def test_lm_logits_on_small_kernel(cuda_device):
     want = ref.rmsnorm(x, lm.norm.weight.detach().cpu(), 1e-5).float() @ lm.lm_head.weight.detach().float().cpu().t()
     assert got.shape == (4, 32000)
     assert max_rel(got, want) < TOL
+
+
+@pytest.mark.parametrize("rows,d_ff,stride", [(8192, 2112, 4352), (7, 100, 256), (33, 64, 128)])
+def test_silu_mul_matches_host_reference(rows, d_ff, stride, cuda_device):
+    """m3_silu_mul on a concatenated gate / up projection: 16-byte pieces (d_ff and the row
+    stride multiples of 8) and the element path (d_ff = 100)."""
+    g = torch.Generator().manual_seed(rows + d_ff)
+    gu = (torch.randn(rows, stride, generator=g) * 2).to(torch.bfloat16)
+    want = F.silu(gu[:, :d_ff].float()) * gu[:, d_ff:2 * d_ff].float()
+    with torch.no_grad():
+        got = ops.silu_mul(gu.to(cuda_device), d_ff)
+    assert got.shape == (rows, d_ff) and got.dtype == torch.bfloat16
+    assert max_rel(got, want) < TOL
+
+
+def test_swiglu_hidden_one_gemm_matches_two(cuda_device):
+    """SwiGLU.hidden in bf16 without autograd (one GEMM over [w_gate; w_up], padded to whole
+    256-column tiles, then m3_silu_mul) against the two-GEMM form with autograd on."""
+    from mamba3_amd.block import SwiGLU
+    torch.manual_seed(0)
+    mlp = SwiGLU(768, 2112).to(cuda_device, torch.bfloat16)
+    x = torch.randn(3, 100, 768, device=cuda_device).to(torch.bfloat16)
+    with torch.no_grad():
+        fused = mlp.hidden(x)
+        assert mlp.__dict__["_gate_up"][1].shape == (4352, 768)
+    two = mlp.hidden(x)  # autograd on: the two-GEMM form
+    assert fused.shape == two.shape == (3, 100, 2112)
+    assert max_rel(fused, two.detach()) < BF16_TOL
