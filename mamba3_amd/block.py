@@ -65,7 +65,7 @@ class SwiGLU(nn.Module):
             cache = (key, w)
             self.__dict__["_gate_up"] = cache
         gu = F.linear(x.reshape(-1, x.shape[-1]), cache[1])
-        return ops.silu_mul(gu, d_ff).view(*x.shape[:-1], d_ff)
+        return ops.silu_mul_fast(gu, d_ff).view(*x.shape[:-1], d_ff)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         return self.w_down(self.hidden(x))
@@ -158,17 +158,17 @@ class KulaMambaBlock(nn.Module):
     def _small_step_tail(self, x: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
         """x + s out_proj(y), then the MLP residual, on the small-batch kernels."""
         s = self.residual_scale
-        x = ops.small_linear(y, None, 0.0, self.ssm.out_proj.weight, x, s)
+        x = ops.small_linear_fast(y, None, 0.0, self.ssm.out_proj.weight, x, s)
         if self.use_mlp:
             mlp = self.mlp
-            h = ops.small_swiglu(x, self.mlp_norm.weight, float(self.mlp_norm.eps),
+            h = ops.small_swiglu_fast(x, self.mlp_norm.weight, float(self.mlp_norm.eps),
                                  mlp.w_gate.weight, mlp.w_up.weight)
-            x = ops.small_linear(h, None, 0.0, mlp.w_down.weight, x, s)
+            x = ops.small_linear_fast(h, None, 0.0, mlp.w_down.weight, x, s)
         return x
 
     def step(self, x: torch.Tensor, ssm_state: dict):
         if self._small_step_usable(x):
-            proj = ops.small_linear(x, self.ssm_norm.weight, float(self.ssm_norm.eps),
+            proj = ops.small_linear_fast(x, self.ssm_norm.weight, float(self.ssm_norm.eps),
                                     self.ssm.in_proj.weight, None, 1.0)
             y, new_state = self.ssm._step_from_proj(proj, ssm_state)
             return self._small_step_tail(x, y), new_state
@@ -301,7 +301,7 @@ def _block_step_into(block: KulaMambaBlock, x: torch.Tensor, st_in: dict, st_out
     ssm = block.ssm
     small = block._small_step_usable(x)
     if small:
-        proj = ops.small_linear(x, block.ssm_norm.weight, float(block.ssm_norm.eps),
+        proj = ops.small_linear_fast(x, block.ssm_norm.weight, float(block.ssm_norm.eps),
                                 ssm.in_proj.weight, None, 1.0)
     else:
         proj = ssm.in_proj(block.ssm_norm(x))
@@ -323,7 +323,7 @@ def _lm_logits(lm: "KulaMambaLM", x: torch.Tensor) -> torch.Tensor:
     w = lm.lm_head.weight
     if (lm.lm_head.bias is None and lm.norm.dim in (-1, 1)
             and ops.small_proj_usable(x, lm.norm.weight, w, norm=True)):
-        return ops.small_linear(x, lm.norm.weight, float(lm.norm.eps), w, None, 1.0)
+        return ops.small_linear_fast(x, lm.norm.weight, float(lm.norm.eps), w, None, 1.0)
     return lm.lm_head(lm.norm(x))
 
 

@@ -233,7 +233,7 @@ class KulaMamba(nn.Module):
         y, state = self._step_pre_out(hidden_states, ssm_state, dt_scale)
         w = self.out_proj.weight
         if self.out_proj.bias is None and ops.small_proj_usable(y, w):
-            out = ops.small_linear(y, None, 0.0, w, None, 1.0)
+            out = ops.small_linear_fast(y, None, 0.0, w, None, 1.0)
         else:
             out = self.out_proj(y)
         if not squeeze:
@@ -248,7 +248,7 @@ class KulaMamba(nn.Module):
         _native.require_gpu(x_in)
         w = self.in_proj.weight
         if self.in_proj.bias is None and ops.small_proj_usable(x_in, w):
-            proj = ops.small_linear(x_in, None, 0.0, w, None, 1.0)
+            proj = ops.small_linear_fast(x_in, None, 0.0, w, None, 1.0)
         else:
             proj = self.in_proj(x_in)
         return self._step_from_proj(proj, ssm_state, dt_scale)
@@ -259,7 +259,7 @@ class KulaMamba(nn.Module):
         self._check_norm_eps()
         h_in, prev_in, angle_in = self._check_state(ssm_state, proj.shape[0])
         scale = self._dt_scale(dt_scale, (proj.shape[0], self.nheads), proj.device)
-        y, h_out, prev_out, angle_out = ops.step(proj, *self._small_params(), scale, h_in,
+        y, h_out, prev_out, angle_out = ops.step_fast(proj, *self._small_params(), scale, h_in,
                                                  prev_in, angle_in, *ops.layer_args(self))
         return y, {"h": h_out, "angle": angle_out, "prev_BX": prev_out}
 

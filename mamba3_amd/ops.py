@@ -270,8 +270,7 @@ prefill_train.register_autograd(_prefill_train_backward, setup_context=_prefill_
 
 
 # ---------------------------------------------------------------------------- step
-@torch.library.custom_op(f"{NS}::step", mutates_args=())
-def step(proj: torch.Tensor, A_log: torch.Tensor, D: torch.Tensor, dt_bias: torch.Tensor,
+def _step_eager(proj: torch.Tensor, A_log: torch.Tensor, D: torch.Tensor, dt_bias: torch.Tensor,
          B_norm_w: torch.Tensor, C_norm_w: torch.Tensor, B_bias: torch.Tensor,
          C_bias: torch.Tensor, mimo_x: torch.Tensor, mimo_z: torch.Tensor,
          mimo_down: torch.Tensor, dt_scale: Optional[torch.Tensor], h: torch.Tensor,
@@ -288,6 +287,9 @@ def step(proj: torch.Tensor, A_log: torch.Tensor, D: torch.Tensor, dt_bias: torc
               mimo_down, dt_scale, h, prev_bx, angle, *out, nheads, headdim, d_state,
               mimo_rank, ngroups, trap, cplx, eps)
     return tuple(out)
+
+
+step = torch.library.custom_op(f"{NS}::step", _step_eager, mutates_args=())
 
 
 @step.register_fake
@@ -552,8 +554,7 @@ def small_proj_usable(x: torch.Tensor, *weights, norm: bool = False) -> bool:
     return True
 
 
-@torch.library.custom_op(f"{NS}::small_linear", mutates_args=())
-def small_linear(x: torch.Tensor, norm_w: Optional[torch.Tensor], eps: float, weight: torch.Tensor,
+def _small_linear_eager(x: torch.Tensor, norm_w: Optional[torch.Tensor], eps: float, weight: torch.Tensor,
                  residual: Optional[torch.Tensor], scale: float) -> torch.Tensor:
     """m3_small_linear: [residual +] scale * (n W^T), n = RMSNorm(x; norm_w) or x, for bf16
     x (m <= 8, k) (check with small_proj_usable); no backward."""
@@ -564,13 +565,15 @@ def small_linear(x: torch.Tensor, norm_w: Optional[torch.Tensor], eps: float, we
     return out
 
 
+small_linear = torch.library.custom_op(f"{NS}::small_linear", _small_linear_eager, mutates_args=())
+
+
 @small_linear.register_fake
 def _(x, norm_w, eps, weight, residual, scale):
     return x.new_empty(x.shape[0], weight.shape[0])
 
 
-@torch.library.custom_op(f"{NS}::small_swiglu", mutates_args=())
-def small_swiglu(x: torch.Tensor, norm_w: Optional[torch.Tensor], eps: float,
+def _small_swiglu_eager(x: torch.Tensor, norm_w: Optional[torch.Tensor], eps: float,
                  w_gate: torch.Tensor, w_up: torch.Tensor) -> torch.Tensor:
     """m3_small_swiglu: silu(n W_gate^T) * (n W_up^T), n = RMSNorm(x; norm_w) or x, for bf16
     x (m <= 8, k); no backward."""
@@ -580,13 +583,15 @@ def small_swiglu(x: torch.Tensor, norm_w: Optional[torch.Tensor], eps: float,
     return out
 
 
+small_swiglu = torch.library.custom_op(f"{NS}::small_swiglu", _small_swiglu_eager, mutates_args=())
+
+
 @small_swiglu.register_fake
 def _(x, norm_w, eps, w_gate, w_up):
     return x.new_empty(x.shape[0], w_gate.shape[0])
 
 
-@torch.library.custom_op(f"{NS}::silu_mul", mutates_args=())
-def silu_mul(gate_up: torch.Tensor, d_ff: int) -> torch.Tensor:
+def _silu_mul_eager(gate_up: torch.Tensor, d_ff: int) -> torch.Tensor:
     """m3_silu_mul: silu(gate_up[..., :d_ff]) * gate_up[..., d_ff:2 d_ff] for bf16 rows (the
     output of one GEMM over [w_gate; w_up]); no backward."""
     _native.require_gpu(gate_up)
@@ -598,6 +603,33 @@ def silu_mul(gate_up: torch.Tensor, d_ff: int) -> torch.Tensor:
     return out.view(*gate_up.shape[:-1], d_ff)
 
 
+silu_mul = torch.library.custom_op(f"{NS}::silu_mul", _silu_mul_eager, mutates_args=())
+
+
 @silu_mul.register_fake
 def _(gate_up, d_ff):
     return gate_up.new_empty(*gate_up.shape[:-1], d_ff)
+
+
+# ---------------------------------------------------------------- eager decode calls
+def _direct() -> bool:
+    """Eager calls with autograd off bypass the dispatcher: its per-call host time is what a
+    per-token decode loop waits on. Traced calls and calls under autograd go through the
+    registered ops (whose missing backward then raises)."""
+    return not torch.is_grad_enabled() and not torch.compiler.is_compiling()
+
+
+def step_fast(*args):
+    return (_step_eager if _direct() else step)(*args)
+
+
+def small_linear_fast(*args):
+    return (_small_linear_eager if _direct() else small_linear)(*args)
+
+
+def small_swiglu_fast(*args):
+    return (_small_swiglu_eager if _direct() else small_swiglu)(*args)
+
+
+def silu_mul_fast(*args):
+    return (_silu_mul_eager if _direct() else silu_mul)(*args)
