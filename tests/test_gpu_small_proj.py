@@ -157,3 +157,27 @@ def test_swiglu_hidden_one_gemm_matches_two(cuda_device):
     two = mlp.hidden(x)  # autograd on: the two-GEMM form
     assert fused.shape == two.shape == (3, 100, 2112)
     assert max_rel(fused, two.detach()) < BF16_TOL
+
+
+def test_d2048_block_step_on_small_kernels_matches_unfused_step(cuda_device):
+    """The d_model-2048 block (d_state 256, headdim 128, rank 4; in_proj K 2048 with its
+    norm, out_proj K 4096, w_down K 5504) at batch 4 on the small-batch kernels against the
+    library path."""
+    torch.manual_seed(0)
+    block = mamba3_amd.KulaMambaBlock(2048, d_state=256, headdim=128, mimo_rank=4,
+                                      residual_scale=0.125).to(cuda_device, torch.bfloat16).eval()
+    g = torch.Generator().manual_seed(5)
+    x0 = torch.randn(4, 32, 2048, generator=g).to(torch.bfloat16).to(cuda_device)
+    tok = torch.randn(4, 2048, generator=g).to(torch.bfloat16).to(cuda_device)
+    with torch.no_grad():
+        _, st = block.prefill(x0)
+        assert block._small_step_usable(tok)
+        y_small, st_small = block.step(tok, st)
+        block._small_step_usable = lambda x: False
+        y_lib, st_lib = block.step(tok, st)
+        del block._small_step_usable
+        # 8 rows: w_down's 5504-wide rows no longer fit the staged LDS, so the library runs
+        assert not block._small_step_usable(torch.cat([tok, tok]))
+    assert max_rel(y_small, y_lib) < BF16_TOL
+    for k in ("h", "prev_BX", "angle"):
+        assert max_rel(st_small[k], st_lib[k]) < BF16_TOL, k
