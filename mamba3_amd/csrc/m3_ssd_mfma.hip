@@ -3,10 +3,11 @@
 //
 // Work decomposition
 // ------------------
-// The sequence of every (batch, head) is cut into S segments of whole 64-token chunks.
-// One 512-thread workgroup (8 waves) owns one (batch, head, segment) and walks its
-// chunks in order, carrying the (P=64, N=128) fp32 state in MFMA accumulators, so no
-// per-chunk state ever goes to HBM. Three launches:
+// The sequence of every (batch, head) is cut into S segments of whole 64-token chunks
+// (mfma_plan: one segment, equal segments, or a short first and a long second segment
+// when the pairs leave CUs free). One 1024-thread workgroup (16 waves) owns one (batch,
+// head, segment) and walks its chunks in order, carrying the (P=64, N=128) fp32 state in
+// MFMA accumulators, so no per-chunk state ever goes to HBM. Three launches:
 //   1. bc_norm:    per token and group, B^ = RMSNorm(B) * w + bias and C^ likewise in
 //                  f16 (shared by every head, so computed once), pair-packed so that a
 //                  RoPE pair (n=2i, n=2i+1) of one rank is one 32-bit word.
@@ -100,6 +101,8 @@ struct __align__(16) Smem {
 
 struct Args {
     int B, T, H, G, S, cps;
+    int first;  // chunks of segment 0 (segments 1.. have cps chunks, the last may be shorter)
+    int order;  // 1: two segments, dispatched long-first per XCD (ssd_chunks<true>)
     int trap, cplx;
     int64_t rs;
     ProjLayout pl;
@@ -355,17 +358,28 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
 
     const int nseg = kFull ? a.S : a.S - 1;
-    // XCD-aware order: consecutive workgroups of one batch row land on one XCD.
+    // Workgroup i runs on XCD i % 8. Consecutive (batch, head) pairs (one batch row shares
+    // B^ / C^) are kept on one XCD. Split plan (a.order): each XCD first gets the long second
+    // segments of its pairs, one per CU, then the short first segments, which cycle through
+    // the remaining CUs while the long ones run.
     const int nblk = gridDim.x;
-    const int blk = (nblk % 8 == 0) ? (blockIdx.x % 8) * (nblk / 8) + blockIdx.x / 8 : blockIdx.x;
-    const int seg = blk % nseg;
-    const int bh = blk / nseg;
+    int seg, bh;
+    if (kFull && a.order) {
+        const int L = nblk / 16;  // pairs per XCD
+        const int i = blockIdx.x / 8;
+        seg = i < L ? 1 : 0;
+        bh = (blockIdx.x % 8) * L + (i < L ? i : i - L);
+    } else {
+        const int blk = (nblk % 8 == 0) ? (blockIdx.x % 8) * (nblk / 8) + blockIdx.x / 8 : blockIdx.x;
+        seg = blk % nseg;
+        bh = blk / nseg;
+    }
     const int b = bh / a.H, h = bh % a.H;
     const int grp = h / (a.H / a.G);
     const int T = a.T;
     const int K = (T + Q - 1) / Q;
-    const int k_begin = seg * a.cps;
-    const int k_end = min(K, k_begin + a.cps);
+    const int k_begin = seg == 0 ? 0 : a.first + (seg - 1) * a.cps;
+    const int k_end = min(K, seg == 0 ? a.first : k_begin + a.cps);
     const int rs = (int)a.rs;
     const int bnrs = a.G * NR;  // elements between tokens in Bn / Cn
 
@@ -946,28 +960,79 @@ bool mfma_prefill_supported(const m3_layer_desc& d, const void* proj, const void
     return true;
 }
 
-// Segments per (batch, head). One workgroup occupies a CU, so the full pass takes
-// ceil(B*H*S / 256) rounds of ceil(K/S) chunks, and the state-only pass adds about a third
-// of that per segment but the last. Pick the S that minimises this estimate.
-static void mfma_segments(const m3_layer_desc& d, int& S, int& cps) {
+// Work plan of the chunk walk: every (batch, head) sequence is cut into S segments, segment 0
+// of `first` chunks and the others of `cps` chunks (the last may be shorter). Segments after
+// the first need their predecessors' end states, from a state-only pass over segments
+// 0..S-2 launched before the full pass.
+struct SegPlan {
+    int S, cps, first, order;
+};
+
+// Costs in chunk-times of one full-pass workgroup (one workgroup fills a CU). The state-only
+// pass takes 0.45 of that per chunk (measured at (8, 8192): 2.17 us against 4.85 us); a
+// split plan also pays one more launch and each segment's combine of earlier states.
+constexpr double kStatePassCost = 0.45;
+constexpr int kXcds = 8, kCusPerXcd = 32;
+
+// Makespan of workgroups of the given lengths dispatched in order onto the CUs of one XCD,
+// each to the CU that frees first.
+static double xcd_makespan(const double* len, int n) {
+    double cu[kCusPerXcd] = {};
+    double end = 0.0;
+    for (int i = 0; i < n; ++i) {
+        double* c = std::min_element(cu, cu + kCusPerXcd);
+        *c += len[i];
+        end = std::max(end, *c);
+    }
+    return end;
+}
+
+// Uniform plans (S equal segments, workgroups of a launch spread evenly over the XCDs) and,
+// when the (batch, head) pairs fill at most one CU each and divide evenly over the XCDs, the
+// long-first split: segment 0 short, segment 1 long, the long segments start at once and the
+// short ones cycle through the CUs left over. Pick the cheapest.
+static SegPlan mfma_plan(const m3_layer_desc& d) {
     const int K = (d.seqlen + mf::Q - 1) / mf::Q;
     const int64_t bh = (int64_t)d.batch * d.nheads;
-    const int64_t cus = 256;
-    double best = 1e30;
-    S = 1;
-    for (int s = 1; s <= std::min(K, 64); ++s) {
+    // The search below costs tens of microseconds of host time; the workspace query and the
+    // launch of one call ask for the same shape, so the last plan is kept per thread.
+    thread_local int64_t memo_bh = -1;
+    thread_local int memo_K = -1;
+    thread_local SegPlan memo{1, 1, 1, 0};
+    if (bh == memo_bh && K == memo_K) return memo;
+    const int64_t cus = (int64_t)kXcds * kCusPerXcd;
+    auto rounds = [&](int64_t n) { return (double)((n + cus - 1) / cus); };
+    SegPlan best{1, K, K, 0};
+    double best_cost = rounds(bh) * K;
+    for (int s = 2; s <= std::min(K, 64); ++s) {
         const int c = (K + s - 1) / s;
         const int seff = (K + c - 1) / c;
-        const double full = (double)((bh * seff + cus - 1) / cus) * c;
-        const double part = seff > 1 ? 0.35 * (double)((bh * (seff - 1) + cus - 1) / cus) * c : 0.0;
-        const double cost = full + part + 0.5 * seff;  // small per-segment combine cost
-        if (cost < best - 1e-9) {
-            best = cost;
-            S = seff;
+        if (seff != s) continue;
+        const double cost = rounds(bh * s) * c + kStatePassCost * rounds(bh * (s - 1)) * c + 1.0 + 0.25 * (s - 1);
+        if (cost < best_cost - 1e-9) {
+            best_cost = cost;
+            best = SegPlan{s, c, c, 0};
         }
     }
-    cps = (K + S - 1) / S;
-    S = (K + cps - 1) / cps;
+    if (bh % kXcds == 0 && bh <= cus && K >= 2) {
+        const int L = (int)(bh / kXcds);
+        double len[2 * kCusPerXcd];
+        for (int f = 1; f <= K / 2; ++f) {
+            for (int i = 0; i < L; ++i) {
+                len[i] = K - f;
+                len[L + i] = f;
+            }
+            const double cost = kStatePassCost * f + xcd_makespan(len, 2 * L) + 1.0 + 0.25;
+            if (cost < best_cost - 1e-9) {
+                best_cost = cost;
+                best = SegPlan{2, K - f, f, 1};
+            }
+        }
+    }
+    memo_bh = bh;
+    memo_K = K;
+    memo = best;
+    return best;
 }
 
 // B^ / C^ rows of every (token, group) of the layer, pair-packed f16 (bc_norm).
@@ -982,8 +1047,7 @@ void launch_bc_norm(const m3_layer_desc& d, const m3_layer_params& p, const void
 }
 
 size_t mfma_prefill_workspace(const m3_layer_desc& d) {
-    int S, cps;
-    mfma_segments(d, S, cps);
+    const int S = mfma_plan(d).S;
     const size_t ntg = (size_t)d.batch * d.seqlen * d.ngroups;
     const size_t nseg = (size_t)d.batch * d.nheads * (S - 1);
     const size_t bc_bytes = 2 * ntg * mf::NR * sizeof(f16);
@@ -993,10 +1057,11 @@ size_t mfma_prefill_workspace(const m3_layer_desc& d) {
 int launch_mfma_prefill(const m3_layer_desc& d, const m3_layer_params& p, const void* proj,
                         const float* dt_scale, void* y_out, float* h_final, float* angle,
                         float* prev_bx, void* workspace, hipStream_t stream) {
-    int S, cps;
-    mfma_segments(d, S, cps);
+    const SegPlan plan = mfma_plan(d);
+    const int S = plan.S;
     mf::Args a;
-    a.B = d.batch; a.T = d.seqlen; a.H = d.nheads; a.G = d.ngroups; a.S = S; a.cps = cps;
+    a.B = d.batch; a.T = d.seqlen; a.H = d.nheads; a.G = d.ngroups;
+    a.S = S; a.cps = plan.cps; a.first = plan.first; a.order = plan.order;
     a.trap = d.use_trapezoidal; a.cplx = d.use_complex;
     a.rs = d.proj_row_stride;
     a.pl = proj_layout(d);
