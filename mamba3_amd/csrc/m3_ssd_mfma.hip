@@ -90,12 +90,12 @@ struct __align__(16) Smem {
     f16 X[2][Q * R][P];       // X rows (u,r') = x_u * mimo_x[r'], columns p swizzled (xsw);
                               // double-buffered by chunk parity
     f16 H[P][N + PAD];        // incoming state times kHScale
-    unsigned Gt[2][Q][P];     // gate factors (g_0, g_1) as a bf16 pair per (t, p), columns
-                              // swizzled (gsw); the low half is then replaced by the output.
-                              // Double-buffered by chunk parity.
+    bf16 Zt[2][Q][P];         // z of the chunk per (t, p), columns swizzled (zsw); each entry
+                              // is replaced in place by the gated output. Double-buffered by
+                              // chunk parity.
     Tok tok[NSLOT];
     float rot[NH];            // per-pair angle scratch (prologue / epilogue)
-    float mzdT[4][P];         // per p: -mimo_z[0] log2e, -mimo_z[1] log2e, mimo_down*mimo_z [0], [1]
+    f32x4 mzd[P];             // per p: -mimo_z[0] log2e, -mimo_z[1] log2e, mimo_down*mimo_z [0], [1]
     f16 mxT[R][P];            // mimo_x per rank and p
 };
 
@@ -132,9 +132,10 @@ __device__ __forceinline__ int sw_cb(int row, int col) { return col ^ (32 * ((ro
 // transpose reads of the MFMA operands (4 rows x 16 columns per 16 lanes, 8 rows per
 // 32-lane pass) and the 128-bit row writes are free of bank conflicts.
 __device__ __forceinline__ int xsw(int row, int col) { return col ^ (16 * ((row >> 1) & 3)); }
-// Gate tile [t][p] of 32-bit words: 16-word groups swapped on every other token pair, so
-// the MFMA waves' 32-bit accesses (rows 2 apart across 16-lane groups) use distinct banks.
-__device__ __forceinline__ int gsw(int t, int p) { return p ^ (16 * ((t >> 1) & 1)); }
+// z tile [t][p] of bf16: 16-column groups XOR-swizzled by (t/2)%4, so the MFMA waves'
+// 16-bit accesses (16 consecutive columns per 16-lane group, the four groups on rows 2
+// apart) use distinct banks; the helpers' 128-bit row accesses stay contiguous.
+__device__ __forceinline__ int zsw(int t, int p) { return p ^ (16 * ((t >> 1) & 3)); }
 
 
 
@@ -195,8 +196,8 @@ __global__ __launch_bounds__(256) void bc_norm(const bf16* __restrict__ proj, in
 //   G2  Y += S X as the A operand. The pair's accumulator rows give this lane the k values
 //       (u,r') = 32 s2 + 4 g + v and 32 s2 + 16 + 4 g + v (g = lane/16, v < 4); the X
 //       operand is read with transpose reads in the same row order.
-// Then out[t][p] = y_0 g_0 + y_1 g_1 with the gate factors of the gate tile; the bf16
-// result replaces the low half of the factor word.
+// Then out[t][p] = sum_r mimo_down_r silu(z mimo_z_r) y_r from z in the z tile; the bf16
+// result replaces z there.
 template <int I>
 __device__ __forceinline__ void out_block(Smem& sm, const Tok& tk, int par, int g16, int l16, float D_h) {
     constexpr int NP = I / 2 + 1;  // column-block pairs
@@ -320,26 +321,33 @@ __device__ __forceinline__ void out_block(Smem& sm, const Tok& tk, int par, int 
         M3_FENCE();
     }
 
-    // out = y_0 g_0 + y_1 g_1, written over the low half of the factor word.
+    // Gate and MIMO down-projection, out = sum_r mimo_down_r silu(z mimo_z_r) y_r. With
+    // e_r = exp(-z mimo_z_r) (clamped at 2^60 so the products stay finite) and
+    // w_r = mimo_down_r mimo_z_r y_r: out = z (w_0 (1 + e_1) + w_1 (1 + e_0)) / ((1+e_0)(1+e_1)).
 #pragma unroll
     for (int pt = 0; pt < 4; ++pt) {
         const int p = 16 * pt + l16;
+        const f32x4 m = sm.mzd[p];
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
             const int t = 8 * I + 2 * g16 + tt;
-            unsigned* gp = &sm.Gt[par][t][gsw(t, p)];
-            const unsigned gw = *gp;
-            const float o = yacc[pt][2 * tt] * bf16_f32(gw & 0xffffu) +
-                            yacc[pt][2 * tt + 1] * __builtin_bit_cast(float, gw & 0xffff0000u);
-            *reinterpret_cast<bf16*>(gp) = (bf16)o;
+            bf16* zp = &sm.Zt[par][t][zsw(t, p)];
+            const float z = (float)*zp;
+            const float e0 = __builtin_amdgcn_exp2f(fminf(z * m[0], 60.f));
+            const float e1 = __builtin_amdgcn_exp2f(fminf(z * m[1], 60.f));
+            const float d0 = 1.f + e0;
+            const float zi = z * __builtin_amdgcn_rcpf(__builtin_fmaf(d0, e1, d0));
+            const float w0 = yacc[pt][2 * tt] * m[2];
+            const float w1 = yacc[pt][2 * tt + 1] * m[3];
+            *zp = (bf16)(zi * (__builtin_fmaf(w0, e1, w0) + __builtin_fmaf(w1, e0, w1)));
         }
     }
 }
 
 // Pipelined chunk walk, per chunk k:
 //   barrier A -> M(k): MFMA waves: state update G4 on chunk k's tiles, output block of
-//                chunk k. Helper waves: RoPE rotation, X rows and gate factors of chunk k+1
-//                (X rows and gate factors straight into the buffers of the other parity),
+//                chunk k, gated from the z tile. Helper waves: RoPE rotation, X rows and z of
+//                chunk k+1 (X rows and z straight into the buffers of the other parity),
 //                reads of chunk k+2 issued as registers free up.
 //   barrier B -> W(k+1): MFMA waves write the f16 state copy H_{k+1}; helper waves store
 //                chunk k's output and write the C~ / B~ tiles of chunk k+1.
@@ -348,7 +356,7 @@ __device__ __forceinline__ void out_block(Smem& sm, const Tok& tk, int par, int 
 //                each SIMD carries blocks {s, 7-s} (the same causal work); wave 0 also
 //                computes the token scalars two chunks ahead.
 //   helper wave 8+h: RoPE pairs 16 (h%4) + 2 (lane%8) + {0, 1} for tokens 8 (lane/8) +
-//                4 (h/4) + {0..3}; X rows and gate factors of token 8h + lane/8, columns
+//                4 (h/4) + {0..3}; X rows and z of token 8h + lane/8, columns
 //                8 (lane%8) .. +7. Helpers issue every global read and store, so the MFMA
 //                waves never wait on memory.
 template <bool kFull>
@@ -390,10 +398,8 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
     const int lane0 = tid & 63;
     if (kFull && tid < P) {
         const float z0 = a.prm.mimo_z[(h * P + tid) * R], z1 = a.prm.mimo_z[(h * P + tid) * R + 1];
-        sm.mzdT[0][tid] = -z0 * kLog2e;
-        sm.mzdT[1][tid] = -z1 * kLog2e;
-        sm.mzdT[2][tid] = a.prm.mimo_down[(h * P + tid) * R] * z0;
-        sm.mzdT[3][tid] = a.prm.mimo_down[(h * P + tid) * R + 1] * z1;
+        sm.mzd[tid] = f32x4{-z0 * kLog2e, -z1 * kLog2e, a.prm.mimo_down[(h * P + tid) * R] * z0,
+                            a.prm.mimo_down[(h * P + tid) * R + 1] * z1};
     }
     if (tid < P) {
         sm.mxT[0][tid] = (f16)a.prm.mimo_x[(h * P + tid) * R];
@@ -814,33 +820,12 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
             *reinterpret_cast<f16x8*>(&sm.X[par][2 * t][xsw(2 * t, p)]) = xv * mx0;
             *reinterpret_cast<f16x8*>(&sm.X[par][2 * t + 1][xsw(2 * t + 1, p)]) = xv * mx1;
         };
-        // ---- gate factors g_r = mimo_down_r silu(z mimo_z_r) of token tx, columns p0..p0+7,
-        // into gate buffer par: with e_r = exp(-z mimo_z_r) (clamped at 2^60 so the product
-        // stays finite), g_r = (mimo_down_r mimo_z_r) z (1 + e_{1-r}) / ((1+e_0)(1+e_1)).
-        auto gate = [&](int par) {
+        // ---- z of token 8 hw + lane/8, columns 8 (lane%8) .. +7, into z tile par (the MFMA
+        // waves apply the gate in their output epilogue)
+        auto stage_z = [&](int par) {
             const int lane = opaque(threadIdx.x & 63);
             const int t = 8 * hw + (lane >> 3), p = 8 * (lane & 7);
-#pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-                const f32x4 a0 = *reinterpret_cast<const f32x4*>(&sm.mzdT[0][p + 4 * hh]);
-                const f32x4 a1 = *reinterpret_cast<const f32x4*>(&sm.mzdT[1][p + 4 * hh]);
-                const f32x4 b0 = *reinterpret_cast<const f32x4*>(&sm.mzdT[2][p + 4 * hh]);
-                const f32x4 b1 = *reinterpret_cast<const f32x4*>(&sm.mzdT[3][p + 4 * hh]);
-                u32x4 gw;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const unsigned zw = zr[2 * hh + (i >> 1)];
-                    const float z = (i & 1) ? __builtin_bit_cast(float, zw & 0xffff0000u) : bf16_f32(zw & 0xffffu);
-                    const float e0 = __builtin_amdgcn_exp2f(fminf(z * a0[i], 60.f));
-                    const float e1 = __builtin_amdgcn_exp2f(fminf(z * a1[i], 60.f));
-                    const float zi = z * __builtin_amdgcn_rcpf((1.f + e0) * (1.f + e1));
-                    const float g0 = zi * __builtin_fmaf(b0[i], e1, b0[i]);
-                    const float g1 = zi * __builtin_fmaf(b1[i], e0, b1[i]);
-                    const bf16x2 gp = bf16x2{(bf16)g0, (bf16)g1};
-                    gw[i] = __builtin_bit_cast(unsigned, gp);
-                }
-                *reinterpret_cast<u32x4*>(&sm.Gt[par][t][gsw(t, p + 4 * hh)]) = gw;
-            }
+            *reinterpret_cast<u32x4*>(&sm.Zt[par][t][zsw(t, p)]) = zr;
         };
         // ---- W phase: tiles of the prepared chunk
         auto write_tiles = [&]() {
@@ -864,16 +849,11 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
                 M3_LDS_FENCE();
             }
         };
-        // ---- W phase: chunk kk's output (low halves of its gate buffer) to HBM
+        // ---- W phase: chunk kk's output (its z tile, overwritten by the MFMA waves) to HBM
         auto store_out = [&](int kk) {
             const int lane = opaque(threadIdx.x & 63);
             const int t = 8 * hw + (lane >> 3), p = 8 * (lane & 7);
-            const u32x4 w0 = *reinterpret_cast<const u32x4*>(&sm.Gt[kk & 1][t][gsw(t, p)]);
-            const u32x4 w1 = *reinterpret_cast<const u32x4*>(&sm.Gt[kk & 1][t][gsw(t, p + 4)]);
-            const u32x4 o = {__builtin_amdgcn_perm(w0[1], w0[0], 0x05040100u),
-                             __builtin_amdgcn_perm(w0[3], w0[2], 0x05040100u),
-                             __builtin_amdgcn_perm(w1[1], w1[0], 0x05040100u),
-                             __builtin_amdgcn_perm(w1[3], w1[2], 0x05040100u)};
+            const u32x4 o = *reinterpret_cast<const u32x4*>(&sm.Zt[kk & 1][t][zsw(t, p)]);
             const int s0 = kk * Q;
             const int HP = a.H * P;
             const __amdgpu_buffer_rsrc_t ry =
@@ -881,7 +861,7 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
             __builtin_amdgcn_raw_buffer_store_b128(o, ry, (t * HP + h * P + p) * 2, 0, kStream);
         };
 
-        // prologue: first chunk's tiles and gate factors, reads of the second chunk
+        // prologue: first chunk's tiles and z, reads of the second chunk
         load_all(k_begin);
         __syncthreads();
         prep_x(k_begin & 1);
@@ -889,7 +869,7 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
         load_x(k_begin + 1);
         M3_FENCE();
         if (kFull) {
-            gate(k_begin & 1);
+            stage_z(k_begin & 1);
             M3_FENCE();
             load_z(k_begin + 1);
             M3_FENCE();
@@ -910,7 +890,7 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
                 load_x(k + 2);
                 M3_FENCE();
                 if (kFull) {
-                    gate((k + 1) & 1);
+                    stage_z((k + 1) & 1);
                     M3_FENCE();
                     load_z(k + 2);
                     M3_FENCE();
