@@ -23,11 +23,13 @@
 // lanes) sum the lanes of a row, and lane m of the row writes output m.
 #include "m3_common.h"
 #include "m3_kernels.h"
+#include "m3_mfma.h"
 
 namespace m3 {
 
 constexpr int kGvThreads = 128;
 constexpr int kGvU = 8;  // weight pieces in flight per lane
+constexpr int kGvStage = 4;  // activation pieces staged per thread and pass
 
 typedef unsigned gv_u32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 gv_bf16x2 __attribute__((ext_vector_type(2)));
@@ -106,15 +108,36 @@ __global__ __launch_bounds__(kGvThreads) void gemv_small(GemvArgs a) {
     load_group(0);
 
     // Stage the activations (rows past M and the trailing piece are zero) and the norm weight.
-    for (int i = tid; i <= MM * kv; i += kGvThreads) {
-        gv_u32x4 v = {0u, 0u, 0u, 0u};
-        if (i / kv < M) v = *reinterpret_cast<const gv_u32x4*>(a.x + (int64_t)i * 8);
-        *reinterpret_cast<gv_u32x4*>(sx + (int64_t)i * 8) = v;
+    // Buffer reads past the M rows (and past the weight) return zero, so every read of a
+    // pass is issued unconditionally, before the pass's stores: one round trip per pass.
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, (int64_t)M * K * 2);
+    const int nstage = MM * kv + 1;
+    for (int i0 = 0; i0 < nstage; i0 += kGvThreads * kGvStage) {
+        gv_u32x4 v[kGvStage];
+#pragma unroll
+        for (int u = 0; u < kGvStage; ++u)
+            v[u] = __builtin_amdgcn_raw_buffer_load_b128(rx, (i0 + u * kGvThreads + tid) * 16, 0, 0);
+#pragma unroll
+        for (int u = 0; u < kGvStage; ++u) {
+            const int i = i0 + u * kGvThreads + tid;
+            if (i < nstage) *reinterpret_cast<gv_u32x4*>(sx + (int64_t)i * 8) = v[u];
+        }
     }
     bf16* snw = sx + (MM * kv + 1) * 8;
-    if constexpr (kNorm)
-        for (int i = tid; i < kv; i += kGvThreads)
-            *reinterpret_cast<gv_u32x4*>(snw + i * 8) = *reinterpret_cast<const gv_u32x4*>(a.nw + i * 8);
+    if constexpr (kNorm) {
+        const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.nw, (int64_t)K * 2);
+        for (int i0 = 0; i0 < kv; i0 += kGvThreads * kGvStage) {
+            gv_u32x4 v[kGvStage];
+#pragma unroll
+            for (int u = 0; u < kGvStage; ++u)
+                v[u] = __builtin_amdgcn_raw_buffer_load_b128(rw, (i0 + u * kGvThreads + tid) * 16, 0, 0);
+#pragma unroll
+            for (int u = 0; u < kGvStage; ++u) {
+                const int i = i0 + u * kGvThreads + tid;
+                if (i < kv) *reinterpret_cast<gv_u32x4*>(snw + i * 8) = v[u];
+            }
+        }
+    }
     __syncthreads();
     if constexpr (kNorm) {
         // fp32 sum of squares per row: 16-byte pieces per thread, a wave butterfly, the two

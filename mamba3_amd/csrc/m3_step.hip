@@ -68,9 +68,12 @@ __device__ __forceinline__ void st_angle(void* p, int64_t i, float v, bool is_bf
     else reinterpret_cast<float*>(p)[i] = v;
 }
 
-template <typename T, int RM, bool kExactR, int LPR, int VW, int NV, bool kFull>
+// RPL: rows in flight per lane (kStepRowsPerLane, or 1 when a workgroup's rows are one per
+// lane: then those rows' reads are issued with the prologue's, before its arithmetic).
+template <typename T, int RM, bool kExactR, int LPR, int VW, int NV, bool kFull, int RPL>
 __global__ __launch_bounds__(kStepThreads) void step_kernel(StepArgs a) {
     typedef typename StepVec<VW>::type vec;
+    constexpr bool kEarly = RPL == 1;
     constexpr int CPL = VW * NV;               // state columns per lane
     constexpr int kRows = kStepThreads / LPR;  // rows handled per pass of the block
     const int tid = threadIdx.x;
@@ -148,6 +151,36 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(StepArgs a) {
         }
     }
 
+    // Incoming state rows (the outgoing state is stored normally so the next step finds it
+    // in the caches). All loads are unconditional and issued before the arithmetic that uses
+    // them: rows past the block's end read its last row and lanes past the row end read the
+    // row's last vector (their B / C columns are zero); neither stores anything.
+    const int64_t sbase = ((int64_t)b * a.H + h) * P * N;
+    const vec* hin = reinterpret_cast<const vec*>(a.h_in + sbase);
+    const vec* pin = reinterpret_cast<const vec*>(a.prev_in + sbase);
+    vec* hout = reinterpret_cast<vec*>(a.h_out + sbase);
+    vec* pout = reinterpret_cast<vec*>(a.prev_out + sbase);
+    const int nvr = N / VW;       // vectors per row (P * N <= 256 * 512: int offsets)
+    const int v0 = q * NV;        // this lane's first vector in the row
+    // this workgroup's rows [pb, pe)
+    const int pb = ps * (P / a.psplit), pe = pb + P / a.psplit;
+    vec hv[RPL][NV], pv[RPL][NV];
+    T xv[RPL];
+    auto load_rows = [&](int pbase) {
+#pragma unroll
+        for (int it = 0; it < RPL; ++it) {
+            const int p = pbase + it * kRows < pe ? pbase + it * kRows : pe - 1;
+#pragma unroll
+            for (int v = 0; v < NV; ++v) {
+                const int vi = v0 + v < nvr ? v0 + v : nvr - 1;
+                hv[it][v] = __builtin_nontemporal_load(&hin[p * nvr + vi]);
+                pv[it][v] = __builtin_nontemporal_load(&pin[p * nvr + vi]);
+            }
+            xv[it] = pr[a.pl.x + (int64_t)h * P + p];
+        }
+    };
+    if constexpr (kEarly) load_rows(pb + row0 < pe ? pb + row0 : pe - 1);
+
     // Per-head scalars (mamba3/mamba3.py:278-282, 290-296).
     const float sc = sc_raw * scf + (1.f - scf);
     const TokenGate tg = token_gate(dt_raw, dt_bias, sc, -expf(A_log), lam_raw * trapf, a.trap != 0);
@@ -212,38 +245,12 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(StepArgs a) {
     const float* mx = a.prm.mimo_x + (int64_t)h * P * R;
     const float* mz = a.prm.mimo_z + (int64_t)h * P * R;
     const float* md = a.prm.mimo_down + (int64_t)h * P * R;
-    const int64_t sbase = ((int64_t)b * a.H + h) * P * N;
-    const vec* hin = reinterpret_cast<const vec*>(a.h_in + sbase);
-    const vec* pin = reinterpret_cast<const vec*>(a.prev_in + sbase);
-    vec* hout = reinterpret_cast<vec*>(a.h_out + sbase);
-    vec* pout = reinterpret_cast<vec*>(a.prev_out + sbase);
     T* yo = reinterpret_cast<T*>(a.y_out) + (int64_t)b * a.H * P + (int64_t)h * P;
-    const int nvr = N / VW;       // vectors per row (P * N <= 256 * 512: int offsets)
-    const int v0 = q * NV;        // this lane's first vector in the row
 
-    // this workgroup's rows [pb, pe)
-    const int pb = ps * (P / a.psplit), pe = pb + P / a.psplit;
-    for (int pbase = pb + row0; pbase < pe; pbase += kRows * kStepRowsPerLane) {
-        vec hv[kStepRowsPerLane][NV], pv[kStepRowsPerLane][NV];
-        T xv[kStepRowsPerLane];
-        // Streaming reads of the incoming state (the outgoing state is stored normally so
-        // the next step finds it in the caches). All loads are unconditional and issued
-        // before the arithmetic: rows past the block's end read its last row and lanes past
-        // the row end read the row's last vector (their B / C columns are zero); neither
-        // stores anything.
+    for (int pbase = pb + row0; pbase < pe; pbase += kRows * RPL) {
+        if (!kEarly || pbase != pb + row0) load_rows(pbase);
 #pragma unroll
-        for (int it = 0; it < kStepRowsPerLane; ++it) {
-            const int p = pbase + it * kRows < pe ? pbase + it * kRows : pe - 1;
-#pragma unroll
-            for (int v = 0; v < NV; ++v) {
-                const int vi = v0 + v < nvr ? v0 + v : nvr - 1;
-                hv[it][v] = __builtin_nontemporal_load(&hin[p * nvr + vi]);
-                pv[it][v] = __builtin_nontemporal_load(&pin[p * nvr + vi]);
-            }
-            xv[it] = pr[a.pl.x + (int64_t)h * P + p];
-        }
-#pragma unroll
-        for (int it = 0; it < kStepRowsPerLane; ++it) {
+        for (int it = 0; it < RPL; ++it) {
             const int p = pbase + it * kRows;
             if (p < pe) {
                 float xr[RM];
@@ -306,54 +313,63 @@ static void step_layout(int N, int& vw, int& nv, int& lpr) {
 
 // Reachable layouts: one vector per lane for any power-of-two lane count (N <= 64 VW);
 // several vectors per lane only with all 64 lanes (N > 256, or N > 128 with VW = 2).
-template <typename T, int RM, bool kX, int VW, bool kF>
+template <typename T, int RM, bool kX, int VW, bool kF, int RPL>
 static void launch_step_l(int lpr, dim3 grid, hipStream_t stream, const StepArgs& a) {
     switch (lpr) {
-        case 1: hipLaunchKernelGGL((step_kernel<T, RM, kX, 1, VW, 1, kF>), grid, dim3(kStepThreads), 0, stream, a); break;
-        case 2: hipLaunchKernelGGL((step_kernel<T, RM, kX, 2, VW, 1, kF>), grid, dim3(kStepThreads), 0, stream, a); break;
-        case 4: hipLaunchKernelGGL((step_kernel<T, RM, kX, 4, VW, 1, kF>), grid, dim3(kStepThreads), 0, stream, a); break;
-        case 8: hipLaunchKernelGGL((step_kernel<T, RM, kX, 8, VW, 1, kF>), grid, dim3(kStepThreads), 0, stream, a); break;
-        case 16: hipLaunchKernelGGL((step_kernel<T, RM, kX, 16, VW, 1, kF>), grid, dim3(kStepThreads), 0, stream, a); break;
-        case 32: hipLaunchKernelGGL((step_kernel<T, RM, kX, 32, VW, 1, kF>), grid, dim3(kStepThreads), 0, stream, a); break;
-        default: hipLaunchKernelGGL((step_kernel<T, RM, kX, 64, VW, 1, kF>), grid, dim3(kStepThreads), 0, stream, a); break;
+        case 1: hipLaunchKernelGGL((step_kernel<T, RM, kX, 1, VW, 1, kF, RPL>), grid, dim3(kStepThreads), 0, stream, a); break;
+        case 2: hipLaunchKernelGGL((step_kernel<T, RM, kX, 2, VW, 1, kF, RPL>), grid, dim3(kStepThreads), 0, stream, a); break;
+        case 4: hipLaunchKernelGGL((step_kernel<T, RM, kX, 4, VW, 1, kF, RPL>), grid, dim3(kStepThreads), 0, stream, a); break;
+        case 8: hipLaunchKernelGGL((step_kernel<T, RM, kX, 8, VW, 1, kF, RPL>), grid, dim3(kStepThreads), 0, stream, a); break;
+        case 16: hipLaunchKernelGGL((step_kernel<T, RM, kX, 16, VW, 1, kF, RPL>), grid, dim3(kStepThreads), 0, stream, a); break;
+        case 32: hipLaunchKernelGGL((step_kernel<T, RM, kX, 32, VW, 1, kF, RPL>), grid, dim3(kStepThreads), 0, stream, a); break;
+        default: hipLaunchKernelGGL((step_kernel<T, RM, kX, 64, VW, 1, kF, RPL>), grid, dim3(kStepThreads), 0, stream, a); break;
     }
 }
 
 template <typename T, int RM, bool kX>
 static void launch_step_v(int vw, int nv, int lpr, dim3 grid, hipStream_t stream, const StepArgs& a) {
+    constexpr int R8 = kStepRowsPerLane;
     if (nv == 1) {
-        if (vw == 4) launch_step_l<T, RM, kX, 4, false>(lpr, grid, stream, a);
-        else launch_step_l<T, RM, kX, 2, false>(lpr, grid, stream, a);
+        if (vw == 4) launch_step_l<T, RM, kX, 4, false, R8>(lpr, grid, stream, a);
+        else launch_step_l<T, RM, kX, 2, false, R8>(lpr, grid, stream, a);
     } else if (vw == 4) {
-        hipLaunchKernelGGL((step_kernel<T, RM, kX, 64, 4, 2, false>), grid, dim3(kStepThreads), 0, stream, a);
+        hipLaunchKernelGGL((step_kernel<T, RM, kX, 64, 4, 2, false, R8>), grid, dim3(kStepThreads), 0, stream, a);
     } else if (nv == 2) {
-        hipLaunchKernelGGL((step_kernel<T, RM, kX, 64, 2, 2, false>), grid, dim3(kStepThreads), 0, stream, a);
+        hipLaunchKernelGGL((step_kernel<T, RM, kX, 64, 2, 2, false, R8>), grid, dim3(kStepThreads), 0, stream, a);
     } else {
-        hipLaunchKernelGGL((step_kernel<T, RM, kX, 64, 2, 4, false>), grid, dim3(kStepThreads), 0, stream, a);
+        hipLaunchKernelGGL((step_kernel<T, RM, kX, 64, 2, 4, false, R8>), grid, dim3(kStepThreads), 0, stream, a);
     }
 }
 
-// Full layouts (4-column vectors, every lane inside the row, exact rank).
+// Full layouts (4-column vectors, every lane inside the row, exact rank). one_row: each
+// workgroup's P / psplit rows are at most one per lane (small batches).
 template <typename T, int RM>
-static void launch_step_full(int nv, int lpr, dim3 grid, hipStream_t stream, const StepArgs& a) {
-    if (nv == 2) hipLaunchKernelGGL((step_kernel<T, RM, true, 64, 4, 2, true>), grid, dim3(kStepThreads), 0, stream, a);
-    else launch_step_l<T, RM, true, 4, true>(lpr, grid, stream, a);
+static void launch_step_full(int nv, int lpr, bool one_row, dim3 grid, hipStream_t stream, const StepArgs& a) {
+    constexpr int R8 = kStepRowsPerLane;
+    if (nv == 2) {
+        if (one_row) hipLaunchKernelGGL((step_kernel<T, RM, true, 64, 4, 2, true, 1>), grid, dim3(kStepThreads), 0, stream, a);
+        else hipLaunchKernelGGL((step_kernel<T, RM, true, 64, 4, 2, true, R8>), grid, dim3(kStepThreads), 0, stream, a);
+    } else if (one_row) {
+        launch_step_l<T, RM, true, 4, true, 1>(lpr, grid, stream, a);
+    } else {
+        launch_step_l<T, RM, true, 4, true, R8>(lpr, grid, stream, a);
+    }
 }
 
 // Ranks 1, 2 and 4 are compile-time constants; the others run under RM = 8 with the rank
 // as a run-time bound.
 template <typename T>
-static void launch_step_t(int N, int R, int vw, int nv, int lpr, dim3 grid, hipStream_t stream,
+static void launch_step_t(int N, int R, int vw, int nv, int lpr, bool one_row, dim3 grid, hipStream_t stream,
                           const StepArgs& a) {
     const bool full = vw == 4 && N == lpr * vw * nv;
     if (R == 1) {
-        if (full) launch_step_full<T, 1>(nv, lpr, grid, stream, a);
+        if (full) launch_step_full<T, 1>(nv, lpr, one_row, grid, stream, a);
         else launch_step_v<T, 1, true>(vw, nv, lpr, grid, stream, a);
     } else if (R == 2) {
-        if (full) launch_step_full<T, 2>(nv, lpr, grid, stream, a);
+        if (full) launch_step_full<T, 2>(nv, lpr, one_row, grid, stream, a);
         else launch_step_v<T, 2, true>(vw, nv, lpr, grid, stream, a);
     } else if (R == 4) {
-        if (full) launch_step_full<T, 4>(nv, lpr, grid, stream, a);
+        if (full) launch_step_full<T, 4>(nv, lpr, one_row, grid, stream, a);
         else launch_step_v<T, 4, true>(vw, nv, lpr, grid, stream, a);
     } else {
         launch_step_v<T, 8, false>(vw, nv, lpr, grid, stream, a);
@@ -382,8 +398,9 @@ int launch_step(const m3_layer_desc& d, const m3_layer_params& p, const void* pr
     while (a.psplit < 8 && (int64_t)d.batch * d.nheads * a.psplit < 1024 && d.headdim % (2 * a.psplit) == 0)
         a.psplit *= 2;
     const dim3 grid((unsigned)(d.batch * d.nheads * a.psplit));
-    if (d.dtype == M3_DTYPE_BF16) launch_step_t<bf16>(d.d_state, d.mimo_rank, vw, nv, lpr, grid, stream, a);
-    else launch_step_t<float>(d.d_state, d.mimo_rank, vw, nv, lpr, grid, stream, a);
+    const bool one_row = d.headdim / a.psplit <= kStepThreads / lpr;
+    if (d.dtype == M3_DTYPE_BF16) launch_step_t<bf16>(d.d_state, d.mimo_rank, vw, nv, lpr, one_row, grid, stream, a);
+    else launch_step_t<float>(d.d_state, d.mimo_rank, vw, nv, lpr, one_row, grid, stream, a);
     return hipGetLastError() == hipSuccess ? M3_OK : M3_ERR_LAUNCH;
 }
 
