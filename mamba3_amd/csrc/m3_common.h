@@ -1,5 +1,6 @@
 // Device-side helpers shared by the Mamba-3 kernels (gfx950, wave64).
 #pragma once
+#include <type_traits>
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -30,6 +31,23 @@ template <int width>
 __device__ __forceinline__ float group_sum(float v) {
 #pragma unroll
     for (int off = width / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+// The same sum with DPP lane moves inside a row of 16 lanes (swap neighbours, swap pairs,
+// mirror within the half-row, mirror within the row; every source lane is valid) and lane
+// shuffles across rows: after each step every lane holds the sum of its aligned group.
+template <int width>
+__device__ __forceinline__ float lane_sum(float v) {
+    auto dpp = [](float x, auto ctrl) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), decltype(ctrl)::value, 0xF, 0xF, false));
+    };
+    if constexpr (width >= 2) v += dpp(v, std::integral_constant<int, 0xB1>{});
+    if constexpr (width >= 4) v += dpp(v, std::integral_constant<int, 0x4E>{});
+    if constexpr (width >= 8) v += dpp(v, std::integral_constant<int, 0x141>{});
+    if constexpr (width >= 16) v += dpp(v, std::integral_constant<int, 0x140>{});
+    if constexpr (width >= 32) v += __shfl_xor(v, 16, kWave);
+    if constexpr (width >= 64) v += __shfl_xor(v, 32, kWave);
     return v;
 }
 

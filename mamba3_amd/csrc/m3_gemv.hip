@@ -110,8 +110,21 @@ __global__ __launch_bounds__(kGvThreads) void gemv_small(GemvArgs a) {
     // Stage the activations (rows past M and the trailing piece are zero) and the norm weight.
     // Buffer reads past the M rows (and past the weight) return zero, so every read of a
     // pass is issued unconditionally, before the pass's stores: one round trip per pass.
+    // With the norm, each thread also sums the squares of its pieces per row (fp32) while
+    // they are in registers.
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, (int64_t)M * K * 2);
     const int nstage = MM * kv + 1;
+    // the norm weight's first pass is read ahead of the activations
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.nw, kNorm ? (int64_t)K * 2 : 0);
+    gv_u32x4 wv0[kGvStage];
+    if constexpr (kNorm) {
+#pragma unroll
+        for (int u = 0; u < kGvStage; ++u)
+            wv0[u] = __builtin_amdgcn_raw_buffer_load_b128(rw, (u * kGvThreads + tid) * 16, 0, 0);
+    }
+    float ss[MM];
+#pragma unroll
+    for (int m = 0; m < MM; ++m) ss[m] = 0.f;
     for (int i0 = 0; i0 < nstage; i0 += kGvThreads * kGvStage) {
         gv_u32x4 v[kGvStage];
 #pragma unroll
@@ -121,41 +134,40 @@ __global__ __launch_bounds__(kGvThreads) void gemv_small(GemvArgs a) {
         for (int u = 0; u < kGvStage; ++u) {
             const int i = i0 + u * kGvThreads + tid;
             if (i < nstage) *reinterpret_cast<gv_u32x4*>(sx + (int64_t)i * 8) = v[u];
+            if constexpr (kNorm) {
+                // pieces past the M rows read zero and add nothing
+                const gv_bf16x8 xv = __builtin_bit_cast(gv_bf16x8, v[u]);
+                float q = 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) q += (float)xv[e] * (float)xv[e];
+                const int m = i / kv;
+#pragma unroll
+                for (int mm = 0; mm < MM; ++mm) ss[mm] += m == mm ? q : 0.f;
+            }
         }
     }
     bf16* snw = sx + (MM * kv + 1) * 8;
     if constexpr (kNorm) {
-        const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.nw, (int64_t)K * 2);
         for (int i0 = 0; i0 < kv; i0 += kGvThreads * kGvStage) {
             gv_u32x4 v[kGvStage];
 #pragma unroll
             for (int u = 0; u < kGvStage; ++u)
-                v[u] = __builtin_amdgcn_raw_buffer_load_b128(rw, (i0 + u * kGvThreads + tid) * 16, 0, 0);
+                v[u] = i0 == 0 ? wv0[u] : __builtin_amdgcn_raw_buffer_load_b128(rw, (i0 + u * kGvThreads + tid) * 16, 0, 0);
 #pragma unroll
             for (int u = 0; u < kGvStage; ++u) {
                 const int i = i0 + u * kGvThreads + tid;
                 if (i < kv) *reinterpret_cast<gv_u32x4*>(snw + i * 8) = v[u];
             }
         }
+    } else {
+        __syncthreads();
     }
-    __syncthreads();
     if constexpr (kNorm) {
-        // fp32 sum of squares per row: 16-byte pieces per thread, a wave butterfly, the two
-        // waves' partials; then x * s and the weight, rounded as the reference's RMSNorm
-        float ss[MM];
-#pragma unroll
-        for (int m = 0; m < MM; ++m) ss[m] = 0.f;
-        for (int c = tid; c < kv; c += kGvThreads) {
-#pragma unroll
-            for (int m = 0; m < MM; ++m) {
-                const gv_bf16x8 xv = *reinterpret_cast<const gv_bf16x8*>(sx + m * K + c * 8);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) ss[m] += (float)xv[e] * (float)xv[e];
-            }
-        }
+        // fp32 sum of squares per row: the threads' partials, a wave sum, the two waves'
+        // partials; then x * s and the weight, rounded as the reference's RMSNorm
 #pragma unroll
         for (int m = 0; m < MM; ++m) {
-            const float t = group_sum<64>(ss[m]);
+            const float t = sum_lanes<64>(ss[m]);
             if ((tid & 63) == 0) sss[tid >> 6][m] = t;
         }
         __syncthreads();

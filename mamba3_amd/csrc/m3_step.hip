@@ -199,8 +199,8 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(StepArgs a) {
             ssb += Bv[j][r] * Bv[j][r];
             ssc += Cv[j][r] * Cv[j][r];
         }
-    ssb = group_sum<LPR>(ssb);
-    ssc = group_sum<LPR>(ssc);
+    ssb = lane_sum<LPR>(ssb);
+    ssc = lane_sum<LPR>(ssc);
     const float rb = rsqrtf(ssb / NR + a.eps), rc = rsqrtf(ssc / NR + a.eps);
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
@@ -280,7 +280,7 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(StepArgs a) {
                 }
                 float yr[RM];
 #pragma unroll
-                for (int r = 0; r < RM; ++r) yr[r] = group_sum<LPR>(yacc[r]);
+                for (int r = 0; r < RM; ++r) yr[r] = lane_sum<LPR>(yacc[r]);
                 if (q == 0) {
                     const float z = ld_f32(pr + a.pl.z + (int64_t)h * P + p);
                     float out = 0.f;
