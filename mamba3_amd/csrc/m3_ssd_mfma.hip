@@ -421,42 +421,78 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
     const bool pair_lane = wv >= NMW && hw < 4 && q8 == 0;
     float phi_start0 = 0.f, phi_start1 = 0.f;
     if (kFull && seg > 0) {
-        // H = sum_i exp(sum_{l=i+1}^{seg-1} D_l) R(-sum_{l=i}^{seg-1} Phi_l) S_i
+        // H = sum_i exp(sum_{l=i+1}^{seg-1} D_l) R(-sum_{l=i}^{seg-1} Phi_l) S_i over the
+        // preceding segments i < seg. The suffix sums (per-pair angles, log-weights) are
+        // taken in the order of a walk from seg-1 down, from reads issued eight at a time,
+        // into the C~ tile (unused until the first tiles are written); the MFMA waves then
+        // read the segment states two at a time. Index clamps and zero weights keep every
+        // read unconditional.
         const int g16 = lane0 >> 4, l16 = lane0 & 15;
         const int64_t sbase = (int64_t)bh * (a.S - 1);
-        float dsum = 0.f;
-        for (int i = seg - 1; i >= 0; --i) {
-            __syncthreads();
-            if (tid < NH) {
-                const float acc = (i == seg - 1) ? 0.f : sm.rot[tid];
-                sm.rot[tid] = acc + a.seg_angle[(sbase + i) * NH + tid];
-            }
-            __syncthreads();
-            if (wv < NMW) {
-                const float wgt = __expf(dsum);
-                const float* Si = a.seg_state + (sbase + i) * (int64_t)N * P;
-                const int n0 = 16 * wv + 4 * g16;
-                float s0, c0, s1, c1;
-                sincosf(-sm.rot[n0 / 2], &s0, &c0);
-                sincosf(-sm.rot[n0 / 2 + 1], &s1, &c1);
+        float* rotA = reinterpret_cast<float*>(&sm.C[0][0]);  // [i][pair], i < seg <= 63
+        float* lw = rotA + 64 * NH;                          // [i]
+        if (tid < NH) {
+            float acc = 0.f;
+            for (int i0 = seg - 1; i0 >= 0; i0 -= 8) {
+                float v[8];
 #pragma unroll
-                for (int pt = 0; pt < 4; ++pt) {
-                    const int p = 16 * pt + l16;
-                    const float e0 = Si[(n0 + 0) * P + p], o0 = Si[(n0 + 1) * P + p];
-                    const float e1 = Si[(n0 + 2) * P + p], o1 = Si[(n0 + 3) * P + p];
-                    hacc[pt][0] += wgt * (e0 * c0 - o0 * s0);
-                    hacc[pt][1] += wgt * (e0 * s0 + o0 * c0);
-                    hacc[pt][2] += wgt * (e1 * c1 - o1 * s1);
-                    hacc[pt][3] += wgt * (e1 * s1 + o1 * c1);
+                for (int u = 0; u < 8; ++u) v[u] = a.seg_angle[(sbase + max(i0 - u, 0)) * NH + tid];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    acc += i0 - u >= 0 ? v[u] : 0.f;
+                    if (i0 - u >= 0) rotA[(i0 - u) * NH + tid] = acc;
                 }
             }
-            dsum += a.seg_decay[sbase + i];
+        } else if (tid == 64) {
+            float acc = 0.f;
+            for (int i0 = seg - 1; i0 >= 0; i0 -= 8) {
+                float v[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) v[u] = a.seg_decay[sbase + max(i0 - u, 0)];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    if (i0 - u >= 0) lw[i0 - u] = acc;
+                    acc += i0 - u >= 0 ? v[u] : 0.f;
+                }
+            }
         }
         __syncthreads();
-        if (pair_lane) {
-            phi_start0 = sm.rot[pa0];  // sum_{l<seg} Phi_l
-            phi_start1 = sm.rot[pa0 + 1];
+        if (wv < NMW) {
+            const int n0 = 16 * wv + 4 * g16;
+            for (int i0 = seg - 1; i0 >= 0; i0 -= 2) {
+                float sv[2][4][4];  // [segment][pt][n0 + e]
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const float* Si = a.seg_state + (sbase + max(i0 - u, 0)) * (int64_t)N * P;
+#pragma unroll
+                    for (int pt = 0; pt < 4; ++pt)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) sv[u][pt][e] = Si[(n0 + e) * P + 16 * pt + l16];
+                }
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const int i = max(i0 - u, 0);
+                    const float wgt = i0 - u >= 0 ? __expf(lw[i]) : 0.f;
+                    float s0, c0, s1, c1;
+                    sincosf(-rotA[i * NH + n0 / 2], &s0, &c0);
+                    sincosf(-rotA[i * NH + n0 / 2 + 1], &s1, &c1);
+#pragma unroll
+                    for (int pt = 0; pt < 4; ++pt) {
+                        const float e0 = sv[u][pt][0], o0 = sv[u][pt][1];
+                        const float e1 = sv[u][pt][2], o1 = sv[u][pt][3];
+                        hacc[pt][0] += wgt * (e0 * c0 - o0 * s0);
+                        hacc[pt][1] += wgt * (e0 * s0 + o0 * c0);
+                        hacc[pt][2] += wgt * (e1 * c1 - o1 * s1);
+                        hacc[pt][3] += wgt * (e1 * s1 + o1 * c1);
+                    }
+                }
+            }
         }
+        if (pair_lane) {
+            phi_start0 = rotA[pa0];  // sum_{l<seg} Phi_l
+            phi_start1 = rotA[pa0 + 1];
+        }
+        __syncthreads();  // the C~ tile is written after this
     }
 
     const bf16* proj_b = a.proj + (int64_t)b * T * a.rs;
