@@ -143,6 +143,8 @@ __device__ __forceinline__ int zsw(int t, int p) { return p ^ (16 * ((t >> 1) & 
 // 1. Normalised B^ / C^ per (token, group): x * rsqrt(mean(x^2) + eps) * w + bias,
 //    stored pair-packed: word 2i+r of the row = (value[n=2i][r], value[n=2i+1][r]).
 // ---------------------------------------------------------------------------------
+constexpr int kBcTok = 4;  // (token, group) rows per wave of bc_norm
+
 __global__ __launch_bounds__(256) void bc_norm(const bf16* __restrict__ proj, int64_t rs,
                                                int64_t offB, int64_t offC, int G,
                                                int64_t ntok_grp, float eps,
@@ -151,36 +153,54 @@ __global__ __launch_bounds__(256) void bc_norm(const bf16* __restrict__ proj, in
                                                const float* __restrict__ wC,
                                                const float* __restrict__ biasC,
                                                f16* __restrict__ Bn, f16* __restrict__ Cn) {
+    // A wave normalises kBcTok consecutive (token, group) rows: all their reads go out
+    // together, the weights and biases are read once (rows past the end read the last row
+    // and store nothing). Lane = pair i; raw order at 4i: (n=2i,r0) (2i,r1) (2i+1,r0) (2i+1,r1).
     const int lane = threadIdx.x & 63;
-    const int64_t tg = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (tg >= ntok_grp) return;
-    const int64_t tok = tg / G;
-    const int g = (int)(tg % G);
-    const bf16* row = proj + tok * rs;
-    // lane = pair i; raw order at 4i: (n=2i,r0) (2i,r1) (2i+1,r0) (2i+1,r1)
-    const bf16x4 vb = *reinterpret_cast<const bf16x4*>(row + offB + (int64_t)g * NR + 4 * lane);
-    const bf16x4 vc = *reinterpret_cast<const bf16x4*>(row + offC + (int64_t)g * NR + 4 * lane);
-    float b[4], c[4], sb = 0.f, sc = 0.f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        b[j] = (float)vb[j];
-        c[j] = (float)vc[j];
-        sb += b[j] * b[j];
-        sc += c[j] * c[j];
-    }
-    sb = group_sum<64>(sb);
-    sc = group_sum<64>(sc);
-    const float rb = rsqrtf(sb * (1.f / NR) + eps), rc = rsqrtf(sc * (1.f / NR) + eps);
+    const int64_t tg0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * kBcTok;
+    if (tg0 >= ntok_grp) return;
     const int e = 4 * lane;
-    float ob[4], oc[4];
+    bf16x4 vb[kBcTok], vc[kBcTok];
+    int gg[kBcTok];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        ob[j] = b[j] * rb * wB[e + j] + biasB[(int64_t)g * NR + e + j];
-        oc[j] = c[j] * rc * wC[e + j] + biasC[(int64_t)g * NR + e + j];
+    for (int k = 0; k < kBcTok; ++k) {
+        const int64_t tg = tg0 + k < ntok_grp ? tg0 + k : ntok_grp - 1;
+        const int64_t tok = tg / G;
+        gg[k] = (int)(tg % G);
+        const bf16* row = proj + tok * rs;
+        vb[k] = *reinterpret_cast<const bf16x4*>(row + offB + (int64_t)gg[k] * NR + e);
+        vc[k] = *reinterpret_cast<const bf16x4*>(row + offC + (int64_t)gg[k] * NR + e);
     }
-    // pair-packed: (e_r0, o_r0, e_r1, o_r1)
-    *reinterpret_cast<f16x4*>(Bn + tg * NR + e) = f16x4{(f16)ob[0], (f16)ob[2], (f16)ob[1], (f16)ob[3]};
-    *reinterpret_cast<f16x4*>(Cn + tg * NR + e) = f16x4{(f16)oc[0], (f16)oc[2], (f16)oc[1], (f16)oc[3]};
+    const f32x4 wb4 = *reinterpret_cast<const f32x4*>(wB + e);
+    const f32x4 wc4 = *reinterpret_cast<const f32x4*>(wC + e);
+#pragma unroll
+    for (int k = 0; k < kBcTok; ++k) {
+        const int64_t tg = tg0 + k;
+        const f32x4 bb4 = *reinterpret_cast<const f32x4*>(biasB + (int64_t)gg[k] * NR + e);
+        const f32x4 bc4 = *reinterpret_cast<const f32x4*>(biasC + (int64_t)gg[k] * NR + e);
+        float b[4], c[4], sb = 0.f, sc = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            b[j] = (float)vb[k][j];
+            c[j] = (float)vc[k][j];
+            sb += b[j] * b[j];
+            sc += c[j] * c[j];
+        }
+        sb = lane_sum<64>(sb);
+        sc = lane_sum<64>(sc);
+        const float rb = rsqrtf(sb * (1.f / NR) + eps), rc = rsqrtf(sc * (1.f / NR) + eps);
+        float ob[4], oc[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            ob[j] = b[j] * rb * wb4[j] + bb4[j];
+            oc[j] = c[j] * rc * wc4[j] + bc4[j];
+        }
+        // pair-packed: (e_r0, o_r0, e_r1, o_r1)
+        if (tg < ntok_grp) {
+            *reinterpret_cast<f16x4*>(Bn + tg * NR + e) = f16x4{(f16)ob[0], (f16)ob[2], (f16)ob[1], (f16)ob[3]};
+            *reinterpret_cast<f16x4*>(Cn + tg * NR + e) = f16x4{(f16)oc[0], (f16)oc[2], (f16)oc[1], (f16)oc[3]};
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------------
@@ -1056,7 +1076,8 @@ void launch_bc_norm(const m3_layer_desc& d, const m3_layer_params& p, const void
                     f16* bn, f16* cn, hipStream_t stream) {
     const ProjLayout pl = proj_layout(d);
     const int64_t ntg = (int64_t)d.batch * d.seqlen * d.ngroups;
-    hipLaunchKernelGGL(mf::bc_norm, dim3((unsigned)((ntg + 3) / 4)), dim3(256), 0, stream,
+    const int64_t rows_per_block = 4 * mf::kBcTok;
+    hipLaunchKernelGGL(mf::bc_norm, dim3((unsigned)((ntg + rows_per_block - 1) / rows_per_block)), dim3(256), 0, stream,
                        reinterpret_cast<const bf16*>(proj), d.proj_row_stride, pl.B, pl.C,
                        d.ngroups, ntg, d.rms_eps, p.B_norm_w, p.B_bias, p.C_norm_w, p.C_bias,
                        bn, cn);
