@@ -214,8 +214,8 @@ def bench_layer_fp32_d768(args, torch, mamba3_amd):
                        "unit": "TFLOP/s", "frac": round(tf / PEAK_FP32_TFLOPS, 4),
                        "traffic": traffic.get("layer_fp32"),
                        "traffic_source": traffic_source(ROOT / "profiles" / "kernel_trace_fp32_layer_d768.md"),
-                       "kernel": "native fp32 SSD core (all launches of m3_prefill_fwd: preparation, "
-                                 "fp32-MFMA chunk kernels, gate)",
+                       "kernel": "native fp32 SSD core (all launches of m3_prefill_fwd: bc_norm_f32 "
+                                 "and the fused fp32-MFMA kernel ssd_f32)",
                        "algorithmic_flops": flops, "avg_ms": round(core_ms, 4)}
     if not args.no_cpu_baseline:
         from oracle import reference_path as ref

@@ -71,6 +71,11 @@ typedef struct m3_layer_desc {
  * biases, or mimo_x, in a trained checkpoint) sets this flag: such layers then run on the
  * fp32 generic kernel, which has no such range limit. */
 #define M3_FLAG_NO_F16_OPERANDS 1
+/* fp32 layers: m3_prefill_fwd keeps the intermediates m3_layer_bwd differentiates through in
+ * its workspace (the staged fp32 layer path). Without it an fp32 layer with d_state 128,
+ * headdim 64, mimo_rank 2 runs the fused fp32 kernel, whose workspace holds only the
+ * normalised B^ / C^. */
+#define M3_FLAG_FOR_BACKWARD 2
 
 /* Small per-layer parameters, all fp32 device arrays. Names follow the reference's
  * parameters (mamba3/mamba3.py:95-111). */
@@ -146,7 +151,7 @@ int m3_scan_bwd(const float* decay, const float* h_states, const float* grad, fl
 /*
  * Backward of m3_prefill_fwd for fp32 layers (desc->dtype fp32, mimo_rank 1/2/4/8), from the
  * workspace of that forward call, which holds its intermediates (pass the same buffer, unchanged,
- * with its size). Replaces the reference's autograd through mamba3/mamba3.py:197-256 (ATen's
+ * with its size; that forward ran with M3_FLAG_FOR_BACKWARD in desc->flags, as does this call). Replaces the reference's autograd through mamba3/mamba3.py:197-256 (ATen's
  * backward of the dt softplus, the B/C RMSNorm + bias, the RoPE rotation and its angle cumsum,
  * the MIMO and trapezoid terms and the SiLU gate) and through chunked_ssd (see
  * m3_chunked_ssd_bwd). Inputs: g_out [B,T,H*P] = dL/d(gated output), and nullable g_h

@@ -72,6 +72,7 @@ class LayerDesc(ctypes.Structure):
 
 
 M3_FLAG_NO_F16_OPERANDS = 1
+M3_FLAG_FOR_BACKWARD = 2
 
 
 class LayerParams(ctypes.Structure):

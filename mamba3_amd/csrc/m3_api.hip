@@ -28,7 +28,7 @@ int check_desc(const m3_layer_desc* d) {
     if (d->use_complex != 0 && d->use_complex != 1) return M3_ERR_INVALID_SHAPE;
     if (d->proj_row_stride < proj_layout(*d).width) return M3_ERR_INVALID_SHAPE;
     if (!(d->rms_eps >= 0.f)) return M3_ERR_INVALID_SHAPE;
-    if (d->flags & ~M3_FLAG_NO_F16_OPERANDS) return M3_ERR_INVALID_SHAPE;
+    if (d->flags & ~(M3_FLAG_NO_F16_OPERANDS | M3_FLAG_FOR_BACKWARD)) return M3_ERR_INVALID_SHAPE;
     // Kernel limits: headdim <= 256, d_state <= 512, rank <= 8.
     if (d->headdim > 256 || d->d_state > 512 || d->mimo_rank > 8) return M3_ERR_UNSUPPORTED;
     return M3_OK;
@@ -52,15 +52,17 @@ int check_scan_bwd_shape(int64_t batch, int64_t nchunks, int64_t nheads, int64_t
 // Which prefill kernel a call dispatches to: the d_state 128 / headdim 64 / rank 2 MFMA
 // kernel (bf16, aligned rows, 16-byte aligned proj / y_out), the general MFMA kernel
 // (bf16, d_state 64/128/256, rank 1/2/4, headdim % 32 == 0, 16-byte aligned h_final) --
-// both with f16 operands, so not under M3_FLAG_NO_F16_OPERANDS -- the fp32 layer path on
-// the fp32-MFMA chunk kernels (fp32, rank 1/2/4/8) or the generic one.
-enum class PrefillPath { kMfma, kWide, kFp32, kGeneric };
+// both with f16 operands, so not under M3_FLAG_NO_F16_OPERANDS -- the fused fp32 kernel
+// (fp32, d_state 128 / headdim 64 / rank 2, not under M3_FLAG_FOR_BACKWARD), the fp32 layer
+// path on the fp32-MFMA chunk kernels (fp32, rank 1/2/4/8) or the generic one.
+enum class PrefillPath { kMfma, kWide, kFp32Fused, kFp32, kGeneric };
 
 PrefillPath prefill_path(const m3_layer_desc& d, const void* proj, const void* y_out,
-                         const void* h_final) {
+                         const void* h_final, const void* prev_bx) {
     const bool f16_ok = !(d.flags & M3_FLAG_NO_F16_OPERANDS);
     if (f16_ok && m3::mfma_prefill_supported(d, proj, y_out)) return PrefillPath::kMfma;
     if (f16_ok && m3::wide_prefill_supported(d) && aligned(h_final, 16)) return PrefillPath::kWide;
+    if (m3::fused_fp32_prefill_supported(d, proj, y_out, h_final, prev_bx)) return PrefillPath::kFp32Fused;
     if (m3::fp32_layer_supported(d)) return PrefillPath::kFp32;
     return PrefillPath::kGeneric;
 }
@@ -69,6 +71,7 @@ size_t prefill_path_workspace(const m3_layer_desc& d, PrefillPath path) {
     switch (path) {
         case PrefillPath::kMfma: return m3::mfma_prefill_workspace(d);
         case PrefillPath::kWide: return m3::wide_prefill_workspace(d);
+        case PrefillPath::kFp32Fused: return m3::fused_fp32_prefill_workspace(d);
         case PrefillPath::kFp32: return m3::fp32_layer_workspace(d);
         default: return m3::generic_prefill_workspace(d);
     }
@@ -94,6 +97,9 @@ int launch_prefill_path(PrefillPath path, const m3_layer_desc& d, const m3_layer
         case PrefillPath::kWide:
             return m3::launch_wide_prefill(d, p, proj, dt_scale, y_out, h_final, angle, prev_bx,
                                            ws, stream);
+        case PrefillPath::kFp32Fused:
+            return m3::launch_fused_fp32_prefill(d, p, proj, dt_scale, y_out, h_final, angle,
+                                                 prev_bx, ws, stream);
         case PrefillPath::kFp32:
             return m3::launch_fp32_layer(d, p, proj, dt_scale, y_out, h_final, angle, prev_bx,
                                          ws, stream) == 0
@@ -205,6 +211,8 @@ int m3_scan_bwd(const float* decay, const float* h_states, const float* grad, fl
 static size_t prefill_workspace(const m3_layer_desc& d) {
     size_t n = m3::generic_prefill_workspace(d);
     n = std::max(n, m3::fp32_layer_workspace(d));
+    if (m3::fused_fp32_prefill_supported(d, nullptr, nullptr, nullptr, nullptr))
+        n = std::max(n, m3::fused_fp32_prefill_workspace(d));
     if (m3::mfma_prefill_supported(d, nullptr, nullptr)) n = std::max(n, m3::mfma_prefill_workspace(d));
     if (m3::wide_prefill_supported(d)) n = std::max(n, m3::wide_prefill_workspace(d));
     return n;
@@ -223,7 +231,7 @@ int m3_prefill_fwd(const m3_layer_desc* desc, const m3_layer_params* params, con
                    float* prev_bx, void* workspace, size_t workspace_bytes, void* stream) {
     int st = check_prefill_args(desc, params, proj, y_out);
     if (st != M3_OK) return st;
-    const PrefillPath path = prefill_path(*desc, proj, y_out, h_final);
+    const PrefillPath path = prefill_path(*desc, proj, y_out, h_final, prev_bx);
     const size_t need = prefill_path_workspace(*desc, path);
     if (need > 0 && (!workspace || workspace_bytes < need)) return M3_ERR_WORKSPACE;
     if (workspace && !aligned(workspace, 256)) return M3_ERR_MISALIGNED;
@@ -236,7 +244,7 @@ int m3_prefill_fwd_noalloc(const m3_layer_desc* desc, const m3_layer_params* par
                            float* angle, float* prev_bx, void* stream) {
     int st = check_prefill_args(desc, params, proj, y_out);
     if (st != M3_OK) return st;
-    const PrefillPath path = prefill_path(*desc, proj, y_out, h_final);
+    const PrefillPath path = prefill_path(*desc, proj, y_out, h_final, prev_bx);
     const size_t need = prefill_path_workspace(*desc, path);
     if (need > M3_NOALLOC_SCRATCH_BYTES) return M3_ERR_SCRATCH_LIMIT;
     void* ws = nullptr;

@@ -98,6 +98,14 @@ struct Fp32LayerParts {
 };
 Fp32LayerParts fp32_layer_parts(const m3_layer_desc& d, void* workspace);
 bool fp32_layer_supported(const m3_layer_desc& d);
+// Fused fp32 prefill (m3_ssd_f32.hip): d_state 128, headdim 64, rank 2, without
+// M3_FLAG_FOR_BACKWARD; 16-byte aligned rows of proj and y_out, h_final and prev_bx.
+bool fused_fp32_prefill_supported(const m3_layer_desc& d, const void* proj, const void* y_out,
+                                  const void* h_final, const void* prev_bx);
+size_t fused_fp32_prefill_workspace(const m3_layer_desc& d);
+int launch_fused_fp32_prefill(const m3_layer_desc& d, const m3_layer_params& p, const void* proj,
+                              const float* dt_scale, void* y_out, float* h_final, float* angle,
+                              float* prev_bx, void* workspace, hipStream_t stream);
 size_t fp32_layer_workspace(const m3_layer_desc& d);
 int launch_fp32_layer(const m3_layer_desc& d, const m3_layer_params& p, const void* proj,
                       const float* dt_scale, void* y_out, float* h_final, float* angle,

@@ -146,9 +146,13 @@ def _(proj, A_log, D, dt_bias, B_norm_w, C_norm_w, B_bias, C_bias, mimo_x, mimo_
 
 # ------------------------------------------------------------ prefill for training
 def _train_desc(proj, nheads, headdim, d_state, mimo_rank, ngroups, trap, cplx, eps):
+    """fp32 descriptor of the training forward and of m3_layer_bwd: the forward keeps the
+    intermediates the backward reads (M3_FLAG_FOR_BACKWARD)."""
     Bat, T, W = proj.shape
-    return _desc(Bat, T, nheads, headdim, d_state, mimo_rank, ngroups, trap, cplx, eps,
+    desc = _desc(Bat, T, nheads, headdim, d_state, mimo_rank, ngroups, trap, cplx, eps,
                  torch.float32, W)
+    desc.flags |= _native.M3_FLAG_FOR_BACKWARD
+    return desc
 
 
 @torch.library.custom_op(f"{NS}::prefill_train", mutates_args=())

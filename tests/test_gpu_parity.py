@@ -607,6 +607,42 @@ def test_fp32_step_matches_oracle_from_random_state(cuda_device):
         assert max_rel(st2[k], st_ref[k]) < FP32_TOL, k
 
 
+# ------------------------------------------------------------------ fused fp32 prefill
+# fp32 layers with d_state 128 / headdim 64 / rank 2 run on the fused fp32 kernel
+# (m3_ssd_f32.hip, 32-token chunks) when the forward keeps no intermediates for
+# m3_layer_bwd; under autograd the staged fp32 layer path runs instead. Lengths of one token,
+# one chunk plus one and ending mid-chunk, the layer variants and dt_scale: the fused path
+# against the fp64 oracle at 1e-4, and the training forward against the fused one.
+F32_FUSED_CASES = [
+    (dict(), 1, False), (dict(), 33, False), (dict(), 300, True),
+    (dict(use_trapezoidal=False), 100, False), (dict(use_complex_ssm=False), 100, False),
+    (dict(ngroups=2), 77, True),
+]
+
+
+@pytest.mark.parametrize("extra,T,scaled", F32_FUSED_CASES)
+def test_fp32_fused_prefill_matches_oracle(extra, T, scaled, cuda_device):
+    kw = dict(d_model=768, d_state=128, headdim=64, mimo_rank=2, **extra)
+    print(f"fused fp32 prefill {extra} T={T} dt_scale={scaled}", flush=True)
+    torch.manual_seed(5)
+    layer = mamba3_amd.KulaMamba(**kw).to(cuda_device).eval()
+    p = {k: v.detach().double().cpu() for k, v in layer.state_dict().items()}
+    g = torch.Generator().manual_seed(T)
+    x = torch.randn(2, T, 768, generator=g)
+    ds = torch.rand(2, T, layer.nheads, generator=g) + 0.5 if scaled else None
+    dsd = ds.to(cuda_device) if scaled else None
+    with torch.no_grad():
+        y, st = layer.prefill(x.to(cuda_device), dt_scale=dsd)
+    y_ref, st_ref = ref.layer_forward(oracle_cfg(kw), p, x.double(),
+                                      dt_scale=ds.double() if scaled else None, return_state=True)
+    assert max_rel(y, y_ref) < FP32_TOL
+    for k in ("h", "prev_BX", "angle"):
+        assert max_rel(st[k], st_ref[k]) < FP32_TOL, k
+    xg = x.to(cuda_device).requires_grad_()
+    y_train = layer(xg, dt_scale=dsd)
+    assert max_rel(y_train.detach(), y) < FP32_TOL
+
+
 # ------------------------------------------------------------------ general MFMA prefill kernel
 # bf16 layers with d_state 64/128/256, rank 1/2/4 and headdim % 32 == 0 (other than
 # d_state 128 / headdim 64 / rank 2) run on the general MFMA kernel: one case per
