@@ -11,15 +11,17 @@
 // Two launches:
 //   1. bc_norm_f32: per (token, group), B^ = RMSNorm(B) * w + bias and C^ likewise, fp32, in
 //      the reference's (n, r) order (mamba3/mamba3.py:19-35, 147-157).
-//   2. ssd_f32: one 512-thread workgroup (8 waves) per (batch, head) walks the sequence in
-//      chunks of Q = 32 tokens (rows (t, r) = 2t + r, 64 rows), carrying the fp32 state
-//      H^T [n][p] in MFMA accumulators (wave w owns rows n = 16w .. 16w+15). Per chunk:
+//   2. ssd_f32<PB>: one 512-thread workgroup (8 waves) per (batch, head, block of PB of the 64
+//      headdim columns) walks the sequence in chunks of Q = 32 tokens (rows (t, r) = 2t + r,
+//      64 rows), carrying its columns of the fp32 state H^T [n][p] in MFMA accumulators (wave
+//      w owns rows n = 16w .. 16w+15). PB = 32 when the (batch, head) pairs alone leave CUs
+//      idle: two workgroups per pair then repeat the scores and the rotation. Per chunk:
 //        prep   token scalars; X rows x_u mimo_x[r] and z into LDS; the state copy H;
 //               the RoPE angles (a prefix over 8 groups of 4 tokens per pair) and the
 //               rotated C~ / B~ tiles (mamba3/mamba3.py:38-45, 160-166)
 //        G1     S = (C~ B~^T) * Lc on the 10 causal 16 x 16 blocks, into LDS, with
 //               Lc[t][u] = [u<=t] exp(c_t - c_u) (a_u + [u<t] b_u) and D on the diagonal
-//        G3+G2  Y = diag(e^{c_t}) C~ H^T + S X (waves: 16-row block w/2, 32 columns)
+//        G3+G2  Y = diag(e^{c_t}) C~ H^T + S X (waves: 16-row block w/2, PB/2 columns)
 //        G4     H^T = e^{c_end} H^T + (B~ diag(w))^T X, w_u = e^{c_end - c_u} (a_u + b_u)
 //        gate   out = sum_r mimo_down_r silu(z mimo_z_r) y_r (mamba3/mamba3.py:233-239)
 //      The angles stay absolute (the walk starts at t = 0), so the final state, angle and
@@ -42,19 +44,18 @@ constexpr int NH = N / 2;
 constexpr int ROWS = Q * R;
 constexpr int THREADS = 512;
 constexpr int CST = N + 1;
-constexpr int XST = P + 1;
 constexpr int SST = ROWS + 1;
-constexpr int HST = P + 1;
 
+template <int PB>
 struct Smem {
-    float C[ROWS][CST];    // C~ rows (t, r)
-    float B[ROWS][CST];    // B~ rows (u, r)
-    float X[ROWS][XST];    // x_u mimo_x[p, r], rows (u, r)
-    float S[ROWS][SST];    // masked scores, rows (t, r), columns (u, r')
-    float H[N][HST];       // state H^T at the chunk start
-    float Z[Q][P];         // z
-    float part[8][NH];     // per 4-token group: sum of dt theta, per pair
-    float phi_run[2][NH];  // pair angles at the end of the previous chunk (by chunk parity)
+    float C[ROWS][CST];      // C~ rows (t, r)
+    float B[ROWS][CST];      // B~ rows (u, r)
+    float X[ROWS][PB + 1];   // x_u mimo_x[p, r], rows (u, r), this block's columns
+    float S[ROWS][SST];      // masked scores, rows (t, r), columns (u, r')
+    float H[N][PB + 1];      // state H^T at the chunk start, this block's columns
+    float Z[Q][PB];          // z
+    float part[8][NH];       // per 4-token group: sum of dt theta, per pair
+    float phi_run[2][NH];    // pair angles at the end of the previous chunk (by chunk parity)
     float dtv[Q + 1], lamv[Q + 1];  // dt and lambda of the chunk's tokens and the next one
     float c[Q], ec[Q], av[Q], bv[Q], w[Q];
 };
@@ -124,8 +125,13 @@ __global__ __launch_bounds__(256) void bc_norm_f32(const float* __restrict__ pro
     *reinterpret_cast<f32x4*>(Cn + tg * NR + e) = oc;
 }
 
+template <int PB>
 __global__ __launch_bounds__(THREADS, 1) void ssd_f32(Args a) {
-    __shared__ Smem sm;
+    constexpr int NPT = PB / 16;          // column tiles of the block
+    constexpr int TPW = NPT / 2;          // output tiles per wave (row block wave / 2)
+    constexpr int XE = PB * Q / THREADS;  // X / Z elements per thread
+    constexpr int NPE = PB * N / THREADS; // prev_BX elements per thread
+    __shared__ Smem<PB> sm;
     const int tid = threadIdx.x;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63;
@@ -133,7 +139,9 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_f32(Args a) {
 
     // XCD-aware order: consecutive workgroups of one batch row land on one XCD.
     const int nblk = gridDim.x;
-    const int bh = (nblk % 8 == 0) ? (blockIdx.x % 8) * (nblk / 8) + blockIdx.x / 8 : blockIdx.x;
+    const int blk = (nblk % 8 == 0) ? (blockIdx.x % 8) * (nblk / 8) + blockIdx.x / 8 : blockIdx.x;
+    const int bh = blk / (P / PB);
+    const int pc = (blk % (P / PB)) * PB;  // first headdim column of the block
     const int b = bh / a.H, h = bh % a.H;
     const int grp = h / (a.H / a.G);
     const int T = a.T;
@@ -145,74 +153,61 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_f32(Args a) {
     const float dtb = a.prm.dt_bias[h];
     const float* prow = a.proj + (int64_t)b * T * a.rs;
 
-    // prep roles: X / Z element block (token xu, columns xp .. xp+3), and the rotation job
-    // (tokens 4 wv .. 4 wv + 3 of pair lane)
-    const int xu = tid >> 4, xp = 4 * (tid & 15);
-    float mx0[4], mx1[4];
+    // prep roles: X / Z element block (token xu, block columns xp .. xp + XE - 1), and the
+    // rotation job (tokens 4 wv .. 4 wv + 3 of pair lane)
+    const int xu = tid >> 4, xp = XE * (tid & 15);
+    float mx0[XE], mx1[XE];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        mx0[j] = a.prm.mimo_x[(h * P + xp + j) * R];
-        mx1[j] = a.prm.mimo_x[(h * P + xp + j) * R + 1];
+    for (int j = 0; j < XE; ++j) {
+        mx0[j] = a.prm.mimo_x[(h * P + pc + xp + j) * R];
+        mx1[j] = a.prm.mimo_x[(h * P + pc + xp + j) * R + 1];
     }
-    // output roles: row block I, columns 16 pt of the two tiles
+    // output roles: row block I, block column tiles ptb .. ptb + TPW - 1
     const int I = wv >> 1;
-    const int ptb = 2 * (wv & 1);
-    float mz[2][2], md[2][2];
+    const int ptb = TPW * (wv & 1);
+    float mz[TPW][2], md[TPW][2];
 #pragma unroll
-    for (int q = 0; q < 2; ++q)
+    for (int q = 0; q < TPW; ++q)
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const int p = 16 * (ptb + q) + l16;
+            const int p = pc + 16 * (ptb + q) + l16;
             mz[q][r] = a.prm.mimo_z[(h * P + p) * R + r];
             md[q][r] = a.prm.mimo_down[(h * P + p) * R + r];
         }
     if (tid < NH) sm.phi_run[0][tid] = 0.f;
 
-    f32x4 hacc[4];
+    f32x4 hacc[NPT];
 #pragma unroll
-    for (int pt = 0; pt < 4; ++pt) hacc[pt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int pt = 0; pt < NPT; ++pt) hacc[pt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    for (int k = 0; k < K; ++k) {
-        const int s0 = k * Q;
-        const int par = k & 1;
-        __syncthreads();  // the previous chunk's tiles are consumed
-        // ---- prep 1: token scalars, X / Z rows, state copy, raw B^ / C^ and theta
-        if (tid <= Q) {
-            const int tok = s0 + tid;
-            float dt = 0.f, lam = 1.f;
-            if (tok < T) {
-                const float* pr = prow + (int64_t)tok * a.rs;
-                dt = softplus_f(pr[a.pl.dt + h] + dtb);
-                if (a.dt_scale) dt *= a.dt_scale[((int64_t)b * T + tok) * a.H + h];
-                if (a.trap) lam = sigmoid_f(pr[a.pl.lam + h]);
-            }
-            sm.dtv[tid] = dt;
-            sm.lamv[tid] = lam;
-        }
-        {
-            const int tok = s0 + xu;
-            f32x4 xv = {0.f, 0.f, 0.f, 0.f}, zv = {0.f, 0.f, 0.f, 0.f};
-            if (tok < T) {
-                const float* pr = prow + (int64_t)tok * a.rs + h * P + xp;
-                xv = *reinterpret_cast<const f32x4*>(pr + a.pl.x);
-                zv = *reinterpret_cast<const f32x4*>(pr + a.pl.z);
-            }
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                sm.X[2 * xu][xp + j] = xv[j] * mx0[j];
-                sm.X[2 * xu + 1][xp + j] = xv[j] * mx1[j];
-                sm.Z[xu][xp + j] = zv[j];
-            }
+    // Raw reads of one chunk (tokens past T read nothing and keep zeros): dt / lambda /
+    // dt_scale of token tid (tid <= Q, one past the chunk for b_u), x and z of token xu, and
+    // the B^ / C^ rows and theta of tokens 4 wv .. 4 wv + 3, pair lane. Issued a chunk ahead.
+    float rdt = 0.f, rlam = 0.f, rsc = 1.f;
+    float xv[XE], zv[XE];
+    f32x4 rb[4], rc[4];
+    float th[4];
+    auto load_chunk = [&](int kk) {
+        const int s0n = kk * Q;
+        if (tid <= Q && s0n + tid < T) {
+            const float* pr = prow + (int64_t)(s0n + tid) * a.rs;
+            rdt = pr[a.pl.dt + h];
+            if (a.trap) rlam = pr[a.pl.lam + h];
+            if (a.dt_scale) rsc = a.dt_scale[((int64_t)b * T + s0n + tid) * a.H + h];
         }
 #pragma unroll
-        for (int pt = 0; pt < 4; ++pt)
+        for (int j = 0; j < XE; ++j) xv[j] = zv[j] = 0.f;
+        if (s0n + xu < T) {
+            const float* pr = prow + (int64_t)(s0n + xu) * a.rs + h * P + pc + xp;
 #pragma unroll
-            for (int v = 0; v < 4; ++v) sm.H[16 * wv + 4 * g4 + v][16 * pt + l16] = hacc[pt][v];
-        f32x4 rb[4], rc[4];
-        float th[4];
+            for (int j = 0; j < XE; ++j) {
+                xv[j] = pr[a.pl.x + j];
+                zv[j] = pr[a.pl.z + j];
+            }
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int tok = s0 + 4 * wv + j;
+            const int tok = s0n + 4 * wv + j;
             rb[j] = f32x4{0.f, 0.f, 0.f, 0.f};
             rc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
             th[j] = 0.f;
@@ -223,6 +218,34 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_f32(Args a) {
                 if (a.cplx) th[j] = prow[(int64_t)tok * a.rs + a.pl.theta + lane];
             }
         }
+    };
+    load_chunk(0);
+
+    for (int k = 0; k < K; ++k) {
+        const int s0 = k * Q;
+        const int par = k & 1;
+        __syncthreads();  // the previous chunk's tiles are consumed
+        // ---- prep 1: token scalars, X / Z rows and the state copy into LDS, from the raw
+        // reads issued during the previous chunk's contractions
+        if (tid <= Q) {
+            float dt = 0.f, lam = 1.f;
+            if (s0 + tid < T) {
+                dt = softplus_f(rdt + dtb) * rsc;
+                if (a.trap) lam = sigmoid_f(rlam);
+            }
+            sm.dtv[tid] = dt;
+            sm.lamv[tid] = lam;
+        }
+#pragma unroll
+        for (int j = 0; j < XE; ++j) {
+            sm.X[2 * xu][xp + j] = xv[j] * mx0[j];
+            sm.X[2 * xu + 1][xp + j] = xv[j] * mx1[j];
+            sm.Z[xu][xp + j] = zv[j];
+        }
+#pragma unroll
+        for (int pt = 0; pt < NPT; ++pt)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) sm.H[16 * wv + 4 * g4 + v][16 * pt + l16] = hacc[pt][v];
         __syncthreads();
         // ---- prep 2: chunk scalars (wave 0, lane = token: a prefix scan of A dt) and the
         // angle partial sums
@@ -271,6 +294,7 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_f32(Args a) {
             }
             if (wv == 7) sm.phi_run[par ^ 1][lane] = phi;
         }
+        if (k + 1 < K) load_chunk(k + 1);  // consumed by the next chunk's prep
         __syncthreads();
         // ---- G1: masked scores of the causal blocks (I, J), J <= I; wave w takes blocks w
         // and w + 8 of the list (0,0) (1,0) (1,1) (2,0) (2,1) (2,2) (3,0) (3,1) (3,2) (3,3)
@@ -297,51 +321,51 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_f32(Args a) {
             }
         }
         __syncthreads();
-        // ---- G3 + G2: output rows 16 I .. 16 I + 15, columns 16 (ptb + q) + l16
-        f32x4 yacc[2];
+        // ---- G3 + G2: output rows 16 I .. 16 I + 15, block columns 16 (ptb + q) + l16
+        f32x4 yacc[TPW];
 #pragma unroll
-        for (int q = 0; q < 2; ++q) yacc[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int q = 0; q < TPW; ++q) yacc[q] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll 4
         for (int k0 = 0; k0 < N; k0 += 4) {
             const float av = sm.C[16 * I + l16][k0 + g4];
 #pragma unroll
-            for (int q = 0; q < 2; ++q) yacc[q] = mfma4(av, sm.H[k0 + g4][16 * (ptb + q) + l16], yacc[q]);
+            for (int q = 0; q < TPW; ++q) yacc[q] = mfma4(av, sm.H[k0 + g4][16 * (ptb + q) + l16], yacc[q]);
         }
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
             const float e = sm.ec[(16 * I + 4 * g4 + v) >> 1];
 #pragma unroll
-            for (int q = 0; q < 2; ++q) yacc[q][v] *= e;
+            for (int q = 0; q < TPW; ++q) yacc[q][v] *= e;
         }
         for (int k0 = 0; k0 < 16 * (I + 1); k0 += 4) {
             const float sv = sm.S[16 * I + l16][k0 + g4];
 #pragma unroll
-            for (int q = 0; q < 2; ++q) yacc[q] = mfma4(sv, sm.X[k0 + g4][16 * (ptb + q) + l16], yacc[q]);
+            for (int q = 0; q < TPW; ++q) yacc[q] = mfma4(sv, sm.X[k0 + g4][16 * (ptb + q) + l16], yacc[q]);
         }
         // ---- G4: state update on this wave's rows n = 16 wv .. 16 wv + 15
         {
             const float dec = sm.ec[Q - 1];
 #pragma unroll
-            for (int pt = 0; pt < 4; ++pt) hacc[pt] *= dec;
+            for (int pt = 0; pt < NPT; ++pt) hacc[pt] *= dec;
 #pragma unroll 4
             for (int k0 = 0; k0 < ROWS; k0 += 4) {
                 const float bw = sm.B[k0 + g4][16 * wv + l16] * sm.w[(k0 + g4) >> 1];
 #pragma unroll
-                for (int pt = 0; pt < 4; ++pt) hacc[pt] = mfma4(bw, sm.X[k0 + g4][16 * pt + l16], hacc[pt]);
+                for (int pt = 0; pt < NPT; ++pt) hacc[pt] = mfma4(bw, sm.X[k0 + g4][16 * pt + l16], hacc[pt]);
             }
         }
         // ---- gate and MIMO-down; rows 4 g4 + 2 tt + r of the block are (t, r)
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            const int p = 16 * (ptb + q) + l16;
+        for (int q = 0; q < TPW; ++q) {
+            const int pl = 16 * (ptb + q) + l16;  // block column
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt) {
                 const int t = 8 * I + 2 * g4 + tt;
                 if (s0 + t < T) {
-                    const float z = sm.Z[t][p];
+                    const float z = sm.Z[t][pl];
                     const float o = md[q][0] * yacc[q][2 * tt] * silu_hw(z * mz[q][0]) +
                                     md[q][1] * yacc[q][2 * tt + 1] * silu_hw(z * mz[q][1]);
-                    a.y_out[((int64_t)b * T + s0 + t) * HP + h * P + p] = o;
+                    a.y_out[((int64_t)b * T + s0 + t) * HP + h * P + pc + pl] = o;
                 }
             }
         }
@@ -349,20 +373,20 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_f32(Args a) {
     __syncthreads();
     // ---- outputs of the walk
     if (a.h_final) {
-        float* hf = a.h_final + (int64_t)bh * P * N;
+        float* hf = a.h_final + (int64_t)bh * P * N + (int64_t)pc * N;
 #pragma unroll
-        for (int pt = 0; pt < 4; ++pt)
+        for (int pt = 0; pt < NPT; ++pt)
             *reinterpret_cast<f32x4*>(&hf[(16 * pt + l16) * N + 16 * wv + 4 * g4]) = hacc[pt];
     }
-    if (a.angle && tid < NH) a.angle[(int64_t)bh * NH + tid] = a.cplx ? sm.phi_run[K & 1][tid] : 0.f;
+    if (a.angle && pc == 0 && tid < NH) a.angle[(int64_t)bh * NH + tid] = a.cplx ? sm.phi_run[K & 1][tid] : 0.f;
     if (a.prev_bx) {
         // B~_{T-1} x_r,{T-1}^T from the last chunk's tiles (still in LDS)
         const int ul = (T - 1) - (K - 1) * Q;
-        const int p = tid >> 3, n0 = 16 * (tid & 7);
+        const int p = tid / (N / NPE), n0 = NPE * (tid % (N / NPE));  // block column p
         const float x0 = sm.X[2 * ul][p], x1 = sm.X[2 * ul + 1][p];
-        float* pb = a.prev_bx + (int64_t)bh * P * N + (int64_t)p * N + n0;
+        float* pb = a.prev_bx + (int64_t)bh * P * N + (int64_t)(pc + p) * N + n0;
 #pragma unroll
-        for (int j = 0; j < 16; j += 4) {
+        for (int j = 0; j < NPE; j += 4) {
             f32x4 o;
 #pragma unroll
             for (int e = 0; e < 4; ++e) o[e] = sm.B[2 * ul][n0 + j + e] * x0 + sm.B[2 * ul + 1][n0 + j + e] * x1;
@@ -415,7 +439,12 @@ int launch_fused_fp32_prefill(const m3_layer_desc& d, const m3_layer_params& p, 
     a.h_final = h_final;
     a.angle = angle;
     a.prev_bx = prev_bx;
-    hipLaunchKernelGGL(f32k::ssd_f32, dim3((unsigned)(d.batch * d.nheads)), dim3(f32k::THREADS), 0, stream, a);
+    // two 32-column blocks per (batch, head) while the pairs alone leave CUs idle
+    const int64_t bh = (int64_t)d.batch * d.nheads;
+    if (bh < 256)
+        hipLaunchKernelGGL(f32k::ssd_f32<32>, dim3((unsigned)(bh * 2)), dim3(f32k::THREADS), 0, stream, a);
+    else
+        hipLaunchKernelGGL(f32k::ssd_f32<64>, dim3((unsigned)bh), dim3(f32k::THREADS), 0, stream, a);
     return hipGetLastError() == hipSuccess ? M3_OK : M3_ERR_LAUNCH;
 }
 
