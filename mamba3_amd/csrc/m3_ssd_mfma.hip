@@ -1005,9 +1005,13 @@ struct SegPlan {
 };
 
 // Costs in chunk-times of one full-pass workgroup (one workgroup fills a CU). The state-only
-// pass takes 0.45 of that per chunk (measured at (8, 8192): 2.17 us against 4.85 us); a
-// split plan also pays one more launch and each segment's combine of earlier states.
+// pass takes 0.45 of that per chunk (measured at (8, 8192): 2.17 us against 4.85 us). Every
+// workgroup also pays a fixed cost for its pipeline fill and drain (1.5 chunk-times in the
+// full pass, 1.0 in the state pass: fitted to (4, 2048), where two equal segments beat one,
+// eight and long-first splits); a split plan pays one more launch and each segment's
+// combine of earlier states.
 constexpr double kStatePassCost = 0.45;
+constexpr double kSegFixed = 1.5, kStateSegFixed = 1.0;
 constexpr int kXcds = 8, kCusPerXcd = 32;
 
 // Makespan of workgroups of the given lengths dispatched in order onto the CUs of one XCD,
@@ -1039,12 +1043,13 @@ static SegPlan mfma_plan(const m3_layer_desc& d) {
     const int64_t cus = (int64_t)kXcds * kCusPerXcd;
     auto rounds = [&](int64_t n) { return (double)((n + cus - 1) / cus); };
     SegPlan best{1, K, K, 0};
-    double best_cost = rounds(bh) * K;
+    double best_cost = rounds(bh) * (K + kSegFixed);
     for (int s = 2; s <= std::min(K, 64); ++s) {
         const int c = (K + s - 1) / s;
         const int seff = (K + c - 1) / c;
         if (seff != s) continue;
-        const double cost = rounds(bh * s) * c + kStatePassCost * rounds(bh * (s - 1)) * c + 1.0 + 0.25 * (s - 1);
+        const double cost = rounds(bh * s) * (c + kSegFixed) +
+                            rounds(bh * (s - 1)) * (kStatePassCost * c + kStateSegFixed) + 1.0 + 0.25 * (s - 1);
         if (cost < best_cost - 1e-9) {
             best_cost = cost;
             best = SegPlan{s, c, c, 0};
@@ -1055,10 +1060,10 @@ static SegPlan mfma_plan(const m3_layer_desc& d) {
         double len[2 * kCusPerXcd];
         for (int f = 1; f <= K / 2; ++f) {
             for (int i = 0; i < L; ++i) {
-                len[i] = K - f;
-                len[L + i] = f;
+                len[i] = K - f + kSegFixed;
+                len[L + i] = f + kSegFixed;
             }
-            const double cost = kStatePassCost * f + xcd_makespan(len, 2 * L) + 1.0 + 0.25;
+            const double cost = kStatePassCost * f + kStateSegFixed + xcd_makespan(len, 2 * L) + 1.0 + 0.25;
             if (cost < best_cost - 1e-9) {
                 best_cost = cost;
                 best = SegPlan{2, K - f, f, 1};

@@ -122,7 +122,7 @@ def test_lm_d768_24_layers_prefill_and_greedy_decode(cuda_device):
     assert worst < max(BF16_TOL, worst16)
 
 
-@pytest.mark.parametrize("B,T,split", [(8, 512, False), (2, 1200, True), (8, 1000, True), (6, 1024, True)])
+@pytest.mark.parametrize("B,T,split", [(8, 512, False), (2, 1200, True), (8, 1500, True), (6, 1580, True)])
 def test_bf16_d768_prefill_plans_match_fp32_oracle(B, T, split, cuda_device):
     """The fused d768 prefill in each of its work plans, every batch row against the fp32
     oracle (mamba3/mamba3.py:192-258, mamba3/ssd.py:118-244): y, h, prev_BX and angle.
@@ -133,9 +133,9 @@ def test_bf16_d768_prefill_plans_match_fp32_oracle(B, T, split, cuda_device):
     * x (2, 1200, 768): 48 pairs, so each sequence is cut into 5 equal segments: a state-only
       pass, then each segment combines its predecessors' end states (rotated into its RoPE
       frame).
-    * x (8, 1000, 768) and (6, 1024, 768): the long-first split (the form the (8, 8192)
-      workload runs in). Two segments per pair, 4 + 12 chunks (a partial last chunk) and
-      5 + 11 chunks, 24 and 18 pairs per XCD: the long second segments are dispatched first,
+    * x (8, 1500, 768) and (6, 1580, 768): the long-first split (the form the (8, 8192)
+      workload runs in). Two segments per pair, 5 + 19 and 8 + 17 chunks (both end
+      mid-chunk), 24 and 18 pairs per XCD: the long second segments are dispatched first,
       the short first segments fill the remaining CUs.
     The plan is checked through the workspace size (segment states only when split)."""
     kw = dict(d_model=768, d_state=128, headdim=64, mimo_rank=2)
