@@ -73,6 +73,7 @@ struct __align__(16) Smem {
     Tok tok[2];           // by chunk parity
     float phi[Q][N / 2];  // RoPE angle of each (token, pair) of the chunk being prepared
     u32x4 th[Q][N / 16];  // theta of that chunk, bf16, 8 pairs per entry
+    float mz[PB][R], md[PB][R], mx[PB][R];  // mimo_z, mimo_down, mimo_x of the block's columns
 };
 
 struct Args {
@@ -228,18 +229,16 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
     const bool g4_wave = wave * TPW < N / 8;
     const int tt = (wave & 7) >> 1, pt = wave & 1;
     const int pe = p0 + 16 * pt + l16;  // this lane's output column
-    float mzr[R], mdr[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        mzr[r] = a.prm.mimo_z[(int64_t)(hp + pe) * R + r];
-        mdr[r] = a.prm.mimo_down[(int64_t)(hp + pe) * R + r];
-    }
     // X preparation jobs: column xp of tokens xt0 + m * (THREADS / PB) below Q, m < XJ.
     constexpr int XJ = (Q * PB + THREADS - 1) / THREADS;
     const int xp = tid % PB, xt0 = tid / PB;
-    float mxr[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) mxr[r] = a.prm.mimo_x[(int64_t)(hp + p0 + xp) * R + r];
+    if (tid < PB * R) {
+        const int c = tid / R, r = tid % R;
+        const int64_t e = (int64_t)(hp + p0 + c) * R + r;
+        sm.mz[c][r] = a.prm.mimo_z[e];
+        sm.md[c][r] = a.prm.mimo_down[e];
+        sm.mx[c][r] = a.prm.mimo_x[e];
+    }
     // theta staging jobs: units of 8 pairs of one token.
     constexpr int THU = Q * NH / 8;
     constexpr int THJ = (THU + THREADS - 1) / THREADS;
@@ -393,8 +392,9 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
             XRow<R> xv, xw;
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                xv.v[r] = (f16)(xval * mxr[r]);
-                xw.v[r] = (f16)(xval * mxr[r] * w);
+                const float mxr = sm.mx[xp][r];
+                xv.v[r] = (f16)(xval * mxr);
+                xw.v[r] = (f16)(xval * mxr * w);
             }
             *reinterpret_cast<XRow<R>*>(&sm.XT[kk & 1][xp][t * R]) = xv;
             *reinterpret_cast<XRow<R>*>(&sm.XwT[xp][t * R]) = xw;
@@ -482,31 +482,47 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
         }
 
         // Causal score tiles (ti, ui), ui <= ti, listed row by row: waves 8..15 take tiles
-        // 0..7, waves 8 and 9 also tiles 8 and 9.
+        // 0..7, waves 8 and 9 also tiles 8 and 9. A lane's four u-rows 16 ui + 4 g16 + v
+        // cover NU tokens; their mask factors are read (unconditionally: every index is
+        // below Q) and formed before the contraction.
         for (int idx = wave - 8; idx >= 0 && idx < 10; idx += 8) {
             const int ti = idx < 1 ? 0 : idx < 3 ? 1 : idx < 6 ? 2 : 3;
             const int ui = idx - ti * (ti + 1) / 2;
+            constexpr int NU = R >= 4 ? 1 : 4 / R;
+            const unsigned trow = 16 * ti + l16, t = trow / R;
+            const unsigned ub = (unsigned)(16 * ui + 4 * g16) / R;
+            // operands one k-step ahead of the MFMA that takes them
+            const f16* pa = &sm.B[16 * ui + l16][8 * g16];
+            const f16* pb = &sm.C[16 * ti + l16][8 * g16];
+            f16x8 A = *reinterpret_cast<const f16x8*>(pa);
+            f16x8 Bo = *reinterpret_cast<const f16x8*>(pb);
+            const float ct = tk.c2[t];
+            float fu[NU];
+#pragma unroll
+            for (int j = 0; j < NU; ++j) {
+                const unsigned u = ub + j;
+                const float e = __builtin_amdgcn_exp2f(ct - tk.c2[u]);
+                const float ab = tk.av[u] + (u < t ? tk.bv[u] : 0.f);
+                fu[j] = u <= t ? e * ab : 0.f;
+            }
             f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int s = 0; s < KN; ++s) {
-                const f16x8 A = *reinterpret_cast<const f16x8*>(&sm.B[16 * ui + l16][32 * s + 8 * g16]);
-                const f16x8 Bo = *reinterpret_cast<const f16x8*>(&sm.C[16 * ti + l16][32 * s + 8 * g16]);
+                f16x8 An = A, Bn = Bo;
+                if (s + 1 < KN) {
+                    An = *reinterpret_cast<const f16x8*>(pa + 32 * (s + 1));
+                    Bn = *reinterpret_cast<const f16x8*>(pb + 32 * (s + 1));
+                }
                 sacc = mfma16(A, Bo, sacc);
+                A = An;
+                Bo = Bn;
             }
             // lane: u-row 16 ui + 4 g16 + v, t-row 16 ti + l16
-            const int trow = 16 * ti + l16;
-            const int t = trow / R;
-            const float ct = tk.c2[t];
             f16x4 sv;
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const int urow = 16 * ui + 4 * g16 + v;
-                const int u = urow / R;
-                float val = 0.f;
-                if (u <= t)
-                    val = sacc[v] * __builtin_amdgcn_exp2f(ct - tk.c2[u]) * (tk.av[u] + (u < t ? tk.bv[u] : 0.f));
-                if (urow == trow) val += Dh;
-                sv[v] = (f16)val;
+                const float val = sacc[v] * fu[v * NU / 4];
+                sv[v] = (f16)(16 * ui + 4 * g16 + v == (int)trow ? val + Dh : val);
             }
             *reinterpret_cast<f16x4*>(&sm.S[trow][16 * ui + 4 * g16]) = sv;
         }
@@ -533,8 +549,8 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
             float o = 0.f;
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                const float zr = z * mzr[r];
-                o += mdr[r] * zr * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-zr * kLog2e)) * yacc[q * R + r];
+                const float zr = z * sm.mz[16 * pt + l16][r];
+                o += sm.md[16 * pt + l16][r] * zr * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-zr * kLog2e)) * yacc[q * R + r];
             }
             if (st < T) __builtin_nontemporal_store((bf16)o, &a.y_out[((int64_t)b * T + st) * a.H * a.P + hp + pe]);
             }
