@@ -198,7 +198,8 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
     constexpr int TPL = 4 / R;     // tokens per lane in an output tile
     __shared__ Smem<N, R> sm;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // wave index in an SGPR, so the role branches below are scalar branches
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g16 = lane >> 4, l16 = lane & 15;
     // Workgroups go to the 8 XCDs round-robin; renumber them so that consecutive logical
     // workgroups -- the column blocks and heads of one batch row, which read the same
@@ -367,7 +368,9 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
 #pragma unroll
         for (int m = 0; m < J; ++m) {
             const int t = rt0 + m * TSTEP;
-            if (t >= Q) break;  // threads past the chunk's jobs (small d_state)
+            if (Q * NH % THREADS != 0 && t >= Q) break;  // threads past the chunk's jobs (small d_state)
+            // Tokens past the end get a zero factor, which zeroes their rows (the clamped
+            // words they rotate are finite).
             const bool valid = s0 + t < T;
             f16x2 kA = f16x2{(f16)1.f, (f16)0.f};
             if (a.cplx) {
@@ -375,11 +378,12 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
                 fast_sincos(sm.phi[t][ri], sn, cs);
                 kA = f16x2{(f16)cs, (f16)sn};
             }
+            kA = as_f16x2(valid ? bits(kA) : 0u);
             const f16x2 kS = __builtin_shufflevector(kA, kA, 1, 0);
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                *reinterpret_cast<unsigned*>(&sm.B[t * R + r][2 * ri]) = valid ? rotate_pair(pwb[m][r], kA, kS) : 0u;
-                *reinterpret_cast<unsigned*>(&sm.C[t * R + r][2 * ri]) = valid ? rotate_pair(pwc[m][r], kA, kS) : 0u;
+                *reinterpret_cast<unsigned*>(&sm.B[t * R + r][2 * ri]) = rotate_pair(pwb[m][r], kA, kS);
+                *reinterpret_cast<unsigned*>(&sm.C[t * R + r][2 * ri]) = rotate_pair(pwc[m][r], kA, kS);
             }
         }
         // X rows (t, r) = x_t * mimo_x[p, r] (mamba3/mamba3.py:210), and times w_t.
@@ -502,7 +506,7 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
             for (int j = 0; j < NU; ++j) {
                 const unsigned u = ub + j;
                 const float e = __builtin_amdgcn_exp2f(ct - tk.c2[u]);
-                const float ab = tk.av[u] + (u < t ? tk.bv[u] : 0.f);
+                const float ab = fmaf(tk.bv[u], u < t ? 1.f : 0.f, tk.av[u]);
                 fu[j] = u <= t ? e * ab : 0.f;
             }
             f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -537,6 +541,9 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
 
         // ---- output ----
         if (out_wave) {
+            // y rows of this chunk; stores past the last token fall outside and are dropped
+            const __amdgpu_buffer_rsrc_t ry =
+                make_rsrc(a.y_out + ((int64_t)b * T + s0) * a.H * a.P, (int64_t)(T - s0) * a.H * a.P * 2);
             for (int s = 0; s <= tt / 2; ++s) {
                 const f16x8 A = *reinterpret_cast<const f16x8*>(&sm.S[16 * tt + l16][32 * s + 8 * g16]);
                 const f16x8 Bo = *reinterpret_cast<const f16x8*>(&sm.XT[k & 1][16 * pt + l16][32 * s + 8 * g16]);
@@ -552,7 +559,8 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
                 const float zr = z * sm.mz[16 * pt + l16][r];
                 o += sm.md[16 * pt + l16][r] * zr * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-zr * kLog2e)) * yacc[q * R + r];
             }
-            if (st < T) __builtin_nontemporal_store((bf16)o, &a.y_out[((int64_t)b * T + st) * a.H * a.P + hp + pe]);
+            __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, (bf16)o), ry,
+                                                  ((st - s0) * a.H * a.P + hp + pe) * 2, 0, kStream);
             }
         }
         if (g4_wave) {
