@@ -43,7 +43,11 @@ namespace wd {
 constexpr int ROWS = 64;              // (t, r) rows per chunk
 constexpr int PB = 32;                // headdim columns per workgroup
 constexpr int THREADS = 1024;         // 16 waves: 0-7 own output tiles, 8-15 score tiles
-constexpr int PAD = 8;                // f16 row padding of the LDS tiles
+constexpr int PAD = 8;                // f16 row padding of the X, S and H tiles
+// f16 row padding of the C~ / B~ tiles: a row stride of 8 (mod 16) 32-bit words keeps the
+// operand and transpose reads of those tiles free of most bank conflicts (a stride of
+// 4 (mod 16) words, padding 8, measured 5% slower at d_state 256).
+constexpr int PADCB = 16;
 constexpr float kHScale = 1.f / 256.f;  // the f16 state copy holds h * kHScale
 
 struct Tok {
@@ -64,8 +68,8 @@ struct __align__(2 * R) XRow {
 template <int N, int R>
 struct __align__(16) Smem {
     static constexpr int Q = ROWS / R;
-    f16 C[ROWS][N + PAD];
-    f16 B[ROWS][N + PAD];
+    f16 C[ROWS][N + PADCB];
+    f16 B[ROWS][N + PADCB];
     f16 XT[2][PB][ROWS + PAD];  // by chunk parity: G2 of chunk k reads while chunk k+1's is written
     f16 XwT[PB][ROWS + PAD];
     f16 S[ROWS][ROWS + PAD];
@@ -466,7 +470,7 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
                     const int nt = jt >> 1, ptj = jt & 1;
                     const f16* bp = &sm.B[32 * s + 8 * g16 + (l16 >> 2)][16 * nt + 4 * (l16 & 3)];
                     const f16x4 lo = ld_tr(bp);
-                    const f16x4 hi = ld_tr(bp + 4 * (N + PAD));
+                    const f16x4 hi = ld_tr(bp + 4 * (N + PADCB));
                     const f16x8 A = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
                     const f16x8 Bo = *reinterpret_cast<const f16x8*>(&sm.XwT[16 * ptj + l16][32 * s + 8 * g16]);
                     hacc[j] = mfma16(A, Bo, hacc[j]);
