@@ -236,7 +236,10 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
     const int pe = p0 + 16 * pt + l16;  // this lane's output column
     // X preparation jobs: column xp of tokens xt0 + m * (THREADS / PB) below Q, m < XJ.
     constexpr int XJ = (Q * PB + THREADS - 1) / THREADS;
-    const int xp = tid % PB, xt0 = tid / PB;
+    // (on the score waves first: the output waves also run G2, the gate and the store in
+    // the phase that prepares X)
+    const int xtid = Q * PB <= THREADS / 2 ? tid ^ (THREADS / 2) : tid;
+    const int xp = xtid % PB, xt0 = xtid / PB;
     if (tid < PB * R) {
         const int c = tid / R, r = tid % R;
         const int64_t e = (int64_t)(hp + p0 + c) * R + r;
