@@ -50,6 +50,11 @@ __device__ __forceinline__ float fast_silu(float x) {
 __device__ __forceinline__ float fast_softplus(float x) {
     return x > 20.f ? x : __logf(1.f + fast_exp(x));
 }
+// The same through the hardware log2 alone: 1 + e^x >= 1 needs no denormal range handling
+// (about 20 instructions fewer than __logf; results differ in the last bits).
+__device__ __forceinline__ float fast_softplus_hw(float x) {
+    return x > 20.f ? x : __builtin_amdgcn_logf(1.f + fast_exp(x)) * 0.69314718055994531f;
+}
 
 // Lane exchange through ds_bpermute: value of lane src. The index is computed by the
 // caller from its own lane number, so no address register lives across loops.

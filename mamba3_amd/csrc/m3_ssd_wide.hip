@@ -328,10 +328,15 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
         const int t = lane;
         const bool v0 = t < Q && s0 + t < T, v1 = t < Q && s0 + t + 1 < T;
         // mamba3/mamba3.py:200-204, 212-216
-        const float dt_t = v0 ? fast_softplus(bf(rdt0) + dtb) * sc0 : 0.f;
-        const float dt_n = v1 ? fast_softplus(bf(rdt1) + dtb) * sc1 : 0.f;
-        const float lam_t = v0 && a.trap ? __builtin_amdgcn_rcpf(1.f + fast_exp(-bf(rlam0))) : 1.f;
-        const float lam_n = v1 && a.trap ? __builtin_amdgcn_rcpf(1.f + fast_exp(-bf(rlam1))) : 1.f;
+        // computed for every lane (the clamped reads are finite), then selected
+        const float sp_t = fast_softplus_hw(bf(rdt0) + dtb) * sc0;
+        const float sp_n = fast_softplus_hw(bf(rdt1) + dtb) * sc1;
+        const float sg_t = __builtin_amdgcn_rcpf(1.f + fast_exp(-bf(rlam0)));
+        const float sg_n = __builtin_amdgcn_rcpf(1.f + fast_exp(-bf(rlam1)));
+        const float dt_t = v0 ? sp_t : 0.f;
+        const float dt_n = v1 ? sp_n : 0.f;
+        const float lam_t = v0 && a.trap ? sg_t : 1.f;
+        const float lam_n = v1 && a.trap ? sg_n : 1.f;
         const float c2 = wave_incl_scan(Ah * dt_t * kLog2e);
         const float c2_end = readlane(c2, Q - 1);
         if (wave == kAngleWave0 + NWA - 1) {
