@@ -13,8 +13,10 @@
 //   * a chunk has 64 (t, r) rows, i.e. Q = 64 / R tokens;
 //   * sixteen waves (four per SIMD) share both phases of a chunk: contract (waves 0-7 the
 //     inter-chunk output of their tile, waves 8-15 the score tiles, all the state update;
-//     two score waves also the next chunk's token scalars and RoPE angles), then output
-//     (waves 0-7 the intra-chunk output, gate and store; all the next chunk's tiles).
+//     two score waves compute the next chunk's token scalars and RoPE angles instead of a
+//     tile, and output waves 0-1 take their tiles), then output (waves 0-7 the intra-chunk
+//     output, gate and store; all the next chunk's B~ / C~ tiles, the score waves its X
+//     rows).
 //
 // Per chunk, in LDS (f16 unless noted):
 //   C [(t,r)][n], B [(u,r')][n]       C~ / B~: normalised B^ / C^ (bc_norm_wide) rotated
@@ -497,11 +499,17 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
             for (int v = 0; v < 4; ++v) yacc[v] *= tk.ec[(16 * tt + 4 * g16 + v) / R];
         }
 
-        // Causal score tiles (ti, ui), ui <= ti, listed row by row: waves 8..15 take tiles
-        // 0..7, waves 8 and 9 also tiles 8 and 9. A lane's four u-rows 16 ui + 4 g16 + v
-        // cover NU tokens; their mask factors are read (unconditionally: every index is
-        // below Q) and formed before the contraction.
-        for (int idx = wave - 8; idx >= 0 && idx < 10; idx += 8) {
+        // Causal score tiles (ti, ui), ui <= ti, listed row by row as 0..9: waves 8..15 take
+        // tile wave-8, waves 8 and 9 also tiles 8 and 9, except the angle waves, whose tiles
+        // go to output waves 0.. (which then run a tile and G3, as much as the waves with
+        // two tiles). A lane's four u-rows 16 ui + 4 g16 + v cover NU tokens; their mask
+        // factors are read (unconditionally: every index is below Q) and formed before the
+        // contraction.
+        const int tile0 = wave >= 8 ? (angle_wave ? -1 : wave - 8) : (wave < NWA ? kAngleWave0 - 8 + wave : -1);
+        const int tile1 = wave == 8 || wave == 9 ? wave : -1;
+        for (int c = 0; c < 2; ++c) {
+            const int idx = c == 0 ? tile0 : tile1;
+            if (idx < 0) break;
             const int ti = idx < 1 ? 0 : idx < 3 ? 1 : idx < 6 ? 2 : 3;
             const int ui = idx - ti * (ti + 1) / 2;
             constexpr int NU = R >= 4 ? 1 : 4 / R;
