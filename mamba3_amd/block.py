@@ -20,13 +20,22 @@ from . import _native, ops
 from .layer import KulaMamba, RMSNorm
 
 
-def add_scaled_linear(x: torch.Tensor, lin: nn.Linear, inp: torch.Tensor, scale: float) -> torch.Tensor:
+def add_scaled_linear(x: torch.Tensor, lin: nn.Linear, inp: torch.Tensor, scale: float,
+                      inplace: bool = False) -> torch.Tensor:
     """x + scale * lin(inp) as one GEMM: the residual x enters hipBLASLt as C with beta = 1
     and the scale as alpha, so the projection's output is neither rounded nor stored before
     the add (the reference runs the projection, the scale and the add as three ops,
-    mamba3/block.py:84-91)."""
-    out = torch.addmm(x.reshape(-1, x.shape[-1]), inp.reshape(-1, inp.shape[-1]), lin.weight.t(),
-                      beta=1.0, alpha=scale)
+    mamba3/block.py:84-91). torch.addmm first copies x into its new output; with inplace
+    (x is the caller's own intermediate and no autograd graph needs it) the GEMM accumulates
+    into x itself and that copy is saved."""
+    inp2 = inp.reshape(-1, inp.shape[-1])
+    if inplace and x.is_contiguous():
+        x2 = x.view(-1, x.shape[-1])
+        x2.addmm_(inp2, lin.weight.t(), beta=1.0, alpha=scale)
+        if lin.bias is not None:
+            x2.add_(lin.bias, alpha=scale)
+        return x
+    out = torch.addmm(x.reshape(-1, x.shape[-1]), inp2, lin.weight.t(), beta=1.0, alpha=scale)
     if lin.bias is not None:
         out = out + lin.bias * scale
     return out.view(x.shape)
@@ -116,25 +125,30 @@ class KulaMambaBlock(nn.Module):
 
     # The residual adds run as the beta = 1 input of the out_proj / w_down GEMMs
     # (add_scaled_linear); with gradient checkpointing the branches are recomputed whole.
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
+    def forward(self, x: torch.Tensor, _own_input: bool = False) -> torch.Tensor:
+        """_own_input (internal): x is an intermediate of the caller's forward
+        (KulaMambaLM), so without autograd the first residual add may overwrite it. The
+        second add overwrites the first one's output whenever no autograd graph needs it."""
         ckpt = self.gradient_checkpointing and self.training
+        nograd = not torch.is_grad_enabled()
         if ckpt:
             h = grad_checkpoint(self._ssm_forward, self.ssm_norm(x), use_reentrant=False)
             x = x + h * self.residual_scale
         else:
             y, _ = self.ssm._pre_out(self.ssm_norm(x))
-            x = add_scaled_linear(x, self.ssm.out_proj, y, self.residual_scale)
+            x = add_scaled_linear(x, self.ssm.out_proj, y, self.residual_scale,
+                                  inplace=_own_input and nograd)
         if self.use_mlp:
             if ckpt:
                 m = grad_checkpoint(self._mlp_forward, self.mlp_norm(x), use_reentrant=False)
                 x = x + m * self.residual_scale
             else:
-                x = self._mlp_residual(x)
+                x = self._mlp_residual(x, inplace=nograd)
         return x
 
-    def _mlp_residual(self, x: torch.Tensor) -> torch.Tensor:
+    def _mlp_residual(self, x: torch.Tensor, inplace: bool = False) -> torch.Tensor:
         return add_scaled_linear(x, self.mlp.w_down, self.mlp.hidden(self.mlp_norm(x)),
-                                 self.residual_scale)
+                                 self.residual_scale, inplace=inplace)
 
     def _small_step_usable(self, x: torch.Tensor) -> bool:
         """The decode step runs on the small-batch projection kernels (norm + in_proj,
@@ -247,7 +261,7 @@ class KulaMambaLM(nn.Module):
     def forward(self, input_ids: torch.Tensor, labels: torch.Tensor | None = None) -> dict:
         x = self.embedding(input_ids)
         for layer in self.layers:
-            x = layer(x)
+            x = layer(x, _own_input=True)
         logits = self.lm_head(self.norm(x))
         result = {"logits": logits}
         if labels is not None:
