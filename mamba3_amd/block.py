@@ -189,14 +189,17 @@ class KulaMambaBlock(nn.Module):
         y, new_state = self.ssm._step_pre_out(self.ssm_norm(x), ssm_state)
         x = add_scaled_linear(x, self.ssm.out_proj, y.view(*x.shape[:-1], -1), self.residual_scale)
         if self.use_mlp:
-            x = self._mlp_residual(x)
+            x = self._mlp_residual(x, inplace=not torch.is_grad_enabled())
         return x, new_state
 
-    def prefill(self, x: torch.Tensor):
+    def prefill(self, x: torch.Tensor, _own_input: bool = False):
+        """_own_input as in forward."""
+        nograd = not torch.is_grad_enabled()
         y, state = self.ssm._pre_out(self.ssm_norm(x), return_state=True)
-        x = add_scaled_linear(x, self.ssm.out_proj, y, self.residual_scale)
+        x = add_scaled_linear(x, self.ssm.out_proj, y, self.residual_scale,
+                              inplace=_own_input and nograd)
         if self.use_mlp:
-            x = self._mlp_residual(x)
+            x = self._mlp_residual(x, inplace=nograd)
         return x, state
 
 
@@ -282,7 +285,7 @@ class KulaMambaLM(nn.Module):
         x = self.embedding(input_ids)
         states = []
         for layer in self.layers:
-            x, st = layer.prefill(x)
+            x, st = layer.prefill(x, _own_input=True)
             states.append(st)
         logits = self.lm_head(self.norm(x)[:, -1])
         out = [input_ids]
