@@ -72,9 +72,10 @@ typedef struct m3_layer_desc {
  * fp32 generic kernel, which has no such range limit. */
 #define M3_FLAG_NO_F16_OPERANDS 1
 /* fp32 layers: m3_prefill_fwd keeps the intermediates m3_layer_bwd differentiates through in
- * its workspace (the staged fp32 layer path). Without it an fp32 layer with d_state 128,
- * headdim 64, mimo_rank 2 runs the fused fp32 kernel, whose workspace holds only the
- * normalised B^ / C^. */
+ * its workspace (the fp32 layer workspace; for d_state 128, headdim 64, mimo_rank 2 the fused
+ * fp32 kernel writes them as it walks the sequence, other shapes run the staged fp32 layer
+ * path). Without it an fp32 layer of that shape runs the fused fp32 kernel alone, whose
+ * workspace holds only the normalised B^ / C^. */
 #define M3_FLAG_FOR_BACKWARD 2
 
 /* Small per-layer parameters, all fp32 device arrays. Names follow the reference's

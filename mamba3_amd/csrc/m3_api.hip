@@ -53,9 +53,10 @@ int check_scan_bwd_shape(int64_t batch, int64_t nchunks, int64_t nheads, int64_t
 // kernel (bf16, aligned rows, 16-byte aligned proj / y_out), the general MFMA kernel
 // (bf16, d_state 64/128/256, rank 1/2/4, headdim % 32 == 0, 16-byte aligned h_final) --
 // both with f16 operands, so not under M3_FLAG_NO_F16_OPERANDS -- the fused fp32 kernel
-// (fp32, d_state 128 / headdim 64 / rank 2, not under M3_FLAG_FOR_BACKWARD), the fp32 layer
-// path on the fp32-MFMA chunk kernels (fp32, rank 1/2/4/8) or the generic one.
-enum class PrefillPath { kMfma, kWide, kFp32Fused, kFp32, kGeneric };
+// (fp32, d_state 128 / headdim 64 / rank 2; under M3_FLAG_FOR_BACKWARD it also writes the
+// staged operands of the layer backward into the fp32 layer workspace), the fp32 layer path
+// on the fp32-MFMA chunk kernels (fp32, rank 1/2/4/8) or the generic one.
+enum class PrefillPath { kMfma, kWide, kFp32Fused, kFp32FusedTrain, kFp32, kGeneric };
 
 PrefillPath prefill_path(const m3_layer_desc& d, const void* proj, const void* y_out,
                          const void* h_final, const void* prev_bx) {
@@ -63,6 +64,8 @@ PrefillPath prefill_path(const m3_layer_desc& d, const void* proj, const void* y
     if (f16_ok && m3::mfma_prefill_supported(d, proj, y_out)) return PrefillPath::kMfma;
     if (f16_ok && m3::wide_prefill_supported(d) && aligned(h_final, 16)) return PrefillPath::kWide;
     if (m3::fused_fp32_prefill_supported(d, proj, y_out, h_final, prev_bx)) return PrefillPath::kFp32Fused;
+    if ((d.flags & M3_FLAG_FOR_BACKWARD) && m3::fused_fp32_train_supported(d, proj, y_out, h_final, prev_bx))
+        return PrefillPath::kFp32FusedTrain;
     if (m3::fp32_layer_supported(d)) return PrefillPath::kFp32;
     return PrefillPath::kGeneric;
 }
@@ -72,6 +75,7 @@ size_t prefill_path_workspace(const m3_layer_desc& d, PrefillPath path) {
         case PrefillPath::kMfma: return m3::mfma_prefill_workspace(d);
         case PrefillPath::kWide: return m3::wide_prefill_workspace(d);
         case PrefillPath::kFp32Fused: return m3::fused_fp32_prefill_workspace(d);
+        case PrefillPath::kFp32FusedTrain:
         case PrefillPath::kFp32: return m3::fp32_layer_workspace(d);
         default: return m3::generic_prefill_workspace(d);
     }
@@ -100,6 +104,13 @@ int launch_prefill_path(PrefillPath path, const m3_layer_desc& d, const m3_layer
         case PrefillPath::kFp32Fused:
             return m3::launch_fused_fp32_prefill(d, p, proj, dt_scale, y_out, h_final, angle,
                                                  prev_bx, ws, stream);
+        case PrefillPath::kFp32FusedTrain: {
+            const m3::Fp32LayerParts parts = m3::fp32_layer_parts(d, ws);
+            size_t bytes = 0;
+            void* scratch_rows = m3::fp32_layer_scratch(d, ws, &bytes);
+            return m3::launch_fused_fp32_prefill(d, p, proj, dt_scale, y_out, h_final, angle,
+                                                 prev_bx, scratch_rows, stream, &parts);
+        }
         case PrefillPath::kFp32:
             return m3::launch_fp32_layer(d, p, proj, dt_scale, y_out, h_final, angle, prev_bx,
                                          ws, stream) == 0

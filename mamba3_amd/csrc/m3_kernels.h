@@ -102,10 +102,18 @@ bool fp32_layer_supported(const m3_layer_desc& d);
 // M3_FLAG_FOR_BACKWARD; 16-byte aligned rows of proj and y_out, h_final and prev_bx.
 bool fused_fp32_prefill_supported(const m3_layer_desc& d, const void* proj, const void* y_out,
                                   const void* h_final, const void* prev_bx);
+// The same kernel for the training forward (M3_FLAG_FOR_BACKWARD): it also writes the staged
+// per-token operands the layer backward reads (fp32_layer_parts of the fp32 layer workspace)
+// and keeps its B^ / C^ rows in that workspace's chunk-kernel region.
+bool fused_fp32_train_supported(const m3_layer_desc& d, const void* proj, const void* y_out,
+                                const void* h_final, const void* prev_bx);
+// The chunk-kernel region of the fp32 layer workspace (pointer into ws, and its size).
+void* fp32_layer_scratch(const m3_layer_desc& d, void* ws, size_t* bytes);
 size_t fused_fp32_prefill_workspace(const m3_layer_desc& d);
 int launch_fused_fp32_prefill(const m3_layer_desc& d, const m3_layer_params& p, const void* proj,
                               const float* dt_scale, void* y_out, float* h_final, float* angle,
-                              float* prev_bx, void* workspace, hipStream_t stream);
+                              float* prev_bx, void* workspace, hipStream_t stream,
+                              const Fp32LayerParts* stage = nullptr);
 size_t fp32_layer_workspace(const m3_layer_desc& d);
 int launch_fp32_layer(const m3_layer_desc& d, const m3_layer_params& p, const void* proj,
                       const float* dt_scale, void* y_out, float* h_final, float* angle,

@@ -295,6 +295,12 @@ Fp32LayerParts fp32_layer_parts(const m3_layer_desc& d, void* workspace) {
                           part(6), trap ? part(7) : nullptr, part(8), part(9)};
 }
 
+void* fp32_layer_scratch(const m3_layer_desc& d, void* ws, size_t* bytes) {
+    const lp::Plan pl = lp::plan(d);
+    *bytes = pl.total - pl.chunk_off;
+    return ws ? reinterpret_cast<char*>(ws) + pl.chunk_off : nullptr;
+}
+
 bool fp32_layer_supported(const m3_layer_desc& d) {
     return d.dtype == M3_DTYPE_F32 && prep_lds(d) <= 64 * 1024 &&
            chunked_fwd_mfma_workspace(d.batch, d.seqlen, d.nheads, d.headdim, d.d_state,

@@ -26,6 +26,9 @@
 //        gate   out = sum_r mimo_down_r silu(z mimo_z_r) y_r (mamba3/mamba3.py:233-239)
 //      The angles stay absolute (the walk starts at t = 0), so the final state, angle and
 //      prev_BX = B~_{T-1} x_r,{T-1}^T need no frame change (mamba3/mamba3.py:241-256).
+//      For the training forward (M3_FLAG_FOR_BACKWARD) the walk also stores, from the
+//      values it holds, the per-token operands the layer backward reads, in the staged
+//      fp32 layer path's layouts (m3_layer_fp32.hip), instead of that path's five launches.
 // LDS rows have odd strides (in 32-bit words), so the column reads of the MFMA operands (16
 // lanes on 16 rows) hit distinct banks.
 #include "m3_common.h"
@@ -74,6 +77,11 @@ struct Args {
     float* h_final;   // [B][H][P][N] or null
     float* angle;     // [B][H][NH] or null
     float* prev_bx;   // [B][H][P][N] or null
+    // With stage set, the per-token operands the layer backward reads (the staged fp32
+    // layer's layouts, token row (b T + t) H + h): dt, A, angles, x_r, x_g, x_b, B~, B~ of
+    // the previous token, C~ and y before the gate.
+    Fp32LayerParts st;
+    int stage;
 };
 
 __device__ __forceinline__ f32x4 mfma4(float a, float b, const f32x4& c) {
@@ -175,6 +183,8 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_f32(Args a) {
             md[q][r] = a.prm.mimo_down[(h * P + p) * R + r];
         }
     if (tid < NH) sm.phi_run[0][tid] = 0.f;
+    const bool st_head = a.stage && pc == 0;  // per-(token, head) operands: one block writes them
+    if (st_head && tid == 0) a.st.A[h] = Ah;
 
     f32x4 hacc[NPT];
 #pragma unroll
@@ -235,6 +245,7 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_f32(Args a) {
             }
             sm.dtv[tid] = dt;
             sm.lamv[tid] = lam;
+            if (st_head && tid < Q && s0 + tid < T) a.st.dt[((int64_t)b * T + s0 + tid) * a.H + h] = dt;
         }
 #pragma unroll
         for (int j = 0; j < XE; ++j) {
@@ -247,6 +258,23 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_f32(Args a) {
 #pragma unroll
             for (int v = 0; v < 4; ++v) sm.H[16 * wv + 4 * g4 + v][16 * pt + l16] = hacc[pt][v];
         __syncthreads();
+        if (a.stage && s0 + xu < T) {
+            // x_r, x_g = lambda_t x_r and x_b of the next token = (1 - lambda_{t+1})
+            // exp(A dt_{t+1}) x_r (mamba3/mamba3.py:210-224), this thread's X elements
+            const int64_t e0 = (((int64_t)b * T + s0 + xu) * a.H + h) * (P * R) + (int64_t)(pc + xp) * R;
+            const float lam = sm.lamv[xu];
+            const float sbn = a.trap ? (1.f - sm.lamv[xu + 1]) * expf(Ah * sm.dtv[xu + 1]) : 0.f;
+#pragma unroll
+            for (int j = 0; j < XE; ++j) {
+                const f32x2 xr = f32x2{xv[j] * mx0[j], xv[j] * mx1[j]};
+                *reinterpret_cast<f32x2*>(a.st.xr + e0 + j * R) = xr;
+                *reinterpret_cast<f32x2*>(a.st.xg + e0 + j * R) = xr * lam;
+                if (a.trap) {
+                    if (s0 + xu + 1 < T) *reinterpret_cast<f32x2*>(a.st.xb + e0 + (int64_t)a.H * P * R + j * R) = xr * sbn;
+                    if (s0 + xu == 0) *reinterpret_cast<f32x2*>(a.st.xb + e0 + j * R) = f32x2{0.f, 0.f};
+                }
+            }
+        }
         // ---- prep 2: chunk scalars (wave 0, lane = token: a prefix scan of A dt) and the
         // angle partial sums
         if (wv == 0) {
@@ -281,15 +309,30 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_f32(Args a) {
                 phi -= sm.dtv[t] * th[j];
                 float sn, cs;
                 sincosf(phi, &sn, &cs);
+                f32x4 bt, ct;  // (n=2i, r0) (2i, r1) (2i+1, r0) (2i+1, r1)
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
                     // pair lane holds (n=2i, r0) (2i, r1) (2i+1, r0) (2i+1, r1)
                     const float be = rb[j][r], bo = rb[j][2 + r];
                     const float ce = rc[j][r], co = rc[j][2 + r];
-                    sm.B[2 * t + r][2 * lane] = be * cs - bo * sn;
-                    sm.B[2 * t + r][2 * lane + 1] = be * sn + bo * cs;
-                    sm.C[2 * t + r][2 * lane] = ce * cs - co * sn;
-                    sm.C[2 * t + r][2 * lane + 1] = ce * sn + co * cs;
+                    bt[r] = be * cs - bo * sn;
+                    bt[2 + r] = be * sn + bo * cs;
+                    ct[r] = ce * cs - co * sn;
+                    ct[2 + r] = ce * sn + co * cs;
+                    sm.B[2 * t + r][2 * lane] = bt[r];
+                    sm.B[2 * t + r][2 * lane + 1] = bt[2 + r];
+                    sm.C[2 * t + r][2 * lane] = ct[r];
+                    sm.C[2 * t + r][2 * lane + 1] = ct[2 + r];
+                }
+                if (st_head && s0 + t < T) {
+                    const int64_t tk = ((int64_t)b * T + s0 + t) * a.H + h;
+                    *reinterpret_cast<f32x4*>(a.st.Bt + tk * NR + 4 * lane) = bt;
+                    *reinterpret_cast<f32x4*>(a.st.Ct + tk * NR + 4 * lane) = ct;
+                    if (a.trap) {
+                        if (s0 + t + 1 < T) *reinterpret_cast<f32x4*>(a.st.Bb + (tk + a.H) * NR + 4 * lane) = bt;
+                        if (s0 + t == 0) *reinterpret_cast<f32x4*>(a.st.Bb + tk * NR + 4 * lane) = f32x4{0.f, 0.f, 0.f, 0.f};
+                    }
+                    a.st.phi[tk * NH + lane] = phi;
                 }
             }
             if (wv == 7) sm.phi_run[par ^ 1][lane] = phi;
@@ -362,6 +405,9 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_f32(Args a) {
             for (int tt = 0; tt < 2; ++tt) {
                 const int t = 8 * I + 2 * g4 + tt;
                 if (s0 + t < T) {
+                    if (a.stage)
+                        *reinterpret_cast<f32x2*>(a.st.ys + (((int64_t)b * T + s0 + t) * a.H + h) * (P * R) + (int64_t)(pc + pl) * R) =
+                            f32x2{yacc[q][2 * tt], yacc[q][2 * tt + 1]};
                     const float z = sm.Z[t][pl];
                     const float o = md[q][0] * yacc[q][2 * tt] * silu_hw(z * mz[q][0]) +
                                     md[q][1] * yacc[q][2 * tt + 1] * silu_hw(z * mz[q][1]);
@@ -397,10 +443,9 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_f32(Args a) {
 
 }  // namespace f32k
 
-bool fused_fp32_prefill_supported(const m3_layer_desc& d, const void* proj, const void* y_out,
-                                  const void* h_final, const void* prev_bx) {
+static bool fused_fp32_shape_ok(const m3_layer_desc& d, const void* proj, const void* y_out,
+                                const void* h_final, const void* prev_bx) {
     if (d.dtype != M3_DTYPE_F32) return false;
-    if (d.flags & M3_FLAG_FOR_BACKWARD) return false;
     if (d.d_state != f32k::N || d.headdim != f32k::P || d.mimo_rank != f32k::R) return false;
     const ProjLayout pl = proj_layout(d);
     // 16-byte reads of the B / C rows and of x / z
@@ -411,13 +456,27 @@ bool fused_fp32_prefill_supported(const m3_layer_desc& d, const void* proj, cons
     return true;
 }
 
+bool fused_fp32_prefill_supported(const m3_layer_desc& d, const void* proj, const void* y_out,
+                                  const void* h_final, const void* prev_bx) {
+    return !(d.flags & M3_FLAG_FOR_BACKWARD) && fused_fp32_shape_ok(d, proj, y_out, h_final, prev_bx);
+}
+
+bool fused_fp32_train_supported(const m3_layer_desc& d, const void* proj, const void* y_out,
+                                const void* h_final, const void* prev_bx) {
+    if (!fused_fp32_shape_ok(d, proj, y_out, h_final, prev_bx) || !fp32_layer_supported(d)) return false;
+    size_t bytes = 0;
+    fp32_layer_scratch(d, nullptr, &bytes);
+    return bytes >= fused_fp32_prefill_workspace(d);
+}
+
 size_t fused_fp32_prefill_workspace(const m3_layer_desc& d) {
     return 2 * (size_t)d.batch * d.seqlen * d.ngroups * f32k::NR * sizeof(float) + 256;
 }
 
 int launch_fused_fp32_prefill(const m3_layer_desc& d, const m3_layer_params& p, const void* proj,
                               const float* dt_scale, void* y_out, float* h_final, float* angle,
-                              float* prev_bx, void* workspace, hipStream_t stream) {
+                              float* prev_bx, void* workspace, hipStream_t stream,
+                              const Fp32LayerParts* stage) {
     const ProjLayout pl = proj_layout(d);
     const int64_t nrows = (int64_t)d.batch * d.seqlen * d.ngroups;
     float* bn = reinterpret_cast<float*>(workspace);
@@ -439,6 +498,8 @@ int launch_fused_fp32_prefill(const m3_layer_desc& d, const m3_layer_params& p, 
     a.h_final = h_final;
     a.angle = angle;
     a.prev_bx = prev_bx;
+    a.st = stage ? *stage : Fp32LayerParts{};
+    a.stage = stage != nullptr;
     // two 32-column blocks per (batch, head) while the pairs alone leave CUs idle
     const int64_t bh = (int64_t)d.batch * d.nheads;
     if (bh < 256)

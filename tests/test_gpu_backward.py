@@ -229,6 +229,49 @@ def test_layer_state_gradients_match_oracle(kw, cuda_device):
         assert max_rel(p.grad, params[name].grad) < FP32_TOL, name
 
 
+D768_KW = dict(d_model=768, d_state=128, headdim=64, mimo_rank=2)
+
+
+@pytest.mark.parametrize("extra", [{}, dict(use_trapezoidal=False), dict(use_complex_ssm=False)],
+                         ids=["default", "trapezoid-off", "complex-off"])
+def test_layer_d768_fused_training_forward_state_gradients(extra, cuda_device):
+    """The d_model 768 shape (d_state 128, headdim 64, rank 2) trains on the fused fp32
+    prefill kernel, which also writes the per-token operands m3_layer_bwd reads. Two
+    sequences of 93 tokens (a partial last 32-token chunk) and a loss over the output and
+    every state tensor (h, angle, prev_BX): the input's and every parameter's gradient
+    against the fp64 oracle layer."""
+    kw = dict(D768_KW, **extra)
+    print(f"d768 fused training forward {kw}", flush=True)
+    torch.manual_seed(0)
+    layer = mamba3_amd.KulaMamba(**kw).to(cuda_device).train()
+    H, P, N = layer.nheads, layer.headdim, layer.d_state
+    g = torch.Generator().manual_seed(31)
+    x = torch.randn(2, 93, 768, generator=g)
+    w = torch.randn(2, 93, 768, generator=g)
+    wst = {"h": torch.randn(2, H, P, N, generator=g), "angle": torch.randn(2, H, N // 2, generator=g),
+           "prev_BX": torch.randn(2, H, P, N, generator=g)}
+    params = {k: v.detach().double().cpu().clone().requires_grad_()
+              for k, v in layer.state_dict().items()}
+    xr = x.double().requires_grad_()
+    out_ref, st_ref = ref.layer_forward(oracle_cfg(kw), params, xr, return_state=True)
+    loss = (out_ref * w.double()).sum()
+    for k, v in wst.items():
+        loss = loss + (st_ref[k].double() * v.double()).sum()
+    loss.backward()
+    xd = x.to(cuda_device).requires_grad_()
+    out, st = layer.prefill(xd)
+    loss = (out * w.to(cuda_device)).sum()
+    for k, v in wst.items():
+        loss = loss + (st[k] * v.to(cuda_device)).sum()
+    loss.backward()
+    assert max_rel(out, out_ref) < FP32_TOL
+    for k in wst:
+        assert max_rel(st[k], st_ref[k]) < FP32_TOL, k
+    assert max_rel(xd.grad, xr.grad) < FP32_TOL
+    for name, p in layer.named_parameters():
+        assert max_rel(p.grad, params[name].grad) < FP32_TOL, name
+
+
 def test_layer_training_runs_on_the_native_backward(cuda_device):
     """The parity tests above go through m3_layer_bwd: it covers every configuration they use."""
     from mamba3_amd import _native
