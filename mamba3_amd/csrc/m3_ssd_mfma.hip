@@ -588,10 +588,10 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
             const int lane = opaque(threadIdx.x & 63);
             const int s0 = kk * Q;
             const __amdgpu_buffer_rsrc_t rp = make_rsrc(proj_b + (int64_t)s0 * a.rs, (int64_t)max(T - s0, 0) * a.rs * 2);
-            sdt = ld_u16(rp, (lane * rs + (int)a.pl.dt + h) * 2);
+            sdt = ld_u16(rp, (__mul24(lane, rs) + (int)a.pl.dt + h) * 2);
             sdt64 = ld_u16(rp, (Q * rs + (int)a.pl.dt + h) * 2);
             if (a.trap) {
-                slam = ld_u16(rp, (lane * rs + (int)a.pl.lam + h) * 2);
+                slam = ld_u16(rp, (__mul24(lane, rs) + (int)a.pl.lam + h) * 2);
                 slam64 = ld_u16(rp, (Q * rs + (int)a.pl.lam + h) * 2);
             }
             if (a.dt_scale) {
@@ -733,12 +733,12 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
         auto load_x = [&](int kk) {
             const int lane = opaque(threadIdx.x & 63);
             const int t = 8 * hw + (lane >> 3), p = 8 * (lane & 7);
-            xr = __builtin_amdgcn_raw_buffer_load_b128(rsrc_proj(kk), (t * rs + (int)a.pl.x + h * P + p) * 2, 0, kStream);
+            xr = __builtin_amdgcn_raw_buffer_load_b128(rsrc_proj(kk), (__mul24(t, rs) + (int)a.pl.x + h * P + p) * 2, 0, kStream);
         };
         auto load_z = [&](int kk) {
             const int lane = opaque(threadIdx.x & 63);
             const int t = 8 * hw + (lane >> 3), p = 8 * (lane & 7);
-            zr = __builtin_amdgcn_raw_buffer_load_b128(rsrc_proj(kk), (t * rs + (int)a.pl.z + h * P + p) * 2, 0, kStream);
+            zr = __builtin_amdgcn_raw_buffer_load_b128(rsrc_proj(kk), (__mul24(t, rs) + (int)a.pl.z + h * P + p) * 2, 0, kStream);
         };
         auto load_th = [&](int kk) {
             const int lane = opaque(threadIdx.x & 63);
@@ -749,30 +749,32 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
             // 0, so the angles stay zero): no branch, so the reads stay where they are written.
             const __amdgpu_buffer_rsrc_t rth =
                 make_rsrc(proj_b + (int64_t)s0 * a.rs, a.cplx ? (int64_t)max(T - s0, 0) * a.rs * 2 : 0);
-            const int vth = (8 * q * rs + (a.cplx ? (int)a.pl.theta : 0) + pa) * 2;
+            const int vth = (__mul24(8 * q, rs) + (a.cplx ? (int)a.pl.theta : 0) + pa) * 2;
 #pragma unroll
             for (int j = 0; j < 8; ++j) rawth[j] = __builtin_amdgcn_raw_buffer_load_b32(rth, vth, j * rs * 2, 0);
         };
-        auto load_bc = [&](int kk, int j) {  // token 8q + 4th + j
+        // the four tokens' B^ / C^ words of this lane: one offset, the token step in soffset
+        auto load_bc4 = [&](int kk) {
             const int lane = opaque(threadIdx.x & 63);
             const int q = lane >> 3;
             const int pa = 16 * (hw & 3) + 2 * (lane & 7);
             const int s0 = kk * Q;
             const int left = max(T - s0, 0);
             const int64_t bcbytes = left > 0 ? ((int64_t)(left - 1) * bnrs + NR) * 2 : 0;
-            const int vbc = ((8 * q + 4 * th) * bnrs + 4 * pa) * 2;
-            rawB[j] = __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(bn_b + (int64_t)s0 * bnrs, bcbytes), vbc,
-                                                            j * bnrs * 2, 0);
-            if (kFull)
-                rawC[j] = __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(cn_b + (int64_t)s0 * bnrs, bcbytes), vbc,
-                                                                j * bnrs * 2, 0);
+            const int vbc = (__mul24(8 * q + 4 * th, bnrs) + 4 * pa) * 2;
+            const __amdgpu_buffer_rsrc_t rb = make_rsrc(bn_b + (int64_t)s0 * bnrs, bcbytes);
+            const __amdgpu_buffer_rsrc_t rc = make_rsrc(cn_b + (int64_t)s0 * bnrs, bcbytes);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                rawB[j] = __builtin_amdgcn_raw_buffer_load_b128(rb, vbc, j * bnrs * 2, 0);
+                if (kFull) rawC[j] = __builtin_amdgcn_raw_buffer_load_b128(rc, vbc, j * bnrs * 2, 0);
+            }
         };
         auto load_all = [&](int kk) {
             load_x(kk);
             if (kFull) load_z(kk);
             load_th(kk);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) load_bc(kk, j);
+            load_bc4(kk);
         };
         // ---- RoPE rotation of this lane's four tokens, two pairs, both ranks
         // kn: chunk whose theta reads are issued once the prefix has used this chunk's.
@@ -892,16 +894,19 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
             for (int j = 0; j < 4; ++j) {
                 const int row = 2 * (8 * q + 4 * th + j);
                 const int col = sw_cb(row, 2 * pa);  // rows row, row+1 share the swizzle
+                const int off = __mul24(row, (N + PAD) * 2) + col * 2;  // bytes
+                char* cbase = reinterpret_cast<char*>(&sm.C[0][0]) + off;
+                char* bbase = reinterpret_cast<char*>(&sm.B[0][0]) + off;
                 // The fences keep these as single 64-bit stores.
                 if (kFull) {
-                    *reinterpret_cast<u32x2*>(&sm.C[row][col]) = outC[j][0];
+                    *reinterpret_cast<u32x2*>(cbase) = outC[j][0];
                     M3_LDS_FENCE();
-                    *reinterpret_cast<u32x2*>(&sm.C[row + 1][col]) = outC[j][1];
+                    *reinterpret_cast<u32x2*>(cbase + (N + PAD) * 2) = outC[j][1];
                     M3_LDS_FENCE();
                 }
-                *reinterpret_cast<u32x2*>(&sm.B[row][col]) = outB[j][0];
+                *reinterpret_cast<u32x2*>(bbase) = outB[j][0];
                 M3_LDS_FENCE();
-                *reinterpret_cast<u32x2*>(&sm.B[row + 1][col]) = outB[j][1];
+                *reinterpret_cast<u32x2*>(bbase + (N + PAD) * 2) = outB[j][1];
                 M3_LDS_FENCE();
             }
         };
@@ -914,7 +919,7 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
             const int HP = a.H * P;
             const __amdgpu_buffer_rsrc_t ry =
                 make_rsrc(a.y_out + ((int64_t)b * T + s0) * HP, (int64_t)max(T - s0, 0) * HP * 2);
-            __builtin_amdgcn_raw_buffer_store_b128(o, ry, (t * HP + h * P + p) * 2, 0, kStream);
+            __builtin_amdgcn_raw_buffer_store_b128(o, ry, (__mul24(t, HP) + h * P + p) * 2, 0, kStream);
         };
 
         // prologue: first chunk's tiles and z, reads of the second chunk
@@ -939,8 +944,7 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
             if (more) {
                 // B^ / C^ of chunk k+1 (shared by all heads of the batch row, mostly L2
                 // hits) are read now and rotated last; x, z and theta are a chunk ahead.
-#pragma unroll
-                for (int j = 0; j < 4; ++j) load_bc(k + 1, j);
+                load_bc4(k + 1);
                 prep_x((k + 1) & 1);
                 M3_FENCE();
                 load_x(k + 2);
@@ -989,6 +993,11 @@ bool mfma_prefill_supported(const m3_layer_desc& d, const void* proj, const void
     // 128-bit x / z loads and y stores, 32-bit theta loads.
     if (d.proj_row_stride % 8 != 0 || pl.x % 8 != 0 || pl.z % 8 != 0 || pl.theta % 2 != 0) return false;
     if (reinterpret_cast<uintptr_t>(proj) % 16 != 0 || reinterpret_cast<uintptr_t>(y_out) % 16 != 0)
+        return false;
+    // Row offsets are formed with 24-bit multiplies (v_mul_i32_i24): the row strides stay
+    // below 2^23 elements.
+    if (d.proj_row_stride >= (1 << 23) || (int64_t)d.ngroups * mf::NR >= (1 << 23) ||
+        (int64_t)d.nheads * d.headdim >= (1 << 23))
         return false;
     // 32-bit buffer offsets: one batch row of proj (and of B^/C^) stays below 2 GiB.
     if ((int64_t)(d.seqlen + 1) * d.proj_row_stride * 2 >= ((int64_t)1 << 31)) return false;
