@@ -13,7 +13,9 @@
 //                  RoPE pair (n=2i, n=2i+1) of one rank is one 32-bit word.
 //   2. ssd_chunks<false> for segments 0..S-2: only the state update, giving each
 //                  segment's end state from a zero start plus its total log-decay and
-//                  total RoPE angle increment.
+//                  total RoPE angle increment. When its workgroups leave CUs idle, launch
+//                  1 covers only the tokens this pass reads and spare workgroups of this
+//                  launch normalise the other tokens' B^ / C^ (read only by launch 3).
 //   3. ssd_chunks<true> for all segments: combines the preceding segments' end states
 //                  into the incoming state, then computes every chunk's output.
 //
@@ -99,6 +101,26 @@ struct __align__(16) Smem {
     f16 mxT[R][P];            // mimo_x per rank and p
 };
 
+// The (token, group) rows of tokens [lo, hi) of every batch row, numbered consecutively:
+// logical row l is batch row l / per_b, physical row (b T + lo) G + l % per_b.
+struct BcRows {
+    const bf16* proj;
+    int64_t rs, offB, offC;
+    int G;
+    float eps;
+    const float *wB, *biasB, *wC, *biasC;
+    f16 *Bn, *Cn;
+    int64_t nrows;  // logical rows: batch * (hi - lo) * G
+    int64_t per_b;  // (hi - lo) * G
+    int64_t skip;   // (T - (hi - lo)) * G: physical rows between batch rows' ranges
+    int64_t lo_g;   // lo * G
+    __device__ __forceinline__ int64_t phys(int64_t l) const {
+        if (skip == 0) return l + lo_g;  // the whole sequence
+        const int64_t b = l / per_b;
+        return l + b * skip + lo_g;
+    }
+};
+
 struct Args {
     int B, T, H, G, S, cps;
     int first;  // chunks of segment 0 (segments 1.. have cps chunks, the last may be shorter)
@@ -118,6 +140,10 @@ struct Args {
     float* h_final;
     float* angle;
     float* prev_bx;
+    // ssd_chunks<false>: workgroups past the nstate state-pass ones normalise bcr's rows
+    // (the tokens the state pass does not read) on the CUs the state pass leaves idle.
+    int nstate;
+    BcRows bcr;
 };
 
 
@@ -145,62 +171,60 @@ __device__ __forceinline__ int zsw(int t, int p) { return p ^ (16 * ((t >> 1) & 
 // ---------------------------------------------------------------------------------
 constexpr int kBcTok = 4;  // (token, group) rows per wave of bc_norm
 
-__global__ __launch_bounds__(256) void bc_norm(const bf16* __restrict__ proj, int64_t rs,
-                                               int64_t offB, int64_t offC, int G,
-                                               int64_t ntok_grp, float eps,
-                                               const float* __restrict__ wB,
-                                               const float* __restrict__ biasB,
-                                               const float* __restrict__ wC,
-                                               const float* __restrict__ biasC,
-                                               f16* __restrict__ Bn, f16* __restrict__ Cn) {
-    // A wave normalises kBcTok consecutive (token, group) rows: all their reads go out
-    // together, the weights and biases are read once (rows past the end read the last row
-    // and store nothing). Lane = pair i; raw order at 4i: (n=2i,r0) (2i,r1) (2i+1,r0) (2i+1,r1).
-    const int lane = threadIdx.x & 63;
-    const int64_t tg0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * kBcTok;
-    if (tg0 >= ntok_grp) return;
+// A wave normalises KR consecutive logical rows starting at l0: all their reads go out
+// together, the weights are read once (rows past the end read the last row and store
+// nothing). Lane = pair i; raw order at 4i: (n=2i,r0) (2i,r1) (2i+1,r0) (2i+1,r1).
+template <int KR>
+__device__ __forceinline__ void bc_norm_rows(const BcRows& c, int64_t l0, int lane) {
     const int e = 4 * lane;
-    bf16x4 vb[kBcTok], vc[kBcTok];
-    int gg[kBcTok];
+    bf16x4 vb[KR], vc[KR];
+    int gg[KR];
+    int64_t tgp[KR];
 #pragma unroll
-    for (int k = 0; k < kBcTok; ++k) {
-        const int64_t tg = tg0 + k < ntok_grp ? tg0 + k : ntok_grp - 1;
-        const int64_t tok = tg / G;
-        gg[k] = (int)(tg % G);
-        const bf16* row = proj + tok * rs;
-        vb[k] = *reinterpret_cast<const bf16x4*>(row + offB + (int64_t)gg[k] * NR + e);
-        vc[k] = *reinterpret_cast<const bf16x4*>(row + offC + (int64_t)gg[k] * NR + e);
+    for (int k = 0; k < KR; ++k) {
+        const int64_t tg = c.phys(l0 + k < c.nrows ? l0 + k : c.nrows - 1);
+        tgp[k] = tg;
+        const int64_t tok = tg / c.G;
+        gg[k] = (int)(tg % c.G);
+        const bf16* row = c.proj + tok * c.rs;
+        vb[k] = *reinterpret_cast<const bf16x4*>(row + c.offB + (int64_t)gg[k] * NR + e);
+        vc[k] = *reinterpret_cast<const bf16x4*>(row + c.offC + (int64_t)gg[k] * NR + e);
     }
-    const f32x4 wb4 = *reinterpret_cast<const f32x4*>(wB + e);
-    const f32x4 wc4 = *reinterpret_cast<const f32x4*>(wC + e);
+    const f32x4 wb4 = *reinterpret_cast<const f32x4*>(c.wB + e);
+    const f32x4 wc4 = *reinterpret_cast<const f32x4*>(c.wC + e);
 #pragma unroll
-    for (int k = 0; k < kBcTok; ++k) {
-        const int64_t tg = tg0 + k;
-        const f32x4 bb4 = *reinterpret_cast<const f32x4*>(biasB + (int64_t)gg[k] * NR + e);
-        const f32x4 bc4 = *reinterpret_cast<const f32x4*>(biasC + (int64_t)gg[k] * NR + e);
-        float b[4], c[4], sb = 0.f, sc = 0.f;
+    for (int k = 0; k < KR; ++k) {
+        const f32x4 bb4 = *reinterpret_cast<const f32x4*>(c.biasB + (int64_t)gg[k] * NR + e);
+        const f32x4 bc4 = *reinterpret_cast<const f32x4*>(c.biasC + (int64_t)gg[k] * NR + e);
+        float b[4], cc[4], sb = 0.f, sc = 0.f;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             b[j] = (float)vb[k][j];
-            c[j] = (float)vc[k][j];
+            cc[j] = (float)vc[k][j];
             sb += b[j] * b[j];
-            sc += c[j] * c[j];
+            sc += cc[j] * cc[j];
         }
         sb = lane_sum<64>(sb);
         sc = lane_sum<64>(sc);
-        const float rb = rsqrtf(sb * (1.f / NR) + eps), rc = rsqrtf(sc * (1.f / NR) + eps);
+        const float rb = rsqrtf(sb * (1.f / NR) + c.eps), rc = rsqrtf(sc * (1.f / NR) + c.eps);
         float ob[4], oc[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             ob[j] = b[j] * rb * wb4[j] + bb4[j];
-            oc[j] = c[j] * rc * wc4[j] + bc4[j];
+            oc[j] = cc[j] * rc * wc4[j] + bc4[j];
         }
         // pair-packed: (e_r0, o_r0, e_r1, o_r1)
-        if (tg < ntok_grp) {
-            *reinterpret_cast<f16x4*>(Bn + tg * NR + e) = f16x4{(f16)ob[0], (f16)ob[2], (f16)ob[1], (f16)ob[3]};
-            *reinterpret_cast<f16x4*>(Cn + tg * NR + e) = f16x4{(f16)oc[0], (f16)oc[2], (f16)oc[1], (f16)oc[3]};
+        if (l0 + k < c.nrows) {
+            *reinterpret_cast<f16x4*>(c.Bn + tgp[k] * NR + e) = f16x4{(f16)ob[0], (f16)ob[2], (f16)ob[1], (f16)ob[3]};
+            *reinterpret_cast<f16x4*>(c.Cn + tgp[k] * NR + e) = f16x4{(f16)oc[0], (f16)oc[2], (f16)oc[1], (f16)oc[3]};
         }
     }
+}
+
+__global__ __launch_bounds__(256) void bc_norm(BcRows c) {
+    const int64_t l0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * kBcTok;
+    if (l0 >= c.nrows) return;
+    bc_norm_rows<kBcTok>(c, l0, threadIdx.x & 63);
 }
 
 // ---------------------------------------------------------------------------------
@@ -386,11 +410,20 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
 
     const int nseg = kFull ? a.S : a.S - 1;
+    if (!kFull && (int)blockIdx.x >= a.nstate) {
+        // Spare workgroup of the state pass: B^ / C^ of the tokens past the state pass
+        // (read only by the full pass), eight rows per wave and flight. No barrier, no LDS.
+        const int nw = (gridDim.x - a.nstate) * (THREADS / 64);
+        const int gw = (blockIdx.x - a.nstate) * (THREADS / 64) + wv;
+        for (int64_t l0 = (int64_t)gw * 8; l0 < a.bcr.nrows; l0 += (int64_t)nw * 8)
+            bc_norm_rows<8>(a.bcr, l0, tid & 63);
+        return;
+    }
     // Workgroup i runs on XCD i % 8. Consecutive (batch, head) pairs (one batch row shares
     // B^ / C^) are kept on one XCD. Split plan (a.order): each XCD first gets the long second
     // segments of its pairs, one per CU, then the short first segments, which cycle through
     // the remaining CUs while the long ones run.
-    const int nblk = gridDim.x;
+    const int nblk = kFull ? (int)gridDim.x : a.nstate;
     int seg, bh;
     if (kFull && a.order) {
         const int L = nblk / 16;  // pairs per XCD
@@ -1085,16 +1118,41 @@ static SegPlan mfma_plan(const m3_layer_desc& d) {
     return best;
 }
 
+// The (token, group) rows of tokens [lo, hi) of every batch row.
+static mf::BcRows bc_rows(const m3_layer_desc& d, const m3_layer_params& p, const void* proj,
+                          f16* bn, f16* cn, int64_t lo, int64_t hi) {
+    const ProjLayout pl = proj_layout(d);
+    mf::BcRows c;
+    c.proj = reinterpret_cast<const bf16*>(proj);
+    c.rs = d.proj_row_stride;
+    c.offB = pl.B;
+    c.offC = pl.C;
+    c.G = d.ngroups;
+    c.eps = d.rms_eps;
+    c.wB = p.B_norm_w;
+    c.biasB = p.B_bias;
+    c.wC = p.C_norm_w;
+    c.biasC = p.C_bias;
+    c.Bn = bn;
+    c.Cn = cn;
+    c.per_b = (hi - lo) * d.ngroups;
+    c.nrows = (int64_t)d.batch * c.per_b;
+    c.skip = (int64_t)d.seqlen * d.ngroups - c.per_b;
+    c.lo_g = lo * d.ngroups;
+    return c;
+}
+
+static void launch_bc_rows(const mf::BcRows& c, hipStream_t stream) {
+    const int64_t rows_per_block = 4 * mf::kBcTok;
+    if (c.nrows > 0)
+        hipLaunchKernelGGL(mf::bc_norm, dim3((unsigned)((c.nrows + rows_per_block - 1) / rows_per_block)),
+                           dim3(256), 0, stream, c);
+}
+
 // B^ / C^ rows of every (token, group) of the layer, pair-packed f16 (bc_norm).
 void launch_bc_norm(const m3_layer_desc& d, const m3_layer_params& p, const void* proj,
                     f16* bn, f16* cn, hipStream_t stream) {
-    const ProjLayout pl = proj_layout(d);
-    const int64_t ntg = (int64_t)d.batch * d.seqlen * d.ngroups;
-    const int64_t rows_per_block = 4 * mf::kBcTok;
-    hipLaunchKernelGGL(mf::bc_norm, dim3((unsigned)((ntg + rows_per_block - 1) / rows_per_block)), dim3(256), 0, stream,
-                       reinterpret_cast<const bf16*>(proj), d.proj_row_stride, pl.B, pl.C,
-                       d.ngroups, ntg, d.rms_eps, p.B_norm_w, p.B_bias, p.C_norm_w, p.C_bias,
-                       bn, cn);
+    launch_bc_rows(bc_rows(d, p, proj, bn, cn, 0, d.seqlen), stream);
 }
 
 size_t mfma_prefill_workspace(const m3_layer_desc& d) {
@@ -1134,10 +1192,22 @@ int launch_mfma_prefill(const m3_layer_desc& d, const m3_layer_params& p, const 
     a.angle = angle;
     a.prev_bx = prev_bx;
 
-    launch_bc_norm(d, p, proj, bn, cn, stream);
+    // With a state pass that leaves CUs idle, the B^ / C^ of the tokens it reads are
+    // normalised first and those of the other tokens by spare workgroups of the state pass.
+    a.nstate = (int)nseg;
+    const int ncu = kXcds * kCusPerXcd;
+    const int64_t t_state = S > 1 ? std::min<int64_t>(d.seqlen, (int64_t)(plan.first + (S - 2) * plan.cps) * mf::Q) : 0;
+    const int nspare = (S > 1 && nseg < ncu && t_state < d.seqlen) ? ncu - (int)nseg : 0;
+    if (nspare > 0) {
+        launch_bc_rows(bc_rows(d, p, proj, bn, cn, 0, t_state), stream);
+        a.bcr = bc_rows(d, p, proj, bn, cn, t_state, d.seqlen);
+    } else {
+        launch_bc_norm(d, p, proj, bn, cn, stream);
+        a.bcr = bc_rows(d, p, proj, bn, cn, 0, 0);
+    }
     if (S > 1)
-        hipLaunchKernelGGL(mf::ssd_chunks<false>, dim3((unsigned)(d.batch * d.nheads * (S - 1))),
-                           dim3(mf::THREADS), 0, stream, a);
+        hipLaunchKernelGGL(mf::ssd_chunks<false>, dim3((unsigned)(nseg + nspare)), dim3(mf::THREADS), 0,
+                           stream, a);
     hipLaunchKernelGGL(mf::ssd_chunks<true>, dim3((unsigned)(d.batch * d.nheads * S)),
                        dim3(mf::THREADS), 0, stream, a);
     return hipGetLastError() == hipSuccess ? M3_OK : M3_ERR_LAUNCH;

@@ -318,6 +318,28 @@ def test_layer_forward_gradients_with_dt_scale(cuda_device):
         assert max_rel(p.grad, pg[name]) < FP32_TOL, name
 
 
+def test_layer_d768_fused_training_forward_with_dt_scale(cuda_device):
+    """dt_scale through the fused fp32 training forward (d_model 768 shape): the output, the
+    input's, dt_scale's and every parameter's gradient against the fp64 oracle."""
+    torch.manual_seed(0)
+    layer = mamba3_amd.KulaMamba(**D768_KW).to(cuda_device).train()
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(1, 70, 768, generator=g)
+    w = torch.randn(1, 70, 768, generator=g)
+    ds = torch.rand(1, 70, layer.nheads, generator=g) + 0.5
+    wh = torch.randn(1, layer.nheads, 64, 128, generator=g)
+    out_ref, pg, xg_ref = _oracle_layer_grads(D768_KW, layer, x, w, wh, dt_scale=ds)
+    xd = x.to(cuda_device).requires_grad_()
+    dsd = ds.to(cuda_device).requires_grad_()
+    out, st = layer.prefill(xd, dt_scale=dsd)
+    ((out * w.to(cuda_device)).sum() + (st["h"] * wh.to(cuda_device)).sum()).backward()
+    assert max_rel(out, out_ref) < FP32_TOL
+    assert max_rel(xd.grad, xg_ref) < FP32_TOL
+    assert max_rel(dsd.grad, pg["dt_scale"]) < FP32_TOL
+    for name, p in layer.named_parameters():
+        assert max_rel(p.grad, pg[name]) < FP32_TOL, name
+
+
 def test_layer_bf16_gradients_match_fp32_oracle(cuda_device):
     kw = dict(d_model=128, d_state=64, headdim=32, mimo_rank=2)
     torch.manual_seed(0)
