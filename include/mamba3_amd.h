@@ -227,6 +227,28 @@ int m3_step_fwd(const m3_layer_desc* desc, const m3_layer_params* params,
                 void* angle_out, void* stream);
 
 /*
+ * Backward of m3_step_fwd. Replaces ATen's autograd through KulaMamba.step between in_proj
+ * and out_proj (mamba3/mamba3.py:275-322, with _process_BC_step :170-190), which the
+ * reference differentiates like any other torch code. fp32 only (desc->dtype F32; a bf16
+ * caller upcasts): proj [B,proj_row_stride], dt_scale [B,H] or NULL, h_in, prev_bx_in
+ * [B,H,P,N], angle_in [B,H,N/2] as passed to the forward; g_y [B,H*P] = dL/dy (the gated
+ * output); g_h_out, g_prev_bx_out [B,H,P,N] and g_angle_out [B,H,N/2] = dL/d(new state), each
+ * NULL for zero. Outputs: g_proj (the in_proj columns of each row written), g_h_in,
+ * g_prev_bx_in, g_angle_in, and the parameter gradients `grads` (written, not accumulated;
+ * grads->dt_scale [B,H] when not NULL). Deterministic. Supported: d_state <= 512,
+ * mimo_rank <= 8, 4 (2 N R + N/2 + 2 P R + P) floats of LDS per head within 64 KiB.
+ * workspace: m3_step_bwd_workspace_size() bytes, 256-byte aligned.
+ */
+int m3_step_bwd_workspace_size(const m3_layer_desc* desc, size_t* bytes);
+int m3_step_bwd(const m3_layer_desc* desc, const m3_layer_params* params, const float* proj,
+                const float* dt_scale, const float* h_in, const float* prev_bx_in,
+                const float* angle_in, const float* g_y, const float* g_h_out,
+                const float* g_prev_bx_out, const float* g_angle_out, float* g_proj,
+                float* g_h_in, float* g_prev_bx_in, float* g_angle_in,
+                const m3_layer_param_grads* grads, void* workspace, size_t workspace_bytes,
+                void* stream);
+
+/*
  * Chunked SSD on pre-processed, head-expanded inputs: the public op
  * chunked_ssd (mamba3/ssd.py:118-244). All tensors are in `dtype` except h_init,
  * h_final (fp32) and A, D (fp32 [H]).

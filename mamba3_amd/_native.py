@@ -43,6 +43,8 @@ EXPORTED_SYMBOLS = (
     "m3_small_linear",
     "m3_small_swiglu",
     "m3_silu_mul",
+    "m3_step_bwd_workspace_size",
+    "m3_step_bwd",
 )
 
 M3_ERR_SCRATCH_LIMIT = 8
@@ -144,6 +146,12 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.m3_layer_bwd.argtypes = ([ctypes.POINTER(LayerDesc), ctypes.POINTER(LayerParams)]
                                  + [_vp] * 3 + [ctypes.c_size_t] + [_vp] * 5
                                  + [ctypes.POINTER(LayerParamGrads), _vp, ctypes.c_size_t, _vp])
+    lib.m3_step_bwd_workspace_size.restype = ctypes.c_int
+    lib.m3_step_bwd_workspace_size.argtypes = [ctypes.POINTER(LayerDesc), ctypes.POINTER(ctypes.c_size_t)]
+    lib.m3_step_bwd.restype = ctypes.c_int
+    lib.m3_step_bwd.argtypes = ([ctypes.POINTER(LayerDesc), ctypes.POINTER(LayerParams)]
+                                + [_vp] * 13
+                                + [ctypes.POINTER(LayerParamGrads), _vp, ctypes.c_size_t, _vp])
     lib.m3_chunked_ssd_bwd_workspace_size.restype = ctypes.c_int
     lib.m3_chunked_ssd_bwd_workspace_size.argtypes = [_i32] * 7 + [ctypes.POINTER(ctypes.c_size_t)]
     lib.m3_chunked_ssd_bwd.restype = ctypes.c_int
@@ -316,6 +324,29 @@ def layer_bwd(desc: LayerDesc, params: LayerParams, proj, dt_scale, fwd_ws, g_ou
                              ptr(g_prev), ptr(g_proj), ctypes.byref(grads), ptr(ws), n,
                              stream_of(proj)),
           "m3_layer_bwd")
+
+
+def step_bwd_supported(desc: LayerDesc) -> bool:
+    """True when m3_step_bwd covers this (fp32) layer shape."""
+    n = ctypes.c_size_t(0)
+    st = lib().m3_step_bwd_workspace_size(ctypes.byref(desc), ctypes.byref(n))
+    return st == 0 and n.value > 0
+
+
+def step_bwd(desc: LayerDesc, params: LayerParams, proj, dt_scale, h_in, prev_in, angle_in, g_y,
+             g_h, g_prev, g_angle, g_proj, g_h_in, g_prev_in, g_angle_in,
+             grads: LayerParamGrads) -> None:
+    """m3_step_bwd; allocates its workspace."""
+    n = ctypes.c_size_t(0)
+    check(lib().m3_step_bwd_workspace_size(ctypes.byref(desc), ctypes.byref(n)),
+          "m3_step_bwd_workspace_size")
+    ws = torch.empty(n.value, dtype=torch.uint8, device=proj.device)
+    check(lib().m3_step_bwd(ctypes.byref(desc), ctypes.byref(params), ptr(proj), ptr(dt_scale),
+                            ptr(h_in), ptr(prev_in), ptr(angle_in), ptr(g_y), ptr(g_h),
+                            ptr(g_prev), ptr(g_angle), ptr(g_proj), ptr(g_h_in), ptr(g_prev_in),
+                            ptr(g_angle_in), ctypes.byref(grads), ptr(ws), n.value,
+                            stream_of(proj)),
+          "m3_step_bwd")
 
 
 def rmsnorm_fwd(x, weight, y, rstd, eps: float) -> None:

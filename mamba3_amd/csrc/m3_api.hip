@@ -324,6 +324,43 @@ int m3_step_fwd(const m3_layer_desc* desc, const m3_layer_params* params, const 
                            as_stream(stream));
 }
 
+int m3_step_bwd_workspace_size(const m3_layer_desc* desc, size_t* bytes) {
+    if (!bytes) return M3_ERR_NULL_POINTER;
+    const int st = check_desc(desc);
+    if (st != M3_OK) return st;
+    *bytes = m3::step_bwd_workspace(*desc);
+    return *bytes > 0 ? M3_OK : M3_ERR_UNSUPPORTED;
+}
+
+int m3_step_bwd(const m3_layer_desc* desc, const m3_layer_params* params, const float* proj,
+                const float* dt_scale, const float* h_in, const float* prev_bx_in,
+                const float* angle_in, const float* g_y, const float* g_h_out,
+                const float* g_prev_bx_out, const float* g_angle_out, float* g_proj,
+                float* g_h_in, float* g_prev_bx_in, float* g_angle_in,
+                const m3_layer_param_grads* grads, void* workspace, size_t workspace_bytes,
+                void* stream) {
+    int st = check_desc(desc);
+    if (st != M3_OK) return st;
+    st = check_params(params);
+    if (st != M3_OK) return st;
+    if (desc->dtype != M3_DTYPE_F32) return M3_ERR_UNSUPPORTED;
+    if (!proj || !h_in || !prev_bx_in || !angle_in || !g_y || !g_proj || !g_h_in ||
+        !g_prev_bx_in || !g_angle_in || !grads)
+        return M3_ERR_NULL_POINTER;
+    if (!grads->A_log || !grads->D || !grads->dt_bias || !grads->B_norm_w || !grads->C_norm_w ||
+        !grads->B_bias || !grads->C_bias || !grads->mimo_x || !grads->mimo_z || !grads->mimo_down)
+        return M3_ERR_NULL_POINTER;
+    const size_t need = m3::step_bwd_workspace(*desc);
+    if (need == 0) return M3_ERR_UNSUPPORTED;
+    if (!workspace || workspace_bytes < need) return M3_ERR_WORKSPACE;
+    if (!aligned(workspace, 256)) return M3_ERR_MISALIGNED;
+    return m3::launch_step_bwd(*desc, *params, proj, dt_scale, h_in, prev_bx_in, angle_in, g_y,
+                               g_h_out, g_prev_bx_out, g_angle_out, g_proj, g_h_in, g_prev_bx_in,
+                               g_angle_in, *grads, workspace, as_stream(stream)) == 0
+               ? M3_OK
+               : M3_ERR_LAUNCH;
+}
+
 static bool norm_dtypes_ok(int xd, int wd, int yd) {
     auto ok = [](int t) { return t == M3_DTYPE_F32 || t == M3_DTYPE_BF16; };
     if (!ok(xd) || !ok(wd) || !ok(yd)) return false;

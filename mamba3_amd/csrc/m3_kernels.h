@@ -127,6 +127,16 @@ int launch_layer_bwd(const m3_layer_desc& d, const m3_layer_params& p, const voi
                      const float* g_h, const float* g_angle, const float* g_prev, float* g_proj,
                      const m3_layer_param_grads& g, void* workspace, hipStream_t stream);
 
+// Backward of the decode step (m3_step_bwd.hip): supported shapes, workspace bytes and
+// launcher (fp32 proj, states and gradients).
+bool step_bwd_supported(const m3_layer_desc& d);
+size_t step_bwd_workspace(const m3_layer_desc& d);
+int launch_step_bwd(const m3_layer_desc& d, const m3_layer_params& p, const float* proj,
+                    const float* dt_scale, const float* h, const float* prev, const float* ang,
+                    const float* gy, const float* gH, const float* gP, const float* gA,
+                    float* g_proj, float* g_h, float* g_prev, float* g_ang,
+                    const m3_layer_param_grads& out, void* workspace, hipStream_t stream);
+
 // Block RMSNorm (m3_norm.hip): forward, and backward workspace bytes and launcher.
 int launch_rmsnorm_fwd(const void* x, int xdtype, const void* w, int wdtype, void* y,
                        int ydtype, float* rstd, int64_t rows, int d, float eps,

@@ -227,8 +227,9 @@ class KulaMamba(nn.Module):
 
     def step(self, hidden_states: torch.Tensor, ssm_state: dict, dt_scale=None):
         """One decode step (mamba3/mamba3.py:267-322). `hidden_states` is (B, d_model)
-        or (B, 1, d_model); the output has the same rank. Returns a new state dict. The
-        step kernel has no backward: backward through its output raises."""
+        or (B, 1, d_model); the output has the same rank. Returns a new state dict. Under
+        autograd the step is differentiable (m3_step_bwd) with respect to the input, the
+        incoming state, the parameters and dt_scale, as the reference's is."""
         squeeze = hidden_states.dim() == 2
         y, state = self._step_pre_out(hidden_states, ssm_state, dt_scale)
         w = self.out_proj.weight

@@ -283,7 +283,7 @@ def _step_eager(proj: torch.Tensor, A_log: torch.Tensor, D: torch.Tensor, dt_bia
          eps: float) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
     """m3_step_fwd on one token per row: proj (B,W) and the state -> (y (B,H*P), new h,
     new prev_BX, new angle). The state comes back in new tensors (h and prev_BX fp32,
-    angle in its input dtype). No autograd formula: backward through it raises."""
+    angle in its input dtype). Its autograd formula is m3_step_bwd."""
     out = [torch.empty(proj.shape[0], nheads * headdim, device=proj.device, dtype=proj.dtype),
            torch.empty_like(h, dtype=torch.float32), torch.empty_like(prev_bx, dtype=torch.float32),
            torch.empty_like(angle)]
@@ -301,6 +301,79 @@ def _(proj, A_log, D, dt_bias, B_norm_w, C_norm_w, B_bias, C_bias, mimo_x, mimo_
       dt_scale, h, prev_bx, angle, nheads, headdim, d_state, mimo_rank, ngroups, trap, cplx, eps):
     return (proj.new_empty(proj.shape[0], nheads * headdim), h.new_empty(h.shape, dtype=torch.float32),
             prev_bx.new_empty(prev_bx.shape, dtype=torch.float32), angle.new_empty(angle.shape))
+
+
+@torch.library.custom_op(f"{NS}::step_bwd", mutates_args=())
+def step_bwd(proj: torch.Tensor, A_log: torch.Tensor, D: torch.Tensor, dt_bias: torch.Tensor,
+             B_norm_w: torch.Tensor, C_norm_w: torch.Tensor, B_bias: torch.Tensor,
+             C_bias: torch.Tensor, mimo_x: torch.Tensor, mimo_z: torch.Tensor,
+             mimo_down: torch.Tensor, dt_scale: Optional[torch.Tensor], h: torch.Tensor,
+             prev_bx: torch.Tensor, angle: torch.Tensor, g_y: torch.Tensor,
+             g_h: Optional[torch.Tensor], g_prev: Optional[torch.Tensor],
+             g_angle: Optional[torch.Tensor], nheads: int, headdim: int, d_state: int,
+             mimo_rank: int, ngroups: int, trap: bool, cplx: bool,
+             eps: float) -> list[torch.Tensor]:
+    """m3_step_bwd: gradients of step's outputs with respect to proj, the ten parameters,
+    dt_scale (zeros when None) and the incoming h, prev_BX and angle, all fp32."""
+    proj32 = proj.detach().float().contiguous()
+    desc = _desc(proj32.shape[0], 1, nheads, headdim, d_state, mimo_rank, ngroups, trap, cplx,
+                 eps, torch.float32, proj32.stride(0))
+    if not _native.step_bwd_supported(desc):
+        raise _native.NativeError(
+            f"KulaMamba.step backward: this shape (d_state={d_state}, headdim={headdim}, "
+            f"mimo_rank={mimo_rank}) is not supported by m3_step_bwd")
+    params = (A_log, D, dt_bias, B_norm_w, C_norm_w, B_bias, C_bias, mimo_x, mimo_z, mimo_down)
+    pack, f32 = _f32_params(params)
+
+    def f32c(t):
+        return None if t is None else t.detach().float().contiguous()
+
+    g_proj = torch.zeros_like(proj32)
+    grads = [torch.empty_like(t) for t in f32]
+    g_dts = torch.zeros(proj32.shape[0], nheads, device=proj.device, dtype=torch.float32)
+    h32, prev32, ang32 = f32c(h), f32c(prev_bx), f32c(angle)
+    g_h_in, g_prev_in, g_ang_in = (torch.empty_like(h32), torch.empty_like(prev32),
+                                   torch.empty_like(ang32))
+    _native.step_bwd(desc, pack, proj32, f32c(dt_scale), h32, prev32, ang32, f32c(g_y), f32c(g_h),
+                     f32c(g_prev), f32c(g_angle), g_proj, g_h_in, g_prev_in, g_ang_in,
+                     _native.LayerParamGrads(*[t.data_ptr() for t in grads],
+                                             g_dts.data_ptr() if dt_scale is not None else None))
+    return [g_proj, *grads, g_dts, g_h_in, g_prev_in, g_ang_in]
+
+
+@step_bwd.register_fake
+def _(proj, A_log, D, dt_bias, B_norm_w, C_norm_w, B_bias, C_bias, mimo_x, mimo_z, mimo_down,
+      dt_scale, h, prev_bx, angle, g_y, g_h, g_prev, g_angle, nheads, headdim, d_state,
+      mimo_rank, ngroups, trap, cplx, eps):
+    params = (A_log, D, dt_bias, B_norm_w, C_norm_w, B_bias, C_bias, mimo_x, mimo_z, mimo_down)
+    f = torch.float32
+    return [proj.new_empty(proj.shape, dtype=f), *[t.new_empty(t.shape, dtype=f) for t in params],
+            proj.new_empty(proj.shape[0], nheads, dtype=f), h.new_empty(h.shape, dtype=f),
+            prev_bx.new_empty(prev_bx.shape, dtype=f), angle.new_empty(angle.shape, dtype=f)]
+
+
+def _step_setup(ctx, inputs, output):
+    ctx.cfg = inputs[15:]
+    ctx.has_scale = inputs[11] is not None
+    ctx.save_for_backward(*inputs[:15])
+    ctx.set_materialize_grads(False)
+
+
+def _step_backward(ctx, g_y, g_h, g_prev, g_angle):
+    proj, *rest = ctx.saved_tensors
+    params, dt_scale, h, prev_bx, angle = rest[:10], rest[10], rest[11], rest[12], rest[13]
+    if g_y is None:
+        g_y = proj.new_zeros(proj.shape[0], ctx.cfg[0] * ctx.cfg[1], dtype=torch.float32)
+    out = step_bwd(proj, *params, dt_scale, h, prev_bx, angle, g_y, g_h, g_prev, g_angle,
+                   *ctx.cfg)
+    g_proj, g_params, g_dts, g_hin, g_pin, g_ain = out[0], out[1:11], out[11], out[12], out[13], out[14]
+    grads = [g_proj.to(proj.dtype)] + [g.to(p.dtype) for g, p in zip(g_params, params)]
+    grads.append(g_dts if ctx.has_scale else None)
+    grads += [g_hin.to(h.dtype), g_pin.to(prev_bx.dtype), g_ain.to(angle.dtype)]
+    return (*grads, None, None, None, None, None, None, None, None)
+
+
+step.register_autograd(_step_backward, setup_context=_step_setup)
 
 
 def step_into(proj, A_log, D, dt_bias, B_norm_w, C_norm_w, B_bias, C_bias, mimo_x, mimo_z,
@@ -619,7 +692,7 @@ def _(gate_up, d_ff):
 def _direct() -> bool:
     """Eager calls with autograd off bypass the dispatcher: its per-call host time is what a
     per-token decode loop waits on. Traced calls and calls under autograd go through the
-    registered ops (whose missing backward then raises)."""
+    registered ops and their autograd formulas."""
     return not torch.is_grad_enabled() and not torch.compiler.is_compiling()
 
 

@@ -395,10 +395,97 @@ def test_lm_gradient_checkpointing_gives_the_same_gradients(cuda_device):
         assert torch.equal(g0[n], g1[n]), n
 
 
-def test_step_backward_raises_instead_of_wrong_gradients(cuda_device):
+STEP_KW = LAYER_KW[:5] + [dict(d_model=768, d_state=128, headdim=64, mimo_rank=2),
+                          dict(d_model=64, d_state=48, headdim=16, mimo_rank=8, ngroups=2)]
+
+
+@pytest.mark.parametrize("kw", STEP_KW, ids=lambda k: "-".join(f"{a}{b}" for a, b in k.items()))
+def test_step_gradients_match_oracle(kw, cuda_device):
+    """Autograd through KulaMamba.step (m3_step_bwd between in_proj and out_proj) against
+    autograd through the fp64 oracle step (mamba3/mamba3.py:267-322) from a random state: a
+    loss over the output and every new-state tensor; the gradients of the input, of the
+    incoming h, prev_BX and angle, of every parameter and of dt_scale at 1e-4."""
+    print(f"step backward {kw}", flush=True)
     torch.manual_seed(0)
-    layer = mamba3_amd.KulaMamba(64, d_state=16, headdim=16).to(cuda_device).train()
-    st = layer.allocate_inference_state(1)
-    out, _ = layer.step(torch.randn(1, 64, device=cuda_device), st)
-    with pytest.raises(RuntimeError, match="mamba3_amd.step"):
-        out.sum().backward()
+    layer = mamba3_amd.KulaMamba(**kw).to(cuda_device).train()
+    H, P, N = layer.nheads, layer.headdim, layer.d_state
+    g = torch.Generator().manual_seed(17)
+    Bat = 3
+    x = torch.randn(Bat, kw["d_model"], generator=g)
+    st = {"h": torch.randn(Bat, H, P, N, generator=g), "prev_BX": torch.randn(Bat, H, P, N, generator=g),
+          "angle": torch.randn(Bat, H, N // 2, generator=g)}
+    ds = torch.rand(Bat, H, generator=g) + 0.5
+    w = torch.randn(Bat, kw["d_model"], generator=g)
+    wst = {k: torch.randn(v.shape, generator=g) for k, v in st.items()}
+
+    params = {k: v.detach().double().cpu().clone().requires_grad_()
+              for k, v in layer.state_dict().items()}
+    xr = x.double().requires_grad_()
+    st_r = {k: v.double().requires_grad_() for k, v in st.items()}
+    ds_r = ds.double().requires_grad_()
+    out_r, new_r = ref.layer_step(oracle_cfg(kw), params, xr, st_r, dt_scale=ds_r)
+    loss = (out_r * w.double()).sum()
+    for k in wst:
+        loss = loss + (new_r[k] * wst[k].double()).sum()
+    loss.backward()
+
+    xd = x.to(cuda_device).requires_grad_()
+    st_d = {k: v.to(cuda_device).requires_grad_() for k, v in st.items()}
+    ds_d = ds.to(cuda_device).requires_grad_()
+    out, new = layer.step(xd, st_d, dt_scale=ds_d)
+    loss = (out * w.to(cuda_device)).sum()
+    for k in wst:
+        loss = loss + (new[k] * wst[k].to(cuda_device)).sum()
+    loss.backward()
+    assert max_rel(out, out_r) < FP32_TOL
+    assert max_rel(xd.grad, xr.grad) < FP32_TOL
+    assert max_rel(ds_d.grad, ds_r.grad) < FP32_TOL
+    for k in st:
+        assert max_rel(st_d[k].grad, st_r[k].grad) < FP32_TOL, k
+    for name, p in layer.named_parameters():
+        assert max_rel(p.grad, params[name].grad) < FP32_TOL, name
+
+
+def test_step_gradients_of_the_output_alone(cuda_device):
+    """A loss over the output only (the new state's gradients are None) and no dt_scale."""
+    kw = dict(d_model=64, d_state=16, headdim=16, mimo_rank=2)
+    torch.manual_seed(0)
+    layer = mamba3_amd.KulaMamba(**kw).to(cuda_device).train()
+    H, P, N = layer.nheads, layer.headdim, layer.d_state
+    g = torch.Generator().manual_seed(18)
+    x = torch.randn(2, 64, generator=g)
+    st = {"h": torch.randn(2, H, P, N, generator=g), "prev_BX": torch.randn(2, H, P, N, generator=g),
+          "angle": torch.randn(2, H, N // 2, generator=g)}
+    params = {k: v.detach().double().cpu().clone().requires_grad_()
+              for k, v in layer.state_dict().items()}
+    xr = x.double().requires_grad_()
+    out_r, _ = ref.layer_step(oracle_cfg(kw), params, xr, {k: v.double() for k, v in st.items()})
+    out_r.square().sum().backward()
+    xd = x.to(cuda_device).requires_grad_()
+    out, _ = layer.step(xd, {k: v.to(cuda_device) for k, v in st.items()})
+    out.square().sum().backward()
+    assert max_rel(xd.grad, xr.grad) < FP32_TOL
+    for name, p in layer.named_parameters():
+        assert max_rel(p.grad, params[name].grad) < FP32_TOL, name
+
+
+def test_lm_step_chain_backpropagates(cuda_device):
+    """Gradients flow through a few chained decode steps of a two-layer LM (state carried from
+    step to step) and are finite; bf16 parameters get bf16 gradients."""
+    torch.manual_seed(0)
+    lm = mamba3_amd.KulaMambaLM(vocab_size=64, d_model=64, n_layers=2, d_state=16, headdim=16,
+                                mimo_rank=2).to(cuda_device, torch.bfloat16).train()
+    states = [blk.ssm.allocate_inference_state(2) for blk in lm.layers]
+    loss = 0.0
+    tok = torch.tensor([3, 5], device=cuda_device)
+    for _ in range(3):
+        x = lm.embedding(tok)
+        for i, blk in enumerate(lm.layers):
+            x, states[i] = blk.step(x, states[i])
+        logits = lm.lm_head(lm.norm(x))
+        loss = loss + logits.float().logsumexp(-1).sum()
+        tok = logits.argmax(-1)
+    loss.backward()
+    for name, p in lm.named_parameters():
+        assert p.grad is not None and p.grad.dtype == p.dtype, name
+        assert torch.isfinite(p.grad.float()).all(), name
