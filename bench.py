@@ -134,7 +134,8 @@ def cpu_model():
 def base_result(args, value, ms_per_step, workload, batch, seq_len, dtype="bf16"):
     return {
         "metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
+        "steps": args.steps, "warmup": args.warmup, "settle_s": SETTLE_S,
+        "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": dtype,
         "data": "synthetic: N(0,1) inputs / uniform ids, seeded random init weights",
         "config": {"workload": workload, "global_batch": batch, "seq_len": seq_len,
@@ -531,11 +532,34 @@ WORKLOADS = {"prefill_d2048": bench_prefill_d2048, "ssd_bwd_d768": bench_ssd_bwd
                                                                     "scan_bwd_d768")}
 
 
-def time_events(torch, fn, steps, warmup):
-    """Warmup, then `steps` calls bracketed by synchronize. Returns (wall seconds, average
-    ms per call from two HIP events on the current stream -- the stream the native entry
-    points launch on -- around the whole timed region, so per-call host gaps are not
-    counted while the launches queue ahead of the GPU)."""
+SETTLE_S = 0.5
+
+
+def settle(torch, fn, seconds):
+    """Run `fn` back to back, untimed, for at least `seconds` of wall time. From idle the
+    chip needs some 50 back-to-back calls of the (8, 8192, 768) prefill (tens of ms) to
+    reach its sustained clock; calls 3-23 average 0.58-0.63 ms, calls 50-400 0.49-0.52 ms.
+    Settling before the warm-up steps makes the timed steps measure the sustained rate
+    whatever --warmup is. Returns the number of calls made."""
+    n = 0
+    if seconds <= 0:
+        return n
+    t_end = time.perf_counter() + seconds
+    while True:
+        for _ in range(8):
+            fn()
+        n += 8
+        torch.cuda.synchronize()
+        if time.perf_counter() >= t_end:
+            return n
+
+
+def time_events(torch, fn, steps, warmup, settle_s=None):
+    """Clock settle, warmup, then `steps` calls bracketed by synchronize. Returns (wall
+    seconds, average ms per call from two HIP events on the current stream -- the stream
+    the native entry points launch on -- around the whole timed region, so per-call host
+    gaps are not counted while the launches queue ahead of the GPU)."""
+    settle(torch, fn, SETTLE_S if settle_s is None else settle_s)
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -599,13 +623,16 @@ def cpu_baseline(torch, layer_sd, x_cpu, dec_inputs):
 
 
 def main() -> int:
+    global SETTLE_S
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    # Back to back, the chip takes some 50 calls (tens of ms) to reach its steady clock:
-    # at (8, 8192, 768) calls 3-23 average 0.63 ms and calls 50-400 0.52 ms. The default
-    # warmup covers that ramp, so the timed steps measure the sustained rate.
+    # The clock settle before each measurement (--settle-s) covers the chip's clock ramp;
+    # the warm-up steps come after it.
     ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--settle-s", type=float, default=SETTLE_S,
+                    help="untimed back-to-back calls, in seconds of wall time, before each "
+                         "measurement's warm-up steps (clock settle)")
     ap.add_argument("--decode-steps", type=int, default=200)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", default="prefill_d768",
@@ -615,6 +642,7 @@ def main() -> int:
                     help="also run one 256 MiB device-to-device copy (the known-size kernel that "
                          "scales FETCH_SIZE / WRITE_SIZE in rocprofv3 --pmc runs)")
     args = ap.parse_args()
+    SETTLE_S = args.settle_s
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1"}))
         return 2
@@ -707,6 +735,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle_s": SETTLE_S,
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True,
         "scaling": "weak",

@@ -265,9 +265,17 @@ def zero_state(cfg: LayerCfg, batch: int, dtype=torch.float32) -> dict:
 
 def layer_step(cfg: LayerCfg, p: dict, x_tok: torch.Tensor, state: dict, dt_scale=None):
     """mamba3/mamba3.py:267-322 for x_tok (B, d_model). Returns (out (B,d_model), state)."""
-    H, P, N, R = cfg.H, cfg.headdim, cfg.d_state, cfg.mimo_rank
-    Bat = x_tok.shape[0]
     proj = F.linear(x_tok, p["in_proj.weight"], p.get("in_proj.bias"))
+    y, new_state = layer_step_core(cfg, p, proj, state, dt_scale)
+    out = F.linear(y, p["out_proj.weight"], p.get("out_proj.bias"))
+    return out, new_state
+
+
+def layer_step_core(cfg: LayerCfg, p: dict, proj: torch.Tensor, state: dict, dt_scale=None):
+    """The step between in_proj and out_proj (mamba3/mamba3.py:275-317): in_proj output
+    proj (B, W) -> (gated activation (B, d_inner) that feeds out_proj, new state)."""
+    H, P, N, R = cfg.H, cfg.headdim, cfg.d_state, cfg.mimo_rank
+    Bat = proj.shape[0]
     z, xf, Bf, Cf, dt_raw, lam_raw, theta = split_proj(cfg, proj)
     dt = F.softplus(dt_raw + p["dt_bias"])
     if dt_scale is not None:
@@ -296,11 +304,10 @@ def layer_step(cfg: LayerCfg, p: dict, x_tok: torch.Tensor, state: dict, dt_scal
     h = (dA[:, :, None, None].float() * state["h"].float()
          + gamma[:, :, None, None].float() * cur.float()
          + beta[:, :, None, None].float() * state["prev_BX"].float())
-    y_r = torch.einsum("bhnr,bhpn->bhpr", Ct.float(), h).to(x_tok.dtype) + p["D"][None, :, None, None] * x_r
+    y_r = torch.einsum("bhnr,bhpn->bhpr", Ct.float(), h).to(proj.dtype) + p["D"][None, :, None, None] * x_r
     z_r = z.reshape(Bat, H, P).unsqueeze(-1) * p["mimo_z"][None]
     y = ((y_r * F.silu(z_r)) * p["mimo_down"][None]).sum(dim=-1).reshape(Bat, cfg.d_inner)
-    out = F.linear(y, p["out_proj.weight"], p.get("out_proj.bias"))
-    return out, {"h": h, "angle": angle, "prev_BX": cur.float()}
+    return y, {"h": h, "angle": angle, "prev_BX": cur.float()}
 
 
 def _block_sub(p: dict, prefix: str) -> dict:

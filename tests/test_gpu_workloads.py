@@ -35,25 +35,38 @@ def _l2(a: torch.Tensor, b: torch.Tensor) -> float:
     return ((a - b).norm() / b.norm()).item()
 
 
+def _layer_params(block) -> dict:
+    return {k: v.detach().float().cpu() for k, v in block.ssm.state_dict().items()}
+
+
+def _state_err(got: dict, want: dict) -> dict:
+    return {k: max_rel(got[k], want[k]) for k in ("h", "prev_BX", "angle")}
+
+
 def test_lm_d768_24_layers_prefill_and_greedy_decode(cuda_device):
     """KulaMambaLM(32000, 768, n_layers=24, d_state=128, headdim=64, mimo_rank=2,
     residual_scale='depth') in bf16, seed 0; ids (4, 2048) uniform from seed 5
     (mamba3/block.py:110-231).
 
-    * Teacher-forced logits of batch row 0 at positions 0..255 against the oracle's
-      24-block forward of ids[0, :256] in fp32 on the bf16-rounded weights.
-    * generate(256, temperature=0): finite logits; the captured decode graph and the eager
-      step loop give the same tokens.
-    * Every decode step's logits, teacher-forced on the generated tokens from the GPU's
-      prefilled states, against the oracle's 24-block step chain from the same states.
-      The oracle's own greedy choice is reported, not gated (bf16 argmax near-ties).
-
-    Tolerance: the whole model runs in bf16 (residual stream, norms, projections, MLP), and
-    the reference's own algorithm run in bf16 is itself 4.3-4.6e-2 (prefill logits) and
-    ~2e-2 (decode steps) away from fp32 here, so 2e-2 on 24-layer logits is out of reach
-    for any bf16 execution. Each check therefore passes at max(2e-2, the error of the
-    oracle run in bf16 on the same inputs, with an fp32 angle state like this build's);
-    the normwise L2 error of the prefill logits is reported."""
+    The hot path is checked layer by layer at the fixed 2e-2 (normwise max-relative
+    against the fp32 oracle on the same bf16 in_proj output), on the activations the
+    model itself produces:
+    * prefill: for each of the 24 blocks, the in_proj output of the GPU's own ssm_norm of
+      the block input; the native SSD core (`ssd_from_proj`) on batch row 0, positions
+      [:256], against `layer_core` (mamba3/mamba3.py:199-256): y, h, prev_BX and angle;
+      and row 0 [:256] of the same core run over the whole (4, 2048) batch against the
+      same y (a different work plan);
+    * decode: the first 32 steps of the teacher-forced decode, each block's step kernel
+      (`_step_from_proj`) from the GPU's own incoming state against `layer_step_core`
+      (mamba3/mamba3.py:275-317) from the same state: y, h, prev_BX and angle.
+    End to end (reported; a fixed bound catches gross errors only): teacher-forced logits
+    of row 0 [:256] against the oracle's 24-block forward, and every decode step's logits
+    from the GPU's prefilled states against the oracle's step chain. The whole model runs
+    in bf16 (residual stream, norms, projections, MLP): the reference's own algorithm run
+    in bf16 on the same inputs is itself ~4.3e-2 (prefill logits) from fp32, so the
+    end-to-end figures say little about the hot path and carry a 6e-2 bound. generate(256,
+    temperature=0): the captured decode graph and the eager step loop give the same
+    tokens; the oracle's own greedy choice is reported (bf16 argmax near-ties)."""
     dev = cuda_device
     torch.manual_seed(0)
     lm = mamba3_amd.KulaMambaLM(32000, 768, n_layers=24, d_state=128, headdim=64, mimo_rank=2,
@@ -62,22 +75,45 @@ def test_lm_d768_24_layers_prefill_and_greedy_decode(cuda_device):
     p = {k: v.detach().float().cpu() for k, v in lm.state_dict().items()}
     p16 = {k: v.detach().cpu() for k, v in lm.state_dict().items()}
     cfg = ref.LayerCfg(d_model=768, d_state=128, headdim=64, mimo_rank=2)
+    W = 3696  # d_in_proj
     scale = 1.0 / math.sqrt(2 * 24)
     torch.manual_seed(5)
     ids = torch.randint(0, 32000, (4, 2048))
     ids_d = ids.to(dev)
 
+    # ---- prefill, layer by layer (the LM's own blocks, in order)
+    worst_layer = {"y": 0.0, "y_full": 0.0, "h": 0.0, "prev_BX": 0.0, "angle": 0.0}
     with torch.no_grad():
+        x = lm.embedding(ids_d)
+        states = []
+        for j, block in enumerate(lm.layers):
+            proj = block.ssm._in_proj_wide(block.ssm_norm(x))
+            y_full, _ = block.ssm.ssd_from_proj(proj)
+            y, st = block.ssm.ssd_from_proj(proj[0:1, :256], return_state=True)
+            y_ref, st_ref = ref.layer_core(cfg, _layer_params(block),
+                                           proj[0:1, :256, :W].float().cpu(), return_state=True)
+            errs = {"y": max_rel(y, y_ref), "y_full": max_rel(y_full[0:1, :256], y_ref),
+                    **_state_err(st, st_ref)}
+            print(f"cfg4 prefill block {j}: " + ", ".join(f"{k} {v:.2e}" for k, v in errs.items()),
+                  flush=True)
+            for k, v in errs.items():
+                assert v < BF16_TOL, (j, k, v)
+                worst_layer[k] = max(worst_layer[k], v)
+            del proj, y_full
+            x, st_full = block.prefill(x)
+            states.append(st_full)
         logits = lm(ids_d)["logits"]
         assert torch.isfinite(logits).all()
         row0 = logits[0:1, :256].float().cpu()
         del logits
         want = ref.lm_forward(cfg, p, ids[0:1, :256], 24, scale)
         want16 = ref.lm_forward(cfg, p16, ids[0:1, :256], 24, scale)
+    print("cfg4 prefill, worst over the 24 blocks: "
+          + ", ".join(f"{k} {v:.2e}" for k, v in worst_layer.items()), flush=True)
     err, err16 = max_rel(row0, want), max_rel(want16, want)
     print(f"cfg4 prefill logits row 0 [:256]: max-rel {err:.3e} (oracle in bf16: {err16:.3e}), "
           f"L2 {_l2(row0, want):.3e} (oracle in bf16: {_l2(want16, want):.3e})", flush=True)
-    assert err < max(BF16_TOL, err16)
+    assert err < 6e-2
 
     n_new = 256
     with torch.no_grad():
@@ -90,13 +126,10 @@ def test_lm_d768_24_layers_prefill_and_greedy_decode(cuda_device):
     assert torch.equal(graphed, eager)
     gen = graphed[:, 2048:].cpu()
 
-    # Teacher-forced decode from the GPU's prefilled states.
+    # ---- teacher-forced decode from the GPU's prefilled states
+    n_layer_steps = 32
+    worst_step = {"y": 0.0, "h": 0.0, "prev_BX": 0.0, "angle": 0.0}
     with torch.no_grad():
-        x = lm.embedding(ids_d)
-        states = []
-        for layer in lm.layers:
-            x, st = layer.prefill(x)
-            states.append(st)
         first = lm.lm_head(lm.norm(x[:, -1])).float()
         assert torch.equal(first.argmax(-1).cpu(), gen[:, 0])
         st_ref = [{k: v.float().cpu() for k, v in st.items()} for st in states]
@@ -107,8 +140,18 @@ def test_lm_d768_24_layers_prefill_and_greedy_decode(cuda_device):
         for i in range(n_new - 1):
             tok = gen[:, i]
             xe = lm.embedding(tok.to(dev))
-            for j, layer in enumerate(lm.layers):
-                xe, states[j] = layer.step(xe, states[j])
+            for j, block in enumerate(lm.layers):
+                if i < n_layer_steps:
+                    proj = block.ssm.in_proj(block.ssm_norm(xe))
+                    y, st = block.ssm._step_from_proj(proj, states[j])
+                    y_ref, st_r = ref.layer_step_core(
+                        cfg, _layer_params(block), proj.float().cpu(),
+                        {k: v.float().cpu() for k, v in states[j].items()})
+                    errs = {"y": max_rel(y, y_ref), **_state_err(st, st_r)}
+                    for k, v in errs.items():
+                        assert v < BF16_TOL, (i, j, k, v)
+                        worst_step[k] = max(worst_step[k], v)
+                xe, states[j] = block.step(xe, states[j])
             got = lm.lm_head(lm.norm(xe)).float().cpu()
             assert torch.isfinite(got).all()
             want, st_ref = ref.lm_step(cfg, p, tok, st_ref, scale)
@@ -116,10 +159,12 @@ def test_lm_d768_24_layers_prefill_and_greedy_decode(cuda_device):
             worst = max(worst, max_rel(got, want))
             worst16 = max(worst16, max_rel(want16, want))
             agree += int((want.argmax(-1) == gen[:, i + 1]).sum())
+    print(f"cfg4 decode, worst over {n_layer_steps} steps x 24 blocks: "
+          + ", ".join(f"{k} {v:.2e}" for k, v in worst_step.items()), flush=True)
     total = 4 * (n_new - 1)
     print(f"cfg4 decode: worst step logits max-rel {worst:.3e} (oracle in bf16: {worst16:.3e}); "
           f"oracle greedy agrees on {agree}/{total} tokens", flush=True)
-    assert worst < max(BF16_TOL, worst16)
+    assert worst < 6e-2
 
 
 @pytest.mark.parametrize("B,T,split", [(8, 512, False), (2, 1200, True), (8, 1500, True), (6, 1580, True)])

@@ -361,3 +361,44 @@ def test_oracle_lm_steps_equal_parallel_logits():
         for t in range(5, ids.shape[1]):
             logits, states = ref.lm_step(cfg, p, ids[:, t], states, scale)
             assert max_rel(logits, full[:, t]) < TOL, t
+
+
+def test_oracle_step_dt_scale_equals_reference_forward():
+    """The step's dt_scale branch (mamba3/mamba3.py:278-282): one layer_step per token with
+    that token's dt_scale, from a zero state, reproduces the reference-written forward
+    output under the same per-token dt_scale, and the fp64 recurrence's final state.
+    Applying dt_scale to the decay dA alone (the angle and the trapezoid weights left
+    unscaled) must break the outputs; that slip is emulated exactly by the oracle step
+    without dt_scale on a layer whose A_log is shifted by log(dt_scale) for each token."""
+    g, cfg, p, x = _run_layer_case("layer_tiny_dtscale")
+    s = torch.from_numpy(g["dt_scale"])
+    want = torch.from_numpy(g["y"])
+    T = x.shape[1]
+    with torch.no_grad():
+        st = ref.zero_state(cfg, x.shape[0])
+        outs = []
+        for t in range(T):
+            o, st = ref.layer_step(cfg, p, x[:, t], st, dt_scale=s[:, t])
+            outs.append(o)
+        got = torch.stack(outs, 1)
+        assert max_rel(got, want) < 1e-4
+        proj = F.linear(x, p["in_proj.weight"])
+        _, st64 = rec.layer_core_recurrent(cfg, p, proj, dt_scale=s)
+        for k in ("h", "angle", "prev_BX"):
+            assert max_rel(st[k], st64[k]) < 1e-5, k
+        # planted slip: dt_scale on dA only (batch row 0; the shift is per head)
+        st = ref.zero_state(cfg, 1)
+        bad = []
+        for t in range(T):
+            pt = dict(p)
+            pt["A_log"] = p["A_log"] + torch.log(s[0, t])
+            o, st = ref.layer_step(cfg, pt, x[0:1, t], st)
+            bad.append(o)
+        assert max_rel(torch.stack(bad, 1), want[0:1]) > 1e-2
+        # and dt_scale dropped altogether
+        st = ref.zero_state(cfg, x.shape[0])
+        drop = []
+        for t in range(T):
+            o, st = ref.layer_step(cfg, p, x[:, t], st)
+            drop.append(o)
+        assert max_rel(torch.stack(drop, 1), want) > 1e-2
