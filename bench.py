@@ -677,6 +677,18 @@ def main() -> int:
         wall, kern_ms = time_events(torch, lambda: layer.ssd_from_proj(proj, return_state=True),
                                     args.steps, args.warmup)
         ms_per_step = wall * 1e3 / args.steps
+        # The same call on a checkpoint whose B/C norm weights, biases and mimo_x are 32x
+        # larger (B^ row bound ~720 against the f16 operand limit 128): the kernels bring
+        # the operands into range by power-of-two scales, so it runs on the same kernels.
+        import copy
+        big = copy.deepcopy(layer)
+        for name in ("B_norm.weight", "C_norm.weight", "B_bias", "C_bias", "mimo_x"):
+            big.get_parameter(name).mul_(32.0)
+        big_desc = big._desc(BATCH, SEQLEN, proj)
+        big_kernel = _native.prefill_kernel_name(big_desc, proj)
+        _, big_ms = time_events(torch, lambda: big.ssd_from_proj(proj, return_state=True),
+                                max(5, args.steps // 2), args.warmup)
+        del big
         _, layer_ms = time_events(torch, lambda: layer.prefill(x), max(3, args.steps // 4), 1)
         # the layer's two GEMMs alone, on the shapes the prefill runs them at
         y_in = torch.randn(BATCH, SEQLEN, layer.d_inner, device=dev).to(torch.bfloat16)
@@ -753,6 +765,8 @@ def main() -> int:
                      "traffic_source": traffic_source(TRAFFIC_FILE),
                      "kernel": "native SSD prefill (all launches of m3_prefill_fwd)",
                      "algorithmic_flops": flops, "avg_ms": round(kern_ms, 4)},
+        "large_params_x32": {"kernel": big_kernel, "avg_ms": round(big_ms, 4),
+                             "ratio_to_default": round(big_ms / kern_ms, 3)},
         "whole_layer_prefill_tok_s": round(tokens / (layer_ms * 1e-3), 1),
         "whole_layer": whole_layer_line(tokens, layer_ms, in_ms, out_ms, kern_ms, flops,
                                         D_MODEL, layer.in_proj.out_features, layer.d_inner),

@@ -64,12 +64,14 @@ typedef struct m3_layer_desc {
     int32_t flags;            /* M3_FLAG_* bits (0 by default) */
 } m3_layer_desc;
 
-/* The bf16 MFMA prefill kernels hold these as f16 MFMA operands: the normalised B^ / C^
- * values (|v| <= sqrt(N R) max|w| + max|bias|), x * mimo_x, the decay-masked scores
- * C~.B~ * exp(c_t - c_u) (a_u + b_u) and the state copy h / 256, each below 65504 in
- * magnitude. A caller whose parameters may break that (e.g. large B/C norm weights or
- * biases, or mimo_x, in a trained checkpoint) sets this flag: such layers then run on the
- * fp32 generic kernel, which has no such range limit. */
+/* The bf16 MFMA prefill kernels hold the normalised B^ / C^ values, x * mimo_x, the
+ * decay-masked scores and a copy of the state as f16 MFMA operands. They bring large
+ * parameters into the f16 range themselves: B^, C^ and x * mimo_x are held divided by
+ * powers of two derived from the parameters (one rank's B^ row norm sqrt(N R) max|w| +
+ * sqrt(N) max|bias| to at most 128, |mimo_x| to at most 256) and the fp32 epilogues undo
+ * them, so any checkpoint runs on them. Left to the caller: activations of ordinary size
+ * (|x * mimo_x| / 2^k below 65504, dt below ~4). This flag forces the fp32 generic kernel
+ * instead (VALU, about 100x slower), for callers that want no f16 operand at all. */
 #define M3_FLAG_NO_F16_OPERANDS 1
 /* fp32 layers: m3_prefill_fwd keeps the intermediates m3_layer_bwd differentiates through in
  * its workspace (the fp32 layer workspace; for d_state 128, headdim 64, mimo_rank 2 the fused
@@ -113,8 +115,19 @@ typedef struct m3_layer_param_grads {
 
 const char* m3_status_string(int status);
 
-/* Library version as major*10000 + minor*100 + patch. */
+/* Library version as major*10000 + minor*100 + patch. 0.2.0 (200): m3_layer_param_grads
+ * gained its dt_scale field and m3_prefill_kernel_name was added; 0.1.0 (100) had neither. */
 int m3_version(void);
+
+/*
+ * Name of the prefill kernel m3_prefill_fwd would run for these arguments (the dispatch
+ * depends on the shape, dtype, flags and the pointers' alignment): "mfma_d128_p64_r2",
+ * "mfma_general", "fp32_fused", "fp32_fused_train", "fp32_layer" or "generic"; NULL for an
+ * invalid descriptor. No counterpart in the reference (one ATen path). A static string.
+ */
+const char* m3_prefill_kernel_name(const m3_layer_desc* desc, const void* proj,
+                                   const void* y_out, const float* h_final,
+                                   const float* prev_bx);
 
 /*
  * Inter-chunk state scan. Replaces the reference's native `scan_forward`
@@ -200,7 +213,8 @@ int m3_prefill_fwd(const m3_layer_desc* desc, const m3_layer_params* params,
  * m3_prefill_fwd, but the workspace is a static array of the library on each GPU
  * (M3_NOALLOC_SCRATCH_BYTES, held from the first call on that GPU until the process
  * ends); calls needing more return M3_ERR_SCRATCH_LIMIT and launch nothing. It calls no
- * allocator. The scratch keeps the last call's contents and needs no clearing (every
+ * allocator. M3_FLAG_FOR_BACKWARD is refused (M3_ERR_UNSUPPORTED): the backward's operands
+ * would be left in the shared scratch, which the next call overwrites. The scratch keeps the last call's contents and needs no clearing (every
  * kernel writes what it later reads). All calls on one GPU share the array: calls that
  * overlap in time on one GPU (other streams or threads) race and must be serialised by
  * the caller.

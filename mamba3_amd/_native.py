@@ -45,6 +45,7 @@ EXPORTED_SYMBOLS = (
     "m3_silu_mul",
     "m3_step_bwd_workspace_size",
     "m3_step_bwd",
+    "m3_prefill_kernel_name",
 )
 
 M3_ERR_SCRATCH_LIMIT = 8
@@ -107,6 +108,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.m3_scan_bwd.restype = ctypes.c_int
     lib.m3_scan_bwd.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t,
                                 _i64, _i64, _i64, _i64, _vp]
+    lib.m3_prefill_kernel_name.restype = ctypes.c_char_p
+    lib.m3_prefill_kernel_name.argtypes = [ctypes.POINTER(LayerDesc), _vp, _vp, _vp, _vp]
     lib.m3_prefill_workspace_size.restype = ctypes.c_int
     lib.m3_prefill_workspace_size.argtypes = [ctypes.POINTER(LayerDesc),
                                               ctypes.POINTER(ctypes.c_size_t)]
@@ -227,6 +230,15 @@ def prefill_workspace_bytes(desc: LayerDesc) -> int:
     check(lib().m3_prefill_workspace_size(ctypes.byref(desc), ctypes.byref(n)),
           "m3_prefill_workspace_size")
     return n.value
+
+
+def prefill_kernel_name(desc: LayerDesc, proj=None, y_out=None, h_final=None, prev_bx=None) -> str:
+    """Name of the prefill kernel m3_prefill_fwd runs for these arguments."""
+    name = lib().m3_prefill_kernel_name(ctypes.byref(desc), ptr(proj), ptr(y_out), ptr(h_final),
+                                        ptr(prev_bx))
+    if name is None:
+        raise NativeError("m3_prefill_kernel_name: invalid layer descriptor")
+    return name.decode()
 
 
 def prefill_fwd(desc: LayerDesc, params: LayerParams, proj, dt_scale, y_out, h_final, angle,

@@ -52,7 +52,9 @@ int check_scan_bwd_shape(int64_t batch, int64_t nchunks, int64_t nheads, int64_t
 // Which prefill kernel a call dispatches to: the d_state 128 / headdim 64 / rank 2 MFMA
 // kernel (bf16, aligned rows, 16-byte aligned proj / y_out), the general MFMA kernel
 // (bf16, d_state 64/128/256, rank 1/2/4, headdim % 32 == 0, 16-byte aligned h_final) --
-// both with f16 operands, so not under M3_FLAG_NO_F16_OPERANDS -- the fused fp32 kernel
+// both with f16 operands (scaled by powers of two for large parameters), so not under
+// M3_FLAG_NO_F16_OPERANDS, which a caller may set to force the generic fp32 kernel -- the
+// fused fp32 kernel
 // (fp32, d_state 128 / headdim 64 / rank 2; under M3_FLAG_FOR_BACKWARD it also writes the
 // staged operands of the layer backward into the fp32 layer workspace), the fp32 layer path
 // on the fp32-MFMA chunk kernels (fp32, rank 1/2/4/8) or the generic one.
@@ -177,7 +179,20 @@ const char* m3_status_string(int status) {
     }
 }
 
-int m3_version(void) { return 100; }
+int m3_version(void) { return 200; }
+
+const char* m3_prefill_kernel_name(const m3_layer_desc* desc, const void* proj, const void* y_out,
+                                   const float* h_final, const float* prev_bx) {
+    if (check_desc(desc) != M3_OK) return nullptr;
+    switch (prefill_path(*desc, proj, y_out, h_final, prev_bx)) {
+        case PrefillPath::kMfma: return "mfma_d128_p64_r2";
+        case PrefillPath::kWide: return "mfma_general";
+        case PrefillPath::kFp32Fused: return "fp32_fused";
+        case PrefillPath::kFp32FusedTrain: return "fp32_fused_train";
+        case PrefillPath::kFp32: return "fp32_layer";
+        default: return "generic";
+    }
+}
 
 int m3_scan_fwd(const float* decay, const float* h_chunk, const float* h_init,
                 float* h_states, int64_t batch, int64_t nchunks, int64_t nheads, int64_t pn,
@@ -255,6 +270,9 @@ int m3_prefill_fwd_noalloc(const m3_layer_desc* desc, const m3_layer_params* par
                            float* angle, float* prev_bx, void* stream) {
     int st = check_prefill_args(desc, params, proj, y_out);
     if (st != M3_OK) return st;
+    // The backward's operands would land in the shared scratch, which the next call
+    // overwrites and no caller can hand to m3_layer_bwd.
+    if (desc->flags & M3_FLAG_FOR_BACKWARD) return M3_ERR_UNSUPPORTED;
     const PrefillPath path = prefill_path(*desc, proj, y_out, h_final, prev_bx);
     const size_t need = prefill_path_workspace(*desc, path);
     if (need > M3_NOALLOC_SCRATCH_BYTES) return M3_ERR_SCRATCH_LIMIT;

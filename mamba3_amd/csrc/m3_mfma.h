@@ -3,6 +3,7 @@
 #pragma once
 
 #include "m3_common.h"
+#include "mamba3_amd.h"
 
 namespace m3 {
 
@@ -133,6 +134,99 @@ __device__ __forceinline__ u32x2 ld_b64(__amdgpu_buffer_rsrc_t r, int off_elems)
 
 __device__ __forceinline__ f16x8 cat8(const f16x4& lo, const f16x4& hi) {
     return f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// ---- power-of-two scales of the f16 MFMA operands
+// The bf16 prefill kernels hold the normalised B^ / C^ values, x * mimo_x, the decay-masked
+// scores and a copy of the state as f16 operands. A layer whose parameters would take them
+// past the f16 range holds B^ / sB, C^ / sC and x * mimo_x / sX instead, each s the least
+// power of two >= 1 that brings the parameter bound below its limit; scaling by a power of
+// two changes no mantissa bit, and with every s = 1 the arithmetic is the unscaled one.
+// The fp32 epilogues undo the scales: y by sB sC sX (folded into mimo_down), the skip term
+// D enters the scores divided by sB sC, and the state (carried as h / (sB sX)) is
+// multiplied back by sB sX where it leaves the kernel (final state, prev_BX).
+//
+// Bound of one rank's B^ row (N values): the RMS-normalised row over N R values has norm
+// sqrt(N R), so the row of w * v + bias has norm at most sqrt(N R) max|w| + sqrt(N) max|bias|.
+// Limit 128 keeps every score |C~ . B~| <= 16384 before the decay mask; mimo_x is brought to
+// |mimo_x| / sX <= 256 (x * mimo_x / sX below 65504 for |x| < 256). bc_norm and the chunk
+// kernels evaluate the same expressions on the same parameters, so they agree bit for bit.
+constexpr float kBcRowLimit = 128.f;
+constexpr float kMimoXLimit = 256.f;
+
+// Least power of two s >= 1 with bound <= limit * s (limit a power of two; a non-finite
+// bound gets 2^100).
+__device__ __forceinline__ float f16_down_scale(float bound, float limit) {
+    const float q = fminf(bound * (1.f / limit), 0x1p100f);  // fminf(NaN, c) = c
+    if (!(q > 1.f)) return 1.f;
+    int e;
+    const float m = frexpf(q, &e);  // q = m 2^e, m in [0.5, 1)
+    return ldexpf(1.f, m == 0.5f ? e - 1 : e);
+}
+
+template <int N, int R>
+__device__ __forceinline__ float bc_row_scale(float max_w, float max_bias) {
+    const float bound = __builtin_fmaf(__builtin_sqrtf((float)(N * R)), max_w,
+                                       __builtin_sqrtf((float)N) * max_bias);
+    return f16_down_scale(bound, kBcRowLimit);
+}
+
+// Max over the 64 lanes of a wave (every lane gets it, the same value): DPP permutations
+// inside each 16-lane row (swap neighbours, swap pairs, half-row and row mirrors), then
+// the four row maxima through readlane. No LDS traffic.
+__device__ __forceinline__ float wave_max(float v) {
+    auto dpp = [](float x, auto ctrl) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x),
+                                                                     decltype(ctrl)::value, 0xF, 0xF, false));
+    };
+    v = fmaxf(v, dpp(v, std::integral_constant<int, 0xB1>{}));
+    v = fmaxf(v, dpp(v, std::integral_constant<int, 0x4E>{}));
+    v = fmaxf(v, dpp(v, std::integral_constant<int, 0x141>{}));
+    v = fmaxf(v, dpp(v, std::integral_constant<int, 0x140>{}));
+    auto rl = [&](int l) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l)); };
+    return fmaxf(fmaxf(rl(0), rl(16)), fmaxf(rl(32), rl(48)));
+}
+
+// max |p[i]| over i < n, by one wave (every lane gets it).
+__device__ __forceinline__ float wave_absmax(const float* p, int n, int lane) {
+    float m = 0.f;
+    for (int i = lane; i < n; i += kWave) m = fmaxf(m, fabsf(p[i]));
+    return wave_max(m);
+}
+
+__device__ __forceinline__ float uniform(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
+}
+
+// The scales of one (group, head) of a layer, by one wave.
+struct F16Scales {
+    float inv_x;   // 1 / sX: multiplies mimo_x in the X operands
+    float inv_bc;  // 1 / (sB sC): multiplies D in the scores
+    float out;     // sB sC sX: multiplies y
+    float state;   // sB sX: multiplies the state where it leaves the kernel
+    // the same values held in scalar registers (read from LDS by every lane)
+    __device__ __forceinline__ F16Scales in_sgprs() const {
+        return F16Scales{uniform(inv_x), uniform(inv_bc), uniform(out), uniform(state)};
+    }
+};
+
+// sX of head h alone (its x * mimo_x operands): the state-only pass needs nothing else.
+template <int R>
+__device__ __forceinline__ float mimo_x_scale(const m3_layer_params& prm, int h, int P, int lane) {
+    return f16_down_scale(wave_absmax(prm.mimo_x + (int64_t)h * P * R, P * R, lane), kMimoXLimit);
+}
+
+template <int N, int R>
+__device__ __forceinline__ F16Scales layer_f16_scales(const m3_layer_params& prm, int grp, int h,
+                                                      int P, int lane) {
+    const float mwb = wave_absmax(prm.B_norm_w, N * R, lane);
+    const float mwc = wave_absmax(prm.C_norm_w, N * R, lane);
+    const float mbb = wave_absmax(prm.B_bias + (int64_t)grp * N * R, N * R, lane);
+    const float mbc = wave_absmax(prm.C_bias + (int64_t)grp * N * R, N * R, lane);
+    const float mx = wave_absmax(prm.mimo_x + (int64_t)h * P * R, P * R, lane);
+    const float sb = bc_row_scale<N, R>(mwb, mbb), sc = bc_row_scale<N, R>(mwc, mbc);
+    const float sx = f16_down_scale(mx, kMimoXLimit);
+    return F16Scales{1.f / sx, 1.f / (sb * sc), sb * sc * sx, sb * sx};
 }
 
 }  // namespace m3

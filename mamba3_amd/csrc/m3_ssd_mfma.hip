@@ -97,6 +97,7 @@ struct __align__(16) Smem {
                               // chunk parity.
     Tok tok[NSLOT];
     float rot[NH];            // per-pair angle scratch (prologue / epilogue)
+    F16Scales scl;            // operand scales of the (group, head)
     f32x4 mzd[P];             // per p: -mimo_z[0] log2e, -mimo_z[1] log2e, mimo_down*mimo_z [0], [1]
     f16 mxT[R][P];            // mimo_x per rank and p
 };
@@ -192,10 +193,27 @@ __device__ __forceinline__ void bc_norm_rows(const BcRows& c, int64_t l0, int la
     }
     const f32x4 wb4 = *reinterpret_cast<const f32x4*>(c.wB + e);
     const f32x4 wc4 = *reinterpret_cast<const f32x4*>(c.wC + e);
+    auto absmax4 = [](f32x4 v) { return fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))); };
+    // Operand scales of a group (1 unless the parameters are large): those of the first
+    // row's group, recomputed for a row of another group (a scalar branch: a row is one
+    // wave's).
+    const float mwb = wave_max(absmax4(wb4)), mwc = wave_max(absmax4(wc4));
+    auto scales_of = [&](int g, float& ib, float& ic) {
+        const f32x4 bb4 = *reinterpret_cast<const f32x4*>(c.biasB + (int64_t)g * NR + e);
+        const f32x4 bc4 = *reinterpret_cast<const f32x4*>(c.biasC + (int64_t)g * NR + e);
+        ib = 1.f / bc_row_scale<N, R>(mwb, wave_max(absmax4(bb4)));
+        ic = 1.f / bc_row_scale<N, R>(mwc, wave_max(absmax4(bc4)));
+    };
+    const int g0 = __builtin_amdgcn_readfirstlane(gg[0]);
+    float ib0, ic0;
+    scales_of(g0, ib0, ic0);
 #pragma unroll
     for (int k = 0; k < KR; ++k) {
         const f32x4 bb4 = *reinterpret_cast<const f32x4*>(c.biasB + (int64_t)gg[k] * NR + e);
         const f32x4 bc4 = *reinterpret_cast<const f32x4*>(c.biasC + (int64_t)gg[k] * NR + e);
+        float ib = ib0, ic = ic0;
+        const int gk = __builtin_amdgcn_readfirstlane(gg[k]);
+        if (gk != g0) scales_of(gk, ib, ic);
         float b[4], cc[4], sb = 0.f, sc = 0.f;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -210,8 +228,8 @@ __device__ __forceinline__ void bc_norm_rows(const BcRows& c, int64_t l0, int la
         float ob[4], oc[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            ob[j] = b[j] * rb * wb4[j] + bb4[j];
-            oc[j] = cc[j] * rc * wc4[j] + bc4[j];
+            ob[j] = (b[j] * rb * wb4[j] + bb4[j]) * ib;
+            oc[j] = (cc[j] * rc * wc4[j] + bc4[j]) * ic;
         }
         // pair-packed: (e_r0, o_r0, e_r1, o_r1)
         if (l0 + k < c.nrows) {
@@ -442,18 +460,27 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
     const int bnrs = a.G * NR;  // elements between tokens in Bn / Cn
 
     const float A2 = -__expf(a.prm.A_log[h]) * kLog2e;
-    const float D_h = a.prm.D[h];
     const float dtb = a.prm.dt_bias[h];
 
     const int lane0 = tid & 63;
+    if (wv == 0) {
+        // the state pass only forms X operands (its states stay in the scaled frame)
+        const F16Scales sc = kFull ? layer_f16_scales<N, R>(a.prm, grp, h, P, lane0)
+                                   : F16Scales{1.f / mimo_x_scale<R>(a.prm, h, P, lane0), 1.f, 1.f, 1.f};
+        if (lane0 == 0) sm.scl = sc;
+    }
+    __syncthreads();
+    const F16Scales scl = sm.scl.in_sgprs();
+    // the skip term D enters the masked scores, which carry 1 / (sB sC)
+    const float D_h = a.prm.D[h] * scl.inv_bc;
     if (kFull && tid < P) {
         const float z0 = a.prm.mimo_z[(h * P + tid) * R], z1 = a.prm.mimo_z[(h * P + tid) * R + 1];
-        sm.mzd[tid] = f32x4{-z0 * kLog2e, -z1 * kLog2e, a.prm.mimo_down[(h * P + tid) * R] * z0,
-                            a.prm.mimo_down[(h * P + tid) * R + 1] * z1};
+        sm.mzd[tid] = f32x4{-z0 * kLog2e, -z1 * kLog2e, a.prm.mimo_down[(h * P + tid) * R] * z0 * scl.out,
+                            a.prm.mimo_down[(h * P + tid) * R + 1] * z1 * scl.out};
     }
     if (tid < P) {
-        sm.mxT[0][tid] = (f16)a.prm.mimo_x[(h * P + tid) * R];
-        sm.mxT[1][tid] = (f16)a.prm.mimo_x[(h * P + tid) * R + 1];
+        sm.mxT[0][tid] = (f16)(a.prm.mimo_x[(h * P + tid) * R] * scl.inv_x);
+        sm.mxT[1][tid] = (f16)(a.prm.mimo_x[(h * P + tid) * R + 1] * scl.inv_x);
     }
 
     // State accumulators of the MFMA waves: wave w owns the H^T rows n in [16w, 16w+16),
@@ -718,7 +745,7 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
                 sincosf(sm.rot[n0 / 2 + 1], &s1, &c1);
 #pragma unroll
                 for (int pt = 0; pt < 4; ++pt) {
-                    const f32x4 v = hacc[pt];
+                    const f32x4 v = hacc[pt] * scl.state;
                     const f32x4 o = {v[0] * c0 - v[1] * s0, v[0] * s0 + v[1] * c0,
                                      v[2] * c1 - v[3] * s1, v[2] * s1 + v[3] * c1};
                     *reinterpret_cast<f32x4*>(&hf[(16 * pt + l16) * N + n0]) = o;
@@ -742,7 +769,8 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
                     const int p = 8 * wv + j;
                     const float x0 = (float)sm.X[(K - 1) & 1][2 * ul][xsw(2 * ul, p)];
                     const float x1 = (float)sm.X[(K - 1) & 1][2 * ul + 1][xsw(2 * ul + 1, p)];
-                    *reinterpret_cast<f32x2*>(&pb[p * N + 2 * pp]) = f32x2{ae0 * x0 + ae1 * x1, ao0 * x0 + ao1 * x1};
+                    *reinterpret_cast<f32x2*>(&pb[p * N + 2 * pp]) =
+                        f32x2{ae0 * x0 + ae1 * x1, ao0 * x0 + ao1 * x1} * scl.state;
                 }
             }
         }

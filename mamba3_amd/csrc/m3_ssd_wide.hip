@@ -79,7 +79,8 @@ struct __align__(16) Smem {
     Tok tok[2];           // by chunk parity
     float phi[Q][N / 2];  // RoPE angle of each (token, pair) of the chunk being prepared
     u32x4 th[Q][N / 16];  // theta of that chunk, bf16, 8 pairs per entry
-    float mz[PB][R], md[PB][R], mx[PB][R];  // mimo_z, mimo_down, mimo_x of the block's columns
+    float mz[PB][R], md[PB][R], mx[PB][R];  // mimo_z, mimo_down * sB sC sX, mimo_x / sX of the block's columns
+    F16Scales scl;                          // operand scales of the (group, head)
 };
 
 struct Args {
@@ -146,6 +147,9 @@ __global__ __launch_bounds__(256) void bc_norm_wide(const bf16* __restrict__ pro
     const float rb = rsqrtf(sb * (1.f / NR) + eps), rc = rsqrtf(sc * (1.f / NR) + eps);
     const float* bB = biasB + (int64_t)g * NR;
     const float* bC = biasC + (int64_t)g * NR;
+    // operand scales of the row's group (1 unless the parameters are large)
+    const float ib = 1.f / bc_row_scale<N, R>(wave_absmax(wB, NR, lane), wave_absmax(bB, NR, lane));
+    const float ic = 1.f / bc_row_scale<N, R>(wave_absmax(wC, NR, lane), wave_absmax(bC, NR, lane));
 #pragma unroll
     for (int j = 0; j < PPL; ++j) {
         const int i = lane + 64 * j;
@@ -153,10 +157,10 @@ __global__ __launch_bounds__(256) void bc_norm_wide(const bf16* __restrict__ pro
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const int e0 = 2 * i * R + r, e1 = e0 + R;
-            const f16x2 ob = f16x2{(f16)(vb[j][r] * rb * wB[e0] + bB[e0]),
-                                   (f16)(vb[j][R + r] * rb * wB[e1] + bB[e1])};
-            const f16x2 oc = f16x2{(f16)(vc[j][r] * rc * wC[e0] + bC[e0]),
-                                   (f16)(vc[j][R + r] * rc * wC[e1] + bC[e1])};
+            const f16x2 ob = f16x2{(f16)((vb[j][r] * rb * wB[e0] + bB[e0]) * ib),
+                                   (f16)((vb[j][R + r] * rb * wB[e1] + bB[e1]) * ib)};
+            const f16x2 oc = f16x2{(f16)((vc[j][r] * rc * wC[e0] + bC[e0]) * ic),
+                                   (f16)((vc[j][R + r] * rc * wC[e1] + bC[e1]) * ic)};
             *reinterpret_cast<f16x2*>(Bn + tg * NR + 2 * (i * R + r)) = ob;
             *reinterpret_cast<f16x2*>(Cn + tg * NR + 2 * (i * R + r)) = oc;
         }
@@ -225,8 +229,15 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
     const f16* Cn = a.Cn + (int64_t)b * T * nrs + (int64_t)grp * NR;
     const int nchunks = (T + Q - 1) / Q;
     const float Ah = -expf(a.prm.A_log[h]);
-    const float Dh = a.prm.D[h];
     const float dtb = a.prm.dt_bias[h];
+    if (wave == 0) {
+        const F16Scales sc = layer_f16_scales<N, R>(a.prm, grp, h, a.P, lane);
+        if (lane == 0) sm.scl = sc;
+    }
+    __syncthreads();
+    const F16Scales scl = sm.scl.in_sgprs();
+    // the skip term D enters the masked scores, which carry 1 / (sB sC)
+    const float Dh = a.prm.D[h] * scl.inv_bc;
     const int hp = h * a.P;  // first column of this head in x, z and y
 
     // Waves 0-7: output tile rows 16 tt .. 16 tt + 15, columns 16 pt .. 16 pt + 15 (G3, G2,
@@ -246,8 +257,8 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
         const int c = tid / R, r = tid % R;
         const int64_t e = (int64_t)(hp + p0 + c) * R + r;
         sm.mz[c][r] = a.prm.mimo_z[e];
-        sm.md[c][r] = a.prm.mimo_down[e];
-        sm.mx[c][r] = a.prm.mimo_x[e];
+        sm.md[c][r] = a.prm.mimo_down[e] * scl.out;
+        sm.mx[c][r] = a.prm.mimo_x[e] * scl.inv_x;
     }
     // theta staging jobs: units of 8 pairs of one token.
     constexpr int THU = Q * NH / 8;
@@ -611,7 +622,7 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
             const int jt = wave * TPW + j;
             const int nt = jt >> 1, ptj = jt & 1;
             const int p = p0 + 16 * ptj + l16;
-            *reinterpret_cast<f32x4*>(a.h_final + ((int64_t)bh * a.P + p) * N + 16 * nt + 4 * g16) = hacc[j];
+            *reinterpret_cast<f32x4*>(a.h_final + ((int64_t)bh * a.P + p) * N + 16 * nt + 4 * g16) = hacc[j] * scl.state;
         }
     }
     if (a.angle && pblk == 0 && angle_wave && ai < NH)
@@ -625,7 +636,7 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
             float v = 0.f;
 #pragma unroll
             for (int r = 0; r < R; ++r) v += (float)sm.B[tl * R + r][n] * (float)sm.XT[(nchunks - 1) & 1][p][tl * R + r];
-            a.prev_bx[((int64_t)bh * a.P + p0 + p) * N + n] = v;
+            a.prev_bx[((int64_t)bh * a.P + p0 + p) * N + n] = v * scl.state;
         }
     }
 }

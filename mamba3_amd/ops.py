@@ -16,7 +16,6 @@ source tensor and version.
 
 from __future__ import annotations
 
-import math
 import weakref
 from collections import OrderedDict
 from typing import Optional
@@ -31,19 +30,9 @@ NS = "mamba3_amd"
 _F32_CACHE: "OrderedDict[tuple, list]" = OrderedDict()
 _F32_CACHE_MAX = 256
 
-# Parameter bounds under which the bf16 MFMA prefill kernels keep their f16 operands in
-# range for activations of ordinary size: every rank's normalised B^ / C^ row has norm at
-# most 128 (sqrt(N R) max|w| + sqrt(N) max|bias|, so a score C~.B~ is at most 16384 before
-# the decay mask, which scales it by at most dt), and |mimo_x| <= 256 (x * mimo_x stays
-# below 65504 for |x| < 256). Layers beyond them run with M3_FLAG_NO_F16_OPERANDS.
-F16_ROW_NORM_MAX = 128.0
-F16_MIMO_X_MAX = 256.0
-
-
 def _cache_entry(params) -> list:
-    """[LayerParams, fp32 tensors, weak refs, f16 verdict or None] for the ten layer
-    parameters. An entry is used only while every source tensor is the same live object at
-    the same version."""
+    """[LayerParams, fp32 tensors, weak refs] for the ten layer parameters. An entry is
+    used only while every source tensor is the same live object at the same version."""
     key = tuple((t.data_ptr(), t._version, t.dtype, t.device) for t in params)
     hit = _F32_CACHE.get(key)
     if hit is not None and all(r() is t for r, t in zip(hit[2], params)):
@@ -52,7 +41,7 @@ def _cache_entry(params) -> list:
     with torch.no_grad():
         f32 = [t.detach().float().contiguous() for t in params]
     entry = [_native.LayerParams(*[t.data_ptr() for t in f32]), f32,
-             [weakref.ref(t) for t in params], None]
+             [weakref.ref(t) for t in params]]
     _F32_CACHE[key] = entry
     while len(_F32_CACHE) > _F32_CACHE_MAX:
         _F32_CACHE.popitem(last=False)
@@ -63,21 +52,6 @@ def _f32_params(params) -> tuple:
     """(LayerParams, fp32 tensors) for the ten layer parameters (cached)."""
     entry = _cache_entry(params)
     return entry[0], entry[1]
-
-
-def f16_operands_ok(params, d_state: int, mimo_rank: int) -> bool:
-    """True when the layer's parameters are within F16_ROW_NORM_MAX / F16_MIMO_X_MAX (one
-    host read per parameter version)."""
-    entry = _cache_entry(params)
-    if entry[3] is None:
-        _, _, _, Bw, Cw, Bb, Cb, mx, _, _ = entry[1]
-        with torch.no_grad():
-            nr, n = math.sqrt(d_state * mimo_rank), math.sqrt(d_state)
-            norms = torch.stack([nr * Bw.abs().max() + n * Bb.abs().max(),
-                                 nr * Cw.abs().max() + n * Cb.abs().max()])
-            ok = bool((norms.max() <= F16_ROW_NORM_MAX) & (mx.abs().max() <= F16_MIMO_X_MAX))
-        entry[3] = ok
-    return entry[3]
 
 
 def _desc(batch, seqlen, nheads, headdim, d_state, mimo_rank, ngroups, trap, cplx, eps,
@@ -102,9 +76,7 @@ def prefill(proj: torch.Tensor, A_log: torch.Tensor, D: torch.Tensor, dt_bias: t
             eps: float, return_state: bool) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor,
                                                      torch.Tensor]:
     """m3_prefill_fwd: in_proj output (B,T,W) -> (y (B,T,H*P) in proj.dtype, h, angle,
-    prev_BX). Without return_state the three state tensors are empty. bf16 layers whose
-    parameters exceed the f16 operand bounds (f16_operands_ok) run on the fp32 generic
-    kernel."""
+    prev_BX). Without return_state the three state tensors are empty."""
     _native.require_gpu(proj)
     proj = proj.contiguous()
     Bat, T, _ = proj.shape
@@ -112,8 +84,6 @@ def prefill(proj: torch.Tensor, A_log: torch.Tensor, D: torch.Tensor, dt_bias: t
                  proj.dtype, proj.stride(-2))
     params = (A_log, D, dt_bias, B_norm_w, C_norm_w, B_bias, C_bias, mimo_x, mimo_z, mimo_down)
     pack, _ = _f32_params(params)
-    if proj.dtype != torch.float32 and not f16_operands_ok(params, d_state, mimo_rank):
-        desc.flags |= _native.M3_FLAG_NO_F16_OPERANDS
     dev = proj.device
     y = torch.empty(Bat, T, nheads * headdim, device=dev, dtype=proj.dtype)
     if return_state:

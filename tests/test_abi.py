@@ -42,7 +42,8 @@ def test_status_strings(lib):
     for code in range(1, 8):
         assert lib.m3_status_string(code) != b"unknown status"
     assert lib.m3_status_string(99) == b"unknown status"
-    assert lib.m3_version() >= 100
+    # 0.2.0: m3_layer_param_grads has its dt_scale field, m3_prefill_kernel_name exists
+    assert lib.m3_version() == 200
 
 
 def test_scan_rejects_bad_arguments(lib):
@@ -309,3 +310,58 @@ def test_silu_mul_rejects_bad_arguments(lib):
     assert lib.m3_silu_mul(fake, 0, 8, 16, fake, None) == 2
     assert lib.m3_silu_mul(fake, 4, 8, 15, fake, None) == 2  # the row must hold gate and up
     assert lib.m3_silu_mul(fake, 1 << 30, 1 << 10, 1 << 11, fake, None) == 2  # 32-bit grid
+
+
+def test_ctypes_structs_match_the_header(tmp_path):
+    """sizeof and every field offset of the ctypes mirrors of m3_layer_desc,
+    m3_layer_params and m3_layer_param_grads equal the C header's, compiled with gcc."""
+    import shutil
+    import subprocess
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    structs = {"m3_layer_desc": _native.LayerDesc, "m3_layer_params": _native.LayerParams,
+               "m3_layer_param_grads": _native.LayerParamGrads}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "mamba3_amd.h"',
+             'int main(void) {']
+    for cname, cls in structs.items():
+        lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for field, _ in cls._fields_:
+            lines.append(f'printf("{cname} {field} %zu\\n", offsetof({cname}, {field}));')
+    lines += ["return 0;", "}"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines) + "\n")
+    exe = tmp_path / "layout"
+    subprocess.run([cc, f"-I{ROOT / 'include'}", str(src), "-o", str(exe)], check=True)
+    got = {}
+    for line in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.splitlines():
+        cname, field, val = line.split()
+        got[(cname, field)] = int(val)
+    for cname, cls in structs.items():
+        assert got[(cname, "size")] == ctypes.sizeof(cls), cname
+        for field, _ in cls._fields_:
+            assert got[(cname, field)] == getattr(cls, field).offset, (cname, field)
+
+
+def test_prefill_kernel_name_and_noalloc_refusal(lib):
+    """The dispatch query names the kernel from the descriptor alone (null pointers are
+    aligned); the no-allocation entry refuses M3_FLAG_FOR_BACKWARD before any launch."""
+    def desc(**kw):
+        d = dict(batch=2, seqlen=64, nheads=24, headdim=64, d_state=128, mimo_rank=2, ngroups=1,
+                 use_trapezoidal=1, use_complex=1, dtype=1, proj_row_stride=3696, rms_eps=1e-5,
+                 flags=0)
+        d.update(kw)
+        return _native.LayerDesc(**d)
+    name = lambda d: lib.m3_prefill_kernel_name(ctypes.byref(d), None, None, None, None)
+    assert name(desc()) == b"mfma_d128_p64_r2"
+    assert name(desc(flags=_native.M3_FLAG_NO_F16_OPERANDS)) == b"generic"
+    assert name(desc(headdim=32, nheads=48, d_state=256, mimo_rank=4, proj_row_stride=
+                     2 * 1536 + 2 * 256 * 4 + 3 * 48 + 128)) == b"mfma_general"
+    assert name(desc(dtype=0)) == b"fp32_fused"
+    assert name(desc(dtype=0, mimo_rank=4, proj_row_stride=3072 + 2 * 512 + 3 * 24 + 64)) == b"fp32_layer"
+    assert name(desc(batch=0)) is None
+    fake = ctypes.c_void_p(256)
+    params = _native.LayerParams(*([256] * 10))
+    d = desc(dtype=0, flags=_native.M3_FLAG_FOR_BACKWARD)
+    assert lib.m3_prefill_fwd_noalloc(ctypes.byref(d), ctypes.byref(params), fake, None, fake,
+                                      None, None, None, None) == 3

@@ -424,22 +424,24 @@ def test_bf16_d768_variants_match_fp32_oracle(extra, cuda_device):
 @pytest.mark.parametrize("scale", [4.0, 32.0, 256.0])
 def test_bf16_d768_large_parameters_match_fp32_oracle(scale, cuda_device):
     """A checkpoint with large B/C norm weights and biases and mimo_x (all multiplied by
-    `scale`). x4 stays within the (conservative) f16 operand bounds and runs on the MFMA
-    kernel; x32 and x256 exceed them, so the layer runs on the fp32 generic kernel
-    (M3_FLAG_NO_F16_OPERANDS). All match the fp32 oracle. At x256 the f16 kernel, forced
-    through the C-ABI, overflows: the scores C~.B~ reach ~1e7 before the decay mask."""
-    from mamba3_amd import ops
+    `scale`): one rank's B^ row bound sqrt(N R) max|w| + sqrt(N) max|bias| reaches ~90 at
+    x4, ~720 at x32 and ~5800 at x256, and |mimo_x| ~256 at x256. The MFMA kernel still
+    runs (its f16 operands are held divided by powers of two derived from the parameters,
+    mamba3/mamba3.py:147-168 has no such limit) and matches the fp32 oracle; so does the
+    generic fp32 kernel that M3_FLAG_NO_F16_OPERANDS forces."""
     kw = dict(d_model=768, d_state=128, headdim=64, mimo_rank=2)
     layer, cfg, _ = _bf16_pair(kw, cuda_device, seed=9)
     with torch.no_grad():
         for name in ("B_norm.weight", "C_norm.weight", "B_bias", "C_bias", "mimo_x"):
             layer.get_parameter(name).mul_(scale)
     p = {k: v.detach().float().cpu() for k, v in layer.state_dict().items()}
-    fast = ops.f16_operands_ok(layer._small_params(), 128, 2)
-    assert fast == (scale == 4.0)
     torch.manual_seed(10)
     x = torch.randn(1, 300, 768).to(torch.bfloat16)
     with torch.no_grad():
+        proj = layer.in_proj(x.to(cuda_device)).contiguous()
+        y_in = torch.empty(1, 300, layer.d_inner, device=cuda_device, dtype=torch.bfloat16)
+        desc = layer._desc(1, 300, proj)
+        assert _native.prefill_kernel_name(desc, proj, y_in) == "mfma_d128_p64_r2"
         y, st = layer.prefill(x.to(cuda_device))
         y_ref, st_ref = ref.layer_forward(cfg, p, x.float(), return_state=True)
     assert max_rel(y.float(), y_ref) < BF16_TOL
@@ -447,14 +449,37 @@ def test_bf16_d768_large_parameters_match_fp32_oracle(scale, cuda_device):
         assert max_rel(st[k], st_ref[k]) < BF16_TOL, k
     if scale == 256.0:
         with torch.no_grad():
-            proj = layer.in_proj(x.to(cuda_device)).contiguous()
-            desc = layer._desc(1, 300, proj)  # flags 0: the f16 MFMA kernel
+            desc.flags |= _native.M3_FLAG_NO_F16_OPERANDS
+            assert _native.prefill_kernel_name(desc, proj, y_in) == "generic"
             n = _native.prefill_workspace_bytes(desc)
             ws = torch.empty(n, device=cuda_device, dtype=torch.uint8)
-            yf = torch.empty(1, 300, layer.d_inner, device=cuda_device, dtype=torch.bfloat16)
-            _native.prefill_fwd(desc, layer._param_pack(), proj, None, yf, None, None, None, ws, n)
-            forced = layer.out_proj(yf).float()
-        assert not (torch.isfinite(forced).all() and max_rel(forced, y_ref) < BF16_TOL)
+            _native.prefill_fwd(desc, layer._param_pack(), proj, None, y_in, None, None, None, ws, n)
+            forced = layer.out_proj(y_in).float()
+        assert max_rel(forced, y_ref) < BF16_TOL
+
+
+@pytest.mark.parametrize("scale", [1.0, 64.0])
+def test_bf16_general_kernel_large_parameters_match_fp32_oracle(scale, cuda_device):
+    """The general MFMA kernel (d_state 256, rank 4, headdim 64, two groups) with B/C norm
+    weights and biases and mimo_x multiplied by `scale` (x64: B^ row bound ~2000, |mimo_x|
+    ~64): same kernel, every output against the fp32 oracle."""
+    kw = dict(d_model=256, d_state=256, headdim=64, mimo_rank=4, ngroups=2)
+    layer, cfg, _ = _bf16_pair(kw, cuda_device, seed=11)
+    with torch.no_grad():
+        for name in ("B_norm.weight", "C_norm.weight", "B_bias", "C_bias", "mimo_x"):
+            layer.get_parameter(name).mul_(scale)
+    p = {k: v.detach().float().cpu() for k, v in layer.state_dict().items()}
+    torch.manual_seed(12)
+    x = torch.randn(2, 150, 256).to(torch.bfloat16)
+    with torch.no_grad():
+        proj = layer.in_proj(x.to(cuda_device)).contiguous()
+        h_out = torch.empty(2, layer.nheads, 64, 256, device=cuda_device)
+        assert _native.prefill_kernel_name(layer._desc(2, 150, proj), proj, None, h_out) == "mfma_general"
+        y, st = layer.prefill(x.to(cuda_device))
+        y_ref, st_ref = ref.layer_forward(cfg, p, x.float(), return_state=True)
+    assert max_rel(y.float(), y_ref) < BF16_TOL
+    for k in ("h", "prev_BX", "angle"):
+        assert max_rel(st[k], st_ref[k]) < BF16_TOL, k
 
 
 def test_bf16_d768_dt_scale_matches_fp32_oracle(cuda_device):
