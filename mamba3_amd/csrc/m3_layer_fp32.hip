@@ -25,6 +25,7 @@ namespace lp {
 
 struct Args {
     int B, T, H, P, N, R, G, trap, cplx;
+    int HT;  // heads whose sin / cos lp_prep holds in LDS at a time
     int64_t rs;  // proj row stride
     ProjLayout pl;
     float eps;
@@ -133,7 +134,7 @@ __global__ __launch_bounds__(NTH) void lp_angles(Args a) {
 // head's RoPE pairs in LDS, then the rotated rows of every head and the x terms, as flat loops
 // over (head, element).
 __global__ __launch_bounds__(NTH) void lp_prep(Args a) {
-    // B^ [G*N*R], C^ [G*N*R], reduction scratch [2*NTH], sin / cos [H*N/2] each
+    // B^ [G*N*R], C^ [G*N*R], reduction scratch [2*NTH], sin / cos [HT*N/2] each
     extern __shared__ float sm[];
     const int bt = blockIdx.x, b = bt / a.T, t = bt % a.T;
     const int NR = a.N * a.R, GNR = a.G * NR, NH = a.N / 2;
@@ -141,7 +142,7 @@ __global__ __launch_bounds__(NTH) void lp_prep(Args a) {
     float* Ch = sm + GNR;
     float* red = sm + 2 * GNR;
     float* sn = red + 2 * NTH;
-    float* cn = sn + (int64_t)a.H * NH;
+    float* cn = sn + (int64_t)a.HT * NH;
     const float* row = a.proj + ((int64_t)b * a.T + t) * a.rs;
     const int64_t tok0 = ((int64_t)b * a.T + t) * a.H;  // token row of head 0
     const int tid = threadIdx.x;
@@ -170,27 +171,33 @@ __global__ __launch_bounds__(NTH) void lp_prep(Args a) {
         }
         __syncthreads();
     }
-    if (a.cplx) {
-        for (int j = tid; j < a.H * NH; j += NTH) sincosf(a.phi[tok0 * NH + j], &sn[j], &cn[j]);
-        __syncthreads();
-    }
     const int hpg = a.H / a.G;
-    for (int j = tid; j < a.H * NR; j += NTH) {
-        const int h = j / NR, e = j % NR, g = h / hpg;
-        const int n = e / a.R, r = e % a.R, i = n >> 1;
-        const int64_t ev = (int64_t)g * NR + (2 * i) * a.R + r, od = ev + a.R;
-        float vb = Bh[(int64_t)g * NR + e], vc = Ch[(int64_t)g * NR + e];
+    // heads in tiles of HT, so the sin / cos of a tile fit in LDS whatever H * N is
+    for (int h0 = 0; h0 < a.H; h0 += a.HT) {
+        const int nh = min(a.HT, a.H - h0);
         if (a.cplx) {
-            const float s = sn[h * NH + i], c = cn[h * NH + i];
-            vb = (n & 1) ? Bh[ev] * s + Bh[od] * c : Bh[ev] * c - Bh[od] * s;
-            vc = (n & 1) ? Ch[ev] * s + Ch[od] * c : Ch[ev] * c - Ch[od] * s;
+            if (h0 > 0) __syncthreads();  // the previous tile's sin / cos are read
+            for (int j = tid; j < nh * NH; j += NTH)
+                sincosf(a.phi[(tok0 + h0) * NH + j], &sn[j], &cn[j]);
+            __syncthreads();
         }
-        const int64_t tok = tok0 + h;
-        a.Bt[tok * NR + e] = vb;
-        a.Ct[tok * NR + e] = vc;
-        if (a.trap) {
-            if (t + 1 < a.T) a.Bb[(tok + a.H) * NR + e] = vb;  // B_b[t+1] = B~[t]
-            if (t == 0) a.Bb[tok * NR + e] = 0.f;
+        for (int j = tid; j < nh * NR; j += NTH) {
+            const int hl = j / NR, h = h0 + hl, e = j % NR, g = h / hpg;
+            const int n = e / a.R, r = e % a.R, i = n >> 1;
+            const int64_t ev = (int64_t)g * NR + (2 * i) * a.R + r, od = ev + a.R;
+            float vb = Bh[(int64_t)g * NR + e], vc = Ch[(int64_t)g * NR + e];
+            if (a.cplx) {
+                const float s = sn[hl * NH + i], c = cn[hl * NH + i];
+                vb = (n & 1) ? Bh[ev] * s + Bh[od] * c : Bh[ev] * c - Bh[od] * s;
+                vc = (n & 1) ? Ch[ev] * s + Ch[od] * c : Ch[ev] * c - Ch[od] * s;
+            }
+            const int64_t tok = tok0 + h;
+            a.Bt[tok * NR + e] = vb;
+            a.Ct[tok * NR + e] = vc;
+            if (a.trap) {
+                if (t + 1 < a.T) a.Bb[(tok + a.H) * NR + e] = vb;  // B_b[t+1] = B~[t]
+                if (t == 0) a.Bb[tok * NR + e] = 0.f;
+            }
         }
     }
     const int PR = a.P * a.R;
@@ -279,10 +286,22 @@ Plan plan(const m3_layer_desc& d) {
 }  // namespace lp
 
 namespace {
-// LDS of lp_prep: B^ and C^ of every group, the reduction scratch, sin / cos of every pair.
+constexpr size_t kPrepLds = 64 * 1024;
+
+// LDS of lp_prep without the sin / cos tiles: B^ and C^ of every group, the reduction
+// scratch.
+size_t prep_lds_fixed(const m3_layer_desc& d) {
+    return (2 * (size_t)d.ngroups * d.d_state * d.mimo_rank + 2 * lp::NTH) * sizeof(float);
+}
+// Heads per sin / cos tile: as many as fit next to the fixed part (0: nothing fits).
+int prep_heads_per_tile(const m3_layer_desc& d) {
+    const size_t fixed = prep_lds_fixed(d);
+    if (fixed >= kPrepLds) return 0;
+    const size_t per_head = (size_t)d.d_state * sizeof(float);  // sin and cos of N/2 pairs
+    return (int)std::min<size_t>(d.nheads, (kPrepLds - fixed) / per_head);
+}
 size_t prep_lds(const m3_layer_desc& d) {
-    return (2 * (size_t)d.ngroups * d.d_state * d.mimo_rank + 2 * lp::NTH +
-            (size_t)d.nheads * d.d_state) * sizeof(float);
+    return prep_lds_fixed(d) + (size_t)prep_heads_per_tile(d) * d.d_state * sizeof(float);
 }
 }  // namespace
 
@@ -302,7 +321,7 @@ void* fp32_layer_scratch(const m3_layer_desc& d, void* ws, size_t* bytes) {
 }
 
 bool fp32_layer_supported(const m3_layer_desc& d) {
-    return d.dtype == M3_DTYPE_F32 && prep_lds(d) <= 64 * 1024 &&
+    return d.dtype == M3_DTYPE_F32 && prep_heads_per_tile(d) > 0 &&
            chunked_fwd_mfma_workspace(d.batch, d.seqlen, d.nheads, d.headdim, d.d_state,
                                       d.mimo_rank, d.use_trapezoidal != 0) > 0;
 }
@@ -322,6 +341,7 @@ int launch_fp32_layer(const m3_layer_desc& d, const m3_layer_params& p, const vo
     a.B = d.batch, a.T = d.seqlen, a.H = d.nheads, a.P = d.headdim, a.N = d.d_state;
     a.R = d.mimo_rank, a.G = d.ngroups, a.trap = d.use_trapezoidal, a.cplx = d.use_complex;
     a.rs = d.proj_row_stride, a.pl = proj_layout(d), a.eps = d.rms_eps, a.prm = p;
+    a.HT = prep_heads_per_tile(d);
     a.proj = reinterpret_cast<const float*>(proj);
     a.dt_scale = dt_scale;
     a.dt = part(0), a.A = part(1), a.phi = part(2), a.xg = part(3);
@@ -331,7 +351,7 @@ int launch_fp32_layer(const m3_layer_desc& d, const m3_layer_params& p, const vo
     a.y = reinterpret_cast<float*>(y_out), a.h_final = h_final, a.angle = angle;
     a.prev_bx = prev_bx;
     const size_t lds = prep_lds(d);
-    if (lds > 64 * 1024) return 1;
+    if (a.HT <= 0 || lds > kPrepLds) return 1;
     const int64_t nbth = (int64_t)d.batch * d.seqlen * d.nheads;
     hipLaunchKernelGGL(lp_dt, dim3((unsigned)((std::max<int64_t>(nbth, d.nheads) + NTH - 1) / NTH)),
                        dim3(NTH), 0, stream, a);

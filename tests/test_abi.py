@@ -115,9 +115,14 @@ def test_workspace_query_and_desc_validation(lib):
     # ranks the chunk kernels do not cover run on the generic kernel (state in LDS): none
     assert lib.m3_prefill_workspace_size(ctypes.byref(_desc(mimo_rank=3)), ctypes.byref(n)) == 0
     assert n.value == 0
-    # so do layers whose per-token preparation would not fit its 64 KB of LDS (H * N floats of
-    # sin / cos): 64 heads x d_state 256
+    # wide layers run there too: the per-token preparation holds the sin / cos of a tile of
+    # heads at a time (64 heads x d_state 256 needed 64 KB of them at once)
     assert lib.m3_prefill_workspace_size(ctypes.byref(_desc(nheads=64, d_state=256)),
+                                         ctypes.byref(n)) == 0
+    assert n.value > 0
+    # a layer whose normalised B^ and C^ of every group alone exceed 64 KB of LDS runs on the
+    # generic kernel: 32 groups x d_state 256 x rank 2
+    assert lib.m3_prefill_workspace_size(ctypes.byref(_desc(nheads=32, ngroups=32, d_state=256)),
                                          ctypes.byref(n)) == 0
     assert n.value == 0
     # bf16 d_state 128 / headdim 64 / rank 2: normalised B^ and C^ in f16, per token

@@ -197,6 +197,30 @@ def test_layer_d768_gradients_match_oracle(cuda_device):
         assert max_rel(p.grad, pg[name]) < FP32_TOL, name
 
 
+def test_layer_d4096_gradients_match_oracle(cuda_device):
+    """KulaMamba(d_model=4096) with the reference defaults (128 heads, headdim 64, d_state
+    128, rank 2; mamba3/mamba3.py:50-64) over 40 tokens: the training forward keeps the
+    sin / cos of the RoPE rotation for a tile of heads at a time, so a layer this wide
+    trains like the reference's. Every parameter's gradient and the input's against the
+    fp64 oracle layer."""
+    kw = dict(d_model=4096)
+    torch.manual_seed(0)
+    layer = mamba3_amd.KulaMamba(**kw).to(cuda_device).train()
+    assert layer.nheads == 128
+    g = torch.Generator().manual_seed(31)
+    x = torch.randn(1, 40, 4096, generator=g)
+    w = torch.randn(1, 40, 4096, generator=g)
+    wh = torch.randn(1, layer.nheads, 64, 128, generator=g)
+    out_ref, pg, xg_ref = _oracle_layer_grads(kw, layer, x, w, wh)
+    xd = x.to(cuda_device).requires_grad_()
+    out, st = layer.prefill(xd)
+    ((out * w.to(cuda_device)).sum() + (st["h"] * wh.to(cuda_device)).sum()).backward()
+    assert max_rel(out, out_ref) < FP32_TOL
+    assert max_rel(xd.grad, xg_ref) < FP32_TOL
+    for name, p in layer.named_parameters():
+        assert max_rel(p.grad, pg[name]) < FP32_TOL, name
+
+
 @pytest.mark.parametrize("kw", [LAYER_KW[0], LAYER_KW[3], LAYER_KW[2]],
                          ids=["default", "rank4-groups2", "complex-off"])
 def test_layer_state_gradients_match_oracle(kw, cuda_device):
