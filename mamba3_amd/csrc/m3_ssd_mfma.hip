@@ -67,7 +67,11 @@ constexpr int NR = N * R;
 constexpr int NH = N / 2;
 constexpr int THREADS = 1024;  // 8 MFMA waves + 8 helper waves, four per SIMD
 constexpr int NMW = 8;          // waves 0..7 run the MFMA work, 8..15 are helpers
-constexpr int PAD = 8;
+// f16 row padding of the C~, B~ and H tiles: a row stride of 72 32-bit words. Their MFMA
+// operand reads (ds_read_b128, 16 rows x 64 bytes per wave) run at 1.5x the LDS throughput
+// of a 68-word stride (16 waves per CU, all CUs busy), and the transposed B~ reads and the
+// tile stores stay conflict-free.
+constexpr int PAD = 16;
 
 
 constexpr int NSLOT = 3;

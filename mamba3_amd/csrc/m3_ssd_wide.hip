@@ -45,7 +45,12 @@ namespace wd {
 constexpr int ROWS = 64;              // (t, r) rows per chunk
 constexpr int PB = 32;                // headdim columns per workgroup
 constexpr int THREADS = 1024;         // 16 waves: 0-7 own output tiles, 8-15 score tiles
-constexpr int PAD = 8;                // f16 row padding of the X, S and H tiles
+constexpr int PAD = 8;                // f16 row padding of the S and H tiles
+// f16 row padding of the X^T / Xw^T tiles: a row stride of 40 32-bit words (their G2 / G4
+// operand reads, 16 rows x 64 bytes per wave, run 1.4-1.8% faster over the whole call than
+// at 36; 44, 48 and 52 were no better). The 256 x 1 instantiation has no LDS to spare.
+template <int N, int R>
+constexpr int padx() { return (N == 256 && R == 1) ? 8 : 16; }
 // f16 row padding of the C~ / B~ tiles: a row stride of 8 (mod 16) 32-bit words keeps the
 // operand and transpose reads of those tiles free of most bank conflicts (a stride of
 // 4 (mod 16) words, padding 8, measured 5% slower at d_state 256).
@@ -72,8 +77,8 @@ struct __align__(16) Smem {
     static constexpr int Q = ROWS / R;
     f16 C[ROWS][N + PADCB];
     f16 B[ROWS][N + PADCB];
-    f16 XT[2][PB][ROWS + PAD];  // by chunk parity: G2 of chunk k reads while chunk k+1's is written
-    f16 XwT[PB][ROWS + PAD];
+    f16 XT[2][PB][ROWS + padx<N, R>()];  // by chunk parity: G2 of chunk k reads while chunk k+1's is written
+    f16 XwT[PB][ROWS + padx<N, R>()];
     f16 S[ROWS][ROWS + PAD];
     f16 H[PB][N + PAD];
     Tok tok[2];           // by chunk parity
