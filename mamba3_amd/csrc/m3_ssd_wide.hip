@@ -114,60 +114,156 @@ __device__ __forceinline__ float readlane(float v, int l) {
 // ---------------------------------------------------------------------------------
 // Normalised B^ / C^ per (token, group) (mamba3/mamba3.py:19-35, 142-157): RMSNorm over
 // the N*R row times the weight, plus the bias, in f16, pair-packed: the 32-bit word
-// i*R + r holds (value[n=2i][r], value[n=2i+1][r]). One wave per row.
+// i*R + r holds (value[n=2i][r], value[n=2i+1][r]).
 // ---------------------------------------------------------------------------------
+constexpr int kWideBcRows = 4;  // (token, group) rows per wave of bc_norm_wide
+
+// The 2R raw bf16 of one RoPE pair of a B / C row as R words (two elements per word, in
+// order), by one vector load when the row layout allows it.
+template <int R>
+__device__ __forceinline__ void load_raw_pair(const bf16* p, bool vec, unsigned (&w)[R]) {
+    if (vec) {
+        if constexpr (R == 4) {
+            const u32x4 v = *reinterpret_cast<const u32x4*>(p);
+            w[0] = v[0]; w[1] = v[1]; w[2] = v[2]; w[3] = v[3];
+        } else if constexpr (R == 2) {
+            const u32x2 v = *reinterpret_cast<const u32x2*>(p);
+            w[0] = v[0]; w[1] = v[1];
+        } else {
+            w[0] = *reinterpret_cast<const unsigned*>(p);
+        }
+    } else {
+        const unsigned short* q = reinterpret_cast<const unsigned short*>(p);
+#pragma unroll
+        for (int e = 0; e < R; ++e) w[e] = (unsigned)q[2 * e] | ((unsigned)q[2 * e + 1] << 16);
+    }
+}
+
+// Raw element e of a pair's words, as float.
+template <int R>
+__device__ __forceinline__ float raw_elem(const unsigned (&w)[R], int e) {
+    return __builtin_bit_cast(float, (e & 1) ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16));
+}
+
+// One wave normalises kWideBcRows consecutive (token, group) rows: all their reads are
+// issued first, the norm weights are read once, the biases and the operand scales once per
+// distinct group of the rows (a scalar branch: a row is one wave's).
 template <int N, int R>
 __global__ __launch_bounds__(256) void bc_norm_wide(const bf16* __restrict__ proj, int64_t rs,
                                                     int64_t offB, int64_t offC, int G,
-                                                    int64_t nrows, float eps,
+                                                    int64_t nrows, float eps, int vec,
                                                     const float* __restrict__ wB,
                                                     const float* __restrict__ biasB,
                                                     const float* __restrict__ wC,
                                                     const float* __restrict__ biasC,
                                                     f16* __restrict__ Bn, f16* __restrict__ Cn) {
-    constexpr int NH = N / 2, NR = N * R, PPL = (NH + 63) / 64;
+    constexpr int NH = N / 2, NR = N * R, PPL = (NH + 63) / 64, KR = kWideBcRows;
     const int lane = threadIdx.x & 63;
-    const int64_t tg = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (tg >= nrows) return;
-    const int64_t tok = tg / G;
-    const int g = (int)(tg % G);
-    const bf16* rowB = proj + tok * rs + offB + (int64_t)g * NR;
-    const bf16* rowC = proj + tok * rs + offC + (int64_t)g * NR;
-    // pair i covers raw elements 2iR .. 2iR+2R-1: (n=2i, r) at 2iR + r, (n=2i+1, r) at 2iR + R + r
-    float vb[PPL][2 * R], vc[PPL][2 * R];
-    float sb = 0.f, sc = 0.f;
+    const int64_t l0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * KR;
+    if (l0 >= nrows) return;
+    // Lane pairs i = lane + 64 j (j < PPL); pair i covers raw elements 2iR .. 2iR+2R-1:
+    // (n=2i, r) at 2iR + r, (n=2i+1, r) at 2iR + R + r. Rows past the end read the last row
+    // and store nothing.
+    unsigned rwb[KR][PPL][R], rwc[KR][PPL][R];
+    int gg[KR];
+#pragma unroll
+    for (int k = 0; k < KR; ++k) {
+        const int64_t tg = l0 + k < nrows ? l0 + k : nrows - 1;
+        const int64_t tok = tg / G;
+        gg[k] = (int)(tg % G);
+        const bf16* rowB = proj + tok * rs + offB + (int64_t)gg[k] * NR;
+        const bf16* rowC = proj + tok * rs + offC + (int64_t)gg[k] * NR;
+#pragma unroll
+        for (int j = 0; j < PPL; ++j) {
+            const int i = lane + 64 * j;
+            if (i < NH) {
+                load_raw_pair<R>(rowB + 2 * i * R, vec, rwb[k][j]);
+                load_raw_pair<R>(rowC + 2 * i * R, vec, rwc[k][j]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < R; ++e) rwb[k][j][e] = rwc[k][j][e] = 0u;
+            }
+        }
+    }
+    float wvb[PPL][2 * R], wvc[PPL][2 * R];
+    float mwb = 0.f, mwc = 0.f;
 #pragma unroll
     for (int j = 0; j < PPL; ++j) {
         const int i = lane + 64 * j;
 #pragma unroll
         for (int e = 0; e < 2 * R; ++e) {
-            vb[j][e] = i < NH ? (float)rowB[2 * i * R + e] : 0.f;
-            vc[j][e] = i < NH ? (float)rowC[2 * i * R + e] : 0.f;
-            sb += vb[j][e] * vb[j][e];
-            sc += vc[j][e] * vc[j][e];
+            wvb[j][e] = i < NH ? wB[2 * i * R + e] : 0.f;
+            wvc[j][e] = i < NH ? wC[2 * i * R + e] : 0.f;
+            mwb = fmaxf(mwb, fabsf(wvb[j][e]));
+            mwc = fmaxf(mwc, fabsf(wvc[j][e]));
         }
     }
-    sb = group_sum<64>(sb);
-    sc = group_sum<64>(sc);
-    const float rb = rsqrtf(sb * (1.f / NR) + eps), rc = rsqrtf(sc * (1.f / NR) + eps);
-    const float* bB = biasB + (int64_t)g * NR;
-    const float* bC = biasC + (int64_t)g * NR;
-    // operand scales of the row's group (1 unless the parameters are large)
-    const float ib = 1.f / bc_row_scale<N, R>(wave_absmax(wB, NR, lane), wave_absmax(bB, NR, lane));
-    const float ic = 1.f / bc_row_scale<N, R>(wave_absmax(wC, NR, lane), wave_absmax(bC, NR, lane));
+    mwb = wave_max(mwb);
+    mwc = wave_max(mwc);
+    float bvb[PPL][2 * R], bvc[PPL][2 * R];
+    float ib = 1.f, ic = 1.f;
+    int gcur = -1;
 #pragma unroll
-    for (int j = 0; j < PPL; ++j) {
-        const int i = lane + 64 * j;
-        if (i >= NH) continue;
+    for (int k = 0; k < KR; ++k) {
+        const int gk = __builtin_amdgcn_readfirstlane(gg[k]);
+        if (gk != gcur) {
+            // biases and operand scales of the row's group (1 unless the parameters are large)
+            gcur = gk;
+            float mbb = 0.f, mbc = 0.f;
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const int e0 = 2 * i * R + r, e1 = e0 + R;
-            const f16x2 ob = f16x2{(f16)((vb[j][r] * rb * wB[e0] + bB[e0]) * ib),
-                                   (f16)((vb[j][R + r] * rb * wB[e1] + bB[e1]) * ib)};
-            const f16x2 oc = f16x2{(f16)((vc[j][r] * rc * wC[e0] + bC[e0]) * ic),
-                                   (f16)((vc[j][R + r] * rc * wC[e1] + bC[e1]) * ic)};
-            *reinterpret_cast<f16x2*>(Bn + tg * NR + 2 * (i * R + r)) = ob;
-            *reinterpret_cast<f16x2*>(Cn + tg * NR + 2 * (i * R + r)) = oc;
+            for (int j = 0; j < PPL; ++j) {
+                const int i = lane + 64 * j;
+#pragma unroll
+                for (int e = 0; e < 2 * R; ++e) {
+                    bvb[j][e] = i < NH ? biasB[(int64_t)gk * NR + 2 * i * R + e] : 0.f;
+                    bvc[j][e] = i < NH ? biasC[(int64_t)gk * NR + 2 * i * R + e] : 0.f;
+                    mbb = fmaxf(mbb, fabsf(bvb[j][e]));
+                    mbc = fmaxf(mbc, fabsf(bvc[j][e]));
+                }
+            }
+            ib = 1.f / bc_row_scale<N, R>(mwb, wave_max(mbb));
+            ic = 1.f / bc_row_scale<N, R>(mwc, wave_max(mbc));
+        }
+        float sb = 0.f, sc = 0.f;
+#pragma unroll
+        for (int j = 0; j < PPL; ++j)
+#pragma unroll
+            for (int e = 0; e < 2 * R; ++e) {
+                const float vb = raw_elem<R>(rwb[k][j], e), vc = raw_elem<R>(rwc[k][j], e);
+                sb += vb * vb;
+                sc += vc * vc;
+            }
+        sb = lane_sum<64>(sb);
+        sc = lane_sum<64>(sc);
+        const float nb = rsqrtf(sb * (1.f / NR) + eps), nc = rsqrtf(sc * (1.f / NR) + eps);
+        if (l0 + k >= nrows) continue;
+        const int64_t tg = l0 + k;
+#pragma unroll
+        for (int j = 0; j < PPL; ++j) {
+            const int i = lane + 64 * j;
+            if (i >= NH) continue;
+            // pair-packed: word r = (value[n=2i][r], value[n=2i+1][r])
+            unsigned ob[R], oc[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const int e0 = r, e1 = R + r;
+                ob[r] = bits(f16x2{(f16)((raw_elem<R>(rwb[k][j], e0) * nb * wvb[j][e0] + bvb[j][e0]) * ib),
+                                   (f16)((raw_elem<R>(rwb[k][j], e1) * nb * wvb[j][e1] + bvb[j][e1]) * ib)});
+                oc[r] = bits(f16x2{(f16)((raw_elem<R>(rwc[k][j], e0) * nc * wvc[j][e0] + bvc[j][e0]) * ic),
+                                   (f16)((raw_elem<R>(rwc[k][j], e1) * nc * wvc[j][e1] + bvc[j][e1]) * ic)});
+            }
+            f16* pb = Bn + tg * NR + 2 * i * R;
+            f16* pc = Cn + tg * NR + 2 * i * R;
+            if constexpr (R == 4) {
+                *reinterpret_cast<u32x4*>(pb) = u32x4{ob[0], ob[1], ob[2], ob[3]};
+                *reinterpret_cast<u32x4*>(pc) = u32x4{oc[0], oc[1], oc[2], oc[3]};
+            } else if constexpr (R == 2) {
+                *reinterpret_cast<u32x2*>(pb) = u32x2{ob[0], ob[1]};
+                *reinterpret_cast<u32x2*>(pc) = u32x2{oc[0], oc[1]};
+            } else {
+                *reinterpret_cast<unsigned*>(pb) = ob[0];
+                *reinterpret_cast<unsigned*>(pc) = oc[0];
+            }
         }
     }
 }
@@ -668,9 +764,13 @@ int launch(const m3_layer_desc& d, const m3_layer_params& p, const void* proj,
     a.h_final = h_final;
     a.angle = angle;
     a.prev_bx = prev_bx;
-    hipLaunchKernelGGL((bc_norm_wide<N, R>), dim3((unsigned)((nrows + 3) / 4)), dim3(256), 0, stream,
-                       a.proj, a.rs, a.pl.B, a.pl.C, a.G, nrows, d.rms_eps, p.B_norm_w, p.B_bias,
-                       p.C_norm_w, p.C_bias, bn, cn);
+    // vector loads of a pair's 2R raw values when every row offset keeps them aligned
+    const int vec = a.rs % (2 * R) == 0 && a.pl.B % (2 * R) == 0 && a.pl.C % (2 * R) == 0 &&
+                    reinterpret_cast<uintptr_t>(proj) % (4 * R) == 0;
+    constexpr int rows_per_block = 4 * kWideBcRows;
+    hipLaunchKernelGGL((bc_norm_wide<N, R>), dim3((unsigned)((nrows + rows_per_block - 1) / rows_per_block)),
+                       dim3(256), 0, stream, a.proj, a.rs, a.pl.B, a.pl.C, a.G, nrows, d.rms_eps, vec,
+                       p.B_norm_w, p.B_bias, p.C_norm_w, p.C_bias, bn, cn);
     hipLaunchKernelGGL((ssd_wide<N, R>), dim3((unsigned)(d.batch * d.nheads * a.PS)), dim3(THREADS), 0,
                        stream, a);
     return hipGetLastError() == hipSuccess ? M3_OK : M3_ERR_LAUNCH;
