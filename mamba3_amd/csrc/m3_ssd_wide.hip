@@ -364,7 +364,8 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
     // theta staging jobs: units of 8 pairs of one token.
     constexpr int THU = Q * NH / 8;
     constexpr int THJ = (THU + THREADS - 1) / THREADS;
-    const bool thvec = a.rs % 8 == 0 && a.pl.theta % 8 == 0;
+    const bool thvec = a.rs % 8 == 0 && a.pl.theta % 8 == 0 &&
+                       reinterpret_cast<uintptr_t>(a.proj) % 16 == 0;
 
     // ---- per-chunk inputs, read into registers at least a phase before they are used ----
     // Rotation jobs: this thread's RoPE pair ri at tokens rt0 + m * TSTEP (m < J).

@@ -702,6 +702,44 @@ def test_bf16_wide_prefill_matches_fp32_oracle(kw, T, cuda_device):
         assert max_rel(st[k], st_ref[k]) < BF16_TOL, k
 
 
+@pytest.mark.parametrize("kw,expect", [
+    (dict(d_model=256, d_state=256, headdim=128, mimo_rank=4, ngroups=2), "mfma_general"),
+    (dict(d_model=256, d_state=128, headdim=32, mimo_rank=2), "mfma_general"),
+    (dict(d_model=128, d_state=64, headdim=32, mimo_rank=1), "mfma_general"),
+])
+def test_general_kernel_odd_proj_row_stride_equals_contiguous(kw, expect, cuda_device):
+    """proj handed over through the C-ABI with an odd row stride (a column slice of a wider
+    buffer, as a caller's fused projection may give): the B / C normalisation reads each
+    pair's raw values element by element instead of with one vector load, and every output
+    equals, bit for bit, that of the same values at the contiguous stride."""
+    dev = cuda_device
+    layer, _, _ = _bf16_pair(kw, dev, seed=15)
+    torch.manual_seed(16)
+    Bat, T = 2, 77
+    x = torch.randn(Bat, T, kw["d_model"]).to(torch.bfloat16).to(dev)
+    outs = []
+    with torch.no_grad():
+        proj = layer.in_proj(x).contiguous()
+        W = proj.shape[-1]
+        wide = torch.zeros(Bat, T, W + 1, dtype=proj.dtype, device=dev)
+        wide[..., :W] = proj
+        for src in (proj, wide):
+            desc = layer._desc(Bat, T, src)
+            assert desc.proj_row_stride == src.stride(-2)
+            y = torch.empty(Bat, T, layer.d_inner, device=dev, dtype=torch.bfloat16)
+            h = torch.empty(Bat, layer.nheads, layer.headdim, layer.d_state, device=dev)
+            angle = torch.empty(Bat, layer.nheads, layer.d_state // 2, device=dev)
+            prev = torch.empty_like(h)
+            assert _native.prefill_kernel_name(desc, src, y, h, prev) == expect
+            n = _native.prefill_workspace_bytes(desc)
+            ws = torch.empty(n, device=dev, dtype=torch.uint8)
+            _native.prefill_fwd(desc, layer._param_pack(), src, None, y, h, angle, prev, ws, n)
+            outs.append((y, h, angle, prev))
+    assert outs[1][0].isfinite().all()
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+
+
 def test_bf16_d2048_prefill_matches_fp32_oracle(cuda_device):
     """The d_model 2048 layer (d_state 256, headdim 128, rank 4), with dt_scale."""
     kw = dict(d_model=2048, d_state=256, headdim=128, mimo_rank=4)
