@@ -3,12 +3,16 @@
 //   h_states[b,0,h,:]   = h_init[b,h,:] or 0
 //   h_states[b,k+1,h,:] = decay[b,k,h] * h_states[b,k,h,:] + h_chunk[b,k,h,:]
 //
-// Design: the recurrence is independent per (b,h,j) column, so every lane owns one
-// float4 column slice and walks k. A wave reads/writes 1 KiB contiguous per k, and the
-// loads of kUnroll consecutive chunks are issued before the dependent FMA chain, so
-// each wave keeps kUnroll x 1 KiB in flight. HBM-bound: B*K*H*PN*8 bytes + decay. Every
-// h_chunk element is read once and every state written once, so both go through
-// non-temporal (streaming) loads and stores, which keep them out of the caches' way.
+// Design: the recurrence is independent per (b,h,j) column, so lanes own float4 column
+// slices and walk k. HBM-bound: B*K*H*PN*8 bytes + decay. Every h_chunk element is read
+// once and every state written once, so both go through non-temporal (streaming) loads and
+// stores, which keep them out of the caches' way. Memory-level parallelism comes from
+// several columns per lane, not from several k per column: a lane owns kScanCols float4
+// columns 64 apart, so a wave's loads of one k cover kScanCols KiB contiguous. Loads of
+// consecutive k of one column lie H*PN*4 bytes apart, a power of two for the usual
+// shapes (4 MiB at 32 heads x 256 x 128), and a burst of them measured 20% slower at that
+// stride (the older one-column-per-lane kernels, kept for rows that are not a multiple of
+// 64 * kScanCols float4 columns, issue kScanUnroll k ahead).
 #include "m3_common.h"
 #include "m3_kernels.h"
 #include "m3_mfma.h"
@@ -17,6 +21,55 @@ namespace m3 {
 
 constexpr int kScanUnroll = 8;
 constexpr int kScanBlock = 256;
+constexpr int kScanCols = 8;  // float4 columns per lane of the column-blocked kernels
+
+// A wave's columns: 64 * kScanCols consecutive float4 columns of one (b, h) row; lane l
+// owns j4 = j40 + 64 c, c < kScanCols.
+struct ScanCols {
+    int64_t bh, base;  // (b, h); float4 offset of (b, 0, h, j40)
+    int64_t kstride;   // float4 units between k
+    int j40, h, w;     // first column of the lane, head, wave index within the row
+    const float* dptr; // decay[b, k, h] at k * H
+    __device__ ScanCols(const float* decay, int64_t wcol0, int K, int H, int pn4, int lane) {
+        bh = wcol0 / pn4;
+        j40 = (int)(wcol0 % pn4) + lane;
+        w = (int)(wcol0 % pn4) / (64 * kScanCols);
+        h = (int)(bh % H);
+        const int64_t b = bh / H;
+        kstride = (int64_t)H * pn4;
+        base = (b * K * H + h) * (int64_t)pn4 + j40;
+        dptr = decay + b * K * H + h;
+    }
+};
+
+// Forward, column-blocked: per k the wave issues kScanCols 1 KiB loads before the FMAs.
+__global__ __launch_bounds__(kScanBlock) void scan_fwd_cols(
+    const float* __restrict__ decay, const f32x4* __restrict__ h_chunk,
+    const f32x4* __restrict__ h_init, f32x4* __restrict__ h_states, int K, int H,
+    int pn4, int64_t total_cols) {
+    const int lane = threadIdx.x & 63;
+    const int64_t wcol0 = ((int64_t)blockIdx.x * (kScanBlock / 64) + (threadIdx.x >> 6)) * (64 * kScanCols);
+    if (wcol0 >= total_cols) return;  // whole waves
+    const ScanCols c(decay, wcol0, K, H, pn4, lane);
+    f32x4 s[kScanCols];
+#pragma unroll
+    for (int i = 0; i < kScanCols; ++i) {
+        s[i] = h_init ? h_init[c.bh * pn4 + c.j40 + 64 * i] : f32x4{0.f, 0.f, 0.f, 0.f};
+        __builtin_nontemporal_store(s[i], &h_states[c.base + 64 * i]);
+    }
+    for (int k = 0; k < K - 1; ++k) {
+        const int64_t o = c.base + (int64_t)k * c.kstride;
+        f32x4 v[kScanCols];
+#pragma unroll
+        for (int i = 0; i < kScanCols; ++i) v[i] = __builtin_nontemporal_load(&h_chunk[o + 64 * i]);
+        const float d = c.dptr[(int64_t)k * H];
+#pragma unroll
+        for (int i = 0; i < kScanCols; ++i) {
+            s[i] = d * s[i] + v[i];
+            __builtin_nontemporal_store(s[i], &h_states[o + c.kstride + 64 * i]);
+        }
+    }
+}
 
 __global__ __launch_bounds__(kScanBlock) void scan_fwd_vec4(
     const float* __restrict__ decay, const f32x4* __restrict__ h_chunk,
@@ -84,8 +137,9 @@ __global__ __launch_bounds__(kScanBlock) void scan_fwd_scalar(
 //   d_chunk[k] = G[k+1] (k < K-1),  d_chunk[K-1] = 0
 //   d_decay[k] = sum_j G[k+1][j] h[k][j] (k < K-1),  d_decay[K-1] = 0
 //   d_h_init   = G[0]
-// Pass 1: every lane owns a float4 column and walks k down; each wave reduces its share of
-// the d_decay sum (DPP scan, fixed order) and writes one partial per (b,k,h,wave).
+// Pass 1: lanes own float4 columns (kScanCols each, or one in the fallback kernel) and
+// walk k down; each wave reduces its share of the d_decay sum (DPP scan, fixed order) and
+// writes one partial per (b,k,h,wave).
 // Pass 2 adds the partials of every (b,k,h) in wave order: deterministic, no atomics.
 // ---------------------------------------------------------------------------------
 constexpr int kScanBwdBlock = 256;
@@ -93,6 +147,52 @@ constexpr int kScanBwdBlock = 256;
 // Sum over the wave in a fixed order (DPP inclusive scan; lane 63 holds the total).
 __device__ __forceinline__ float wave_sum_dpp(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wave_incl_scan(v)), 63));
+}
+
+// Backward, column-blocked (columns as in scan_fwd_cols): per k the wave issues its
+// 2 kScanCols loads together; its d_decay partial sums the lane's columns in order, then
+// the wave (one partial per (b,k,h,wave)).
+__global__ __launch_bounds__(kScanBwdBlock) void scan_bwd_cols(
+    const float* __restrict__ decay, const f32x4* __restrict__ h_states,
+    const f32x4* __restrict__ grad, f32x4* __restrict__ d_chunk, f32x4* __restrict__ d_h_init,
+    float* __restrict__ part, int K, int H, int pn4, int64_t total_cols) {
+    const int lane = threadIdx.x & 63;
+    const int64_t wcol0 = ((int64_t)blockIdx.x * (kScanBwdBlock / 64) + (threadIdx.x >> 6)) * (64 * kScanCols);
+    if (wcol0 >= total_cols) return;  // whole waves
+    const ScanCols c(decay, wcol0, K, H, pn4, lane);
+    const int nw = pn4 / (64 * kScanCols);
+    float* pptr = part + (c.base - c.j40) / pn4 * nw + c.w;  // (b,k,h,w) at k * H * nw
+    f32x4 g[kScanCols];
+    const int64_t last = c.base + (int64_t)(K - 1) * c.kstride;
+#pragma unroll
+    for (int i = 0; i < kScanCols; ++i) {
+        g[i] = __builtin_nontemporal_load(&grad[last + 64 * i]);
+        __builtin_nontemporal_store(f32x4{0.f, 0.f, 0.f, 0.f}, &d_chunk[last + 64 * i]);
+    }
+    for (int k = K - 2; k >= 0; --k) {
+        const int64_t o = c.base + (int64_t)k * c.kstride;
+        f32x4 hs[kScanCols], gk[kScanCols];
+#pragma unroll
+        for (int i = 0; i < kScanCols; ++i) {
+            hs[i] = __builtin_nontemporal_load(&h_states[o + 64 * i]);
+            gk[i] = __builtin_nontemporal_load(&grad[o + 64 * i]);
+        }
+        float dot = 0.f;
+#pragma unroll
+        for (int i = 0; i < kScanCols; ++i) {
+            __builtin_nontemporal_store(g[i], &d_chunk[o + 64 * i]);
+            dot += g[i][0] * hs[i][0] + g[i][1] * hs[i][1] + g[i][2] * hs[i][2] + g[i][3] * hs[i][3];
+        }
+        const float acc = wave_sum_dpp(dot);
+        if (lane == 0) pptr[(int64_t)k * H * nw] = acc;
+        const float d = c.dptr[(int64_t)k * H];
+#pragma unroll
+        for (int i = 0; i < kScanCols; ++i) g[i] = gk[i] + d * g[i];
+    }
+    if (d_h_init) {
+#pragma unroll
+        for (int i = 0; i < kScanCols; ++i) d_h_init[c.bh * pn4 + c.j40 + 64 * i] = g[i];
+    }
 }
 
 // PN % 256 == 0: a wave's 64 float4 columns belong to one (b,h); nw = PN / 256 waves per (b,h).
@@ -211,7 +311,19 @@ int launch_scan_bwd(const float* decay, const float* h_states, const float* grad
     const bool vec = (PN % 256 == 0) &&
                      ((reinterpret_cast<uintptr_t>(h_states) | reinterpret_cast<uintptr_t>(grad) |
                        reinterpret_cast<uintptr_t>(d_chunk) | reinterpret_cast<uintptr_t>(d_h_init)) % 16 == 0);
-    if (vec) {
+    if (vec && (PN / 4) % (64 * kScanCols) == 0) {
+        const int64_t cols = B * H * (PN / 4);
+        const int64_t waves = cols / (64 * kScanCols);
+        hipLaunchKernelGGL(scan_bwd_cols, dim3((unsigned)((waves + kScanBwdBlock / 64 - 1) / (kScanBwdBlock / 64))),
+                           dim3(kScanBwdBlock), 0, stream, decay,
+                           reinterpret_cast<const f32x4*>(h_states), reinterpret_cast<const f32x4*>(grad),
+                           reinterpret_cast<f32x4*>(d_chunk), reinterpret_cast<f32x4*>(d_h_init), workspace,
+                           (int)K, (int)H, (int)(PN / 4), cols);
+        const int64_t n = B * K * H;
+        hipLaunchKernelGGL(scan_bwd_reduce, dim3((unsigned)((n + kScanBwdBlock - 1) / kScanBwdBlock)),
+                           dim3(kScanBwdBlock), 0, stream, workspace, d_decay, (int)K, (int)H,
+                           (int)(PN / (256 * kScanCols)), n);
+    } else if (vec) {
         const int64_t cols = B * H * (PN / 4);
         hipLaunchKernelGGL(scan_bwd_vec4, dim3((unsigned)((cols + kScanBwdBlock - 1) / kScanBwdBlock)),
                            dim3(kScanBwdBlock), 0, stream, decay,
@@ -235,7 +347,14 @@ int launch_scan_fwd(const float* decay, const float* h_chunk, const float* h_ini
     const bool vec = (PN % 4 == 0) &&
                      ((reinterpret_cast<uintptr_t>(h_chunk) | reinterpret_cast<uintptr_t>(h_states) |
                        reinterpret_cast<uintptr_t>(h_init)) % 16 == 0);
-    if (vec) {
+    if (vec && (PN / 4) % (64 * kScanCols) == 0) {
+        const int64_t cols = B * H * (PN / 4);
+        const int64_t waves = cols / (64 * kScanCols);
+        hipLaunchKernelGGL(scan_fwd_cols, dim3((unsigned)((waves + kScanBlock / 64 - 1) / (kScanBlock / 64))),
+                           dim3(kScanBlock), 0, stream, decay, reinterpret_cast<const f32x4*>(h_chunk),
+                           reinterpret_cast<const f32x4*>(h_init), reinterpret_cast<f32x4*>(h_states),
+                           (int)K, (int)H, (int)(PN / 4), cols);
+    } else if (vec) {
         const int64_t cols = B * H * (PN / 4);
         const int64_t blocks = (cols + kScanBlock - 1) / kScanBlock;
         hipLaunchKernelGGL(scan_fwd_vec4, dim3((unsigned)blocks), dim3(kScanBlock), 0, stream,
