@@ -24,6 +24,7 @@ the same format:
                   decay (8, 128, 24), h_chunk (8, 128, 24, 64*128) and h_init, fp32: GB/s.
   scan_d2048      the same at the d_model 2048 shape: (2, 256, 32, 128*256).
   scan_bwd_d768   the scan's backward (m3_scan_bwd) at the scan_d768 shape: GB/s.
+  scan_bwd_d2048  the same at the scan_d2048 shape.
   ssd_bwd_d768    the chunked SSD's backward (m3_chunked_ssd_bwd, fp32) at the d_model 768
                   prefill shape (8, 8192): tokens/s, roofline over the call's GEMM FLOPs.
   layer_bwd_d768  the fp32 layer's backward (m3_layer_bwd) for x (4, 1024, 768): tokens/s
@@ -293,15 +294,15 @@ def bench_scan(args, torch, shape, name):
     ms = wall * 1e3 / args.steps
     nbytes = B * K * H * (PN * 8 + 4) + B * H * PN * 4
     gbs = nbytes / (kern_ms * 1e-3) / 1e9
-    traffic = recorded_traffic(ROOT / "profiles" / "scan_d768_trace_and_traffic.md", (name,))
+    traffic = recorded_traffic(ROOT / "profiles" / "scan_d768_d2048_trace_and_traffic.md", (name,))
     res = base_result(args, nbytes / (ms * 1e-3) / 1e9, ms,
                       f"ssd_scan (m3_scan_fwd), decay ({B}, {K}, {H}), h_chunk ({B}, {K}, {H}, {PN}) "
                       "and h_init, fp32, resident in HBM", B, K, dtype="fp32")
     res["unit"] = "GB/s"
     res["roofline"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                        "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic.get(name),
-                       "traffic_source": traffic_source(ROOT / "profiles" / "scan_d768_trace_and_traffic.md"),
-                       "kernel": "scan_fwd_vec4", "algorithmic_bytes": nbytes,
+                       "traffic_source": traffic_source(ROOT / "profiles" / "scan_d768_d2048_trace_and_traffic.md"),
+                       "kernel": "scan_fwd_cols (or scan_fwd_vec4)", "algorithmic_bytes": nbytes,
                        "avg_ms": round(kern_ms, 4)}
     if not args.no_cpu_baseline:
         from oracle import reference_path as ref
@@ -341,11 +342,11 @@ def bench_scan_bwd(args, torch, shape, name):
                       f"ssd_scan backward (m3_scan_bwd), states and gradient ({B}, {K}, {H}, {PN}), "
                       "fp32, resident in HBM", B, K, dtype="fp32")
     res["unit"] = "GB/s"
-    traffic = recorded_traffic(ROOT / "profiles" / "scan_d768_trace_and_traffic.md", (name,))
+    traffic = recorded_traffic(ROOT / "profiles" / "scan_d768_d2048_trace_and_traffic.md", (name,))
     res["roofline"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                        "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic.get(name),
-                       "traffic_source": traffic_source(ROOT / "profiles" / "scan_d768_trace_and_traffic.md"),
-                       "kernel": "scan_bwd_vec4 + scan_bwd_reduce", "algorithmic_bytes": nbytes,
+                       "traffic_source": traffic_source(ROOT / "profiles" / "scan_d768_d2048_trace_and_traffic.md"),
+                       "kernel": "scan_bwd_cols (or scan_bwd_vec4) + scan_bwd_reduce", "algorithmic_bytes": nbytes,
                        "avg_ms": round(kern_ms, 4)}
     if not args.no_cpu_baseline:
         from oracle import reference_path as ref
@@ -529,7 +530,9 @@ WORKLOADS = {"prefill_d2048": bench_prefill_d2048, "ssd_bwd_d768": bench_ssd_bwd
              "scan_d768": lambda args, torch, m: bench_scan(args, torch, (8, 128, 24, 8192), "scan_d768"),
              "scan_d2048": lambda args, torch, m: bench_scan(args, torch, (2, 256, 32, 32768), "scan_d2048"),
              "scan_bwd_d768": lambda args, torch, m: bench_scan_bwd(args, torch, (8, 128, 24, 8192),
-                                                                    "scan_bwd_d768")}
+                                                                    "scan_bwd_d768"),
+             "scan_bwd_d2048": lambda args, torch, m: bench_scan_bwd(args, torch, (2, 256, 32, 32768),
+                                                                     "scan_bwd_d2048")}
 
 
 SETTLE_S = 0.5
