@@ -11,8 +11,9 @@
 // columns 64 apart, so a wave's loads of one k cover kScanCols KiB contiguous. Loads of
 // consecutive k of one column lie H*PN*4 bytes apart, a power of two for the usual
 // shapes (4 MiB at 32 heads x 256 x 128), and a burst of them measured 20% slower at that
-// stride (the older one-column-per-lane kernels, kept for rows that are not a multiple of
-// 64 * kScanCols float4 columns, issue kScanUnroll k ahead).
+// stride. The older one-column-per-lane kernels (kScanUnroll k ahead) serve rows that are
+// not a multiple of 64 * kScanCols float4 columns, and problems too small to give the
+// column-blocked kernels two waves per CU.
 #include "m3_common.h"
 #include "m3_kernels.h"
 #include "m3_mfma.h"
@@ -22,6 +23,11 @@ namespace m3 {
 constexpr int kScanUnroll = 8;
 constexpr int kScanBlock = 256;
 constexpr int kScanCols = 8;  // float4 columns per lane of the column-blocked kernels
+// The column-blocked kernels run when they still give every CU two waves (512 waves of
+// 64 x kScanCols columns); below that the one-column-per-lane kernels keep more loads in
+// flight (backward at (4, 33, 24, 8192), 384 waves: 56 against 82 us; at (8, 128, 24,
+// 8192), 768 waves: 0.461 against 0.415 ms the other way).
+constexpr int64_t kScanColsMin = 512 * 64 * kScanCols;
 
 // A wave's columns: 64 * kScanCols consecutive float4 columns of one (b, h) row; lane l
 // owns j4 = j40 + 64 c, c < kScanCols.
@@ -311,7 +317,7 @@ int launch_scan_bwd(const float* decay, const float* h_states, const float* grad
     const bool vec = (PN % 256 == 0) &&
                      ((reinterpret_cast<uintptr_t>(h_states) | reinterpret_cast<uintptr_t>(grad) |
                        reinterpret_cast<uintptr_t>(d_chunk) | reinterpret_cast<uintptr_t>(d_h_init)) % 16 == 0);
-    if (vec && (PN / 4) % (64 * kScanCols) == 0) {
+    if (vec && (PN / 4) % (64 * kScanCols) == 0 && B * H * (PN / 4) >= kScanColsMin) {
         const int64_t cols = B * H * (PN / 4);
         const int64_t waves = cols / (64 * kScanCols);
         hipLaunchKernelGGL(scan_bwd_cols, dim3((unsigned)((waves + kScanBwdBlock / 64 - 1) / (kScanBwdBlock / 64))),
@@ -347,7 +353,7 @@ int launch_scan_fwd(const float* decay, const float* h_chunk, const float* h_ini
     const bool vec = (PN % 4 == 0) &&
                      ((reinterpret_cast<uintptr_t>(h_chunk) | reinterpret_cast<uintptr_t>(h_states) |
                        reinterpret_cast<uintptr_t>(h_init)) % 16 == 0);
-    if (vec && (PN / 4) % (64 * kScanCols) == 0) {
+    if (vec && (PN / 4) % (64 * kScanCols) == 0 && B * H * (PN / 4) >= kScanColsMin) {
         const int64_t cols = B * H * (PN / 4);
         const int64_t waves = cols / (64 * kScanCols);
         hipLaunchKernelGGL(scan_fwd_cols, dim3((unsigned)((waves + kScanBlock / 64 - 1) / (kScanBlock / 64))),

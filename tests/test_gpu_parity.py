@@ -217,7 +217,7 @@ def test_lm_decode_graph_replays_equal_eager_steps(cuda_device):
 
 # ------------------------------------------------------------------ scan
 @pytest.mark.parametrize("shape", [(2, 4, 3, 8), (2, 7, 3, 10), (1, 33, 2, 32768), (8, 16, 24, 8192),
-                                   (1, 1, 2, 2048), (2, 5, 3, 1024)])
+                                   (1, 3, 2, 1 << 20), (1, 1, 2, 1 << 20)])
 @pytest.mark.parametrize("with_init", [True, False])
 def test_scan_matches_closed_form(shape, with_init, cuda_device):
     B, K, H, PN = shape
@@ -236,13 +236,14 @@ def test_scan_matches_closed_form(shape, with_init, cuda_device):
 
 
 @pytest.mark.parametrize("shape", [(2, 7, 3, 512), (2, 9, 3, 100), (1, 33, 2, 1024),
-                                   (8, 16, 24, 8192), (1, 1, 2, 256), (2, 5, 3, 2048),
-                                   (1, 1, 2, 2048)])
+                                   (8, 16, 24, 8192), (1, 1, 2, 256), (1, 3, 2, 1 << 20),
+                                   (1, 1, 2, 1 << 20)])
 @pytest.mark.parametrize("with_init", [True, False])
 def test_scan_backward_matches_oracle(shape, with_init, cuda_device):
-    """ssd_scan's backward (m3_scan_bwd: eight float4 columns per lane for PN % 2048 == 0,
-    one for other PN % 256 == 0, the per-(b,h) block path otherwise) through autograd against
-    the oracle's backward (mamba3/scan.py:47-62)."""
+    """ssd_scan's backward (m3_scan_bwd: eight float4 columns per lane for PN % 2048 == 0 and
+    at least 262,144 float4 columns in all, one per lane for other PN % 256 == 0, the
+    per-(b,h) block path otherwise) through autograd against the oracle's backward
+    (mamba3/scan.py:47-62)."""
     B, K, H, PN = shape
     g = torch.Generator().manual_seed(K * 7 + PN)
     d = torch.rand(B, K, H, generator=g) * 0.5 + 0.5
