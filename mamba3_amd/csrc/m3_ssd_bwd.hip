@@ -161,31 +161,40 @@ struct Chunk {
     static constexpr int QB = 128 / R2 >= 64 ? 64 : 128 / R2;
     const Args* a;
     int b, k, h;
-    __device__ bool real(int t) const { return k * QB + t < a->s.T; }
-    __device__ float dtv(int t) const {
-        return real(t) ? a->dt[row(a->s, b, k * QB + t, h)] : 0.f;
+    // Token 0 of the chunk in every per-token array, the 32-bit element strides between
+    // consecutive tokens and the number of tokens below T: the GEMM operand fetches (one
+    // element each) are then a compare and two 24-bit multiply-adds.
+    int nt, tsP, tsN, tsH;
+    const float *xg0, *xb0, *bg0, *bb0, *c0, *dy0, *dt0;
+    __device__ Chunk(const Args* a_, int b_, int k_, int h_) : a(a_), b(b_), k(k_), h(h_) {
+        const Shape& s = a->s;
+        nt = min(QB, s.T - k * QB);
+        tsP = s.H * s.P * R;
+        tsN = s.H * s.N * R;
+        tsH = s.H;
+        const int64_t r0 = row(s, b, k * QB, h);
+        const int64_t oP = r0 * s.P * R, oN = r0 * s.N * R;
+        xg0 = a->xg + oP;
+        bg0 = a->Bg + oN;
+        xb0 = BETA ? a->xb + oP : nullptr;
+        bb0 = BETA ? a->Bb + oN : nullptr;
+        c0 = a->C + oN;
+        dy0 = a->dy ? a->dy + oP : nullptr;
+        dt0 = a->dt + r0;
     }
+    __device__ bool real(int t) const { return t < nt; }
+    __device__ float dtv(int t) const { return real(t) ? dt0[t * tsH] : 0.f; }
     // x factor j of token t (x_g for j < R, else x_b), without dt.
     __device__ float x(int t, int p, int j) const {
-        const Shape& s = a->s;
         if (!real(t)) return 0.f;
-        const float* base = j < R ? a->xg : a->xb;
-        return base[row(s, b, k * QB + t, h) * s.P * R + (int64_t)p * R + (j < R ? j : j - R)];
+        return j < R ? xg0[t * tsP + p * R + j] : xb0[t * tsP + p * R + (j - R)];
     }
     __device__ float bf(int t, int n, int j) const {
-        const Shape& s = a->s;
         if (!real(t)) return 0.f;
-        const float* base = j < R ? a->Bg : a->Bb;
-        return base[row(s, b, k * QB + t, h) * s.N * R + (int64_t)n * R + (j < R ? j : j - R)];
+        return j < R ? bg0[t * tsN + n * R + j] : bb0[t * tsN + n * R + (j - R)];
     }
-    __device__ float c(int t, int n, int r) const {
-        const Shape& s = a->s;
-        return real(t) ? a->C[row(s, b, k * QB + t, h) * s.N * R + (int64_t)n * R + r] : 0.f;
-    }
-    __device__ float dy(int t, int p, int r) const {
-        const Shape& s = a->s;
-        return real(t) ? a->dy[row(s, b, k * QB + t, h) * s.P * R + (int64_t)p * R + r] : 0.f;
-    }
+    __device__ float c(int t, int n, int r) const { return real(t) ? c0[t * tsN + n * R + r] : 0.f; }
+    __device__ float dy(int t, int p, int r) const { return real(t) ? dy0[t * tsP + p * R + r] : 0.f; }
 };
 
 // ---- K0: c_t (inclusive cumsum of A dt within the chunk) and the chunk decays.
