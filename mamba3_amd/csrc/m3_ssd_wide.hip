@@ -82,7 +82,7 @@ struct __align__(16) Smem {
     f16 S[ROWS][ROWS + PAD];
     f16 H[PB][N + PAD];
     Tok tok[2];           // by chunk parity
-    float phi[Q][N / 2];  // RoPE angle of each (token, pair) of the chunk being prepared
+    alignas(16) float phi[Q][N / 2];  // RoPE angle of each (token, pair) of the chunk being prepared
     u32x4 th[Q][N / 16];  // theta of that chunk, bf16, 8 pairs per entry
     float mz[PB][R], md[PB][R], mx[PB][R];  // mimo_z, mimo_down * sB sC sX, mimo_x / sX of the block's columns
     F16Scales scl;                          // operand scales of the (group, head)
@@ -368,18 +368,23 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
                        reinterpret_cast<uintptr_t>(a.proj) % 16 == 0;
 
     // ---- per-chunk inputs, read into registers at least a phase before they are used ----
-    // Rotation jobs: this thread's RoPE pair ri at tokens rt0 + m * TSTEP (m < J).
-    constexpr int J = (Q * NH + THREADS - 1) / THREADS;  // jobs at tokens below Q
-    constexpr int TSTEP = THREADS / NH;
-    const int ri = tid % NH, rt0 = tid / NH;
-    unsigned pwb[J][R], pwc[J][R];
+    // Rotation jobs: this thread's two adjacent RoPE pairs 2 ri, 2 ri + 1 at tokens
+    // rt0 + m * TSTEP (m < J), so each C~ / B~ row segment goes out as one 64-bit store.
+    constexpr int NP2 = NH / 2;
+    constexpr int J = (Q * NP2 + THREADS - 1) / THREADS;  // jobs at tokens below Q
+    constexpr int TSTEP = THREADS / NP2;
+    const int ri = tid % NP2, rt0 = tid / NP2;
+    unsigned pwb[J][2][R], pwc[J][2][R];
     auto load_bc = [&](int kk) {
 #pragma unroll
         for (int m = 0; m < J; ++m) {
             const int st = kk * Q + rt0 + m * TSTEP;
-            const int64_t off = (int64_t)min(st, T - 1) * nrs + 2 * ri * R;  // in range; zeroed when used
-            load_pair_words<R>(Bn + off, pwb[m]);
-            load_pair_words<R>(Cn + off, pwc[m]);
+            const int64_t off = (int64_t)min(st, T - 1) * nrs + 4 * ri * R;  // in range; zeroed when used
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                load_pair_words<R>(Bn + off + 2 * e * R, pwb[m][e]);
+                load_pair_words<R>(Cn + off + 2 * e * R, pwc[m][e]);
+            }
         }
     };
     // x of the X job (8 columns, raw bf16) and theta of the staging jobs.
@@ -495,22 +500,29 @@ __global__ __launch_bounds__(THREADS) void ssd_wide(Args a) {
 #pragma unroll
         for (int m = 0; m < J; ++m) {
             const int t = rt0 + m * TSTEP;
-            if (Q * NH % THREADS != 0 && t >= Q) break;  // threads past the chunk's jobs (small d_state)
+            if (Q * NP2 % THREADS != 0 && t >= Q) break;  // threads past the chunk's jobs (small d_state)
             // Tokens past the end get a zero factor, which zeroes their rows (the clamped
             // words they rotate are finite).
             const bool valid = s0 + t < T;
-            f16x2 kA = f16x2{(f16)1.f, (f16)0.f};
-            if (a.cplx) {
-                float sn, cs;
-                fast_sincos(sm.phi[t][ri], sn, cs);
-                kA = f16x2{(f16)cs, (f16)sn};
+            f16x2 kA[2], kS[2];
+            const f32x2 ph = a.cplx ? *reinterpret_cast<const f32x2*>(&sm.phi[t][2 * ri]) : f32x2{0.f, 0.f};
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                f16x2 k = f16x2{(f16)1.f, (f16)0.f};
+                if (a.cplx) {
+                    float sn, cs;
+                    fast_sincos(ph[e], sn, cs);
+                    k = f16x2{(f16)cs, (f16)sn};
+                }
+                kA[e] = as_f16x2(valid ? bits(k) : 0u);
+                kS[e] = __builtin_shufflevector(kA[e], kA[e], 1, 0);
             }
-            kA = as_f16x2(valid ? bits(kA) : 0u);
-            const f16x2 kS = __builtin_shufflevector(kA, kA, 1, 0);
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                *reinterpret_cast<unsigned*>(&sm.B[t * R + r][2 * ri]) = rotate_pair(pwb[m][r], kA, kS);
-                *reinterpret_cast<unsigned*>(&sm.C[t * R + r][2 * ri]) = rotate_pair(pwc[m][r], kA, kS);
+                *reinterpret_cast<u32x2*>(&sm.B[t * R + r][4 * ri]) =
+                    u32x2{rotate_pair(pwb[m][0][r], kA[0], kS[0]), rotate_pair(pwb[m][1][r], kA[1], kS[1])};
+                *reinterpret_cast<u32x2*>(&sm.C[t * R + r][4 * ri]) =
+                    u32x2{rotate_pair(pwc[m][0][r], kA[0], kS[0]), rotate_pair(pwc[m][1][r], kA[1], kS[1])};
             }
         }
         // X rows (t, r) = x_t * mimo_x[p, r] (mamba3/mamba3.py:210), and times w_t.
