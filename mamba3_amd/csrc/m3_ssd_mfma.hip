@@ -409,11 +409,12 @@ __device__ __forceinline__ void out_block(Smem& sm, const Tok& tk, int par, int 
 
 // Pipelined chunk walk, per chunk k:
 //   barrier A -> M(k): MFMA waves: state update G4 on chunk k's tiles, output block of
-//                chunk k, gated from the z tile. Helper waves: RoPE rotation, X rows and z of
-//                chunk k+1 (X rows and z straight into the buffers of the other parity),
-//                reads of chunk k+2 issued as registers free up.
-//   barrier B -> W(k+1): MFMA waves write the f16 state copy H_{k+1}; helper waves store
-//                chunk k's output and write the C~ / B~ tiles of chunk k+1.
+//                chunk k, gated from the z tile. Helper waves: chunk k-1's output to HBM,
+//                then RoPE rotation, X rows and z of chunk k+1 (X rows and z straight into
+//                the buffers of the other parity), reads of chunk k+2 issued as registers
+//                free up.
+//   barrier B -> W(k+1): MFMA waves write the f16 state copy H_{k+1}; helper waves write
+//                the C~ / B~ tiles of chunk k+1.
 // Roles (SIMD s runs waves s, s+4, s+8, s+12):
 //   MFMA wave w < 8: state rows n = 16w .. 16w+15; output block w (w < 4) or 11-w, so
 //                each SIMD carries blocks {s, 7-s} (the same causal work); wave 0 also
@@ -972,7 +973,7 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
                 M3_LDS_FENCE();
             }
         };
-        // ---- W phase: chunk kk's output (its z tile, overwritten by the MFMA waves) to HBM
+        // ---- chunk kk's output (its z tile, overwritten by the MFMA waves) to HBM
         auto store_out = [&](int kk) {
             const int lane = opaque(threadIdx.x & 63);
             const int t = 8 * hw + (lane >> 3), p = 8 * (lane & 7);
@@ -1003,6 +1004,10 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
         for (int k = k_begin; k < k_end; ++k) {
             const bool more = k + 1 < k_end;
             __syncthreads();
+            // chunk k-1's output (gated in its z tile by the MFMA waves in M(k-1)) to HBM,
+            // first thing in M(k): stage_z below then overwrites the same lane's entries of
+            // that z tile with chunk k+1's z
+            if (kFull && k > k_begin) store_out(k - 1);
             if (more) {
                 // B^ / C^ of chunk k+1 (shared by all heads of the batch row, mostly L2
                 // hits) are read now and rotated last; x, z and theta are a chunk ahead.
@@ -1020,11 +1025,11 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_chunks(Args a) {
                 prep(k + 1, k + 2);
             }
             __syncthreads();
-            if (kFull) store_out(k);
             if (more) write_tiles();
         }
-        // ---- segment end (helper waves: per-pair angles)
+        // ---- segment end (helper waves: the last chunk's output, per-pair angles)
         __syncthreads();
+        if (kFull) store_out(k_end - 1);
         if (!kFull) {
             const int64_t sidx = (int64_t)bh * (a.S - 1) + seg;
             if (pair_lane) {
