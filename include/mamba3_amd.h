@@ -163,7 +163,7 @@ int m3_scan_bwd(const float* decay, const float* h_states, const float* grad, fl
                 int64_t batch, int64_t nchunks, int64_t nheads, int64_t pn, void* stream);
 
 /*
- * Backward of m3_prefill_fwd for fp32 layers (desc->dtype fp32, mimo_rank 1/2/4/8), from the
+ * Backward of m3_prefill_fwd for fp32 layers (desc->dtype fp32, mimo_rank 1..8), from the
  * workspace of that forward call, which holds its intermediates (pass the same buffer, unchanged,
  * with its size; that forward ran with M3_FLAG_FOR_BACKWARD in desc->flags, as does this call). Replaces the reference's autograd through mamba3/mamba3.py:197-256 (ATen's
  * backward of the dt softplus, the B/C RMSNorm + bias, the RoPE rotation and its angle cumsum,

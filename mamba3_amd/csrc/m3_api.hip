@@ -57,7 +57,7 @@ int check_scan_bwd_shape(int64_t batch, int64_t nchunks, int64_t nheads, int64_t
 // fused fp32 kernel
 // (fp32, d_state 128 / headdim 64 / rank 2; under M3_FLAG_FOR_BACKWARD it also writes the
 // staged operands of the layer backward into the fp32 layer workspace), the fp32 layer path
-// on the fp32-MFMA chunk kernels (fp32, rank 1/2/4/8) or the generic one.
+// on the fp32-MFMA chunk kernels (fp32, rank 1..8) or the generic one.
 enum class PrefillPath { kMfma, kWide, kFp32Fused, kFp32FusedTrain, kFp32, kGeneric };
 
 PrefillPath prefill_path(const m3_layer_desc& d, const void* proj, const void* y_out,

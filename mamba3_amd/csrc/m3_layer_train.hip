@@ -258,10 +258,11 @@ __global__ __launch_bounds__(NTH) void tb_x(Args a) {
 // partials, the reduction scratch.
 __device__ __forceinline__ int bc_hs(int N) { return max(1, NTH / (N / 2)); }
 
-// The 2R values of pair i (even column, ranks 0..R-1, then odd column) are contiguous and
-// 8R-byte aligned: one vector load per array.
+// The K = 2R values of pair i (even column, ranks 0..R-1, then odd column) are contiguous
+// and 8R-byte aligned: 16-byte loads when R is even, else 8-byte ones.
 template <int K>
 __device__ __forceinline__ void ldv(const float* p, float (&v)[K]) {
+    static_assert(K % 2 == 0, "pairs hold an even number of values");
     if constexpr (K % 4 == 0) {
 #pragma unroll
         for (int j = 0; j < K / 4; ++j) {
@@ -270,9 +271,12 @@ __device__ __forceinline__ void ldv(const float* p, float (&v)[K]) {
             for (int k = 0; k < 4; ++k) v[4 * j + k] = q[k];
         }
     } else {
-        const f32x2 q = *reinterpret_cast<const f32x2*>(p);
-        v[0] = q[0];
-        v[1] = q[1];
+#pragma unroll
+        for (int j = 0; j < K / 2; ++j) {
+            const f32x2 q = *reinterpret_cast<const f32x2*>(p + 2 * j);
+            v[2 * j] = q[0];
+            v[2 * j + 1] = q[1];
+        }
     }
 }
 
@@ -660,8 +664,13 @@ int launch_layer_bwd(const m3_layer_desc& d, const m3_layer_params& p, const voi
     switch (a.R) {
         case 1: hipLaunchKernelGGL(tb_bc<1>, gbc, dim3(NTH), bc_lds(d), stream, a); break;
         case 2: hipLaunchKernelGGL(tb_bc<2>, gbc, dim3(NTH), bc_lds(d), stream, a); break;
+        case 3: hipLaunchKernelGGL(tb_bc<3>, gbc, dim3(NTH), bc_lds(d), stream, a); break;
         case 4: hipLaunchKernelGGL(tb_bc<4>, gbc, dim3(NTH), bc_lds(d), stream, a); break;
-        default: hipLaunchKernelGGL(tb_bc<8>, gbc, dim3(NTH), bc_lds(d), stream, a); break;
+        case 5: hipLaunchKernelGGL(tb_bc<5>, gbc, dim3(NTH), bc_lds(d), stream, a); break;
+        case 6: hipLaunchKernelGGL(tb_bc<6>, gbc, dim3(NTH), bc_lds(d), stream, a); break;
+        case 7: hipLaunchKernelGGL(tb_bc<7>, gbc, dim3(NTH), bc_lds(d), stream, a); break;
+        case 8: hipLaunchKernelGGL(tb_bc<8>, gbc, dim3(NTH), bc_lds(d), stream, a); break;
+        default: return 1;
     }
     if (a.cplx) {
         const int nc = (a.T + kAC - 1) / kAC;

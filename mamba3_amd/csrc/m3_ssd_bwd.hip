@@ -24,7 +24,9 @@
 //                - q_t + [t = Qb-1] (sum_s q_s + exp(c_end) <dH, H_k>),
 //                Z = sum_{r,j} G o DX,  q_s = sum_{p,j} Xf[s,p,j] (state term of dXf)[s,p,j]
 //   d(A dt_t)  = sum_{t'>=t} dc_t';  ddt_t = A d(A dt_t) + sum_{p,j} dXf[s,p,j] x[s,p,j]
-// Qb = 64 / R2 (a power of two), so that the score tiles are at most 128 x 128. The chunk
+// Qb = min(64, 128 / R2), so that the score tiles are at most 128 x 128. R here is the rank
+// of the tiles, a power of two: ranks 3, 5, 6 and 7 run on tiles of rank 4 or 8 whose extra
+// slots read as zero (their rows and columns of G, DX, M and DM are zero). The chunk
 // states H_k and dH come from the state scan kernels over K+1 chunks, the last one carrying
 // dL/dh_final. Every sum runs in a fixed order: results are deterministic.
 #include <hip/hip_runtime.h>
@@ -40,10 +42,11 @@ constexpr int KT = 16;    // contraction step
 constexpr int NTH = 256;  // threads per tile block
 constexpr int TW = 128;   // wide output tile (columns over N or the score columns)
 
+// R: the arrays' rank; RT: the rank of the tiles (R rounded up to 1, 2, 4 or 8).
 struct Shape {
-    int B, T, H, P, N, R, R2, Qb, K, nPt, nNt;
+    int B, T, H, P, N, R, RT, R2, Qb, K, nPt, nNt;
     int64_t PN;
-    int QR() const { return Qb * R; }
+    int QR() const { return Qb * RT; }
     int QR2() const { return Qb * R2; }
 };
 
@@ -154,8 +157,11 @@ __device__ __forceinline__ void zero(f32x4 (&acc)[NJ]) {
     for (int j = 0; j < NJ; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
 }
 
-// Accessors of chunk (b, k, h). Token positions at or past T read as 0.
-template <int R, bool BETA>
+// Accessors of chunk (b, k, h). Token positions at or past T read as 0. R is the rank of
+// the tiles; with PADR the arrays hold a smaller rank s.R (3 for R = 4; 5, 6 or 7 for R = 8)
+// and the tile slots of the missing ranks read as 0, so every score, state and output term
+// of the real ranks is the unpadded one, and the kernels store nothing for those slots.
+template <int R, bool BETA, bool PADR>
 struct Chunk {
     static constexpr int R2 = BETA ? 2 * R : R;
     static constexpr int QB = 128 / R2 >= 64 ? 64 : 128 / R2;
@@ -164,16 +170,17 @@ struct Chunk {
     // Token 0 of the chunk in every per-token array, the 32-bit element strides between
     // consecutive tokens and the number of tokens below T: the GEMM operand fetches (one
     // element each) are then a compare and two 24-bit multiply-adds.
-    int nt, tsP, tsN, tsH;
+    int nt, tsP, tsN, tsH, ra;
     const float *xg0, *xb0, *bg0, *bb0, *c0, *dy0, *dt0;
     __device__ Chunk(const Args* a_, int b_, int k_, int h_) : a(a_), b(b_), k(k_), h(h_) {
         const Shape& s = a->s;
+        ra = PADR ? s.R : R;
         nt = min(QB, s.T - k * QB);
-        tsP = s.H * s.P * R;
-        tsN = s.H * s.N * R;
+        tsP = s.H * s.P * rk();
+        tsN = s.H * s.N * rk();
         tsH = s.H;
         const int64_t r0 = row(s, b, k * QB, h);
-        const int64_t oP = r0 * s.P * R, oN = r0 * s.N * R;
+        const int64_t oP = r0 * s.P * rk(), oN = r0 * s.N * rk();
         xg0 = a->xg + oP;
         bg0 = a->Bg + oN;
         xb0 = BETA ? a->xb + oP : nullptr;
@@ -182,23 +189,36 @@ struct Chunk {
         dy0 = a->dy ? a->dy + oP : nullptr;
         dt0 = a->dt + r0;
     }
+    // The arrays' rank (R unless PADR).
+    __device__ int rk() const {
+        if constexpr (PADR) return ra;
+        return R;
+    }
+    // Whether rank slot r (< R) of the tiles holds a real rank.
+    __device__ bool has(int r) const { return !PADR || r < rk(); }
     __device__ bool real(int t) const { return t < nt; }
     __device__ float dtv(int t) const { return real(t) ? dt0[t * tsH] : 0.f; }
-    // x factor j of token t (x_g for j < R, else x_b), without dt.
+    // x factor j of token t (x_g rank j for j < R, else x_b rank j - R), without dt.
     __device__ float x(int t, int p, int j) const {
-        if (!real(t)) return 0.f;
-        return j < R ? xg0[t * tsP + p * R + j] : xb0[t * tsP + p * R + (j - R)];
+        const int r = j < R ? j : j - R;
+        if (!real(t) || !has(r)) return 0.f;
+        return (j < R ? xg0 : xb0)[t * tsP + p * rk() + r];
     }
     __device__ float bf(int t, int n, int j) const {
-        if (!real(t)) return 0.f;
-        return j < R ? bg0[t * tsN + n * R + j] : bb0[t * tsN + n * R + (j - R)];
+        const int r = j < R ? j : j - R;
+        if (!real(t) || !has(r)) return 0.f;
+        return (j < R ? bg0 : bb0)[t * tsN + n * rk() + r];
     }
-    __device__ float c(int t, int n, int r) const { return real(t) ? c0[t * tsN + n * R + r] : 0.f; }
-    __device__ float dy(int t, int p, int r) const { return real(t) ? dy0[t * tsP + p * R + r] : 0.f; }
+    __device__ float c(int t, int n, int r) const {
+        return real(t) && has(r) ? c0[t * tsN + n * rk() + r] : 0.f;
+    }
+    __device__ float dy(int t, int p, int r) const {
+        return real(t) && has(r) ? dy0[t * tsP + p * rk() + r] : 0.f;
+    }
 };
 
 // ---- K0: c_t (inclusive cumsum of A dt within the chunk) and the chunk decays.
-template <int R, bool BETA>
+template <int R, bool BETA, bool PADR>
 __global__ __launch_bounds__(64) void bwd_cum(Args a) {
     BW_CONSTS
     const Shape& s = a.s;
@@ -217,7 +237,7 @@ __global__ __launch_bounds__(64) void bwd_cum(Args a) {
 //   hext[k][p,n] = sum_{s,j} exp(c_end - c_s) Xf[s,p,j] Bf[s,n,j]
 //   gext[k][p,n] = sum_{t,r} exp(c_t) dy[t,p,r] C[t,n,r]
 // plus the extra chunk K: hext = 0, gext = dL/dh_final (or 0). Tiles of 64 p x 128 n.
-template <int R, bool BETA>
+template <int R, bool BETA, bool PADR>
 __global__ __launch_bounds__(NTH) void bwd_states(Args a) {
     BW_CONSTS
     __shared__ Lds<TW> l;
@@ -226,7 +246,7 @@ __global__ __launch_bounds__(NTH) void bwd_states(Args a) {
     const int ch = blockIdx.x, h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
     const int pt = blockIdx.y / s.nNt, nt = blockIdx.y % s.nNt;
     const int p0 = pt * TT, n0 = nt * TW;
-    const Chunk<R, BETA> q{&a, b, k, h};
+    const Chunk<R, BETA, PADR> q{&a, b, k, h};
     if (threadIdx.x < QB) cs[threadIdx.x] = a.cum[(int64_t)ch * QB + threadIdx.x];
     __syncthreads();
     if (threadIdx.x < QB) {  // per-token weights of the two contractions
@@ -299,7 +319,7 @@ __global__ __launch_bounds__(NTH) void bwd_states(Args a) {
 // ---- K1: masked scores M = W o G and DM = W o DX of the chunk, and the intra-chunk part of
 // dc: sum_s W Z[t,s] - sum_t' W Z[t',t]. One block per chunk, looping over its 64 x 128 tiles;
 // W o G waits in LDS while DX is formed.
-template <int R, bool BETA>
+template <int R, bool BETA, bool PADR>
 __global__ __launch_bounds__(NTH) void bwd_scores(Args a) {
     BW_CONSTS
     __shared__ Lds<TW> l;
@@ -307,7 +327,7 @@ __global__ __launch_bounds__(NTH) void bwd_scores(Args a) {
     __shared__ float cs[64], dts[64], rowacc[64], colacc[64];
     const Shape& s = a.s;
     const int ch = blockIdx.x, h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
-    const Chunk<R, BETA> q{&a, b, k, h};
+    const Chunk<R, BETA, PADR> q{&a, b, k, h};
     const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
     if (tid < 64) {
         cs[tid] = tid < QB ? a.cum[(int64_t)ch * QB + tid] : 0.f;
@@ -405,7 +425,7 @@ __device__ __forceinline__ void tile_token_sums(const float (&v)[4], int per, fl
 
 // ---- K3: dXf rows (s,j) x columns p; writes dx_g / dx_b = dt_s dXf and the per-token
 // partials q_s (state term . Xf) and sum_{p,j} dXf x.
-template <int R, bool BETA>
+template <int R, bool BETA, bool PADR>
 __global__ __launch_bounds__(NTH, 4) void bwd_dxf(Args a) {
     BW_CONSTS
     __shared__ Lds<TT> l;
@@ -415,7 +435,7 @@ __global__ __launch_bounds__(NTH, 4) void bwd_dxf(Args a) {
     const int ch = blockIdx.x, h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
     const int rt = blockIdx.y / s.nPt, pt = blockIdx.y % s.nPt;
     const int m0 = rt * TT, p0 = pt * TT;
-    const Chunk<R, BETA> q{&a, b, k, h};
+    const Chunk<R, BETA, PADR> q{&a, b, k, h};
     const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
     if (tid < QB) cs[tid] = a.cum[(int64_t)ch * QB + tid];
     __syncthreads();
@@ -457,14 +477,15 @@ __global__ __launch_bounds__(NTH, 4) void bwd_dxf(Args a) {
         const int m = m0 + 4 * ty + i, t = m / R2, j = m % R2;
         const float d = q.dtv(t);
         rv[i] = 0.f;
-        const bool w = q.real(t);
+        const int jr = j < R ? j : j - R;
+        const bool w = q.real(t) && q.has(jr);
         float* out = j < R ? a.dxg : a.dxb;
-        const int64_t base = row(s, b, k * QB + t, h) * s.P * R + (j < R ? j : j - R);
+        const int64_t base = row(s, b, k * QB + t, h) * s.P * q.rk() + jr;
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
             const int p = p0 + tcol(tx, jj);
             rv[i] += acc[jj][i] * xv[i][jj];
-            if (w && p < s.P) out[base + (int64_t)p * R] = d * acc[jj][i];
+            if (w && p < s.P) out[base + (int64_t)p * q.rk()] = d * acc[jj][i];
         }
     }
     tile_token_sums(rv, per, red, outv);
@@ -472,7 +493,7 @@ __global__ __launch_bounds__(NTH, 4) void bwd_dxf(Args a) {
 }
 
 // ---- K4: dBf rows (s,j) x columns n; writes dB_g / dB_b.
-template <int R, bool BETA>
+template <int R, bool BETA, bool PADR>
 __global__ __launch_bounds__(NTH, 4) void bwd_dbf(Args a) {
     BW_CONSTS
     __shared__ Lds<TW> l;
@@ -482,7 +503,7 @@ __global__ __launch_bounds__(NTH, 4) void bwd_dbf(Args a) {
     const int rt = blockIdx.y / s.nNt, nt = blockIdx.y % s.nNt;
     const int m0 = rt * TT, n0 = nt * TW;
     constexpr int NJ = TW / 16;
-    const Chunk<R, BETA> q{&a, b, k, h};
+    const Chunk<R, BETA, PADR> q{&a, b, k, h};
     const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
     if (tid < QB) {
         cs[tid] = a.cum[(int64_t)ch * QB + tid];
@@ -517,19 +538,20 @@ __global__ __launch_bounds__(NTH, 4) void bwd_dbf(Args a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int m = m0 + 4 * ty + i, t = m / R2, j = m % R2;
-        if (!q.real(t)) continue;
+        const int jr = j < R ? j : j - R;
+        if (!q.real(t) || !q.has(jr)) continue;
         float* out = j < R ? a.dBg : a.dBb;
-        const int64_t base = row(s, b, k * QB + t, h) * s.N * R + (j < R ? j : j - R);
+        const int64_t base = row(s, b, k * QB + t, h) * s.N * q.rk() + jr;
 #pragma unroll
         for (int jj = 0; jj < NJ; ++jj) {
             const int n = n0 + tcol(tx, jj);
-            if (n < s.N) out[base + (int64_t)n * R] = acc[jj][i];
+            if (n < s.N) out[base + (int64_t)n * q.rk()] = acc[jj][i];
         }
     }
 }
 
 // ---- K5: dC rows (t,r) x columns n, and the per-token partials sum_{n,r} C dC_inter.
-template <int R, bool BETA>
+template <int R, bool BETA, bool PADR>
 __global__ __launch_bounds__(NTH) void bwd_dc(Args a) {
     BW_CONSTS
     __shared__ Lds<TW> l;
@@ -540,7 +562,7 @@ __global__ __launch_bounds__(NTH) void bwd_dc(Args a) {
     const int rt = blockIdx.y / s.nNt, nt = blockIdx.y % s.nNt;
     const int m0 = rt * TT, n0 = nt * TW;
     constexpr int NJ = TW / 16;
-    const Chunk<R, BETA> q{&a, b, k, h};
+    const Chunk<R, BETA, PADR> q{&a, b, k, h};
     const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
     if (tid < QB) cs[tid] = a.cum[(int64_t)ch * QB + tid];
     __syncthreads();
@@ -578,25 +600,25 @@ __global__ __launch_bounds__(NTH) void bwd_dc(Args a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int m = m0 + 4 * ty + i, t = m / R, r = m % R;
-        if (!q.real(t)) continue;
-        const int64_t base = row(s, b, k * QB + t, h) * s.N * R + r;
+        if (!q.real(t) || !q.has(r)) continue;
+        const int64_t base = row(s, b, k * QB + t, h) * s.N * q.rk() + r;
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
             const int n = n0 + tcol(tx, j);
-            if (n < s.N) a.dC[base + (int64_t)n * R] = acc[j][i];
+            if (n < s.N) a.dC[base + (int64_t)n * q.rk()] = acc[j][i];
         }
     }
 }
 
 // ---- K6: per chunk: dc -> d(A dt) (suffix sums), ddt, the chunk's partials of dA and dD,
 // and dx_raw = D dy.
-template <int R, bool BETA>
+template <int R, bool BETA, bool PADR>
 __global__ __launch_bounds__(NTH) void bwd_tokens(Args a) {
     BW_CONSTS
     __shared__ float dcs[64], part[NTH];
     const Shape& s = a.s;
     const int ch = blockIdx.x, h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
-    const Chunk<R, BETA> q{&a, b, k, h};
+    const Chunk<R, BETA, PADR> q{&a, b, k, h};
     const int tid = threadIdx.x;
     if (tid < 64) {
         const int t = tid;
@@ -631,7 +653,7 @@ __global__ __launch_bounds__(NTH) void bwd_tokens(Args a) {
     // dD partial and dx_raw over the chunk's real tokens.
     const float Dh = a.D[h];
     const int nreal = min(QB, s.T - k * QB);
-    const int per_tok = s.P * R;
+    const int per_tok = s.P * q.rk();
     float v = 0.f;
     for (int e = tid; e < nreal * per_tok; e += NTH) {
         const int t = e / per_tok, pr = e % per_tok;
@@ -678,7 +700,7 @@ __global__ __launch_bounds__(NTH) void bwd_reduce(Args a) {
 
 // ---- forward output: y rows (t,r) x columns p of the chunk,
 //   y = (W o G) Xf + exp(c_t) C H_k^T + D x_raw   (M = W o G from bwd_scores in forward mode)
-template <int R, bool BETA>
+template <int R, bool BETA, bool PADR>
 __global__ __launch_bounds__(NTH, 4) void fwd_out(Args a) {
     BW_CONSTS
     __shared__ Lds<TT> l;
@@ -687,7 +709,7 @@ __global__ __launch_bounds__(NTH, 4) void fwd_out(Args a) {
     const int ch = blockIdx.x, h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
     const int rt = blockIdx.y / s.nPt, pt = blockIdx.y % s.nPt;
     const int m0 = rt * TT, p0 = pt * TT;
-    const Chunk<R, BETA> q{&a, b, k, h};
+    const Chunk<R, BETA, PADR> q{&a, b, k, h};
     const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
     if (tid < QB) {
         cs[tid] = a.cum[(int64_t)ch * QB + tid];
@@ -722,12 +744,12 @@ __global__ __launch_bounds__(NTH, 4) void fwd_out(Args a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int m = m0 + 4 * ty + i, t = m / R, r = m % R;
-        if (!q.real(t)) continue;
-        const int64_t base = row(s, b, k * QB + t, h) * s.P * R + r;
+        if (!q.real(t) || !q.has(r)) continue;
+        const int64_t base = row(s, b, k * QB + t, h) * s.P * q.rk() + r;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int p = p0 + tcol(tx, j);
-            if (p < s.P) a.y[base + (int64_t)p * R] = acc[j][i] + Dh * a.xr[base + (int64_t)p * R];
+            if (p < s.P) a.y[base + (int64_t)p * q.rk()] = acc[j][i] + Dh * a.xr[base + (int64_t)p * q.rk()];
         }
     }
 }
@@ -751,8 +773,9 @@ struct Plan {
 inline size_t al(size_t x) { return (x + 255) & ~(size_t)255; }
 
 bool make_shape(int B, int T, int H, int P, int N, int R, bool beta, Shape& s) {
-    if (R != 1 && R != 2 && R != 4 && R != 8) return false;
-    s.B = B, s.T = T, s.H = H, s.P = P, s.N = N, s.R = R, s.R2 = beta ? 2 * R : R;
+    if (R < 1 || R > 8) return false;
+    const int RT = R <= 2 ? R : R <= 4 ? 4 : 8;
+    s.B = B, s.T = T, s.H = H, s.P = P, s.N = N, s.R = R, s.RT = RT, s.R2 = beta ? 2 * RT : RT;
     s.Qb = 128 / s.R2 >= 64 ? 64 : 128 / s.R2;  // as BW_CONSTS
     s.K = (T + s.Qb - 1) / s.Qb;
     s.nPt = (P + TT - 1) / TT;
@@ -788,23 +811,23 @@ Plan make_plan(const Shape& s) {
     return pl;
 }
 
-template <int R, bool BETA>
+template <int R, bool BETA, bool PADR>
 int launch(const Args& a, const float* h_init, float* dh_init, float* scan_ws, hipStream_t stream) {
     BW_CONSTS
     const Shape& s = a.s;
     const unsigned nch = (unsigned)((int64_t)s.B * s.K * s.H);
     constexpr int nRt = QR / TT, nRt2 = QR2 / TT;
-    hipLaunchKernelGGL((bwd_cum<R, BETA>), dim3(nch), dim3(64), 0, stream, a);
-    hipLaunchKernelGGL((bwd_states<R, BETA>), dim3(nch, s.nPt * s.nNt), dim3(NTH), 0, stream, a);
+    hipLaunchKernelGGL((bwd_cum<R, BETA, PADR>), dim3(nch), dim3(64), 0, stream, a);
+    hipLaunchKernelGGL((bwd_states<R, BETA, PADR>), dim3(nch, s.nPt * s.nNt), dim3(NTH), 0, stream, a);
     if (launch_scan_fwd(a.dec, a.hext, h_init, a.Hs, s.B, s.K + 1, s.H, s.PN, stream) != 0) return 1;
     if (launch_scan_bwd(a.dec, a.Hs, a.gext, a.ddec, a.dch, dh_init, scan_ws, s.B, s.K + 1, s.H,
                         s.PN, stream) != 0)
         return 1;
-    hipLaunchKernelGGL((bwd_scores<R, BETA>), dim3(nch), dim3(NTH), 0, stream, a);
-    hipLaunchKernelGGL((bwd_dxf<R, BETA>), dim3(nch, nRt2 * s.nPt), dim3(NTH), 0, stream, a);
-    hipLaunchKernelGGL((bwd_dbf<R, BETA>), dim3(nch, nRt2 * s.nNt), dim3(NTH), 0, stream, a);
-    hipLaunchKernelGGL((bwd_dc<R, BETA>), dim3(nch, nRt * s.nNt), dim3(NTH), 0, stream, a);
-    hipLaunchKernelGGL((bwd_tokens<R, BETA>), dim3(nch), dim3(NTH), 0, stream, a);
+    hipLaunchKernelGGL((bwd_scores<R, BETA, PADR>), dim3(nch), dim3(NTH), 0, stream, a);
+    hipLaunchKernelGGL((bwd_dxf<R, BETA, PADR>), dim3(nch, nRt2 * s.nPt), dim3(NTH), 0, stream, a);
+    hipLaunchKernelGGL((bwd_dbf<R, BETA, PADR>), dim3(nch, nRt2 * s.nNt), dim3(NTH), 0, stream, a);
+    hipLaunchKernelGGL((bwd_dc<R, BETA, PADR>), dim3(nch, nRt * s.nNt), dim3(NTH), 0, stream, a);
+    hipLaunchKernelGGL((bwd_tokens<R, BETA, PADR>), dim3(nch), dim3(NTH), 0, stream, a);
     hipLaunchKernelGGL(bwd_reduce, dim3(s.H), dim3(NTH), 0, stream, a);
     return hipGetLastError() == hipSuccess ? 0 : 1;
 }
@@ -825,17 +848,17 @@ Plan make_plan_fwd(const Shape& s) {
     return pl;
 }
 
-template <int R, bool BETA>
+template <int R, bool BETA, bool PADR>
 int launch_fwd(const Args& a, const float* h_init, hipStream_t stream) {
     BW_CONSTS
     const Shape& s = a.s;
     const unsigned nch = (unsigned)((int64_t)s.B * s.K * s.H);
     constexpr int nRt = QR / TT;
-    hipLaunchKernelGGL((bwd_cum<R, BETA>), dim3(nch), dim3(64), 0, stream, a);
-    hipLaunchKernelGGL((bwd_states<R, BETA>), dim3(nch, s.nPt * s.nNt), dim3(NTH), 0, stream, a);
+    hipLaunchKernelGGL((bwd_cum<R, BETA, PADR>), dim3(nch), dim3(64), 0, stream, a);
+    hipLaunchKernelGGL((bwd_states<R, BETA, PADR>), dim3(nch, s.nPt * s.nNt), dim3(NTH), 0, stream, a);
     if (launch_scan_fwd(a.dec, a.hext, h_init, a.Hs, s.B, s.K + 1, s.H, s.PN, stream) != 0) return 1;
-    hipLaunchKernelGGL((bwd_scores<R, BETA>), dim3(nch), dim3(NTH), 0, stream, a);
-    hipLaunchKernelGGL((fwd_out<R, BETA>), dim3(nch, nRt * s.nPt), dim3(NTH), 0, stream, a);
+    hipLaunchKernelGGL((bwd_scores<R, BETA, PADR>), dim3(nch), dim3(NTH), 0, stream, a);
+    hipLaunchKernelGGL((fwd_out<R, BETA, PADR>), dim3(nch, nRt * s.nPt), dim3(NTH), 0, stream, a);
     if (a.hfin) hipLaunchKernelGGL(fwd_final, dim3(s.B * s.H), dim3(NTH), 0, stream, a);
     return hipGetLastError() == hipSuccess ? 0 : 1;
 }
@@ -866,15 +889,20 @@ int launch_chunked_fwd_mfma(int B, int T, int H, int P, int N, int R, const floa
     a.xr = x_raw, a.hinit = h_init;
     a.cum = part(0), a.dec = part(1), a.hext = part(2), a.Hs = part(3), a.M = part(4);
     a.fwd = 1, a.y = y, a.hfin = h_final;
-    switch (R * 2 + (x_b != nullptr ? 1 : 0)) {
-        case 2: return launch_fwd<1, false>(a, h_init, stream);
-        case 3: return launch_fwd<1, true>(a, h_init, stream);
-        case 4: return launch_fwd<2, false>(a, h_init, stream);
-        case 5: return launch_fwd<2, true>(a, h_init, stream);
-        case 8: return launch_fwd<4, false>(a, h_init, stream);
-        case 9: return launch_fwd<4, true>(a, h_init, stream);
-        case 16: return launch_fwd<8, false>(a, h_init, stream);
-        case 17: return launch_fwd<8, true>(a, h_init, stream);
+    const bool pad = s.RT != s.R;
+    switch (s.RT * 4 + (x_b != nullptr ? 2 : 0) + (pad ? 1 : 0)) {
+        case 4: return launch_fwd<1, false, false>(a, h_init, stream);
+        case 6: return launch_fwd<1, true, false>(a, h_init, stream);
+        case 8: return launch_fwd<2, false, false>(a, h_init, stream);
+        case 10: return launch_fwd<2, true, false>(a, h_init, stream);
+        case 16: return launch_fwd<4, false, false>(a, h_init, stream);
+        case 17: return launch_fwd<4, false, true>(a, h_init, stream);
+        case 18: return launch_fwd<4, true, false>(a, h_init, stream);
+        case 19: return launch_fwd<4, true, true>(a, h_init, stream);
+        case 32: return launch_fwd<8, false, false>(a, h_init, stream);
+        case 33: return launch_fwd<8, false, true>(a, h_init, stream);
+        case 34: return launch_fwd<8, true, false>(a, h_init, stream);
+        case 35: return launch_fwd<8, true, true>(a, h_init, stream);
         default: return 1;
     }
 }
@@ -916,16 +944,20 @@ int launch_chunked_bwd(int B, int T, int H, int P, int N, int R, const float* x_
     float* scan_ws = reinterpret_cast<float*>(ws + pl.scan_off);
     a.fwd = 0, a.y = nullptr, a.hfin = nullptr;
 
-    const bool beta = x_b != nullptr;
-    switch (R * 2 + (beta ? 1 : 0)) {
-        case 2: return launch<1, false>(a, h_init, dh_init, scan_ws, stream);
-        case 3: return launch<1, true>(a, h_init, dh_init, scan_ws, stream);
-        case 4: return launch<2, false>(a, h_init, dh_init, scan_ws, stream);
-        case 5: return launch<2, true>(a, h_init, dh_init, scan_ws, stream);
-        case 8: return launch<4, false>(a, h_init, dh_init, scan_ws, stream);
-        case 9: return launch<4, true>(a, h_init, dh_init, scan_ws, stream);
-        case 16: return launch<8, false>(a, h_init, dh_init, scan_ws, stream);
-        case 17: return launch<8, true>(a, h_init, dh_init, scan_ws, stream);
+    const bool beta = x_b != nullptr, pad = s.RT != s.R;
+    switch (s.RT * 4 + (beta ? 2 : 0) + (pad ? 1 : 0)) {
+        case 4: return launch<1, false, false>(a, h_init, dh_init, scan_ws, stream);
+        case 6: return launch<1, true, false>(a, h_init, dh_init, scan_ws, stream);
+        case 8: return launch<2, false, false>(a, h_init, dh_init, scan_ws, stream);
+        case 10: return launch<2, true, false>(a, h_init, dh_init, scan_ws, stream);
+        case 16: return launch<4, false, false>(a, h_init, dh_init, scan_ws, stream);
+        case 17: return launch<4, false, true>(a, h_init, dh_init, scan_ws, stream);
+        case 18: return launch<4, true, false>(a, h_init, dh_init, scan_ws, stream);
+        case 19: return launch<4, true, true>(a, h_init, dh_init, scan_ws, stream);
+        case 32: return launch<8, false, false>(a, h_init, dh_init, scan_ws, stream);
+        case 33: return launch<8, false, true>(a, h_init, dh_init, scan_ws, stream);
+        case 34: return launch<8, true, false>(a, h_init, dh_init, scan_ws, stream);
+        case 35: return launch<8, true, true>(a, h_init, dh_init, scan_ws, stream);
         default: return 1;
     }
 }

@@ -71,7 +71,10 @@ def test_chunked_bwd_workspace_and_validation(lib):
     states = 4 * (K + 1) * 24 * 64 * 128 * 4
     scores = 4 * K * 24 * 64 * 128 * 4
     assert n.value >= 4 * states + 2 * scores
-    assert lib.m3_chunked_ssd_bwd_workspace_size(4, 1024, 24, 64, 128, 3, 1, ctypes.byref(n)) == 3
+    # rank 3 on rank-4 tiles; rank 9 is beyond every kernel
+    assert lib.m3_chunked_ssd_bwd_workspace_size(4, 1024, 24, 64, 128, 3, 1, ctypes.byref(n)) == 0
+    assert n.value > 0
+    assert lib.m3_chunked_ssd_bwd_workspace_size(4, 1024, 24, 64, 128, 9, 1, ctypes.byref(n)) == 3
     assert lib.m3_chunked_ssd_bwd_workspace_size(4, 1024, 24, 64, 128, 2, 2, ctypes.byref(n)) == 2
     assert lib.m3_chunked_ssd_bwd_workspace_size(0, 1024, 24, 64, 128, 2, 1, ctypes.byref(n)) == 2
     assert lib.m3_chunked_ssd_bwd_workspace_size(1, 8, 1, 8, 128, 2, 1, None) == 1
@@ -87,9 +90,9 @@ def test_chunked_bwd_workspace_and_validation(lib):
     o = list(outs)
     o[1] = None
     assert lib.m3_chunked_ssd_bwd(*args(ins, o), fake, 1 << 30, None) == 1
-    # rank 3 is not supported by the backward
+    # rank 9 is beyond every kernel
     a = args(ins, outs)
-    a[5] = 3
+    a[5] = 9
     assert lib.m3_chunked_ssd_bwd(*a, fake, 1 << 30, None) == 3
     # no workspace
     assert lib.m3_chunked_ssd_bwd(*args(ins, outs), None, 0, None) == 4
@@ -112,9 +115,9 @@ def test_workspace_query_and_desc_validation(lib):
     # workspace (B=1, T=4, H=8, P=16, N=16, R=2 with beta terms: chunks of 32 tokens)
     assert lib.m3_prefill_workspace_size(ctypes.byref(_desc()), ctypes.byref(n)) == 0
     assert n.value >= 4 * 8 * (3 * 16 * 2 + 3 * 16 * 2 + 16 * 2) * 4
-    # ranks the chunk kernels do not cover run on the generic kernel (state in LDS): none
+    # rank 3 runs there too, on the chunk kernels' rank-4 tiles
     assert lib.m3_prefill_workspace_size(ctypes.byref(_desc(mimo_rank=3)), ctypes.byref(n)) == 0
-    assert n.value == 0
+    assert n.value > 0
     # wide layers run there too: the per-token preparation holds the sin / cos of a tile of
     # heads at a time (64 heads x d_state 256 needed 64 KB of them at once)
     assert lib.m3_prefill_workspace_size(ctypes.byref(_desc(nheads=64, d_state=256)),
@@ -178,9 +181,15 @@ def test_layer_bwd_workspace_and_validation(lib):
     n = ctypes.c_size_t(0)
     d32 = _desc(seqlen=64)
     assert lib.m3_layer_bwd_workspace_size(ctypes.byref(d32), ctypes.byref(n)) == 0 and n.value > 0
-    # bf16 layers and ranks outside 1/2/4/8 are not covered (they train through the fallback)
+    # every rank up to 8 is covered (3, 5, 6 and 7 on the chunk kernels' rank-4 / rank-8 tiles)
+    for r in (3, 5, 6, 7):
+        assert lib.m3_layer_bwd_workspace_size(ctypes.byref(_desc(seqlen=64, mimo_rank=r)),
+                                               ctypes.byref(n)) == 0 and n.value > 0
+    # bf16 layers are not covered (the autograd path runs bf16 layers in fp32), nor layers
+    # whose B^ / C^ rows of every group exceed the 64 KB of LDS of the B/C kernel
     assert lib.m3_layer_bwd_workspace_size(ctypes.byref(_desc(dtype=1)), ctypes.byref(n)) == 3
-    assert lib.m3_layer_bwd_workspace_size(ctypes.byref(_desc(mimo_rank=3)), ctypes.byref(n)) == 3
+    assert lib.m3_layer_bwd_workspace_size(ctypes.byref(_desc(d_state=256, mimo_rank=8)),
+                                           ctypes.byref(n)) == 3
     assert lib.m3_layer_bwd_workspace_size(ctypes.byref(_desc(batch=0)), ctypes.byref(n)) == 2
     fake = ctypes.c_void_p(256)
     params = _native.LayerParams(*([256] * 10))
@@ -207,11 +216,13 @@ def test_chunked_fwd_workspace_query(lib):
     assert lib.m3_chunked_ssd_fwd_workspace_size(4, 1024, 24, 64, 128, 2, 0, 1, ctypes.byref(n)) == 0
     K = 1024 // 32
     assert n.value >= 2 * 4 * (K + 1) * 24 * 64 * 128 * 4 + 4 * K * 24 * 64 * 128 * 4
-    # bf16 and unsupported ranks take the generic kernel: no workspace
+    # bf16 takes the generic kernel: no workspace
     assert lib.m3_chunked_ssd_fwd_workspace_size(4, 1024, 24, 64, 128, 2, 1, 1, ctypes.byref(n)) == 0
     assert n.value == 0
+    # rank 3 with beta terms runs on rank-4 tiles: 16-token chunks, W o G of 64 x 128 per chunk
     assert lib.m3_chunked_ssd_fwd_workspace_size(4, 1024, 24, 64, 128, 3, 0, 1, ctypes.byref(n)) == 0
-    assert n.value == 0
+    K = 1024 // 16
+    assert n.value >= 2 * 4 * (K + 1) * 24 * 64 * 128 * 4 + 4 * K * 24 * 64 * 128 * 4
     assert lib.m3_chunked_ssd_fwd_workspace_size(4, 1024, 24, 64, 128, 2, 0, 2, ctypes.byref(n)) == 2
     assert lib.m3_chunked_ssd_fwd_workspace_size(4, 1024, 24, 64, 128, 2, 7, 1, ctypes.byref(n)) == 3
 

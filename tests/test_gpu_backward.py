@@ -33,6 +33,12 @@ CASES = [
     (1, 50, 2, 16, 16, 8, True, False, True),
     (1, 200, 1, 64, 128, 2, False, True, False),
     (1, 1, 2, 16, 32, 2, True, True, True),
+    # ranks 3, 5, 6, 7: rank-4 / rank-8 tiles with their extra slots read as zero
+    (1, 90, 2, 16, 32, 3, True, True, True),
+    (1, 70, 2, 16, 32, 3, False, False, True),
+    (1, 45, 2, 16, 16, 5, False, True, False),
+    (2, 33, 1, 32, 32, 6, True, True, True),
+    (1, 20, 2, 8, 16, 7, True, False, True),
 ]
 
 
@@ -119,8 +125,8 @@ def test_chunked_ssd_backward_is_deterministic(cuda_device):
 
 
 def test_chunked_ssd_unsupported_rank_fails_before_the_forward(cuda_device):
-    x = torch.randn(1, 8, 1, 4, 3, device=cuda_device, requires_grad=True)
-    Bm = torch.randn(1, 8, 1, 8, 3, device=cuda_device)
+    x = torch.randn(1, 8, 1, 4, 9, device=cuda_device, requires_grad=True)
+    Bm = torch.randn(1, 8, 1, 8, 9, device=cuda_device)
     with pytest.raises(RuntimeError, match="not supported"):
         mamba3_amd.chunked_ssd(x, None, Bm, None, Bm, torch.rand(1, 8, 1, device=cuda_device),
                                -torch.ones(1, device=cuda_device), torch.ones(1, device=cuda_device),
@@ -136,6 +142,11 @@ LAYER_KW = [
          use_complex_ssm=False),
     dict(d_model=128, d_state=64, headdim=32, mimo_rank=2),
     dict(d_model=128, d_state=32, headdim=128, mimo_rank=2),  # slots wider than a wave
+    # ranks 3, 5, 6, 7 (the chunk kernels on rank-4 / rank-8 tiles)
+    dict(d_model=64, d_state=16, headdim=16, mimo_rank=3),
+    dict(d_model=64, d_state=16, headdim=16, mimo_rank=5, ngroups=2),
+    dict(d_model=64, d_state=32, headdim=16, mimo_rank=6, use_trapezoidal=False),
+    dict(d_model=64, d_state=16, headdim=16, mimo_rank=7, use_complex_ssm=False),
 ]
 
 
@@ -306,11 +317,11 @@ def test_layer_training_runs_on_the_native_backward(cuda_device):
 
 
 def test_layer_training_outside_the_native_backward_raises(cuda_device):
-    """Shapes m3_layer_bwd does not cover (here rank 3) raise a clear error when trained,
-    rather than falling back to another implementation; without gradients the same layer
-    runs (on the generic prefill kernel)."""
+    """Shapes m3_layer_bwd does not cover (here d_state 256 at rank 8: the B^ / C^ rows of
+    the group exceed the B/C kernel's 64 KB of LDS) raise a clear error when trained, rather
+    than falling back to another implementation; without gradients the same layer runs."""
     from mamba3_amd import _native
-    kw = dict(d_model=64, d_state=16, headdim=16, mimo_rank=3)
+    kw = dict(d_model=64, d_state=256, headdim=16, mimo_rank=8)
     torch.manual_seed(0)
     layer = mamba3_amd.KulaMamba(**kw).to(cuda_device).train()
     x = torch.randn(2, 40, 64, device=cuda_device)

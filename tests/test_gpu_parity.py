@@ -93,11 +93,12 @@ def test_chunked_ssd_matches_reference_golden(name, cuda_device):
     assert max_rel(res.h_final, torch.from_numpy(g["h_final"])) < FP32_TOL
 
 
-@pytest.mark.parametrize("beta,R", [(True, 2), (False, 1), (True, 4), (False, 3)])
+@pytest.mark.parametrize("beta,R", [(True, 2), (False, 1), (True, 4), (False, 3), (True, 3),
+                                    (False, 5), (True, 6), (True, 7)])
 def test_chunked_ssd_generic_and_mfma_paths_match_oracle(beta, R, cuda_device):
     """fp32 chunked_ssd on both native paths (the fp32-MFMA chunk kernels, used when a
-    workspace is given and the rank is 1/2/4/8, and the generic kernel) and in bf16 against
-    the fp32 oracle (mamba3/ssd.py:118-244)."""
+    workspace is given -- ranks 3, 5, 6 and 7 on their rank-4 / rank-8 tiles -- and the
+    generic kernel) and in bf16 against the fp32 oracle (mamba3/ssd.py:118-244)."""
     g = torch.Generator().manual_seed(13)
     Bt, T, H, P, N = 2, 150, 3, 16, 32
     r = lambda *s: torch.randn(*s, generator=g)

@@ -22,7 +22,8 @@ PATHS = [
     (dict(d_model=768, d_state=128, headdim=64, mimo_rank=2), torch.bfloat16, "d768 MFMA"),
     (dict(d_model=128, d_state=64, headdim=32, mimo_rank=4), torch.bfloat16, "general MFMA"),
     (dict(d_model=128, d_state=32, headdim=32, mimo_rank=2), torch.float32, "fp32 layer"),
-    (dict(d_model=64, d_state=16, headdim=16, mimo_rank=3), torch.float32, "generic"),
+    (dict(d_model=64, d_state=16, headdim=16, mimo_rank=3), torch.float32, "fp32 layer rank 3"),
+    (dict(d_model=64, d_state=16, headdim=16, mimo_rank=3), torch.bfloat16, "generic"),
 ]
 
 
