@@ -249,8 +249,8 @@ int m3_step_fwd(const m3_layer_desc* desc, const m3_layer_params* params,
  * output); g_h_out, g_prev_bx_out [B,H,P,N] and g_angle_out [B,H,N/2] = dL/d(new state), each
  * NULL for zero. Outputs: g_proj (the in_proj columns of each row written), g_h_in,
  * g_prev_bx_in, g_angle_in, and the parameter gradients `grads` (written, not accumulated;
- * grads->dt_scale [B,H] when not NULL). Deterministic. Supported: d_state <= 512,
- * mimo_rank <= 8, 4 (2 N R + N/2 + 2 P R + P) floats of LDS per head within 64 KiB.
+ * grads->dt_scale [B,H] when not NULL). Deterministic. Supported: every layer the API takes
+ * (even d_state <= 512, headdim <= 256, mimo_rank <= 8; at most 100 KiB of LDS per head).
  * workspace: m3_step_bwd_workspace_size() bytes, 256-byte aligned.
  */
 int m3_step_bwd_workspace_size(const m3_layer_desc* desc, size_t* bytes);

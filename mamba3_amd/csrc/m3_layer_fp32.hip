@@ -130,23 +130,25 @@ __global__ __launch_bounds__(NTH) void lp_angles(Args a) {
     }
 }
 
-// One block per (b, t): normalised B^ / C^ of every group in LDS, the sin / cos of every
-// head's RoPE pairs in LDS, then the rotated rows of every head and the x terms, as flat loops
-// over (head, element).
+// One block per (b, t), one group at a time: the group's normalised B^ / C^ in LDS, the sin /
+// cos of a tile of its heads' RoPE pairs in LDS, then the rotated rows of those heads, as flat
+// loops over (head, element); then the x terms of every head.
 __global__ __launch_bounds__(NTH) void lp_prep(Args a) {
-    // B^ [G*N*R], C^ [G*N*R], reduction scratch [2*NTH], sin / cos [HT*N/2] each
+    // B^ [N*R], C^ [N*R], reduction scratch [2*NTH], sin / cos [HT*N/2] each
     extern __shared__ float sm[];
     const int bt = blockIdx.x, b = bt / a.T, t = bt % a.T;
-    const int NR = a.N * a.R, GNR = a.G * NR, NH = a.N / 2;
+    const int NR = a.N * a.R, NH = a.N / 2;
     float* Bh = sm;
-    float* Ch = sm + GNR;
-    float* red = sm + 2 * GNR;
+    float* Ch = sm + NR;
+    float* red = sm + 2 * NR;
     float* sn = red + 2 * NTH;
     float* cn = sn + (int64_t)a.HT * NH;
     const float* row = a.proj + ((int64_t)b * a.T + t) * a.rs;
     const int64_t tok0 = ((int64_t)b * a.T + t) * a.H;  // token row of head 0
     const int tid = threadIdx.x;
+    const int hpg = a.H / a.G;
     for (int g = 0; g < a.G; ++g) {
+        if (g > 0) __syncthreads();  // the previous group's rows and sin / cos are read
         float sb = 0.f, sc = 0.f;
         for (int e = tid; e < NR; e += NTH) {
             const float vb = row[a.pl.B + (int64_t)g * NR + e], vc = row[a.pl.C + (int64_t)g * NR + e];
@@ -166,37 +168,37 @@ __global__ __launch_bounds__(NTH) void lp_prep(Args a) {
         const float rb = rsqrtf(red[0] / NR + a.eps), rc = rsqrtf(red[NTH] / NR + a.eps);
         for (int e = tid; e < NR; e += NTH) {
             const int64_t o = (int64_t)g * NR + e;
-            Bh[o] = row[a.pl.B + o] * rb * a.prm.B_norm_w[e] + a.prm.B_bias[o];
-            Ch[o] = row[a.pl.C + o] * rc * a.prm.C_norm_w[e] + a.prm.C_bias[o];
+            Bh[e] = row[a.pl.B + o] * rb * a.prm.B_norm_w[e] + a.prm.B_bias[o];
+            Ch[e] = row[a.pl.C + o] * rc * a.prm.C_norm_w[e] + a.prm.C_bias[o];
         }
         __syncthreads();
-    }
-    const int hpg = a.H / a.G;
-    // heads in tiles of HT, so the sin / cos of a tile fit in LDS whatever H * N is
-    for (int h0 = 0; h0 < a.H; h0 += a.HT) {
-        const int nh = min(a.HT, a.H - h0);
-        if (a.cplx) {
-            if (h0 > 0) __syncthreads();  // the previous tile's sin / cos are read
-            for (int j = tid; j < nh * NH; j += NTH)
-                sincosf(a.phi[(tok0 + h0) * NH + j], &sn[j], &cn[j]);
-            __syncthreads();
-        }
-        for (int j = tid; j < nh * NR; j += NTH) {
-            const int hl = j / NR, h = h0 + hl, e = j % NR, g = h / hpg;
-            const int n = e / a.R, r = e % a.R, i = n >> 1;
-            const int64_t ev = (int64_t)g * NR + (2 * i) * a.R + r, od = ev + a.R;
-            float vb = Bh[(int64_t)g * NR + e], vc = Ch[(int64_t)g * NR + e];
+        // the group's heads in tiles of HT, so the sin / cos of a tile fit in LDS whatever
+        // H * N is
+        for (int h0 = g * hpg; h0 < (g + 1) * hpg; h0 += a.HT) {
+            const int nh = min(a.HT, (g + 1) * hpg - h0);
             if (a.cplx) {
-                const float s = sn[hl * NH + i], c = cn[hl * NH + i];
-                vb = (n & 1) ? Bh[ev] * s + Bh[od] * c : Bh[ev] * c - Bh[od] * s;
-                vc = (n & 1) ? Ch[ev] * s + Ch[od] * c : Ch[ev] * c - Ch[od] * s;
+                if (h0 > g * hpg) __syncthreads();  // the previous tile's sin / cos are read
+                for (int j = tid; j < nh * NH; j += NTH)
+                    sincosf(a.phi[(tok0 + h0) * NH + j], &sn[j], &cn[j]);
+                __syncthreads();
             }
-            const int64_t tok = tok0 + h;
-            a.Bt[tok * NR + e] = vb;
-            a.Ct[tok * NR + e] = vc;
-            if (a.trap) {
-                if (t + 1 < a.T) a.Bb[(tok + a.H) * NR + e] = vb;  // B_b[t+1] = B~[t]
-                if (t == 0) a.Bb[tok * NR + e] = 0.f;
+            for (int j = tid; j < nh * NR; j += NTH) {
+                const int hl = j / NR, h = h0 + hl, e = j % NR;
+                const int n = e / a.R, r = e % a.R, i = n >> 1;
+                const int ev = (2 * i) * a.R + r, od = ev + a.R;
+                float vb = Bh[e], vc = Ch[e];
+                if (a.cplx) {
+                    const float s = sn[hl * NH + i], c = cn[hl * NH + i];
+                    vb = (n & 1) ? Bh[ev] * s + Bh[od] * c : Bh[ev] * c - Bh[od] * s;
+                    vc = (n & 1) ? Ch[ev] * s + Ch[od] * c : Ch[ev] * c - Ch[od] * s;
+                }
+                const int64_t tok = tok0 + h;
+                a.Bt[tok * NR + e] = vb;
+                a.Ct[tok * NR + e] = vc;
+                if (a.trap) {
+                    if (t + 1 < a.T) a.Bb[(tok + a.H) * NR + e] = vb;  // B_b[t+1] = B~[t]
+                    if (t == 0) a.Bb[tok * NR + e] = 0.f;
+                }
             }
         }
     }
@@ -288,17 +290,18 @@ Plan plan(const m3_layer_desc& d) {
 namespace {
 constexpr size_t kPrepLds = 64 * 1024;
 
-// LDS of lp_prep without the sin / cos tiles: B^ and C^ of every group, the reduction
-// scratch.
+// LDS of lp_prep without the sin / cos tiles: B^ and C^ of one group, the reduction scratch
+// (at most 34 KB: d_state <= 512, rank <= 8).
 size_t prep_lds_fixed(const m3_layer_desc& d) {
-    return (2 * (size_t)d.ngroups * d.d_state * d.mimo_rank + 2 * lp::NTH) * sizeof(float);
+    return (2 * (size_t)d.d_state * d.mimo_rank + 2 * lp::NTH) * sizeof(float);
 }
-// Heads per sin / cos tile: as many as fit next to the fixed part (0: nothing fits).
+// Heads per sin / cos tile: as many of a group's heads as fit next to the fixed part (0:
+// nothing fits).
 int prep_heads_per_tile(const m3_layer_desc& d) {
     const size_t fixed = prep_lds_fixed(d);
-    if (fixed >= kPrepLds) return 0;
+    if (fixed >= kPrepLds || d.ngroups <= 0 || d.nheads % d.ngroups != 0) return 0;
     const size_t per_head = (size_t)d.d_state * sizeof(float);  // sin and cos of N/2 pairs
-    return (int)std::min<size_t>(d.nheads, (kPrepLds - fixed) / per_head);
+    return (int)std::min<size_t>(d.nheads / d.ngroups, (kPrepLds - fixed) / per_head);
 }
 size_t prep_lds(const m3_layer_desc& d) {
     return prep_lds_fixed(d) + (size_t)prep_heads_per_tile(d) * d.d_state * sizeof(float);

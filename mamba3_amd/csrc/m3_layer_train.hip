@@ -252,10 +252,11 @@ __global__ __launch_bounds__(NTH) void tb_x(Args a) {
     }
 }
 
-// ---- B / C: one block per (b, TBC tokens). Thread (pair i, head group hg) handles the heads
-// h = hg (mod HS) of pair i and accumulates into its own LDS partial of dL/dB^, dL/dC^; the HS
-// partials are then summed in order. LDS: the partials, dL/dB^, dL/dC^, the parameter
-// partials, the reduction scratch.
+// ---- B / C: one block per (b, TBC tokens), one group g at a time, token by token. Thread
+// (pair i, head slot hg) handles the heads g hpg + hl, hl = hg (mod HS), of pair i and
+// accumulates into its own LDS partial of the group's dL/dB^, dL/dC^; the HS partials are
+// then summed in order. LDS: the partials, dL/dB^, dL/dC^, the parameter partials of the
+// group, the reduction scratch.
 __device__ __forceinline__ int bc_hs(int N) { return max(1, NTH / (N / 2)); }
 
 // The K = 2R values of pair i (even column, ranks 0..R-1, then odd column) are contiguous
@@ -285,95 +286,96 @@ __global__ __launch_bounds__(NTH) void tb_bc(Args a) {
     extern __shared__ float sm[];
     const int NR = a.N * R, GNR = a.G * NR, NH = a.N / 2, hpg = a.H / a.G;
     const int HS = bc_hs(a.N);
-    float* qB = sm;                 // [HS][GNR]
-    float* qC = qB + HS * GNR;      // [HS][GNR]
-    float* gBh = qC + HS * GNR;
-    float* gCh = gBh + GNR;
-    float* pBw = gCh + GNR;
+    float* qB = sm;                 // [HS][NR]
+    float* qC = qB + HS * NR;       // [HS][NR]
+    float* gBh = qC + HS * NR;
+    float* gCh = gBh + NR;
+    float* pBw = gCh + NR;
     float* pCw = pBw + NR;
     float* pBb = pCw + NR;
-    float* pCb = pBb + GNR;
-    float* red = pCb + GNR;
+    float* pCb = pBb + NR;
+    float* red = pCb + NR;
     const int nTB = (a.T + TBC - 1) / TBC;
     const int tb = blockIdx.x % nTB, b = blockIdx.x / nTB;
+    const int64_t ob = (int64_t)blockIdx.x;
     const int tid = threadIdx.x;
-    const int hg = tid / NH < HS ? tid / NH : a.H;  // a.H: no heads for this thread
+    const int hg = tid / NH < HS ? tid / NH : hpg;  // hpg: no heads for this thread
     const int i0 = tid % NH;
     for (int e = tid; e < NR; e += NTH) pBw[e] = pCw[e] = 0.f;
-    for (int e = tid; e < GNR; e += NTH) pBb[e] = pCb[e] = 0.f;
     const int t1 = min(a.T, (tb + 1) * TBC);
-    for (int t = tb * TBC; t < t1; ++t) {
-        const int64_t tok = (int64_t)b * a.T + t;
-        const float* row = a.proj + tok * a.rs;
-        for (int e = tid; e < HS * GNR; e += NTH) qB[e] = qC[e] = 0.f;
-        __syncthreads();
-        for (int h = hg; h < a.H; h += HS) {
-            const int g = h / hpg;
-            const int64_t th = tok * a.H + h;
-            const int64_t bt = th * NR;
-            float* qb = qB + (int64_t)hg * GNR;
-            float* qc = qC + (int64_t)hg * GNR;
-            for (int i = i0; i < NH; i += NTH) {
-                float s = 0.f, c = 1.f;
-                if (a.cplx) sincosf(a.f.phi[th * NH + i], &s, &c);
-                float gphi = 0.f;
-                const int64_t e0 = bt + (int64_t)(2 * i) * R;
-                float gb[2 * R], gc[2 * R], vb[2 * R], vc[2 * R];
-                ldv<2 * R>(a.gBt + e0, gb);
-                ldv<2 * R>(a.gCt + e0, gc);
-                if (a.trap && t + 1 < a.T) {
-                    float nb[2 * R];
-                    ldv<2 * R>(a.gBb + e0 + (int64_t)a.H * NR, nb);
+    for (int g = 0; g < a.G; ++g) {
+        for (int e = tid; e < NR; e += NTH) pBb[e] = pCb[e] = 0.f;
+        for (int t = tb * TBC; t < t1; ++t) {
+            const int64_t tok = (int64_t)b * a.T + t;
+            const float* row = a.proj + tok * a.rs;
+            for (int e = tid; e < HS * NR; e += NTH) qB[e] = qC[e] = 0.f;
+            __syncthreads();
+            for (int hl = hg; hl < hpg; hl += HS) {
+                const int h = g * hpg + hl;
+                const int64_t th = tok * a.H + h;
+                const int64_t bt = th * NR;
+                float* qb = qB + (int64_t)hg * NR;
+                float* qc = qC + (int64_t)hg * NR;
+                for (int i = i0; i < NH; i += NTH) {
+                    float s = 0.f, c = 1.f;
+                    if (a.cplx) sincosf(a.f.phi[th * NH + i], &s, &c);
+                    float gphi = 0.f;
+                    const int64_t e0 = bt + (int64_t)(2 * i) * R;
+                    float gb[2 * R], gc[2 * R], vb[2 * R], vc[2 * R];
+                    ldv<2 * R>(a.gBt + e0, gb);
+                    ldv<2 * R>(a.gCt + e0, gc);
+                    if (a.trap && t + 1 < a.T) {
+                        float nb[2 * R];
+                        ldv<2 * R>(a.gBb + e0 + (int64_t)a.H * NR, nb);
 #pragma unroll
-                    for (int k = 0; k < 2 * R; ++k) gb[k] += nb[k];
-                }
-                if (a.cplx) {
-                    ldv<2 * R>(a.f.Bt + e0, vb);
-                    ldv<2 * R>(a.f.Ct + e0, vc);
-                }
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    float gbe = gb[r], gbo = gb[R + r];
-                    if (t == a.T - 1 && a.gprev) {
-                        const float* gp = a.gprev + ((int64_t)b * a.H + h) * a.P * a.N;
-                        const float* xr = a.f.xr + th * a.P * R + r;
-                        for (int pp = 0; pp < a.P; ++pp) {
-                            gbe += gp[(int64_t)pp * a.N + 2 * i] * xr[(int64_t)pp * R];
-                            gbo += gp[(int64_t)pp * a.N + 2 * i + 1] * xr[(int64_t)pp * R];
-                        }
+                        for (int k = 0; k < 2 * R; ++k) gb[k] += nb[k];
                     }
-                    const float gce = gc[r], gco = gc[R + r];
-                    if (a.cplx) gphi += gbo * vb[r] - gbe * vb[R + r] + gco * vc[r] - gce * vc[R + r];
-                    const int64_t je = (int64_t)g * NR + (2 * i) * R + r, jo = je + R;
-                    qb[je] += gbe * c + gbo * s;
-                    qb[jo] += gbo * c - gbe * s;
-                    qc[je] += gce * c + gco * s;
-                    qc[jo] += gco * c - gce * s;
+                    if (a.cplx) {
+                        ldv<2 * R>(a.f.Bt + e0, vb);
+                        ldv<2 * R>(a.f.Ct + e0, vc);
+                    }
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        float gbe = gb[r], gbo = gb[R + r];
+                        if (t == a.T - 1 && a.gprev) {
+                            const float* gp = a.gprev + ((int64_t)b * a.H + h) * a.P * a.N;
+                            const float* xr = a.f.xr + th * a.P * R + r;
+                            for (int pp = 0; pp < a.P; ++pp) {
+                                gbe += gp[(int64_t)pp * a.N + 2 * i] * xr[(int64_t)pp * R];
+                                gbo += gp[(int64_t)pp * a.N + 2 * i + 1] * xr[(int64_t)pp * R];
+                            }
+                        }
+                        const float gce = gc[r], gco = gc[R + r];
+                        if (a.cplx) gphi += gbo * vb[r] - gbe * vb[R + r] + gco * vc[r] - gce * vc[R + r];
+                        const int je = (2 * i) * R + r, jo = je + R;
+                        qb[je] += gbe * c + gbo * s;
+                        qb[jo] += gbo * c - gbe * s;
+                        qc[je] += gce * c + gco * s;
+                        qc[jo] += gco * c - gce * s;
+                    }
+                    if (a.cplx) a.gphi[th * NH + i] = gphi;
                 }
-                if (a.cplx) a.gphi[th * NH + i] = gphi;
             }
-        }
-        __syncthreads();
-        for (int e = tid; e < GNR; e += NTH) {
-            float sb = 0.f, sc = 0.f;
-            for (int k = 0; k < HS; ++k) {
-                sb += qB[(int64_t)k * GNR + e];
-                sc += qC[(int64_t)k * GNR + e];
+            __syncthreads();
+            for (int e = tid; e < NR; e += NTH) {
+                float sb = 0.f, sc = 0.f;
+                for (int k = 0; k < HS; ++k) {
+                    sb += qB[(int64_t)k * NR + e];
+                    sc += qC[(int64_t)k * NR + e];
+                }
+                gBh[e] = sb;
+                gCh[e] = sc;
             }
-            gBh[e] = sb;
-            gCh[e] = sc;
-        }
-        __syncthreads();
-        // RMSNorm backward per group; parameter partials
-        for (int g = 0; g < a.G; ++g) {
+            __syncthreads();
+            // RMSNorm backward of group g; parameter partials
             const float* vb = row + a.pl.B + (int64_t)g * NR;
             const float* vc = row + a.pl.C + (int64_t)g * NR;
             float sb = 0.f, sc = 0.f, wb = 0.f, wc = 0.f;
             for (int e = tid; e < NR; e += NTH) {
                 sb += vb[e] * vb[e];
                 sc += vc[e] * vc[e];
-                wb += gBh[g * NR + e] * a.prm.B_norm_w[e] * vb[e];
-                wc += gCh[g * NR + e] * a.prm.C_norm_w[e] * vc[e];
+                wb += gBh[e] * a.prm.B_norm_w[e] * vb[e];
+                wc += gCh[e] * a.prm.C_norm_w[e] * vc[e];
             }
             sb = block_sum(sb, red);
             sc = block_sum(sc, red);
@@ -382,25 +384,24 @@ __global__ __launch_bounds__(NTH) void tb_bc(Args a) {
             const float rb = rsqrtf(sb / NR + a.eps), rc = rsqrtf(sc / NR + a.eps);
             const float kb = rb * rb * rb * wb / NR, kc = rc * rc * rc * wc / NR;
             for (int e = tid; e < NR; e += NTH) {
-                const float gb = gBh[g * NR + e], gc = gCh[g * NR + e];
+                const float gb = gBh[e], gc = gCh[e];
                 a.gproj[tok * a.rs + a.pl.B + (int64_t)g * NR + e] = rb * a.prm.B_norm_w[e] * gb - vb[e] * kb;
                 a.gproj[tok * a.rs + a.pl.C + (int64_t)g * NR + e] = rc * a.prm.C_norm_w[e] * gc - vc[e] * kc;
                 pBw[e] += gb * vb[e] * rb;
                 pCw[e] += gc * vc[e] * rc;
-                pBb[g * NR + e] += gb;
-                pCb[g * NR + e] += gc;
+                pBb[e] += gb;
+                pCb[e] += gc;
             }
+            __syncthreads();
         }
-        __syncthreads();
+        for (int e = tid; e < NR; e += NTH) {
+            a.p_Bb[ob * GNR + (int64_t)g * NR + e] = pBb[e];
+            a.p_Cb[ob * GNR + (int64_t)g * NR + e] = pCb[e];
+        }
     }
-    const int64_t ob = (int64_t)blockIdx.x;
     for (int e = tid; e < NR; e += NTH) {
         a.p_Bw[ob * NR + e] = pBw[e];
         a.p_Cw[ob * NR + e] = pCw[e];
-    }
-    for (int e = tid; e < GNR; e += NTH) {
-        a.p_Bb[ob * GNR + e] = pBb[e];
-        a.p_Cb[ob * GNR + e] = pCb[e];
     }
 }
 
@@ -614,17 +615,30 @@ Plan plan(const m3_layer_desc& d) {
     return p;
 }
 
+// LDS of tb_bc: (2 HS + 6) N R + NTH floats, at most 132 KB (d_state 512, rank 8).
+constexpr size_t kBcMaxLds = 160 * 1024;  // gfx950's LDS per workgroup
 size_t bc_lds(const m3_layer_desc& d) {
-    const size_t NR = (size_t)d.d_state * d.mimo_rank, GNR = d.ngroups * NR;
+    const size_t NR = (size_t)d.d_state * d.mimo_rank;
     const size_t HS = std::max(1, NTH / (d.d_state / 2));
-    return ((2 * HS + 4) * GNR + 2 * NR + NTH) * sizeof(float);
+    return ((2 * HS + 6) * NR + NTH) * sizeof(float);
+}
+
+// tb_bc<R> with `lds` bytes of dynamic LDS; above 64 KB the kernel's limit is raised first.
+template <int R>
+int launch_bc(const Args& a, dim3 grid, size_t lds, hipStream_t stream) {
+    if (lds > 64 * 1024 &&
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&tb_bc<R>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+        return 1;
+    hipLaunchKernelGGL(tb_bc<R>, grid, dim3(NTH), lds, stream, a);
+    return 0;
 }
 
 
 }  // namespace tb
 
 size_t layer_bwd_workspace(const m3_layer_desc& d) {
-    if (!fp32_layer_supported(d) || tb::bc_lds(d) > 64 * 1024 || d.mimo_rank > 8) return 0;
+    if (!fp32_layer_supported(d) || tb::bc_lds(d) > tb::kBcMaxLds || d.mimo_rank > 8) return 0;
     return tb::plan(d).total;
 }
 
@@ -661,17 +675,20 @@ int launch_layer_bwd(const m3_layer_desc& d, const m3_layer_params& p, const voi
         return 1;
     hipLaunchKernelGGL(tb_x, dim3(gbh), dim3(NTH), 0, stream, a);
     const dim3 gbc((unsigned)((int64_t)a.B * nTC));
+    const size_t lbc = bc_lds(d);
+    int st = 1;
     switch (a.R) {
-        case 1: hipLaunchKernelGGL(tb_bc<1>, gbc, dim3(NTH), bc_lds(d), stream, a); break;
-        case 2: hipLaunchKernelGGL(tb_bc<2>, gbc, dim3(NTH), bc_lds(d), stream, a); break;
-        case 3: hipLaunchKernelGGL(tb_bc<3>, gbc, dim3(NTH), bc_lds(d), stream, a); break;
-        case 4: hipLaunchKernelGGL(tb_bc<4>, gbc, dim3(NTH), bc_lds(d), stream, a); break;
-        case 5: hipLaunchKernelGGL(tb_bc<5>, gbc, dim3(NTH), bc_lds(d), stream, a); break;
-        case 6: hipLaunchKernelGGL(tb_bc<6>, gbc, dim3(NTH), bc_lds(d), stream, a); break;
-        case 7: hipLaunchKernelGGL(tb_bc<7>, gbc, dim3(NTH), bc_lds(d), stream, a); break;
-        case 8: hipLaunchKernelGGL(tb_bc<8>, gbc, dim3(NTH), bc_lds(d), stream, a); break;
-        default: return 1;
+        case 1: st = launch_bc<1>(a, gbc, lbc, stream); break;
+        case 2: st = launch_bc<2>(a, gbc, lbc, stream); break;
+        case 3: st = launch_bc<3>(a, gbc, lbc, stream); break;
+        case 4: st = launch_bc<4>(a, gbc, lbc, stream); break;
+        case 5: st = launch_bc<5>(a, gbc, lbc, stream); break;
+        case 6: st = launch_bc<6>(a, gbc, lbc, stream); break;
+        case 7: st = launch_bc<7>(a, gbc, lbc, stream); break;
+        case 8: st = launch_bc<8>(a, gbc, lbc, stream); break;
+        default: break;
     }
+    if (st != 0) return 1;
     if (a.cplx) {
         const int nc = (a.T + kAC - 1) / kAC;
         const int64_t na = (int64_t)a.B * nc * a.H * (a.N / 2);

@@ -404,9 +404,15 @@ Plan plan(const m3_layer_desc& d) {
 
 }  // namespace sb
 
+// Both kernels' LDS stays within gfx950's 160 KB per workgroup for every shape the API takes
+// (sb_head at most 100 KB: d_state 512, headdim 256, rank 8); above 64 KB a kernel's dynamic
+// LDS limit is raised before its launch.
+constexpr size_t kStepBwdMaxLds = 160 * 1024;
+
 bool step_bwd_supported(const m3_layer_desc& d) {
     return d.d_state % 2 == 0 && d.d_state <= 2 * sb::NTH && d.mimo_rank >= 1 &&
-           d.mimo_rank <= sb::RMAX && sb::head_lds(d) <= 64 * 1024 && sb::group_lds(d) <= 64 * 1024;
+           d.mimo_rank <= sb::RMAX && sb::head_lds(d) <= kStepBwdMaxLds &&
+           sb::group_lds(d) <= kStepBwdMaxLds;
 }
 
 size_t step_bwd_workspace(const m3_layer_desc& d) {
@@ -433,6 +439,13 @@ int launch_step_bwd(const m3_layer_desc& d, const m3_layer_params& p, const floa
     a.pBhat = part(0), a.pChat = part(1), a.pth = part(2), a.pAlog = part(3), a.pD = part(4);
     a.pdtb = part(5), a.pmx = part(6), a.pmz = part(7), a.pmd = part(8);
     a.pBb = part(9), a.pCb = part(10), a.pBw = part(11), a.pCw = part(12);
+    auto raise_lds = [](const void* f, size_t lds) {
+        return lds <= 64 * 1024 ||
+               hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) == hipSuccess;
+    };
+    if (!raise_lds(reinterpret_cast<const void*>(&sb_head), head_lds(d)) ||
+        !raise_lds(reinterpret_cast<const void*>(&sb_group), group_lds(d)))
+        return 1;
     hipLaunchKernelGGL(sb_head, dim3((unsigned)(d.batch * d.nheads)), dim3(NTH), head_lds(d), stream, a);
     hipLaunchKernelGGL(sb_group, dim3((unsigned)(d.batch * d.ngroups)), dim3(NTH), group_lds(d), stream, a);
     const int64_t B = d.batch, H = d.nheads, G = d.ngroups;

@@ -144,7 +144,7 @@ def prefill_train(proj: torch.Tensor, A_log: torch.Tensor, D: torch.Tensor,
         raise _native.NativeError(
             f"training through KulaMamba(d_state={d_state}, headdim={headdim}, "
             f"mimo_rank={mimo_rank}, ngroups={ngroups}) is not supported by m3_layer_bwd "
-            "(its per-token B/C working set exceeds 64 KB of LDS, or the rank exceeds 8); "
+            "(the rank exceeds 8 or the shape exceeds the kernels' limits); "
             "run this layer without gradients")
     pack, _ = _f32_params((A_log, D, dt_bias, B_norm_w, C_norm_w, B_bias, C_bias, mimo_x,
                            mimo_z, mimo_down))
