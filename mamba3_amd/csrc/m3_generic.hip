@@ -382,7 +382,17 @@ int launch_generic_prefill(const m3_layer_desc& d, const m3_layer_params& p, con
                                       hipFuncAttributeMaxDynamicSharedMemorySize, kGenMaxLdsBig) == hipSuccess
                       ? kGenMaxLdsBig : kGenMaxLds;
     A.s.Qi = gen_pick_chunk(A.s.N, A.s.Pb, A.s.R, A.s.Rb, d.use_complex != 0, true, max_lds);
+    // A block's state rows that do not fit the LDS even at one token per chunk (d_state 512
+    // with headdim 256 at large batch x heads): narrower column blocks, PS the next divisor
+    // of P.
+    for (int ps = PS + 1; A.s.Qi == 0 && ps <= A.s.P; ++ps) {
+        if (A.s.P % ps != 0) continue;
+        A.s.PS = ps;
+        A.s.Pb = A.s.P / ps;
+        A.s.Qi = gen_pick_chunk(A.s.N, A.s.Pb, A.s.R, A.s.Rb, d.use_complex != 0, true, max_lds);
+    }
     if (A.s.Qi == 0) return M3_ERR_UNSUPPORTED;
+    PS = A.s.PS;
     A.L = gen_lds_plan(A.s.Qi, A.s.N, A.s.Pb, A.s.R, A.s.Rb, d.use_complex != 0, true);
     A.pl = proj_layout(d);
     A.row_stride = d.proj_row_stride;
@@ -506,7 +516,17 @@ int launch_generic_chunked(int B, int T, int H, int P, int N, int R, int dtype,
     a.s.Rb = x_b ? 2 * R : R;
     a.s.G = 1;
     a.s.Pb = P; a.s.PS = 1;
-    a.s.Qi = gen_pick_chunk(N, P, R, a.s.Rb, false);
+    // Up to the CU's full LDS when 64 KB holds less than one token per chunk (d_state 512 at
+    // rank 8 with the beta terms).
+    int max_lds = kGenMaxLds;
+    a.s.Qi = gen_pick_chunk(N, P, R, a.s.Rb, false, false, max_lds);
+    if (a.s.Qi == 0) {
+        const void* f = dtype == M3_DTYPE_BF16 ? reinterpret_cast<const void*>(&gen_chunked<bf16>)
+                                               : reinterpret_cast<const void*>(&gen_chunked<float>);
+        if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kGenMaxLdsBig) == hipSuccess)
+            max_lds = kGenMaxLdsBig;
+        a.s.Qi = gen_pick_chunk(N, P, R, a.s.Rb, false, false, max_lds);
+    }
     if (a.s.Qi == 0) return M3_ERR_UNSUPPORTED;
     a.L = gen_lds_plan(a.s.Qi, N, P, R, a.s.Rb, false);
     a.x_g = x_g; a.x_b = x_b; a.B_g = B_g; a.B_b = B_b; a.C = C; a.dt = dt; a.x_raw = x_raw;

@@ -410,6 +410,44 @@ def test_bf16_prefill_matches_fp32_oracle(kw, shape, cuda_device):
         assert max_rel(st[k], st_ref[k]) < BF16_TOL, k
 
 
+def test_bf16_generic_prefill_with_state_rows_beyond_the_lds(cuda_device):
+    """d_state 512, headdim 256, rank 8 in bf16 (the generic kernel) at batch x heads = 130:
+    a whole head's state rows would need 525 KB of LDS, so the launch narrows the headdim
+    column blocks until they fit; output and state against the fp32 oracle (its chunk size
+    of 4 keeps the oracle's per-chunk outer products small; the kernel ignores it)."""
+    kw = dict(d_model=256, d_state=512, headdim=256, mimo_rank=8, chunk_size=4)
+    layer, cfg, p = _bf16_pair(kw, cuda_device)
+    torch.manual_seed(4)
+    x = torch.randn(65, 5, 256).to(torch.bfloat16)
+    with torch.no_grad():
+        y, st = layer.prefill(x.to(cuda_device))
+        y_ref, st_ref = ref.layer_forward(cfg, p, x.float(), return_state=True)
+    assert max_rel(y.float(), y_ref) < BF16_TOL
+    for k in ("h", "prev_BX", "angle"):
+        assert max_rel(st[k], st_ref[k]) < BF16_TOL, k
+
+
+def test_bf16_chunked_ssd_beyond_64kb_of_lds(cuda_device):
+    """bf16 chunked_ssd (the generic kernel) at d_state 512, rank 8 with the beta terms, where
+    one token per chunk needs 76 KB of LDS: the kernel's LDS limit is raised to 160 KB."""
+    g = torch.Generator().manual_seed(19)
+    Bt, T, H, P, N, R = 1, 10, 1, 256, 512, 8
+    r = lambda *s: torch.randn(*s, generator=g)
+    x_g, x_b, x_raw = r(Bt, T, H, P, R), r(Bt, T, H, P, R), r(Bt, T, H, P, R)
+    B_g, B_b, C = r(Bt, T, H, N, R), r(Bt, T, H, N, R), r(Bt, T, H, N, R)
+    dt = torch.rand(Bt, T, H, generator=g) * 0.3
+    A, D = -torch.rand(H, generator=g) - 0.1, r(H)
+    bf = lambda t: t.to(torch.bfloat16)
+    y_ref, h_ref = ref.chunked_ssd(*[bf(t).double() for t in (x_g, x_b, B_g, B_b, C, dt)],
+                                   A.double(), D.double(), bf(x_raw).double(), 64,
+                                   return_final_state=True)
+    dev = cuda_device
+    out = mamba3_amd.chunked_ssd(*[bf(t).to(dev) for t in (x_g, x_b, B_g, B_b, C, dt)],
+                                 A.to(dev), D.to(dev), bf(x_raw).to(dev), return_final_state=True)
+    assert max_rel(out.y, y_ref) < BF16_TOL
+    assert max_rel(out.h_final, h_ref) < BF16_TOL
+
+
 @pytest.mark.parametrize("extra", [dict(ngroups=2), dict(use_trapezoidal=False),
                                    dict(use_complex_ssm=False), dict(ngroups=24)])
 def test_bf16_d768_variants_match_fp32_oracle(extra, cuda_device):
