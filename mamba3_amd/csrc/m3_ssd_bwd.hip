@@ -95,14 +95,18 @@ struct Lds {
 // tcol(tx, j) = tx + 16 j; its accumulator acc[j][v].
 __device__ __forceinline__ int tcol(int tx, int j) { return tx + 16 * j; }
 
-// acc[j][v] += sum_k fa(4 ty + v, k) fb(k, tcol(tx, j)) over k < kdim, for the 64 x TN tile of
-// a 256-thread block, on fp32 MFMA. fa / fb return 0 outside the operands. AK / BK pick the
-// order in which consecutive threads fetch an operand: k fastest (for operands contiguous
-// along k in memory) or row / column fastest. The operands of step k0 + KT are loaded into
-// registers while step k0 is multiplied.
-template <int TN, bool AK, bool BK, class FA, class FB>
-__device__ __forceinline__ void gemm_acc(f32x4 (&acc)[TN / 16], int kdim, FA fa, FB fb,
-                                         Lds<TN>& l) {
+// acc[j][v] += sum_k A(4 ty + v, k) B(k, tcol(tx, j)) over k < kdim, for the 64 x TN tile of
+// a 256-thread block, on fp32 MFMA. Each operand comes as a load and a finish: la(m, k) /
+// lb(k, n) read element (m, k) / (k, n) from an address that is in bounds for every row
+// m < 64 (column n < TN) and k < kdim, without a branch; fa(m, k, v) / fb(k, n, v) turn the
+// loaded value into the operand's (zero outside the operand, scaled) once it has arrived,
+// also without a branch. The loads of step k0 + KT are issued while step k0 is multiplied and
+// finished as they are stored to LDS, so no load waits inside the step that issues it. AK / BK
+// pick the order in which consecutive threads fetch an operand: k fastest (for operands
+// contiguous along k in memory) or row / column fastest.
+template <int TN, bool AK, bool BK, class LA, class FA, class LB, class FB>
+__device__ __forceinline__ void gemm_acc(f32x4 (&acc)[TN / 16], int kdim, LA la, FA fa, LB lb,
+                                         FB fb, Lds<TN>& l) {
     constexpr int NA = KT * TT / NTH;  // A elements per thread and step
     constexpr int NB = KT * TN / NTH;  // B elements per thread and step
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -115,12 +119,12 @@ __device__ __forceinline__ void gemm_acc(f32x4 (&acc)[TN / 16], int kdim, FA fa,
 #pragma unroll
         for (int i = 0; i < NA; ++i) {
             const int e = tid + NTH * i;
-            ra[i] = k0 + ak(e) < kdim ? fa(am(e), k0 + ak(e)) : 0.f;
+            ra[i] = la(am(e), min(k0 + ak(e), kdim - 1));
         }
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
             const int e = tid + NTH * i;
-            rb[i] = k0 + bk(e) < kdim ? fb(k0 + bk(e), bn(e)) : 0.f;
+            rb[i] = lb(min(k0 + bk(e), kdim - 1), bn(e));
         }
     };
     fetch(0);
@@ -128,13 +132,15 @@ __device__ __forceinline__ void gemm_acc(f32x4 (&acc)[TN / 16], int kdim, FA fa,
     for (int k0 = 0; k0 < kdim; k0 += KT) {
 #pragma unroll
         for (int i = 0; i < NA; ++i) {
-            const int e = tid + NTH * i;
-            l.A[ak(e)][am(e)] = ra[i];
+            const int e = tid + NTH * i, k = k0 + ak(e);
+            const float v = fa(am(e), min(k, kdim - 1), ra[i]);
+            l.A[ak(e)][am(e)] = k < kdim ? v : 0.f;
         }
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
-            const int e = tid + NTH * i;
-            l.B[bk(e)][bn(e)] = rb[i];
+            const int e = tid + NTH * i, k = k0 + bk(e);
+            const float v = fb(min(k, kdim - 1), bn(e), rb[i]);
+            l.B[bk(e)][bn(e)] = k < kdim ? v : 0.f;
         }
         __syncthreads();
         if (k0 + KT < kdim) fetch(k0 + KT);
@@ -197,6 +203,27 @@ struct Chunk {
     // Whether rank slot r (< R) of the tiles holds a real rank.
     __device__ bool has(int r) const { return !PADR || r < rk(); }
     __device__ bool real(int t) const { return t < nt; }
+    // Loads without a branch: the token is clamped into the chunk's real tokens and the rank
+    // slot into the array's ranks, so the address is in bounds for any t < QB + 64 and column
+    // below P (N); ok() / okj() say whether the loaded value is a real element (the operands
+    // are zero where it is not).
+    __device__ int tcl(int t) const { return min(t, nt - 1); }
+    __device__ int rcl(int r) const {
+        if constexpr (PADR) return min(r, ra - 1);
+        return r;
+    }
+    __device__ bool ok(int t, int r) const { return real(t) && has(r); }
+    __device__ bool okj(int t, int j) const { return ok(t, j < R ? j : j - R); }
+    __device__ float lx(int t, int p, int j) const {
+        const bool g = !BETA || j < R;
+        return (g ? xg0 : xb0)[tcl(t) * tsP + p * rk() + rcl(g ? j : j - R)];
+    }
+    __device__ float lbf(int t, int n, int j) const {
+        const bool g = !BETA || j < R;
+        return (g ? bg0 : bb0)[tcl(t) * tsN + n * rk() + rcl(g ? j : j - R)];
+    }
+    __device__ float lc(int t, int n, int r) const { return c0[tcl(t) * tsN + n * rk() + rcl(r)]; }
+    __device__ float ldy(int t, int p, int r) const { return dy0[tcl(t) * tsP + p * rk() + rcl(r)]; }
     __device__ float dtv(int t) const { return real(t) ? dt0[t * tsH] : 0.f; }
     // x factor j of token t (x_g rank j for j < R, else x_b rank j - R), without dt.
     __device__ float x(int t, int p, int j) const {
@@ -259,15 +286,16 @@ __global__ __launch_bounds__(NTH) void bwd_states(Args a) {
     constexpr int NJ = TW / 16;
     f32x4 acc[NJ];
     zero(acc);
+    const int pmax = s.P - 1, nmax = s.N - 1;
     gemm_acc<TW, false, false>(acc, QB * R2,
-                 [&](int mm, int j) {
-                     const int p = p0 + mm, t = j / R2;
-                     return p < s.P ? wx[t] * q.x(t, p, j % R2) : 0.f;
+                 [&](int mm, int j) { return q.lx(j / R2, min(p0 + mm, pmax), j % R2); },
+                 [&](int mm, int j, float v) {
+                     const int t = j / R2;
+                     const float w = wx[t];
+                     return p0 + mm < s.P && q.okj(t, j % R2) ? w * v : 0.f;
                  },
-                 [&](int j, int nn) {
-                     const int n = n0 + nn;
-                     return n < s.N ? q.bf(j / R2, n, j % R2) : 0.f;
-                 },
+                 [&](int j, int nn) { return q.lbf(j / R2, min(n0 + nn, nmax), j % R2); },
+                 [&](int j, int nn, float v) { return n0 + nn < s.N && q.okj(j / R2, j % R2) ? v : 0.f; },
                  l);
     float* ho = a.hext + chx(s, b, k, h) * s.PN;
 #pragma unroll
@@ -280,14 +308,14 @@ __global__ __launch_bounds__(NTH) void bwd_states(Args a) {
     if (!a.fwd) {
     zero(acc);
     gemm_acc<TW, false, false>(acc, QB * R,
-                 [&](int mm, int j) {
-                     const int p = p0 + mm, t = j / R;
-                     return p < s.P ? ec[t] * q.dy(t, p, j % R) : 0.f;
+                 [&](int mm, int j) { return q.ldy(j / R, min(p0 + mm, pmax), j % R); },
+                 [&](int mm, int j, float v) {
+                     const int t = j / R;
+                     const float w = ec[t];
+                     return p0 + mm < s.P && q.ok(t, j % R) ? w * v : 0.f;
                  },
-                 [&](int j, int nn) {
-                     const int n = n0 + nn;
-                     return n < s.N ? q.c(j / R, n, j % R) : 0.f;
-                 },
+                 [&](int j, int nn) { return q.lc(j / R, min(n0 + nn, nmax), j % R); },
+                 [&](int j, int nn, float v) { return n0 + nn < s.N && q.ok(j / R, j % R) ? v : 0.f; },
                  l);
     float* go = a.gext + chx(s, b, k, h) * s.PN;
 #pragma unroll
@@ -345,10 +373,12 @@ __global__ __launch_bounds__(NTH) void bwd_scores(Args a) {
             zero(g);
             // G[(t,r),(s,j)] = sum_n C[t,n,r] Bf[s,n,j]
             gemm_acc<TW, true, true>(g, s.N,
-                         [&](int mm, int n) { const int m = m0 + mm; return q.c(m / R, n, m % R); },
-                         [&](int n, int cc) {
+                         [&](int mm, int n) { const int m = m0 + mm; return q.lc(m / R, n, m % R); },
+                         [&](int mm, int n, float v) { const int m = m0 + mm; return q.ok(m / R, m % R) ? v : 0.f; },
+                         [&](int n, int cc) { const int c = c0 + cc; return q.lbf(c / R2, n, c % R2); },
+                         [&](int n, int cc, float v) {
                              const int c = c0 + cc;
-                             return c < QR2 ? q.bf(c / R2, n, c % R2) : 0.f;
+                             return c < QR2 && q.okj(c / R2, c % R2) ? v : 0.f;
                          },
                          l);
 #pragma unroll
@@ -366,10 +396,13 @@ __global__ __launch_bounds__(NTH) void bwd_scores(Args a) {
             // the zp writes above before the reads below
             zero(g);
             gemm_acc<TW, true, true>(g, s.P,
-                         [&](int mm, int p) { const int m = m0 + mm; return q.dy(m / R, p, m % R); },
-                         [&](int p, int cc) {
-                             const int c = c0 + cc, t = c / R2;
-                             return c < QR2 ? dts[t] * q.x(t, p, c % R2) : 0.f;
+                         [&](int mm, int p) { const int m = m0 + mm; return q.ldy(m / R, p, m % R); },
+                         [&](int mm, int p, float v) { const int m = m0 + mm; return q.ok(m / R, m % R) ? v : 0.f; },
+                         [&](int p, int cc) { const int c = c0 + cc; return q.lx(c / R2, p, c % R2); },
+                         [&](int p, int cc, float v) {
+                             const int c = c0 + cc, t = min(c / R2, 63);
+                             const float d = dts[t];
+                             return c < QR2 && q.okj(c / R2, c % R2) ? d * v : 0.f;
                          },
                          l);
 #pragma unroll
@@ -443,9 +476,12 @@ __global__ __launch_bounds__(NTH, 4) void bwd_dxf(Args a) {
     const float* dH = a.dch + chx(s, b, k, h) * s.PN;
     f32x4 acc[4];
     zero(acc);
+    const int pmax = s.P - 1;
     gemm_acc<TT, true, true>(acc, s.N,
-             [&](int mm, int n) { const int m = m0 + mm; return q.bf(m / R2, n, m % R2); },
-             [&](int n, int pp) { const int p = p0 + pp; return p < s.P ? dH[(int64_t)p * s.N + n] : 0.f; },
+             [&](int mm, int n) { const int m = m0 + mm; return q.lbf(m / R2, n, m % R2); },
+             [&](int mm, int n, float v) { const int m = m0 + mm; return q.okj(m / R2, m % R2) ? v : 0.f; },
+             [&](int n, int pp) { return dH[min(p0 + pp, pmax) * s.N + n]; },
+             [&](int n, int pp, float v) { return p0 + pp < s.P ? v : 0.f; },
              l);
     float xv[4][4], rv[4];
 #pragma unroll
@@ -466,11 +502,10 @@ __global__ __launch_bounds__(NTH, 4) void bwd_dxf(Args a) {
     if (tid < nts) a.pState[((int64_t)ch * s.nPt + pt) * QB + m0 / per + tid] = outv[tid];
     const float* Mi = a.M + (int64_t)ch * QR * QR2;
     gemm_acc<TT, false, false>(acc, QR,
-             [&](int mm, int jr) { return Mi[(int64_t)jr * QR2 + m0 + mm]; },
-             [&](int jr, int pp) {
-                 const int p = p0 + pp;
-                 return p < s.P ? q.dy(jr / R, p, jr % R) : 0.f;
-             },
+             [&](int mm, int jr) { return Mi[jr * QR2 + m0 + mm]; },
+             [&](int mm, int jr, float v) { return v; },
+             [&](int jr, int pp) { return q.ldy(jr / R, min(p0 + pp, pmax), jr % R); },
+             [&](int jr, int pp, float v) { return p0 + pp < s.P && q.ok(jr / R, jr % R) ? v : 0.f; },
              l);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -514,12 +549,16 @@ __global__ __launch_bounds__(NTH, 4) void bwd_dbf(Args a) {
     const float* dH = a.dch + chx(s, b, k, h) * s.PN;
     f32x4 acc[NJ];
     zero(acc);
+    const int nmax = s.N - 1;
     gemm_acc<TW, true, false>(acc, s.P,
-             [&](int mm, int p) {
+             [&](int mm, int p) { const int m = m0 + mm; return q.lx(m / R2, p, m % R2); },
+             [&](int mm, int p, float v) {
                  const int m = m0 + mm, t = m / R2;
-                 return dts[t] * q.x(t, p, m % R2);
+                 const float d = dts[t];
+                 return q.okj(t, m % R2) ? d * v : 0.f;
              },
-             [&](int p, int nn) { const int n = n0 + nn; return n < s.N ? dH[(int64_t)p * s.N + n] : 0.f; },
+             [&](int p, int nn) { return dH[p * s.N + min(n0 + nn, nmax)]; },
+             [&](int p, int nn, float v) { return n0 + nn < s.N ? v : 0.f; },
              l);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -529,11 +568,10 @@ __global__ __launch_bounds__(NTH, 4) void bwd_dbf(Args a) {
     }
     const float* DMi = a.DM + (int64_t)ch * QR * QR2;
     gemm_acc<TW, false, false>(acc, QR,
-             [&](int mm, int jr) { return DMi[(int64_t)jr * QR2 + m0 + mm]; },
-             [&](int jr, int nn) {
-                 const int n = n0 + nn;
-                 return n < s.N ? q.c(jr / R, n, jr % R) : 0.f;
-             },
+             [&](int mm, int jr) { return DMi[jr * QR2 + m0 + mm]; },
+             [&](int mm, int jr, float v) { return v; },
+             [&](int jr, int nn) { return q.lc(jr / R, min(n0 + nn, nmax), jr % R); },
+             [&](int jr, int nn, float v) { return n0 + nn < s.N && q.ok(jr / R, jr % R) ? v : 0.f; },
              l);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -569,9 +607,12 @@ __global__ __launch_bounds__(NTH) void bwd_dc(Args a) {
     const float* Hk = a.Hs + chx(s, b, k, h) * s.PN;
     f32x4 acc[NJ];
     zero(acc);
+    const int nmax = s.N - 1;
     gemm_acc<TW, true, false>(acc, s.P,
-             [&](int mm, int p) { const int m = m0 + mm; return q.dy(m / R, p, m % R); },
-             [&](int p, int nn) { const int n = n0 + nn; return n < s.N ? Hk[(int64_t)p * s.N + n] : 0.f; },
+             [&](int mm, int p) { const int m = m0 + mm; return q.ldy(m / R, p, m % R); },
+             [&](int mm, int p, float v) { const int m = m0 + mm; return q.ok(m / R, m % R) ? v : 0.f; },
+             [&](int p, int nn) { return Hk[p * s.N + min(n0 + nn, nmax)]; },
+             [&](int p, int nn, float v) { return n0 + nn < s.N ? v : 0.f; },
              l);
     float rv[4];
 #pragma unroll
@@ -591,11 +632,10 @@ __global__ __launch_bounds__(NTH) void bwd_dc(Args a) {
     if (tid < nts) a.pInter[((int64_t)ch * s.nNt + nt) * QB + m0 / per + tid] = outv[tid];
     const float* DMi = a.DM + (int64_t)ch * QR * QR2;
     gemm_acc<TW, true, false>(acc, QR2,
-             [&](int mm, int jc) { return DMi[(int64_t)(m0 + mm) * QR2 + jc]; },
-             [&](int jc, int nn) {
-                 const int n = n0 + nn;
-                 return n < s.N ? q.bf(jc / R2, n, jc % R2) : 0.f;
-             },
+             [&](int mm, int jc) { return DMi[(m0 + mm) * QR2 + jc]; },
+             [&](int mm, int jc, float v) { return v; },
+             [&](int jc, int nn) { return q.lbf(jc / R2, min(n0 + nn, nmax), jc % R2); },
+             [&](int jc, int nn, float v) { return n0 + nn < s.N && q.okj(jc / R2, jc % R2) ? v : 0.f; },
              l);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -719,12 +759,12 @@ __global__ __launch_bounds__(NTH, 4) void fwd_out(Args a) {
     const float* Hk = a.Hs + chx(s, b, k, h) * s.PN;
     f32x4 acc[4];
     zero(acc);
+    const int pmax = s.P - 1;
     gemm_acc<TT, true, true>(acc, s.N,
-                             [&](int mm, int n) { const int m = m0 + mm; return q.c(m / R, n, m % R); },
-                             [&](int n, int pp) {
-                                 const int p = p0 + pp;
-                                 return p < s.P ? Hk[(int64_t)p * s.N + n] : 0.f;
-                             },
+                             [&](int mm, int n) { const int m = m0 + mm; return q.lc(m / R, n, m % R); },
+                             [&](int mm, int n, float v) { const int m = m0 + mm; return q.ok(m / R, m % R) ? v : 0.f; },
+                             [&](int n, int pp) { return Hk[min(p0 + pp, pmax) * s.N + n]; },
+                             [&](int n, int pp, float v) { return p0 + pp < s.P ? v : 0.f; },
                              l);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -734,10 +774,13 @@ __global__ __launch_bounds__(NTH, 4) void fwd_out(Args a) {
     }
     const float* Mi = a.M + (int64_t)ch * QR * QR2;
     gemm_acc<TT, true, false>(acc, QR2,
-                              [&](int mm, int jc) { return Mi[(int64_t)(m0 + mm) * QR2 + jc]; },
-                              [&](int jc, int pp) {
-                                  const int p = p0 + pp, u = jc / R2;
-                                  return p < s.P ? dts[u] * q.x(u, p, jc % R2) : 0.f;
+                              [&](int mm, int jc) { return Mi[(m0 + mm) * QR2 + jc]; },
+                              [&](int mm, int jc, float v) { return v; },
+                              [&](int jc, int pp) { return q.lx(jc / R2, min(p0 + pp, pmax), jc % R2); },
+                              [&](int jc, int pp, float v) {
+                                  const int u = jc / R2;
+                                  const float d = dts[u];
+                                  return p0 + pp < s.P && q.okj(u, jc % R2) ? d * v : 0.f;
                               },
                               l);
     const float Dh = a.D[h];
