@@ -177,7 +177,7 @@ struct Chunk {
     // consecutive tokens and the number of tokens below T: the GEMM operand fetches (one
     // element each) are then a compare and two 24-bit multiply-adds.
     int nt, tsP, tsN, tsH, ra;
-    const float *xg0, *xb0, *bg0, *bb0, *c0, *dy0, *dt0;
+    const float *xg0, *xb0, *bg0, *bb0, *c0, *dy0, *dt0, *xr0;
     __device__ Chunk(const Args* a_, int b_, int k_, int h_) : a(a_), b(b_), k(k_), h(h_) {
         const Shape& s = a->s;
         ra = PADR ? s.R : R;
@@ -194,6 +194,7 @@ struct Chunk {
         c0 = a->C + oN;
         dy0 = a->dy ? a->dy + oP : nullptr;
         dt0 = a->dt + r0;
+        xr0 = a->xr + oP;
     }
     // The arrays' rank (R unless PADR).
     __device__ int rk() const {
@@ -224,6 +225,8 @@ struct Chunk {
     }
     __device__ float lc(int t, int n, int r) const { return c0[tcl(t) * tsN + n * rk() + rcl(r)]; }
     __device__ float ldy(int t, int p, int r) const { return dy0[tcl(t) * tsP + p * rk() + rcl(r)]; }
+    __device__ float lxr(int t, int p, int r) const { return xr0[tcl(t) * tsP + p * rk() + rcl(r)]; }
+    __device__ float ldt(int t) const { return dt0[tcl(t) * tsH]; }
     __device__ float dtv(int t) const { return real(t) ? dt0[t * tsH] : 0.f; }
     // x factor j of token t (x_g rank j for j < R, else x_b rank j - R), without dt.
     __device__ float x(int t, int p, int j) const {
@@ -353,6 +356,7 @@ __global__ __launch_bounds__(NTH) void bwd_scores(Args a) {
     __shared__ Lds<TW> l;
     __shared__ float zp[TT][TW + 1];
     __shared__ float cs[64], dts[64], rowacc[64], colacc[64];
+    __shared__ float rowp[4][TT], colp[2][TW];
     const Shape& s = a.s;
     const int ch = blockIdx.x, h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
     const Chunk<R, BETA, PADR> q{&a, b, k, h};
@@ -416,20 +420,33 @@ __global__ __launch_bounds__(NTH) void bwd_scores(Args a) {
                     zp[4 * ty + i][tcol(tx, j)] *= g[j][i];
                 }
             __syncthreads();
-            // Z over the (r, j) blocks of the tile, summed into rows (t) and columns (s).
-            const int nt = TT / R, ns = min(TW, QR2 - c0) / R2;
+            // Z over the (r, j) blocks of the tile, summed into rows (t) and columns (s): first
+            // every thread sums 32 entries of one row (a quarter of it) and 32 of one column
+            // (half of it), then the token totals add those partials, all in a fixed order.
+            const int nt = TT / R, nc = min(TW, QR2 - c0), ns = nc / R2;
+            {
+                const int rr = tid & 63, c4 = 32 * (tid >> 6);
+                float v = 0.f;
+#pragma unroll 8
+                for (int i = 0; i < 32; ++i) v += c4 + i < nc ? zp[rr][c4 + i] : 0.f;
+                rowp[tid >> 6][rr] = v;
+                const int cc = tid & 127, r2 = 32 * (tid >> 7);
+                float w = 0.f;
+#pragma unroll 8
+                for (int i = 0; i < 32; ++i) w += zp[r2 + i][cc];
+                colp[tid >> 7][cc] = w;
+            }
+            __syncthreads();
             if (tid < nt) {
                 float v = 0.f;
-                for (int u = 0; u < ns; ++u)
-                    for (int r = 0; r < R; ++r)
-                        for (int j = 0; j < R2; ++j) v += zp[tid * R + r][u * R2 + j];
+#pragma unroll
+                for (int r = 0; r < R; ++r)
+                    for (int qq = 0; qq < 4; ++qq) v += rowp[qq][tid * R + r];
                 rowacc[m0 / R + tid] += v;
             } else if (tid >= 128 && tid < 128 + ns) {
                 const int u = tid - 128;
                 float v = 0.f;
-                for (int t = 0; t < nt; ++t)
-                    for (int r = 0; r < R; ++r)
-                        for (int j = 0; j < R2; ++j) v += zp[t * R + r][u * R2 + j];
+                for (int j = 0; j < R2; ++j) v += colp[0][u * R2 + j] + colp[1][u * R2 + j];
                 colacc[c0 / R2 + u] += v;
             }
             __syncthreads();
@@ -477,22 +494,32 @@ __global__ __launch_bounds__(NTH, 4) void bwd_dxf(Args a) {
     f32x4 acc[4];
     zero(acc);
     const int pmax = s.P - 1;
+    // this thread's x factors and dt, read in one batch ahead of the contraction (clamped
+    // addresses; masked below)
+    float xv[4][4], dv[4], rv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = m0 + 4 * ty + i, t = m / R2, j = m % R2;
+        dv[i] = q.ldt(t);
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) xv[i][jj] = q.lx(t, min(p0 + tcol(tx, jj), pmax), j);
+    }
     gemm_acc<TT, true, true>(acc, s.N,
              [&](int mm, int n) { const int m = m0 + mm; return q.lbf(m / R2, n, m % R2); },
              [&](int mm, int n, float v) { const int m = m0 + mm; return q.okj(m / R2, m % R2) ? v : 0.f; },
              [&](int n, int pp) { return dH[min(p0 + pp, pmax) * s.N + n]; },
              [&](int n, int pp, float v) { return p0 + pp < s.P ? v : 0.f; },
              l);
-    float xv[4][4], rv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int m = m0 + 4 * ty + i, t = m / R2, j = m % R2;
-        const float e = __expf(cend - cs[t]), d = q.dtv(t);
+        const bool okr = q.okj(t, j);
+        dv[i] = okr ? dv[i] : 0.f;
+        const float e = __expf(cend - cs[t]), d = dv[i];
         rv[i] = 0.f;
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
-            const int p = p0 + tcol(tx, jj);
-            xv[i][jj] = p < s.P ? q.x(t, p, j) : 0.f;
+            xv[i][jj] = okr && p0 + tcol(tx, jj) < s.P ? xv[i][jj] : 0.f;
             acc[jj][i] *= e;
             rv[i] += d * xv[i][jj] * acc[jj][i];
         }
@@ -510,7 +537,7 @@ __global__ __launch_bounds__(NTH, 4) void bwd_dxf(Args a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int m = m0 + 4 * ty + i, t = m / R2, j = m % R2;
-        const float d = q.dtv(t);
+        const float d = dv[i];
         rv[i] = 0.f;
         const int jr = j < R ? j : j - R;
         const bool w = q.real(t) && q.has(jr);
@@ -615,16 +642,26 @@ __global__ __launch_bounds__(NTH) void bwd_dc(Args a) {
              [&](int p, int nn, float v) { return n0 + nn < s.N ? v : 0.f; },
              l);
     float rv[4];
+    {
+        // C of this thread's rows, read in one batch (clamped addresses, masked below)
+        float cv[4][NJ];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int m = m0 + 4 * ty + i, t = m / R, r = m % R;
-        const float e = __expf(cs[t]);
-        rv[i] = 0.f;
+        for (int i = 0; i < 4; ++i) {
+            const int m = m0 + 4 * ty + i;
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-            const int n = n0 + tcol(tx, j);
-            acc[j][i] *= e;
-            if (n < s.N) rv[i] += q.c(t, n, r) * acc[j][i];
+            for (int j = 0; j < NJ; ++j) cv[i][j] = q.lc(m / R, min(n0 + tcol(tx, j), nmax), m % R);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int m = m0 + 4 * ty + i, t = m / R, r = m % R;
+            const bool okr = q.ok(t, r);
+            const float e = __expf(cs[t]);
+            rv[i] = 0.f;
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                acc[j][i] *= e;
+                if (okr && n0 + tcol(tx, j) < s.N) rv[i] += cv[i][j] * acc[j][i];
+            }
         }
     }
     const int per = R, nts = TT / per;
@@ -760,6 +797,14 @@ __global__ __launch_bounds__(NTH, 4) void fwd_out(Args a) {
     f32x4 acc[4];
     zero(acc);
     const int pmax = s.P - 1;
+    // x_raw of this thread's outputs, read in one batch ahead of the contractions
+    float xrv[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = m0 + 4 * ty + i;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xrv[i][j] = q.lxr(m / R, min(p0 + tcol(tx, j), pmax), m % R);
+    }
     gemm_acc<TT, true, true>(acc, s.N,
                              [&](int mm, int n) { const int m = m0 + mm; return q.lc(m / R, n, m % R); },
                              [&](int mm, int n, float v) { const int m = m0 + mm; return q.ok(m / R, m % R) ? v : 0.f; },
@@ -792,7 +837,7 @@ __global__ __launch_bounds__(NTH, 4) void fwd_out(Args a) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int p = p0 + tcol(tx, j);
-            if (p < s.P) a.y[base + (int64_t)p * q.rk()] = acc[j][i] + Dh * a.xr[base + (int64_t)p * q.rk()];
+            if (p < s.P) a.y[base + (int64_t)p * q.rk()] = acc[j][i] + Dh * xrv[i][j];
         }
     }
 }
