@@ -418,7 +418,7 @@ def bench_ssd_bwd(args, torch, mamba3_amd):
                        "unit": "TFLOP/s", "frac": round(tflops / PEAK_FP32_TFLOPS, 4),
                        "traffic": traffic.get("ssd_bwd"),
                        "traffic_source": traffic_source(ROOT / "profiles" / "ssd_bwd_d768_trace_and_traffic.md"),
-                       "kernel": "m3_chunked_ssd_bwd, all kernels of one call (fp32 VALU GEMM tiles "
+                       "kernel": "m3_chunked_ssd_bwd, all kernels of one call (fp32-MFMA GEMM tiles "
                                  "against the fp32 matrix peak)",
                        "algorithmic_flops": flops, "avg_ms": round(kern_ms, 4)}
     if not args.no_cpu_baseline:
