@@ -76,6 +76,21 @@ struct Args {
 __device__ __forceinline__ int64_t chx(const Shape& s, int b, int k, int h) {
     return ((int64_t)b * (s.K + 1) + k) * s.H + h;
 }
+// Chunk and tile of a block of a kernel with `tiles` output tiles per chunk, launched as one
+// dimension of tile_grid(nch, tiles) blocks: the tiles of a chunk are 8 block indices apart, so
+// they run on one XCD (workgroups are dealt round-robin over the 8 XCDs) at about the same
+// time and share the chunk's operands through that XCD's L2. False for the padding blocks.
+constexpr int kXcds = 8;
+__device__ __forceinline__ bool chunk_tile(int nch, int tiles, int& ch, int& tile) {
+    const int L = blockIdx.x, rest = L / kXcds;
+    tile = rest % tiles;
+    ch = (rest / tiles) * kXcds + L % kXcds;
+    return ch < nch;
+}
+inline unsigned tile_grid(int64_t nch, int tiles) {
+    return (unsigned)((nch + kXcds - 1) / kXcds * kXcds * tiles);
+}
+
 // Offset of token row (b, tg, h) of a (B,T,H,X,R) tensor, in units of X*R elements.
 __device__ __forceinline__ int64_t row(const Shape& s, int b, int tg, int h) {
     return ((int64_t)b * s.T + tg) * s.H + h;
@@ -273,8 +288,10 @@ __global__ __launch_bounds__(NTH) void bwd_states(Args a) {
     __shared__ Lds<TW> l;
     __shared__ float cs[64], wx[64], ec[64];
     const Shape& s = a.s;
-    const int ch = blockIdx.x, h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
-    const int pt = blockIdx.y / s.nNt, nt = blockIdx.y % s.nNt;
+    int ch, tile;
+    if (!chunk_tile(s.B * s.K * s.H, s.nPt * s.nNt, ch, tile)) return;
+    const int h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
+    const int pt = tile / s.nNt, nt = tile % s.nNt;
     const int p0 = pt * TT, n0 = nt * TW;
     const Chunk<R, BETA, PADR> q{&a, b, k, h};
     if (threadIdx.x < QB) cs[threadIdx.x] = a.cum[(int64_t)ch * QB + threadIdx.x];
@@ -482,8 +499,10 @@ __global__ __launch_bounds__(NTH, 4) void bwd_dxf(Args a) {
     __shared__ float red[TT][17];
     __shared__ float cs[64], outv[64];
     const Shape& s = a.s;
-    const int ch = blockIdx.x, h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
-    const int rt = blockIdx.y / s.nPt, pt = blockIdx.y % s.nPt;
+    int ch, tile;
+    if (!chunk_tile(s.B * s.K * s.H, QR2 / TT * s.nPt, ch, tile)) return;
+    const int h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
+    const int rt = tile / s.nPt, pt = tile % s.nPt;
     const int m0 = rt * TT, p0 = pt * TT;
     const Chunk<R, BETA, PADR> q{&a, b, k, h};
     const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
@@ -561,8 +580,10 @@ __global__ __launch_bounds__(NTH, 4) void bwd_dbf(Args a) {
     __shared__ Lds<TW> l;
     __shared__ float cs[64], dts[64];
     const Shape& s = a.s;
-    const int ch = blockIdx.x, h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
-    const int rt = blockIdx.y / s.nNt, nt = blockIdx.y % s.nNt;
+    int ch, tile;
+    if (!chunk_tile(s.B * s.K * s.H, QR2 / TT * s.nNt, ch, tile)) return;
+    const int h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
+    const int rt = tile / s.nNt, nt = tile % s.nNt;
     const int m0 = rt * TT, n0 = nt * TW;
     constexpr int NJ = TW / 16;
     const Chunk<R, BETA, PADR> q{&a, b, k, h};
@@ -623,8 +644,10 @@ __global__ __launch_bounds__(NTH) void bwd_dc(Args a) {
     __shared__ float red[TT][17];
     __shared__ float cs[64], outv[64];
     const Shape& s = a.s;
-    const int ch = blockIdx.x, h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
-    const int rt = blockIdx.y / s.nNt, nt = blockIdx.y % s.nNt;
+    int ch, tile;
+    if (!chunk_tile(s.B * s.K * s.H, QR / TT * s.nNt, ch, tile)) return;
+    const int h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
+    const int rt = tile / s.nNt, nt = tile % s.nNt;
     const int m0 = rt * TT, n0 = nt * TW;
     constexpr int NJ = TW / 16;
     const Chunk<R, BETA, PADR> q{&a, b, k, h};
@@ -783,8 +806,10 @@ __global__ __launch_bounds__(NTH, 4) void fwd_out(Args a) {
     __shared__ Lds<TT> l;
     __shared__ float cs[64], dts[64];
     const Shape& s = a.s;
-    const int ch = blockIdx.x, h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
-    const int rt = blockIdx.y / s.nPt, pt = blockIdx.y % s.nPt;
+    int ch, tile;
+    if (!chunk_tile(s.B * s.K * s.H, QR / TT * s.nPt, ch, tile)) return;
+    const int h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
+    const int rt = tile / s.nPt, pt = tile % s.nPt;
     const int m0 = rt * TT, p0 = pt * TT;
     const Chunk<R, BETA, PADR> q{&a, b, k, h};
     const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
@@ -906,15 +931,15 @@ int launch(const Args& a, const float* h_init, float* dh_init, float* scan_ws, h
     const unsigned nch = (unsigned)((int64_t)s.B * s.K * s.H);
     constexpr int nRt = QR / TT, nRt2 = QR2 / TT;
     hipLaunchKernelGGL((bwd_cum<R, BETA, PADR>), dim3(nch), dim3(64), 0, stream, a);
-    hipLaunchKernelGGL((bwd_states<R, BETA, PADR>), dim3(nch, s.nPt * s.nNt), dim3(NTH), 0, stream, a);
+    hipLaunchKernelGGL((bwd_states<R, BETA, PADR>), dim3(tile_grid(nch, s.nPt * s.nNt)), dim3(NTH), 0, stream, a);
     if (launch_scan_fwd(a.dec, a.hext, h_init, a.Hs, s.B, s.K + 1, s.H, s.PN, stream) != 0) return 1;
     if (launch_scan_bwd(a.dec, a.Hs, a.gext, a.ddec, a.dch, dh_init, scan_ws, s.B, s.K + 1, s.H,
                         s.PN, stream) != 0)
         return 1;
     hipLaunchKernelGGL((bwd_scores<R, BETA, PADR>), dim3(nch), dim3(NTH), 0, stream, a);
-    hipLaunchKernelGGL((bwd_dxf<R, BETA, PADR>), dim3(nch, nRt2 * s.nPt), dim3(NTH), 0, stream, a);
-    hipLaunchKernelGGL((bwd_dbf<R, BETA, PADR>), dim3(nch, nRt2 * s.nNt), dim3(NTH), 0, stream, a);
-    hipLaunchKernelGGL((bwd_dc<R, BETA, PADR>), dim3(nch, nRt * s.nNt), dim3(NTH), 0, stream, a);
+    hipLaunchKernelGGL((bwd_dxf<R, BETA, PADR>), dim3(tile_grid(nch, nRt2 * s.nPt)), dim3(NTH), 0, stream, a);
+    hipLaunchKernelGGL((bwd_dbf<R, BETA, PADR>), dim3(tile_grid(nch, nRt2 * s.nNt)), dim3(NTH), 0, stream, a);
+    hipLaunchKernelGGL((bwd_dc<R, BETA, PADR>), dim3(tile_grid(nch, nRt * s.nNt)), dim3(NTH), 0, stream, a);
     hipLaunchKernelGGL((bwd_tokens<R, BETA, PADR>), dim3(nch), dim3(NTH), 0, stream, a);
     hipLaunchKernelGGL(bwd_reduce, dim3(s.H), dim3(NTH), 0, stream, a);
     return hipGetLastError() == hipSuccess ? 0 : 1;
@@ -943,10 +968,10 @@ int launch_fwd(const Args& a, const float* h_init, hipStream_t stream) {
     const unsigned nch = (unsigned)((int64_t)s.B * s.K * s.H);
     constexpr int nRt = QR / TT;
     hipLaunchKernelGGL((bwd_cum<R, BETA, PADR>), dim3(nch), dim3(64), 0, stream, a);
-    hipLaunchKernelGGL((bwd_states<R, BETA, PADR>), dim3(nch, s.nPt * s.nNt), dim3(NTH), 0, stream, a);
+    hipLaunchKernelGGL((bwd_states<R, BETA, PADR>), dim3(tile_grid(nch, s.nPt * s.nNt)), dim3(NTH), 0, stream, a);
     if (launch_scan_fwd(a.dec, a.hext, h_init, a.Hs, s.B, s.K + 1, s.H, s.PN, stream) != 0) return 1;
     hipLaunchKernelGGL((bwd_scores<R, BETA, PADR>), dim3(nch), dim3(NTH), 0, stream, a);
-    hipLaunchKernelGGL((fwd_out<R, BETA, PADR>), dim3(nch, nRt * s.nPt), dim3(NTH), 0, stream, a);
+    hipLaunchKernelGGL((fwd_out<R, BETA, PADR>), dim3(tile_grid(nch, nRt * s.nPt)), dim3(NTH), 0, stream, a);
     if (a.hfin) hipLaunchKernelGGL(fwd_final, dim3(s.B * s.H), dim3(NTH), 0, stream, a);
     return hipGetLastError() == hipSuccess ? 0 : 1;
 }
