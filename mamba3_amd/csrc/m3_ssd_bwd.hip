@@ -755,12 +755,33 @@ __global__ __launch_bounds__(NTH) void bwd_tokens(Args a) {
     const int nreal = min(QB, s.T - k * QB);
     const int per_tok = s.P * q.rk();
     float v = 0.f;
-    for (int e = tid; e < nreal * per_tok; e += NTH) {
-        const int t = e / per_tok, pr = e % per_tok;
-        const int64_t o = row(s, b, k * QB + t, h) * per_tok + pr;
-        const float g = a.dy[o];
-        v += g * a.xr[o];
-        a.dxr[o] = Dh * g;
+    const float* __restrict__ dy = a.dy;
+    const float* __restrict__ xr = a.xr;
+    float* __restrict__ dxr = a.dxr;
+    const bool vec = per_tok % 4 == 0 &&
+                     ((reinterpret_cast<uintptr_t>(dy) | reinterpret_cast<uintptr_t>(xr) |
+                       reinterpret_cast<uintptr_t>(dxr)) & 15) == 0;
+    if (vec) {  // 16-byte pieces of each token's row
+        const int q4 = per_tok / 4;
+        for (int e = tid; e < nreal * q4; e += NTH) {
+            const int t = e / q4, pr = e % q4;
+            const int64_t o = row(s, b, k * QB + t, h) * per_tok + 4 * pr;
+            const f32x4 g = *reinterpret_cast<const f32x4*>(dy + o);
+            const f32x4 x = *reinterpret_cast<const f32x4*>(xr + o);
+            v += g[0] * x[0];
+            v += g[1] * x[1];
+            v += g[2] * x[2];
+            v += g[3] * x[3];
+            *reinterpret_cast<f32x4*>(dxr + o) = g * Dh;
+        }
+    } else {
+        for (int e = tid; e < nreal * per_tok; e += NTH) {
+            const int t = e / per_tok, pr = e % per_tok;
+            const int64_t o = row(s, b, k * QB + t, h) * per_tok + pr;
+            const float g = dy[o];
+            v += g * xr[o];
+            dxr[o] = Dh * g;
+        }
     }
     part[tid] = v;
     __syncthreads();
