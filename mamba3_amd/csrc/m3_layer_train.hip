@@ -73,6 +73,45 @@ struct Args {
 
 __device__ __forceinline__ float sigm(float v) { return 1.f / (1.f + expf(-v)); }
 
+// The R values of one (token, head, column) of a (B,T,H,X,R) workspace array are contiguous and
+// 4R-byte aligned: 16-byte accesses when R % 4 == 0, 8-byte ones when R is
+// even, else one per value.
+template <int R>
+__device__ __forceinline__ void ldr(const float* p, float (&v)[R]) {
+    if constexpr (R % 4 == 0) {
+#pragma unroll
+        for (int j = 0; j < R / 4; ++j) {
+            const f32x4 q = *reinterpret_cast<const f32x4*>(p + 4 * j);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) v[4 * j + k] = q[k];
+        }
+    } else if constexpr (R % 2 == 0) {
+#pragma unroll
+        for (int j = 0; j < R / 2; ++j) {
+            const f32x2 q = *reinterpret_cast<const f32x2*>(p + 2 * j);
+            v[2 * j] = q[0];
+            v[2 * j + 1] = q[1];
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < R; ++j) v[j] = p[j];
+    }
+}
+template <int R>
+__device__ __forceinline__ void str(float* p, const float (&v)[R]) {
+    if constexpr (R % 4 == 0) {
+#pragma unroll
+        for (int j = 0; j < R / 4; ++j)
+            *reinterpret_cast<f32x4*>(p + 4 * j) = f32x4{v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]};
+    } else if constexpr (R % 2 == 0) {
+#pragma unroll
+        for (int j = 0; j < R / 2; ++j) *reinterpret_cast<f32x2*>(p + 2 * j) = f32x2{v[2 * j], v[2 * j + 1]};
+    } else {
+#pragma unroll
+        for (int j = 0; j < R; ++j) p[j] = v[j];
+    }
+}
+
 // Sum over the block (blockDim.x a power of two, at most NTH), in a fixed order.
 __device__ float block_sum(float v, float* red) {
     const int tid = threadIdx.x;
@@ -90,6 +129,7 @@ __device__ float block_sum(float v, float* red) {
 // ---- gate: one block per (b, token block, h) of NTH threads = slots of PT threads (PT = P
 // rounded up to a power of two), slot s handling tokens t0 + s, t0 + s + slots, ...; the
 // slots' parameter partials are added in order.
+template <int R>
 __global__ __launch_bounds__(NTH) void tb_gate(Args a) {
     __shared__ float red[2][NTH];
     const int nTB = (a.T + TBK - 1) / TBK;
@@ -100,30 +140,40 @@ __global__ __launch_bounds__(NTH) void tb_gate(Args a) {
     const int tid = threadIdx.x, slot = tid / PT, p = tid % PT;
     const bool col = p < a.P;
     const int64_t HP = (int64_t)a.H * a.P;
-    float pmd[8] = {0, 0, 0, 0, 0, 0, 0, 0}, pmz[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    float pmd[R], pmz[R], mz[R], md[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) pmd[r] = pmz[r] = 0.f;
     const int t1 = min(a.T, (tb + 1) * TBK);
     if (col) {
+        // parameters (caller pointers of any alignment): read once per thread
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            mz[r] = a.prm.mimo_z[((int64_t)h * a.P + p) * R + r];
+            md[r] = a.prm.mimo_down[((int64_t)h * a.P + p) * R + r];
+        }
         for (int t = tb * TBK + slot; t < t1; t += slots) {
             const int64_t tok = (int64_t)b * a.T + t;
             const float z = a.proj[tok * a.rs + a.pl.z + (int64_t)h * a.P + p];
             const float g = a.gout[tok * HP + (int64_t)h * a.P + p];
-            const int64_t yb = (tok * a.H + h) * a.P * a.R + (int64_t)p * a.R;
+            const int64_t yb = (tok * a.H + h) * a.P * R + (int64_t)p * R;
+            float y[R], gy[R];
+            ldr<R>(a.f.ys + yb, y);
             float gz = 0.f;
-            for (int r = 0; r < a.R; ++r) {
-                const int64_t pr = ((int64_t)h * a.P + p) * a.R + r;
-                const float mz = a.prm.mimo_z[pr], md = a.prm.mimo_down[pr];
-                const float zz = z * mz, sg = sigm(zz), silu = zz * sg, ds = sg * (1.f + zz * (1.f - sg));
-                const float y = a.f.ys[yb + r];
-                a.gys[yb + r] = g * md * silu;
-                gz += g * md * y * ds * mz;
-                pmd[r] += g * y * silu;
-                pmz[r] += g * md * y * ds * z;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const float zz = z * mz[r], sg = sigm(zz), silu = zz * sg, ds = sg * (1.f + zz * (1.f - sg));
+                gy[r] = g * md[r] * silu;
+                gz += g * md[r] * y[r] * ds * mz[r];
+                pmd[r] += g * y[r] * silu;
+                pmz[r] += g * md[r] * y[r] * ds * z;
             }
+            str<R>(a.gys + yb, gy);
             a.gproj[tok * a.rs + a.pl.z + (int64_t)h * a.P + p] = gz;
         }
     }
-    const int64_t o = (((int64_t)b * nTB + tb) * HP + (int64_t)h * a.P + p) * a.R;
-    for (int r = 0; r < a.R; ++r) {
+    const int64_t o = (((int64_t)b * nTB + tb) * HP + (int64_t)h * a.P + p) * R;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
         __syncthreads();
         red[0][tid] = pmd[r];
         red[1][tid] = pmz[r];
@@ -143,6 +193,7 @@ __global__ __launch_bounds__(NTH) void tb_gate(Args a) {
 // ---- x terms: one block per (b, token block, h) of NTH threads = slots of PT threads (PT = P
 // rounded up to a power of two): slot s handles tokens t0 + s, t0 + s + slots, ...; the
 // per-token sums over p are segmented block sums; the slots' partials are added in order.
+template <int R>
 __global__ __launch_bounds__(NTH) void tb_x(Args a) {
     __shared__ float red[2][NTH];
     __shared__ float part[NTH / 64];  // per slot: dL/dA
@@ -153,9 +204,13 @@ __global__ __launch_bounds__(NTH) void tb_x(Args a) {
     const int slots = NTH / PT;
     const int tid = threadIdx.x, slot = tid / PT, p = tid % PT;
     const bool col = p < a.P;
-    const int PR = a.P * a.R;
+    const int PR = a.P * R;
     const float Ah = a.f.A[h];
-    float pmx[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    float pmx[R], mx[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) pmx[r] = 0.f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) mx[r] = col ? a.prm.mimo_x[((int64_t)h * a.P + p) * R + r] : 0.f;
     float gA = 0.f;
     const int t0 = tb * TBK, t1 = min(a.T, (tb + 1) * TBK);
     const int rounds = (t1 - t0 + slots - 1) / slots;
@@ -177,23 +232,33 @@ __global__ __launch_bounds__(NTH) void tb_x(Args a) {
         float sl = 0.f, sa = 0.f;
         if (col && act) {
             const float x = row[a.pl.x + (int64_t)h * a.P + p];
+            const int64_t e0 = th * PR + (int64_t)p * R;
+            float gxr[R], gxg[R], gxb[R], xrv[R], gxbn[R], xrp[R];
+            ldr<R>(a.gxr + e0, gxr);
+            ldr<R>(a.gxg + e0, gxg);
+            if (a.trap) {
+                ldr<R>(a.gxb + e0, gxb);
+                ldr<R>(a.f.xr + e0, xrv);
+                if (t + 1 < a.T) ldr<R>(a.gxb + e0 + (int64_t)a.H * PR, gxbn);  // next token's
+                if (t > 0) ldr<R>(a.f.xr + e0 - (int64_t)a.H * PR, xrp);          // previous token's
+            }
             float gx = 0.f;
-            for (int r = 0; r < a.R; ++r) {
-                const int64_t e = th * PR + (int64_t)p * a.R + r;
-                float g = a.gxr[e] + (a.trap ? lam : 1.f) * a.gxg[e];
-                if (a.trap && t + 1 < a.T) g += (1.f - lamn) * dAn * a.gxb[e + (int64_t)a.H * PR];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                float g = gxr[r] + (a.trap ? lam : 1.f) * gxg[r];
+                if (a.trap && t + 1 < a.T) g += (1.f - lamn) * dAn * gxbn[r];
                 if (t == a.T - 1 && a.gprev) {
                     const float* gp = a.gprev + (((int64_t)b * a.H + h) * a.P + p) * a.N;
-                    const float* bt = a.f.Bt + th * a.N * a.R + r;
-                    for (int n = 0; n < a.N; ++n) g += gp[n] * bt[(int64_t)n * a.R];
+                    const float* bt = a.f.Bt + th * a.N * R + r;
+                    for (int n = 0; n < a.N; ++n) g += gp[n] * bt[(int64_t)n * R];
                 }
-                const float mx = a.prm.mimo_x[((int64_t)h * a.P + p) * a.R + r];
-                gx += g * mx;
+                gx += g * mx[r];
                 pmx[r] += g * x;
-                if (a.trap) {
-                    sl += a.gxg[e] * a.f.xr[e];
-                    if (t > 0) sa += a.gxb[e] * a.f.xr[e - (int64_t)a.H * PR];
-                }
+                if (a.trap) sl += gxg[r] * xrv[r];
+            }
+            if (a.trap && t > 0) {
+#pragma unroll
+                for (int r = 0; r < R; ++r) sa += gxb[r] * xrp[r];
             }
             a.gproj[tok * a.rs + a.pl.x + (int64_t)h * a.P + p] = gx;
         }
@@ -232,14 +297,15 @@ __global__ __launch_bounds__(NTH) void tb_x(Args a) {
     }
     // the slots' mimo_x partials and dL/dA, added in slot order
     float* pm = &red[0][0];  // one rank at a time
-    for (int r = 0; r < a.R; ++r) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
         __syncthreads();
         pm[tid] = pmx[r];
         __syncthreads();
         if (slot == 0 && col) {
             float s = 0.f;
             for (int k = 0; k < slots; ++k) s += pm[k * PT + p];
-            const int64_t o = (((int64_t)b * nTB + tb) * a.H * a.P + (int64_t)h * a.P + p) * a.R;
+            const int64_t o = (((int64_t)b * nTB + tb) * a.H * a.P + (int64_t)h * a.P + p) * R;
             a.p_mx[o + r] = s;
         }
     }
@@ -667,13 +733,33 @@ int launch_layer_bwd(const m3_layer_desc& d, const m3_layer_params& p, const voi
 
     const int nTB = (a.T + TBK - 1) / TBK, nTC = (a.T + TBC - 1) / TBC;
     const unsigned gbh = (unsigned)((int64_t)a.B * nTB * a.H);
-    hipLaunchKernelGGL(tb_gate, dim3(gbh), dim3(NTH), 0, stream, a);
+    switch (a.R) {
+        case 1: hipLaunchKernelGGL(tb_gate<1>, dim3(gbh), dim3(NTH), 0, stream, a); break;
+        case 2: hipLaunchKernelGGL(tb_gate<2>, dim3(gbh), dim3(NTH), 0, stream, a); break;
+        case 3: hipLaunchKernelGGL(tb_gate<3>, dim3(gbh), dim3(NTH), 0, stream, a); break;
+        case 4: hipLaunchKernelGGL(tb_gate<4>, dim3(gbh), dim3(NTH), 0, stream, a); break;
+        case 5: hipLaunchKernelGGL(tb_gate<5>, dim3(gbh), dim3(NTH), 0, stream, a); break;
+        case 6: hipLaunchKernelGGL(tb_gate<6>, dim3(gbh), dim3(NTH), 0, stream, a); break;
+        case 7: hipLaunchKernelGGL(tb_gate<7>, dim3(gbh), dim3(NTH), 0, stream, a); break;
+        case 8: hipLaunchKernelGGL(tb_gate<8>, dim3(gbh), dim3(NTH), 0, stream, a); break;
+        default: return 1;
+    }
     if (launch_chunked_bwd(a.B, a.T, a.H, a.P, a.N, a.R, a.f.xg, a.f.xb, a.f.Bt, a.f.Bb, a.f.Ct,
                            a.f.dt, a.f.A, p.D, a.f.xr, nullptr, a.gys, g_h, a.gxg, a.gxb, a.gBt,
                            a.gBb, a.gCt, a.gdtc, a.gAc, a.gD, a.gxr, nullptr,
                            ws + pl.chunk_off, stream) != 0)
         return 1;
-    hipLaunchKernelGGL(tb_x, dim3(gbh), dim3(NTH), 0, stream, a);
+    switch (a.R) {
+        case 1: hipLaunchKernelGGL(tb_x<1>, dim3(gbh), dim3(NTH), 0, stream, a); break;
+        case 2: hipLaunchKernelGGL(tb_x<2>, dim3(gbh), dim3(NTH), 0, stream, a); break;
+        case 3: hipLaunchKernelGGL(tb_x<3>, dim3(gbh), dim3(NTH), 0, stream, a); break;
+        case 4: hipLaunchKernelGGL(tb_x<4>, dim3(gbh), dim3(NTH), 0, stream, a); break;
+        case 5: hipLaunchKernelGGL(tb_x<5>, dim3(gbh), dim3(NTH), 0, stream, a); break;
+        case 6: hipLaunchKernelGGL(tb_x<6>, dim3(gbh), dim3(NTH), 0, stream, a); break;
+        case 7: hipLaunchKernelGGL(tb_x<7>, dim3(gbh), dim3(NTH), 0, stream, a); break;
+        case 8: hipLaunchKernelGGL(tb_x<8>, dim3(gbh), dim3(NTH), 0, stream, a); break;
+        default: return 1;
+    }
     const dim3 gbc((unsigned)((int64_t)a.B * nTC));
     const size_t lbc = bc_lds(d);
     int st = 1;
