@@ -321,8 +321,9 @@ __global__ __launch_bounds__(NTH) void tb_x(Args a) {
 // ---- B / C: one block per (b, TBC tokens), one group g at a time, token by token. Thread
 // (pair i, head slot hg) handles the heads g hpg + hl, hl = hg (mod HS), of pair i and
 // accumulates into its own LDS partial of the group's dL/dB^, dL/dC^; the HS partials are
-// then summed in order. LDS: the partials, dL/dB^, dL/dC^, the parameter partials of the
-// group, the reduction scratch.
+// then summed in order. The rotated rows dL/dphi needs are formed again from the group's
+// normalised B^ / C^ (kept in LDS) and the cos / sin, not read back. LDS: the partials,
+// dL/dB^, dL/dC^, the parameter partials of the group, B^ / C^, the reduction scratch.
 __device__ __forceinline__ int bc_hs(int N) { return max(1, NTH / (N / 2)); }
 
 // The K = 2R values of pair i (even column, ranks 0..R-1, then odd column) are contiguous
@@ -354,13 +355,16 @@ __global__ __launch_bounds__(NTH) void tb_bc(Args a) {
     const int HS = bc_hs(a.N);
     float* qB = sm;                 // [HS][NR]
     float* qC = qB + HS * NR;       // [HS][NR]
-    float* gBh = qC + HS * NR;
-    float* gCh = gBh + NR;
-    float* pBw = gCh + NR;
+    float* nx = qC + HS * NR;
+    float* gBh = HS > 1 ? nx : qB;  // with one head slot its partial is the sum
+    float* gCh = HS > 1 ? nx + NR : qC;
+    float* pBw = nx + (HS > 1 ? 2 * NR : 0);
     float* pCw = pBw + NR;
     float* pBb = pCw + NR;
     float* pCb = pBb + NR;
-    float* red = pCb + NR;
+    float* Bh = pCb + NR;           // the token's normalised B^ / C^ of group g
+    float* Ch = Bh + NR;
+    float* red = Ch + NR;
     const int nTB = (a.T + TBC - 1) / TBC;
     const int tb = blockIdx.x % nTB, b = blockIdx.x / nTB;
     const int64_t ob = (int64_t)blockIdx.x;
@@ -374,6 +378,24 @@ __global__ __launch_bounds__(NTH) void tb_bc(Args a) {
         for (int t = tb * TBC; t < t1; ++t) {
             const int64_t tok = (int64_t)b * a.T + t;
             const float* row = a.proj + tok * a.rs;
+            const float* vb = row + a.pl.B + (int64_t)g * NR;
+            const float* vc = row + a.pl.C + (int64_t)g * NR;
+            // RMS of the raw rows, then (with RoPE) B^ / C^ in LDS: the rotated rows of every
+            // head are formed from them again below instead of being read back
+            float sb = 0.f, sc = 0.f;
+            for (int e = tid; e < NR; e += NTH) {
+                sb += vb[e] * vb[e];
+                sc += vc[e] * vc[e];
+            }
+            sb = block_sum(sb, red);
+            sc = block_sum(sc, red);
+            const float rb = rsqrtf(sb / NR + a.eps), rc = rsqrtf(sc / NR + a.eps);
+            if (a.cplx) {
+                for (int e = tid; e < NR; e += NTH) {
+                    Bh[e] = vb[e] * rb * a.prm.B_norm_w[e] + a.prm.B_bias[(int64_t)g * NR + e];
+                    Ch[e] = vc[e] * rc * a.prm.C_norm_w[e] + a.prm.C_bias[(int64_t)g * NR + e];
+                }
+            }
             for (int e = tid; e < HS * NR; e += NTH) qB[e] = qC[e] = 0.f;
             __syncthreads();
             for (int hl = hg; hl < hpg; hl += HS) {
@@ -387,7 +409,7 @@ __global__ __launch_bounds__(NTH) void tb_bc(Args a) {
                     if (a.cplx) sincosf(a.f.phi[th * NH + i], &s, &c);
                     float gphi = 0.f;
                     const int64_t e0 = bt + (int64_t)(2 * i) * R;
-                    float gb[2 * R], gc[2 * R], vb[2 * R], vc[2 * R];
+                    float gb[2 * R], gc[2 * R];
                     ldv<2 * R>(a.gBt + e0, gb);
                     ldv<2 * R>(a.gCt + e0, gc);
                     if (a.trap && t + 1 < a.T) {
@@ -395,10 +417,6 @@ __global__ __launch_bounds__(NTH) void tb_bc(Args a) {
                         ldv<2 * R>(a.gBb + e0 + (int64_t)a.H * NR, nb);
 #pragma unroll
                         for (int k = 0; k < 2 * R; ++k) gb[k] += nb[k];
-                    }
-                    if (a.cplx) {
-                        ldv<2 * R>(a.f.Bt + e0, vb);
-                        ldv<2 * R>(a.f.Ct + e0, vc);
                     }
 #pragma unroll
                     for (int r = 0; r < R; ++r) {
@@ -412,8 +430,13 @@ __global__ __launch_bounds__(NTH) void tb_bc(Args a) {
                             }
                         }
                         const float gce = gc[r], gco = gc[R + r];
-                        if (a.cplx) gphi += gbo * vb[r] - gbe * vb[R + r] + gco * vc[r] - gce * vc[R + r];
                         const int je = (2 * i) * R + r, jo = je + R;
+                        if (a.cplx) {
+                            // the rotated rows: e' = e cos - o sin, o' = e sin + o cos
+                            const float be = Bh[je] * c - Bh[jo] * s, bo = Bh[je] * s + Bh[jo] * c;
+                            const float ce = Ch[je] * c - Ch[jo] * s, co = Ch[je] * s + Ch[jo] * c;
+                            gphi += gbo * be - gbe * bo + gco * ce - gce * co;
+                        }
                         qb[je] += gbe * c + gbo * s;
                         qb[jo] += gbo * c - gbe * s;
                         qc[je] += gce * c + gco * s;
@@ -423,31 +446,26 @@ __global__ __launch_bounds__(NTH) void tb_bc(Args a) {
                 }
             }
             __syncthreads();
-            for (int e = tid; e < NR; e += NTH) {
-                float sb = 0.f, sc = 0.f;
-                for (int k = 0; k < HS; ++k) {
-                    sb += qB[(int64_t)k * NR + e];
-                    sc += qC[(int64_t)k * NR + e];
+            if (HS > 1) {
+                for (int e = tid; e < NR; e += NTH) {
+                    float sbh = 0.f, sch = 0.f;
+                    for (int k = 0; k < HS; ++k) {
+                        sbh += qB[(int64_t)k * NR + e];
+                        sch += qC[(int64_t)k * NR + e];
+                    }
+                    gBh[e] = sbh;
+                    gCh[e] = sch;
                 }
-                gBh[e] = sb;
-                gCh[e] = sc;
+                __syncthreads();
             }
-            __syncthreads();
             // RMSNorm backward of group g; parameter partials
-            const float* vb = row + a.pl.B + (int64_t)g * NR;
-            const float* vc = row + a.pl.C + (int64_t)g * NR;
-            float sb = 0.f, sc = 0.f, wb = 0.f, wc = 0.f;
+            float wb = 0.f, wc = 0.f;
             for (int e = tid; e < NR; e += NTH) {
-                sb += vb[e] * vb[e];
-                sc += vc[e] * vc[e];
                 wb += gBh[e] * a.prm.B_norm_w[e] * vb[e];
                 wc += gCh[e] * a.prm.C_norm_w[e] * vc[e];
             }
-            sb = block_sum(sb, red);
-            sc = block_sum(sc, red);
             wb = block_sum(wb, red);
             wc = block_sum(wc, red);
-            const float rb = rsqrtf(sb / NR + a.eps), rc = rsqrtf(sc / NR + a.eps);
             const float kb = rb * rb * rb * wb / NR, kc = rc * rc * rc * wc / NR;
             for (int e = tid; e < NR; e += NTH) {
                 const float gb = gBh[e], gc = gCh[e];
@@ -681,12 +699,13 @@ Plan plan(const m3_layer_desc& d) {
     return p;
 }
 
-// LDS of tb_bc: (2 HS + 6) N R + NTH floats, at most 132 KB (d_state 512, rank 8).
+// LDS of tb_bc: (2 HS + 8) N R + NTH floats, 2 N R fewer with one head slot (HS = 1 at
+// d_state 512), so at most 132 KB (d_state 512, rank 8).
 constexpr size_t kBcMaxLds = 160 * 1024;  // gfx950's LDS per workgroup
 size_t bc_lds(const m3_layer_desc& d) {
     const size_t NR = (size_t)d.d_state * d.mimo_rank;
     const size_t HS = std::max(1, NTH / (d.d_state / 2));
-    return ((2 * HS + 6) * NR + NTH) * sizeof(float);
+    return ((2 * HS + (HS > 1 ? 2 : 0) + 6) * NR + NTH) * sizeof(float);
 }
 
 // tb_bc<R> with `lds` bytes of dynamic LDS; above 64 KB the kernel's limit is raised first.
