@@ -83,20 +83,33 @@ int launch_chunked_fwd_mfma(int B, int T, int H, int P, int N, int R, const floa
                             const float* h_init, float* y, float* h_final, void* workspace,
                             hipStream_t stream);
 size_t chunked_bwd_workspace(int B, int T, int H, int P, int N, int R, bool beta);
+// Byte offset, in the fp32-MFMA chunk forward's workspace, of its chunk-start states
+// (B, K+1, H, P, N): the hs_pre a backward of the same shape may take.
+size_t chunked_fwd_hs_offset(int B, int T, int H, int P, int N, int R, bool beta);
+// Tokens per chunk of the fp32-MFMA chunk kernels (0 for shapes they do not take).
+int chunked_chunk_tokens(int R, bool beta);
 int launch_chunked_bwd(int B, int T, int H, int P, int N, int R, const float* x_g,
                        const float* x_b, const float* B_g, const float* B_b, const float* C,
                        const float* dt, const float* A, const float* D, const float* x_raw,
                        const float* h_init, const float* dy, const float* dh_final, float* dx_g,
                        float* dx_b, float* dB_g, float* dB_b, float* dC, float* ddt, float* dA,
                        float* dD, float* dx_raw, float* dh_init, void* workspace,
-                       hipStream_t stream);
+                       hipStream_t stream, const float* hs_pre = nullptr);
 
 // fp32 layer prefill on the fp32-MFMA chunk kernels (preparation, chunked SSD, gate).
 // Its workspace holds chunked_ssd's inputs and the SSD output, which the layer backward reads.
+// The training forward's per-token operands of the layer backward, and Hs: the chunk-start
+// states (B, K+1, H, P, N) in the fp32 chunk kernels' chunking (entry 0 the zero start,
+// entry K the final state), which the backward reads instead of recomputing them.
 struct Fp32LayerParts {
-    float *dt, *A, *phi, *xg, *xb, *xr, *Bt, *Bb, *Ct, *ys;
+    float *dt, *A, *phi, *xg, *xb, *xr, *Bt, *Bb, *Ct, *ys, *Hs;
 };
 Fp32LayerParts fp32_layer_parts(const m3_layer_desc& d, void* workspace);
+// Whether the training forward leaves valid chunk-start states in Fp32LayerParts::Hs (then the
+// fused fp32 forward keeps its B^ rows at the chunk-kernel region's start and its C^ rows
+// lp::al(fp32_layer_hs_bytes) past Hs), and their size.
+bool fp32_layer_hs_ok(const m3_layer_desc& d);
+size_t fp32_layer_hs_bytes(const m3_layer_desc& d);
 bool fp32_layer_supported(const m3_layer_desc& d);
 // Fused fp32 prefill (m3_ssd_f32.hip): d_state 128, headdim 64, rank 2, without
 // M3_FLAG_FOR_BACKWARD; 16-byte aligned rows of proj and y_out, h_final and prev_bx.

@@ -313,8 +313,33 @@ Fp32LayerParts fp32_layer_parts(const m3_layer_desc& d, void* workspace) {
     char* ws = reinterpret_cast<char*>(workspace);
     auto part = [&](int i) { return reinterpret_cast<float*>(ws + pl.off[i]); };
     const bool trap = d.use_trapezoidal != 0;
+    float* hs = reinterpret_cast<float*>(
+        ws + pl.chunk_off + chunked_fwd_hs_offset(d.batch, d.seqlen, d.nheads, d.headdim, d.d_state,
+                                                  d.mimo_rank, trap));
     return Fp32LayerParts{part(0), part(1), part(2), part(3), trap ? part(4) : nullptr, part(5),
-                          part(6), trap ? part(7) : nullptr, part(8), part(9)};
+                          part(6), trap ? part(7) : nullptr, part(8), part(9), hs};
+}
+
+// The chunk-start states of the training forward (Fp32LayerParts::Hs) are valid for the
+// backward when the fused fp32 forward can keep its B^ rows below them and its C^ rows above
+// them in the chunk-kernel region (the staged forward's chunk kernels always write them).
+// Decided from the descriptor alone, so the forward that writes them and the backward that
+// reads them agree.
+size_t fp32_layer_hs_bytes(const m3_layer_desc& d) {
+    const int qb = chunked_chunk_tokens(d.mimo_rank, d.use_trapezoidal != 0);
+    if (qb <= 0) return 0;
+    const size_t K = (d.seqlen + qb - 1) / qb;
+    return (size_t)d.batch * (K + 1) * d.nheads * d.headdim * d.d_state * sizeof(float);
+}
+bool fp32_layer_hs_ok(const m3_layer_desc& d) {
+    const bool trap = d.use_trapezoidal != 0;
+    const size_t hs = chunked_fwd_hs_offset(d.batch, d.seqlen, d.nheads, d.headdim, d.d_state,
+                                            d.mimo_rank, trap);
+    const size_t region = chunked_fwd_mfma_workspace(d.batch, d.seqlen, d.nheads, d.headdim,
+                                                     d.d_state, d.mimo_rank, trap);
+    const size_t rows = (size_t)d.batch * d.seqlen * d.ngroups * d.d_state * d.mimo_rank * sizeof(float);
+    const size_t hsb = fp32_layer_hs_bytes(d);
+    return hs > 0 && hsb > 0 && rows <= hs && hs + lp::al(hsb) + rows <= region;
 }
 
 void* fp32_layer_scratch(const m3_layer_desc& d, void* ws, size_t* bytes) {

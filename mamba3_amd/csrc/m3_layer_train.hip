@@ -766,7 +766,7 @@ int launch_layer_bwd(const m3_layer_desc& d, const m3_layer_params& p, const voi
     if (launch_chunked_bwd(a.B, a.T, a.H, a.P, a.N, a.R, a.f.xg, a.f.xb, a.f.Bt, a.f.Bb, a.f.Ct,
                            a.f.dt, a.f.A, p.D, a.f.xr, nullptr, a.gys, g_h, a.gxg, a.gxb, a.gBt,
                            a.gBb, a.gCt, a.gdtc, a.gAc, a.gD, a.gxr, nullptr,
-                           ws + pl.chunk_off, stream) != 0)
+                           ws + pl.chunk_off, stream, fp32_layer_hs_ok(d) ? a.f.Hs : nullptr) != 0)
         return 1;
     switch (a.R) {
         case 1: hipLaunchKernelGGL(tb_x<1>, dim3(gbh), dim3(NTH), 0, stream, a); break;

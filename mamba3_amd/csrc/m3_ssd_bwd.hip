@@ -68,6 +68,9 @@ struct Args {
         *pA, *pD;
     // forward (fwd = 1): the chunk-state and score kernels skip their gradient halves
     int fwd;
+    // have_hs = 1: the chunk-start states Hs come from the forward (the chunk-local states and
+    // the forward scan are skipped)
+    int have_hs;
     float *y, *hfin;
 };
 
@@ -305,8 +308,9 @@ __global__ __launch_bounds__(NTH) void bwd_states(Args a) {
     const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
     constexpr int NJ = TW / 16;
     f32x4 acc[NJ];
-    zero(acc);
     const int pmax = s.P - 1, nmax = s.N - 1;
+    if (!a.have_hs) {
+    zero(acc);
     gemm_acc<TW, false, false>(acc, QB * R2,
                  [&](int mm, int j) { return q.lx(j / R2, min(p0 + mm, pmax), j % R2); },
                  [&](int mm, int j, float v) {
@@ -325,6 +329,7 @@ __global__ __launch_bounds__(NTH) void bwd_states(Args a) {
             const int p = p0 + 4 * ty + i, n = n0 + tcol(tx, j);
             if (p < s.P && n < s.N) ho[(int64_t)p * s.N + n] = acc[j][i];
         }
+    }
     if (!a.fwd) {
     zero(acc);
     gemm_acc<TW, false, false>(acc, QB * R,
@@ -357,7 +362,7 @@ __global__ __launch_bounds__(NTH) void bwd_states(Args a) {
                 const int p = p0 + 4 * ty + i, n = n0 + tcol(tx, j);
                 if (p < s.P && n < s.N) {
                     const int64_t o = (int64_t)p * s.N + n;
-                    he[o] = 0.f;
+                    if (!a.have_hs) he[o] = 0.f;
                     if (!a.fwd) ge[o] = df ? df[o] : 0.f;
                 }
             }
@@ -953,7 +958,9 @@ int launch(const Args& a, const float* h_init, float* dh_init, float* scan_ws, h
     constexpr int nRt = QR / TT, nRt2 = QR2 / TT;
     hipLaunchKernelGGL((bwd_cum<R, BETA, PADR>), dim3(nch), dim3(64), 0, stream, a);
     hipLaunchKernelGGL((bwd_states<R, BETA, PADR>), dim3(tile_grid(nch, s.nPt * s.nNt)), dim3(NTH), 0, stream, a);
-    if (launch_scan_fwd(a.dec, a.hext, h_init, a.Hs, s.B, s.K + 1, s.H, s.PN, stream) != 0) return 1;
+    if (!a.have_hs &&
+        launch_scan_fwd(a.dec, a.hext, h_init, a.Hs, s.B, s.K + 1, s.H, s.PN, stream) != 0)
+        return 1;
     if (launch_scan_bwd(a.dec, a.Hs, a.gext, a.ddec, a.dch, dh_init, scan_ws, s.B, s.K + 1, s.H,
                         s.PN, stream) != 0)
         return 1;
@@ -1041,6 +1048,17 @@ int launch_chunked_fwd_mfma(int B, int T, int H, int P, int N, int R, const floa
     }
 }
 
+size_t chunked_fwd_hs_offset(int B, int T, int H, int P, int N, int R, bool beta) {
+    bw::Shape s;
+    if (!bw::make_shape(B, T, H, P, N, R, beta, s)) return 0;
+    return bw::make_plan_fwd(s).off[3];
+}
+
+int chunked_chunk_tokens(int R, bool beta) {
+    bw::Shape s;
+    return bw::make_shape(1, 1, 1, 1, 2, R, beta, s) ? s.Qb : 0;
+}
+
 bool chunked_bwd_shape_ok(int B, int T, int H, int P, int N, int R, bool beta) {
     bw::Shape s;
     if (!bw::make_shape(B, T, H, P, N, R, beta, s)) return false;
@@ -1059,7 +1077,7 @@ int launch_chunked_bwd(int B, int T, int H, int P, int N, int R, const float* x_
                        const float* h_init, const float* dy, const float* dh_final, float* dx_g,
                        float* dx_b, float* dB_g, float* dB_b, float* dC, float* ddt, float* dA,
                        float* dD, float* dx_raw, float* dh_init, void* workspace,
-                       hipStream_t stream) {
+                       hipStream_t stream, const float* hs_pre) {
     using namespace bw;
     Shape s;
     if (!make_shape(B, T, H, P, N, R, x_b != nullptr, s)) return 1;
@@ -1077,6 +1095,8 @@ int launch_chunked_bwd(int B, int T, int H, int P, int N, int R, const float* x_
     a.pInter = part(10), a.pState = part(11), a.pDt = part(12), a.pA = part(13), a.pD = part(14);
     float* scan_ws = reinterpret_cast<float*>(ws + pl.scan_off);
     a.fwd = 0, a.y = nullptr, a.hfin = nullptr;
+    a.have_hs = hs_pre != nullptr;
+    if (hs_pre) a.Hs = const_cast<float*>(hs_pre);  // read only
 
     const bool beta = x_b != nullptr, pad = s.RT != s.R;
     switch (s.RT * 4 + (beta ? 2 : 0) + (pad ? 1 : 0)) {

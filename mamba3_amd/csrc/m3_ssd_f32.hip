@@ -82,6 +82,10 @@ struct Args {
     // the previous token, C~ and y before the gate.
     Fp32LayerParts st;
     int stage;
+    // With hs_every > 0 the walk also stores its chunk-start states into st.Hs in the layer
+    // backward's chunking: the state entering every hs_every-th chunk k at entry k / hs_every
+    // of (B, hs_K + 1, H, P, N) (the zero start at entry 0), and the final state at entry hs_K.
+    int hs_every, hs_K;
 };
 
 __device__ __forceinline__ f32x4 mfma4(float a, float b, const f32x4& c) {
@@ -257,6 +261,12 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_f32(Args a) {
         for (int pt = 0; pt < NPT; ++pt)
 #pragma unroll
             for (int v = 0; v < 4; ++v) sm.H[16 * wv + 4 * g4 + v][16 * pt + l16] = hacc[pt][v];
+        if (a.hs_every > 0 && k == 0) {  // the zero start state
+            float* hk = a.st.Hs + ((int64_t)b * (a.hs_K + 1) * a.H + h) * (P * N) + (int64_t)pc * N;
+#pragma unroll
+            for (int pt = 0; pt < NPT; ++pt)
+                *reinterpret_cast<f32x4*>(&hk[(16 * pt + l16) * N + 16 * wv + 4 * g4]) = hacc[pt];
+        }
         __syncthreads();
         if (a.stage && s0 + xu < T) {
             // x_r, x_g = lambda_t x_r and x_b of the next token = (1 - lambda_{t+1})
@@ -397,6 +407,27 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_f32(Args a) {
                 for (int pt = 0; pt < NPT; ++pt) hacc[pt] = mfma4(bw, sm.X[k0 + g4][16 * pt + l16], hacc[pt]);
             }
         }
+        // ---- the state entering chunk k + 1 for the layer backward. The walk folds the beta
+        // term of the next chunk's first token into this chunk (b_{Q-1} B~_{Q-1} x_{Q-1}^T, the
+        // last row pair of the tiles); the chunk kernels count it in the next chunk, so it is
+        // taken out of the stored state (b = 0 without the trapezoid).
+        if (a.hs_every > 0 && (k + 1) % a.hs_every == 0 && k + 1 < K) {
+            const float bq = sm.bv[Q - 1];
+            float* hk = a.st.Hs + (((int64_t)b * (a.hs_K + 1) + (k + 1) / a.hs_every) * a.H + h) * (P * N) +
+                        (int64_t)pc * N;
+#pragma unroll
+            for (int pt = 0; pt < NPT; ++pt) {
+                const int pl = 16 * pt + l16;
+                const float x0 = sm.X[2 * (Q - 1)][pl], x1 = sm.X[2 * (Q - 1) + 1][pl];
+                f32x4 o;
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int n = 16 * wv + 4 * g4 + v;
+                    o[v] = hacc[pt][v] - bq * (sm.B[2 * (Q - 1)][n] * x0 + sm.B[2 * (Q - 1) + 1][n] * x1);
+                }
+                *reinterpret_cast<f32x4*>(&hk[pl * N + 16 * wv + 4 * g4]) = o;
+            }
+        }
         // ---- gate and MIMO-down; rows 4 g4 + 2 tt + r of the block are (t, r)
 #pragma unroll
         for (int q = 0; q < TPW; ++q) {
@@ -418,6 +449,12 @@ __global__ __launch_bounds__(THREADS, 1) void ssd_f32(Args a) {
     }
     __syncthreads();
     // ---- outputs of the walk
+    if (a.hs_every > 0) {
+        float* hk = a.st.Hs + (((int64_t)b * (a.hs_K + 1) + a.hs_K) * a.H + h) * (P * N) + (int64_t)pc * N;
+#pragma unroll
+        for (int pt = 0; pt < NPT; ++pt)
+            *reinterpret_cast<f32x4*>(&hk[(16 * pt + l16) * N + 16 * wv + 4 * g4]) = hacc[pt];
+    }
     if (a.h_final) {
         float* hf = a.h_final + (int64_t)bh * P * N + (int64_t)pc * N;
 #pragma unroll
@@ -481,6 +518,21 @@ int launch_fused_fp32_prefill(const m3_layer_desc& d, const m3_layer_params& p, 
     const int64_t nrows = (int64_t)d.batch * d.seqlen * d.ngroups;
     float* bn = reinterpret_cast<float*>(workspace);
     float* cn = bn + nrows * f32k::NR;
+    // Training forward with room for the chunk-start states (workspace = the fp32 layer
+    // workspace's chunk-kernel region, whose Hs part is stage->Hs): C^ rows past them.
+    const bool hs = stage && stage->Hs && fp32_layer_hs_ok(d);
+    int hs_every = 0, hs_K = 0;
+    if (hs) {
+        const bool trap = d.use_trapezoidal != 0;
+        const size_t off = chunked_fwd_hs_offset(d.batch, d.seqlen, d.nheads, d.headdim, d.d_state,
+                                                 d.mimo_rank, trap);
+        const size_t hsb = (fp32_layer_hs_bytes(d) + 255) & ~(size_t)255;
+        cn = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + off + hsb);
+        const int qb = chunked_chunk_tokens(d.mimo_rank, trap);
+        if (qb % f32k::Q != 0) return M3_ERR_UNSUPPORTED;
+        hs_every = qb / f32k::Q;
+        hs_K = (d.seqlen + qb - 1) / qb;
+    }
     hipLaunchKernelGGL(f32k::bc_norm_f32, dim3((unsigned)((nrows + 3) / 4)), dim3(256), 0, stream,
                        reinterpret_cast<const float*>(proj), d.proj_row_stride, pl.B, pl.C, d.ngroups,
                        nrows, d.rms_eps, p.B_norm_w, p.B_bias, p.C_norm_w, p.C_bias, bn, cn);
@@ -500,6 +552,8 @@ int launch_fused_fp32_prefill(const m3_layer_desc& d, const m3_layer_params& p, 
     a.prev_bx = prev_bx;
     a.st = stage ? *stage : Fp32LayerParts{};
     a.stage = stage != nullptr;
+    a.hs_every = hs_every;
+    a.hs_K = hs_K;
     // two 32-column blocks per (batch, head) while the pairs alone leave CUs idle
     const int64_t bh = (int64_t)d.batch * d.nheads;
     if (bh < 256)
