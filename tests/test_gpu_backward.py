@@ -270,8 +270,12 @@ def test_layer_state_gradients_match_oracle(kw, cuda_device):
 D768_KW = dict(d_model=768, d_state=128, headdim=64, mimo_rank=2)
 
 
-@pytest.mark.parametrize("extra", [{}, dict(use_trapezoidal=False), dict(use_complex_ssm=False)],
-                         ids=["default", "trapezoid-off", "complex-off"])
+@pytest.mark.parametrize("extra", [{}, dict(use_trapezoidal=False), dict(use_complex_ssm=False),
+                                   # 24 groups without the trapezoid: the forward's B^ / C^ rows
+                                   # leave no room for the chunk-start states, which the
+                                   # backward then recomputes
+                                   dict(use_trapezoidal=False, ngroups=24)],
+                         ids=["default", "trapezoid-off", "complex-off", "trapezoid-off-24-groups"])
 def test_layer_d768_fused_training_forward_state_gradients(extra, cuda_device):
     """The d_model 768 shape (d_state 128, headdim 64, rank 2) trains on the fused fp32
     prefill kernel, which also writes the per-token operands m3_layer_bwd reads. Two
