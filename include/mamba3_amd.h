@@ -164,7 +164,8 @@ int m3_scan_bwd(const float* decay, const float* h_states, const float* grad, fl
 
 /*
  * Backward of m3_prefill_fwd for fp32 layers (desc->dtype fp32, mimo_rank 1..8), from the
- * workspace of that forward call, which holds its intermediates (pass the same buffer, unchanged,
+ * workspace of that forward call, which holds its intermediates (the per-token operands and,
+ * for most shapes, the chunk-start states the backward then does not recompute; pass the same buffer, unchanged,
  * with its size; that forward ran with M3_FLAG_FOR_BACKWARD in desc->flags, as does this call). Replaces the reference's autograd through mamba3/mamba3.py:197-256 (ATen's
  * backward of the dt softplus, the B/C RMSNorm + bias, the RoPE rotation and its angle cumsum,
  * the MIMO and trapezoid terms and the SiLU gate) and through chunked_ssd (see
