@@ -14,9 +14,10 @@
 // pieces) share an output row and split K into 16-byte pieces (lane s reads
 // k = 8 s + 8 LPR j), so the lanes of a row read contiguous bytes, and every lane issues all
 // its pieces before it uses them, ahead of the activations' staging: one memory round trip
-// per kernel, spread over N * LPR / 128 blocks of 128 threads. The (normalised) activations
-// are staged once per block in LDS as bf16 (with the norm weight), padded to MM rows with
-// zeros and followed by one zero piece that
+// per kernel, spread over N * LPR / 256 blocks of 256 threads. The (normalised) activations
+// are staged once per block in LDS as bf16 (with the norm weight), so larger blocks stage
+// them fewer times (256 threads: +8% LM decode against 128; 512 is slower), padded to MM rows
+// with zeros and followed by one zero piece that
 // stands in for the steps past K in the last group of 8 (whose weight reads are clamped to
 // the last piece of the row). Every row group reads the same LDS addresses (broadcast). Dot
 // products accumulate in fp32 (v_dot2_f32_bf16); DPP steps (and lane shuffles beyond 16
@@ -27,7 +28,7 @@
 
 namespace m3 {
 
-constexpr int kGvThreads = 128;
+constexpr int kGvThreads = 256;
 constexpr int kGvU = 8;  // weight pieces in flight per lane
 constexpr int kGvStage = 4;  // activation pieces staged per thread and pass
 
@@ -163,8 +164,8 @@ __global__ __launch_bounds__(kGvThreads) void gemv_small(GemvArgs a) {
         __syncthreads();
     }
     if constexpr (kNorm) {
-        // fp32 sum of squares per row: the threads' partials, a wave sum, the two waves'
-        // partials; then x * s and the weight, rounded as the reference's RMSNorm
+        // fp32 sum of squares per row: the threads' partials, a wave sum, the waves' partials
+        // in order; then x * s and the weight, rounded as the reference's RMSNorm
 #pragma unroll
         for (int m = 0; m < MM; ++m) {
             const float t = sum_lanes<64>(ss[m]);
@@ -173,7 +174,10 @@ __global__ __launch_bounds__(kGvThreads) void gemv_small(GemvArgs a) {
         __syncthreads();
         for (int i = tid; i < MM * kv; i += kGvThreads) {
             const int m = i / kv, c = i - m * kv;
-            const float sc = (float)(bf16)rsqrtf((sss[0][m] + sss[1][m]) / (float)K + a.eps);
+            float sq = 0.f;
+#pragma unroll
+            for (int w = 0; w < kGvThreads / 64; ++w) sq += sss[w][m];
+            const float sc = (float)(bf16)rsqrtf(sq / (float)K + a.eps);
             gv_bf16x8 xv = *reinterpret_cast<const gv_bf16x8*>(sx + (int64_t)i * 8);
             const gv_bf16x8 wv = *reinterpret_cast<const gv_bf16x8*>(snw + c * 8);
 #pragma unroll
