@@ -92,6 +92,37 @@ def test_chunked_ssd_backward_matches_oracle(case, cuda_device):
         assert gk.dtype == torch.float32 and gk.shape == leaf[k].shape
 
 
+def test_chunked_ssd_backward_bf16_inputs(cuda_device):
+    """bf16 inputs (the backward upcasts them and runs in fp32; gradients come back in the
+    inputs' dtype) against autograd through the fp64 oracle on the bf16-rounded inputs, at
+    the bf16 tolerance; rank 3 with the beta terms (the padded tiles)."""
+    case = (2, 77, 2, 16, 32, 3, True, True, True)
+    B, T, H, P, N, R = case[:6]
+    ins = {k: (v.to(torch.bfloat16).double() if v is not None and k not in ("A", "D", "h_init") else v)
+           for k, v in _inputs(case, seed=31).items()}
+    g = torch.Generator().manual_seed(32)
+    dy = torch.randn(B, T, H, P, R, generator=g, dtype=torch.float64)
+    dhf = torch.randn(B, H, P, N, generator=g, dtype=torch.float64)
+    leaf = {k: (v.clone().requires_grad_() if v is not None else None) for k, v in ins.items()}
+    y, hf = ref.chunked_ssd(*[leaf[k] for k in NAMES[:9]], chunk_size=64, h_init=leaf["h_init"],
+                            return_final_state=True)
+    ((y * dy).sum() + (hf * dhf).sum()).backward()
+    dev = cuda_device
+    bf = {"A", "D", "h_init"}
+    gl = {k: (v.to(dev, torch.float32 if k in bf else torch.bfloat16).requires_grad_()
+              if v is not None else None) for k, v in ins.items()}
+    out = mamba3_amd.chunked_ssd(*[gl[k] for k in NAMES[:9]], h_init=gl["h_init"],
+                                 return_final_state=True)
+    ((out.y.float() * dy.float().to(dev)).sum() + (out.h_final * dhf.float().to(dev)).sum()).backward()
+    assert out.y.dtype == torch.bfloat16
+    for k, v in gl.items():
+        if v is None:
+            continue
+        assert v.grad.dtype == v.dtype, k
+        err = max_rel(v.grad.float(), leaf[k].grad)
+        assert err < BF16_TOL, (k, err)
+
+
 def test_chunked_ssd_backward_long_sequence(cuda_device):
     """2048 tokens (64 backward chunks): gradients carried through the state scans over many
     chunks, against the fp64 oracle at the fp32 tolerance."""
