@@ -37,7 +37,8 @@ int launch_scan_fwd(const float* decay, const float* h_chunk, const float* h_ini
                     float* h_states, int64_t B, int64_t K, int64_t H, int64_t PN,
                     hipStream_t stream);
 
-// Backward of the scan: workspace bytes (0 when PN % 256 != 0) and launcher.
+// Backward of the scan: workspace bytes (0 when PN % 256 != 0) and launcher. grad and
+// d_chunk may be the same array (in place).
 size_t scan_bwd_workspace(int64_t B, int64_t K, int64_t H, int64_t PN);
 int launch_scan_bwd(const float* decay, const float* h_states, const float* grad,
                     float* d_decay, float* d_chunk, float* d_h_init, float* workspace,
@@ -82,7 +83,9 @@ int launch_chunked_fwd_mfma(int B, int T, int H, int P, int N, int R, const floa
                             const float* dt, const float* A, const float* D, const float* x_raw,
                             const float* h_init, float* y, float* h_final, void* workspace,
                             hipStream_t stream);
-size_t chunked_bwd_workspace(int B, int T, int H, int P, int N, int R, bool beta);
+// Workspace of launch_chunked_bwd; hs_given: the call passes hs_pre (less space).
+size_t chunked_bwd_workspace(int B, int T, int H, int P, int N, int R, bool beta,
+                             bool hs_given = false);
 // Byte offset, in the fp32-MFMA chunk forward's workspace, of its chunk-start states
 // (B, K+1, H, P, N): the hs_pre a backward of the same shape may take.
 size_t chunked_fwd_hs_offset(int B, int T, int H, int P, int N, int R, bool beta);

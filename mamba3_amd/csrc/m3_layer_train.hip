@@ -694,7 +694,7 @@ Plan plan(const m3_layer_desc& d) {
     }
     p.chunk_off = o;
     o += al(chunked_bwd_workspace(d.batch, d.seqlen, d.nheads, d.headdim, d.d_state, d.mimo_rank,
-                                  trap));
+                                  trap, fp32_layer_hs_ok(d)));
     p.total = o;
     return p;
 }

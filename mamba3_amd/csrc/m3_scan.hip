@@ -147,6 +147,9 @@ __global__ __launch_bounds__(kScanBlock) void scan_fwd_scalar(
 // walk k down; each wave reduces its share of the d_decay sum (DPP scan, fixed order) and
 // writes one partial per (b,k,h,wave).
 // Pass 2 adds the partials of every (b,k,h) in wave order: deterministic, no atomics.
+// grad and d_chunk may be one array (the backward then runs in place): every thread reads an
+// element of grad before it writes the same element of d_chunk, and touches no other
+// thread's elements, so neither pointer is declared __restrict__.
 // ---------------------------------------------------------------------------------
 constexpr int kScanBwdBlock = 256;
 
@@ -160,7 +163,7 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
 // the wave (one partial per (b,k,h,wave)).
 __global__ __launch_bounds__(kScanBwdBlock) void scan_bwd_cols(
     const float* __restrict__ decay, const f32x4* __restrict__ h_states,
-    const f32x4* __restrict__ grad, f32x4* __restrict__ d_chunk, f32x4* __restrict__ d_h_init,
+    const f32x4* grad, f32x4* d_chunk, f32x4* __restrict__ d_h_init,
     float* __restrict__ part, int K, int H, int pn4, int64_t total_cols) {
     const int lane = threadIdx.x & 63;
     const int64_t wcol0 = ((int64_t)blockIdx.x * (kScanBwdBlock / 64) + (threadIdx.x >> 6)) * (64 * kScanCols);
@@ -204,7 +207,7 @@ __global__ __launch_bounds__(kScanBwdBlock) void scan_bwd_cols(
 // PN % 256 == 0: a wave's 64 float4 columns belong to one (b,h); nw = PN / 256 waves per (b,h).
 __global__ __launch_bounds__(kScanBwdBlock) void scan_bwd_vec4(
     const float* __restrict__ decay, const f32x4* __restrict__ h_states,
-    const f32x4* __restrict__ grad, f32x4* __restrict__ d_chunk, f32x4* __restrict__ d_h_init,
+    const f32x4* grad, f32x4* d_chunk, f32x4* __restrict__ d_h_init,
     float* __restrict__ part, int K, int H, int pn4, int64_t total_cols) {
     const int64_t col = (int64_t)blockIdx.x * kScanBwdBlock + threadIdx.x;
     if (col >= total_cols) return;  // total_cols is a multiple of 64: whole waves exit
@@ -252,7 +255,7 @@ __global__ __launch_bounds__(kScanBwdBlock) void scan_bwd_reduce(const float* __
 // so the result does not depend on timing.
 __global__ __launch_bounds__(kScanBwdBlock) void scan_bwd_block(
     const float* __restrict__ decay, const float* __restrict__ h_states,
-    const float* __restrict__ grad, float* __restrict__ d_chunk, float* __restrict__ d_decay,
+    const float* grad, float* d_chunk, float* __restrict__ d_decay,
     float* __restrict__ d_h_init, int K, int H, int PN) {
     constexpr int kMaxPer = 64;                      // columns per thread and tile
     constexpr int kTile = kScanBwdBlock * kMaxPer;  // columns per tile
@@ -283,8 +286,9 @@ __global__ __launch_bounds__(kScanBwdBlock) void scan_bwd_block(
                 const int j = tid + i * kScanBwdBlock;
                 if (j < cols) {
                     acc += g[i] * h_states[o + j];
+                    const float gk = grad[o + j];
                     d_chunk[o + j] = g[i];
-                    g[i] = grad[o + j] + d * g[i];
+                    g[i] = gk + d * g[i];
                 }
             }
             acc = wave_sum_dpp(acc);

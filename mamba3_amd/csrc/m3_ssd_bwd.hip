@@ -923,16 +923,19 @@ bool make_shape(int B, int T, int H, int P, int N, int R, bool beta, Shape& s) {
     return true;
 }
 
-Plan make_plan(const Shape& s) {
+// hs_given: the chunk-start states come from the forward, so the chunk-local states hext and
+// the scanned states Hs take no space. The reverse scan runs in place: dch is gext.
+Plan make_plan(const Shape& s, bool hs_given) {
     Plan pl;
     pl.s = s;
     const size_t BKH = (size_t)s.B * s.K * s.H, BK1H = (size_t)s.B * (s.K + 1) * s.H;
+    const size_t states = hs_given ? 0 : BK1H * s.PN;
     const size_t sizes[15] = {
         BKH * s.Qb,                              // cum
         BK1H,                                    // dec
         BK1H,                                    // ddec
-        BK1H * s.PN, BK1H * s.PN, BK1H * s.PN,   // hext, Hs, gext
-        BK1H * s.PN,                             // dch
+        states, states, BK1H * s.PN,             // hext, Hs, gext
+        0,                                       // dch (= gext)
         BKH * s.QR() * s.QR2(),                  // M
         BKH * s.QR() * s.QR2(),                  // DM
         BKH * s.Qb,                              // dcI
@@ -1065,10 +1068,10 @@ bool chunked_bwd_shape_ok(int B, int T, int H, int P, int N, int R, bool beta) {
     return true;
 }
 
-size_t chunked_bwd_workspace(int B, int T, int H, int P, int N, int R, bool beta) {
+size_t chunked_bwd_workspace(int B, int T, int H, int P, int N, int R, bool beta, bool hs_given) {
     bw::Shape s;
     if (!bw::make_shape(B, T, H, P, N, R, beta, s)) return 0;
-    return bw::make_plan(s).total;
+    return bw::make_plan(s, hs_given).total;
 }
 
 int launch_chunked_bwd(int B, int T, int H, int P, int N, int R, const float* x_g,
@@ -1081,7 +1084,7 @@ int launch_chunked_bwd(int B, int T, int H, int P, int N, int R, const float* x_
     using namespace bw;
     Shape s;
     if (!make_shape(B, T, H, P, N, R, x_b != nullptr, s)) return 1;
-    const Plan pl = make_plan(s);
+    const Plan pl = make_plan(s, hs_pre != nullptr);
     char* ws = reinterpret_cast<char*>(workspace);
     auto part = [&](int i) { return reinterpret_cast<float*>(ws + pl.off[i]); };
     Args a;
@@ -1091,7 +1094,7 @@ int launch_chunked_bwd(int B, int T, int H, int P, int N, int R, const float* x_
     a.dxg = dx_g, a.dxb = dx_b, a.dBg = dB_g, a.dBb = dB_b, a.dC = dC, a.ddt = ddt, a.dA = dA;
     a.dD = dD, a.dxr = dx_raw, a.dhinit = dh_init;
     a.cum = part(0), a.dec = part(1), a.ddec = part(2), a.hext = part(3), a.Hs = part(4);
-    a.gext = part(5), a.dch = part(6), a.M = part(7), a.DM = part(8), a.dcI = part(9);
+    a.gext = part(5), a.dch = a.gext, a.M = part(7), a.DM = part(8), a.dcI = part(9);
     a.pInter = part(10), a.pState = part(11), a.pDt = part(12), a.pA = part(13), a.pD = part(14);
     float* scan_ws = reinterpret_cast<float*>(ws + pl.scan_off);
     a.fwd = 0, a.y = nullptr, a.hfin = nullptr;
