@@ -24,7 +24,9 @@
 //                - q_t + [t = Qb-1] (sum_s q_s + exp(c_end) <dH, H_k>),
 //                Z = sum_{r,j} G o DX,  q_s = sum_{p,j} Xf[s,p,j] (state term of dXf)[s,p,j]
 //   d(A dt_t)  = sum_{t'>=t} dc_t';  ddt_t = A d(A dt_t) + sum_{p,j} dXf[s,p,j] x[s,p,j]
-// Qb = min(64, 128 / R2), so that the score tiles are at most 128 x 128. R here is the rank
+// Qb = min(64, 128 / R2), so that the score tiles are at most 128 x 128; with the beta terms
+// they are one 64 x 128 tile, which bwd_fused keeps in LDS (M and DM never reach memory),
+// otherwise bwd_scores writes M and DM for bwd_dxf / bwd_dbf / bwd_dc. R here is the rank
 // of the tiles, a power of two: ranks 3, 5, 6 and 7 run on tiles of rank 4 or 8 whose extra
 // slots read as zero (their rows and columns of G, DX, M and DM are zero). The chunk
 // states H_k and dH come from the state scan kernels over K+1 chunks, the last one carrying
@@ -113,6 +115,15 @@ struct Lds {
 // tcol(tx, j) = tx + 16 j; its accumulator acc[j][v].
 __device__ __forceinline__ int tcol(int tx, int j) { return tx + 16 * j; }
 
+// threadIdx.x through an empty asm: values derived from it are formed where they are used and
+// cannot be hoisted out of the GEMM or tile that uses them (a kernel running several GEMMs in
+// sequence would otherwise keep every GEMM's per-thread addresses live from its entry).
+__device__ __forceinline__ int opaque_tid() {
+    int t = threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
+}
+
 // acc[j][v] += sum_k A(4 ty + v, k) B(k, tcol(tx, j)) over k < kdim, for the 64 x TN tile of
 // a 256-thread block, on fp32 MFMA. Each operand comes as a load and a finish: la(m, k) /
 // lb(k, n) read element (m, k) / (k, n) from an address that is in bounds for every row
@@ -127,7 +138,7 @@ __device__ __forceinline__ void gemm_acc(f32x4 (&acc)[TN / 16], int kdim, LA la,
                                          FB fb, Lds<TN>& l) {
     constexpr int NA = KT * TT / NTH;  // A elements per thread and step
     constexpr int NB = KT * TN / NTH;  // B elements per thread and step
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = opaque_tid(), lane = tid & 63, wave = tid >> 6;
     auto ak = [](int e) { return AK ? e % KT : e / TT; };
     auto am = [](int e) { return AK ? e / KT : e % TT; };
     auto bk = [](int e) { return BK ? e % KT : e / TN; };
@@ -165,6 +176,46 @@ __device__ __forceinline__ void gemm_acc(f32x4 (&acc)[TN / 16], int kdim, LA la,
 #pragma unroll
         for (int k4 = 0; k4 < KT; k4 += 4) {
             const float av = l.A[k4 + (lane >> 4)][16 * wave + (lane & 15)];
+#pragma unroll
+            for (int j = 0; j < TN / 16; ++j) {
+                const float bv = l.B[k4 + (lane >> 4)][16 * j + (lane & 15)];
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[j], 0, 0, 0);
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// As gemm_acc, with the A operand read by the MFMA steps straight from an LDS matrix:
+// A(m, k) = as(m, k) for m < 64 and k < kdim (a multiple of KT); only B is staged.
+template <int TN, bool BK, class AS, class LB, class FB>
+__device__ __forceinline__ void gemm_lds_a(f32x4 (&acc)[TN / 16], int kdim, AS as, LB lb, FB fb,
+                                           Lds<TN>& l) {
+    constexpr int NB = KT * TN / NTH;
+    const int tid = opaque_tid(), lane = tid & 63, wave = tid >> 6;
+    auto bk = [](int e) { return BK ? e % KT : e / TN; };
+    auto bn = [](int e) { return BK ? e / KT : e % TN; };
+    float rb[NB];
+    auto fetch = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            const int e = tid + NTH * i;
+            rb[i] = lb(k0 + bk(e), bn(e));
+        }
+    };
+    fetch(0);
+#pragma unroll 1
+    for (int k0 = 0; k0 < kdim; k0 += KT) {
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            const int e = tid + NTH * i;
+            l.B[bk(e)][bn(e)] = fb(k0 + bk(e), bn(e), rb[i]);
+        }
+        __syncthreads();
+        if (k0 + KT < kdim) fetch(k0 + KT);
+#pragma unroll
+        for (int k4 = 0; k4 < KT; k4 += 4) {
+            const float av = as(16 * wave + (lane & 15), k0 + k4 + (lane >> 4));
 #pragma unroll
             for (int j = 0; j < TN / 16; ++j) {
                 const float bv = l.B[k4 + (lane >> 4)][16 * j + (lane & 15)];
@@ -495,24 +546,32 @@ __device__ __forceinline__ void tile_token_sums(const float (&v)[4], int per, fl
     __syncthreads();
 }
 
+// Score elements (row (t,r), column (s,j)) for the consumer tiles below: the chunk's W o G /
+// W o DX scratch in global memory (row stride QR2), or the fused kernel's LDS tile.
+struct ScoresGlobal {
+    static constexpr bool kLds = false;
+    const float* p;
+    int stride;
+    __device__ __forceinline__ float operator()(int m, int c) const { return p[m * stride + c]; }
+};
+struct ScoresLds {
+    static constexpr bool kLds = true;
+    float (*S)[TW + 1];
+    __device__ __forceinline__ float operator()(int m, int c) const { return S[m][c]; }
+};
+
 // ---- K3: dXf rows (s,j) x columns p; writes dx_g / dx_b = dt_s dXf and the per-token
-// partials q_s (state term . Xf) and sum_{p,j} dXf x.
-template <int R, bool BETA, bool PADR>
-__global__ __launch_bounds__(NTH, 4) void bwd_dxf(Args a) {
+// partials q_s (state term . Xf) and sum_{p,j} dXf x. M(m, c) gives W o G; cs holds c of
+// the chunk's tokens.
+template <int R, bool BETA, bool PADR, class SM>
+__device__ __forceinline__ void dxf_tile(const Args& a, const Chunk<R, BETA, PADR>& q, int ch,
+                                         int rt, int pt, SM M, Lds<TT>& l, float (*red)[17],
+                                         const float* cs, float* outv) {
     BW_CONSTS
-    __shared__ Lds<TT> l;
-    __shared__ float red[TT][17];
-    __shared__ float cs[64], outv[64];
     const Shape& s = a.s;
-    int ch, tile;
-    if (!chunk_tile(s.B * s.K * s.H, QR2 / TT * s.nPt, ch, tile)) return;
-    const int h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
-    const int rt = tile / s.nPt, pt = tile % s.nPt;
+    const int b = q.b, k = q.k, h = q.h;
     const int m0 = rt * TT, p0 = pt * TT;
-    const Chunk<R, BETA, PADR> q{&a, b, k, h};
-    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
-    if (tid < QB) cs[tid] = a.cum[(int64_t)ch * QB + tid];
-    __syncthreads();
+    const int tid = opaque_tid(), tx = tid & 15, ty = tid >> 4;
     const float cend = cs[QB - 1];
     const float* dH = a.dch + chx(s, b, k, h) * s.PN;
     f32x4 acc[4];
@@ -551,13 +610,15 @@ __global__ __launch_bounds__(NTH, 4) void bwd_dxf(Args a) {
     const int per = R2, nts = TT / per;
     tile_token_sums(rv, per, red, outv);
     if (tid < nts) a.pState[((int64_t)ch * s.nPt + pt) * QB + m0 / per + tid] = outv[tid];
-    const float* Mi = a.M + (int64_t)ch * QR * QR2;
-    gemm_acc<TT, false, false>(acc, QR,
-             [&](int mm, int jr) { return Mi[jr * QR2 + m0 + mm]; },
-             [&](int mm, int jr, float v) { return v; },
-             [&](int jr, int pp) { return q.ldy(jr / R, min(p0 + pp, pmax), jr % R); },
-             [&](int jr, int pp, float v) { return p0 + pp < s.P && q.ok(jr / R, jr % R) ? v : 0.f; },
-             l);
+    {
+        auto lb = [&](int jr, int pp) { return q.ldy(jr / R, min(p0 + pp, pmax), jr % R); };
+        auto fb = [&](int jr, int pp, float v) { return p0 + pp < s.P && q.ok(jr / R, jr % R) ? v : 0.f; };
+        if constexpr (SM::kLds)
+            gemm_lds_a<TT, false>(acc, QR, [&](int mm, int jr) { return M(jr, m0 + mm); }, lb, fb, l);
+        else
+            gemm_acc<TT, false, false>(acc, QR, [&](int mm, int jr) { return M(jr, m0 + mm); },
+                                       [&](int mm, int jr, float v) { return v; }, lb, fb, l);
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int m = m0 + 4 * ty + i, t = m / R2, j = m % R2;
@@ -578,26 +639,34 @@ __global__ __launch_bounds__(NTH, 4) void bwd_dxf(Args a) {
     if (tid < nts) a.pDt[((int64_t)ch * s.nPt + pt) * QB + m0 / per + tid] = outv[tid];
 }
 
-// ---- K4: dBf rows (s,j) x columns n; writes dB_g / dB_b.
 template <int R, bool BETA, bool PADR>
-__global__ __launch_bounds__(NTH, 4) void bwd_dbf(Args a) {
+__global__ __launch_bounds__(NTH, 4) void bwd_dxf(Args a) {
     BW_CONSTS
-    __shared__ Lds<TW> l;
-    __shared__ float cs[64], dts[64];
+    __shared__ Lds<TT> l;
+    __shared__ float red[TT][17];
+    __shared__ float cs[64], outv[64];
     const Shape& s = a.s;
     int ch, tile;
-    if (!chunk_tile(s.B * s.K * s.H, QR2 / TT * s.nNt, ch, tile)) return;
+    if (!chunk_tile(s.B * s.K * s.H, QR2 / TT * s.nPt, ch, tile)) return;
     const int h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
-    const int rt = tile / s.nNt, nt = tile % s.nNt;
+    const Chunk<R, BETA, PADR> q{&a, b, k, h};
+    if (threadIdx.x < QB) cs[threadIdx.x] = a.cum[(int64_t)ch * QB + threadIdx.x];
+    __syncthreads();
+    dxf_tile(a, q, ch, tile / s.nPt, tile % s.nPt, ScoresGlobal{a.M + (int64_t)ch * QR * QR2, QR2},
+             l, red, cs, outv);
+}
+
+// ---- K4: dBf rows (s,j) x columns n; writes dB_g / dB_b. DM(m, c) gives W o DX.
+template <int R, bool BETA, bool PADR, class SM>
+__device__ __forceinline__ void dbf_tile(const Args& a, const Chunk<R, BETA, PADR>& q, int rt,
+                                         int nt, SM DM, Lds<TW>& l, const float* cs,
+                                         const float* dts) {
+    BW_CONSTS
+    const Shape& s = a.s;
+    const int b = q.b, k = q.k, h = q.h;
     const int m0 = rt * TT, n0 = nt * TW;
     constexpr int NJ = TW / 16;
-    const Chunk<R, BETA, PADR> q{&a, b, k, h};
-    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
-    if (tid < QB) {
-        cs[tid] = a.cum[(int64_t)ch * QB + tid];
-        dts[tid] = q.dtv(tid);
-    }
-    __syncthreads();
+    const int tid = opaque_tid(), ty = tid >> 4, tx = tid & 15;
     const float cend = cs[QB - 1];
     const float* dH = a.dch + chx(s, b, k, h) * s.PN;
     f32x4 acc[NJ];
@@ -619,13 +688,15 @@ __global__ __launch_bounds__(NTH, 4) void bwd_dbf(Args a) {
 #pragma unroll
         for (int j = 0; j < NJ; ++j) acc[j][i] *= e;
     }
-    const float* DMi = a.DM + (int64_t)ch * QR * QR2;
-    gemm_acc<TW, false, false>(acc, QR,
-             [&](int mm, int jr) { return DMi[jr * QR2 + m0 + mm]; },
-             [&](int mm, int jr, float v) { return v; },
-             [&](int jr, int nn) { return q.lc(jr / R, min(n0 + nn, nmax), jr % R); },
-             [&](int jr, int nn, float v) { return n0 + nn < s.N && q.ok(jr / R, jr % R) ? v : 0.f; },
-             l);
+    {
+        auto lb = [&](int jr, int nn) { return q.lc(jr / R, min(n0 + nn, nmax), jr % R); };
+        auto fb = [&](int jr, int nn, float v) { return n0 + nn < s.N && q.ok(jr / R, jr % R) ? v : 0.f; };
+        if constexpr (SM::kLds)
+            gemm_lds_a<TW, false>(acc, QR, [&](int mm, int jr) { return DM(jr, m0 + mm); }, lb, fb, l);
+        else
+            gemm_acc<TW, false, false>(acc, QR, [&](int mm, int jr) { return DM(jr, m0 + mm); },
+                                       [&](int mm, int jr, float v) { return v; }, lb, fb, l);
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int m = m0 + 4 * ty + i, t = m / R2, j = m % R2;
@@ -641,24 +712,37 @@ __global__ __launch_bounds__(NTH, 4) void bwd_dbf(Args a) {
     }
 }
 
-// ---- K5: dC rows (t,r) x columns n, and the per-token partials sum_{n,r} C dC_inter.
 template <int R, bool BETA, bool PADR>
-__global__ __launch_bounds__(NTH) void bwd_dc(Args a) {
+__global__ __launch_bounds__(NTH, 4) void bwd_dbf(Args a) {
     BW_CONSTS
     __shared__ Lds<TW> l;
-    __shared__ float red[TT][17];
-    __shared__ float cs[64], outv[64];
+    __shared__ float cs[64], dts[64];
     const Shape& s = a.s;
     int ch, tile;
-    if (!chunk_tile(s.B * s.K * s.H, QR / TT * s.nNt, ch, tile)) return;
+    if (!chunk_tile(s.B * s.K * s.H, QR2 / TT * s.nNt, ch, tile)) return;
     const int h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
-    const int rt = tile / s.nNt, nt = tile % s.nNt;
+    const Chunk<R, BETA, PADR> q{&a, b, k, h};
+    if (threadIdx.x < QB) {
+        cs[threadIdx.x] = a.cum[(int64_t)ch * QB + threadIdx.x];
+        dts[threadIdx.x] = q.dtv(threadIdx.x);
+    }
+    __syncthreads();
+    dbf_tile(a, q, tile / s.nNt, tile % s.nNt, ScoresGlobal{a.DM + (int64_t)ch * QR * QR2, QR2}, l,
+             cs, dts);
+}
+
+// ---- K5: dC rows (t,r) x columns n, and the per-token partials sum_{n,r} C dC_inter.
+// DM(m, c) gives W o DX.
+template <int R, bool BETA, bool PADR, class SM>
+__device__ __forceinline__ void dc_tile(const Args& a, const Chunk<R, BETA, PADR>& q, int ch,
+                                        int rt, int nt, SM DM, Lds<TW>& l, float (*red)[17],
+                                        const float* cs, float* outv) {
+    BW_CONSTS
+    const Shape& s = a.s;
+    const int b = q.b, k = q.k, h = q.h;
     const int m0 = rt * TT, n0 = nt * TW;
     constexpr int NJ = TW / 16;
-    const Chunk<R, BETA, PADR> q{&a, b, k, h};
-    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
-    if (tid < QB) cs[tid] = a.cum[(int64_t)ch * QB + tid];
-    __syncthreads();
+    const int tid = opaque_tid(), tx = tid & 15, ty = tid >> 4;
     const float* Hk = a.Hs + chx(s, b, k, h) * s.PN;
     f32x4 acc[NJ];
     zero(acc);
@@ -695,13 +779,15 @@ __global__ __launch_bounds__(NTH) void bwd_dc(Args a) {
     const int per = R, nts = TT / per;
     tile_token_sums(rv, per, red, outv);
     if (tid < nts) a.pInter[((int64_t)ch * s.nNt + nt) * QB + m0 / per + tid] = outv[tid];
-    const float* DMi = a.DM + (int64_t)ch * QR * QR2;
-    gemm_acc<TW, true, false>(acc, QR2,
-             [&](int mm, int jc) { return DMi[(m0 + mm) * QR2 + jc]; },
-             [&](int mm, int jc, float v) { return v; },
-             [&](int jc, int nn) { return q.lbf(jc / R2, min(n0 + nn, nmax), jc % R2); },
-             [&](int jc, int nn, float v) { return n0 + nn < s.N && q.okj(jc / R2, jc % R2) ? v : 0.f; },
-             l);
+    {
+        auto lb = [&](int jc, int nn) { return q.lbf(jc / R2, min(n0 + nn, nmax), jc % R2); };
+        auto fb = [&](int jc, int nn, float v) { return n0 + nn < s.N && q.okj(jc / R2, jc % R2) ? v : 0.f; };
+        if constexpr (SM::kLds)
+            gemm_lds_a<TW, false>(acc, QR2, [&](int mm, int jc) { return DM(m0 + mm, jc); }, lb, fb, l);
+        else
+            gemm_acc<TW, true, false>(acc, QR2, [&](int mm, int jc) { return DM(m0 + mm, jc); },
+                                      [&](int mm, int jc, float v) { return v; }, lb, fb, l);
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int m = m0 + 4 * ty + i, t = m / R, r = m % R;
@@ -713,6 +799,126 @@ __global__ __launch_bounds__(NTH) void bwd_dc(Args a) {
             if (n < s.N) a.dC[base + (int64_t)n * q.rk()] = acc[j][i];
         }
     }
+}
+
+template <int R, bool BETA, bool PADR>
+__global__ __launch_bounds__(NTH) void bwd_dc(Args a) {
+    BW_CONSTS
+    __shared__ Lds<TW> l;
+    __shared__ float red[TT][17];
+    __shared__ float cs[64], outv[64];
+    const Shape& s = a.s;
+    int ch, tile;
+    if (!chunk_tile(s.B * s.K * s.H, QR / TT * s.nNt, ch, tile)) return;
+    const int h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
+    const Chunk<R, BETA, PADR> q{&a, b, k, h};
+    if (threadIdx.x < QB) cs[threadIdx.x] = a.cum[(int64_t)ch * QB + threadIdx.x];
+    __syncthreads();
+    dc_tile(a, q, ch, tile / s.nNt, tile % s.nNt, ScoresGlobal{a.DM + (int64_t)ch * QR * QR2, QR2},
+            l, red, cs, outv);
+}
+
+// ---- K3-5 fused, for chunks whose score tiles are one 64 x 128 tile (every rank with the
+// beta terms: QR = Qb R = 64, QR2 = Qb 2R = 128). One block per chunk forms W o G in an LDS
+// tile, runs the dXf tiles on it, forms DX, takes the Z sums of (W o G) o DX element by
+// element while it replaces the tile by W o DX, then runs the dC and dBf tiles on that. W o G
+// and W o DX never reach HBM, and each operand of the chunk is read by one block within a
+// short window instead of by four kernels.
+template <int R, bool BETA, bool PADR>
+__global__ __launch_bounds__(NTH, 3) void bwd_fused(Args a) {
+    BW_CONSTS
+    static_assert(QR == TT && QR2 == TW, "one 64 x 128 score tile per chunk");
+    __shared__ Lds<TW> l;
+    __shared__ float S[TT][TW + 1];
+    __shared__ float red[TT][17];
+    __shared__ float cs[64], dts[64], outv[64], zrow[64], zcol[64];
+    const Shape& s = a.s;
+    const int ch = blockIdx.x, h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
+    const Chunk<R, BETA, PADR> q{&a, b, k, h};
+    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+    if (tid < 64) {
+        cs[tid] = tid < QB ? a.cum[(int64_t)ch * QB + tid] : 0.f;
+        dts[tid] = tid < QB ? q.dtv(tid) : 0.f;
+    }
+    __syncthreads();
+    constexpr int NJ = TW / 16;
+    const ScoresLds Sat{S};
+    f32x4 g[NJ];
+    // W o G -> S: G[(t,r),(s,j)] = sum_n C[t,n,r] Bf[s,n,j]
+    zero(g);
+    gemm_acc<TW, true, true>(g, s.N,
+                 [&](int m, int n) { return q.lc(m / R, n, m % R); },
+                 [&](int m, int n, float v) { return q.ok(m / R, m % R) ? v : 0.f; },
+                 [&](int n, int c) { return q.lbf(c / R2, n, c % R2); },
+                 [&](int n, int c, float v) { return q.okj(c / R2, c % R2) ? v : 0.f; },
+                 l);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const int m = 4 * ty + i, c = tcol(tx, j), t = m / R, u = c / R2;
+            S[m][c] = u <= t ? __expf(cs[t] - cs[u]) * g[j][i] : 0.f;
+        }
+    __syncthreads();
+#pragma unroll 1
+    for (int rt = 0; rt < QR2 / TT; ++rt)
+#pragma unroll 1
+        for (int pt = 0; pt < s.nPt; ++pt)
+            dxf_tile(a, q, ch, rt, pt, Sat, reinterpret_cast<Lds<TT>&>(l), red, cs, outv);
+    // DX[(t,r),(s,j)] = sum_p dy[t,p,r] dt_s x[s,p,j]
+    zero(g);
+    gemm_acc<TW, true, true>(g, s.P,
+                 [&](int m, int p) { return q.ldy(m / R, p, m % R); },
+                 [&](int m, int p, float v) { return q.ok(m / R, m % R) ? v : 0.f; },
+                 [&](int p, int c) { return q.lx(c / R2, p, c % R2); },
+                 [&](int p, int c, float v) { return q.okj(c / R2, c % R2) ? dts[c / R2] * v : 0.f; },
+                 l);
+    {
+        // Z = (W o G) o DX at this thread's elements (each thread reads and then overwrites
+        // only its own elements of S), summed over its columns per row and over its rows per
+        // column; the 16 partials of each row and column are then added in a fixed order.
+        float zr[4], zc[NJ];
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) zc[j] = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            zr[i] = 0.f;
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                const int m = 4 * ty + i, c = tcol(tx, j), t = m / R, u = c / R2;
+                const float z = S[m][c] * g[j][i];
+                zr[i] += z;
+                zc[j] += z;
+                S[m][c] = u <= t ? __expf(cs[t] - cs[u]) * g[j][i] : 0.f;
+            }
+        }
+        float(*cp)[TW] = reinterpret_cast<float(*)[TW]>(&l.B[0][0]);  // 16 x 128 of l.B's 16 x 145
+#pragma unroll
+        for (int i = 0; i < 4; ++i) red[4 * ty + i][tx] = zr[i];
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) cp[ty][tcol(tx, j)] = zc[j];
+        __syncthreads();
+        if (tid < QB) {
+            float v = 0.f;
+            for (int r = 0; r < R; ++r)
+                for (int x = 0; x < 16; ++x) v += red[tid * R + r][x];
+            zrow[tid] = v;
+        } else if (tid >= 128 && tid < 128 + QB) {
+            const int u = tid - 128;
+            float v = 0.f;
+            for (int j = 0; j < R2; ++j)
+                for (int y = 0; y < 16; ++y) v += cp[y][u * R2 + j];
+            zcol[u] = v;
+        }
+        __syncthreads();
+        if (tid < QB) a.dcI[(int64_t)ch * QB + tid] = zrow[tid] - zcol[tid];
+    }
+#pragma unroll 1
+    for (int nt = 0; nt < s.nNt; ++nt) dc_tile(a, q, ch, 0, nt, Sat, l, red, cs, outv);
+#pragma unroll 1
+    for (int rt = 0; rt < QR2 / TT; ++rt)
+#pragma unroll 1
+        for (int nt = 0; nt < s.nNt; ++nt) dbf_tile(a, q, rt, nt, Sat, l, cs, dts);
 }
 
 // ---- K6: per chunk: dc -> d(A dt) (suffix sums), ddt, the chunk's partials of dA and dD,
@@ -924,20 +1130,23 @@ bool make_shape(int B, int T, int H, int P, int N, int R, bool beta, Shape& s) {
 }
 
 // hs_given: the chunk-start states come from the forward, so the chunk-local states hext and
-// the scanned states Hs take no space. The reverse scan runs in place: dch is gext.
+// the scanned states Hs take no space. The reverse scan runs in place: dch is gext. With the
+// beta terms the score scratch M / DM takes no space either.
 Plan make_plan(const Shape& s, bool hs_given) {
     Plan pl;
     pl.s = s;
     const size_t BKH = (size_t)s.B * s.K * s.H, BK1H = (size_t)s.B * (s.K + 1) * s.H;
     const size_t states = hs_given ? 0 : BK1H * s.PN;
+    // with the beta terms one fused kernel keeps W o G / W o DX in LDS (bwd_fused)
+    const size_t scores = s.R2 == 2 * s.RT ? 0 : BKH * s.QR() * s.QR2();
     const size_t sizes[15] = {
         BKH * s.Qb,                              // cum
         BK1H,                                    // dec
         BK1H,                                    // ddec
         states, states, BK1H * s.PN,             // hext, Hs, gext
         0,                                       // dch (= gext)
-        BKH * s.QR() * s.QR2(),                  // M
-        BKH * s.QR() * s.QR2(),                  // DM
+        scores,                                  // M
+        scores,                                  // DM
         BKH * s.Qb,                              // dcI
         BKH * s.nNt * s.Qb,                      // pInter
         BKH * s.nPt * s.Qb, BKH * s.nPt * s.Qb,  // pState, pDt
@@ -967,10 +1176,14 @@ int launch(const Args& a, const float* h_init, float* dh_init, float* scan_ws, h
     if (launch_scan_bwd(a.dec, a.Hs, a.gext, a.ddec, a.dch, dh_init, scan_ws, s.B, s.K + 1, s.H,
                         s.PN, stream) != 0)
         return 1;
-    hipLaunchKernelGGL((bwd_scores<R, BETA, PADR>), dim3(nch), dim3(NTH), 0, stream, a);
-    hipLaunchKernelGGL((bwd_dxf<R, BETA, PADR>), dim3(tile_grid(nch, nRt2 * s.nPt)), dim3(NTH), 0, stream, a);
-    hipLaunchKernelGGL((bwd_dbf<R, BETA, PADR>), dim3(tile_grid(nch, nRt2 * s.nNt)), dim3(NTH), 0, stream, a);
-    hipLaunchKernelGGL((bwd_dc<R, BETA, PADR>), dim3(tile_grid(nch, nRt * s.nNt)), dim3(NTH), 0, stream, a);
+    if constexpr (QR == TT && QR2 == TW) {
+        hipLaunchKernelGGL((bwd_fused<R, BETA, PADR>), dim3(nch), dim3(NTH), 0, stream, a);
+    } else {
+        hipLaunchKernelGGL((bwd_scores<R, BETA, PADR>), dim3(nch), dim3(NTH), 0, stream, a);
+        hipLaunchKernelGGL((bwd_dxf<R, BETA, PADR>), dim3(tile_grid(nch, nRt2 * s.nPt)), dim3(NTH), 0, stream, a);
+        hipLaunchKernelGGL((bwd_dbf<R, BETA, PADR>), dim3(tile_grid(nch, nRt2 * s.nNt)), dim3(NTH), 0, stream, a);
+        hipLaunchKernelGGL((bwd_dc<R, BETA, PADR>), dim3(tile_grid(nch, nRt * s.nNt)), dim3(NTH), 0, stream, a);
+    }
     hipLaunchKernelGGL((bwd_tokens<R, BETA, PADR>), dim3(nch), dim3(NTH), 0, stream, a);
     hipLaunchKernelGGL(bwd_reduce, dim3(s.H), dim3(NTH), 0, stream, a);
     return hipGetLastError() == hipSuccess ? 0 : 1;

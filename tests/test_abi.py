@@ -70,9 +70,13 @@ def test_chunked_bwd_workspace_and_validation(lib):
     K = 1024 // 32
     states = 4 * (K + 1) * 24 * 64 * 128 * 4
     scores = 4 * K * 24 * 64 * 128 * 4
-    # chunk-local, scanned and adjoint states (the reverse scan runs in place), M and DM
-    assert n.value >= 3 * states + 2 * scores
-    assert n.value < 4 * states + 2 * scores
+    # chunk-local, scanned and adjoint states (the reverse scan runs in place); with the beta
+    # terms the masked scores stay in LDS (one fused kernel per chunk)
+    assert 3 * states <= n.value < 3 * states + scores
+    assert lib.m3_chunked_ssd_bwd_workspace_size(4, 1024, 24, 64, 128, 2, 0, ctypes.byref(n)) == 0
+    K0 = 1024 // 64  # without the beta terms: chunks of 64 tokens, 128 x 128 score tiles in scratch
+    states0 = 4 * (K0 + 1) * 24 * 64 * 128 * 4
+    assert n.value >= 3 * states0 + 2 * 4 * K0 * 24 * 128 * 128 * 4
     # rank 3 on rank-4 tiles; rank 9 is beyond every kernel
     assert lib.m3_chunked_ssd_bwd_workspace_size(4, 1024, 24, 64, 128, 3, 1, ctypes.byref(n)) == 0
     assert n.value > 0
