@@ -48,6 +48,7 @@ EXPORTED_SYMBOLS = (
     "m3_prefill_kernel_name",
 )
 
+M3_ERR_UNSUPPORTED = 3
 M3_ERR_SCRATCH_LIMIT = 8
 NOALLOC_SCRATCH_BYTES = 64 << 20
 

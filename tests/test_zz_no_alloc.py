@@ -2,8 +2,8 @@
 per-device scratch, against m3_prefill_fwd with a caller workspace: the same kernels on
 the same inputs, so every output must be bitwise equal. Two calls in a row, the second
 smaller (the scratch keeps the first call's contents), on each dispatch path; a workload
-beyond the scratch is refused before any launch; and the entry point under HIP graph
-capture, replayed with eager work in between."""
+beyond the scratch and the training forward are refused before any launch; and the entry
+point under HIP graph capture, replayed with eager work in between."""
 
 from __future__ import annotations
 
@@ -85,6 +85,25 @@ def test_noalloc_refuses_a_workspace_beyond_its_scratch(cuda_device):
         *[t.data_ptr() for t in outs], _native.stream_of(proj))
     assert st == _native.M3_ERR_SCRATCH_LIMIT
     assert "scratch" in _native.lib().m3_status_string(st).decode()
+    torch.cuda.synchronize()
+    assert bool((outs[0] == 7.0).all())
+
+
+def test_noalloc_refuses_the_training_forward(cuda_device):
+    """M3_FLAG_FOR_BACKWARD asks the forward to keep the backward's operands in its
+    workspace; here that would be the shared scratch, which the next call overwrites, so the
+    call returns M3_ERR_UNSUPPORTED and launches nothing (the outputs keep their fill)."""
+    layer = _layer(PATHS[2][0], torch.float32, cuda_device)
+    B, T = 1, 64
+    proj = torch.zeros(B, T, layer.in_proj.out_features, device=cuda_device)
+    desc = layer._desc(B, T, proj)
+    desc.flags |= _native.M3_FLAG_FOR_BACKWARD
+    outs = _outputs(layer, B, T, cuda_device, torch.float32)
+    outs[0].fill_(7.0)
+    st = _native.lib().m3_prefill_fwd_noalloc(
+        ctypes.byref(desc), ctypes.byref(layer._param_pack()), proj.data_ptr(), None,
+        *[t.data_ptr() for t in outs], _native.stream_of(proj))
+    assert st == _native.M3_ERR_UNSUPPORTED
     torch.cuda.synchronize()
     assert bool((outs[0] == 7.0).all())
 
