@@ -822,8 +822,8 @@ __global__ __launch_bounds__(NTH) void bwd_dc(Args a) {
 // beta terms: QR = Qb R = 64, QR2 = Qb 2R = 128). One block per chunk forms W o G in an LDS
 // tile, runs the dXf tiles on it, forms DX, takes the Z sums of (W o G) o DX element by
 // element while it replaces the tile by W o DX, then runs the dC and dBf tiles on that. W o G
-// and W o DX never reach HBM, and each operand of the chunk is read by one block within a
-// short window instead of by four kernels.
+// and W o DX never reach HBM. (The chunk's operands are still read about three times over its
+// ten GEMMs; with 96 blocks per XCD in flight those re-reads mostly miss the L2.)
 template <int R, bool BETA, bool PADR>
 __global__ __launch_bounds__(NTH, 3) void bwd_fused(Args a) {
     BW_CONSTS
