@@ -647,7 +647,7 @@ def main() -> int:
     args = ap.parse_args()
     SETTLE_S = args.settle_s
     if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1"}))
+        print(json.dumps({"error": "bench.py measures one GPU only (the SSD path is single-GPU work); run with --gpus 1"}))
         return 2
 
     import torch

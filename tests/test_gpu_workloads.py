@@ -133,7 +133,7 @@ def test_lm_d768_24_layers_prefill_and_greedy_decode(cuda_device):
         first = lm.lm_head(lm.norm(x[:, -1])).float()
         assert torch.equal(first.argmax(-1).cpu(), gen[:, 0])
         st_ref = [{k: v.float().cpu() for k, v in st.items()} for st in states]
-        # the bf16 oracle chain holds its angle in fp32 as this build does (a bf16 running
+        # the bf16 oracle chain holds its angle in fp32 as the HIP path does (a bf16 running
         # angle, the reference's choice, alone drifts by whole radians at these positions)
         st16 = [{k: v.float().cpu() for k, v in st.items()} for st in states]
         worst, worst16, agree = 0.0, 0.0, 0
