@@ -33,6 +33,9 @@ CASES = [
     (1, 50, 2, 16, 16, 8, True, False, True),
     (1, 200, 1, 64, 128, 2, False, True, False),
     (1, 1, 2, 16, 32, 2, True, True, True),
+    # two headdim and two d_state tiles, each second one partial (96 = 64 + 32, 160 = 128 + 32)
+    (1, 70, 2, 96, 160, 2, True, True, True),
+    (1, 45, 1, 96, 160, 1, False, False, True),
     # ranks 3, 5, 6, 7: rank-4 / rank-8 tiles with their extra slots read as zero
     (1, 90, 2, 16, 32, 3, True, True, True),
     (1, 70, 2, 16, 32, 3, False, False, True),
