@@ -97,7 +97,10 @@ int launch_chunked_bwd(int B, int T, int H, int P, int N, int R, const float* x_
                        const float* h_init, const float* dy, const float* dh_final, float* dx_g,
                        float* dx_b, float* dB_g, float* dB_b, float* dC, float* ddt, float* dA,
                        float* dD, float* dx_raw, float* dh_init, void* workspace,
-                       hipStream_t stream, const float* hs_pre = nullptr);
+                       hipStream_t stream, const float* hs_pre = nullptr, bool comb_b = false);
+// comb_b (needs the beta terms): dB_g receives dB_g[t] + dB_b[t + 1] and dB_b only the b part
+// of each chunk's first token, as (B, K, H, N, R) rows with K chunks of
+// chunked_chunk_tokens(R, true) tokens (they belong to the previous chunk's last token).
 
 // fp32 layer prefill on the fp32-MFMA chunk kernels (preparation, chunked SSD, gate).
 // Its workspace holds chunked_ssd's inputs and the SSD output, which the layer backward reads.

@@ -56,6 +56,10 @@ constexpr int kAC = 64;  // tokens per chunk of the angle suffix scan
 
 struct Args {
     int B, T, H, P, N, R, G, trap, cplx;
+    // With the trapezoid: tokens per chunk of the chunked backward and chunks per sequence.
+    // gBt then holds dL/dB~ from both B factors except the b part of each chunk's first token,
+    // which gBb holds as (B, K, H, N, R) rows (it belongs to the previous chunk's last token).
+    int qb, nk;
     int64_t rs;
     ProjLayout pl;
     float eps;
@@ -412,9 +416,10 @@ __global__ __launch_bounds__(NTH) void tb_bc(Args a) {
                     float gb[2 * R], gc[2 * R];
                     ldv<2 * R>(a.gBt + e0, gb);
                     ldv<2 * R>(a.gCt + e0, gc);
-                    if (a.trap && t + 1 < a.T) {
+                    if (a.trap && t + 1 < a.T && (t + 1) % a.qb == 0) {
                         float nb[2 * R];
-                        ldv<2 * R>(a.gBb + e0 + (int64_t)a.H * NR, nb);
+                        const int64_t ck = ((int64_t)b * a.nk + (t + 1) / a.qb) * a.H + h;
+                        ldv<2 * R>(a.gBb + ck * NR + (int64_t)(2 * i) * R, nb);
 #pragma unroll
                         for (int k = 0; k < 2 * R; ++k) gb[k] += nb[k];
                     }
@@ -675,9 +680,11 @@ Plan plan(const m3_layer_desc& d) {
     const size_t BTH = B * T * H, X = BTH * P * R, BN = BTH * N * R, NH = N / 2;
     const size_t nTB = (T + TBK - 1) / TBK, nTC = (T + TBC - 1) / TBC, nc = (T + kAC - 1) / kAC;
     const bool trap = d.use_trapezoidal != 0;
+    const int qb = trap ? chunked_chunk_tokens(d.mimo_rank, true) : 0;
+    const size_t bnd = trap && qb > 0 ? B * ((T + qb - 1) / qb) * H * N * R : 0;
     const size_t sizes[26] = {
         X, X, trap ? X : 0, X,                         // gys, gxg, gxb, gxr
-        BN, trap ? BN : 0, BN,                         // gBt, gBb, gCt
+        BN, trap ? bnd : 0, BN,                        // gBt, gBb (chunk-start rows), gCt
         BTH, H, H, BTH,                                // gdtc, gAc, gD, gdtx
         BTH * NH, BTH * NH, B * nc * H * NH,           // gphi, Phi, Phi_sum
         B * nTB * H,                                   // gA_part
@@ -738,6 +745,9 @@ int launch_layer_bwd(const m3_layer_desc& d, const m3_layer_params& p, const voi
     Args a;
     a.B = d.batch, a.T = d.seqlen, a.H = d.nheads, a.P = d.headdim, a.N = d.d_state;
     a.R = d.mimo_rank, a.G = d.ngroups, a.trap = d.use_trapezoidal, a.cplx = d.use_complex;
+    a.qb = a.trap ? chunked_chunk_tokens(a.R, true) : 1;
+    a.nk = (a.T + a.qb - 1) / a.qb;
+    if (a.qb <= 0) return 1;
     a.rs = d.proj_row_stride, a.pl = proj_layout(d), a.eps = d.rms_eps, a.prm = p;
     a.proj = reinterpret_cast<const float*>(proj);
     a.dt_scale = dt_scale;
@@ -766,7 +776,8 @@ int launch_layer_bwd(const m3_layer_desc& d, const m3_layer_params& p, const voi
     if (launch_chunked_bwd(a.B, a.T, a.H, a.P, a.N, a.R, a.f.xg, a.f.xb, a.f.Bt, a.f.Bb, a.f.Ct,
                            a.f.dt, a.f.A, p.D, a.f.xr, nullptr, a.gys, g_h, a.gxg, a.gxb, a.gBt,
                            a.gBb, a.gCt, a.gdtc, a.gAc, a.gD, a.gxr, nullptr,
-                           ws + pl.chunk_off, stream, fp32_layer_hs_ok(d) ? a.f.Hs : nullptr) != 0)
+                           ws + pl.chunk_off, stream, fp32_layer_hs_ok(d) ? a.f.Hs : nullptr,
+                           a.trap != 0) != 0)
         return 1;
     switch (a.R) {
         case 1: hipLaunchKernelGGL(tb_x<1>, dim3(gbh), dim3(NTH), 0, stream, a); break;

@@ -73,6 +73,11 @@ struct Args {
     // have_hs = 1: the chunk-start states Hs come from the forward (the chunk-local states and
     // the forward scan are skipped)
     int have_hs;
+    // comb_b = 1 (the layer's backward, with the beta terms): dBg receives dB_g[t] + dB_b[t + 1]
+    // (B_b of a token is the rotated B of the token before it) and dBb only the b part of
+    // each chunk's first token, as (B, K, H, N, R) rows, which belong to the previous chunk's
+    // last token
+    int comb_b;
     float *y, *hfin;
 };
 
@@ -163,6 +168,62 @@ __device__ __forceinline__ void gemm_acc(f32x4 (&acc)[TN / 16], int kdim, LA la,
         for (int i = 0; i < NA; ++i) {
             const int e = tid + NTH * i, k = k0 + ak(e);
             const float v = fa(am(e), min(k, kdim - 1), ra[i]);
+            l.A[ak(e)][am(e)] = k < kdim ? v : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            const int e = tid + NTH * i, k = k0 + bk(e);
+            const float v = fb(min(k, kdim - 1), bn(e), rb[i]);
+            l.B[bk(e)][bn(e)] = k < kdim ? v : 0.f;
+        }
+        __syncthreads();
+        if (k0 + KT < kdim) fetch(k0 + KT);
+#pragma unroll
+        for (int k4 = 0; k4 < KT; k4 += 4) {
+            const float av = l.A[k4 + (lane >> 4)][16 * wave + (lane & 15)];
+#pragma unroll
+            for (int j = 0; j < TN / 16; ++j) {
+                const float bv = l.B[k4 + (lane >> 4)][16 * j + (lane & 15)];
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[j], 0, 0, 0);
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// As gemm_acc<TN, true, BK>, with each A element the sum of two finished loads:
+// A(m, k) = fa(m, k, la(m, k)) + fa2(m, k, la2(m, k)).
+template <int TN, bool BK, class LA, class FA, class LA2, class FA2, class LB, class FB>
+__device__ __forceinline__ void gemm_acc_a2(f32x4 (&acc)[TN / 16], int kdim, LA la, FA fa, LA2 la2,
+                                            FA2 fa2, LB lb, FB fb, Lds<TN>& l) {
+    constexpr int NA = KT * TT / NTH;
+    constexpr int NB = KT * TN / NTH;
+    const int tid = opaque_tid(), lane = tid & 63, wave = tid >> 6;
+    auto ak = [](int e) { return e % KT; };
+    auto am = [](int e) { return e / KT; };
+    auto bk = [](int e) { return BK ? e % KT : e / TN; };
+    auto bn = [](int e) { return BK ? e / KT : e % TN; };
+    float ra[NA], ra2[NA], rb[NB];
+    auto fetch = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < NA; ++i) {
+            const int e = tid + NTH * i, k = min(k0 + ak(e), kdim - 1);
+            ra[i] = la(am(e), k);
+            ra2[i] = la2(am(e), k);
+        }
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            const int e = tid + NTH * i;
+            rb[i] = lb(min(k0 + bk(e), kdim - 1), bn(e));
+        }
+    };
+    fetch(0);
+#pragma unroll 1
+    for (int k0 = 0; k0 < kdim; k0 += KT) {
+#pragma unroll
+        for (int i = 0; i < NA; ++i) {
+            const int e = tid + NTH * i, k = k0 + ak(e), kc = min(k, kdim - 1);
+            const float v = fa(am(e), kc, ra[i]) + fa2(am(e), kc, ra2[i]);
             l.A[ak(e)][am(e)] = k < kdim ? v : 0.f;
         }
 #pragma unroll
@@ -818,6 +879,71 @@ __global__ __launch_bounds__(NTH) void bwd_dc(Args a) {
             l, red, cs, outv);
 }
 
+// ---- K4 with the B factor gradients combined (Args::comb_b): rows (t, r) of the chunk's
+// tokens get dB_g[t] + dB_b[t + 1]. The b part of token t + 1 enters through the operands
+// (DM^T rows and e dt x rows of the two factors summed), so the tile has Qb R rows instead of
+// 2 Qb R. Token 0's b part goes to its own row block (dBb, (B, K, H, N, R)), formed on the
+// VALU. ed[t] = exp(c_end - c_t) dt_t.
+template <int R, bool BETA, bool PADR>
+__device__ __forceinline__ void dbf_comb_tile(const Args& a, const Chunk<R, BETA, PADR>& q, int ch,
+                                              int nt, ScoresLds DM, Lds<TW>& l, const float* ed) {
+    BW_CONSTS
+    static_assert(BETA && QR == TT, "rows (t, r) of one tile");
+    const Shape& s = a.s;
+    const int b = q.b, k = q.k, h = q.h;
+    const int n0 = nt * TW;
+    constexpr int NJ = TW / 16;
+    const int tid = opaque_tid(), ty = tid >> 4, tx = tid & 15;
+    const float* dH = a.dch + chx(s, b, k, h) * s.PN;
+    f32x4 acc[NJ];
+    zero(acc);
+    const int nmax = s.N - 1;
+    auto lbh = [&](int p, int nn) { return dH[p * s.N + min(n0 + nn, nmax)]; };
+    auto fbh = [&](int p, int nn, float v) { return n0 + nn < s.N ? v : 0.f; };
+    // e dt x_g of token t plus e dt x_b of token t + 1
+    gemm_acc_a2<TW, false>(acc, s.P,
+             [&](int m, int p) { return q.lx(m / R, p, m % R); },
+             [&](int m, int p, float v) { const int t = m / R; return q.ok(t, m % R) ? ed[t] * v : 0.f; },
+             [&](int m, int p) { return q.lx(m / R + 1, p, R + m % R); },
+             [&](int m, int p, float v) {
+                 const int t = min(m / R + 1, QB - 1);
+                 return m / R + 1 < QB && q.ok(t, m % R) ? ed[t] * v : 0.f;
+             },
+             lbh, fbh, l);
+    gemm_lds_a<TW, false>(acc, QR,
+             [&](int m, int kk) {
+                 const int t = m / R, r = m % R;
+                 const float g = DM(kk, t * R2 + r);
+                 return t + 1 < QB ? g + DM(kk, (t + 1) * R2 + R + r) : g;
+             },
+             [&](int jr, int nn) { return q.lc(jr / R, min(n0 + nn, nmax), jr % R); },
+             [&](int jr, int nn, float v) { return n0 + nn < s.N && q.ok(jr / R, jr % R) ? v : 0.f; },
+             l);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = 4 * ty + i, t = m / R, r = m % R;
+        if (!q.real(t) || !q.has(r)) continue;
+        const int64_t base = row(s, b, k * QB + t, h) * s.N * q.rk() + r;
+#pragma unroll
+        for (int jj = 0; jj < NJ; ++jj) {
+            const int n = n0 + tcol(tx, jj);
+            if (n < s.N) a.dBg[base + (int64_t)n * q.rk()] = acc[jj][i];
+        }
+    }
+    // token 0's b part: sum_{(t,r')} DM[(t,r'),(0,R+r)] C[t,n,r'] + ed[0] sum_p x_b[0,p,r] dH[p,n]
+    for (int e = tid; e < TW * R; e += NTH) {
+        const int n = n0 + e / R, r = e % R;
+        if (n >= s.N || !q.has(r)) continue;
+        float v = 0.f;
+#pragma unroll 16
+        for (int kk = 0; kk < QR; ++kk) v += DM(kk, R + r) * q.lc(kk / R, n, kk % R);
+        float w = 0.f;
+#pragma unroll 16
+        for (int p = 0; p < s.P; ++p) w += q.lx(0, p, R + r) * dH[p * s.N + n];
+        a.dBb[((int64_t)ch * s.N + n) * q.rk() + r] = v + ed[0] * w;
+    }
+}
+
 // ---- K3-5 fused, for chunks whose score tiles are one 64 x 128 tile (every rank with the
 // beta terms: QR = Qb R = 64, QR2 = Qb 2R = 128). One block per chunk forms W o G in an LDS
 // tile, runs the dXf tiles on it, forms DX, takes the Z sums of (W o G) o DX element by
@@ -831,7 +957,7 @@ __global__ __launch_bounds__(NTH, 3) void bwd_fused(Args a) {
     __shared__ Lds<TW> l;
     __shared__ float S[TT][TW + 1];
     __shared__ float red[TT][17];
-    __shared__ float cs[64], dts[64], outv[64], zrow[64], zcol[64];
+    __shared__ float cs[64], dts[64], outv[64], zrow[64], zcol[64], ed[64];
     const Shape& s = a.s;
     const int ch = blockIdx.x, h = ch % s.H, k = (ch / s.H) % s.K, b = ch / (s.H * s.K);
     const Chunk<R, BETA, PADR> q{&a, b, k, h};
@@ -841,6 +967,7 @@ __global__ __launch_bounds__(NTH, 3) void bwd_fused(Args a) {
         dts[tid] = tid < QB ? q.dtv(tid) : 0.f;
     }
     __syncthreads();
+    if (tid < 64) ed[tid] = tid < QB ? __expf(cs[QB - 1] - cs[tid]) * dts[tid] : 0.f;
     constexpr int NJ = TW / 16;
     const ScoresLds Sat{S};
     f32x4 g[NJ];
@@ -915,10 +1042,15 @@ __global__ __launch_bounds__(NTH, 3) void bwd_fused(Args a) {
     }
 #pragma unroll 1
     for (int nt = 0; nt < s.nNt; ++nt) dc_tile(a, q, ch, 0, nt, Sat, l, red, cs, outv);
+    if (a.comb_b) {
 #pragma unroll 1
-    for (int rt = 0; rt < QR2 / TT; ++rt)
+        for (int nt = 0; nt < s.nNt; ++nt) dbf_comb_tile(a, q, ch, nt, Sat, l, ed);
+    } else {
 #pragma unroll 1
-        for (int nt = 0; nt < s.nNt; ++nt) dbf_tile(a, q, rt, nt, Sat, l, cs, dts);
+        for (int rt = 0; rt < QR2 / TT; ++rt)
+#pragma unroll 1
+            for (int nt = 0; nt < s.nNt; ++nt) dbf_tile(a, q, rt, nt, Sat, l, cs, dts);
+    }
 }
 
 // ---- K6: per chunk: dc -> d(A dt) (suffix sums), ddt, the chunk's partials of dA and dD,
@@ -1293,10 +1425,11 @@ int launch_chunked_bwd(int B, int T, int H, int P, int N, int R, const float* x_
                        const float* h_init, const float* dy, const float* dh_final, float* dx_g,
                        float* dx_b, float* dB_g, float* dB_b, float* dC, float* ddt, float* dA,
                        float* dD, float* dx_raw, float* dh_init, void* workspace,
-                       hipStream_t stream, const float* hs_pre) {
+                       hipStream_t stream, const float* hs_pre, bool comb_b) {
     using namespace bw;
     Shape s;
     if (!make_shape(B, T, H, P, N, R, x_b != nullptr, s)) return 1;
+    if (comb_b && x_b == nullptr) return 1;
     const Plan pl = make_plan(s, hs_pre != nullptr);
     char* ws = reinterpret_cast<char*>(workspace);
     auto part = [&](int i) { return reinterpret_cast<float*>(ws + pl.off[i]); };
@@ -1313,6 +1446,7 @@ int launch_chunked_bwd(int B, int T, int H, int P, int N, int R, const float* x_
     a.fwd = 0, a.y = nullptr, a.hfin = nullptr;
     a.have_hs = hs_pre != nullptr;
     if (hs_pre) a.Hs = const_cast<float*>(hs_pre);  // read only
+    a.comb_b = comb_b ? 1 : 0;
 
     const bool beta = x_b != nullptr, pad = s.RT != s.R;
     switch (s.RT * 4 + (beta ? 2 : 0) + (pad ? 1 : 0)) {
