@@ -936,7 +936,10 @@ __device__ __forceinline__ void dbf_comb_tile(const Args& a, const Chunk<R, BETA
         if (n >= s.N || !q.has(r)) continue;
         float v = 0.f;
 #pragma unroll 16
-        for (int kk = 0; kk < QR; ++kk) v += DM(kk, R + r) * q.lc(kk / R, n, kk % R);
+        for (int kk = 0; kk < QR; ++kk) {
+            const float cv = q.lc(kk / R, n, kk % R);  // clamped load, masked after it arrives
+            v += DM(kk, R + r) * (q.ok(kk / R, kk % R) ? cv : 0.f);
+        }
         float w = 0.f;
 #pragma unroll 16
         for (int p = 0; p < s.P; ++p) w += q.lx(0, p, R + r) * dH[p * s.N + n];
