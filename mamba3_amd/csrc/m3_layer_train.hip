@@ -402,30 +402,42 @@ __global__ __launch_bounds__(NTH) void tb_bc(Args a) {
             }
             for (int e = tid; e < HS * NR; e += NTH) qB[e] = qC[e] = 0.f;
             __syncthreads();
+            // This thread's heads of the group (one RoPE pair each: N / 2 <= NTH), software-
+            // pipelined: the next head's angle and gradient rows are loaded before this head's
+            // math. nb: the b part of the next chunk's first token, at chunk ends.
+            const bool bnd = a.trap && t + 1 < a.T && (t + 1) % a.qb == 0;
+            const int64_t ckb = bnd ? ((int64_t)b * a.nk + (t + 1) / a.qb) * a.H : 0;
+            const int i = i0;
+            float ph = 0.f, gb[2 * R], gc[2 * R], nb[2 * R];
+            auto fetch = [&](int hl) {
+                const int64_t th = tok * a.H + g * hpg + hl;
+                const int64_t e0 = th * NR + (int64_t)(2 * i) * R;
+                if (a.cplx) ph = a.f.phi[th * NH + i];
+                ldv<2 * R>(a.gBt + e0, gb);
+                ldv<2 * R>(a.gCt + e0, gc);
+                if (bnd) ldv<2 * R>(a.gBb + (ckb + g * hpg + hl) * NR + (int64_t)(2 * i) * R, nb);
+            };
+            if (hg < hpg) fetch(hg);
             for (int hl = hg; hl < hpg; hl += HS) {
                 const int h = g * hpg + hl;
                 const int64_t th = tok * a.H + h;
-                const int64_t bt = th * NR;
                 float* qb = qB + (int64_t)hg * NR;
                 float* qc = qC + (int64_t)hg * NR;
-                for (int i = i0; i < NH; i += NTH) {
-                    float s = 0.f, c = 1.f;
-                    if (a.cplx) sincosf(a.f.phi[th * NH + i], &s, &c);
-                    float gphi = 0.f;
-                    const int64_t e0 = bt + (int64_t)(2 * i) * R;
-                    float gb[2 * R], gc[2 * R];
-                    ldv<2 * R>(a.gBt + e0, gb);
-                    ldv<2 * R>(a.gCt + e0, gc);
-                    if (a.trap && t + 1 < a.T && (t + 1) % a.qb == 0) {
-                        float nb[2 * R];
-                        const int64_t ck = ((int64_t)b * a.nk + (t + 1) / a.qb) * a.H + h;
-                        ldv<2 * R>(a.gBb + ck * NR + (int64_t)(2 * i) * R, nb);
+                float cgb[2 * R], cgc[2 * R];
 #pragma unroll
-                        for (int k = 0; k < 2 * R; ++k) gb[k] += nb[k];
-                    }
+                for (int k = 0; k < 2 * R; ++k) {
+                    cgb[k] = bnd ? gb[k] + nb[k] : gb[k];
+                    cgc[k] = gc[k];
+                }
+                const float cph = ph;
+                if (hl + HS < hpg) fetch(hl + HS);
+                {
+                    float s = 0.f, c = 1.f;
+                    if (a.cplx) sincosf(cph, &s, &c);
+                    float gphi = 0.f;
 #pragma unroll
                     for (int r = 0; r < R; ++r) {
-                        float gbe = gb[r], gbo = gb[R + r];
+                        float gbe = cgb[r], gbo = cgb[R + r];
                         if (t == a.T - 1 && a.gprev) {
                             const float* gp = a.gprev + ((int64_t)b * a.H + h) * a.P * a.N;
                             const float* xr = a.f.xr + th * a.P * R + r;
@@ -434,7 +446,7 @@ __global__ __launch_bounds__(NTH) void tb_bc(Args a) {
                                 gbo += gp[(int64_t)pp * a.N + 2 * i + 1] * xr[(int64_t)pp * R];
                             }
                         }
-                        const float gce = gc[r], gco = gc[R + r];
+                        const float gce = cgc[r], gco = cgc[R + r];
                         const int je = (2 * i) * R + r, jo = je + R;
                         if (a.cplx) {
                             // the rotated rows: e' = e cos - o sin, o' = e sin + o cos
