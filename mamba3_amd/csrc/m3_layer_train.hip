@@ -218,34 +218,67 @@ __global__ __launch_bounds__(NTH) void tb_x(Args a) {
     float gA = 0.f;
     const int t0 = tb * TBK, t1 = min(a.T, (tb + 1) * TBK);
     const int rounds = (t1 - t0 + slots - 1) / slots;
-    for (int k = 0; k < rounds; ++k) {
+    // One round's inputs, loaded a round ahead of their use (a one-deep software pipeline):
+    // lambda and dt of the token and the next one (raw), x, and the gradient / x rows.
+    struct In {
+        float lr, dtv, lrn, dtn, x;
+        float gxr[R], gxg[R], gxb[R], xrv[R], gxbn[R], xrp[R];
+    };
+    auto fetch = [&](int k, In& v) {
         const int t = t0 + k * slots + slot;
         const bool act = t < t1;
         const int64_t tok = (int64_t)b * a.T + (act ? t : t0);
         const int64_t th = tok * a.H + h;
         const float* row = a.proj + tok * a.rs;
+        v.lr = v.dtv = v.lrn = v.dtn = v.x = 0.f;
+        if (a.trap && act) {
+            v.lr = row[a.pl.lam + h];
+            v.dtv = a.f.dt[th];
+            if (t + 1 < a.T) {
+                v.lrn = row[a.rs + a.pl.lam + h];
+                v.dtn = a.f.dt[th + a.H];
+            }
+        }
+        if (col && act) {
+            v.x = row[a.pl.x + (int64_t)h * a.P + p];
+            const int64_t e0 = th * PR + (int64_t)p * R;
+            ldr<R>(a.gxr + e0, v.gxr);
+            ldr<R>(a.gxg + e0, v.gxg);
+            if (a.trap) {
+                ldr<R>(a.gxb + e0, v.gxb);
+                ldr<R>(a.f.xr + e0, v.xrv);
+                if (t + 1 < a.T) ldr<R>(a.gxb + e0 + (int64_t)a.H * PR, v.gxbn);  // next token's
+                if (t > 0) ldr<R>(a.f.xr + e0 - (int64_t)a.H * PR, v.xrp);        // previous token's
+            }
+        }
+    };
+    In nxt;
+    if (rounds > 0) fetch(0, nxt);
+    for (int k = 0; k < rounds; ++k) {
+        const In in = nxt;
+        if (k + 1 < rounds) fetch(k + 1, nxt);
+        const int t = t0 + k * slots + slot;
+        const bool act = t < t1;
+        const int64_t tok = (int64_t)b * a.T + (act ? t : t0);
+        const int64_t th = tok * a.H + h;
         float lam = 1.f, dA = 1.f, lamn = 1.f, dAn = 1.f;
         if (a.trap && act) {
-            lam = sigm(row[a.pl.lam + h]);
-            dA = expf(Ah * a.f.dt[th]);
+            lam = sigm(in.lr);
+            dA = expf(Ah * in.dtv);
             if (t + 1 < a.T) {
-                lamn = sigm(row[a.rs + a.pl.lam + h]);
-                dAn = expf(Ah * a.f.dt[th + a.H]);
+                lamn = sigm(in.lrn);
+                dAn = expf(Ah * in.dtn);
             }
         }
         float sl = 0.f, sa = 0.f;
         if (col && act) {
-            const float x = row[a.pl.x + (int64_t)h * a.P + p];
-            const int64_t e0 = th * PR + (int64_t)p * R;
-            float gxr[R], gxg[R], gxb[R], xrv[R], gxbn[R], xrp[R];
-            ldr<R>(a.gxr + e0, gxr);
-            ldr<R>(a.gxg + e0, gxg);
-            if (a.trap) {
-                ldr<R>(a.gxb + e0, gxb);
-                ldr<R>(a.f.xr + e0, xrv);
-                if (t + 1 < a.T) ldr<R>(a.gxb + e0 + (int64_t)a.H * PR, gxbn);  // next token's
-                if (t > 0) ldr<R>(a.f.xr + e0 - (int64_t)a.H * PR, xrp);          // previous token's
-            }
+            const float x = in.x;
+            const float(&gxr)[R] = in.gxr;
+            const float(&gxg)[R] = in.gxg;
+            const float(&gxb)[R] = in.gxb;
+            const float(&xrv)[R] = in.xrv;
+            const float(&gxbn)[R] = in.gxbn;
+            const float(&xrp)[R] = in.xrp;
             float gx = 0.f;
 #pragma unroll
             for (int r = 0; r < R; ++r) {
@@ -293,7 +326,7 @@ __global__ __launch_bounds__(NTH) void tb_x(Args a) {
                     a.gproj[tok * a.rs + a.pl.lam + h] = glam * lam * (1.f - lam);
                     a.gdtx[th] = gdA * dA * Ah;
                 }
-                gA += gdA * dA * a.f.dt[th];
+                gA += gdA * dA * in.dtv;
             }
         } else if (act && p == 0) {
             a.gdtx[th] = 0.f;
