@@ -843,11 +843,47 @@ __device__ __forceinline__ void dc_tile(const Args& a, const Chunk<R, BETA, PADR
     {
         auto lb = [&](int jc, int nn) { return q.lbf(jc / R2, min(n0 + nn, nmax), jc % R2); };
         auto fb = [&](int jc, int nn, float v) { return n0 + nn < s.N && q.okj(jc / R2, jc % R2) ? v : 0.f; };
-        if constexpr (SM::kLds)
-            gemm_lds_a<TW, false>(acc, QR2, [&](int mm, int jc) { return DM(m0 + mm, jc); }, lb, fb, l);
-        else
+        if constexpr (SM::kLds) {
+            if constexpr (BETA && QR == TT) {
+                if (a.comb_b) {
+                    // B_b of token s is B_g of token s - 1: the contraction runs over the Qb R
+                    // columns (s, r) of B_g, with DM's two columns that meet each summed, and
+                    // token 0's B_b enters below as a rank-R update
+                    gemm_lds_a<TW, false>(acc, QR,
+                             [&](int mm, int kc) {
+                                 const int u = kc / R, r = kc % R;
+                                 const float g = DM(m0 + mm, u * R2 + r);
+                                 return u + 1 < QB ? g + DM(m0 + mm, (u + 1) * R2 + R + r) : g;
+                             },
+                             [&](int kc, int nn) { return q.lbf(kc / R, min(n0 + nn, nmax), kc % R); },
+                             [&](int kc, int nn, float v) { return n0 + nn < s.N && q.okj(kc / R, kc % R) ? v : 0.f; },
+                             l);
+#pragma unroll 1
+                    for (int r = 0; r < R; ++r) {
+                        float bb[NJ];
+#pragma unroll
+                        for (int j = 0; j < NJ; ++j) {
+                            const int n = n0 + tcol(tx, j);
+                            const float v = q.lbf(0, min(n, nmax), R + r);
+                            bb[j] = n < s.N && q.okj(0, R + r) ? v : 0.f;
+                        }
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const float d = DM(m0 + 4 * ty + i, R + r);
+#pragma unroll
+                            for (int j = 0; j < NJ; ++j) acc[j][i] += d * bb[j];
+                        }
+                    }
+                } else {
+                    gemm_lds_a<TW, false>(acc, QR2, [&](int mm, int jc) { return DM(m0 + mm, jc); }, lb, fb, l);
+                }
+            } else {
+                gemm_lds_a<TW, false>(acc, QR2, [&](int mm, int jc) { return DM(m0 + mm, jc); }, lb, fb, l);
+            }
+        } else {
             gemm_acc<TW, true, false>(acc, QR2, [&](int mm, int jc) { return DM(m0 + mm, jc); },
                                       [&](int mm, int jc, float v) { return v; }, lb, fb, l);
+        }
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -975,20 +1011,53 @@ __global__ __launch_bounds__(NTH, 3) void bwd_fused(Args a) {
     const ScoresLds Sat{S};
     f32x4 g[NJ];
     // W o G -> S: G[(t,r),(s,j)] = sum_n C[t,n,r] Bf[s,n,j]
-    zero(g);
-    gemm_acc<TW, true, true>(g, s.N,
-                 [&](int m, int n) { return q.lc(m / R, n, m % R); },
-                 [&](int m, int n, float v) { return q.ok(m / R, m % R) ? v : 0.f; },
-                 [&](int n, int c) { return q.lbf(c / R2, n, c % R2); },
-                 [&](int n, int c, float v) { return q.okj(c / R2, c % R2) ? v : 0.f; },
-                 l);
+    if (a.comb_b) {
+        // B_b of token s is B_g of token s - 1, so the b columns of G are its g columns one
+        // token later: a 64 x (Qb R) GEMM whose values are stored twice (each with its own
+        // W), and token 0's b columns (B_b of token 0) on the VALU
+        f32x4 gg[4];
+        zero(gg);
+        gemm_acc<TT, true, true>(gg, s.N,
+                     [&](int m, int n) { return q.lc(m / R, n, m % R); },
+                     [&](int m, int n, float v) { return q.ok(m / R, m % R) ? v : 0.f; },
+                     [&](int n, int c) { return q.lbf(c / R, n, c % R); },
+                     [&](int n, int c, float v) { return q.okj(c / R, c % R) ? v : 0.f; },
+                     reinterpret_cast<Lds<TT>&>(l));
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-            const int m = 4 * ty + i, c = tcol(tx, j), t = m / R, u = c / R2;
-            S[m][c] = u <= t ? __expf(cs[t] - cs[u]) * g[j][i] : 0.f;
+            for (int j = 0; j < 4; ++j) {
+                const int m = 4 * ty + i, c = tcol(tx, j), t = m / R, u = c / R, r = c % R;
+                S[m][u * R2 + r] = u <= t ? __expf(cs[t] - cs[u]) * gg[j][i] : 0.f;
+                if (u + 1 < QB)
+                    S[m][(u + 1) * R2 + R + r] = u + 1 <= t ? __expf(cs[t] - cs[u + 1]) * gg[j][i] : 0.f;
+            }
+        for (int e = tid; e < TT * R; e += NTH) {
+            const int m = e / R, r = e % R, t = m / R;
+            float v = 0.f;
+#pragma unroll 16
+            for (int n = 0; n < s.N; ++n) {
+                const float cv = q.lc(t, n, m % R), bv = q.lbf(0, n, R + r);
+                v += cv * bv;
+            }
+            S[m][R + r] = q.ok(t, m % R) && q.okj(0, R + r) ? __expf(cs[t] - cs[0]) * v : 0.f;
         }
+    } else {
+        zero(g);
+        gemm_acc<TW, true, true>(g, s.N,
+                     [&](int m, int n) { return q.lc(m / R, n, m % R); },
+                     [&](int m, int n, float v) { return q.ok(m / R, m % R) ? v : 0.f; },
+                     [&](int n, int c) { return q.lbf(c / R2, n, c % R2); },
+                     [&](int n, int c, float v) { return q.okj(c / R2, c % R2) ? v : 0.f; },
+                     l);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                const int m = 4 * ty + i, c = tcol(tx, j), t = m / R, u = c / R2;
+                S[m][c] = u <= t ? __expf(cs[t] - cs[u]) * g[j][i] : 0.f;
+            }
+    }
     __syncthreads();
 #pragma unroll 1
     for (int rt = 0; rt < QR2 / TT; ++rt)
