@@ -225,6 +225,38 @@ def test_layer_prefill_gradients_match_oracle(kw, cuda_device):
         assert err < FP32_TOL, (name, err)
 
 
+@pytest.mark.parametrize("rank,T", [(2, 1), (2, 32), (2, 33), (2, 64), (1, 65), (4, 17)])
+def test_layer_gradients_at_chunk_edges(rank, T, cuda_device):
+    """Sequence lengths at the chunk edges of the backward (chunks of 32 tokens at rank 2, 64
+    at rank 1, 16 at rank 4 with the trapezoid): one token, exactly one chunk, one token past
+    a chunk end (where the B gradient of the chunk's first token goes to the previous
+    chunk's last token), against the fp64 oracle layer. A gradient that vanishes
+    identically (A_log at one token: A only scales the zero initial state) is checked
+    against the layer's gradient scale, since the oracle's value is fp64 rounding noise."""
+    kw = dict(d_model=64, d_state=16, headdim=16, mimo_rank=rank)
+    print(f"layer backward at chunk edges rank {rank} T {T}", flush=True)
+    torch.manual_seed(0)
+    layer = mamba3_amd.KulaMamba(**kw).to(cuda_device).train()
+    H, P, N = layer.nheads, layer.headdim, layer.d_state
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(2, T, kw["d_model"], generator=g)
+    w = torch.randn(2, T, kw["d_model"], generator=g)
+    wh = torch.randn(2, H, P, N, generator=g)
+    out_ref, pg, xg_ref = _oracle_layer_grads(kw, layer, x, w, wh)
+    xd = x.to(cuda_device).requires_grad_()
+    out, st = layer.prefill(xd)
+    ((out * w.to(cuda_device)).sum() + (st["h"] * wh.to(cuda_device)).sum()).backward()
+    assert max_rel(out, out_ref) < FP32_TOL
+    assert max_rel(xd.grad, xg_ref) < FP32_TOL
+    scale = max(v.abs().max().item() for v in pg.values())
+    for name, p in layer.named_parameters():
+        if pg[name].abs().max().item() < 1e-8 * scale:
+            err = p.grad.detach().abs().max().item() / scale
+        else:
+            err = max_rel(p.grad, pg[name])
+        assert err < FP32_TOL, (name, err)
+
+
 def test_layer_d768_gradients_match_oracle(cuda_device):
     """The d_model 768 layer (24 heads, headdim 64, d_state 128, rank 2) over 160 tokens:
     every parameter's gradient and the input's against the fp64 oracle layer."""
